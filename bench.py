@@ -1,0 +1,376 @@
+"""Decode-step throughput of the Flow transformer on one MI355X.
+
+Workload (the headline line): batched decode, B=64 independent streams,
+12 layers, d=512, 8x64 heads, FFN 2048, Q8_0 weights (per-row scales),
+per-stream contexts c ~ U{1..2048} (keys attended, including the appended
+one), paged fp32 KV with block size 16 and shuffled block tables. One "step"
+advances every stream by one frame. Inputs and KV are resident in HBM when
+the timed region starts; data is synthetic (seeded).
+
+Also reported in the same JSON line: B=1 decode (12 layers, context 256 ->
+256+steps), the single Q8 matvec (2048x512, rotating >256 MB of weight
+copies), one attention layer vs context length, the roofline of the
+dominant kernel (split attention) timed with HIP events on its stream, and
+the CPU baseline (the C restatement of the reference step, on host cores).
+
+  python bench.py [--gpus 1] [--steps K] [--warmup W] [--batch 64] [--layers 12]
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import importlib.util
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+PKG_DIR = os.path.join(ROOT, "speech-mac_amd")
+
+HBM_PEAK_GBS = 8000.0
+KV_BYTES_PER_KEY = 2 * 512 * 4          # K + V fp32 per key per layer
+Q8_LAYER_BYTES = (1536 + 512 + 2048) * 512 * 34 // 32 + 512 * 2048 * 34 // 32
+
+
+def package():
+    spec = importlib.util.spec_from_file_location(
+        "speech_mac_amd", os.path.join(PKG_DIR, "__init__.py"),
+        submodule_search_locations=[PKG_DIR])
+    mod = importlib.util.module_from_spec(spec)
+    sys.modules["speech_mac_amd"] = mod
+    spec.loader.exec_module(mod)
+    return mod
+
+
+P_I32 = ctypes.POINTER(ctypes.c_int32)
+P_F32 = ctypes.POINTER(ctypes.c_float)
+P_SZ = ctypes.POINTER(ctypes.c_size_t)
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+class Timer:
+    def __init__(self, lib, stream):
+        self.lib, self.stream = lib, stream
+        self.a, self.b = ctypes.c_void_p(), ctypes.c_void_p()
+        assert lib.pgpu_event_create(ctypes.byref(self.a))
+        assert lib.pgpu_event_create(ctypes.byref(self.b))
+
+    def start(self):
+        assert self.lib.pgpu_event_record(self.a, self.stream)
+
+    def stop_ms(self) -> float:
+        assert self.lib.pgpu_event_record(self.b, self.stream)
+        ms = ctypes.c_float()
+        assert self.lib.pgpu_event_elapsed_ms(self.a, self.b, ctypes.byref(ms))
+        return ms.value
+
+
+class DecodeSetup:
+    """Model + pool + batch with synthetic contexts, ready to step."""
+
+    def __init__(self, pkg, lib, layers, streams, lengths, headroom, seed):
+        import speech_mac_amd.synthetic as syn
+        self.lib, self.layers, self.streams = lib, layers, streams
+        self.lengths = np.asarray(lengths, np.int64)
+        self.max_positions = int(self.lengths.max()) + headroom
+        assert self.max_positions <= 8192
+        self.table_len = (self.max_positions + 15) // 16
+        blocks = streams * self.table_len
+        views = pkg.Views()
+        self.views = views
+        weights = views.layers(syn.flow_model(seed, layers))
+        self.model, self.pool, self.batch = ctypes.c_void_p(), ctypes.c_void_p(), ctypes.c_void_p()
+        assert lib.phonon_flow_model_create(weights, layers, ctypes.byref(self.model))
+        assert lib.phonon_kv_pool_create(layers, blocks, ctypes.byref(self.pool))
+        assert lib.phonon_kv_pool_fill_normal(self.pool, seed + 1)
+        ids = np.zeros(blocks, np.int32)
+        assert lib.phonon_kv_pool_alloc(self.pool, blocks, ids.ctypes.data_as(P_I32))
+        perm = np.random.default_rng(seed + 2).permutation(ids)   # shuffled tables
+        self.tables = np.ascontiguousarray(perm.reshape(streams, self.table_len).astype(np.int32))
+        assert lib.phonon_flow_batch_create(self.model, self.pool, streams, self.max_positions,
+                                            ctypes.byref(self.batch))
+        self.stream = lib.phonon_flow_batch_stream(self.batch)
+        self.din = lib.phonon_flow_batch_device_inputs(self.batch)
+        self.dout = lib.phonon_flow_batch_device_outputs(self.batch)
+        x = np.random.default_rng(seed + 3).standard_normal((streams, 512)).astype(np.float32)
+        assert lib.pgpu_copy_h2d(self.stream, self.din, x.ctypes.data, x.nbytes)
+        self.reset()
+
+    def reset(self):
+        pos = self.lengths.astype(np.uintp)
+        assert self.lib.phonon_flow_batch_set_streams(
+            self.batch, self.streams, pos.ctypes.data_as(P_SZ), self.tables.ctypes.data_as(P_I32),
+            self.table_len)
+
+    def step(self):
+        # Output feeds the next step's input: a closed-loop decode.
+        assert self.lib.phonon_flow_batch_step_device(self.batch, self.din, 10000.0, self.dout)
+        self.din, self.dout = self.dout, self.din
+
+    def positions(self):
+        out = np.zeros(self.streams, np.uintp)
+        assert self.lib.phonon_flow_batch_positions(self.batch, out.ctypes.data_as(P_SZ))
+        return out.astype(np.int64)
+
+    def close(self):
+        self.lib.phonon_flow_batch_destroy(self.batch)
+        self.lib.phonon_kv_pool_destroy(self.pool)
+        self.lib.phonon_flow_model_destroy(self.model)
+
+
+def step_bytes(layers, contexts):
+    """Algorithmic HBM bytes of one step: Q8 weights once, every attended
+    key's K+V once per layer, one appended K+V row per stream per layer."""
+    contexts = np.asarray(contexts, np.int64)
+    return layers * Q8_LAYER_BYTES + int(layers * np.sum(KV_BYTES_PER_KEY * contexts
+                                                         + KV_BYTES_PER_KEY))
+
+
+def run_decode(pkg, lib, layers, streams, lengths, steps, warmup, seed):
+    d = DecodeSetup(pkg, lib, layers, streams, lengths, steps + warmup + 1, seed)
+    for _ in range(warmup):
+        d.step()
+    assert lib.phonon_flow_batch_sync(d.batch), "non-finite value during warmup"
+    first = d.positions()
+    timer = Timer(lib, d.stream)
+    assert lib.pgpu_stream_sync(d.stream)
+    t0 = time.perf_counter()
+    timer.start()
+    for _ in range(steps):
+        d.step()
+    ms = timer.stop_ms()
+    assert lib.pgpu_stream_sync(d.stream)
+    wall = time.perf_counter() - t0
+    clean = lib.phonon_flow_batch_sync(d.batch)
+    # keys attended at step i = position + 1
+    total_bytes = sum(step_bytes(layers, first + i + 1) for i in range(steps))
+    return d, {"ms": ms, "wall_s": wall, "clean": bool(clean), "bytes": total_bytes,
+               "first_positions": first}
+
+
+def attention_roofline(pkg, lib, d, iterations=20):
+    """Average duration of the split-attention kernel alone on the decode
+    workload (layer 0 of the pool, the streams' current contexts), timed with
+    HIP events on the stream it is launched on."""
+    pos = d.positions()
+    view = pkg.PgpuPagedKv()
+    assert lib.phonon_kv_pool_view(d.pool, ctypes.byref(view))
+    streams = d.streams
+    max_splits = (d.max_positions + 255) // 256
+    q = pkg.DeviceBuffer(lib, streams * 512 * 4)
+    q.upload(np.random.default_rng(5).standard_normal((streams, 512)).astype(np.float32) * 0.125)
+    tables = pkg.DeviceBuffer(lib, d.tables.nbytes)
+    tables.upload(d.tables)
+    positions = pkg.DeviceBuffer(lib, streams * 4)
+    positions.upload(pos.astype(np.int32))
+    out = pkg.DeviceBuffer(lib, streams * 512 * 4)
+    slots = streams * 8 * max_splits
+    part = pkg.DeviceBuffer(lib, slots * 66 * 4)
+    tickets = pkg.DeviceBuffer(lib, streams * 8 * 4 + 4)
+    lib.pgpu_memset(d.stream, tickets.ptr, 0, streams * 8 * 4 + 4)
+    scratch = pkg.PgpuAttentionScratch(part.ptr, part.ptr + slots * 64 * 4, tickets.ptr,
+                                       streams, max_splits)
+    status = tickets.ptr + streams * 8 * 4
+
+    def launch():
+        assert lib.pgpu_attention(d.stream, q.ptr, ctypes.byref(view), 0, tables.ptr,
+                                  d.table_len, positions.ptr, streams, 8, max_splits, None,
+                                  out.ptr, ctypes.byref(scratch), status)
+
+    for _ in range(3):
+        launch()
+    timer = Timer(lib, d.stream)
+    timer.start()
+    for _ in range(iterations):
+        launch()
+    ms = timer.stop_ms() / iterations
+    contexts = pos + 1
+    kv_bytes = int(KV_BYTES_PER_KEY * contexts.sum())
+    traffic = kv_bytes + streams * 512 * 4 * 2
+    achieved = kv_bytes / (ms * 1e-3) / 1e9
+    st = np.zeros(1, np.int32)
+    lib.pgpu_copy_d2h(d.stream, st.ctypes.data, status, 4)
+    for b in (q, tables, positions, out, part, tickets):
+        b.free()
+    return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+            "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+            "kernel": "pgpu::k_attention", "us_per_launch": round(ms * 1e3, 2),
+            "algorithmic_bytes_per_launch": kv_bytes, "read_bytes_incl_q_out": traffic,
+            "status_clean": int(st[0]) == 0}
+
+
+def q8_matvec_bench(pkg, lib, seed=1, calls=2000):
+    """Config: single Q8 matvec 2048x512; 300 rotating weight copies (>256 MB)."""
+    import speech_mac_amd.synthetic as syn
+    rng = np.random.default_rng(seed)
+    w = syn.q8_matrix(rng, 2048, 512)
+    x = rng.standard_normal(512).astype(np.float32)
+    copies = 300
+    h = ctypes.c_void_p()
+    assert lib.phonon_q8_device_create(w.ctypes.data, 2048, 512, copies, ctypes.byref(h))
+    stream = ctypes.c_void_p()
+    assert lib.pgpu_stream_create(ctypes.byref(stream))
+    dx = pkg.DeviceBuffer(lib, 512 * 4)
+    dx.upload(x)
+    dy = pkg.DeviceBuffer(lib, 2048 * 4)
+    for i in range(20):
+        assert lib.phonon_q8_device_matvec(h, i % copies, dx.ptr, dy.ptr, 1, stream)
+    timer = Timer(lib, stream)
+    res = {}
+    for label, rotate in (("rotating_300_copies", True), ("same_copy_cache_resident", False)):
+        timer.start()
+        for i in range(calls):
+            assert lib.phonon_q8_device_matvec(h, i % copies if rotate else 0, dx.ptr, dy.ptr, 1,
+                                               stream)
+        ms = timer.stop_ms() / calls
+        nbytes = lib.phonon_q8_device_bytes_per_call(h, 1)
+        res[label] = {"us_per_call": round(ms * 1e3, 3),
+                      "GBps": round(nbytes / (ms * 1e-3) / 1e9, 1)}
+    assert lib.phonon_q8_device_status(h, stream)
+    res["bytes_per_call"] = int(lib.phonon_q8_device_bytes_per_call(h, 1))
+    res["launches_per_call"] = 2
+    dx.free()
+    dy.free()
+    lib.phonon_q8_device_destroy(h)
+    lib.pgpu_stream_destroy(stream)
+    return res
+
+
+def attention_curve(pkg, lib, seed=9):
+    """One attention layer decode (H=8, dh=64): append + attention per step,
+    vs context length, as one 1-layer batched step of one stream."""
+    out = {}
+    reps = 20
+    for c in (1, 2, 16, 128, 511, 512, 513, 1024, 2048):
+        d = DecodeSetup(pkg, lib, 1, 1, [c - 1], reps + 8, seed)
+        for _ in range(3):
+            d.step()
+        d.reset()
+        timer = Timer(lib, d.stream)
+        timer.start()
+        for _ in range(reps):
+            d.step()
+        ms = timer.stop_ms() / reps
+        d.close()
+        out[str(c)] = round(ms * 1e3, 2)
+    return {"us_per_layer_step_vs_context": out,
+            "note": f"one stream, one layer (LN, QKV+RoPE+append, attention, out, MLP) as a "
+                    f"graph replay; contexts c .. c+{reps - 1}"}
+
+
+def cpu_baseline(pkg, lib, layers, lengths, seed, budget_s=12.0):
+    """The C restatement of the reference step (oracle) on host threads, one
+    pthread per stream group, on a bounded sample of streams of the same
+    context distribution; reported in frames/s."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import oracle_py
+    import helpers
+    import speech_mac_amd.synthetic as syn
+    oracle = oracle_py.Oracle()
+    om = oracle_py.OracleModel(oracle, helpers.oracle_layers(oracle, syn.flow_model(seed, layers)))
+    threads = max(1, min(16, os.cpu_count() or 1))
+    sample = list(np.asarray(lengths)[:threads])
+    cap = int(max(sample)) + 2
+    n = len(sample)
+    tile = np.random.default_rng(seed).standard_normal(1 << 16).astype(np.float32)
+    total = n * layers * cap * 512
+    keys = np.resize(tile, total).reshape(n, layers, cap, 512)
+    vals = np.resize(tile[::-1].copy(), total).reshape(n, layers, cap, 512)
+    x = np.random.default_rng(seed + 1).standard_normal((n, 512)).astype(np.float32)
+    steps, elapsed = 0, 0.0
+    pos = np.array(sample, np.int64)
+    while elapsed < budget_s and steps < 8:
+        t0 = time.perf_counter()
+        ok, y = om.stack_step_streams(keys, vals, cap, pos + steps, x, threads)
+        elapsed += time.perf_counter() - t0
+        assert ok
+        steps += 1
+        if steps == 1 and elapsed * 3 > budget_s:
+            break
+    frames = n * steps
+    return {"value": round(frames / elapsed, 2), "unit": "frames/s", "cores": threads,
+            "kind": "port",
+            "sample": f"{n} streams x {steps} step(s), 12-layer oracle stack step, contexts "
+                      f"from the same U{{1..2048}} draw, one pthread per stream, {elapsed:.1f} s"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--batch", type=int, default=64)
+    ap.add_argument("--layers", type=int, default=12)
+    ap.add_argument("--seed", type=int, default=2026)
+    ap.add_argument("--skip-extras", action="store_true",
+                    help="only the headline B=64 line (no B=1, matvec, curve, CPU)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU: streams are independent and "
+                          "would shard across GPUs with no collectives; --gpus must be 1"}))
+        sys.exit(2)
+    pkg = package()
+    lib = pkg.load()
+    if lib.pgpu_device_init() != 1:
+        raise SystemExit("no gfx950 device: " + pkg.last_error(lib))
+    name = ctypes.create_string_buffer(256)
+    lib.pgpu_device_name(name, 256)
+    log(f"device: {name.value.decode()}")
+
+    lengths = np.random.default_rng(args.seed).integers(1, 2049, size=args.batch) - 1
+    log(f"B={args.batch} L={args.layers}: contexts {lengths.min() + 1}..{lengths.max() + 1}")
+    d, r = run_decode(pkg, lib, args.layers, args.batch, lengths, args.steps, args.warmup,
+                      args.seed)
+    ms_step = r["ms"] / args.steps
+    value = args.batch * args.steps / (r["ms"] * 1e-3)
+    gbs = r["bytes"] / (r["ms"] * 1e-3) / 1e9
+    log(f"B={args.batch}: {ms_step * 1e3:.1f} us/step, {value:.0f} frames/s, {gbs:.0f} GB/s "
+        f"({gbs / HBM_PEAK_GBS:.1%} of HBM), clean={r['clean']}")
+    roof = attention_roofline(pkg, lib, d)
+    log(f"attention kernel: {roof['us_per_launch']} us/launch, {roof['achieved']} GB/s")
+    d.close()
+
+    line = {
+        "metric": "decode frames/sec at B=64 (12L d512 Q8); achieved HBM GB/s vs peak",
+        "value": round(value, 1), "unit": "frames/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms_step, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "fp32",
+        "data": "synthetic (seeded Q8 weights, N(0,1) KV contexts)",
+        "config": {"workload": f"batched decode B={args.batch}, {args.layers} layers d512 "
+                               "8x64 FFN2048, Q8_0 per-row scales, contexts U{1..2048}, paged fp32 "
+                               "KV block 16, shuffled tables",
+                   "global_batch": args.batch, "seq_len": 2048, "parallelism": "none (1 GPU)"},
+        "hbm": {"algorithmic_bytes_per_step": int(r["bytes"] / args.steps),
+                "achieved_GBps": round(gbs, 1), "frac_of_peak": round(gbs / HBM_PEAK_GBS, 4),
+                "all_steps_finite": r["clean"]},
+        "roofline": roof,
+    }
+    if not args.skip_extras:
+        b1_steps = 750
+        d1, r1 = run_decode(pkg, lib, args.layers, 1, [256], b1_steps, 10, args.seed)
+        d1.close()
+        line["b1"] = {"frames_per_s": round(b1_steps / (r1["ms"] * 1e-3), 1),
+                      "us_per_step": round(r1["ms"] * 1e3 / b1_steps, 2),
+                      "effective_GBps": round(r1["bytes"] / (r1["ms"] * 1e-3) / 1e9, 1),
+                      "workload": "B=1, 12 layers, context 256 (synthetic prefill) then 750 "
+                                  "decode frames, hipGraph replay per step",
+                      "clean": r1["clean"]}
+        log(f"B=1: {line['b1']['us_per_step']} us/step")
+        line["q8_matvec_2048x512"] = q8_matvec_bench(pkg, lib)
+        log(f"q8 matvec: {line['q8_matvec_2048x512']}")
+        line["attention_layer_curve"] = attention_curve(pkg, lib)
+        log(f"attention curve: {line['attention_layer_curve']}")
+        line["cpu_baseline"] = cpu_baseline(pkg, lib, args.layers, lengths, args.seed)
+        log(f"cpu baseline: {line['cpu_baseline']}")
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

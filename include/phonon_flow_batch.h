@@ -1,0 +1,110 @@
+/* Batched decode step for many independent streams on one MI355X.
+ *
+ * New API with no single counterpart in the reference: speech-mac decodes one
+ * request per thread with a contiguous per-request cache (PhononKvCache,
+ * src/phonon_transformer.h:16-22). Here B streams advance one position per
+ * step through the same L-layer Flow transformer (the math of
+ * phonon_flow_stack_step, src/phonon_transformer.c:455-482, per stream),
+ * sharing one read of the weights per step, over a paged KV pool with block
+ * tables. The single-stream functions of phonon_transformer.h are built on it.
+ *
+ * Conventions follow the reference: 1 = success, 0 = failure; buffers are
+ * borrowed. Objects are not thread-safe: use one batch per thread. */
+#ifndef PHONON_FLOW_BATCH_H
+#define PHONON_FLOW_BATCH_H
+
+#include "phonon_gpu.h"
+#include "phonon_transformer.h"
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define PHONON_KV_BLOCK_POSITIONS 16
+#define PHONON_FLOW_MAX_POSITIONS 8192
+
+typedef struct PhononFlowModel PhononFlowModel;
+typedef struct PhononKvPool PhononKvPool;
+typedef struct PhononFlowBatch PhononFlowBatch;
+
+/* Device copy of `layers` layers: the analog of phonon_pack_prepare_linears
+ * (src/phonon_pack.c:413-448) for device memory. Q8_0 matrices keep 34 B per
+ * 32 weights, repacked into MFMA fragment order; BF16 matrices stay bf16.
+ * Fails on a shape, dtype or byte-count mismatch or a non-finite weight. The
+ * host views may be released or changed afterwards without effect. */
+int phonon_flow_model_create(const PhononFlowLayerWeights *weights, size_t layers,
+                             PhononFlowModel **model);
+void phonon_flow_model_destroy(PhononFlowModel *model);
+size_t phonon_flow_model_layers(const PhononFlowModel *model);
+size_t phonon_flow_model_device_bytes(const PhononFlowModel *model);
+
+/* Pool of `blocks` KV blocks; a block holds K and V of 16 positions for all
+ * `layers` layers (64 KiB per layer, fp32). Blocks are handed out by id. */
+int phonon_kv_pool_create(size_t layers, size_t blocks, PhononKvPool **pool);
+void phonon_kv_pool_destroy(PhononKvPool *pool);
+size_t phonon_kv_pool_free_blocks(const PhononKvPool *pool);
+int phonon_kv_pool_alloc(PhononKvPool *pool, size_t count, int32_t *blocks);
+int phonon_kv_pool_release(PhononKvPool *pool, size_t count, const int32_t *blocks);
+/* Fills every block with deterministic N(0,1) values (synthetic contexts). */
+int phonon_kv_pool_fill_normal(PhononKvPool *pool, uint64_t seed);
+/* Copy positions [first, first+count) of all layers between the pool (through
+ * `table`, host array of block ids covering those positions) and host arrays
+ * in the reference layout keys[(layer*capacity + position)*512]. */
+int phonon_kv_pool_write(PhononKvPool *pool, const int32_t *table, size_t table_len,
+                         size_t first, size_t count, const float *keys, const float *values,
+                         size_t capacity);
+int phonon_kv_pool_read(const PhononKvPool *pool, const int32_t *table, size_t table_len,
+                        size_t first, size_t count, float *keys, float *values,
+                        size_t capacity);
+/* The pool's device description, for the kernels of phonon_gpu.h. */
+int phonon_kv_pool_view(const PhononKvPool *pool, pgpu_paged_kv *view);
+
+/* A batch of up to max_streams streams of at most max_positions positions
+ * (<= 8192) each, bound to a model and a pool with the model's layer count. */
+int phonon_flow_batch_create(const PhononFlowModel *model, PhononKvPool *pool,
+                             size_t max_streams, size_t max_positions, PhononFlowBatch **batch);
+void phonon_flow_batch_destroy(PhononFlowBatch *batch);
+/* Sets the active streams: positions[s] is the position stream s decodes
+ * next (= its committed length); tables[s*table_len + i] is the pool block
+ * of positions [16i, 16i+16), and must cover positions[s] + steps - 1 for
+ * every step run before the next call. */
+int phonon_flow_batch_set_streams(PhononFlowBatch *batch, size_t streams,
+                                  const size_t *positions, const int32_t *tables,
+                                  size_t table_len);
+/* One decode step of every active stream: inputs/outputs host [streams][512].
+ * Appends one K/V row per layer at each stream's position, then advances the
+ * positions. Returns 0 (positions still advanced, outputs unspecified) if
+ * any value is non-finite or a position is not covered by its table. */
+int phonon_flow_batch_step(PhononFlowBatch *batch, const float *inputs, float theta,
+                           float *outputs);
+/* The same step with device-resident inputs/outputs [streams][512] (dev),
+ * enqueued on the batch's stream without waiting. The step is captured into a
+ * HIP graph on first use and replayed afterwards. */
+int phonon_flow_batch_step_device(PhononFlowBatch *batch, const float *inputs, float theta,
+                                  float *outputs);
+/* Waits for enqueued steps; returns 1 iff no step since the last call saw a
+ * non-finite value or an uncovered position (and clears that record). */
+int phonon_flow_batch_sync(PhononFlowBatch *batch);
+/* Current positions (host mirror) of the active streams. */
+int phonon_flow_batch_positions(const PhononFlowBatch *batch, size_t *positions);
+/* The batch's HIP stream (for event timing by the caller). */
+void *phonon_flow_batch_stream(const PhononFlowBatch *batch);
+/* Device buffers of [max_streams][512] fp32 owned by the batch, convenient
+ * as step_device inputs/outputs. */
+float *phonon_flow_batch_device_inputs(PhononFlowBatch *batch);
+float *phonon_flow_batch_device_outputs(PhononFlowBatch *batch);
+
+/* Registers a device copy of weights[0..layers) for the single-stream
+ * functions of phonon_transformer.h: later calls with this same array (same
+ * view pointers) use it instead of uploading per call. Like the reference's
+ * prepared materializations, the registered weights must not change. */
+int phonon_flow_prepare_weights(const PhononFlowLayerWeights *weights, size_t layers);
+void phonon_flow_release_weights(const PhononFlowLayerWeights *weights);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

@@ -1,0 +1,123 @@
+/* Thin C-ABI layer between the C17 host code and the hand-written gfx950
+ * kernels of libphonon_mi355x. Plain pointers and sizes only. Device
+ * pointers are marked (dev); `stream` is a HIP stream handle (NULL = the
+ * null stream). Functions return 1 on success, 0 on failure, and kernels
+ * report non-finite results or invalid indexes by OR-ing a bit into a device
+ * status word: 1 = non-finite value, 2 = position/block outside its table.
+ *
+ * This layer has no counterpart in the reference (a CPU-only C17 program);
+ * it is what the drop-in functions of phonon_q8.h / phonon_transformer.h and
+ * the batched API of phonon_flow_batch.h are built on. */
+#ifndef PHONON_GPU_H
+#define PHONON_GPU_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* A projection matrix resident in device memory in MFMA fragment order.
+ * q8 = 1: `values` holds int8 (1 B/weight) and `scales` fp16 bits, one per
+ * 32-column block of a row; q8 = 0: `values` holds bf16 and scales is NULL.
+ * Fragment order: record (16-row tile t, 32-column block kb) at
+ * (t*columns/32 + kb); inside it lane l in 0..63 holds row 16t + l%16,
+ * columns 32kb + 8(l/16) .. +7. Scales: [t][kb][16 rows]. */
+typedef struct {
+    int q8;
+    size_t rows, columns;
+    const void *values;
+    const uint16_t *scales;
+} pgpu_matrix;
+
+/* Paged fp32 KV pool: per layer [block][head 8][K|V][16 positions][64]. */
+typedef struct {
+    float *base;          /* (dev) */
+    int layers;
+    size_t blocks;        /* blocks per layer */
+    size_t layer_stride;  /* floats per layer = blocks * 8 * 2 * 16 * 64 */
+} pgpu_paged_kv;
+
+/* Split-attention scratch: partial results and per-(stream, head) tickets.
+ * tickets must be zero before the first launch; kernels leave them zero. */
+typedef struct {
+    float *part_acc;      /* (dev) [max_streams*8*max_splits][64] */
+    float *part_ml;       /* (dev) [max_streams*8*max_splits][2] */
+    int *tickets;         /* (dev) [max_streams*8] */
+    int max_streams, max_splits;
+} pgpu_attention_scratch;
+
+/* -- device, memory, streams, events, graphs (pgpu_runtime.hip) -- */
+const char *pgpu_last_error(void);
+int pgpu_device_init(void);
+int pgpu_device_name(char *buffer, size_t size);
+void *pgpu_malloc(size_t bytes);
+void pgpu_free(void *ptr);
+int pgpu_memset(void *stream, void *dst, int value, size_t bytes);
+/* Host copies complete before returning. */
+int pgpu_copy_h2d(void *stream, void *dst, const void *src, size_t bytes);
+int pgpu_copy_d2h(void *stream, void *dst, const void *src, size_t bytes);
+int pgpu_copy_d2d(void *stream, void *dst, const void *src, size_t bytes);
+int pgpu_stream_create(void **stream);
+void pgpu_stream_destroy(void *stream);
+int pgpu_stream_sync(void *stream);
+int pgpu_event_create(void **event);
+void pgpu_event_destroy(void *event);
+int pgpu_event_record(void *event, void *stream);
+int pgpu_event_elapsed_ms(void *start, void *stop, float *ms);
+int pgpu_graph_begin(void *stream);
+int pgpu_graph_end(void *stream, void **exec);
+int pgpu_graph_launch(void *exec, void *stream);
+void pgpu_graph_destroy(void *exec);
+int pgpu_check_launch(void);
+
+/* -- projections (pgpu_gemm.hip); xs = split fragments of the input rows,
+ * streams rounded up to 16 in its allocation -- */
+int pgpu_gemm_store(void *stream, const pgpu_matrix *w, const uint16_t *xs, int streams,
+                    const float *bias, float *out, int ld_out, int *status);
+int pgpu_gemm_residual(void *stream, const pgpu_matrix *w, const uint16_t *xs, int streams,
+                       const float *residual, float *out, int *status);
+int pgpu_gemm_gelu_split(void *stream, const pgpu_matrix *w, const uint16_t *xs, int streams,
+                         uint16_t *out_split, int *status);
+/* Fused QKV projection: RoPE on q and k, q scaled by 1/8 into q_out
+ * [streams][512], k and v appended to the pool at (layer, positions[s]). */
+int pgpu_gemm_qkv(void *stream, const pgpu_matrix *w, const uint16_t *xs, int streams,
+                  const pgpu_paged_kv *kv, int layer, const int32_t *tables, int table_stride,
+                  const int32_t *positions, const float *rope, float *q_out, int *status);
+
+/* -- attention (pgpu_attention.hip): stream s attends positions[s]+1 keys;
+ * max_splits * 256 must cover every context. Output as split fragments
+ * and/or fp32 rows. -- */
+int pgpu_attention(void *stream, const float *q, const pgpu_paged_kv *kv, int layer,
+                   const int32_t *tables, int table_stride, const int32_t *positions,
+                   int streams, int heads, int max_splits, uint16_t *out_split, float *out,
+                   const pgpu_attention_scratch *scratch, int *status);
+
+/* -- rows and elements (pgpu_elementwise.hip) -- */
+int pgpu_ln_split(void *stream, const float *x, int streams, const float *w, const float *b,
+                  float eps, uint16_t *xs, float *y, int *status);
+int pgpu_split_rows(void *stream, const float *x, int streams, int k_cols, uint16_t *xs,
+                    int *status);
+int pgpu_norm_row(void *stream, const float *x, int width, const float *w, const float *b,
+                  float eps, int rms, float *y, int *status);
+int pgpu_gelu(void *stream, float *values, size_t count, int *status);
+int pgpu_rope(void *stream, float *values, int heads, int head_width, const float *cos_sin,
+              int *status);
+/* Copies positions [first_position, first_position+count) of layers
+ * [first_layer, first_layer+layers) between the pool (through `table`, dev)
+ * and contiguous rows (dev): `keys`/`values` point at the row of
+ * (first_layer, first_position); layer y, position x after them lies
+ * (y*capacity + x) rows further (the reference [layer][capacity][512] layout
+ * when capacity is the cache capacity). */
+int pgpu_kv_copy(void *stream, const pgpu_paged_kv *kv, const int32_t *table,
+                 int first_position, int count, int first_layer, int layers, float *keys,
+                 float *values, size_t capacity, int to_contiguous, int *status);
+int pgpu_fill_normal(void *stream, float *dst, size_t count, uint64_t seed);
+int pgpu_advance_positions(void *stream, int32_t *positions, int streams);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

@@ -1,0 +1,72 @@
+/* CPU restatement of the speech-mac Flow-transformer decode step.
+ *
+ * TEST INFRASTRUCTURE ONLY. This library is the checker for the MI355X
+ * product (libphonon_mi355x): only tests/, __graft_entry__.smoke() and the
+ * cpu_baseline leg of bench.py load it. The product never links, calls or
+ * falls back to it.
+ *
+ * Every function follows the arithmetic order of the reference C path
+ * (file:line cited per function) with two portable substitutions that the
+ * reference's own build cannot avoid off macOS:
+ *   - Accelerate cblas_sgemm -> a sequential fp32 dot product per output,
+ *     then alpha/beta as reference BLAS applies them;
+ *   - SLEEF expf4/sinf4/cosf4 -> the system libm expf/sinf/cosf.
+ * Pinning status per function is listed in oracle/README.md.
+ */
+#ifndef PHONON_ORACLE_H
+#define PHONON_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+typedef struct {
+    uint16_t scale_bits;
+    int8_t values[32];
+} OracleQ8Block;
+
+/* One Flow layer with linear weights already expanded to fp32 (row-major
+ * [rows][columns]) and norm vectors decoded to fp32. */
+typedef struct {
+    const float *qkv;     /* [1536][512] */
+    const float *out;     /* [512][512] */
+    const float *mlp_in;  /* [2048][512] */
+    const float *mlp_out; /* [512][2048] */
+    const float *norm1_weight, *norm1_bias, *norm2_weight, *norm2_bias; /* [512] each */
+} OracleLayer;
+
+float oracle_half_to_float(uint16_t bits);
+int oracle_bf16_to_float(const uint16_t *values, size_t count, float *output);
+int oracle_q8_dot(const OracleQ8Block *blocks, const float *input, size_t elements,
+                  float *result);
+int oracle_q8_matvec(const OracleQ8Block *weights, const float *input, size_t rows,
+                     size_t columns, float *output);
+int oracle_q8_expand(const OracleQ8Block *blocks, size_t rows, size_t columns, float *expanded);
+int oracle_linear_batch(const float *expanded, const float *input, size_t rows, size_t columns,
+                        const float *bias, float *output, size_t batch);
+int oracle_rms_norm(const float *input, const float *weight, size_t width, float epsilon,
+                    float *output);
+int oracle_layer_norm(const float *input, const float *weight, const float *bias, size_t width,
+                      float epsilon, float *output);
+int oracle_erf_gelu(float *values, size_t count);
+int oracle_rope_interleaved(float *values, size_t width, size_t heads, size_t position,
+                            float theta);
+int oracle_attention(const float query[64], const float *keys, const float *values, size_t count,
+                     size_t stride, float output[64]);
+/* Contiguous cache layout of the reference: keys[(layer*capacity+pos)*512 + c]. */
+int oracle_kv_append(float *keys, float *values, size_t layers, size_t capacity, size_t layer,
+                     size_t position, const float *key, const float *value);
+int oracle_layer_step(const OracleLayer *weights, float *keys, float *values, size_t layers,
+                      size_t capacity, size_t layer, size_t position, const float input[512],
+                      float theta, float output[512]);
+int oracle_stack_step(const OracleLayer *weights, size_t layers, float *keys, float *values,
+                      size_t capacity, size_t position, const float input[512], float theta,
+                      float output[512]);
+/* Runs independent streams' stack steps over `threads` pthreads (the CPU
+ * baseline for batched decode). Stream s uses keys/values + s*layers*capacity*512
+ * and positions[s]; inputs/outputs are [streams][512]. Returns 1 iff all succeed. */
+int oracle_stack_step_streams(const OracleLayer *weights, size_t layers, float *keys,
+                              float *values, size_t capacity, size_t streams,
+                              const size_t *positions, const float *inputs, float theta,
+                              float *outputs, size_t threads);
+
+#endif

@@ -1,0 +1,297 @@
+"""speech-mac Flow-transformer decode step on the MI355X.
+
+Python binding (ctypes) of libphonon_mi355x.so, the C-ABI library built from
+csrc/ (gfx950 HIP kernels) and host/ (C17 host layer). The numerical work
+always runs in that library on the GPU; this module only declares the C
+signatures and moves numpy arrays in and out. It never computes results
+itself and has no CPU fallback: loading fails loudly when the library is
+missing.
+
+The directory name is not an identifier, so import it by path::
+
+    spec = importlib.util.spec_from_file_location(
+        "speech_mac_amd", "speech-mac_amd/__init__.py",
+        submodule_search_locations=["speech-mac_amd"])
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "lib", "libphonon_mi355x.so")
+INCLUDE_DIR = os.path.join(os.path.dirname(HERE), "include")
+
+WIDTH, HEADS, HEAD_DIM, FFN = 512, 8, 64, 2048
+REFERENCE_LAYERS = 9
+BLOCK_POSITIONS = 16
+MAX_POSITIONS = 8192
+PACK_Q8_0, PACK_BF16 = 1, 2
+
+Q8_BLOCK = np.dtype([("scale_bits", "<u2"), ("values", "i1", (32,))], align=False)
+assert Q8_BLOCK.itemsize == 34
+
+
+def build(jobs: int = 8) -> None:
+    """Compile every HIP and C source of the library for gfx950 (always)."""
+    subprocess.run(["make", "-s", "-B", "-C", HERE, f"-j{jobs}"], check=True)
+
+
+# --------------------------------------------------------------------- C types
+_sz = ctypes.c_size_t
+_i = ctypes.c_int
+_vp = ctypes.c_void_p
+_f = ctypes.c_float
+_fp = ctypes.POINTER(ctypes.c_float)
+_i32p = ctypes.POINTER(ctypes.c_int32)
+_szp = ctypes.POINTER(ctypes.c_size_t)
+_u16p = ctypes.POINTER(ctypes.c_uint16)
+_ip = ctypes.POINTER(ctypes.c_int)
+
+
+class PhononTensorView(ctypes.Structure):
+    _fields_ = [("dtype", ctypes.c_int), ("rank", ctypes.c_uint),
+                ("shape", ctypes.c_uint64 * 8), ("data", _vp),
+                ("byte_count", _sz), ("linear_data", _vp)]
+
+
+class PhononFlowLayerWeights(ctypes.Structure):
+    _fields_ = [(n, ctypes.POINTER(PhononTensorView)) for n in (
+        "qkv", "attention_out", "mlp_in", "mlp_out",
+        "norm1_weight", "norm1_bias", "norm2_weight", "norm2_bias")]
+
+
+class PhononKvCache(ctypes.Structure):
+    _fields_ = [("capacity", _sz), ("length", _sz), ("keys", _fp), ("values", _fp)]
+
+
+class PgpuMatrix(ctypes.Structure):
+    _fields_ = [("q8", _i), ("rows", _sz), ("columns", _sz), ("values", _vp), ("scales", _vp)]
+
+
+class PgpuPagedKv(ctypes.Structure):
+    _fields_ = [("base", _vp), ("layers", _i), ("blocks", _sz), ("layer_stride", _sz)]
+
+
+class PgpuAttentionScratch(ctypes.Structure):
+    _fields_ = [("part_acc", _vp), ("part_ml", _vp), ("tickets", _vp),
+                ("max_streams", _i), ("max_splits", _i)]
+
+
+CANCEL_POLL = ctypes.CFUNCTYPE(ctypes.c_int, _vp)
+_wp = ctypes.POINTER(PhononFlowLayerWeights)
+_cachep = ctypes.POINTER(PhononKvCache)
+_viewp = ctypes.POINTER(PhononTensorView)
+_mp = ctypes.POINTER(PgpuMatrix)
+_kvp = ctypes.POINTER(PgpuPagedKv)
+_scp = ctypes.POINTER(PgpuAttentionScratch)
+_pp = ctypes.POINTER(_vp)
+
+# Every function declared in include/*.h: name -> (restype, argtypes).
+EXPORTS = {
+    # phonon_q8.h
+    "phonon_q8_dot": (_i, [_vp, _fp, _sz, _fp]),
+    "phonon_q8_matvec": (_i, [_vp, _fp, _sz, _sz, _fp]),
+    # phonon_q8_device.h
+    "phonon_q8_device_create": (_i, [_vp, _sz, _sz, _sz, _pp]),
+    "phonon_q8_device_destroy": (None, [_vp]),
+    "phonon_q8_device_matvec": (_i, [_vp, _sz, _vp, _vp, _sz, _vp]),
+    "phonon_q8_device_status": (_i, [_vp, _vp]),
+    "phonon_q8_device_bytes_per_call": (_sz, [_vp, _sz]),
+    # phonon_transformer.h
+    "phonon_kv_cache_init": (_i, [_cachep, _sz]),
+    "phonon_kv_cache_reset": (None, [_cachep]),
+    "phonon_kv_cache_destroy": (None, [_cachep]),
+    "phonon_kv_cache_append": (_i, [_cachep, _sz, _sz, _fp, _fp, _sz]),
+    "phonon_kv_cache_commit_position": (_i, [_cachep, _sz]),
+    "phonon_rms_norm": (_i, [_fp, _fp, _sz, _f, _fp]),
+    "phonon_layer_norm": (_i, [_fp, _fp, _fp, _sz, _f, _fp]),
+    "phonon_erf_gelu": (_i, [_fp, _sz]),
+    "phonon_rope_interleaved": (_i, [_fp, _sz, _sz, _sz, _f]),
+    "phonon_linear": (_i, [_viewp, _fp, _sz, _sz, _fp, _fp]),
+    "phonon_linear_batch": (_i, [_viewp, _fp, _sz, _sz, _fp, _fp, _sz]),
+    "phonon_flow_layer_step": (_i, [_wp, _cachep, _sz, _sz, _fp, _f, _fp]),
+    "phonon_flow_stack_step": (_i, [_wp, _cachep, _sz, _fp, _f, _fp]),
+    "phonon_flow_stack_step_cancel": (_i, [_wp, _cachep, _sz, _fp, _f, _fp, CANCEL_POLL, _vp]),
+    "phonon_flow_stack_prefill_cancel": (_i, [_wp, _cachep, _fp, _sz, _f, _fp, CANCEL_POLL,
+                                              _vp]),
+    "phonon_flow_stack_prefill": (_i, [_wp, _cachep, _fp, _sz, _f, _fp]),
+    "phonon_attention_test": (_i, [_fp, _fp, _fp, _sz, _sz, _fp]),
+    # phonon_flow_batch.h
+    "phonon_flow_model_create": (_i, [_wp, _sz, _pp]),
+    "phonon_flow_model_destroy": (None, [_vp]),
+    "phonon_flow_model_layers": (_sz, [_vp]),
+    "phonon_flow_model_device_bytes": (_sz, [_vp]),
+    "phonon_kv_pool_create": (_i, [_sz, _sz, _pp]),
+    "phonon_kv_pool_destroy": (None, [_vp]),
+    "phonon_kv_pool_free_blocks": (_sz, [_vp]),
+    "phonon_kv_pool_alloc": (_i, [_vp, _sz, _i32p]),
+    "phonon_kv_pool_release": (_i, [_vp, _sz, _i32p]),
+    "phonon_kv_pool_fill_normal": (_i, [_vp, ctypes.c_uint64]),
+    "phonon_kv_pool_write": (_i, [_vp, _i32p, _sz, _sz, _sz, _fp, _fp, _sz]),
+    "phonon_kv_pool_read": (_i, [_vp, _i32p, _sz, _sz, _sz, _fp, _fp, _sz]),
+    "phonon_kv_pool_view": (_i, [_vp, _kvp]),
+    "phonon_flow_batch_create": (_i, [_vp, _vp, _sz, _sz, _pp]),
+    "phonon_flow_batch_destroy": (None, [_vp]),
+    "phonon_flow_batch_set_streams": (_i, [_vp, _sz, _szp, _i32p, _sz]),
+    "phonon_flow_batch_step": (_i, [_vp, _fp, _f, _fp]),
+    "phonon_flow_batch_step_device": (_i, [_vp, _vp, _f, _vp]),
+    "phonon_flow_batch_sync": (_i, [_vp]),
+    "phonon_flow_batch_positions": (_i, [_vp, _szp]),
+    "phonon_flow_batch_stream": (_vp, [_vp]),
+    "phonon_flow_batch_device_inputs": (_vp, [_vp]),
+    "phonon_flow_batch_device_outputs": (_vp, [_vp]),
+    "phonon_flow_prepare_weights": (_i, [_wp, _sz]),
+    "phonon_flow_release_weights": (None, [_wp]),
+    # phonon_gpu.h
+    "pgpu_last_error": (ctypes.c_char_p, []),
+    "pgpu_device_init": (_i, []),
+    "pgpu_device_name": (_i, [ctypes.c_char_p, _sz]),
+    "pgpu_malloc": (_vp, [_sz]),
+    "pgpu_free": (None, [_vp]),
+    "pgpu_memset": (_i, [_vp, _vp, _i, _sz]),
+    "pgpu_copy_h2d": (_i, [_vp, _vp, _vp, _sz]),
+    "pgpu_copy_d2h": (_i, [_vp, _vp, _vp, _sz]),
+    "pgpu_copy_d2d": (_i, [_vp, _vp, _vp, _sz]),
+    "pgpu_stream_create": (_i, [_pp]),
+    "pgpu_stream_destroy": (None, [_vp]),
+    "pgpu_stream_sync": (_i, [_vp]),
+    "pgpu_event_create": (_i, [_pp]),
+    "pgpu_event_destroy": (None, [_vp]),
+    "pgpu_event_record": (_i, [_vp, _vp]),
+    "pgpu_event_elapsed_ms": (_i, [_vp, _vp, _fp]),
+    "pgpu_graph_begin": (_i, [_vp]),
+    "pgpu_graph_end": (_i, [_vp, _pp]),
+    "pgpu_graph_launch": (_i, [_vp, _vp]),
+    "pgpu_graph_destroy": (None, [_vp]),
+    "pgpu_check_launch": (_i, []),
+    "pgpu_gemm_store": (_i, [_vp, _mp, _vp, _i, _vp, _vp, _i, _vp]),
+    "pgpu_gemm_residual": (_i, [_vp, _mp, _vp, _i, _vp, _vp, _vp]),
+    "pgpu_gemm_gelu_split": (_i, [_vp, _mp, _vp, _i, _vp, _vp]),
+    "pgpu_gemm_qkv": (_i, [_vp, _mp, _vp, _i, _kvp, _i, _vp, _i, _vp, _vp, _vp, _vp]),
+    "pgpu_attention": (_i, [_vp, _vp, _kvp, _i, _vp, _i, _vp, _i, _i, _i, _vp, _vp, _scp,
+                            _vp]),
+    "pgpu_ln_split": (_i, [_vp, _vp, _i, _vp, _vp, _f, _vp, _vp, _vp]),
+    "pgpu_split_rows": (_i, [_vp, _vp, _i, _i, _vp, _vp]),
+    "pgpu_norm_row": (_i, [_vp, _vp, _i, _vp, _vp, _f, _i, _vp, _vp]),
+    "pgpu_gelu": (_i, [_vp, _vp, _sz, _vp]),
+    "pgpu_rope": (_i, [_vp, _vp, _i, _i, _vp, _vp]),
+    "pgpu_kv_copy": (_i, [_vp, _kvp, _vp, _i, _i, _i, _i, _vp, _vp, _sz, _i, _vp]),
+    "pgpu_fill_normal": (_i, [_vp, _vp, _sz, ctypes.c_uint64]),
+    "pgpu_advance_positions": (_i, [_vp, _vp, _i]),
+}
+
+_LIB = None
+
+
+def load(path: str = LIB_PATH) -> ctypes.CDLL:
+    """Load libphonon_mi355x.so and declare every exported signature.
+    Raises when the library is not built: there is no fallback."""
+    global _LIB
+    if _LIB is not None and path == LIB_PATH:
+        return _LIB
+    if not os.path.exists(path):
+        raise RuntimeError(f"{path} is missing: build it with __graft_entry__.build() "
+                           "(make -C speech-mac_amd)")
+    lib = ctypes.CDLL(path)
+    for name, (restype, argtypes) in EXPORTS.items():
+        fn = getattr(lib, name)
+        fn.restype = restype
+        fn.argtypes = argtypes
+    if path == LIB_PATH:
+        _LIB = lib
+    return lib
+
+
+def last_error(lib) -> str:
+    msg = lib.pgpu_last_error()
+    return msg.decode() if msg else ""
+
+
+def fptr(a: np.ndarray):
+    assert a.dtype == np.float32 and a.flags.c_contiguous
+    return a.ctypes.data_as(_fp)
+
+
+def vptr(a: np.ndarray):
+    return ctypes.c_void_p(a.ctypes.data)
+
+
+# ------------------------------------------------------------- host helpers
+class Views:
+    """Keeps numpy buffers and PhononTensorView structs alive together."""
+
+    def __init__(self):
+        self.keep = []
+
+    def q8(self, blocks: np.ndarray, rows: int, cols: int) -> PhononTensorView:
+        assert blocks.dtype == Q8_BLOCK and blocks.size == rows * cols // 32
+        blocks = np.ascontiguousarray(blocks)
+        self.keep.append(blocks)
+        v = PhononTensorView(PACK_Q8_0, 2, (ctypes.c_uint64 * 8)(rows, cols), blocks.ctypes.data,
+                             blocks.nbytes, None)
+        self.keep.append(v)
+        return v
+
+    def bf16(self, bits: np.ndarray, shape) -> PhononTensorView:
+        bits = np.ascontiguousarray(bits, np.uint16)
+        self.keep.append(bits)
+        v = PhononTensorView(PACK_BF16, len(shape), (ctypes.c_uint64 * 8)(*shape),
+                             bits.ctypes.data, bits.nbytes, None)
+        self.keep.append(v)
+        return v
+
+    def layers(self, layer_dicts) -> ctypes.Array:
+        """layer dicts (see synthetic.flow_layer) -> PhononFlowLayerWeights[L]."""
+        arr = (PhononFlowLayerWeights * len(layer_dicts))()
+        for i, d in enumerate(layer_dicts):
+            def mat(key, rows, cols):
+                if d[key].dtype == Q8_BLOCK:
+                    return self.q8(d[key], rows, cols)
+                return self.bf16(d[key], (rows, cols))
+            views = [mat("qkv", 3 * WIDTH, WIDTH), mat("out", WIDTH, WIDTH),
+                     mat("mlp_in", FFN, WIDTH), mat("mlp_out", WIDTH, FFN)]
+            views += [self.bf16(d[k], (WIDTH,)) for k in
+                      ("norm1_weight", "norm1_bias", "norm2_weight", "norm2_bias")]
+            arr[i] = PhononFlowLayerWeights(*[ctypes.pointer(v) for v in views])
+        self.keep.append(arr)
+        return arr
+
+
+class DeviceBuffer:
+    """Device allocation through the library's pgpu_malloc (no torch)."""
+
+    def __init__(self, lib, nbytes: int):
+        self.lib = lib
+        self.nbytes = int(nbytes)
+        self.ptr = lib.pgpu_malloc(self.nbytes)
+        if not self.ptr:
+            raise MemoryError(f"pgpu_malloc({nbytes}): {last_error(lib)}")
+
+    def upload(self, a: np.ndarray, stream=None):
+        a = np.ascontiguousarray(a)
+        assert a.nbytes <= self.nbytes
+        if not self.lib.pgpu_copy_h2d(stream, self.ptr, a.ctypes.data, a.nbytes):
+            raise RuntimeError(last_error(self.lib))
+
+    def download(self, shape, dtype=np.float32, stream=None) -> np.ndarray:
+        out = np.empty(shape, dtype)
+        assert out.nbytes <= self.nbytes
+        if not self.lib.pgpu_copy_d2h(stream, out.ctypes.data, self.ptr, out.nbytes):
+            raise RuntimeError(last_error(self.lib))
+        return out
+
+    def free(self):
+        if self.ptr:
+            self.lib.pgpu_stream_sync(None)
+            self.lib.pgpu_free(self.ptr)
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass

@@ -1,0 +1,239 @@
+// Single-query causal attention over a paged fp32 KV pool, split over keys.
+//
+// Replaces flow_attention (src/phonon_transformer.c:338-404), called per head
+// by phonon_flow_layer_step (src/phonon_transformer.c:429-435). Softmax is
+// online: the reference uses 512-key blocks, this kernel 64-key wave blocks
+// merged in fixed order; results agree to fp32 rounding (tolerance-checked).
+//
+// Pool layout, per layer: [block][head][K|V][16 positions][64] fp32, so one
+// (block, head) tile of keys is 4 KB contiguous and its values follow it.
+// Work-group (split j, head h, stream s) covers keys [256j, 256j+256) of
+// stream s: wave w takes blocks 16j+4w .. 16j+4w+3. Each lane loads float4s
+// at tile offsets 256*i + 4*lane (i = 0..3), i.e. key 4i + lane/16, dims
+// 4*(lane%16) .. +3: every load instruction reads 1 KB contiguous.
+// Scores reduce over the 16 lanes of a key (DPP row reductions).
+// Splits of one (s, h) are merged by the last work-group to finish (atomic
+// ticket), which also resets the ticket so the kernel can be replayed.
+#include "pgpu_common.hpp"
+#include "phonon_gpu.h"
+
+namespace pgpu {
+
+struct AttnArgs {
+    const float *q;           // [streams][512], RoPE'd, scaled by 1/8
+    const float *kv;
+    size_t layer_stride;
+    unsigned blocks;          // blocks per layer; table entries must be below
+    int layer;
+    const int32_t *tables;
+    int table_stride;
+    const int32_t *positions; // keys attended = positions[s] + 1
+    int streams, max_splits;
+    uint16_t *out_split;      // optional: split fragments, 16 blocks per row
+    float *out;               // optional: [streams][512]
+    float *part_acc;          // [streams*8*max_splits][64]
+    float *part_ml;           // [streams*8*max_splits][2]
+    int *tickets;             // [streams*8], zero between launches
+    int *status;
+};
+
+__device__ inline float row16_sum(float v) {
+    v += __shfl_xor(v, 1);
+    v += __shfl_xor(v, 2);
+    v += __shfl_xor(v, 4);
+    v += __shfl_xor(v, 8);
+    return v;
+}
+
+__global__ __launch_bounds__(256) void k_attention(AttnArgs a) {
+    const int split = blockIdx.x, head = blockIdx.y, s = blockIdx.z;
+    const int count = a.positions[s] + 1;
+    const int nsplit = (count + kSplitKeys - 1) / kSplitKeys;
+    // A context the grid or the block table cannot cover is an error, never
+    // a partial read: flag it once and let every work-group exit.
+    if (count < 1 || nsplit > a.max_splits || count > a.table_stride * kBlockPos) {
+        if (split == 0 && threadIdx.x == 0) atomicOr(a.status, 2);
+        return;
+    }
+    if (split * kSplitKeys >= count) return;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int krow = lane >> 4, dcol = lane & 15;
+
+    const float4 q = *(const float4 *)(a.q + (size_t)s * kWidth + head * kHeadDim + dcol * 4);
+    const int32_t *table = a.tables + (size_t)s * a.table_stride;
+    const float *layer_kv = a.kv + (size_t)a.layer * a.layer_stride;
+    const int first_block = split * 16 + wave * 4;
+
+    float4 kr[4][4], vr[4][4];
+    bool bad_block = false;
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+        const int b = first_block + t;
+        const bool valid = b * kBlockPos < count && (unsigned)table[b] < a.blocks;
+        bad_block |= b * kBlockPos < count && !valid;
+        if (valid) {
+            const float *tile =
+                layer_kv + ((size_t)table[b] * kHeads + head) * 2048 + lane * 4;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                kr[t][i] = *(const float4 *)(tile + i * 256);
+                vr[t][i] = *(const float4 *)(tile + 1024 + i * 256);
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                kr[t][i] = make_float4(0.f, 0.f, 0.f, 0.f);
+                vr[t][i] = make_float4(0.f, 0.f, 0.f, 0.f);
+            }
+        }
+    }
+    if (bad_block && lane == 0) atomicOr(a.status, 2);
+
+    float score[4][4];
+    float m = -INFINITY;
+#pragma unroll
+    for (int t = 0; t < 4; t++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const float4 k = kr[t][i];
+            float d = q.x * k.x;
+            d = fmaf(q.y, k.y, d);
+            d = fmaf(q.z, k.z, d);
+            d = fmaf(q.w, k.w, d);
+            d = row16_sum(d);
+            const int key = (first_block + t) * kBlockPos + i * 4 + krow;
+            score[t][i] = key < count ? d : -INFINITY;
+            m = fmaxf(m, score[t][i]);
+        }
+    m = fmaxf(m, __shfl_xor(m, 16));
+    m = fmaxf(m, __shfl_xor(m, 32));
+
+    float l = 0.0f;
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int t = 0; t < 4; t++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const float p = score[t][i] == -INFINITY ? 0.0f : expf(score[t][i] - m);
+            l += p;
+            acc.x = fmaf(p, vr[t][i].x, acc.x);
+            acc.y = fmaf(p, vr[t][i].y, acc.y);
+            acc.z = fmaf(p, vr[t][i].z, acc.z);
+            acc.w = fmaf(p, vr[t][i].w, acc.w);
+        }
+    // Lanes of one key row hold the same l; sum the four rows.
+    l += __shfl_xor(l, 16);
+    l += __shfl_xor(l, 32);
+    acc.x += __shfl_xor(acc.x, 16);
+    acc.y += __shfl_xor(acc.y, 16);
+    acc.z += __shfl_xor(acc.z, 16);
+    acc.w += __shfl_xor(acc.w, 16);
+    acc.x += __shfl_xor(acc.x, 32);
+    acc.y += __shfl_xor(acc.y, 32);
+    acc.z += __shfl_xor(acc.z, 32);
+    acc.w += __shfl_xor(acc.w, 32);
+
+    __shared__ float4 wave_acc[4][16];
+    __shared__ float wave_m[4], wave_l[4];
+    if (lane < 16) wave_acc[wave][lane] = acc;
+    if (lane == 0) {
+        wave_m[wave] = m;
+        wave_l[wave] = l;
+    }
+    __syncthreads();
+    if (wave != 0 || lane >= 16) return;  // no barrier follows
+
+    // Merge the four waves (fixed order). A wave without keys has l = 0.
+    float mm = wave_m[0];
+#pragma unroll
+    for (int w = 1; w < 4; w++) mm = fmaxf(mm, wave_m[w]);
+    float ll = 0.0f;
+    float4 aa = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int w = 0; w < 4; w++) {
+        if (wave_l[w] == 0.0f) continue;
+        const float f = expf(wave_m[w] - mm);
+        ll = fmaf(wave_l[w], f, ll);
+        const float4 x = wave_acc[w][lane];
+        aa.x = fmaf(x.x, f, aa.x);
+        aa.y = fmaf(x.y, f, aa.y);
+        aa.z = fmaf(x.z, f, aa.z);
+        aa.w = fmaf(x.w, f, aa.w);
+    }
+
+    const int sh = s * kHeads + head;
+    if (nsplit > 1) {
+        const size_t slot = (size_t)sh * a.max_splits + split;
+        *(float4 *)(a.part_acc + slot * 64 + lane * 4) = aa;
+        if (lane == 0) {
+            a.part_ml[slot * 2] = mm;
+            a.part_ml[slot * 2 + 1] = ll;
+        }
+        __threadfence();
+        int ticket = 0;
+        if (lane == 0) ticket = atomicAdd(&a.tickets[sh], 1);
+        ticket = __shfl(ticket, 0);
+        if (ticket != nsplit - 1) return;
+        __threadfence();
+        // Last split: merge all splits of (s, head) in split order.
+        const size_t first = (size_t)sh * a.max_splits;
+        mm = -INFINITY;
+        for (int j = 0; j < nsplit; j++) mm = fmaxf(mm, a.part_ml[(first + j) * 2]);
+        ll = 0.0f;
+        aa = make_float4(0.f, 0.f, 0.f, 0.f);
+        for (int j = 0; j < nsplit; j++) {
+            const float f = expf(a.part_ml[(first + j) * 2] - mm);
+            ll = fmaf(a.part_ml[(first + j) * 2 + 1], f, ll);
+            const float4 x = *(const float4 *)(a.part_acc + (first + j) * 64 + lane * 4);
+            aa.x = fmaf(x.x, f, aa.x);
+            aa.y = fmaf(x.y, f, aa.y);
+            aa.z = fmaf(x.z, f, aa.z);
+            aa.w = fmaf(x.w, f, aa.w);
+        }
+        if (lane == 0) atomicExch(&a.tickets[sh], 0);
+    }
+
+    const float inv = 1.0f / ll;
+    float o[4] = {aa.x * inv, aa.y * inv, aa.z * inv, aa.w * inv};
+    bool bad = !(ll > 0.0f) || !isfinite(ll);
+#pragma unroll
+    for (int r = 0; r < 4; r++) bad |= !isfinite(o[r]);
+    const int col = head * kHeadDim + lane * 4;
+    if (a.out) *(float4 *)(a.out + (size_t)s * kWidth + col) = make_float4(o[0], o[1], o[2], o[3]);
+    if (a.out_split) store_split<4>(a.out_split, s, col, kWidth / 32, o);
+    if (bad) atomicOr(a.status, 1);
+}
+
+}  // namespace pgpu
+
+using namespace pgpu;
+
+extern "C" int pgpu_attention(void *stream, const float *q, const pgpu_paged_kv *kv, int layer,
+                              const int32_t *tables, int table_stride, const int32_t *positions,
+                              int streams, int heads, int max_splits, uint16_t *out_split,
+                              float *out, const pgpu_attention_scratch *scratch, int *status) {
+    if (streams <= 0 || heads <= 0 || heads > kHeads || max_splits <= 0 || layer < 0 ||
+        layer >= kv->layers || max_splits > scratch->max_splits ||
+        streams > scratch->max_streams)
+        return 0;
+    AttnArgs a;
+    a.q = q;
+    a.kv = kv->base;
+    a.layer_stride = kv->layer_stride;
+    a.blocks = (unsigned)kv->blocks;
+    a.layer = layer;
+    a.tables = tables;
+    a.table_stride = table_stride;
+    a.positions = positions;
+    a.streams = streams;
+    a.max_splits = max_splits;
+    a.out_split = out_split;
+    a.out = out;
+    a.part_acc = scratch->part_acc;
+    a.part_ml = scratch->part_ml;
+    a.tickets = scratch->tickets;
+    a.status = status;
+    hipLaunchKernelGGL(k_attention, dim3(max_splits, heads, streams), dim3(256), 0,
+                       (hipStream_t)stream, a);
+    return hipGetLastError() == hipSuccess;
+}

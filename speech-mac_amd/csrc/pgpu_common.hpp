@@ -1,0 +1,118 @@
+// Shared device helpers for the gfx950 decode-step kernels.
+//
+// Activation operands of the projections are kept in "split fragment" form:
+// every fp32 activation x is written as three bf16 terms hi + mid + lo that
+// sum to x exactly (truncation split: hi keeps the top 8 significand bits,
+// mid the next 8, lo the remaining <= 8), laid out in the operand order of
+// v_mfma_f32_16x16x32_bf16 so that one lane's B operand is 16 contiguous
+// bytes. With int8 (or bf16) weights every MFMA product is exact in fp32, so
+// three bf16 MFMAs reproduce an fp32 dot product to fp32 accumulation error.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace pgpu {
+
+constexpr int kWidth = 512;      // model width D
+constexpr int kHeads = 8;        // attention heads
+constexpr int kHeadDim = 64;     // head width
+constexpr int kFfn = 2048;       // MLP width
+constexpr int kBlockPos = 16;    // positions per KV block
+constexpr int kSplitKeys = 256;  // keys per attention work-group (16 blocks)
+constexpr int kMaxPositions = 8192;
+
+typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
+typedef __attribute__((ext_vector_type(4))) float f32x4;
+
+// Index (in bf16 elements) of activation x[s][k], part p (0 hi, 1 mid, 2 lo),
+// inside a split-fragment buffer whose rows have kb_count 32-wide blocks.
+// Record (stream tile st, block kb, part p) holds 64 lanes x 8 bf16; lane
+// g*16 + n carries stream st*16+n, columns kb*32 + g*8 .. +7.
+__host__ __device__ inline size_t split_index(int s, int k, int p, int kb_count) {
+    const int st = s >> 4, n = s & 15, kb = k >> 5, g = (k >> 3) & 3, j = k & 7;
+    return ((size_t)(st * kb_count + kb) * 3 + p) * 512 + (size_t)(g * 16 + n) * 8 + j;
+}
+
+__device__ inline uint32_t fbits(float x) { return __float_as_uint(x); }
+__device__ inline float bitsf(uint32_t u) { return __uint_as_float(u); }
+
+// Exact three-term truncation split; returns the bf16 bit patterns.
+__device__ inline void split3(float x, uint16_t &hi, uint16_t &mid, uint16_t &lo) {
+    const uint32_t h = fbits(x) & 0xffff0000u;
+    const float r1 = __fsub_rn(x, bitsf(h));
+    const uint32_t m = fbits(r1) & 0xffff0000u;
+    const float r2 = __fsub_rn(r1, bitsf(m));
+    hi = (uint16_t)(h >> 16);
+    mid = (uint16_t)(m >> 16);
+    lo = (uint16_t)(fbits(r2) >> 16);
+}
+
+// Writes n (n = 4 or 8) consecutive activations of one stream starting at a
+// column k that is a multiple of n, as three contiguous n*2-byte stores.
+template <int N>
+__device__ inline void store_split(uint16_t *__restrict__ xs, int s, int k, int kb_count,
+                                   const float *v) {
+    uint16_t h[N], m[N], l[N];
+#pragma unroll
+    for (int i = 0; i < N; i++) split3(v[i], h[i], m[i], l[i]);
+    const size_t base = split_index(s, k, 0, kb_count);
+    if constexpr (N == 8) {
+        uint4 a, b, c;
+        a.x = h[0] | (uint32_t)h[1] << 16; a.y = h[2] | (uint32_t)h[3] << 16;
+        a.z = h[4] | (uint32_t)h[5] << 16; a.w = h[6] | (uint32_t)h[7] << 16;
+        b.x = m[0] | (uint32_t)m[1] << 16; b.y = m[2] | (uint32_t)m[3] << 16;
+        b.z = m[4] | (uint32_t)m[5] << 16; b.w = m[6] | (uint32_t)m[7] << 16;
+        c.x = l[0] | (uint32_t)l[1] << 16; c.y = l[2] | (uint32_t)l[3] << 16;
+        c.z = l[4] | (uint32_t)l[5] << 16; c.w = l[6] | (uint32_t)l[7] << 16;
+        *(uint4 *)(xs + base) = a;
+        *(uint4 *)(xs + base + 512) = b;
+        *(uint4 *)(xs + base + 1024) = c;
+    } else {
+        static_assert(N == 4, "4 or 8 columns");
+        uint2 a, b, c;
+        a.x = h[0] | (uint32_t)h[1] << 16; a.y = h[2] | (uint32_t)h[3] << 16;
+        b.x = m[0] | (uint32_t)m[1] << 16; b.y = m[2] | (uint32_t)m[3] << 16;
+        c.x = l[0] | (uint32_t)l[1] << 16; c.y = l[2] | (uint32_t)l[3] << 16;
+        *(uint2 *)(xs + base) = a;
+        *(uint2 *)(xs + base + 512) = b;
+        *(uint2 *)(xs + base + 1024) = c;
+    }
+}
+
+__device__ inline float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+}
+
+__device__ inline float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+    return v;
+}
+
+// Records a non-finite result: one atomic per wave at most.
+__device__ inline void flag_nonfinite(int *status, bool bad) {
+    if (__any(bad) && (threadIdx.x & 63) == 0) atomicOr(status, 1);
+}
+
+// A&S 7.1.26 erf with the fmaf chain of the reference's Torch-NEON
+// adaptation (src/phonon_transformer.c:190-200); exp from the device libm.
+__device__ inline float erf_as7126(float x) {
+    const float t = 1.0f / fmaf(0.3275911f, fabsf(x), 1.0f);
+    float r = fmaf(1.061405429f, t, -1.453152027f);
+    r = fmaf(r, t, 1.421413741f);
+    r = fmaf(r, t, -0.284496736f);
+    r = fmaf(r, t, 0.254829592f);
+    const float neg_exp = -expf(-__fmul_rn(x, x));
+    return copysignf(fmaf(__fmul_rn(t, neg_exp), r, 1.0f), x);
+}
+
+// 0.5*x*(1+erf(x/sqrt2)), unfused as in src/phonon_transformer.c:208-211.
+__device__ inline float gelu_erf(float x) {
+    const float e = erf_as7126(__fmul_rn(x, 0.7071067811865475244f));
+    return __fmul_rn(__fmul_rn(0.5f, x), __fadd_rn(1.0f, e));
+}
+
+}  // namespace pgpu

@@ -1,0 +1,69 @@
+/* Internal interfaces of the C17 host layer of libphonon_mi355x. */
+#ifndef PH_INTERNAL_H
+#define PH_INTERNAL_H
+
+#include "phonon_flow_batch.h"
+#include "phonon_gpu.h"
+#include "phonon_q8.h"
+#include "phonon_transformer.h"
+
+#include <stddef.h>
+#include <stdint.h>
+
+enum { PH_WIDTH = 512, PH_HEADS = 8, PH_HEAD = 64, PH_FFN = 2048, PH_SPLIT_KEYS = 256 };
+
+/* Device selection and the library's own HIP stream (created once). */
+int ph_init(void);
+void *ph_stream(void);
+/* Serializes the single-stream API (shared scratch and stream). */
+void ph_lock(void);
+void ph_unlock(void);
+
+/* Grow-only device scratch owned by the library, for the primitives. */
+void *ph_scratch(int slot, size_t bytes);
+
+/* IEEE binary16 -> binary32 (exact) and its finiteness. */
+float ph_half_to_float(uint16_t bits);
+int ph_half_finite(uint16_t bits);
+int ph_bf16_finite(uint16_t bits);
+float ph_bf16_to_float(uint16_t bits);
+
+/* Repack a [rows][columns] Q8_0 or BF16 view into MFMA fragment order and
+ * upload it, padding rows to 16 and columns to 32 with zeros. `*device`
+ * receives the single allocation backing `out` (free with pgpu_free). */
+int ph_matrix_upload(const PhononTensorView *view, size_t rows, size_t columns,
+                     pgpu_matrix *out, void **device);
+/* Decode a BF16 [count] view into `host` (fails on non-finite values). */
+int ph_vector_decode(const PhononTensorView *view, size_t count, float *host);
+
+/* (cos, sin) of pair i at `position` for a 64-wide head: fp32 inverse
+ * frequency 1/powf(theta, 2i/64) and fp32 phase, as
+ * src/phonon_transformer.c:228-233 computes them. */
+void ph_rope_row(float theta, size_t position, size_t head_width, float *cos_sin);
+/* Device table [8192][32] of (cos, sin) for theta (cached per theta). */
+const float *ph_rope_table(float theta);
+
+int ph_all_finite(const float *values, size_t count);
+int ph_overlap(const void *a, size_t a_bytes, const void *b, size_t b_bytes);
+
+/* Enqueue layers [first, first+count) of the step for the batch's active
+ * streams, reading the residual stream from `input` and leaving it in
+ * `output` (both dev [streams][512]); pool layer = model layer + pool_offset. */
+int ph_batch_enqueue_layers(PhononFlowBatch *batch, size_t first, size_t count,
+                            size_t pool_offset, const float *input, float *output,
+                            float theta);
+int ph_batch_set_single(PhononFlowBatch *batch, size_t position, const int32_t *table_dev);
+int ph_batch_bind_model(PhononFlowBatch *batch, const PhononFlowModel *model);
+float *ph_batch_in(PhononFlowBatch *batch);
+float *ph_batch_out(PhononFlowBatch *batch);
+size_t ph_batch_table_len(const PhononFlowBatch *batch);
+int ph_batch_status(PhononFlowBatch *batch);
+const int32_t *ph_batch_tables(const PhononFlowBatch *batch);
+float *ph_batch_scratch_rows(PhononFlowBatch *batch);
+void *ph_batch_stream(const PhononFlowBatch *batch);
+const pgpu_paged_kv *ph_pool_kv(const PhononKvPool *pool);
+int *ph_batch_status_word(PhononFlowBatch *batch);
+const PhononFlowModel *ph_registered_model(const PhononFlowLayerWeights *weights,
+                                           size_t layers);
+
+#endif

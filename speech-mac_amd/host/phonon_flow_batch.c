@@ -1,0 +1,586 @@
+/* Batched Flow decode step over a paged KV pool (phonon_flow_batch.h).
+ *
+ * One step of B streams runs, per layer (src/phonon_transformer.c:406-453):
+ *   LN1 -> split fragments            pgpu_ln_split
+ *   QKV projection + RoPE + append    pgpu_gemm_qkv
+ *   attention over the pool           pgpu_attention   (-> split fragments)
+ *   out projection + residual         pgpu_gemm_residual
+ *   LN2 -> split fragments            pgpu_ln_split
+ *   MLP in projection + GELU          pgpu_gemm_gelu_split
+ *   MLP out projection + residual     pgpu_gemm_residual
+ * then advances every stream's position on the device. */
+#include "ph_internal.h"
+
+#include <math.h>
+#include <pthread.h>
+#include <stdlib.h>
+#include <string.h>
+
+struct PhononFlowModel {
+    size_t layers;
+    pgpu_matrix *qkv, *out, *mlp_in, *mlp_out;
+    float *norms; /* dev [layers][4][512]: norm1 w, b, norm2 w, b */
+    void **allocations;
+    size_t allocation_count, device_bytes;
+};
+
+struct PhononKvPool {
+    pgpu_paged_kv kv;
+    int32_t *free_ids;
+    size_t free_count;
+    unsigned char *in_use;
+};
+
+struct PhononFlowBatch {
+    const PhononFlowModel *model;
+    PhononKvPool *pool;
+    size_t max_streams, padded_streams, max_positions, table_len, max_splits, streams;
+    void *stream;
+    float *x, *r, *q, *in, *out, *rows;
+    uint16_t *xs, *xh;
+    int32_t *positions, *tables;
+    int *status;
+    pgpu_attention_scratch scratch;
+    size_t *host_positions;
+    void *graph;
+    size_t graph_streams;
+    float graph_theta;
+    const float *graph_input;
+    float *graph_output;
+};
+
+/* ---------------------------------------------------------------- model -- */
+
+void phonon_flow_model_destroy(PhononFlowModel *model) {
+    if (!model)
+        return;
+    if (model->allocation_count)
+        (void)pgpu_stream_sync(ph_stream());
+    for (size_t i = 0; i < model->allocation_count; i++)
+        pgpu_free(model->allocations[i]);
+    free(model->allocations);
+    free(model->qkv);
+    free(model->out);
+    free(model->mlp_in);
+    free(model->mlp_out);
+    free(model);
+}
+
+int phonon_flow_model_create(const PhononFlowLayerWeights *weights, size_t layers,
+                             PhononFlowModel **model) {
+    if (!model)
+        return 0;
+    *model = NULL;
+    if (!weights || !layers || layers > 64 || !ph_init())
+        return 0;
+    PhononFlowModel *m = calloc(1, sizeof(*m));
+    if (!m)
+        return 0;
+    m->layers = layers;
+    m->qkv = calloc(layers, sizeof(pgpu_matrix));
+    m->out = calloc(layers, sizeof(pgpu_matrix));
+    m->mlp_in = calloc(layers, sizeof(pgpu_matrix));
+    m->mlp_out = calloc(layers, sizeof(pgpu_matrix));
+    m->allocations = calloc(layers * 4 + 1, sizeof(void *));
+    float *norms = malloc(layers * 4 * PH_WIDTH * sizeof(float));
+    int ok = m->qkv && m->out && m->mlp_in && m->mlp_out && m->allocations && norms;
+    for (size_t l = 0; ok && l < layers; l++) {
+        const PhononFlowLayerWeights *w = &weights[l];
+        struct {
+            const PhononTensorView *view;
+            size_t rows, columns;
+            pgpu_matrix *dst;
+        } mats[4] = {{w->qkv, 3 * PH_WIDTH, PH_WIDTH, &m->qkv[l]},
+                     {w->attention_out, PH_WIDTH, PH_WIDTH, &m->out[l]},
+                     {w->mlp_in, PH_FFN, PH_WIDTH, &m->mlp_in[l]},
+                     {w->mlp_out, PH_WIDTH, PH_FFN, &m->mlp_out[l]}};
+        for (int i = 0; ok && i < 4; i++) {
+            void *dev = NULL;
+            ok = ph_matrix_upload(mats[i].view, mats[i].rows, mats[i].columns, mats[i].dst, &dev);
+            if (ok) {
+                m->allocations[m->allocation_count++] = dev;
+                m->device_bytes += mats[i].dst->rows * mats[i].dst->columns *
+                                   (mats[i].dst->q8 ? 1 : 2) +
+                                   (mats[i].dst->q8 ? mats[i].dst->rows * mats[i].dst->columns / 16 : 0);
+            }
+        }
+        float *n = norms + l * 4 * PH_WIDTH;
+        ok = ok && ph_vector_decode(w->norm1_weight, PH_WIDTH, n) &&
+             ph_vector_decode(w->norm1_bias, PH_WIDTH, n + PH_WIDTH) &&
+             ph_vector_decode(w->norm2_weight, PH_WIDTH, n + 2 * PH_WIDTH) &&
+             ph_vector_decode(w->norm2_bias, PH_WIDTH, n + 3 * PH_WIDTH);
+    }
+    if (ok) {
+        m->norms = pgpu_malloc(layers * 4 * PH_WIDTH * sizeof(float));
+        ok = m->norms != NULL;
+        if (ok) {
+            m->allocations[m->allocation_count++] = m->norms;
+            ok = pgpu_copy_h2d(ph_stream(), m->norms, norms, layers * 4 * PH_WIDTH * sizeof(float));
+        }
+    }
+    free(norms);
+    if (!ok) {
+        phonon_flow_model_destroy(m);
+        return 0;
+    }
+    *model = m;
+    return 1;
+}
+
+size_t phonon_flow_model_layers(const PhononFlowModel *model) {
+    return model ? model->layers : 0;
+}
+
+size_t phonon_flow_model_device_bytes(const PhononFlowModel *model) {
+    return model ? model->device_bytes : 0;
+}
+
+/* ----------------------------------------------------------------- pool -- */
+
+int phonon_kv_pool_create(size_t layers, size_t blocks, PhononKvPool **pool) {
+    if (!pool)
+        return 0;
+    *pool = NULL;
+    const size_t block_floats = (size_t)PH_HEADS * 2 * 16 * PH_HEAD;
+    if (!layers || layers > 64 || !blocks || blocks > INT32_MAX ||
+        blocks > SIZE_MAX / (layers * block_floats * sizeof(float)) || !ph_init())
+        return 0;
+    PhononKvPool *p = calloc(1, sizeof(*p));
+    if (!p)
+        return 0;
+    p->kv.layers = (int)layers;
+    p->kv.blocks = blocks;
+    p->kv.layer_stride = blocks * block_floats;
+    p->kv.base = pgpu_malloc(layers * p->kv.layer_stride * sizeof(float));
+    p->free_ids = malloc(blocks * sizeof(int32_t));
+    p->in_use = calloc(blocks, 1);
+    if (!p->kv.base || !p->free_ids || !p->in_use) {
+        phonon_kv_pool_destroy(p);
+        return 0;
+    }
+    /* Hand out low ids first. */
+    for (size_t i = 0; i < blocks; i++)
+        p->free_ids[i] = (int32_t)(blocks - 1 - i);
+    p->free_count = blocks;
+    *pool = p;
+    return 1;
+}
+
+void phonon_kv_pool_destroy(PhononKvPool *pool) {
+    if (!pool)
+        return;
+    if (pool->kv.base) {
+        (void)pgpu_stream_sync(ph_stream());
+        pgpu_free(pool->kv.base);
+    }
+    free(pool->free_ids);
+    free(pool->in_use);
+    free(pool);
+}
+
+size_t phonon_kv_pool_free_blocks(const PhononKvPool *pool) {
+    return pool ? pool->free_count : 0;
+}
+
+int phonon_kv_pool_alloc(PhononKvPool *pool, size_t count, int32_t *blocks) {
+    if (!pool || (count && !blocks) || count > pool->free_count)
+        return 0;
+    for (size_t i = 0; i < count; i++) {
+        blocks[i] = pool->free_ids[--pool->free_count];
+        pool->in_use[blocks[i]] = 1;
+    }
+    return 1;
+}
+
+int phonon_kv_pool_release(PhononKvPool *pool, size_t count, const int32_t *blocks) {
+    if (!pool || (count && !blocks))
+        return 0;
+    for (size_t i = 0; i < count; i++)
+        if (blocks[i] < 0 || (size_t)blocks[i] >= pool->kv.blocks || !pool->in_use[blocks[i]])
+            return 0;
+    for (size_t i = 0; i < count; i++) {
+        pool->in_use[blocks[i]] = 0;
+        pool->free_ids[pool->free_count++] = blocks[i];
+    }
+    return 1;
+}
+
+int phonon_kv_pool_fill_normal(PhononKvPool *pool, uint64_t seed) {
+    if (!pool)
+        return 0;
+    return pgpu_fill_normal(ph_stream(), pool->kv.base, pool->kv.layers * pool->kv.layer_stride,
+                            seed) &&
+           pgpu_stream_sync(ph_stream());
+}
+
+const pgpu_paged_kv *ph_pool_kv(const PhononKvPool *pool) { return &pool->kv; }
+
+int phonon_kv_pool_view(const PhononKvPool *pool, pgpu_paged_kv *view) {
+    if (!pool || !view)
+        return 0;
+    *view = pool->kv;
+    return 1;
+}
+
+static int pool_copy(const PhononKvPool *pool, const int32_t *table, size_t table_len,
+                     size_t first, size_t count, float *keys, float *values, size_t capacity,
+                     int to_host) {
+    if (!pool || !table || !keys || !values || !count || first + count > capacity ||
+        first + count > table_len * 16 || capacity > PHONON_FLOW_MAX_POSITIONS)
+        return 0;
+    for (size_t i = first / 16; i < (first + count + 15) / 16; i++)
+        if (table[i] < 0 || (size_t)table[i] >= pool->kv.blocks)
+            return 0;
+    const size_t layers = (size_t)pool->kv.layers;
+    const size_t bytes = layers * capacity * PH_WIDTH * sizeof(float);
+    void *stream = ph_stream();
+    float *dk = pgpu_malloc(bytes), *dv = pgpu_malloc(bytes);
+    int32_t *dt = pgpu_malloc(table_len * sizeof(int32_t));
+    int *status = pgpu_malloc(sizeof(int));
+    int ok = dk && dv && dt && status && pgpu_memset(stream, status, 0, sizeof(int)) &&
+             pgpu_copy_h2d(stream, dt, table, table_len * sizeof(int32_t));
+    if (ok && !to_host)
+        ok = pgpu_copy_h2d(stream, dk, keys, bytes) && pgpu_copy_h2d(stream, dv, values, bytes);
+    ok = ok && pgpu_kv_copy(stream, &pool->kv, dt, (int)first, (int)count, 0, (int)layers,
+                            dk + first * PH_WIDTH, dv + first * PH_WIDTH, capacity, to_host,
+                            status);
+    int st = 1;
+    ok = ok && pgpu_copy_d2h(stream, &st, status, sizeof(int)) && st == 0;
+    if (ok && to_host)
+        ok = pgpu_copy_d2h(stream, keys, dk, bytes) && pgpu_copy_d2h(stream, values, dv, bytes);
+    (void)pgpu_stream_sync(stream);
+    pgpu_free(dk);
+    pgpu_free(dv);
+    pgpu_free(dt);
+    pgpu_free(status);
+    return ok;
+}
+
+int phonon_kv_pool_write(PhononKvPool *pool, const int32_t *table, size_t table_len,
+                         size_t first, size_t count, const float *keys, const float *values,
+                         size_t capacity) {
+    return pool_copy(pool, table, table_len, first, count, (float *)keys, (float *)values,
+                     capacity, 0);
+}
+
+int phonon_kv_pool_read(const PhononKvPool *pool, const int32_t *table, size_t table_len,
+                        size_t first, size_t count, float *keys, float *values,
+                        size_t capacity) {
+    return pool_copy(pool, table, table_len, first, count, keys, values, capacity, 1);
+}
+
+/* ---------------------------------------------------------------- batch -- */
+
+void phonon_flow_batch_destroy(PhononFlowBatch *b) {
+    if (!b)
+        return;
+    if (b->stream)
+        (void)pgpu_stream_sync(b->stream);
+    pgpu_graph_destroy(b->graph);
+    void *bufs[] = {b->x,         b->r,       b->q,       b->in,      b->out,
+                    b->rows,      b->xs,      b->xh,      b->positions, b->tables,
+                    b->status,    b->scratch.part_acc, b->scratch.part_ml, b->scratch.tickets};
+    for (size_t i = 0; i < sizeof(bufs) / sizeof(bufs[0]); i++)
+        pgpu_free(bufs[i]);
+    pgpu_stream_destroy(b->stream);
+    free(b->host_positions);
+    free(b);
+}
+
+int phonon_flow_batch_create(const PhononFlowModel *model, PhononKvPool *pool,
+                             size_t max_streams, size_t max_positions, PhononFlowBatch **batch) {
+    if (!batch)
+        return 0;
+    *batch = NULL;
+    if (!model || !pool || !max_streams || max_streams > 4096 || !max_positions ||
+        max_positions > PHONON_FLOW_MAX_POSITIONS || (size_t)pool->kv.layers < model->layers ||
+        !ph_init())
+        return 0;
+    PhononFlowBatch *b = calloc(1, sizeof(*b));
+    if (!b)
+        return 0;
+    b->model = model;
+    b->pool = pool;
+    b->max_streams = max_streams;
+    b->padded_streams = (max_streams + 15) / 16 * 16;
+    b->max_positions = max_positions;
+    b->table_len = (max_positions + 15) / 16;
+    b->max_splits = (max_positions + PH_SPLIT_KEYS - 1) / PH_SPLIT_KEYS;
+    const size_t rows = b->padded_streams * PH_WIDTH * sizeof(float);
+    const size_t split512 = b->padded_streams * PH_WIDTH * 3 * sizeof(uint16_t);
+    const size_t slots = max_streams * PH_HEADS * b->max_splits;
+    int ok = pgpu_stream_create(&b->stream);
+    b->x = pgpu_malloc(rows);
+    b->r = pgpu_malloc(rows);
+    b->q = pgpu_malloc(rows);
+    b->in = pgpu_malloc(rows);
+    b->out = pgpu_malloc(rows);
+    b->rows = pgpu_malloc(2 * (size_t)pool->kv.layers * PH_WIDTH * sizeof(float));
+    b->xs = pgpu_malloc(split512);
+    b->xh = pgpu_malloc(split512 * 4);
+    b->positions = pgpu_malloc(b->padded_streams * sizeof(int32_t));
+    b->tables = pgpu_malloc(max_streams * b->table_len * sizeof(int32_t));
+    b->status = pgpu_malloc(sizeof(int));
+    b->scratch.part_acc = pgpu_malloc(slots * 64 * sizeof(float));
+    b->scratch.part_ml = pgpu_malloc(slots * 2 * sizeof(float));
+    b->scratch.tickets = pgpu_malloc(max_streams * PH_HEADS * sizeof(int));
+    b->scratch.max_streams = (int)max_streams;
+    b->scratch.max_splits = (int)b->max_splits;
+    b->host_positions = calloc(max_streams, sizeof(size_t));
+    ok = ok && b->x && b->r && b->q && b->in && b->out && b->rows && b->xs && b->xh &&
+         b->positions && b->tables && b->status && b->scratch.part_acc && b->scratch.part_ml &&
+         b->scratch.tickets && b->host_positions;
+    /* Zero everything a kernel may read before writing (padding streams of the
+     * split fragments, tickets, status). */
+    ok = ok && pgpu_memset(b->stream, b->xs, 0, split512) &&
+         pgpu_memset(b->stream, b->xh, 0, split512 * 4) &&
+         pgpu_memset(b->stream, b->positions, 0, b->padded_streams * sizeof(int32_t)) &&
+         pgpu_memset(b->stream, b->tables, 0, max_streams * b->table_len * sizeof(int32_t)) &&
+         pgpu_memset(b->stream, b->status, 0, sizeof(int)) &&
+         pgpu_memset(b->stream, b->scratch.tickets, 0, max_streams * PH_HEADS * sizeof(int)) &&
+         pgpu_memset(b->stream, b->x, 0, rows) && pgpu_memset(b->stream, b->in, 0, rows) &&
+         pgpu_stream_sync(b->stream);
+    if (!ok) {
+        phonon_flow_batch_destroy(b);
+        return 0;
+    }
+    *batch = b;
+    return 1;
+}
+
+int phonon_flow_batch_set_streams(PhononFlowBatch *b, size_t streams, const size_t *positions,
+                                  const int32_t *tables, size_t table_len) {
+    if (!b || !streams || streams > b->max_streams || !positions || !tables ||
+        table_len != b->table_len)
+        return 0;
+    int32_t *pos32 = malloc(streams * sizeof(int32_t));
+    if (!pos32)
+        return 0;
+    for (size_t s = 0; s < streams; s++) {
+        if (positions[s] >= b->max_positions) {
+            free(pos32);
+            return 0;
+        }
+        pos32[s] = (int32_t)positions[s];
+    }
+    int ok = pgpu_stream_sync(b->stream) &&
+             pgpu_copy_h2d(b->stream, b->positions, pos32, streams * sizeof(int32_t)) &&
+             pgpu_copy_h2d(b->stream, b->tables, tables, streams * table_len * sizeof(int32_t));
+    free(pos32);
+    if (!ok)
+        return 0;
+    memcpy(b->host_positions, positions, streams * sizeof(size_t));
+    b->streams = streams;
+    return 1;
+}
+
+int ph_batch_bind_model(PhononFlowBatch *b, const PhononFlowModel *model) {
+    if (!b || !model || model->layers > (size_t)b->pool->kv.layers)
+        return 0;
+    if (b->model != model) {
+        pgpu_graph_destroy(b->graph);
+        b->graph = NULL;
+        b->model = model;
+    }
+    return 1;
+}
+
+int ph_batch_set_single(PhononFlowBatch *b, size_t position, const int32_t *table_dev) {
+    int32_t p = (int32_t)position;
+    if (!pgpu_copy_h2d(b->stream, b->positions, &p, sizeof(p)) ||
+        !pgpu_copy_d2d(b->stream, b->tables, table_dev, b->table_len * sizeof(int32_t)))
+        return 0;
+    b->host_positions[0] = position;
+    b->streams = 1;
+    return 1;
+}
+
+int ph_batch_enqueue_layers(PhononFlowBatch *b, size_t first, size_t count, size_t pool_offset,
+                            const float *input, float *output, float theta) {
+    const PhononFlowModel *m = b->model;
+    if (!b->streams || first + count > m->layers ||
+        first + count + pool_offset > (size_t)b->pool->kv.layers)
+        return 0;
+    const float *rope = ph_rope_table(theta);
+    if (!rope)
+        return 0;
+    void *st = b->stream;
+    const int n = (int)b->streams;
+    const float *cur = input;
+    /* A layer reads its input only in LN1 and the out-projection residual,
+     * both before its last kernel writes `next`, so in-place is safe. */
+    for (size_t l = first; l < first + count; l++) {
+        const float *norm = m->norms + l * 4 * PH_WIDTH;
+        float *next = (l + 1 == first + count) ? output : b->x;
+        if (!pgpu_ln_split(st, cur, n, norm, norm + PH_WIDTH, 1e-5f, b->xs, NULL, b->status) ||
+            !pgpu_gemm_qkv(st, &m->qkv[l], b->xs, n, &b->pool->kv, (int)(l + pool_offset),
+                           b->tables, (int)b->table_len, b->positions, rope, b->q, b->status) ||
+            !pgpu_attention(st, b->q, &b->pool->kv, (int)(l + pool_offset), b->tables,
+                            (int)b->table_len, b->positions, n, PH_HEADS, (int)b->max_splits,
+                            b->xs, NULL, &b->scratch, b->status) ||
+            !pgpu_gemm_residual(st, &m->out[l], b->xs, n, cur, b->r, b->status) ||
+            !pgpu_ln_split(st, b->r, n, norm + 2 * PH_WIDTH, norm + 3 * PH_WIDTH, 1e-5f, b->xs,
+                           NULL, b->status) ||
+            !pgpu_gemm_gelu_split(st, &m->mlp_in[l], b->xs, n, b->xh, b->status) ||
+            !pgpu_gemm_residual(st, &m->mlp_out[l], b->xh, n, b->r, next, b->status))
+            return 0;
+        cur = next;
+    }
+    return 1;
+}
+
+static int enqueue_step(PhononFlowBatch *b, const float *input, float *output, float theta) {
+    return ph_batch_enqueue_layers(b, 0, b->model->layers, 0, input, output, theta) &&
+           pgpu_advance_positions(b->stream, b->positions, (int)b->streams);
+}
+
+int phonon_flow_batch_step_device(PhononFlowBatch *b, const float *inputs, float theta,
+                                  float *outputs) {
+    if (!b || !b->streams || !inputs || !outputs)
+        return 0;
+    for (size_t s = 0; s < b->streams; s++)
+        if (b->host_positions[s] >= b->max_positions)
+            return 0;
+    if (!b->graph || b->graph_streams != b->streams || b->graph_theta != theta ||
+        b->graph_input != inputs || b->graph_output != outputs) {
+        pgpu_graph_destroy(b->graph);
+        b->graph = NULL;
+        if (!ph_rope_table(theta) || !pgpu_graph_begin(b->stream))
+            return 0;
+        const int enqueued = enqueue_step(b, inputs, outputs, theta);
+        void *exec = NULL;
+        const int ended = pgpu_graph_end(b->stream, &exec);
+        if (!enqueued || !ended) {
+            pgpu_graph_destroy(exec);
+            return 0;
+        }
+        b->graph = exec;
+        b->graph_streams = b->streams;
+        b->graph_theta = theta;
+        b->graph_input = inputs;
+        b->graph_output = outputs;
+    }
+    if (!pgpu_graph_launch(b->graph, b->stream))
+        return 0;
+    for (size_t s = 0; s < b->streams; s++)
+        b->host_positions[s]++;
+    return 1;
+}
+
+int phonon_flow_batch_sync(PhononFlowBatch *b) {
+    if (!b || !pgpu_stream_sync(b->stream))
+        return 0;
+    int st = 0;
+    if (!pgpu_copy_d2h(b->stream, &st, b->status, sizeof(int)))
+        return 0;
+    if (st && !pgpu_memset(b->stream, b->status, 0, sizeof(int)))
+        return 0;
+    return pgpu_stream_sync(b->stream) && st == 0;
+}
+
+int phonon_flow_batch_step(PhononFlowBatch *b, const float *inputs, float theta,
+                           float *outputs) {
+    if (!b || !b->streams || !inputs || !outputs)
+        return 0;
+    const size_t bytes = b->streams * PH_WIDTH * sizeof(float);
+    if (!pgpu_copy_h2d(b->stream, b->in, inputs, bytes) ||
+        !phonon_flow_batch_step_device(b, b->in, theta, b->out))
+        return 0;
+    const int clean = phonon_flow_batch_sync(b);
+    if (!pgpu_copy_d2h(b->stream, outputs, b->out, bytes))
+        return 0;
+    return clean && ph_all_finite(outputs, b->streams * PH_WIDTH);
+}
+
+int phonon_flow_batch_positions(const PhononFlowBatch *b, size_t *positions) {
+    if (!b || !positions)
+        return 0;
+    memcpy(positions, b->host_positions, b->streams * sizeof(size_t));
+    return 1;
+}
+
+void *phonon_flow_batch_stream(const PhononFlowBatch *b) { return b ? b->stream : NULL; }
+float *phonon_flow_batch_device_inputs(PhononFlowBatch *b) { return b ? b->in : NULL; }
+float *phonon_flow_batch_device_outputs(PhononFlowBatch *b) { return b ? b->out : NULL; }
+
+int ph_batch_status(PhononFlowBatch *b) { return phonon_flow_batch_sync(b); }
+float *ph_batch_in(PhononFlowBatch *b) { return b->in; }
+float *ph_batch_out(PhononFlowBatch *b) { return b->out; }
+size_t ph_batch_table_len(const PhononFlowBatch *b) { return b->table_len; }
+const int32_t *ph_batch_tables(const PhononFlowBatch *b) { return b->tables; }
+float *ph_batch_scratch_rows(PhononFlowBatch *b) { return b->rows; }
+void *ph_batch_stream(const PhononFlowBatch *b) { return b->stream; }
+int *ph_batch_status_word(PhononFlowBatch *b) { return b->status; }
+
+/* ------------------------------------------------------------- registry -- */
+
+typedef struct Registered {
+    const PhononFlowLayerWeights *weights;
+    size_t layers;
+    const PhononTensorView *views[64][8];
+    PhononFlowModel *model;
+    struct Registered *next;
+} Registered;
+
+static pthread_mutex_t g_registry_lock = PTHREAD_MUTEX_INITIALIZER;
+static Registered *g_registry;
+
+static void snapshot_views(const PhononFlowLayerWeights *w, size_t layers,
+                           const PhononTensorView *views[64][8]) {
+    for (size_t l = 0; l < layers; l++) {
+        const PhononTensorView *v[8] = {w[l].qkv,          w[l].attention_out, w[l].mlp_in,
+                                        w[l].mlp_out,      w[l].norm1_weight,  w[l].norm1_bias,
+                                        w[l].norm2_weight, w[l].norm2_bias};
+        memcpy(views[l], v, sizeof(v));
+    }
+}
+
+int phonon_flow_prepare_weights(const PhononFlowLayerWeights *weights, size_t layers) {
+    if (!weights || !layers || layers > 64)
+        return 0;
+    Registered *r = calloc(1, sizeof(*r));
+    if (!r || !phonon_flow_model_create(weights, layers, &r->model)) {
+        free(r);
+        return 0;
+    }
+    r->weights = weights;
+    r->layers = layers;
+    snapshot_views(weights, layers, r->views);
+    phonon_flow_release_weights(weights);
+    pthread_mutex_lock(&g_registry_lock);
+    r->next = g_registry;
+    g_registry = r;
+    pthread_mutex_unlock(&g_registry_lock);
+    return 1;
+}
+
+void phonon_flow_release_weights(const PhononFlowLayerWeights *weights) {
+    pthread_mutex_lock(&g_registry_lock);
+    for (Registered **p = &g_registry; *p;) {
+        if ((*p)->weights == weights) {
+            Registered *dead = *p;
+            *p = dead->next;
+            phonon_flow_model_destroy(dead->model);
+            free(dead);
+        } else {
+            p = &(*p)->next;
+        }
+    }
+    pthread_mutex_unlock(&g_registry_lock);
+}
+
+const PhononFlowModel *ph_registered_model(const PhononFlowLayerWeights *weights,
+                                           size_t layers) {
+    const PhononFlowModel *found = NULL;
+    pthread_mutex_lock(&g_registry_lock);
+    for (Registered *r = g_registry; r && !found; r = r->next) {
+        if (r->weights != weights || r->layers != layers)
+            continue;
+        const PhononTensorView *now[64][8];
+        snapshot_views(weights, layers, now);
+        if (!memcmp(now, r->views, layers * sizeof(now[0])))
+            found = r->model;
+    }
+    pthread_mutex_unlock(&g_registry_lock);
+    return found;
+}

@@ -1,0 +1,179 @@
+/* phonon_q8_dot / phonon_q8_matvec on the MI355X (phonon_q8.h), and the
+ * device-resident matrices of phonon_q8_device.h.
+ *
+ * Argument checks follow src/phonon_q8.c:36-92. The arithmetic per row is
+ * the reference's: for every 32-column block, partial = sum q*x, then
+ * sum += scale * partial (the partial computed exactly on split bf16 MFMA
+ * terms, see pgpu_gemm.hip). */
+#include "phonon_q8_device.h"
+#include "ph_internal.h"
+
+#include <stdlib.h>
+#include <string.h>
+
+struct PhononQ8Device {
+    pgpu_matrix *copies;
+    void **allocations;
+    size_t count, rows, columns, max_batch;
+    uint16_t *xs;
+    int *status;
+};
+
+void phonon_q8_device_destroy(PhononQ8Device *m) {
+    if (!m)
+        return;
+    (void)pgpu_stream_sync(NULL);
+    for (size_t i = 0; i < m->count; i++)
+        pgpu_free(m->allocations[i]);
+    pgpu_free(m->xs);
+    pgpu_free(m->status);
+    free(m->copies);
+    free(m->allocations);
+    free(m);
+}
+
+int phonon_q8_device_create(const PhononQ8Block *weights, size_t rows, size_t columns,
+                            size_t copies, PhononQ8Device **matrix) {
+    if (!matrix)
+        return 0;
+    *matrix = NULL;
+    if (!weights || !rows || rows % 16 || !columns || columns % 32 || !copies ||
+        copies > 100000 || rows > SIZE_MAX / columns || !ph_init())
+        return 0;
+    PhononQ8Device *m = calloc(1, sizeof(*m));
+    if (!m)
+        return 0;
+    m->copies = calloc(copies, sizeof(pgpu_matrix));
+    m->allocations = calloc(copies, sizeof(void *));
+    m->rows = rows;
+    m->columns = columns;
+    m->max_batch = 64;
+    PhononTensorView view = {.dtype = PHONON_PACK_Q8_0,
+                             .rank = 2,
+                             .shape = {rows, columns},
+                             .data = weights,
+                             .byte_count = rows * columns / 32 * sizeof(PhononQ8Block)};
+    int ok = m->copies && m->allocations;
+    for (size_t i = 0; ok && i < copies; i++) {
+        ok = ph_matrix_upload(&view, rows, columns, &m->copies[i], &m->allocations[i]);
+        if (ok)
+            m->count++;
+    }
+    const size_t split_bytes = m->max_batch * (ok ? m->copies[0].columns : 0) * 3 * 2;
+    if (ok) {
+        m->xs = pgpu_malloc(split_bytes);
+        m->status = pgpu_malloc(sizeof(int));
+        ok = m->xs && m->status && pgpu_memset(NULL, m->xs, 0, split_bytes) &&
+             pgpu_memset(NULL, m->status, 0, sizeof(int)) && pgpu_stream_sync(NULL);
+    }
+    if (!ok) {
+        phonon_q8_device_destroy(m);
+        return 0;
+    }
+    *matrix = m;
+    return 1;
+}
+
+int phonon_q8_device_matvec(PhononQ8Device *m, size_t copy, const float *x, float *y,
+                            size_t batch, void *stream) {
+    if (!m || copy >= m->count || !x || !y || !batch || batch > m->max_batch)
+        return 0;
+    const pgpu_matrix *w = &m->copies[copy];
+    if (w->columns != m->columns)
+        return 0; /* padded columns would need a padded input */
+    return pgpu_split_rows(stream, x, (int)batch, (int)w->columns, m->xs, m->status) &&
+           pgpu_gemm_store(stream, w, m->xs, (int)batch, NULL, y, (int)w->rows, m->status);
+}
+
+int phonon_q8_device_status(PhononQ8Device *m, void *stream) {
+    int st = 1;
+    if (!m || !pgpu_stream_sync(stream) || !pgpu_copy_d2h(stream, &st, m->status, sizeof(int)))
+        return 0;
+    if (st && !(pgpu_memset(stream, m->status, 0, sizeof(int)) && pgpu_stream_sync(stream)))
+        return 0;
+    return st == 0;
+}
+
+size_t phonon_q8_device_bytes_per_call(const PhononQ8Device *m, size_t batch) {
+    if (!m)
+        return 0;
+    return m->rows * m->columns / 32 * sizeof(PhononQ8Block) +
+           batch * (m->columns + m->rows) * sizeof(float);
+}
+
+/* ------------------------------------------------------------- drop-ins -- */
+
+int phonon_q8_matvec(const PhononQ8Block *weights, const float *input, size_t rows,
+                     size_t columns, float *output) {
+    if (weights == NULL || input == NULL || output == NULL || rows == 0 || columns == 0 ||
+        columns % 32 != 0 || rows > SIZE_MAX / (columns / 32) ||
+        columns > SIZE_MAX / sizeof(*input) || rows > SIZE_MAX / sizeof(*output))
+        return 0;
+    const size_t input_bytes = columns * sizeof(float), output_bytes = rows * sizeof(float);
+    const size_t blocks = rows * (columns / 32);
+    if (blocks > SIZE_MAX / sizeof(PhononQ8Block))
+        return 0;
+    const size_t weight_bytes = blocks * sizeof(PhononQ8Block);
+    if ((uintptr_t)input > UINTPTR_MAX - input_bytes ||
+        (uintptr_t)output > UINTPTR_MAX - output_bytes ||
+        (uintptr_t)weights > UINTPTR_MAX - weight_bytes ||
+        ph_overlap(input, input_bytes, output, output_bytes) ||
+        ph_overlap(weights, weight_bytes, output, output_bytes))
+        return 0;
+    /* The reference fails on the first non-finite scale or input. */
+    if (!ph_all_finite(input, columns))
+        return 0;
+    for (size_t i = 0; i < blocks; i++)
+        if (!ph_half_finite(weights[i].scale_bits))
+            return 0;
+    if (rows > INT32_MAX / 2 || columns > INT32_MAX / 2 || !ph_init())
+        return 0;
+    ph_lock();
+    void *s = ph_stream();
+    pgpu_matrix w;
+    void *wdev = NULL;
+    PhononTensorView view = {.dtype = PHONON_PACK_Q8_0,
+                             .rank = 2,
+                             .shape = {rows, columns},
+                             .data = weights,
+                             .byte_count = weight_bytes};
+    int ok = ph_matrix_upload(&view, rows, columns, &w, &wdev);
+    float *x = ok ? ph_scratch(2, columns * sizeof(float)) : NULL;
+    float *y = ok ? ph_scratch(3, w.rows * sizeof(float)) : NULL;
+    uint16_t *xs = ok ? ph_scratch(5, 16 * columns * 3 * sizeof(uint16_t)) : NULL;
+    int *status = ph_scratch(1, sizeof(int));
+    float *host = ok ? malloc(w.rows * sizeof(float)) : NULL;
+    int st = 1;
+    ok = ok && x && y && xs && status && host && pgpu_memset(s, status, 0, sizeof(int)) &&
+         pgpu_memset(s, xs, 0, 16 * columns * 3 * sizeof(uint16_t)) &&
+         pgpu_copy_h2d(s, x, input, input_bytes) &&
+         pgpu_split_rows(s, x, 1, (int)columns, xs, status) &&
+         pgpu_gemm_store(s, &w, xs, 1, NULL, y, (int)w.rows, status) &&
+         pgpu_copy_d2h(s, &st, status, sizeof(int)) &&
+         pgpu_copy_d2h(s, host, y, w.rows * sizeof(float));
+    if (ok && st == 0)
+        memcpy(output, host, output_bytes);
+    (void)pgpu_stream_sync(s);
+    pgpu_free(wdev);
+    ph_unlock();
+    free(host);
+    return ok && st == 0;
+}
+
+int phonon_q8_dot(const PhononQ8Block *blocks, const float *input, size_t elements,
+                  float *result) {
+    if (blocks == NULL || input == NULL || result == NULL || elements == 0 ||
+        elements % 32 != 0 || elements / 32 > SIZE_MAX / sizeof(*blocks) ||
+        elements > SIZE_MAX / sizeof(*input))
+        return 0;
+    const size_t block_bytes = elements / 32 * sizeof(*blocks);
+    const size_t input_bytes = elements * sizeof(*input);
+    if ((uintptr_t)blocks > UINTPTR_MAX - block_bytes ||
+        (uintptr_t)input > UINTPTR_MAX - input_bytes)
+        return 0;
+    float out;
+    if (!phonon_q8_matvec(blocks, input, 1, elements, &out))
+        return 0;
+    *result = out;
+    return 1;
+}

@@ -1,0 +1,507 @@
+"""GPU parity of the decode step itself, through the C-ABI: KV pool and
+cache data movement (bit-exact), the single-stream drop-ins of
+phonon_transformer.h, and the batched paged API, against the CPU oracle.
+
+Conditioning note: with the benchmark weight distribution (Q8 scales
+U[1e-3, 1e-2]) 12 stacked layers saturate softmax and amplify rounding so
+much that the oracle itself differs from float64 by ~1e-3 normwise. Tight
+(1e-4) multi-step stack parity therefore uses the same generator with scales
+x0.1 ("well-conditioned"); the benchmark distribution is checked per layer
+at 1e-4 from identical caches, and over the full stack by comparing both
+the GPU and the oracle against float64."""
+import ctypes
+
+import numpy as np
+import pytest
+
+import helpers
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-4
+L9 = 9
+
+
+def fp(a):
+    return a.ctypes.data_as(ctypes.POINTER(ctypes.c_float))
+
+
+def i32p(a):
+    return a.ctypes.data_as(ctypes.POINTER(ctypes.c_int32))
+
+
+def scaled_model(syn, seed, layers, factor=0.1):
+    model = syn.flow_model(seed, layers)
+    for layer in model:
+        for name in helpers.SHAPES:
+            sc = layer[name]["scale_bits"].view(np.float16).astype(np.float32) * factor
+            layer[name]["scale_bits"] = sc.astype(np.float16).view(np.uint16)
+    return model
+
+
+class Cache:
+    """A PhononKvCache created by the product (host arrays + device copy)."""
+
+    def __init__(self, lib, capacity):
+        self.lib = lib
+        self.c = lib.phonon_kv_cache_init.argtypes[0]._type_()
+        assert lib.phonon_kv_cache_init(ctypes.byref(self.c), capacity)
+        self.capacity = capacity
+
+    def keys(self):
+        return np.ctypeslib.as_array(self.c.keys, shape=(L9, self.capacity, 512))
+
+    def values(self):
+        return np.ctypeslib.as_array(self.c.values, shape=(L9, self.capacity, 512))
+
+    def ref(self):
+        return ctypes.byref(self.c)
+
+    def destroy(self):
+        self.lib.phonon_kv_cache_destroy(ctypes.byref(self.c))
+
+
+# --------------------------------------------------------------- KV movement
+def test_pool_roundtrip_bit_exact_shuffled(lib):
+    layers, blocks, cap = 3, 24, 300
+    pool = ctypes.c_void_p()
+    assert lib.phonon_kv_pool_create(layers, blocks, ctypes.byref(pool))
+    ids = np.zeros(blocks, np.int32)
+    assert lib.phonon_kv_pool_alloc(pool, blocks, i32p(ids))
+    assert lib.phonon_kv_pool_free_blocks(pool) == 0
+    rng = np.random.default_rng(61)
+    table = rng.permutation(ids)[: (cap + 15) // 16].astype(np.int32)
+    k = rng.standard_normal((layers, cap, 512)).astype(np.float32)
+    v = rng.standard_normal((layers, cap, 512)).astype(np.float32)
+    assert lib.phonon_kv_pool_write(pool, i32p(table), table.size, 0, cap, fp(k), fp(v), cap)
+    k2 = np.zeros_like(k)
+    v2 = np.zeros_like(v)
+    assert lib.phonon_kv_pool_read(pool, i32p(table), table.size, 0, cap, fp(k2), fp(v2), cap)
+    assert np.array_equal(k.view(np.uint32), k2.view(np.uint32))
+    assert np.array_equal(v.view(np.uint32), v2.view(np.uint32))
+    # A partial window lands exactly where the table says.
+    k3 = np.zeros_like(k)
+    v3 = np.zeros_like(v)
+    assert lib.phonon_kv_pool_read(pool, i32p(table), table.size, 37, 20, fp(k3), fp(v3), cap)
+    assert np.array_equal(k3[:, 37:57], k[:, 37:57]) and not k3[:, :37].any()
+    # Out-of-pool block ids are rejected on the host.
+    bad = table.copy()
+    bad[0] = blocks
+    assert not lib.phonon_kv_pool_read(pool, i32p(bad), bad.size, 0, 16, fp(k3), fp(v3), cap)
+    assert lib.phonon_kv_pool_release(pool, blocks, i32p(ids))
+    assert not lib.phonon_kv_pool_release(pool, 1, i32p(ids))
+    lib.phonon_kv_pool_destroy(pool)
+
+
+def test_kv_cache_layout_and_lifecycle(lib):
+    """tests/test_phonon_transformer.c:586-607 against the drop-in cache."""
+    cache = Cache(lib, 2)
+    other = Cache(lib, 2)
+    k = np.arange(512, dtype=np.float32)
+    v = -k
+    assert lib.phonon_kv_cache_append(cache.ref(), 8, 1, fp(k), fp(v), 512)
+    assert cache.keys().reshape(-1)[(8 * 2 + 1) * 512 + 7] == 7.0
+    assert cache.c.length == 0
+    assert lib.phonon_kv_cache_commit_position(cache.ref(), 0) and cache.c.length == 1
+    assert not lib.phonon_kv_cache_commit_position(cache.ref(), 0)
+    assert other.c.length == 0
+    assert not lib.phonon_kv_cache_append(cache.ref(), 9, 0, fp(k), fp(v), 512)
+    assert not lib.phonon_kv_cache_append(cache.ref(), 0, 2, fp(k), fp(v), 512)
+    assert not lib.phonon_kv_cache_append(cache.ref(), 0, 0, fp(k), fp(v), 511)
+    kn = k.copy()
+    kn[3] = np.nan
+    assert not lib.phonon_kv_cache_append(cache.ref(), 0, 0, fp(kn), fp(v), 512)
+    lib.phonon_kv_cache_reset(cache.ref())
+    assert cache.c.length == 0
+    cache.destroy()
+    other.destroy()
+    assert not cache.c.keys and not cache.c.values
+
+
+# ------------------------------------------------------- single-stream steps
+def oracle_for(oracle, oracle_mod, model):
+    return oracle_mod.OracleModel(oracle, helpers.oracle_layers(oracle, model))
+
+
+def test_layer_step_benchmark_weights_vs_oracle(lib, oracle, oracle_mod, syn, pkg):
+    """One layer (benchmark weight distribution) at several positions, from
+    identical cache histories: 1e-4 normwise."""
+    model = syn.flow_model(71, 1)
+    om = oracle_for(oracle, oracle_mod, model)
+    views = pkg.Views()
+    w = views.layers(model)
+    rng = np.random.default_rng(72)
+    layer = 4
+    for pos in (0, 1, 17, 300, 1100):
+        cap = pos + 1
+        cache = Cache(lib, cap)
+        hist_k = (rng.standard_normal((pos, 512)) * 8).astype(np.float32)
+        hist_v = (rng.standard_normal((pos, 512)) * 8).astype(np.float32)
+        for p in range(pos):
+            assert lib.phonon_kv_cache_append(cache.ref(), layer, p, fp(hist_k[p]),
+                                              fp(hist_v[p]), 512)
+        cache.c.length = pos
+        okeys = np.zeros((1, cap, 512), np.float32)
+        ovals = np.zeros_like(okeys)
+        okeys[0, :pos] = hist_k
+        ovals[0, :pos] = hist_v
+        x = (rng.standard_normal(512) * 20).astype(np.float32)
+        out = np.zeros(512, np.float32)
+        assert lib.phonon_flow_layer_step(w, cache.ref(), layer, pos, fp(x), 10000.0, fp(out))
+        ok, ref = om.layer_step(okeys, ovals, cap, 0, pos, x)
+        assert ok
+        err = helpers.normwise(out, ref)
+        print("layer step pos", pos, "normwise", err)
+        assert err <= TOL
+        # The appended row is mirrored into the host arrays.
+        assert helpers.normwise(cache.keys()[layer, pos], okeys[0, pos]) <= TOL
+        assert helpers.normwise(cache.values()[layer, pos], ovals[0, pos]) <= TOL
+        assert cache.c.length == pos  # a layer step does not commit
+        cache.destroy()
+
+
+def test_stack_step_well_conditioned_vs_oracle(lib, oracle, oracle_mod, syn, pkg):
+    """Nine layers (the drop-in's PHONON_FLOW_LAYERS), 24 successive steps."""
+    model = scaled_model(syn, 81, L9)
+    om = oracle_for(oracle, oracle_mod, model)
+    views = pkg.Views()
+    w = views.layers(model)
+    steps = 24
+    cache = Cache(lib, steps)
+    okeys = np.zeros((L9, steps, 512), np.float32)
+    ovals = np.zeros_like(okeys)
+    rng = np.random.default_rng(82)
+    for pos in range(steps):
+        x = rng.standard_normal(512).astype(np.float32)
+        out = np.zeros(512, np.float32)
+        assert lib.phonon_flow_stack_step(w, cache.ref(), pos, fp(x), 10000.0, fp(out))
+        assert cache.c.length == pos + 1
+        ok, ref = om.stack_step(okeys, ovals, steps, pos, x)
+        assert ok
+        assert helpers.normwise(out, ref) <= TOL, (pos, helpers.normwise(out, ref))
+    assert helpers.normwise(cache.keys(), okeys) <= TOL
+    assert helpers.normwise(cache.values(), ovals) <= TOL
+    # Wrong position / full cache are rejected.
+    out = np.zeros(512, np.float32)
+    x = np.zeros(512, np.float32)
+    assert not lib.phonon_flow_stack_step(w, cache.ref(), 3, fp(x), 10000.0, fp(out))
+    assert not lib.phonon_flow_stack_step(w, cache.ref(), steps, fp(x), 10000.0, fp(out))
+    cache.destroy()
+
+
+def zero_model(pkg):
+    z = {name: np.zeros(r * c, np.uint16) for name, (r, c) in helpers.SHAPES.items()}
+    z["norm1_weight"] = np.full(512, 0x3F80, np.uint16)
+    z["norm2_weight"] = np.full(512, 0x3F80, np.uint16)
+    z["norm1_bias"] = np.zeros(512, np.uint16)
+    z["norm2_bias"] = np.zeros(512, np.uint16)
+    return z
+
+
+def test_stack_invariants_identity_causality_isolation(lib, pkg):
+    """tests/test_phonon_transformer.c:707-855 on the drop-ins."""
+    views = pkg.Views()
+    zl = zero_model(pkg)
+    w = views.layers([zl] * L9)
+    state = (np.arange(512) / 512).astype(np.float32)
+    out = np.zeros(512, np.float32)
+    cache = Cache(lib, 2)
+    assert lib.phonon_flow_layer_step(w, cache.ref(), 0, 0, fp(state), 10000.0, fp(out))
+    assert np.array_equal(out, state)
+    assert lib.phonon_flow_stack_step(w, cache.ref(), 0, fp(state), 10000.0, fp(out))
+    assert cache.c.length == 1 and np.array_equal(out, state)
+    assert lib.phonon_flow_stack_step(w, cache.ref(), 1, fp(state), 10000.0, fp(out))
+    assert cache.c.length == 2
+    cache.destroy()
+    # Nonzero V and output paths: the output depends on the cache.
+    z2 = dict(zl)
+    z2["qkv"] = zl["qkv"].copy()
+    z2["qkv"][1024 * 512] = 0x3F80
+    z2["out"] = zl["out"].copy()
+    z2["out"][0] = 0x3F80
+    w2 = views.layers([z2] * L9)
+    causal = Cache(lib, 2)
+    first = np.zeros(512, np.float32)
+    first[0] = 1
+    second = np.zeros(512, np.float32)
+    second[0] = 3
+    out0 = np.zeros(512, np.float32)
+    out1 = np.zeros(512, np.float32)
+    assert lib.phonon_flow_stack_step(w2, causal.ref(), 0, fp(first), 10000.0, fp(out0))
+    assert lib.phonon_flow_stack_step(w2, causal.ref(), 1, fp(second), 10000.0, fp(out1))
+    assert out0[0] > 1 and out1[0] > 3
+    causal.destroy()
+    # Request isolation and reset.
+    a, b, r = Cache(lib, 2), Cache(lib, 2), Cache(lib, 2)
+    div = np.zeros(512, np.float32)
+    div[0] = 1
+    shared = np.zeros(512, np.float32)
+    shared[0] = 3
+    aout, bout, rout = (np.zeros(512, np.float32) for _ in range(3))
+    assert lib.phonon_flow_stack_step(w2, a.ref(), 0, fp(div), 10000.0, fp(aout))
+    div[0] = -7
+    assert lib.phonon_flow_stack_step(w2, b.ref(), 0, fp(div), 10000.0, fp(bout))
+    assert lib.phonon_flow_stack_step(w2, a.ref(), 1, fp(shared), 10000.0, fp(aout))
+    one = np.zeros(512, np.float32)
+    one[0] = 1
+    assert lib.phonon_flow_stack_step(w2, r.ref(), 0, fp(one), 10000.0, fp(rout))
+    assert lib.phonon_flow_stack_step(w2, r.ref(), 1, fp(shared), 10000.0, fp(rout))
+    assert np.max(np.abs(aout - rout)) < 1e-6
+    lib.phonon_kv_cache_reset(a.ref())
+    assert lib.phonon_flow_stack_step(w2, a.ref(), 0, fp(one), 10000.0, fp(aout))
+    assert a.c.length == 1 and abs(aout[0] - bout[0]) > 1e-4
+    for c in (a, b, r):
+        c.destroy()
+
+
+def test_cancel_resets_and_prefill_contract(lib, pkg):
+    views = pkg.Views()
+    zl = zero_model(pkg)
+    w = views.layers([zl] * L9)
+    calls = {"n": 0}
+
+    @pkg.CANCEL_POLL
+    def cancel_at_third(_ctx):
+        calls["n"] += 1
+        return int(calls["n"] == 3)
+
+    cache = Cache(lib, 4)
+    x = np.ones(512, np.float32)
+    out = np.full(512, 5.0, np.float32)
+    assert lib.phonon_flow_stack_step(w, cache.ref(), 0, fp(x), 10000.0, fp(out))
+    assert cache.c.length == 1
+    assert not lib.phonon_flow_stack_step_cancel(w, cache.ref(), 1, fp(x), 10000.0, fp(out),
+                                                 cancel_at_third, None)
+    assert cache.c.length == 0 and calls["n"] == 3
+    cache.destroy()
+    # Prefill (src/phonon_transformer.c:619-709 contract).
+    pa, pb = Cache(lib, 2), Cache(lib, 2)
+    state = (np.arange(512) / 512).astype(np.float32)
+    inp = np.concatenate([state, -(np.arange(512) / 256).astype(np.float32)])
+    o = np.zeros(512, np.float32)
+    assert not lib.phonon_flow_stack_prefill(w, pa.ref(), fp(inp), 0, 10000.0, fp(o))
+    assert not lib.phonon_flow_stack_prefill(w, pa.ref(), fp(inp), 3, 10000.0, fp(o))
+    assert not lib.phonon_flow_stack_prefill(w, pa.ref(), fp(inp), 8193, 10000.0, fp(o))
+    assert lib.phonon_flow_stack_prefill(w, pa.ref(), fp(inp), 2, 10000.0, fp(o))
+    assert pa.c.length == 2 and pb.c.length == 0 and np.array_equal(o, inp[512:])
+    assert not lib.phonon_flow_stack_prefill(w, pa.ref(), fp(inp), 1, 10000.0, fp(o))
+    assert pa.c.length == 2
+    lib.phonon_kv_cache_reset(pa.ref())
+    o[0] = 123.0
+    bad = inp.copy()
+    bad[0] = np.nan
+    assert not lib.phonon_flow_stack_prefill(w, pa.ref(), fp(bad), 2, 10000.0, fp(o))
+    assert pa.c.length == 0 and o[0] == 123.0
+    assert lib.phonon_flow_stack_prefill(w, pa.ref(), fp(inp), 1, 10000.0, fp(o))
+    assert pa.c.length == 1
+    assert lib.phonon_flow_stack_step(w, pa.ref(), 1, fp(state), 10000.0, fp(o))
+    assert pa.c.length == 2 and pb.c.length == 0
+    pa.destroy()
+    pb.destroy()
+
+
+def test_prefill_matches_oracle_stack(lib, oracle, oracle_mod, syn, pkg):
+    model = scaled_model(syn, 91, L9)
+    om = oracle_for(oracle, oracle_mod, model)
+    views = pkg.Views()
+    w = views.layers(model)
+    n = 20
+    rng = np.random.default_rng(92)
+    inp = rng.standard_normal((n, 512)).astype(np.float32)
+    cache = Cache(lib, n + 1)
+    out = np.zeros(512, np.float32)
+    assert lib.phonon_flow_stack_prefill(w, cache.ref(), fp(inp), n, 10000.0, fp(out))
+    okeys = np.zeros((L9, n + 1, 512), np.float32)
+    ovals = np.zeros_like(okeys)
+    for p in range(n):
+        ok, ref = om.stack_step(okeys, ovals, n + 1, p, inp[p])
+    assert cache.c.length == n and helpers.normwise(out, ref) <= TOL
+    assert helpers.normwise(cache.keys()[:, :n], okeys[:, :n]) <= TOL
+    cache.destroy()
+
+
+# --------------------------------------------------------------- batched API
+class Batch:
+    def __init__(self, lib, model_views, layers, streams, max_positions, pool_blocks):
+        self.lib = lib
+        self.model = ctypes.c_void_p()
+        self.pool = ctypes.c_void_p()
+        self.batch = ctypes.c_void_p()
+        assert lib.phonon_flow_model_create(model_views, layers, ctypes.byref(self.model))
+        assert lib.phonon_kv_pool_create(layers, pool_blocks, ctypes.byref(self.pool))
+        assert lib.phonon_flow_batch_create(self.model, self.pool, streams, max_positions,
+                                            ctypes.byref(self.batch))
+        self.table_len = (max_positions + 15) // 16
+
+    def close(self):
+        self.lib.phonon_flow_batch_destroy(self.batch)
+        self.lib.phonon_kv_pool_destroy(self.pool)
+        self.lib.phonon_flow_model_destroy(self.model)
+
+
+def test_batch_ragged_shuffled_vs_oracle(lib, oracle, oracle_mod, syn, pkg):
+    layers = 2
+    model = scaled_model(syn, 101, layers)
+    om = oracle_for(oracle, oracle_mod, model)
+    views = pkg.Views()
+    w = views.layers(model)
+    lengths = np.array([0, 1, 15, 16, 17, 255, 256, 700])
+    streams, steps = len(lengths), 3
+    max_pos = 720
+    table_len = (max_pos + 15) // 16
+    blocks = streams * table_len + 5
+    bt = Batch(lib, w, layers, streams, max_pos, blocks)
+    ids = np.zeros(blocks, np.int32)
+    assert lib.phonon_kv_pool_alloc(bt.pool, blocks, i32p(ids))
+    rng = np.random.default_rng(102)
+    tables = rng.permutation(ids)[: streams * table_len].reshape(streams, table_len).astype(
+        np.int32)
+    okeys = np.zeros((streams, layers, max_pos, 512), np.float32)
+    ovals = np.zeros_like(okeys)
+    for s, n in enumerate(lengths):
+        if n:
+            okeys[s, :, :n] = rng.standard_normal((layers, n, 512)).astype(np.float32)
+            ovals[s, :, :n] = rng.standard_normal((layers, n, 512)).astype(np.float32)
+            assert lib.phonon_kv_pool_write(bt.pool, i32p(tables[s]), table_len, 0, int(n),
+                                            fp(okeys[s]), fp(ovals[s]), max_pos)
+    pos = lengths.astype(np.uintp)
+    assert lib.phonon_flow_batch_set_streams(
+        bt.batch, streams, pos.ctypes.data_as(ctypes.POINTER(ctypes.c_size_t)),
+        i32p(np.ascontiguousarray(tables)), table_len)
+    for step in range(steps):
+        x = rng.standard_normal((streams, 512)).astype(np.float32)
+        y = np.zeros_like(x)
+        assert lib.phonon_flow_batch_step(bt.batch, fp(x), 10000.0, fp(y))
+        for s in range(streams):
+            ok, ref = om.stack_step(okeys[s], ovals[s], max_pos, int(lengths[s]) + step, x[s])
+            assert ok
+            err = helpers.normwise(y[s], ref)
+            assert err <= TOL, (step, s, err)
+    got = np.zeros(streams, np.uintp)
+    assert lib.phonon_flow_batch_positions(
+        bt.batch, got.ctypes.data_as(ctypes.POINTER(ctypes.c_size_t)))
+    assert np.array_equal(got, lengths + steps)
+    # The rows appended on the device match the oracle's cache rows.
+    for s in (0, 5, 7):
+        k = np.zeros((layers, max_pos, 512), np.float32)
+        v = np.zeros_like(k)
+        n0 = int(lengths[s])
+        assert lib.phonon_kv_pool_read(bt.pool, i32p(tables[s]), table_len, n0, steps, fp(k),
+                                       fp(v), max_pos)
+        assert helpers.normwise(k[:, n0:n0 + steps], okeys[s, :, n0:n0 + steps]) <= TOL
+        assert helpers.normwise(v[:, n0:n0 + steps], ovals[s, :, n0:n0 + steps]) <= TOL
+    bt.close()
+
+
+def test_batch_block_placement_does_not_change_bits(lib, syn, pkg):
+    """Same contexts through identity vs shuffled block tables: outputs and
+    appended rows are bit-identical (block indexing is pure addressing)."""
+    layers = 2
+    model = syn.flow_model(111, layers)
+    views = pkg.Views()
+    w = views.layers(model)
+    lengths = np.array([5, 40, 333, 257])
+    streams, max_pos = len(lengths), 400
+    table_len = (max_pos + 15) // 16
+    blocks = streams * table_len
+    rng = np.random.default_rng(112)
+    ctx_k = rng.standard_normal((streams, layers, max_pos, 512)).astype(np.float32)
+    ctx_v = rng.standard_normal((streams, layers, max_pos, 512)).astype(np.float32)
+    x = rng.standard_normal((streams, 2, 512)).astype(np.float32)
+    results = []
+    for shuffle in (False, True):
+        bt = Batch(lib, w, layers, streams, max_pos, blocks)
+        ids = np.zeros(blocks, np.int32)
+        assert lib.phonon_kv_pool_alloc(bt.pool, blocks, i32p(ids))
+        ids = np.sort(ids)
+        if shuffle:
+            ids = np.random.default_rng(113).permutation(ids)
+        tables = np.ascontiguousarray(ids.reshape(streams, table_len).astype(np.int32))
+        for s in range(streams):
+            assert lib.phonon_kv_pool_write(bt.pool, i32p(tables[s]), table_len, 0,
+                                            int(lengths[s]), fp(ctx_k[s]), fp(ctx_v[s]), max_pos)
+        pos = lengths.astype(np.uintp)
+        assert lib.phonon_flow_batch_set_streams(
+            bt.batch, streams, pos.ctypes.data_as(ctypes.POINTER(ctypes.c_size_t)), i32p(tables),
+            table_len)
+        outs = []
+        for step in range(2):
+            y = np.zeros((streams, 512), np.float32)
+            assert lib.phonon_flow_batch_step(bt.batch, fp(np.ascontiguousarray(x[:, step])),
+                                              10000.0, fp(y))
+            outs.append(y)
+        rows = []
+        for s in range(streams):
+            k = np.zeros((layers, max_pos, 512), np.float32)
+            v = np.zeros_like(k)
+            assert lib.phonon_kv_pool_read(bt.pool, i32p(tables[s]), table_len, 0,
+                                           int(lengths[s]) + 2, fp(k), fp(v), max_pos)
+            rows.append((k, v))
+        results.append((outs, rows))
+        bt.close()
+    (o1, r1), (o2, r2) = results
+    for a, b in zip(o1, o2):
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    for (k1, v1), (k2, v2) in zip(r1, r2):
+        assert np.array_equal(k1.view(np.uint32), k2.view(np.uint32))
+        assert np.array_equal(v1.view(np.uint32), v2.view(np.uint32))
+
+
+def test_batch_graph_replay_equals_legacy_path(lib, syn, pkg):
+    """The captured-graph batched step (B=1) and the drop-in stack step (no
+    graph) run the same kernels: bit-identical outputs over 6 replays."""
+    model = scaled_model(syn, 121, L9)
+    views = pkg.Views()
+    w = views.layers(model)
+    steps = 6
+    bt = Batch(lib, w, L9, 1, 32, 2)
+    ids = np.zeros(2, np.int32)
+    assert lib.phonon_kv_pool_alloc(bt.pool, 2, i32p(ids))
+    table = np.ascontiguousarray(np.sort(ids).astype(np.int32))
+    pos = np.zeros(1, np.uintp)
+    assert lib.phonon_flow_batch_set_streams(
+        bt.batch, 1, pos.ctypes.data_as(ctypes.POINTER(ctypes.c_size_t)), i32p(table), 2)
+    cache = Cache(lib, 32)
+    rng = np.random.default_rng(122)
+    for step in range(steps):
+        x = rng.standard_normal(512).astype(np.float32)
+        a = np.zeros(512, np.float32)
+        b = np.zeros(512, np.float32)
+        assert lib.phonon_flow_batch_step(bt.batch, fp(x), 10000.0, fp(a))
+        assert lib.phonon_flow_stack_step(w, cache.ref(), step, fp(x), 10000.0, fp(b))
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), step
+    cache.destroy()
+    bt.close()
+
+
+def test_batch_reports_nonfinite_and_uncovered_positions(lib, syn, pkg):
+    layers = 1
+    model = scaled_model(syn, 131, layers)
+    views = pkg.Views()
+    w = views.layers(model)
+    bt = Batch(lib, w, layers, 2, 64, 8)
+    ids = np.zeros(8, np.int32)
+    assert lib.phonon_kv_pool_alloc(bt.pool, 8, i32p(ids))
+    tables = np.ascontiguousarray(np.sort(ids).reshape(2, 4).astype(np.int32))
+    pos = np.array([3, 5], np.uintp)
+    szp = pos.ctypes.data_as(ctypes.POINTER(ctypes.c_size_t))
+    assert lib.phonon_flow_batch_set_streams(bt.batch, 2, szp, i32p(tables), 4)
+    x = np.ones((2, 512), np.float32)
+    y = np.zeros_like(x)
+    assert lib.phonon_flow_batch_step(bt.batch, fp(x), 10000.0, fp(y))
+    x[1, 7] = np.inf
+    assert lib.phonon_flow_batch_set_streams(bt.batch, 2, szp, i32p(tables), 4)
+    assert not lib.phonon_flow_batch_step(bt.batch, fp(x), 10000.0, fp(y))
+    # A table entry outside the pool is reported, never dereferenced.
+    x[1, 7] = 1.0
+    bad = tables.copy()
+    bad[0, 0] = 100000
+    assert lib.phonon_flow_batch_set_streams(bt.batch, 2, szp, i32p(bad), 4)
+    assert not lib.phonon_flow_batch_step(bt.batch, fp(x), 10000.0, fp(y))
+    # Recovers once the table is valid again.
+    assert lib.phonon_flow_batch_set_streams(bt.batch, 2, szp, i32p(tables), 4)
+    assert lib.phonon_flow_batch_step(bt.batch, fp(x), 10000.0, fp(y))
+    # Positions beyond max_positions are refused on the host.
+    far = np.array([64, 0], np.uintp)
+    assert not lib.phonon_flow_batch_set_streams(
+        bt.batch, 2, far.ctypes.data_as(ctypes.POINTER(ctypes.c_size_t)), i32p(tables), 4)
+    bt.close()
