@@ -49,7 +49,9 @@ typedef struct {
 } pgpu_attention_scratch;
 
 /* -- device, memory, streams, events, graphs (pgpu_runtime.hip) -- */
+/* Text of the last failure on this thread (HIP error or failed check). */
 const char *pgpu_last_error(void);
+void pgpu_record_error(const char *what);
 int pgpu_device_init(void);
 int pgpu_device_name(char *buffer, size_t size);
 void *pgpu_malloc(size_t bytes);

@@ -148,6 +148,7 @@ EXPORTS = {
     "phonon_flow_release_weights": (None, [_wp]),
     # phonon_gpu.h
     "pgpu_last_error": (ctypes.c_char_p, []),
+    "pgpu_record_error": (None, [ctypes.c_char_p]),
     "pgpu_device_init": (_i, []),
     "pgpu_device_name": (_i, [ctypes.c_char_p, _sz]),
     "pgpu_malloc": (_vp, [_sz]),

@@ -114,7 +114,10 @@ __global__ __launch_bounds__(256) void k_attention(AttnArgs a) {
     for (int t = 0; t < 4; t++)
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            const float p = score[t][i] == -INFINITY ? 0.0f : expf(score[t][i] - m);
+            // Slots past the context hold whatever the pool held before:
+            // they are skipped, never multiplied by a zero weight.
+            if (score[t][i] == -INFINITY) continue;
+            const float p = expf(score[t][i] - m);
             l += p;
             acc.x = fmaf(p, vr[t][i].x, acc.x);
             acc.y = fmaf(p, vr[t][i].y, acc.y);
@@ -215,7 +218,7 @@ extern "C" int pgpu_attention(void *stream, const float *q, const pgpu_paged_kv 
     if (streams <= 0 || heads <= 0 || heads > kHeads || max_splits <= 0 || layer < 0 ||
         layer >= kv->layers || max_splits > scratch->max_splits ||
         streams > scratch->max_streams)
-        return 0;
+        return bad_arguments("pgpu_attention");
     AttnArgs a;
     a.q = q;
     a.kv = kv->base;
@@ -235,5 +238,5 @@ extern "C" int pgpu_attention(void *stream, const float *q, const pgpu_paged_kv 
     a.status = status;
     hipLaunchKernelGGL(k_attention, dim3(max_splits, heads, streams), dim3(256), 0,
                        (hipStream_t)stream, a);
-    return hipGetLastError() == hipSuccess;
+    return launch_ok("pgpu_attention");
 }

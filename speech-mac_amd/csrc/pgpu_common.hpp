@@ -11,8 +11,29 @@
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+#include <stdio.h>
+
+extern "C" void pgpu_record_error(const char *what);
 
 namespace pgpu {
+
+// Launch bookkeeping of the C-ABI launchers: 1 on success, else 0 with the
+// reason kept for pgpu_last_error().
+inline int launch_ok(const char *name) {
+    const hipError_t e = hipGetLastError();
+    if (e == hipSuccess) return 1;
+    char text[256];
+    snprintf(text, sizeof(text), "%s: launch failed: %s", name, hipGetErrorString(e));
+    pgpu_record_error(text);
+    return 0;
+}
+
+inline int bad_arguments(const char *name) {
+    char text[256];
+    snprintf(text, sizeof(text), "%s: invalid arguments", name);
+    pgpu_record_error(text);
+    return 0;
+}
 
 constexpr int kWidth = 512;      // model width D
 constexpr int kHeads = 8;        // attention heads

@@ -221,47 +221,45 @@ __global__ void k_advance(int32_t *positions, int streams) {
 
 using namespace pgpu;
 
-static inline bool ok_launch() { return hipGetLastError() == hipSuccess; }
-
 extern "C" int pgpu_ln_split(void *stream, const float *x, int streams, const float *w,
                              const float *b, float eps, uint16_t *xs, float *y, int *status) {
-    if (streams <= 0 || (!xs && !y)) return 0;
+    if (streams <= 0 || (!xs && !y)) return bad_arguments(__func__);
     hipLaunchKernelGGL(k_ln_split, dim3((streams + 3) / 4), dim3(256), 0, (hipStream_t)stream,
                        x, streams, w, b, eps, xs, y, status);
-    return ok_launch();
+    return launch_ok(__func__);
 }
 
 extern "C" int pgpu_split_rows(void *stream, const float *x, int streams, int k_cols,
                                uint16_t *xs, int *status) {
-    if (streams <= 0 || k_cols <= 0 || k_cols % 32) return 0;
+    if (streams <= 0 || k_cols <= 0 || k_cols % 32) return bad_arguments(__func__);
     const size_t threads = (size_t)streams * (k_cols / 8);
     hipLaunchKernelGGL(k_split_rows, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0,
                        (hipStream_t)stream, x, streams, k_cols, xs, status);
-    return ok_launch();
+    return launch_ok(__func__);
 }
 
 extern "C" int pgpu_norm_row(void *stream, const float *x, int width, const float *w,
                              const float *b, float eps, int rms, float *y, int *status) {
-    if (width <= 0) return 0;
+    if (width <= 0) return bad_arguments(__func__);
     hipLaunchKernelGGL(k_norm_row, dim3(1), dim3(256), 0, (hipStream_t)stream, x, width, w, b,
                        eps, rms, y, status);
-    return ok_launch();
+    return launch_ok(__func__);
 }
 
 extern "C" int pgpu_gelu(void *stream, float *values, size_t count, int *status) {
     if (!count) return 1;
     hipLaunchKernelGGL(k_gelu, dim3((unsigned)((count + 255) / 256)), dim3(256), 0,
                        (hipStream_t)stream, values, count, status);
-    return ok_launch();
+    return launch_ok(__func__);
 }
 
 extern "C" int pgpu_rope(void *stream, float *values, int heads, int head_width,
                          const float *cos_sin, int *status) {
-    if (heads <= 0 || head_width <= 0 || head_width % 2) return 0;
+    if (heads <= 0 || head_width <= 0 || head_width % 2) return bad_arguments(__func__);
     const int pairs = heads * head_width / 2;
     hipLaunchKernelGGL(k_rope, dim3((pairs + 255) / 256), dim3(256), 0, (hipStream_t)stream,
                        values, heads, head_width, (const float2 *)cos_sin, status);
-    return ok_launch();
+    return launch_ok(__func__);
 }
 
 extern "C" int pgpu_kv_copy(void *stream, const pgpu_paged_kv *kv, const int32_t *table,
@@ -270,15 +268,15 @@ extern "C" int pgpu_kv_copy(void *stream, const pgpu_paged_kv *kv, const int32_t
                             int *status) {
     if (count <= 0 || layers <= 0 || first_layer < 0 || first_layer + layers > kv->layers ||
         first_position < 0 || (layers > 1 && (size_t)count > capacity))
-        return 0;
+        return bad_arguments(__func__);
     hipLaunchKernelGGL(k_kv_copy, dim3(count, layers), dim3(128), 0, (hipStream_t)stream,
                        kv->base, kv->layer_stride, (unsigned)kv->blocks, table, first_position,
                        first_layer, keys, values, capacity, to_contiguous ? 1 : 0, status);
-    return ok_launch();
+    return launch_ok(__func__);
 }
 
 extern "C" int pgpu_fill_normal(void *stream, float *dst, size_t count, uint64_t seed) {
-    if (count % 2) return 0;
+    if (count % 2) return bad_arguments(__func__);
     const size_t pairs = count / 2;
     const size_t grid = (pairs + 255) / 256;
     const size_t max_grid = (size_t)1 << 30;
@@ -286,14 +284,14 @@ extern "C" int pgpu_fill_normal(void *stream, float *dst, size_t count, uint64_t
         const size_t chunk = grid - first < max_grid ? grid - first : max_grid;
         hipLaunchKernelGGL(k_fill_normal, dim3((unsigned)chunk), dim3(256), 0,
                            (hipStream_t)stream, dst, pairs, first * 256, seed);
-        if (!ok_launch()) return 0;
+        if (!launch_ok(__func__)) return 0;
     }
     return 1;
 }
 
 extern "C" int pgpu_advance_positions(void *stream, int32_t *positions, int streams) {
-    if (streams <= 0) return 0;
+    if (streams <= 0) return bad_arguments(__func__);
     hipLaunchKernelGGL(k_advance, dim3((streams + 255) / 256), dim3(256), 0,
                        (hipStream_t)stream, positions, streams);
-    return ok_launch();
+    return launch_ok(__func__);
 }

@@ -205,10 +205,10 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
 template <int EPI, bool Q8>
 static int launch(const GemmArgs &a, hipStream_t stream) {
     if (a.n_rows <= 0 || a.n_rows % 16 || a.k_cols <= 0 || a.k_cols % 32 || a.streams <= 0)
-        return 0;
+        return bad_arguments("pgpu_gemm");
     dim3 grid(a.n_rows / 16, (a.streams + 15) / 16);
     hipLaunchKernelGGL((k_gemm<EPI, Q8>), grid, dim3(256), 0, stream, a);
-    return hipGetLastError() == hipSuccess;
+    return launch_ok("pgpu_gemm");
 }
 
 static GemmArgs base_args(const pgpu_matrix *w, const uint16_t *xs, int streams, int *status) {
@@ -262,7 +262,7 @@ extern "C" int pgpu_gemm_qkv(void *stream, const pgpu_matrix *w, const uint16_t 
                              const int32_t *tables, int table_stride, const int32_t *positions,
                              const float *rope, float *q_out, int *status) {
     if (w->rows != 3 * kWidth || w->columns != kWidth || layer < 0 || layer >= kv->layers)
-        return 0;
+        return bad_arguments("pgpu_gemm_qkv");
     GemmArgs a = base_args(w, xs, streams, status);
     a.q_out = q_out;
     a.kv = kv->base;

@@ -17,6 +17,10 @@ static int check(hipError_t e, const char *what) {
 
 extern "C" const char *pgpu_last_error(void) { return g_error; }
 
+extern "C" void pgpu_record_error(const char *what) {
+    snprintf(g_error, sizeof(g_error), "%s", what ? what : "");
+}
+
 extern "C" int pgpu_device_init(void) {
     static int initialized = 0;
     if (initialized) return 1;

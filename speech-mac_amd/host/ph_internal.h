@@ -19,6 +19,10 @@ void *ph_stream(void);
 void ph_lock(void);
 void ph_unlock(void);
 
+/* Records why a call fails (readable through pgpu_last_error) and returns 0;
+ * a HIP error already recorded by the failing call is kept. */
+int ph_fail(const char *why);
+
 /* Grow-only device scratch owned by the library, for the primitives. */
 void *ph_scratch(int slot, size_t bytes);
 

@@ -4,6 +4,7 @@
 
 #include <math.h>
 #include <pthread.h>
+#include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
 
@@ -26,6 +27,15 @@ int ph_init(void) {
 }
 
 void *ph_stream(void) { return g_stream; }
+
+int ph_fail(const char *why) {
+    char text[256];
+    const char *prior = pgpu_last_error();
+    snprintf(text, sizeof(text), "%s%s%s", why, prior && *prior ? " <- " : "",
+             prior ? prior : "");
+    pgpu_record_error(text);
+    return 0;
+}
 void ph_lock(void) { pthread_mutex_lock(&g_lock); }
 void ph_unlock(void) { pthread_mutex_unlock(&g_lock); }
 

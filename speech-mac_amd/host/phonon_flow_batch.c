@@ -154,7 +154,10 @@ int phonon_kv_pool_create(size_t layers, size_t blocks, PhononKvPool **pool) {
     p->kv.base = pgpu_malloc(layers * p->kv.layer_stride * sizeof(float));
     p->free_ids = malloc(blocks * sizeof(int32_t));
     p->in_use = calloc(blocks, 1);
-    if (!p->kv.base || !p->free_ids || !p->in_use) {
+    /* Zeroed so that never-written slots read as finite values. */
+    if (!p->kv.base || !p->free_ids || !p->in_use ||
+        !pgpu_memset(ph_stream(), p->kv.base, 0, layers * p->kv.layer_stride * sizeof(float)) ||
+        !pgpu_stream_sync(ph_stream())) {
         phonon_kv_pool_destroy(p);
         return 0;
     }
@@ -231,23 +234,30 @@ static int pool_copy(const PhononKvPool *pool, const int32_t *table, size_t tabl
     for (size_t i = first / 16; i < (first + count + 15) / 16; i++)
         if (table[i] < 0 || (size_t)table[i] >= pool->kv.blocks)
             return 0;
+    /* Device staging holds only the requested rows, [layer][count][512]. */
     const size_t layers = (size_t)pool->kv.layers;
-    const size_t bytes = layers * capacity * PH_WIDTH * sizeof(float);
+    const size_t row_bytes = count * PH_WIDTH * sizeof(float);
+    const size_t bytes = layers * row_bytes;
     void *stream = ph_stream();
     float *dk = pgpu_malloc(bytes), *dv = pgpu_malloc(bytes);
     int32_t *dt = pgpu_malloc(table_len * sizeof(int32_t));
     int *status = pgpu_malloc(sizeof(int));
     int ok = dk && dv && dt && status && pgpu_memset(stream, status, 0, sizeof(int)) &&
              pgpu_copy_h2d(stream, dt, table, table_len * sizeof(int32_t));
-    if (ok && !to_host)
-        ok = pgpu_copy_h2d(stream, dk, keys, bytes) && pgpu_copy_h2d(stream, dv, values, bytes);
-    ok = ok && pgpu_kv_copy(stream, &pool->kv, dt, (int)first, (int)count, 0, (int)layers,
-                            dk + first * PH_WIDTH, dv + first * PH_WIDTH, capacity, to_host,
-                            status);
+    for (size_t l = 0; ok && !to_host && l < layers; l++) {
+        const size_t host = (l * capacity + first) * PH_WIDTH, dev = l * count * PH_WIDTH;
+        ok = pgpu_copy_h2d(stream, dk + dev, keys + host, row_bytes) &&
+             pgpu_copy_h2d(stream, dv + dev, values + host, row_bytes);
+    }
+    ok = ok && pgpu_kv_copy(stream, &pool->kv, dt, (int)first, (int)count, 0, (int)layers, dk,
+                            dv, count, to_host, status);
     int st = 1;
     ok = ok && pgpu_copy_d2h(stream, &st, status, sizeof(int)) && st == 0;
-    if (ok && to_host)
-        ok = pgpu_copy_d2h(stream, keys, dk, bytes) && pgpu_copy_d2h(stream, values, dv, bytes);
+    for (size_t l = 0; ok && to_host && l < layers; l++) {
+        const size_t host = (l * capacity + first) * PH_WIDTH, dev = l * count * PH_WIDTH;
+        ok = pgpu_copy_d2h(stream, keys + host, dk + dev, row_bytes) &&
+             pgpu_copy_d2h(stream, values + host, dv + dev, row_bytes);
+    }
     (void)pgpu_stream_sync(stream);
     pgpu_free(dk);
     pgpu_free(dv);

@@ -366,13 +366,13 @@ static int run_position(const PhononFlowModel *model, Mirror *m, PhononKvCache *
     *cancelled = 0;
     const size_t layers = phonon_flow_model_layers(model);
     if (!m->batch && !phonon_flow_batch_create(model, m->pool, 1, m->positions, &m->batch))
-        return 0;
+        return ph_fail("decode step: batch creation failed");
     PhononFlowBatch *b = m->batch;
     void *s = ph_batch_stream(b);
     float *in = ph_batch_in(b), *out = ph_batch_out(b);
     if (!ph_batch_bind_model(b, model) || !ph_batch_set_single(b, position, m->table_dev) ||
         !pgpu_copy_h2d(s, in, input, PHONON_FLOW_WIDTH * sizeof(float)))
-        return 0;
+        return ph_fail("decode step: setting up the stream failed");
     for (size_t l = 0; l < layers; l++) {
         if (cancel && cancel(context)) {
             *cancelled = 1;
@@ -380,7 +380,7 @@ static int run_position(const PhononFlowModel *model, Mirror *m, PhononKvCache *
             return 0;
         }
         if (!ph_batch_enqueue_layers(b, l, 1, pool_first, l ? out : in, out, theta))
-            return 0;
+            return ph_fail("decode step: enqueueing a layer failed");
     }
     if (cancel && cancel(context)) {
         *cancelled = 1;
@@ -388,10 +388,13 @@ static int run_position(const PhononFlowModel *model, Mirror *m, PhononKvCache *
         return 0;
     }
     float *rows = ph_batch_scratch_rows(b);
-    int clean = pgpu_kv_copy(s, ph_pool_kv(m->pool), m->table_dev, (int)position, 1,
-                             (int)pool_first, (int)layers, rows, rows + layers * PH_WIDTH, 1, 1,
-                             ph_batch_status_word(b));
-    clean = ph_batch_status(b) && clean;
+    if (!pgpu_kv_copy(s, ph_pool_kv(m->pool), m->table_dev, (int)position, 1, (int)pool_first,
+                      (int)layers, rows, rows + layers * PH_WIDTH, 1, 1,
+                      ph_batch_status_word(b))) {
+        (void)ph_batch_status(b);
+        return ph_fail("decode step: copying appended rows failed");
+    }
+    const int clean = ph_batch_status(b);
     float *host_rows = malloc(2 * layers * PH_WIDTH * sizeof(float));
     int ok = host_rows &&
              pgpu_copy_d2h(s, host_rows, rows, 2 * layers * PH_WIDTH * sizeof(float)) &&
@@ -404,7 +407,12 @@ static int run_position(const PhononFlowModel *model, Mirror *m, PhononKvCache *
                    PH_WIDTH * sizeof(float));
         }
     free(host_rows);
-    return ok && clean && ph_all_finite(output, PHONON_FLOW_WIDTH);
+    if (!ok)
+        return ph_fail("decode step: reading results failed");
+    if (!clean)
+        return ph_fail("decode step: non-finite value or uncovered position on the device");
+    return ph_all_finite(output, PHONON_FLOW_WIDTH) ||
+           ph_fail("decode step: non-finite output");
 }
 
 /* Model for `layers` layers of `weights`: the registered device copy, or a
@@ -415,8 +423,11 @@ static const PhononFlowModel *model_for(const PhononFlowLayerWeights *weights, s
     const PhononFlowModel *m = ph_registered_model(weights, layers);
     if (m)
         return m;
-    if (!phonon_flow_model_create(weights, layers, owned))
+    if (!phonon_flow_model_create(weights, layers, owned)) {
+        ph_fail("decode step: weights rejected (shape, dtype, size or non-finite value) or "
+                "upload failed");
         return NULL;
+    }
     return *owned;
 }
 

@@ -473,6 +473,38 @@ def test_batch_graph_replay_equals_legacy_path(lib, syn, pkg):
     bt.close()
 
 
+def test_unwritten_pool_slots_never_reach_the_output(lib, oracle, oracle_mod, syn, pkg):
+    """Regression: slots past a stream's context inside its last block may
+    hold anything (here NaN); attention must skip them, not weight them 0."""
+    layers = 1
+    model = scaled_model(syn, 141, layers)
+    om = oracle_for(oracle, oracle_mod, model)
+    views = pkg.Views()
+    w = views.layers(model)
+    max_pos, length = 64, 21
+    bt = Batch(lib, w, layers, 1, max_pos, 4)
+    ids = np.zeros(4, np.int32)
+    assert lib.phonon_kv_pool_alloc(bt.pool, 4, i32p(ids))
+    table = np.ascontiguousarray(np.sort(ids).astype(np.int32))
+    rng = np.random.default_rng(142)
+    k = rng.standard_normal((layers, max_pos, 512)).astype(np.float32)
+    v = rng.standard_normal((layers, max_pos, 512)).astype(np.float32)
+    k[:, length:] = np.nan
+    v[:, length:] = np.nan
+    assert lib.phonon_kv_pool_write(bt.pool, i32p(table), 4, 0, max_pos, fp(k), fp(v), max_pos)
+    pos = np.array([length], np.uintp)
+    assert lib.phonon_flow_batch_set_streams(
+        bt.batch, 1, pos.ctypes.data_as(ctypes.POINTER(ctypes.c_size_t)), i32p(table), 4)
+    x = rng.standard_normal((1, 512)).astype(np.float32)
+    y = np.zeros_like(x)
+    assert lib.phonon_flow_batch_step(bt.batch, fp(x), 10000.0, fp(y)), pkg.last_error(lib)
+    k[:, length:] = 0
+    v[:, length:] = 0
+    ok, ref = om.stack_step(k, v, max_pos, length, x[0])
+    assert ok and helpers.normwise(y[0], ref) <= TOL
+    bt.close()
+
+
 def test_batch_reports_nonfinite_and_uncovered_positions(lib, syn, pkg):
     layers = 1
     model = scaled_model(syn, 131, layers)
