@@ -169,19 +169,17 @@ def attention_roofline(pkg, lib, d, iterations=20):
     tables.upload(d.tables)
     positions = pkg.DeviceBuffer(lib, streams * 4)
     positions.upload(pos.astype(np.int32))
-    out = pkg.DeviceBuffer(lib, streams * 512 * 4)
     slots = streams * 8 * max_splits
     part = pkg.DeviceBuffer(lib, slots * 66 * 4)
-    tickets = pkg.DeviceBuffer(lib, streams * 8 * 4 + 4)
-    lib.pgpu_memset(d.stream, tickets.ptr, 0, streams * 8 * 4 + 4)
-    scratch = pkg.PgpuAttentionScratch(part.ptr, part.ptr + slots * 64 * 4, tickets.ptr,
-                                       streams, max_splits)
-    status = tickets.ptr + streams * 8 * 4
+    words = pkg.DeviceBuffer(lib, 4)
+    lib.pgpu_memset(d.stream, words.ptr, 0, 4)
+    scratch = pkg.PgpuAttentionScratch(part.ptr, part.ptr + slots * 64 * 4, streams, max_splits)
+    status = words.ptr
 
     def launch():
         assert lib.pgpu_attention(d.stream, q.ptr, ctypes.byref(view), 0, tables.ptr,
-                                  d.table_len, positions.ptr, streams, 8, max_splits, None,
-                                  out.ptr, ctypes.byref(scratch), status)
+                                  d.table_len, positions.ptr, streams, 8, max_splits,
+                                  ctypes.byref(scratch), status)
 
     for _ in range(3):
         launch()
@@ -196,7 +194,7 @@ def attention_roofline(pkg, lib, d, iterations=20):
     achieved = kv_bytes / (ms * 1e-3) / 1e9
     st = np.zeros(1, np.int32)
     lib.pgpu_copy_d2h(d.stream, st.ctypes.data, status, 4)
-    for b in (q, tables, positions, out, part, tickets):
+    for b in (q, tables, positions, part, words):
         b.free()
     return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
             "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
@@ -277,7 +275,8 @@ def cpu_baseline(pkg, lib, layers, lengths, seed, budget_s=12.0):
     om = oracle_py.OracleModel(oracle, helpers.oracle_layers(oracle, syn.flow_model(seed, layers)))
     threads = max(1, min(16, os.cpu_count() or 1))
     sample = list(np.asarray(lengths)[:threads])
-    cap = int(max(sample)) + 2
+    max_steps = 8
+    cap = int(max(sample)) + max_steps + 1
     n = len(sample)
     tile = np.random.default_rng(seed).standard_normal(1 << 16).astype(np.float32)
     total = n * layers * cap * 512
@@ -286,7 +285,7 @@ def cpu_baseline(pkg, lib, layers, lengths, seed, budget_s=12.0):
     x = np.random.default_rng(seed + 1).standard_normal((n, 512)).astype(np.float32)
     steps, elapsed = 0, 0.0
     pos = np.array(sample, np.int64)
-    while elapsed < budget_s and steps < 8:
+    while elapsed < budget_s and steps < max_steps:
         t0 = time.perf_counter()
         ok, y = om.stack_step_streams(keys, vals, cap, pos + steps, x, threads)
         elapsed += time.perf_counter() - t0

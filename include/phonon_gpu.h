@@ -39,14 +39,32 @@ typedef struct {
     size_t layer_stride;  /* floats per layer = blocks * 8 * 2 * 16 * 64 */
 } pgpu_paged_kv;
 
-/* Split-attention scratch: partial results and per-(stream, head) tickets.
- * tickets must be zero before the first launch; kernels leave them zero. */
+/* Split-attention partials: for (stream s, head h, split j) at slot
+ * (s*8 + h)*max_splits + j, the unnormalised P.V row (64 floats) and the
+ * split's (max score, sum of exp). */
 typedef struct {
     float *part_acc;      /* (dev) [max_streams*8*max_splits][64] */
     float *part_ml;       /* (dev) [max_streams*8*max_splits][2] */
-    int *tickets;         /* (dev) [max_streams*8] */
     int max_streams, max_splits;
 } pgpu_attention_scratch;
+
+/* The activation operand of a projection, exactly one of:
+ *  split     - split fragments (3 bf16 terms per value) of the input rows,
+ *              with the stream count rounded up to 16 in the allocation;
+ *  ln_rows   - fp32 rows [streams][512], LayerNorm'ed (ln_weight, ln_bias,
+ *              ln_epsilon) inside the projection;
+ *  attn_acc  - split-attention partials (attn_acc/attn_ml as in
+ *              pgpu_attention_scratch, attn_positions and attn_max_splits as
+ *              given to pgpu_attention), merged inside the projection.
+ * ln_rows and attn_acc need a 512-column matrix. */
+typedef struct {
+    const uint16_t *split;
+    const float *ln_rows, *ln_weight, *ln_bias;
+    float ln_epsilon;
+    const float *attn_acc, *attn_ml;
+    const int32_t *attn_positions;
+    int attn_max_splits;
+} pgpu_gemm_input;
 
 /* -- device, memory, streams, events, graphs (pgpu_runtime.hip) -- */
 /* Text of the last failure on this thread (HIP error or failed check). */
@@ -74,27 +92,33 @@ int pgpu_graph_launch(void *exec, void *stream);
 void pgpu_graph_destroy(void *exec);
 int pgpu_check_launch(void);
 
-/* -- projections (pgpu_gemm.hip); xs = split fragments of the input rows,
- * streams rounded up to 16 in its allocation -- */
-int pgpu_gemm_store(void *stream, const pgpu_matrix *w, const uint16_t *xs, int streams,
+/* -- projections (pgpu_gemm.hip): out[s][r] = sum_c x[s][c] * W[r][c] -- */
+/* out = x.W^T (+ bias), rows of ld_out floats. */
+int pgpu_gemm_store(void *stream, const pgpu_matrix *w, const pgpu_gemm_input *x, int streams,
                     const float *bias, float *out, int ld_out, int *status);
-int pgpu_gemm_residual(void *stream, const pgpu_matrix *w, const uint16_t *xs, int streams,
-                       const float *residual, float *out, int *status);
-int pgpu_gemm_gelu_split(void *stream, const pgpu_matrix *w, const uint16_t *xs, int streams,
-                         uint16_t *out_split, int *status);
+/* out = residual + x.W^T, rows of W->rows floats (out may alias residual). */
+int pgpu_gemm_residual(void *stream, const pgpu_matrix *w, const pgpu_gemm_input *x,
+                       int streams, const float *residual, float *out, int *status);
+/* out_split = split fragments of GELU(x.W^T) (the next projection's input). */
+int pgpu_gemm_gelu_split(void *stream, const pgpu_matrix *w, const pgpu_gemm_input *x,
+                         int streams, uint16_t *out_split, int *status);
 /* Fused QKV projection: RoPE on q and k, q scaled by 1/8 into q_out
  * [streams][512], k and v appended to the pool at (layer, positions[s]). */
-int pgpu_gemm_qkv(void *stream, const pgpu_matrix *w, const uint16_t *xs, int streams,
+int pgpu_gemm_qkv(void *stream, const pgpu_matrix *w, const pgpu_gemm_input *x, int streams,
                   const pgpu_paged_kv *kv, int layer, const int32_t *tables, int table_stride,
                   const int32_t *positions, const float *rope, float *q_out, int *status);
 
 /* -- attention (pgpu_attention.hip): stream s attends positions[s]+1 keys;
- * max_splits * 256 must cover every context. Output as split fragments
- * and/or fp32 rows. -- */
+ * max_splits * 256 must cover every context. Writes the per-split partials
+ * into `scratch`; pgpu_attention_merge (or a projection with an attn_acc
+ * input) turns them into the attention output. -- */
 int pgpu_attention(void *stream, const float *q, const pgpu_paged_kv *kv, int layer,
                    const int32_t *tables, int table_stride, const int32_t *positions,
-                   int streams, int heads, int max_splits, uint16_t *out_split, float *out,
+                   int streams, int heads, int max_splits,
                    const pgpu_attention_scratch *scratch, int *status);
+int pgpu_attention_merge(void *stream, const pgpu_attention_scratch *scratch,
+                         const int32_t *positions, int streams, int heads, int max_splits,
+                         float *out, uint16_t *out_split, int *status);
 
 /* -- rows and elements (pgpu_elementwise.hip) -- */
 int pgpu_ln_split(void *stream, const float *x, int streams, const float *w, const float *b,

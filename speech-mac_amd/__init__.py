@@ -77,8 +77,13 @@ class PgpuPagedKv(ctypes.Structure):
 
 
 class PgpuAttentionScratch(ctypes.Structure):
-    _fields_ = [("part_acc", _vp), ("part_ml", _vp), ("tickets", _vp),
-                ("max_streams", _i), ("max_splits", _i)]
+    _fields_ = [("part_acc", _vp), ("part_ml", _vp), ("max_streams", _i), ("max_splits", _i)]
+
+
+class PgpuGemmInput(ctypes.Structure):
+    _fields_ = [("split", _vp), ("ln_rows", _vp), ("ln_weight", _vp), ("ln_bias", _vp),
+                ("ln_epsilon", _f), ("attn_acc", _vp), ("attn_ml", _vp),
+                ("attn_positions", _vp), ("attn_max_splits", _i)]
 
 
 CANCEL_POLL = ctypes.CFUNCTYPE(ctypes.c_int, _vp)
@@ -88,6 +93,7 @@ _viewp = ctypes.POINTER(PhononTensorView)
 _mp = ctypes.POINTER(PgpuMatrix)
 _kvp = ctypes.POINTER(PgpuPagedKv)
 _scp = ctypes.POINTER(PgpuAttentionScratch)
+_gip = ctypes.POINTER(PgpuGemmInput)
 _pp = ctypes.POINTER(_vp)
 
 # Every function declared in include/*.h: name -> (restype, argtypes).
@@ -169,12 +175,12 @@ EXPORTS = {
     "pgpu_graph_launch": (_i, [_vp, _vp]),
     "pgpu_graph_destroy": (None, [_vp]),
     "pgpu_check_launch": (_i, []),
-    "pgpu_gemm_store": (_i, [_vp, _mp, _vp, _i, _vp, _vp, _i, _vp]),
-    "pgpu_gemm_residual": (_i, [_vp, _mp, _vp, _i, _vp, _vp, _vp]),
-    "pgpu_gemm_gelu_split": (_i, [_vp, _mp, _vp, _i, _vp, _vp]),
-    "pgpu_gemm_qkv": (_i, [_vp, _mp, _vp, _i, _kvp, _i, _vp, _i, _vp, _vp, _vp, _vp]),
-    "pgpu_attention": (_i, [_vp, _vp, _kvp, _i, _vp, _i, _vp, _i, _i, _i, _vp, _vp, _scp,
-                            _vp]),
+    "pgpu_gemm_store": (_i, [_vp, _mp, _gip, _i, _vp, _vp, _i, _vp]),
+    "pgpu_gemm_residual": (_i, [_vp, _mp, _gip, _i, _vp, _vp, _vp]),
+    "pgpu_gemm_gelu_split": (_i, [_vp, _mp, _gip, _i, _vp, _vp]),
+    "pgpu_gemm_qkv": (_i, [_vp, _mp, _gip, _i, _kvp, _i, _vp, _i, _vp, _vp, _vp, _vp]),
+    "pgpu_attention": (_i, [_vp, _vp, _kvp, _i, _vp, _i, _vp, _i, _i, _i, _scp, _vp]),
+    "pgpu_attention_merge": (_i, [_vp, _scp, _vp, _i, _i, _i, _vp, _vp, _vp]),
     "pgpu_ln_split": (_i, [_vp, _vp, _i, _vp, _vp, _f, _vp, _vp, _vp]),
     "pgpu_split_rows": (_i, [_vp, _vp, _i, _i, _vp, _vp]),
     "pgpu_norm_row": (_i, [_vp, _vp, _i, _vp, _vp, _f, _i, _vp, _vp]),

@@ -10,10 +10,14 @@
 // Work-group (split j, head h, stream s) covers keys [256j, 256j+256) of
 // stream s: wave w takes blocks 16j+4w .. 16j+4w+3. Each lane loads float4s
 // at tile offsets 256*i + 4*lane (i = 0..3), i.e. key 4i + lane/16, dims
-// 4*(lane%16) .. +3: every load instruction reads 1 KB contiguous.
-// Scores reduce over the 16 lanes of a key (DPP row reductions).
-// Splits of one (s, h) are merged by the last work-group to finish (atomic
-// ticket), which also resets the ticket so the kernel can be replayed.
+// 4*(lane%16) .. +3: every load instruction reads 1 KB contiguous, and all
+// 32 loads of a wave are in flight together.
+//
+// Each work-group writes its split's (max, sum, unnormalised P.V) partial;
+// the splits are merged by whoever consumes the output (the out-projection
+// prologue in the decode step, or k_attention_merge). There is no
+// cross-work-group handshake: on gfx950 an agent-scope fence writes back and
+// invalidates the whole L2 and costs far more than a separate merge.
 #include "pgpu_common.hpp"
 #include "phonon_gpu.h"
 
@@ -29,11 +33,8 @@ struct AttnArgs {
     int table_stride;
     const int32_t *positions; // keys attended = positions[s] + 1
     int streams, max_splits;
-    uint16_t *out_split;      // optional: split fragments, 16 blocks per row
-    float *out;               // optional: [streams][512]
     float *part_acc;          // [streams*8*max_splits][64]
     float *part_ml;           // [streams*8*max_splits][2]
-    int *tickets;             // [streams*8], zero between launches
     int *status;
 };
 
@@ -56,36 +57,50 @@ __global__ __launch_bounds__(256) void k_attention(AttnArgs a) {
         return;
     }
     if (split * kSplitKeys >= count) return;
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    // The wave index is uniform: readfirstlane lets the block ids below come
+    // from scalar loads, so no vector-load wait sits between the K/V loads.
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
     const int krow = lane >> 4, dcol = lane & 15;
 
     const float4 q = *(const float4 *)(a.q + (size_t)s * kWidth + head * kHeadDim + dcol * 4);
-    const int32_t *table = a.tables + (size_t)s * a.table_stride;
+    const int32_t *__restrict__ table = a.tables + (size_t)s * a.table_stride;
     const float *layer_kv = a.kv + (size_t)a.layer * a.layer_stride;
     const int first_block = split * 16 + wave * 4;
+    const int stream_blocks = (count + kBlockPos - 1) / kBlockPos;
+    const int last_block = min(first_block + 3, stream_blocks - 1);  // < first_block: no keys
 
-    float4 kr[4][4], vr[4][4];
+    // Block ids first (uniform), then every K/V load of the wave at once.
+    // Blocks past the context re-read the last valid block (their keys are
+    // masked below); an id outside the pool is flagged and replaced by 0.
+    int ids[4];
     bool bad_block = false;
 #pragma unroll
     for (int t = 0; t < 4; t++) {
-        const int b = first_block + t;
-        const bool valid = b * kBlockPos < count && (unsigned)table[b] < a.blocks;
-        bad_block |= b * kBlockPos < count && !valid;
-        if (valid) {
-            const float *tile =
-                layer_kv + ((size_t)table[b] * kHeads + head) * 2048 + lane * 4;
+        const int b = min(first_block + t, max(last_block, first_block));
+        const int id = last_block >= first_block ? table[b] : 0;
+        bad_block |= (unsigned)id >= a.blocks;
+        ids[t] = (unsigned)id < a.blocks ? id : 0;
+    }
+    float4 kr[4][4], vr[4][4];
+    if (last_block >= first_block) {
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            const float *tile = layer_kv + ((size_t)ids[t] * kHeads + head) * 2048 + lane * 4;
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 kr[t][i] = *(const float4 *)(tile + i * 256);
                 vr[t][i] = *(const float4 *)(tile + 1024 + i * 256);
             }
-        } else {
+        }
+    } else {
+#pragma unroll
+        for (int t = 0; t < 4; t++)
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 kr[t][i] = make_float4(0.f, 0.f, 0.f, 0.f);
                 vr[t][i] = make_float4(0.f, 0.f, 0.f, 0.f);
             }
-        }
     }
     if (bad_block && lane == 0) atomicOr(a.status, 2);
 
@@ -163,48 +178,43 @@ __global__ __launch_bounds__(256) void k_attention(AttnArgs a) {
         aa.z = fmaf(x.z, f, aa.z);
         aa.w = fmaf(x.w, f, aa.w);
     }
+    const size_t slot = ((size_t)s * kHeads + head) * a.max_splits + split;
+    *(float4 *)(a.part_acc + slot * 64 + lane * 4) = aa;
+    if (lane == 0) *(float2 *)(a.part_ml + slot * 2) = make_float2(mm, ll);
+}
 
-    const int sh = s * kHeads + head;
-    if (nsplit > 1) {
-        const size_t slot = (size_t)sh * a.max_splits + split;
-        *(float4 *)(a.part_acc + slot * 64 + lane * 4) = aa;
-        if (lane == 0) {
-            a.part_ml[slot * 2] = mm;
-            a.part_ml[slot * 2 + 1] = ll;
-        }
-        __threadfence();
-        int ticket = 0;
-        if (lane == 0) ticket = atomicAdd(&a.tickets[sh], 1);
-        ticket = __shfl(ticket, 0);
-        if (ticket != nsplit - 1) return;
-        __threadfence();
-        // Last split: merge all splits of (s, head) in split order.
-        const size_t first = (size_t)sh * a.max_splits;
-        mm = -INFINITY;
-        for (int j = 0; j < nsplit; j++) mm = fmaxf(mm, a.part_ml[(first + j) * 2]);
-        ll = 0.0f;
-        aa = make_float4(0.f, 0.f, 0.f, 0.f);
-        for (int j = 0; j < nsplit; j++) {
-            const float f = expf(a.part_ml[(first + j) * 2] - mm);
-            ll = fmaf(a.part_ml[(first + j) * 2 + 1], f, ll);
-            const float4 x = *(const float4 *)(a.part_acc + (first + j) * 64 + lane * 4);
-            aa.x = fmaf(x.x, f, aa.x);
-            aa.y = fmaf(x.y, f, aa.y);
-            aa.z = fmaf(x.z, f, aa.z);
-            aa.w = fmaf(x.w, f, aa.w);
-        }
-        if (lane == 0) atomicExch(&a.tickets[sh], 0);
+// Merge of the split partials into fp32 rows and/or split fragments, one
+// wave per (head, stream): lane d produces dimension d.
+__global__ __launch_bounds__(64) void k_attention_merge(const float *__restrict__ part_acc,
+                                                        const float *__restrict__ part_ml,
+                                                        const int32_t *__restrict__ positions,
+                                                        int max_splits, float *out,
+                                                        uint16_t *out_split, int *status) {
+    const int head = blockIdx.x, s = blockIdx.y, d = threadIdx.x;
+    const int count = positions[s] + 1;
+    const int nsplit = min((count + kSplitKeys - 1) / kSplitKeys, max_splits);
+    const size_t first = ((size_t)s * kHeads + head) * max_splits;
+    float mx = -INFINITY;
+    for (int j = 0; j < nsplit; j++) mx = fmaxf(mx, part_ml[(first + j) * 2]);
+    float total = 0.0f, acc = 0.0f;
+    for (int j = 0; j < nsplit; j++) {
+        const float f = expf(part_ml[(first + j) * 2] - mx);
+        total = fmaf(part_ml[(first + j) * 2 + 1], f, total);
+        acc = fmaf(part_acc[(first + j) * 64 + d], f, acc);
     }
-
-    const float inv = 1.0f / ll;
-    float o[4] = {aa.x * inv, aa.y * inv, aa.z * inv, aa.w * inv};
-    bool bad = !(ll > 0.0f) || !isfinite(ll);
-#pragma unroll
-    for (int r = 0; r < 4; r++) bad |= !isfinite(o[r]);
-    const int col = head * kHeadDim + lane * 4;
-    if (a.out) *(float4 *)(a.out + (size_t)s * kWidth + col) = make_float4(o[0], o[1], o[2], o[3]);
-    if (a.out_split) store_split<4>(a.out_split, s, col, kWidth / 32, o);
-    if (bad) atomicOr(a.status, 1);
+    const float o = acc * (1.0f / total);
+    const bool bad = !(total > 0.0f) || !isfinite(total) || !isfinite(o);
+    const int col = head * kHeadDim + d;
+    if (out) out[(size_t)s * kWidth + col] = o;
+    if (out_split) {
+        uint16_t h, m, l;
+        split3(o, h, m, l);
+        const size_t base = split_index(s, col, 0, kWidth / 32);
+        out_split[base] = h;
+        out_split[base + 512] = m;
+        out_split[base + 1024] = l;
+    }
+    flag_nonfinite(status, bad);
 }
 
 }  // namespace pgpu
@@ -213,8 +223,8 @@ using namespace pgpu;
 
 extern "C" int pgpu_attention(void *stream, const float *q, const pgpu_paged_kv *kv, int layer,
                               const int32_t *tables, int table_stride, const int32_t *positions,
-                              int streams, int heads, int max_splits, uint16_t *out_split,
-                              float *out, const pgpu_attention_scratch *scratch, int *status) {
+                              int streams, int heads, int max_splits,
+                              const pgpu_attention_scratch *scratch, int *status) {
     if (streams <= 0 || heads <= 0 || heads > kHeads || max_splits <= 0 || layer < 0 ||
         layer >= kv->layers || max_splits > scratch->max_splits ||
         streams > scratch->max_streams)
@@ -230,13 +240,24 @@ extern "C" int pgpu_attention(void *stream, const float *q, const pgpu_paged_kv 
     a.positions = positions;
     a.streams = streams;
     a.max_splits = max_splits;
-    a.out_split = out_split;
-    a.out = out;
     a.part_acc = scratch->part_acc;
     a.part_ml = scratch->part_ml;
-    a.tickets = scratch->tickets;
     a.status = status;
     hipLaunchKernelGGL(k_attention, dim3(max_splits, heads, streams), dim3(256), 0,
                        (hipStream_t)stream, a);
     return launch_ok("pgpu_attention");
+}
+
+extern "C" int pgpu_attention_merge(void *stream, const pgpu_attention_scratch *scratch,
+                                    const int32_t *positions, int streams, int heads,
+                                    int max_splits, float *out, uint16_t *out_split,
+                                    int *status) {
+    if (streams <= 0 || heads <= 0 || heads > kHeads || max_splits <= 0 ||
+        max_splits > scratch->max_splits || streams > scratch->max_streams ||
+        (!out && !out_split))
+        return bad_arguments("pgpu_attention_merge");
+    hipLaunchKernelGGL(k_attention_merge, dim3(heads, streams), dim3(64), 0,
+                       (hipStream_t)stream, scratch->part_acc, scratch->part_ml, positions,
+                       max_splits, out, out_split, status);
+    return launch_ok("pgpu_attention_merge");
 }

@@ -1,8 +1,12 @@
 // Projection kernel of the decode step: Y[s][n] = sum_k X[s][k] * W[n][k]
-// for B streams, on v_mfma_f32_16x16x32_bf16.
+// for B streams, on v_mfma_f32_16x16x32_bf16, with the producer of X fused
+// in front and the consumer of Y fused behind.
 //
 // Replaces the fp32 SGEMM of phonon_linear (src/phonon_transformer.c:253-313)
-// and the row dot of phonon_q8_matvec (src/phonon_q8.c:36-92).
+// and the row dot of phonon_q8_matvec (src/phonon_q8.c:36-92); with its
+// prologues/epilogues it also carries LayerNorm (:153-185), the attention
+// output normalisation (:395-403), RoPE + KV append (:425-427), GELU
+// (:202-216) and the residual adds (:440-451) of phonon_flow_layer_step.
 //
 // Operands
 //   W  Q8_0: int8 values in MFMA A-fragment order, one 512-byte record per
@@ -10,7 +14,10 @@
 //      8*(l/16) .. +7. The per-(row, block) fp16 scales sit in a separate
 //      plane [tile][block][16]. Bytes per weight: 1 + 2/32 (same as Q8_0).
 //   W  BF16: the same fragment order with bf16 values (1024-byte records).
-//   X  split fragments (pgpu_common.hpp): three bf16 terms per activation.
+//   X  split fragments (pgpu_common.hpp): three bf16 terms per activation,
+//      read from global memory (SRC_SPLIT) or built in LDS by the prologue:
+//      SRC_LN   LayerNorm of fp32 rows [streams][512];
+//      SRC_ATTN merge of the split-attention partials (max, sum, acc).
 // Arithmetic
 //   Q8: per 32-column block, c = W_q8 . (X_hi + X_mid + X_lo) by three MFMAs
 //   from zero (int8 and bf16 terms multiply exactly), then acc += scale*c,
@@ -27,10 +34,17 @@
 
 namespace pgpu {
 
+enum Source { SRC_SPLIT = 0, SRC_LN = 1, SRC_ATTN = 2 };
 enum Epilogue { EPI_STORE = 0, EPI_RESIDUAL = 1, EPI_GELU_SPLIT = 2, EPI_QKV = 3 };
 
 struct GemmArgs {
-    const uint16_t *xs;       // split-fragment input, k_cols/32 blocks per row
+    const uint16_t *xs;       // SRC_SPLIT: split fragments, k_cols/32 blocks per row
+    const float *ln_x;        // SRC_LN: [streams][512] rows to normalise
+    const float *ln_w, *ln_b; // SRC_LN: [512] affine
+    float ln_eps;
+    const float *part_acc;    // SRC_ATTN: [streams*8*max_splits][64]
+    const float *part_ml;     // SRC_ATTN: [streams*8*max_splits][2]
+    int max_splits;
     const void *w;            // weight fragments
     const uint16_t *wscale;   // Q8 only
     int n_rows, k_cols, streams;
@@ -47,7 +61,7 @@ struct GemmArgs {
     int layer;
     const int32_t *tables;
     int table_stride;
-    const int32_t *positions;
+    const int32_t *positions; // QKV and SRC_ATTN
     const float2 *rope;       // [8192][32] (cos, sin)
     int *status;
 };
@@ -70,45 +84,213 @@ __device__ inline float half_to_float(uint32_t bits16) {
     return __half2float(__ushort_as_half((unsigned short)bits16));
 }
 
-template <int EPI, bool Q8>
+// Writes 32 activations of stream n (0..15 in the tile), columns
+// [32kb, 32kb+32), into an LDS fragment buffer laid out [kb][part][512].
+__device__ inline void lds_store_block(uint16_t *bsh, int n, int kb, const float *v) {
+#pragma unroll
+    for (int g = 0; g < 4; g++) {
+        uint16_t h[8], m[8], l[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) split3(v[g * 8 + i], h[i], m[i], l[i]);
+        uint16_t *rec = bsh + kb * 1536 + (g * 16 + n) * 8;
+#pragma unroll
+        for (int p = 0; p < 3; p++) {
+            const uint16_t *src = p == 0 ? h : (p == 1 ? m : l);
+            uint4 q;
+            q.x = src[0] | (uint32_t)src[1] << 16;
+            q.y = src[2] | (uint32_t)src[3] << 16;
+            q.z = src[4] | (uint32_t)src[5] << 16;
+            q.w = src[6] | (uint32_t)src[7] << 16;
+            *(uint4 *)(rec + p * 512) = q;
+        }
+    }
+}
+
+// LayerNorm of 16 streams' 512-wide rows into LDS split fragments. Thread
+// (n = tid/16, j = tid%16) owns columns [32j, 32j+32) of stream n; the 16
+// threads of a stream are 16 adjacent lanes of one wave. Two-pass fp32
+// moments; y = ((x - mean) * rstd) * w + b unfused, as the reference writes
+// it (src/phonon_transformer.c:179-183).
+__device__ inline bool prologue_ln(const GemmArgs &a, int st, uint16_t *bsh) {
+    const int n = threadIdx.x >> 4, j = threadIdx.x & 15;
+    const int s = st * 16 + n;
+    float v[32];
+    const bool live = s < a.streams;
+    if (live) {
+        const float4 *row = (const float4 *)(a.ln_x + (size_t)s * kWidth + j * 32);
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const float4 x = row[i];
+            v[4 * i] = x.x;
+            v[4 * i + 1] = x.y;
+            v[4 * i + 2] = x.z;
+            v[4 * i + 3] = x.w;
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 32; i++) v[i] = 0.0f;
+    }
+    float sum = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 32; i++) sum += v[i];
+#pragma unroll
+    for (int o = 1; o < 16; o <<= 1) sum += __shfl_xor(sum, o);
+    const float mean = sum * (1.0f / kWidth);
+    float sq = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 32; i++) {
+        const float c = v[i] - mean;
+        sq = fmaf(c, c, sq);
+    }
+#pragma unroll
+    for (int o = 1; o < 16; o <<= 1) sq += __shfl_xor(sq, o);
+    const float rstd = 1.0f / sqrtf(sq * (1.0f / kWidth) + a.ln_eps);
+    bool bad = false;
+    const float4 *w4 = (const float4 *)(a.ln_w + j * 32);
+    const float4 *b4 = (const float4 *)(a.ln_b + j * 32);
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const float4 w = w4[i], b = b4[i];
+        const float ws[4] = {w.x, w.y, w.z, w.w}, bs[4] = {b.x, b.y, b.z, b.w};
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            float &y = v[4 * i + c];
+            y = __fadd_rn(__fmul_rn(__fmul_rn(__fsub_rn(y, mean), rstd), ws[c]), bs[c]);
+            bad |= live && !isfinite(y);
+        }
+    }
+    if (!live) {
+#pragma unroll
+        for (int i = 0; i < 32; i++) v[i] = 0.0f;
+    }
+    lds_store_block(bsh, n, j, v);
+    return bad;
+}
+
+// Merges the split-attention partials of 16 streams x 8 heads into LDS split
+// fragments: out = sum_j acc_j e^(m_j - M) / sum_j l_j e^(m_j - M), M = max m_j
+// (the normalisation after P.V of src/phonon_transformer.c:395-403, merged
+// over splits in split order). Thread (n = tid/16, head h = (tid/2)%8,
+// half = tid%2) produces 32 dims = column block 2h + half of stream n.
+__device__ inline bool prologue_attn(const GemmArgs &a, int st, uint16_t *bsh) {
+    const int n = threadIdx.x >> 4, h = (threadIdx.x >> 1) & 7, half = threadIdx.x & 1;
+    const int s = st * 16 + n;
+    float v[32];
+#pragma unroll
+    for (int i = 0; i < 32; i++) v[i] = 0.0f;
+    bool bad = false;
+    if (s < a.streams) {
+        const int count = a.positions[s] + 1;
+        const int nsplit = min((count + kSplitKeys - 1) / kSplitKeys, a.max_splits);
+        const size_t first = ((size_t)s * kHeads + h) * a.max_splits;
+        float mx = -INFINITY;
+        for (int j = 0; j < nsplit; j++) mx = fmaxf(mx, a.part_ml[(first + j) * 2]);
+        float total = 0.0f;
+        for (int j = 0; j < nsplit; j++) {
+            const float f = expf(a.part_ml[(first + j) * 2] - mx);
+            total = fmaf(a.part_ml[(first + j) * 2 + 1], f, total);
+            const float4 *acc = (const float4 *)(a.part_acc + (first + j) * 64 + half * 32);
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const float4 x = acc[i];
+                v[4 * i] = fmaf(x.x, f, v[4 * i]);
+                v[4 * i + 1] = fmaf(x.y, f, v[4 * i + 1]);
+                v[4 * i + 2] = fmaf(x.z, f, v[4 * i + 2]);
+                v[4 * i + 3] = fmaf(x.w, f, v[4 * i + 3]);
+            }
+        }
+        bad = !(total > 0.0f) || !isfinite(total);
+        const float inv = 1.0f / total;
+#pragma unroll
+        for (int i = 0; i < 32; i++) {
+            v[i] *= inv;
+            bad |= !isfinite(v[i]);
+        }
+        if (bad) {
+#pragma unroll
+            for (int i = 0; i < 32; i++) v[i] = 0.0f;
+        }
+    }
+    lds_store_block(bsh, n, 2 * h + half, v);
+    return bad;
+}
+
+template <int SRC, int EPI, bool Q8, int CH>
 __global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
     const int tile = blockIdx.x, st = blockIdx.y;
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    // Uniform per wave (readfirstlane): the block loop below is scalar control.
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
     const int kbn = a.k_cols >> 5;
     const int per_wave = (kbn + 3) >> 2;
     const int kb_begin = wave * per_wave;
     const int kb_end = min(kbn, kb_begin + per_wave);
 
-    const uint16_t *xs = a.xs + (size_t)st * kbn * 1536 + lane * 8;
+    // Prologue-built operands hold 16 streams x 512 columns x 3 terms (48 KB).
+    __shared__ uint16_t bsh[SRC == SRC_SPLIT ? 8 : 16 * 1536];
+    bool bad_in = false;
+    if constexpr (SRC == SRC_LN) bad_in = prologue_ln(a, st, bsh);
+    if constexpr (SRC == SRC_ATTN) bad_in = prologue_attn(a, st, bsh);
+    if constexpr (SRC != SRC_SPLIT) {
+        flag_nonfinite(a.status, bad_in);
+        __syncthreads();
+    }
+
+    const uint16_t *xs = SRC == SRC_SPLIT ? a.xs + (size_t)st * kbn * 1536 + lane * 8
+                                          : bsh + lane * 8;
     f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-    if constexpr (Q8) {
-        const int8_t *wq = (const int8_t *)a.w + (size_t)tile * kbn * 512 + lane * 8;
-        const uint16_t *ws = a.wscale + (size_t)tile * kbn * 16 + (lane >> 4) * 4;
-        for (int kb = kb_begin; kb < kb_end; kb++) {
-            const bf16x8 wa = q8_to_bf16(*(const uint2 *)(wq + (size_t)kb * 512));
-            const uint2 sc = *(const uint2 *)(ws + (size_t)kb * 16);
-            const bf16x8 xh = *(const bf16x8 *)(xs + (size_t)kb * 1536);
-            const bf16x8 xm = *(const bf16x8 *)(xs + (size_t)kb * 1536 + 512);
-            const bf16x8 xl = *(const bf16x8 *)(xs + (size_t)kb * 1536 + 1024);
-            f32x4 c = {0.0f, 0.0f, 0.0f, 0.0f};
-            c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wa, xh, c, 0, 0, 0);
-            c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wa, xm, c, 0, 0, 0);
-            c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wa, xl, c, 0, 0, 0);
-            acc[0] = fmaf(half_to_float(sc.x & 0xffffu), c[0], acc[0]);
-            acc[1] = fmaf(half_to_float(sc.x >> 16), c[1], acc[1]);
-            acc[2] = fmaf(half_to_float(sc.y & 0xffffu), c[2], acc[2]);
-            acc[3] = fmaf(half_to_float(sc.y >> 16), c[3], acc[3]);
+    // Chunks of CH blocks: all loads of a chunk are issued before its MFMAs
+    // (past the wave's range the last block is re-read and not used).
+    for (int kb0 = kb_begin; kb0 < kb_end; kb0 += CH) {
+        bf16x8 xh[CH], xm[CH], xl[CH];
+#pragma unroll
+        for (int u = 0; u < CH; u++) {
+            const size_t kb = (size_t)min(kb0 + u, kb_end - 1);
+            xh[u] = *(const bf16x8 *)(xs + kb * 1536);
+            xm[u] = *(const bf16x8 *)(xs + kb * 1536 + 512);
+            xl[u] = *(const bf16x8 *)(xs + kb * 1536 + 1024);
         }
-    } else {
-        const uint16_t *wb = (const uint16_t *)a.w + (size_t)tile * kbn * 512 + lane * 8;
-        for (int kb = kb_begin; kb < kb_end; kb++) {
-            const bf16x8 wa = *(const bf16x8 *)(wb + (size_t)kb * 512);
-            const bf16x8 xh = *(const bf16x8 *)(xs + (size_t)kb * 1536);
-            const bf16x8 xm = *(const bf16x8 *)(xs + (size_t)kb * 1536 + 512);
-            const bf16x8 xl = *(const bf16x8 *)(xs + (size_t)kb * 1536 + 1024);
-            acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wa, xh, acc, 0, 0, 0);
-            acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wa, xm, acc, 0, 0, 0);
-            acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wa, xl, acc, 0, 0, 0);
+        if constexpr (Q8) {
+            const int8_t *wq = (const int8_t *)a.w + (size_t)tile * kbn * 512 + lane * 8;
+            const uint16_t *ws = a.wscale + (size_t)tile * kbn * 16 + (lane >> 4) * 4;
+            uint2 raw[CH], sc[CH];
+#pragma unroll
+            for (int u = 0; u < CH; u++) {
+                const size_t kb = (size_t)min(kb0 + u, kb_end - 1);
+                raw[u] = *(const uint2 *)(wq + kb * 512);
+                sc[u] = *(const uint2 *)(ws + kb * 16);
+            }
+            // No control flow between the loads and the MFMAs (the scheduler
+            // then keeps the loads together): a re-read block gets scale 0.
+#pragma unroll
+            for (int u = 0; u < CH; u++) {
+                const bool used = kb0 + u < kb_end;
+                const bf16x8 wa = q8_to_bf16(raw[u]);
+                f32x4 c = {0.0f, 0.0f, 0.0f, 0.0f};
+                c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wa, xh[u], c, 0, 0, 0);
+                c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wa, xm[u], c, 0, 0, 0);
+                c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wa, xl[u], c, 0, 0, 0);
+                const uint2 s = used ? sc[u] : make_uint2(0u, 0u);
+                acc[0] = fmaf(half_to_float(s.x & 0xffffu), c[0], acc[0]);
+                acc[1] = fmaf(half_to_float(s.x >> 16), c[1], acc[1]);
+                acc[2] = fmaf(half_to_float(s.y & 0xffffu), c[2], acc[2]);
+                acc[3] = fmaf(half_to_float(s.y >> 16), c[3], acc[3]);
+            }
+        } else {
+            const uint16_t *wb = (const uint16_t *)a.w + (size_t)tile * kbn * 512 + lane * 8;
+            bf16x8 wa[CH];
+#pragma unroll
+            for (int u = 0; u < CH; u++) {
+                const size_t kb = (size_t)min(kb0 + u, kb_end - 1);
+                wa[u] = *(const bf16x8 *)(wb + kb * 512);
+            }
+#pragma unroll
+            for (int u = 0; u < CH; u++) {
+                if (kb0 + u >= kb_end) wa[u] = bf16x8{};  // re-read block adds 0
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wa[u], xh[u], acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wa[u], xm[u], acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wa[u], xl[u], acc, 0, 0, 0);
+            }
         }
     }
 
@@ -202,68 +384,107 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
     flag_nonfinite(a.status, bad);
 }
 
-template <int EPI, bool Q8>
+template <int SRC, int EPI, bool Q8>
 static int launch(const GemmArgs &a, hipStream_t stream) {
-    if (a.n_rows <= 0 || a.n_rows % 16 || a.k_cols <= 0 || a.k_cols % 32 || a.streams <= 0)
+    if (a.n_rows <= 0 || a.n_rows % 16 || a.k_cols <= 0 || a.k_cols % 32 || a.streams <= 0 ||
+        (SRC != SRC_SPLIT && a.k_cols != kWidth))
         return bad_arguments("pgpu_gemm");
     dim3 grid(a.n_rows / 16, (a.streams + 15) / 16);
-    hipLaunchKernelGGL((k_gemm<EPI, Q8>), grid, dim3(256), 0, stream, a);
+    // Up to 4 column blocks per wave (K <= 512): one chunk of 4; else chunks of 8.
+    if (a.k_cols <= 512)
+        hipLaunchKernelGGL((k_gemm<SRC, EPI, Q8, 4>), grid, dim3(256), 0, stream, a);
+    else
+        hipLaunchKernelGGL((k_gemm<SRC, EPI, Q8, 8>), grid, dim3(256), 0, stream, a);
     return launch_ok("pgpu_gemm");
 }
 
-static GemmArgs base_args(const pgpu_matrix *w, const uint16_t *xs, int streams, int *status) {
-    GemmArgs a = {};
-    a.xs = xs;
+template <int EPI>
+static int dispatch(const GemmArgs &a, int q8, hipStream_t stream) {
+    const int src = a.ln_x ? SRC_LN : (a.part_acc ? SRC_ATTN : SRC_SPLIT);
+    if (src == SRC_LN)
+        return q8 ? launch<SRC_LN, EPI, true>(a, stream) : launch<SRC_LN, EPI, false>(a, stream);
+    if (src == SRC_ATTN)
+        return q8 ? launch<SRC_ATTN, EPI, true>(a, stream)
+                  : launch<SRC_ATTN, EPI, false>(a, stream);
+    return q8 ? launch<SRC_SPLIT, EPI, true>(a, stream)
+              : launch<SRC_SPLIT, EPI, false>(a, stream);
+}
+
+// Fills the operand-source fields from a pgpu_gemm_input.
+static bool set_input(GemmArgs &a, const pgpu_gemm_input *in) {
+    if (!in) return false;
+    const int kinds = (in->split != nullptr) + (in->ln_rows != nullptr) +
+                      (in->attn_acc != nullptr);
+    if (kinds != 1) return false;
+    a.xs = in->split;
+    a.ln_x = in->ln_rows;
+    a.ln_w = in->ln_weight;
+    a.ln_b = in->ln_bias;
+    a.ln_eps = in->ln_epsilon;
+    a.part_acc = in->attn_acc;
+    a.part_ml = in->attn_ml;
+    a.max_splits = in->attn_max_splits;
+    if (a.ln_x && (!a.ln_w || !a.ln_b)) return false;
+    if (a.part_acc && (!a.part_ml || a.max_splits <= 0 || !in->attn_positions)) return false;
+    if (a.part_acc) a.positions = in->attn_positions;
+    return true;
+}
+
+static bool base_args(GemmArgs &a, const pgpu_matrix *w, const pgpu_gemm_input *in, int streams,
+                      int *status) {
+    a = GemmArgs{};
     a.w = w->values;
     a.wscale = w->scales;
     a.n_rows = (int)w->rows;
     a.k_cols = (int)w->columns;
     a.streams = streams;
     a.status = status;
-    return a;
+    return set_input(a, in);
 }
 
 }  // namespace pgpu
 
 using namespace pgpu;
 
-extern "C" int pgpu_gemm_store(void *stream, const pgpu_matrix *w, const uint16_t *xs,
+extern "C" int pgpu_gemm_store(void *stream, const pgpu_matrix *w, const pgpu_gemm_input *in,
                                int streams, const float *bias, float *out, int ld_out,
                                int *status) {
-    GemmArgs a = base_args(w, xs, streams, status);
+    GemmArgs a;
+    if (!base_args(a, w, in, streams, status)) return bad_arguments("pgpu_gemm_store");
     a.out = out;
     a.ld_out = ld_out;
     a.bias = bias;
-    return w->q8 ? launch<EPI_STORE, true>(a, (hipStream_t)stream)
-                 : launch<EPI_STORE, false>(a, (hipStream_t)stream);
+    return dispatch<EPI_STORE>(a, w->q8, (hipStream_t)stream);
 }
 
-extern "C" int pgpu_gemm_residual(void *stream, const pgpu_matrix *w, const uint16_t *xs,
+extern "C" int pgpu_gemm_residual(void *stream, const pgpu_matrix *w, const pgpu_gemm_input *in,
                                   int streams, const float *residual, float *out, int *status) {
-    GemmArgs a = base_args(w, xs, streams, status);
+    GemmArgs a;
+    if (!base_args(a, w, in, streams, status)) return bad_arguments("pgpu_gemm_residual");
     a.out = out;
     a.ld_out = (int)w->rows;
     a.residual = residual;
-    return w->q8 ? launch<EPI_RESIDUAL, true>(a, (hipStream_t)stream)
-                 : launch<EPI_RESIDUAL, false>(a, (hipStream_t)stream);
+    return dispatch<EPI_RESIDUAL>(a, w->q8, (hipStream_t)stream);
 }
 
-extern "C" int pgpu_gemm_gelu_split(void *stream, const pgpu_matrix *w, const uint16_t *xs,
-                                    int streams, uint16_t *out_split, int *status) {
-    GemmArgs a = base_args(w, xs, streams, status);
+extern "C" int pgpu_gemm_gelu_split(void *stream, const pgpu_matrix *w,
+                                    const pgpu_gemm_input *in, int streams, uint16_t *out_split,
+                                    int *status) {
+    GemmArgs a;
+    if (!base_args(a, w, in, streams, status)) return bad_arguments("pgpu_gemm_gelu_split");
     a.out_split = out_split;
     a.out_kb = (int)w->rows / 32;
-    return w->q8 ? launch<EPI_GELU_SPLIT, true>(a, (hipStream_t)stream)
-                 : launch<EPI_GELU_SPLIT, false>(a, (hipStream_t)stream);
+    return dispatch<EPI_GELU_SPLIT>(a, w->q8, (hipStream_t)stream);
 }
 
-extern "C" int pgpu_gemm_qkv(void *stream, const pgpu_matrix *w, const uint16_t *xs,
+extern "C" int pgpu_gemm_qkv(void *stream, const pgpu_matrix *w, const pgpu_gemm_input *in,
                              int streams, const pgpu_paged_kv *kv, int layer,
                              const int32_t *tables, int table_stride, const int32_t *positions,
                              const float *rope, float *q_out, int *status) {
-    if (w->rows != 3 * kWidth || w->columns != kWidth || layer < 0 || layer >= kv->layers)
+    GemmArgs a;
+    if (w->rows != 3 * kWidth || w->columns != kWidth || layer < 0 || layer >= kv->layers ||
+        !base_args(a, w, in, streams, status) || a.part_acc)
         return bad_arguments("pgpu_gemm_qkv");
-    GemmArgs a = base_args(w, xs, streams, status);
     a.q_out = q_out;
     a.kv = kv->base;
     a.layer_stride = kv->layer_stride;
@@ -273,6 +494,5 @@ extern "C" int pgpu_gemm_qkv(void *stream, const pgpu_matrix *w, const uint16_t 
     a.table_stride = table_stride;
     a.positions = positions;
     a.rope = (const float2 *)rope;
-    return w->q8 ? launch<EPI_QKV, true>(a, (hipStream_t)stream)
-                 : launch<EPI_QKV, false>(a, (hipStream_t)stream);
+    return dispatch<EPI_QKV>(a, w->q8, (hipStream_t)stream);
 }

@@ -1,13 +1,12 @@
 /* Batched Flow decode step over a paged KV pool (phonon_flow_batch.h).
  *
- * One step of B streams runs, per layer (src/phonon_transformer.c:406-453):
- *   LN1 -> split fragments            pgpu_ln_split
- *   QKV projection + RoPE + append    pgpu_gemm_qkv
- *   attention over the pool           pgpu_attention   (-> split fragments)
- *   out projection + residual         pgpu_gemm_residual
- *   LN2 -> split fragments            pgpu_ln_split
- *   MLP in projection + GELU          pgpu_gemm_gelu_split
- *   MLP out projection + residual     pgpu_gemm_residual
+ * One step of B streams runs five kernels per layer
+ * (src/phonon_transformer.c:406-453):
+ *   LN1 + QKV projection + RoPE + append      pgpu_gemm_qkv
+ *   split attention over the pool (partials)  pgpu_attention
+ *   split merge + out projection + residual   pgpu_gemm_residual
+ *   LN2 + MLP in projection + GELU            pgpu_gemm_gelu_split
+ *   MLP out projection + residual             pgpu_gemm_residual
  * then advances every stream's position on the device. */
 #include "ph_internal.h"
 
@@ -37,7 +36,7 @@ struct PhononFlowBatch {
     size_t max_streams, padded_streams, max_positions, table_len, max_splits, streams;
     void *stream;
     float *x, *r, *q, *in, *out, *rows;
-    uint16_t *xs, *xh;
+    uint16_t *xh; /* split fragments of the MLP hidden rows */
     int32_t *positions, *tables;
     int *status;
     pgpu_attention_scratch scratch;
@@ -287,9 +286,9 @@ void phonon_flow_batch_destroy(PhononFlowBatch *b) {
     if (b->stream)
         (void)pgpu_stream_sync(b->stream);
     pgpu_graph_destroy(b->graph);
-    void *bufs[] = {b->x,         b->r,       b->q,       b->in,      b->out,
-                    b->rows,      b->xs,      b->xh,      b->positions, b->tables,
-                    b->status,    b->scratch.part_acc, b->scratch.part_ml, b->scratch.tickets};
+    void *bufs[] = {b->x,    b->r,  b->q,         b->in,     b->out,
+                    b->rows, b->xh, b->positions, b->tables, b->status,
+                    b->scratch.part_acc, b->scratch.part_ml};
     for (size_t i = 0; i < sizeof(bufs) / sizeof(bufs[0]); i++)
         pgpu_free(bufs[i]);
     pgpu_stream_destroy(b->stream);
@@ -317,7 +316,7 @@ int phonon_flow_batch_create(const PhononFlowModel *model, PhononKvPool *pool,
     b->table_len = (max_positions + 15) / 16;
     b->max_splits = (max_positions + PH_SPLIT_KEYS - 1) / PH_SPLIT_KEYS;
     const size_t rows = b->padded_streams * PH_WIDTH * sizeof(float);
-    const size_t split512 = b->padded_streams * PH_WIDTH * 3 * sizeof(uint16_t);
+    const size_t split2048 = b->padded_streams * PH_FFN * 3 * sizeof(uint16_t);
     const size_t slots = max_streams * PH_HEADS * b->max_splits;
     int ok = pgpu_stream_create(&b->stream);
     b->x = pgpu_malloc(rows);
@@ -326,28 +325,24 @@ int phonon_flow_batch_create(const PhononFlowModel *model, PhononKvPool *pool,
     b->in = pgpu_malloc(rows);
     b->out = pgpu_malloc(rows);
     b->rows = pgpu_malloc(2 * (size_t)pool->kv.layers * PH_WIDTH * sizeof(float));
-    b->xs = pgpu_malloc(split512);
-    b->xh = pgpu_malloc(split512 * 4);
+    b->xh = pgpu_malloc(split2048);
     b->positions = pgpu_malloc(b->padded_streams * sizeof(int32_t));
     b->tables = pgpu_malloc(max_streams * b->table_len * sizeof(int32_t));
     b->status = pgpu_malloc(sizeof(int));
     b->scratch.part_acc = pgpu_malloc(slots * 64 * sizeof(float));
     b->scratch.part_ml = pgpu_malloc(slots * 2 * sizeof(float));
-    b->scratch.tickets = pgpu_malloc(max_streams * PH_HEADS * sizeof(int));
     b->scratch.max_streams = (int)max_streams;
     b->scratch.max_splits = (int)b->max_splits;
     b->host_positions = calloc(max_streams, sizeof(size_t));
-    ok = ok && b->x && b->r && b->q && b->in && b->out && b->rows && b->xs && b->xh &&
-         b->positions && b->tables && b->status && b->scratch.part_acc && b->scratch.part_ml &&
-         b->scratch.tickets && b->host_positions;
+    ok = ok && b->x && b->r && b->q && b->in && b->out && b->rows && b->xh && b->positions &&
+         b->tables && b->status && b->scratch.part_acc && b->scratch.part_ml &&
+         b->host_positions;
     /* Zero everything a kernel may read before writing (padding streams of the
-     * split fragments, tickets, status). */
-    ok = ok && pgpu_memset(b->stream, b->xs, 0, split512) &&
-         pgpu_memset(b->stream, b->xh, 0, split512 * 4) &&
+     * split fragments, positions, status). */
+    ok = ok && pgpu_memset(b->stream, b->xh, 0, split2048) &&
          pgpu_memset(b->stream, b->positions, 0, b->padded_streams * sizeof(int32_t)) &&
          pgpu_memset(b->stream, b->tables, 0, max_streams * b->table_len * sizeof(int32_t)) &&
          pgpu_memset(b->stream, b->status, 0, sizeof(int)) &&
-         pgpu_memset(b->stream, b->scratch.tickets, 0, max_streams * PH_HEADS * sizeof(int)) &&
          pgpu_memset(b->stream, b->x, 0, rows) && pgpu_memset(b->stream, b->in, 0, rows) &&
          pgpu_stream_sync(b->stream);
     if (!ok) {
@@ -417,22 +412,29 @@ int ph_batch_enqueue_layers(PhononFlowBatch *b, size_t first, size_t count, size
     void *st = b->stream;
     const int n = (int)b->streams;
     const float *cur = input;
-    /* A layer reads its input only in LN1 and the out-projection residual,
-     * both before its last kernel writes `next`, so in-place is safe. */
+    /* A layer reads its input only in the QKV prologue and the out-projection
+     * residual, both before its last kernel writes `next`: in-place is safe. */
     for (size_t l = first; l < first + count; l++) {
         const float *norm = m->norms + l * 4 * PH_WIDTH;
         float *next = (l + 1 == first + count) ? output : b->x;
-        if (!pgpu_ln_split(st, cur, n, norm, norm + PH_WIDTH, 1e-5f, b->xs, NULL, b->status) ||
-            !pgpu_gemm_qkv(st, &m->qkv[l], b->xs, n, &b->pool->kv, (int)(l + pool_offset),
-                           b->tables, (int)b->table_len, b->positions, rope, b->q, b->status) ||
-            !pgpu_attention(st, b->q, &b->pool->kv, (int)(l + pool_offset), b->tables,
-                            (int)b->table_len, b->positions, n, PH_HEADS, (int)b->max_splits,
-                            b->xs, NULL, &b->scratch, b->status) ||
-            !pgpu_gemm_residual(st, &m->out[l], b->xs, n, cur, b->r, b->status) ||
-            !pgpu_ln_split(st, b->r, n, norm + 2 * PH_WIDTH, norm + 3 * PH_WIDTH, 1e-5f, b->xs,
-                           NULL, b->status) ||
-            !pgpu_gemm_gelu_split(st, &m->mlp_in[l], b->xs, n, b->xh, b->status) ||
-            !pgpu_gemm_residual(st, &m->mlp_out[l], b->xh, n, b->r, next, b->status))
+        const int pool_layer = (int)(l + pool_offset);
+        const pgpu_gemm_input ln1 = {.ln_rows = cur, .ln_weight = norm,
+                                     .ln_bias = norm + PH_WIDTH, .ln_epsilon = 1e-5f};
+        const pgpu_gemm_input att = {.attn_acc = b->scratch.part_acc,
+                                     .attn_ml = b->scratch.part_ml,
+                                     .attn_positions = b->positions,
+                                     .attn_max_splits = (int)b->max_splits};
+        const pgpu_gemm_input ln2 = {.ln_rows = b->r, .ln_weight = norm + 2 * PH_WIDTH,
+                                     .ln_bias = norm + 3 * PH_WIDTH, .ln_epsilon = 1e-5f};
+        const pgpu_gemm_input hidden = {.split = b->xh};
+        if (!pgpu_gemm_qkv(st, &m->qkv[l], &ln1, n, &b->pool->kv, pool_layer, b->tables,
+                           (int)b->table_len, b->positions, rope, b->q, b->status) ||
+            !pgpu_attention(st, b->q, &b->pool->kv, pool_layer, b->tables, (int)b->table_len,
+                            b->positions, n, PH_HEADS, (int)b->max_splits, &b->scratch,
+                            b->status) ||
+            !pgpu_gemm_residual(st, &m->out[l], &att, n, cur, b->r, b->status) ||
+            !pgpu_gemm_gelu_split(st, &m->mlp_in[l], &ln2, n, b->xh, b->status) ||
+            !pgpu_gemm_residual(st, &m->mlp_out[l], &hidden, n, b->r, next, b->status))
             return 0;
         cur = next;
     }

@@ -81,8 +81,9 @@ int phonon_q8_device_matvec(PhononQ8Device *m, size_t copy, const float *x, floa
     const pgpu_matrix *w = &m->copies[copy];
     if (w->columns != m->columns)
         return 0; /* padded columns would need a padded input */
+    const pgpu_gemm_input in = {.split = m->xs};
     return pgpu_split_rows(stream, x, (int)batch, (int)w->columns, m->xs, m->status) &&
-           pgpu_gemm_store(stream, w, m->xs, (int)batch, NULL, y, (int)w->rows, m->status);
+           pgpu_gemm_store(stream, w, &in, (int)batch, NULL, y, (int)w->rows, m->status);
 }
 
 int phonon_q8_device_status(PhononQ8Device *m, void *stream) {
@@ -144,11 +145,12 @@ int phonon_q8_matvec(const PhononQ8Block *weights, const float *input, size_t ro
     int *status = ph_scratch(1, sizeof(int));
     float *host = ok ? malloc(w.rows * sizeof(float)) : NULL;
     int st = 1;
+    const pgpu_gemm_input in = {.split = xs};
     ok = ok && x && y && xs && status && host && pgpu_memset(s, status, 0, sizeof(int)) &&
          pgpu_memset(s, xs, 0, 16 * columns * 3 * sizeof(uint16_t)) &&
          pgpu_copy_h2d(s, x, input, input_bytes) &&
          pgpu_split_rows(s, x, 1, (int)columns, xs, status) &&
-         pgpu_gemm_store(s, &w, xs, 1, NULL, y, (int)w.rows, status) &&
+         pgpu_gemm_store(s, &w, &in, 1, NULL, y, (int)w.rows, status) &&
          pgpu_copy_d2h(s, &st, status, sizeof(int)) &&
          pgpu_copy_d2h(s, host, y, w.rows * sizeof(float));
     if (ok && st == 0)

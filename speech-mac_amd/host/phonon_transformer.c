@@ -335,8 +335,9 @@ int phonon_linear_batch(const PhononTensorView *weight, const float *input, size
         }
     }
     int st = 1;
+    const pgpu_gemm_input in = {.split = xs};
     ok = ok && pgpu_split_rows(s, x, (int)batch, (int)pcol, xs, status) &&
-         pgpu_gemm_store(s, &w, xs, (int)batch, b, y, (int)prow, status) &&
+         pgpu_gemm_store(s, &w, &in, (int)batch, b, y, (int)prow, status) &&
          pgpu_copy_d2h(s, &st, status, sizeof(int)) &&
          pgpu_copy_d2h(s, host, y, batch * prow * sizeof(float));
     if (ok && st == 0)
@@ -571,18 +572,22 @@ int phonon_attention_test(const float query[64], const float *keys, const float 
     const int splits = (int)((count + PH_SPLIT_KEYS - 1) / PH_SPLIT_KEYS);
     float *dq = ok ? ph_scratch(2, 2 * PH_WIDTH * sizeof(float)) : NULL;
     int32_t *dt = ok ? ph_scratch(3, (table_len + 1) * sizeof(int32_t)) : NULL;
-    float *part = ok ? ph_scratch(4, (size_t)splits * 66 * sizeof(float)) : NULL;
-    int *words = ok ? ph_scratch(5, 2 * sizeof(int)) : NULL;
+    /* Partials of one stream, head 0: slots j = 0 .. splits-1. */
+    float *part = ok ? ph_scratch(4, (size_t)splits * PH_HEADS * 66 * sizeof(float)) : NULL;
+    int *words = ok ? ph_scratch(5, sizeof(int)) : NULL;
     int st = 1;
     if (ok && dq && dt && part && words) {
         const int32_t position = (int32_t)(count - 1);
-        pgpu_attention_scratch scratch = {part, part + splits * 64, words + 1, 1, splits};
-        ok = pgpu_memset(s, words, 0, 2 * sizeof(int)) &&
+        pgpu_attention_scratch scratch = {part, part + (size_t)splits * PH_HEADS * 64, 1,
+                                          splits};
+        ok = pgpu_memset(s, words, 0, sizeof(int)) &&
              pgpu_copy_h2d(s, dq, q, PH_WIDTH * sizeof(float)) &&
              pgpu_copy_h2d(s, dt, table, table_len * sizeof(int32_t)) &&
              pgpu_copy_h2d(s, dt + table_len, &position, sizeof(int32_t)) &&
              pgpu_attention(s, dq, ph_pool_kv(pool), 0, dt, (int)table_len, dt + table_len, 1, 1,
-                            splits, NULL, dq + PH_WIDTH, &scratch, words) &&
+                            splits, &scratch, words) &&
+             pgpu_attention_merge(s, &scratch, dt + table_len, 1, 1, splits, dq + PH_WIDTH, NULL,
+                                  words) &&
              pgpu_copy_d2h(s, &st, words, sizeof(int)) &&
              pgpu_copy_d2h(s, output, dq + PH_WIDTH, 64 * sizeof(float));
     } else {
