@@ -132,8 +132,13 @@ def step_bytes(layers, contexts):
                                                          + KV_BYTES_PER_KEY))
 
 
-def run_decode(pkg, lib, layers, streams, lengths, steps, warmup, seed):
+def run_decode(pkg, lib, layers, streams, lengths, steps, warmup, seed, groups=None,
+               eager=False):
     d = DecodeSetup(pkg, lib, layers, streams, lengths, steps + warmup + 1, seed)
+    if groups:
+        assert lib.phonon_flow_batch_set_groups(d.batch, groups)
+    if eager:
+        assert lib.phonon_flow_batch_set_graph(d.batch, 0)
     for _ in range(warmup):
         d.step()
     assert lib.phonon_flow_batch_sync(d.batch), "non-finite value during warmup"
@@ -308,6 +313,10 @@ def main():
     ap.add_argument("--batch", type=int, default=64)
     ap.add_argument("--layers", type=int, default=12)
     ap.add_argument("--seed", type=int, default=2026)
+    ap.add_argument("--groups", type=int, default=0,
+                    help="concurrent stream groups of the step (0 = library default)")
+    ap.add_argument("--eager", action="store_true",
+                    help="launch the step's kernels directly instead of a graph replay")
     ap.add_argument("--skip-extras", action="store_true",
                     help="only the headline B=64 line (no B=1, matvec, curve, CPU)")
     args = ap.parse_args()
@@ -326,7 +335,7 @@ def main():
     lengths = np.random.default_rng(args.seed).integers(1, 2049, size=args.batch) - 1
     log(f"B={args.batch} L={args.layers}: contexts {lengths.min() + 1}..{lengths.max() + 1}")
     d, r = run_decode(pkg, lib, args.layers, args.batch, lengths, args.steps, args.warmup,
-                      args.seed)
+                      args.seed, args.groups, args.eager)
     ms_step = r["ms"] / args.steps
     value = args.batch * args.steps / (r["ms"] * 1e-3)
     gbs = r["bytes"] / (r["ms"] * 1e-3) / 1e9

@@ -84,6 +84,15 @@ int phonon_flow_batch_step(PhononFlowBatch *batch, const float *inputs, float th
  * HIP graph on first use and replayed afterwards. */
 int phonon_flow_batch_step_device(PhononFlowBatch *batch, const float *inputs, float theta,
                                   float *outputs);
+/* Runs the streams as `groups` (1..4) independent groups of whole 16-stream
+ * tiles, each on its own HIP stream inside the step's graph, so one group's
+ * projections overlap another's attention. Results do not depend on it.
+ * Default 2 (a batch of at most 16 streams always runs as one group). */
+int phonon_flow_batch_set_groups(PhononFlowBatch *batch, size_t groups);
+/* use_graph = 1 (default): step_device replays a captured HIP graph;
+ * 0: it launches the step's kernels directly (e.g. for a caller that is
+ * itself capturing a graph). Results are identical. */
+int phonon_flow_batch_set_graph(PhononFlowBatch *batch, int use_graph);
 /* Waits for enqueued steps; returns 1 iff no step since the last call saw a
  * non-finite value or an uncovered position (and clears that record). */
 int phonon_flow_batch_sync(PhononFlowBatch *batch);

@@ -86,6 +86,8 @@ int pgpu_event_create(void **event);
 void pgpu_event_destroy(void *event);
 int pgpu_event_record(void *event, void *stream);
 int pgpu_event_elapsed_ms(void *start, void *stop, float *ms);
+/* Work enqueued on `stream` after this call waits for `event`. */
+int pgpu_stream_wait_event(void *stream, void *event);
 int pgpu_graph_begin(void *stream);
 int pgpu_graph_end(void *stream, void **exec);
 int pgpu_graph_launch(void *exec, void *stream);

@@ -146,6 +146,8 @@ EXPORTS = {
     "phonon_flow_batch_step": (_i, [_vp, _fp, _f, _fp]),
     "phonon_flow_batch_step_device": (_i, [_vp, _vp, _f, _vp]),
     "phonon_flow_batch_sync": (_i, [_vp]),
+    "phonon_flow_batch_set_groups": (_i, [_vp, _sz]),
+    "phonon_flow_batch_set_graph": (_i, [_vp, _i]),
     "phonon_flow_batch_positions": (_i, [_vp, _szp]),
     "phonon_flow_batch_stream": (_vp, [_vp]),
     "phonon_flow_batch_device_inputs": (_vp, [_vp]),
@@ -170,6 +172,7 @@ EXPORTS = {
     "pgpu_event_destroy": (None, [_vp]),
     "pgpu_event_record": (_i, [_vp, _vp]),
     "pgpu_event_elapsed_ms": (_i, [_vp, _vp, _fp]),
+    "pgpu_stream_wait_event": (_i, [_vp, _vp]),
     "pgpu_graph_begin": (_i, [_vp]),
     "pgpu_graph_end": (_i, [_vp, _pp]),
     "pgpu_graph_launch": (_i, [_vp, _vp]),

@@ -84,15 +84,21 @@ __device__ inline float half_to_float(uint32_t bits16) {
     return __half2float(__ushort_as_half((unsigned short)bits16));
 }
 
+// LDS operand buffer of the prologues: for column block kb, three 1 KB
+// records (one per term) of 64 lanes x 8 bf16, in the MFMA B-operand order.
+// Consecutive blocks are kLdsBlock elements apart: the 16-byte pad puts the
+// 16 blocks one writer wave touches on distinct banks.
+constexpr int kLdsBlock = 1536 + 8;
+
 // Writes 32 activations of stream n (0..15 in the tile), columns
-// [32kb, 32kb+32), into an LDS fragment buffer laid out [kb][part][512].
+// [32kb, 32kb+32), into the LDS operand buffer.
 __device__ inline void lds_store_block(uint16_t *bsh, int n, int kb, const float *v) {
 #pragma unroll
     for (int g = 0; g < 4; g++) {
         uint16_t h[8], m[8], l[8];
 #pragma unroll
         for (int i = 0; i < 8; i++) split3(v[g * 8 + i], h[i], m[i], l[i]);
-        uint16_t *rec = bsh + kb * 1536 + (g * 16 + n) * 8;
+        uint16_t *rec = bsh + kb * kLdsBlock + (g * 16 + n) * 8;
 #pragma unroll
         for (int p = 0; p < 3; p++) {
             const uint16_t *src = p == 0 ? h : (p == 1 ? m : l);
@@ -215,6 +221,105 @@ __device__ inline bool prologue_attn(const GemmArgs &a, int st, uint16_t *bsh) {
     return bad;
 }
 
+// One chunk of CH column blocks of this lane's weight fragments.
+template <bool Q8, int CH>
+struct WChunk;
+template <int CH>
+struct WChunk<true, CH> {
+    uint2 raw[CH], sc[CH];
+};
+template <int CH>
+struct WChunk<false, CH> {
+    bf16x8 w[CH];
+};
+
+template <bool Q8, int CH>
+__device__ inline void load_weights(WChunk<Q8, CH> &c, const GemmArgs &a, int tile, int kbn,
+                                    int lane, int kb0, int kb_end) {
+#pragma unroll
+    for (int u = 0; u < CH; u++) {
+        const size_t kb = (size_t)min(kb0 + u, kb_end - 1);
+        if constexpr (Q8) {
+            c.raw[u] = *(const uint2 *)((const int8_t *)a.w + ((size_t)tile * kbn + kb) * 512 +
+                                        lane * 8);
+            c.sc[u] = *(const uint2 *)(a.wscale + ((size_t)tile * kbn + kb) * 16 +
+                                       (lane >> 4) * 4);
+        } else {
+            c.w[u] = *(const bf16x8 *)((const uint16_t *)a.w + ((size_t)tile * kbn + kb) * 512 +
+                                       lane * 8);
+        }
+    }
+}
+
+// acc += W_chunk . X_chunk. No control flow between loads and MFMAs: a block
+// past the wave's range contributes 0 (scale 0 / zero fragment).
+template <bool Q8, int CH>
+__device__ inline void mfma_chunk(f32x4 &acc, const WChunk<Q8, CH> &w, const bf16x8 *xh,
+                                  const bf16x8 *xm, const bf16x8 *xl, int kb0, int kb_end) {
+#pragma unroll
+    for (int u = 0; u < CH; u++) {
+        const bool used = kb0 + u < kb_end;
+        if constexpr (Q8) {
+            const bf16x8 wa = q8_to_bf16(w.raw[u]);
+            f32x4 c = {0.0f, 0.0f, 0.0f, 0.0f};
+            c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wa, xh[u], c, 0, 0, 0);
+            c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wa, xm[u], c, 0, 0, 0);
+            c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wa, xl[u], c, 0, 0, 0);
+            const uint2 s = used ? w.sc[u] : make_uint2(0u, 0u);
+            acc[0] = fmaf(half_to_float(s.x & 0xffffu), c[0], acc[0]);
+            acc[1] = fmaf(half_to_float(s.x >> 16), c[1], acc[1]);
+            acc[2] = fmaf(half_to_float(s.y & 0xffffu), c[2], acc[2]);
+            acc[3] = fmaf(half_to_float(s.y >> 16), c[3], acc[3]);
+        } else {
+            const bf16x8 wa = used ? w.w[u] : bf16x8{};
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wa, xh[u], acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wa, xm[u], acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wa, xl[u], acc, 0, 0, 0);
+        }
+    }
+}
+
+// Operands of the epilogue of one lane (rows row0..row0+3 of stream s).
+struct EpiOperands {
+    float4 add;          // STORE: bias, RESIDUAL: residual
+    bool has_add;
+    float2 cs0, cs1;     // QKV: (cos, sin) of the lane's two RoPE pairs
+    int pos, block;      // QKV: append position and its pool block
+    bool ok;             // QKV: position and block are valid
+};
+
+template <int EPI>
+__device__ inline void load_epilogue(EpiOperands &e, const GemmArgs &a, int s, int row0,
+                                     bool live) {
+    e.add = make_float4(0.f, 0.f, 0.f, 0.f);
+    e.has_add = false;
+    if (!live) return;
+    if constexpr (EPI == EPI_STORE) {
+        if (a.bias) {
+            e.add = *(const float4 *)(a.bias + row0);
+            e.has_add = true;
+        }
+    } else if constexpr (EPI == EPI_RESIDUAL) {
+        e.add = *(const float4 *)(a.residual + (size_t)s * a.ld_out + row0);
+        e.has_add = true;
+    } else if constexpr (EPI == EPI_QKV) {
+        // Positions past the rope table or the block table, and block ids
+        // outside the pool, are errors: flagged, and nothing is written.
+        int pos = a.positions[s];
+        e.ok = pos >= 0 && pos < kMaxPositions && (pos >> 4) < a.table_stride;
+        e.block = 0;
+        if (e.ok) {
+            e.block = a.tables[(size_t)s * a.table_stride + (pos >> 4)];
+            e.ok = (unsigned)e.block < a.blocks;
+        }
+        if (!e.ok) pos = 0;
+        e.pos = pos;
+        const int d0 = (row0 & 511) & 63;
+        e.cs0 = a.rope[(size_t)pos * 32 + (d0 >> 1)];
+        e.cs1 = a.rope[(size_t)pos * 32 + (d0 >> 1) + 1];
+    }
+}
+
 template <int SRC, int EPI, bool Q8, int CH>
 __global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
     const int tile = blockIdx.x, st = blockIdx.y;
@@ -226,8 +331,21 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
     const int kb_begin = wave * per_wave;
     const int kb_end = min(kbn, kb_begin + per_wave);
 
+    // D fragment of this lane: rows row0 .. row0+3 of stream s.
+    const int s = st * 16 + (lane & 15);
+    const int row0 = tile * 16 + (lane >> 4) * 4;
+    const bool live = s < a.streams;
+
+    // Everything that does not depend on the prologue is requested first, so
+    // its memory latency overlaps the prologue: the first weight chunk and
+    // the epilogue's operands (wave 0 runs the epilogue).
+    WChunk<Q8, CH> w;
+    if (kb_begin < kb_end) load_weights(w, a, tile, kbn, lane, kb_begin, kb_end);
+    EpiOperands e;
+    if (wave == 0) load_epilogue<EPI>(e, a, s, row0, live);
+
     // Prologue-built operands hold 16 streams x 512 columns x 3 terms (48 KB).
-    __shared__ uint16_t bsh[SRC == SRC_SPLIT ? 8 : 16 * 1536];
+    __shared__ uint16_t bsh[SRC == SRC_SPLIT ? 8 : 16 * kLdsBlock];
     bool bad_in = false;
     if constexpr (SRC == SRC_LN) bad_in = prologue_ln(a, st, bsh);
     if constexpr (SRC == SRC_ATTN) bad_in = prologue_attn(a, st, bsh);
@@ -239,59 +357,25 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
     const uint16_t *xs = SRC == SRC_SPLIT ? a.xs + (size_t)st * kbn * 1536 + lane * 8
                                           : bsh + lane * 8;
     f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-    // Chunks of CH blocks: all loads of a chunk are issued before its MFMAs
-    // (past the wave's range the last block is re-read and not used).
+    // Chunks of CH blocks; the next chunk's weights are requested before the
+    // current chunk's MFMAs (past the wave's range the last block is re-read
+    // and not used).
     for (int kb0 = kb_begin; kb0 < kb_end; kb0 += CH) {
         bf16x8 xh[CH], xm[CH], xl[CH];
 #pragma unroll
         for (int u = 0; u < CH; u++) {
-            const size_t kb = (size_t)min(kb0 + u, kb_end - 1);
-            xh[u] = *(const bf16x8 *)(xs + kb * 1536);
-            xm[u] = *(const bf16x8 *)(xs + kb * 1536 + 512);
-            xl[u] = *(const bf16x8 *)(xs + kb * 1536 + 1024);
+            // Column blocks are 1536 elements apart in global split buffers,
+            // kLdsBlock apart in the padded LDS operand buffer.
+            const size_t kb = (size_t)min(kb0 + u, kb_end - 1) *
+                              (SRC == SRC_SPLIT ? 1536 : kLdsBlock);
+            xh[u] = *(const bf16x8 *)(xs + kb);
+            xm[u] = *(const bf16x8 *)(xs + kb + 512);
+            xl[u] = *(const bf16x8 *)(xs + kb + 1024);
         }
-        if constexpr (Q8) {
-            const int8_t *wq = (const int8_t *)a.w + (size_t)tile * kbn * 512 + lane * 8;
-            const uint16_t *ws = a.wscale + (size_t)tile * kbn * 16 + (lane >> 4) * 4;
-            uint2 raw[CH], sc[CH];
-#pragma unroll
-            for (int u = 0; u < CH; u++) {
-                const size_t kb = (size_t)min(kb0 + u, kb_end - 1);
-                raw[u] = *(const uint2 *)(wq + kb * 512);
-                sc[u] = *(const uint2 *)(ws + kb * 16);
-            }
-            // No control flow between the loads and the MFMAs (the scheduler
-            // then keeps the loads together): a re-read block gets scale 0.
-#pragma unroll
-            for (int u = 0; u < CH; u++) {
-                const bool used = kb0 + u < kb_end;
-                const bf16x8 wa = q8_to_bf16(raw[u]);
-                f32x4 c = {0.0f, 0.0f, 0.0f, 0.0f};
-                c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wa, xh[u], c, 0, 0, 0);
-                c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wa, xm[u], c, 0, 0, 0);
-                c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wa, xl[u], c, 0, 0, 0);
-                const uint2 s = used ? sc[u] : make_uint2(0u, 0u);
-                acc[0] = fmaf(half_to_float(s.x & 0xffffu), c[0], acc[0]);
-                acc[1] = fmaf(half_to_float(s.x >> 16), c[1], acc[1]);
-                acc[2] = fmaf(half_to_float(s.y & 0xffffu), c[2], acc[2]);
-                acc[3] = fmaf(half_to_float(s.y >> 16), c[3], acc[3]);
-            }
-        } else {
-            const uint16_t *wb = (const uint16_t *)a.w + (size_t)tile * kbn * 512 + lane * 8;
-            bf16x8 wa[CH];
-#pragma unroll
-            for (int u = 0; u < CH; u++) {
-                const size_t kb = (size_t)min(kb0 + u, kb_end - 1);
-                wa[u] = *(const bf16x8 *)(wb + kb * 512);
-            }
-#pragma unroll
-            for (int u = 0; u < CH; u++) {
-                if (kb0 + u >= kb_end) wa[u] = bf16x8{};  // re-read block adds 0
-                acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wa[u], xh[u], acc, 0, 0, 0);
-                acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wa[u], xm[u], acc, 0, 0, 0);
-                acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wa[u], xl[u], acc, 0, 0, 0);
-            }
-        }
+        WChunk<Q8, CH> next;
+        if (kb0 + CH < kb_end) load_weights(next, a, tile, kbn, lane, kb0 + CH, kb_end);
+        mfma_chunk(acc, w, xh, xm, xl, kb0, kb_end);
+        w = next;
     }
 
     __shared__ f32x4 partial[4][64];
@@ -308,25 +392,21 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
         v[3] = __fadd_rn(v[3], p[3]);
     }
 
-    // D fragment: lane holds rows row0 .. row0+3 of stream s.
-    const int s = st * 16 + (lane & 15);
-    const int row0 = tile * 16 + (lane >> 4) * 4;
-    const bool live = s < a.streams;
     bool bad = false;
     if constexpr (EPI == EPI_STORE || EPI == EPI_RESIDUAL) {
         if (live) {
             float *o = a.out + (size_t)s * a.ld_out + row0;
+            const float add[4] = {e.add.x, e.add.y, e.add.z, e.add.w};
+            float y[4];
 #pragma unroll
             for (int r = 0; r < 4; r++) {
-                float y = v[r];
-                if constexpr (EPI == EPI_STORE) {
-                    if (a.bias) y = __fadd_rn(y, a.bias[row0 + r]);
-                } else {
-                    y = __fadd_rn(a.residual[(size_t)s * a.ld_out + row0 + r], y);
-                }
-                bad |= !isfinite(y);
-                o[r] = y;
+                // bias + dot (STORE) or residual + dot (RESIDUAL); 0 + dot
+                // without a bias is exact.
+                y[r] = EPI == EPI_STORE ? (e.has_add ? __fadd_rn(v[r], add[r]) : v[r])
+                                        : __fadd_rn(add[r], v[r]);
+                bad |= !isfinite(y[r]);
             }
+            *(float4 *)o = make_float4(y[0], y[1], y[2], y[3]);
         }
     } else if constexpr (EPI == EPI_GELU_SPLIT) {
         if (live) {
@@ -342,24 +422,13 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
         if (live) {
             const int part = row0 >> 9, rr = row0 & 511;
             const int head = rr >> 6, d0 = rr & 63;
-            int pos = a.positions[s];
-            int block = 0;
-            // Positions past the rope table or the block table, and block ids
-            // outside the pool, are errors: flag them and write nothing.
-            bool ok = pos >= 0 && pos < kMaxPositions && (pos >> 4) < a.table_stride;
-            if (ok) {
-                block = a.tables[(size_t)s * a.table_stride + (pos >> 4)];
-                ok = (unsigned)block < a.blocks;
-            }
-            if (!ok) {
-                atomicOr(a.status, 2);
-                pos = 0;
-            }
+            const bool ok = e.ok;
+            const int pos = e.pos, block = e.block;
+            if (!ok) atomicOr(a.status, 2);
             float o[4] = {v[0], v[1], v[2], v[3]};
             if (part < 2) {
                 // Interleaved pairs (d0, d0+1), (d0+2, d0+3): pair index d0/2.
-                const float2 cs0 = a.rope[(size_t)pos * 32 + (d0 >> 1)];
-                const float2 cs1 = a.rope[(size_t)pos * 32 + (d0 >> 1) + 1];
+                const float2 cs0 = e.cs0, cs1 = e.cs1;
                 o[0] = __fsub_rn(__fmul_rn(v[0], cs0.x), __fmul_rn(v[1], cs0.y));
                 o[1] = __fadd_rn(__fmul_rn(v[0], cs0.y), __fmul_rn(v[1], cs0.x));
                 o[2] = __fsub_rn(__fmul_rn(v[2], cs1.x), __fmul_rn(v[3], cs1.y));

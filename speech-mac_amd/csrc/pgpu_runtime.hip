@@ -125,6 +125,11 @@ extern "C" int pgpu_event_elapsed_ms(void *start, void *stop, float *ms) {
                  "hipEventElapsedTime");
 }
 
+extern "C" int pgpu_stream_wait_event(void *stream, void *event) {
+    return check(hipStreamWaitEvent((hipStream_t)stream, (hipEvent_t)event, 0),
+                 "hipStreamWaitEvent");
+}
+
 extern "C" int pgpu_graph_begin(void *stream) {
     return check(hipStreamBeginCapture((hipStream_t)stream, hipStreamCaptureModeThreadLocal),
                  "hipStreamBeginCapture");

@@ -46,6 +46,10 @@ struct PhononFlowBatch {
     float graph_theta;
     const float *graph_input;
     float *graph_output;
+    int eager;                         /* launch kernels directly, no graph */
+    size_t groups;                     /* stream groups run concurrently */
+    void *side[PH_MAX_GROUPS - 1];     /* HIP streams of groups 1.. */
+    void *fork, *join[PH_MAX_GROUPS - 1];
 };
 
 /* ---------------------------------------------------------------- model -- */
@@ -286,6 +290,13 @@ void phonon_flow_batch_destroy(PhononFlowBatch *b) {
     if (b->stream)
         (void)pgpu_stream_sync(b->stream);
     pgpu_graph_destroy(b->graph);
+    for (size_t g = 0; g + 1 < PH_MAX_GROUPS; g++) {
+        if (b->side[g])
+            (void)pgpu_stream_sync(b->side[g]);
+        pgpu_stream_destroy(b->side[g]);
+        pgpu_event_destroy(b->join[g]);
+    }
+    pgpu_event_destroy(b->fork);
     void *bufs[] = {b->x,    b->r,  b->q,         b->in,     b->out,
                     b->rows, b->xh, b->positions, b->tables, b->status,
                     b->scratch.part_acc, b->scratch.part_ml};
@@ -318,7 +329,10 @@ int phonon_flow_batch_create(const PhononFlowModel *model, PhononKvPool *pool,
     const size_t rows = b->padded_streams * PH_WIDTH * sizeof(float);
     const size_t split2048 = b->padded_streams * PH_FFN * 3 * sizeof(uint16_t);
     const size_t slots = max_streams * PH_HEADS * b->max_splits;
-    int ok = pgpu_stream_create(&b->stream);
+    b->groups = PH_DEFAULT_GROUPS;
+    int ok = pgpu_stream_create(&b->stream) && pgpu_event_create(&b->fork);
+    for (size_t g = 0; ok && g + 1 < PH_MAX_GROUPS; g++)
+        ok = pgpu_stream_create(&b->side[g]) && pgpu_event_create(&b->join[g]);
     b->x = pgpu_malloc(rows);
     b->r = pgpu_malloc(rows);
     b->q = pgpu_malloc(rows);
@@ -400,50 +414,117 @@ int ph_batch_set_single(PhononFlowBatch *b, size_t position, const int32_t *tabl
     return 1;
 }
 
-int ph_batch_enqueue_layers(PhononFlowBatch *b, size_t first, size_t count, size_t pool_offset,
-                            const float *input, float *output, float theta) {
+/* Enqueues layers [first, first+count) for streams [s0, s0+n) of the batch
+ * (s0 a multiple of 16) on `stream`. Every buffer is used at the group's
+ * offset, so groups share no memory and may run concurrently. */
+static int enqueue_group(PhononFlowBatch *b, void *stream, size_t s0, size_t n, size_t first,
+                         size_t count, size_t pool_offset, const float *input, float *output,
+                         const float *rope) {
     const PhononFlowModel *m = b->model;
-    if (!b->streams || first + count > m->layers ||
-        first + count + pool_offset > (size_t)b->pool->kv.layers)
-        return 0;
-    const float *rope = ph_rope_table(theta);
-    if (!rope)
-        return 0;
-    void *st = b->stream;
-    const int n = (int)b->streams;
-    const float *cur = input;
+    const size_t slot0 = s0 * PH_HEADS * b->max_splits;
+    const pgpu_attention_scratch scratch = {b->scratch.part_acc + slot0 * 64,
+                                            b->scratch.part_ml + slot0 * 2, (int)n,
+                                            (int)b->max_splits};
+    float *x = b->x + s0 * PH_WIDTH, *r = b->r + s0 * PH_WIDTH, *q = b->q + s0 * PH_WIDTH;
+    uint16_t *xh = b->xh + (s0 / 16) * (PH_FFN / 32) * 1536;
+    const int32_t *positions = b->positions + s0, *tables = b->tables + s0 * b->table_len;
+    const float *cur = input + s0 * PH_WIDTH;
     /* A layer reads its input only in the QKV prologue and the out-projection
      * residual, both before its last kernel writes `next`: in-place is safe. */
     for (size_t l = first; l < first + count; l++) {
         const float *norm = m->norms + l * 4 * PH_WIDTH;
-        float *next = (l + 1 == first + count) ? output : b->x;
+        float *next = (l + 1 == first + count) ? output + s0 * PH_WIDTH : x;
         const int pool_layer = (int)(l + pool_offset);
         const pgpu_gemm_input ln1 = {.ln_rows = cur, .ln_weight = norm,
                                      .ln_bias = norm + PH_WIDTH, .ln_epsilon = 1e-5f};
-        const pgpu_gemm_input att = {.attn_acc = b->scratch.part_acc,
-                                     .attn_ml = b->scratch.part_ml,
-                                     .attn_positions = b->positions,
+        const pgpu_gemm_input att = {.attn_acc = scratch.part_acc,
+                                     .attn_ml = scratch.part_ml,
+                                     .attn_positions = positions,
                                      .attn_max_splits = (int)b->max_splits};
-        const pgpu_gemm_input ln2 = {.ln_rows = b->r, .ln_weight = norm + 2 * PH_WIDTH,
+        const pgpu_gemm_input ln2 = {.ln_rows = r, .ln_weight = norm + 2 * PH_WIDTH,
                                      .ln_bias = norm + 3 * PH_WIDTH, .ln_epsilon = 1e-5f};
-        const pgpu_gemm_input hidden = {.split = b->xh};
-        if (!pgpu_gemm_qkv(st, &m->qkv[l], &ln1, n, &b->pool->kv, pool_layer, b->tables,
-                           (int)b->table_len, b->positions, rope, b->q, b->status) ||
-            !pgpu_attention(st, b->q, &b->pool->kv, pool_layer, b->tables, (int)b->table_len,
-                            b->positions, n, PH_HEADS, (int)b->max_splits, &b->scratch,
+        const pgpu_gemm_input hidden = {.split = xh};
+        if (!pgpu_gemm_qkv(stream, &m->qkv[l], &ln1, (int)n, &b->pool->kv, pool_layer, tables,
+                           (int)b->table_len, positions, rope, q, b->status) ||
+            !pgpu_attention(stream, q, &b->pool->kv, pool_layer, tables, (int)b->table_len,
+                            positions, (int)n, PH_HEADS, (int)b->max_splits, &scratch,
                             b->status) ||
-            !pgpu_gemm_residual(st, &m->out[l], &att, n, cur, b->r, b->status) ||
-            !pgpu_gemm_gelu_split(st, &m->mlp_in[l], &ln2, n, b->xh, b->status) ||
-            !pgpu_gemm_residual(st, &m->mlp_out[l], &hidden, n, b->r, next, b->status))
+            !pgpu_gemm_residual(stream, &m->out[l], &att, (int)n, cur, r, b->status) ||
+            !pgpu_gemm_gelu_split(stream, &m->mlp_in[l], &ln2, (int)n, xh, b->status) ||
+            !pgpu_gemm_residual(stream, &m->mlp_out[l], &hidden, (int)n, r, next, b->status))
             return 0;
         cur = next;
     }
     return 1;
 }
 
+int ph_batch_enqueue_layers(PhononFlowBatch *b, size_t first, size_t count, size_t pool_offset,
+                            const float *input, float *output, float theta) {
+    if (!b->streams || first + count > b->model->layers ||
+        first + count + pool_offset > (size_t)b->pool->kv.layers)
+        return 0;
+    const float *rope = ph_rope_table(theta);
+    return rope && enqueue_group(b, b->stream, 0, b->streams, first, count, pool_offset, input,
+                                 output, rope);
+}
+
+/* Stream groups of the step: tiles of 16 streams dealt into `groups` runs.
+ * Returns the group count actually used (a group holds >= 1 tile). */
+static size_t group_bounds(const PhononFlowBatch *b, size_t *first, size_t *count) {
+    const size_t tiles = (b->streams + 15) / 16;
+    const size_t groups = b->groups < tiles ? b->groups : tiles;
+    for (size_t g = 0; g < groups; g++) {
+        const size_t t0 = tiles * g / groups, t1 = tiles * (g + 1) / groups;
+        first[g] = t0 * 16;
+        const size_t end = t1 * 16 < b->streams ? t1 * 16 : b->streams;
+        count[g] = end - first[g];
+    }
+    return groups;
+}
+
+/* One step: each stream group runs all layers on its own HIP stream (forked
+ * from and joined back into the batch stream), so one group's latency-bound
+ * projections overlap another group's bandwidth-bound attention. */
 static int enqueue_step(PhononFlowBatch *b, const float *input, float *output, float theta) {
-    return ph_batch_enqueue_layers(b, 0, b->model->layers, 0, input, output, theta) &&
-           pgpu_advance_positions(b->stream, b->positions, (int)b->streams);
+    const float *rope = ph_rope_table(theta);
+    size_t first[PH_MAX_GROUPS], count[PH_MAX_GROUPS];
+    const size_t groups = group_bounds(b, first, count);
+    if (!rope || !groups)
+        return 0;
+    if (groups > 1 && !pgpu_event_record(b->fork, b->stream))
+        return 0;
+    for (size_t g = 1; g < groups; g++)
+        if (!pgpu_stream_wait_event(b->side[g - 1], b->fork))
+            return 0;
+    for (size_t g = 0; g < groups; g++)
+        if (!enqueue_group(b, g ? b->side[g - 1] : b->stream, first[g], count[g], 0,
+                           b->model->layers, 0, input, output, rope))
+            return 0;
+    for (size_t g = 1; g < groups; g++)
+        if (!pgpu_event_record(b->join[g - 1], b->side[g - 1]) ||
+            !pgpu_stream_wait_event(b->stream, b->join[g - 1]))
+            return 0;
+    return pgpu_advance_positions(b->stream, b->positions, (int)b->streams);
+}
+
+int phonon_flow_batch_set_groups(PhononFlowBatch *b, size_t groups) {
+    if (!b || !groups || groups > PH_MAX_GROUPS)
+        return 0;
+    if (b->groups != groups) {
+        pgpu_graph_destroy(b->graph);
+        b->graph = NULL;
+        b->groups = groups;
+    }
+    return 1;
+}
+
+int phonon_flow_batch_set_graph(PhononFlowBatch *b, int use_graph) {
+    if (!b)
+        return 0;
+    b->eager = !use_graph;
+    pgpu_graph_destroy(b->graph);
+    b->graph = NULL;
+    return 1;
 }
 
 int phonon_flow_batch_step_device(PhononFlowBatch *b, const float *inputs, float theta,
@@ -453,6 +534,13 @@ int phonon_flow_batch_step_device(PhononFlowBatch *b, const float *inputs, float
     for (size_t s = 0; s < b->streams; s++)
         if (b->host_positions[s] >= b->max_positions)
             return 0;
+    if (b->eager) {
+        if (!enqueue_step(b, inputs, outputs, theta))
+            return 0;
+        for (size_t s = 0; s < b->streams; s++)
+            b->host_positions[s]++;
+        return 1;
+    }
     if (!b->graph || b->graph_streams != b->streams || b->graph_theta != theta ||
         b->graph_input != inputs || b->graph_output != outputs) {
         pgpu_graph_destroy(b->graph);

@@ -446,6 +446,50 @@ def test_batch_block_placement_does_not_change_bits(lib, syn, pkg):
         assert np.array_equal(v1.view(np.uint32), v2.view(np.uint32))
 
 
+def test_stream_groups_do_not_change_bits(lib, syn, pkg):
+    """1, 2 or 4 concurrent stream groups (separate HIP streams in the graph)
+    compute every stream identically."""
+    layers = 2
+    model = syn.flow_model(151, layers)
+    views = pkg.Views()
+    w = views.layers(model)
+    rng = np.random.default_rng(152)
+    streams, max_pos = 40, 300
+    lengths = rng.integers(0, 280, size=streams)
+    table_len = (max_pos + 15) // 16
+    blocks = streams * table_len
+    ctx = rng.standard_normal((2, streams, layers, max_pos, 512)).astype(np.float32)
+    x = rng.standard_normal((3, streams, 512)).astype(np.float32)
+    results = []
+    for groups in (1, 2, 4):
+        bt = Batch(lib, w, layers, streams, max_pos, blocks)
+        assert lib.phonon_flow_batch_set_groups(bt.batch, groups)
+        ids = np.zeros(blocks, np.int32)
+        assert lib.phonon_kv_pool_alloc(bt.pool, blocks, i32p(ids))
+        tables = np.ascontiguousarray(np.sort(ids).reshape(streams, table_len).astype(np.int32))
+        for s in range(streams):
+            if lengths[s]:
+                assert lib.phonon_kv_pool_write(bt.pool, i32p(tables[s]), table_len, 0,
+                                                int(lengths[s]), fp(ctx[0, s]), fp(ctx[1, s]),
+                                                max_pos)
+        pos = lengths.astype(np.uintp)
+        assert lib.phonon_flow_batch_set_streams(
+            bt.batch, streams, pos.ctypes.data_as(ctypes.POINTER(ctypes.c_size_t)),
+            i32p(tables), table_len)
+        outs = []
+        for step in range(3):
+            y = np.zeros((streams, 512), np.float32)
+            assert lib.phonon_flow_batch_step(bt.batch, fp(np.ascontiguousarray(x[step])),
+                                              10000.0, fp(y)), pkg.last_error(lib)
+            outs.append(y.view(np.uint32).copy())
+        results.append(outs)
+        bt.close()
+    for other in results[1:]:
+        for a, b in zip(results[0], other):
+            assert np.array_equal(a, b)
+    assert not lib.phonon_flow_batch_set_groups(None, 2)
+
+
 def test_batch_graph_replay_equals_legacy_path(lib, syn, pkg):
     """The captured-graph batched step (B=1) and the drop-in stack step (no
     graph) run the same kernels: bit-identical outputs over 6 replays."""
