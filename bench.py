@@ -159,10 +159,26 @@ def run_decode(pkg, lib, layers, streams, lengths, steps, warmup, seed, groups=N
                "first_positions": first}
 
 
+PMC_SUMMARY = "profiles/k_attention_b64_hbm_traffic.md"
+
+
+def pmc_traffic():
+    """(traffic, algorithmic) bytes per split-attention launch recorded from
+    the rocprofv3 --pmc passes, or None if the summary is absent."""
+    try:
+        with open(os.path.join(ROOT, PMC_SUMMARY)) as f:
+            fields = dict(line.split(":", 1) for line in f if line.startswith(
+                ("traffic_bytes_per_launch:", "algorithmic_bytes_per_launch:")))
+        return (int(fields["traffic_bytes_per_launch"]),
+                int(fields["algorithmic_bytes_per_launch"]))
+    except (OSError, KeyError, ValueError):
+        return None
+
+
 def attention_roofline(pkg, lib, d, iterations=20):
     """Average duration of the split-attention kernel alone on the decode
-    workload (layer 0 of the pool, the streams' current contexts), timed with
-    HIP events on the stream it is launched on."""
+    workload (the layers of the pool in turn, the streams' current contexts),
+    timed with HIP events on the stream it is launched on."""
     pos = d.positions()
     view = pkg.PgpuPagedKv()
     assert lib.phonon_kv_pool_view(d.pool, ctypes.byref(view))
@@ -181,17 +197,19 @@ def attention_roofline(pkg, lib, d, iterations=20):
     scratch = pkg.PgpuAttentionScratch(part.ptr, part.ptr + slots * 64 * 4, streams, max_splits)
     status = words.ptr
 
-    def launch():
-        assert lib.pgpu_attention(d.stream, q.ptr, ctypes.byref(view), 0, tables.ptr,
+    def launch(layer):
+        assert lib.pgpu_attention(d.stream, q.ptr, ctypes.byref(view), layer, tables.ptr,
                                   d.table_len, positions.ptr, streams, 8, max_splits,
                                   ctypes.byref(scratch), status)
 
-    for _ in range(3):
-        launch()
+    # Layers in turn, as in a decode step: a launch never finds the previous
+    # launch's keys in the last-level cache.
+    for i in range(3):
+        launch(i % d.layers)
     timer = Timer(lib, d.stream)
     timer.start()
-    for _ in range(iterations):
-        launch()
+    for i in range(iterations):
+        launch((i + 3) % d.layers)
     ms = timer.stop_ms() / iterations
     contexts = pos + 1
     kv_bytes = int(KV_BYTES_PER_KEY * contexts.sum())
@@ -201,11 +219,59 @@ def attention_roofline(pkg, lib, d, iterations=20):
     lib.pgpu_copy_d2h(d.stream, st.ctypes.data, status, 4)
     for b in (q, tables, positions, part, words):
         b.free()
+    measured = pmc_traffic()
+    traffic_bytes = None
+    if measured:
+        # Counter passes are a separate run (bench.py --pmc-program): their
+        # traffic/algorithmic ratio applied to this launch's contexts.
+        traffic_bytes = int(round(kv_bytes * measured[0] / measured[1]))
     return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-            "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+            "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic_bytes,
+            "traffic_source": f"{PMC_SUMMARY} (FETCH_SIZE/WRITE_SIZE, copy-calibrated): "
+                              f"{measured[0]} B for {measured[1]} B algorithmic"
+                              if measured else None,
             "kernel": "pgpu::k_attention", "us_per_launch": round(ms * 1e3, 2),
             "algorithmic_bytes_per_launch": kv_bytes, "read_bytes_incl_q_out": traffic,
             "status_clean": int(st[0]) == 0}
+
+
+def calibration_copy(pkg, lib, d, repeats=5):
+    """A plain copy of known size for scaling hardware byte counters: all
+    layers of positions [0, n) of stream 0 from the pool to contiguous rows
+    (pgpu_kv_copy, 16 KiB-aligned 4 KiB tiles). Returns bytes read (= bytes
+    written) per launch."""
+    view = pkg.PgpuPagedKv()
+    assert lib.phonon_kv_pool_view(d.pool, ctypes.byref(view))
+    n = (d.max_positions // 16) * 16
+    row_bytes = 512 * 4
+    keys = pkg.DeviceBuffer(lib, d.layers * n * row_bytes)
+    values = pkg.DeviceBuffer(lib, d.layers * n * row_bytes)
+    tables = pkg.DeviceBuffer(lib, d.tables.nbytes)
+    tables.upload(d.tables)
+    words = pkg.DeviceBuffer(lib, 4)
+    lib.pgpu_memset(d.stream, words.ptr, 0, 4)
+    for _ in range(repeats):
+        assert lib.pgpu_kv_copy(d.stream, ctypes.byref(view), tables.ptr, 0, n, 0, d.layers,
+                                keys.ptr, values.ptr, n, 1, words.ptr)
+    assert lib.pgpu_stream_sync(d.stream)
+    for b in (keys, values, tables, words):
+        b.free()
+    return 2 * d.layers * n * row_bytes
+
+
+def pmc_program(pkg, lib, args):
+    """Short program for hardware-counter passes: the B=64 decode contexts,
+    20 launches of the split-attention kernel alone, then a calibration copy
+    of known size. Prints the algorithmic bytes of both."""
+    lengths = np.random.default_rng(args.seed).integers(1, 2049, size=args.batch) - 1
+    d = DecodeSetup(pkg, lib, args.layers, args.batch, lengths, 64, args.seed)
+    roof = attention_roofline(pkg, lib, d)
+    copied = calibration_copy(pkg, lib, d)
+    d.close()
+    print(json.dumps({"k_attention_algorithmic_bytes": roof["algorithmic_bytes_per_launch"],
+                      "k_attention_us": roof["us_per_launch"],
+                      "k_kv_copy_bytes_read": copied, "k_kv_copy_bytes_written": copied}),
+          flush=True)
 
 
 def q8_matvec_bench(pkg, lib, seed=1, calls=2000):
@@ -319,6 +385,9 @@ def main():
                     help="launch the step's kernels directly instead of a graph replay")
     ap.add_argument("--skip-extras", action="store_true",
                     help="only the headline B=64 line (no B=1, matvec, curve, CPU)")
+    ap.add_argument("--pmc-program", action="store_true",
+                    help="run only the attention kernel and a calibration copy, for "
+                         "rocprofv3 --pmc passes")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU: streams are independent and "
@@ -331,6 +400,9 @@ def main():
     name = ctypes.create_string_buffer(256)
     lib.pgpu_device_name(name, 256)
     log(f"device: {name.value.decode()}")
+    if args.pmc_program:
+        pmc_program(pkg, lib, args)
+        return
 
     lengths = np.random.default_rng(args.seed).integers(1, 2049, size=args.batch) - 1
     log(f"B={args.batch} L={args.layers}: contexts {lengths.min() + 1}..{lengths.max() + 1}")

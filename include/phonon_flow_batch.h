@@ -85,9 +85,9 @@ int phonon_flow_batch_step(PhononFlowBatch *batch, const float *inputs, float th
 int phonon_flow_batch_step_device(PhononFlowBatch *batch, const float *inputs, float theta,
                                   float *outputs);
 /* Runs the streams as `groups` (1..4) independent groups of whole 16-stream
- * tiles, each on its own HIP stream inside the step's graph, so one group's
- * projections overlap another's attention. Results do not depend on it.
- * Default 2 (a batch of at most 16 streams always runs as one group). */
+ * tiles, each on its own HIP stream inside the step's graph. Results do not
+ * depend on it. Default 1: on MI355X under ROCm 7 kernels of different HIP
+ * streams were measured not to overlap, so more groups only add launches. */
 int phonon_flow_batch_set_groups(PhononFlowBatch *batch, size_t groups);
 /* use_graph = 1 (default): step_device replays a captured HIP graph;
  * 0: it launches the step's kernels directly (e.g. for a caller that is

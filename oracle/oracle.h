@@ -11,7 +11,9 @@
  *   - Accelerate cblas_sgemm -> a sequential fp32 dot product per output,
  *     then alpha/beta as reference BLAS applies them;
  *   - SLEEF expf4/sinf4/cosf4 -> the system libm expf/sinf/cosf.
- * Pinning status per function is listed in oracle/README.md.
+ * Every function is pinned by tests/test_oracle.py: golden vectors from the
+ * reference's own tests, the compiled reference phonon_q8.c (oracle/_ref),
+ * closed forms, special cases and fp64 restatements. None is unpinned.
  */
 #ifndef PHONON_ORACLE_H
 #define PHONON_ORACLE_H

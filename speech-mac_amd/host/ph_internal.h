@@ -11,7 +11,7 @@
 #include <stdint.h>
 
 enum { PH_WIDTH = 512, PH_HEADS = 8, PH_HEAD = 64, PH_FFN = 2048, PH_SPLIT_KEYS = 256 };
-enum { PH_MAX_GROUPS = 4, PH_DEFAULT_GROUPS = 2 };
+enum { PH_MAX_GROUPS = 4, PH_DEFAULT_GROUPS = 1 };
 
 /* Device selection and the library's own HIP stream (created once). */
 int ph_init(void);
