@@ -38,13 +38,7 @@ struct AttnArgs {
     int *status;
 };
 
-__device__ inline float row16_sum(float v) {
-    v += __shfl_xor(v, 1);
-    v += __shfl_xor(v, 2);
-    v += __shfl_xor(v, 4);
-    v += __shfl_xor(v, 8);
-    return v;
-}
+
 
 __global__ __launch_bounds__(256) void k_attention(AttnArgs a) {
     const int split = blockIdx.x, head = blockIdx.y, s = blockIdx.z;

@@ -101,6 +101,20 @@ __device__ inline void store_split(uint16_t *__restrict__ xs, int s, int k, int 
     }
 }
 
+// Sum over each row of 16 lanes (DPP row rotations, then quad permutes; no
+// LDS traffic). Every lane of a row gets the same bits.
+__device__ inline float row16_sum(float v) {
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v),
+                                                                0x128, 0xf, 0xf, false));
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v),
+                                                                0x124, 0xf, 0xf, false));
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v),
+                                                                0x4E, 0xf, 0xf, false));
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v),
+                                                                0xB1, 0xf, 0xf, false));
+    return v;
+}
+
 __device__ inline float wave_sum(float v) {
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);

@@ -23,10 +23,15 @@
 //   from zero (int8 and bf16 terms multiply exactly), then acc += scale*c,
 //   i.e. the reference phonon_q8_dot order "sum += scale * partial".
 //   BF16: the three MFMAs chain straight into the accumulator.
-// Work decomposition
-//   One work-group = 16 output rows x 16 streams; its 4 waves split the
-//   column blocks into 4 contiguous ranges and are summed in LDS in wave
-//   order, so results do not depend on scheduling.
+// Work decomposition (results never depend on scheduling)
+//   SRC_SPLIT (k_gemm): one work-group = 16 output rows x 16 streams; its 4
+//   waves split the column blocks into 4 contiguous ranges, summed in LDS in
+//   wave order.
+//   SRC_LN / SRC_ATTN (k_gemm_tiles, K = 512): one work-group = 64 rows x 16
+//   streams; the prologue runs once, each wave takes a quarter of the
+//   column blocks of all 4 tiles, and the quarters are summed in wave order.
+//   One prologue per 4 tiles instead of per tile: the prologue, not the
+//   MFMAs, is what the kernel's latency is made of.
 #include <hip/hip_fp16.h>
 
 #include "pgpu_common.hpp"
@@ -114,9 +119,10 @@ __device__ inline void lds_store_block(uint16_t *bsh, int n, int kb, const float
 
 // LayerNorm of 16 streams' 512-wide rows into LDS split fragments. Thread
 // (n = tid/16, j = tid%16) owns columns [32j, 32j+32) of stream n; the 16
-// threads of a stream are 16 adjacent lanes of one wave. Two-pass fp32
-// moments; y = ((x - mean) * rstd) * w + b unfused, as the reference writes
-// it (src/phonon_transformer.c:179-183).
+// threads of a stream are one 16-lane row of a wave, so the row sums are DPP
+// row reductions. Two-pass fp32 moments (four partial sums per thread);
+// y = ((x - mean) * rstd) * w + b unfused, as the reference writes it
+// (src/phonon_transformer.c:179-183).
 __device__ inline bool prologue_ln(const GemmArgs &a, int st, uint16_t *bsh) {
     const int n = threadIdx.x >> 4, j = threadIdx.x & 15;
     const int s = st * 16 + n;
@@ -136,35 +142,37 @@ __device__ inline bool prologue_ln(const GemmArgs &a, int st, uint16_t *bsh) {
 #pragma unroll
         for (int i = 0; i < 32; i++) v[i] = 0.0f;
     }
-    float sum = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 32; i++) sum += v[i];
-#pragma unroll
-    for (int o = 1; o < 16; o <<= 1) sum += __shfl_xor(sum, o);
-    const float mean = sum * (1.0f / kWidth);
-    float sq = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 32; i++) {
-        const float c = v[i] - mean;
-        sq = fmaf(c, c, sq);
-    }
-#pragma unroll
-    for (int o = 1; o < 16; o <<= 1) sq += __shfl_xor(sq, o);
-    const float rstd = 1.0f / sqrtf(sq * (1.0f / kWidth) + a.ln_eps);
-    bool bad = false;
-    const float4 *w4 = (const float4 *)(a.ln_w + j * 32);
-    const float4 *b4 = (const float4 *)(a.ln_b + j * 32);
+    float4 wv[8], bv[8];
 #pragma unroll
     for (int i = 0; i < 8; i++) {
-        const float4 w = w4[i], b = b4[i];
-        const float ws[4] = {w.x, w.y, w.z, w.w}, bs[4] = {b.x, b.y, b.z, b.w};
+        wv[i] = ((const float4 *)(a.ln_w + j * 32))[i];
+        bv[i] = ((const float4 *)(a.ln_b + j * 32))[i];
+    }
+    float s4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int i = 0; i < 32; i++) s4[i & 3] += v[i];
+    const float mean = row16_sum((s4[0] + s4[1]) + (s4[2] + s4[3])) * (1.0f / kWidth);
+    float q4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int i = 0; i < 32; i++) {
+        const float c = __fsub_rn(v[i], mean);
+        q4[i & 3] = fmaf(c, c, q4[i & 3]);
+    }
+    const float var = row16_sum((q4[0] + q4[1]) + (q4[2] + q4[3])) * (1.0f / kWidth);
+    const float rstd = 1.0f / sqrtf(var + a.ln_eps);
+    bool bad = false;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const float ws[4] = {wv[i].x, wv[i].y, wv[i].z, wv[i].w};
+        const float bs[4] = {bv[i].x, bv[i].y, bv[i].z, bv[i].w};
 #pragma unroll
         for (int c = 0; c < 4; c++) {
             float &y = v[4 * i + c];
             y = __fadd_rn(__fmul_rn(__fmul_rn(__fsub_rn(y, mean), rstd), ws[c]), bs[c]);
-            bad |= live && !isfinite(y);
+            bad |= !isfinite(y);
         }
     }
+    bad &= live;
     if (!live) {
 #pragma unroll
         for (int i = 0; i < 32; i++) v[i] = 0.0f;
@@ -178,6 +186,8 @@ __device__ inline bool prologue_ln(const GemmArgs &a, int st, uint16_t *bsh) {
 // (the normalisation after P.V of src/phonon_transformer.c:395-403, merged
 // over splits in split order). Thread (n = tid/16, head h = (tid/2)%8,
 // half = tid%2) produces 32 dims = column block 2h + half of stream n.
+// Loads are issued in groups (8 split maxima, then 2 splits' rows) so their
+// latencies overlap instead of following one another.
 __device__ inline bool prologue_attn(const GemmArgs &a, int st, uint16_t *bsh) {
     const int n = threadIdx.x >> 4, h = (threadIdx.x >> 1) & 7, half = threadIdx.x & 1;
     const int s = st * 16 + n;
@@ -189,20 +199,39 @@ __device__ inline bool prologue_attn(const GemmArgs &a, int st, uint16_t *bsh) {
         const int count = a.positions[s] + 1;
         const int nsplit = min((count + kSplitKeys - 1) / kSplitKeys, a.max_splits);
         const size_t first = ((size_t)s * kHeads + h) * a.max_splits;
+        const float2 *ml = (const float2 *)a.part_ml + first;
         float mx = -INFINITY;
-        for (int j = 0; j < nsplit; j++) mx = fmaxf(mx, a.part_ml[(first + j) * 2]);
-        float total = 0.0f;
-        for (int j = 0; j < nsplit; j++) {
-            const float f = expf(a.part_ml[(first + j) * 2] - mx);
-            total = fmaf(a.part_ml[(first + j) * 2 + 1], f, total);
-            const float4 *acc = (const float4 *)(a.part_acc + (first + j) * 64 + half * 32);
+        for (int j0 = 0; j0 < nsplit; j0 += 8) {
+            float m8[8];
 #pragma unroll
-            for (int i = 0; i < 8; i++) {
-                const float4 x = acc[i];
-                v[4 * i] = fmaf(x.x, f, v[4 * i]);
-                v[4 * i + 1] = fmaf(x.y, f, v[4 * i + 1]);
-                v[4 * i + 2] = fmaf(x.z, f, v[4 * i + 2]);
-                v[4 * i + 3] = fmaf(x.w, f, v[4 * i + 3]);
+            for (int u = 0; u < 8; u++) m8[u] = j0 + u < nsplit ? ml[j0 + u].x : -INFINITY;
+#pragma unroll
+            for (int u = 0; u < 8; u++) mx = fmaxf(mx, m8[u]);
+        }
+        float total = 0.0f;
+        for (int j0 = 0; j0 < nsplit; j0 += 2) {
+            float2 ml2[2];
+            float4 acc[2][8];
+#pragma unroll
+            for (int u = 0; u < 2; u++) {
+                const int j = min(j0 + u, nsplit - 1);
+                ml2[u] = ml[j];
+                const float4 *src = (const float4 *)(a.part_acc + (first + j) * 64 + half * 32);
+#pragma unroll
+                for (int i = 0; i < 8; i++) acc[u][i] = src[i];
+            }
+#pragma unroll
+            for (int u = 0; u < 2; u++) {
+                if (j0 + u >= nsplit) break;
+                const float f = expf(ml2[u].x - mx);
+                total = fmaf(ml2[u].y, f, total);
+#pragma unroll
+                for (int i = 0; i < 8; i++) {
+                    v[4 * i] = fmaf(acc[u][i].x, f, v[4 * i]);
+                    v[4 * i + 1] = fmaf(acc[u][i].y, f, v[4 * i + 1]);
+                    v[4 * i + 2] = fmaf(acc[u][i].z, f, v[4 * i + 2]);
+                    v[4 * i + 3] = fmaf(acc[u][i].w, f, v[4 * i + 3]);
+                }
             }
         }
         bad = !(total > 0.0f) || !isfinite(total);
@@ -320,78 +349,11 @@ __device__ inline void load_epilogue(EpiOperands &e, const GemmArgs &a, int s, i
     }
 }
 
-template <int SRC, int EPI, bool Q8, int CH>
-__global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
-    const int tile = blockIdx.x, st = blockIdx.y;
-    // Uniform per wave (readfirstlane): the block loop below is scalar control.
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int lane = threadIdx.x & 63;
-    const int kbn = a.k_cols >> 5;
-    const int per_wave = (kbn + 3) >> 2;
-    const int kb_begin = wave * per_wave;
-    const int kb_end = min(kbn, kb_begin + per_wave);
-
-    // D fragment of this lane: rows row0 .. row0+3 of stream s.
-    const int s = st * 16 + (lane & 15);
-    const int row0 = tile * 16 + (lane >> 4) * 4;
-    const bool live = s < a.streams;
-
-    // Everything that does not depend on the prologue is requested first, so
-    // its memory latency overlaps the prologue: the first weight chunk and
-    // the epilogue's operands (wave 0 runs the epilogue).
-    WChunk<Q8, CH> w;
-    if (kb_begin < kb_end) load_weights(w, a, tile, kbn, lane, kb_begin, kb_end);
-    EpiOperands e;
-    if (wave == 0) load_epilogue<EPI>(e, a, s, row0, live);
-
-    // Prologue-built operands hold 16 streams x 512 columns x 3 terms (48 KB).
-    __shared__ uint16_t bsh[SRC == SRC_SPLIT ? 8 : 16 * kLdsBlock];
-    bool bad_in = false;
-    if constexpr (SRC == SRC_LN) bad_in = prologue_ln(a, st, bsh);
-    if constexpr (SRC == SRC_ATTN) bad_in = prologue_attn(a, st, bsh);
-    if constexpr (SRC != SRC_SPLIT) {
-        flag_nonfinite(a.status, bad_in);
-        __syncthreads();
-    }
-
-    const uint16_t *xs = SRC == SRC_SPLIT ? a.xs + (size_t)st * kbn * 1536 + lane * 8
-                                          : bsh + lane * 8;
-    f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-    // Chunks of CH blocks; the next chunk's weights are requested before the
-    // current chunk's MFMAs (past the wave's range the last block is re-read
-    // and not used).
-    for (int kb0 = kb_begin; kb0 < kb_end; kb0 += CH) {
-        bf16x8 xh[CH], xm[CH], xl[CH];
-#pragma unroll
-        for (int u = 0; u < CH; u++) {
-            // Column blocks are 1536 elements apart in global split buffers,
-            // kLdsBlock apart in the padded LDS operand buffer.
-            const size_t kb = (size_t)min(kb0 + u, kb_end - 1) *
-                              (SRC == SRC_SPLIT ? 1536 : kLdsBlock);
-            xh[u] = *(const bf16x8 *)(xs + kb);
-            xm[u] = *(const bf16x8 *)(xs + kb + 512);
-            xl[u] = *(const bf16x8 *)(xs + kb + 1024);
-        }
-        WChunk<Q8, CH> next;
-        if (kb0 + CH < kb_end) load_weights(next, a, tile, kbn, lane, kb0 + CH, kb_end);
-        mfma_chunk(acc, w, xh, xm, xl, kb0, kb_end);
-        w = next;
-    }
-
-    __shared__ f32x4 partial[4][64];
-    partial[wave][lane] = acc;
-    __syncthreads();
-    if (wave != 0) return;  // no barrier follows
-    f32x4 v = partial[0][lane];
-#pragma unroll
-    for (int w = 1; w < 4; w++) {
-        const f32x4 p = partial[w][lane];
-        v[0] = __fadd_rn(v[0], p[0]);
-        v[1] = __fadd_rn(v[1], p[1]);
-        v[2] = __fadd_rn(v[2], p[2]);
-        v[3] = __fadd_rn(v[3], p[3]);
-    }
-
+// Consumer of one lane's four results v (rows row0..row0+3 of stream s).
+// Returns true if a non-finite value was produced.
+template <int EPI>
+__device__ inline bool epilogue(const GemmArgs &a, const EpiOperands &e, const f32x4 &v, int s,
+                                int row0, bool live) {
     bool bad = false;
     if constexpr (EPI == EPI_STORE || EPI == EPI_RESIDUAL) {
         if (live) {
@@ -450,7 +412,143 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
             }
         }
     }
-    flag_nonfinite(a.status, bad);
+    return bad;
+}
+
+// Projection of split-fragment rows from global memory (any K): one
+// work-group = 16 rows x 16 streams; its 4 waves split the column blocks into
+// 4 contiguous ranges and are summed in LDS in wave order.
+template <int EPI, bool Q8, int CH>
+__global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
+    const int tile = blockIdx.x, st = blockIdx.y;
+    // Uniform per wave (readfirstlane): the block loop below is scalar control.
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    const int kbn = a.k_cols >> 5;
+    const int per_wave = (kbn + 3) >> 2;
+    const int kb_begin = wave * per_wave;
+    const int kb_end = min(kbn, kb_begin + per_wave);
+
+    // D fragment of this lane: rows row0 .. row0+3 of stream s.
+    const int s = st * 16 + (lane & 15);
+    const int row0 = tile * 16 + (lane >> 4) * 4;
+    const bool live = s < a.streams;
+
+    // The first weight chunk and the epilogue's operands (wave 0 runs the
+    // epilogue) are requested first.
+    WChunk<Q8, CH> w;
+    if (kb_begin < kb_end) load_weights(w, a, tile, kbn, lane, kb_begin, kb_end);
+    EpiOperands e;
+    if (wave == 0) load_epilogue<EPI>(e, a, s, row0, live);
+
+    const uint16_t *xs = a.xs + (size_t)st * kbn * 1536 + lane * 8;
+    f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    // Chunks of CH blocks; the next chunk's weights are requested before the
+    // current chunk's MFMAs (past the wave's range the last block is re-read
+    // and not used).
+    for (int kb0 = kb_begin; kb0 < kb_end; kb0 += CH) {
+        bf16x8 xh[CH], xm[CH], xl[CH];
+#pragma unroll
+        for (int u = 0; u < CH; u++) {
+            const size_t kb = (size_t)min(kb0 + u, kb_end - 1) * 1536;
+            xh[u] = *(const bf16x8 *)(xs + kb);
+            xm[u] = *(const bf16x8 *)(xs + kb + 512);
+            xl[u] = *(const bf16x8 *)(xs + kb + 1024);
+        }
+        WChunk<Q8, CH> next;
+        if (kb0 + CH < kb_end) load_weights(next, a, tile, kbn, lane, kb0 + CH, kb_end);
+        mfma_chunk(acc, w, xh, xm, xl, kb0, kb_end);
+        w = next;
+    }
+
+    __shared__ f32x4 partial[4][64];
+    partial[wave][lane] = acc;
+    __syncthreads();
+    if (wave != 0) return;  // no barrier follows
+    f32x4 v = partial[0][lane];
+#pragma unroll
+    for (int w = 1; w < 4; w++) {
+        const f32x4 p = partial[w][lane];
+        v[0] = __fadd_rn(v[0], p[0]);
+        v[1] = __fadd_rn(v[1], p[1]);
+        v[2] = __fadd_rn(v[2], p[2]);
+        v[3] = __fadd_rn(v[3], p[3]);
+    }
+
+    flag_nonfinite(a.status, epilogue<EPI>(a, e, v, s, row0, live));
+}
+
+// Projection whose operand a prologue builds (LayerNorm or the attention
+// merge; K = 512): one work-group = 4 row tiles x 16 streams, so the
+// prologue runs once per 64 rows. Wave w takes column blocks [4w, 4w+4) of
+// all 4 tiles: it reads its B operands from LDS once, and its 4 tile
+// accumulators are independent MFMA chains. The 4 waves' partial sums are
+// then added in wave order (the order of k_gemm), and wave w finishes tile w.
+// The wave's weights and epilogue operands are requested before the
+// prologue, so their latency overlaps it.
+template <int SRC, int EPI, bool Q8>
+__global__ __launch_bounds__(256) void k_gemm_tiles(GemmArgs a) {
+    constexpr int kbn = kWidth / 32, KBW = kbn / 4, TPW = 4;
+    const int st = blockIdx.y;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    const int tiles = a.n_rows >> 4;
+    const int tile0 = blockIdx.x * TPW;
+    const int kb0 = wave * KBW;
+    const int s = st * 16 + (lane & 15);
+    const bool live = s < a.streams;
+
+    // Weights of blocks [kb0, kb0+4) of the 4 tiles (a tile past the matrix
+    // re-reads the last one; its results are not stored).
+    WChunk<Q8, KBW> w[TPW];
+#pragma unroll
+    for (int t = 0; t < TPW; t++)
+        load_weights(w[t], a, min(tile0 + t, tiles - 1), kbn, lane, kb0, kb0 + KBW);
+    // This wave finishes tile tile0 + wave.
+    const int tile = tile0 + wave;
+    const bool active = tile < tiles;  // uniform per wave
+    const int row0 = tile * 16 + (lane >> 4) * 4;
+    EpiOperands e;
+    if (active) load_epilogue<EPI>(e, a, s, row0, live);
+
+    __shared__ uint16_t bsh[16 * kLdsBlock];
+    const bool bad_in = SRC == SRC_LN ? prologue_ln(a, st, bsh) : prologue_attn(a, st, bsh);
+    flag_nonfinite(a.status, bad_in);
+    __syncthreads();
+
+    bf16x8 xh[KBW], xm[KBW], xl[KBW];
+    const uint16_t *xs = bsh + kb0 * kLdsBlock + lane * 8;
+#pragma unroll
+    for (int u = 0; u < KBW; u++) {
+        xh[u] = *(const bf16x8 *)(xs + u * kLdsBlock);
+        xm[u] = *(const bf16x8 *)(xs + u * kLdsBlock + 512);
+        xl[u] = *(const bf16x8 *)(xs + u * kLdsBlock + 1024);
+    }
+    f32x4 acc[TPW];
+#pragma unroll
+    for (int t = 0; t < TPW; t++) {
+        acc[t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        mfma_chunk(acc[t], w[t], xh, xm, xl, kb0, kb0 + KBW);
+    }
+
+    // Partial sums through LDS (the operand buffer is free once every wave
+    // has its B operands): partial[t][w] for tile t, wave w.
+    __syncthreads();
+    f32x4 *partial = (f32x4 *)bsh;
+#pragma unroll
+    for (int t = 0; t < TPW; t++) partial[(t * 4 + wave) * 64 + lane] = acc[t];
+    __syncthreads();
+    if (!active) return;  // no barrier follows
+    f32x4 v = partial[(wave * 4) * 64 + lane];
+#pragma unroll
+    for (int w2 = 1; w2 < 4; w2++) {
+        const f32x4 p = partial[(wave * 4 + w2) * 64 + lane];
+        v[0] = __fadd_rn(v[0], p[0]);
+        v[1] = __fadd_rn(v[1], p[1]);
+        v[2] = __fadd_rn(v[2], p[2]);
+        v[3] = __fadd_rn(v[3], p[3]);
+    }
+    flag_nonfinite(a.status, epilogue<EPI>(a, e, v, s, row0, live));
 }
 
 template <int SRC, int EPI, bool Q8>
@@ -458,12 +556,17 @@ static int launch(const GemmArgs &a, hipStream_t stream) {
     if (a.n_rows <= 0 || a.n_rows % 16 || a.k_cols <= 0 || a.k_cols % 32 || a.streams <= 0 ||
         (SRC != SRC_SPLIT && a.k_cols != kWidth))
         return bad_arguments("pgpu_gemm");
-    dim3 grid(a.n_rows / 16, (a.streams + 15) / 16);
-    // Up to 4 column blocks per wave (K <= 512): one chunk of 4; else chunks of 8.
-    if (a.k_cols <= 512)
-        hipLaunchKernelGGL((k_gemm<SRC, EPI, Q8, 4>), grid, dim3(256), 0, stream, a);
-    else
-        hipLaunchKernelGGL((k_gemm<SRC, EPI, Q8, 8>), grid, dim3(256), 0, stream, a);
+    if constexpr (SRC != SRC_SPLIT) {
+        const dim3 grid((a.n_rows / 16 + 3) / 4, (a.streams + 15) / 16);
+        hipLaunchKernelGGL((k_gemm_tiles<SRC, EPI, Q8>), grid, dim3(256), 0, stream, a);
+    } else {
+        const dim3 grid(a.n_rows / 16, (a.streams + 15) / 16);
+        // Up to 4 column blocks per wave (K <= 512): one chunk of 4; else chunks of 8.
+        if (a.k_cols <= 512)
+            hipLaunchKernelGGL((k_gemm<EPI, Q8, 4>), grid, dim3(256), 0, stream, a);
+        else
+            hipLaunchKernelGGL((k_gemm<EPI, Q8, 8>), grid, dim3(256), 0, stream, a);
+    }
     return launch_ok("pgpu_gemm");
 }
 
