@@ -27,11 +27,12 @@
 //   SRC_SPLIT (k_gemm): one work-group = 16 output rows x 16 streams; its 4
 //   waves split the column blocks into 4 contiguous ranges, summed in LDS in
 //   wave order.
-//   SRC_LN / SRC_ATTN (k_gemm_tiles, K = 512): one work-group = 64 rows x 16
-//   streams; the prologue runs once, each wave takes a quarter of the
-//   column blocks of all 4 tiles, and the quarters are summed in wave order.
-//   One prologue per 4 tiles instead of per tile: the prologue, not the
-//   MFMAs, is what the kernel's latency is made of.
+//   SRC_LN / SRC_ATTN (k_gemm_wide, K = 512): one 1024-thread work-group =
+//   64 rows x 16 streams; the prologue runs once with one wave per stream,
+//   then 16 waves take (tile, quarter of the column blocks) pairs and the
+//   quarters are summed in order. One prologue per 4 tiles, spread over 16
+//   waves: the prologue, not the MFMAs, is what the kernel's latency is
+//   made of.
 #include <hip/hip_fp16.h>
 
 #include "pgpu_common.hpp"
@@ -95,105 +96,91 @@ __device__ inline float half_to_float(uint32_t bits16) {
 // 16 blocks one writer wave touches on distinct banks.
 constexpr int kLdsBlock = 1536 + 8;
 
-// Writes 32 activations of stream n (0..15 in the tile), columns
-// [32kb, 32kb+32), into the LDS operand buffer.
-__device__ inline void lds_store_block(uint16_t *bsh, int n, int kb, const float *v) {
+// Writes 8 activations of stream n (0..15 in the tile), columns
+// [32kb + 8g, 32kb + 8g + 8), into the LDS operand buffer: one 16-byte
+// record per split term.
+__device__ inline void lds_store8(uint16_t *bsh, int n, int kb, int g, const float *v) {
+    uint16_t h[8], m[8], l[8];
 #pragma unroll
-    for (int g = 0; g < 4; g++) {
-        uint16_t h[8], m[8], l[8];
+    for (int i = 0; i < 8; i++) split3(v[i], h[i], m[i], l[i]);
+    uint16_t *rec = bsh + kb * kLdsBlock + (g * 16 + n) * 8;
 #pragma unroll
-        for (int i = 0; i < 8; i++) split3(v[g * 8 + i], h[i], m[i], l[i]);
-        uint16_t *rec = bsh + kb * kLdsBlock + (g * 16 + n) * 8;
-#pragma unroll
-        for (int p = 0; p < 3; p++) {
-            const uint16_t *src = p == 0 ? h : (p == 1 ? m : l);
-            uint4 q;
-            q.x = src[0] | (uint32_t)src[1] << 16;
-            q.y = src[2] | (uint32_t)src[3] << 16;
-            q.z = src[4] | (uint32_t)src[5] << 16;
-            q.w = src[6] | (uint32_t)src[7] << 16;
-            *(uint4 *)(rec + p * 512) = q;
-        }
+    for (int p = 0; p < 3; p++) {
+        const uint16_t *src = p == 0 ? h : (p == 1 ? m : l);
+        uint4 q;
+        q.x = src[0] | (uint32_t)src[1] << 16;
+        q.y = src[2] | (uint32_t)src[3] << 16;
+        q.z = src[4] | (uint32_t)src[5] << 16;
+        q.w = src[6] | (uint32_t)src[7] << 16;
+        *(uint4 *)(rec + p * 512) = q;
     }
 }
 
-// LayerNorm of 16 streams' 512-wide rows into LDS split fragments. Thread
-// (n = tid/16, j = tid%16) owns columns [32j, 32j+32) of stream n; the 16
-// threads of a stream are one 16-lane row of a wave, so the row sums are DPP
-// row reductions. Two-pass fp32 moments (four partial sums per thread);
-// y = ((x - mean) * rstd) * w + b unfused, as the reference writes it
-// (src/phonon_transformer.c:179-183).
+// Sum over the 64 lanes of a wave; every lane gets the same bits.
+__device__ inline float wave_sum64(float v) {
+    v = row16_sum(v);
+    v += __shfl_xor(v, 16);
+    v += __shfl_xor(v, 32);
+    return v;
+}
+
+// LayerNorm of 16 streams' 512-wide rows into LDS split fragments, by a
+// 1024-thread work-group: wave n normalises stream n, lane j owns columns
+// [8j, 8j+8). Two-pass fp32 moments; y = ((x - mean) * rstd) * w + b
+// unfused, as the reference writes it (src/phonon_transformer.c:179-183).
 __device__ inline bool prologue_ln(const GemmArgs &a, int st, uint16_t *bsh) {
-    const int n = threadIdx.x >> 4, j = threadIdx.x & 15;
+    const int n = threadIdx.x >> 6, j = threadIdx.x & 63;
     const int s = st * 16 + n;
-    float v[32];
-    const bool live = s < a.streams;
+    const bool live = s < a.streams;  // uniform per wave
+    float v[8];
+    const float4 w0 = *(const float4 *)(a.ln_w + j * 8), w1 = *(const float4 *)(a.ln_w + j * 8 + 4);
+    const float4 b0 = *(const float4 *)(a.ln_b + j * 8), b1 = *(const float4 *)(a.ln_b + j * 8 + 4);
     if (live) {
-        const float4 *row = (const float4 *)(a.ln_x + (size_t)s * kWidth + j * 32);
-#pragma unroll
-        for (int i = 0; i < 8; i++) {
-            const float4 x = row[i];
-            v[4 * i] = x.x;
-            v[4 * i + 1] = x.y;
-            v[4 * i + 2] = x.z;
-            v[4 * i + 3] = x.w;
-        }
+        const float4 x0 = *(const float4 *)(a.ln_x + (size_t)s * kWidth + j * 8);
+        const float4 x1 = *(const float4 *)(a.ln_x + (size_t)s * kWidth + j * 8 + 4);
+        v[0] = x0.x; v[1] = x0.y; v[2] = x0.z; v[3] = x0.w;
+        v[4] = x1.x; v[5] = x1.y; v[6] = x1.z; v[7] = x1.w;
     } else {
 #pragma unroll
-        for (int i = 0; i < 32; i++) v[i] = 0.0f;
+        for (int i = 0; i < 8; i++) v[i] = 0.0f;
     }
-    float4 wv[8], bv[8];
+    const float mean =
+        wave_sum64(((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]))) *
+        (1.0f / kWidth);
+    float q2[2] = {0.0f, 0.0f};
 #pragma unroll
     for (int i = 0; i < 8; i++) {
-        wv[i] = ((const float4 *)(a.ln_w + j * 32))[i];
-        bv[i] = ((const float4 *)(a.ln_b + j * 32))[i];
-    }
-    float s4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-    for (int i = 0; i < 32; i++) s4[i & 3] += v[i];
-    const float mean = row16_sum((s4[0] + s4[1]) + (s4[2] + s4[3])) * (1.0f / kWidth);
-    float q4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-    for (int i = 0; i < 32; i++) {
         const float c = __fsub_rn(v[i], mean);
-        q4[i & 3] = fmaf(c, c, q4[i & 3]);
+        q2[i & 1] = fmaf(c, c, q2[i & 1]);
     }
-    const float var = row16_sum((q4[0] + q4[1]) + (q4[2] + q4[3])) * (1.0f / kWidth);
+    const float var = wave_sum64(q2[0] + q2[1]) * (1.0f / kWidth);
     const float rstd = 1.0f / sqrtf(var + a.ln_eps);
+    const float ws[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+    const float bs[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
     bool bad = false;
 #pragma unroll
     for (int i = 0; i < 8; i++) {
-        const float ws[4] = {wv[i].x, wv[i].y, wv[i].z, wv[i].w};
-        const float bs[4] = {bv[i].x, bv[i].y, bv[i].z, bv[i].w};
-#pragma unroll
-        for (int c = 0; c < 4; c++) {
-            float &y = v[4 * i + c];
-            y = __fadd_rn(__fmul_rn(__fmul_rn(__fsub_rn(y, mean), rstd), ws[c]), bs[c]);
-            bad |= !isfinite(y);
-        }
+        v[i] = __fadd_rn(__fmul_rn(__fmul_rn(__fsub_rn(v[i], mean), rstd), ws[i]), bs[i]);
+        bad |= !isfinite(v[i]);
+        if (!live) v[i] = 0.0f;
     }
-    bad &= live;
-    if (!live) {
-#pragma unroll
-        for (int i = 0; i < 32; i++) v[i] = 0.0f;
-    }
-    lds_store_block(bsh, n, j, v);
-    return bad;
+    lds_store8(bsh, n, j >> 2, j & 3, v);
+    return bad && live;
 }
 
 // Merges the split-attention partials of 16 streams x 8 heads into LDS split
 // fragments: out = sum_j acc_j e^(m_j - M) / sum_j l_j e^(m_j - M), M = max m_j
 // (the normalisation after P.V of src/phonon_transformer.c:395-403, merged
-// over splits in split order). Thread (n = tid/16, head h = (tid/2)%8,
-// half = tid%2) produces 32 dims = column block 2h + half of stream n.
-// Loads are issued in groups (8 split maxima, then 2 splits' rows) so their
-// latencies overlap instead of following one another.
+// over splits in split order), by a 1024-thread work-group: wave n merges
+// stream n, lane (h = j/8, part = j%8) dims [8 part, 8 part + 8) of head h.
+// Loads are issued in groups of splits so their latencies overlap.
 __device__ inline bool prologue_attn(const GemmArgs &a, int st, uint16_t *bsh) {
-    const int n = threadIdx.x >> 4, h = (threadIdx.x >> 1) & 7, half = threadIdx.x & 1;
+    const int n = threadIdx.x >> 6, j = threadIdx.x & 63;
+    const int h = j >> 3, part = j & 7;
     const int s = st * 16 + n;
-    float v[32];
+    float v[8];
 #pragma unroll
-    for (int i = 0; i < 32; i++) v[i] = 0.0f;
+    for (int i = 0; i < 8; i++) v[i] = 0.0f;
     bool bad = false;
     if (s < a.streams) {
         const int count = a.positions[s] + 1;
@@ -209,24 +196,24 @@ __device__ inline bool prologue_attn(const GemmArgs &a, int st, uint16_t *bsh) {
             for (int u = 0; u < 8; u++) mx = fmaxf(mx, m8[u]);
         }
         float total = 0.0f;
-        for (int j0 = 0; j0 < nsplit; j0 += 2) {
-            float2 ml2[2];
-            float4 acc[2][8];
+        for (int j0 = 0; j0 < nsplit; j0 += 4) {
+            float2 ml4[4];
+            float4 acc[4][2];
 #pragma unroll
-            for (int u = 0; u < 2; u++) {
-                const int j = min(j0 + u, nsplit - 1);
-                ml2[u] = ml[j];
-                const float4 *src = (const float4 *)(a.part_acc + (first + j) * 64 + half * 32);
-#pragma unroll
-                for (int i = 0; i < 8; i++) acc[u][i] = src[i];
+            for (int u = 0; u < 4; u++) {
+                const int js = min(j0 + u, nsplit - 1);
+                ml4[u] = ml[js];
+                const float4 *src = (const float4 *)(a.part_acc + (first + js) * 64 + part * 8);
+                acc[u][0] = src[0];
+                acc[u][1] = src[1];
             }
 #pragma unroll
-            for (int u = 0; u < 2; u++) {
+            for (int u = 0; u < 4; u++) {
                 if (j0 + u >= nsplit) break;
-                const float f = expf(ml2[u].x - mx);
-                total = fmaf(ml2[u].y, f, total);
+                const float f = expf(ml4[u].x - mx);
+                total = fmaf(ml4[u].y, f, total);
 #pragma unroll
-                for (int i = 0; i < 8; i++) {
+                for (int i = 0; i < 2; i++) {
                     v[4 * i] = fmaf(acc[u][i].x, f, v[4 * i]);
                     v[4 * i + 1] = fmaf(acc[u][i].y, f, v[4 * i + 1]);
                     v[4 * i + 2] = fmaf(acc[u][i].z, f, v[4 * i + 2]);
@@ -237,16 +224,17 @@ __device__ inline bool prologue_attn(const GemmArgs &a, int st, uint16_t *bsh) {
         bad = !(total > 0.0f) || !isfinite(total);
         const float inv = 1.0f / total;
 #pragma unroll
-        for (int i = 0; i < 32; i++) {
+        for (int i = 0; i < 8; i++) {
             v[i] *= inv;
             bad |= !isfinite(v[i]);
         }
         if (bad) {
 #pragma unroll
-            for (int i = 0; i < 32; i++) v[i] = 0.0f;
+            for (int i = 0; i < 8; i++) v[i] = 0.0f;
         }
     }
-    lds_store_block(bsh, n, 2 * h + half, v);
+    // Column 64h + 8 part: block 2h + part/4, group part%4.
+    lds_store8(bsh, n, 2 * h + (part >> 2), part & 3, v);
     return bad;
 }
 
@@ -479,70 +467,61 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
 }
 
 // Projection whose operand a prologue builds (LayerNorm or the attention
-// merge; K = 512): one work-group = 4 row tiles x 16 streams, so the
-// prologue runs once per 64 rows. Wave w takes column blocks [4w, 4w+4) of
-// all 4 tiles: it reads its B operands from LDS once, and its 4 tile
-// accumulators are independent MFMA chains. The 4 waves' partial sums are
-// then added in wave order (the order of k_gemm), and wave w finishes tile w.
-// The wave's weights and epilogue operands are requested before the
+// merge; K = 512), by a 1024-thread work-group of 4 row tiles x 16 streams.
+// The prologue runs once per 64 rows with 8 values per lane (one wave per
+// stream), which keeps its latency short. Wave w = 4q + t then computes
+// column blocks [4q, 4q+4) of tile t; the 4 quarters of a tile are added in
+// quarter order (as k_gemm adds its waves), and wave t finishes tile t. The
+// wave's weights and the epilogue operands are requested before the
 // prologue, so their latency overlaps it.
 template <int SRC, int EPI, bool Q8>
-__global__ __launch_bounds__(256) void k_gemm_tiles(GemmArgs a) {
-    constexpr int kbn = kWidth / 32, KBW = kbn / 4, TPW = 4;
+__global__ __launch_bounds__(1024) void k_gemm_wide(GemmArgs a) {
+    constexpr int kbn = kWidth / 32, KBW = kbn / 4;
     const int st = blockIdx.y;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     const int tiles = a.n_rows >> 4;
-    const int tile0 = blockIdx.x * TPW;
-    const int kb0 = wave * KBW;
+    const int t = wave & 3, q = wave >> 2;
+    const int tile = blockIdx.x * 4 + t;
+    const bool active = tile < tiles;  // uniform per wave
+    const int kb0 = q * KBW;
     const int s = st * 16 + (lane & 15);
     const bool live = s < a.streams;
-
-    // Weights of blocks [kb0, kb0+4) of the 4 tiles (a tile past the matrix
-    // re-reads the last one; its results are not stored).
-    WChunk<Q8, KBW> w[TPW];
-#pragma unroll
-    for (int t = 0; t < TPW; t++)
-        load_weights(w[t], a, min(tile0 + t, tiles - 1), kbn, lane, kb0, kb0 + KBW);
-    // This wave finishes tile tile0 + wave.
-    const int tile = tile0 + wave;
-    const bool active = tile < tiles;  // uniform per wave
     const int row0 = tile * 16 + (lane >> 4) * 4;
+
+    WChunk<Q8, KBW> w;
+    if (active) load_weights(w, a, tile, kbn, lane, kb0, kb0 + KBW);
     EpiOperands e;
-    if (active) load_epilogue<EPI>(e, a, s, row0, live);
+    if (active && q == 0) load_epilogue<EPI>(e, a, s, row0, live);
 
     __shared__ uint16_t bsh[16 * kLdsBlock];
     const bool bad_in = SRC == SRC_LN ? prologue_ln(a, st, bsh) : prologue_attn(a, st, bsh);
     flag_nonfinite(a.status, bad_in);
     __syncthreads();
 
-    bf16x8 xh[KBW], xm[KBW], xl[KBW];
-    const uint16_t *xs = bsh + kb0 * kLdsBlock + lane * 8;
+    f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (active) {
+        bf16x8 xh[KBW], xm[KBW], xl[KBW];
+        const uint16_t *xs = bsh + kb0 * kLdsBlock + lane * 8;
 #pragma unroll
-    for (int u = 0; u < KBW; u++) {
-        xh[u] = *(const bf16x8 *)(xs + u * kLdsBlock);
-        xm[u] = *(const bf16x8 *)(xs + u * kLdsBlock + 512);
-        xl[u] = *(const bf16x8 *)(xs + u * kLdsBlock + 1024);
+        for (int u = 0; u < KBW; u++) {
+            xh[u] = *(const bf16x8 *)(xs + u * kLdsBlock);
+            xm[u] = *(const bf16x8 *)(xs + u * kLdsBlock + 512);
+            xl[u] = *(const bf16x8 *)(xs + u * kLdsBlock + 1024);
+        }
+        mfma_chunk(acc, w, xh, xm, xl, kb0, kb0 + KBW);
     }
-    f32x4 acc[TPW];
-#pragma unroll
-    for (int t = 0; t < TPW; t++) {
-        acc[t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-        mfma_chunk(acc[t], w[t], xh, xm, xl, kb0, kb0 + KBW);
-    }
-
-    // Partial sums through LDS (the operand buffer is free once every wave
-    // has its B operands): partial[t][w] for tile t, wave w.
+    // Quarter sums through LDS (the operand buffer is free once every wave
+    // has its B operands): partial[q][t].
     __syncthreads();
     f32x4 *partial = (f32x4 *)bsh;
-#pragma unroll
-    for (int t = 0; t < TPW; t++) partial[(t * 4 + wave) * 64 + lane] = acc[t];
+    partial[wave * 64 + lane] = acc;
     __syncthreads();
-    if (!active) return;  // no barrier follows
-    f32x4 v = partial[(wave * 4) * 64 + lane];
+    if (q != 0 || !active) return;  // no barrier follows
+    f32x4 v = acc;
 #pragma unroll
-    for (int w2 = 1; w2 < 4; w2++) {
-        const f32x4 p = partial[(wave * 4 + w2) * 64 + lane];
+    for (int q2 = 1; q2 < 4; q2++) {
+        const f32x4 p = partial[(q2 * 4 + t) * 64 + lane];
         v[0] = __fadd_rn(v[0], p[0]);
         v[1] = __fadd_rn(v[1], p[1]);
         v[2] = __fadd_rn(v[2], p[2]);
@@ -558,7 +537,7 @@ static int launch(const GemmArgs &a, hipStream_t stream) {
         return bad_arguments("pgpu_gemm");
     if constexpr (SRC != SRC_SPLIT) {
         const dim3 grid((a.n_rows / 16 + 3) / 4, (a.streams + 15) / 16);
-        hipLaunchKernelGGL((k_gemm_tiles<SRC, EPI, Q8>), grid, dim3(256), 0, stream, a);
+        hipLaunchKernelGGL((k_gemm_wide<SRC, EPI, Q8>), grid, dim3(1024), 0, stream, a);
     } else {
         const dim3 grid(a.n_rows / 16, (a.streams + 15) / 16);
         // Up to 4 column blocks per wave (K <= 512): one chunk of 4; else chunks of 8.
