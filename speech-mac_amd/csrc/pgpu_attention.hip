@@ -40,6 +40,15 @@ struct AttnArgs {
 
 
 
+// K/V bytes are read once per step: non-temporal loads, so the stream does
+// not displace what the other kernels of the step re-read from the caches
+// (projection weights, activations).
+__device__ inline float4 stream_load(const float *p) {
+    typedef float f4 __attribute__((ext_vector_type(4)));
+    const f4 v = __builtin_nontemporal_load((const f4 *)p);
+    return make_float4(v.x, v.y, v.z, v.w);
+}
+
 __global__ __launch_bounds__(256) void k_attention(AttnArgs a) {
     const int split = blockIdx.x, head = blockIdx.y, s = blockIdx.z;
     const int count = a.positions[s] + 1;
@@ -83,8 +92,8 @@ __global__ __launch_bounds__(256) void k_attention(AttnArgs a) {
             const float *tile = layer_kv + ((size_t)ids[t] * kHeads + head) * 2048 + lane * 4;
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                kr[t][i] = *(const float4 *)(tile + i * 256);
-                vr[t][i] = *(const float4 *)(tile + 1024 + i * 256);
+                kr[t][i] = stream_load(tile + i * 256);
+                vr[t][i] = stream_load(tile + 1024 + i * 256);
             }
         }
     } else {

@@ -24,9 +24,9 @@
 //   i.e. the reference phonon_q8_dot order "sum += scale * partial".
 //   BF16: the three MFMAs chain straight into the accumulator.
 // Work decomposition (results never depend on scheduling)
-//   SRC_SPLIT (k_gemm): one work-group = 16 output rows x 16 streams; its 4
-//   waves split the column blocks into 4 contiguous ranges, summed in LDS in
-//   wave order.
+//   SRC_SPLIT (k_gemm): one work-group = 16 output rows x 16 streams; its
+//   16 waves split the column blocks into 16 contiguous ranges, summed in
+//   LDS in wave order.
 //   SRC_LN / SRC_ATTN (k_gemm_wide, K = 512): one 1024-thread work-group =
 //   64 rows x 16 streams; the prologue runs once with one wave per stream,
 //   then 16 waves take (tile, quarter of the column blocks) pairs and the
@@ -404,16 +404,18 @@ __device__ inline bool epilogue(const GemmArgs &a, const EpiOperands &e, const f
 }
 
 // Projection of split-fragment rows from global memory (any K): one
-// work-group = 16 rows x 16 streams; its 4 waves split the column blocks into
-// 4 contiguous ranges and are summed in LDS in wave order.
+// 1024-thread work-group = 16 rows x 16 streams; its 16 waves split the
+// column blocks into 16 contiguous ranges (4 blocks each at K = 2048, all
+// requested at once), summed in LDS in wave order.
 template <int EPI, bool Q8, int CH>
-__global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
+__global__ __launch_bounds__(1024) void k_gemm(GemmArgs a) {
+    constexpr int NW = 16;
     const int tile = blockIdx.x, st = blockIdx.y;
     // Uniform per wave (readfirstlane): the block loop below is scalar control.
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     const int kbn = a.k_cols >> 5;
-    const int per_wave = (kbn + 3) >> 2;
+    const int per_wave = (kbn + NW - 1) / NW;
     const int kb_begin = wave * per_wave;
     const int kb_end = min(kbn, kb_begin + per_wave);
 
@@ -449,13 +451,13 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
         w = next;
     }
 
-    __shared__ f32x4 partial[4][64];
+    __shared__ f32x4 partial[NW][64];
     partial[wave][lane] = acc;
     __syncthreads();
     if (wave != 0) return;  // no barrier follows
     f32x4 v = partial[0][lane];
 #pragma unroll
-    for (int w = 1; w < 4; w++) {
+    for (int w = 1; w < NW; w++) {
         const f32x4 p = partial[w][lane];
         v[0] = __fadd_rn(v[0], p[0]);
         v[1] = __fadd_rn(v[1], p[1]);
@@ -540,11 +542,11 @@ static int launch(const GemmArgs &a, hipStream_t stream) {
         hipLaunchKernelGGL((k_gemm_wide<SRC, EPI, Q8>), grid, dim3(1024), 0, stream, a);
     } else {
         const dim3 grid(a.n_rows / 16, (a.streams + 15) / 16);
-        // Up to 4 column blocks per wave (K <= 512): one chunk of 4; else chunks of 8.
-        if (a.k_cols <= 512)
-            hipLaunchKernelGGL((k_gemm<EPI, Q8, 4>), grid, dim3(256), 0, stream, a);
+        // Up to 4 column blocks per wave (K <= 2048): one chunk of 4; else chunks of 8.
+        if (a.k_cols <= 2048)
+            hipLaunchKernelGGL((k_gemm<EPI, Q8, 4>), grid, dim3(1024), 0, stream, a);
         else
-            hipLaunchKernelGGL((k_gemm<EPI, Q8, 8>), grid, dim3(256), 0, stream, a);
+            hipLaunchKernelGGL((k_gemm<EPI, Q8, 8>), grid, dim3(1024), 0, stream, a);
     }
     return launch_ok("pgpu_gemm");
 }
