@@ -41,11 +41,17 @@ struct PhononFlowBatch {
     int *status;
     pgpu_attention_scratch scratch;
     size_t *host_positions;
-    void *graph;
-    size_t graph_streams;
-    float graph_theta;
-    const float *graph_input;
-    float *graph_output;
+    /* Captured steps, keyed by what the capture baked in. Two entries, so a
+     * caller that alternates two buffers (output feeding the next input)
+     * replays both without capturing again. */
+    struct {
+        void *exec;
+        size_t streams;
+        float theta;
+        const float *input;
+        float *output;
+    } graphs[2];
+    size_t graph_victim;
     int eager;                         /* launch kernels directly, no graph */
     size_t groups;                     /* stream groups run concurrently */
     void *side[PH_MAX_GROUPS - 1];     /* HIP streams of groups 1.. */
@@ -284,12 +290,19 @@ int phonon_kv_pool_read(const PhononKvPool *pool, const int32_t *table, size_t t
 
 /* ---------------------------------------------------------------- batch -- */
 
+static void drop_graphs(PhononFlowBatch *b) {
+    for (size_t i = 0; i < 2; i++) {
+        pgpu_graph_destroy(b->graphs[i].exec);
+        b->graphs[i].exec = NULL;
+    }
+}
+
 void phonon_flow_batch_destroy(PhononFlowBatch *b) {
     if (!b)
         return;
     if (b->stream)
         (void)pgpu_stream_sync(b->stream);
-    pgpu_graph_destroy(b->graph);
+    drop_graphs(b);
     for (size_t g = 0; g + 1 < PH_MAX_GROUPS; g++) {
         if (b->side[g])
             (void)pgpu_stream_sync(b->side[g]);
@@ -397,8 +410,7 @@ int ph_batch_bind_model(PhononFlowBatch *b, const PhononFlowModel *model) {
     if (!b || !model || model->layers > (size_t)b->pool->kv.layers)
         return 0;
     if (b->model != model) {
-        pgpu_graph_destroy(b->graph);
-        b->graph = NULL;
+        drop_graphs(b);
         b->model = model;
     }
     return 1;
@@ -511,8 +523,7 @@ int phonon_flow_batch_set_groups(PhononFlowBatch *b, size_t groups) {
     if (!b || !groups || groups > PH_MAX_GROUPS)
         return 0;
     if (b->groups != groups) {
-        pgpu_graph_destroy(b->graph);
-        b->graph = NULL;
+        drop_graphs(b);
         b->groups = groups;
     }
     return 1;
@@ -522,8 +533,7 @@ int phonon_flow_batch_set_graph(PhononFlowBatch *b, int use_graph) {
     if (!b)
         return 0;
     b->eager = !use_graph;
-    pgpu_graph_destroy(b->graph);
-    b->graph = NULL;
+    drop_graphs(b);
     return 1;
 }
 
@@ -541,26 +551,32 @@ int phonon_flow_batch_step_device(PhononFlowBatch *b, const float *inputs, float
             b->host_positions[s]++;
         return 1;
     }
-    if (!b->graph || b->graph_streams != b->streams || b->graph_theta != theta ||
-        b->graph_input != inputs || b->graph_output != outputs) {
-        pgpu_graph_destroy(b->graph);
-        b->graph = NULL;
+    void *exec = NULL;
+    for (size_t i = 0; i < 2 && !exec; i++)
+        if (b->graphs[i].exec && b->graphs[i].streams == b->streams &&
+            b->graphs[i].theta == theta && b->graphs[i].input == inputs &&
+            b->graphs[i].output == outputs)
+            exec = b->graphs[i].exec;
+    if (!exec) {
+        const size_t slot = b->graph_victim;
+        pgpu_graph_destroy(b->graphs[slot].exec);
+        b->graphs[slot].exec = NULL;
         if (!ph_rope_table(theta) || !pgpu_graph_begin(b->stream))
             return 0;
         const int enqueued = enqueue_step(b, inputs, outputs, theta);
-        void *exec = NULL;
         const int ended = pgpu_graph_end(b->stream, &exec);
         if (!enqueued || !ended) {
             pgpu_graph_destroy(exec);
             return 0;
         }
-        b->graph = exec;
-        b->graph_streams = b->streams;
-        b->graph_theta = theta;
-        b->graph_input = inputs;
-        b->graph_output = outputs;
+        b->graphs[slot].exec = exec;
+        b->graphs[slot].streams = b->streams;
+        b->graphs[slot].theta = theta;
+        b->graphs[slot].input = inputs;
+        b->graphs[slot].output = outputs;
+        b->graph_victim = 1 - slot;
     }
-    if (!pgpu_graph_launch(b->graph, b->stream))
+    if (!pgpu_graph_launch(exec, b->stream))
         return 0;
     for (size_t s = 0; s < b->streams; s++)
         b->host_positions[s]++;
