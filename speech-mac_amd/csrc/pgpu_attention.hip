@@ -7,7 +7,7 @@
 //
 // Pool layout, per layer: [block][head][K|V][16 positions][64] fp32, so one
 // (block, head) tile of keys is 4 KB contiguous and its values follow it.
-// Work-group (split j, head h, stream s) covers keys [256j, 256j+256) of
+// Work-group (head h, split j, stream s) covers keys [256j, 256j+256) of
 // stream s: wave w takes blocks 16j+4w .. 16j+4w+3. Each lane loads float4s
 // at tile offsets 256*i + 4*lane (i = 0..3), i.e. key 4i + lane/16, dims
 // 4*(lane%16) .. +3: every load instruction reads 1 KB contiguous, and all
@@ -50,7 +50,9 @@ __device__ inline float4 stream_load(const float *p) {
 }
 
 __global__ __launch_bounds__(256) void k_attention(AttnArgs a) {
-    const int split = blockIdx.x, head = blockIdx.y, s = blockIdx.z;
+    // Heads vary fastest across the grid: work-groups dispatched together
+    // read all 8 heads' tiles of the same blocks (64 KB contiguous each).
+    const int head = blockIdx.x, split = blockIdx.y, s = blockIdx.z;
     const int count = a.positions[s] + 1;
     const int nsplit = (count + kSplitKeys - 1) / kSplitKeys;
     // A context the grid or the block table cannot cover is an error, never
@@ -246,7 +248,7 @@ extern "C" int pgpu_attention(void *stream, const float *q, const pgpu_paged_kv 
     a.part_acc = scratch->part_acc;
     a.part_ml = scratch->part_ml;
     a.status = status;
-    hipLaunchKernelGGL(k_attention, dim3(max_splits, heads, streams), dim3(256), 0,
+    hipLaunchKernelGGL(k_attention, dim3(heads, max_splits, streams), dim3(256), 0,
                        (hipStream_t)stream, a);
     return launch_ok("pgpu_attention");
 }

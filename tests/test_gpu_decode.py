@@ -517,6 +517,57 @@ def test_batch_graph_replay_equals_legacy_path(lib, syn, pkg):
     bt.close()
 
 
+def test_graph_ping_pong_equals_eager(lib, syn, pkg):
+    """Closed-loop decode on device buffers that swap roles every step (each
+    output is the next input): the two captured graphs replayed in turn give
+    the same bits as launching the kernels directly, and a third buffer pair
+    (a fresh capture replacing one of the two) does too."""
+    layers = 2
+    model = scaled_model(syn, 161, layers)
+    views = pkg.Views()
+    w = views.layers(model)
+    streams, max_pos, steps = 5, 96, 7
+    table_len = (max_pos + 15) // 16
+    blocks = streams * table_len
+    rng = np.random.default_rng(162)
+    lengths = rng.integers(0, 60, size=streams)
+    x0 = rng.standard_normal((streams, 512)).astype(np.float32)
+    runs = []
+    for eager in (False, True):
+        bt = Batch(lib, w, layers, streams, max_pos, blocks)
+        assert lib.phonon_flow_batch_set_graph(bt.batch, 0 if eager else 1)
+        ids = np.zeros(blocks, np.int32)
+        assert lib.phonon_kv_pool_alloc(bt.pool, blocks, i32p(ids))
+        tables = np.ascontiguousarray(ids.reshape(streams, table_len).astype(np.int32))
+        pos = lengths.astype(np.uintp)
+        assert lib.phonon_flow_batch_set_streams(
+            bt.batch, streams, pos.ctypes.data_as(ctypes.POINTER(ctypes.c_size_t)),
+            i32p(tables), table_len)
+        bufs = [pkg.DeviceBuffer(lib, x0.nbytes) for _ in range(3)]
+        bufs[0].upload(x0)
+        stream = lib.phonon_flow_batch_stream(bt.batch)
+        outs = []
+        src, dst = 0, 1
+        for step in range(steps):
+            if step == 4:
+                dst = 2  # a third pair: one cached graph is replaced
+            assert lib.phonon_flow_batch_step_device(bt.batch, bufs[src].ptr, 10000.0,
+                                                     bufs[dst].ptr), pkg.last_error(lib)
+            assert lib.pgpu_stream_sync(stream)
+            y = np.zeros_like(x0)
+            assert lib.pgpu_copy_d2h(stream, y.ctypes.data, bufs[dst].ptr, y.nbytes)
+            assert lib.pgpu_stream_sync(stream)
+            outs.append(y.view(np.uint32).copy())
+            src, dst = dst, src
+        assert lib.phonon_flow_batch_sync(bt.batch)
+        runs.append(outs)
+        for b in bufs:
+            b.free()
+        bt.close()
+    for a, b in zip(runs[0], runs[1]):
+        assert np.array_equal(a, b)
+
+
 def test_unwritten_pool_slots_never_reach_the_output(lib, oracle, oracle_mod, syn, pkg):
     """Regression: slots past a stream's context inside its last block may
     hold anything (here NaN); attention must skip them, not weight them 0."""
