@@ -84,6 +84,20 @@ int phonon_flow_batch_step(PhononFlowBatch *batch, const float *inputs, float th
  * HIP graph on first use and replayed afterwards. */
 int phonon_flow_batch_step_device(PhononFlowBatch *batch, const float *inputs, float theta,
                                   float *outputs);
+/* Batched prefill (the batched form of phonon_flow_stack_prefill,
+ * src/phonon_transformer.c:622-702, for many streams and chunks): positions
+ * [first[i], first[i] + counts[i]) of stream i, whose block table is row i of
+ * `tables` (host [streams][table_len]), all run through the model's layers in
+ * one pass. inputs/outputs (dev) hold one [512] row per position, stream by
+ * stream in position order; each output row is what a decode step at that
+ * position returns. Positions below first[i] must already be in the pool.
+ * Uses the batch's stream slots (sum of counts <= max_streams): call
+ * phonon_flow_batch_set_streams before the next phonon_flow_batch_step*.
+ * Enqueued without waiting; phonon_flow_batch_sync reports non-finite values. */
+int phonon_flow_batch_prefill_device(PhononFlowBatch *batch, size_t streams, const size_t *first,
+                                     const size_t *counts, const int32_t *tables,
+                                     size_t table_len, const float *inputs, float theta,
+                                     float *outputs);
 /* Runs the streams as `groups` (1..4) independent groups of whole 16-stream
  * tiles, each on its own HIP stream inside the step's graph. Results do not
  * depend on it. Default 1: on MI355X under ROCm 7 kernels of different HIP

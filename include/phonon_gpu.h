@@ -143,6 +143,10 @@ int pgpu_kv_copy(void *stream, const pgpu_paged_kv *kv, const int32_t *table,
                  float *values, size_t capacity, int to_contiguous, int *status);
 int pgpu_fill_normal(void *stream, float *dst, size_t count, uint64_t seed);
 int pgpu_advance_positions(void *stream, int32_t *positions, int streams);
+/* dst[r][0..width) = src[map[r]][0..width) for r < rows (int32 rows; map
+ * entries must index rows of src). */
+int pgpu_gather_rows(void *stream, int32_t *dst, const int32_t *src, const int32_t *map,
+                     int rows, int width);
 
 #ifdef __cplusplus
 }

@@ -145,6 +145,7 @@ EXPORTS = {
     "phonon_flow_batch_set_streams": (_i, [_vp, _sz, _szp, _i32p, _sz]),
     "phonon_flow_batch_step": (_i, [_vp, _fp, _f, _fp]),
     "phonon_flow_batch_step_device": (_i, [_vp, _vp, _f, _vp]),
+    "phonon_flow_batch_prefill_device": (_i, [_vp, _sz, _vp, _vp, _vp, _sz, _vp, _f, _vp]),
     "phonon_flow_batch_sync": (_i, [_vp]),
     "phonon_flow_batch_set_groups": (_i, [_vp, _sz]),
     "phonon_flow_batch_set_graph": (_i, [_vp, _i]),
@@ -192,6 +193,7 @@ EXPORTS = {
     "pgpu_kv_copy": (_i, [_vp, _kvp, _vp, _i, _i, _i, _i, _vp, _vp, _sz, _i, _vp]),
     "pgpu_fill_normal": (_i, [_vp, _vp, _sz, ctypes.c_uint64]),
     "pgpu_advance_positions": (_i, [_vp, _vp, _i]),
+    "pgpu_gather_rows": (_i, [_vp, _vp, _vp, _vp, _i, _i]),
 }
 
 _LIB = None

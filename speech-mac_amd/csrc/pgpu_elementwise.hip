@@ -217,6 +217,14 @@ __global__ void k_advance(int32_t *positions, int streams) {
     if (s < streams) positions[s] += 1;
 }
 
+// dst row r = src row map[r] (int32 rows of `width`): per-token copies of a
+// stream's block table for a batched prefill. Grid (ceil(width/256), rows).
+__global__ void k_gather_rows(int32_t *__restrict__ dst, const int32_t *__restrict__ src,
+                              const int32_t *__restrict__ map, int width) {
+    const int i = blockIdx.x * 256 + threadIdx.x, r = blockIdx.y;
+    if (i < width) dst[(size_t)r * width + i] = src[(size_t)map[r] * width + i];
+}
+
 }  // namespace pgpu
 
 using namespace pgpu;
@@ -293,5 +301,13 @@ extern "C" int pgpu_advance_positions(void *stream, int32_t *positions, int stre
     if (streams <= 0) return bad_arguments(__func__);
     hipLaunchKernelGGL(k_advance, dim3((streams + 255) / 256), dim3(256), 0,
                        (hipStream_t)stream, positions, streams);
+    return launch_ok(__func__);
+}
+
+extern "C" int pgpu_gather_rows(void *stream, int32_t *dst, const int32_t *src,
+                                const int32_t *map, int rows, int width) {
+    if (!dst || !src || !map || rows <= 0 || width <= 0) return bad_arguments(__func__);
+    hipLaunchKernelGGL(k_gather_rows, dim3((width + 255) / 256, rows), dim3(256), 0,
+                       (hipStream_t)stream, dst, src, map, width);
     return launch_ok(__func__);
 }

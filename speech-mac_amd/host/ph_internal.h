@@ -58,6 +58,8 @@ int ph_batch_enqueue_layers(PhononFlowBatch *batch, size_t first, size_t count,
                             size_t pool_offset, const float *input, float *output,
                             float theta);
 int ph_batch_set_single(PhononFlowBatch *batch, size_t position, const int32_t *table_dev);
+int ph_batch_set_prefill(PhononFlowBatch *batch, size_t streams, const size_t *first,
+                         const size_t *counts, const int32_t *tables_dev);
 int ph_batch_bind_model(PhononFlowBatch *batch, const PhononFlowModel *model);
 float *ph_batch_in(PhononFlowBatch *batch);
 float *ph_batch_out(PhononFlowBatch *batch);

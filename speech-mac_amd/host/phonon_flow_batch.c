@@ -38,6 +38,7 @@ struct PhononFlowBatch {
     float *x, *r, *q, *in, *out, *rows;
     uint16_t *xh; /* split fragments of the MLP hidden rows */
     int32_t *positions, *tables;
+    int32_t *table_src, *table_map; /* prefill staging, allocated on first use */
     int *status;
     pgpu_attention_scratch scratch;
     size_t *host_positions;
@@ -312,7 +313,7 @@ void phonon_flow_batch_destroy(PhononFlowBatch *b) {
     pgpu_event_destroy(b->fork);
     void *bufs[] = {b->x,    b->r,  b->q,         b->in,     b->out,
                     b->rows, b->xh, b->positions, b->tables, b->status,
-                    b->scratch.part_acc, b->scratch.part_ml};
+                    b->scratch.part_acc, b->scratch.part_ml, b->table_src, b->table_map};
     for (size_t i = 0; i < sizeof(bufs) / sizeof(bufs[0]); i++)
         pgpu_free(bufs[i]);
     pgpu_stream_destroy(b->stream);
@@ -517,6 +518,61 @@ static int enqueue_step(PhononFlowBatch *b, const float *input, float *output, f
             !pgpu_stream_wait_event(b->stream, b->join[g - 1]))
             return 0;
     return pgpu_advance_positions(b->stream, b->positions, (int)b->streams);
+}
+
+/* Pseudo-streams of a batched prefill: position first[i] + k (k < counts[i])
+ * of stream i becomes its own stream with block-table row i of tables_dev
+ * (device, [streams][table_len]). A step then runs every such position
+ * through all layers at once: each layer's projection appends the K/V of all
+ * of them before its attention runs, and position p attends p + 1 keys, so
+ * the pass is causal and computes what `counts` consecutive steps would. */
+int ph_batch_set_prefill(PhononFlowBatch *b, size_t streams, const size_t *first,
+                         const size_t *counts, const int32_t *tables_dev) {
+    size_t total = 0;
+    for (size_t i = 0; i < streams; i++) {
+        if (!counts[i] || first[i] >= b->max_positions ||
+            counts[i] > b->max_positions - first[i] || counts[i] > b->max_streams - total)
+            return 0;
+        total += counts[i];
+    }
+    if (!total)
+        return 0;
+    if (!b->table_map && !(b->table_map = pgpu_malloc(b->max_streams * sizeof(int32_t))))
+        return 0;
+    int32_t *pos32 = malloc(total * sizeof(int32_t)), *map = malloc(total * sizeof(int32_t));
+    int ok = pos32 && map;
+    for (size_t i = 0, p = 0; ok && i < streams; i++)
+        for (size_t k = 0; k < counts[i]; k++, p++) {
+            pos32[p] = (int32_t)(first[i] + k);
+            map[p] = (int32_t)i;
+            b->host_positions[p] = first[i] + k;
+        }
+    ok = ok && pgpu_stream_sync(b->stream) &&
+         pgpu_copy_h2d(b->stream, b->positions, pos32, total * sizeof(int32_t)) &&
+         pgpu_copy_h2d(b->stream, b->table_map, map, total * sizeof(int32_t)) &&
+         pgpu_gather_rows(b->stream, b->tables, tables_dev, b->table_map, (int)total,
+                          (int)b->table_len);
+    free(pos32);
+    free(map);
+    if (ok)
+        b->streams = total;
+    return ok;
+}
+
+int phonon_flow_batch_prefill_device(PhononFlowBatch *b, size_t streams, const size_t *first,
+                                     const size_t *counts, const int32_t *tables,
+                                     size_t table_len, const float *inputs, float theta,
+                                     float *outputs) {
+    if (!b || !streams || streams > b->max_streams || !first || !counts || !tables ||
+        table_len != b->table_len || !inputs || !outputs || !isfinite(theta) || theta <= 0.0f)
+        return 0;
+    if (!b->table_src &&
+        !(b->table_src = pgpu_malloc(b->max_streams * b->table_len * sizeof(int32_t))))
+        return 0;
+    return pgpu_stream_sync(b->stream) &&
+           pgpu_copy_h2d(b->stream, b->table_src, tables, streams * table_len * sizeof(int32_t)) &&
+           ph_batch_set_prefill(b, streams, first, counts, b->table_src) &&
+           enqueue_step(b, inputs, outputs, theta);
 }
 
 int phonon_flow_batch_set_groups(PhononFlowBatch *b, size_t groups) {

@@ -18,10 +18,14 @@ typedef struct Mirror {
     const float *keys;
     size_t capacity, positions, table_len;
     PhononKvPool *pool;
-    int32_t *table_dev;
-    PhononFlowBatch *batch;
+    int32_t *table_host, *table_dev;
+    PhononFlowBatch *batch;   /* one stream: decode steps */
+    PhononFlowBatch *prefill; /* up to PH_PREFILL_CHUNK positions at once */
     struct Mirror *next;
 } Mirror;
+
+/* Positions a prefill runs through the layers together. */
+enum { PH_PREFILL_CHUNK = 512 };
 
 static Mirror *g_mirrors; /* guarded by ph_lock */
 
@@ -29,7 +33,9 @@ static void mirror_free(Mirror *m) {
     if (!m)
         return;
     phonon_flow_batch_destroy(m->batch);
+    phonon_flow_batch_destroy(m->prefill);
     phonon_kv_pool_destroy(m->pool);
+    free(m->table_host);
     if (m->table_dev) {
         (void)pgpu_stream_sync(ph_stream());
         pgpu_free(m->table_dev);
@@ -81,7 +87,7 @@ static Mirror *mirror_create(const PhononKvCache *cache) {
     if (ok && rows && cache->keys && cache->values)
         ok = phonon_kv_pool_write(m->pool, table, m->table_len, 0, rows, cache->keys,
                                   cache->values, cache->capacity);
-    free(table);
+    m->table_host = table;
     if (!ok) {
         mirror_free(m);
         return NULL;
@@ -416,6 +422,55 @@ static int run_position(const PhononFlowModel *model, Mirror *m, PhononKvCache *
            ph_fail("decode step: non-finite output");
 }
 
+/* Prefill of positions [0, length) for the stream of `m`: chunks of up to
+ * PH_PREFILL_CHUNK positions, each run through all layers in one batched
+ * pass (phonon_flow_batch_prefill_device semantics), polling `cancel` before
+ * every layer and after the last; then the appended K/V rows are copied back
+ * into the cache's host arrays and `output` receives the last position's
+ * output (src/phonon_transformer.c:692). */
+static int run_prefill(const PhononFlowModel *model, Mirror *m, PhononKvCache *cache,
+                       const float *input, size_t length, float theta, float *output,
+                       PhononCancelPoll cancel, void *context, int *cancelled) {
+    *cancelled = 0;
+    const size_t layers = phonon_flow_model_layers(model);
+    const size_t chunk = m->positions < PH_PREFILL_CHUNK ? m->positions : PH_PREFILL_CHUNK;
+    if (!m->prefill && !phonon_flow_batch_create(model, m->pool, chunk, m->positions, &m->prefill))
+        return ph_fail("prefill: batch creation failed");
+    PhononFlowBatch *b = m->prefill;
+    void *s = ph_batch_stream(b);
+    float *in = ph_batch_in(b), *out = ph_batch_out(b);
+    if (!ph_batch_bind_model(b, model))
+        return ph_fail("prefill: binding the model failed");
+    size_t last = 0;
+    for (size_t start = 0; start < length; start += chunk) {
+        const size_t n = length - start < chunk ? length - start : chunk;
+        if (!ph_batch_set_prefill(b, 1, &start, &n, m->table_dev) ||
+            !pgpu_copy_h2d(s, in, input + start * PH_WIDTH, n * PH_WIDTH * sizeof(float)))
+            return ph_fail("prefill: setting up the positions failed");
+        for (size_t l = 0; l < layers; l++) {
+            if (cancel && cancel(context)) {
+                *cancelled = 1;
+                (void)ph_batch_status(b);
+                return 0;
+            }
+            if (!ph_batch_enqueue_layers(b, l, 1, 0, l ? out : in, out, theta))
+                return ph_fail("prefill: enqueueing a layer failed");
+        }
+        if (!ph_batch_status(b))
+            return ph_fail("prefill: non-finite value or uncovered position on the device");
+        last = n - 1;
+    }
+    if (cancel && cancel(context)) {
+        *cancelled = 1;
+        return 0;
+    }
+    if (!pgpu_copy_d2h(s, output, out + last * PH_WIDTH, PH_WIDTH * sizeof(float)) ||
+        !phonon_kv_pool_read(m->pool, m->table_host, m->table_len, 0, length, cache->keys,
+                             cache->values, cache->capacity))
+        return ph_fail("prefill: reading results failed");
+    return ph_all_finite(output, PHONON_FLOW_WIDTH) || ph_fail("prefill: non-finite output");
+}
+
 /* Model for `layers` layers of `weights`: the registered device copy, or a
  * fresh upload owned by the caller (*owned). */
 static const PhononFlowModel *model_for(const PhononFlowLayerWeights *weights, size_t layers,
@@ -513,13 +568,12 @@ int phonon_flow_stack_prefill_cancel(const PhononFlowLayerWeights weights[PHONON
     PhononFlowModel *owned = NULL;
     const PhononFlowModel *model = model_for(weights, PHONON_FLOW_LAYERS, &owned);
     Mirror *m = model ? mirror_get(cache) : NULL;
-    int ok = m != NULL, cancelled = 0;
+    int cancelled = 0;
     float result[PHONON_FLOW_WIDTH];
-    for (size_t row = 0; ok && row < length; row++)
-        ok = run_position(model, m, cache, 0, row, input + row * PHONON_FLOW_WIDTH, theta, result,
-                          cancel, context, &cancelled);
-    if (m && m->batch && owned)
-        (void)ph_batch_status(m->batch);
+    const int ok = m && run_prefill(model, m, cache, input, length, theta, result, cancel,
+                                    context, &cancelled);
+    if (m && m->prefill && owned)
+        (void)ph_batch_status(m->prefill);
     phonon_flow_model_destroy(owned);
     ph_unlock();
     if (!ok || cancelled) {

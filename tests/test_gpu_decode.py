@@ -568,6 +568,84 @@ def test_graph_ping_pong_equals_eager(lib, syn, pkg):
         assert np.array_equal(a, b)
 
 
+def test_batched_prefill_equals_single_steps(lib, syn, pkg):
+    """phonon_flow_batch_prefill_device over several streams and chunks
+    (a fresh stream, a continuation after an existing context, a one-position
+    chunk) gives, bit for bit, the outputs and appended K/V of decoding the
+    same positions one step at a time."""
+    layers = 2
+    model = scaled_model(syn, 171, layers)
+    views = pkg.Views()
+    w = views.layers(model)
+    max_pos = 80
+    table_len = (max_pos + 15) // 16
+    first = [0, 10, 0]
+    counts = [30, 15, 1]
+    nstreams = len(first)
+    rng = np.random.default_rng(172)
+    ctx_k = rng.standard_normal((layers, max_pos, 512)).astype(np.float32)
+    ctx_v = rng.standard_normal((layers, max_pos, 512)).astype(np.float32)
+    xs = [rng.standard_normal((c, 512)).astype(np.float32) for c in counts]
+
+    def setup(max_streams):
+        bt = Batch(lib, w, layers, max_streams, max_pos, nstreams * table_len)
+        ids = np.zeros(nstreams * table_len, np.int32)
+        assert lib.phonon_kv_pool_alloc(bt.pool, ids.size, i32p(ids))
+        tables = np.ascontiguousarray(ids.reshape(nstreams, table_len))
+        # stream 1 starts with a 10-position context
+        assert lib.phonon_kv_pool_write(bt.pool, i32p(tables[1]), table_len, 0, first[1],
+                                        fp(ctx_k), fp(ctx_v), max_pos)
+        return bt, tables
+
+    # batched prefill
+    total = sum(counts)
+    bt, tables = setup(total)
+    din = pkg.DeviceBuffer(lib, total * 512 * 4)
+    dout = pkg.DeviceBuffer(lib, total * 512 * 4)
+    din.upload(np.concatenate(xs))
+    f = np.array(first, np.uintp)
+    c = np.array(counts, np.uintp)
+    szp = ctypes.POINTER(ctypes.c_size_t)
+    assert lib.phonon_flow_batch_prefill_device(bt.batch, nstreams, f.ctypes.data_as(szp),
+                                                c.ctypes.data_as(szp), i32p(tables), table_len,
+                                                din.ptr, 10000.0, dout.ptr), pkg.last_error(lib)
+    assert lib.phonon_flow_batch_sync(bt.batch)
+    got = dout.download((total, 512))
+    kv_got = []
+    for i in range(nstreams):
+        k = np.zeros((layers, max_pos, 512), np.float32)
+        v = np.zeros_like(k)
+        end = first[i] + counts[i]
+        assert lib.phonon_kv_pool_read(bt.pool, i32p(tables[i]), table_len, 0, end, fp(k), fp(v),
+                                       max_pos)
+        kv_got.append((k[:, :end].copy(), v[:, :end].copy()))
+    din.free()
+    dout.free()
+    bt.close()
+
+    # the same positions one decode step at a time, one stream at a time
+    bt, tables = setup(1)
+    want = []
+    for i in range(nstreams):
+        pos = np.array([first[i]], np.uintp)
+        assert lib.phonon_flow_batch_set_streams(bt.batch, 1, pos.ctypes.data_as(szp),
+                                                 i32p(tables[i]), table_len)
+        for t in range(counts[i]):
+            y = np.zeros((1, 512), np.float32)
+            assert lib.phonon_flow_batch_step(bt.batch, fp(np.ascontiguousarray(xs[i][t:t + 1])),
+                                              10000.0, fp(y)), pkg.last_error(lib)
+            want.append(y[0])
+        end = first[i] + counts[i]
+        k = np.zeros((layers, max_pos, 512), np.float32)
+        v = np.zeros_like(k)
+        assert lib.phonon_kv_pool_read(bt.pool, i32p(tables[i]), table_len, 0, end, fp(k), fp(v),
+                                       max_pos)
+        assert np.array_equal(k[:, :end].view(np.uint32), kv_got[i][0].view(np.uint32)), i
+        assert np.array_equal(v[:, :end].view(np.uint32), kv_got[i][1].view(np.uint32)), i
+    bt.close()
+    assert np.array_equal(np.stack(want).view(np.uint32), got.view(np.uint32))
+
+
 def test_unwritten_pool_slots_never_reach_the_output(lib, oracle, oracle_mod, syn, pkg):
     """Regression: slots past a stream's context inside its last block may
     hold anything (here NaN); attention must skip them, not weight them 0."""
