@@ -274,6 +274,93 @@ def pmc_program(pkg, lib, args):
           flush=True)
 
 
+def large_batch_with_prefill(pkg, lib, seed, layers=12, streams=256, new_streams=16, chunk=256,
+                             iterations=4, warmup=1):
+    """Large-batch decode with interleaved prefill: every iteration advances
+    `streams` streams (contexts U{256..8192-headroom}, paged KV block 16,
+    shuffled tables) by one decode step and prefills a `chunk`-position prompt
+    for each of `new_streams` newly admitted streams (batched causal prefill:
+    all their positions through all layers in one pass)."""
+    import speech_mac_amd.synthetic as syn
+    rng = np.random.default_rng(seed + 50)
+    steps = iterations + warmup
+    max_positions = 8192
+    lengths = rng.integers(256, max_positions - steps, size=streams) - 1  # positions
+    table_len = max_positions // 16
+    decode_blocks = int(np.sum((lengths + steps + 16) // 16))
+    prefill_blocks = new_streams * (chunk // 16)
+    views = pkg.Views()
+    weights = views.layers(syn.flow_model(seed, layers))
+    model, pool, dec, pre = (ctypes.c_void_p() for _ in range(4))
+    assert lib.phonon_flow_model_create(weights, layers, ctypes.byref(model))
+    assert lib.phonon_kv_pool_create(layers, decode_blocks + prefill_blocks, ctypes.byref(pool))
+    assert lib.phonon_kv_pool_fill_normal(pool, seed + 51)
+    ids = np.zeros(decode_blocks + prefill_blocks, np.int32)
+    assert lib.phonon_kv_pool_alloc(pool, ids.size, ids.ctypes.data_as(P_I32))
+    ids = np.random.default_rng(seed + 52).permutation(ids).astype(np.int32)
+    tables = np.zeros((streams, table_len), np.int32)
+    at = 0
+    for s_i in range(streams):
+        need = int((lengths[s_i] + steps + 16) // 16)
+        tables[s_i, :need] = ids[at:at + need]
+        at += need
+    pre_tables = np.zeros((new_streams, table_len), np.int32)
+    pre_tables[:, :chunk // 16] = ids[at:at + prefill_blocks].reshape(new_streams, chunk // 16)
+    assert lib.phonon_flow_batch_create(model, pool, streams, max_positions, ctypes.byref(dec))
+    assert lib.phonon_flow_batch_create(model, pool, new_streams * chunk, max_positions,
+                                        ctypes.byref(pre))
+    pos = lengths.astype(np.uintp)
+    assert lib.phonon_flow_batch_set_streams(dec, streams, pos.ctypes.data_as(P_SZ),
+                                             tables.ctypes.data_as(P_I32), table_len)
+    stream = lib.phonon_flow_batch_stream(dec)
+    pstream = lib.phonon_flow_batch_stream(pre)
+    din, dout = lib.phonon_flow_batch_device_inputs(dec), lib.phonon_flow_batch_device_outputs(dec)
+    pin, pout = lib.phonon_flow_batch_device_inputs(pre), lib.phonon_flow_batch_device_outputs(pre)
+    x = np.random.default_rng(seed + 53).standard_normal((streams, 512)).astype(np.float32)
+    assert lib.pgpu_copy_h2d(stream, din, x.ctypes.data, x.nbytes)
+    px = np.random.default_rng(seed + 54).standard_normal((new_streams * chunk, 512))
+    px = px.astype(np.float32)
+    assert lib.pgpu_copy_h2d(pstream, pin, px.ctypes.data, px.nbytes)
+    first = np.zeros(new_streams, np.uintp)
+    counts = np.full(new_streams, chunk, np.uintp)
+    dec_t, pre_t = Timer(lib, stream), Timer(lib, pstream)
+    dec_ms = pre_ms = 0.0
+    for it in range(steps):
+        dec_t.start()
+        assert lib.phonon_flow_batch_step_device(dec, din, 10000.0, dout)
+        d_ms = dec_t.stop_ms()
+        din, dout = dout, din
+        pre_t.start()
+        assert lib.phonon_flow_batch_prefill_device(
+            pre, new_streams, first.ctypes.data_as(P_SZ), counts.ctypes.data_as(P_SZ),
+            pre_tables.ctypes.data_as(P_I32), table_len, pin, 10000.0, pout)
+        p_ms = pre_t.stop_ms()
+        if it >= warmup:
+            dec_ms += d_ms
+            pre_ms += p_ms
+    clean = bool(lib.phonon_flow_batch_sync(dec)) and bool(lib.phonon_flow_batch_sync(pre))
+    lib.phonon_flow_batch_destroy(pre)
+    lib.phonon_flow_batch_destroy(dec)
+    lib.phonon_kv_pool_destroy(pool)
+    lib.phonon_flow_model_destroy(model)
+    keys = sum(int(np.sum(lengths + warmup + i + 1)) for i in range(iterations)) / iterations
+    dec_bytes = layers * Q8_LAYER_BYTES + layers * KV_BYTES_PER_KEY * (keys + streams)
+    per_it_ms = (dec_ms + pre_ms) / iterations
+    return {"workload": f"B={streams} decode, contexts U{{256..{max_positions - steps}}}, "
+                        f"{layers} layers; plus {new_streams} x {chunk}-position prefills per "
+                        f"iteration (batched causal prefill)",
+            "iteration_ms": round(per_it_ms, 3),
+            "decode_ms": round(dec_ms / iterations, 3),
+            "decode_frames_per_s": round(streams / (dec_ms / iterations * 1e-3), 1),
+            "decode_GBps": round(dec_bytes / (dec_ms / iterations * 1e-3) / 1e9, 1),
+            "decode_frac_of_hbm": round(dec_bytes / (dec_ms / iterations * 1e-3) / 1e9
+                                        / HBM_PEAK_GBS, 4),
+            "prefill_ms": round(pre_ms / iterations, 3),
+            "prefill_tokens_per_s": round(new_streams * chunk / (pre_ms / iterations * 1e-3), 1),
+            "frames_per_s_incl_prefill": round(streams / (per_it_ms * 1e-3), 1),
+            "clean": clean}
+
+
 def q8_matvec_bench(pkg, lib, seed=1, calls=2000):
     """Config: single Q8 matvec 2048x512; 300 rotating weight copies (>256 MB)."""
     import speech_mac_amd.synthetic as syn
@@ -385,6 +472,8 @@ def main():
                     help="launch the step's kernels directly instead of a graph replay")
     ap.add_argument("--skip-extras", action="store_true",
                     help="only the headline B=64 line (no B=1, matvec, curve, CPU)")
+    ap.add_argument("--large-batch", action="store_true",
+                    help="run only the B=256 decode + batched prefill workload")
     ap.add_argument("--pmc-program", action="store_true",
                     help="run only the attention kernel and a calibration copy, for "
                          "rocprofv3 --pmc passes")
@@ -402,6 +491,9 @@ def main():
     log(f"device: {name.value.decode()}")
     if args.pmc_program:
         pmc_program(pkg, lib, args)
+        return
+    if args.large_batch:
+        print(json.dumps(large_batch_with_prefill(pkg, lib, args.seed)), flush=True)
         return
 
     lengths = np.random.default_rng(args.seed).integers(1, 2049, size=args.batch) - 1
@@ -443,6 +535,8 @@ def main():
                                   "decode frames, hipGraph replay per step",
                       "clean": r1["clean"]}
         log(f"B=1: {line['b1']['us_per_step']} us/step")
+        line["b256_with_prefill"] = large_batch_with_prefill(pkg, lib, args.seed)
+        log(f"B=256 + prefill: {line['b256_with_prefill']}")
         line["q8_matvec_2048x512"] = q8_matvec_bench(pkg, lib)
         log(f"q8 matvec: {line['q8_matvec_2048x512']}")
         line["attention_layer_curve"] = attention_curve(pkg, lib)

@@ -34,6 +34,7 @@ struct PhononFlowBatch {
     const PhononFlowModel *model;
     PhononKvPool *pool;
     size_t max_streams, padded_streams, max_positions, table_len, max_splits, streams;
+    size_t splits; /* attention splits of the work being enqueued (<= max_splits) */
     void *stream;
     float *x, *r, *q, *in, *out, *rows;
     uint16_t *xh; /* split fragments of the MLP hidden rows */
@@ -47,7 +48,7 @@ struct PhononFlowBatch {
      * replays both without capturing again. */
     struct {
         void *exec;
-        size_t streams;
+        size_t streams, splits;
         float theta;
         const float *input;
         float *output;
@@ -427,6 +428,19 @@ int ph_batch_set_single(PhononFlowBatch *b, size_t position, const int32_t *tabl
     return 1;
 }
 
+/* Attention splits covering every active stream's context after `ahead`
+ * more steps (capped by the batch's maximum): the attention grid and the
+ * partial layout are sized by the live contexts, not by max_positions. */
+static size_t splits_for(const PhononFlowBatch *b, size_t ahead) {
+    size_t top = 0;
+    for (size_t s = 0; s < b->streams; s++)
+        if (b->host_positions[s] > top)
+            top = b->host_positions[s];
+    const size_t keys = top + 1 + ahead;
+    const size_t splits = (keys + PH_SPLIT_KEYS - 1) / PH_SPLIT_KEYS;
+    return splits < b->max_splits ? splits : b->max_splits;
+}
+
 /* Enqueues layers [first, first+count) for streams [s0, s0+n) of the batch
  * (s0 a multiple of 16) on `stream`. Every buffer is used at the group's
  * offset, so groups share no memory and may run concurrently. */
@@ -434,10 +448,10 @@ static int enqueue_group(PhononFlowBatch *b, void *stream, size_t s0, size_t n, 
                          size_t count, size_t pool_offset, const float *input, float *output,
                          const float *rope) {
     const PhononFlowModel *m = b->model;
-    const size_t slot0 = s0 * PH_HEADS * b->max_splits;
+    const size_t slot0 = s0 * PH_HEADS * b->splits;
     const pgpu_attention_scratch scratch = {b->scratch.part_acc + slot0 * 64,
                                             b->scratch.part_ml + slot0 * 2, (int)n,
-                                            (int)b->max_splits};
+                                            (int)b->splits};
     float *x = b->x + s0 * PH_WIDTH, *r = b->r + s0 * PH_WIDTH, *q = b->q + s0 * PH_WIDTH;
     uint16_t *xh = b->xh + (s0 / 16) * (PH_FFN / 32) * 1536;
     const int32_t *positions = b->positions + s0, *tables = b->tables + s0 * b->table_len;
@@ -453,14 +467,14 @@ static int enqueue_group(PhononFlowBatch *b, void *stream, size_t s0, size_t n, 
         const pgpu_gemm_input att = {.attn_acc = scratch.part_acc,
                                      .attn_ml = scratch.part_ml,
                                      .attn_positions = positions,
-                                     .attn_max_splits = (int)b->max_splits};
+                                     .attn_max_splits = (int)b->splits};
         const pgpu_gemm_input ln2 = {.ln_rows = r, .ln_weight = norm + 2 * PH_WIDTH,
                                      .ln_bias = norm + 3 * PH_WIDTH, .ln_epsilon = 1e-5f};
         const pgpu_gemm_input hidden = {.split = xh};
         if (!pgpu_gemm_qkv(stream, &m->qkv[l], &ln1, (int)n, &b->pool->kv, pool_layer, tables,
                            (int)b->table_len, positions, rope, q, b->status) ||
             !pgpu_attention(stream, q, &b->pool->kv, pool_layer, tables, (int)b->table_len,
-                            positions, (int)n, PH_HEADS, (int)b->max_splits, &scratch,
+                            positions, (int)n, PH_HEADS, (int)b->splits, &scratch,
                             b->status) ||
             !pgpu_gemm_residual(stream, &m->out[l], &att, (int)n, cur, r, b->status) ||
             !pgpu_gemm_gelu_split(stream, &m->mlp_in[l], &ln2, (int)n, xh, b->status) ||
@@ -477,6 +491,7 @@ int ph_batch_enqueue_layers(PhononFlowBatch *b, size_t first, size_t count, size
         first + count + pool_offset > (size_t)b->pool->kv.layers)
         return 0;
     const float *rope = ph_rope_table(theta);
+    b->splits = splits_for(b, 0);
     return rope && enqueue_group(b, b->stream, 0, b->streams, first, count, pool_offset, input,
                                  output, rope);
 }
@@ -572,7 +587,7 @@ int phonon_flow_batch_prefill_device(PhononFlowBatch *b, size_t streams, const s
     return pgpu_stream_sync(b->stream) &&
            pgpu_copy_h2d(b->stream, b->table_src, tables, streams * table_len * sizeof(int32_t)) &&
            ph_batch_set_prefill(b, streams, first, counts, b->table_src) &&
-           enqueue_step(b, inputs, outputs, theta);
+           (b->splits = splits_for(b, 0)) > 0 && enqueue_step(b, inputs, outputs, theta);
 }
 
 int phonon_flow_batch_set_groups(PhononFlowBatch *b, size_t groups) {
@@ -601,22 +616,27 @@ int phonon_flow_batch_step_device(PhononFlowBatch *b, const float *inputs, float
         if (b->host_positions[s] >= b->max_positions)
             return 0;
     if (b->eager) {
+        b->splits = splits_for(b, 0);
         if (!enqueue_step(b, inputs, outputs, theta))
             return 0;
         for (size_t s = 0; s < b->streams; s++)
             b->host_positions[s]++;
         return 1;
     }
+    /* A captured step covers contexts up to its attention grid: captured with
+     * 256 positions of headroom, re-captured when a context outgrows it. */
+    const size_t need = splits_for(b, 0);
     void *exec = NULL;
     for (size_t i = 0; i < 2 && !exec; i++)
         if (b->graphs[i].exec && b->graphs[i].streams == b->streams &&
-            b->graphs[i].theta == theta && b->graphs[i].input == inputs &&
-            b->graphs[i].output == outputs)
+            b->graphs[i].splits >= need && b->graphs[i].theta == theta &&
+            b->graphs[i].input == inputs && b->graphs[i].output == outputs)
             exec = b->graphs[i].exec;
     if (!exec) {
         const size_t slot = b->graph_victim;
         pgpu_graph_destroy(b->graphs[slot].exec);
         b->graphs[slot].exec = NULL;
+        b->splits = splits_for(b, PH_SPLIT_KEYS);
         if (!ph_rope_table(theta) || !pgpu_graph_begin(b->stream))
             return 0;
         const int enqueued = enqueue_step(b, inputs, outputs, theta);
@@ -627,6 +647,7 @@ int phonon_flow_batch_step_device(PhononFlowBatch *b, const float *inputs, float
         }
         b->graphs[slot].exec = exec;
         b->graphs[slot].streams = b->streams;
+        b->graphs[slot].splits = b->splits;
         b->graphs[slot].theta = theta;
         b->graphs[slot].input = inputs;
         b->graphs[slot].output = outputs;
