@@ -23,16 +23,15 @@
 //   from zero (int8 and bf16 terms multiply exactly), then acc += scale*c,
 //   i.e. the reference phonon_q8_dot order "sum += scale * partial".
 //   BF16: the three MFMAs chain straight into the accumulator.
-// Work decomposition (results never depend on scheduling)
-//   SRC_SPLIT (k_gemm): one work-group = 16 output rows x 16 streams; its
-//   16 waves split the column blocks into 16 contiguous ranges, summed in
-//   LDS in wave order.
-//   SRC_LN / SRC_ATTN (k_gemm_wide, K = 512): one 1024-thread work-group =
-//   64 rows x 16 streams; the prologue runs once with one wave per stream,
-//   then 16 waves take (tile, quarter of the column blocks) pairs and the
-//   quarters are summed in order. One prologue per 4 tiles, spread over 16
-//   waves: the prologue, not the MFMAs, is what the kernel's latency is
-//   made of.
+// Work decomposition (results never depend on scheduling): tasks of one
+// 1024-thread work-group
+//   SRC_SPLIT (gemm_split_task): 1 row tile x 16 streams; its 16 waves split
+//   the column blocks into 16 ranges, summed in LDS in wave order.
+//   SRC_LN / SRC_ATTN (gemm_wide_task, K = 512): 4 row tiles x 16 streams;
+//   the prologue runs once with one wave per stream, then 16 waves take
+//   (tile, quarter of the column blocks) pairs and the quarters are summed
+//   in order. One prologue per 4 tiles, spread over 16 waves: the prologue,
+//   not the MFMAs, is what the kernel's latency is made of.
 #include <hip/hip_fp16.h>
 
 #include "pgpu_common.hpp"
@@ -403,29 +402,34 @@ __device__ inline bool epilogue(const GemmArgs &a, const EpiOperands &e, const f
     return bad;
 }
 
-// Projection of split-fragment rows from global memory (any K): one
-// 1024-thread work-group = 16 rows x 16 streams; its 16 waves split the
-// column blocks into 16 contiguous ranges (4 blocks each at K = 2048, all
-// requested at once), summed in LDS in wave order.
+// Tasks: the unit of work of one 1024-thread work-group, run by the
+// single-phase kernels below (one task per work-group) and by the decode
+// layer kernel (several tasks per work-group, phase after phase), so both
+// produce the same bits.
+
+// LDS of a task: the prologue's operand buffer, reused for partial sums.
+constexpr int kTaskLds = 16 * kLdsBlock;
+
+// Split-fragment rows from global memory (any K): one row tile x 16
+// streams. The 16 waves split the column blocks into 16 contiguous ranges
+// (4 blocks each at K = 2048, all requested at once; chunks of CH, the next
+// chunk's weights requested before the current chunk's MFMAs), summed in
+// LDS in wave order.
 template <int EPI, bool Q8, int CH>
-__global__ __launch_bounds__(1024) void k_gemm(GemmArgs a) {
+__device__ inline void gemm_split_task(const GemmArgs &a, int tile, int st, uint16_t *lds) {
     constexpr int NW = 16;
-    const int tile = blockIdx.x, st = blockIdx.y;
-    // Uniform per wave (readfirstlane): the block loop below is scalar control.
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     const int kbn = a.k_cols >> 5;
-    const int per_wave = (kbn + NW - 1) / NW;
-    const int kb_begin = wave * per_wave;
-    const int kb_end = min(kbn, kb_begin + per_wave);
+    const int per = (kbn + NW - 1) / NW;
+    const int kb_begin = wave * per;
+    const int kb_end = min(kbn, kb_begin + per);
 
     // D fragment of this lane: rows row0 .. row0+3 of stream s.
     const int s = st * 16 + (lane & 15);
     const int row0 = tile * 16 + (lane >> 4) * 4;
     const bool live = s < a.streams;
 
-    // The first weight chunk and the epilogue's operands (wave 0 runs the
-    // epilogue) are requested first.
     WChunk<Q8, CH> w;
     if (kb_begin < kb_end) load_weights(w, a, tile, kbn, lane, kb_begin, kb_end);
     EpiOperands e;
@@ -433,9 +437,6 @@ __global__ __launch_bounds__(1024) void k_gemm(GemmArgs a) {
 
     const uint16_t *xs = a.xs + (size_t)st * kbn * 1536 + lane * 8;
     f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-    // Chunks of CH blocks; the next chunk's weights are requested before the
-    // current chunk's MFMAs (past the wave's range the last block is re-read
-    // and not used).
     for (int kb0 = kb_begin; kb0 < kb_end; kb0 += CH) {
         bf16x8 xh[CH], xm[CH], xl[CH];
 #pragma unroll
@@ -451,41 +452,37 @@ __global__ __launch_bounds__(1024) void k_gemm(GemmArgs a) {
         w = next;
     }
 
-    __shared__ f32x4 partial[NW][64];
-    partial[wave][lane] = acc;
+    f32x4 *partial = (f32x4 *)lds;
+    __syncthreads();  // the buffer may still be read by a previous task
+    partial[wave * 64 + lane] = acc;
     __syncthreads();
-    if (wave != 0) return;  // no barrier follows
-    f32x4 v = partial[0][lane];
+    if (wave != 0) return;
+    f32x4 v = acc;
 #pragma unroll
-    for (int w = 1; w < NW; w++) {
-        const f32x4 p = partial[w][lane];
+    for (int w2 = 1; w2 < NW; w2++) {
+        const f32x4 p = partial[w2 * 64 + lane];
         v[0] = __fadd_rn(v[0], p[0]);
         v[1] = __fadd_rn(v[1], p[1]);
         v[2] = __fadd_rn(v[2], p[2]);
         v[3] = __fadd_rn(v[3], p[3]);
     }
-
     flag_nonfinite(a.status, epilogue<EPI>(a, e, v, s, row0, live));
 }
 
-// Projection whose operand a prologue builds (LayerNorm or the attention
-// merge; K = 512), by a 1024-thread work-group of 4 row tiles x 16 streams.
-// The prologue runs once per 64 rows with 8 values per lane (one wave per
-// stream), which keeps its latency short. Wave w = 4q + t then computes
-// column blocks [4q, 4q+4) of tile t; the 4 quarters of a tile are added in
-// quarter order (as k_gemm adds its waves), and wave t finishes tile t. The
-// wave's weights and the epilogue operands are requested before the
-// prologue, so their latency overlaps it.
+// Operand built by a prologue (LayerNorm or the attention merge; K = 512):
+// 4 row tiles x 16 streams. The prologue runs once per 64 rows with 8
+// values per lane (one wave per stream); wave w = 4q + t then computes
+// column blocks [4q, 4q+4) of tile t, and the 4 quarters of a tile are
+// added in order. The wave's weights and the epilogue operands are
+// requested before the prologue, so their latency overlaps it.
 template <int SRC, int EPI, bool Q8>
-__global__ __launch_bounds__(1024) void k_gemm_wide(GemmArgs a) {
+__device__ inline void gemm_wide_task(const GemmArgs &a, int bx, int st, uint16_t *bsh) {
     constexpr int kbn = kWidth / 32, KBW = kbn / 4;
-    const int st = blockIdx.y;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
-    const int tiles = a.n_rows >> 4;
     const int t = wave & 3, q = wave >> 2;
-    const int tile = blockIdx.x * 4 + t;
-    const bool active = tile < tiles;  // uniform per wave
+    const int tile = bx * 4 + t;
+    const bool active = tile < (a.n_rows >> 4);  // uniform per wave
     const int kb0 = q * KBW;
     const int s = st * 16 + (lane & 15);
     const bool live = s < a.streams;
@@ -496,7 +493,7 @@ __global__ __launch_bounds__(1024) void k_gemm_wide(GemmArgs a) {
     EpiOperands e;
     if (active && q == 0) load_epilogue<EPI>(e, a, s, row0, live);
 
-    __shared__ uint16_t bsh[16 * kLdsBlock];
+    __syncthreads();  // the buffer may still be read by a previous task
     const bool bad_in = SRC == SRC_LN ? prologue_ln(a, st, bsh) : prologue_attn(a, st, bsh);
     flag_nonfinite(a.status, bad_in);
     __syncthreads();
@@ -519,7 +516,7 @@ __global__ __launch_bounds__(1024) void k_gemm_wide(GemmArgs a) {
     f32x4 *partial = (f32x4 *)bsh;
     partial[wave * 64 + lane] = acc;
     __syncthreads();
-    if (q != 0 || !active) return;  // no barrier follows
+    if (q != 0 || !active) return;
     f32x4 v = acc;
 #pragma unroll
     for (int q2 = 1; q2 < 4; q2++) {
@@ -532,6 +529,18 @@ __global__ __launch_bounds__(1024) void k_gemm_wide(GemmArgs a) {
     flag_nonfinite(a.status, epilogue<EPI>(a, e, v, s, row0, live));
 }
 
+template <int EPI, bool Q8, int CH>
+__global__ __launch_bounds__(1024) void k_gemm(GemmArgs a) {
+    __shared__ uint16_t lds[16 * 64 * 8];  // 16 waves x 64 lanes x f32x4
+    gemm_split_task<EPI, Q8, CH>(a, blockIdx.x, blockIdx.y, lds);
+}
+
+template <int SRC, int EPI, bool Q8>
+__global__ __launch_bounds__(1024) void k_gemm_wide(GemmArgs a) {
+    __shared__ uint16_t bsh[kTaskLds];
+    gemm_wide_task<SRC, EPI, Q8>(a, blockIdx.x, blockIdx.y, bsh);
+}
+
 template <int SRC, int EPI, bool Q8>
 static int launch(const GemmArgs &a, hipStream_t stream) {
     if (a.n_rows <= 0 || a.n_rows % 16 || a.k_cols <= 0 || a.k_cols % 32 || a.streams <= 0 ||
@@ -542,11 +551,7 @@ static int launch(const GemmArgs &a, hipStream_t stream) {
         hipLaunchKernelGGL((k_gemm_wide<SRC, EPI, Q8>), grid, dim3(1024), 0, stream, a);
     } else {
         const dim3 grid(a.n_rows / 16, (a.streams + 15) / 16);
-        // Up to 4 column blocks per wave (K <= 2048): one chunk of 4; else chunks of 8.
-        if (a.k_cols <= 2048)
-            hipLaunchKernelGGL((k_gemm<EPI, Q8, 4>), grid, dim3(1024), 0, stream, a);
-        else
-            hipLaunchKernelGGL((k_gemm<EPI, Q8, 8>), grid, dim3(1024), 0, stream, a);
+        hipLaunchKernelGGL((k_gemm<EPI, Q8, 4>), grid, dim3(1024), 0, stream, a);
     }
     return launch_ok("pgpu_gemm");
 }
