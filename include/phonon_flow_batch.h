@@ -103,6 +103,14 @@ int phonon_flow_batch_prefill_device(PhononFlowBatch *batch, size_t streams, con
  * depend on it. Default 1: on MI355X under ROCm 7 kernels of different HIP
  * streams were measured not to overlap, so more groups only add launches. */
 int phonon_flow_batch_set_groups(PhononFlowBatch *batch, size_t groups);
+/* enable = 1: a batch of more than 16 streams runs each step as paired
+ * launches, one stream group's attention beside the other group's
+ * projections (device-wide barriers between the projection phases);
+ * 0 (default): one launch per kernel of each layer. Results are identical.
+ * On MI355X the paired form is slower at B=64 (1240 vs 875 us per step): a
+ * kernel's register budget is that of its largest role, so its 1024-thread
+ * work-groups run one per CU, and each chain barrier costs 5-6 us. */
+int phonon_flow_batch_set_pipeline(PhononFlowBatch *batch, int enable);
 /* use_graph = 1 (default): step_device replays a captured HIP graph;
  * 0: it launches the step's kernels directly (e.g. for a caller that is
  * itself capturing a graph). Results are identical. */

@@ -110,6 +110,44 @@ int pgpu_gemm_qkv(void *stream, const pgpu_matrix *w, const pgpu_gemm_input *x, 
                   const pgpu_paged_kv *kv, int layer, const int32_t *tables, int table_stride,
                   const int32_t *positions, const float *rope, float *q_out, int *status);
 
+/* -- paired decode launch (pgpu_gemm.hip) --
+ * One launch holding the split attention of one stream group and, beside
+ * it, the projection chain of another group whose attention has finished:
+ * out projection + residual, LayerNorm 2 + MLP in + GELU, MLP out +
+ * residual, then LayerNorm 1 + QKV + RoPE + KV append of the next layer.
+ * Results are bit-identical to the single-phase launches. Pointers are at
+ * the group's first stream (tile-aligned); streams are counted from there. */
+typedef struct {
+    const float *q;                     /* (dev) [streams][512] */
+    const int32_t *tables, *positions;  /* (dev) */
+    int streams, layer;
+    pgpu_attention_scratch scratch;     /* max_splits: the launch's split count */
+} pgpu_pair_attention;
+
+typedef struct {
+    int streams, layer;                 /* the layer whose attention has finished */
+    const pgpu_matrix *out, *mlp_in, *mlp_out;
+    const pgpu_matrix *qkv_next;        /* NULL on the last layer */
+    const float *norm2_weight, *norm2_bias;       /* (dev) [512] */
+    const float *norm1_next_weight, *norm1_next_bias;
+    float ln_epsilon;
+    const float *input;                 /* (dev) layer input rows (residual) */
+    float *r;                           /* (dev) out projection + residual rows */
+    uint16_t *hidden;                   /* (dev) MLP hidden, split fragments */
+    float *output;                      /* (dev) layer output rows */
+    float *q_next;                      /* (dev) next layer's q rows */
+    const int32_t *tables, *positions;  /* (dev) */
+    pgpu_attention_scratch scratch;     /* the partials of `layer` */
+} pgpu_pair_chain;
+
+/* Either part may be NULL (not both). `counter` (dev) must be 0 at launch
+ * and is used by this launch only. Status bit 4: a chain barrier timed out. */
+int pgpu_decode_pair(void *stream, const pgpu_pair_attention *attention,
+                     const pgpu_pair_chain *chain, const pgpu_paged_kv *kv, int table_stride,
+                     const float *rope, unsigned *counter, int *status);
+/* Fills n 32-bit words with `value` (a kernel: usable inside a captured graph). */
+int pgpu_fill_u32(void *stream, uint32_t *dst, size_t n, uint32_t value);
+
 /* -- attention (pgpu_attention.hip): stream s attends positions[s]+1 keys;
  * max_splits * 256 must cover every context. Writes the per-split partials
  * into `scratch`; pgpu_attention_merge (or a projection with an attn_acc

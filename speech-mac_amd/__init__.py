@@ -145,6 +145,7 @@ EXPORTS = {
     "phonon_flow_batch_set_streams": (_i, [_vp, _sz, _szp, _i32p, _sz]),
     "phonon_flow_batch_step": (_i, [_vp, _fp, _f, _fp]),
     "phonon_flow_batch_step_device": (_i, [_vp, _vp, _f, _vp]),
+    "phonon_flow_batch_set_pipeline": (_i, [_vp, _i]),
     "phonon_flow_batch_prefill_device": (_i, [_vp, _sz, _vp, _vp, _vp, _sz, _vp, _f, _vp]),
     "phonon_flow_batch_sync": (_i, [_vp]),
     "phonon_flow_batch_set_groups": (_i, [_vp, _sz]),
@@ -194,6 +195,8 @@ EXPORTS = {
     "pgpu_fill_normal": (_i, [_vp, _vp, _sz, ctypes.c_uint64]),
     "pgpu_advance_positions": (_i, [_vp, _vp, _i]),
     "pgpu_gather_rows": (_i, [_vp, _vp, _vp, _vp, _i, _i]),
+    "pgpu_fill_u32": (_i, [_vp, _vp, _sz, ctypes.c_uint32]),
+    "pgpu_decode_pair": (_i, [_vp, _vp, _vp, _kvp, _i, _vp, _vp, _vp]),
 }
 
 _LIB = None

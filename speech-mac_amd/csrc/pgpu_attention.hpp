@@ -1,0 +1,184 @@
+// Split-attention unit shared by the attention kernels (pgpu_attention.hip)
+// and the paired decode kernel (pgpu_gemm.hip). See pgpu_attention.hip for
+// the pool layout and the work decomposition.
+#pragma once
+
+#include "pgpu_common.hpp"
+
+namespace pgpu {
+
+struct AttnArgs {
+    const float *q;           // [streams][512], RoPE'd, scaled by 1/8
+    const float *kv;
+    size_t layer_stride;
+    unsigned blocks;          // blocks per layer; table entries must be below
+    int layer;
+    const int32_t *tables;
+    int table_stride;
+    const int32_t *positions; // keys attended = positions[s] + 1
+    int streams, max_splits;
+    float *part_acc;          // [streams*8*max_splits][64]
+    float *part_ml;           // [streams*8*max_splits][2]
+    int *status;
+};
+
+
+
+// K/V bytes are read once per step: non-temporal loads, so the stream does
+// not displace what the other kernels of the step re-read from the caches
+// (projection weights, activations).
+__device__ inline float4 stream_load(const float *p) {
+    typedef float f4 __attribute__((ext_vector_type(4)));
+    const f4 v = __builtin_nontemporal_load((const f4 *)p);
+    return make_float4(v.x, v.y, v.z, v.w);
+}
+
+// Waves per split unit and K/V blocks per wave: a unit of 8 waves x 2 blocks
+// covers one 256-key split; each wave keeps its 16 float4 of K/V in
+// flight at once (64 registers), so a 1024-thread work-group (2 units) stays
+// within 128 registers per lane.
+constexpr int kUnitWaves = 8, kBlocksPerWave = 2;
+
+struct AttnShared {
+    float4 acc[kUnitWaves][16];
+    float m[kUnitWaves], l[kUnitWaves];
+};
+
+// Split `split` of head `head` of stream `s`, by the unit's 8 waves (`wave`
+// = 0..7 within the unit). Every wave of the work-group must call it (it
+// holds one work-group barrier); a unit without live keys (or that does not
+// `exist`: past the end of a grid) only takes part in the barrier. Writes
+// the split's (max, sum, unnormalised P.V) partial.
+__device__ inline void attend_split(const AttnArgs &a, int head, int split, int s, int wave,
+                                    AttnShared &sh, bool exists = true) {
+    const int lane = threadIdx.x & 63;
+    const int krow = lane >> 4, dcol = lane & 15;
+    const int count = exists ? a.positions[s] + 1 : 0;
+    const int nsplit = (count + kSplitKeys - 1) / kSplitKeys;
+    // A context the grid or the block table cannot cover is an error, never
+    // a partial read: flag it once, and the unit computes nothing.
+    const bool covered =
+        count >= 1 && nsplit <= a.max_splits && count <= a.table_stride * kBlockPos;
+    if (exists && !covered && split == 0 && wave == 0 && lane == 0) atomicOr(a.status, 2);
+    const bool live = covered && split * kSplitKeys < count;  // uniform per unit
+
+    float m = -INFINITY, l = 0.0f;
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (live) {
+        const float4 q = *(const float4 *)(a.q + (size_t)s * kWidth + head * kHeadDim + dcol * 4);
+        const int32_t *__restrict__ table = a.tables + (size_t)s * a.table_stride;
+        const float *layer_kv = a.kv + (size_t)a.layer * a.layer_stride;
+        const int first_block = split * 16 + wave * kBlocksPerWave;
+        const int stream_blocks = (count + kBlockPos - 1) / kBlockPos;
+        // < first_block: this wave has no keys
+        const int last_block = min(first_block + kBlocksPerWave - 1, stream_blocks - 1);
+
+        // Block ids first (uniform), then every K/V load of the wave at once.
+        // Blocks past the context re-read the last valid block (their keys
+        // are masked below); an id outside the pool is flagged and replaced.
+        int ids[kBlocksPerWave];
+        bool bad_block = false;
+#pragma unroll
+        for (int t = 0; t < kBlocksPerWave; t++) {
+            const int b = min(first_block + t, max(last_block, first_block));
+            const int id = last_block >= first_block ? table[b] : 0;
+            bad_block |= (unsigned)id >= a.blocks;
+            ids[t] = (unsigned)id < a.blocks ? id : 0;
+        }
+        float4 kr[kBlocksPerWave][4], vr[kBlocksPerWave][4];
+        if (last_block >= first_block) {
+#pragma unroll
+            for (int t = 0; t < kBlocksPerWave; t++) {
+                const float *tile =
+                    layer_kv + ((size_t)ids[t] * kHeads + head) * 2048 + lane * 4;
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    kr[t][i] = stream_load(tile + i * 256);
+                    vr[t][i] = stream_load(tile + 1024 + i * 256);
+                }
+            }
+        } else {
+#pragma unroll
+            for (int t = 0; t < kBlocksPerWave; t++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    kr[t][i] = make_float4(0.f, 0.f, 0.f, 0.f);
+                    vr[t][i] = make_float4(0.f, 0.f, 0.f, 0.f);
+                }
+        }
+        if (bad_block && lane == 0) atomicOr(a.status, 2);
+
+        float score[kBlocksPerWave][4];
+#pragma unroll
+        for (int t = 0; t < kBlocksPerWave; t++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const float4 k = kr[t][i];
+                float d = q.x * k.x;
+                d = fmaf(q.y, k.y, d);
+                d = fmaf(q.z, k.z, d);
+                d = fmaf(q.w, k.w, d);
+                d = row16_sum(d);
+                const int key = (first_block + t) * kBlockPos + i * 4 + krow;
+                score[t][i] = key < count ? d : -INFINITY;
+                m = fmaxf(m, score[t][i]);
+            }
+        m = fmaxf(m, __shfl_xor(m, 16));
+        m = fmaxf(m, __shfl_xor(m, 32));
+#pragma unroll
+        for (int t = 0; t < kBlocksPerWave; t++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                // Slots past the context hold whatever the pool held before:
+                // they are skipped, never multiplied by a zero weight.
+                if (score[t][i] == -INFINITY) continue;
+                const float e = expf(score[t][i] - m);
+                l += e;
+                acc.x = fmaf(e, vr[t][i].x, acc.x);
+                acc.y = fmaf(e, vr[t][i].y, acc.y);
+                acc.z = fmaf(e, vr[t][i].z, acc.z);
+                acc.w = fmaf(e, vr[t][i].w, acc.w);
+            }
+        // Lanes of one key row hold the same l; sum the four rows.
+        l += __shfl_xor(l, 16);
+        l += __shfl_xor(l, 32);
+        acc.x += __shfl_xor(acc.x, 16);
+        acc.y += __shfl_xor(acc.y, 16);
+        acc.z += __shfl_xor(acc.z, 16);
+        acc.w += __shfl_xor(acc.w, 16);
+        acc.x += __shfl_xor(acc.x, 32);
+        acc.y += __shfl_xor(acc.y, 32);
+        acc.z += __shfl_xor(acc.z, 32);
+        acc.w += __shfl_xor(acc.w, 32);
+        if (lane < 16) sh.acc[wave][lane] = acc;
+        if (lane == 0) {
+            sh.m[wave] = m;
+            sh.l[wave] = l;
+        }
+    }
+    __syncthreads();
+    if (!live || wave != 0 || lane >= 16) return;
+
+    // Merge the unit's waves (fixed order). A wave without keys has l = 0.
+    float mm = sh.m[0];
+#pragma unroll
+    for (int w = 1; w < kUnitWaves; w++) mm = fmaxf(mm, sh.m[w]);
+    float ll = 0.0f;
+    float4 aa = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int w = 0; w < kUnitWaves; w++) {
+        if (sh.l[w] == 0.0f) continue;
+        const float f = expf(sh.m[w] - mm);
+        ll = fmaf(sh.l[w], f, ll);
+        const float4 x = sh.acc[w][lane];
+        aa.x = fmaf(x.x, f, aa.x);
+        aa.y = fmaf(x.y, f, aa.y);
+        aa.z = fmaf(x.z, f, aa.z);
+        aa.w = fmaf(x.w, f, aa.w);
+    }
+    const size_t slot = ((size_t)s * kHeads + head) * a.max_splits + split;
+    *(float4 *)(a.part_acc + slot * 64 + lane * 4) = aa;
+    if (lane == 0) *(float2 *)(a.part_ml + slot * 2) = make_float2(mm, ll);
+}
+
+}  // namespace pgpu

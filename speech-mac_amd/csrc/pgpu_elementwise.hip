@@ -217,6 +217,11 @@ __global__ void k_advance(int32_t *positions, int streams) {
     if (s < streams) positions[s] += 1;
 }
 
+__global__ void k_fill_u32(uint32_t *dst, size_t n, uint32_t value) {
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i < n) dst[i] = value;
+}
+
 // dst row r = src row map[r] (int32 rows of `width`): per-token copies of a
 // stream's block table for a batched prefill. Grid (ceil(width/256), rows).
 __global__ void k_gather_rows(int32_t *__restrict__ dst, const int32_t *__restrict__ src,
@@ -309,5 +314,12 @@ extern "C" int pgpu_gather_rows(void *stream, int32_t *dst, const int32_t *src,
     if (!dst || !src || !map || rows <= 0 || width <= 0) return bad_arguments(__func__);
     hipLaunchKernelGGL(k_gather_rows, dim3((width + 255) / 256, rows), dim3(256), 0,
                        (hipStream_t)stream, dst, src, map, width);
+    return launch_ok(__func__);
+}
+
+extern "C" int pgpu_fill_u32(void *stream, uint32_t *dst, size_t n, uint32_t value) {
+    if (!dst || !n) return bad_arguments(__func__);
+    hipLaunchKernelGGL(k_fill_u32, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
+                       (hipStream_t)stream, dst, n, value);
     return launch_ok(__func__);
 }

@@ -34,6 +34,7 @@
 //   not the MFMAs, is what the kernel's latency is made of.
 #include <hip/hip_fp16.h>
 
+#include "pgpu_attention.hpp"
 #include "pgpu_common.hpp"
 #include "phonon_gpu.h"
 
@@ -541,6 +542,89 @@ __global__ __launch_bounds__(1024) void k_gemm_wide(GemmArgs a) {
     gemm_wide_task<SRC, EPI, Q8>(a, blockIdx.x, blockIdx.y, bsh);
 }
 
+// ---------------------------------------------------------------------
+// Paired decode kernel: one launch holds the split attention of one stream
+// group (layer l) and the projection chain of another group that follows
+// its own attention: out projection, MLP in, MLP out and the next layer's
+// QKV (src/phonon_transformer.c:437-451, 418-427). The attention is HBM
+// bound and the projections are latency chains, so running them side by
+// side hides the chain. Work-groups [0, chain_wgs) run the chain, phase
+// after phase, with a device-wide barrier between phases; they hold the
+// lowest block ids, so all of them are resident before any attention
+// work-group starts. The rest run two attention split units each. Every
+// task is the code of the single-phase kernels, so results are bit-identical
+// to running the phases one launch at a time.
+
+enum ChainPhase { PH_OUT = 0, PH_MLP_IN = 1, PH_MLP_OUT = 2, PH_QKV = 3 };
+
+struct PairArgs {
+    AttnArgs att;           // attention of streams [att_stream0, +att_streams)
+    int att_stream0, att_units;  // units = 8 heads x att.max_splits x streams
+    GemmArgs chain[4];      // ChainPhase order, for stream tiles [st0, st0 + tiles)
+    int phases;             // 0, 3 (last layer) or 4
+    int st0, tiles, chain_wgs;
+    unsigned *counter;      // zero at launch; one per launch
+    int *status;
+};
+
+// Device-wide barrier among the chain's work-groups: release, count, wait,
+// acquire. The wait is bounded: a work-group that waits too long flags
+// status bit 4 (results are then unspecified) and goes on, so the kernel
+// always ends.
+__device__ inline void chain_barrier(unsigned *counter, unsigned target, int *status) {
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        __threadfence();
+        atomicAdd(counter, 1u);
+        int spins = 0;
+        while (__hip_atomic_load(counter, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
+            if (++spins > (1 << 20)) {
+                atomicOr(status, 4);
+                break;
+            }
+            __builtin_amdgcn_s_sleep(2);
+        }
+        __threadfence();
+    }
+    __syncthreads();
+}
+
+template <bool Q8>
+__global__ __launch_bounds__(1024) void k_decode_pair(PairArgs p) {
+    __shared__ uint4 lds4[kTaskLds / 8];
+    uint16_t *lds = (uint16_t *)lds4;
+    if ((int)blockIdx.x < p.chain_wgs) {
+        for (int ph = 0; ph < p.phases; ph++) {
+            if (ph > 0) chain_barrier(p.counter, (unsigned)(p.chain_wgs * ph), p.status);
+            const GemmArgs &a = p.chain[ph];
+            const int nx = ph == PH_MLP_OUT ? a.n_rows / 16 : (a.n_rows / 16 + 3) / 4;
+            const int tasks = nx * p.tiles;
+            for (int task = blockIdx.x; task < tasks; task += p.chain_wgs) {
+                const int bx = task % nx, st = p.st0 + task / nx;
+                if (ph == PH_OUT)
+                    gemm_wide_task<SRC_ATTN, EPI_RESIDUAL, Q8>(a, bx, st, lds);
+                else if (ph == PH_MLP_IN)
+                    gemm_wide_task<SRC_LN, EPI_GELU_SPLIT, Q8>(a, bx, st, lds);
+                else if (ph == PH_MLP_OUT)
+                    gemm_split_task<EPI_RESIDUAL, Q8, 4>(a, bx, st, lds);
+                else
+                    gemm_wide_task<SRC_LN, EPI_QKV, Q8>(a, bx, st, lds);
+            }
+        }
+        return;
+    }
+    // Attention: units (head fastest, then split, then stream), two per
+    // work-group (waves 0-7 and 8-15).
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int u = ((int)blockIdx.x - p.chain_wgs) * 2 + (wave >> 3);
+    const bool exists = u < p.att_units;
+    const int head = u & 7, rest = u >> 3;
+    const int split = rest % p.att.max_splits;
+    const int s = p.att_stream0 + (exists ? rest / p.att.max_splits : 0);
+    AttnShared *sh = (AttnShared *)lds4;
+    attend_split(p.att, head, split, s, wave & 7, sh[wave >> 3], exists);
+}
+
 template <int SRC, int EPI, bool Q8>
 static int launch(const GemmArgs &a, hipStream_t stream) {
     if (a.n_rows <= 0 || a.n_rows % 16 || a.k_cols <= 0 || a.k_cols % 32 || a.streams <= 0 ||
@@ -653,4 +737,117 @@ extern "C" int pgpu_gemm_qkv(void *stream, const pgpu_matrix *w, const pgpu_gemm
     a.positions = positions;
     a.rope = (const float2 *)rope;
     return dispatch<EPI_QKV>(a, w->q8, (hipStream_t)stream);
+}
+
+static bool chain_phase_args(GemmArgs &a, const pgpu_matrix *w, const pgpu_gemm_input &in,
+                             int streams, int *status) {
+    return w && w->values && (!w->q8 || w->scales) && base_args(a, w, &in, streams, status) &&
+           a.n_rows > 0 && a.n_rows % 16 == 0 && a.k_cols > 0 && a.k_cols % 32 == 0;
+}
+
+extern "C" int pgpu_decode_pair(void *stream, const pgpu_pair_attention *att,
+                                const pgpu_pair_chain *ch, const pgpu_paged_kv *kv,
+                                int table_stride, const float *rope, unsigned *counter,
+                                int *status) {
+    if ((!att && !ch) || !kv || !status || table_stride <= 0 || (ch && (!counter || !rope)))
+        return bad_arguments("pgpu_decode_pair");
+    PairArgs p{};
+    p.status = status;
+    p.counter = counter;
+    int q8 = -1;
+    if (att) {
+        const pgpu_attention_scratch &sc = att->scratch;
+        if (!att->q || !att->tables || !att->positions || att->streams <= 0 ||
+            att->layer < 0 || att->layer >= kv->layers || sc.max_splits <= 0 ||
+            att->streams > sc.max_streams)
+            return bad_arguments("pgpu_decode_pair");
+        AttnArgs &a = p.att;
+        a.q = att->q;
+        a.kv = kv->base;
+        a.layer_stride = kv->layer_stride;
+        a.blocks = (unsigned)kv->blocks;
+        a.layer = att->layer;
+        a.tables = att->tables;
+        a.table_stride = table_stride;
+        a.positions = att->positions;
+        a.streams = att->streams;
+        a.max_splits = sc.max_splits;
+        a.part_acc = sc.part_acc;
+        a.part_ml = sc.part_ml;
+        a.status = status;
+        p.att_units = kHeads * sc.max_splits * att->streams;
+    }
+    if (ch) {
+        const int n = ch->streams;
+        if (n <= 0 || ch->layer < 0 || ch->layer >= kv->layers ||
+            (ch->qkv_next && ch->layer + 1 >= kv->layers) || !ch->out || !ch->mlp_in ||
+            !ch->mlp_out || ch->out->rows != (size_t)kWidth || ch->mlp_in->columns != (size_t)kWidth ||
+            ch->mlp_out->rows != (size_t)kWidth || ch->mlp_out->columns != ch->mlp_in->rows ||
+            ch->scratch.max_splits <= 0 || n > ch->scratch.max_streams)
+            return bad_arguments("pgpu_decode_pair");
+        q8 = ch->out->q8;
+        if (ch->mlp_in->q8 != q8 || ch->mlp_out->q8 != q8 || (ch->qkv_next && ch->qkv_next->q8 != q8))
+            return bad_arguments("pgpu_decode_pair");
+        pgpu_gemm_input in{};
+        in.attn_acc = ch->scratch.part_acc;
+        in.attn_ml = ch->scratch.part_ml;
+        in.attn_positions = ch->positions;
+        in.attn_max_splits = ch->scratch.max_splits;
+        GemmArgs &o = p.chain[PH_OUT];
+        if (!chain_phase_args(o, ch->out, in, n, status)) return bad_arguments("pgpu_decode_pair");
+        o.out = ch->r;
+        o.ld_out = kWidth;
+        o.residual = ch->input;
+        in = pgpu_gemm_input{};
+        in.ln_rows = ch->r;
+        in.ln_weight = ch->norm2_weight;
+        in.ln_bias = ch->norm2_bias;
+        in.ln_epsilon = ch->ln_epsilon;
+        GemmArgs &mi = p.chain[PH_MLP_IN];
+        if (!chain_phase_args(mi, ch->mlp_in, in, n, status) || mi.k_cols != kWidth)
+            return bad_arguments("pgpu_decode_pair");
+        mi.out_split = ch->hidden;
+        mi.out_kb = mi.n_rows / 32;
+        in = pgpu_gemm_input{};
+        in.split = ch->hidden;
+        GemmArgs &mo = p.chain[PH_MLP_OUT];
+        if (!chain_phase_args(mo, ch->mlp_out, in, n, status))
+            return bad_arguments("pgpu_decode_pair");
+        mo.out = ch->output;
+        mo.ld_out = kWidth;
+        mo.residual = ch->r;
+        p.phases = 3;
+        if (ch->qkv_next) {
+            in = pgpu_gemm_input{};
+            in.ln_rows = ch->output;
+            in.ln_weight = ch->norm1_next_weight;
+            in.ln_bias = ch->norm1_next_bias;
+            in.ln_epsilon = ch->ln_epsilon;
+            GemmArgs &q = p.chain[PH_QKV];
+            if (ch->qkv_next->rows != 3 * (size_t)kWidth ||
+                !chain_phase_args(q, ch->qkv_next, in, n, status) || q.k_cols != kWidth)
+                return bad_arguments("pgpu_decode_pair");
+            q.q_out = ch->q_next;
+            q.kv = kv->base;
+            q.layer_stride = kv->layer_stride;
+            q.blocks = (unsigned)kv->blocks;
+            q.layer = ch->layer + 1;
+            q.tables = ch->tables;
+            q.table_stride = table_stride;
+            q.positions = ch->positions;
+            q.rope = (const float2 *)rope;
+            p.phases = 4;
+        }
+        p.st0 = 0;
+        p.tiles = (n + 15) / 16;
+        // One round of tasks per phase (the widest phase has 32 tasks per
+        // tile), at most 64 chain work-groups.
+        p.chain_wgs = min(64, 32 * p.tiles);
+    }
+    const int grid = p.chain_wgs + (p.att_units + 1) / 2;
+    if (q8 == 0)
+        hipLaunchKernelGGL(k_decode_pair<false>, dim3(grid), dim3(1024), 0, (hipStream_t)stream, p);
+    else
+        hipLaunchKernelGGL(k_decode_pair<true>, dim3(grid), dim3(1024), 0, (hipStream_t)stream, p);
+    return launch_ok("pgpu_decode_pair");
 }

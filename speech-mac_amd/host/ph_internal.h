@@ -12,6 +12,8 @@
 
 enum { PH_WIDTH = 512, PH_HEADS = 8, PH_HEAD = 64, PH_FFN = 2048, PH_SPLIT_KEYS = 256 };
 enum { PH_MAX_GROUPS = 4, PH_DEFAULT_GROUPS = 1 };
+/* Launches of a paired decode step: 2 * layers + 2, layers <= 64. */
+enum { PH_MAX_LAUNCHES = 2 * 64 + 2 };
 
 /* Device selection and the library's own HIP stream (created once). */
 int ph_init(void);

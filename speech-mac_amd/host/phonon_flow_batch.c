@@ -40,6 +40,8 @@ struct PhononFlowBatch {
     uint16_t *xh; /* split fragments of the MLP hidden rows */
     int32_t *positions, *tables;
     int32_t *table_src, *table_map; /* prefill staging, allocated on first use */
+    unsigned *counters;             /* barrier counters of the paired launches */
+    int pipeline;                   /* paired launches when >= 2 stream tiles */
     int *status;
     pgpu_attention_scratch scratch;
     size_t *host_positions;
@@ -314,7 +316,8 @@ void phonon_flow_batch_destroy(PhononFlowBatch *b) {
     pgpu_event_destroy(b->fork);
     void *bufs[] = {b->x,    b->r,  b->q,         b->in,     b->out,
                     b->rows, b->xh, b->positions, b->tables, b->status,
-                    b->scratch.part_acc, b->scratch.part_ml, b->table_src, b->table_map};
+                    b->scratch.part_acc, b->scratch.part_ml, b->table_src, b->table_map,
+                    b->counters};
     for (size_t i = 0; i < sizeof(bufs) / sizeof(bufs[0]); i++)
         pgpu_free(bufs[i]);
     pgpu_stream_destroy(b->stream);
@@ -345,6 +348,7 @@ int phonon_flow_batch_create(const PhononFlowModel *model, PhononKvPool *pool,
     const size_t split2048 = b->padded_streams * PH_FFN * 3 * sizeof(uint16_t);
     const size_t slots = max_streams * PH_HEADS * b->max_splits;
     b->groups = PH_DEFAULT_GROUPS;
+    b->pipeline = 0;
     int ok = pgpu_stream_create(&b->stream) && pgpu_event_create(&b->fork);
     for (size_t g = 0; ok && g + 1 < PH_MAX_GROUPS; g++)
         ok = pgpu_stream_create(&b->side[g]) && pgpu_event_create(&b->join[g]);
@@ -358,13 +362,14 @@ int phonon_flow_batch_create(const PhononFlowModel *model, PhononKvPool *pool,
     b->positions = pgpu_malloc(b->padded_streams * sizeof(int32_t));
     b->tables = pgpu_malloc(max_streams * b->table_len * sizeof(int32_t));
     b->status = pgpu_malloc(sizeof(int));
+    b->counters = pgpu_malloc(PH_MAX_LAUNCHES * sizeof(unsigned));
     b->scratch.part_acc = pgpu_malloc(slots * 64 * sizeof(float));
     b->scratch.part_ml = pgpu_malloc(slots * 2 * sizeof(float));
     b->scratch.max_streams = (int)max_streams;
     b->scratch.max_splits = (int)b->max_splits;
     b->host_positions = calloc(max_streams, sizeof(size_t));
     ok = ok && b->x && b->r && b->q && b->in && b->out && b->rows && b->xh && b->positions &&
-         b->tables && b->status && b->scratch.part_acc && b->scratch.part_ml &&
+         b->tables && b->status && b->counters && b->scratch.part_acc && b->scratch.part_ml &&
          b->host_positions;
     /* Zero everything a kernel may read before writing (padding streams of the
      * split fragments, positions, status). */
@@ -510,6 +515,88 @@ static size_t group_bounds(const PhononFlowBatch *b, size_t *first, size_t *coun
     return groups;
 }
 
+/* One step as paired launches (streams in two groups A and B of whole
+ * 16-stream tiles): after the QKV of layer 0 for everyone and the attention
+ * of A's layer 0, every launch runs one group's attention beside the other
+ * group's projection chain (out, MLP, next QKV), alternating:
+ *   attention B(l) + chain A(l),  attention A(l+1) + chain B(l), ...
+ * so the latency-bound projections run under the HBM-bound attention.
+ * 2L + 2 launches per step; bit-identical to enqueue_group. */
+static int enqueue_pipelined(PhononFlowBatch *b, const float *input, float *output,
+                             const float *rope) {
+    const PhononFlowModel *m = b->model;
+    const size_t layers = m->layers, tiles = (b->streams + 15) / 16;
+    const size_t half = tiles / 2;
+    const size_t first[2] = {0, half * 16};
+    const size_t count[2] = {half * 16, b->streams - half * 16};
+    pgpu_pair_attention att[2];
+    pgpu_pair_chain ch[2];
+    for (int g = 0; g < 2; g++) {
+        const size_t s0 = first[g], n = count[g];
+        const size_t slot0 = s0 * PH_HEADS * b->splits;
+        const pgpu_attention_scratch sc = {b->scratch.part_acc + slot0 * 64,
+                                           b->scratch.part_ml + slot0 * 2, (int)n,
+                                           (int)b->splits};
+        att[g] = (pgpu_pair_attention){.q = b->q + s0 * PH_WIDTH,
+                                       .tables = b->tables + s0 * b->table_len,
+                                       .positions = b->positions + s0,
+                                       .streams = (int)n,
+                                       .scratch = sc};
+        ch[g] = (pgpu_pair_chain){.streams = (int)n,
+                                  .ln_epsilon = 1e-5f,
+                                  .r = b->r + s0 * PH_WIDTH,
+                                  .hidden = b->xh + (s0 / 16) * (PH_FFN / 32) * 1536,
+                                  .q_next = b->q + s0 * PH_WIDTH,
+                                  .tables = b->tables + s0 * b->table_len,
+                                  .positions = b->positions + s0,
+                                  .scratch = sc};
+    }
+    const size_t launches = 2 * layers + 2;
+    if (launches > PH_MAX_LAUNCHES || !pgpu_fill_u32(b->stream, b->counters, launches, 0))
+        return 0;
+    /* QKV of layer 0, all streams. */
+    const pgpu_gemm_input ln1 = {.ln_rows = input, .ln_weight = m->norms,
+                                 .ln_bias = m->norms + PH_WIDTH, .ln_epsilon = 1e-5f};
+    if (!pgpu_gemm_qkv(b->stream, &m->qkv[0], &ln1, (int)b->streams, &b->pool->kv, 0, b->tables,
+                       (int)b->table_len, b->positions, rope, b->q, b->status))
+        return 0;
+    size_t launch = 0;
+    att[0].layer = 0;
+    if (!pgpu_decode_pair(b->stream, &att[0], NULL, &b->pool->kv, (int)b->table_len, rope,
+                          b->counters + launch++, b->status))
+        return 0;
+    for (size_t l = 0; l < layers; l++) {
+        const float *norm = m->norms + l * 4 * PH_WIDTH;
+        const float *next_norm = l + 1 < layers ? m->norms + (l + 1) * 4 * PH_WIDTH : NULL;
+        for (int g = 0; g < 2; g++) {
+            const size_t s0 = first[g];
+            pgpu_pair_chain *c = &ch[g];
+            c->layer = (int)l;
+            c->out = &m->out[l];
+            c->mlp_in = &m->mlp_in[l];
+            c->mlp_out = &m->mlp_out[l];
+            c->qkv_next = next_norm ? &m->qkv[l + 1] : NULL;
+            c->norm2_weight = norm + 2 * PH_WIDTH;
+            c->norm2_bias = norm + 3 * PH_WIDTH;
+            c->norm1_next_weight = next_norm;
+            c->norm1_next_bias = next_norm ? next_norm + PH_WIDTH : NULL;
+            c->input = (l == 0 ? input : b->x) + s0 * PH_WIDTH;
+            c->output = (l + 1 == layers ? output : b->x) + s0 * PH_WIDTH;
+        }
+        /* attention B(l) beside chain A(l); then attention A(l+1) beside
+         * chain B(l) (the last chain B runs alone). */
+        att[1].layer = (int)l;
+        if (!pgpu_decode_pair(b->stream, &att[1], &ch[0], &b->pool->kv, (int)b->table_len, rope,
+                              b->counters + launch++, b->status))
+            return 0;
+        att[0].layer = (int)l + 1;
+        if (!pgpu_decode_pair(b->stream, l + 1 < layers ? &att[0] : NULL, &ch[1], &b->pool->kv,
+                              (int)b->table_len, rope, b->counters + launch++, b->status))
+            return 0;
+    }
+    return 1;
+}
+
 /* One step: each stream group runs all layers on its own HIP stream (forked
  * from and joined back into the batch stream), so one group's latency-bound
  * projections overlap another group's bandwidth-bound attention. */
@@ -519,6 +606,9 @@ static int enqueue_step(PhononFlowBatch *b, const float *input, float *output, f
     const size_t groups = group_bounds(b, first, count);
     if (!rope || !groups)
         return 0;
+    if (b->pipeline && groups == 1 && b->streams > 16)
+        return enqueue_pipelined(b, input, output, rope) &&
+               pgpu_advance_positions(b->stream, b->positions, (int)b->streams);
     if (groups > 1 && !pgpu_event_record(b->fork, b->stream))
         return 0;
     for (size_t g = 1; g < groups; g++)
@@ -596,6 +686,16 @@ int phonon_flow_batch_set_groups(PhononFlowBatch *b, size_t groups) {
     if (b->groups != groups) {
         drop_graphs(b);
         b->groups = groups;
+    }
+    return 1;
+}
+
+int phonon_flow_batch_set_pipeline(PhononFlowBatch *b, int enable) {
+    if (!b)
+        return 0;
+    if (b->pipeline != !!enable) {
+        drop_graphs(b);
+        b->pipeline = !!enable;
     }
     return 1;
 }

@@ -646,6 +646,54 @@ def test_batched_prefill_equals_single_steps(lib, syn, pkg):
     assert np.array_equal(np.stack(want).view(np.uint32), got.view(np.uint32))
 
 
+@pytest.mark.parametrize("streams", [17, 40, 64])
+def test_paired_launches_equal_single_phase_launches(lib, syn, pkg, streams):
+    """Paired launches (one group's attention beside the other group's
+    projection chain, device-wide barriers between chain phases) give the
+    same bits as one launch per kernel, over several steps with ragged
+    contexts, in graph replay and in direct launches."""
+    layers = 3
+    model = scaled_model(syn, 181, layers)
+    views = pkg.Views()
+    w = views.layers(model)
+    max_pos = 700
+    table_len = (max_pos + 15) // 16
+    blocks = streams * table_len
+    rng = np.random.default_rng(182)
+    lengths = rng.integers(0, 640, size=streams)
+    ctx = rng.standard_normal((2, layers, max_pos, 512)).astype(np.float32)
+    xs = rng.standard_normal((4, streams, 512)).astype(np.float32)
+    runs = []
+    for pipeline, graph in ((0, 1), (1, 1), (1, 0)):
+        bt = Batch(lib, w, layers, streams, max_pos, blocks)
+        assert lib.phonon_flow_batch_set_pipeline(bt.batch, pipeline)
+        assert lib.phonon_flow_batch_set_graph(bt.batch, graph)
+        ids = np.zeros(blocks, np.int32)
+        assert lib.phonon_kv_pool_alloc(bt.pool, blocks, i32p(ids))
+        tables = np.ascontiguousarray(
+            np.random.default_rng(183).permutation(ids).reshape(streams, table_len))
+        for s_i in range(streams):
+            if lengths[s_i]:
+                assert lib.phonon_kv_pool_write(bt.pool, i32p(tables[s_i]), table_len, 0,
+                                                int(lengths[s_i]), fp(ctx[0]), fp(ctx[1]),
+                                                max_pos)
+        pos = lengths.astype(np.uintp)
+        assert lib.phonon_flow_batch_set_streams(
+            bt.batch, streams, pos.ctypes.data_as(ctypes.POINTER(ctypes.c_size_t)),
+            i32p(tables), table_len)
+        outs = []
+        for step in range(xs.shape[0]):
+            y = np.zeros((streams, 512), np.float32)
+            assert lib.phonon_flow_batch_step(bt.batch, fp(np.ascontiguousarray(xs[step])),
+                                              10000.0, fp(y)), pkg.last_error(lib)
+            outs.append(y.view(np.uint32).copy())
+        runs.append(outs)
+        bt.close()
+    for other in runs[1:]:
+        for a, b in zip(runs[0], other):
+            assert np.array_equal(a, b)
+
+
 def test_unwritten_pool_slots_never_reach_the_output(lib, oracle, oracle_mod, syn, pkg):
     """Regression: slots past a stream's context inside its last block may
     hold anything (here NaN); attention must skip them, not weight them 0."""
