@@ -170,10 +170,11 @@ __device__ inline bool prologue_ln(const GemmArgs &a, int st, uint16_t *bsh) {
 
 // Merges the split-attention partials of 16 streams x 8 heads into LDS split
 // fragments: out = sum_j acc_j e^(m_j - M) / sum_j l_j e^(m_j - M), M = max m_j
-// (the normalisation after P.V of src/phonon_transformer.c:395-403, merged
-// over splits in split order), by a 1024-thread work-group: wave n merges
-// stream n, lane (h = j/8, part = j%8) dims [8 part, 8 part + 8) of head h.
-// Loads are issued in groups of splits so their latencies overlap.
+// (the normalisation after P.V of src/phonon_transformer.c:395-403), by a
+// 1024-thread work-group: wave n merges stream n, lane (h = j/8, part = j%8)
+// dims [8 part, 8 part + 8) of head h. Single pass in split order with a
+// running maximum (accumulators rescaled when it grows), so every load of a
+// group of 8 splits is issued at once: one memory round trip per 8 splits.
 __device__ inline bool prologue_attn(const GemmArgs &a, int st, uint16_t *bsh) {
     const int n = threadIdx.x >> 6, j = threadIdx.x & 63;
     const int h = j >> 3, part = j & 7;
@@ -187,37 +188,32 @@ __device__ inline bool prologue_attn(const GemmArgs &a, int st, uint16_t *bsh) {
         const int nsplit = min((count + kSplitKeys - 1) / kSplitKeys, a.max_splits);
         const size_t first = ((size_t)s * kHeads + h) * a.max_splits;
         const float2 *ml = (const float2 *)a.part_ml + first;
-        float mx = -INFINITY;
+        float mx = -INFINITY, total = 0.0f;
         for (int j0 = 0; j0 < nsplit; j0 += 8) {
-            float m8[8];
+            float2 ml8[8];
+            float4 acc[8][2];
 #pragma unroll
-            for (int u = 0; u < 8; u++) m8[u] = j0 + u < nsplit ? ml[j0 + u].x : -INFINITY;
-#pragma unroll
-            for (int u = 0; u < 8; u++) mx = fmaxf(mx, m8[u]);
-        }
-        float total = 0.0f;
-        for (int j0 = 0; j0 < nsplit; j0 += 4) {
-            float2 ml4[4];
-            float4 acc[4][2];
-#pragma unroll
-            for (int u = 0; u < 4; u++) {
+            for (int u = 0; u < 8; u++) {
                 const int js = min(j0 + u, nsplit - 1);
-                ml4[u] = ml[js];
+                ml8[u] = ml[js];
                 const float4 *src = (const float4 *)(a.part_acc + (first + js) * 64 + part * 8);
                 acc[u][0] = src[0];
                 acc[u][1] = src[1];
             }
 #pragma unroll
-            for (int u = 0; u < 4; u++) {
+            for (int u = 0; u < 8; u++) {
                 if (j0 + u >= nsplit) break;
-                const float f = expf(ml4[u].x - mx);
-                total = fmaf(ml4[u].y, f, total);
+                const float m_new = fmaxf(mx, ml8[u].x);
+                const float keep = expf(mx - m_new);  // 0 for the first split
+                const float f = expf(ml8[u].x - m_new);
+                mx = m_new;
+                total = fmaf(ml8[u].y, f, total * keep);
 #pragma unroll
                 for (int i = 0; i < 2; i++) {
-                    v[4 * i] = fmaf(acc[u][i].x, f, v[4 * i]);
-                    v[4 * i + 1] = fmaf(acc[u][i].y, f, v[4 * i + 1]);
-                    v[4 * i + 2] = fmaf(acc[u][i].z, f, v[4 * i + 2]);
-                    v[4 * i + 3] = fmaf(acc[u][i].w, f, v[4 * i + 3]);
+                    v[4 * i] = fmaf(acc[u][i].x, f, v[4 * i] * keep);
+                    v[4 * i + 1] = fmaf(acc[u][i].y, f, v[4 * i + 1] * keep);
+                    v[4 * i + 2] = fmaf(acc[u][i].z, f, v[4 * i + 2] * keep);
+                    v[4 * i + 3] = fmaf(acc[u][i].w, f, v[4 * i + 3] * keep);
                 }
             }
         }

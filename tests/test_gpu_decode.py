@@ -392,6 +392,49 @@ def test_batch_ragged_shuffled_vs_oracle(lib, oracle, oracle_mod, syn, pkg):
     bt.close()
 
 
+@pytest.mark.parametrize("streams, layers, lo, hi", [(64, 12, 1, 2048), (256, 2, 256, 8192)])
+def test_batch_full_size_vs_oracle(lib, oracle, oracle_mod, syn, pkg, streams, layers, lo, hi):
+    """The batched step at the benchmark shapes (B=64 x 12 layers, contexts
+    U{1..2048}; B=256, contexts U{256..8192}) against the oracle's stack step
+    for every stream. Every stream attends its own shuffled copy of the same
+    context rows (one host array), so the check stays small on the host."""
+    model = scaled_model(syn, 191, layers)
+    om = oracle_for(oracle, oracle_mod, model)
+    views = pkg.Views()
+    w = views.layers(model)
+    rng = np.random.default_rng(192)
+    lengths = rng.integers(lo, hi + 1, size=streams) - 1   # positions; keys = lengths + 1
+    max_pos = int(lengths.max()) + 1
+    table_len = (max_pos + 15) // 16
+    blocks = streams * table_len
+    keys = rng.standard_normal((layers, max_pos, 512)).astype(np.float32)
+    vals = rng.standard_normal((layers, max_pos, 512)).astype(np.float32)
+    bt = Batch(lib, w, layers, streams, max_pos, blocks)
+    ids = np.zeros(blocks, np.int32)
+    assert lib.phonon_kv_pool_alloc(bt.pool, blocks, i32p(ids))
+    tables = np.ascontiguousarray(rng.permutation(ids).reshape(streams, table_len))
+    for s in range(streams):
+        if lengths[s]:
+            assert lib.phonon_kv_pool_write(bt.pool, i32p(tables[s]), table_len, 0,
+                                            int(lengths[s]), fp(keys), fp(vals), max_pos)
+    pos = lengths.astype(np.uintp)
+    assert lib.phonon_flow_batch_set_streams(
+        bt.batch, streams, pos.ctypes.data_as(ctypes.POINTER(ctypes.c_size_t)), i32p(tables),
+        table_len)
+    x = rng.standard_normal((streams, 512)).astype(np.float32)
+    y = np.zeros_like(x)
+    assert lib.phonon_flow_batch_step(bt.batch, fp(x), 10000.0, fp(y)), pkg.last_error(lib)
+    bt.close()
+    for s in range(streams):
+        p = int(lengths[s])
+        row_k, row_v = keys[:, p].copy(), vals[:, p].copy()   # the oracle appends at p
+        ok, ref = om.stack_step(keys, vals, max_pos, p, x[s])
+        keys[:, p], vals[:, p] = row_k, row_v
+        assert ok
+        err = helpers.normwise(y[s], ref)
+        assert err <= TOL, (s, int(lengths[s]), err)
+
+
 def test_batch_block_placement_does_not_change_bits(lib, syn, pkg):
     """Same contexts through identity vs shuffled block tables: outputs and
     appended rows are bit-identical (block indexing is pure addressing)."""
