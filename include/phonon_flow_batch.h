@@ -103,14 +103,30 @@ int phonon_flow_batch_prefill_device(PhononFlowBatch *batch, size_t streams, con
  * depend on it. Default 1: on MI355X under ROCm 7 kernels of different HIP
  * streams were measured not to overlap, so more groups only add launches. */
 int phonon_flow_batch_set_groups(PhononFlowBatch *batch, size_t groups);
-/* enable = 1: a batch of more than 16 streams runs each step as paired
- * launches, one stream group's attention beside the other group's
- * projections (device-wide barriers between the projection phases);
- * 0 (default): one launch per kernel of each layer. Results are identical.
- * On MI355X the paired form is slower at B=64 (1240 vs 875 us per step): a
- * kernel's register budget is that of its largest role, so its 1024-thread
- * work-groups run one per CU, and each chain barrier costs 5-6 us. */
-int phonon_flow_batch_set_pipeline(PhononFlowBatch *batch, int enable);
+/* mode 2: each step (and batched prefill) is one launch holding every
+ * layer's work as a dataflow graph of work-group tasks (pgpu_flow_launch):
+ * one 16-stream tile's projections run while other tiles' attention
+ * streams K/V, and no launch boundary separates the phases. mode 0: one
+ * launch per phase of each layer. mode 1 (default): one launch for the
+ * decode batch sizes where that measured faster on MI355X (33..96 streams),
+ * phase by phase otherwise. Results are identical (both run the same task
+ * code). Batches over 4096 streams, models over 63 layers and models mixing
+ * Q8 and BF16 matrices always run phase by phase. */
+int phonon_flow_batch_set_pipeline(PhononFlowBatch *batch, int mode);
+/* Placement of the projection chains in the one-launch step's task list
+ * (pgpu_flow_placement); NULL restores the default. Results do not depend
+ * on it. */
+int phonon_flow_batch_set_placement(PhononFlowBatch *batch, const pgpu_flow_placement *place);
+/* Task timeline of the one-launch step: while set, every step whose task
+ * list fits `capacity` tasks writes, for task i, trace[3i .. 3i+2] = start,
+ * inputs ready, end on the GPU's constant 100 MHz clock (trace: dev,
+ * 3 * capacity words). NULL, 0 turns it off. */
+int phonon_flow_batch_set_trace(PhononFlowBatch *batch, uint64_t *trace, size_t capacity);
+/* The one-launch step's current task list (pgpu_flow_schedule order):
+ * returns the task count, and copies it when capacity suffices; 0 before the
+ * first one-launch step. */
+size_t phonon_flow_batch_schedule(const PhononFlowBatch *batch, uint32_t *schedule,
+                                  size_t capacity);
 /* use_graph = 1 (default): step_device replays a captured HIP graph;
  * 0: it launches the step's kernels directly (e.g. for a caller that is
  * itself capturing a graph). Results are identical. */

@@ -110,41 +110,99 @@ int pgpu_gemm_qkv(void *stream, const pgpu_matrix *w, const pgpu_gemm_input *x, 
                   const pgpu_paged_kv *kv, int layer, const int32_t *tables, int table_stride,
                   const int32_t *positions, const float *rope, float *q_out, int *status);
 
-/* -- paired decode launch (pgpu_gemm.hip) --
- * One launch holding the split attention of one stream group and, beside
- * it, the projection chain of another group whose attention has finished:
- * out projection + residual, LayerNorm 2 + MLP in + GELU, MLP out +
- * residual, then LayerNorm 1 + QKV + RoPE + KV append of the next layer.
- * Results are bit-identical to the single-phase launches. Pointers are at
- * the group's first stream (tile-aligned); streams are counted from there. */
-typedef struct {
-    const float *q;                     /* (dev) [streams][512] */
-    const int32_t *tables, *positions;  /* (dev) */
-    int streams, layer;
-    pgpu_attention_scratch scratch;     /* max_splits: the launch's split count */
-} pgpu_pair_attention;
+/* -- one-launch decode step (pgpu_flow.hip) --
+ * A whole decode step of B streams (all layers) in one launch: every
+ * work-group runs one task of the step, named by its descriptor in
+ * `schedule`, and first waits (on counters in device memory) for the tasks
+ * whose outputs it reads. Tasks, per 16-stream tile t and layer l:
+ *   QKV    LayerNorm 1 + QKV projection + RoPE + K/V append, 64 rows each
+ *   ATTN   one 256-key split of one (stream, head); the last split of a
+ *          (stream, head) to finish merges all its splits
+ *   OUT    out projection + residual, 64 rows each
+ *   MLP_IN LayerNorm 2 + MLP in projection + GELU, 64 rows each
+ *   MLP_OUT MLP out projection + residual, 16 rows each
+ * Descriptor (PGPU_FLOW_TASK) bits: kind [0,3), layer [3,9), tile [9,17),
+ * index [17,32); an
+ * ATTN index is head | split << 3 | (stream in tile) << 11. A schedule must
+ * list every task of the step once, each after every task it depends on
+ * (then the launch cannot deadlock); ATTN tasks of (stream, head) must cover
+ * the splits of its context. Status bit 4: a wait timed out (1 s), the
+ * step's results are then unspecified. */
+#define PGPU_FLOW_QKV 0
+#define PGPU_FLOW_ATTN 1
+#define PGPU_FLOW_OUT 2
+#define PGPU_FLOW_MLP_IN 3
+#define PGPU_FLOW_MLP_OUT 4
+#define PGPU_FLOW_QKV_ALL 5        /* counter only (tile 0): QKV tasks of all tiles */
+#define PGPU_FLOW_KINDS 6
+#define PGPU_FLOW_QKV_TASKS 24     /* per tile and layer */
+#define PGPU_FLOW_OUT_TASKS 8
+#define PGPU_FLOW_MLP_IN_TASKS 32
+#define PGPU_FLOW_MLP_OUT_TASKS 32
+#define PGPU_FLOW_COUNTER_STRIDE 16 /* 32-bit words between phase counters */
+
+#define PGPU_FLOW_TASK(kind, layer, tile, index)                                      \
+    ((uint32_t)(kind) | (uint32_t)(layer) << 3 | (uint32_t)(tile) << 9 |             \
+     (uint32_t)(index) << 17)
 
 typedef struct {
-    int streams, layer;                 /* the layer whose attention has finished */
-    const pgpu_matrix *out, *mlp_in, *mlp_out;
-    const pgpu_matrix *qkv_next;        /* NULL on the last layer */
-    const float *norm2_weight, *norm2_bias;       /* (dev) [512] */
-    const float *norm1_next_weight, *norm1_next_bias;
-    float ln_epsilon;
-    const float *input;                 /* (dev) layer input rows (residual) */
-    float *r;                           /* (dev) out projection + residual rows */
-    uint16_t *hidden;                   /* (dev) MLP hidden, split fragments */
-    float *output;                      /* (dev) layer output rows */
-    float *q_next;                      /* (dev) next layer's q rows */
-    const int32_t *tables, *positions;  /* (dev) */
-    pgpu_attention_scratch scratch;     /* the partials of `layer` */
-} pgpu_pair_chain;
+    const void *values[4];      /* (dev) qkv, out, mlp_in, mlp_out fragments */
+    const uint16_t *scales[4];  /* (dev) their Q8 scale planes (NULL: bf16) */
+    const float *norms;         /* (dev) [4][512]: norm1 w, b, norm2 w, b */
+} pgpu_flow_layer;
 
-/* Either part may be NULL (not both). `counter` (dev) must be 0 at launch
- * and is used by this launch only. Status bit 4: a chain barrier timed out. */
-int pgpu_decode_pair(void *stream, const pgpu_pair_attention *attention,
-                     const pgpu_pair_chain *chain, const pgpu_paged_kv *kv, int table_stride,
-                     const float *rope, unsigned *counter, int *status);
+typedef struct {
+    const pgpu_flow_layer *layers; /* (dev) [layer_count] */
+    int layer_count, q8, streams, tiles, prefill;
+    int pool_offset;               /* pool layer of model layer 0 */
+    const float *input;            /* (dev) [streams][512] layer-0 input */
+    float *output;                 /* (dev) [streams][512] last layer's output */
+    float *act;                    /* (dev) [layer_count][4][tiles*16][512]: x, r, q, attn */
+    uint16_t *hidden;              /* (dev) [layer_count][tiles][64*1536] split fragments */
+    float *part_acc;               /* (dev) [layer_count][tiles*16][8][max_splits][64] */
+    float *part_ml;                /* (dev) [layer_count][tiles*16][8][ml_group] */
+    int max_splits, ml_group;      /* ml_group: floats per (max, sum) group, % 32 == 0 */
+    const int32_t *tables, *positions; /* (dev) */
+    int table_stride;
+    const float *rope;             /* (dev) [8192][32] (cos, sin) */
+    const uint32_t *schedule;      /* (dev) one descriptor per work-group */
+    unsigned tasks;
+    unsigned *phase;               /* (dev) [layer_count][tiles][KINDS] x COUNTER_STRIDE, 0 */
+    unsigned *split_done;          /* (dev) [layer_count][tiles*16][8], 0 */
+    int *status;
+    uint64_t *trace;               /* (dev) NULL, or [tasks][3]: start, inputs ready, end
+                                      (constant 100 MHz clock) of each task */
+} pgpu_flow_step;
+
+/* Placement of each tile's projection chain in a task list, on a model
+ * clock where every attention split task takes unit_us: the tile's OUT,
+ * MLP_IN, MLP_OUT and next-layer QKV tasks are listed after_us[0..3] after
+ * its last attention task (non-decreasing; a tile's next attention always
+ * waits for its QKV). All zero: each chain right behind its attention. */
+typedef struct {
+    float unit_us;
+    float after_us[4];
+} pgpu_flow_placement;
+
+/* The task list of a step of `streams` streams through `layers` layers,
+ * where stream s lists splits[s] attention splits per head (its context's
+ * splits, plus any headroom: splits past the live context end at once).
+ * Returns the task count; writes the descriptors when `schedule` holds at
+ * least that many (`capacity`). Order: QKV of layer 0 for every tile; then
+ * for each layer l and tile t, ATTN(t, l) by (stream, split, head) with
+ * heads fastest, with the chains OUT, MLP_IN, MLP_OUT (l) and QKV (l+1) of
+ * earlier tiles interleaved as `place` (NULL: all zero) sets. Every task
+ * follows the tasks it waits for; prefill = 1 lists all QKV of a layer
+ * before its first ATTN (and ignores `place`). Host code only. */
+size_t pgpu_flow_schedule(size_t streams, size_t layers, const size_t *splits,
+                          const pgpu_flow_placement *place, int prefill, uint32_t *schedule,
+                          size_t capacity);
+/* prefill = 1: pseudo-streams of one stream share its block table, so an
+ * ATTN task waits for the QKV tasks of every tile (one layer-wide count). */
+int pgpu_flow_launch(void *stream, const pgpu_flow_step *step, const pgpu_paged_kv *kv);
+/* After a step: zero `n` counter words and advance positions[0..streams). */
+int pgpu_flow_finish(void *stream, unsigned *counters, size_t n, int32_t *positions,
+                     int streams);
 /* Fills n 32-bit words with `value` (a kernel: usable inside a captured graph). */
 int pgpu_fill_u32(void *stream, uint32_t *dst, size_t n, uint32_t value);
 

@@ -146,6 +146,9 @@ EXPORTS = {
     "phonon_flow_batch_step": (_i, [_vp, _fp, _f, _fp]),
     "phonon_flow_batch_step_device": (_i, [_vp, _vp, _f, _vp]),
     "phonon_flow_batch_set_pipeline": (_i, [_vp, _i]),
+    "phonon_flow_batch_set_trace": (_i, [_vp, _vp, _sz]),
+    "phonon_flow_batch_set_placement": (_i, [_vp, _vp]),
+    "phonon_flow_batch_schedule": (_sz, [_vp, ctypes.POINTER(ctypes.c_uint32), _sz]),
     "phonon_flow_batch_prefill_device": (_i, [_vp, _sz, _vp, _vp, _vp, _sz, _vp, _f, _vp]),
     "phonon_flow_batch_sync": (_i, [_vp]),
     "phonon_flow_batch_set_groups": (_i, [_vp, _sz]),
@@ -196,7 +199,10 @@ EXPORTS = {
     "pgpu_advance_positions": (_i, [_vp, _vp, _i]),
     "pgpu_gather_rows": (_i, [_vp, _vp, _vp, _vp, _i, _i]),
     "pgpu_fill_u32": (_i, [_vp, _vp, _sz, ctypes.c_uint32]),
-    "pgpu_decode_pair": (_i, [_vp, _vp, _vp, _kvp, _i, _vp, _vp, _vp]),
+    "pgpu_flow_schedule": (_sz, [_sz, _sz, _szp, _vp, _i, ctypes.POINTER(ctypes.c_uint32),
+                                 _sz]),
+    "pgpu_flow_launch": (_i, [_vp, _vp, _kvp]),
+    "pgpu_flow_finish": (_i, [_vp, _vp, _sz, _vp, _i]),
 }
 
 _LIB = None
@@ -274,6 +280,11 @@ class Views:
             arr[i] = PhononFlowLayerWeights(*[ctypes.pointer(v) for v in views])
         self.keep.append(arr)
         return arr
+
+
+class PgpuFlowPlacement(ctypes.Structure):
+    """pgpu_flow_placement (phonon_gpu.h)."""
+    _fields_ = [("unit_us", ctypes.c_float), ("after_us", ctypes.c_float * 4)]
 
 
 class DeviceBuffer:

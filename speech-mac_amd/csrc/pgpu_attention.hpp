@@ -1,5 +1,5 @@
 // Split-attention unit shared by the attention kernels (pgpu_attention.hip)
-// and the paired decode kernel (pgpu_gemm.hip). See pgpu_attention.hip for
+// and the one-launch decode step (pgpu_flow.hip). See pgpu_attention.hip for
 // the pool layout and the work decomposition.
 #pragma once
 
@@ -47,10 +47,21 @@ struct AttnShared {
 // Split `split` of head `head` of stream `s`, by the unit's 8 waves (`wave`
 // = 0..7 within the unit). Every wave of the work-group must call it (it
 // holds one work-group barrier); a unit without live keys (or that does not
-// `exist`: past the end of a grid) only takes part in the barrier. Writes
-// the split's (max, sum, unnormalised P.V) partial.
-__device__ inline void attend_split(const AttnArgs &a, int head, int split, int s, int wave,
-                                    AttnShared &sh, bool exists = true) {
+// `exist`: past the end of a grid) only takes part in the barrier. Returns
+// whether the unit had keys; if so, lanes 0..15 of wave 0 hold the split's
+// partial: max score mm, sum of exp ll and the unnormalised P.V dims
+// [4 lane, 4 lane + 4) in aa.
+//
+// `ready()` is called by every wave before the unit reads anything written
+// in the current step (the one-launch step waits there for the QKV tasks).
+struct NoBarrier {
+    __device__ void operator()() const {}
+};
+
+template <class Ready = NoBarrier>
+__device__ inline bool attend_unit(const AttnArgs &a, int head, int split, int s, int wave,
+                                   AttnShared &sh, bool exists, float4 &aa, float &mm,
+                                   float &ll, const Ready &ready = Ready{}) {
     const int lane = threadIdx.x & 63;
     const int krow = lane >> 4, dcol = lane & 15;
     const int count = exists ? a.positions[s] + 1 : 0;
@@ -64,18 +75,17 @@ __device__ inline void attend_split(const AttnArgs &a, int head, int split, int 
 
     float m = -INFINITY, l = 0.0f;
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (live) {
-        const float4 q = *(const float4 *)(a.q + (size_t)s * kWidth + head * kHeadDim + dcol * 4);
+    const int first_block = split * 16 + wave * kBlocksPerWave;
+    const int stream_blocks = (count + kBlockPos - 1) / kBlockPos;
+    // < first_block: this wave has no keys
+    const int last_block = min(first_block + kBlocksPerWave - 1, stream_blocks - 1);
+    float4 kr[kBlocksPerWave][4], vr[kBlocksPerWave][4];
+    // Block ids first (uniform), then every K/V load of the wave at once.
+    // Blocks past the context re-read the last valid block (their keys are
+    // masked below); an id outside the pool is flagged and replaced.
+    auto load_kv = [&]() {
         const int32_t *__restrict__ table = a.tables + (size_t)s * a.table_stride;
         const float *layer_kv = a.kv + (size_t)a.layer * a.layer_stride;
-        const int first_block = split * 16 + wave * kBlocksPerWave;
-        const int stream_blocks = (count + kBlockPos - 1) / kBlockPos;
-        // < first_block: this wave has no keys
-        const int last_block = min(first_block + kBlocksPerWave - 1, stream_blocks - 1);
-
-        // Block ids first (uniform), then every K/V load of the wave at once.
-        // Blocks past the context re-read the last valid block (their keys
-        // are masked below); an id outside the pool is flagged and replaced.
         int ids[kBlocksPerWave];
         bool bad_block = false;
 #pragma unroll
@@ -85,7 +95,6 @@ __device__ inline void attend_split(const AttnArgs &a, int head, int split, int 
             bad_block |= (unsigned)id >= a.blocks;
             ids[t] = (unsigned)id < a.blocks ? id : 0;
         }
-        float4 kr[kBlocksPerWave][4], vr[kBlocksPerWave][4];
         if (last_block >= first_block) {
 #pragma unroll
             for (int t = 0; t < kBlocksPerWave; t++) {
@@ -107,6 +116,11 @@ __device__ inline void attend_split(const AttnArgs &a, int head, int split, int 
                 }
         }
         if (bad_block && lane == 0) atomicOr(a.status, 2);
+    };
+    ready();
+    if (live) {
+        load_kv();
+        const float4 q = *(const float4 *)(a.q + (size_t)s * kWidth + head * kHeadDim + dcol * 4);
 
         float score[kBlocksPerWave][4];
 #pragma unroll
@@ -157,14 +171,14 @@ __device__ inline void attend_split(const AttnArgs &a, int head, int split, int 
         }
     }
     __syncthreads();
-    if (!live || wave != 0 || lane >= 16) return;
+    if (!live || wave != 0 || lane >= 16) return live;
 
     // Merge the unit's waves (fixed order). A wave without keys has l = 0.
-    float mm = sh.m[0];
+    mm = sh.m[0];
 #pragma unroll
     for (int w = 1; w < kUnitWaves; w++) mm = fmaxf(mm, sh.m[w]);
-    float ll = 0.0f;
-    float4 aa = make_float4(0.f, 0.f, 0.f, 0.f);
+    ll = 0.0f;
+    aa = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
     for (int w = 0; w < kUnitWaves; w++) {
         if (sh.l[w] == 0.0f) continue;
@@ -176,6 +190,18 @@ __device__ inline void attend_split(const AttnArgs &a, int head, int split, int 
         aa.z = fmaf(x.z, f, aa.z);
         aa.w = fmaf(x.w, f, aa.w);
     }
+    return true;
+}
+
+// attend_unit, then the split's (max, sum, unnormalised P.V) partial into
+// the pgpu_attention_scratch layout.
+__device__ inline void attend_split(const AttnArgs &a, int head, int split, int s, int wave,
+                                    AttnShared &sh, bool exists = true) {
+    float4 aa;
+    float mm, ll;
+    const bool live = attend_unit(a, head, split, s, wave, sh, exists, aa, mm, ll);
+    const int lane = threadIdx.x & 63;
+    if (!live || wave != 0 || lane >= 16) return;
     const size_t slot = ((size_t)s * kHeads + head) * a.max_splits + split;
     *(float4 *)(a.part_acc + slot * 64 + lane * 4) = aa;
     if (lane == 0) *(float2 *)(a.part_ml + slot * 2) = make_float2(mm, ll);

@@ -1,0 +1,362 @@
+// One-launch decode step: every layer of a batched decode step
+// (phonon_flow_stack_step, src/phonon_transformer.c:455-482, for B streams)
+// in a single kernel launch, as a dataflow graph of work-group tasks.
+//
+// Why: a step is 5 dependent phases per layer. Run as one launch per phase,
+// every phase boundary drains and refills the whole GPU, and the
+// latency-bound projections (~1-3 MB of weights) serialise with the
+// HBM-bound attention (~270 MB of K/V per layer at B=64). Here the phases
+// are per 16-stream tile: tile t's projection chain (out, MLP, next QKV)
+// runs while other tiles' attention streams K/V, and no launch gap separates
+// the phases.
+//
+// Scheduling. Work-group i runs the task of schedule[i] (pgpu_flow_task).
+// The host lists the tasks so that every task comes after the tasks it
+// depends on. Work-groups are dispatched in index order, so the
+// lowest-numbered unfinished task always has its inputs done and is running
+// or about to be dispatched: the launch cannot deadlock. A task that
+// starts before its inputs are ready waits (one lane polls a counter) while
+// holding its slot.
+//
+// Synchronisation without cache maintenance. Each XCD has its own L2, and
+// an agent-scope fence writes back or invalidates a whole L2. Instead:
+//  - every value a task writes for another task is stored write-through at
+//    device scope (global_store ... sc1: pgpu_gemm.hpp store_wt), and the
+//    storing waves drain vmcnt before the task's counter is incremented;
+//  - every such value lives at an address that no task reads before it is
+//    written within the launch (activations, partials and merged outputs
+//    have one buffer per layer; an appended K/V slot is read only by the
+//    attention of its own layer), so a consumer's plain load cannot hit a
+//    stale line in its L1 or L2: caches start the launch clean;
+//  - counters are atomics; a waiting lane polls with device-scope loads.
+// Read-only operands (weights, norms, positions, block tables, the RoPE
+// table, older K/V) are plain loads and stay cacheable.
+//
+// Every wait is bounded (1 s of the 100 MHz constant clock): a task that
+// times out sets status bit 4, and every other waiter then stops waiting,
+// so the launch always ends.
+#include "pgpu_attention.hpp"
+#include "pgpu_gemm.hpp"
+#include "phonon_gpu.h"
+
+namespace pgpu {
+namespace {
+
+constexpr uint64_t kWaitTicks = 100000000ull;  // 1 s at 100 MHz
+
+__device__ inline unsigned *phase_counter(const pgpu_flow_step &f, int layer, int tile,
+                                          int kind) {
+    return f.phase + ((size_t)(layer * f.tiles + tile) * PGPU_FLOW_KINDS + kind) *
+                         PGPU_FLOW_COUNTER_STRIDE;
+}
+
+// Waits until each of `count` counters (stride `step` words) holds at least
+// `target`; one lane polls, then the work-group barrier releases the rest.
+struct FlowWait {
+    const unsigned *flag;
+    int count, step;
+    unsigned target;
+    int *status;
+    __device__ void operator()() const {
+        if (threadIdx.x == 0) {
+            const uint64_t t0 = wall_clock64();
+            for (int i = 0; i < count; i++) {
+                const unsigned *c = flag + (size_t)i * step;
+                while (__hip_atomic_load(c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
+                    if ((__hip_atomic_load(status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) &
+                         4) ||
+                        wall_clock64() - t0 > kWaitTicks) {
+                        atomicOr(status, 4);
+                        i = count;
+                        break;
+                    }
+                    __builtin_amdgcn_s_sleep(2);
+                }
+            }
+        }
+        __syncthreads();
+    }
+};
+
+__device__ inline FlowWait wait_for(const pgpu_flow_step &f, int layer, int tile, int kind,
+                                    unsigned target) {
+    return FlowWait{phase_counter(f, layer, tile, kind), 1, 0, target, f.status};
+}
+
+// Task timeline (optional): slot 0 = start, 1 = inputs ready, 2 = end.
+__device__ inline void trace_mark(const pgpu_flow_step &f, int slot) {
+    if (f.trace && threadIdx.x == 0) f.trace[(size_t)blockIdx.x * 3 + slot] = wall_clock64();
+}
+
+// Completes a task: every wave's write-through stores have drained, then
+// one lane counts the task (and, if given, a second counter).
+__device__ inline void flow_signal(const pgpu_flow_step &f, unsigned *flag,
+                                   unsigned *also = nullptr) {
+    __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        __hip_atomic_fetch_add(flag, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (also) __hip_atomic_fetch_add(also, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    trace_mark(f, 2);
+}
+
+// Wait functor that also records when the inputs were ready.
+struct TracedWait {
+    FlowWait w;
+    const pgpu_flow_step *f;
+    __device__ void operator()() const {
+        w();
+        trace_mark(*f, 1);
+    }
+};
+
+// Per-layer activation rows [tiles*16][512]: 0 = layer output x, 1 = r (out
+// projection + residual), 2 = q, 3 = merged attention output.
+__device__ inline float *act_rows(const pgpu_flow_step &f, int layer, int which) {
+    return f.act + ((size_t)layer * 4 + which) * (size_t)f.tiles * 16 * kWidth;
+}
+
+__device__ inline float *layer_output(const pgpu_flow_step &f, int layer) {
+    return layer + 1 == f.layer_count ? f.output : act_rows(f, layer, 0);
+}
+
+__device__ inline const float *layer_input(const pgpu_flow_step &f, int layer) {
+    return layer == 0 ? f.input : act_rows(f, layer - 1, 0);
+}
+
+__device__ inline uint16_t *hidden_rows(const pgpu_flow_step &f, int layer) {
+    return f.hidden + (size_t)layer * f.tiles * (kFfn / 32) * 1536;
+}
+
+__device__ inline GemmArgs base_args(const pgpu_flow_step &f, const pgpu_flow_layer &ly,
+                                     int which) {
+    GemmArgs a{};
+    a.w = ly.values[which];
+    a.wscale = ly.scales[which];
+    a.streams = f.streams;
+    a.status = f.status;
+    return a;
+}
+
+// ATTN task: split `split` of (stream t*16 + n, head). The split's partial
+// goes to the (layer, stream, head) group; the split that finds the others
+// done (its count reaches nsplit) merges them in split order into the
+// attention row, with the arithmetic of the single-phase merge.
+__device__ inline void attention_task(const pgpu_flow_step &f, const pgpu_paged_kv &kv,
+                                      int layer, int tile, int index, AttnShared &sh) {
+    const int head = index & 7, split = (index >> 3) & 255, n = index >> 11;
+    const int s = tile * 16 + n;
+    if (s >= f.streams) return;  // uniform
+    const int count = f.positions[s] + 1;
+    const int nsplit = (count + kSplitKeys - 1) / kSplitKeys;
+    const bool covered =
+        count >= 1 && nsplit <= f.max_splits && count <= f.table_stride * kBlockPos;
+    // Exactly one task per (stream, head) completes it: the last of its
+    // splits to finish, or split 0 when the context is not covered (the
+    // unit flags it; the row stays zero).
+    if (covered ? split >= nsplit : split != 0) return;
+    const TracedWait ready{
+        f.prefill
+            ? wait_for(f, layer, 0, PGPU_FLOW_QKV_ALL, (unsigned)(PGPU_FLOW_QKV_TASKS * f.tiles))
+            : wait_for(f, layer, tile, PGPU_FLOW_QKV, PGPU_FLOW_QKV_TASKS),
+        &f};
+
+    AttnArgs a;
+    a.q = act_rows(f, layer, 2);
+    a.kv = kv.base;
+    a.layer_stride = kv.layer_stride;
+    a.blocks = (unsigned)kv.blocks;
+    a.layer = layer + f.pool_offset;
+    a.tables = f.tables;
+    a.table_stride = f.table_stride;
+    a.positions = f.positions;
+    a.streams = f.streams;
+    a.max_splits = f.max_splits;
+    a.part_acc = nullptr;
+    a.part_ml = nullptr;
+    a.status = f.status;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    float4 aa;
+    float mm, ll;
+    attend_unit(a, head, split, s, wave, sh, true, aa, mm, ll, ready);
+    if (wave != 0) return;
+
+    const int lane = threadIdx.x & 63, d = (lane & 15) * 4;
+    const size_t group = ((size_t)layer * f.tiles * 16 + s) * kHeads + head;
+    float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    bool finish = !covered, bad = false;
+    if (covered && nsplit == 1) {
+        float mx = -INFINITY, total = 0.0f;
+        const float acc[4] = {aa.x, aa.y, aa.z, aa.w};
+        merge_step(mx, total, v, 4, mm, ll, acc);
+        bad = merge_finish<4>(total, v);
+        finish = true;
+    } else if (covered) {
+        float *acc = f.part_acc + group * f.max_splits * 64;
+        float *ml = f.part_ml + group * f.ml_group;
+        if (lane < 16) store_wt(acc + split * 64 + d, aa);
+        if (lane == 0) store_wt((float2 *)(ml + 2 * split), make_float2(mm, ll));
+        __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        unsigned done = 0;
+        if (lane == 0)
+            done = __hip_atomic_fetch_add(f.split_done + group, 1u, __ATOMIC_RELAXED,
+                                          __HIP_MEMORY_SCOPE_AGENT);
+        done = __shfl(done, 0);
+        if (done + 1 == (unsigned)nsplit) {
+            bad = merge_splits<4>(acc, ml, nsplit, d, v);
+            finish = true;
+        }
+    }
+    if (!finish) {
+        trace_mark(f, 2);
+        return;
+    }
+    if (lane < 16)
+        store_wt(act_rows(f, layer, 3) + (size_t)s * kWidth + head * kHeadDim + d,
+                 make_float4(v[0], v[1], v[2], v[3]));
+    flag_nonfinite(f.status, bad && lane < 16);
+    __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    if (lane == 0)
+        __hip_atomic_fetch_add(phase_counter(f, layer, tile, PGPU_FLOW_ATTN), 1u,
+                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    trace_mark(f, 2);
+}
+
+template <bool Q8>
+__device__ inline void flow_step_task(const pgpu_flow_step &f, const pgpu_paged_kv &kv,
+                                      uint4 *lds4) {
+    uint16_t *lds = (uint16_t *)lds4;
+    trace_mark(f, 0);
+    const uint32_t desc = f.schedule[blockIdx.x];
+    const int kind = desc & 7, layer = (desc >> 3) & 63, tile = (desc >> 9) & 255,
+              index = desc >> 17;
+    const pgpu_flow_layer &ly = f.layers[layer];
+    const float *norm = ly.norms;
+    const int live = min(16, f.streams - tile * 16);
+    switch (kind) {
+    case PGPU_FLOW_QKV: {
+        GemmArgs a = base_args(f, ly, 0);
+        a.ln_x = layer_input(f, layer);
+        a.ln_w = norm;
+        a.ln_b = norm + kWidth;
+        a.ln_eps = 1e-5f;
+        a.n_rows = 3 * kWidth;
+        a.k_cols = kWidth;
+        a.q_out = act_rows(f, layer, 2);
+        a.kv = kv.base;
+        a.layer_stride = kv.layer_stride;
+        a.blocks = (unsigned)kv.blocks;
+        a.layer = layer + f.pool_offset;
+        a.tables = f.tables;
+        a.table_stride = f.table_stride;
+        a.positions = f.positions;
+        a.rope = (const float2 *)f.rope;
+        const FlowWait w = layer == 0 ? FlowWait{nullptr, 0, 0, 0u, f.status}
+                                      : wait_for(f, layer - 1, tile, PGPU_FLOW_MLP_OUT,
+                                                 PGPU_FLOW_MLP_OUT_TASKS);
+        gemm_wide_task<SRC_LN, EPI_QKV, Q8>(a, index, tile, lds, TracedWait{w, &f});
+        flow_signal(f, phase_counter(f, layer, tile, PGPU_FLOW_QKV),
+                    f.prefill ? phase_counter(f, layer, 0, PGPU_FLOW_QKV_ALL) : nullptr);
+        break;
+    }
+    case PGPU_FLOW_ATTN:
+        attention_task(f, kv, layer, tile, index, *(AttnShared *)lds4);
+        break;
+    case PGPU_FLOW_OUT: {
+        GemmArgs a = base_args(f, ly, 1);
+        a.ln_x = act_rows(f, layer, 3);
+        a.n_rows = kWidth;
+        a.k_cols = kWidth;
+        a.out = act_rows(f, layer, 1);
+        a.ld_out = kWidth;
+        a.residual = layer_input(f, layer);
+        gemm_wide_task<SRC_ROWS, EPI_RESIDUAL, Q8>(
+            a, index, tile, lds,
+            TracedWait{wait_for(f, layer, tile, PGPU_FLOW_ATTN, (unsigned)(kHeads * live)), &f});
+        flow_signal(f, phase_counter(f, layer, tile, PGPU_FLOW_OUT));
+        break;
+    }
+    case PGPU_FLOW_MLP_IN: {
+        GemmArgs a = base_args(f, ly, 2);
+        a.ln_x = act_rows(f, layer, 1);
+        a.ln_w = norm + 2 * kWidth;
+        a.ln_b = norm + 3 * kWidth;
+        a.ln_eps = 1e-5f;
+        a.n_rows = kFfn;
+        a.k_cols = kWidth;
+        a.out_split = hidden_rows(f, layer);
+        a.out_kb = kFfn / 32;
+        gemm_wide_task<SRC_LN, EPI_GELU_SPLIT, Q8>(
+            a, index, tile, lds,
+            TracedWait{wait_for(f, layer, tile, PGPU_FLOW_OUT, PGPU_FLOW_OUT_TASKS), &f});
+        flow_signal(f, phase_counter(f, layer, tile, PGPU_FLOW_MLP_IN));
+        break;
+    }
+    case PGPU_FLOW_MLP_OUT: {
+        GemmArgs a = base_args(f, ly, 3);
+        a.xs = hidden_rows(f, layer);
+        a.n_rows = kWidth;
+        a.k_cols = kFfn;
+        a.out = layer_output(f, layer);
+        a.ld_out = kWidth;
+        a.residual = act_rows(f, layer, 1);
+        gemm_split_task<EPI_RESIDUAL, Q8>(
+            a, index, tile, lds,
+            TracedWait{wait_for(f, layer, tile, PGPU_FLOW_MLP_IN, PGPU_FLOW_MLP_IN_TASKS), &f});
+        flow_signal(f, phase_counter(f, layer, tile, PGPU_FLOW_MLP_OUT));
+        break;
+    }
+    default:
+        break;
+    }
+}
+
+// Two 512-thread work-groups per CU: the projection tasks' registers and
+// 49 KB of LDS (the prologue's operand buffer) set the occupancy.
+template <bool Q8>
+__global__ __launch_bounds__(kTaskThreads) void k_flow_step(pgpu_flow_step f, pgpu_paged_kv kv) {
+    __shared__ uint4 lds4[kTaskLds / 8];
+    flow_step_task<Q8>(f, kv, lds4);
+}
+
+__global__ void k_flow_finish(unsigned *counters, size_t n, int32_t *positions, int streams) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    for (size_t j = i; j < n; j += (size_t)gridDim.x * blockDim.x) counters[j] = 0u;
+    if (i < (size_t)streams) positions[i] += 1;
+}
+
+}  // namespace
+}  // namespace pgpu
+
+using namespace pgpu;
+
+extern "C" int pgpu_flow_launch(void *stream, const pgpu_flow_step *step,
+                                const pgpu_paged_kv *kv) {
+    if (!step || !kv || !step->layers || step->layer_count <= 0 || step->layer_count > 64 ||
+        step->streams <= 0 || step->tiles != (step->streams + 15) / 16 || step->tiles > 256 ||
+        !step->input || !step->output || !step->act || !step->hidden || !step->part_acc ||
+        !step->part_ml || step->max_splits <= 0 || step->max_splits > 255 ||
+        step->ml_group < 2 * step->max_splits || step->ml_group % 32 || !step->tables ||
+        !step->positions || step->table_stride <= 0 || !step->rope || !step->schedule ||
+        !step->tasks || !step->phase || !step->split_done || !step->status ||
+        step->pool_offset < 0 || step->pool_offset + step->layer_count > kv->layers)
+        return bad_arguments("pgpu_flow_launch");
+    if (step->q8)
+        hipLaunchKernelGGL(k_flow_step<true>, dim3(step->tasks), dim3(kTaskThreads), 0,
+                           (hipStream_t)stream, *step, *kv);
+    else
+        hipLaunchKernelGGL(k_flow_step<false>, dim3(step->tasks), dim3(kTaskThreads), 0,
+                           (hipStream_t)stream, *step, *kv);
+    return launch_ok("pgpu_flow_launch");
+}
+
+extern "C" int pgpu_flow_finish(void *stream, unsigned *counters, size_t n, int32_t *positions,
+                                int streams) {
+    if (!counters || !n || !positions || streams <= 0) return bad_arguments("pgpu_flow_finish");
+    const size_t work = n > (size_t)streams ? n : (size_t)streams;
+    const unsigned blocks = (unsigned)((work + 255) / 256 < 1024 ? (work + 255) / 256 : 1024);
+    hipLaunchKernelGGL(k_flow_finish, dim3(blocks), dim3(256), 0, (hipStream_t)stream, counters,
+                       n, positions, streams);
+    return launch_ok("pgpu_flow_finish");
+}

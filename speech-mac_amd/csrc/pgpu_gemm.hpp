@@ -1,0 +1,660 @@
+// Projection tasks of the decode step: Y[s][n] = sum_k X[s][k] * W[n][k] for
+// one 16-stream tile, on v_mfma_f32_16x16x32_bf16, with the producer of X
+// fused in front (prologue) and the consumer of Y behind (epilogue).
+//
+// A task is the work of one 512-thread (8-wave) work-group. The same task
+// code runs in the single-phase kernels (pgpu_gemm.hip, one task per
+// work-group) and in the one-launch decode step (pgpu_flow.hip, where a
+// task first waits for the tasks it depends on), so both produce the same
+// bits.
+//
+// Replaces the fp32 SGEMM of phonon_linear (src/phonon_transformer.c:253-313)
+// and the row dot of phonon_q8_matvec (src/phonon_q8.c:36-92); with its
+// prologues/epilogues it also carries LayerNorm (:153-185), the attention
+// output normalisation (:395-403), RoPE + KV append (:425-427), GELU
+// (:202-216) and the residual adds (:440-451) of phonon_flow_layer_step.
+//
+// Operands
+//   W  Q8_0: int8 values in MFMA A-fragment order, one 512-byte record per
+//      (16-row tile, 32-column block); lane l holds row l%16, columns
+//      8*(l/16) .. +7. The per-(row, block) fp16 scales sit in a separate
+//      plane [tile][block][16]. Bytes per weight: 1 + 2/32 (same as Q8_0).
+//   W  BF16: the same fragment order with bf16 values (1024-byte records).
+//   X  split fragments (pgpu_common.hpp): three bf16 terms per activation,
+//      read from global memory (SRC_SPLIT) or built in LDS by a prologue:
+//      SRC_LN   LayerNorm of fp32 rows [streams][512];
+//      SRC_ROWS fp32 rows [streams][512] as they are;
+//      SRC_ATTN merge of the split-attention partials (max, sum, acc).
+// Arithmetic
+//   Q8: per 32-column block, c = W_q8 . (X_hi + X_mid + X_lo) by three MFMAs
+//   from zero (int8 and bf16 terms multiply exactly), then acc += scale*c,
+//   i.e. the reference phonon_q8_dot order "sum += scale * partial".
+//   BF16: the three MFMAs chain straight into the accumulator.
+// Stores of task outputs are device-scope write-through (sc1), so a task on
+// another XCD that waits for this one reads them from memory; see
+// pgpu_flow.hip.
+#pragma once
+
+#include <hip/hip_fp16.h>
+
+#include "pgpu_common.hpp"
+
+namespace pgpu {
+
+enum Source { SRC_SPLIT = 0, SRC_LN = 1, SRC_ATTN = 2, SRC_ROWS = 3 };
+enum Epilogue { EPI_STORE = 0, EPI_RESIDUAL = 1, EPI_GELU_SPLIT = 2, EPI_QKV = 3 };
+
+constexpr int kTaskWaves = 8, kTaskThreads = 64 * kTaskWaves;
+
+struct GemmArgs {
+    const uint16_t *xs;       // SRC_SPLIT: split fragments, k_cols/32 blocks per row
+    const float *ln_x;        // SRC_LN / SRC_ROWS: [streams][512] rows
+    const float *ln_w, *ln_b; // SRC_LN: [512] affine
+    float ln_eps;
+    const float *part_acc;    // SRC_ATTN: [streams*8*max_splits][64]
+    const float *part_ml;     // SRC_ATTN: [streams*8*max_splits][2]
+    int max_splits;
+    const void *w;            // weight fragments
+    const uint16_t *wscale;   // Q8 only
+    int n_rows, k_cols, streams;
+    float *out;               // STORE / RESIDUAL: [streams][ld_out]
+    int ld_out;
+    const float *bias;        // STORE: optional [n_rows]
+    const float *residual;    // RESIDUAL: [streams][ld_out]
+    uint16_t *out_split;      // GELU_SPLIT: split fragments with out_kb blocks per row
+    int out_kb;
+    float *q_out;             // QKV: [streams][512]
+    float *kv;                // QKV: paged pool base
+    size_t layer_stride;      // floats per layer of the pool
+    unsigned blocks;          // QKV: blocks per layer of the pool
+    int layer;
+    const int32_t *tables;
+    int table_stride;
+    const int32_t *positions; // QKV and SRC_ATTN
+    const float2 *rope;       // [8192][32] (cos, sin)
+    int *status;
+};
+
+// ---------------------------------------------------------------------------
+// Device-scope write-through stores (global_store sc1): visible in memory to
+// every XCD once the wave's vmcnt drains.
+__device__ inline void store_wt(float *p, float4 v) {
+    const uint64_t lo = (uint64_t)fbits(v.x) | (uint64_t)fbits(v.y) << 32;
+    const uint64_t hi = (uint64_t)fbits(v.z) | (uint64_t)fbits(v.w) << 32;
+    __hip_atomic_store((uint64_t *)p, lo, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store((uint64_t *)p + 1, hi, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ inline void store_wt(float2 *p, float2 v) {
+    const uint64_t u = (uint64_t)fbits(v.x) | (uint64_t)fbits(v.y) << 32;
+    __hip_atomic_store((uint64_t *)p, u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ inline void store_wt(uint2 *p, uint2 v) {
+    const uint64_t u = (uint64_t)v.x | (uint64_t)v.y << 32;
+    __hip_atomic_store((uint64_t *)p, u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// 4 consecutive activations of stream s from column k (k % 4 == 0) as
+// split fragments: three 8-byte write-through stores.
+__device__ inline void store_split4_wt(uint16_t *__restrict__ xs, int s, int k, int kb_count,
+                                       const float *v) {
+    uint16_t h[4], m[4], l[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) split3(v[i], h[i], m[i], l[i]);
+    const size_t base = split_index(s, k, 0, kb_count);
+    store_wt((uint2 *)(xs + base), make_uint2(h[0] | (uint32_t)h[1] << 16, h[2] | (uint32_t)h[3] << 16));
+    store_wt((uint2 *)(xs + base + 512),
+             make_uint2(m[0] | (uint32_t)m[1] << 16, m[2] | (uint32_t)m[3] << 16));
+    store_wt((uint2 *)(xs + base + 1024),
+             make_uint2(l[0] | (uint32_t)l[1] << 16, l[2] | (uint32_t)l[3] << 16));
+}
+
+// ---------------------------------------------------------------------------
+__device__ inline bf16x8 q8_to_bf16(uint2 raw) {
+    typedef __attribute__((ext_vector_type(4))) uint32_t u32x4;
+    u32x4 packed;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const uint32_t word = i < 2 ? raw.x : raw.y;
+        const int shift = (i & 1) * 16;
+        const float f0 = (float)(int8_t)(word >> shift);
+        const float f1 = (float)(int8_t)(word >> (shift + 8));
+        packed[i] = (fbits(f0) >> 16) | (fbits(f1) & 0xffff0000u);
+    }
+    return __builtin_bit_cast(bf16x8, packed);
+}
+
+__device__ inline float half_to_float(uint32_t bits16) {
+    return __half2float(__ushort_as_half((unsigned short)bits16));
+}
+
+// LDS operand buffer of the prologues: for column block kb, three 1 KB
+// records (one per term) of 64 lanes x 8 bf16, in the MFMA B-operand order.
+// Consecutive blocks are kLdsBlock elements apart: the 16-byte pad puts the
+// 16 blocks one writer wave touches on distinct banks.
+constexpr int kLdsBlock = 1536 + 8;
+// LDS of a task: the prologue's operand buffer, reused for partial sums.
+constexpr int kTaskLds = 16 * kLdsBlock;
+
+// Writes 8 activations of stream n (0..15 in the tile), columns
+// [32kb + 8g, 32kb + 8g + 8), into the LDS operand buffer: one 16-byte
+// record per split term.
+__device__ inline void lds_store8(uint16_t *bsh, int n, int kb, int g, const float *v) {
+    uint16_t h[8], m[8], l[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) split3(v[i], h[i], m[i], l[i]);
+    uint16_t *rec = bsh + kb * kLdsBlock + (g * 16 + n) * 8;
+#pragma unroll
+    for (int p = 0; p < 3; p++) {
+        const uint16_t *src = p == 0 ? h : (p == 1 ? m : l);
+        uint4 q;
+        q.x = src[0] | (uint32_t)src[1] << 16;
+        q.y = src[2] | (uint32_t)src[3] << 16;
+        q.z = src[4] | (uint32_t)src[5] << 16;
+        q.w = src[6] | (uint32_t)src[7] << 16;
+        *(uint4 *)(rec + p * 512) = q;
+    }
+}
+
+// Sum over the 64 lanes of a wave; every lane gets the same bits.
+__device__ inline float wave_sum64(float v) {
+    v = row16_sum(v);
+    v += __shfl_xor(v, 16);
+    v += __shfl_xor(v, 32);
+    return v;
+}
+
+// ---------------------------------------------------------------------------
+// Prologues: 16 streams' 512-wide operand rows into LDS split fragments, by
+// the task's 8 waves; wave w takes streams 2w and 2w+1 of the tile, lane j
+// columns [8j, 8j+8) of each.
+
+// Operand rows of the wave's two streams (2w, 2w+1 of tile st): lane j
+// holds columns [8j, 8j+8); rows past `streams` read as zeros.
+struct Rows2 {
+    float v[2][8];
+    bool live[2];
+};
+
+__device__ inline void rows_load(Rows2 &r, const float *x, int streams, int st) {
+    const int wave = threadIdx.x >> 6, j = threadIdx.x & 63;
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+        const int s = st * 16 + 2 * wave + i;
+        r.live[i] = s < streams;  // uniform per wave
+        if (r.live[i]) {
+            const float4 x0 = *(const float4 *)(x + (size_t)s * kWidth + j * 8);
+            const float4 x1 = *(const float4 *)(x + (size_t)s * kWidth + j * 8 + 4);
+            r.v[i][0] = x0.x; r.v[i][1] = x0.y; r.v[i][2] = x0.z; r.v[i][3] = x0.w;
+            r.v[i][4] = x1.x; r.v[i][5] = x1.y; r.v[i][6] = x1.z; r.v[i][7] = x1.w;
+        } else {
+#pragma unroll
+            for (int k = 0; k < 8; k++) r.v[i][k] = 0.0f;
+        }
+    }
+}
+
+// LayerNorm of the loaded rows into the LDS operand buffer: two-pass fp32
+// moments per stream (one wave), then y = ((x - mean) * rstd) * w + b
+// unfused, as the reference writes it (src/phonon_transformer.c:179-183).
+// Returns true if a live output is not finite.
+__device__ inline bool rows_ln(Rows2 &r, const float *lw, const float *lb, float eps,
+                               uint16_t *bsh) {
+    const int wave = threadIdx.x >> 6, j = threadIdx.x & 63;
+    const float4 w0 = *(const float4 *)(lw + j * 8), w1 = *(const float4 *)(lw + j * 8 + 4);
+    const float4 b0 = *(const float4 *)(lb + j * 8), b1 = *(const float4 *)(lb + j * 8 + 4);
+    const float ws[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+    const float bs[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+    bool bad = false;
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+        float *u = r.v[i];
+        const float mean =
+            wave_sum64(((u[0] + u[1]) + (u[2] + u[3])) + ((u[4] + u[5]) + (u[6] + u[7]))) *
+            (1.0f / kWidth);
+        float q2[2] = {0.0f, 0.0f};
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const float c = __fsub_rn(u[k], mean);
+            q2[k & 1] = fmaf(c, c, q2[k & 1]);
+        }
+        const float var = wave_sum64(q2[0] + q2[1]) * (1.0f / kWidth);
+        const float rstd = 1.0f / sqrtf(var + eps);
+        bool bad_i = false;
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            u[k] = __fadd_rn(__fmul_rn(__fmul_rn(__fsub_rn(u[k], mean), rstd), ws[k]), bs[k]);
+            bad_i |= !isfinite(u[k]);
+            if (!r.live[i]) u[k] = 0.0f;
+        }
+        bad |= bad_i && r.live[i];
+        lds_store8(bsh, 2 * wave + i, j >> 2, j & 3, u);
+    }
+    return bad;
+}
+
+// The loaded rows as they are (the merged attention output).
+__device__ inline void rows_plain(const Rows2 &r, uint16_t *bsh) {
+    const int wave = threadIdx.x >> 6, j = threadIdx.x & 63;
+#pragma unroll
+    for (int i = 0; i < 2; i++) lds_store8(bsh, 2 * wave + i, j >> 2, j & 3, r.v[i]);
+}
+
+// Merge of one (stream, head)'s split partials:
+// out = sum_j acc_j e^(m_j - M) / sum_j l_j e^(m_j - M), M = max m_j (the
+// normalisation after P.V of src/phonon_transformer.c:395-403), as a single
+// pass in split order with a running maximum mx (the accumulators v are
+// rescaled when it grows). merge_step folds in split j; the per-dimension
+// arithmetic does not depend on how many dimensions a lane holds.
+__device__ inline void merge_step(float &mx, float &total, float *v, int n, float m_j, float l_j,
+                                  const float *acc_j) {
+    const float m_new = fmaxf(mx, m_j);
+    const float keep = expf(mx - m_new);  // 0 for the first split
+    const float f = expf(m_j - m_new);
+    mx = m_new;
+    total = fmaf(l_j, f, total * keep);
+    for (int i = 0; i < n; i++) v[i] = fmaf(acc_j[i], f, v[i] * keep);
+}
+
+// v /= total; returns true (and zeros) if the result is not finite or the
+// sum is not positive.
+template <int N>
+__device__ inline bool merge_finish(float total, float *v) {
+    bool bad = !(total > 0.0f) || !isfinite(total);
+    const float inv = 1.0f / total;
+#pragma unroll
+    for (int i = 0; i < N; i++) {
+        v[i] *= inv;
+        bad |= !isfinite(v[i]);
+    }
+    if (bad) {
+#pragma unroll
+        for (int i = 0; i < N; i++) v[i] = 0.0f;
+    }
+    return bad;
+}
+
+// All splits of one (stream, head), dims [dim0, dim0 + N): split j's acc row
+// is at acc + 64j, its (max, sum) at ml + 2j. Every load of a group of G
+// splits is issued at once (one memory round trip per G splits); the result
+// does not depend on G.
+template <int N, int G = 8>
+__device__ inline bool merge_splits(const float *acc, const float *ml, int nsplit, int dim0,
+                                    float *v) {
+#pragma unroll
+    for (int i = 0; i < N; i++) v[i] = 0.0f;
+    float mx = -INFINITY, total = 0.0f;
+    for (int j0 = 0; j0 < nsplit; j0 += G) {
+        float2 ml8[G];
+        float a8[G][N];
+#pragma unroll
+        for (int u = 0; u < G; u++) {
+            const int js = min(j0 + u, nsplit - 1);
+            ml8[u] = *(const float2 *)(ml + 2 * js);
+#pragma unroll
+            for (int k = 0; k < N / 4; k++) {
+                const float4 q = *(const float4 *)(acc + js * 64 + dim0 + 4 * k);
+                a8[u][4 * k] = q.x;
+                a8[u][4 * k + 1] = q.y;
+                a8[u][4 * k + 2] = q.z;
+                a8[u][4 * k + 3] = q.w;
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < G; u++) {
+            if (j0 + u >= nsplit) break;
+            merge_step(mx, total, v, N, ml8[u].x, ml8[u].y, a8[u]);
+        }
+    }
+    return merge_finish<N>(total, v);
+}
+
+// Merge of the split partials of 16 streams x 8 heads (layout of
+// pgpu_attention_scratch): wave w merges streams 2w, 2w+1; lane
+// (h = j/8, part = j%8) dims [8 part, 8 part + 8) of head h.
+__device__ inline bool prologue_attn(const GemmArgs &a, int st, uint16_t *bsh) {
+    const int wave = threadIdx.x >> 6, j = threadIdx.x & 63;
+    const int h = j >> 3, part = j & 7;
+    bool bad = false;
+#pragma unroll 1
+    for (int i = 0; i < 2; i++) {
+        const int n = 2 * wave + i, s = st * 16 + n;
+        float v[8];
+        if (s < a.streams) {
+            const int count = a.positions[s] + 1;
+            const int nsplit = min((count + kSplitKeys - 1) / kSplitKeys, a.max_splits);
+            const size_t first = ((size_t)s * kHeads + h) * a.max_splits;
+            bad |= merge_splits<8>(a.part_acc + first * 64, a.part_ml + first * 2, nsplit,
+                                   part * 8, v);
+        } else {
+#pragma unroll
+            for (int k = 0; k < 8; k++) v[k] = 0.0f;
+        }
+        // Column 64h + 8 part: block 2h + part/4, group part%4.
+        lds_store8(bsh, n, 2 * h + (part >> 2), part & 3, v);
+    }
+    return bad;
+}
+
+// ---------------------------------------------------------------------------
+// Weights of one lane: CH column blocks.
+template <bool Q8, int CH>
+struct WChunk;
+template <int CH>
+struct WChunk<true, CH> {
+    uint2 raw[CH], sc[CH];
+};
+template <int CH>
+struct WChunk<false, CH> {
+    bf16x8 w[CH];
+};
+
+// Blocks kb0 .. kb0+CH-1 of row tile `tile` (clamped to kb_end - 1).
+template <bool Q8, int CH>
+__device__ inline void load_weights(WChunk<Q8, CH> &c, const GemmArgs &a, int tile, int kbn,
+                                    int lane, int kb0, int kb_end) {
+#pragma unroll
+    for (int u = 0; u < CH; u++) {
+        const size_t kb = (size_t)min(kb0 + u, kb_end - 1);
+        if constexpr (Q8) {
+            c.raw[u] = *(const uint2 *)((const int8_t *)a.w + ((size_t)tile * kbn + kb) * 512 +
+                                        lane * 8);
+            c.sc[u] = *(const uint2 *)(a.wscale + ((size_t)tile * kbn + kb) * 16 +
+                                       (lane >> 4) * 4);
+        } else {
+            c.w[u] = *(const bf16x8 *)((const uint16_t *)a.w + ((size_t)tile * kbn + kb) * 512 +
+                                       lane * 8);
+        }
+    }
+}
+
+// acc += W_block . X_block for block u of a chunk; `used` false makes the
+// block contribute 0 (scale 0 / zero fragment) with no control flow.
+template <bool Q8, int CH>
+__device__ inline void mfma_block(f32x4 &acc, const WChunk<Q8, CH> &w, int u, const bf16x8 &xh,
+                                  const bf16x8 &xm, const bf16x8 &xl, bool used) {
+    if constexpr (Q8) {
+        const bf16x8 wa = q8_to_bf16(w.raw[u]);
+        f32x4 c = {0.0f, 0.0f, 0.0f, 0.0f};
+        c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wa, xh, c, 0, 0, 0);
+        c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wa, xm, c, 0, 0, 0);
+        c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wa, xl, c, 0, 0, 0);
+        const uint2 s = used ? w.sc[u] : make_uint2(0u, 0u);
+        acc[0] = fmaf(half_to_float(s.x & 0xffffu), c[0], acc[0]);
+        acc[1] = fmaf(half_to_float(s.x >> 16), c[1], acc[1]);
+        acc[2] = fmaf(half_to_float(s.y & 0xffffu), c[2], acc[2]);
+        acc[3] = fmaf(half_to_float(s.y >> 16), c[3], acc[3]);
+    } else {
+        const bf16x8 wa = used ? w.w[u] : bf16x8{};
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wa, xh, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wa, xm, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wa, xl, acc, 0, 0, 0);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Epilogue operands of one lane (rows row0..row0+3 of stream s).
+struct EpiOperands {
+    float4 add;          // STORE: bias, RESIDUAL: residual
+    bool has_add;
+    float2 cs0, cs1;     // QKV: (cos, sin) of the lane's two RoPE pairs
+    int pos, block;      // QKV: append position and its pool block
+    bool ok;             // QKV: position and block are valid
+};
+
+// Operands that no task of the step writes (bias, positions, block tables,
+// RoPE table): may be loaded before the task waits for its inputs.
+template <int EPI>
+__device__ inline void load_epilogue_static(EpiOperands &e, const GemmArgs &a, int s, int row0,
+                                            bool live) {
+    e.add = make_float4(0.f, 0.f, 0.f, 0.f);
+    e.has_add = false;
+    e.ok = false;
+    if (!live) return;
+    if constexpr (EPI == EPI_STORE) {
+        if (a.bias) {
+            e.add = *(const float4 *)(a.bias + row0);
+            e.has_add = true;
+        }
+    } else if constexpr (EPI == EPI_QKV) {
+        // Positions past the rope table or the block table, and block ids
+        // outside the pool, are errors: flagged, and nothing is written.
+        int pos = a.positions[s];
+        e.ok = pos >= 0 && pos < kMaxPositions && (pos >> 4) < a.table_stride;
+        e.block = 0;
+        if (e.ok) {
+            e.block = a.tables[(size_t)s * a.table_stride + (pos >> 4)];
+            e.ok = (unsigned)e.block < a.blocks;
+        }
+        if (!e.ok) pos = 0;
+        e.pos = pos;
+        const int d0 = (row0 & 511) & 63;
+        e.cs0 = a.rope[(size_t)pos * 32 + (d0 >> 1)];
+        e.cs1 = a.rope[(size_t)pos * 32 + (d0 >> 1) + 1];
+    }
+}
+
+// Operands produced by earlier tasks of the step (the residual rows): loaded
+// only after the task's wait.
+template <int EPI>
+__device__ inline void load_epilogue_dynamic(EpiOperands &e, const GemmArgs &a, int s, int row0,
+                                             bool live) {
+    if constexpr (EPI == EPI_RESIDUAL) {
+        if (live) {
+            e.add = *(const float4 *)(a.residual + (size_t)s * a.ld_out + row0);
+            e.has_add = true;
+        }
+    }
+}
+
+// Consumer of one lane's four results v (rows row0..row0+3 of stream s).
+// Returns true if a non-finite value was produced.
+template <int EPI>
+__device__ inline bool epilogue(const GemmArgs &a, const EpiOperands &e, const f32x4 &v, int s,
+                                int row0, bool live) {
+    bool bad = false;
+    if constexpr (EPI == EPI_STORE || EPI == EPI_RESIDUAL) {
+        if (live) {
+            float *o = a.out + (size_t)s * a.ld_out + row0;
+            const float add[4] = {e.add.x, e.add.y, e.add.z, e.add.w};
+            float y[4];
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                // bias + dot (STORE) or residual + dot (RESIDUAL); 0 + dot
+                // without a bias is exact.
+                y[r] = EPI == EPI_STORE ? (e.has_add ? __fadd_rn(v[r], add[r]) : v[r])
+                                        : __fadd_rn(add[r], v[r]);
+                bad |= !isfinite(y[r]);
+            }
+            store_wt(o, make_float4(y[0], y[1], y[2], y[3]));
+        }
+    } else if constexpr (EPI == EPI_GELU_SPLIT) {
+        if (live) {
+            float g[4];
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                g[r] = gelu_erf(v[r]);
+                bad |= !isfinite(g[r]);
+            }
+            store_split4_wt(a.out_split, s, row0, a.out_kb, g);
+        }
+    } else {  // EPI_QKV: rows [0,512) q, [512,1024) k, [1024,1536) v
+        if (live) {
+            const int part = row0 >> 9, rr = row0 & 511;
+            const int head = rr >> 6, d0 = rr & 63;
+            const bool ok = e.ok;
+            const int pos = e.pos, block = e.block;
+            if (!ok) atomicOr(a.status, 2);
+            float o[4] = {v[0], v[1], v[2], v[3]};
+            if (part < 2) {
+                // Interleaved pairs (d0, d0+1), (d0+2, d0+3): pair index d0/2.
+                const float2 cs0 = e.cs0, cs1 = e.cs1;
+                o[0] = __fsub_rn(__fmul_rn(v[0], cs0.x), __fmul_rn(v[1], cs0.y));
+                o[1] = __fadd_rn(__fmul_rn(v[0], cs0.y), __fmul_rn(v[1], cs0.x));
+                o[2] = __fsub_rn(__fmul_rn(v[2], cs1.x), __fmul_rn(v[3], cs1.y));
+                o[3] = __fadd_rn(__fmul_rn(v[2], cs1.y), __fmul_rn(v[3], cs1.x));
+            }
+#pragma unroll
+            for (int r = 0; r < 4; r++) bad |= !isfinite(o[r]);
+            if (part == 0) {
+                // The 1/sqrt(64) score scale is a power of two: folding it
+                // into q is exact.
+                store_wt(a.q_out + (size_t)s * kWidth + rr,
+                         make_float4(o[0] * 0.125f, o[1] * 0.125f, o[2] * 0.125f, o[3] * 0.125f));
+            } else if (ok) {
+                float *dst = a.kv + (size_t)a.layer * a.layer_stride +
+                             ((size_t)block * kHeads + head) * 2048 + (part - 1) * 1024 +
+                             (pos & 15) * 64 + d0;
+                store_wt(dst, make_float4(o[0], o[1], o[2], o[3]));
+            }
+        }
+    }
+    return bad;
+}
+
+// A task's wait for its inputs: NoWait in the single-phase kernels. Every
+// wait ends with a work-group barrier.
+struct NoWait {
+    __device__ void operator()() const { __syncthreads(); }
+};
+
+// ---------------------------------------------------------------------------
+// Operand built by a prologue (K = 512): 4 row tiles (64 rows) x 16
+// streams. The 8 waves each take (tile t = w%4, column half w/4): 8 blocks
+// of 3 MFMAs, and the halves are added in order through LDS. The wave's
+// weights and the epilogue's static operands are requested before the wait,
+// so their latency overlaps it and the prologue (a projection task is on the
+// step's latency-critical chain).
+template <int SRC, int EPI, bool Q8, class Wait>
+__device__ inline void gemm_wide_task(const GemmArgs &a, int bx, int st, uint16_t *bsh,
+                                      const Wait &wait) {
+    constexpr int kbn = kWidth / 32, KBW = kbn / 2;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    const int t = wave & 3, half = wave >> 2;
+    const int tile = bx * 4 + t;
+    const bool active = tile < (a.n_rows >> 4);  // uniform per wave
+    const int kb0 = half * KBW;
+    const int s = st * 16 + (lane & 15);
+    const bool live = s < a.streams;
+    const int row0 = tile * 16 + (lane >> 4) * 4;
+
+    WChunk<Q8, KBW> w;
+    if (active) load_weights(w, a, tile, kbn, lane, kb0, kb0 + KBW);
+    EpiOperands e;
+    if (active && half == 0) load_epilogue_static<EPI>(e, a, s, row0, live);
+    wait();
+    if (active && half == 0) load_epilogue_dynamic<EPI>(e, a, s, row0, live);
+
+    bool bad_in = false;
+    if constexpr (SRC == SRC_ATTN) {
+        bad_in = prologue_attn(a, st, bsh);
+    } else {
+        Rows2 r;
+        rows_load(r, a.ln_x, a.streams, st);
+        if constexpr (SRC == SRC_LN)
+            bad_in = rows_ln(r, a.ln_w, a.ln_b, a.ln_eps, bsh);
+        else
+            rows_plain(r, bsh);
+    }
+    flag_nonfinite(a.status, bad_in);
+    __syncthreads();
+
+    f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (active) {
+#pragma unroll
+        for (int c = 0; c < KBW / 4; c++) {
+            bf16x8 xh[4], xm[4], xl[4];
+            const uint16_t *xs = bsh + (kb0 + 4 * c) * kLdsBlock + lane * 8;
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                xh[u] = *(const bf16x8 *)(xs + u * kLdsBlock);
+                xm[u] = *(const bf16x8 *)(xs + u * kLdsBlock + 512);
+                xl[u] = *(const bf16x8 *)(xs + u * kLdsBlock + 1024);
+            }
+#pragma unroll
+            for (int u = 0; u < 4; u++) mfma_block(acc, w, 4 * c + u, xh[u], xm[u], xl[u], true);
+        }
+    }
+    // Half sums through LDS (the operand buffer is free once every wave has
+    // its B operands).
+    __syncthreads();
+    f32x4 *partial = (f32x4 *)bsh;
+    if (half == 1) partial[t * 64 + lane] = acc;
+    __syncthreads();
+    if (half == 0 && active) {
+        const f32x4 p = partial[t * 64 + lane];
+        f32x4 v;
+        v[0] = __fadd_rn(acc[0], p[0]);
+        v[1] = __fadd_rn(acc[1], p[1]);
+        v[2] = __fadd_rn(acc[2], p[2]);
+        v[3] = __fadd_rn(acc[3], p[3]);
+        flag_nonfinite(a.status, epilogue<EPI>(a, e, v, s, row0, live));
+    }
+}
+
+// Split-fragment rows from global memory (any K): one row tile x 16 streams.
+// The 8 waves split the column blocks into 8 contiguous ranges (8 blocks
+// each at K = 2048), in chunks of 4 with the next chunk's weights requested
+// before the current chunk's MFMAs; the ranges are summed in LDS in wave
+// order.
+template <int EPI, bool Q8, class Wait>
+__device__ inline void gemm_split_task(const GemmArgs &a, int tile, int st, uint16_t *lds,
+                                       const Wait &wait) {
+    constexpr int CH = 4;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    const int kbn = a.k_cols >> 5;
+    const int per = (kbn + kTaskWaves - 1) / kTaskWaves;
+    const int kb_begin = wave * per;
+    const int kb_end = min(kbn, kb_begin + per);
+
+    // D fragment of this lane: rows row0 .. row0+3 of stream s.
+    const int s = st * 16 + (lane & 15);
+    const int row0 = tile * 16 + (lane >> 4) * 4;
+    const bool live = s < a.streams;
+
+    WChunk<Q8, CH> w;
+    if (kb_begin < kb_end) load_weights(w, a, tile, kbn, lane, kb_begin, kb_end);
+    EpiOperands e;
+    if (wave == 0) load_epilogue_static<EPI>(e, a, s, row0, live);
+    wait();
+    if (wave == 0) load_epilogue_dynamic<EPI>(e, a, s, row0, live);
+
+    const uint16_t *xs = a.xs + (size_t)st * kbn * 1536 + lane * 8;
+    f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int kb0 = kb_begin; kb0 < kb_end; kb0 += CH) {
+        bf16x8 xh[CH], xm[CH], xl[CH];
+#pragma unroll
+        for (int u = 0; u < CH; u++) {
+            const size_t kb = (size_t)min(kb0 + u, kb_end - 1) * 1536;
+            xh[u] = *(const bf16x8 *)(xs + kb);
+            xm[u] = *(const bf16x8 *)(xs + kb + 512);
+            xl[u] = *(const bf16x8 *)(xs + kb + 1024);
+        }
+        WChunk<Q8, CH> next;
+        if (kb0 + CH < kb_end) load_weights(next, a, tile, kbn, lane, kb0 + CH, kb_end);
+#pragma unroll
+        for (int u = 0; u < CH; u++) mfma_block(acc, w, u, xh[u], xm[u], xl[u], kb0 + u < kb_end);
+        w = next;
+    }
+
+    f32x4 *partial = (f32x4 *)lds;
+    partial[wave * 64 + lane] = acc;
+    __syncthreads();
+    if (wave == 0) {
+        f32x4 v = acc;
+#pragma unroll
+        for (int w2 = 1; w2 < kTaskWaves; w2++) {
+            const f32x4 p = partial[w2 * 64 + lane];
+            v[0] = __fadd_rn(v[0], p[0]);
+            v[1] = __fadd_rn(v[1], p[1]);
+            v[2] = __fadd_rn(v[2], p[2]);
+            v[3] = __fadd_rn(v[3], p[3]);
+        }
+        flag_nonfinite(a.status, epilogue<EPI>(a, e, v, s, row0, live));
+    }
+}
+
+}  // namespace pgpu

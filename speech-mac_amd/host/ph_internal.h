@@ -12,8 +12,17 @@
 
 enum { PH_WIDTH = 512, PH_HEADS = 8, PH_HEAD = 64, PH_FFN = 2048, PH_SPLIT_KEYS = 256 };
 enum { PH_MAX_GROUPS = 4, PH_DEFAULT_GROUPS = 1 };
-/* Launches of a paired decode step: 2 * layers + 2, layers <= 64. */
-enum { PH_MAX_LAUNCHES = 2 * 64 + 2 };
+/* The one-launch step keeps this many positions of headroom in its task
+ * schedule (and captured graph) before it has to rebuild them. */
+enum { PH_FLOW_HEADROOM = 256 };
+/* Decode batches of this many 16-stream tiles run as one launch by default
+ * (phonon_flow_batch_set_pipeline): measured faster there on MI355X (B = 64:
+ * 764 vs 913 us per 12-layer step; B = 32: 746 vs 653; B = 128: 1546 vs
+ * 1463). */
+enum { PH_FLOW_MIN_TILES = 3, PH_FLOW_MAX_TILES = 6 };
+/* Chain placement of the one-launch step's task list (pgpu_flow_placement):
+ * measured on MI355X at B = 64 (ph_flow_schedule.c). */
+pgpu_flow_placement ph_flow_default_placement(void);
 
 /* Device selection and the library's own HIP stream (created once). */
 int ph_init(void);

@@ -19,6 +19,8 @@ struct PhononFlowModel {
     size_t layers;
     pgpu_matrix *qkv, *out, *mlp_in, *mlp_out;
     float *norms; /* dev [layers][4][512]: norm1 w, b, norm2 w, b */
+    pgpu_flow_layer *flow_layers; /* dev [layers]: operands of the one-launch step */
+    int q8;                       /* 1/0: every matrix Q8/BF16; -1: mixed */
     void **allocations;
     size_t allocation_count, device_bytes;
 };
@@ -40,8 +42,23 @@ struct PhononFlowBatch {
     uint16_t *xh; /* split fragments of the MLP hidden rows */
     int32_t *positions, *tables;
     int32_t *table_src, *table_map; /* prefill staging, allocated on first use */
-    unsigned *counters;             /* barrier counters of the paired launches */
-    int pipeline;                   /* paired launches when >= 2 stream tiles */
+    int flow;                       /* 1: one launch per step (pgpu_flow_launch) */
+    struct {
+        size_t cap, cap_layers;     /* padded streams and layers the buffers hold */
+        float *act, *part_acc, *part_ml;
+        uint16_t *hidden;
+        unsigned *counters;         /* all zero between steps */
+        size_t counter_words;
+        uint32_t *schedule, *host_schedule;
+        size_t schedule_cap, host_cap, tasks;
+        size_t *cover;              /* [max_streams] splits the schedule lists per stream */
+        size_t streams, layers;     /* what the schedule was built for (0: none) */
+        int prefill;
+        unsigned version;           /* bumped by every rebuild */
+        pgpu_flow_placement place;  /* chain placement in the task list */
+        uint64_t *trace;            /* (dev) optional task timeline, trace_cap tasks */
+        size_t trace_cap;
+    } fl;
     int *status;
     pgpu_attention_scratch scratch;
     size_t *host_positions;
@@ -54,6 +71,8 @@ struct PhononFlowBatch {
         float theta;
         const float *input;
         float *output;
+        int flow;
+        unsigned version;
     } graphs[2];
     size_t graph_victim;
     int eager;                         /* launch kernels directly, no graph */
@@ -94,7 +113,7 @@ int phonon_flow_model_create(const PhononFlowLayerWeights *weights, size_t layer
     m->out = calloc(layers, sizeof(pgpu_matrix));
     m->mlp_in = calloc(layers, sizeof(pgpu_matrix));
     m->mlp_out = calloc(layers, sizeof(pgpu_matrix));
-    m->allocations = calloc(layers * 4 + 1, sizeof(void *));
+    m->allocations = calloc(layers * 4 + 2, sizeof(void *));
     float *norms = malloc(layers * 4 * PH_WIDTH * sizeof(float));
     int ok = m->qkv && m->out && m->mlp_in && m->mlp_out && m->allocations && norms;
     for (size_t l = 0; ok && l < layers; l++) {
@@ -132,6 +151,30 @@ int phonon_flow_model_create(const PhononFlowLayerWeights *weights, size_t layer
         }
     }
     free(norms);
+    /* Operand table of the one-launch step (pgpu_flow_launch). */
+    pgpu_flow_layer *table = ok ? calloc(layers, sizeof(pgpu_flow_layer)) : NULL;
+    ok = ok && table;
+    m->q8 = ok ? m->qkv[0].q8 : 0;
+    for (size_t l = 0; ok && l < layers; l++) {
+        const pgpu_matrix *mats[4] = {&m->qkv[l], &m->out[l], &m->mlp_in[l], &m->mlp_out[l]};
+        for (int i = 0; i < 4; i++) {
+            table[l].values[i] = mats[i]->values;
+            table[l].scales[i] = mats[i]->scales;
+            if (mats[i]->q8 != m->q8)
+                m->q8 = -1;
+        }
+        table[l].norms = m->norms + l * 4 * PH_WIDTH;
+    }
+    if (ok) {
+        m->flow_layers = pgpu_malloc(layers * sizeof(pgpu_flow_layer));
+        ok = m->flow_layers != NULL;
+        if (ok) {
+            m->allocations[m->allocation_count++] = m->flow_layers;
+            ok = pgpu_copy_h2d(ph_stream(), m->flow_layers, table,
+                               layers * sizeof(pgpu_flow_layer));
+        }
+    }
+    free(table);
     if (!ok) {
         phonon_flow_model_destroy(m);
         return 0;
@@ -317,11 +360,14 @@ void phonon_flow_batch_destroy(PhononFlowBatch *b) {
     void *bufs[] = {b->x,    b->r,  b->q,         b->in,     b->out,
                     b->rows, b->xh, b->positions, b->tables, b->status,
                     b->scratch.part_acc, b->scratch.part_ml, b->table_src, b->table_map,
-                    b->counters};
+                    b->fl.act, b->fl.part_acc, b->fl.part_ml, b->fl.hidden, b->fl.counters,
+                    b->fl.schedule};
     for (size_t i = 0; i < sizeof(bufs) / sizeof(bufs[0]); i++)
         pgpu_free(bufs[i]);
     pgpu_stream_destroy(b->stream);
     free(b->host_positions);
+    free(b->fl.host_schedule);
+    free(b->fl.cover);
     free(b);
 }
 
@@ -348,7 +394,8 @@ int phonon_flow_batch_create(const PhononFlowModel *model, PhononKvPool *pool,
     const size_t split2048 = b->padded_streams * PH_FFN * 3 * sizeof(uint16_t);
     const size_t slots = max_streams * PH_HEADS * b->max_splits;
     b->groups = PH_DEFAULT_GROUPS;
-    b->pipeline = 0;
+    b->flow = 1;
+    b->fl.place = ph_flow_default_placement();
     int ok = pgpu_stream_create(&b->stream) && pgpu_event_create(&b->fork);
     for (size_t g = 0; ok && g + 1 < PH_MAX_GROUPS; g++)
         ok = pgpu_stream_create(&b->side[g]) && pgpu_event_create(&b->join[g]);
@@ -362,15 +409,15 @@ int phonon_flow_batch_create(const PhononFlowModel *model, PhononKvPool *pool,
     b->positions = pgpu_malloc(b->padded_streams * sizeof(int32_t));
     b->tables = pgpu_malloc(max_streams * b->table_len * sizeof(int32_t));
     b->status = pgpu_malloc(sizeof(int));
-    b->counters = pgpu_malloc(PH_MAX_LAUNCHES * sizeof(unsigned));
     b->scratch.part_acc = pgpu_malloc(slots * 64 * sizeof(float));
     b->scratch.part_ml = pgpu_malloc(slots * 2 * sizeof(float));
     b->scratch.max_streams = (int)max_streams;
     b->scratch.max_splits = (int)b->max_splits;
     b->host_positions = calloc(max_streams, sizeof(size_t));
+    b->fl.cover = calloc(max_streams, sizeof(size_t));
     ok = ok && b->x && b->r && b->q && b->in && b->out && b->rows && b->xh && b->positions &&
-         b->tables && b->status && b->counters && b->scratch.part_acc && b->scratch.part_ml &&
-         b->host_positions;
+         b->tables && b->status && b->scratch.part_acc && b->scratch.part_ml &&
+         b->host_positions && b->fl.cover;
     /* Zero everything a kernel may read before writing (padding streams of the
      * split fragments, positions, status). */
     ok = ok && pgpu_memset(b->stream, b->xh, 0, split2048) &&
@@ -515,88 +562,6 @@ static size_t group_bounds(const PhononFlowBatch *b, size_t *first, size_t *coun
     return groups;
 }
 
-/* One step as paired launches (streams in two groups A and B of whole
- * 16-stream tiles): after the QKV of layer 0 for everyone and the attention
- * of A's layer 0, every launch runs one group's attention beside the other
- * group's projection chain (out, MLP, next QKV), alternating:
- *   attention B(l) + chain A(l),  attention A(l+1) + chain B(l), ...
- * so the latency-bound projections run under the HBM-bound attention.
- * 2L + 2 launches per step; bit-identical to enqueue_group. */
-static int enqueue_pipelined(PhononFlowBatch *b, const float *input, float *output,
-                             const float *rope) {
-    const PhononFlowModel *m = b->model;
-    const size_t layers = m->layers, tiles = (b->streams + 15) / 16;
-    const size_t half = tiles / 2;
-    const size_t first[2] = {0, half * 16};
-    const size_t count[2] = {half * 16, b->streams - half * 16};
-    pgpu_pair_attention att[2];
-    pgpu_pair_chain ch[2];
-    for (int g = 0; g < 2; g++) {
-        const size_t s0 = first[g], n = count[g];
-        const size_t slot0 = s0 * PH_HEADS * b->splits;
-        const pgpu_attention_scratch sc = {b->scratch.part_acc + slot0 * 64,
-                                           b->scratch.part_ml + slot0 * 2, (int)n,
-                                           (int)b->splits};
-        att[g] = (pgpu_pair_attention){.q = b->q + s0 * PH_WIDTH,
-                                       .tables = b->tables + s0 * b->table_len,
-                                       .positions = b->positions + s0,
-                                       .streams = (int)n,
-                                       .scratch = sc};
-        ch[g] = (pgpu_pair_chain){.streams = (int)n,
-                                  .ln_epsilon = 1e-5f,
-                                  .r = b->r + s0 * PH_WIDTH,
-                                  .hidden = b->xh + (s0 / 16) * (PH_FFN / 32) * 1536,
-                                  .q_next = b->q + s0 * PH_WIDTH,
-                                  .tables = b->tables + s0 * b->table_len,
-                                  .positions = b->positions + s0,
-                                  .scratch = sc};
-    }
-    const size_t launches = 2 * layers + 2;
-    if (launches > PH_MAX_LAUNCHES || !pgpu_fill_u32(b->stream, b->counters, launches, 0))
-        return 0;
-    /* QKV of layer 0, all streams. */
-    const pgpu_gemm_input ln1 = {.ln_rows = input, .ln_weight = m->norms,
-                                 .ln_bias = m->norms + PH_WIDTH, .ln_epsilon = 1e-5f};
-    if (!pgpu_gemm_qkv(b->stream, &m->qkv[0], &ln1, (int)b->streams, &b->pool->kv, 0, b->tables,
-                       (int)b->table_len, b->positions, rope, b->q, b->status))
-        return 0;
-    size_t launch = 0;
-    att[0].layer = 0;
-    if (!pgpu_decode_pair(b->stream, &att[0], NULL, &b->pool->kv, (int)b->table_len, rope,
-                          b->counters + launch++, b->status))
-        return 0;
-    for (size_t l = 0; l < layers; l++) {
-        const float *norm = m->norms + l * 4 * PH_WIDTH;
-        const float *next_norm = l + 1 < layers ? m->norms + (l + 1) * 4 * PH_WIDTH : NULL;
-        for (int g = 0; g < 2; g++) {
-            const size_t s0 = first[g];
-            pgpu_pair_chain *c = &ch[g];
-            c->layer = (int)l;
-            c->out = &m->out[l];
-            c->mlp_in = &m->mlp_in[l];
-            c->mlp_out = &m->mlp_out[l];
-            c->qkv_next = next_norm ? &m->qkv[l + 1] : NULL;
-            c->norm2_weight = norm + 2 * PH_WIDTH;
-            c->norm2_bias = norm + 3 * PH_WIDTH;
-            c->norm1_next_weight = next_norm;
-            c->norm1_next_bias = next_norm ? next_norm + PH_WIDTH : NULL;
-            c->input = (l == 0 ? input : b->x) + s0 * PH_WIDTH;
-            c->output = (l + 1 == layers ? output : b->x) + s0 * PH_WIDTH;
-        }
-        /* attention B(l) beside chain A(l); then attention A(l+1) beside
-         * chain B(l) (the last chain B runs alone). */
-        att[1].layer = (int)l;
-        if (!pgpu_decode_pair(b->stream, &att[1], &ch[0], &b->pool->kv, (int)b->table_len, rope,
-                              b->counters + launch++, b->status))
-            return 0;
-        att[0].layer = (int)l + 1;
-        if (!pgpu_decode_pair(b->stream, l + 1 < layers ? &att[0] : NULL, &ch[1], &b->pool->kv,
-                              (int)b->table_len, rope, b->counters + launch++, b->status))
-            return 0;
-    }
-    return 1;
-}
-
 /* One step: each stream group runs all layers on its own HIP stream (forked
  * from and joined back into the batch stream), so one group's latency-bound
  * projections overlap another group's bandwidth-bound attention. */
@@ -606,9 +571,6 @@ static int enqueue_step(PhononFlowBatch *b, const float *input, float *output, f
     const size_t groups = group_bounds(b, first, count);
     if (!rope || !groups)
         return 0;
-    if (b->pipeline && groups == 1 && b->streams > 16)
-        return enqueue_pipelined(b, input, output, rope) &&
-               pgpu_advance_positions(b->stream, b->positions, (int)b->streams);
     if (groups > 1 && !pgpu_event_record(b->fork, b->stream))
         return 0;
     for (size_t g = 1; g < groups; g++)
@@ -623,6 +585,162 @@ static int enqueue_step(PhononFlowBatch *b, const float *input, float *output, f
             !pgpu_stream_wait_event(b->stream, b->join[g - 1]))
             return 0;
     return pgpu_advance_positions(b->stream, b->positions, (int)b->streams);
+}
+
+/* ------------------------------------------------------ one-launch step -- */
+
+/* Floats of one (layer, stream, head) group of (max, sum) pairs: padded to
+ * whole 128-byte lines, so no two groups share a cache line. */
+static size_t flow_ml_group(const PhononFlowBatch *b) {
+    return (2 * b->max_splits + 31) / 32 * 32;
+}
+
+/* When a step runs as one launch: always (flow = 2), or, by default
+ * (flow = 1), for the decode batch sizes where it measured faster on MI355X
+ * than one launch per phase (PH_FLOW_MIN_TILES..PH_FLOW_MAX_TILES 16-stream
+ * tiles; prefill and larger batches are attention-bound, and the separate
+ * attention kernel streams K/V faster). */
+static int flow_usable(const PhononFlowBatch *b, int prefill) {
+    if (!b->flow || b->model->q8 < 0 || b->model->layers > 63 || b->streams > 4096)
+        return 0;
+    const size_t tiles = (b->streams + 15) / 16;
+    return b->flow == 2 ||
+           (!prefill && tiles >= PH_FLOW_MIN_TILES && tiles <= PH_FLOW_MAX_TILES);
+}
+
+/* Grows the per-layer buffers of the one-launch step to hold `streams`
+ * streams of the model's layers. Every value a step's task hands to another
+ * has its own address per layer (see pgpu_flow.hip). */
+static int flow_reserve(PhononFlowBatch *b, size_t streams) {
+    const size_t cap = (streams + 15) / 16 * 16, layers = b->model->layers;
+    if (cap <= b->fl.cap && layers <= b->fl.cap_layers)
+        return 1;
+    const size_t new_cap = cap > b->fl.cap ? cap : b->fl.cap;
+    const size_t new_layers = layers > b->fl.cap_layers ? layers : b->fl.cap_layers;
+    if (!pgpu_stream_sync(b->stream))
+        return 0;
+    drop_graphs(b);
+    void *old[] = {b->fl.act, b->fl.part_acc, b->fl.part_ml, b->fl.hidden, b->fl.counters};
+    for (size_t i = 0; i < sizeof(old) / sizeof(old[0]); i++)
+        pgpu_free(old[i]);
+    b->fl.act = NULL;
+    b->fl.part_acc = b->fl.part_ml = NULL;
+    b->fl.hidden = NULL;
+    b->fl.counters = NULL;
+    b->fl.cap = b->fl.cap_layers = 0;
+    b->fl.streams = 0; /* the schedule is rebuilt against the new buffers */
+    const size_t groups = new_layers * new_cap * PH_HEADS;
+    b->fl.counter_words = new_layers * (new_cap / 16) * PGPU_FLOW_KINDS *
+                              PGPU_FLOW_COUNTER_STRIDE + groups;
+    b->fl.act = pgpu_malloc(new_layers * 4 * new_cap * PH_WIDTH * sizeof(float));
+    b->fl.part_acc = pgpu_malloc(groups * b->max_splits * 64 * sizeof(float));
+    b->fl.part_ml = pgpu_malloc(groups * flow_ml_group(b) * sizeof(float));
+    b->fl.hidden = pgpu_malloc(new_layers * new_cap * PH_FFN * 3 * sizeof(uint16_t));
+    b->fl.counters = pgpu_malloc(b->fl.counter_words * sizeof(unsigned));
+    if (!b->fl.act || !b->fl.part_acc || !b->fl.part_ml || !b->fl.hidden || !b->fl.counters ||
+        !pgpu_memset(b->stream, b->fl.counters, 0, b->fl.counter_words * sizeof(unsigned)) ||
+        !pgpu_memset(b->stream, b->fl.hidden, 0,
+                     new_layers * new_cap * PH_FFN * 3 * sizeof(uint16_t)) ||
+        !pgpu_stream_sync(b->stream))
+        return 0;
+    b->fl.cap = new_cap;
+    b->fl.cap_layers = new_layers;
+    return 1;
+}
+
+/* Rebuilds (and uploads) the step's task list (pgpu_flow_schedule) when the
+ * streams, the layers or a context outgrow it. A stream lists the splits of
+ * its context PH_FLOW_HEADROOM positions ahead; tasks past its live context
+ * end at once. */
+static int flow_schedule(PhononFlowBatch *b, int prefill) {
+    const size_t streams = b->streams, layers = b->model->layers;
+    int valid = b->fl.streams == streams && b->fl.layers == layers && b->fl.prefill == prefill;
+    for (size_t s = 0; valid && s < streams; s++)
+        valid = (b->host_positions[s] + PH_SPLIT_KEYS) / PH_SPLIT_KEYS <= b->fl.cover[s];
+    if (valid)
+        return 1;
+    b->fl.streams = 0; /* no valid schedule until the new one is uploaded */
+    for (size_t s = 0; s < streams; s++) {
+        size_t need = (b->host_positions[s] + PH_FLOW_HEADROOM + PH_SPLIT_KEYS) / PH_SPLIT_KEYS;
+        b->fl.cover[s] = need < b->max_splits ? need : b->max_splits;
+    }
+    const size_t tasks =
+        pgpu_flow_schedule(streams, layers, b->fl.cover, &b->fl.place, prefill, NULL, 0);
+    if (tasks > b->fl.host_cap) {
+        uint32_t *grown = realloc(b->fl.host_schedule, tasks * sizeof(uint32_t));
+        if (!grown)
+            return 0;
+        b->fl.host_schedule = grown;
+        b->fl.host_cap = tasks;
+    }
+    uint32_t *d = b->fl.host_schedule;
+    const size_t k = pgpu_flow_schedule(streams, layers, b->fl.cover, &b->fl.place, prefill, d,
+                                        b->fl.host_cap);
+    if (k != tasks)
+        return ph_fail("flow schedule: task count mismatch");
+    if (!pgpu_stream_sync(b->stream))
+        return 0;
+    drop_graphs(b);
+    if (tasks > b->fl.schedule_cap) {
+        pgpu_free(b->fl.schedule);
+        b->fl.schedule = pgpu_malloc(tasks * sizeof(uint32_t));
+        b->fl.schedule_cap = b->fl.schedule ? tasks : 0;
+        if (!b->fl.schedule)
+            return 0;
+    }
+    if (!pgpu_copy_h2d(b->stream, b->fl.schedule, d, tasks * sizeof(uint32_t)))
+        return 0;
+    b->fl.tasks = tasks;
+    b->fl.streams = streams;
+    b->fl.layers = layers;
+    b->fl.prefill = prefill;
+    b->fl.version++;
+    return 1;
+}
+
+/* Makes buffers and schedule ready for the batch's current streams (outside
+ * any graph capture). */
+static int flow_prepare(PhononFlowBatch *b, int prefill) {
+    return flow_reserve(b, b->streams) && flow_schedule(b, prefill);
+}
+
+/* One step as a single launch, then the launch that zeroes its counters and
+ * advances the positions. */
+static int enqueue_flow(PhononFlowBatch *b, const float *input, float *output, float theta) {
+    const PhononFlowModel *m = b->model;
+    const float *rope = ph_rope_table(theta);
+    const size_t tiles = (b->streams + 15) / 16, layers = m->layers;
+    if (!rope)
+        return 0;
+    const size_t phase_words = layers * tiles * PGPU_FLOW_KINDS * PGPU_FLOW_COUNTER_STRIDE;
+    const pgpu_flow_step f = {.layers = m->flow_layers,
+                              .layer_count = (int)layers,
+                              .q8 = m->q8,
+                              .streams = (int)b->streams,
+                              .tiles = (int)tiles,
+                              .prefill = b->fl.prefill,
+                              .pool_offset = 0,
+                              .input = input,
+                              .output = output,
+                              .act = b->fl.act,
+                              .hidden = b->fl.hidden,
+                              .part_acc = b->fl.part_acc,
+                              .part_ml = b->fl.part_ml,
+                              .max_splits = (int)b->max_splits,
+                              .ml_group = (int)flow_ml_group(b),
+                              .tables = b->tables,
+                              .positions = b->positions,
+                              .table_stride = (int)b->table_len,
+                              .rope = rope,
+                              .schedule = b->fl.schedule,
+                              .tasks = (unsigned)b->fl.tasks,
+                              .phase = b->fl.counters,
+                              .split_done = b->fl.counters + phase_words,
+                              .status = b->status,
+                              .trace = b->fl.trace_cap >= b->fl.tasks ? b->fl.trace : NULL};
+    const size_t used = phase_words + layers * tiles * 16 * PH_HEADS;
+    return pgpu_flow_launch(b->stream, &f, &b->pool->kv) &&
+           pgpu_flow_finish(b->stream, b->fl.counters, used, b->positions, (int)b->streams);
 }
 
 /* Pseudo-streams of a batched prefill: position first[i] + k (k < counts[i])
@@ -674,10 +792,13 @@ int phonon_flow_batch_prefill_device(PhononFlowBatch *b, size_t streams, const s
     if (!b->table_src &&
         !(b->table_src = pgpu_malloc(b->max_streams * b->table_len * sizeof(int32_t))))
         return 0;
-    return pgpu_stream_sync(b->stream) &&
-           pgpu_copy_h2d(b->stream, b->table_src, tables, streams * table_len * sizeof(int32_t)) &&
-           ph_batch_set_prefill(b, streams, first, counts, b->table_src) &&
-           (b->splits = splits_for(b, 0)) > 0 && enqueue_step(b, inputs, outputs, theta);
+    if (!pgpu_stream_sync(b->stream) ||
+        !pgpu_copy_h2d(b->stream, b->table_src, tables, streams * table_len * sizeof(int32_t)) ||
+        !ph_batch_set_prefill(b, streams, first, counts, b->table_src))
+        return 0;
+    if (flow_usable(b, 1))
+        return flow_prepare(b, 1) && enqueue_flow(b, inputs, outputs, theta);
+    return (b->splits = splits_for(b, 0)) > 0 && enqueue_step(b, inputs, outputs, theta);
 }
 
 int phonon_flow_batch_set_groups(PhononFlowBatch *b, size_t groups) {
@@ -690,12 +811,39 @@ int phonon_flow_batch_set_groups(PhononFlowBatch *b, size_t groups) {
     return 1;
 }
 
-int phonon_flow_batch_set_pipeline(PhononFlowBatch *b, int enable) {
+int phonon_flow_batch_set_placement(PhononFlowBatch *b, const pgpu_flow_placement *place) {
     if (!b)
         return 0;
-    if (b->pipeline != !!enable) {
+    b->fl.place = place ? *place : ph_flow_default_placement();
+    b->fl.streams = 0; /* rebuild the task list */
+    drop_graphs(b);
+    return 1;
+}
+
+int phonon_flow_batch_set_trace(PhononFlowBatch *b, uint64_t *trace, size_t capacity) {
+    if (!b || (!trace) != (!capacity))
+        return 0;
+    drop_graphs(b);
+    b->fl.trace = trace;
+    b->fl.trace_cap = capacity;
+    return 1;
+}
+
+size_t phonon_flow_batch_schedule(const PhononFlowBatch *b, uint32_t *schedule,
+                                  size_t capacity) {
+    if (!b || !b->fl.streams)
+        return 0;
+    if (schedule && capacity >= b->fl.tasks)
+        memcpy(schedule, b->fl.host_schedule, b->fl.tasks * sizeof(uint32_t));
+    return b->fl.tasks;
+}
+
+int phonon_flow_batch_set_pipeline(PhononFlowBatch *b, int mode) {
+    if (!b || mode < 0 || mode > 2)
+        return 0;
+    if (b->flow != mode) {
         drop_graphs(b);
-        b->pipeline = !!enable;
+        b->flow = mode;
     }
     return 1;
 }
@@ -715,22 +863,29 @@ int phonon_flow_batch_step_device(PhononFlowBatch *b, const float *inputs, float
     for (size_t s = 0; s < b->streams; s++)
         if (b->host_positions[s] >= b->max_positions)
             return 0;
+    const int flow = flow_usable(b, 0);
+    if (flow && !flow_prepare(b, 0))
+        return 0;
     if (b->eager) {
         b->splits = splits_for(b, 0);
-        if (!enqueue_step(b, inputs, outputs, theta))
+        if (!(flow ? enqueue_flow(b, inputs, outputs, theta)
+                   : enqueue_step(b, inputs, outputs, theta)))
             return 0;
         for (size_t s = 0; s < b->streams; s++)
             b->host_positions[s]++;
         return 1;
     }
-    /* A captured step covers contexts up to its attention grid: captured with
-     * 256 positions of headroom, re-captured when a context outgrows it. */
+    /* A captured step covers contexts up to its attention grid (phase by
+     * phase) or its task schedule (one launch): captured with 256 positions
+     * of headroom, re-captured when a context outgrows it. */
     const size_t need = splits_for(b, 0);
     void *exec = NULL;
     for (size_t i = 0; i < 2 && !exec; i++)
         if (b->graphs[i].exec && b->graphs[i].streams == b->streams &&
-            b->graphs[i].splits >= need && b->graphs[i].theta == theta &&
-            b->graphs[i].input == inputs && b->graphs[i].output == outputs)
+            b->graphs[i].flow == flow &&
+            (flow ? b->graphs[i].version == b->fl.version : b->graphs[i].splits >= need) &&
+            b->graphs[i].theta == theta && b->graphs[i].input == inputs &&
+            b->graphs[i].output == outputs)
             exec = b->graphs[i].exec;
     if (!exec) {
         const size_t slot = b->graph_victim;
@@ -739,7 +894,8 @@ int phonon_flow_batch_step_device(PhononFlowBatch *b, const float *inputs, float
         b->splits = splits_for(b, PH_SPLIT_KEYS);
         if (!ph_rope_table(theta) || !pgpu_graph_begin(b->stream))
             return 0;
-        const int enqueued = enqueue_step(b, inputs, outputs, theta);
+        const int enqueued = flow ? enqueue_flow(b, inputs, outputs, theta)
+                                  : enqueue_step(b, inputs, outputs, theta);
         const int ended = pgpu_graph_end(b->stream, &exec);
         if (!enqueued || !ended) {
             pgpu_graph_destroy(exec);
@@ -751,6 +907,8 @@ int phonon_flow_batch_step_device(PhononFlowBatch *b, const float *inputs, float
         b->graphs[slot].theta = theta;
         b->graphs[slot].input = inputs;
         b->graphs[slot].output = outputs;
+        b->graphs[slot].flow = flow;
+        b->graphs[slot].version = b->fl.version;
         b->graph_victim = 1 - slot;
     }
     if (!pgpu_graph_launch(exec, b->stream))

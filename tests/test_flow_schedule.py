@@ -1,0 +1,152 @@
+"""CPU checks of the one-launch step's task list (pgpu_flow_schedule).
+
+The launch cannot deadlock if every task is listed after every task it
+waits for (work-groups are dispatched in list order, so the lowest unfinished
+task always has its inputs done). These tests decode the descriptors the
+library builds and replay the waits of pgpu_flow.hip against the list order.
+"""
+import ctypes
+
+import numpy as np
+import pytest
+
+QKV, ATTN, OUT, MLP_IN, MLP_OUT = range(5)
+TASKS = {QKV: 24, OUT: 8, MLP_IN: 32, MLP_OUT: 32}
+
+
+PLACEMENTS = [None, (0.024, (4.0, 10.0, 16.0, 22.0)), (0.001, (0.0, 0.0, 0.0, 0.0)),
+              (1.0, (50.0, 20.0, 900.0, 1e6)), (0.05, (1e9, 1e9, 1e9, 1e9))]
+
+
+def build(lib, splits, layers, place=None, prefill=0):
+    splits = np.ascontiguousarray(splits, dtype=np.uintp)
+    szp = splits.ctypes.data_as(ctypes.POINTER(ctypes.c_size_t))
+    pp = None
+    if place is not None:
+        import speech_mac_amd as pkg
+        pl = pkg.PgpuFlowPlacement(place[0], (ctypes.c_float * 4)(*place[1]))
+        pp = ctypes.byref(pl)
+    n = lib.pgpu_flow_schedule(len(splits), layers, szp, pp, prefill, None, 0)
+    out = np.zeros(n, np.uint32)
+    got = lib.pgpu_flow_schedule(len(splits), layers, szp, pp, prefill,
+                                 out.ctypes.data_as(ctypes.POINTER(ctypes.c_uint32)), n)
+    assert got == n
+    return out
+
+
+def decode(d):
+    d = d.astype(np.int64)
+    return d & 7, (d >> 3) & 63, (d >> 9) & 255, d >> 17
+
+
+def check_order(sched, splits, layers, prefill=False):
+    """Replays the step: each task must find its waits satisfied by the tasks
+    listed before it. Raises AssertionError at the first violation."""
+    streams = len(splits)
+    tiles = (streams + 15) // 16
+    kind, layer, tile, index = decode(sched)
+    done = np.zeros((layers, tiles, 5), np.int64)
+    merged = np.zeros((layers, streams, 8), np.int64)   # ATTN tasks seen per (s, head)
+    seen = set()
+    for i in range(len(sched)):
+        k, l, t, x = int(kind[i]), int(layer[i]), int(tile[i]), int(index[i])
+        key = (k, l, t, x)
+        assert key not in seen, f"task {key} listed twice"
+        seen.add(key)
+        assert l < layers and t < tiles
+        live = min(16, streams - 16 * t)
+        if k == QKV:
+            assert x < TASKS[QKV]
+            if l > 0:
+                assert done[l - 1, t, MLP_OUT] == TASKS[MLP_OUT], f"QKV({l},{t}) before MLP_OUT"
+        elif k == ATTN:
+            h, j, n = x & 7, (x >> 3) & 255, x >> 11
+            assert n < live and j < splits[16 * t + n]
+            need = range(tiles) if prefill else [t]
+            for t2 in need:
+                assert done[l, t2, QKV] == TASKS[QKV], f"ATTN({l},{t}) before QKV({l},{t2})"
+            merged[l, 16 * t + n, h] += 1
+            if merged[l, 16 * t + n, h] == splits[16 * t + n]:
+                done[l, t, ATTN] += 1   # the (stream, head) is merged
+        elif k == OUT:
+            assert x < TASKS[OUT]
+            assert done[l, t, ATTN] == 8 * live, f"OUT({l},{t}) before its attention"
+        elif k == MLP_IN:
+            assert x < TASKS[MLP_IN]
+            assert done[l, t, OUT] == TASKS[OUT], f"MLP_IN({l},{t}) before OUT"
+        elif k == MLP_OUT:
+            assert x < TASKS[MLP_OUT]
+            assert done[l, t, MLP_IN] == TASKS[MLP_IN], f"MLP_OUT({l},{t}) before MLP_IN"
+        else:
+            raise AssertionError(f"bad kind {k}")
+        if k != ATTN:
+            done[l, t, k] += 1
+    # every task of the step is listed
+    for l in range(layers):
+        for t in range(tiles):
+            live = min(16, streams - 16 * t)
+            for k, n in TASKS.items():
+                assert done[l, t, k] == n, (l, t, k)
+            assert done[l, t, ATTN] == 8 * live
+    return True
+
+
+@pytest.mark.parametrize("streams,layers", [(1, 1), (1, 12), (5, 3), (16, 2), (17, 4),
+                                            (40, 12), (64, 12), (256, 2)])
+@pytest.mark.parametrize("place", range(len(PLACEMENTS)))
+def test_schedule_lists_every_task_after_its_inputs(pkg, streams, layers, place):
+    lib = pkg.load()
+    rng = np.random.default_rng(streams * 100 + layers)
+    splits = rng.integers(1, 33, size=streams)
+    chain = sum(TASKS.values())
+    count = layers * ((streams + 15) // 16) * chain + layers * 8 * int(splits.sum())
+    sched = build(lib, splits, layers, PLACEMENTS[place])
+    assert len(sched) == count
+    assert check_order(sched, splits, layers)
+    pre = build(lib, splits, layers, PLACEMENTS[place], prefill=1)
+    assert len(pre) == count
+    assert check_order(pre, splits, layers, prefill=True)
+
+
+def test_schedule_puts_each_chain_behind_its_own_attention(pkg):
+    """Tile t's OUT tasks follow its last ATTN task directly, ahead of tile
+    t+1's attention (the overlap the order exists for)."""
+    lib = pkg.load()
+    splits = np.full(48, 3)
+    sched = build(lib, splits, 2)
+    kind, layer, tile, _ = decode(sched)
+    for l in range(2):
+        for t in range(3):
+            attn = np.flatnonzero((kind == ATTN) & (layer == l) & (tile == t))
+            outs = np.flatnonzero((kind == OUT) & (layer == l) & (tile == t))
+            assert outs[0] == attn[-1] + 1
+            if t < 2:
+                nxt = np.flatnonzero((kind == ATTN) & (layer == l) & (tile == t + 1))
+                assert nxt[0] > outs[-1]
+
+
+def test_order_checker_rejects_planted_mistakes(pkg):
+    """The replay is not vacuous: moving one task ahead of an input, dropping
+    a task, or listing one twice each fail it."""
+    lib = pkg.load()
+    splits = np.array([2, 1, 3, 1, 2] * 4)
+    sched = build(lib, splits, 2)
+    kind, layer, tile, _ = decode(sched)
+    cases = []
+    # an OUT task moved in front of the last ATTN of its tile
+    o = int(np.flatnonzero((kind == OUT) & (layer == 1) & (tile == 0))[0])
+    a = int(np.flatnonzero((kind == ATTN) & (layer == 1) & (tile == 0))[-1])
+    bad = sched.copy()
+    bad[a], bad[o] = sched[o], sched[a]
+    cases.append(bad)
+    # a QKV of layer 1 moved in front of the last MLP_OUT of layer 0
+    q = int(np.flatnonzero((kind == QKV) & (layer == 1) & (tile == 1))[0])
+    m = int(np.flatnonzero((kind == MLP_OUT) & (layer == 0) & (tile == 1))[-1])
+    bad = sched.copy()
+    bad[m], bad[q] = sched[q], sched[m]
+    cases.append(bad)
+    cases.append(np.delete(sched, len(sched) // 2))          # a task missing
+    cases.append(np.insert(sched, 10, sched[3]))             # a task twice
+    for bad in cases:
+        with pytest.raises(AssertionError):
+            check_order(bad, splits, 2)

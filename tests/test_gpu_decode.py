@@ -611,11 +611,13 @@ def test_graph_ping_pong_equals_eager(lib, syn, pkg):
         assert np.array_equal(a, b)
 
 
-def test_batched_prefill_equals_single_steps(lib, syn, pkg):
+@pytest.mark.parametrize("mode", [0, 2])
+def test_batched_prefill_equals_single_steps(lib, syn, pkg, mode):
     """phonon_flow_batch_prefill_device over several streams and chunks
     (a fresh stream, a continuation after an existing context, a one-position
     chunk) gives, bit for bit, the outputs and appended K/V of decoding the
-    same positions one step at a time."""
+    same positions one step at a time, phase by phase (mode 0) and as one
+    launch (mode 2)."""
     layers = 2
     model = scaled_model(syn, 171, layers)
     views = pkg.Views()
@@ -643,6 +645,7 @@ def test_batched_prefill_equals_single_steps(lib, syn, pkg):
     # batched prefill
     total = sum(counts)
     bt, tables = setup(total)
+    assert lib.phonon_flow_batch_set_pipeline(bt.batch, mode)
     din = pkg.DeviceBuffer(lib, total * 512 * 4)
     dout = pkg.DeviceBuffer(lib, total * 512 * 4)
     din.upload(np.concatenate(xs))
@@ -689,17 +692,17 @@ def test_batched_prefill_equals_single_steps(lib, syn, pkg):
     assert np.array_equal(np.stack(want).view(np.uint32), got.view(np.uint32))
 
 
-@pytest.mark.parametrize("streams", [17, 40, 64])
-def test_paired_launches_equal_single_phase_launches(lib, syn, pkg, streams):
-    """Paired launches (one group's attention beside the other group's
-    projection chain, device-wide barriers between chain phases) give the
-    same bits as one launch per kernel, over several steps with ragged
-    contexts, in graph replay and in direct launches."""
+@pytest.mark.parametrize("streams", [1, 16, 17, 40, 64])
+def test_one_launch_step_equals_phase_launches(lib, syn, pkg, streams):
+    """The one-launch step (every layer's tasks in one dataflow launch) gives
+    the same bits as one launch per phase, over several steps with ragged
+    contexts, in graph replay and in direct launches; then again after the
+    contexts jump past the task schedule's headroom (schedule rebuilt)."""
     layers = 3
     model = scaled_model(syn, 181, layers)
     views = pkg.Views()
     w = views.layers(model)
-    max_pos = 700
+    max_pos = 1200
     table_len = (max_pos + 15) // 16
     blocks = streams * table_len
     rng = np.random.default_rng(182)
@@ -707,9 +710,10 @@ def test_paired_launches_equal_single_phase_launches(lib, syn, pkg, streams):
     ctx = rng.standard_normal((2, layers, max_pos, 512)).astype(np.float32)
     xs = rng.standard_normal((4, streams, 512)).astype(np.float32)
     runs = []
-    for pipeline, graph in ((0, 1), (1, 1), (1, 0)):
+    for flow, graph in ((0, 1), (2, 1), (2, 0)):
+        print(f"one-launch vs phases: streams={streams} flow={flow} graph={graph}", flush=True)
         bt = Batch(lib, w, layers, streams, max_pos, blocks)
-        assert lib.phonon_flow_batch_set_pipeline(bt.batch, pipeline)
+        assert lib.phonon_flow_batch_set_pipeline(bt.batch, flow)
         assert lib.phonon_flow_batch_set_graph(bt.batch, graph)
         ids = np.zeros(blocks, np.int32)
         assert lib.phonon_kv_pool_alloc(bt.pool, blocks, i32p(ids))
@@ -720,16 +724,18 @@ def test_paired_launches_equal_single_phase_launches(lib, syn, pkg, streams):
                 assert lib.phonon_kv_pool_write(bt.pool, i32p(tables[s_i]), table_len, 0,
                                                 int(lengths[s_i]), fp(ctx[0]), fp(ctx[1]),
                                                 max_pos)
-        pos = lengths.astype(np.uintp)
-        assert lib.phonon_flow_batch_set_streams(
-            bt.batch, streams, pos.ctypes.data_as(ctypes.POINTER(ctypes.c_size_t)),
-            i32p(tables), table_len)
         outs = []
-        for step in range(xs.shape[0]):
-            y = np.zeros((streams, 512), np.float32)
-            assert lib.phonon_flow_batch_step(bt.batch, fp(np.ascontiguousarray(xs[step])),
-                                              10000.0, fp(y)), pkg.last_error(lib)
-            outs.append(y.view(np.uint32).copy())
+        for jump in (0, 300):
+            pos = (lengths + jump).astype(np.uintp)
+            assert lib.phonon_flow_batch_set_streams(
+                bt.batch, streams, pos.ctypes.data_as(ctypes.POINTER(ctypes.c_size_t)),
+                i32p(tables), table_len)
+            for step in range(xs.shape[0] // 2):
+                y = np.zeros((streams, 512), np.float32)
+                x = np.ascontiguousarray(xs[step + (2 if jump else 0)])
+                assert lib.phonon_flow_batch_step(bt.batch, fp(x), 10000.0, fp(y)), \
+                    pkg.last_error(lib)
+                outs.append(y.view(np.uint32).copy())
         runs.append(outs)
         bt.close()
     for other in runs[1:]:
