@@ -118,9 +118,10 @@ int phonon_flow_batch_set_pipeline(PhononFlowBatch *batch, int mode);
  * on it. */
 int phonon_flow_batch_set_placement(PhononFlowBatch *batch, const pgpu_flow_placement *place);
 /* Task timeline of the one-launch step: while set, every step whose task
- * list fits `capacity` tasks writes, for task i, trace[3i .. 3i+2] = start,
- * inputs ready, end on the GPU's constant 100 MHz clock (trace: dev,
- * 3 * capacity words). NULL, 0 turns it off. */
+ * list fits `capacity` tasks writes, for task i, trace[4i .. 4i+2] = start,
+ * inputs ready, end on the GPU's constant 100 MHz clock and trace[4i+3] =
+ * where it ran (XCC id << 32 | HW_ID register) (trace: dev, 4 * capacity
+ * words). NULL, 0 turns it off. */
 int phonon_flow_batch_set_trace(PhononFlowBatch *batch, uint64_t *trace, size_t capacity);
 /* The one-launch step's current task list (pgpu_flow_schedule order):
  * returns the task count, and copies it when capacity suffices; 0 before the
@@ -134,6 +135,10 @@ int phonon_flow_batch_set_graph(PhononFlowBatch *batch, int use_graph);
 /* Waits for enqueued steps; returns 1 iff no step since the last call saw a
  * non-finite value or an uncovered position (and clears that record). */
 int phonon_flow_batch_sync(PhononFlowBatch *batch);
+/* The step status word since the last phonon_flow_batch_sync, without
+ * clearing it: bit 0 non-finite value, 1 position/block outside its table,
+ * 2 (value 4) a one-launch wait timed out. Waits for enqueued steps. */
+int phonon_flow_batch_status(PhononFlowBatch *batch, int *status);
 /* Current positions (host mirror) of the active streams. */
 int phonon_flow_batch_positions(const PhononFlowBatch *batch, size_t *positions);
 /* The batch's HIP stream (for event timing by the caller). */

@@ -170,8 +170,9 @@ typedef struct {
     unsigned *phase;               /* (dev) [layer_count][tiles][KINDS] x COUNTER_STRIDE, 0 */
     unsigned *split_done;          /* (dev) [layer_count][tiles*16][8], 0 */
     int *status;
-    uint64_t *trace;               /* (dev) NULL, or [tasks][3]: start, inputs ready, end
-                                      (constant 100 MHz clock) of each task */
+    uint64_t *trace;               /* (dev) NULL, or [tasks][4]: start, inputs ready, end
+                                      (constant 100 MHz clock) of each task, and where it
+                                      ran (XCC id << 32 | HW_ID register) */
 } pgpu_flow_step;
 
 /* Placement of each tile's projection chain in a task list, on a model

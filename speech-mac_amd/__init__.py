@@ -151,6 +151,7 @@ EXPORTS = {
     "phonon_flow_batch_schedule": (_sz, [_vp, ctypes.POINTER(ctypes.c_uint32), _sz]),
     "phonon_flow_batch_prefill_device": (_i, [_vp, _sz, _vp, _vp, _vp, _sz, _vp, _f, _vp]),
     "phonon_flow_batch_sync": (_i, [_vp]),
+    "phonon_flow_batch_status": (_i, [_vp, _vp]),
     "phonon_flow_batch_set_groups": (_i, [_vp, _sz]),
     "phonon_flow_batch_set_graph": (_i, [_vp, _i]),
     "phonon_flow_batch_positions": (_i, [_vp, _szp]),

@@ -83,9 +83,16 @@ __device__ inline FlowWait wait_for(const pgpu_flow_step &f, int layer, int tile
     return FlowWait{phase_counter(f, layer, tile, kind), 1, 0, target, f.status};
 }
 
-// Task timeline (optional): slot 0 = start, 1 = inputs ready, 2 = end.
+// Task timeline (optional): slot 0 = start, 1 = inputs ready, 2 = end,
+// 3 = where it ran: XCC id << 32 | HW_ID (CU, shader array and engine).
 __device__ inline void trace_mark(const pgpu_flow_step &f, int slot) {
-    if (f.trace && threadIdx.x == 0) f.trace[(size_t)blockIdx.x * 3 + slot] = wall_clock64();
+    if (!f.trace || threadIdx.x != 0) return;
+    f.trace[(size_t)blockIdx.x * 4 + slot] = wall_clock64();
+    if (slot == 0) {
+        const uint32_t xcc = __builtin_amdgcn_s_getreg((3 << 11) | 20);  // HW_REG_XCC_ID[3:0]
+        const uint32_t hw = __builtin_amdgcn_s_getreg((31 << 11) | 4);   // HW_REG_HW_ID
+        f.trace[(size_t)blockIdx.x * 4 + 3] = (uint64_t)xcc << 32 | hw;
+    }
 }
 
 // Completes a task: every wave's write-through stores have drained, then
@@ -136,6 +143,7 @@ __device__ inline GemmArgs base_args(const pgpu_flow_step &f, const pgpu_flow_la
     a.wscale = ly.scales[which];
     a.streams = f.streams;
     a.status = f.status;
+    a.wt_out = true;  // read by tasks on other XCDs within the launch
     return a;
 }
 

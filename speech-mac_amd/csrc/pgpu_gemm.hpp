@@ -30,9 +30,9 @@
 //   from zero (int8 and bf16 terms multiply exactly), then acc += scale*c,
 //   i.e. the reference phonon_q8_dot order "sum += scale * partial".
 //   BF16: the three MFMAs chain straight into the accumulator.
-// Stores of task outputs are device-scope write-through (sc1), so a task on
-// another XCD that waits for this one reads them from memory; see
-// pgpu_flow.hip.
+// q and appended K/V are stored device-scope write-through (sc1), and the
+// other outputs too when GemmArgs::wt_out is set, so a task on another XCD
+// that waits for this one reads them from memory; see pgpu_flow.hip.
 #pragma once
 
 #include <hip/hip_fp16.h>
@@ -73,6 +73,7 @@ struct GemmArgs {
     const int32_t *positions; // QKV and SRC_ATTN
     const float2 *rope;       // [8192][32] (cos, sin)
     int *status;
+    bool wt_out;              // STORE / RESIDUAL / GELU_SPLIT outputs write-through
 };
 
 // ---------------------------------------------------------------------------
@@ -95,19 +96,38 @@ __device__ inline void store_wt(uint2 *p, uint2 v) {
     __hip_atomic_store((uint64_t *)p, u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// A task output: write-through (read by tasks on other XCDs within the
+// launch) or a plain store (read after the launch, or by tasks on the same
+// XCD through its L2).
+template <class T>
+__device__ inline void store_out(T *p, T v, bool wt) {
+    if (wt)
+        store_wt(p, v);
+    else
+        *p = v;
+}
+
+__device__ inline void store_out(float *p, float4 v, bool wt) {
+    if (wt)
+        store_wt(p, v);
+    else
+        *(float4 *)p = v;
+}
+
 // 4 consecutive activations of stream s from column k (k % 4 == 0) as
-// split fragments: three 8-byte write-through stores.
-__device__ inline void store_split4_wt(uint16_t *__restrict__ xs, int s, int k, int kb_count,
-                                       const float *v) {
+// split fragments: three 8-byte stores.
+__device__ inline void store_split4(uint16_t *__restrict__ xs, int s, int k, int kb_count,
+                                    const float *v, bool wt) {
     uint16_t h[4], m[4], l[4];
 #pragma unroll
     for (int i = 0; i < 4; i++) split3(v[i], h[i], m[i], l[i]);
     const size_t base = split_index(s, k, 0, kb_count);
-    store_wt((uint2 *)(xs + base), make_uint2(h[0] | (uint32_t)h[1] << 16, h[2] | (uint32_t)h[3] << 16));
-    store_wt((uint2 *)(xs + base + 512),
-             make_uint2(m[0] | (uint32_t)m[1] << 16, m[2] | (uint32_t)m[3] << 16));
-    store_wt((uint2 *)(xs + base + 1024),
-             make_uint2(l[0] | (uint32_t)l[1] << 16, l[2] | (uint32_t)l[3] << 16));
+    store_out((uint2 *)(xs + base),
+              make_uint2(h[0] | (uint32_t)h[1] << 16, h[2] | (uint32_t)h[3] << 16), wt);
+    store_out((uint2 *)(xs + base + 512),
+              make_uint2(m[0] | (uint32_t)m[1] << 16, m[2] | (uint32_t)m[3] << 16), wt);
+    store_out((uint2 *)(xs + base + 1024),
+              make_uint2(l[0] | (uint32_t)l[1] << 16, l[2] | (uint32_t)l[3] << 16), wt);
 }
 
 // ---------------------------------------------------------------------------
@@ -454,6 +474,7 @@ template <int EPI>
 __device__ inline bool epilogue(const GemmArgs &a, const EpiOperands &e, const f32x4 &v, int s,
                                 int row0, bool live) {
     bool bad = false;
+    const bool wt = a.wt_out;
     if constexpr (EPI == EPI_STORE || EPI == EPI_RESIDUAL) {
         if (live) {
             float *o = a.out + (size_t)s * a.ld_out + row0;
@@ -467,7 +488,7 @@ __device__ inline bool epilogue(const GemmArgs &a, const EpiOperands &e, const f
                                         : __fadd_rn(add[r], v[r]);
                 bad |= !isfinite(y[r]);
             }
-            store_wt(o, make_float4(y[0], y[1], y[2], y[3]));
+            store_out(o, make_float4(y[0], y[1], y[2], y[3]), wt);
         }
     } else if constexpr (EPI == EPI_GELU_SPLIT) {
         if (live) {
@@ -477,7 +498,7 @@ __device__ inline bool epilogue(const GemmArgs &a, const EpiOperands &e, const f
                 g[r] = gelu_erf(v[r]);
                 bad |= !isfinite(g[r]);
             }
-            store_split4_wt(a.out_split, s, row0, a.out_kb, g);
+            store_split4(a.out_split, s, row0, a.out_kb, g, wt);
         }
     } else {  // EPI_QKV: rows [0,512) q, [512,1024) k, [1024,1536) v
         if (live) {

@@ -918,6 +918,12 @@ int phonon_flow_batch_step_device(PhononFlowBatch *b, const float *inputs, float
     return 1;
 }
 
+int phonon_flow_batch_status(PhononFlowBatch *b, int *status) {
+    if (!b || !status || !pgpu_stream_sync(b->stream))
+        return 0;
+    return pgpu_copy_d2h(b->stream, status, b->status, sizeof(int));
+}
+
 int phonon_flow_batch_sync(PhononFlowBatch *b) {
     if (!b || !pgpu_stream_sync(b->stream))
         return 0;
