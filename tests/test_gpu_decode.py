@@ -338,7 +338,16 @@ class Batch:
         self.lib.phonon_flow_model_destroy(self.model)
 
 
-def test_batch_ragged_shuffled_vs_oracle(lib, oracle, oracle_mod, syn, pkg):
+def set_step_mode(lib, batch, mode):
+    """Pipeline mode: 0 phase by phase, 1 auto, 2 one launch."""
+    assert lib.phonon_flow_batch_set_pipeline(batch, mode)
+
+
+@pytest.mark.parametrize("mode", [0, 2])
+def test_batch_ragged_shuffled_vs_oracle(lib, oracle, oracle_mod, syn, pkg, mode):
+    """Ragged contexts through shuffled tables, phase by phase and as one
+    launch, against the oracle's stack step per stream; the appended K/V rows
+    too."""
     layers = 2
     model = scaled_model(syn, 101, layers)
     om = oracle_for(oracle, oracle_mod, model)
@@ -350,6 +359,7 @@ def test_batch_ragged_shuffled_vs_oracle(lib, oracle, oracle_mod, syn, pkg):
     table_len = (max_pos + 15) // 16
     blocks = streams * table_len + 5
     bt = Batch(lib, w, layers, streams, max_pos, blocks)
+    set_step_mode(lib, bt.batch, mode)
     ids = np.zeros(blocks, np.int32)
     assert lib.phonon_kv_pool_alloc(bt.pool, blocks, i32p(ids))
     rng = np.random.default_rng(102)
@@ -392,11 +402,15 @@ def test_batch_ragged_shuffled_vs_oracle(lib, oracle, oracle_mod, syn, pkg):
     bt.close()
 
 
-@pytest.mark.parametrize("streams, layers, lo, hi", [(64, 12, 1, 2048), (256, 2, 256, 8192)])
-def test_batch_full_size_vs_oracle(lib, oracle, oracle_mod, syn, pkg, streams, layers, lo, hi):
+@pytest.mark.parametrize("streams, layers, lo, hi, mode",
+                         [(64, 12, 1, 2048, 1), (64, 12, 1, 2048, 0), (256, 2, 256, 8192, 1),
+                          (256, 2, 256, 8192, 2)])
+def test_batch_full_size_vs_oracle(lib, oracle, oracle_mod, syn, pkg, streams, layers, lo, hi,
+                                   mode):
     """The batched step at the benchmark shapes (B=64 x 12 layers, contexts
     U{1..2048}; B=256, contexts U{256..8192}) against the oracle's stack step
-    for every stream. Every stream attends its own shuffled copy of the same
+    for every stream, in the default mode (B=64: one launch; B=256: phase by
+    phase) and another. Every stream attends its own shuffled copy of the same
     context rows (one host array), so the check stays small on the host."""
     model = scaled_model(syn, 191, layers)
     om = oracle_for(oracle, oracle_mod, model)
@@ -410,6 +424,7 @@ def test_batch_full_size_vs_oracle(lib, oracle, oracle_mod, syn, pkg, streams, l
     keys = rng.standard_normal((layers, max_pos, 512)).astype(np.float32)
     vals = rng.standard_normal((layers, max_pos, 512)).astype(np.float32)
     bt = Batch(lib, w, layers, streams, max_pos, blocks)
+    set_step_mode(lib, bt.batch, mode)
     ids = np.zeros(blocks, np.int32)
     assert lib.phonon_kv_pool_alloc(bt.pool, blocks, i32p(ids))
     tables = np.ascontiguousarray(rng.permutation(ids).reshape(streams, table_len))
@@ -645,7 +660,7 @@ def test_batched_prefill_equals_single_steps(lib, syn, pkg, mode):
     # batched prefill
     total = sum(counts)
     bt, tables = setup(total)
-    assert lib.phonon_flow_batch_set_pipeline(bt.batch, mode)
+    set_step_mode(lib, bt.batch, mode)
     din = pkg.DeviceBuffer(lib, total * 512 * 4)
     dout = pkg.DeviceBuffer(lib, total * 512 * 4)
     din.upload(np.concatenate(xs))
@@ -713,7 +728,7 @@ def test_one_launch_step_equals_phase_launches(lib, syn, pkg, streams):
     for flow, graph in ((0, 1), (2, 1), (2, 0)):
         print(f"one-launch vs phases: streams={streams} flow={flow} graph={graph}", flush=True)
         bt = Batch(lib, w, layers, streams, max_pos, blocks)
-        assert lib.phonon_flow_batch_set_pipeline(bt.batch, flow)
+        set_step_mode(lib, bt.batch, flow)
         assert lib.phonon_flow_batch_set_graph(bt.batch, graph)
         ids = np.zeros(blocks, np.int32)
         assert lib.phonon_kv_pool_alloc(bt.pool, blocks, i32p(ids))
