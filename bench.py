@@ -10,8 +10,9 @@ the timed region starts; data is synthetic (seeded).
 Also reported in the same JSON line: B=1 decode (12 layers, context 256 ->
 256+steps), the single Q8 matvec (2048x512, rotating >256 MB of weight
 copies), one attention layer vs context length, the roofline of the
-dominant kernel (split attention) timed with HIP events on its stream, and
-the CPU baseline (the C restatement of the reference step, on host cores).
+dominant kernel (the one-launch step kernel at B=64) timed with HIP events
+on its stream, and the CPU baseline (the C restatement of the reference
+step, on host cores).
 
   python bench.py [--gpus 1] [--steps K] [--warmup W] [--batch 64] [--layers 12]
 """
@@ -134,7 +135,8 @@ def step_bytes(layers, contexts):
 
 def run_decode(pkg, lib, layers, streams, lengths, steps, warmup, seed, groups=None,
                eager=False):
-    d = DecodeSetup(pkg, lib, layers, streams, lengths, steps + warmup + 1, seed)
+    # headroom: the timed steps, then the roofline's timed launches
+    d = DecodeSetup(pkg, lib, layers, streams, lengths, steps + warmup + 41, seed)
     if groups:
         assert lib.phonon_flow_batch_set_groups(d.batch, groups)
     if eager:
@@ -160,13 +162,14 @@ def run_decode(pkg, lib, layers, streams, lengths, steps, warmup, seed, groups=N
 
 
 PMC_SUMMARY = "profiles/k_attention_b64_hbm_traffic.md"
+FLOW_PMC_SUMMARY = "profiles/k_flow_step_b64_hbm_traffic.md"
 
 
-def pmc_traffic():
-    """(traffic, algorithmic) bytes per split-attention launch recorded from
-    the rocprofv3 --pmc passes, or None if the summary is absent."""
+def pmc_traffic(summary=PMC_SUMMARY):
+    """(traffic, algorithmic) bytes per launch recorded from the rocprofv3
+    --pmc passes in `summary`, or None if the summary is absent."""
     try:
-        with open(os.path.join(ROOT, PMC_SUMMARY)) as f:
+        with open(os.path.join(ROOT, summary)) as f:
             fields = dict(line.split(":", 1) for line in f if line.startswith(
                 ("traffic_bytes_per_launch:", "algorithmic_bytes_per_launch:")))
         return (int(fields["traffic_bytes_per_launch"]),
@@ -235,6 +238,58 @@ def attention_roofline(pkg, lib, d, iterations=20):
             "status_clean": int(st[0]) == 0}
 
 
+def flow_roofline(pkg, lib, d, steps=20):
+    """Average duration of the one-launch step kernel (k_flow_step: every
+    layer's projections, K/V appends and attention of one decode step) on
+    the decode workload, timed with HIP events recorded on the batch's stream
+    right before and after each launch (the counter reset that follows it is
+    outside). Continues the decode from where the timed run left it. Returns
+    None if the batch does not run its step as one launch."""
+    events = []
+    for _ in range(2 * steps):
+        e = ctypes.c_void_p()
+        assert lib.pgpu_event_create(ctypes.byref(e))
+        events.append(e)
+    step_bytes_sum = 0
+    for i in range(steps):
+        step_bytes_sum += step_bytes(d.layers, d.positions() + 1)
+        assert lib.phonon_flow_batch_set_timing(d.batch, events[2 * i], events[2 * i + 1])
+        d.step()
+    assert lib.phonon_flow_batch_set_timing(d.batch, None, None)
+    assert lib.pgpu_stream_sync(d.stream)
+    clean = bool(lib.phonon_flow_batch_sync(d.batch))
+    total_ms = 0.0
+    for i in range(steps):
+        ms = ctypes.c_float()
+        if not lib.pgpu_event_elapsed_ms(events[2 * i], events[2 * i + 1], ctypes.byref(ms)):
+            total_ms = None   # events never recorded: the step ran phase by phase
+            break
+        total_ms += ms.value
+    for e in events:
+        lib.pgpu_event_destroy(e)
+    if total_ms is None:
+        return None
+    us = total_ms / steps * 1e3
+    per_launch = step_bytes_sum / steps
+    achieved = step_bytes_sum / (total_ms * 1e-3) / 1e9
+    measured = pmc_traffic(FLOW_PMC_SUMMARY)
+    traffic_bytes = None
+    if measured:
+        # Counter passes are a separate run (bench.py --pmc-program): their
+        # traffic/algorithmic ratio applied to this run's contexts.
+        traffic_bytes = int(round(per_launch * measured[0] / measured[1]))
+    return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+            "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic_bytes,
+            "traffic_source": f"{FLOW_PMC_SUMMARY} (FETCH_SIZE/WRITE_SIZE, copy-calibrated): "
+                              f"{measured[0]} B for {measured[1]} B algorithmic"
+                              if measured else None,
+            "kernel": "pgpu::k_flow_step<true>", "us_per_launch": round(us, 2),
+            "launches": steps, "algorithmic_bytes_per_launch": int(per_launch),
+            "algorithmic_bytes": "Q8 weights of 12 layers once + K/V of every attended key "
+                                 "per layer + the appended K/V row per stream per layer",
+            "status_clean": clean}
+
+
 def calibration_copy(pkg, lib, d, repeats=5):
     """A plain copy of known size for scaling hardware byte counters: all
     layers of positions [0, n) of stream 0 from the pool to contiguous rows
@@ -261,15 +316,22 @@ def calibration_copy(pkg, lib, d, repeats=5):
 
 def pmc_program(pkg, lib, args):
     """Short program for hardware-counter passes: the B=64 decode contexts,
-    20 launches of the split-attention kernel alone, then a calibration copy
-    of known size. Prints the algorithmic bytes of both."""
+    20 launches of the split-attention kernel alone, 10 decode steps (one
+    k_flow_step launch each), then a calibration copy of known size. Prints
+    the algorithmic bytes of each."""
     lengths = np.random.default_rng(args.seed).integers(1, 2049, size=args.batch) - 1
     d = DecodeSetup(pkg, lib, args.layers, args.batch, lengths, 64, args.seed)
     roof = attention_roofline(pkg, lib, d)
+    for _ in range(3):
+        d.step()
+    flow = flow_roofline(pkg, lib, d, steps=10)
     copied = calibration_copy(pkg, lib, d)
     d.close()
     print(json.dumps({"k_attention_algorithmic_bytes": roof["algorithmic_bytes_per_launch"],
                       "k_attention_us": roof["us_per_launch"],
+                      "k_flow_step_algorithmic_bytes": flow["algorithmic_bytes_per_launch"]
+                      if flow else None,
+                      "k_flow_step_us": flow["us_per_launch"] if flow else None,
                       "k_kv_copy_bytes_read": copied, "k_kv_copy_bytes_written": copied}),
           flush=True)
 
@@ -505,8 +567,10 @@ def main():
     gbs = r["bytes"] / (r["ms"] * 1e-3) / 1e9
     log(f"B={args.batch}: {ms_step * 1e3:.1f} us/step, {value:.0f} frames/s, {gbs:.0f} GB/s "
         f"({gbs / HBM_PEAK_GBS:.1%} of HBM), clean={r['clean']}")
-    roof = attention_roofline(pkg, lib, d)
-    log(f"attention kernel: {roof['us_per_launch']} us/launch, {roof['achieved']} GB/s")
+    # The dominant kernel: the one-launch step kernel where the batch runs
+    # its step as one launch (B=64), else the split-attention kernel.
+    roof = flow_roofline(pkg, lib, d) or attention_roofline(pkg, lib, d)
+    log(f"{roof['kernel']}: {roof['us_per_launch']} us/launch, {roof['achieved']} GB/s")
     d.close()
 
     line = {

@@ -128,6 +128,12 @@ int phonon_flow_batch_set_trace(PhononFlowBatch *batch, uint64_t *trace, size_t 
  * first one-launch step. */
 size_t phonon_flow_batch_schedule(const PhononFlowBatch *batch, uint32_t *schedule,
                                   size_t capacity);
+/* Kernel timing: while `before` and `after` are events (pgpu_event_create),
+ * each step launches its kernels directly (no graph replay) and records
+ * `before` right before and `after` right after its one-launch kernel
+ * (k_flow_step; the counter reset that follows it is outside) on the batch's
+ * stream. Phase-by-phase steps record nothing. NULL, NULL turns it off. */
+int phonon_flow_batch_set_timing(PhononFlowBatch *batch, void *before, void *after);
 /* use_graph = 1 (default): step_device replays a captured HIP graph;
  * 0: it launches the step's kernels directly (e.g. for a caller that is
  * itself capturing a graph). Results are identical. */

@@ -76,6 +76,7 @@ struct PhononFlowBatch {
     } graphs[2];
     size_t graph_victim;
     int eager;                         /* launch kernels directly, no graph */
+    void *time_before, *time_after;    /* events around the next step's kernels, or NULL */
     size_t groups;                     /* stream groups run concurrently */
     void *side[PH_MAX_GROUPS - 1];     /* HIP streams of groups 1.. */
     void *fork, *join[PH_MAX_GROUPS - 1];
@@ -739,7 +740,9 @@ static int enqueue_flow(PhononFlowBatch *b, const float *input, float *output, f
                               .status = b->status,
                               .trace = b->fl.trace_cap >= b->fl.tasks ? b->fl.trace : NULL};
     const size_t used = phase_words + layers * tiles * 16 * PH_HEADS;
-    return pgpu_flow_launch(b->stream, &f, &b->pool->kv) &&
+    return (!b->time_before || pgpu_event_record(b->time_before, b->stream)) &&
+           pgpu_flow_launch(b->stream, &f, &b->pool->kv) &&
+           (!b->time_after || pgpu_event_record(b->time_after, b->stream)) &&
            pgpu_flow_finish(b->stream, b->fl.counters, used, b->positions, (int)b->streams);
 }
 
@@ -848,6 +851,14 @@ int phonon_flow_batch_set_pipeline(PhononFlowBatch *b, int mode) {
     return 1;
 }
 
+int phonon_flow_batch_set_timing(PhononFlowBatch *b, void *before, void *after) {
+    if (!b || (!before) != (!after))
+        return 0;
+    b->time_before = before;
+    b->time_after = after;
+    return 1;
+}
+
 int phonon_flow_batch_set_graph(PhononFlowBatch *b, int use_graph) {
     if (!b)
         return 0;
@@ -866,7 +877,7 @@ int phonon_flow_batch_step_device(PhononFlowBatch *b, const float *inputs, float
     const int flow = flow_usable(b, 0);
     if (flow && !flow_prepare(b, 0))
         return 0;
-    if (b->eager) {
+    if (b->eager || b->time_before) {
         b->splits = splits_for(b, 0);
         if (!(flow ? enqueue_flow(b, inputs, outputs, theta)
                    : enqueue_step(b, inputs, outputs, theta)))
