@@ -44,27 +44,48 @@ struct AttnShared {
     float m[kUnitWaves], l[kUnitWaves];
 };
 
+// What a unit found, uniform over the unit.
+enum UnitState {
+    UNIT_EMPTY = 0,      // the split starts past the context (or the unit does not exist)
+    UNIT_LIVE = 1,       // keys attended; the partial is in wave 0
+    UNIT_UNCOVERED = 2,  // the context does not fit the grid or the table (flagged)
+};
+
+// A unit's inputs gate. probe() is issued with the unit's first loads;
+// pass(probe, needed) is then called by every thread before the unit reads
+// anything written in the current step (the one-launch step waits there for
+// the QKV tasks, unless the unit has nothing to do). NoGate: no wait.
+struct NoGate {
+    __device__ unsigned probe() const { return 0u; }
+    __device__ void pass(unsigned, bool) const {}
+};
+
 // Split `split` of head `head` of stream `s`, by the unit's 8 waves (`wave`
 // = 0..7 within the unit). Every wave of the work-group must call it (it
 // holds one work-group barrier); a unit without live keys (or that does not
-// `exist`: past the end of a grid) only takes part in the barrier. Returns
-// whether the unit had keys; if so, lanes 0..15 of wave 0 hold the split's
-// partial: max score mm, sum of exp ll and the unnormalised P.V dims
-// [4 lane, 4 lane + 4) in aa.
-//
-// `ready()` is called by every wave before the unit reads anything written
-// in the current step (the one-launch step waits there for the QKV tasks).
-struct NoBarrier {
-    __device__ void operator()() const {}
-};
-
-template <class Ready = NoBarrier>
-__device__ inline bool attend_unit(const AttnArgs &a, int head, int split, int s, int wave,
-                                   AttnShared &sh, bool exists, float4 &aa, float &mm,
-                                   float &ll, const Ready &ready = Ready{}) {
+// `exist`: past the end of a grid) only takes part in the barrier. If the
+// result is UNIT_LIVE, lanes 0..15 of wave 0 hold the split's partial: max
+// score mm, sum of exp ll and the unnormalised P.V dims [4 lane, 4 lane + 4)
+// in aa. `count` receives the stream's keys (0 if the unit does not exist).
+template <class Gate = NoGate>
+__device__ inline int attend_unit(const AttnArgs &a, int head, int split, int s, int wave,
+                                  AttnShared &sh, bool exists, float4 &aa, float &mm, float &ll,
+                                  int &count, const Gate &gate = Gate{}) {
     const int lane = threadIdx.x & 63;
     const int krow = lane >> 4, dcol = lane & 15;
-    const int count = exists ? a.positions[s] + 1 : 0;
+    const int first_block = split * 16 + wave * kBlocksPerWave;
+    // First loads, in flight together: the context length, the wave's block
+    // table entries (index clamped into the row; entries past the context
+    // are not used) and the gate's first check.
+    const int32_t *__restrict__ table = a.tables + (size_t)s * a.table_stride;
+    const int position = exists ? a.positions[s] : -1;
+    int ids[kBlocksPerWave];
+#pragma unroll
+    for (int t = 0; t < kBlocksPerWave; t++)
+        ids[t] = exists ? table[min(first_block + t, a.table_stride - 1)] : 0;
+    const unsigned probe = gate.probe();
+
+    count = position + 1;
     const int nsplit = (count + kSplitKeys - 1) / kSplitKeys;
     // A context the grid or the block table cannot cover is an error, never
     // a partial read: flag it once, and the unit computes nothing.
@@ -72,54 +93,38 @@ __device__ inline bool attend_unit(const AttnArgs &a, int head, int split, int s
         count >= 1 && nsplit <= a.max_splits && count <= a.table_stride * kBlockPos;
     if (exists && !covered && split == 0 && wave == 0 && lane == 0) atomicOr(a.status, 2);
     const bool live = covered && split * kSplitKeys < count;  // uniform per unit
+    gate.pass(probe, live);
 
     float m = -INFINITY, l = 0.0f;
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-    const int first_block = split * 16 + wave * kBlocksPerWave;
+    // Blocks [first_block, first_block + kBlocksPerWave) of this wave that
+    // hold keys; the others load nothing (their keys are masked below).
     const int stream_blocks = (count + kBlockPos - 1) / kBlockPos;
-    // < first_block: this wave has no keys
-    const int last_block = min(first_block + kBlocksPerWave - 1, stream_blocks - 1);
     float4 kr[kBlocksPerWave][4], vr[kBlocksPerWave][4];
-    // Block ids first (uniform), then every K/V load of the wave at once.
-    // Blocks past the context re-read the last valid block (their keys are
-    // masked below); an id outside the pool is flagged and replaced.
-    auto load_kv = [&]() {
-        const int32_t *__restrict__ table = a.tables + (size_t)s * a.table_stride;
+    if (live) {
         const float *layer_kv = a.kv + (size_t)a.layer * a.layer_stride;
-        int ids[kBlocksPerWave];
         bool bad_block = false;
 #pragma unroll
         for (int t = 0; t < kBlocksPerWave; t++) {
-            const int b = min(first_block + t, max(last_block, first_block));
-            const int id = last_block >= first_block ? table[b] : 0;
-            bad_block |= (unsigned)id >= a.blocks;
-            ids[t] = (unsigned)id < a.blocks ? id : 0;
-        }
-        if (last_block >= first_block) {
-#pragma unroll
-            for (int t = 0; t < kBlocksPerWave; t++) {
-                const float *tile =
-                    layer_kv + ((size_t)ids[t] * kHeads + head) * 2048 + lane * 4;
+            if (first_block + t < stream_blocks) {  // uniform per wave
+                // An id outside the pool is flagged and replaced.
+                bad_block |= (unsigned)ids[t] >= a.blocks;
+                const int id = (unsigned)ids[t] < a.blocks ? ids[t] : 0;
+                const float *tile = layer_kv + ((size_t)id * kHeads + head) * 2048 + lane * 4;
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
                     kr[t][i] = stream_load(tile + i * 256);
                     vr[t][i] = stream_load(tile + 1024 + i * 256);
                 }
-            }
-        } else {
-#pragma unroll
-            for (int t = 0; t < kBlocksPerWave; t++)
+            } else {
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
                     kr[t][i] = make_float4(0.f, 0.f, 0.f, 0.f);
                     vr[t][i] = make_float4(0.f, 0.f, 0.f, 0.f);
                 }
+            }
         }
         if (bad_block && lane == 0) atomicOr(a.status, 2);
-    };
-    ready();
-    if (live) {
-        load_kv();
         const float4 q = *(const float4 *)(a.q + (size_t)s * kWidth + head * kHeadDim + dcol * 4);
 
         float score[kBlocksPerWave][4];
@@ -171,7 +176,8 @@ __device__ inline bool attend_unit(const AttnArgs &a, int head, int split, int s
         }
     }
     __syncthreads();
-    if (!live || wave != 0 || lane >= 16) return live;
+    const int state = live ? UNIT_LIVE : (exists && !covered ? UNIT_UNCOVERED : UNIT_EMPTY);
+    if (!live || wave != 0 || lane >= 16) return state;
 
     // Merge the unit's waves (fixed order). A wave without keys has l = 0.
     mm = sh.m[0];
@@ -190,7 +196,7 @@ __device__ inline bool attend_unit(const AttnArgs &a, int head, int split, int s
         aa.z = fmaf(x.z, f, aa.z);
         aa.w = fmaf(x.w, f, aa.w);
     }
-    return true;
+    return state;
 }
 
 // attend_unit, then the split's (max, sum, unnormalised P.V) partial into
@@ -199,9 +205,10 @@ __device__ inline void attend_split(const AttnArgs &a, int head, int split, int 
                                     AttnShared &sh, bool exists = true) {
     float4 aa;
     float mm, ll;
-    const bool live = attend_unit(a, head, split, s, wave, sh, exists, aa, mm, ll);
+    int count;
+    const int state = attend_unit(a, head, split, s, wave, sh, exists, aa, mm, ll, count);
     const int lane = threadIdx.x & 63;
-    if (!live || wave != 0 || lane >= 16) return;
+    if (state != UNIT_LIVE || wave != 0 || lane >= 16) return;
     const size_t slot = ((size_t)s * kHeads + head) * a.max_splits + split;
     *(float4 *)(a.part_acc + slot * 64 + lane * 4) = aa;
     if (lane == 0) *(float2 *)(a.part_ml + slot * 2) = make_float2(mm, ll);

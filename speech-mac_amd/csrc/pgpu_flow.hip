@@ -50,37 +50,42 @@ __device__ inline unsigned *phase_counter(const pgpu_flow_step &f, int layer, in
                          PGPU_FLOW_COUNTER_STRIDE;
 }
 
-// Waits until each of `count` counters (stride `step` words) holds at least
-// `target`; one lane polls, then the work-group barrier releases the rest.
+// Wait until a counter holds at least `target` (no wait if `flag` is null):
+// one lane polls, then the work-group barrier releases the rest. probe()
+// issues the first check on its own, so that a task can send it together
+// with its other first loads and pass() only polls again if that check
+// found the count short.
 struct FlowWait {
     const unsigned *flag;
-    int count, step;
     unsigned target;
     int *status;
-    __device__ void operator()() const {
-        if (threadIdx.x == 0) {
+    __device__ unsigned probe() const {
+        return threadIdx.x == 0 && flag
+                   ? __hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                   : target;
+    }
+    // `first` is probe()'s value; needed = false skips the wait (the task
+    // found it has nothing to do). Every thread must call it.
+    __device__ void pass(unsigned first, bool needed = true) const {
+        if (threadIdx.x == 0 && needed && first < target) {
             const uint64_t t0 = wall_clock64();
-            for (int i = 0; i < count; i++) {
-                const unsigned *c = flag + (size_t)i * step;
-                while (__hip_atomic_load(c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
-                    if ((__hip_atomic_load(status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) &
-                         4) ||
-                        wall_clock64() - t0 > kWaitTicks) {
-                        atomicOr(status, 4);
-                        i = count;
-                        break;
-                    }
-                    __builtin_amdgcn_s_sleep(2);
+            while (__hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
+                if ((__hip_atomic_load(status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) & 4) ||
+                    wall_clock64() - t0 > kWaitTicks) {
+                    atomicOr(status, 4);
+                    break;
                 }
+                __builtin_amdgcn_s_sleep(2);
             }
         }
         __syncthreads();
     }
+    __device__ void operator()() const { pass(probe()); }
 };
 
 __device__ inline FlowWait wait_for(const pgpu_flow_step &f, int layer, int tile, int kind,
                                     unsigned target) {
-    return FlowWait{phase_counter(f, layer, tile, kind), 1, 0, target, f.status};
+    return FlowWait{phase_counter(f, layer, tile, kind), target, f.status};
 }
 
 // Task timeline (optional): slot 0 = start, 1 = inputs ready, 2 = end,
@@ -108,14 +113,16 @@ __device__ inline void flow_signal(const pgpu_flow_step &f, unsigned *flag,
     trace_mark(f, 2);
 }
 
-// Wait functor that also records when the inputs were ready.
+// FlowWait that also records when the inputs were ready.
 struct TracedWait {
     FlowWait w;
     const pgpu_flow_step *f;
-    __device__ void operator()() const {
-        w();
+    __device__ unsigned probe() const { return w.probe(); }
+    __device__ void pass(unsigned first, bool needed = true) const {
+        w.pass(first, needed);
         trace_mark(*f, 1);
     }
+    __device__ void operator()() const { pass(probe()); }
 };
 
 // Per-layer activation rows [tiles*16][512]: 0 = layer output x, 1 = r (out
@@ -150,20 +157,14 @@ __device__ inline GemmArgs base_args(const pgpu_flow_step &f, const pgpu_flow_la
 // ATTN task: split `split` of (stream t*16 + n, head). The split's partial
 // goes to the (layer, stream, head) group; the split that finds the others
 // done (its count reaches nsplit) merges them in split order into the
-// attention row, with the arithmetic of the single-phase merge.
+// attention row, with the arithmetic of the single-phase merge. A split past
+// the context ends without a trace; if the context is not covered, split 0
+// completes the (stream, head) with a zero row (the unit flags it).
 __device__ inline void attention_task(const pgpu_flow_step &f, const pgpu_paged_kv &kv,
                                       int layer, int tile, int index, AttnShared &sh) {
     const int head = index & 7, split = (index >> 3) & 255, n = index >> 11;
     const int s = tile * 16 + n;
     if (s >= f.streams) return;  // uniform
-    const int count = f.positions[s] + 1;
-    const int nsplit = (count + kSplitKeys - 1) / kSplitKeys;
-    const bool covered =
-        count >= 1 && nsplit <= f.max_splits && count <= f.table_stride * kBlockPos;
-    // Exactly one task per (stream, head) completes it: the last of its
-    // splits to finish, or split 0 when the context is not covered (the
-    // unit flags it; the row stays zero).
-    if (covered ? split >= nsplit : split != 0) return;
     const TracedWait ready{
         f.prefill
             ? wait_for(f, layer, 0, PGPU_FLOW_QKV_ALL, (unsigned)(PGPU_FLOW_QKV_TASKS * f.tiles))
@@ -187,8 +188,11 @@ __device__ inline void attention_task(const pgpu_flow_step &f, const pgpu_paged_
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     float4 aa;
     float mm, ll;
-    attend_unit(a, head, split, s, wave, sh, true, aa, mm, ll, ready);
-    if (wave != 0) return;
+    int count;
+    const int state = attend_unit(a, head, split, s, wave, sh, true, aa, mm, ll, count, ready);
+    if (wave != 0 || state == UNIT_EMPTY || (state == UNIT_UNCOVERED && split != 0)) return;
+    const bool covered = state == UNIT_LIVE;
+    const int nsplit = (count + kSplitKeys - 1) / kSplitKeys;
 
     const int lane = threadIdx.x & 63, d = (lane & 15) * 4;
     const size_t group = ((size_t)layer * f.tiles * 16 + s) * kHeads + head;
@@ -260,7 +264,7 @@ __device__ inline void flow_step_task(const pgpu_flow_step &f, const pgpu_paged_
         a.table_stride = f.table_stride;
         a.positions = f.positions;
         a.rope = (const float2 *)f.rope;
-        const FlowWait w = layer == 0 ? FlowWait{nullptr, 0, 0, 0u, f.status}
+        const FlowWait w = layer == 0 ? FlowWait{nullptr, 0u, f.status}
                                       : wait_for(f, layer - 1, tile, PGPU_FLOW_MLP_OUT,
                                                  PGPU_FLOW_MLP_OUT_TASKS);
         gemm_wide_task<SRC_LN, EPI_QKV, Q8>(a, index, tile, lds, TracedWait{w, &f});
