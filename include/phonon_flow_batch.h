@@ -108,7 +108,7 @@ int phonon_flow_batch_set_groups(PhononFlowBatch *batch, size_t groups);
  * one 16-stream tile's projections run while other tiles' attention
  * streams K/V, and no launch boundary separates the phases. mode 0: one
  * launch per phase of each layer. mode 1 (default): one launch for the
- * decode batch sizes where that measured faster on MI355X (33..96 streams),
+ * decode batch sizes where that measured faster on MI355X (17..160 streams),
  * phase by phase otherwise. Results are identical (both run the same task
  * code). Batches over 4096 streams, models over 63 layers and models mixing
  * Q8 and BF16 matrices always run phase by phase. */
@@ -128,6 +128,10 @@ int phonon_flow_batch_set_trace(PhononFlowBatch *batch, uint64_t *trace, size_t 
  * first one-launch step. */
 size_t phonon_flow_batch_schedule(const PhononFlowBatch *batch, uint32_t *schedule,
                                   size_t capacity);
+/* One-launch step: 256-key attention splits per ATTN task (1 or 2; 0, the
+ * default: chosen by the batch size). Results are identical for every
+ * choice. */
+int phonon_flow_batch_set_attention_rounds(PhononFlowBatch *batch, int rounds);
 /* Kernel timing: while `before` and `after` are events (pgpu_event_create),
  * each step launches its kernels directly (no graph replay) and records
  * `before` right before and `after` right after its one-launch kernel

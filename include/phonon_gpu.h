@@ -116,17 +116,19 @@ int pgpu_gemm_qkv(void *stream, const pgpu_matrix *w, const pgpu_gemm_input *x, 
  * `schedule`, and first waits (on counters in device memory) for the tasks
  * whose outputs it reads. Tasks, per 16-stream tile t and layer l:
  *   QKV    LayerNorm 1 + QKV projection + RoPE + K/V append, 64 rows each
- *   ATTN   one 256-key split of one (stream, head); the last split of a
- *          (stream, head) to finish merges all its splits
+ *   ATTN   attn_rounds (1..PGPU_FLOW_ATTN_ROUNDS) consecutive 256-key splits
+ *          of one (stream, head), one after the other; the task that
+ *          completes a (stream, head) merges all its splits
  *   OUT    out projection + residual, 64 rows each
  *   MLP_IN LayerNorm 2 + MLP in projection + GELU, 64 rows each
  *   MLP_OUT MLP out projection + residual, 16 rows each
  * Descriptor (PGPU_FLOW_TASK) bits: kind [0,3), layer [3,9), tile [9,17),
  * index [17,32); an
- * ATTN index is head | split << 3 | (stream in tile) << 11. A schedule must
- * list every task of the step once, each after every task it depends on
- * (then the launch cannot deadlock); ATTN tasks of (stream, head) must cover
- * the splits of its context. Status bit 4: a wait timed out (1 s), the
+ * ATTN index is head | unit << 3 | (stream in tile) << 11, for splits
+ * [unit, unit + 1) x attn_rounds. A schedule must list every task
+ * of the step once, each after every task it depends on (then the launch
+ * cannot deadlock); ATTN tasks of (stream, head) must cover the splits of
+ * its context. Status bit 4: a wait timed out (1 s), the
  * step's results are then unspecified. */
 #define PGPU_FLOW_QKV 0
 #define PGPU_FLOW_ATTN 1
@@ -140,6 +142,7 @@ int pgpu_gemm_qkv(void *stream, const pgpu_matrix *w, const pgpu_gemm_input *x, 
 #define PGPU_FLOW_MLP_IN_TASKS 32
 #define PGPU_FLOW_MLP_OUT_TASKS 32
 #define PGPU_FLOW_COUNTER_STRIDE 16 /* 32-bit words between phase counters */
+#define PGPU_FLOW_ATTN_ROUNDS 2    /* most 256-key splits per ATTN task */
 
 #define PGPU_FLOW_TASK(kind, layer, tile, index)                                      \
     ((uint32_t)(kind) | (uint32_t)(layer) << 3 | (uint32_t)(tile) << 9 |             \
@@ -169,6 +172,7 @@ typedef struct {
     unsigned tasks;
     unsigned *phase;               /* (dev) [layer_count][tiles][KINDS] x COUNTER_STRIDE, 0 */
     unsigned *split_done;          /* (dev) [layer_count][tiles*16][8], 0 */
+    int attn_rounds;               /* 256-key splits per ATTN task, 1..PGPU_FLOW_ATTN_ROUNDS */
     int *status;
     uint64_t *trace;               /* (dev) NULL, or [tasks][4]: start, inputs ready, end
                                       (constant 100 MHz clock) of each task, and where it
@@ -186,8 +190,8 @@ typedef struct {
 } pgpu_flow_placement;
 
 /* The task list of a step of `streams` streams through `layers` layers,
- * where stream s lists splits[s] attention splits per head (its context's
- * splits, plus any headroom: splits past the live context end at once).
+ * where stream s lists units[s] ATTN tasks per head (covering its context's
+ * splits, plus any headroom: tasks past the live context end at once).
  * Returns the task count; writes the descriptors when `schedule` holds at
  * least that many (`capacity`). Order: QKV of layer 0 for every tile; then
  * for each layer l and tile t, ATTN(t, l) by (stream, split, head) with
@@ -195,7 +199,7 @@ typedef struct {
  * earlier tiles interleaved as `place` (NULL: all zero) sets. Every task
  * follows the tasks it waits for; prefill = 1 lists all QKV of a layer
  * before its first ATTN (and ignores `place`). Host code only. */
-size_t pgpu_flow_schedule(size_t streams, size_t layers, const size_t *splits,
+size_t pgpu_flow_schedule(size_t streams, size_t layers, const size_t *units,
                           const pgpu_flow_placement *place, int prefill, uint32_t *schedule,
                           size_t capacity);
 /* prefill = 1: pseudo-streams of one stream share its block table, so an

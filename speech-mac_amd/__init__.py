@@ -155,6 +155,7 @@ EXPORTS = {
     "phonon_flow_batch_set_groups": (_i, [_vp, _sz]),
     "phonon_flow_batch_set_graph": (_i, [_vp, _i]),
     "phonon_flow_batch_set_timing": (_i, [_vp, _vp, _vp]),
+    "phonon_flow_batch_set_attention_rounds": (_i, [_vp, _i]),
     "phonon_flow_batch_positions": (_i, [_vp, _szp]),
     "phonon_flow_batch_stream": (_vp, [_vp]),
     "phonon_flow_batch_device_inputs": (_vp, [_vp]),

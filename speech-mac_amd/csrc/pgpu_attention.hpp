@@ -34,9 +34,8 @@ __device__ inline float4 stream_load(const float *p) {
 }
 
 // Waves per split unit and K/V blocks per wave: a unit of 8 waves x 2 blocks
-// covers one 256-key split; each wave keeps its 16 float4 of K/V in
-// flight at once (64 registers), so a 1024-thread work-group (2 units) stays
-// within 128 registers per lane.
+// covers one 256-key split; each wave keeps its 16 float4 of K/V in flight
+// at once (64 registers).
 constexpr int kUnitWaves = 8, kBlocksPerWave = 2;
 
 struct AttnShared {
@@ -60,29 +59,39 @@ struct NoGate {
     __device__ void pass(unsigned, bool) const {}
 };
 
-// Split `split` of head `head` of stream `s`, by the unit's 8 waves (`wave`
-// = 0..7 within the unit). Every wave of the work-group must call it (it
-// holds one work-group barrier); a unit without live keys (or that does not
-// `exist`: past the end of a grid) only takes part in the barrier. If the
-// result is UNIT_LIVE, lanes 0..15 of wave 0 hold the split's partial: max
-// score mm, sum of exp ll and the unnormalised P.V dims [4 lane, 4 lane + 4)
-// in aa. `count` receives the stream's keys (0 if the unit does not exist).
-template <class Gate = NoGate>
-__device__ inline int attend_unit(const AttnArgs &a, int head, int split, int s, int wave,
-                                  AttnShared &sh, bool exists, float4 &aa, float &mm, float &ll,
-                                  int &count, const Gate &gate = Gate{}) {
+// Splits split0 .. split0 + ROUNDS - 1 of head `head` of stream `s`, one
+// after the other, by the unit's 8 waves (`wave` = 0..7 within the unit).
+// Each split's partial is computed exactly as a one-round unit computes it;
+// the next split's K (V) loads go out as soon as the current split's K (V)
+// registers are consumed, so they overlap its softmax and wave merge. Every
+// wave of the work-group must call it (it holds one work-group barrier); a
+// unit without live keys (or that does not `exist`: past the end of a grid)
+// only takes part in the barrier. If the result is UNIT_LIVE, lanes 0..15 of
+// wave 0 hold the partial of each split r that starts inside the context:
+// max score mm[r], sum of exp ll[r] and the unnormalised P.V dims
+// [4 lane, 4 lane + 4) in aa[r]. `count` receives the stream's keys (0 if
+// the unit does not exist). sh holds ROUNDS AttnShared. `rounds` (at most
+// ROUNDS, uniform) limits the splits at run time.
+template <int ROUNDS = 1, class Gate = NoGate>
+__device__ inline int attend_unit(const AttnArgs &a, int head, int split0, int s, int wave,
+                                  AttnShared *sh, bool exists, float4 *aa, float *mm, float *ll,
+                                  int &count, const Gate &gate = Gate{}, int rounds = ROUNDS) {
     const int lane = threadIdx.x & 63;
     const int krow = lane >> 4, dcol = lane & 15;
-    const int first_block = split * 16 + wave * kBlocksPerWave;
     // First loads, in flight together: the context length, the wave's block
     // table entries (index clamped into the row; entries past the context
     // are not used) and the gate's first check.
     const int32_t *__restrict__ table = a.tables + (size_t)s * a.table_stride;
     const int position = exists ? a.positions[s] : -1;
-    int ids[kBlocksPerWave];
+    int ids[ROUNDS][kBlocksPerWave];
 #pragma unroll
-    for (int t = 0; t < kBlocksPerWave; t++)
-        ids[t] = exists ? table[min(first_block + t, a.table_stride - 1)] : 0;
+    for (int r = 0; r < ROUNDS; r++)
+#pragma unroll
+        for (int t = 0; t < kBlocksPerWave; t++)
+            ids[r][t] = exists && r < rounds
+                            ? table[min((split0 + r) * 16 + wave * kBlocksPerWave + t,
+                                        a.table_stride - 1)]
+                            : 0;
     const unsigned probe = gate.probe();
 
     count = position + 1;
@@ -91,110 +100,126 @@ __device__ inline int attend_unit(const AttnArgs &a, int head, int split, int s,
     // a partial read: flag it once, and the unit computes nothing.
     const bool covered =
         count >= 1 && nsplit <= a.max_splits && count <= a.table_stride * kBlockPos;
-    if (exists && !covered && split == 0 && wave == 0 && lane == 0) atomicOr(a.status, 2);
-    const bool live = covered && split * kSplitKeys < count;  // uniform per unit
+    if (exists && !covered && split0 == 0 && wave == 0 && lane == 0) atomicOr(a.status, 2);
+    const bool live = covered && split0 * kSplitKeys < count;  // uniform per unit
     gate.pass(probe, live);
 
-    float m = -INFINITY, l = 0.0f;
-    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-    // Blocks [first_block, first_block + kBlocksPerWave) of this wave that
-    // hold keys; the others load nothing (their keys are masked below).
-    const int stream_blocks = (count + kBlockPos - 1) / kBlockPos;
-    float4 kr[kBlocksPerWave][4], vr[kBlocksPerWave][4];
     if (live) {
+        // Blocks of this wave that hold keys load; the others load nothing
+        // (their keys are masked below).
+        const int stream_blocks = (count + kBlockPos - 1) / kBlockPos;
         const float *layer_kv = a.kv + (size_t)a.layer * a.layer_stride;
         bool bad_block = false;
+        float4 kr[kBlocksPerWave][4], vr[kBlocksPerWave][4];
+        auto load = [&](int r, bool values) {
 #pragma unroll
-        for (int t = 0; t < kBlocksPerWave; t++) {
-            if (first_block + t < stream_blocks) {  // uniform per wave
-                // An id outside the pool is flagged and replaced.
-                bad_block |= (unsigned)ids[t] >= a.blocks;
-                const int id = (unsigned)ids[t] < a.blocks ? ids[t] : 0;
-                const float *tile = layer_kv + ((size_t)id * kHeads + head) * 2048 + lane * 4;
+            for (int t = 0; t < kBlocksPerWave; t++) {
+                float4 *dst = values ? vr[t] : kr[t];
+                if ((split0 + r) * 16 + wave * kBlocksPerWave + t < stream_blocks) {  // uniform
+                    // An id outside the pool is flagged and replaced.
+                    bad_block |= (unsigned)ids[r][t] >= a.blocks;
+                    const int id = (unsigned)ids[r][t] < a.blocks ? ids[r][t] : 0;
+                    const float *tile = layer_kv + ((size_t)id * kHeads + head) * 2048 +
+                                        (values ? 1024 : 0) + lane * 4;
+#pragma unroll
+                    for (int i = 0; i < 4; i++) dst[i] = stream_load(tile + i * 256);
+                } else {
+#pragma unroll
+                    for (int i = 0; i < 4; i++) dst[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+                }
+            }
+        };
+        load(0, false);
+        load(0, true);
+        const float4 q = *(const float4 *)(a.q + (size_t)s * kWidth + head * kHeadDim + dcol * 4);
+#pragma unroll
+        for (int r = 0; r < ROUNDS; r++) {
+            if (r >= rounds || (split0 + r) * kSplitKeys >= count) break;  // uniform
+            const bool next = r + 1 < rounds && (split0 + r + 1) * kSplitKeys < count;
+            const int first_block = (split0 + r) * 16 + wave * kBlocksPerWave;
+            float m = -INFINITY, l = 0.0f;
+            float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+            float score[kBlocksPerWave][4];
+#pragma unroll
+            for (int t = 0; t < kBlocksPerWave; t++)
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
-                    kr[t][i] = stream_load(tile + i * 256);
-                    vr[t][i] = stream_load(tile + 1024 + i * 256);
+                    const float4 k = kr[t][i];
+                    float d = q.x * k.x;
+                    d = fmaf(q.y, k.y, d);
+                    d = fmaf(q.z, k.z, d);
+                    d = fmaf(q.w, k.w, d);
+                    d = row16_sum(d);
+                    const int key = (first_block + t) * kBlockPos + i * 4 + krow;
+                    score[t][i] = key < count ? d : -INFINITY;
+                    m = fmaxf(m, score[t][i]);
                 }
-            } else {
+            if (next) load(r + 1, false);
+            m = fmaxf(m, __shfl_xor(m, 16));
+            m = fmaxf(m, __shfl_xor(m, 32));
+#pragma unroll
+            for (int t = 0; t < kBlocksPerWave; t++)
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
-                    kr[t][i] = make_float4(0.f, 0.f, 0.f, 0.f);
-                    vr[t][i] = make_float4(0.f, 0.f, 0.f, 0.f);
+                    // Slots past the context hold whatever the pool held
+                    // before: they are skipped, never multiplied by a zero
+                    // weight.
+                    if (score[t][i] == -INFINITY) continue;
+                    const float e = expf(score[t][i] - m);
+                    l += e;
+                    acc.x = fmaf(e, vr[t][i].x, acc.x);
+                    acc.y = fmaf(e, vr[t][i].y, acc.y);
+                    acc.z = fmaf(e, vr[t][i].z, acc.z);
+                    acc.w = fmaf(e, vr[t][i].w, acc.w);
                 }
+            if (next) load(r + 1, true);
+            // Lanes of one key row hold the same l; sum the four rows.
+            l += __shfl_xor(l, 16);
+            l += __shfl_xor(l, 32);
+            acc.x += __shfl_xor(acc.x, 16);
+            acc.y += __shfl_xor(acc.y, 16);
+            acc.z += __shfl_xor(acc.z, 16);
+            acc.w += __shfl_xor(acc.w, 16);
+            acc.x += __shfl_xor(acc.x, 32);
+            acc.y += __shfl_xor(acc.y, 32);
+            acc.z += __shfl_xor(acc.z, 32);
+            acc.w += __shfl_xor(acc.w, 32);
+            if (lane < 16) sh[r].acc[wave][lane] = acc;
+            if (lane == 0) {
+                sh[r].m[wave] = m;
+                sh[r].l[wave] = l;
             }
         }
         if (bad_block && lane == 0) atomicOr(a.status, 2);
-        const float4 q = *(const float4 *)(a.q + (size_t)s * kWidth + head * kHeadDim + dcol * 4);
-
-        float score[kBlocksPerWave][4];
-#pragma unroll
-        for (int t = 0; t < kBlocksPerWave; t++)
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const float4 k = kr[t][i];
-                float d = q.x * k.x;
-                d = fmaf(q.y, k.y, d);
-                d = fmaf(q.z, k.z, d);
-                d = fmaf(q.w, k.w, d);
-                d = row16_sum(d);
-                const int key = (first_block + t) * kBlockPos + i * 4 + krow;
-                score[t][i] = key < count ? d : -INFINITY;
-                m = fmaxf(m, score[t][i]);
-            }
-        m = fmaxf(m, __shfl_xor(m, 16));
-        m = fmaxf(m, __shfl_xor(m, 32));
-#pragma unroll
-        for (int t = 0; t < kBlocksPerWave; t++)
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                // Slots past the context hold whatever the pool held before:
-                // they are skipped, never multiplied by a zero weight.
-                if (score[t][i] == -INFINITY) continue;
-                const float e = expf(score[t][i] - m);
-                l += e;
-                acc.x = fmaf(e, vr[t][i].x, acc.x);
-                acc.y = fmaf(e, vr[t][i].y, acc.y);
-                acc.z = fmaf(e, vr[t][i].z, acc.z);
-                acc.w = fmaf(e, vr[t][i].w, acc.w);
-            }
-        // Lanes of one key row hold the same l; sum the four rows.
-        l += __shfl_xor(l, 16);
-        l += __shfl_xor(l, 32);
-        acc.x += __shfl_xor(acc.x, 16);
-        acc.y += __shfl_xor(acc.y, 16);
-        acc.z += __shfl_xor(acc.z, 16);
-        acc.w += __shfl_xor(acc.w, 16);
-        acc.x += __shfl_xor(acc.x, 32);
-        acc.y += __shfl_xor(acc.y, 32);
-        acc.z += __shfl_xor(acc.z, 32);
-        acc.w += __shfl_xor(acc.w, 32);
-        if (lane < 16) sh.acc[wave][lane] = acc;
-        if (lane == 0) {
-            sh.m[wave] = m;
-            sh.l[wave] = l;
-        }
     }
     __syncthreads();
     const int state = live ? UNIT_LIVE : (exists && !covered ? UNIT_UNCOVERED : UNIT_EMPTY);
     if (!live || wave != 0 || lane >= 16) return state;
 
-    // Merge the unit's waves (fixed order). A wave without keys has l = 0.
-    mm = sh.m[0];
+    // Merge the unit's waves (fixed order), per split. A wave without keys
+    // has l = 0.
 #pragma unroll
-    for (int w = 1; w < kUnitWaves; w++) mm = fmaxf(mm, sh.m[w]);
-    ll = 0.0f;
-    aa = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int r = 0; r < ROUNDS; r++) {
+        if (r >= rounds || (split0 + r) * kSplitKeys >= count) break;
+        float m = sh[r].m[0];
 #pragma unroll
-    for (int w = 0; w < kUnitWaves; w++) {
-        if (sh.l[w] == 0.0f) continue;
-        const float f = expf(sh.m[w] - mm);
-        ll = fmaf(sh.l[w], f, ll);
-        const float4 x = sh.acc[w][lane];
-        aa.x = fmaf(x.x, f, aa.x);
-        aa.y = fmaf(x.y, f, aa.y);
-        aa.z = fmaf(x.z, f, aa.z);
-        aa.w = fmaf(x.w, f, aa.w);
+        for (int w = 1; w < kUnitWaves; w++) m = fmaxf(m, sh[r].m[w]);
+        float l = 0.0f;
+        float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+        for (int w = 0; w < kUnitWaves; w++) {
+            if (sh[r].l[w] == 0.0f) continue;
+            const float f = expf(sh[r].m[w] - m);
+            l = fmaf(sh[r].l[w], f, l);
+            const float4 x = sh[r].acc[w][lane];
+            acc.x = fmaf(x.x, f, acc.x);
+            acc.y = fmaf(x.y, f, acc.y);
+            acc.z = fmaf(x.z, f, acc.z);
+            acc.w = fmaf(x.w, f, acc.w);
+        }
+        mm[r] = m;
+        ll[r] = l;
+        aa[r] = acc;
     }
     return state;
 }
@@ -206,7 +231,7 @@ __device__ inline void attend_split(const AttnArgs &a, int head, int split, int 
     float4 aa;
     float mm, ll;
     int count;
-    const int state = attend_unit(a, head, split, s, wave, sh, exists, aa, mm, ll, count);
+    const int state = attend_unit(a, head, split, s, wave, &sh, exists, &aa, &mm, &ll, count);
     const int lane = threadIdx.x & 63;
     if (state != UNIT_LIVE || wave != 0 || lane >= 16) return;
     const size_t slot = ((size_t)s * kHeads + head) * a.max_splits + split;

@@ -154,15 +154,20 @@ __device__ inline GemmArgs base_args(const pgpu_flow_step &f, const pgpu_flow_la
     return a;
 }
 
-// ATTN task: split `split` of (stream t*16 + n, head). The split's partial
-// goes to the (layer, stream, head) group; the split that finds the others
-// done (its count reaches nsplit) merges them in split order into the
-// attention row, with the arithmetic of the single-phase merge. A split past
-// the context ends without a trace; if the context is not covered, split 0
+// ATTN task: splits [unit, unit + 1) x f.attn_rounds of (stream t*16 + n,
+// head), one after the other. Each split's partial goes
+// to its slot of the (layer, stream, head) group; the task whose splits
+// complete the group's count (nsplit) merges all partials in split order
+// into the attention row, with the arithmetic of the single-phase merge. A
+// task that holds every split merges them from registers. A task past the
+// context ends without a trace; if the context is not covered, pair 0
 // completes the (stream, head) with a zero row (the unit flags it).
+constexpr int kFlowRounds = PGPU_FLOW_ATTN_ROUNDS;
+static_assert(kFlowRounds * sizeof(AttnShared) <= kTaskLds * 2, "attention LDS");
+
 __device__ inline void attention_task(const pgpu_flow_step &f, const pgpu_paged_kv &kv,
-                                      int layer, int tile, int index, AttnShared &sh) {
-    const int head = index & 7, split = (index >> 3) & 255, n = index >> 11;
+                                      int layer, int tile, int index, AttnShared *sh) {
+    const int head = index & 7, split0 = ((index >> 3) & 255) * f.attn_rounds, n = index >> 11;
     const int s = tile * 16 + n;
     if (s >= f.streams) return;  // uniform
     const TracedWait ready{
@@ -186,36 +191,46 @@ __device__ inline void attention_task(const pgpu_flow_step &f, const pgpu_paged_
     a.part_ml = nullptr;
     a.status = f.status;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    float4 aa;
-    float mm, ll;
+    float4 aa[kFlowRounds];
+    float mm[kFlowRounds], ll[kFlowRounds];
     int count;
-    const int state = attend_unit(a, head, split, s, wave, sh, true, aa, mm, ll, count, ready);
-    if (wave != 0 || state == UNIT_EMPTY || (state == UNIT_UNCOVERED && split != 0)) return;
+    const int state = attend_unit<kFlowRounds>(a, head, split0, s, wave, sh, true, aa, mm, ll,
+                                               count, ready, f.attn_rounds);
+    if (wave != 0 || state == UNIT_EMPTY || (state == UNIT_UNCOVERED && split0 != 0)) return;
     const bool covered = state == UNIT_LIVE;
     const int nsplit = (count + kSplitKeys - 1) / kSplitKeys;
+    const int rounds = min(f.attn_rounds, nsplit - split0);  // splits of this task (if covered)
 
     const int lane = threadIdx.x & 63, d = (lane & 15) * 4;
     const size_t group = ((size_t)layer * f.tiles * 16 + s) * kHeads + head;
     float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     bool finish = !covered, bad = false;
-    if (covered && nsplit == 1) {
+    if (covered && nsplit <= f.attn_rounds) {
         float mx = -INFINITY, total = 0.0f;
-        const float acc[4] = {aa.x, aa.y, aa.z, aa.w};
-        merge_step(mx, total, v, 4, mm, ll, acc);
+#pragma unroll
+        for (int r = 0; r < kFlowRounds; r++) {
+            if (r >= nsplit) break;
+            const float acc[4] = {aa[r].x, aa[r].y, aa[r].z, aa[r].w};
+            merge_step(mx, total, v, 4, mm[r], ll[r], acc);
+        }
         bad = merge_finish<4>(total, v);
         finish = true;
     } else if (covered) {
         float *acc = f.part_acc + group * f.max_splits * 64;
         float *ml = f.part_ml + group * f.ml_group;
-        if (lane < 16) store_wt(acc + split * 64 + d, aa);
-        if (lane == 0) store_wt((float2 *)(ml + 2 * split), make_float2(mm, ll));
+#pragma unroll
+        for (int r = 0; r < kFlowRounds; r++) {
+            if (r >= rounds) break;
+            if (lane < 16) store_wt(acc + (split0 + r) * 64 + d, aa[r]);
+            if (lane == 0) store_wt((float2 *)(ml + 2 * (split0 + r)), make_float2(mm[r], ll[r]));
+        }
         __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
         unsigned done = 0;
         if (lane == 0)
-            done = __hip_atomic_fetch_add(f.split_done + group, 1u, __ATOMIC_RELAXED,
-                                          __HIP_MEMORY_SCOPE_AGENT);
+            done = __hip_atomic_fetch_add(f.split_done + group, (unsigned)rounds,
+                                          __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         done = __shfl(done, 0);
-        if (done + 1 == (unsigned)nsplit) {
+        if (done + rounds == (unsigned)nsplit) {
             bad = merge_splits<4>(acc, ml, nsplit, d, v);
             finish = true;
         }
@@ -273,7 +288,7 @@ __device__ inline void flow_step_task(const pgpu_flow_step &f, const pgpu_paged_
         break;
     }
     case PGPU_FLOW_ATTN:
-        attention_task(f, kv, layer, tile, index, *(AttnShared *)lds4);
+        attention_task(f, kv, layer, tile, index, (AttnShared *)lds4);
         break;
     case PGPU_FLOW_OUT: {
         GemmArgs a = base_args(f, ly, 1);
@@ -352,6 +367,7 @@ extern "C" int pgpu_flow_launch(void *stream, const pgpu_flow_step *step,
         step->ml_group < 2 * step->max_splits || step->ml_group % 32 || !step->tables ||
         !step->positions || step->table_stride <= 0 || !step->rope || !step->schedule ||
         !step->tasks || !step->phase || !step->split_done || !step->status ||
+        step->attn_rounds < 1 || step->attn_rounds > PGPU_FLOW_ATTN_ROUNDS ||
         step->pool_offset < 0 || step->pool_offset + step->layer_count > kv->layers)
         return bad_arguments("pgpu_flow_launch");
     if (step->q8)

@@ -5,8 +5,8 @@
  * and the launch cannot deadlock.
  *
  * Within that constraint the list is laid out on a model clock: attention
- * split tasks advance the clock by unit_us each (they stream K/V from HBM at
- * a steady rate), and each projection phase of a tile's chain is listed
+ * tasks advance the clock by unit_us each (they stream K/V from HBM at a
+ * steady rate), and each projection phase of a tile's chain is listed
  * after_us[phase] after the tile's last attention task, i.e. about when its
  * inputs will be ready. A task listed too early holds a work-group slot
  * while it waits; one listed too late delays its chain. The next layer's
@@ -91,24 +91,26 @@ static void flush(Queue *q, int tile, uint32_t *d, size_t *k) {
     }
 }
 
-pgpu_flow_placement ph_flow_default_placement(void) {
-    /* Clock in split tasks (128 KB of K/V each): at B = 64 a 16-stream tile's
-     * attention is ~640 of them. */
-    const pgpu_flow_placement p = {1.0f, {350.0f, 800.0f, 1250.0f, 1700.0f}};
-    return p;
+pgpu_flow_placement ph_flow_default_placement(int rounds) {
+    /* Clock in ATTN tasks (rounds 256-key splits, 128 KB of K/V each): at
+     * B = 64 a 16-stream tile's attention is ~640 splits. Measured on
+     * MI355X at B = 64 (one split per task) and B = 128 (two). */
+    const pgpu_flow_placement one = {1.0f, {350.0f, 800.0f, 1250.0f, 1700.0f}};
+    const pgpu_flow_placement two = {2.0f, {750.0f, 1350.0f, 1950.0f, 2550.0f}};
+    return rounds > 1 ? two : one;
 }
 
-size_t pgpu_flow_schedule(size_t streams, size_t layers, const size_t *splits,
+size_t pgpu_flow_schedule(size_t streams, size_t layers, const size_t *units,
                           const pgpu_flow_placement *place, int prefill, uint32_t *schedule,
                           size_t capacity) {
-    if (!streams || !layers || !splits)
+    if (!streams || !layers || !units)
         return 0;
     const size_t tiles = (streams + 15) / 16;
-    size_t units = 0;
+    size_t attn = 0;
     for (size_t s = 0; s < streams; s++)
-        units += splits[s];
+        attn += units[s];
     const size_t chain = PGPU_FLOW_OUT_TASKS + PGPU_FLOW_MLP_IN_TASKS + PGPU_FLOW_MLP_OUT_TASKS;
-    const size_t tasks = layers * tiles * (PGPU_FLOW_QKV_TASKS + chain) + layers * PH_HEADS * units;
+    const size_t tasks = layers * tiles * (PGPU_FLOW_QKV_TASKS + chain) + layers * PH_HEADS * attn;
     if (!schedule || capacity < tasks)
         return tasks;
     double after[4] = {0.0, 0.0, 0.0, 0.0}, unit_us = 0.0;
@@ -135,7 +137,7 @@ size_t pgpu_flow_schedule(size_t streams, size_t layers, const size_t *splits,
         for (size_t t = 0; t < tiles; t++) {
             flush(&q, (int)t, d, &k);  /* tile t's chain, through its QKV of layer l */
             for (size_t n = 0; n < 16 && t * 16 + n < streams; n++)
-                for (size_t j = 0; j < splits[t * 16 + n]; j++)
+                for (size_t j = 0; j < units[t * 16 + n]; j++)
                     for (uint32_t h = 0; h < PH_HEADS; h++) {
                         while (q.count && q.items[0].at <= now) {
                             emit_phase(d, &k, q.items[0].kind, q.items[0].layer,

@@ -52,6 +52,10 @@ struct PhononFlowBatch {
         uint32_t *schedule, *host_schedule;
         size_t schedule_cap, host_cap, tasks;
         size_t *cover;              /* [max_streams] splits the schedule lists per stream */
+        size_t *units;              /* [max_streams] ATTN tasks per (stream, head) for them */
+        int rounds;                 /* splits per ATTN task the schedule was built for */
+        int rounds_set;             /* 0: by batch size, else the caller's choice */
+        int place_set;              /* the caller set the placement */
         size_t streams, layers;     /* what the schedule was built for (0: none) */
         int prefill;
         unsigned version;           /* bumped by every rebuild */
@@ -369,6 +373,7 @@ void phonon_flow_batch_destroy(PhononFlowBatch *b) {
     free(b->host_positions);
     free(b->fl.host_schedule);
     free(b->fl.cover);
+    free(b->fl.units);
     free(b);
 }
 
@@ -396,7 +401,7 @@ int phonon_flow_batch_create(const PhononFlowModel *model, PhononKvPool *pool,
     const size_t slots = max_streams * PH_HEADS * b->max_splits;
     b->groups = PH_DEFAULT_GROUPS;
     b->flow = 1;
-    b->fl.place = ph_flow_default_placement();
+    b->fl.place = ph_flow_default_placement(1);
     int ok = pgpu_stream_create(&b->stream) && pgpu_event_create(&b->fork);
     for (size_t g = 0; ok && g + 1 < PH_MAX_GROUPS; g++)
         ok = pgpu_stream_create(&b->side[g]) && pgpu_event_create(&b->join[g]);
@@ -416,9 +421,10 @@ int phonon_flow_batch_create(const PhononFlowModel *model, PhononKvPool *pool,
     b->scratch.max_splits = (int)b->max_splits;
     b->host_positions = calloc(max_streams, sizeof(size_t));
     b->fl.cover = calloc(max_streams, sizeof(size_t));
+    b->fl.units = calloc(max_streams, sizeof(size_t));
     ok = ok && b->x && b->r && b->q && b->in && b->out && b->rows && b->xh && b->positions &&
          b->tables && b->status && b->scratch.part_acc && b->scratch.part_ml &&
-         b->host_positions && b->fl.cover;
+         b->host_positions && b->fl.cover && b->fl.units;
     /* Zero everything a kernel may read before writing (padding streams of the
      * split fragments, positions, status). */
     ok = ok && pgpu_memset(b->stream, b->xh, 0, split2048) &&
@@ -599,8 +605,21 @@ static size_t flow_ml_group(const PhononFlowBatch *b) {
 /* When a step runs as one launch: always (flow = 2), or, by default
  * (flow = 1), for the decode batch sizes where it measured faster on MI355X
  * than one launch per phase (PH_FLOW_MIN_TILES..PH_FLOW_MAX_TILES 16-stream
- * tiles; prefill and larger batches are attention-bound, and the separate
- * attention kernel streams K/V faster). */
+ * tiles; B = 1 is faster phase by phase, and prefill and larger batches are
+ * attention-bound, where the separate attention kernel streams K/V
+ * faster). */
+/* Splits per ATTN task: two where the step's attention throughput matters
+ * more than its latency per tile (few tiles, or many), one in between
+ * (measured on MI355X). */
+static int flow_rounds(const PhononFlowBatch *b) {
+    if (b->fl.rounds_set)
+        return b->fl.rounds_set;
+    const size_t tiles = (b->streams + 15) / 16;
+    return tiles >= PH_FLOW_ONE_ROUND_MIN_TILES && tiles <= PH_FLOW_ONE_ROUND_MAX_TILES
+               ? 1
+               : PGPU_FLOW_ATTN_ROUNDS;
+}
+
 static int flow_usable(const PhononFlowBatch *b, int prefill) {
     if (!b->flow || b->model->q8 < 0 || b->model->layers > 63 || b->streams > 4096)
         return 0;
@@ -655,7 +674,9 @@ static int flow_reserve(PhononFlowBatch *b, size_t streams) {
  * end at once. */
 static int flow_schedule(PhononFlowBatch *b, int prefill) {
     const size_t streams = b->streams, layers = b->model->layers;
-    int valid = b->fl.streams == streams && b->fl.layers == layers && b->fl.prefill == prefill;
+    const int rounds = flow_rounds(b);
+    int valid = b->fl.streams == streams && b->fl.layers == layers && b->fl.prefill == prefill &&
+                b->fl.rounds == rounds;
     for (size_t s = 0; valid && s < streams; s++)
         valid = (b->host_positions[s] + PH_SPLIT_KEYS) / PH_SPLIT_KEYS <= b->fl.cover[s];
     if (valid)
@@ -664,9 +685,12 @@ static int flow_schedule(PhononFlowBatch *b, int prefill) {
     for (size_t s = 0; s < streams; s++) {
         size_t need = (b->host_positions[s] + PH_FLOW_HEADROOM + PH_SPLIT_KEYS) / PH_SPLIT_KEYS;
         b->fl.cover[s] = need < b->max_splits ? need : b->max_splits;
+        b->fl.units[s] = (b->fl.cover[s] + rounds - 1) / rounds;
     }
+    const pgpu_flow_placement place =
+        b->fl.place_set ? b->fl.place : ph_flow_default_placement(rounds);
     const size_t tasks =
-        pgpu_flow_schedule(streams, layers, b->fl.cover, &b->fl.place, prefill, NULL, 0);
+        pgpu_flow_schedule(streams, layers, b->fl.units, &place, prefill, NULL, 0);
     if (tasks > b->fl.host_cap) {
         uint32_t *grown = realloc(b->fl.host_schedule, tasks * sizeof(uint32_t));
         if (!grown)
@@ -675,7 +699,7 @@ static int flow_schedule(PhononFlowBatch *b, int prefill) {
         b->fl.host_cap = tasks;
     }
     uint32_t *d = b->fl.host_schedule;
-    const size_t k = pgpu_flow_schedule(streams, layers, b->fl.cover, &b->fl.place, prefill, d,
+    const size_t k = pgpu_flow_schedule(streams, layers, b->fl.units, &place, prefill, d,
                                         b->fl.host_cap);
     if (k != tasks)
         return ph_fail("flow schedule: task count mismatch");
@@ -691,6 +715,7 @@ static int flow_schedule(PhononFlowBatch *b, int prefill) {
     }
     if (!pgpu_copy_h2d(b->stream, b->fl.schedule, d, tasks * sizeof(uint32_t)))
         return 0;
+    b->fl.rounds = rounds;
     b->fl.tasks = tasks;
     b->fl.streams = streams;
     b->fl.layers = layers;
@@ -738,7 +763,8 @@ static int enqueue_flow(PhononFlowBatch *b, const float *input, float *output, f
                               .phase = b->fl.counters,
                               .split_done = b->fl.counters + phase_words,
                               .status = b->status,
-                              .trace = b->fl.trace_cap >= b->fl.tasks ? b->fl.trace : NULL};
+                              .trace = b->fl.trace_cap >= b->fl.tasks ? b->fl.trace : NULL,
+                              .attn_rounds = b->fl.rounds};
     const size_t used = phase_words + layers * tiles * 16 * PH_HEADS;
     return (!b->time_before || pgpu_event_record(b->time_before, b->stream)) &&
            pgpu_flow_launch(b->stream, &f, &b->pool->kv) &&
@@ -817,7 +843,8 @@ int phonon_flow_batch_set_groups(PhononFlowBatch *b, size_t groups) {
 int phonon_flow_batch_set_placement(PhononFlowBatch *b, const pgpu_flow_placement *place) {
     if (!b)
         return 0;
-    b->fl.place = place ? *place : ph_flow_default_placement();
+    b->fl.place = place ? *place : ph_flow_default_placement(1);
+    b->fl.place_set = place != NULL;
     b->fl.streams = 0; /* rebuild the task list */
     drop_graphs(b);
     return 1;
@@ -848,6 +875,13 @@ int phonon_flow_batch_set_pipeline(PhononFlowBatch *b, int mode) {
         drop_graphs(b);
         b->flow = mode;
     }
+    return 1;
+}
+
+int phonon_flow_batch_set_attention_rounds(PhononFlowBatch *b, int rounds) {
+    if (!b || rounds < 0 || rounds > PGPU_FLOW_ATTN_ROUNDS)
+        return 0;
+    b->fl.rounds_set = rounds;
     return 1;
 }
 

@@ -710,9 +710,10 @@ def test_batched_prefill_equals_single_steps(lib, syn, pkg, mode):
 @pytest.mark.parametrize("streams", [1, 16, 17, 40, 64])
 def test_one_launch_step_equals_phase_launches(lib, syn, pkg, streams):
     """The one-launch step (every layer's tasks in one dataflow launch) gives
-    the same bits as one launch per phase, over several steps with ragged
-    contexts, in graph replay and in direct launches; then again after the
-    contexts jump past the task schedule's headroom (schedule rebuilt)."""
+    the same bits as one launch per phase, with one or two attention splits
+    per task, over several steps with ragged contexts, in graph replay and in
+    direct launches; then again after the contexts jump past the task
+    schedule's headroom (schedule rebuilt)."""
     layers = 3
     model = scaled_model(syn, 181, layers)
     views = pkg.Views()
@@ -725,10 +726,12 @@ def test_one_launch_step_equals_phase_launches(lib, syn, pkg, streams):
     ctx = rng.standard_normal((2, layers, max_pos, 512)).astype(np.float32)
     xs = rng.standard_normal((4, streams, 512)).astype(np.float32)
     runs = []
-    for flow, graph in ((0, 1), (2, 1), (2, 0)):
-        print(f"one-launch vs phases: streams={streams} flow={flow} graph={graph}", flush=True)
+    for flow, graph, rounds in ((0, 1, 0), (2, 1, 1), (2, 1, 2), (2, 0, 0)):
+        print(f"one-launch vs phases: streams={streams} flow={flow} graph={graph} "
+              f"rounds={rounds}", flush=True)
         bt = Batch(lib, w, layers, streams, max_pos, blocks)
         set_step_mode(lib, bt.batch, flow)
+        assert lib.phonon_flow_batch_set_attention_rounds(bt.batch, rounds)
         assert lib.phonon_flow_batch_set_graph(bt.batch, graph)
         ids = np.zeros(blocks, np.int32)
         assert lib.phonon_kv_pool_alloc(bt.pool, blocks, i32p(ids))
