@@ -71,11 +71,14 @@ struct NoGate {
 // max score mm[r], sum of exp ll[r] and the unnormalised P.V dims
 // [4 lane, 4 lane + 4) in aa[r]. `count` receives the stream's keys (0 if
 // the unit does not exist). sh holds ROUNDS AttnShared. `rounds` (at most
-// ROUNDS, uniform) limits the splits at run time.
+// ROUNDS, uniform) limits the splits at run time. `early`: every key before
+// the stream's last was written before the gate's inputs (not so in a
+// batched prefill, where earlier positions append in the same launch).
 template <int ROUNDS = 1, class Gate = NoGate>
 __device__ inline int attend_unit(const AttnArgs &a, int head, int split0, int s, int wave,
                                   AttnShared *sh, bool exists, float4 *aa, float *mm, float *ll,
-                                  int &count, const Gate &gate = Gate{}, int rounds = ROUNDS) {
+                                  int &count, const Gate &gate = Gate{}, int rounds = ROUNDS,
+                                  bool early = true) {
     const int lane = threadIdx.x & 63;
     const int krow = lane >> 4, dcol = lane & 15;
     // First loads, in flight together: the context length, the wave's block
@@ -102,35 +105,46 @@ __device__ inline int attend_unit(const AttnArgs &a, int head, int split0, int s
         count >= 1 && nsplit <= a.max_splits && count <= a.table_stride * kBlockPos;
     if (exists && !covered && split0 == 0 && wave == 0 && lane == 0) atomicOr(a.status, 2);
     const bool live = covered && split0 * kSplitKeys < count;  // uniform per unit
+    // Blocks of this wave that hold keys load; the others load nothing
+    // (their keys are masked below). With `early`, the K/V of every block but
+    // the context's last is requested before the gate: a unit that waits for
+    // its inputs has it in flight meanwhile. The last block (it holds the key
+    // this step appends) and q come after.
+    const int stream_blocks = (count + kBlockPos - 1) / kBlockPos;
+    const float *layer_kv = a.kv + (size_t)a.layer * a.layer_stride;
+    bool bad_block = false;
+    float4 kr[kBlocksPerWave][4], vr[kBlocksPerWave][4];
+    // sel 0: blocks before the context's last (zeros past the context);
+    // 1: the context's last block only; 2: every block.
+    auto load = [&](int r, bool values, int sel) {
+#pragma unroll
+        for (int t = 0; t < kBlocksPerWave; t++) {
+            float4 *dst = values ? vr[t] : kr[t];
+            const int b = (split0 + r) * 16 + wave * kBlocksPerWave + t;
+            const bool in = b < stream_blocks, last = b == stream_blocks - 1;  // uniform
+            if (in && (sel == 2 || (sel == 1) == last)) {
+                // An id outside the pool is flagged and replaced.
+                bad_block |= (unsigned)ids[r][t] >= a.blocks;
+                const int id = (unsigned)ids[r][t] < a.blocks ? ids[r][t] : 0;
+                const float *tile = layer_kv + ((size_t)id * kHeads + head) * 2048 +
+                                    (values ? 1024 : 0) + lane * 4;
+#pragma unroll
+                for (int i = 0; i < 4; i++) dst[i] = stream_load(tile + i * 256);
+            } else if (!in && sel != 1) {
+#pragma unroll
+                for (int i = 0; i < 4; i++) dst[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+            }
+        }
+    };
+    if (live && early) {
+        load(0, false, 0);
+        load(0, true, 0);
+    }
     gate.pass(probe, live);
 
     if (live) {
-        // Blocks of this wave that hold keys load; the others load nothing
-        // (their keys are masked below).
-        const int stream_blocks = (count + kBlockPos - 1) / kBlockPos;
-        const float *layer_kv = a.kv + (size_t)a.layer * a.layer_stride;
-        bool bad_block = false;
-        float4 kr[kBlocksPerWave][4], vr[kBlocksPerWave][4];
-        auto load = [&](int r, bool values) {
-#pragma unroll
-            for (int t = 0; t < kBlocksPerWave; t++) {
-                float4 *dst = values ? vr[t] : kr[t];
-                if ((split0 + r) * 16 + wave * kBlocksPerWave + t < stream_blocks) {  // uniform
-                    // An id outside the pool is flagged and replaced.
-                    bad_block |= (unsigned)ids[r][t] >= a.blocks;
-                    const int id = (unsigned)ids[r][t] < a.blocks ? ids[r][t] : 0;
-                    const float *tile = layer_kv + ((size_t)id * kHeads + head) * 2048 +
-                                        (values ? 1024 : 0) + lane * 4;
-#pragma unroll
-                    for (int i = 0; i < 4; i++) dst[i] = stream_load(tile + i * 256);
-                } else {
-#pragma unroll
-                    for (int i = 0; i < 4; i++) dst[i] = make_float4(0.f, 0.f, 0.f, 0.f);
-                }
-            }
-        };
-        load(0, false);
-        load(0, true);
+        load(0, false, early ? 1 : 2);
+        load(0, true, early ? 1 : 2);
         const float4 q = *(const float4 *)(a.q + (size_t)s * kWidth + head * kHeadDim + dcol * 4);
 #pragma unroll
         for (int r = 0; r < ROUNDS; r++) {
@@ -154,7 +168,7 @@ __device__ inline int attend_unit(const AttnArgs &a, int head, int split0, int s
                     score[t][i] = key < count ? d : -INFINITY;
                     m = fmaxf(m, score[t][i]);
                 }
-            if (next) load(r + 1, false);
+            if (next) load(r + 1, false, 2);
             m = fmaxf(m, __shfl_xor(m, 16));
             m = fmaxf(m, __shfl_xor(m, 32));
 #pragma unroll
@@ -172,7 +186,7 @@ __device__ inline int attend_unit(const AttnArgs &a, int head, int split0, int s
                     acc.z = fmaf(e, vr[t][i].z, acc.z);
                     acc.w = fmaf(e, vr[t][i].w, acc.w);
                 }
-            if (next) load(r + 1, true);
+            if (next) load(r + 1, true, 2);
             // Lanes of one key row hold the same l; sum the four rows.
             l += __shfl_xor(l, 16);
             l += __shfl_xor(l, 32);

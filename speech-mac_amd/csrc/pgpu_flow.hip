@@ -195,7 +195,7 @@ __device__ inline void attention_task(const pgpu_flow_step &f, const pgpu_paged_
     float mm[kFlowRounds], ll[kFlowRounds];
     int count;
     const int state = attend_unit<kFlowRounds>(a, head, split0, s, wave, sh, true, aa, mm, ll,
-                                               count, ready, f.attn_rounds);
+                                               count, ready, f.attn_rounds, !f.prefill);
     if (wave != 0 || state == UNIT_EMPTY || (state == UNIT_UNCOVERED && split0 != 0)) return;
     const bool covered = state == UNIT_LIVE;
     const int nsplit = (count + kSplitKeys - 1) / kSplitKeys;

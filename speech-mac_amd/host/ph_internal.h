@@ -19,10 +19,11 @@ enum { PH_FLOW_HEADROOM = 256 };
  * (phonon_flow_batch_set_pipeline): measured faster there on MI355X (B = 64:
  * 764 vs 913 us per 12-layer step; B = 32: 746 vs 653; B = 128: 1546 vs
  * 1463). */
-enum { PH_FLOW_MIN_TILES = 2, PH_FLOW_MAX_TILES = 10 };
-/* One-launch steps of this many 16-stream tiles run one split per ATTN task
- * (the others PGPU_FLOW_ATTN_ROUNDS). */
-enum { PH_FLOW_ONE_ROUND_MIN_TILES = 4, PH_FLOW_ONE_ROUND_MAX_TILES = 4 };
+enum { PH_FLOW_MIN_TILES = 1, PH_FLOW_MAX_TILES = 8 };
+/* One-launch steps of at most PH_FLOW_ONE_ROUND_MAX_STREAMS streams, or of
+ * PH_FLOW_ONE_ROUND_TILES tiles, run one split per ATTN task (the others
+ * PGPU_FLOW_ATTN_ROUNDS). */
+enum { PH_FLOW_ONE_ROUND_MAX_STREAMS = 8, PH_FLOW_ONE_ROUND_TILES = 4 };
 /* Chain placement of the one-launch step's task list (pgpu_flow_placement):
  * measured on MI355X at B = 64 (ph_flow_schedule.c). */
 pgpu_flow_placement ph_flow_default_placement(int rounds);

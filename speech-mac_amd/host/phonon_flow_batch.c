@@ -605,17 +605,16 @@ static size_t flow_ml_group(const PhononFlowBatch *b) {
 /* When a step runs as one launch: always (flow = 2), or, by default
  * (flow = 1), for the decode batch sizes where it measured faster on MI355X
  * than one launch per phase (PH_FLOW_MIN_TILES..PH_FLOW_MAX_TILES 16-stream
- * tiles; B = 1 is faster phase by phase, and prefill and larger batches are
- * attention-bound, where the separate attention kernel streams K/V
- * faster). */
-/* Splits per ATTN task: two where the step's attention throughput matters
- * more than its latency per tile (few tiles, or many), one in between
- * (measured on MI355X). */
+ * tiles; prefill and larger batches are attention-bound, where the separate
+ * attention kernel streams K/V faster). */
+/* Splits per ATTN task: one for a few streams (the step is a latency
+ * chain) and at 4 tiles, two otherwise (fewer, longer attention tasks keep
+ * more K/V in flight per work-group slot); measured on MI355X. */
 static int flow_rounds(const PhononFlowBatch *b) {
     if (b->fl.rounds_set)
         return b->fl.rounds_set;
     const size_t tiles = (b->streams + 15) / 16;
-    return tiles >= PH_FLOW_ONE_ROUND_MIN_TILES && tiles <= PH_FLOW_ONE_ROUND_MAX_TILES
+    return b->streams <= PH_FLOW_ONE_ROUND_MAX_STREAMS || tiles == PH_FLOW_ONE_ROUND_TILES
                ? 1
                : PGPU_FLOW_ATTN_ROUNDS;
 }
