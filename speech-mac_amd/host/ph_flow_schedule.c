@@ -95,7 +95,7 @@ pgpu_flow_placement ph_flow_default_placement(int rounds) {
     /* Clock in ATTN tasks (rounds 256-key splits, 128 KB of K/V each): at
      * B = 64 a 16-stream tile's attention is ~640 splits. Measured on
      * MI355X at B = 64 and 128. */
-    const pgpu_flow_placement one = {1.0f, {350.0f, 800.0f, 1250.0f, 1700.0f}};
+    const pgpu_flow_placement one = {1.0f, {450.0f, 900.0f, 1350.0f, 1800.0f}};
     const pgpu_flow_placement two = {2.0f, {750.0f, 1350.0f, 1950.0f, 2550.0f}};
     return rounds > 1 ? two : one;
 }
