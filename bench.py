@@ -478,8 +478,8 @@ def attention_curve(pkg, lib, seed=9):
         d.close()
         out[str(c)] = round(ms * 1e3, 2)
     return {"us_per_layer_step_vs_context": out,
-            "note": f"one stream, one layer (LN, QKV+RoPE+append, attention, out, MLP) as a "
-                    f"graph replay; contexts c .. c+{reps - 1}"}
+            "note": f"one stream, one layer (LN, QKV+RoPE+append, attention, out, MLP) in "
+                    f"the library's default step mode; contexts c .. c+{reps - 1}"}
 
 
 def cpu_baseline(pkg, lib, layers, lengths, seed, budget_s=10.0):
@@ -596,7 +596,7 @@ def main():
                       "us_per_step": round(r1["ms"] * 1e3 / b1_steps, 2),
                       "effective_GBps": round(r1["bytes"] / (r1["ms"] * 1e-3) / 1e9, 1),
                       "workload": "B=1, 12 layers, context 256 (synthetic prefill) then 750 "
-                                  "decode frames, hipGraph replay per step",
+                                  "decode frames, the library's default step (one launch)",
                       "clean": r1["clean"]}
         log(f"B=1: {line['b1']['us_per_step']} us/step")
         line["b256_with_prefill"] = large_batch_with_prefill(pkg, lib, args.seed)

@@ -138,9 +138,11 @@ int phonon_flow_batch_set_attention_rounds(PhononFlowBatch *batch, int rounds);
  * (k_flow_step; the counter reset that follows it is outside) on the batch's
  * stream. Phase-by-phase steps record nothing. NULL, NULL turns it off. */
 int phonon_flow_batch_set_timing(PhononFlowBatch *batch, void *before, void *after);
-/* use_graph = 1 (default): step_device replays a captured HIP graph;
- * 0: it launches the step's kernels directly (e.g. for a caller that is
- * itself capturing a graph). Results are identical. */
+/* use_graph = 1 (default): a phase-by-phase step_device replays a captured
+ * HIP graph (a one-launch step is always launched directly: its two kernels
+ * gain nothing from a graph); 0: it launches the step's kernels directly
+ * (e.g. for a caller that is itself capturing a graph). Results are
+ * identical. */
 int phonon_flow_batch_set_graph(PhononFlowBatch *batch, int use_graph);
 /* Waits for enqueued steps; returns 1 iff no step since the last call saw a
  * non-finite value or an uncovered position (and clears that record). */

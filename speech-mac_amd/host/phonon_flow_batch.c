@@ -910,7 +910,9 @@ int phonon_flow_batch_step_device(PhononFlowBatch *b, const float *inputs, float
     const int flow = flow_usable(b, 0);
     if (flow && !flow_prepare(b, 0))
         return 0;
-    if (b->eager || b->time_before) {
+    /* A one-launch step is two kernels: launched directly, without the graph
+     * launch's overhead (measured 7 us per step faster on MI355X). */
+    if (b->eager || b->time_before || flow) {
         b->splits = splits_for(b, 0);
         if (!(flow ? enqueue_flow(b, inputs, outputs, theta)
                    : enqueue_step(b, inputs, outputs, theta)))
