@@ -595,3 +595,179 @@ int oracle_stack_step_streams(const OracleLayer *weights, size_t layers, float *
     free(ids);
     return ok;
 }
+
+/* ---------------------------------------------------------------- flow head */
+
+/* src/phonon_sampler.c:229-248 (mean_512): four interleaved 4-lane vectors,
+ * two 16-group chunks, then the vectors and the lanes, in that order. */
+float oracle_mean_512(const float input[512]) {
+    float sums[4][4] = {{0}};
+    for (size_t chunk = 0; chunk < 2; chunk++) {
+        float partial[4][4] = {{0}};
+        for (size_t group = 0; group < 16; group++)
+            for (size_t v = 0; v < 4; v++)
+                for (size_t lane = 0; lane < 4; lane++)
+                    partial[v][lane] += input[chunk * 256 + group * 16 + v * 4 + lane];
+        for (size_t v = 0; v < 4; v++)
+            for (size_t lane = 0; lane < 4; lane++)
+                sums[v][lane] += partial[v][lane];
+    }
+    for (size_t v = 1; v < 4; v++)
+        for (size_t lane = 0; lane < 4; lane++)
+            sums[0][lane] += sums[v][lane];
+    float sum = 0.0f;
+    for (size_t lane = 0; lane < 4; lane++)
+        sum += sums[0][lane];
+    return sum / 512.0f;
+}
+
+/* src/phonon_sampler.c:250-278: float mean (mean_512), variance from double
+ * centred squares around it, eps 1e-6, optional affine. */
+int oracle_flow_layer_norm(const float *input, const float *weight, const float *bias,
+                           float output[512]) {
+    if (!input || !output)
+        return 0;
+    for (size_t i = 0; i < 512; i++)
+        if (!isfinite(input[i]) || (weight && !isfinite(weight[i])) ||
+            (bias && !isfinite(bias[i])))
+            return 0;
+    const float mean = oracle_mean_512(input);
+    double variance_sum = 0.0;
+    for (size_t i = 0; i < 512; i++) {
+        const double centred = (double)input[i] - mean;
+        variance_sum += centred * centred;
+    }
+    const float variance = (float)(variance_sum / 512.0);
+    const float inverse = 1.0f / sqrtf(variance + 1e-6f);
+    for (size_t i = 0; i < 512; i++) {
+        float v = (input[i] - mean) * inverse;
+        if (weight)
+            v = v * weight[i];
+        if (bias)
+            v = v + bias[i];
+        output[i] = v;
+        if (!isfinite(v))
+            return 0;
+    }
+    return 1;
+}
+
+/* src/phonon_math.c:18-28: x / (1 + exp(-x)) (libm in place of SLEEF). */
+int oracle_silu(float *values, size_t count) {
+    if (!values)
+        return 0;
+    for (size_t i = 0; i < count; i++)
+        values[i] = values[i] / (1.0f + expf(-values[i]));
+    return 1;
+}
+
+/* src/phonon_sampler.c:280-305: [cos | sin](value * freqs) -> mlp.0 -> SiLU
+ * -> mlp.2 -> alpha * out / sqrt(mean(out^2) + 1e-5) with mean_512. */
+int oracle_time_embedding(const OracleFlowHead *head, size_t which, float value,
+                          float output[512]) {
+    if (!head || which > 1 || !output || !isfinite(value))
+        return 0;
+    float embedding[256], hidden[512], squares[512];
+    for (size_t i = 0; i < 128; i++) {
+        const float phase = value * head->time_freqs[which][i];
+        embedding[i] = cosf(phase);
+        embedding[128 + i] = sinf(phase);
+    }
+    if (!oracle_linear_batch(head->time_weight[which][0], embedding, 512, 256,
+                             head->time_bias[which][0], hidden, 1) ||
+        !oracle_silu(hidden, 512) ||
+        !oracle_linear_batch(head->time_weight[which][1], hidden, 512, 512,
+                             head->time_bias[which][1], output, 1))
+        return 0;
+    for (size_t i = 0; i < 512; i++)
+        squares[i] = output[i] * output[i];
+    const float inverse = 1.0f / sqrtf(oracle_mean_512(squares) + 1e-5f);
+    for (size_t i = 0; i < 512; i++)
+        output[i] = (head->time_alpha[which][i] * output[i]) * inverse;
+    return 1;
+}
+
+/* h = LN(x) * (1 + scale) + shift, the adaLN modulation of
+ * src/phonon_sampler.c:330-334 and :350-354. */
+static void modulate(float h[512], const float *shift, const float *scale) {
+    for (size_t i = 0; i < 512; i++) {
+        const float one_plus_scale = 1.0f + scale[i];
+        const float scaled = h[i] * one_plus_scale;
+        h[i] = scaled + shift[i];
+    }
+}
+
+/* src/phonon_sampler.c:307-359 (head_forward_cancel, without the cancel
+ * poll). */
+int oracle_flow_head_forward(const OracleFlowHead *head, const float condition[512],
+                             const float state[32], float s, float t, float velocity[32]) {
+    float x[512], y[512], time_s[512], time_t[512], modulation[1536];
+    float h[512], first[512], second[512], normalized[512];
+    if (!head || !condition || !state || !velocity || !isfinite(s) || !isfinite(t) ||
+        !oracle_linear_batch(head->input_weight, state, 512, 32, head->input_bias, x, 1) ||
+        !oracle_linear_batch(head->cond_weight, condition, 512, 512, head->cond_bias, y, 1) ||
+        !oracle_time_embedding(head, 0, s, time_s) || !oracle_time_embedding(head, 1, t, time_t))
+        return 0;
+    for (size_t i = 0; i < 512; i++)
+        y[i] += 0.5f * (time_s[i] + time_t[i]);
+    for (size_t block = 0; block < ORACLE_HEAD_BLOCKS; block++) {
+        memcpy(normalized, y, sizeof(normalized));
+        oracle_silu(normalized, 512);
+        if (!oracle_linear_batch(head->block_ada_weight[block], normalized, 1536, 512,
+                                 head->block_ada_bias[block], modulation, 1) ||
+            !oracle_flow_layer_norm(x, head->block_norm_weight[block],
+                                    head->block_norm_bias[block], h))
+            return 0;
+        modulate(h, modulation, modulation + 512);
+        if (!oracle_linear_batch(head->block_mlp_weight[block][0], h, 512, 512,
+                                 head->block_mlp_bias[block][0], first, 1))
+            return 0;
+        oracle_silu(first, 512);
+        if (!oracle_linear_batch(head->block_mlp_weight[block][1], first, 512, 512,
+                                 head->block_mlp_bias[block][1], second, 1))
+            return 0;
+        for (size_t i = 0; i < 512; i++) {
+            const float gated = modulation[1024 + i] * second[i];
+            x[i] = x[i] + gated;
+        }
+    }
+    memcpy(normalized, y, sizeof(normalized));
+    oracle_silu(normalized, 512);
+    if (!oracle_linear_batch(head->final_ada_weight, normalized, 1024, 512, head->final_ada_bias,
+                             modulation, 1) ||
+        !oracle_flow_layer_norm(x, NULL, NULL, h))
+        return 0;
+    modulate(h, modulation, modulation + 512);
+    return oracle_linear_batch(head->final_weight, h, 32, 512, head->final_bias, velocity, 1);
+}
+
+/* src/phonon_sampler.c:366-393: one Euler step from temperature-scaled
+ * noise at s = 0, t = 1. */
+int oracle_lsd_one_step(const OracleFlowHead *head, const float condition[512],
+                        const float raw_noise[32], float temperature, float output[32]) {
+    float noise[32], velocity[32];
+    if (!head || !condition || !raw_noise || !output || !isfinite(temperature) ||
+        temperature <= 0.0f)
+        return 0;
+    const float scale = sqrtf(temperature);
+    for (size_t i = 0; i < 32; i++) {
+        if (!isfinite(raw_noise[i]))
+            return 0;
+        noise[i] = raw_noise[i] * scale;
+    }
+    if (!oracle_flow_head_forward(head, condition, noise, 0.0f, 1.0f, velocity))
+        return 0;
+    for (size_t i = 0; i < 32; i++) {
+        output[i] = noise[i] + velocity[i];
+        if (!isfinite(output[i]))
+            return 0;
+    }
+    return 1;
+}
+
+/* src/phonon_sampler.c:395-401: the one-row affine flow_lm.out_eos. */
+int oracle_eos_logit(const float *weight, const float *bias, const float state[512],
+                     float *raw_logit) {
+    return weight && bias && state && raw_logit &&
+           oracle_linear_batch(weight, state, 1, 512, bias, raw_logit, 1);
+}

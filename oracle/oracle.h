@@ -71,4 +71,36 @@ int oracle_stack_step_streams(const OracleLayer *weights, size_t layers, float *
                               const size_t *positions, const float *inputs, float theta,
                               float *outputs, size_t threads);
 
+/* Flow head (src/phonon_sampler.h:48-60), linear weights expanded to fp32
+ * row-major [rows][columns], vectors decoded to fp32. */
+#define ORACLE_HEAD_BLOCKS 6
+typedef struct {
+    const float *input_weight, *input_bias;               /* [512][32], [512] */
+    const float *cond_weight, *cond_bias;                 /* [512][512], [512] */
+    const float *time_weight[2][2], *time_bias[2][2];     /* mlp.0 [512][256], mlp.2 [512][512] */
+    const float *time_freqs[2], *time_alpha[2];           /* [128], [512] */
+    const float *block_ada_weight[ORACLE_HEAD_BLOCKS];    /* [1536][512] */
+    const float *block_ada_bias[ORACLE_HEAD_BLOCKS];      /* [1536] */
+    const float *block_norm_weight[ORACLE_HEAD_BLOCKS];   /* [512] */
+    const float *block_norm_bias[ORACLE_HEAD_BLOCKS];     /* [512] */
+    const float *block_mlp_weight[ORACLE_HEAD_BLOCKS][2]; /* [512][512] */
+    const float *block_mlp_bias[ORACLE_HEAD_BLOCKS][2];   /* [512] */
+    const float *final_ada_weight, *final_ada_bias;       /* [1024][512], [1024] */
+    const float *final_weight, *final_bias;               /* [32][512], [32] */
+} OracleFlowHead;
+
+float oracle_mean_512(const float input[512]);
+int oracle_flow_layer_norm(const float *input, const float *weight, const float *bias,
+                           float output[512]);
+int oracle_silu(float *values, size_t count);
+int oracle_time_embedding(const OracleFlowHead *head, size_t which, float value,
+                          float output[512]);
+int oracle_flow_head_forward(const OracleFlowHead *head, const float condition[512],
+                             const float state[32], float s, float t, float velocity[32]);
+int oracle_lsd_one_step(const OracleFlowHead *head, const float condition[512],
+                        const float raw_noise[32], float temperature, float output[32]);
+/* EOS logit: weight [512] (one row) and bias [1] applied to the state. */
+int oracle_eos_logit(const float *weight, const float *bias, const float state[512],
+                     float *raw_logit);
+
 #endif

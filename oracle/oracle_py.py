@@ -30,6 +30,24 @@ class OracleLayer(ctypes.Structure):
         "norm1_weight", "norm1_bias", "norm2_weight", "norm2_bias")]
 
 
+HEAD_BLOCKS = 6
+
+
+class OracleFlowHead(ctypes.Structure):
+    """OracleFlowHead (oracle.h): fp32 weights of the flow head."""
+    _fields_ = ([("input_weight", _f32p), ("input_bias", _f32p), ("cond_weight", _f32p),
+                 ("cond_bias", _f32p), ("time_weight", (_f32p * 2) * 2),
+                 ("time_bias", (_f32p * 2) * 2), ("time_freqs", _f32p * 2),
+                 ("time_alpha", _f32p * 2), ("block_ada_weight", _f32p * HEAD_BLOCKS),
+                 ("block_ada_bias", _f32p * HEAD_BLOCKS),
+                 ("block_norm_weight", _f32p * HEAD_BLOCKS),
+                 ("block_norm_bias", _f32p * HEAD_BLOCKS),
+                 ("block_mlp_weight", (_f32p * 2) * HEAD_BLOCKS),
+                 ("block_mlp_bias", (_f32p * 2) * HEAD_BLOCKS),
+                 ("final_ada_weight", _f32p), ("final_ada_bias", _f32p),
+                 ("final_weight", _f32p), ("final_bias", _f32p)])
+
+
 def build() -> None:
     """Compile liboracle.so (and _ref/ when the reference tree is present)."""
     subprocess.run(["make", "-s", "-C", HERE], check=True)
@@ -66,7 +84,17 @@ class Oracle:
             "oracle_stack_step_streams": [ctypes.POINTER(OracleLayer), _sz, _f32p, _f32p, _sz,
                                           _sz, ctypes.POINTER(_sz), _f32p, ctypes.c_float,
                                           _f32p, _sz],
+            "oracle_flow_layer_norm": [_f32p, _f32p, _f32p, _f32p],
+            "oracle_silu": [_f32p, _sz],
+            "oracle_time_embedding": [ctypes.POINTER(OracleFlowHead), _sz, ctypes.c_float, _f32p],
+            "oracle_flow_head_forward": [ctypes.POINTER(OracleFlowHead), _f32p, _f32p,
+                                         ctypes.c_float, ctypes.c_float, _f32p],
+            "oracle_lsd_one_step": [ctypes.POINTER(OracleFlowHead), _f32p, _f32p,
+                                    ctypes.c_float, _f32p],
+            "oracle_eos_logit": [_f32p, _f32p, _f32p, _f32p],
         }
+        lib.oracle_mean_512.restype = ctypes.c_float
+        lib.oracle_mean_512.argtypes = [_f32p]
         for name, args in sigs.items():
             fn = getattr(lib, name)
             fn.argtypes = args
@@ -133,6 +161,82 @@ class Oracle:
         out = np.zeros(64, np.float32)
         ok = self.lib.oracle_attention(_ptr(q), _ptr(keys), _ptr(values), count, stride, _ptr(out))
         return bool(ok), out
+
+
+    # -- flow head --------------------------------------------------------------------
+    def mean_512(self, x) -> float:
+        return self.lib.oracle_mean_512(_ptr(np.ascontiguousarray(x, np.float32)))
+
+    def flow_layer_norm(self, x, w=None, b=None):
+        x = np.ascontiguousarray(x, np.float32)
+        out = np.zeros(512, np.float32)
+        wp = None if w is None else _ptr(np.ascontiguousarray(w, np.float32))
+        bp = None if b is None else _ptr(np.ascontiguousarray(b, np.float32))
+        ok = self.lib.oracle_flow_layer_norm(_ptr(x), wp, bp, _ptr(out))
+        return bool(ok), out
+
+    def silu(self, x):
+        v = np.array(x, np.float32, copy=True)
+        ok = self.lib.oracle_silu(_ptr(v), v.size)
+        return bool(ok), v
+
+
+class OracleHead:
+    """fp32 weights of one flow head, kept alive for the OracleFlowHead pointers.
+    `head` maps the reference's tensor roles to arrays (see flow_head_arrays)."""
+
+    def __init__(self, oracle: Oracle, head: dict):
+        self.oracle = oracle
+        keep = {k: np.ascontiguousarray(v, np.float32) for k, v in head.items()}
+        self.keep = keep
+        h = OracleFlowHead()
+        for name in ("input_weight", "input_bias", "cond_weight", "cond_bias", "final_ada_weight",
+                     "final_ada_bias", "final_weight", "final_bias"):
+            setattr(h, name, _ptr(keep[name]))
+        for i in range(2):
+            for j in range(2):
+                h.time_weight[i][j] = _ptr(keep[f"time_weight_{i}_{j}"])
+                h.time_bias[i][j] = _ptr(keep[f"time_bias_{i}_{j}"])
+            h.time_freqs[i] = _ptr(keep[f"time_freqs_{i}"])
+            h.time_alpha[i] = _ptr(keep[f"time_alpha_{i}"])
+        for b in range(HEAD_BLOCKS):
+            h.block_ada_weight[b] = _ptr(keep[f"block_ada_weight_{b}"])
+            h.block_ada_bias[b] = _ptr(keep[f"block_ada_bias_{b}"])
+            h.block_norm_weight[b] = _ptr(keep[f"block_norm_weight_{b}"])
+            h.block_norm_bias[b] = _ptr(keep[f"block_norm_bias_{b}"])
+            for j in range(2):
+                h.block_mlp_weight[b][j] = _ptr(keep[f"block_mlp_weight_{b}_{j}"])
+                h.block_mlp_bias[b][j] = _ptr(keep[f"block_mlp_bias_{b}_{j}"])
+        self.h = h
+
+    def time_embedding(self, which: int, value: float):
+        out = np.zeros(512, np.float32)
+        ok = self.oracle.lib.oracle_time_embedding(ctypes.byref(self.h), which, value, _ptr(out))
+        return bool(ok), out
+
+    def forward(self, condition, state, s: float, t: float):
+        c = np.ascontiguousarray(condition, np.float32)
+        x = np.ascontiguousarray(state, np.float32)
+        out = np.zeros(32, np.float32)
+        ok = self.oracle.lib.oracle_flow_head_forward(ctypes.byref(self.h), _ptr(c), _ptr(x), s,
+                                                      t, _ptr(out))
+        return bool(ok), out
+
+    def lsd_one_step(self, condition, raw_noise, temperature: float):
+        c = np.ascontiguousarray(condition, np.float32)
+        n = np.ascontiguousarray(raw_noise, np.float32)
+        out = np.zeros(32, np.float32)
+        ok = self.oracle.lib.oracle_lsd_one_step(ctypes.byref(self.h), _ptr(c), _ptr(n),
+                                                 temperature, _ptr(out))
+        return bool(ok), out
+
+    def eos_logit(self, weight, bias, state):
+        w = np.ascontiguousarray(weight, np.float32)
+        b = np.ascontiguousarray(bias, np.float32)
+        x = np.ascontiguousarray(state, np.float32)
+        out = np.zeros(1, np.float32)
+        ok = self.oracle.lib.oracle_eos_logit(_ptr(w), _ptr(b), _ptr(x), _ptr(out))
+        return bool(ok), float(out[0])
 
 
 class OracleModel:

@@ -116,6 +116,21 @@ def reference_vectors() -> dict:
             "source": "tests/test_phonon_transformer.c:586-607",
             "capacity": 2, "layer": 8, "position": 1, "probe_column": 7,
         },
+        "flow_head_synthetic": {
+            "source": "tests/test_phonon_sampler.c:104-195 (the synthetic BF16 head that "
+                      "tests/helpers.py reference_flow_head_bits rebuilds; condition[i] = "
+                      "((7i mod 13) - 6) / 8, state[i] = ((11i + 3 mod 17) - 8) / 16; "
+                      "s = 0, t = 1; expected from an independent PyTorch 2.7.1 run)",
+            "s": 0.0, "t": 1.0, "tolerance": 2e-4,
+            "expected": [
+                6.749069214, -2.760953903, -6.280110359, 1.966097355, 3.173623323,
+                -1.909553528, -0.930359602, 6.741256714, -2.768766403, -6.287922859,
+                1.958284855, 3.165810823, -1.917366028, -0.852234602, 6.733444214,
+                -2.776578903, -6.295735359, 1.950472355, 3.157998323, -1.925178528,
+                -0.860047102, 6.725631714, -2.784391403, -6.303547859, 2.028597355,
+                3.150185823, -1.932991028, -0.867859602, 6.717819214, -2.792203903,
+                -6.311360359, 2.020784855],
+        },
     }
 
 
@@ -149,8 +164,9 @@ def q8_vectors(ref) -> dict:
 def main():
     with open(os.path.join(HERE, "reference_vectors.json"), "w") as f:
         json.dump(reference_vectors(), f, indent=1)
-    ref = oracle_py.ReferenceQ8()
-    np.savez(os.path.join(HERE, "q8_reference_vectors.npz"), **q8_vectors(ref))
+    if "--json-only" not in sys.argv:
+        ref = oracle_py.ReferenceQ8()
+        np.savez(os.path.join(HERE, "q8_reference_vectors.npz"), **q8_vectors(ref))
     print("wrote", os.listdir(HERE))
 
 

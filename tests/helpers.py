@@ -78,3 +78,93 @@ def normwise(a, b) -> float:
 def elementwise_ok(a, b, atol=1e-5, rtol=1e-3) -> bool:
     """The reference's own gate |a-b| <= 1e-5 + 1e-3|b| (tests/test_phonon_pack.c:446)."""
     return bool(np.all(np.abs(np.asarray(a, np.float64) - b) <= atol + rtol * np.abs(b)))
+
+
+# ------------------------------------------------------------------ flow head
+
+HEAD_BLOCKS = 6
+
+
+def bf16_bits(values) -> np.ndarray:
+    """Upper 16 bits of the fp32 values (exact for values bf16 can hold)."""
+    return (np.asarray(values, np.float32).view(np.uint32) >> 16).astype(np.uint16)
+
+
+def bf16_float(bits) -> np.ndarray:
+    return (np.asarray(bits, np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def reference_flow_head_bits() -> dict:
+    """The synthetic BF16 flow head of tests/test_phonon_sampler.c:104-180 as
+    arrays of bf16 bits: one shared matrix pattern ((5i mod 7) - 3) / 128 that
+    every weight view starts inside at its own element offset, and bias /
+    norm / frequency / alpha vectors of four patterns."""
+    n = 1536 * 512 + 32
+    i = np.arange(n, dtype=np.int64)
+    matrix = bf16_bits((((i * 5) % 7) - 3).astype(np.float32) / 128.0)
+
+    def mat(rows, cols, offset):
+        return matrix[offset: offset + rows * cols].reshape(rows, cols)
+
+    def vec(count, pattern, kind):
+        k = np.arange(count, dtype=np.int64)
+        if kind in (1, 2):
+            v = 1.0 + ((((k * 3 + pattern * 5) % 7) - 3).astype(np.float32) / 128.0)
+        elif kind == 3:
+            v = ((k % 8) + 1).astype(np.float32) / 128.0
+        else:
+            v = (((k * 3 + pattern * 5) % 11) - 5).astype(np.float32) / 128.0
+        return bf16_bits(v)
+
+    h = {"input_weight": mat(512, 32, 1), "input_bias": vec(512, 1, 0),
+         "cond_weight": mat(512, 512, 2), "cond_bias": vec(512, 2, 0)}
+    for t in range(2):
+        h[f"time_weight_{t}_0"] = mat(512, 256, t + 1)
+        h[f"time_bias_{t}_0"] = vec(512, t + 3, 0)
+        h[f"time_weight_{t}_1"] = mat(512, 512, t + 4)
+        h[f"time_bias_{t}_1"] = vec(512, t + 5, 0)
+        h[f"time_freqs_{t}"] = vec(128, 30 + t, 3)
+        h[f"time_alpha_{t}"] = vec(512, 32 + t, 2)
+    for b in range(HEAD_BLOCKS):
+        h[f"block_ada_weight_{b}"] = mat(1536, 512, b + 3)
+        h[f"block_ada_bias_{b}"] = vec(1536, b + 4, 0)
+        h[f"block_norm_weight_{b}"] = vec(512, 10 + b, 1)
+        h[f"block_norm_bias_{b}"] = vec(512, 16 + b, 0)
+        h[f"block_mlp_weight_{b}_0"] = mat(512, 512, b + 9)
+        h[f"block_mlp_bias_{b}_0"] = vec(512, b + 10, 0)
+        h[f"block_mlp_weight_{b}_1"] = mat(512, 512, b + 11)
+        h[f"block_mlp_bias_{b}_1"] = vec(512, b + 12, 0)
+    h["final_ada_weight"] = mat(1024, 512, 22)
+    h["final_ada_bias"] = vec(1024, 23, 0)
+    h["final_weight"] = mat(32, 512, 24)
+    h["final_bias"] = vec(32, 25, 0)
+    return h
+
+
+def reference_flow_head_inputs():
+    """condition and state of tests/test_phonon_sampler.c:185-188."""
+    i = np.arange(512)
+    condition = (((i * 7) % 13) - 6).astype(np.float32) / 8.0
+    j = np.arange(32)
+    state = (((j * 11 + 3) % 17) - 8).astype(np.float32) / 16.0
+    return condition, state
+
+
+def random_flow_head_bits(seed: int, scale: float = 0.04) -> dict:
+    """A random BF16 head of the same shapes (N(0, scale) weights, small
+    biases, norm weights near 1, time frequencies in (0, 1])."""
+    rng = np.random.default_rng(seed)
+    ref = reference_flow_head_bits()
+    out = {}
+    for name, bits in ref.items():
+        shape = bits.shape
+        if "freqs" in name:
+            v = rng.uniform(0.001, 1.0, shape)
+        elif "alpha" in name or "norm_weight" in name:
+            v = 1.0 + 0.1 * rng.standard_normal(shape)
+        elif "bias" in name:
+            v = 0.05 * rng.standard_normal(shape)
+        else:
+            v = scale * rng.standard_normal(shape)
+        out[name] = bf16_bits(np.asarray(v, np.float32))
+    return out
