@@ -104,6 +104,16 @@ int pgpu_gemm_residual(void *stream, const pgpu_matrix *w, const pgpu_gemm_input
 /* out_split = split fragments of GELU(x.W^T) (the next projection's input). */
 int pgpu_gemm_gelu_split(void *stream, const pgpu_matrix *w, const pgpu_gemm_input *x,
                          int streams, uint16_t *out_split, int *status);
+/* out_split = split fragments of SiLU((x.W^T + bias) + bias2), bias and
+ * bias2 optional [W->rows] vectors (W->rows % 32 == 0). */
+int pgpu_gemm_silu_split(void *stream, const pgpu_matrix *w, const pgpu_gemm_input *x,
+                         int streams, const float *bias, const float *bias2, uint16_t *out_split,
+                         int *status);
+/* out = residual + gate * (x.W^T + bias), rows of W->rows floats; gate rows
+ * of ld_gate floats (out may alias residual). */
+int pgpu_gemm_gated(void *stream, const pgpu_matrix *w, const pgpu_gemm_input *x, int streams,
+                    const float *bias, const float *gate, int ld_gate, const float *residual,
+                    float *out, int *status);
 /* Fused QKV projection: RoPE on q and k, q scaled by 1/8 into q_out
  * [streams][512], k and v appended to the pool at (layer, positions[s]). */
 int pgpu_gemm_qkv(void *stream, const pgpu_matrix *w, const pgpu_gemm_input *x, int streams,
@@ -222,6 +232,27 @@ int pgpu_attention(void *stream, const float *q, const pgpu_paged_kv *kv, int la
 int pgpu_attention_merge(void *stream, const pgpu_attention_scratch *scratch,
                          const int32_t *positions, int streams, int heads, int max_splits,
                          float *out, uint16_t *out_split, int *status);
+
+/* -- flow head rows (pgpu_head.hip) -- */
+/* noise = raw * sqrt(temperature) ([streams][32]) and its split fragments
+ * (K = 32); temperature must be positive and finite. */
+int pgpu_head_noise(void *stream, const float *raw, int streams, float temperature, float *noise,
+                    uint16_t *noise_split, int *status);
+/* Split fragments (K = 512) of LN(x; w, b optional, eps) * (1 + scale) +
+ * shift, where shift and scale are rows of ld floats ([streams][ld]). */
+int pgpu_head_ln_mod(void *stream, const float *x, int streams, const float *w, const float *b,
+                     float eps, const float *shift, const float *scale, int ld, uint16_t *xs,
+                     int *status);
+/* Split fragments (K = 256, stream 0) of [cos | sin](value * freqs[128]). */
+int pgpu_head_time_phase(void *stream, const float *freqs, float value, uint16_t *xs,
+                         int *status);
+/* tsum[512] = 0.5 * (alpha0 * out0 / rms(out0) + alpha1 * out1 / rms(out1)),
+ * rms(v) = sqrt(mean(v^2) + 1e-5). */
+int pgpu_head_time_sum(void *stream, const float *out0, const float *out1, const float *alpha0,
+                       const float *alpha1, float *tsum, int *status);
+/* latent = noise + velocity ([streams][32]); if eos: eos[s] = eos_rows[s * eos_ld]. */
+int pgpu_head_finish(void *stream, const float *noise, const float *velocity, int streams,
+                     float *latent, const float *eos_rows, int eos_ld, float *eos, int *status);
 
 /* -- rows and elements (pgpu_elementwise.hip) -- */
 int pgpu_ln_split(void *stream, const float *x, int streams, const float *w, const float *b,

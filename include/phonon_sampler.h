@@ -1,0 +1,91 @@
+/* Flow head of speech-mac's per-frame sampler: the decode output (the
+ * condition) and Gaussian noise give the frame's latent in one LSD Euler
+ * step; the EOS logit is one more affine row of the condition.
+ *
+ * The part of src/phonon_sampler.h:11-81 on the per-frame path: the
+ * PhononFlowHead view struct and the forward / one-step functions keep the
+ * reference's signatures, layouts and 1 = success / 0 = failure convention.
+ * (The noise source, stop rules and the generation loop stay in the
+ * reference.) The batched device API below it is new: one call advances B
+ * streams' frames on the GPU. */
+#ifndef PHONON_SAMPLER_H
+#define PHONON_SAMPLER_H
+
+#include "phonon_pack.h"
+#include "phonon_transformer.h"
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define PHONON_LATENT_WIDTH 32
+#define PHONON_FLOW_HEAD_BLOCKS 6
+
+/* src/phonon_sampler.h:48-60. Views are borrowed (BF16). */
+typedef struct {
+    PhononTensorView input_weight, input_bias, cond_weight, cond_bias;
+    PhononTensorView time_weight[2][2], time_bias[2][2], time_freqs[2], time_alpha[2];
+    PhononTensorView block_ada_weight[PHONON_FLOW_HEAD_BLOCKS];
+    PhononTensorView block_ada_bias[PHONON_FLOW_HEAD_BLOCKS];
+    PhononTensorView block_norm_weight[PHONON_FLOW_HEAD_BLOCKS];
+    PhononTensorView block_norm_bias[PHONON_FLOW_HEAD_BLOCKS];
+    PhononTensorView block_mlp_weight[PHONON_FLOW_HEAD_BLOCKS][2];
+    PhononTensorView block_mlp_bias[PHONON_FLOW_HEAD_BLOCKS][2];
+    PhononTensorView final_ada_weight, final_ada_bias, final_weight, final_bias;
+} PhononFlowHead;
+
+/* src/phonon_sampler.h:64-66: the head's velocity at flow times (s, t) for
+ * a normalized latent state. */
+int phonon_flow_head_forward(const PhononFlowHead *head, const float condition[512],
+                             const float normalized_state[PHONON_LATENT_WIDTH], float s, float t,
+                             float velocity[PHONON_LATENT_WIDTH]);
+/* src/phonon_sampler.h:72-74: noise * sqrt(temperature) plus the velocity at
+ * (s, t) = (0, 1). */
+int phonon_flow_lsd_one_step(const PhononFlowHead *head, const float condition[512],
+                             const float raw_noise[PHONON_LATENT_WIDTH], float temperature,
+                             float normalized_latent[PHONON_LATENT_WIDTH]);
+/* src/phonon_sampler.h:77-79. The cancel poll runs before each of the six
+ * blocks and after the last (as the reference polls); on cancellation
+ * returns 0 without publishing output. */
+int phonon_flow_lsd_one_step_cancel(const PhononFlowHead *head, const float condition[512],
+                                    const float raw_noise[32], float temperature, float output[32],
+                                    PhononCancelPoll cancel, void *context);
+
+/* Device copies of heads for the functions above, keyed by the head's
+ * input_weight.data: uploaded on first use, or ahead of time here (the
+ * analog of phonon_flow_prepare_weights). release frees one. */
+int phonon_flow_head_prepare(const PhononFlowHead *head);
+void phonon_flow_head_release(const PhononFlowHead *head);
+
+/* -- batched device API (new) -- */
+typedef struct PhononFlowHeadDevice PhononFlowHeadDevice;
+
+/* Uploads the head (and, if eos_weight is not NULL, the flow_lm.out_eos row:
+ * weight [1][512], bias [1]) for up to max_streams streams per call.
+ * Time embeddings of the LSD step (s = 0, t = 1) are computed once, here. */
+int phonon_flow_head_device_create(const PhononFlowHead *head, const PhononTensorView *eos_weight,
+                                   const PhononTensorView *eos_bias, size_t max_streams,
+                                   PhononFlowHeadDevice **out);
+void phonon_flow_head_device_destroy(PhononFlowHeadDevice *head);
+/* One LSD step of `streams` streams, enqueued on the head's stream: latents
+ * = noise * sqrt(temperature) + velocity(condition, noise * sqrt(T); 0, 1)
+ * and, if eos_logits is not NULL (and the head has the EOS row), eos_logits[s]
+ * = out_eos . condition[s] + bias (src/phonon_sampler.c:395-401). All
+ * pointers are device buffers: conditions [streams][512], raw_noise
+ * [streams][32], latents [streams][32], eos_logits [streams]. */
+int phonon_flow_head_device_lsd(PhononFlowHeadDevice *head, size_t streams,
+                                const float *conditions, const float *raw_noise,
+                                float temperature, float *latents, float *eos_logits);
+/* The head's HIP stream (for event timing by the caller). */
+void *phonon_flow_head_device_stream(const PhononFlowHeadDevice *head);
+/* Waits for enqueued calls; returns 1 iff none saw a non-finite value (and
+ * clears that record). */
+int phonon_flow_head_device_sync(PhononFlowHeadDevice *head);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

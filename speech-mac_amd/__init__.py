@@ -64,6 +64,23 @@ class PhononFlowLayerWeights(ctypes.Structure):
         "norm1_weight", "norm1_bias", "norm2_weight", "norm2_bias")]
 
 
+HEAD_BLOCKS = 6
+_TV = PhononTensorView
+
+
+class PhononFlowHead(ctypes.Structure):
+    """PhononFlowHead (phonon_sampler.h, src/phonon_sampler.h:48-60)."""
+    _fields_ = [("input_weight", _TV), ("input_bias", _TV), ("cond_weight", _TV),
+                ("cond_bias", _TV), ("time_weight", (_TV * 2) * 2), ("time_bias", (_TV * 2) * 2),
+                ("time_freqs", _TV * 2), ("time_alpha", _TV * 2),
+                ("block_ada_weight", _TV * HEAD_BLOCKS), ("block_ada_bias", _TV * HEAD_BLOCKS),
+                ("block_norm_weight", _TV * HEAD_BLOCKS), ("block_norm_bias", _TV * HEAD_BLOCKS),
+                ("block_mlp_weight", (_TV * 2) * HEAD_BLOCKS),
+                ("block_mlp_bias", (_TV * 2) * HEAD_BLOCKS),
+                ("final_ada_weight", _TV), ("final_ada_bias", _TV), ("final_weight", _TV),
+                ("final_bias", _TV)]
+
+
 class PhononKvCache(ctypes.Structure):
     _fields_ = [("capacity", _sz), ("length", _sz), ("keys", _fp), ("values", _fp)]
 
@@ -205,6 +222,23 @@ EXPORTS = {
     "pgpu_flow_schedule": (_sz, [_sz, _sz, _szp, _vp, _i, ctypes.POINTER(ctypes.c_uint32),
                                  _sz]),
     "pgpu_flow_launch": (_i, [_vp, _vp, _kvp]),
+    "pgpu_gemm_silu_split": (_i, [_vp, _vp, _vp, _i, _vp, _vp, _vp, _vp]),
+    "pgpu_gemm_gated": (_i, [_vp, _vp, _vp, _i, _vp, _vp, _i, _vp, _vp, _vp]),
+    "pgpu_head_noise": (_i, [_vp, _vp, _i, _f, _vp, _vp, _vp]),
+    "pgpu_head_ln_mod": (_i, [_vp, _vp, _i, _vp, _vp, _f, _vp, _vp, _i, _vp, _vp]),
+    "pgpu_head_time_phase": (_i, [_vp, _vp, _f, _vp, _vp]),
+    "pgpu_head_time_sum": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "pgpu_head_finish": (_i, [_vp, _vp, _vp, _i, _vp, _vp, _i, _vp, _vp]),
+    "phonon_flow_head_forward": (_i, [_vp, _vp, _vp, _f, _f, _vp]),
+    "phonon_flow_lsd_one_step": (_i, [_vp, _vp, _vp, _f, _vp]),
+    "phonon_flow_lsd_one_step_cancel": (_i, [_vp, _vp, _vp, _f, _vp, _vp, _vp]),
+    "phonon_flow_head_prepare": (_i, [_vp]),
+    "phonon_flow_head_release": (None, [_vp]),
+    "phonon_flow_head_device_create": (_i, [_vp, _vp, _vp, _sz, _pp]),
+    "phonon_flow_head_device_destroy": (None, [_vp]),
+    "phonon_flow_head_device_lsd": (_i, [_vp, _sz, _vp, _vp, _f, _vp, _vp]),
+    "phonon_flow_head_device_stream": (_vp, [_vp]),
+    "phonon_flow_head_device_sync": (_i, [_vp]),
     "pgpu_flow_finish": (_i, [_vp, _vp, _sz, _vp, _i]),
 }
 
@@ -267,6 +301,31 @@ class Views:
                              bits.ctypes.data, bits.nbytes, None)
         self.keep.append(v)
         return v
+
+    def flow_head(self, bits: dict) -> "PhononFlowHead":
+        """bf16-bit arrays by role (the keys of tests' flow-head builders) ->
+        PhononFlowHead of BF16 views."""
+        h = PhononFlowHead()
+        v = lambda key: self.bf16(bits[key], bits[key].shape)  # noqa: E731
+        for name in ("input_weight", "input_bias", "cond_weight", "cond_bias",
+                     "final_ada_weight", "final_ada_bias", "final_weight", "final_bias"):
+            setattr(h, name, v(name))
+        for i in range(2):
+            for j in range(2):
+                h.time_weight[i][j] = v(f"time_weight_{i}_{j}")
+                h.time_bias[i][j] = v(f"time_bias_{i}_{j}")
+            h.time_freqs[i] = v(f"time_freqs_{i}")
+            h.time_alpha[i] = v(f"time_alpha_{i}")
+        for b in range(HEAD_BLOCKS):
+            h.block_ada_weight[b] = v(f"block_ada_weight_{b}")
+            h.block_ada_bias[b] = v(f"block_ada_bias_{b}")
+            h.block_norm_weight[b] = v(f"block_norm_weight_{b}")
+            h.block_norm_bias[b] = v(f"block_norm_bias_{b}")
+            for j in range(2):
+                h.block_mlp_weight[b][j] = v(f"block_mlp_weight_{b}_{j}")
+                h.block_mlp_bias[b][j] = v(f"block_mlp_bias_{b}_{j}")
+        self.keep.append(h)
+        return h
 
     def layers(self, layer_dicts) -> ctypes.Array:
         """layer dicts (see synthetic.flow_layer) -> PhononFlowLayerWeights[L]."""

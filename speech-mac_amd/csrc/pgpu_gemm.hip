@@ -113,6 +113,35 @@ extern "C" int pgpu_gemm_gelu_split(void *stream, const pgpu_matrix *w,
     return dispatch<EPI_GELU_SPLIT>(a, w->q8, (hipStream_t)stream);
 }
 
+extern "C" int pgpu_gemm_silu_split(void *stream, const pgpu_matrix *w,
+                                    const pgpu_gemm_input *in, int streams, const float *bias,
+                                    const float *bias2, uint16_t *out_split, int *status) {
+    GemmArgs a;
+    if (w->rows % 32 || !base_args(a, w, in, streams, status))
+        return bad_arguments("pgpu_gemm_silu_split");
+    a.bias = bias;
+    a.bias2 = bias2;
+    a.out_split = out_split;
+    a.out_kb = (int)w->rows / 32;
+    return dispatch<EPI_SILU_SPLIT>(a, w->q8, (hipStream_t)stream);
+}
+
+extern "C" int pgpu_gemm_gated(void *stream, const pgpu_matrix *w, const pgpu_gemm_input *in,
+                               int streams, const float *bias, const float *gate, int ld_gate,
+                               const float *residual, float *out, int *status) {
+    GemmArgs a;
+    if (!gate || !residual || ld_gate < (int)w->rows || ld_gate % 4 ||
+        !base_args(a, w, in, streams, status))
+        return bad_arguments("pgpu_gemm_gated");
+    a.bias = bias;
+    a.gate = gate;
+    a.ld_gate = ld_gate;
+    a.residual = residual;
+    a.out = out;
+    a.ld_out = (int)w->rows;
+    return dispatch<EPI_GATED>(a, w->q8, (hipStream_t)stream);
+}
+
 extern "C" int pgpu_gemm_qkv(void *stream, const pgpu_matrix *w, const pgpu_gemm_input *in,
                              int streams, const pgpu_paged_kv *kv, int layer,
                              const int32_t *tables, int table_stride, const int32_t *positions,

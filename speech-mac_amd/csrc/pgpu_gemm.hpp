@@ -42,7 +42,14 @@
 namespace pgpu {
 
 enum Source { SRC_SPLIT = 0, SRC_LN = 1, SRC_ATTN = 2, SRC_ROWS = 3 };
-enum Epilogue { EPI_STORE = 0, EPI_RESIDUAL = 1, EPI_GELU_SPLIT = 2, EPI_QKV = 3 };
+enum Epilogue {
+    EPI_STORE = 0,
+    EPI_RESIDUAL = 1,
+    EPI_GELU_SPLIT = 2,
+    EPI_QKV = 3,
+    EPI_SILU_SPLIT = 4,  // split fragments of SiLU((dot + bias) + bias2)
+    EPI_GATED = 5,       // residual + gate * (dot + bias)
+};
 
 constexpr int kTaskWaves = 8, kTaskThreads = 64 * kTaskWaves;
 
@@ -74,6 +81,9 @@ struct GemmArgs {
     const float2 *rope;       // [8192][32] (cos, sin)
     int *status;
     bool wt_out;              // STORE / RESIDUAL / GELU_SPLIT outputs write-through
+    const float *bias2;       // SILU_SPLIT: optional second [n_rows] vector
+    const float *gate;        // GATED: [streams][ld_gate] rows (columns [0, n_rows))
+    int ld_gate;
 };
 
 // ---------------------------------------------------------------------------
@@ -416,8 +426,11 @@ __device__ inline void mfma_block(f32x4 &acc, const WChunk<Q8, CH> &w, int u, co
 // ---------------------------------------------------------------------------
 // Epilogue operands of one lane (rows row0..row0+3 of stream s).
 struct EpiOperands {
-    float4 add;          // STORE: bias, RESIDUAL: residual
+    float4 add;          // STORE, SILU_SPLIT, GATED: bias; RESIDUAL: residual
     bool has_add;
+    float4 add2;         // SILU_SPLIT: bias2; GATED: residual
+    bool has_add2;
+    float4 gate;         // GATED
     float2 cs0, cs1;     // QKV: (cos, sin) of the lane's two RoPE pairs
     int pos, block;      // QKV: append position and its pool block
     bool ok;             // QKV: position and block are valid
@@ -430,12 +443,19 @@ __device__ inline void load_epilogue_static(EpiOperands &e, const GemmArgs &a, i
                                             bool live) {
     e.add = make_float4(0.f, 0.f, 0.f, 0.f);
     e.has_add = false;
+    e.add2 = make_float4(0.f, 0.f, 0.f, 0.f);
+    e.has_add2 = false;
+    e.gate = make_float4(0.f, 0.f, 0.f, 0.f);
     e.ok = false;
     if (!live) return;
-    if constexpr (EPI == EPI_STORE) {
+    if constexpr (EPI == EPI_STORE || EPI == EPI_SILU_SPLIT || EPI == EPI_GATED) {
         if (a.bias) {
             e.add = *(const float4 *)(a.bias + row0);
             e.has_add = true;
+        }
+        if (EPI == EPI_SILU_SPLIT && a.bias2) {
+            e.add2 = *(const float4 *)(a.bias2 + row0);
+            e.has_add2 = true;
         }
     } else if constexpr (EPI == EPI_QKV) {
         // Positions past the rope table or the block table, and block ids
@@ -464,6 +484,11 @@ __device__ inline void load_epilogue_dynamic(EpiOperands &e, const GemmArgs &a, 
         if (live) {
             e.add = *(const float4 *)(a.residual + (size_t)s * a.ld_out + row0);
             e.has_add = true;
+        }
+    } else if constexpr (EPI == EPI_GATED) {
+        if (live) {
+            e.add2 = *(const float4 *)(a.residual + (size_t)s * a.ld_out + row0);
+            e.gate = *(const float4 *)(a.gate + (size_t)s * a.ld_gate + row0);
         }
     }
 }
@@ -499,6 +524,37 @@ __device__ inline bool epilogue(const GemmArgs &a, const EpiOperands &e, const f
                 bad |= !isfinite(g[r]);
             }
             store_split4(a.out_split, s, row0, a.out_kb, g, wt);
+        }
+    } else if constexpr (EPI == EPI_SILU_SPLIT) {
+        if (live) {
+            const float add[4] = {e.add.x, e.add.y, e.add.z, e.add.w};
+            const float add2[4] = {e.add2.x, e.add2.y, e.add2.z, e.add2.w};
+            float g[4];
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                // bias + dot, then + bias2, then x / (1 + e^-x)
+                float y = e.has_add ? __fadd_rn(v[r], add[r]) : v[r];
+                if (e.has_add2) y = __fadd_rn(y, add2[r]);
+                bad |= !isfinite(y);
+                g[r] = __fdiv_rn(y, __fadd_rn(1.0f, expf(-y)));
+                bad |= !isfinite(g[r]);
+            }
+            store_split4(a.out_split, s, row0, a.out_kb, g, wt);
+        }
+    } else if constexpr (EPI == EPI_GATED) {
+        if (live) {
+            float *o = a.out + (size_t)s * a.ld_out + row0;
+            const float add[4] = {e.add.x, e.add.y, e.add.z, e.add.w};
+            const float res[4] = {e.add2.x, e.add2.y, e.add2.z, e.add2.w};
+            const float gate[4] = {e.gate.x, e.gate.y, e.gate.z, e.gate.w};
+            float y[4];
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const float lin = e.has_add ? __fadd_rn(v[r], add[r]) : v[r];
+                y[r] = __fadd_rn(res[r], __fmul_rn(gate[r], lin));
+                bad |= !isfinite(y[r]);
+            }
+            store_out(o, make_float4(y[0], y[1], y[2], y[3]), wt);
         }
     } else {  // EPI_QKV: rows [0,512) q, [512,1024) k, [1024,1536) v
         if (live) {

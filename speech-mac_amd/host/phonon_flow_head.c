@@ -1,0 +1,415 @@
+/* Flow head on the GPU (phonon_sampler.h): src/phonon_sampler.c:280-401 as
+ * a chain of projections and row kernels over B streams.
+ *
+ * Per call, for B streams (each projection one launch over all streams):
+ *   x    = input_proj(noise)                          [B][512]
+ *   s_y  = SiLU(cond_embed(condition) + tsum)         split fragments
+ *   mod  = [adaLN_0 .. adaLN_5 | final adaLN](s_y)    [B][6*1536 + 1024]
+ *   6 x: h = LN(x)*(1 + scale_b) + shift_b; x += gate_b * mlp_b1(SiLU(mlp_b0(h)))
+ *   h    = LN(x)*(1 + scale_f) + shift_f; velocity = final(h)
+ * SiLU(y) is the same for all seven adaLN projections (they read only the
+ * condition and the time embeddings), so they run as one 10240-row
+ * projection. The time embeddings of the LSD step (s = 0, t = 1) do not
+ * depend on the stream: tsum = 0.5 (time_0(0) + time_1(1)) is computed once
+ * on the device when the head is created. */
+#include "phonon_sampler.h"
+#include "ph_internal.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+
+enum {
+    HB = PHONON_FLOW_HEAD_BLOCKS,
+    ADA = 3 * PH_WIDTH,              /* rows of one block's adaLN */
+    FINAL_ADA = 2 * PH_WIDTH,
+    MOD = HB * ADA + FINAL_ADA,      /* 10240 modulation columns */
+    LAT = PHONON_LATENT_WIDTH,
+    EOS_ROWS = 16,                   /* the EOS row padded to one row tile */
+};
+
+struct PhononFlowHeadDevice {
+    pgpu_matrix input, cond, ada, mlp[HB][2], final, eos, time_w[2][2];
+    void *mats[7 + 2 * HB + 4];
+    size_t nmats;
+    float *vec; /* every bias / norm / frequency / alpha vector, and tsum */
+    float *b_input, *b_cond, *b_ada, *b_mlp[HB][2], *b_final, *b_eos, *b_time[2][2];
+    float *norm_w[HB], *norm_b[HB], *freqs[2], *alpha[2];
+    float *tsum_lsd, *tsum, *time_out; /* time_out: [2][512] */
+    size_t cap;                        /* streams, a multiple of 16 */
+    void *buffers;
+    float *noise, *x, *mod, *velocity, *eos_rows, *stage;
+    uint16_t *noise_split, *cond_split, *silu_split, *h_split, *first_split, *time_split,
+        *time_hidden;
+    int has_eos;
+    int *status;
+    void *stream;
+};
+
+static size_t split_elems(size_t streams, size_t k_cols) {
+    return (streams + 15) / 16 * (k_cols / 32) * 1536;
+}
+
+/* A BF16 [count] vector view into `dst` (fp32). */
+static int vec_view(const PhononTensorView *view, size_t count, float *dst) {
+    return ph_vector_decode(view, count, dst);
+}
+
+static int upload(PhononFlowHeadDevice *h, const PhononTensorView *view, size_t rows,
+                  size_t columns, pgpu_matrix *dst) {
+    void *dev = NULL;
+    if (!ph_matrix_upload(view, rows, columns, dst, &dev))
+        return 0;
+    h->mats[h->nmats++] = dev;
+    return 1;
+}
+
+/* The seven adaLN matrices as one BF16 [10240][512] matrix. */
+static int upload_ada(PhononFlowHeadDevice *h, const PhononFlowHead *head) {
+    uint16_t *all = malloc((size_t)MOD * PH_WIDTH * sizeof(uint16_t));
+    if (!all)
+        return 0;
+    int ok = 1;
+    for (size_t b = 0; ok && b <= HB; b++) {
+        const PhononTensorView *v = b < HB ? &head->block_ada_weight[b] : &head->final_ada_weight;
+        const size_t rows = b < HB ? ADA : FINAL_ADA;
+        ok = v->data && v->dtype == PHONON_PACK_BF16 && v->rank == 2 && v->shape[0] == rows &&
+             v->shape[1] == PH_WIDTH && v->byte_count == rows * PH_WIDTH * sizeof(uint16_t);
+        if (ok)
+            memcpy(all + b * ADA * PH_WIDTH, v->data, rows * PH_WIDTH * sizeof(uint16_t));
+    }
+    PhononTensorView view = {.dtype = PHONON_PACK_BF16,
+                             .rank = 2,
+                             .shape = {MOD, PH_WIDTH},
+                             .data = all,
+                             .byte_count = (size_t)MOD * PH_WIDTH * sizeof(uint16_t)};
+    ok = ok && upload(h, &view, MOD, PH_WIDTH, &h->ada);
+    free(all);
+    return ok;
+}
+
+/* Device float vectors, laid out in one allocation. */
+static int upload_vectors(PhononFlowHeadDevice *h, const PhononFlowHead *head,
+                          const PhononTensorView *eos_bias) {
+    const size_t total = 2 * PH_WIDTH + MOD + HB * 2 * PH_WIDTH + LAT + EOS_ROWS +
+                         2 * 2 * PH_WIDTH + HB * 2 * PH_WIDTH + 2 * 128 + 2 * PH_WIDTH +
+                         2 * PH_WIDTH + 2 * PH_WIDTH;
+    float *host = calloc(total, sizeof(float));
+    float *dev = host ? pgpu_malloc(total * sizeof(float)) : NULL;
+    if (!dev) {
+        free(host);
+        return 0;
+    }
+    h->vec = dev;
+    size_t at = 0;
+    int ok = 1;
+#define SLOT(ptr, count) ((ptr) = dev + at, at += (count), host + at - (count))
+#define TAKE(ptr, count, view) (ok = ok && vec_view((view), (count), SLOT(ptr, count)))
+    TAKE(h->b_input, PH_WIDTH, &head->input_bias);
+    TAKE(h->b_cond, PH_WIDTH, &head->cond_bias);
+    float *ada = SLOT(h->b_ada, MOD);
+    for (size_t b = 0; ok && b < HB; b++)
+        ok = vec_view(&head->block_ada_bias[b], ADA, ada + b * ADA);
+    ok = ok && vec_view(&head->final_ada_bias, FINAL_ADA, ada + HB * ADA);
+    for (size_t b = 0; b < HB; b++)
+        for (size_t j = 0; j < 2; j++)
+            TAKE(h->b_mlp[b][j], PH_WIDTH, &head->block_mlp_bias[b][j]);
+    TAKE(h->b_final, LAT, &head->final_bias);
+    float *eos = SLOT(h->b_eos, EOS_ROWS);
+    if (eos_bias)
+        ok = ok && vec_view(eos_bias, 1, eos);
+    for (size_t i = 0; i < 2; i++)
+        for (size_t j = 0; j < 2; j++)
+            TAKE(h->b_time[i][j], PH_WIDTH, &head->time_bias[i][j]);
+    for (size_t b = 0; b < HB; b++) {
+        TAKE(h->norm_w[b], PH_WIDTH, &head->block_norm_weight[b]);
+        TAKE(h->norm_b[b], PH_WIDTH, &head->block_norm_bias[b]);
+    }
+    for (size_t i = 0; i < 2; i++) {
+        TAKE(h->freqs[i], 128, &head->time_freqs[i]);
+        TAKE(h->alpha[i], PH_WIDTH, &head->time_alpha[i]);
+    }
+    (void)SLOT(h->tsum_lsd, PH_WIDTH);
+    (void)SLOT(h->tsum, PH_WIDTH);
+    (void)SLOT(h->time_out, 2 * PH_WIDTH);
+#undef TAKE
+#undef SLOT
+    ok = ok && at == total && pgpu_copy_h2d(h->stream, dev, host, total * sizeof(float)) &&
+         pgpu_stream_sync(h->stream);
+    free(host);
+    return ok;
+}
+
+static int alloc_buffers(PhononFlowHeadDevice *h, size_t streams) {
+    const size_t cap = (streams + 15) / 16 * 16;
+    const size_t floats = cap * (LAT + PH_WIDTH + MOD + LAT + EOS_ROWS) + PH_WIDTH + LAT;
+    const size_t halves = split_elems(cap, LAT) + 4 * split_elems(cap, PH_WIDTH) +
+                          split_elems(16, 256) + split_elems(16, PH_WIDTH);
+    const size_t bytes = floats * sizeof(float) + halves * sizeof(uint16_t);
+    char *p = pgpu_malloc(bytes);
+    if (!p || !pgpu_memset(h->stream, p, 0, bytes))
+        return 0;
+    h->buffers = p;
+    h->cap = cap;
+    float *f = (float *)p;
+    h->noise = f, f += cap * LAT;
+    h->x = f, f += cap * PH_WIDTH;
+    h->mod = f, f += cap * MOD;
+    h->velocity = f, f += cap * LAT;
+    h->eos_rows = f, f += cap * EOS_ROWS;
+    h->stage = f, f += PH_WIDTH + LAT;
+    uint16_t *u = (uint16_t *)f;
+    h->noise_split = u, u += split_elems(cap, LAT);
+    h->cond_split = u, u += split_elems(cap, PH_WIDTH);
+    h->silu_split = u, u += split_elems(cap, PH_WIDTH);
+    h->h_split = u, u += split_elems(cap, PH_WIDTH);
+    h->first_split = u, u += split_elems(cap, PH_WIDTH);
+    h->time_split = u, u += split_elems(16, 256);
+    h->time_hidden = u;
+    return 1;
+}
+
+/* tsum = 0.5 (time_0(s) + time_1(t)) (src/phonon_sampler.c:280-305, 318-319). */
+static int enqueue_tsum(PhononFlowHeadDevice *h, float s, float t, float *tsum) {
+    for (int which = 0; which < 2; which++) {
+        const pgpu_gemm_input phase = {.split = h->time_split};
+        const pgpu_gemm_input hidden = {.split = h->time_hidden};
+        if (!pgpu_head_time_phase(h->stream, h->freqs[which], which ? t : s, h->time_split,
+                                  h->status) ||
+            !pgpu_gemm_silu_split(h->stream, &h->time_w[which][0], &phase, 1, h->b_time[which][0],
+                                  NULL, h->time_hidden, h->status) ||
+            !pgpu_gemm_store(h->stream, &h->time_w[which][1], &hidden, 1, h->b_time[which][1],
+                             h->time_out + which * PH_WIDTH, PH_WIDTH, h->status))
+            return 0;
+    }
+    return pgpu_head_time_sum(h->stream, h->time_out, h->time_out + PH_WIDTH, h->alpha[0],
+                              h->alpha[1], tsum, h->status);
+}
+
+/* The head's forward for n streams: state_split holds the latent state's
+ * split fragments (K = 32), conditions [n][512]; velocity [n][32] and, if
+ * eos_rows, the padded EOS projection [n][16]. The cancel poll runs before
+ * each block and before the final layer. */
+static int enqueue_forward(PhononFlowHeadDevice *h, size_t n, const float *conditions,
+                           const float *tsum, float *velocity, float *eos_rows,
+                           PhononCancelPoll cancel, void *context) {
+    void *st = h->stream;
+    const int B = (int)n;
+    const pgpu_gemm_input state = {.split = h->noise_split}, cond = {.split = h->cond_split},
+                          silu_y = {.split = h->silu_split}, hin = {.split = h->h_split},
+                          first = {.split = h->first_split};
+    if (!pgpu_split_rows(st, conditions, B, PH_WIDTH, h->cond_split, h->status) ||
+        !pgpu_gemm_store(st, &h->input, &state, B, h->b_input, h->x, PH_WIDTH, h->status) ||
+        !pgpu_gemm_silu_split(st, &h->cond, &cond, B, h->b_cond, tsum, h->silu_split,
+                              h->status) ||
+        !pgpu_gemm_store(st, &h->ada, &silu_y, B, h->b_ada, h->mod, MOD, h->status))
+        return 0;
+    for (size_t b = 0; b < HB; b++) {
+        if (cancel && cancel(context))
+            return 0;
+        const float *mod = h->mod + b * ADA;
+        if (!pgpu_head_ln_mod(st, h->x, B, h->norm_w[b], h->norm_b[b], 1e-6f, mod,
+                              mod + PH_WIDTH, MOD, h->h_split, h->status) ||
+            !pgpu_gemm_silu_split(st, &h->mlp[b][0], &hin, B, h->b_mlp[b][0], NULL,
+                                  h->first_split, h->status) ||
+            !pgpu_gemm_gated(st, &h->mlp[b][1], &first, B, h->b_mlp[b][1], mod + 2 * PH_WIDTH,
+                             MOD, h->x, h->x, h->status))
+            return 0;
+    }
+    const float *fmod = h->mod + HB * ADA;
+    return pgpu_head_ln_mod(st, h->x, B, NULL, NULL, 1e-6f, fmod, fmod + PH_WIDTH, MOD,
+                            h->h_split, h->status) &&
+           pgpu_gemm_store(st, &h->final, &hin, B, h->b_final, velocity, LAT, h->status) &&
+           (!eos_rows ||
+            pgpu_gemm_store(st, &h->eos, &cond, B, h->b_eos, eos_rows, EOS_ROWS, h->status));
+}
+
+int phonon_flow_head_device_create(const PhononFlowHead *head, const PhononTensorView *eos_weight,
+                                   const PhononTensorView *eos_bias, size_t max_streams,
+                                   PhononFlowHeadDevice **out) {
+    if (!out)
+        return 0;
+    *out = NULL;
+    if (!head || !max_streams || max_streams > 4096 || (!eos_weight) != (!eos_bias) || !ph_init())
+        return 0;
+    PhononFlowHeadDevice *h = calloc(1, sizeof(*h));
+    if (!h)
+        return 0;
+    int ok = pgpu_stream_create(&h->stream) && (h->status = pgpu_malloc(sizeof(int))) &&
+             pgpu_memset(h->stream, h->status, 0, sizeof(int)) &&
+             upload(h, &head->input_weight, PH_WIDTH, LAT, &h->input) &&
+             upload(h, &head->cond_weight, PH_WIDTH, PH_WIDTH, &h->cond) && upload_ada(h, head) &&
+             upload(h, &head->final_weight, LAT, PH_WIDTH, &h->final);
+    for (size_t b = 0; ok && b < HB; b++)
+        for (size_t j = 0; ok && j < 2; j++)
+            ok = upload(h, &head->block_mlp_weight[b][j], PH_WIDTH, PH_WIDTH, &h->mlp[b][j]);
+    for (size_t i = 0; ok && i < 2; i++)
+        ok = upload(h, &head->time_weight[i][0], PH_WIDTH, 256, &h->time_w[i][0]) &&
+             upload(h, &head->time_weight[i][1], PH_WIDTH, PH_WIDTH, &h->time_w[i][1]);
+    if (ok && eos_weight) {
+        h->has_eos = 1;
+        ok = upload(h, eos_weight, 1, PH_WIDTH, &h->eos);
+    }
+    ok = ok && upload_vectors(h, head, eos_bias) && alloc_buffers(h, max_streams) &&
+         enqueue_tsum(h, 0.0f, 1.0f, h->tsum_lsd) && phonon_flow_head_device_sync(h);
+    if (!ok) {
+        phonon_flow_head_device_destroy(h);
+        return ph_fail("flow head: bad weights or device allocation");
+    }
+    *out = h;
+    return 1;
+}
+
+void phonon_flow_head_device_destroy(PhononFlowHeadDevice *h) {
+    if (!h)
+        return;
+    if (h->stream)
+        (void)pgpu_stream_sync(h->stream);
+    for (size_t i = 0; i < h->nmats; i++)
+        pgpu_free(h->mats[i]);
+    pgpu_free(h->vec);
+    pgpu_free(h->buffers);
+    pgpu_free(h->status);
+    pgpu_stream_destroy(h->stream);
+    free(h);
+}
+
+void *phonon_flow_head_device_stream(const PhononFlowHeadDevice *h) {
+    return h ? h->stream : NULL;
+}
+
+int phonon_flow_head_device_sync(PhononFlowHeadDevice *h) {
+    int status = 1;
+    if (!h || !pgpu_stream_sync(h->stream) ||
+        !pgpu_copy_d2h(h->stream, &status, h->status, sizeof(int)) ||
+        !pgpu_memset(h->stream, h->status, 0, sizeof(int)) || !pgpu_stream_sync(h->stream))
+        return 0;
+    return status == 0;
+}
+
+int phonon_flow_head_device_lsd(PhononFlowHeadDevice *h, size_t streams,
+                                const float *conditions, const float *raw_noise,
+                                float temperature, float *latents, float *eos_logits) {
+    if (!h || !streams || streams > h->cap || !conditions || !raw_noise || !latents ||
+        (eos_logits && !h->has_eos) || !(temperature > 0.0f) || !isfinite(temperature))
+        return 0;
+    return pgpu_head_noise(h->stream, raw_noise, (int)streams, temperature, h->noise,
+                           h->noise_split, h->status) &&
+           enqueue_forward(h, streams, conditions, h->tsum_lsd, h->velocity,
+                           eos_logits ? h->eos_rows : NULL, NULL, NULL) &&
+           pgpu_head_finish(h->stream, h->noise, h->velocity, (int)streams, latents,
+                            eos_logits ? h->eos_rows : NULL, EOS_ROWS, eos_logits, h->status);
+}
+
+/* ------------------------------------------------ reference-signature API */
+
+enum { REGISTRY = 8 };
+static struct {
+    const void *key;
+    PhononFlowHeadDevice *head;
+} registry[REGISTRY];
+
+/* The device copy of `head` (created on first use); call under ph_lock. */
+static PhononFlowHeadDevice *lookup(const PhononFlowHead *head, int create) {
+    const void *key = head->input_weight.data;
+    for (size_t i = 0; i < REGISTRY; i++)
+        if (registry[i].key && registry[i].key == key)
+            return registry[i].head;
+    if (!create)
+        return NULL;
+    for (size_t i = 0; i < REGISTRY; i++)
+        if (!registry[i].key) {
+            PhononFlowHeadDevice *h = NULL;
+            if (!phonon_flow_head_device_create(head, NULL, NULL, 16, &h))
+                return NULL;
+            registry[i].key = key;
+            registry[i].head = h;
+            return h;
+        }
+    ph_fail("flow head: too many registered heads");
+    return NULL;
+}
+
+int phonon_flow_head_prepare(const PhononFlowHead *head) {
+    if (!head || !head->input_weight.data || !ph_init())
+        return 0;
+    ph_lock();
+    const int ok = lookup(head, 1) != NULL;
+    ph_unlock();
+    return ok;
+}
+
+void phonon_flow_head_release(const PhononFlowHead *head) {
+    if (!head)
+        return;
+    ph_lock();
+    for (size_t i = 0; i < REGISTRY; i++)
+        if (registry[i].key && registry[i].key == head->input_weight.data) {
+            phonon_flow_head_device_destroy(registry[i].head);
+            registry[i].key = NULL;
+            registry[i].head = NULL;
+        }
+    ph_unlock();
+}
+
+/* One stream through the device head: (s, t) = (0, 1) reuses the cached
+ * time embeddings. `raw` is the latent state (lsd = 0) or raw noise scaled
+ * by sqrt(temperature) on the device (lsd = 1). */
+static int single(const PhononFlowHead *head, const float condition[512], const float raw[32],
+                  float s, float t, int lsd, float temperature, float out[32],
+                  PhononCancelPoll cancel, void *context) {
+    if (!head || !condition || !raw || !out || !isfinite(s) || !isfinite(t) ||
+        !ph_all_finite(raw, LAT) || !ph_all_finite(condition, PH_WIDTH) || !ph_init())
+        return 0;
+    ph_lock();
+    PhononFlowHeadDevice *h = lookup(head, 1);
+    float result[LAT];
+    int ok = h != NULL;
+    if (ok) {
+        float staged[PH_WIDTH + LAT];
+        memcpy(staged, condition, sizeof(float) * PH_WIDTH);
+        memcpy(staged + PH_WIDTH, raw, sizeof(float) * LAT);
+        float *cond = h->stage, *state = h->stage + PH_WIDTH;
+        const int lsd_times = s == 0.0f && t == 1.0f;
+        ok = pgpu_copy_h2d(h->stream, h->stage, staged, sizeof(staged)) &&
+             (lsd ? pgpu_head_noise(h->stream, state, 1, temperature, h->noise, h->noise_split,
+                                    h->status)
+                  : pgpu_split_rows(h->stream, state, 1, LAT, h->noise_split, h->status)) &&
+             (lsd_times || enqueue_tsum(h, s, t, h->tsum)) &&
+             enqueue_forward(h, 1, cond, lsd_times ? h->tsum_lsd : h->tsum, h->velocity, NULL,
+                             cancel, context) &&
+             (!lsd || pgpu_head_finish(h->stream, h->noise, h->velocity, 1, h->stage, NULL, 0,
+                                       NULL, h->status)) &&
+             pgpu_copy_d2h(h->stream, result, lsd ? h->stage : h->velocity, sizeof(result)) &&
+             phonon_flow_head_device_sync(h);
+        if (!ok)
+            (void)phonon_flow_head_device_sync(h);  /* drain and clear the record */
+    }
+    ph_unlock();
+    if (!ok || (cancel && cancel(context)))
+        return 0;
+    memcpy(out, result, sizeof(result));
+    return 1;
+}
+
+int phonon_flow_head_forward(const PhononFlowHead *head, const float condition[512],
+                             const float normalized_state[PHONON_LATENT_WIDTH], float s, float t,
+                             float velocity[PHONON_LATENT_WIDTH]) {
+    return single(head, condition, normalized_state, s, t, 0, 1.0f, velocity, NULL, NULL);
+}
+
+int phonon_flow_lsd_one_step_cancel(const PhononFlowHead *head, const float condition[512],
+                                    const float raw_noise[32], float temperature, float output[32],
+                                    PhononCancelPoll cancel, void *context) {
+    if (!(temperature > 0.0f) || !isfinite(temperature))
+        return 0;
+    return single(head, condition, raw_noise, 0.0f, 1.0f, 1, temperature, output, cancel,
+                  context);
+}
+
+int phonon_flow_lsd_one_step(const PhononFlowHead *head, const float condition[512],
+                             const float raw_noise[PHONON_LATENT_WIDTH], float temperature,
+                             float normalized_latent[PHONON_LATENT_WIDTH]) {
+    return phonon_flow_lsd_one_step_cancel(head, condition, raw_noise, temperature,
+                                           normalized_latent, NULL, NULL);
+}

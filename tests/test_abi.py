@@ -57,6 +57,12 @@ def test_struct_layouts_match_the_reference(pkg):
     assert ctypes.sizeof(pkg.PhononKvCache) == 32
     assert pkg.PhononTensorView.data.offset == 8 + 64
     assert ctypes.sizeof(pkg.PhononFlowLayerWeights) == 64
+    # PhononFlowHead: 68 PhononTensorView (96 B each) in the reference's field
+    # order (src/phonon_sampler.h:51-60).
+    assert ctypes.sizeof(pkg.PhononTensorView) == 96
+    assert ctypes.sizeof(pkg.PhononFlowHead) == 68 * 96
+    assert pkg.PhononFlowHead.block_ada_weight.offset == 16 * 96
+    assert pkg.PhononFlowHead.final_ada_weight.offset == 64 * 96
 
 
 def test_library_has_no_cpu_compute_symbols(pkg):

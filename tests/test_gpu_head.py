@@ -1,0 +1,150 @@
+"""GPU parity of the flow head (phonon_sampler.h) through the C-ABI: the
+reference-signature functions against the reference's own synthetic-head
+golden vector and the oracle, and the batched device LSD step (with the EOS
+logit) against the oracle per stream. Tolerance: 1e-4 normwise relative
+(fp32-accurate projections; device expf/sincosf vs libm)."""
+import ctypes
+
+import numpy as np
+import pytest
+
+import helpers
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-4
+GOLD = __import__("json").load(open(helpers.GOLDEN_DIR + "/reference_vectors.json"))
+
+
+def fp(a):
+    return a.ctypes.data_as(ctypes.POINTER(ctypes.c_float))
+
+
+def float_head(bits):
+    return {k: helpers.bf16_float(v) for k, v in bits.items()}
+
+
+def rel(a, b):
+    return float(np.max(np.abs(np.asarray(a, np.float64) - b)) / max(np.max(np.abs(b)), 1e-30))
+
+
+def test_head_forward_matches_reference_golden(lib, pkg, oracle, oracle_mod):
+    """The reference's synthetic head (tests/test_phonon_sampler.c:148-195):
+    velocity at (s, t) = (0, 1) within the reference test's 2e-4 of its
+    PyTorch values, and within 1e-4 of the oracle."""
+    g = GOLD["flow_head_synthetic"]
+    bits = helpers.reference_flow_head_bits()
+    views = pkg.Views()
+    head = views.flow_head(bits)
+    condition, state = helpers.reference_flow_head_inputs()
+    out = np.zeros(32, np.float32)
+    assert lib.phonon_flow_head_forward(ctypes.byref(head), fp(condition), fp(state), 0.0, 1.0,
+                                        fp(out)), pkg.last_error(lib)
+    assert np.max(np.abs(out - np.asarray(g["expected"], np.float32))) < g["tolerance"]
+    ok, ref = oracle_mod.OracleHead(oracle, float_head(bits)).forward(condition, state, 0.0, 1.0)
+    assert ok and rel(out, ref) < TOL
+    lib.phonon_flow_head_release(ctypes.byref(head))
+
+
+def test_head_forward_other_flow_times(lib, pkg, oracle, oracle_mod):
+    bits = helpers.random_flow_head_bits(21)
+    views = pkg.Views()
+    head = views.flow_head(bits)
+    oh = oracle_mod.OracleHead(oracle, float_head(bits))
+    rng = np.random.default_rng(22)
+    for s, t in ((0.0, 1.0), (0.25, 0.75), (0.9, 0.1), (0.0, 1.0)):
+        condition = rng.standard_normal(512).astype(np.float32)
+        state = rng.standard_normal(32).astype(np.float32)
+        out = np.zeros(32, np.float32)
+        assert lib.phonon_flow_head_forward(ctypes.byref(head), fp(condition), fp(state), s, t,
+                                            fp(out)), pkg.last_error(lib)
+        ok, ref = oh.forward(condition, state, s, t)
+        assert ok and rel(out, ref) < TOL, (s, t, rel(out, ref))
+    lib.phonon_flow_head_release(ctypes.byref(head))
+
+
+def test_lsd_one_step_and_cancel(lib, pkg, oracle, oracle_mod):
+    """phonon_flow_lsd_one_step against the oracle; the cancel variant
+    returns 0 when its poll fires (here at the 4th of 7 polls) and succeeds
+    when it never does; a non-positive temperature or a non-finite noise
+    value fails."""
+    bits = helpers.random_flow_head_bits(23)
+    views = pkg.Views()
+    head = views.flow_head(bits)
+    oh = oracle_mod.OracleHead(oracle, float_head(bits))
+    rng = np.random.default_rng(24)
+    condition = rng.standard_normal(512).astype(np.float32)
+    raw = rng.standard_normal(32).astype(np.float32)
+    out = np.zeros(32, np.float32)
+    assert lib.phonon_flow_lsd_one_step(ctypes.byref(head), fp(condition), fp(raw), 0.8, fp(out))
+    ok, ref = oh.lsd_one_step(condition, raw, 0.8)
+    assert ok and rel(out, ref) < TOL
+
+    CANCEL = ctypes.CFUNCTYPE(ctypes.c_int, ctypes.c_void_p)
+    polls = []
+
+    def poll(_ctx):
+        polls.append(1)
+        return 1 if len(polls) == 4 else 0
+
+    cancel = CANCEL(poll)
+    out2 = np.full(32, 7.0, np.float32)
+    assert not lib.phonon_flow_lsd_one_step_cancel(ctypes.byref(head), fp(condition), fp(raw),
+                                                   0.8, fp(out2), cancel, None)
+    assert np.all(out2 == 7.0)  # nothing published
+    never = CANCEL(lambda _ctx: 0)
+    assert lib.phonon_flow_lsd_one_step_cancel(ctypes.byref(head), fp(condition), fp(raw), 0.8,
+                                               fp(out2), never, None)
+    assert np.array_equal(out2, out)
+    assert not lib.phonon_flow_lsd_one_step(ctypes.byref(head), fp(condition), fp(raw), 0.0,
+                                            fp(out))
+    bad = raw.copy()
+    bad[5] = np.nan
+    assert not lib.phonon_flow_lsd_one_step(ctypes.byref(head), fp(condition), fp(bad), 0.8,
+                                            fp(out))
+    lib.phonon_flow_head_release(ctypes.byref(head))
+
+
+@pytest.mark.parametrize("streams", [1, 5, 16, 17, 64])
+def test_batched_lsd_and_eos_vs_oracle(lib, pkg, oracle, oracle_mod, streams):
+    """The device LSD step of B streams with the EOS logit, against the
+    oracle per stream; then a NaN in one stream's noise is reported by
+    sync."""
+    bits = helpers.random_flow_head_bits(25)
+    rng = np.random.default_rng(26)
+    eos_w = helpers.bf16_bits(rng.standard_normal(512).astype(np.float32) * 0.05)
+    eos_b = helpers.bf16_bits(np.array([0.125], np.float32))
+    views = pkg.Views()
+    head = views.flow_head(bits)
+    ew, eb = views.bf16(eos_w.reshape(1, 512), (1, 512)), views.bf16(eos_b, (1,))
+    dev = ctypes.c_void_p()
+    assert lib.phonon_flow_head_device_create(ctypes.byref(head), ctypes.byref(ew),
+                                              ctypes.byref(eb), 64, ctypes.byref(dev)), \
+        pkg.last_error(lib)
+    stream = lib.phonon_flow_head_device_stream(dev)
+    cond = rng.standard_normal((streams, 512)).astype(np.float32)
+    raw = rng.standard_normal((streams, 32)).astype(np.float32)
+    dc, dr = pkg.DeviceBuffer(lib, cond.nbytes), pkg.DeviceBuffer(lib, raw.nbytes)
+    dl, de = pkg.DeviceBuffer(lib, raw.nbytes), pkg.DeviceBuffer(lib, streams * 4)
+    dc.upload(cond)
+    dr.upload(raw)
+    assert lib.phonon_flow_head_device_lsd(dev, streams, dc.ptr, dr.ptr, 0.7, dl.ptr, de.ptr)
+    assert lib.phonon_flow_head_device_sync(dev), pkg.last_error(lib)
+    lat = np.zeros((streams, 32), np.float32)
+    eos = np.zeros(streams, np.float32)
+    assert lib.pgpu_copy_d2h(stream, lat.ctypes.data, dl.ptr, lat.nbytes)
+    assert lib.pgpu_copy_d2h(stream, eos.ctypes.data, de.ptr, eos.nbytes)
+    assert lib.pgpu_stream_sync(stream)
+    oh = oracle_mod.OracleHead(oracle, float_head(bits))
+    for s in range(streams):
+        ok, ref = oh.lsd_one_step(cond[s], raw[s], 0.7)
+        assert ok and rel(lat[s], ref) < TOL, (s, rel(lat[s], ref))
+        ok, e = oh.eos_logit(helpers.bf16_float(eos_w), helpers.bf16_float(eos_b), cond[s])
+        assert ok and abs(eos[s] - e) <= TOL * max(1.0, abs(e)), (s, eos[s], e)
+    raw[streams // 2, 3] = np.inf
+    dr.upload(raw)
+    assert lib.phonon_flow_head_device_lsd(dev, streams, dc.ptr, dr.ptr, 0.7, dl.ptr, None)
+    assert not lib.phonon_flow_head_device_sync(dev)
+    assert lib.phonon_flow_head_device_sync(dev)  # the record was cleared
+    for b in (dc, dr, dl, de):
+        b.free()
+    lib.phonon_flow_head_device_destroy(dev)
