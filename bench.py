@@ -460,6 +460,71 @@ def q8_matvec_bench(pkg, lib, seed=1, calls=2000):
     return res
 
 
+def flow_head_bench(pkg, lib, streams=64, calls=200, seed=11, graph=1):
+    """The flow head's batched LSD step (phonon_flow_head_device_lsd: noise
+    scaling, input/condition projections, seven adaLN projections as one, six
+    residual MLP blocks, final layer, EOS logit) for `streams` streams, on a
+    random BF16 head of the reference's shapes; and the reference-signature
+    phonon_flow_lsd_one_step (one stream, host buffers, synchronous)."""
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import helpers
+    bits = helpers.random_flow_head_bits(seed)
+    rng = np.random.default_rng(seed + 1)
+    eos_w = helpers.bf16_bits(rng.standard_normal(512).astype(np.float32) * 0.05)
+    eos_b = helpers.bf16_bits(np.array([0.1], np.float32))
+    views = pkg.Views()
+    head = views.flow_head(bits)
+    ew, eb = views.bf16(eos_w.reshape(1, 512), (1, 512)), views.bf16(eos_b, (1,))
+    dev = ctypes.c_void_p()
+    assert lib.phonon_flow_head_device_create(ctypes.byref(head), ctypes.byref(ew),
+                                              ctypes.byref(eb), streams, ctypes.byref(dev))
+    assert lib.phonon_flow_head_device_set_graph(dev, graph)
+    stream = lib.phonon_flow_head_device_stream(dev)
+    cond = pkg.DeviceBuffer(lib, streams * 512 * 4)
+    raw = pkg.DeviceBuffer(lib, streams * 32 * 4)
+    lat = pkg.DeviceBuffer(lib, streams * 32 * 4)
+    eos = pkg.DeviceBuffer(lib, streams * 4)
+    cond.upload(rng.standard_normal((streams, 512)).astype(np.float32))
+    raw.upload(rng.standard_normal((streams, 32)).astype(np.float32))
+    for _ in range(5):
+        assert lib.phonon_flow_head_device_lsd(dev, streams, cond.ptr, raw.ptr, 0.7, lat.ptr,
+                                               eos.ptr)
+    assert lib.phonon_flow_head_device_sync(dev)
+    timer = Timer(lib, stream)
+    timer.start()
+    for _ in range(calls):
+        lib.phonon_flow_head_device_lsd(dev, streams, cond.ptr, raw.ptr, 0.7, lat.ptr, eos.ptr)
+    ms = timer.stop_ms() / calls
+    clean = bool(lib.phonon_flow_head_device_sync(dev))
+    weight_bytes = 2 * (512 * 32 + 512 * 512 + 10240 * 512 + 12 * 512 * 512 + 32 * 512 + 512)
+    c1 = np.random.default_rng(seed + 2).standard_normal(512).astype(np.float32)
+    n1 = np.random.default_rng(seed + 3).standard_normal(32).astype(np.float32)
+    o1 = np.zeros(32, np.float32)
+    fpp = lambda a: a.ctypes.data_as(ctypes.POINTER(ctypes.c_float))  # noqa: E731
+    assert lib.phonon_flow_lsd_one_step(ctypes.byref(head), fpp(c1), fpp(n1), 0.7, fpp(o1))
+    t0 = time.perf_counter()
+    reps = 100
+    for _ in range(reps):
+        lib.phonon_flow_lsd_one_step(ctypes.byref(head), fpp(c1), fpp(n1), 0.7, fpp(o1))
+    single_us = (time.perf_counter() - t0) / reps * 1e6
+    lib.phonon_flow_head_release(ctypes.byref(head))
+    for b in (cond, raw, lat, eos):
+        b.free()
+    lib.phonon_flow_head_device_destroy(dev)
+    return {"workload": f"flow head LSD step + EOS logit, B={streams} streams, BF16 head of the "
+                        f"reference's shapes (6 adaLN blocks, 8.68 M weights per step)",
+            "us_per_step": round(ms * 1e3, 2),
+            "frames_per_s": round(streams / (ms * 1e-3), 1),
+            "launches_per_step": 15,
+            "weight_bytes_per_step": weight_bytes,
+            "weight_GBps": round(weight_bytes / (ms * 1e-3) / 1e9, 1),
+            "hbm_frac": round(weight_bytes / (ms * 1e-3) / 8e12, 4),
+            "single_stream_api_us": round(single_us, 1),
+            "single_stream_api": "phonon_flow_lsd_one_step: host buffers in and out, "
+                                 "synchronous",
+            "clean": clean}
+
+
 def attention_curve(pkg, lib, seed=9):
     """One attention layer decode (H=8, dh=64): append + attention per step,
     vs context length, as one 1-layer batched step of one stream."""
@@ -480,6 +545,31 @@ def attention_curve(pkg, lib, seed=9):
     return {"us_per_layer_step_vs_context": out,
             "note": f"one stream, one layer (LN, QKV+RoPE+append, attention, out, MLP) in "
                     f"the library's default step mode; contexts c .. c+{reps - 1}"}
+
+
+def cpu_flow_head(seed=11, budget_s=2.0):
+    """The oracle's LSD step of the flow head (the reference's per-frame CPU
+    head restated in C), one stream per call on one thread."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import oracle_py
+    import helpers
+    bits = helpers.random_flow_head_bits(seed)
+    oh = oracle_py.OracleHead(oracle_py.Oracle(), {k: helpers.bf16_float(v)
+                                                   for k, v in bits.items()})
+    rng = np.random.default_rng(seed + 2)
+    cond = rng.standard_normal(512).astype(np.float32)
+    raw = rng.standard_normal(32).astype(np.float32)
+    frames, elapsed = 0, 0.0
+    while elapsed < budget_s:
+        t0 = time.perf_counter()
+        ok, _ = oh.lsd_one_step(cond, raw, 0.7)
+        elapsed += time.perf_counter() - t0
+        assert ok
+        frames += 1
+    return {"value": round(frames / elapsed, 1), "unit": "frames/s", "cores": 1, "kind": "port",
+            "sample": f"{frames} LSD steps of one stream (flow head forward at (0, 1), "
+                      f"{elapsed:.1f} s)"}
 
 
 def cpu_baseline(pkg, lib, layers, lengths, seed, budget_s=10.0):
@@ -536,6 +626,8 @@ def main():
                     help="only the headline B=64 line (no B=1, matvec, curve, CPU)")
     ap.add_argument("--large-batch", action="store_true",
                     help="run only the B=256 decode + batched prefill workload")
+    ap.add_argument("--flow-head", action="store_true",
+                    help="run only the flow head LSD step measurement")
     ap.add_argument("--pmc-program", action="store_true",
                     help="run only the attention kernel and a calibration copy, for "
                          "rocprofv3 --pmc passes")
@@ -556,6 +648,12 @@ def main():
         return
     if args.large_batch:
         print(json.dumps(large_batch_with_prefill(pkg, lib, args.seed)), flush=True)
+        return
+    if args.flow_head:
+        for streams in (64, 1):
+            for graph in (1, 0):
+                r = flow_head_bench(pkg, lib, streams=streams, graph=graph)
+                print(json.dumps(dict(r, graph=graph)), flush=True)
         return
 
     lengths = np.random.default_rng(args.seed).integers(1, 2049, size=args.batch) - 1
@@ -603,9 +701,13 @@ def main():
         log(f"B=256 + prefill: {line['b256_with_prefill']}")
         line["q8_matvec_2048x512"] = q8_matvec_bench(pkg, lib)
         log(f"q8 matvec: {line['q8_matvec_2048x512']}")
+        line["flow_head"] = {"b64": flow_head_bench(pkg, lib, streams=64),
+                             "b1": flow_head_bench(pkg, lib, streams=1)}
+        log(f"flow head: {line['flow_head']}")
         line["attention_layer_curve"] = attention_curve(pkg, lib)
         log(f"attention curve: {line['attention_layer_curve']}")
         line["cpu_baseline"] = cpu_baseline(pkg, lib, args.layers, lengths, args.seed)
+        line["cpu_baseline"]["flow_head"] = cpu_flow_head()
         log(f"cpu baseline: {line['cpu_baseline']}")
     print(json.dumps(line), flush=True)
 

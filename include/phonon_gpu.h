@@ -233,16 +233,35 @@ int pgpu_attention_merge(void *stream, const pgpu_attention_scratch *scratch,
                          const int32_t *positions, int streams, int heads, int max_splits,
                          float *out, uint16_t *out_split, int *status);
 
-/* -- flow head rows (pgpu_head.hip) -- */
-/* noise = raw * sqrt(temperature) ([streams][32]) and its split fragments
- * (K = 32); temperature must be positive and finite. */
-int pgpu_head_noise(void *stream, const float *raw, int streams, float temperature, float *noise,
-                    uint16_t *noise_split, int *status);
-/* Split fragments (K = 512) of LN(x; w, b optional, eps) * (1 + scale) +
- * shift, where shift and scale are rows of ld floats ([streams][ld]). */
-int pgpu_head_ln_mod(void *stream, const float *x, int streams, const float *w, const float *b,
-                     float eps, const float *shift, const float *scale, int ld, uint16_t *xs,
-                     int *status);
+/* -- flow head launches (pgpu_head.hip); BF16 matrices -- */
+/* One launch of three independent parts: silu_split = split fragments of
+ * SiLU((cond_w . conditions + cond_bias) + tsum) (tsum optional); if eos_w
+ * (16 rows, row 0 live): eos_rows [streams][eos_ld] = eos_w . conditions +
+ * eos_bias; noise = raw * scale ([streams][32], scale positive and finite)
+ * and its split fragments (K = 32). */
+int pgpu_head_front(void *stream, const pgpu_matrix *cond_w, const float *conditions, int streams,
+                    const float *cond_bias, const float *tsum, uint16_t *silu_split,
+                    const pgpu_matrix *eos_w, const float *eos_bias, float *eos_rows, int eos_ld,
+                    const float *raw, float scale, float *noise, uint16_t *noise_split,
+                    int *status);
+/* One launch: mod [streams][ld_mod] = ada_w . silu + ada_bias and
+ * x [streams][512] = input_w . noise + input_bias. */
+int pgpu_head_mod(void *stream, const pgpu_matrix *ada_w, const uint16_t *silu_split, int streams,
+                  const float *ada_bias, float *mod, int ld_mod, const pgpu_matrix *input_w,
+                  const uint16_t *noise_split, const float *input_bias, float *x, int *status);
+/* out_split = split fragments of SiLU(w . h + bias), h = LN(x; norm_w, norm_b
+ * optional, eps) * (1 + scale) + shift, shift = mod rows [streams][ld_mod],
+ * scale 512 columns further. */
+int pgpu_head_mlp_in(void *stream, const pgpu_matrix *w, const float *x, int streams,
+                     const float *norm_w, const float *norm_b, float eps, const float *mod,
+                     int ld_mod, const float *bias, uint16_t *out_split, int *status);
+/* out [streams][w->rows] = (residual +) (w . h + bias), h = LN(x; eps) *
+ * (1 + scale) + shift as above; with a residual, `ones` is a [w->rows]
+ * vector of 1.0f. If eos: eos[s] = eos_rows[s * eos_ld]. */
+int pgpu_head_final(void *stream, const pgpu_matrix *w, const float *x, int streams, float eps,
+                    const float *mod, int ld_mod, const float *bias, const float *residual,
+                    const float *ones, float *out, const float *eos_rows, int eos_ld, float *eos,
+                    int *status);
 /* Split fragments (K = 256, stream 0) of [cos | sin](value * freqs[128]). */
 int pgpu_head_time_phase(void *stream, const float *freqs, float value, uint16_t *xs,
                          int *status);
@@ -250,9 +269,6 @@ int pgpu_head_time_phase(void *stream, const float *freqs, float value, uint16_t
  * rms(v) = sqrt(mean(v^2) + 1e-5). */
 int pgpu_head_time_sum(void *stream, const float *out0, const float *out1, const float *alpha0,
                        const float *alpha1, float *tsum, int *status);
-/* latent = noise + velocity ([streams][32]); if eos: eos[s] = eos_rows[s * eos_ld]. */
-int pgpu_head_finish(void *stream, const float *noise, const float *velocity, int streams,
-                     float *latent, const float *eos_rows, int eos_ld, float *eos, int *status);
 
 /* -- rows and elements (pgpu_elementwise.hip) -- */
 int pgpu_ln_split(void *stream, const float *x, int streams, const float *w, const float *b,

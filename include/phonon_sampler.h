@@ -78,6 +78,10 @@ void phonon_flow_head_device_destroy(PhononFlowHeadDevice *head);
 int phonon_flow_head_device_lsd(PhononFlowHeadDevice *head, size_t streams,
                                 const float *conditions, const float *raw_noise,
                                 float temperature, float *latents, float *eos_logits);
+/* use_graph = 1 (the default): the step's kernels are captured in a HIP
+ * graph per (streams, buffers, temperature), two kept, and replayed; 0:
+ * each kernel is launched directly. */
+int phonon_flow_head_device_set_graph(PhononFlowHeadDevice *head, int use_graph);
 /* The head's HIP stream (for event timing by the caller). */
 void *phonon_flow_head_device_stream(const PhononFlowHeadDevice *head);
 /* Waits for enqueued calls; returns 1 iff none saw a non-finite value (and

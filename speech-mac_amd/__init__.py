@@ -224,11 +224,14 @@ EXPORTS = {
     "pgpu_flow_launch": (_i, [_vp, _vp, _kvp]),
     "pgpu_gemm_silu_split": (_i, [_vp, _vp, _vp, _i, _vp, _vp, _vp, _vp]),
     "pgpu_gemm_gated": (_i, [_vp, _vp, _vp, _i, _vp, _vp, _i, _vp, _vp, _vp]),
-    "pgpu_head_noise": (_i, [_vp, _vp, _i, _f, _vp, _vp, _vp]),
-    "pgpu_head_ln_mod": (_i, [_vp, _vp, _i, _vp, _vp, _f, _vp, _vp, _i, _vp, _vp]),
+    "pgpu_head_front": (_i, [_vp, _vp, _vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _i, _vp, _f,
+                             _vp, _vp, _vp]),
+    "pgpu_head_mod": (_i, [_vp, _vp, _vp, _i, _vp, _vp, _i, _vp, _vp, _vp, _vp, _vp]),
+    "pgpu_head_mlp_in": (_i, [_vp, _vp, _vp, _i, _vp, _vp, _f, _vp, _i, _vp, _vp, _vp]),
+    "pgpu_head_final": (_i, [_vp, _vp, _vp, _i, _f, _vp, _i, _vp, _vp, _vp, _vp, _vp, _i, _vp,
+                             _vp]),
     "pgpu_head_time_phase": (_i, [_vp, _vp, _f, _vp, _vp]),
     "pgpu_head_time_sum": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp]),
-    "pgpu_head_finish": (_i, [_vp, _vp, _vp, _i, _vp, _vp, _i, _vp, _vp]),
     "phonon_flow_head_forward": (_i, [_vp, _vp, _vp, _f, _f, _vp]),
     "phonon_flow_lsd_one_step": (_i, [_vp, _vp, _vp, _f, _vp]),
     "phonon_flow_lsd_one_step_cancel": (_i, [_vp, _vp, _vp, _f, _vp, _vp, _vp]),
@@ -237,6 +240,7 @@ EXPORTS = {
     "phonon_flow_head_device_create": (_i, [_vp, _vp, _vp, _sz, _pp]),
     "phonon_flow_head_device_destroy": (None, [_vp]),
     "phonon_flow_head_device_lsd": (_i, [_vp, _sz, _vp, _vp, _f, _vp, _vp]),
+    "phonon_flow_head_device_set_graph": (_i, [_vp, _i]),
     "phonon_flow_head_device_stream": (_vp, [_vp]),
     "phonon_flow_head_device_sync": (_i, [_vp]),
     "pgpu_flow_finish": (_i, [_vp, _vp, _sz, _vp, _i]),

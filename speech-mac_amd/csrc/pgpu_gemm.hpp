@@ -24,7 +24,11 @@
 //      read from global memory (SRC_SPLIT) or built in LDS by a prologue:
 //      SRC_LN   LayerNorm of fp32 rows [streams][512];
 //      SRC_ROWS fp32 rows [streams][512] as they are;
-//      SRC_ATTN merge of the split-attention partials (max, sum, acc).
+//      SRC_ATTN merge of the split-attention partials (max, sum, acc);
+//      SRC_LN_MOD LayerNorm (optional affine) then adaLN modulation
+//               h * (1 + scale) + shift by per-stream rows (flow head);
+//      SRC_SPLIT_LDS split fragments from global memory copied into LDS
+//               once per work-group (a K = 512 projection of many rows).
 // Arithmetic
 //   Q8: per 32-column block, c = W_q8 . (X_hi + X_mid + X_lo) by three MFMAs
 //   from zero (int8 and bf16 terms multiply exactly), then acc += scale*c,
@@ -41,7 +45,14 @@
 
 namespace pgpu {
 
-enum Source { SRC_SPLIT = 0, SRC_LN = 1, SRC_ATTN = 2, SRC_ROWS = 3 };
+enum Source {
+    SRC_SPLIT = 0,
+    SRC_LN = 1,
+    SRC_ATTN = 2,
+    SRC_ROWS = 3,
+    SRC_LN_MOD = 4,
+    SRC_SPLIT_LDS = 5,
+};
 enum Epilogue {
     EPI_STORE = 0,
     EPI_RESIDUAL = 1,
@@ -84,6 +95,8 @@ struct GemmArgs {
     const float *bias2;       // SILU_SPLIT: optional second [n_rows] vector
     const float *gate;        // GATED: [streams][ld_gate] rows (columns [0, n_rows))
     int ld_gate;
+    const float *mod;         // SRC_LN_MOD: shift row at mod + s * ld_mod, scale at +512
+    int ld_mod;
 };
 
 // ---------------------------------------------------------------------------
@@ -262,6 +275,82 @@ __device__ inline bool rows_ln(Rows2 &r, const float *lw, const float *lb, float
         lds_store8(bsh, 2 * wave + i, j >> 2, j & 3, u);
     }
     return bad;
+}
+
+// LayerNorm with an optional affine (lw, lb may be null), then the adaLN
+// modulation h * (1 + scale) + shift by the stream's own rows (shift at
+// mod + s * ld, scale 512 further), in the element order of the flow head
+// (src/phonon_sampler.c:250-278, 330-334, 350-354); fp32 two-pass moments.
+// Returns true if a live output is not finite.
+__device__ inline bool rows_ln_mod(Rows2 &r, const float *lw, const float *lb, float eps,
+                                   const float *mod, int ld, int streams, int st,
+                                   uint16_t *bsh) {
+    const int wave = threadIdx.x >> 6, j = threadIdx.x & 63;
+    // Every operand is requested before the first reduction: the affine
+    // vectors once (when present), both streams' modulation rows.
+    const bool has_w = lw != nullptr, has_b = lb != nullptr;
+    float4 w0 = make_float4(1.f, 1.f, 1.f, 1.f), w1 = w0;
+    float4 b0 = make_float4(0.f, 0.f, 0.f, 0.f), b1 = b0;
+    if (has_w) w0 = *(const float4 *)(lw + j * 8), w1 = *(const float4 *)(lw + j * 8 + 4);
+    if (has_b) b0 = *(const float4 *)(lb + j * 8), b1 = *(const float4 *)(lb + j * 8 + 4);
+    const float ws[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+    const float bs[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+    float4 m4[2][4];
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+        const int s = min(st * 16 + 2 * wave + i, streams - 1);
+        const float *sh = mod + (size_t)s * ld + j * 8;
+        m4[i][0] = *(const float4 *)sh;
+        m4[i][1] = *(const float4 *)(sh + 4);
+        m4[i][2] = *(const float4 *)(sh + kWidth);
+        m4[i][3] = *(const float4 *)(sh + kWidth + 4);
+    }
+    bool bad = false;
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+        float *u = r.v[i];
+        const float shift[8] = {m4[i][0].x, m4[i][0].y, m4[i][0].z, m4[i][0].w,
+                                m4[i][1].x, m4[i][1].y, m4[i][1].z, m4[i][1].w};
+        const float scale[8] = {m4[i][2].x, m4[i][2].y, m4[i][2].z, m4[i][2].w,
+                                m4[i][3].x, m4[i][3].y, m4[i][3].z, m4[i][3].w};
+        const float mean =
+            wave_sum64(((u[0] + u[1]) + (u[2] + u[3])) + ((u[4] + u[5]) + (u[6] + u[7]))) *
+            (1.0f / kWidth);
+        float q2[2] = {0.0f, 0.0f};
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const float c = __fsub_rn(u[k], mean);
+            q2[k & 1] = fmaf(c, c, q2[k & 1]);
+        }
+        const float var = wave_sum64(q2[0] + q2[1]) * (1.0f / kWidth);
+        const float rstd = 1.0f / sqrtf(__fadd_rn(var, eps));
+        bool bad_i = false;
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            float h = __fmul_rn(__fsub_rn(u[k], mean), rstd);
+            if (has_w) h = __fmul_rn(h, ws[k]);
+            if (has_b) h = __fadd_rn(h, bs[k]);
+            u[k] = __fadd_rn(__fmul_rn(h, __fadd_rn(1.0f, scale[k])), shift[k]);
+            bad_i |= !isfinite(u[k]);
+            if (!r.live[i]) u[k] = 0.0f;
+        }
+        bad |= bad_i && r.live[i];
+        lds_store8(bsh, 2 * wave + i, j >> 2, j & 3, u);
+    }
+    return bad;
+}
+
+// The 16 streams' split fragments of tile st (K = 512) from global memory
+// into the LDS operand buffer: 16 blocks of 1536 halves, each record in the
+// same [term][lane][8] order.
+__device__ inline void split_to_lds(const uint16_t *xs, int st, uint16_t *bsh) {
+    const uint4 *src = (const uint4 *)(xs + (size_t)st * (kWidth / 32) * 1536);
+    constexpr int per_block = 1536 / 8, total = (kWidth / 32) * per_block;
+#pragma unroll
+    for (int i0 = 0; i0 < total; i0 += kTaskThreads) {
+        const int i = i0 + threadIdx.x;
+        *(uint4 *)(bsh + (i / per_block) * kLdsBlock + (i % per_block) * 8) = src[i];
+    }
 }
 
 // The loaded rows as they are (the merged attention output).
@@ -627,11 +716,15 @@ __device__ inline void gemm_wide_task(const GemmArgs &a, int bx, int st, uint16_
     bool bad_in = false;
     if constexpr (SRC == SRC_ATTN) {
         bad_in = prologue_attn(a, st, bsh);
+    } else if constexpr (SRC == SRC_SPLIT_LDS) {
+        split_to_lds(a.xs, st, bsh);
     } else {
         Rows2 r;
         rows_load(r, a.ln_x, a.streams, st);
         if constexpr (SRC == SRC_LN)
             bad_in = rows_ln(r, a.ln_w, a.ln_b, a.ln_eps, bsh);
+        else if constexpr (SRC == SRC_LN_MOD)
+            bad_in = rows_ln_mod(r, a.ln_w, a.ln_b, a.ln_eps, a.mod, a.ld_mod, a.streams, st, bsh);
         else
             rows_plain(r, bsh);
     }

@@ -1,21 +1,27 @@
-// Row kernels of the flow head (src/phonon_sampler.c:229-393) around its
-// projections (pgpu_gemm_*): noise scaling, LayerNorm + adaLN modulation into
-// split fragments, the time embedding's sincos and RMS scaling, and the
-// final Euler update. One wave per 512-wide row where a row is reduced.
+// Launches of the flow head (src/phonon_sampler.c:229-393): its projections
+// (the tasks of pgpu_gemm.hpp, BF16 weights) grouped so that one launch runs
+// every projection whose inputs are ready, with the row work fused into
+// them: noise scaling beside the first projections, LayerNorm + adaLN
+// modulation in front of each block's first MLP projection and of the final
+// layer, the Euler update and the EOS copy in the final launch. A step of B
+// streams is 15 launches: front, modulation + input, 6 x (MLP in, MLP out),
+// final. The time embedding's sincos and RMS scaling run once per (s, t).
 #include <cmath>
 
-#include "pgpu_common.hpp"
+#include "pgpu_gemm.hpp"
 #include "phonon_gpu.h"
 
 namespace pgpu {
 namespace {
 
-// noise = raw * sqrt(T) (src/phonon_sampler.c:371-376) as fp32 rows and as
-// split fragments (K = 32) for the input projection. One thread per 8 values.
-__global__ __launch_bounds__(256) void k_head_noise(const float *__restrict__ raw, int streams,
-                                                    float scale, float *__restrict__ noise,
-                                                    uint16_t *__restrict__ xs, int *status) {
-    const int i = blockIdx.x * 256 + threadIdx.x;
+// noise = raw * scale (src/phonon_sampler.c:371-376 with scale = sqrt(T))
+// as fp32 rows and as split fragments (K = 32) for the input projection.
+// One thread per 8 values; `first` is the thread index of this block's
+// thread 0.
+__device__ inline void noise_rows(const float *__restrict__ raw, int streams, float scale,
+                                  float *__restrict__ noise, uint16_t *__restrict__ xs,
+                                  int *status, int first) {
+    const int i = first + threadIdx.x;
     const int s = i >> 2, g = i & 3;
     if (s >= streams) return;
     const float *r = raw + (size_t)s * 32 + g * 8;
@@ -33,48 +39,89 @@ __global__ __launch_bounds__(256) void k_head_noise(const float *__restrict__ ra
     flag_nonfinite(status, bad);
 }
 
-// h = LN(x) (eps, optional w and b) then h * (1 + scale) + shift, into split
-// fragments (K = 512). Replaces flow_layer_norm and the modulation of
-// src/phonon_sampler.c:250-278, 330-334, 350-354: fp32 two-pass moments
-// instead of the float cascade mean and double variance; then the same
-// element operations in the same order. shift/scale rows: mod + s * ld.
-__global__ __launch_bounds__(256) void k_head_ln_mod(const float *__restrict__ x, int streams,
-                                                     const float *__restrict__ w,
-                                                     const float *__restrict__ b, float eps,
-                                                     const float *__restrict__ shift,
-                                                     const float *__restrict__ scale, int ld,
-                                                     uint16_t *__restrict__ xs, int *status) {
-    const int s = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
-    if (s >= streams) return;
-    const float *row = x + (size_t)s * kWidth + lane * 8;
-    const float4 a0 = *(const float4 *)row, a1 = *(const float4 *)(row + 4);
-    float v[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
-    float sum = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 8; i++) sum += v[i];
-    const float mean = wave_sum(sum) * (1.0f / kWidth);
-    float sq = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 8; i++) {
-        const float c = __fsub_rn(v[i], mean);
-        sq = fmaf(c, c, sq);
+// One projection task of a launch that runs several projections: `index`
+// counts the projection's own work-groups (row group fastest, then the
+// 16-stream tile).
+template <int SRC, int EPI>
+__device__ inline void wide_at(const GemmArgs &a, int index, uint16_t *lds) {
+    const int groups = (a.n_rows / 16 + 3) / 4;
+    gemm_wide_task<SRC, EPI, false>(a, index % groups, index / groups, lds, NoWait{});
+}
+
+template <int EPI>
+__device__ inline void split_at(const GemmArgs &a, int index, uint16_t *lds) {
+    const int tiles = a.n_rows / 16;
+    gemm_split_task<EPI, false>(a, index % tiles, index / tiles, lds, NoWait{});
+}
+
+__host__ __device__ inline int wide_groups(const GemmArgs &a) {
+    return (a.n_rows / 16 + 3) / 4 * ((a.streams + 15) / 16);
+}
+
+__host__ __device__ inline int split_groups(const GemmArgs &a) {
+    return a.n_rows / 16 * ((a.streams + 15) / 16);
+}
+
+struct NoiseArgs {
+    const float *raw;
+    float scale;
+    float *noise;
+    uint16_t *xs;
+};
+
+// First launch of a head step: the condition's projection into split
+// fragments of SiLU(y) (y = cond_embed(c) + tsum), the EOS row of the
+// condition (optional) and the noise rows; none depends on another.
+__global__ __launch_bounds__(kTaskThreads) void k_head_front(GemmArgs cond, GemmArgs eos,
+                                                             int with_eos, NoiseArgs nz) {
+    __shared__ uint4 lds4[kTaskLds / 8];
+    uint16_t *lds = (uint16_t *)lds4;
+    int b = blockIdx.x;
+    const int n_cond = wide_groups(cond);
+    if (b < n_cond) return wide_at<SRC_ROWS, EPI_SILU_SPLIT>(cond, b, lds);
+    b -= n_cond;
+    if (with_eos) {
+        if (b < wide_groups(eos)) return wide_at<SRC_ROWS, EPI_STORE>(eos, b, lds);
+        b -= wide_groups(eos);
     }
-    const float var = wave_sum(sq) * (1.0f / kWidth);
-    const float inverse = 1.0f / sqrtf(__fadd_rn(var, eps));
-    const float *sh = shift + (size_t)s * ld + lane * 8, *sc = scale + (size_t)s * ld + lane * 8;
+    noise_rows(nz.raw, cond.streams, nz.scale, nz.noise, nz.xs, cond.status, b * kTaskThreads);
+}
+
+// Second launch: the seven adaLN projections as one (reading SiLU(y); each
+// work-group copies its 16 streams' fragments into LDS once for 64 rows) and
+// the input projection of the noise.
+__global__ __launch_bounds__(kTaskThreads) void k_head_mod(GemmArgs ada, GemmArgs input) {
+    __shared__ uint4 lds4[kTaskLds / 8];
+    uint16_t *lds = (uint16_t *)lds4;
+    const int b = blockIdx.x, n_ada = wide_groups(ada);
+    if (b < n_ada) return wide_at<SRC_SPLIT_LDS, EPI_STORE>(ada, b, lds);
+    split_at<EPI_STORE>(input, b - n_ada, lds);
+}
+
+// A block's first MLP projection with its LayerNorm and modulation fused in
+// front: split fragments of SiLU(mlp_0(LN(x) * (1 + scale) + shift)).
+__global__ __launch_bounds__(kTaskThreads) void k_head_mlp_in(GemmArgs a) {
+    __shared__ uint4 lds4[kTaskLds / 8];
+    wide_at<SRC_LN_MOD, EPI_SILU_SPLIT>(a, blockIdx.x, (uint16_t *)lds4);
+}
+
+// Last launch: the final layer on the modulated LayerNorm of x, either the
+// velocity (EPI_STORE) or noise + velocity (EPI_GATED with a gate of ones,
+// exact); one more work-group copies the EOS logits out of their padded
+// rows.
+template <int EPI>
+__global__ __launch_bounds__(kTaskThreads) void k_head_final(GemmArgs a, const float *eos_rows,
+                                                             int eos_ld, float *eos) {
+    __shared__ uint4 lds4[kTaskLds / 8];
+    const int n = wide_groups(a);
+    if ((int)blockIdx.x < n) return wide_at<SRC_LN_MOD, EPI>(a, blockIdx.x, (uint16_t *)lds4);
     bool bad = false;
-#pragma unroll
-    for (int i = 0; i < 8; i++) {
-        const int k = lane * 8 + i;
-        float h = __fmul_rn(__fsub_rn(v[i], mean), inverse);
-        if (w) h = __fmul_rn(h, w[k]);
-        if (b) h = __fadd_rn(h, b[k]);
-        const float one_plus_scale = __fadd_rn(1.0f, sc[i]);
-        v[i] = __fadd_rn(__fmul_rn(h, one_plus_scale), sh[i]);
-        bad |= !isfinite(v[i]);
+    for (int s = threadIdx.x; s < a.streams; s += kTaskThreads) {
+        const float e = eos_rows[(size_t)s * eos_ld];
+        eos[s] = e;
+        bad |= !isfinite(e);
     }
-    store_split<8>(xs, s, lane * 8, kWidth / 32, v);
-    flag_nonfinite(status, bad);
+    flag_nonfinite(a.status, bad);
 }
 
 // [cos | sin](value * freqs[0..128)) as split fragments (K = 256) of
@@ -133,51 +180,130 @@ __global__ __launch_bounds__(512) void k_head_time_sum(const float *__restrict__
     flag_nonfinite(status, !isfinite(tsum[i]));
 }
 
-// latent = noise + velocity (src/phonon_sampler.c:380-384); eos[s] =
-// eos_rows[s][0] (the one live row of the padded EOS projection).
-__global__ __launch_bounds__(256) void k_head_finish(const float *__restrict__ noise,
-                                                     const float *__restrict__ velocity,
-                                                     int streams, float *__restrict__ latent,
-                                                     const float *__restrict__ eos_rows,
-                                                     int eos_ld, float *__restrict__ eos,
-                                                     int *status) {
-    const int i = blockIdx.x * 256 + threadIdx.x;
-    if (i >= streams * 32) return;
-    const float y = __fadd_rn(noise[i], velocity[i]);
-    latent[i] = y;
-    bool bad = !isfinite(y);
-    if (eos && (i & 31) == 0) {
-        const float e = eos_rows[(size_t)(i >> 5) * eos_ld];
-        eos[i >> 5] = e;
-        bad |= !isfinite(e);
-    }
-    flag_nonfinite(status, bad);
-}
-
 }  // namespace
 }  // namespace pgpu
 
 using namespace pgpu;
 
-extern "C" int pgpu_head_noise(void *stream, const float *raw, int streams, float temperature,
-                               float *noise, uint16_t *noise_split, int *status) {
-    if (!raw || streams <= 0 || !noise || !noise_split || !(temperature > 0.0f) ||
-        !std::isfinite(temperature))
+static bool bf16_matrix(const pgpu_matrix *w, size_t rows, size_t columns) {
+    return w && w->values && !w->q8 && w->rows == rows && w->columns == columns;
+}
+
+static GemmArgs head_args(const pgpu_matrix *w, int streams, int *status) {
+    GemmArgs a{};
+    a.w = w->values;
+    a.n_rows = (int)w->rows;
+    a.k_cols = (int)w->columns;
+    a.streams = streams;
+    a.status = status;
+    return a;
+}
+
+extern "C" int pgpu_head_front(void *stream, const pgpu_matrix *cond_w, const float *conditions,
+                               int streams, const float *cond_bias, const float *tsum,
+                               uint16_t *silu_split, const pgpu_matrix *eos_w,
+                               const float *eos_bias, float *eos_rows, int eos_ld,
+                               const float *raw, float scale, float *noise,
+                               uint16_t *noise_split, int *status) {
+    if (!bf16_matrix(cond_w, kWidth, kWidth) || !conditions || streams <= 0 || !silu_split ||
+        !raw || !noise || !noise_split || !(scale > 0.0f) || !std::isfinite(scale) ||
+        (eos_w && (!bf16_matrix(eos_w, 16, kWidth) || !eos_rows || eos_ld < 16 || eos_ld % 4)))
         return bad_arguments(__func__);
-    const float scale = sqrtf(temperature);
-    const unsigned blocks = (unsigned)((streams * 4 + 255) / 256);
-    hipLaunchKernelGGL(k_head_noise, dim3(blocks), dim3(256), 0, (hipStream_t)stream, raw,
-                       streams, scale, noise, noise_split, status);
+    GemmArgs cond = head_args(cond_w, streams, status);
+    cond.ln_x = conditions;
+    cond.bias = cond_bias;
+    cond.bias2 = tsum;
+    cond.out_split = silu_split;
+    cond.out_kb = kWidth / 32;
+    GemmArgs eos{};
+    if (eos_w) {
+        eos = head_args(eos_w, streams, status);
+        eos.ln_x = conditions;
+        eos.bias = eos_bias;
+        eos.out = eos_rows;
+        eos.ld_out = eos_ld;
+    }
+    const NoiseArgs nz{raw, scale, noise, noise_split};
+    const int blocks = wide_groups(cond) + (eos_w ? wide_groups(eos) : 0) +
+                       (streams * 4 + kTaskThreads - 1) / kTaskThreads;
+    hipLaunchKernelGGL(k_head_front, dim3((unsigned)blocks), dim3(kTaskThreads), 0,
+                       (hipStream_t)stream, cond, eos, eos_w != nullptr, nz);
     return launch_ok(__func__);
 }
 
-extern "C" int pgpu_head_ln_mod(void *stream, const float *x, int streams, const float *w,
-                                const float *b, float eps, const float *shift, const float *scale,
-                                int ld, uint16_t *xs, int *status) {
-    if (!x || streams <= 0 || !shift || !scale || ld < kWidth || ld % 4 || !xs)
+extern "C" int pgpu_head_mod(void *stream, const pgpu_matrix *ada_w, const uint16_t *silu_split,
+                             int streams, const float *ada_bias, float *mod, int ld_mod,
+                             const pgpu_matrix *input_w, const uint16_t *noise_split,
+                             const float *input_bias, float *x, int *status) {
+    if (!ada_w || !bf16_matrix(ada_w, ada_w->rows, kWidth) || ada_w->rows % 16 || !silu_split ||
+        streams <= 0 || !mod || ld_mod < (int)ada_w->rows || ld_mod % 4 ||
+        !bf16_matrix(input_w, kWidth, 32) || !noise_split || !x)
         return bad_arguments(__func__);
-    hipLaunchKernelGGL(k_head_ln_mod, dim3((unsigned)((streams + 3) / 4)), dim3(256), 0,
-                       (hipStream_t)stream, x, streams, w, b, eps, shift, scale, ld, xs, status);
+    GemmArgs ada = head_args(ada_w, streams, status);
+    ada.xs = silu_split;
+    ada.bias = ada_bias;
+    ada.out = mod;
+    ada.ld_out = ld_mod;
+    GemmArgs input = head_args(input_w, streams, status);
+    input.xs = noise_split;
+    input.bias = input_bias;
+    input.out = x;
+    input.ld_out = kWidth;
+    const int blocks = wide_groups(ada) + split_groups(input);
+    hipLaunchKernelGGL(k_head_mod, dim3((unsigned)blocks), dim3(kTaskThreads), 0,
+                       (hipStream_t)stream, ada, input);
+    return launch_ok(__func__);
+}
+
+extern "C" int pgpu_head_mlp_in(void *stream, const pgpu_matrix *w, const float *x, int streams,
+                                const float *norm_w, const float *norm_b, float eps,
+                                const float *mod, int ld_mod, const float *bias,
+                                uint16_t *out_split, int *status) {
+    if (!bf16_matrix(w, kWidth, kWidth) || !x || streams <= 0 || !mod || ld_mod < 2 * kWidth ||
+        ld_mod % 4 || !out_split || !(eps > 0.0f))
+        return bad_arguments(__func__);
+    GemmArgs a = head_args(w, streams, status);
+    a.ln_x = x;
+    a.ln_w = norm_w;
+    a.ln_b = norm_b;
+    a.ln_eps = eps;
+    a.mod = mod;
+    a.ld_mod = ld_mod;
+    a.bias = bias;
+    a.out_split = out_split;
+    a.out_kb = kWidth / 32;
+    hipLaunchKernelGGL(k_head_mlp_in, dim3((unsigned)wide_groups(a)), dim3(kTaskThreads), 0,
+                       (hipStream_t)stream, a);
+    return launch_ok(__func__);
+}
+
+extern "C" int pgpu_head_final(void *stream, const pgpu_matrix *w, const float *x, int streams,
+                               float eps, const float *mod, int ld_mod, const float *bias,
+                               const float *residual, const float *ones, float *out,
+                               const float *eos_rows, int eos_ld, float *eos, int *status) {
+    if (!w || !bf16_matrix(w, w->rows, kWidth) || w->rows % 16 || !x || streams <= 0 || !mod ||
+        ld_mod < 2 * kWidth || ld_mod % 4 || !out || (residual && !ones) || !(eps > 0.0f) ||
+        (eos && (!eos_rows || eos_ld < 1)))
+        return bad_arguments(__func__);
+    GemmArgs a = head_args(w, streams, status);
+    a.ln_x = x;
+    a.ln_eps = eps;
+    a.mod = mod;
+    a.ld_mod = ld_mod;
+    a.bias = bias;
+    a.out = out;
+    a.ld_out = (int)w->rows;
+    const unsigned blocks = (unsigned)wide_groups(a) + (eos ? 1u : 0u);
+    if (residual) {
+        a.residual = residual;
+        a.gate = ones;
+        a.ld_gate = 0;
+        hipLaunchKernelGGL(k_head_final<EPI_GATED>, dim3(blocks), dim3(kTaskThreads), 0,
+                           (hipStream_t)stream, a, eos_rows, eos_ld, eos);
+    } else {
+        hipLaunchKernelGGL(k_head_final<EPI_STORE>, dim3(blocks), dim3(kTaskThreads), 0,
+                           (hipStream_t)stream, a, eos_rows, eos_ld, eos);
+    }
     return launch_ok(__func__);
 }
 
@@ -195,16 +321,5 @@ extern "C" int pgpu_head_time_sum(void *stream, const float *out0, const float *
     if (!out0 || !out1 || !alpha0 || !alpha1 || !tsum) return bad_arguments(__func__);
     hipLaunchKernelGGL(k_head_time_sum, dim3(1), dim3(512), 0, (hipStream_t)stream, out0, out1,
                        alpha0, alpha1, tsum, status);
-    return launch_ok(__func__);
-}
-
-extern "C" int pgpu_head_finish(void *stream, const float *noise, const float *velocity,
-                                int streams, float *latent, const float *eos_rows, int eos_ld,
-                                float *eos, int *status) {
-    if (!noise || !velocity || streams <= 0 || !latent || (eos && (!eos_rows || eos_ld < 1)))
-        return bad_arguments(__func__);
-    const unsigned blocks = (unsigned)((streams * 32 + 255) / 256);
-    hipLaunchKernelGGL(k_head_finish, dim3(blocks), dim3(256), 0, (hipStream_t)stream, noise,
-                       velocity, streams, latent, eos_rows, eos_ld, eos, status);
     return launch_ok(__func__);
 }

@@ -1,12 +1,13 @@
 /* Flow head on the GPU (phonon_sampler.h): src/phonon_sampler.c:280-401 as
- * a chain of projections and row kernels over B streams.
- *
- * Per call, for B streams (each projection one launch over all streams):
- *   x    = input_proj(noise)                          [B][512]
- *   s_y  = SiLU(cond_embed(condition) + tsum)         split fragments
- *   mod  = [adaLN_0 .. adaLN_5 | final adaLN](s_y)    [B][6*1536 + 1024]
- *   6 x: h = LN(x)*(1 + scale_b) + shift_b; x += gate_b * mlp_b1(SiLU(mlp_b0(h)))
- *   h    = LN(x)*(1 + scale_f) + shift_f; velocity = final(h)
+ * a chain of 15 launches over B streams (pgpu_head.hip):
+ *   front   s_y = SiLU(cond_embed(condition) + tsum)    split fragments
+ *           eos = out_eos . condition + bias            (optional)
+ *           noise = raw * sqrt(T)                        [B][32] + fragments
+ *   mod     mod = [adaLN_0 .. adaLN_5 | final adaLN](s_y) [B][6*1536 + 1024]
+ *           x   = input_proj(noise)                      [B][512]
+ *   6 x     u = SiLU(mlp_b0(LN(x)*(1 + scale_b) + shift_b))
+ *           x += gate_b * mlp_b1(u)
+ *   final   latent = noise + final(LN(x)*(1 + scale_f) + shift_f)
  * SiLU(y) is the same for all seven adaLN projections (they read only the
  * condition and the time embeddings), so they run as one 10240-row
  * projection. The time embeddings of the LSD step (s = 0, t = 1) do not
@@ -36,14 +37,23 @@ struct PhononFlowHeadDevice {
     float *b_input, *b_cond, *b_ada, *b_mlp[HB][2], *b_final, *b_eos, *b_time[2][2];
     float *norm_w[HB], *norm_b[HB], *freqs[2], *alpha[2];
     float *tsum_lsd, *tsum, *time_out; /* time_out: [2][512] */
+    float *ones;                       /* [32] of 1.0f: the Euler update's gate */
     size_t cap;                        /* streams, a multiple of 16 */
     void *buffers;
     float *noise, *x, *mod, *velocity, *eos_rows, *stage;
-    uint16_t *noise_split, *cond_split, *silu_split, *h_split, *first_split, *time_split,
-        *time_hidden;
+    uint16_t *noise_split, *silu_split, *first_split, *time_split, *time_hidden;
     int has_eos;
     int *status;
     void *stream;
+    struct {
+        void *exec;
+        size_t streams;
+        const float *conditions, *raw_noise;
+        float temperature;
+        float *latents, *eos_logits;
+    } graphs[2];
+    size_t graph_victim;
+    int eager; /* launch each kernel directly instead of replaying a graph */
 };
 
 static size_t split_elems(size_t streams, size_t k_cols) {
@@ -93,7 +103,7 @@ static int upload_vectors(PhononFlowHeadDevice *h, const PhononFlowHead *head,
                           const PhononTensorView *eos_bias) {
     const size_t total = 2 * PH_WIDTH + MOD + HB * 2 * PH_WIDTH + LAT + EOS_ROWS +
                          2 * 2 * PH_WIDTH + HB * 2 * PH_WIDTH + 2 * 128 + 2 * PH_WIDTH +
-                         2 * PH_WIDTH + 2 * PH_WIDTH;
+                         2 * PH_WIDTH + 2 * PH_WIDTH + LAT;
     float *host = calloc(total, sizeof(float));
     float *dev = host ? pgpu_malloc(total * sizeof(float)) : NULL;
     if (!dev) {
@@ -132,6 +142,9 @@ static int upload_vectors(PhononFlowHeadDevice *h, const PhononFlowHead *head,
     (void)SLOT(h->tsum_lsd, PH_WIDTH);
     (void)SLOT(h->tsum, PH_WIDTH);
     (void)SLOT(h->time_out, 2 * PH_WIDTH);
+    float *ones = SLOT(h->ones, LAT);
+    for (size_t i = 0; i < LAT; i++)
+        ones[i] = 1.0f;
 #undef TAKE
 #undef SLOT
     ok = ok && at == total && pgpu_copy_h2d(h->stream, dev, host, total * sizeof(float)) &&
@@ -143,7 +156,7 @@ static int upload_vectors(PhononFlowHeadDevice *h, const PhononFlowHead *head,
 static int alloc_buffers(PhononFlowHeadDevice *h, size_t streams) {
     const size_t cap = (streams + 15) / 16 * 16;
     const size_t floats = cap * (LAT + PH_WIDTH + MOD + LAT + EOS_ROWS) + PH_WIDTH + LAT;
-    const size_t halves = split_elems(cap, LAT) + 4 * split_elems(cap, PH_WIDTH) +
+    const size_t halves = split_elems(cap, LAT) + 2 * split_elems(cap, PH_WIDTH) +
                           split_elems(16, 256) + split_elems(16, PH_WIDTH);
     const size_t bytes = floats * sizeof(float) + halves * sizeof(uint16_t);
     char *p = pgpu_malloc(bytes);
@@ -160,9 +173,7 @@ static int alloc_buffers(PhononFlowHeadDevice *h, size_t streams) {
     h->stage = f, f += PH_WIDTH + LAT;
     uint16_t *u = (uint16_t *)f;
     h->noise_split = u, u += split_elems(cap, LAT);
-    h->cond_split = u, u += split_elems(cap, PH_WIDTH);
     h->silu_split = u, u += split_elems(cap, PH_WIDTH);
-    h->h_split = u, u += split_elems(cap, PH_WIDTH);
     h->first_split = u, u += split_elems(cap, PH_WIDTH);
     h->time_split = u, u += split_elems(16, 256);
     h->time_hidden = u;
@@ -186,42 +197,38 @@ static int enqueue_tsum(PhononFlowHeadDevice *h, float s, float t, float *tsum) 
                               h->alpha[1], tsum, h->status);
 }
 
-/* The head's forward for n streams: state_split holds the latent state's
- * split fragments (K = 32), conditions [n][512]; velocity [n][32] and, if
- * eos_rows, the padded EOS projection [n][16]. The cancel poll runs before
- * each block and before the final layer. */
-static int enqueue_forward(PhononFlowHeadDevice *h, size_t n, const float *conditions,
-                           const float *tsum, float *velocity, float *eos_rows,
-                           PhononCancelPoll cancel, void *context) {
+/* The head for n streams: conditions [n][512], raw [n][32] scaled by `scale`
+ * into the state (the noise of an LSD step, or the normalized state itself
+ * with scale 1). Writes the latent noise + velocity (lsd) or the velocity to
+ * out [n][32] and, if eos, the EOS logits. The cancel poll runs before each
+ * block and before the final layer. */
+static int enqueue_head(PhononFlowHeadDevice *h, size_t n, const float *conditions,
+                        const float *raw, float scale, const float *tsum, int lsd, float *out,
+                        float *eos, PhononCancelPoll cancel, void *context) {
     void *st = h->stream;
     const int B = (int)n;
-    const pgpu_gemm_input state = {.split = h->noise_split}, cond = {.split = h->cond_split},
-                          silu_y = {.split = h->silu_split}, hin = {.split = h->h_split},
-                          first = {.split = h->first_split};
-    if (!pgpu_split_rows(st, conditions, B, PH_WIDTH, h->cond_split, h->status) ||
-        !pgpu_gemm_store(st, &h->input, &state, B, h->b_input, h->x, PH_WIDTH, h->status) ||
-        !pgpu_gemm_silu_split(st, &h->cond, &cond, B, h->b_cond, tsum, h->silu_split,
-                              h->status) ||
-        !pgpu_gemm_store(st, &h->ada, &silu_y, B, h->b_ada, h->mod, MOD, h->status))
+    const pgpu_gemm_input first = {.split = h->first_split};
+    if (!pgpu_head_front(st, &h->cond, conditions, B, h->b_cond, tsum, h->silu_split,
+                         eos ? &h->eos : NULL, h->b_eos, h->eos_rows, EOS_ROWS, raw, scale,
+                         h->noise, h->noise_split, h->status) ||
+        !pgpu_head_mod(st, &h->ada, h->silu_split, B, h->b_ada, h->mod, MOD, &h->input,
+                       h->noise_split, h->b_input, h->x, h->status))
         return 0;
     for (size_t b = 0; b < HB; b++) {
         if (cancel && cancel(context))
             return 0;
         const float *mod = h->mod + b * ADA;
-        if (!pgpu_head_ln_mod(st, h->x, B, h->norm_w[b], h->norm_b[b], 1e-6f, mod,
-                              mod + PH_WIDTH, MOD, h->h_split, h->status) ||
-            !pgpu_gemm_silu_split(st, &h->mlp[b][0], &hin, B, h->b_mlp[b][0], NULL,
-                                  h->first_split, h->status) ||
+        if (!pgpu_head_mlp_in(st, &h->mlp[b][0], h->x, B, h->norm_w[b], h->norm_b[b], 1e-6f, mod,
+                              MOD, h->b_mlp[b][0], h->first_split, h->status) ||
             !pgpu_gemm_gated(st, &h->mlp[b][1], &first, B, h->b_mlp[b][1], mod + 2 * PH_WIDTH,
                              MOD, h->x, h->x, h->status))
             return 0;
     }
-    const float *fmod = h->mod + HB * ADA;
-    return pgpu_head_ln_mod(st, h->x, B, NULL, NULL, 1e-6f, fmod, fmod + PH_WIDTH, MOD,
-                            h->h_split, h->status) &&
-           pgpu_gemm_store(st, &h->final, &hin, B, h->b_final, velocity, LAT, h->status) &&
-           (!eos_rows ||
-            pgpu_gemm_store(st, &h->eos, &cond, B, h->b_eos, eos_rows, EOS_ROWS, h->status));
+    if (cancel && cancel(context))
+        return 0;
+    return pgpu_head_final(st, &h->final, h->x, B, 1e-6f, h->mod + HB * ADA, MOD, h->b_final,
+                           lsd ? h->noise : NULL, h->ones, out, h->eos_rows, EOS_ROWS, eos,
+                           h->status);
 }
 
 int phonon_flow_head_device_create(const PhononFlowHead *head, const PhononTensorView *eos_weight,
@@ -265,6 +272,8 @@ void phonon_flow_head_device_destroy(PhononFlowHeadDevice *h) {
         return;
     if (h->stream)
         (void)pgpu_stream_sync(h->stream);
+    for (size_t i = 0; i < 2; i++)
+        pgpu_graph_destroy(h->graphs[i].exec);
     for (size_t i = 0; i < h->nmats; i++)
         pgpu_free(h->mats[i]);
     pgpu_free(h->vec);
@@ -287,18 +296,67 @@ int phonon_flow_head_device_sync(PhononFlowHeadDevice *h) {
     return status == 0;
 }
 
+static int enqueue_lsd(PhononFlowHeadDevice *h, size_t streams, const float *conditions,
+                       const float *raw_noise, float temperature, float *latents,
+                       float *eos_logits) {
+    return enqueue_head(h, streams, conditions, raw_noise, sqrtf(temperature), h->tsum_lsd, 1,
+                        latents, eos_logits, NULL, NULL);
+}
+
+/* The step's kernels are captured once per (streams, buffers, temperature)
+ * and replayed: two captures are kept, so a caller alternating two sets of
+ * buffers replays both. */
 int phonon_flow_head_device_lsd(PhononFlowHeadDevice *h, size_t streams,
                                 const float *conditions, const float *raw_noise,
                                 float temperature, float *latents, float *eos_logits) {
     if (!h || !streams || streams > h->cap || !conditions || !raw_noise || !latents ||
         (eos_logits && !h->has_eos) || !(temperature > 0.0f) || !isfinite(temperature))
         return 0;
-    return pgpu_head_noise(h->stream, raw_noise, (int)streams, temperature, h->noise,
-                           h->noise_split, h->status) &&
-           enqueue_forward(h, streams, conditions, h->tsum_lsd, h->velocity,
-                           eos_logits ? h->eos_rows : NULL, NULL, NULL) &&
-           pgpu_head_finish(h->stream, h->noise, h->velocity, (int)streams, latents,
-                            eos_logits ? h->eos_rows : NULL, EOS_ROWS, eos_logits, h->status);
+    if (h->eager)
+        return enqueue_lsd(h, streams, conditions, raw_noise, temperature, latents, eos_logits);
+    void *exec = NULL;
+    for (size_t i = 0; i < 2 && !exec; i++)
+        if (h->graphs[i].exec && h->graphs[i].streams == streams &&
+            h->graphs[i].conditions == conditions && h->graphs[i].raw_noise == raw_noise &&
+            h->graphs[i].temperature == temperature && h->graphs[i].latents == latents &&
+            h->graphs[i].eos_logits == eos_logits)
+            exec = h->graphs[i].exec;
+    if (!exec) {
+        const size_t slot = h->graph_victim;
+        pgpu_graph_destroy(h->graphs[slot].exec);
+        h->graphs[slot].exec = NULL;
+        if (!pgpu_graph_begin(h->stream))
+            return 0;
+        const int enqueued =
+            enqueue_lsd(h, streams, conditions, raw_noise, temperature, latents, eos_logits);
+        const int ended = pgpu_graph_end(h->stream, &exec);
+        if (!enqueued || !ended) {
+            pgpu_graph_destroy(exec);
+            return 0;
+        }
+        h->graphs[slot].exec = exec;
+        h->graphs[slot].streams = streams;
+        h->graphs[slot].conditions = conditions;
+        h->graphs[slot].raw_noise = raw_noise;
+        h->graphs[slot].temperature = temperature;
+        h->graphs[slot].latents = latents;
+        h->graphs[slot].eos_logits = eos_logits;
+        h->graph_victim = 1 - slot;
+    }
+    return pgpu_graph_launch(exec, h->stream);
+}
+
+int phonon_flow_head_device_set_graph(PhononFlowHeadDevice *h, int use_graph) {
+    if (!h)
+        return 0;
+    if (!pgpu_stream_sync(h->stream))
+        return 0;
+    h->eager = !use_graph;
+    for (size_t i = 0; i < 2; i++) {
+        pgpu_graph_destroy(h->graphs[i].exec);
+        h->graphs[i].exec = NULL;
+    }
+    return 1;
 }
 
 /* ------------------------------------------------ reference-signature API */
@@ -369,18 +427,14 @@ static int single(const PhononFlowHead *head, const float condition[512], const 
         float staged[PH_WIDTH + LAT];
         memcpy(staged, condition, sizeof(float) * PH_WIDTH);
         memcpy(staged + PH_WIDTH, raw, sizeof(float) * LAT);
-        float *cond = h->stage, *state = h->stage + PH_WIDTH;
+        const float *cond = h->stage, *state = h->stage + PH_WIDTH;
         const int lsd_times = s == 0.0f && t == 1.0f;
         ok = pgpu_copy_h2d(h->stream, h->stage, staged, sizeof(staged)) &&
-             (lsd ? pgpu_head_noise(h->stream, state, 1, temperature, h->noise, h->noise_split,
-                                    h->status)
-                  : pgpu_split_rows(h->stream, state, 1, LAT, h->noise_split, h->status)) &&
              (lsd_times || enqueue_tsum(h, s, t, h->tsum)) &&
-             enqueue_forward(h, 1, cond, lsd_times ? h->tsum_lsd : h->tsum, h->velocity, NULL,
-                             cancel, context) &&
-             (!lsd || pgpu_head_finish(h->stream, h->noise, h->velocity, 1, h->stage, NULL, 0,
-                                       NULL, h->status)) &&
-             pgpu_copy_d2h(h->stream, result, lsd ? h->stage : h->velocity, sizeof(result)) &&
+             enqueue_head(h, 1, cond, state, lsd ? sqrtf(temperature) : 1.0f,
+                          lsd_times ? h->tsum_lsd : h->tsum, lsd, h->velocity, NULL, cancel,
+                          context) &&
+             pgpu_copy_d2h(h->stream, result, h->velocity, sizeof(result)) &&
              phonon_flow_head_device_sync(h);
         if (!ok)
             (void)phonon_flow_head_device_sync(h);  /* drain and clear the record */

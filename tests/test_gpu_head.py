@@ -104,11 +104,13 @@ def test_lsd_one_step_and_cancel(lib, pkg, oracle, oracle_mod):
     lib.phonon_flow_head_release(ctypes.byref(head))
 
 
-@pytest.mark.parametrize("streams", [1, 5, 16, 17, 64])
-def test_batched_lsd_and_eos_vs_oracle(lib, pkg, oracle, oracle_mod, streams):
-    """The device LSD step of B streams with the EOS logit, against the
-    oracle per stream; then a NaN in one stream's noise is reported by
-    sync."""
+@pytest.mark.parametrize("streams,graph", [(1, 1), (5, 1), (16, 0), (17, 1), (64, 1), (64, 0)])
+def test_batched_lsd_and_eos_vs_oracle(lib, pkg, oracle, oracle_mod, streams, graph):
+    """The device LSD step of B streams with the EOS logit, replayed from a
+    graph or launched kernel by kernel, against the oracle per stream; then a
+    NaN in one stream's noise is reported by sync, and the same buffers with
+    finite noise again give the first results (a graph replayed with new
+    input contents)."""
     bits = helpers.random_flow_head_bits(25)
     rng = np.random.default_rng(26)
     eos_w = helpers.bf16_bits(rng.standard_normal(512).astype(np.float32) * 0.05)
@@ -120,6 +122,7 @@ def test_batched_lsd_and_eos_vs_oracle(lib, pkg, oracle, oracle_mod, streams):
     assert lib.phonon_flow_head_device_create(ctypes.byref(head), ctypes.byref(ew),
                                               ctypes.byref(eb), 64, ctypes.byref(dev)), \
         pkg.last_error(lib)
+    assert lib.phonon_flow_head_device_set_graph(dev, graph)
     stream = lib.phonon_flow_head_device_stream(dev)
     cond = rng.standard_normal((streams, 512)).astype(np.float32)
     raw = rng.standard_normal((streams, 32)).astype(np.float32)
@@ -140,11 +143,22 @@ def test_batched_lsd_and_eos_vs_oracle(lib, pkg, oracle, oracle_mod, streams):
         assert ok and rel(lat[s], ref) < TOL, (s, rel(lat[s], ref))
         ok, e = oh.eos_logit(helpers.bf16_float(eos_w), helpers.bf16_float(eos_b), cond[s])
         assert ok and abs(eos[s] - e) <= TOL * max(1.0, abs(e)), (s, eos[s], e)
-    raw[streams // 2, 3] = np.inf
-    dr.upload(raw)
+    bad = raw.copy()
+    bad[streams // 2, 3] = np.inf
+    dr.upload(bad)
     assert lib.phonon_flow_head_device_lsd(dev, streams, dc.ptr, dr.ptr, 0.7, dl.ptr, None)
     assert not lib.phonon_flow_head_device_sync(dev)
     assert lib.phonon_flow_head_device_sync(dev)  # the record was cleared
+    dr.upload(raw)
+    for _ in range(3):
+        assert lib.phonon_flow_head_device_lsd(dev, streams, dc.ptr, dr.ptr, 0.7, dl.ptr, de.ptr)
+        assert lib.phonon_flow_head_device_sync(dev)
+        again = np.zeros_like(lat)
+        again_eos = np.zeros_like(eos)
+        assert lib.pgpu_copy_d2h(stream, again.ctypes.data, dl.ptr, again.nbytes)
+        assert lib.pgpu_copy_d2h(stream, again_eos.ctypes.data, de.ptr, again_eos.nbytes)
+        assert lib.pgpu_stream_sync(stream)
+        assert np.array_equal(again, lat) and np.array_equal(again_eos, eos)
     for b in (dc, dr, dl, de):
         b.free()
     lib.phonon_flow_head_device_destroy(dev)
