@@ -16,10 +16,11 @@ enum { PH_MAX_GROUPS = 4, PH_DEFAULT_GROUPS = 1 };
  * schedule (and captured graph) before it has to rebuild them. */
 enum { PH_FLOW_HEADROOM = 256 };
 /* Decode batches of this many 16-stream tiles run as one launch by default
- * (phonon_flow_batch_set_pipeline): measured faster there on MI355X (B = 64:
- * 764 vs 913 us per 12-layer step; B = 32: 746 vs 653; B = 128: 1546 vs
- * 1463). */
-enum { PH_FLOW_MIN_TILES = 1, PH_FLOW_MAX_TILES = 8 };
+ * (phonon_flow_batch_set_pipeline): measured faster there on MI355X (us per
+ * 12-layer step, contexts U{1..2048}, one launch vs phase by phase: B = 1:
+ * 370 vs 400; B = 32: 594 vs 648; B = 64: 765 vs 906; B = 128: 1367 vs
+ * 1431; B = 160: 1794 vs 1819; B = 256: 2776 vs 2637). */
+enum { PH_FLOW_MIN_TILES = 1, PH_FLOW_MAX_TILES = 10 };
 /* One-launch steps of at most PH_FLOW_ONE_ROUND_MAX_STREAMS streams, or of
  * PH_FLOW_ONE_ROUND_TILES tiles, run one split per ATTN task (the others
  * PGPU_FLOW_ATTN_ROUNDS). */
