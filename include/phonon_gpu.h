@@ -135,7 +135,10 @@ int pgpu_gemm_qkv(void *stream, const pgpu_matrix *w, const pgpu_gemm_input *x, 
  * Descriptor (PGPU_FLOW_TASK) bits: kind [0,3), layer [3,9), tile [9,17),
  * index [17,32); an
  * ATTN index is head | unit << 3 | (stream in tile) << 11, for splits
- * [unit, unit + 1) x attn_rounds. A schedule must list every task
+ * [unit, unit + 1) x attn_rounds. QKV task i computes rows [64i, 64i + 64),
+ * i.e. q (i < 8), k (i < 16) or v of head i % 8; an ATTN task of head h
+ * waits for QKV tasks h, 8 + h and 16 + h of its tile (of every tile in a
+ * batched prefill). A schedule must list every task
  * of the step once, each after every task it depends on (then the launch
  * cannot deadlock); ATTN tasks of (stream, head) must cover the splits of
  * its context. Status bit 4: a wait timed out (1 s), the
@@ -146,7 +149,9 @@ int pgpu_gemm_qkv(void *stream, const pgpu_matrix *w, const pgpu_gemm_input *x, 
 #define PGPU_FLOW_MLP_IN 3
 #define PGPU_FLOW_MLP_OUT 4
 #define PGPU_FLOW_QKV_ALL 5        /* counter only (tile 0): QKV tasks of all tiles */
-#define PGPU_FLOW_KINDS 6
+#define PGPU_FLOW_QKV_HEAD 6       /* counters only, 8 per (layer, tile): the three QKV
+                                      tasks of one head (q, k and v rows) */
+#define PGPU_FLOW_KINDS 14
 #define PGPU_FLOW_QKV_TASKS 24     /* per tile and layer */
 #define PGPU_FLOW_OUT_TASKS 8
 #define PGPU_FLOW_MLP_IN_TASKS 32

@@ -173,7 +173,7 @@ __device__ inline void attention_task(const pgpu_flow_step &f, const pgpu_paged_
     const TracedWait ready{
         f.prefill
             ? wait_for(f, layer, 0, PGPU_FLOW_QKV_ALL, (unsigned)(PGPU_FLOW_QKV_TASKS * f.tiles))
-            : wait_for(f, layer, tile, PGPU_FLOW_QKV, PGPU_FLOW_QKV_TASKS),
+            : wait_for(f, layer, tile, PGPU_FLOW_QKV_HEAD + head, 3u),
         &f};
 
     AttnArgs a;
@@ -283,7 +283,8 @@ __device__ inline void flow_step_task(const pgpu_flow_step &f, const pgpu_paged_
                                       : wait_for(f, layer - 1, tile, PGPU_FLOW_MLP_OUT,
                                                  PGPU_FLOW_MLP_OUT_TASKS);
         gemm_wide_task<SRC_LN, EPI_QKV, Q8>(a, index, tile, lds, TracedWait{w, &f});
-        flow_signal(f, phase_counter(f, layer, tile, PGPU_FLOW_QKV),
+        // Rows [64 index, +64): q, k or v of head index % 8.
+        flow_signal(f, phase_counter(f, layer, tile, PGPU_FLOW_QKV_HEAD + (index & 7)),
                     f.prefill ? phase_counter(f, layer, 0, PGPU_FLOW_QKV_ALL) : nullptr);
         break;
     }

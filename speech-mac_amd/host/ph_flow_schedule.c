@@ -39,10 +39,14 @@ static uint32_t phase_tasks(uint32_t kind) {
     }
 }
 
+/* QKV tasks head by head (q, k, v of head 0, then of head 1, ...): the
+ * attention of a head waits only for its own three. */
 static void emit_phase(uint32_t *d, size_t *k, uint32_t kind, uint32_t layer, uint32_t tile) {
     const uint32_t n = phase_tasks(kind);
-    for (uint32_t i = 0; i < n; i++)
-        d[(*k)++] = PGPU_FLOW_TASK(kind, layer, tile, i);
+    for (uint32_t i = 0; i < n; i++) {
+        const uint32_t index = kind == PGPU_FLOW_QKV ? (i % 3) * PH_HEADS + i / 3 : i;
+        d[(*k)++] = PGPU_FLOW_TASK(kind, layer, tile, index);
+    }
 }
 
 /* Sorted insert by (at, seq). */
