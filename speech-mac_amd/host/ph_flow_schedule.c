@@ -97,10 +97,10 @@ static void flush(Queue *q, int tile, uint32_t *d, size_t *k) {
 
 pgpu_flow_placement ph_flow_default_placement(int rounds) {
     /* Clock in ATTN tasks (rounds 256-key splits, 128 KB of K/V each): at
-     * B = 64 a 16-stream tile's attention is ~640 splits. Measured on
-     * MI355X at B = 64 and 128. */
-    const pgpu_flow_placement one = {1.0f, {450.0f, 900.0f, 1350.0f, 1800.0f}};
-    const pgpu_flow_placement two = {2.0f, {750.0f, 1350.0f, 1950.0f, 2550.0f}};
+     * B = 64 a 16-stream tile's attention is ~640 splits. Swept on MI355X
+     * at B = 64 (one split per task) and B = 48, 96, 128, 160 (two). */
+    const pgpu_flow_placement one = {1.0f, {550.0f, 1000.0f, 1450.0f, 1750.0f}};
+    const pgpu_flow_placement two = {2.0f, {1150.0f, 1850.0f, 2550.0f, 3050.0f}};
     return rounds > 1 ? two : one;
 }
 
