@@ -69,9 +69,14 @@ struct FlowWait {
     __device__ void pass(unsigned first, bool needed = true) const {
         if (threadIdx.x == 0 && needed && first < target) {
             const uint64_t t0 = wall_clock64();
-            while (__hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
-                if ((__hip_atomic_load(status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) & 4) ||
-                    wall_clock64() - t0 > kWaitTicks) {
+            // The counter and the status word are loaded together: one
+            // round trip to memory per poll.
+            for (;;) {
+                const unsigned count =
+                    __hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                const int st = __hip_atomic_load(status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                if (count >= target) break;
+                if ((st & 4) || wall_clock64() - t0 > kWaitTicks) {
                     atomicOr(status, 4);
                     break;
                 }
