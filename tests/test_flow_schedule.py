@@ -46,6 +46,7 @@ def check_order(sched, splits, layers, prefill=False):
     tiles = (streams + 15) // 16
     kind, layer, tile, index = decode(sched)
     done = np.zeros((layers, tiles, 5), np.int64)
+    qkv_head = np.zeros((layers, tiles, 8), np.int64)  # QKV tasks done per head (q, k, v)
     merged = np.zeros((layers, streams, 8), np.int64)   # ATTN tasks seen per (s, head)
     seen = set()
     for i in range(len(sched)):
@@ -59,12 +60,18 @@ def check_order(sched, splits, layers, prefill=False):
             assert x < TASKS[QKV]
             if l > 0:
                 assert done[l - 1, t, MLP_OUT] == TASKS[MLP_OUT], f"QKV({l},{t}) before MLP_OUT"
+            qkv_head[l, t, x % 8] += 1   # rows [64x, 64x + 64): q, k or v of head x % 8
         elif k == ATTN:
             h, j, n = x & 7, (x >> 3) & 255, x >> 11
             assert n < live and j < splits[16 * t + n]
-            need = range(tiles) if prefill else [t]
-            for t2 in need:
-                assert done[l, t2, QKV] == TASKS[QKV], f"ATTN({l},{t}) before QKV({l},{t2})"
+            # decode: the head's q, k and v tasks of its tile (pgpu_flow.hip
+            # waits on PGPU_FLOW_QKV_HEAD + h); prefill: every QKV task of
+            # every tile (PGPU_FLOW_QKV_ALL)
+            if prefill:
+                for t2 in range(tiles):
+                    assert done[l, t2, QKV] == TASKS[QKV], f"ATTN({l},{t}) before QKV({l},{t2})"
+            else:
+                assert qkv_head[l, t, h] == 3, f"ATTN({l},{t},head {h}) before its QKV tasks"
             merged[l, 16 * t + n, h] += 1
             if merged[l, 16 * t + n, h] == splits[16 * t + n]:
                 done[l, t, ATTN] += 1   # the (stream, head) is merged
@@ -147,6 +154,30 @@ def test_order_checker_rejects_planted_mistakes(pkg):
     cases.append(bad)
     cases.append(np.delete(sched, len(sched) // 2))          # a task missing
     cases.append(np.insert(sched, 10, sched[3]))             # a task twice
+    # the first ATTN task of (layer 1, tile 0) moved in front of the v task
+    # of its own head
+    kind, layer, tile, index = decode(sched)
+    a = int(np.flatnonzero((kind == ATTN) & (layer == 1) & (tile == 0))[0])
+    h = int(index[a]) & 7
+    v = int(np.flatnonzero((kind == QKV) & (layer == 1) & (tile == 0) & (index == 16 + h))[0])
+    bad = np.insert(np.delete(sched, a), v, sched[a])
+    cases.append(bad)
     for bad in cases:
         with pytest.raises(AssertionError):
             check_order(bad, splits, 2)
+
+
+def test_order_checker_allows_attention_after_its_own_head(pkg):
+    """The per-head rule is what the kernel waits for: an ATTN task of head
+    h may run before another head's QKV tasks of its tile (the checker
+    accepts it), but not before its own head's (rejected above)."""
+    lib = pkg.load()
+    splits = np.array([1] * 16)
+    sched = build(lib, splits, 1)
+    kind, layer, tile, index = decode(sched)
+    qkv = np.flatnonzero(kind == QKV)
+    assert list(index[qkv]) == [(i % 3) * 8 + i // 3 for i in range(24)]  # head by head
+    a = int(np.flatnonzero((kind == ATTN) & ((index & 7) == 0))[0])
+    # move it right behind head 0's three QKV tasks, ahead of heads 1..7
+    moved = np.insert(np.delete(sched, a), int(qkv[2]) + 1, sched[a])
+    assert check_order(moved, splits, 1)
