@@ -51,12 +51,13 @@ typedef struct {
 /* The activation operand of a projection, exactly one of:
  *  split     - split fragments (3 bf16 terms per value) of the input rows,
  *              with the stream count rounded up to 16 in the allocation;
+ *  rows      - fp32 rows [streams][512], split inside the projection;
  *  ln_rows   - fp32 rows [streams][512], LayerNorm'ed (ln_weight, ln_bias,
  *              ln_epsilon) inside the projection;
  *  attn_acc  - split-attention partials (attn_acc/attn_ml as in
  *              pgpu_attention_scratch, attn_positions and attn_max_splits as
  *              given to pgpu_attention), merged inside the projection.
- * ln_rows and attn_acc need a 512-column matrix. */
+ * rows, ln_rows and attn_acc need a 512-column matrix. */
 typedef struct {
     const uint16_t *split;
     const float *ln_rows, *ln_weight, *ln_bias;
@@ -64,6 +65,7 @@ typedef struct {
     const float *attn_acc, *attn_ml;
     const int32_t *attn_positions;
     int attn_max_splits;
+    const float *rows;
 } pgpu_gemm_input;
 
 /* -- device, memory, streams, events, graphs (pgpu_runtime.hip) -- */

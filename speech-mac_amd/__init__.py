@@ -100,7 +100,7 @@ class PgpuAttentionScratch(ctypes.Structure):
 class PgpuGemmInput(ctypes.Structure):
     _fields_ = [("split", _vp), ("ln_rows", _vp), ("ln_weight", _vp), ("ln_bias", _vp),
                 ("ln_epsilon", _f), ("attn_acc", _vp), ("attn_ml", _vp),
-                ("attn_positions", _vp), ("attn_max_splits", _i)]
+                ("attn_positions", _vp), ("attn_max_splits", _i), ("rows", _vp)]
 
 
 CANCEL_POLL = ctypes.CFUNCTYPE(ctypes.c_int, _vp)

@@ -36,6 +36,9 @@ static int launch(const GemmArgs &a, hipStream_t stream) {
 
 template <int EPI>
 static int dispatch(const GemmArgs &a, int q8, hipStream_t stream) {
+    if (a.plain_rows)
+        return q8 ? launch<SRC_ROWS, EPI, true>(a, stream)
+                  : launch<SRC_ROWS, EPI, false>(a, stream);
     const int src = a.ln_x ? SRC_LN : (a.part_acc ? SRC_ATTN : SRC_SPLIT);
     if (src == SRC_LN)
         return q8 ? launch<SRC_LN, EPI, true>(a, stream) : launch<SRC_LN, EPI, false>(a, stream);
@@ -50,17 +53,18 @@ static int dispatch(const GemmArgs &a, int q8, hipStream_t stream) {
 static bool set_input(GemmArgs &a, const pgpu_gemm_input *in) {
     if (!in) return false;
     const int kinds = (in->split != nullptr) + (in->ln_rows != nullptr) +
-                      (in->attn_acc != nullptr);
+                      (in->attn_acc != nullptr) + (in->rows != nullptr);
     if (kinds != 1) return false;
     a.xs = in->split;
-    a.ln_x = in->ln_rows;
+    a.ln_x = in->rows ? in->rows : in->ln_rows;
+    a.plain_rows = in->rows != nullptr;
     a.ln_w = in->ln_weight;
     a.ln_b = in->ln_bias;
     a.ln_eps = in->ln_epsilon;
     a.part_acc = in->attn_acc;
     a.part_ml = in->attn_ml;
     a.max_splits = in->attn_max_splits;
-    if (a.ln_x && (!a.ln_w || !a.ln_b)) return false;
+    if (in->ln_rows && (!a.ln_w || !a.ln_b)) return false;
     if (a.part_acc && (!a.part_ml || a.max_splits <= 0 || !in->attn_positions)) return false;
     if (a.part_acc) a.positions = in->attn_positions;
     return true;

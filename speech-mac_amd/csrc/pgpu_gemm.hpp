@@ -97,6 +97,7 @@ struct GemmArgs {
     int ld_gate;
     const float *mod;         // SRC_LN_MOD: shift row at mod + s * ld_mod, scale at +512
     int ld_mod;
+    bool plain_rows;          // single-phase launch: ln_x rows are used as they are
 };
 
 // ---------------------------------------------------------------------------

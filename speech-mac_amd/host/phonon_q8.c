@@ -81,6 +81,12 @@ int phonon_q8_device_matvec(PhononQ8Device *m, size_t copy, const float *x, floa
     const pgpu_matrix *w = &m->copies[copy];
     if (w->columns != m->columns)
         return 0; /* padded columns would need a padded input */
+    /* 512 columns (rows 16-byte aligned): one launch that splits the rows
+     * inside the projection. */
+    if (w->columns == PH_WIDTH && (uintptr_t)x % 16 == 0) {
+        const pgpu_gemm_input rows = {.rows = x};
+        return pgpu_gemm_store(stream, w, &rows, (int)batch, NULL, y, (int)w->rows, m->status);
+    }
     const pgpu_gemm_input in = {.split = m->xs};
     return pgpu_split_rows(stream, x, (int)batch, (int)w->columns, m->xs, m->status) &&
            pgpu_gemm_store(stream, w, &in, (int)batch, NULL, y, (int)w->rows, m->status);
