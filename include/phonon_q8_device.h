@@ -23,10 +23,12 @@ int phonon_q8_device_create(const PhononQ8Block *weights, size_t rows, size_t co
                             size_t copies, PhononQ8Device **matrix);
 void phonon_q8_device_destroy(PhononQ8Device *matrix);
 /* y[b][r] = dot(row r of copy `copy`, x[b]) for b < batch, with x (dev)
- * [batch][columns] and y (dev) [batch][rows], enqueued on `stream` (a HIP
- * stream, NULL = null stream). The input is first converted to split
- * fragments in a buffer owned by the matrix, so calls on one matrix must not
- * overlap in time. Returns 0 on invalid arguments or a failed launch;
+ * [batch][columns] and y (dev) [batch][rows], both 16-byte aligned,
+ * enqueued on `stream` (a HIP stream, NULL = null stream). With 512 columns
+ * the projection splits the fp32 rows itself (one launch); otherwise the
+ * input is first converted to split fragments in a buffer owned by the
+ * matrix, so calls on one matrix must not overlap in time. Returns 0 on
+ * invalid arguments (a misaligned pointer included) or a failed launch;
  * non-finite outputs are reported by phonon_q8_device_status. */
 int phonon_q8_device_matvec(PhononQ8Device *matrix, size_t copy, const float *x, float *y,
                             size_t batch, void *stream);

@@ -76,14 +76,15 @@ int phonon_q8_device_create(const PhononQ8Block *weights, size_t rows, size_t co
 
 int phonon_q8_device_matvec(PhononQ8Device *m, size_t copy, const float *x, float *y,
                             size_t batch, void *stream) {
-    if (!m || copy >= m->count || !x || !y || !batch || batch > m->max_batch)
+    /* The kernels read x and write y 16 bytes at a time. */
+    if (!m || copy >= m->count || !x || !y || !batch || batch > m->max_batch ||
+        (uintptr_t)x % 16 || (uintptr_t)y % 16)
         return 0;
     const pgpu_matrix *w = &m->copies[copy];
     if (w->columns != m->columns)
         return 0; /* padded columns would need a padded input */
-    /* 512 columns (rows 16-byte aligned): one launch that splits the rows
-     * inside the projection. */
-    if (w->columns == PH_WIDTH && (uintptr_t)x % 16 == 0) {
+    /* 512 columns: one launch that splits the rows inside the projection. */
+    if (w->columns == PH_WIDTH) {
         const pgpu_gemm_input rows = {.rows = x};
         return pgpu_gemm_store(stream, w, &rows, (int)batch, NULL, y, (int)w->rows, m->status);
     }

@@ -124,6 +124,33 @@ def test_q8_device_matvec_batches(lib, oracle, syn, pkg, batch):
     lib.phonon_q8_device_destroy(handle)
 
 
+@pytest.mark.parametrize("batch", [1, 5, 17, 64])
+def test_q8_device_matvec_512_columns_rows_path(lib, oracle, syn, pkg, batch):
+    """The config-1 shape (2048 x 512): 512-column matrices take the one-launch
+    path that splits the fp32 rows inside the projection; against the oracle
+    from an input at a 16-byte offset into its buffer. An input or output
+    that is not 16-byte aligned is rejected before any launch."""
+    rng = np.random.default_rng(300 + batch)
+    rows, cols = 2048, 512
+    w = syn.q8_matrix(rng, rows, cols)
+    x = rng.standard_normal((batch, cols)).astype(np.float32)
+    handle = ctypes.c_void_p()
+    assert lib.phonon_q8_device_create(w.ctypes.data, rows, cols, 1, ctypes.byref(handle))
+    padded = np.concatenate([np.zeros(4, np.float32), x.ravel()])  # x at byte 16 and at 4
+    dx = pkg.DeviceBuffer(lib, padded.nbytes)
+    dx.upload(padded)
+    dy = pkg.DeviceBuffer(lib, batch * rows * 4)
+    assert lib.phonon_q8_device_matvec(handle, 0, dx.ptr + 16, dy.ptr, batch, None)
+    assert lib.phonon_q8_device_status(handle, None)
+    y = dy.download((batch, rows))
+    for b in range(batch):
+        ok, yo = oracle.q8_matvec(w, x[b], rows, cols)
+        assert ok and helpers.normwise(y[b], yo) <= TOL, b
+    assert not lib.phonon_q8_device_matvec(handle, 0, dx.ptr + 12, dy.ptr, batch, None)
+    assert not lib.phonon_q8_device_matvec(handle, 0, dx.ptr + 16, dy.ptr + 4, batch, None)
+    lib.phonon_q8_device_destroy(handle)
+
+
 # ------------------------------------------------------------------- linear
 def test_linear_bf16_known_answer(lib, pkg):
     g = GOLDEN["linear_bf16"]
