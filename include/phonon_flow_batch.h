@@ -108,7 +108,7 @@ int phonon_flow_batch_set_groups(PhononFlowBatch *batch, size_t groups);
  * one 16-stream tile's projections run while other tiles' attention
  * streams K/V, and no launch boundary separates the phases. mode 0: one
  * launch per phase of each layer. mode 1 (default): one launch for the
- * decode batch sizes where that measured faster on MI355X (1..160 streams),
+ * decode batch sizes where that measured faster on MI355X (1..224 streams),
  * phase by phase otherwise. Results are identical (both run the same task
  * code). Batches over 4096 streams, models over 63 layers and models mixing
  * Q8 and BF16 matrices always run phase by phase. */

@@ -18,13 +18,20 @@ enum { PH_FLOW_HEADROOM = 256 };
 /* Decode batches of this many 16-stream tiles run as one launch by default
  * (phonon_flow_batch_set_pipeline): measured faster there on MI355X (us per
  * 12-layer step, contexts U{1..2048}, one launch vs phase by phase: B = 1:
- * 370 vs 400; B = 32: 594 vs 648; B = 64: 765 vs 906; B = 128: 1367 vs
- * 1431; B = 160: 1794 vs 1819; B = 256: 2776 vs 2637). */
-enum { PH_FLOW_MIN_TILES = 1, PH_FLOW_MAX_TILES = 10 };
+ * 349 vs 399; B = 32: 553 vs 648; B = 64: 719 vs 906; B = 128: 1256 vs
+ * 1450; B = 192: 1954 vs 2076; B = 224: 2277 vs 2347; B = 256: 2649 vs
+ * 2642). */
+enum { PH_FLOW_MIN_TILES = 1, PH_FLOW_MAX_TILES = 14 };
 /* One-launch steps of at most PH_FLOW_ONE_ROUND_MAX_STREAMS streams, or of
- * PH_FLOW_ONE_ROUND_TILES tiles, run one split per ATTN task (the others
- * PGPU_FLOW_ATTN_ROUNDS). */
-enum { PH_FLOW_ONE_ROUND_MAX_STREAMS = 8, PH_FLOW_ONE_ROUND_TILES = 4 };
+ * PH_FLOW_ONE_ROUND_MIN_TILES..PH_FLOW_ONE_ROUND_MAX_TILES tiles, run one
+ * split per ATTN task (the others PGPU_FLOW_ATTN_ROUNDS): us per step, one
+ * vs two splits, B = 32: 674 vs 552; B = 48: 693 vs 712; B = 64: 680 vs
+ * 689; B = 80: 890 vs 834. */
+enum {
+    PH_FLOW_ONE_ROUND_MAX_STREAMS = 8,
+    PH_FLOW_ONE_ROUND_MIN_TILES = 3,
+    PH_FLOW_ONE_ROUND_MAX_TILES = 4
+};
 /* Chain placement of the one-launch step's task list (pgpu_flow_placement):
  * measured on MI355X at B = 64 (ph_flow_schedule.c). */
 pgpu_flow_placement ph_flow_default_placement(int rounds);

@@ -608,13 +608,14 @@ static size_t flow_ml_group(const PhononFlowBatch *b) {
  * tiles; prefill and larger batches are attention-bound, where the separate
  * attention kernel streams K/V faster). */
 /* Splits per ATTN task: one for a few streams (the step is a latency
- * chain) and at 4 tiles, two otherwise (fewer, longer attention tasks keep
- * more K/V in flight per work-group slot); measured on MI355X. */
+ * chain) and at 3 and 4 tiles, two otherwise (fewer, longer attention tasks
+ * keep more K/V in flight per work-group slot); measured on MI355X. */
 static int flow_rounds(const PhononFlowBatch *b) {
     if (b->fl.rounds_set)
         return b->fl.rounds_set;
     const size_t tiles = (b->streams + 15) / 16;
-    return b->streams <= PH_FLOW_ONE_ROUND_MAX_STREAMS || tiles == PH_FLOW_ONE_ROUND_TILES
+    return b->streams <= PH_FLOW_ONE_ROUND_MAX_STREAMS ||
+                   (tiles >= PH_FLOW_ONE_ROUND_MIN_TILES && tiles <= PH_FLOW_ONE_ROUND_MAX_TILES)
                ? 1
                : PGPU_FLOW_ATTN_ROUNDS;
 }
