@@ -242,11 +242,13 @@ int pgpu_attention_merge(void *stream, const pgpu_attention_scratch *scratch,
 
 /* -- flow head launches (pgpu_head.hip); BF16 matrices -- */
 /* One launch of three independent parts: silu_split = split fragments of
- * SiLU((cond_w . conditions + cond_bias) + tsum) (tsum optional); if eos_w
- * (16 rows, row 0 live): eos_rows [streams][eos_ld] = eos_w . conditions +
- * eos_bias; noise = raw * scale ([streams][32], scale positive and finite)
- * and its split fragments (K = 32). */
+ * SiLU((cond_w . c + cond_bias) + tsum) (tsum optional); if eos_w (16 rows,
+ * row 0 live): eos_rows [streams][eos_ld] = eos_w . c + eos_bias; noise =
+ * raw * scale ([streams][32], scale positive and finite) and its split
+ * fragments (K = 32). c = the rows `conditions`, or their LayerNorm (eps
+ * 1e-5) with norm_w and norm_b when those are given. */
 int pgpu_head_front(void *stream, const pgpu_matrix *cond_w, const float *conditions, int streams,
+                    const float *norm_w, const float *norm_b,
                     const float *cond_bias, const float *tsum, uint16_t *silu_split,
                     const pgpu_matrix *eos_w, const float *eos_bias, float *eos_rows, int eos_ld,
                     const float *raw, float scale, float *noise, uint16_t *noise_split,

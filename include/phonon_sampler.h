@@ -78,6 +78,25 @@ void phonon_flow_head_device_destroy(PhononFlowHeadDevice *head);
 int phonon_flow_head_device_lsd(PhononFlowHeadDevice *head, size_t streams,
                                 const float *conditions, const float *raw_noise,
                                 float temperature, float *latents, float *eos_logits);
+/* The pieces of the generation loop around the head, for
+ * phonon_flow_head_device_frame (src/phonon_sampler.c:447-483): the
+ * decoder's output norm (flow_lm.out_norm weight and bias, BF16 [512];
+ * LayerNorm eps 1e-5, src/phonon_transformer.c:904-914) in front of the
+ * head, and the latent's embedding (flow_lm.input_linear, BF16 [512][32],
+ * no bias, src/phonon_transformer.c:860-874) behind it. Once per head. */
+int phonon_flow_head_device_set_frame(PhononFlowHeadDevice *head,
+                                      const PhononTensorView *out_norm_weight,
+                                      const PhononTensorView *out_norm_bias,
+                                      const PhononTensorView *input_linear);
+/* One frame of `streams` streams after the decode step (device buffers,
+ * 16-byte aligned): state = out_norm(outputs [streams][512]); latents
+ * [streams][32] = the LSD step at condition `state`; eos_logits (optional)
+ * = out_eos . state + bias; next_inputs [streams][512] = input_linear .
+ * latents + conditions [streams][512] (the next decode step's inputs). */
+int phonon_flow_head_device_frame(PhononFlowHeadDevice *head, size_t streams,
+                                  const float *outputs, const float *conditions,
+                                  const float *raw_noise, float temperature, float *latents,
+                                  float *eos_logits, float *next_inputs);
 /* use_graph = 1 (the default): the step's kernels are captured in a HIP
  * graph per (streams, buffers, temperature), two kept, and replayed; 0:
  * each kernel is launched directly. */

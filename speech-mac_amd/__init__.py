@@ -224,8 +224,8 @@ EXPORTS = {
     "pgpu_flow_launch": (_i, [_vp, _vp, _kvp]),
     "pgpu_gemm_silu_split": (_i, [_vp, _vp, _vp, _i, _vp, _vp, _vp, _vp]),
     "pgpu_gemm_gated": (_i, [_vp, _vp, _vp, _i, _vp, _vp, _i, _vp, _vp, _vp]),
-    "pgpu_head_front": (_i, [_vp, _vp, _vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _i, _vp, _f,
-                             _vp, _vp, _vp]),
+    "pgpu_head_front": (_i, [_vp, _vp, _vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i,
+                             _vp, _f, _vp, _vp, _vp]),
     "pgpu_head_mod": (_i, [_vp, _vp, _vp, _i, _vp, _vp, _i, _vp, _vp, _vp, _vp, _vp]),
     "pgpu_head_mlp_in": (_i, [_vp, _vp, _vp, _i, _vp, _vp, _f, _vp, _i, _vp, _vp, _vp]),
     "pgpu_head_final": (_i, [_vp, _vp, _vp, _i, _f, _vp, _i, _vp, _vp, _vp, _vp, _vp, _i, _vp,
@@ -241,6 +241,8 @@ EXPORTS = {
     "phonon_flow_head_device_destroy": (None, [_vp]),
     "phonon_flow_head_device_lsd": (_i, [_vp, _sz, _vp, _vp, _f, _vp, _vp]),
     "phonon_flow_head_device_set_graph": (_i, [_vp, _i]),
+    "phonon_flow_head_device_set_frame": (_i, [_vp, _vp, _vp, _vp]),
+    "phonon_flow_head_device_frame": (_i, [_vp, _sz, _vp, _vp, _vp, _f, _vp, _vp, _vp]),
     "phonon_flow_head_device_stream": (_vp, [_vp]),
     "phonon_flow_head_device_sync": (_i, [_vp]),
     "pgpu_flow_finish": (_i, [_vp, _vp, _sz, _vp, _i]),

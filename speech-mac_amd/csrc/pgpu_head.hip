@@ -71,17 +71,20 @@ struct NoiseArgs {
 
 // First launch of a head step: the condition's projection into split
 // fragments of SiLU(y) (y = cond_embed(c) + tsum), the EOS row of the
-// condition (optional) and the noise rows; none depends on another.
+// condition (optional) and the noise rows; none depends on another. With
+// SRC = SRC_LN the condition is the LayerNorm of the rows (the decoder's
+// output norm), computed in both projections' prologues.
+template <int SRC>
 __global__ __launch_bounds__(kTaskThreads) void k_head_front(GemmArgs cond, GemmArgs eos,
                                                              int with_eos, NoiseArgs nz) {
     __shared__ uint4 lds4[kTaskLds / 8];
     uint16_t *lds = (uint16_t *)lds4;
     int b = blockIdx.x;
     const int n_cond = wide_groups(cond);
-    if (b < n_cond) return wide_at<SRC_ROWS, EPI_SILU_SPLIT>(cond, b, lds);
+    if (b < n_cond) return wide_at<SRC, EPI_SILU_SPLIT>(cond, b, lds);
     b -= n_cond;
     if (with_eos) {
-        if (b < wide_groups(eos)) return wide_at<SRC_ROWS, EPI_STORE>(eos, b, lds);
+        if (b < wide_groups(eos)) return wide_at<SRC, EPI_STORE>(eos, b, lds);
         b -= wide_groups(eos);
     }
     noise_rows(nz.raw, cond.streams, nz.scale, nz.noise, nz.xs, cond.status, b * kTaskThreads);
@@ -200,17 +203,22 @@ static GemmArgs head_args(const pgpu_matrix *w, int streams, int *status) {
 }
 
 extern "C" int pgpu_head_front(void *stream, const pgpu_matrix *cond_w, const float *conditions,
-                               int streams, const float *cond_bias, const float *tsum,
+                               int streams, const float *norm_w, const float *norm_b,
+                               const float *cond_bias, const float *tsum,
                                uint16_t *silu_split, const pgpu_matrix *eos_w,
                                const float *eos_bias, float *eos_rows, int eos_ld,
                                const float *raw, float scale, float *noise,
                                uint16_t *noise_split, int *status) {
     if (!bf16_matrix(cond_w, kWidth, kWidth) || !conditions || streams <= 0 || !silu_split ||
+        (!norm_w) != (!norm_b) ||
         !raw || !noise || !noise_split || !(scale > 0.0f) || !std::isfinite(scale) ||
         (eos_w && (!bf16_matrix(eos_w, 16, kWidth) || !eos_rows || eos_ld < 16 || eos_ld % 4)))
         return bad_arguments(__func__);
     GemmArgs cond = head_args(cond_w, streams, status);
     cond.ln_x = conditions;
+    cond.ln_w = norm_w;
+    cond.ln_b = norm_b;
+    cond.ln_eps = 1e-5f;
     cond.bias = cond_bias;
     cond.bias2 = tsum;
     cond.out_split = silu_split;
@@ -219,6 +227,9 @@ extern "C" int pgpu_head_front(void *stream, const pgpu_matrix *cond_w, const fl
     if (eos_w) {
         eos = head_args(eos_w, streams, status);
         eos.ln_x = conditions;
+        eos.ln_w = norm_w;
+        eos.ln_b = norm_b;
+        eos.ln_eps = 1e-5f;
         eos.bias = eos_bias;
         eos.out = eos_rows;
         eos.ld_out = eos_ld;
@@ -226,8 +237,12 @@ extern "C" int pgpu_head_front(void *stream, const pgpu_matrix *cond_w, const fl
     const NoiseArgs nz{raw, scale, noise, noise_split};
     const int blocks = wide_groups(cond) + (eos_w ? wide_groups(eos) : 0) +
                        (streams * 4 + kTaskThreads - 1) / kTaskThreads;
-    hipLaunchKernelGGL(k_head_front, dim3((unsigned)blocks), dim3(kTaskThreads), 0,
-                       (hipStream_t)stream, cond, eos, eos_w != nullptr, nz);
+    if (norm_w)
+        hipLaunchKernelGGL(k_head_front<SRC_LN>, dim3((unsigned)blocks), dim3(kTaskThreads), 0,
+                           (hipStream_t)stream, cond, eos, eos_w != nullptr, nz);
+    else
+        hipLaunchKernelGGL(k_head_front<SRC_ROWS>, dim3((unsigned)blocks), dim3(kTaskThreads),
+                           0, (hipStream_t)stream, cond, eos, eos_w != nullptr, nz);
     return launch_ok(__func__);
 }
 

@@ -38,6 +38,10 @@ struct PhononFlowHeadDevice {
     float *norm_w[HB], *norm_b[HB], *freqs[2], *alpha[2];
     float *tsum_lsd, *tsum, *time_out; /* time_out: [2][512] */
     float *ones;                       /* [32] of 1.0f: the Euler update's gate */
+    float *out_norm;                   /* (frame) [2][512] LayerNorm weight, bias */
+    pgpu_matrix input_linear;          /* (frame) [512][32] latent embedding */
+    void *input_linear_dev;
+    int has_frame;
     size_t cap;                        /* streams, a multiple of 16 */
     void *buffers;
     float *noise, *x, *mod, *velocity, *eos_rows, *stage;
@@ -48,9 +52,9 @@ struct PhononFlowHeadDevice {
     struct {
         void *exec;
         size_t streams;
-        const float *conditions, *raw_noise;
+        const float *conditions, *raw_noise, *embed;
         float temperature;
-        float *latents, *eos_logits;
+        float *latents, *eos_logits, *next;
     } graphs[2];
     size_t graph_victim;
     int eager; /* launch each kernel directly instead of replaying a graph */
@@ -203,12 +207,14 @@ static int enqueue_tsum(PhononFlowHeadDevice *h, float s, float t, float *tsum) 
  * out [n][32] and, if eos, the EOS logits. The cancel poll runs before each
  * block and before the final layer. */
 static int enqueue_head(PhononFlowHeadDevice *h, size_t n, const float *conditions,
-                        const float *raw, float scale, const float *tsum, int lsd, float *out,
-                        float *eos, PhononCancelPoll cancel, void *context) {
+                        const float *norm, const float *raw, float scale, const float *tsum,
+                        int lsd, float *out, float *eos, PhononCancelPoll cancel,
+                        void *context) {
     void *st = h->stream;
     const int B = (int)n;
     const pgpu_gemm_input first = {.split = h->first_split};
-    if (!pgpu_head_front(st, &h->cond, conditions, B, h->b_cond, tsum, h->silu_split,
+    if (!pgpu_head_front(st, &h->cond, conditions, B, norm, norm ? norm + PH_WIDTH : NULL,
+                         h->b_cond, tsum, h->silu_split,
                          eos ? &h->eos : NULL, h->b_eos, h->eos_rows, EOS_ROWS, raw, scale,
                          h->noise, h->noise_split, h->status) ||
         !pgpu_head_mod(st, &h->ada, h->silu_split, B, h->b_ada, h->mod, MOD, &h->input,
@@ -277,6 +283,8 @@ void phonon_flow_head_device_destroy(PhononFlowHeadDevice *h) {
     for (size_t i = 0; i < h->nmats; i++)
         pgpu_free(h->mats[i]);
     pgpu_free(h->vec);
+    pgpu_free(h->out_norm);
+    pgpu_free(h->input_linear_dev);
     pgpu_free(h->buffers);
     pgpu_free(h->status);
     pgpu_stream_destroy(h->stream);
@@ -296,30 +304,43 @@ int phonon_flow_head_device_sync(PhononFlowHeadDevice *h) {
     return status == 0;
 }
 
+/* The LSD step; with `next` (a frame): the conditions are the decoder's
+ * outputs, normalized by out_norm in the head's first launch, and next =
+ * input_linear . latents + embed (the latent's embedding, split into
+ * fragments in the noise buffer, which the step no longer needs). */
 static int enqueue_lsd(PhononFlowHeadDevice *h, size_t streams, const float *conditions,
                        const float *raw_noise, float temperature, float *latents,
-                       float *eos_logits) {
-    return enqueue_head(h, streams, conditions, raw_noise, sqrtf(temperature), h->tsum_lsd, 1,
-                        latents, eos_logits, NULL, NULL);
+                       float *eos_logits, const float *embed, float *next) {
+    if (!enqueue_head(h, streams, conditions, next ? h->out_norm : NULL, raw_noise,
+                      sqrtf(temperature), h->tsum_lsd, 1, latents, eos_logits, NULL, NULL))
+        return 0;
+    if (!next)
+        return 1;
+    const pgpu_gemm_input lat = {.split = h->noise_split};
+    return pgpu_split_rows(h->stream, latents, (int)streams, LAT, h->noise_split, h->status) &&
+           pgpu_gemm_residual(h->stream, &h->input_linear, &lat, (int)streams, embed, next,
+                              h->status);
 }
 
 /* The step's kernels are captured once per (streams, buffers, temperature)
  * and replayed: two captures are kept, so a caller alternating two sets of
  * buffers replays both. */
-int phonon_flow_head_device_lsd(PhononFlowHeadDevice *h, size_t streams,
-                                const float *conditions, const float *raw_noise,
-                                float temperature, float *latents, float *eos_logits) {
+static int run_lsd(PhononFlowHeadDevice *h, size_t streams, const float *conditions,
+                   const float *raw_noise, float temperature, float *latents, float *eos_logits,
+                   const float *embed, float *next) {
     if (!h || !streams || streams > h->cap || !conditions || !raw_noise || !latents ||
         (eos_logits && !h->has_eos) || !(temperature > 0.0f) || !isfinite(temperature))
         return 0;
     if (h->eager)
-        return enqueue_lsd(h, streams, conditions, raw_noise, temperature, latents, eos_logits);
+        return enqueue_lsd(h, streams, conditions, raw_noise, temperature, latents, eos_logits,
+                           embed, next);
     void *exec = NULL;
     for (size_t i = 0; i < 2 && !exec; i++)
         if (h->graphs[i].exec && h->graphs[i].streams == streams &&
             h->graphs[i].conditions == conditions && h->graphs[i].raw_noise == raw_noise &&
             h->graphs[i].temperature == temperature && h->graphs[i].latents == latents &&
-            h->graphs[i].eos_logits == eos_logits)
+            h->graphs[i].eos_logits == eos_logits && h->graphs[i].embed == embed &&
+            h->graphs[i].next == next)
             exec = h->graphs[i].exec;
     if (!exec) {
         const size_t slot = h->graph_victim;
@@ -327,8 +348,8 @@ int phonon_flow_head_device_lsd(PhononFlowHeadDevice *h, size_t streams,
         h->graphs[slot].exec = NULL;
         if (!pgpu_graph_begin(h->stream))
             return 0;
-        const int enqueued =
-            enqueue_lsd(h, streams, conditions, raw_noise, temperature, latents, eos_logits);
+        const int enqueued = enqueue_lsd(h, streams, conditions, raw_noise, temperature,
+                                         latents, eos_logits, embed, next);
         const int ended = pgpu_graph_end(h->stream, &exec);
         if (!enqueued || !ended) {
             pgpu_graph_destroy(exec);
@@ -341,9 +362,54 @@ int phonon_flow_head_device_lsd(PhononFlowHeadDevice *h, size_t streams,
         h->graphs[slot].temperature = temperature;
         h->graphs[slot].latents = latents;
         h->graphs[slot].eos_logits = eos_logits;
+        h->graphs[slot].embed = embed;
+        h->graphs[slot].next = next;
         h->graph_victim = 1 - slot;
     }
     return pgpu_graph_launch(exec, h->stream);
+}
+
+int phonon_flow_head_device_lsd(PhononFlowHeadDevice *h, size_t streams,
+                                const float *conditions, const float *raw_noise,
+                                float temperature, float *latents, float *eos_logits) {
+    return run_lsd(h, streams, conditions, raw_noise, temperature, latents, eos_logits, NULL,
+                   NULL);
+}
+
+int phonon_flow_head_device_set_frame(PhononFlowHeadDevice *h,
+                                      const PhononTensorView *out_norm_weight,
+                                      const PhononTensorView *out_norm_bias,
+                                      const PhononTensorView *input_linear) {
+    if (!h || !out_norm_weight || !out_norm_bias || !input_linear || h->has_frame ||
+        !pgpu_stream_sync(h->stream))
+        return 0;
+    float host[2 * PH_WIDTH];
+    if (!vec_view(out_norm_weight, PH_WIDTH, host) ||
+        !vec_view(out_norm_bias, PH_WIDTH, host + PH_WIDTH))
+        return 0;
+    float *dev = pgpu_malloc(sizeof(host));
+    void *wdev = NULL;
+    if (!dev || !pgpu_copy_h2d(h->stream, dev, host, sizeof(host)) ||
+        !ph_matrix_upload(input_linear, PH_WIDTH, LAT, &h->input_linear, &wdev) ||
+        h->input_linear.q8) {
+        pgpu_free(dev);
+        pgpu_free(wdev);
+        return ph_fail("flow head frame: bad out_norm or input_linear");
+    }
+    h->out_norm = dev;
+    h->input_linear_dev = wdev;
+    h->has_frame = 1;
+    return 1;
+}
+
+int phonon_flow_head_device_frame(PhononFlowHeadDevice *h, size_t streams, const float *outputs,
+                                  const float *conditions, const float *raw_noise,
+                                  float temperature, float *latents, float *eos_logits,
+                                  float *next_inputs) {
+    if (!h || !h->has_frame || !conditions || !next_inputs)
+        return 0;
+    return run_lsd(h, streams, outputs, raw_noise, temperature, latents, eos_logits, conditions,
+                   next_inputs);
 }
 
 int phonon_flow_head_device_set_graph(PhononFlowHeadDevice *h, int use_graph) {
@@ -431,7 +497,7 @@ static int single(const PhononFlowHead *head, const float condition[512], const 
         const int lsd_times = s == 0.0f && t == 1.0f;
         ok = pgpu_copy_h2d(h->stream, h->stage, staged, sizeof(staged)) &&
              (lsd_times || enqueue_tsum(h, s, t, h->tsum)) &&
-             enqueue_head(h, 1, cond, state, lsd ? sqrtf(temperature) : 1.0f,
+             enqueue_head(h, 1, cond, NULL, state, lsd ? sqrtf(temperature) : 1.0f,
                           lsd_times ? h->tsum_lsd : h->tsum, lsd, h->velocity, NULL, cancel,
                           context) &&
              pgpu_copy_d2h(h->stream, result, h->velocity, sizeof(result)) &&

@@ -162,3 +162,64 @@ def test_batched_lsd_and_eos_vs_oracle(lib, pkg, oracle, oracle_mod, streams, gr
     for b in (dc, dr, dl, de):
         b.free()
     lib.phonon_flow_head_device_destroy(dev)
+
+
+@pytest.mark.parametrize("streams,graph", [(5, 1), (64, 1), (64, 0)])
+def test_frame_vs_oracle(lib, pkg, oracle, oracle_mod, streams, graph):
+    """One frame after the decode step (phonon_flow_head_device_frame): the
+    output norm (LayerNorm eps 1e-5, src/phonon_transformer.c:904-914), the
+    LSD step and EOS logit at the normalized state, and the next step's
+    input = input_linear . latent + condition (src/phonon_transformer.c:
+    860-874), against the oracle's LayerNorm, head and linear per stream."""
+    bits = helpers.random_flow_head_bits(31)
+    rng = np.random.default_rng(32)
+    eos_w = helpers.bf16_bits(rng.standard_normal(512).astype(np.float32) * 0.05)
+    eos_b = helpers.bf16_bits(np.array([-0.25], np.float32))
+    norm_w = helpers.bf16_bits(1.0 + 0.1 * rng.standard_normal(512).astype(np.float32))
+    norm_b = helpers.bf16_bits(0.1 * rng.standard_normal(512).astype(np.float32))
+    lin = helpers.bf16_bits(rng.standard_normal((512, 32)).astype(np.float32) * 0.2)
+    views = pkg.Views()
+    head = views.flow_head(bits)
+    ew, eb = views.bf16(eos_w.reshape(1, 512), (1, 512)), views.bf16(eos_b, (1,))
+    nw, nb = views.bf16(norm_w, (512,)), views.bf16(norm_b, (512,))
+    lv = views.bf16(lin, (512, 32))
+    dev = ctypes.c_void_p()
+    assert lib.phonon_flow_head_device_create(ctypes.byref(head), ctypes.byref(ew),
+                                              ctypes.byref(eb), 64, ctypes.byref(dev))
+    assert lib.phonon_flow_head_device_set_frame(dev, ctypes.byref(nw), ctypes.byref(nb),
+                                                 ctypes.byref(lv)), pkg.last_error(lib)
+    assert not lib.phonon_flow_head_device_set_frame(dev, ctypes.byref(nw), ctypes.byref(nb),
+                                                     ctypes.byref(lv))  # once per head
+    assert lib.phonon_flow_head_device_set_graph(dev, graph)
+    stream = lib.phonon_flow_head_device_stream(dev)
+    outputs = (rng.standard_normal((streams, 512)) * 3 + 0.5).astype(np.float32)
+    cond = rng.standard_normal((streams, 512)).astype(np.float32)
+    raw = rng.standard_normal((streams, 32)).astype(np.float32)
+    bufs = [pkg.DeviceBuffer(lib, n) for n in (outputs.nbytes, cond.nbytes, raw.nbytes,
+                                               raw.nbytes, streams * 4, cond.nbytes)]
+    do, dc, dr, dl, de, dn = bufs
+    do.upload(outputs)
+    dc.upload(cond)
+    dr.upload(raw)
+    for _ in range(2):  # a replayed graph gives the same frame
+        assert lib.phonon_flow_head_device_frame(dev, streams, do.ptr, dc.ptr, dr.ptr, 0.6,
+                                                 dl.ptr, de.ptr, dn.ptr)
+        assert lib.phonon_flow_head_device_sync(dev), pkg.last_error(lib)
+        lat = dl.download((streams, 32), stream=stream)
+        eos = de.download((streams,), stream=stream)
+        nxt = dn.download((streams, 512), stream=stream)
+        oh = oracle_mod.OracleHead(oracle, float_head(bits))
+        wl = helpers.bf16_float(lin)
+        for s in range(streams):
+            ok, state = oracle.layer_norm(outputs[s], helpers.bf16_float(norm_w),
+                                          helpers.bf16_float(norm_b), 1e-5)
+            assert ok
+            ok, ref = oh.lsd_one_step(state, raw[s], 0.6)
+            assert ok and rel(lat[s], ref) < TOL, (s, rel(lat[s], ref))
+            ok, e = oh.eos_logit(helpers.bf16_float(eos_w), helpers.bf16_float(eos_b), state)
+            assert ok and abs(eos[s] - e) <= TOL * max(1.0, abs(e)), (s, eos[s], e)
+            ok, emb = oracle.linear_batch(wl, lat[s])
+            assert ok and rel(nxt[s], emb[0] + cond[s]) < TOL, s
+    for b in bufs:
+        b.free()
+    lib.phonon_flow_head_device_destroy(dev)
