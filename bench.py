@@ -525,6 +525,82 @@ def flow_head_bench(pkg, lib, streams=64, calls=200, seed=11, graph=1):
             "clean": clean}
 
 
+def frame_loop_bench(pkg, lib, layers=12, streams=64, frames=30, warmup=3, seed=2026,
+                     shared_stream=True):
+    """The whole per-frame loop of B streams on the GPU: the decode step
+    (library default mode), then phonon_flow_head_device_frame (output norm,
+    LSD step + EOS logit, latent embedding + condition) writing the next
+    step's inputs; the head runs on the batch's stream (shared_stream) or on
+    its own, handed over through events. Random BF16 head, out_norm and
+    input_linear of the reference's shapes."""
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import helpers
+    rng = np.random.default_rng(seed + 5)
+    lengths = np.random.default_rng(seed).integers(1, 2049, size=streams) - 1
+    d = DecodeSetup(pkg, lib, layers, streams, lengths, frames + warmup + 8, seed)
+    views = pkg.Views()
+    head = views.flow_head(helpers.random_flow_head_bits(seed + 6))
+    eos_w = helpers.bf16_bits(rng.standard_normal(512).astype(np.float32) * 0.05)
+    ew, eb = views.bf16(eos_w.reshape(1, 512), (1, 512)), views.bf16(
+        helpers.bf16_bits(np.array([0.0], np.float32)), (1,))
+    nw = views.bf16(helpers.bf16_bits(np.ones(512, np.float32)), (512,))
+    nb = views.bf16(helpers.bf16_bits(np.zeros(512, np.float32)), (512,))
+    lv = views.bf16(helpers.bf16_bits(rng.standard_normal((512, 32)).astype(np.float32) * 0.1),
+                    (512, 32))
+    h = ctypes.c_void_p()
+    assert lib.phonon_flow_head_device_create(ctypes.byref(head), ctypes.byref(ew),
+                                              ctypes.byref(eb), streams, ctypes.byref(h))
+    assert lib.phonon_flow_head_device_set_frame(h, ctypes.byref(nw), ctypes.byref(nb),
+                                                 ctypes.byref(lv))
+    if shared_stream:
+        assert lib.phonon_flow_head_device_set_stream(h, d.stream)
+    hs = lib.phonon_flow_head_device_stream(h)
+    cond = pkg.DeviceBuffer(lib, streams * 512 * 4)
+    raw = pkg.DeviceBuffer(lib, streams * 32 * 4)
+    lat = pkg.DeviceBuffer(lib, streams * 32 * 4)
+    eos = pkg.DeviceBuffer(lib, streams * 4)
+    cond.upload(rng.standard_normal((streams, 512)).astype(np.float32))
+    raw.upload(rng.standard_normal((streams, 32)).astype(np.float32))
+    decoded, framed = ctypes.c_void_p(), ctypes.c_void_p()
+    assert lib.pgpu_event_create(ctypes.byref(decoded))
+    assert lib.pgpu_event_create(ctypes.byref(framed))
+    din, dout = d.din, d.dout
+
+    def frame():
+        assert lib.phonon_flow_batch_step_device(d.batch, din, 10000.0, dout)
+        if not shared_stream:
+            assert lib.pgpu_event_record(decoded, d.stream)
+            assert lib.pgpu_stream_wait_event(hs, decoded)
+        assert lib.phonon_flow_head_device_frame(h, streams, dout, cond.ptr, raw.ptr, 0.7, lat.ptr,
+                                                 eos.ptr, din)
+        if not shared_stream:
+            assert lib.pgpu_event_record(framed, hs)
+            assert lib.pgpu_stream_wait_event(d.stream, framed)
+
+    for _ in range(warmup):
+        frame()
+    assert lib.pgpu_stream_sync(d.stream)
+    timer = Timer(lib, d.stream)
+    timer.start()
+    for _ in range(frames):
+        frame()
+    ms = timer.stop_ms() / frames
+    clean = bool(lib.phonon_flow_batch_sync(d.batch)) and bool(
+        lib.phonon_flow_head_device_sync(h))
+    for b in (cond, raw, lat, eos):
+        b.free()
+    lib.pgpu_event_destroy(decoded)
+    lib.pgpu_event_destroy(framed)
+    lib.phonon_flow_head_device_destroy(h)
+    d.close()
+    return {"workload": f"closed per-frame loop, B={streams}: {layers}-layer decode step + "
+                        f"output norm + flow head LSD step + EOS + latent embedding into the "
+                        f"next step's input, contexts U{{1..2048}}",
+            "head_stream": "the batch's" if shared_stream else "its own, events between",
+            "us_per_frame": round(ms * 1e3, 1), "frames_per_s": round(streams / (ms * 1e-3), 1),
+            "clean": clean}
+
+
 def attention_curve(pkg, lib, seed=9):
     """One attention layer decode (H=8, dh=64): append + attention per step,
     vs context length, as one 1-layer batched step of one stream."""
@@ -650,6 +726,8 @@ def main():
         print(json.dumps(large_batch_with_prefill(pkg, lib, args.seed)), flush=True)
         return
     if args.flow_head:
+        for shared in (True, False):
+            print(json.dumps(frame_loop_bench(pkg, lib, shared_stream=shared)), flush=True)
         for streams in (64, 1):
             for graph in (1, 0):
                 r = flow_head_bench(pkg, lib, streams=streams, graph=graph)
@@ -702,7 +780,8 @@ def main():
         line["q8_matvec_2048x512"] = q8_matvec_bench(pkg, lib)
         log(f"q8 matvec: {line['q8_matvec_2048x512']}")
         line["flow_head"] = {"b64": flow_head_bench(pkg, lib, streams=64),
-                             "b1": flow_head_bench(pkg, lib, streams=1)}
+                             "b1": flow_head_bench(pkg, lib, streams=1),
+                             "frame_loop_b64": frame_loop_bench(pkg, lib)}
         log(f"flow head: {line['flow_head']}")
         line["attention_layer_curve"] = attention_curve(pkg, lib)
         log(f"attention curve: {line['attention_layer_curve']}")

@@ -101,7 +101,11 @@ int phonon_flow_head_device_frame(PhononFlowHeadDevice *head, size_t streams,
  * graph per (streams, buffers, temperature), two kept, and replayed; 0:
  * each kernel is launched directly. */
 int phonon_flow_head_device_set_graph(PhononFlowHeadDevice *head, int use_graph);
-/* The head's HIP stream (for event timing by the caller). */
+/* Runs the head's work on `stream` (a caller's HIP stream, e.g. the decode
+ * batch's, so a frame needs no cross-stream hand-off; NULL = the head's
+ * own). The caller keeps that stream alive while the head uses it. */
+int phonon_flow_head_device_set_stream(PhononFlowHeadDevice *head, void *stream);
+/* The head's HIP stream in use (for event timing by the caller). */
 void *phonon_flow_head_device_stream(const PhononFlowHeadDevice *head);
 /* Waits for enqueued calls; returns 1 iff none saw a non-finite value (and
  * clears that record). */

@@ -242,6 +242,7 @@ EXPORTS = {
     "phonon_flow_head_device_lsd": (_i, [_vp, _sz, _vp, _vp, _f, _vp, _vp]),
     "phonon_flow_head_device_set_graph": (_i, [_vp, _i]),
     "phonon_flow_head_device_set_frame": (_i, [_vp, _vp, _vp, _vp]),
+    "phonon_flow_head_device_set_stream": (_i, [_vp, _vp]),
     "phonon_flow_head_device_frame": (_i, [_vp, _sz, _vp, _vp, _vp, _f, _vp, _vp, _vp]),
     "phonon_flow_head_device_stream": (_vp, [_vp]),
     "phonon_flow_head_device_sync": (_i, [_vp]),

@@ -48,7 +48,7 @@ struct PhononFlowHeadDevice {
     uint16_t *noise_split, *silu_split, *first_split, *time_split, *time_hidden;
     int has_eos;
     int *status;
-    void *stream;
+    void *stream, *own_stream; /* the stream in use; the one the head created */
     struct {
         void *exec;
         size_t streams;
@@ -248,7 +248,8 @@ int phonon_flow_head_device_create(const PhononFlowHead *head, const PhononTenso
     PhononFlowHeadDevice *h = calloc(1, sizeof(*h));
     if (!h)
         return 0;
-    int ok = pgpu_stream_create(&h->stream) && (h->status = pgpu_malloc(sizeof(int))) &&
+    int ok = pgpu_stream_create(&h->own_stream) && (h->stream = h->own_stream) &&
+             (h->status = pgpu_malloc(sizeof(int))) &&
              pgpu_memset(h->stream, h->status, 0, sizeof(int)) &&
              upload(h, &head->input_weight, PH_WIDTH, LAT, &h->input) &&
              upload(h, &head->cond_weight, PH_WIDTH, PH_WIDTH, &h->cond) && upload_ada(h, head) &&
@@ -287,7 +288,9 @@ void phonon_flow_head_device_destroy(PhononFlowHeadDevice *h) {
     pgpu_free(h->input_linear_dev);
     pgpu_free(h->buffers);
     pgpu_free(h->status);
-    pgpu_stream_destroy(h->stream);
+    if (h->own_stream && h->stream != h->own_stream)
+        (void)pgpu_stream_sync(h->own_stream);
+    pgpu_stream_destroy(h->own_stream);
     free(h);
 }
 
@@ -410,6 +413,17 @@ int phonon_flow_head_device_frame(PhononFlowHeadDevice *h, size_t streams, const
         return 0;
     return run_lsd(h, streams, outputs, raw_noise, temperature, latents, eos_logits, conditions,
                    next_inputs);
+}
+
+int phonon_flow_head_device_set_stream(PhononFlowHeadDevice *h, void *stream) {
+    if (!h || !pgpu_stream_sync(h->stream))
+        return 0;
+    h->stream = stream ? stream : h->own_stream;
+    for (size_t i = 0; i < 2; i++) {
+        pgpu_graph_destroy(h->graphs[i].exec);
+        h->graphs[i].exec = NULL;
+    }
+    return 1;
 }
 
 int phonon_flow_head_device_set_graph(PhononFlowHeadDevice *h, int use_graph) {

@@ -223,3 +223,38 @@ def test_frame_vs_oracle(lib, pkg, oracle, oracle_mod, streams, graph):
     for b in bufs:
         b.free()
     lib.phonon_flow_head_device_destroy(dev)
+
+
+def test_head_on_a_callers_stream(lib, pkg):
+    """phonon_flow_head_device_set_stream: the LSD step enqueued on a
+    caller's stream (graph re-captured there) gives the bits it gives on the
+    head's own stream; NULL switches back."""
+    bits = helpers.random_flow_head_bits(41)
+    rng = np.random.default_rng(42)
+    views = pkg.Views()
+    head = views.flow_head(bits)
+    dev = ctypes.c_void_p()
+    assert lib.phonon_flow_head_device_create(ctypes.byref(head), None, None, 16,
+                                              ctypes.byref(dev))
+    cond = rng.standard_normal((16, 512)).astype(np.float32)
+    raw = rng.standard_normal((16, 32)).astype(np.float32)
+    dc, dr, dl = (pkg.DeviceBuffer(lib, n) for n in (cond.nbytes, raw.nbytes, raw.nbytes))
+    dc.upload(cond)
+    dr.upload(raw)
+    mine = ctypes.c_void_p()
+    assert lib.pgpu_stream_create(ctypes.byref(mine))
+    outs = []
+    for stream in (None, mine.value, None):
+        assert lib.phonon_flow_head_device_set_stream(dev, stream)
+        assert lib.phonon_flow_head_device_stream(dev) == (stream or
+                                                           lib.phonon_flow_head_device_stream(dev))
+        assert lib.phonon_flow_head_device_lsd(dev, 16, dc.ptr, dr.ptr, 0.9, dl.ptr, None)
+        assert lib.phonon_flow_head_device_sync(dev)
+        outs.append(dl.download((16, 32)))
+    if mine.value:
+        assert lib.phonon_flow_head_device_stream(dev) != mine.value
+    assert np.array_equal(outs[0], outs[1]) and np.array_equal(outs[0], outs[2])
+    for b in (dc, dr, dl):
+        b.free()
+    lib.phonon_flow_head_device_destroy(dev)
+    lib.pgpu_stream_destroy(mine)
