@@ -266,11 +266,12 @@ int pgpu_head_mlp_in(void *stream, const pgpu_matrix *w, const float *x, int str
                      int ld_mod, const float *bias, uint16_t *out_split, int *status);
 /* out [streams][w->rows] = (residual +) (w . h + bias), h = LN(x; eps) *
  * (1 + scale) + shift as above; with a residual, `ones` is a [w->rows]
- * vector of 1.0f. If eos: eos[s] = eos_rows[s * eos_ld]. */
+ * vector of 1.0f, and out_split (optional) receives out's split fragments
+ * (K = w->rows). If eos: eos[s] = eos_rows[s * eos_ld]. */
 int pgpu_head_final(void *stream, const pgpu_matrix *w, const float *x, int streams, float eps,
                     const float *mod, int ld_mod, const float *bias, const float *residual,
-                    const float *ones, float *out, const float *eos_rows, int eos_ld, float *eos,
-                    int *status);
+                    const float *ones, float *out, uint16_t *out_split, const float *eos_rows,
+                    int eos_ld, float *eos, int *status);
 /* Split fragments (K = 256, stream 0) of [cos | sin](value * freqs[128]). */
 int pgpu_head_time_phase(void *stream, const float *freqs, float value, uint16_t *xs,
                          int *status);

@@ -228,8 +228,8 @@ EXPORTS = {
                              _vp, _f, _vp, _vp, _vp]),
     "pgpu_head_mod": (_i, [_vp, _vp, _vp, _i, _vp, _vp, _i, _vp, _vp, _vp, _vp, _vp]),
     "pgpu_head_mlp_in": (_i, [_vp, _vp, _vp, _i, _vp, _vp, _f, _vp, _i, _vp, _vp, _vp]),
-    "pgpu_head_final": (_i, [_vp, _vp, _vp, _i, _f, _vp, _i, _vp, _vp, _vp, _vp, _vp, _i, _vp,
-                             _vp]),
+    "pgpu_head_final": (_i, [_vp, _vp, _vp, _i, _f, _vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _i,
+                             _vp, _vp]),
     "pgpu_head_time_phase": (_i, [_vp, _vp, _f, _vp, _vp]),
     "pgpu_head_time_sum": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "phonon_flow_head_forward": (_i, [_vp, _vp, _vp, _f, _f, _vp]),

@@ -59,7 +59,7 @@ enum Epilogue {
     EPI_GELU_SPLIT = 2,
     EPI_QKV = 3,
     EPI_SILU_SPLIT = 4,  // split fragments of SiLU((dot + bias) + bias2)
-    EPI_GATED = 5,       // residual + gate * (dot + bias)
+    EPI_GATED = 5,       // residual + gate * (dot + bias); optionally also split fragments
 };
 
 constexpr int kTaskWaves = 8, kTaskThreads = 64 * kTaskWaves;
@@ -645,6 +645,7 @@ __device__ inline bool epilogue(const GemmArgs &a, const EpiOperands &e, const f
                 bad |= !isfinite(y[r]);
             }
             store_out(o, make_float4(y[0], y[1], y[2], y[3]), wt);
+            if (a.out_split) store_split4(a.out_split, s, row0, a.out_kb, y, wt);
         }
     } else {  // EPI_QKV: rows [0,512) q, [512,1024) k, [1024,1536) v
         if (live) {

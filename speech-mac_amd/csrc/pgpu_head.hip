@@ -295,14 +295,17 @@ extern "C" int pgpu_head_mlp_in(void *stream, const pgpu_matrix *w, const float 
 extern "C" int pgpu_head_final(void *stream, const pgpu_matrix *w, const float *x, int streams,
                                float eps, const float *mod, int ld_mod, const float *bias,
                                const float *residual, const float *ones, float *out,
-                               const float *eos_rows, int eos_ld, float *eos, int *status) {
+                               uint16_t *out_split, const float *eos_rows, int eos_ld, float *eos,
+                               int *status) {
     if (!w || !bf16_matrix(w, w->rows, kWidth) || w->rows % 16 || !x || streams <= 0 || !mod ||
         ld_mod < 2 * kWidth || ld_mod % 4 || !out || (residual && !ones) || !(eps > 0.0f) ||
-        (eos && (!eos_rows || eos_ld < 1)))
+        (eos && (!eos_rows || eos_ld < 1)) || (out_split && !residual))
         return bad_arguments(__func__);
     GemmArgs a = head_args(w, streams, status);
     a.ln_x = x;
     a.ln_eps = eps;
+    a.out_split = out_split;  // with a residual: the output's split fragments too
+    a.out_kb = (int)w->rows / 32;
     a.mod = mod;
     a.ld_mod = ld_mod;
     a.bias = bias;

@@ -202,14 +202,15 @@ static int enqueue_tsum(PhononFlowHeadDevice *h, float s, float t, float *tsum) 
 }
 
 /* The head for n streams: conditions [n][512], raw [n][32] scaled by `scale`
+ * (out_split: the latent's split fragments too, lsd only)
  * into the state (the noise of an LSD step, or the normalized state itself
  * with scale 1). Writes the latent noise + velocity (lsd) or the velocity to
  * out [n][32] and, if eos, the EOS logits. The cancel poll runs before each
  * block and before the final layer. */
 static int enqueue_head(PhononFlowHeadDevice *h, size_t n, const float *conditions,
                         const float *norm, const float *raw, float scale, const float *tsum,
-                        int lsd, float *out, float *eos, PhononCancelPoll cancel,
-                        void *context) {
+                        int lsd, float *out, uint16_t *out_split, float *eos,
+                        PhononCancelPoll cancel, void *context) {
     void *st = h->stream;
     const int B = (int)n;
     const pgpu_gemm_input first = {.split = h->first_split};
@@ -233,8 +234,8 @@ static int enqueue_head(PhononFlowHeadDevice *h, size_t n, const float *conditio
     if (cancel && cancel(context))
         return 0;
     return pgpu_head_final(st, &h->final, h->x, B, 1e-6f, h->mod + HB * ADA, MOD, h->b_final,
-                           lsd ? h->noise : NULL, h->ones, out, h->eos_rows, EOS_ROWS, eos,
-                           h->status);
+                           lsd ? h->noise : NULL, h->ones, out, out_split, h->eos_rows, EOS_ROWS,
+                           eos, h->status);
 }
 
 int phonon_flow_head_device_create(const PhononFlowHead *head, const PhononTensorView *eos_weight,
@@ -309,19 +310,20 @@ int phonon_flow_head_device_sync(PhononFlowHeadDevice *h) {
 
 /* The LSD step; with `next` (a frame): the conditions are the decoder's
  * outputs, normalized by out_norm in the head's first launch, and next =
- * input_linear . latents + embed (the latent's embedding, split into
- * fragments in the noise buffer, which the step no longer needs). */
+ * input_linear . latents + embed (the latent's embedding; the final launch
+ * writes the latent's split fragments into the noise buffer's, which the
+ * step no longer reads then). */
 static int enqueue_lsd(PhononFlowHeadDevice *h, size_t streams, const float *conditions,
                        const float *raw_noise, float temperature, float *latents,
                        float *eos_logits, const float *embed, float *next) {
     if (!enqueue_head(h, streams, conditions, next ? h->out_norm : NULL, raw_noise,
-                      sqrtf(temperature), h->tsum_lsd, 1, latents, eos_logits, NULL, NULL))
+                      sqrtf(temperature), h->tsum_lsd, 1, latents, next ? h->noise_split : NULL,
+                      eos_logits, NULL, NULL))
         return 0;
     if (!next)
         return 1;
     const pgpu_gemm_input lat = {.split = h->noise_split};
-    return pgpu_split_rows(h->stream, latents, (int)streams, LAT, h->noise_split, h->status) &&
-           pgpu_gemm_residual(h->stream, &h->input_linear, &lat, (int)streams, embed, next,
+    return pgpu_gemm_residual(h->stream, &h->input_linear, &lat, (int)streams, embed, next,
                               h->status);
 }
 
@@ -512,7 +514,7 @@ static int single(const PhononFlowHead *head, const float condition[512], const 
         ok = pgpu_copy_h2d(h->stream, h->stage, staged, sizeof(staged)) &&
              (lsd_times || enqueue_tsum(h, s, t, h->tsum)) &&
              enqueue_head(h, 1, cond, NULL, state, lsd ? sqrtf(temperature) : 1.0f,
-                          lsd_times ? h->tsum_lsd : h->tsum, lsd, h->velocity, NULL, cancel,
+                          lsd_times ? h->tsum_lsd : h->tsum, lsd, h->velocity, NULL, NULL, cancel,
                           context) &&
              pgpu_copy_d2h(h->stream, result, h->velocity, sizeof(result)) &&
              phonon_flow_head_device_sync(h);
