@@ -526,7 +526,7 @@ def flow_head_bench(pkg, lib, streams=64, calls=200, seed=11, graph=1):
 
 
 def frame_loop_bench(pkg, lib, layers=12, streams=64, frames=30, warmup=3, seed=2026,
-                     shared_stream=True):
+                     shared_stream=True, graph=1):
     """The whole per-frame loop of B streams on the GPU: the decode step
     (library default mode), then phonon_flow_head_device_frame (output norm,
     LSD step + EOS logit, latent embedding + condition) writing the next
@@ -554,6 +554,7 @@ def frame_loop_bench(pkg, lib, layers=12, streams=64, frames=30, warmup=3, seed=
                                                  ctypes.byref(lv))
     if shared_stream:
         assert lib.phonon_flow_head_device_set_stream(h, d.stream)
+    assert lib.phonon_flow_head_device_set_graph(h, graph)
     hs = lib.phonon_flow_head_device_stream(h)
     cond = pkg.DeviceBuffer(lib, streams * 512 * 4)
     raw = pkg.DeviceBuffer(lib, streams * 32 * 4)
@@ -597,6 +598,7 @@ def frame_loop_bench(pkg, lib, layers=12, streams=64, frames=30, warmup=3, seed=
                         f"output norm + flow head LSD step + EOS + latent embedding into the "
                         f"next step's input, contexts U{{1..2048}}",
             "head_stream": "the batch's" if shared_stream else "its own, events between",
+            "head_graph": bool(graph),
             "us_per_frame": round(ms * 1e3, 1), "frames_per_s": round(streams / (ms * 1e-3), 1),
             "clean": clean}
 
@@ -726,8 +728,9 @@ def main():
         print(json.dumps(large_batch_with_prefill(pkg, lib, args.seed)), flush=True)
         return
     if args.flow_head:
-        for shared in (True, False):
-            print(json.dumps(frame_loop_bench(pkg, lib, shared_stream=shared)), flush=True)
+        for shared, graph in ((True, 1), (True, 0), (False, 1)):
+            print(json.dumps(frame_loop_bench(pkg, lib, shared_stream=shared, graph=graph)),
+                  flush=True)
         for streams in (64, 1):
             for graph in (1, 0):
                 r = flow_head_bench(pkg, lib, streams=streams, graph=graph)
