@@ -23,6 +23,7 @@ import ctypes
 import importlib.util
 import json
 import os
+import subprocess
 import sys
 import time
 
@@ -423,6 +424,77 @@ def large_batch_with_prefill(pkg, lib, seed, layers=12, streams=256, new_streams
             "clean": clean}
 
 
+def b1_with_prefill(pkg, lib, layers, seed, prompt=256, frames=750, warmup=10):
+    """B=1: one stream, `layers` layers. A `prompt`-position prefill (the
+    batched causal prefill, positions 0..prompt-1 through every layer in one
+    pass), then `frames` decode steps, each step's output fed back as the
+    next input. Run once untimed (prefill + `warmup` steps), then again from
+    position 0: prefill and decode timed separately with HIP events."""
+    import speech_mac_amd.synthetic as syn
+    max_pos = prompt + frames + 16
+    table_len = (max_pos + 15) // 16
+    blocks = table_len + 3
+    views = pkg.Views()
+    weights = views.layers(syn.flow_model(seed, layers))
+    model, pool, batch = ctypes.c_void_p(), ctypes.c_void_p(), ctypes.c_void_p()
+    assert lib.phonon_flow_model_create(weights, layers, ctypes.byref(model))
+    assert lib.phonon_kv_pool_create(layers, blocks, ctypes.byref(pool))
+    ids = np.zeros(blocks, np.int32)
+    assert lib.phonon_kv_pool_alloc(pool, blocks, ids.ctypes.data_as(P_I32))
+    table = np.ascontiguousarray(np.random.default_rng(seed + 60).permutation(ids)[:table_len])
+    assert lib.phonon_flow_batch_create(model, pool, prompt, max_pos, ctypes.byref(batch))
+    stream = lib.phonon_flow_batch_stream(batch)
+    rng = np.random.default_rng(seed + 61)
+    pin = pkg.DeviceBuffer(lib, prompt * 512 * 4)
+    pout = pkg.DeviceBuffer(lib, prompt * 512 * 4)
+    pin.upload(rng.standard_normal((prompt, 512)).astype(np.float32))
+    x0 = rng.standard_normal(512).astype(np.float32)
+    din, dout = lib.phonon_flow_batch_device_inputs(batch), lib.phonon_flow_batch_device_outputs(
+        batch)
+    first = np.zeros(1, np.uintp)
+    counts = np.full(1, prompt, np.uintp)
+    timer = Timer(lib, stream)
+
+    def run(steps):
+        nonlocal din, dout
+        assert lib.pgpu_copy_h2d(stream, din, x0.ctypes.data, x0.nbytes)
+        timer.start()
+        assert lib.phonon_flow_batch_prefill_device(
+            batch, 1, first.ctypes.data_as(P_SZ), counts.ctypes.data_as(P_SZ),
+            table.ctypes.data_as(P_I32), table_len, pin.ptr, 10000.0, pout.ptr)
+        pre_ms = timer.stop_ms()
+        pos = np.array([prompt], np.uintp)
+        assert lib.phonon_flow_batch_set_streams(batch, 1, pos.ctypes.data_as(P_SZ),
+                                                 table.ctypes.data_as(P_I32), table_len)
+        timer.start()
+        for _ in range(steps):
+            assert lib.phonon_flow_batch_step_device(batch, din, 10000.0, dout)
+            din, dout = dout, din
+        dec_ms = timer.stop_ms()
+        return pre_ms, dec_ms
+
+    run(warmup)
+    clean = bool(lib.phonon_flow_batch_sync(batch))
+    pre_ms, dec_ms = run(frames)
+    clean = clean and bool(lib.phonon_flow_batch_sync(batch))
+    pin.free()
+    pout.free()
+    lib.phonon_flow_batch_destroy(batch)
+    lib.phonon_kv_pool_destroy(pool)
+    lib.phonon_flow_model_destroy(model)
+    total_bytes = sum(step_bytes(layers, [prompt + i + 1]) for i in range(frames))
+    return {"frames_per_s": round(frames / (dec_ms * 1e-3), 1),
+            "us_per_step": round(dec_ms * 1e3 / frames, 2),
+            "effective_GBps": round(total_bytes / (dec_ms * 1e-3) / 1e9, 1),
+            "prefill_ms": round(pre_ms, 3),
+            "prefill_tokens_per_s": round(prompt / (pre_ms * 1e-3), 1),
+            "workload": f"B=1, {layers} layers: a {prompt}-position prompt through the batched "
+                        f"prefill, then {frames} decode frames (contexts {prompt + 1}.."
+                        f"{prompt + frames}), each output fed back as the next input; the "
+                        f"library's default step mode",
+            "clean": clean}
+
+
 def q8_matvec_bench(pkg, lib, seed=1, calls=2000):
     """Config: single Q8 matvec 2048x512; 300 rotating weight copies (>256 MB)."""
     import speech_mac_amd.synthetic as syn
@@ -650,10 +722,64 @@ def cpu_flow_head(seed=11, budget_s=2.0):
                       f"{elapsed:.1f} s)"}
 
 
-def cpu_baseline(pkg, lib, layers, lengths, seed, budget_s=10.0):
-    """The C restatement of the reference step (oracle) on host threads, one
-    pthread per stream group, on a bounded sample of streams of the same
-    context distribution; reported in frames/s."""
+def cpu_host():
+    """What the CPU baselines ran on: nproc, the CPUs this process may use,
+    the CPU model and whether SMT is on (lscpu / sysfs)."""
+    info = {"nproc": os.cpu_count(), "usable_cpus": len(os.sched_getaffinity(0))}
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        fields = dict(line.split(":", 1) for line in out.splitlines() if ":" in line)
+        info["model"] = fields.get("Model name", "").strip()
+        info["threads_per_core"] = int(fields.get("Thread(s) per core", "0").strip() or 0)
+    except (OSError, ValueError, subprocess.SubprocessError):
+        pass
+    try:
+        with open("/sys/devices/system/cpu/smt/active") as f:
+            info["smt_active"] = f.read().strip() == "1"
+    except OSError:
+        pass
+    return info
+
+
+def cpu_threads():
+    """Host threads for the batched CPU leg: every CPU this process may use,
+    at most 16 (the GPU box's CPU share for one GPU)."""
+    return max(1, min(16, len(os.sched_getaffinity(0))))
+
+
+def cpu_q8_matvec(seed=1, budget_s=2.0):
+    """The single Q8 matvec (2048x512) on one core: the reference's own
+    phonon_q8.c, compiled from its source into oracle/_ref when that build
+    exists (kind "reference"), else the oracle's restatement, bit-identical
+    to it (kind "port")."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle_py
+    import speech_mac_amd.synthetic as syn
+    rng = np.random.default_rng(seed)
+    w = syn.q8_matrix(rng, 2048, 512)
+    x = rng.standard_normal(512).astype(np.float32)
+    if oracle_py.ReferenceQ8.available():
+        impl, kind = oracle_py.ReferenceQ8(), "reference"
+    else:
+        impl, kind = oracle_py.Oracle(), "port"
+    calls, elapsed = 0, 0.0
+    while elapsed < budget_s:
+        t0 = time.perf_counter()
+        for _ in range(50):
+            ok, _ = impl.q8_matvec(w, x, 2048, 512)
+        elapsed += time.perf_counter() - t0
+        assert ok
+        calls += 50
+    us = elapsed / calls * 1e6
+    return {"value": round(us, 2), "unit": "us/call", "cores": 1, "kind": kind,
+            "GBps": round(1124352 / (us * 1e-6) / 1e9, 2),
+            "sample": f"{calls} calls of phonon_q8_matvec 2048x512 (same weights every call), "
+                      f"{elapsed:.1f} s"}
+
+
+def cpu_b1_stack(layers, seed, budget_s=4.0):
+    """B=1 decode on one core: the oracle's 12-layer stack step at the B=1
+    workload's positions (256 .. 1005 after the 256-position prefill)."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     sys.path.insert(0, os.path.join(ROOT, "tests"))
     import oracle_py
@@ -661,31 +787,64 @@ def cpu_baseline(pkg, lib, layers, lengths, seed, budget_s=10.0):
     import speech_mac_amd.synthetic as syn
     oracle = oracle_py.Oracle()
     om = oracle_py.OracleModel(oracle, helpers.oracle_layers(oracle, syn.flow_model(seed, layers)))
-    threads = max(1, min(16, os.cpu_count() or 1))
-    sample = list(np.asarray(lengths)[:threads])
-    # Every repetition is the same decode step (append at each stream's
-    # position, attend position+1 keys), so the cache needs one free slot.
-    cap = int(max(sample)) + 1
-    n = len(sample)
+    cap = 1006
     tile = np.random.default_rng(seed).standard_normal(1 << 16).astype(np.float32)
-    total = n * layers * cap * 512
-    keys = np.resize(tile, total).reshape(n, layers, cap, 512)
-    vals = np.resize(tile[::-1].copy(), total).reshape(n, layers, cap, 512)
-    x = np.random.default_rng(seed + 1).standard_normal((n, 512)).astype(np.float32)
-    pos = np.array(sample, np.int64)
+    keys = np.resize(tile, layers * cap * 512).reshape(layers, cap, 512)
+    vals = np.resize(tile[::-1].copy(), layers * cap * 512).reshape(layers, cap, 512)
+    x = np.random.default_rng(seed + 1).standard_normal(512).astype(np.float32)
+    positions = np.random.default_rng(seed + 2).integers(256, cap, size=10000)
     steps, elapsed = 0, 0.0
     while elapsed < budget_s:
         t0 = time.perf_counter()
-        ok, y = om.stack_step_streams(keys, vals, cap, pos, x, threads)
+        ok, _ = om.stack_step(keys, vals, cap, int(positions[steps]), x)
         elapsed += time.perf_counter() - t0
         assert ok
         steps += 1
-    frames = n * steps
+    return {"value": round(steps / elapsed, 2), "unit": "frames/s", "cores": 1, "kind": "port",
+            "us_per_step": round(elapsed / steps * 1e6, 1),
+            "sample": f"{steps} single-stream {layers}-layer decode steps (the oracle's stack "
+                      f"step) at positions drawn from 256..1005, {elapsed:.1f} s"}
+
+
+def cpu_baseline(pkg, lib, layers, lengths, seed, budget_s=10.0):
+    """The C restatement of the reference step (oracle) for all B streams of
+    the headline workload, one pthread per stream of a group: streams run
+    in groups of `threads`, one decode step each, at their own contexts;
+    reported in frames/s over the whole batch."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import oracle_py
+    import helpers
+    import speech_mac_amd.synthetic as syn
+    oracle = oracle_py.Oracle()
+    om = oracle_py.OracleModel(oracle, helpers.oracle_layers(oracle, syn.flow_model(seed, layers)))
+    threads = cpu_threads()
+    lengths = np.asarray(lengths, np.int64)
+    groups = [lengths[i:i + threads] for i in range(0, len(lengths), threads)]
+    # Every repetition is the same decode step (append at each stream's
+    # position, attend position+1 keys), so the cache needs one free slot.
+    cap = int(lengths.max()) + 1
+    tile = np.random.default_rng(seed).standard_normal(1 << 16).astype(np.float32)
+    total = threads * layers * cap * 512
+    keys = np.resize(tile, total).reshape(threads, layers, cap, 512)
+    vals = np.resize(tile[::-1].copy(), total).reshape(threads, layers, cap, 512)
+    x = np.random.default_rng(seed + 1).standard_normal((threads, 512)).astype(np.float32)
+    reps, frames, elapsed = 0, 0, 0.0
+    while elapsed < budget_s:
+        for g in groups:
+            n = len(g)
+            t0 = time.perf_counter()
+            ok, _ = om.stack_step_streams(keys[:n], vals[:n], cap, g, x[:n], n)
+            elapsed += time.perf_counter() - t0
+            assert ok
+            frames += n
+        reps += 1
     return {"value": round(frames / elapsed, 2), "unit": "frames/s", "cores": threads,
-            "kind": "port",
-            "sample": f"{n} streams x {steps} repetitions of one 12-layer decode step (the "
-                      f"oracle's stack step) at contexts from the same U{{1..2048}} draw, one "
-                      f"pthread per stream, {elapsed:.1f} s"}
+            "kind": "port", "host": cpu_host(),
+            "sample": f"all {len(lengths)} streams of the headline workload (contexts "
+                      f"U{{1..2048}}), {reps} repetitions of one {layers}-layer decode step each "
+                      f"(the oracle's stack step), {threads} pthreads (one per stream of a group "
+                      f"of {threads}), {elapsed:.1f} s"}
 
 
 def main():
@@ -768,16 +927,8 @@ def main():
         "roofline": roof,
     }
     if not args.skip_extras:
-        b1_steps = 750
-        d1, r1 = run_decode(pkg, lib, args.layers, 1, [256], b1_steps, 10, args.seed)
-        d1.close()
-        line["b1"] = {"frames_per_s": round(b1_steps / (r1["ms"] * 1e-3), 1),
-                      "us_per_step": round(r1["ms"] * 1e3 / b1_steps, 2),
-                      "effective_GBps": round(r1["bytes"] / (r1["ms"] * 1e-3) / 1e9, 1),
-                      "workload": "B=1, 12 layers, context 256 (synthetic prefill) then 750 "
-                                  "decode frames, the library's default step (one launch)",
-                      "clean": r1["clean"]}
-        log(f"B=1: {line['b1']['us_per_step']} us/step")
+        line["b1"] = b1_with_prefill(pkg, lib, args.layers, args.seed)
+        log(f"B=1: {line['b1']}")
         line["b256_with_prefill"] = large_batch_with_prefill(pkg, lib, args.seed)
         log(f"B=256 + prefill: {line['b256_with_prefill']}")
         line["q8_matvec_2048x512"] = q8_matvec_bench(pkg, lib)
@@ -789,6 +940,8 @@ def main():
         line["attention_layer_curve"] = attention_curve(pkg, lib)
         log(f"attention curve: {line['attention_layer_curve']}")
         line["cpu_baseline"] = cpu_baseline(pkg, lib, args.layers, lengths, args.seed)
+        line["cpu_baseline"]["b1_one_core"] = cpu_b1_stack(args.layers, args.seed)
+        line["cpu_baseline"]["q8_matvec_one_core"] = cpu_q8_matvec()
         line["cpu_baseline"]["flow_head"] = cpu_flow_head()
         log(f"cpu baseline: {line['cpu_baseline']}")
     print(json.dumps(line), flush=True)

@@ -299,12 +299,14 @@ extern "C" int pgpu_head_final(void *stream, const pgpu_matrix *w, const float *
                                int *status) {
     if (!w || !bf16_matrix(w, w->rows, kWidth) || w->rows % 16 || !x || streams <= 0 || !mod ||
         ld_mod < 2 * kWidth || ld_mod % 4 || !out || (residual && !ones) || !(eps > 0.0f) ||
-        (eos && (!eos_rows || eos_ld < 1)) || (out_split && !residual))
+        (eos && (!eos_rows || eos_ld < 1)) || (out_split && (!residual || w->rows % 32)))
         return bad_arguments(__func__);
     GemmArgs a = head_args(w, streams, status);
     a.ln_x = x;
     a.ln_eps = eps;
-    a.out_split = out_split;  // with a residual: the output's split fragments too
+    // With a residual: the output's split fragments too, w->rows / 32 column
+    // blocks per row (whole 32-column blocks only).
+    a.out_split = out_split;
     a.out_kb = (int)w->rows / 32;
     a.mod = mod;
     a.ld_mod = ld_mod;

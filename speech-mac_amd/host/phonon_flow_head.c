@@ -336,6 +336,13 @@ static int run_lsd(PhononFlowHeadDevice *h, size_t streams, const float *conditi
     if (!h || !streams || streams > h->cap || !conditions || !raw_noise || !latents ||
         (eos_logits && !h->has_eos) || !(temperature > 0.0f) || !isfinite(temperature))
         return 0;
+    /* The kernels move these rows 16 bytes at a time (float4 loads, 64-bit
+     * write-through stores): a misaligned pointer is an error, as in the Q8
+     * device matvec. */
+    const void *aligned[] = {conditions, raw_noise, latents, embed, next};
+    for (size_t i = 0; i < sizeof(aligned) / sizeof(aligned[0]); i++)
+        if ((uintptr_t)aligned[i] % 16)
+            return ph_fail("flow head: device rows must be 16-byte aligned");
     if (h->eager)
         return enqueue_lsd(h, streams, conditions, raw_noise, temperature, latents, eos_logits,
                            embed, next);

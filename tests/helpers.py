@@ -7,6 +7,7 @@ import os
 import sys
 
 import numpy as np
+from scipy.special import erf
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 PKG_DIR = os.path.join(ROOT, "speech-mac_amd")
@@ -64,6 +65,18 @@ def oracle_layers(oracle, model):
             assert ok
         out.append(d)
     return out
+
+
+def scaled_model(syn, seed, layers, factor=0.1):
+    """The synthetic benchmark model with every Q8 scale multiplied by
+    `factor` (rounded to fp16 again): a well-conditioned stack for tight
+    multi-layer, multi-step parity."""
+    model = syn.flow_model(seed, layers)
+    for layer in model:
+        for name in SHAPES:
+            sc = layer[name]["scale_bits"].view(np.float16).astype(np.float32) * factor
+            layer[name]["scale_bits"] = sc.astype(np.float16).view(np.uint16)
+    return model
 
 
 def normwise(a, b) -> float:
@@ -168,3 +181,50 @@ def random_flow_head_bits(seed: int, scale: float = 0.04) -> dict:
             v = scale * rng.standard_normal(shape)
         out[name] = bf16_bits(np.asarray(v, np.float32))
     return out
+
+
+# ------------------------------------------------- float64 restatements
+# Textbook float64 forms of the layer step, independent of the oracle's and
+# the GPU's operation orders: both fp32 implementations are measured
+# against them.
+
+def rope_phases(pos, theta=10000.0):
+    """fp32 phases pos*freq with freq = 1/powf(theta, 2i/64), powf taken as
+    correctly rounded (float64 pow rounded once to fp32)."""
+    expo = (np.arange(32, dtype=np.float32) * 2) / np.float32(64)
+    powed = np.power(np.float64(np.float32(theta)), expo.astype(np.float64)).astype(np.float32)
+    freq = np.float32(1.0) / powed
+    return (np.float32(pos) * freq).astype(np.float64)
+
+
+def softmax_attention_f64(q, k, v):
+    s = (k.astype(np.float64) @ q.astype(np.float64)) * 0.125
+    p = np.exp(s - s.max())
+    return (p @ v.astype(np.float64)) / p.sum()
+
+
+def f64_layer(w, x, keys, values, pos, theta=10000.0):
+    """Float64 textbook layer step (pre-LN, interleaved RoPE, causal SDPA,
+    erf-GELU MLP), independent of the oracle's operation order."""
+    def ln(v, g, b):
+        return (v - v.mean()) / np.sqrt(v.var() + 1e-5) * g + b
+
+    def rope(v):
+        ph = rope_phases(pos, theta)
+        h = v.reshape(8, 32, 2)
+        c, s = np.cos(ph), np.sin(ph)
+        return np.stack([h[..., 0] * c - h[..., 1] * s, h[..., 0] * s + h[..., 1] * c],
+                        -1).reshape(-1)
+
+    f = {k: np.asarray(a, np.float64) for k, a in w.items()}
+    qkv = f["qkv"] @ ln(x, f["norm1_weight"], f["norm1_bias"])
+    q, k, v = rope(qkv[:512]), rope(qkv[512:1024]), qkv[1024:]
+    keys[pos], values[pos] = k, v
+    att = np.concatenate([softmax_attention_f64(q[h * 64:(h + 1) * 64],
+                                                keys[:pos + 1, h * 64:(h + 1) * 64],
+                                                values[:pos + 1, h * 64:(h + 1) * 64])
+                          for h in range(8)])
+    r = x + f["out"] @ att
+    m = f["mlp_in"] @ ln(r, f["norm2_weight"], f["norm2_bias"])
+    m = 0.5 * m * (1 + erf(m / np.sqrt(2)))
+    return r + f["mlp_out"] @ m

@@ -3,12 +3,14 @@ cache data movement (bit-exact), the single-stream drop-ins of
 phonon_transformer.h, and the batched paged API, against the CPU oracle.
 
 Conditioning note: with the benchmark weight distribution (Q8 scales
-U[1e-3, 1e-2]) 12 stacked layers saturate softmax and amplify rounding so
-much that the oracle itself differs from float64 by ~1e-3 normwise. Tight
-(1e-4) multi-step stack parity therefore uses the same generator with scales
-x0.1 ("well-conditioned"); the benchmark distribution is checked per layer
-at 1e-4 from identical caches, and over the full stack by comparing both
-the GPU and the oracle against float64."""
+U[1e-3, 1e-2]), a 12-layer stack decoding from position 0 with independent
+N(0,1) inputs (a context made of the model's own K/V) saturates softmax and
+amplifies rounding: the oracle itself is then up to ~1e-3 from float64.
+Tight (1e-4) multi-step stack parity here therefore uses the same generator
+with scales x0.1 ("well-conditioned"); the benchmark distribution is
+checked per layer here, and through all 12 layers in test_gpu_configs.py
+(at 1e-4 of the oracle at N(0,1) contexts, and against float64 over a
+self-generated context)."""
 import ctypes
 
 import numpy as np
@@ -29,13 +31,7 @@ def i32p(a):
     return a.ctypes.data_as(ctypes.POINTER(ctypes.c_int32))
 
 
-def scaled_model(syn, seed, layers, factor=0.1):
-    model = syn.flow_model(seed, layers)
-    for layer in model:
-        for name in helpers.SHAPES:
-            sc = layer[name]["scale_bits"].view(np.float16).astype(np.float32) * factor
-            layer[name]["scale_bits"] = sc.astype(np.float16).view(np.uint16)
-    return model
+scaled_model = helpers.scaled_model
 
 
 class Cache:

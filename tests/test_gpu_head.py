@@ -201,6 +201,11 @@ def test_frame_vs_oracle(lib, pkg, oracle, oracle_mod, streams, graph):
     do.upload(outputs)
     dc.upload(cond)
     dr.upload(raw)
+    # Rows are moved 16 bytes at a time: misaligned device rows are rejected.
+    assert not lib.phonon_flow_head_device_frame(dev, streams, do.ptr, dc.ptr + 4, dr.ptr, 0.6,
+                                                 dl.ptr, de.ptr, dn.ptr)
+    assert not lib.phonon_flow_head_device_frame(dev, streams, do.ptr, dc.ptr, dr.ptr, 0.6,
+                                                 dl.ptr, de.ptr, dn.ptr + 8)
     for _ in range(2):  # a replayed graph gives the same frame
         assert lib.phonon_flow_head_device_frame(dev, streams, do.ptr, dc.ptr, dr.ptr, 0.6,
                                                  dl.ptr, de.ptr, dn.ptr)
@@ -243,11 +248,13 @@ def test_head_on_a_callers_stream(lib, pkg):
     dr.upload(raw)
     mine = ctypes.c_void_p()
     assert lib.pgpu_stream_create(ctypes.byref(mine))
+    own = lib.phonon_flow_head_device_stream(dev)  # the head's own stream
+    assert own and own != mine.value
     outs = []
     for stream in (None, mine.value, None):
         assert lib.phonon_flow_head_device_set_stream(dev, stream)
-        assert lib.phonon_flow_head_device_stream(dev) == (stream or
-                                                           lib.phonon_flow_head_device_stream(dev))
+        # NULL restores the head's own stream.
+        assert lib.phonon_flow_head_device_stream(dev) == (stream or own)
         assert lib.phonon_flow_head_device_lsd(dev, 16, dc.ptr, dr.ptr, 0.9, dl.ptr, None)
         assert lib.phonon_flow_head_device_sync(dev)
         outs.append(dl.download((16, 32)))

@@ -10,6 +10,7 @@ import pytest
 from scipy.special import erf
 
 import helpers
+from helpers import f64_layer, rope_phases, softmax_attention_f64
 
 GOLDEN = json.load(open(os.path.join(helpers.GOLDEN_DIR, "reference_vectors.json")))
 Q8GOLD = np.load(os.path.join(helpers.GOLDEN_DIR, "q8_reference_vectors.npz"))
@@ -233,15 +234,6 @@ def test_rope_golden(oracle):
     assert not oracle.rope(q, 3, 0)[0]
 
 
-def rope_phases(pos, theta=10000.0):
-    """fp32 phases pos*freq with freq = 1/powf(theta, 2i/64), powf taken as
-    correctly rounded (float64 pow rounded once to fp32)."""
-    expo = (np.arange(32, dtype=np.float32) * 2) / np.float32(64)
-    powed = np.power(np.float64(np.float32(theta)), expo.astype(np.float64)).astype(np.float32)
-    freq = np.float32(1.0) / powed
-    return (np.float32(pos) * freq).astype(np.float64)
-
-
 def test_rope_float64_rotation(oracle):
     rng = np.random.default_rng(4)
     v = rng.standard_normal(512).astype(np.float32)
@@ -291,12 +283,6 @@ def test_attention_special_cases(oracle):
     assert ok and np.allclose(out, vv.astype(np.float64).mean(0), atol=1e-5)
 
 
-def softmax_attention_f64(q, k, v):
-    s = (k.astype(np.float64) @ q.astype(np.float64)) * 0.125
-    p = np.exp(s - s.max())
-    return (p @ v.astype(np.float64)) / p.sum()
-
-
 def test_attention_float64_bound_strided(oracle):
     rng = np.random.default_rng(8)
     for count in (2, 511, 512, 513, 1500, 2049):
@@ -310,33 +296,6 @@ def test_attention_float64_bound_strided(oracle):
 
 
 # ------------------------------------------------------------ layer / stack
-def f64_layer(w, x, keys, values, pos, theta=10000.0):
-    """Float64 textbook layer step (pre-LN, interleaved RoPE, causal SDPA,
-    erf-GELU MLP), independent of the oracle's operation order."""
-    def ln(v, g, b):
-        return (v - v.mean()) / np.sqrt(v.var() + 1e-5) * g + b
-
-    def rope(v):
-        ph = rope_phases(pos, theta)
-        h = v.reshape(8, 32, 2)
-        c, s = np.cos(ph), np.sin(ph)
-        return np.stack([h[..., 0] * c - h[..., 1] * s, h[..., 0] * s + h[..., 1] * c],
-                        -1).reshape(-1)
-
-    f = {k: np.asarray(a, np.float64) for k, a in w.items()}
-    qkv = f["qkv"] @ ln(x, f["norm1_weight"], f["norm1_bias"])
-    q, k, v = rope(qkv[:512]), rope(qkv[512:1024]), qkv[1024:]
-    keys[pos], values[pos] = k, v
-    att = np.concatenate([softmax_attention_f64(q[h * 64:(h + 1) * 64],
-                                                keys[:pos + 1, h * 64:(h + 1) * 64],
-                                                values[:pos + 1, h * 64:(h + 1) * 64])
-                          for h in range(8)])
-    r = x + f["out"] @ att
-    m = f["mlp_in"] @ ln(r, f["norm2_weight"], f["norm2_bias"])
-    m = 0.5 * m * (1 + erf(m / np.sqrt(2)))
-    return r + f["mlp_out"] @ m
-
-
 def test_stack_step_matches_float64(oracle, oracle_mod, syn):
     layers, steps = 2, 6
     model = syn.flow_model(21, layers)
@@ -414,3 +373,34 @@ def test_kv_append_layout(oracle):
 def oracle_ptr():
     import ctypes
     return ctypes.POINTER(ctypes.c_float)
+
+
+def test_stack_step_streams_equals_single_stream_steps(oracle, oracle_mod, syn):
+    """oracle_stack_step_streams (the threaded CPU baseline) runs, per stream,
+    exactly oracle_stack_step on that stream's own cache: outputs and appended
+    K/V rows are bit-identical, for any thread count, over several steps."""
+    layers, streams, cap, steps = 2, 5, 40, 3
+    om = oracle_mod.OracleModel(oracle, helpers.oracle_layers(oracle, syn.flow_model(23, layers)))
+    rng = np.random.default_rng(24)
+    positions = np.array([0, 3, 17, 31, 36])
+    keys = rng.standard_normal((streams, layers, cap, 512)).astype(np.float32)
+    vals = rng.standard_normal((streams, layers, cap, 512)).astype(np.float32)
+    xs = rng.standard_normal((steps, streams, 512)).astype(np.float32)
+    single_k, single_v = keys.copy(), vals.copy()
+    want = np.zeros((steps, streams, 512), np.float32)
+    for t in range(steps):
+        for s in range(streams):
+            ok, want[t, s] = om.stack_step(single_k[s], single_v[s], cap, positions[s] + t,
+                                           xs[t, s])
+            assert ok
+    for threads in (1, 2, 5, 8):
+        k, v = keys.copy(), vals.copy()
+        for t in range(steps):
+            ok, got = om.stack_step_streams(k, v, cap, positions + t, xs[t], threads)
+            assert ok
+            assert np.array_equal(bits(got), bits(want[t])), (threads, t)
+        assert np.array_equal(bits(k), bits(single_k)) and np.array_equal(bits(v), bits(single_v))
+    # A failing stream (position past the capacity) fails the whole call.
+    ok, _ = om.stack_step_streams(keys.copy(), vals.copy(), cap, np.array([0, 1, 2, 3, cap]),
+                                  xs[0], 3)
+    assert not ok
