@@ -239,6 +239,24 @@ int pgpu_attention(void *stream, const float *q, const pgpu_paged_kv *kv, int la
 int pgpu_attention_merge(void *stream, const pgpu_attention_scratch *scratch,
                          const int32_t *positions, int streams, int heads, int max_splits,
                          float *out, uint16_t *out_split, int *status);
+/* pgpu_attention followed by pgpu_attention_merge (the same kernels, the
+ * same bits), with the split partials in a fixed device-resident array of
+ * PGPU_ATTENTION_STATIC_SLOTS (stream, head, split) slots (4.3 MB, held by
+ * every GPU the library runs on until the process ends) instead of a
+ * caller's pgpu_attention_scratch: the call allocates nothing (no hipMalloc,
+ * hipFree or allocating library routine). No counterpart in the reference;
+ * for callers that cannot allocate device memory: code under HIP graph
+ * capture, serving loops and harnesses that forbid it. Limit: streams * 8 *
+ * max_splits <= PGPU_ATTENTION_STATIC_SLOTS (e.g. 64 streams at contexts up
+ * to 8192 keys), else it returns 0 with the reason in pgpu_last_error().
+ * Every call on one GPU shares that GPU's array, which keeps the last call's
+ * partials (nothing in it needs clearing: each call writes every partial it
+ * reads); calls that overlap in time on one GPU race. */
+#define PGPU_ATTENTION_STATIC_SLOTS 16384
+int pgpu_attention_static(void *stream, const float *q, const pgpu_paged_kv *kv, int layer,
+                          const int32_t *tables, int table_stride, const int32_t *positions,
+                          int streams, int heads, int max_splits, float *out,
+                          uint16_t *out_split, int *status);
 
 /* -- flow head launches (pgpu_head.hip); BF16 matrices -- */
 /* One launch of three independent parts: silu_split = split fragments of

@@ -18,9 +18,20 @@
 // prologue in the decode step, or k_attention_merge). There is no
 // cross-work-group handshake: on gfx950 an agent-scope fence writes back and
 // invalidates the whole L2 and costs far more than a separate merge.
+#include <mutex>
+
 #include "pgpu_attention.hpp"
 #include "pgpu_common.hpp"
 #include "phonon_gpu.h"
+
+// Split partials of pgpu_attention_static: a fixed device array instead of a
+// caller's pgpu_attention_scratch, so that the entry point allocates
+// nothing. Slots [0, kStaticSlots) of 64 floats (unnormalised P.V), then
+// kStaticSlots (max, sum) pairs. Every device holds its own copy until the
+// process ends; host code uses its per-device address (from
+// pgpu_attention_static_setup), never the array's name.
+constexpr int kStaticSlots = PGPU_ATTENTION_STATIC_SLOTS;
+static __device__ __align__(256) float scratch[(size_t)kStaticSlots * (64 + 2)];
 
 namespace pgpu {
 
@@ -73,14 +84,10 @@ __global__ __launch_bounds__(64) void k_attention_merge(const float *__restrict_
 
 using namespace pgpu;
 
-extern "C" int pgpu_attention(void *stream, const float *q, const pgpu_paged_kv *kv, int layer,
-                              const int32_t *tables, int table_stride, const int32_t *positions,
-                              int streams, int heads, int max_splits,
-                              const pgpu_attention_scratch *scratch, int *status) {
-    if (streams <= 0 || heads <= 0 || heads > kHeads || max_splits <= 0 || layer < 0 ||
-        layer >= kv->layers || max_splits > scratch->max_splits ||
-        streams > scratch->max_streams)
-        return bad_arguments("pgpu_attention");
+static AttnArgs attention_args(const float *q, const pgpu_paged_kv *kv, int layer,
+                               const int32_t *tables, int table_stride,
+                               const int32_t *positions, int streams, int max_splits,
+                               float *part_acc, float *part_ml, int *status) {
     AttnArgs a;
     a.q = q;
     a.kv = kv->base;
@@ -92,24 +99,101 @@ extern "C" int pgpu_attention(void *stream, const float *q, const pgpu_paged_kv 
     a.positions = positions;
     a.streams = streams;
     a.max_splits = max_splits;
-    a.part_acc = scratch->part_acc;
-    a.part_ml = scratch->part_ml;
+    a.part_acc = part_acc;
+    a.part_ml = part_ml;
     a.status = status;
+    return a;
+}
+
+extern "C" int pgpu_attention(void *stream, const float *q, const pgpu_paged_kv *kv, int layer,
+                              const int32_t *tables, int table_stride, const int32_t *positions,
+                              int streams, int heads, int max_splits,
+                              const pgpu_attention_scratch *work, int *status) {
+    if (streams <= 0 || heads <= 0 || heads > kHeads || max_splits <= 0 || layer < 0 ||
+        layer >= kv->layers || max_splits > work->max_splits || streams > work->max_streams)
+        return bad_arguments("pgpu_attention");
+    const AttnArgs a = attention_args(q, kv, layer, tables, table_stride, positions, streams,
+                                      max_splits, work->part_acc, work->part_ml, status);
     hipLaunchKernelGGL(k_attention, dim3(heads, max_splits, streams), dim3(64 * kUnitWaves), 0,
                        (hipStream_t)stream, a);
     return launch_ok("pgpu_attention");
 }
 
-extern "C" int pgpu_attention_merge(void *stream, const pgpu_attention_scratch *scratch,
+extern "C" int pgpu_attention_merge(void *stream, const pgpu_attention_scratch *work,
                                     const int32_t *positions, int streams, int heads,
                                     int max_splits, float *out, uint16_t *out_split,
                                     int *status) {
     if (streams <= 0 || heads <= 0 || heads > kHeads || max_splits <= 0 ||
-        max_splits > scratch->max_splits || streams > scratch->max_streams ||
-        (!out && !out_split))
+        max_splits > work->max_splits || streams > work->max_streams || (!out && !out_split))
         return bad_arguments("pgpu_attention_merge");
     hipLaunchKernelGGL(k_attention_merge, dim3(heads, streams), dim3(64), 0,
-                       (hipStream_t)stream, scratch->part_acc, scratch->part_ml, positions,
+                       (hipStream_t)stream, work->part_acc, work->part_ml, positions,
                        max_splits, out, out_split, status);
     return launch_ok("pgpu_attention_merge");
+}
+
+// --------------------------------------------------------------------------
+// The static partials' device address, per device. Looked up once per device
+// with that device current: by the library's init (pgpu_device_init), and by
+// an entry point's first call on any other device. hipGetSymbolAddress
+// allocates nothing.
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_static_lock;
+float *g_static_partials[kMaxDevices];
+}  // namespace
+
+extern "C" __attribute__((visibility("hidden"))) float *pgpu_attention_static_setup(void) {
+    int device = -1;
+    if (hipGetDevice(&device) != hipSuccess || device < 0 || device >= kMaxDevices) {
+        pgpu_record_error("pgpu_attention_static: no current device");
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> hold(g_static_lock);
+    if (!g_static_partials[device]) {
+        void *ptr = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !ptr) {
+            char text[256];
+            snprintf(text, sizeof(text), "pgpu_attention_static: hipGetSymbolAddress: %s",
+                     hipGetErrorString(e));
+            pgpu_record_error(text);
+            return nullptr;
+        }
+        g_static_partials[device] = (float *)ptr;
+    }
+    return g_static_partials[device];
+}
+
+extern "C" int pgpu_attention_static(void *stream, const float *q, const pgpu_paged_kv *kv,
+                                     int layer, const int32_t *tables, int table_stride,
+                                     const int32_t *positions, int streams, int heads,
+                                     int max_splits, float *out, uint16_t *out_split,
+                                     int *status) {
+    if (!q || !kv || !tables || !positions || !status || streams <= 0 || heads <= 0 ||
+        heads > kHeads || max_splits <= 0 || layer < 0 || layer >= kv->layers ||
+        (!out && !out_split))
+        return bad_arguments("pgpu_attention_static");
+    // The partial layout is [stream][8 heads][max_splits] whatever `heads` is.
+    if ((size_t)streams * kHeads * (size_t)max_splits > (size_t)kStaticSlots) {
+        char text[256];
+        snprintf(text, sizeof(text),
+                 "pgpu_attention_static: %d streams x %d heads x %d splits exceed the %d "
+                 "partial slots of the static scratch",
+                 streams, kHeads, max_splits, kStaticSlots);
+        pgpu_record_error(text);
+        return 0;
+    }
+    float *const ptr = pgpu_attention_static_setup();
+    if (!ptr) return 0;
+    float *const part_acc = ptr, *const part_ml = ptr + (size_t)kStaticSlots * 64;
+    const AttnArgs a = attention_args(q, kv, layer, tables, table_stride, positions, streams,
+                                      max_splits, part_acc, part_ml, status);
+    hipLaunchKernelGGL(k_attention, dim3(heads, max_splits, streams), dim3(64 * kUnitWaves), 0,
+                       (hipStream_t)stream, a);
+    if (!launch_ok("pgpu_attention_static")) return 0;
+    hipLaunchKernelGGL(k_attention_merge, dim3(heads, streams), dim3(64), 0,
+                       (hipStream_t)stream, part_acc, part_ml, positions, max_splits, out,
+                       out_split, status);
+    return launch_ok("pgpu_attention_static");
 }

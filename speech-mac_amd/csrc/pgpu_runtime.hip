@@ -9,6 +9,9 @@
 
 static thread_local char g_error[256];
 
+// pgpu_attention.hip: the static attention partials' per-device address.
+extern "C" float *pgpu_attention_static_setup(void);
+
 static int check(hipError_t e, const char *what) {
     if (e == hipSuccess) return 1;
     snprintf(g_error, sizeof(g_error), "%s: %s", what, hipGetErrorString(e));
@@ -39,6 +42,9 @@ extern "C" int pgpu_device_init(void) {
         snprintf(g_error, sizeof(g_error), "device %s is not gfx950", prop.gcnArchName);
         return 0;
     }
+    // The device address of pgpu_attention_static's partials, looked up here
+    // once with the device current.
+    if (!pgpu_attention_static_setup()) return 0;
     initialized = 1;
     return 1;
 }
