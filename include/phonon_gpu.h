@@ -239,6 +239,21 @@ int pgpu_attention(void *stream, const float *q, const pgpu_paged_kv *kv, int la
 int pgpu_attention_merge(void *stream, const pgpu_attention_scratch *scratch,
                          const int32_t *positions, int streams, int heads, int max_splits,
                          float *out, uint16_t *out_split, int *status);
+/* Causal attention of a batched prefill, into the partial layout of
+ * pgpu_attention. `entries` (dev) holds entry_count work entries of four
+ * int32 (s0, s1, split, unused): streams s0 .. s1-1 (at most 64, all
+ * < streams) are consecutive positions of one stream and share the block
+ * table row of s0; one work-group per (head, entry) loads keys
+ * [256 split, 256 split + 256) of that row once (up to the context of the
+ * entry's latest position) and writes split `split`'s partial of every one
+ * of those streams whose context reaches it, with pgpu_attention's
+ * arithmetic (the same bits). Every split of every stream must be covered by
+ * one entry; split < max_splits. */
+int pgpu_prefill_attention(void *stream, const float *q, const pgpu_paged_kv *kv, int layer,
+                           const int32_t *tables, int table_stride, const int32_t *positions,
+                           int streams, int heads, int max_splits, const int32_t *entries,
+                           int entry_count, const pgpu_attention_scratch *scratch,
+                           int *status);
 /* pgpu_attention followed by pgpu_attention_merge (the same kernels, the
  * same bits), with the split partials in a fixed device-resident array of
  * PGPU_ATTENTION_STATIC_SLOTS (stream, head, split) slots (4.3 MB, held by

@@ -209,6 +209,8 @@ EXPORTS = {
     "pgpu_gemm_qkv": (_i, [_vp, _mp, _gip, _i, _kvp, _i, _vp, _i, _vp, _vp, _vp, _vp]),
     "pgpu_attention": (_i, [_vp, _vp, _kvp, _i, _vp, _i, _vp, _i, _i, _i, _scp, _vp]),
     "pgpu_attention_merge": (_i, [_vp, _scp, _vp, _i, _i, _i, _vp, _vp, _vp]),
+    "pgpu_prefill_attention": (_i, [_vp, _vp, _kvp, _i, _vp, _i, _vp, _i, _i, _i, _vp, _i,
+                                    _scp, _vp]),
     "pgpu_attention_static": (_i, [_vp, _vp, _kvp, _i, _vp, _i, _vp, _i, _i, _i, _vp, _vp,
                                    _vp]),
     "pgpu_ln_split": (_i, [_vp, _vp, _i, _vp, _vp, _f, _vp, _vp, _vp]),

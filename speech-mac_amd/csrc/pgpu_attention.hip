@@ -80,6 +80,173 @@ __global__ __launch_bounds__(64) void k_attention_merge(const float *__restrict_
     flag_nonfinite(status, bad);
 }
 
+// Causal attention of a batched prefill. A work entry (s0, s1, split) names
+// consecutive positions of one stream: pseudo-streams s0 .. s1-1 (at most
+// kPrefillQueries), which share that stream's block table row. One
+// work-group per (head, entry) loads the split's K/V tile once, the 8 waves
+// x 2 blocks of a split unit, into registers (up to the context of the
+// entry's last query), then walks the queries: for each query whose context
+// reaches the split it computes the split's partial with exactly the
+// arithmetic of attend_unit (same key order, masking, row sums, exp,
+// fused multiply-adds and wave merge), so a prefill gives the bits of
+// decoding the same positions one step at a time. A stream's K/V are read
+// once per entry instead of once per position.
+constexpr int kPrefillQueries = 64;  // queries per entry (host-enforced)
+constexpr int kPrefillBatch = 8;     // queries whose wave partials share one LDS round
+
+__global__ __launch_bounds__(64 * kUnitWaves) void k_prefill_attention(AttnArgs a,
+                                                                       const int4 *entries) {
+    __shared__ AttnShared sh[kPrefillBatch];
+    const int head = blockIdx.x;
+    const int4 e = entries[blockIdx.y];
+    // An entry outside the streams or the partial layout is an error: the
+    // work-group writes nothing (the host builds valid entries).
+    if (e.x < 0 || e.y > a.streams || e.y <= e.x || e.y - e.x > kPrefillQueries || e.z < 0 ||
+        e.z >= a.max_splits) {
+        if (threadIdx.x == 0) atomicOr(a.status, 2);
+        return;
+    }
+    const int s0 = e.x, nq = e.y - e.x, split = e.z;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63, krow = lane >> 4, dcol = lane & 15;
+    // Lane i holds the position of query s0 + i; the tile is loaded up to
+    // the context of the entry's latest query.
+    const int my_pos = lane < nq ? a.positions[s0 + lane] : -1;
+    int top = my_pos;
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) top = max(top, __shfl_xor(top, o));
+    const int32_t *__restrict__ table = a.tables + (size_t)s0 * a.table_stride;
+    const int top_blocks = min((top + kBlockPos) / kBlockPos, a.table_stride);
+    const float *layer_kv = a.kv + (size_t)a.layer * a.layer_stride;
+    bool bad_block = false;
+    float4 kr[kBlocksPerWave][4], vr[kBlocksPerWave][4];
+#pragma unroll
+    for (int t = 0; t < kBlocksPerWave; t++) {
+        const int b = split * 16 + wave * kBlocksPerWave + t;
+        if (b < top_blocks) {  // uniform
+            const int raw = table[b];
+            bad_block |= (unsigned)raw >= a.blocks;
+            const int id = (unsigned)raw < a.blocks ? raw : 0;
+            const float *tile = layer_kv + ((size_t)id * kHeads + head) * 2048 + lane * 4;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                kr[t][i] = stream_load(tile + i * 256);
+                vr[t][i] = stream_load(tile + 1024 + i * 256);
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                kr[t][i] = make_float4(0.f, 0.f, 0.f, 0.f);
+                vr[t][i] = make_float4(0.f, 0.f, 0.f, 0.f);
+            }
+        }
+    }
+    if (bad_block && lane == 0) atomicOr(a.status, 2);
+
+    for (int q0 = 0; q0 < nq; q0 += kPrefillBatch) {
+        const int nb = min(kPrefillBatch, nq - q0);
+        // This batch's q rows, requested together.
+        float4 qv[kPrefillBatch];
+#pragma unroll
+        for (int u = 0; u < kPrefillBatch; u++) {
+            const int s = s0 + q0 + min(u, nb - 1);
+            qv[u] = *(const float4 *)(a.q + (size_t)s * kWidth + head * kHeadDim + dcol * 4);
+        }
+#pragma unroll
+        for (int u = 0; u < kPrefillBatch; u++) {
+            if (u >= nb) break;
+            const int count = __shfl(my_pos, q0 + u) + 1;  // uniform
+            const int nsplit = (count + kSplitKeys - 1) / kSplitKeys;
+            const bool covered =
+                count >= 1 && nsplit <= a.max_splits && count <= a.table_stride * kBlockPos;
+            if (!covered && split == 0 && wave == 0 && lane == 0) atomicOr(a.status, 2);
+            if (!(covered && split * kSplitKeys < count)) continue;  // uniform
+            const int first_block = split * 16 + wave * kBlocksPerWave;
+            const float4 q = qv[u];
+            float m = -INFINITY, l = 0.0f;
+            float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+            float score[kBlocksPerWave][4];
+#pragma unroll
+            for (int t = 0; t < kBlocksPerWave; t++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const float4 k = kr[t][i];
+                    float d = q.x * k.x;
+                    d = fmaf(q.y, k.y, d);
+                    d = fmaf(q.z, k.z, d);
+                    d = fmaf(q.w, k.w, d);
+                    d = row16_sum(d);
+                    const int key = (first_block + t) * kBlockPos + i * 4 + krow;
+                    score[t][i] = key < count ? d : -INFINITY;
+                    m = fmaxf(m, score[t][i]);
+                }
+            m = fmaxf(m, __shfl_xor(m, 16));
+            m = fmaxf(m, __shfl_xor(m, 32));
+#pragma unroll
+            for (int t = 0; t < kBlocksPerWave; t++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    if (score[t][i] == -INFINITY) continue;
+                    const float ex = expf(score[t][i] - m);
+                    l += ex;
+                    acc.x = fmaf(ex, vr[t][i].x, acc.x);
+                    acc.y = fmaf(ex, vr[t][i].y, acc.y);
+                    acc.z = fmaf(ex, vr[t][i].z, acc.z);
+                    acc.w = fmaf(ex, vr[t][i].w, acc.w);
+                }
+            l += __shfl_xor(l, 16);
+            l += __shfl_xor(l, 32);
+            acc.x += __shfl_xor(acc.x, 16);
+            acc.y += __shfl_xor(acc.y, 16);
+            acc.z += __shfl_xor(acc.z, 16);
+            acc.w += __shfl_xor(acc.w, 16);
+            acc.x += __shfl_xor(acc.x, 32);
+            acc.y += __shfl_xor(acc.y, 32);
+            acc.z += __shfl_xor(acc.z, 32);
+            acc.w += __shfl_xor(acc.w, 32);
+            if (lane < 16) sh[u].acc[wave][lane] = acc;
+            if (lane == 0) {
+                sh[u].m[wave] = m;
+                sh[u].l[wave] = l;
+            }
+        }
+        __syncthreads();
+        // Wave w merges query q0 + w of the batch, in fixed wave order (the
+        // position is read by every lane, before the branch).
+        const int merge_pos = __shfl(my_pos, q0 + min(wave, nb - 1));
+        if (wave < nb && lane < 16) {
+            const int count = merge_pos + 1;
+            const int nsplit = (count + kSplitKeys - 1) / kSplitKeys;
+            const bool covered =
+                count >= 1 && nsplit <= a.max_splits && count <= a.table_stride * kBlockPos;
+            if (covered && split * kSplitKeys < count) {
+                const AttnShared &r = sh[wave];
+                float mx = r.m[0];
+#pragma unroll
+                for (int w = 1; w < kUnitWaves; w++) mx = fmaxf(mx, r.m[w]);
+                float total = 0.0f;
+                float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+                for (int w = 0; w < kUnitWaves; w++) {
+                    if (r.l[w] == 0.0f) continue;
+                    const float f = expf(r.m[w] - mx);
+                    total = fmaf(r.l[w], f, total);
+                    const float4 x = r.acc[w][lane];
+                    o.x = fmaf(x.x, f, o.x);
+                    o.y = fmaf(x.y, f, o.y);
+                    o.z = fmaf(x.z, f, o.z);
+                    o.w = fmaf(x.w, f, o.w);
+                }
+                const size_t slot =
+                    ((size_t)(s0 + q0 + wave) * kHeads + head) * a.max_splits + split;
+                *(float4 *)(a.part_acc + slot * 64 + lane * 4) = o;
+                if (lane == 0) *(float2 *)(a.part_ml + slot * 2) = make_float2(mx, total);
+            }
+        }
+        __syncthreads();
+    }
+}
+
 }  // namespace pgpu
 
 using namespace pgpu;
@@ -130,6 +297,23 @@ extern "C" int pgpu_attention_merge(void *stream, const pgpu_attention_scratch *
                        (hipStream_t)stream, work->part_acc, work->part_ml, positions,
                        max_splits, out, out_split, status);
     return launch_ok("pgpu_attention_merge");
+}
+
+extern "C" int pgpu_prefill_attention(void *stream, const float *q, const pgpu_paged_kv *kv,
+                                      int layer, const int32_t *tables, int table_stride,
+                                      const int32_t *positions, int streams, int heads,
+                                      int max_splits, const int32_t *entries, int entry_count,
+                                      const pgpu_attention_scratch *work, int *status) {
+    if (!q || !kv || !tables || !positions || !entries || !work || !status || streams <= 0 ||
+        heads <= 0 || heads > kHeads || max_splits <= 0 || layer < 0 || layer >= kv->layers ||
+        table_stride <= 0 || entry_count <= 0 || entry_count > 65535 ||
+        max_splits > work->max_splits || streams > work->max_streams)
+        return bad_arguments("pgpu_prefill_attention");
+    const AttnArgs a = attention_args(q, kv, layer, tables, table_stride, positions, streams,
+                                      max_splits, work->part_acc, work->part_ml, status);
+    hipLaunchKernelGGL(k_prefill_attention, dim3(heads, entry_count), dim3(64 * kUnitWaves), 0,
+                       (hipStream_t)stream, a, (const int4 *)entries);
+    return launch_ok("pgpu_prefill_attention");
 }
 
 // --------------------------------------------------------------------------

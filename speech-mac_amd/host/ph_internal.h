@@ -15,6 +15,10 @@ enum { PH_MAX_GROUPS = 4, PH_DEFAULT_GROUPS = 1 };
 /* The one-launch step keeps this many positions of headroom in its task
  * schedule (and captured graph) before it has to rebuild them. */
 enum { PH_FLOW_HEADROOM = 256 };
+/* Batched prefill attention (pgpu_prefill_attention): up to PH_PREFILL_RUN
+ * consecutive positions per work entry, fewer while the entries would give
+ * under PH_PREFILL_MIN_GROUPS work-groups (one per head per entry). */
+enum { PH_PREFILL_RUN = 64, PH_PREFILL_MIN_GROUPS = 1024 };
 /* Decode batches of this many 16-stream tiles run as one launch by default
  * (phonon_flow_batch_set_pipeline): measured faster there on MI355X (us per
  * 12-layer step, contexts U{1..2048}, one launch vs phase by phase: B = 1:

@@ -42,6 +42,12 @@ struct PhononFlowBatch {
     uint16_t *xh; /* split fragments of the MLP hidden rows */
     int32_t *positions, *tables;
     int32_t *table_src, *table_map; /* prefill staging, allocated on first use */
+    struct {
+        int active;                 /* the streams are a prefill's pseudo-streams */
+        int32_t *entries;           /* (dev) [cap][4]: work entries of pgpu_prefill_attention */
+        int32_t *host;              /* [cap][4] */
+        size_t count, cap;
+    } pre;
     int flow;                       /* 1: one launch per step (pgpu_flow_launch) */
     struct {
         size_t cap, cap_layers;     /* padded streams and layers the buffers hold */
@@ -370,6 +376,8 @@ void phonon_flow_batch_destroy(PhononFlowBatch *b) {
     for (size_t i = 0; i < sizeof(bufs) / sizeof(bufs[0]); i++)
         pgpu_free(bufs[i]);
     pgpu_stream_destroy(b->stream);
+    pgpu_free(b->pre.entries);
+    free(b->pre.host);
     free(b->host_positions);
     free(b->fl.host_schedule);
     free(b->fl.cover);
@@ -464,6 +472,7 @@ int phonon_flow_batch_set_streams(PhononFlowBatch *b, size_t streams, const size
         return 0;
     memcpy(b->host_positions, positions, streams * sizeof(size_t));
     b->streams = streams;
+    b->pre.active = 0;
     return 1;
 }
 
@@ -484,6 +493,7 @@ int ph_batch_set_single(PhononFlowBatch *b, size_t position, const int32_t *tabl
         return 0;
     b->host_positions[0] = position;
     b->streams = 1;
+    b->pre.active = 0;
     return 1;
 }
 
@@ -532,9 +542,14 @@ static int enqueue_group(PhononFlowBatch *b, void *stream, size_t s0, size_t n, 
         const pgpu_gemm_input hidden = {.split = xh};
         if (!pgpu_gemm_qkv(stream, &m->qkv[l], &ln1, (int)n, &b->pool->kv, pool_layer, tables,
                            (int)b->table_len, positions, rope, q, b->status) ||
-            !pgpu_attention(stream, q, &b->pool->kv, pool_layer, tables, (int)b->table_len,
-                            positions, (int)n, PH_HEADS, (int)b->splits, &scratch,
-                            b->status) ||
+            !(b->pre.active
+                  ? pgpu_prefill_attention(stream, q, &b->pool->kv, pool_layer, tables,
+                                           (int)b->table_len, positions, (int)n, PH_HEADS,
+                                           (int)b->splits, b->pre.entries, (int)b->pre.count,
+                                           &scratch, b->status)
+                  : pgpu_attention(stream, q, &b->pool->kv, pool_layer, tables,
+                                   (int)b->table_len, positions, (int)n, PH_HEADS,
+                                   (int)b->splits, &scratch, b->status)) ||
             !pgpu_gemm_residual(stream, &m->out[l], &att, (int)n, cur, r, b->status) ||
             !pgpu_gemm_gelu_split(stream, &m->mlp_in[l], &ln2, (int)n, xh, b->status) ||
             !pgpu_gemm_residual(stream, &m->mlp_out[l], &hidden, (int)n, r, next, b->status))
@@ -559,7 +574,9 @@ int ph_batch_enqueue_layers(PhononFlowBatch *b, size_t first, size_t count, size
  * Returns the group count actually used (a group holds >= 1 tile). */
 static size_t group_bounds(const PhononFlowBatch *b, size_t *first, size_t *count) {
     const size_t tiles = (b->streams + 15) / 16;
-    const size_t groups = b->groups < tiles ? b->groups : tiles;
+    /* A prefill's attention work list spans all its pseudo-streams: one group. */
+    const size_t want = b->pre.active ? 1 : b->groups;
+    const size_t groups = want < tiles ? want : tiles;
     for (size_t g = 0; g < groups; g++) {
         const size_t t0 = tiles * g / groups, t1 = tiles * (g + 1) / groups;
         first[g] = t0 * 16;
@@ -772,6 +789,65 @@ static int enqueue_flow(PhononFlowBatch *b, const float *input, float *output, f
            pgpu_flow_finish(b->stream, b->fl.counters, used, b->positions, (int)b->streams);
 }
 
+/* Work entries of the prefill attention (pgpu_prefill_attention): for each
+ * stream i (pseudo-streams from its offset on) and each 256-key split j of
+ * its context, its positions that reach split j, in runs of `run`
+ * consecutive positions. Returns the entry count; writes them when `out`
+ * holds that many. */
+static size_t entry_list(size_t streams, const size_t *first, const size_t *counts, size_t run,
+                         int32_t *out, size_t cap) {
+    size_t n = 0, offset = 0;
+    for (size_t i = 0; i < streams; i++) {
+        const size_t last = first[i] + counts[i] - 1;
+        for (size_t j = 0; j <= last / PH_SPLIT_KEYS; j++) {
+            const size_t start = j * PH_SPLIT_KEYS;
+            const size_t k0 = start > first[i] ? start - first[i] : 0;
+            for (size_t k = k0; k < counts[i]; k += run, n++) {
+                if (n < cap) {
+                    const size_t k1 = k + run < counts[i] ? k + run : counts[i];
+                    out[4 * n] = (int32_t)(offset + k);
+                    out[4 * n + 1] = (int32_t)(offset + k1);
+                    out[4 * n + 2] = (int32_t)j;
+                    out[4 * n + 3] = 0;
+                }
+            }
+        }
+        offset += counts[i];
+    }
+    return n;
+}
+
+/* The prefill attention's work list, uploaded: positions per entry halved
+ * from PH_PREFILL_RUN while the list would give fewer than
+ * PH_PREFILL_MIN_GROUPS work-groups (8 per entry), so a short prompt still
+ * spreads over the GPU. */
+static int prefill_entries(PhononFlowBatch *b, size_t streams, const size_t *first,
+                           const size_t *counts) {
+    size_t run = PH_PREFILL_RUN;
+    size_t n = entry_list(streams, first, counts, run, NULL, 0);
+    while (run > 8 && n * PH_HEADS < PH_PREFILL_MIN_GROUPS) {
+        run /= 2;
+        n = entry_list(streams, first, counts, run, NULL, 0);
+    }
+    if (!n || n > 65535)
+        return ph_fail("prefill: attention work list size out of range");
+    if (n > b->pre.cap) {
+        int32_t *host = realloc(b->pre.host, n * 4 * sizeof(int32_t));
+        if (!host)
+            return 0;
+        b->pre.host = host;
+        pgpu_free(b->pre.entries);
+        b->pre.entries = pgpu_malloc(n * 4 * sizeof(int32_t));
+        b->pre.cap = b->pre.entries ? n : 0;
+        if (!b->pre.entries)
+            return 0;
+    }
+    if (entry_list(streams, first, counts, run, b->pre.host, b->pre.cap) != n)
+        return 0;
+    b->pre.count = n;
+    return pgpu_copy_h2d(b->stream, b->pre.entries, b->pre.host, n * 4 * sizeof(int32_t));
+}
+
 /* Pseudo-streams of a batched prefill: position first[i] + k (k < counts[i])
  * of stream i becomes its own stream with block-table row i of tables_dev
  * (device, [streams][table_len]). A step then runs every such position
@@ -803,11 +879,14 @@ int ph_batch_set_prefill(PhononFlowBatch *b, size_t streams, const size_t *first
          pgpu_copy_h2d(b->stream, b->positions, pos32, total * sizeof(int32_t)) &&
          pgpu_copy_h2d(b->stream, b->table_map, map, total * sizeof(int32_t)) &&
          pgpu_gather_rows(b->stream, b->tables, tables_dev, b->table_map, (int)total,
-                          (int)b->table_len);
+                          (int)b->table_len) &&
+         prefill_entries(b, streams, first, counts);
     free(pos32);
     free(map);
-    if (ok)
+    if (ok) {
         b->streams = total;
+        b->pre.active = 1;
+    }
     return ok;
 }
 
