@@ -2,17 +2,14 @@
  * src/phonon_transformer.h (src/phonon_transformer.h:1-103). Same types, same
  * signatures, same 1 = success / 0 = failure convention. Every numerical
  * function runs on the MI355X (libphonon_mi355x); host buffers are borrowed
- * and copied to and from device memory inside each call.
- *
- * Not provided here (outside the decode step): phonon_flow_condition,
- * phonon_voice_project, phonon_flow_prepare_prefix, phonon_flow_load_layers,
- * phonon_flow_embed_*, phonon_flow_normalize_latent, phonon_flow_output_norm
- * (they read a PhononPack or serve the frontend). */
+ * and copied to and from device memory inside each call. The pack-side
+ * helpers at the end (src/phonon_transformer.h:75-103) read a PhononPack. */
 #ifndef PHONON_TRANSFORMER_H
 #define PHONON_TRANSFORMER_H
 
 #include "phonon_pack.h"
 #include <stddef.h>
+#include <stdint.h>
 
 #ifdef __cplusplus
 extern "C" {
@@ -92,6 +89,35 @@ int phonon_flow_stack_prefill_cancel(const PhononFlowLayerWeights weights[PHONON
 int phonon_flow_stack_prefill(const PhononFlowLayerWeights weights[PHONON_FLOW_LAYERS],
                               PhononKvCache *cache, const float *input, size_t length, float theta,
                               float output[512]);
+
+/* Pack-side helpers, src/phonon_transformer.h:75-103
+ * (src/phonon_transformer.c:711-914): voice projection, speaker/duration
+ * conditioning, prefix rows, the nine layers' views by checkpoint name,
+ * token / BOS / latent embedding into a step input, latent normalization
+ * and the decoder's output LayerNorm. */
+int phonon_voice_project(const float *voice_latents, size_t frames,
+                         const PhononTensorView *projection, float *projected);
+int phonon_flow_condition(const PhononTensorView *speaker_embeddings,
+                          const PhononTensorView *speaker_projection,
+                          const PhononTensorView *duration_projection, size_t speaker_count,
+                          float duration_delta, float output[PHONON_FLOW_WIDTH]);
+int phonon_flow_prepare_prefix(const int32_t *ids, size_t tokens, const float *token_embeddings,
+                               size_t prompt_id, size_t bos_id, const float *projected_voice,
+                               size_t voice_frames, const float *bos_latent_projection,
+                               float *prefix_embeddings);
+int phonon_flow_load_layers(const PhononPack *pack,
+                            PhononTensorView storage[PHONON_FLOW_LAYERS][8],
+                            PhononFlowLayerWeights weights[PHONON_FLOW_LAYERS]);
+int phonon_flow_embed_tokens(const PhononPack *pack, const int32_t *ids, size_t count,
+                             float *embeddings);
+int phonon_flow_embed_bos(const PhononPack *pack, const float condition[PHONON_FLOW_WIDTH],
+                          float output[PHONON_FLOW_WIDTH]);
+int phonon_flow_embed_latent(const PhononPack *pack, const float latent[32],
+                             const float condition[PHONON_FLOW_WIDTH],
+                             float output[PHONON_FLOW_WIDTH]);
+int phonon_flow_normalize_latent(const PhononPack *pack, const float denormalized[32],
+                                 float normalized[32]);
+int phonon_flow_output_norm(const PhononPack *pack, float values[PHONON_FLOW_WIDTH]);
 
 /* Test seam of src/phonon_transformer_test.h:8-9 (phonon_attention_test,
  * src/phonon_transformer.c:578-582): single-query attention of one head over

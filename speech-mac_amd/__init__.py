@@ -143,6 +143,26 @@ EXPORTS = {
                                               _vp]),
     "phonon_flow_stack_prefill": (_i, [_wp, _cachep, _fp, _sz, _f, _fp]),
     "phonon_attention_test": (_i, [_fp, _fp, _fp, _sz, _sz, _fp]),
+    "phonon_voice_project": (_i, [_fp, _sz, _viewp, _fp]),
+    "phonon_flow_condition": (_i, [_viewp, _viewp, _viewp, _sz, _f, _fp]),
+    "phonon_flow_prepare_prefix": (_i, [_i32p, _sz, _fp, _sz, _sz, _fp, _sz, _fp, _fp]),
+    "phonon_flow_load_layers": (_i, [_vp, _vp, _vp]),
+    "phonon_flow_embed_tokens": (_i, [_vp, _i32p, _sz, _fp]),
+    "phonon_flow_embed_bos": (_i, [_vp, _fp, _fp]),
+    "phonon_flow_embed_latent": (_i, [_vp, _fp, _fp, _fp]),
+    "phonon_flow_normalize_latent": (_i, [_vp, _fp, _fp]),
+    "phonon_flow_output_norm": (_i, [_vp, _fp]),
+    # phonon_pack.h
+    "phonon_pack_open": (_i, [ctypes.c_char_p, _pp]),
+    "phonon_pack_open_for_tests": (_i, [ctypes.c_char_p, _pp]),
+    "phonon_pack_close": (None, [_vp]),
+    "phonon_pack_prepare_linears": (_i, [_vp]),
+    "phonon_pack_prepare_linears_for_tests": (_i, [_vp, _sz]),
+    "phonon_tensor_expand_linear": (_i, [_viewp, ctypes.POINTER(_fp)]),
+    "phonon_pack_tensor_count": (_sz, [_vp]),
+    "phonon_pack_tensor": (_i, [_vp, ctypes.c_char_p, _viewp]),
+    "phonon_pack_tensor_at": (_i, [_vp, _sz, ctypes.POINTER(ctypes.c_char_p), _szp, _viewp]),
+    "phonon_bf16_to_float": (_i, [_vp, _sz, _fp]),
     # phonon_flow_batch.h
     "phonon_flow_model_create": (_i, [_wp, _sz, _pp]),
     "phonon_flow_model_destroy": (None, [_vp]),

@@ -228,3 +228,48 @@ def f64_layer(w, x, keys, values, pos, theta=10000.0):
     m = f["mlp_in"] @ ln(r, f["norm2_weight"], f["norm2_bias"])
     m = 0.5 * m * (1 + erf(m / np.sqrt(2)))
     return r + f["mlp_out"] @ m
+
+
+# ------------------------------------------------------------ kpack v1 files
+KPACK_SOURCE = "f6acc8f43cb296be31341b4428a6f01b6402659cd0039b624c4aea224936cf95"
+KPACK_CONFIG = "3e89e90b9e7ae5a74c6b4e694960c37fd2ec85906d84adfcc1440c64307aa4f1"
+KPACK_Q8, KPACK_BF16 = 1, 2
+
+
+def kpack_bytes(tensors) -> bytes:
+    """A kpack v1 file image (the layout src/phonon_pack.c:87-290 reads):
+    `tensors` is a list of (name, dtype, shape, payload bytes). Payload
+    ranges are 8-byte aligned; the metadata is padded with spaces so the
+    payload starts 8-byte aligned; digests are SHA-256 (hashlib)."""
+    import hashlib
+    import struct
+    index, payload = bytearray(), bytearray()
+    for name, dtype, shape, data in tensors:
+        payload += b"\0" * (-len(payload) % 8)
+        nb = name.encode()
+        index += struct.pack("<HBB", len(nb), dtype, len(shape))
+        index += b"".join(struct.pack("<Q", d) for d in shape)
+        index += struct.pack("<QQ", len(payload), len(data)) + nb
+        payload += data
+    meta = (f'{{"config_sha256":"{KPACK_CONFIG}","model":"gradium/phonon-40m-en",'
+            f'"revision":"cc738b7e4d182c2ba1bafb8062aa4846af000637","source":"model.q8.gguf",'
+            f'"source_sha256":"{KPACK_SOURCE}","tensors":209}}').encode()
+    meta += b" " * (-(192 + 4 + len(meta) + len(index)) % 8)
+    header = bytearray(192)
+    header[0:8] = b"PHNQ8P1\0"
+    header[8:32] = struct.pack("<IIQQ", 1, len(tensors), len(index), len(payload))
+    header[32:64] = bytes.fromhex(KPACK_SOURCE)
+    header[64:96] = bytes.fromhex(KPACK_CONFIG)
+    header[96:128] = hashlib.sha256(bytes(index)).digest()
+    header[128:160] = hashlib.sha256(bytes(payload)).digest()
+    header[160:192] = hashlib.sha256(meta).digest()
+    return bytes(header) + struct.pack("<I", len(meta)) + meta + bytes(index) + bytes(payload)
+
+
+def kpack_synthetic():
+    """The reference's synthetic pack (tests/test_phonon_pack.c:56-133): 36
+    Q8_0 [1, 32] tensors of 32 ones at scale 1.0 (fp16 0x3c00), then 173 BF16
+    [1] tensors holding 1.0."""
+    q8 = b"\x00\x3c" + b"\x01" * 32
+    return [(f"flow_lm.fixture_{i:03d}.weight", KPACK_Q8, (1, 32), q8) if i < 36 else
+            (f"mimi.fixture_{i:03d}.weight", KPACK_BF16, (1,), b"\x80\x3f") for i in range(209)]
