@@ -424,12 +424,13 @@ def large_batch_with_prefill(pkg, lib, seed, layers=12, streams=256, new_streams
             "clean": clean}
 
 
-def b1_with_prefill(pkg, lib, layers, seed, prompt=256, frames=750, warmup=10):
+def b1_with_prefill(pkg, lib, layers, seed, prompt=256, frames=750, warmup=10, mode=None):
     """B=1: one stream, `layers` layers. A `prompt`-position prefill (the
     batched causal prefill, positions 0..prompt-1 through every layer in one
     pass), then `frames` decode steps, each step's output fed back as the
     next input. Run once untimed (prefill + `warmup` steps), then again from
-    position 0: prefill and decode timed separately with HIP events."""
+    position 0: prefill and decode timed separately with HIP events. `mode`:
+    the step's pipeline mode (None: the library's default)."""
     import speech_mac_amd.synthetic as syn
     max_pos = prompt + frames + 16
     table_len = (max_pos + 15) // 16
@@ -443,6 +444,8 @@ def b1_with_prefill(pkg, lib, layers, seed, prompt=256, frames=750, warmup=10):
     assert lib.phonon_kv_pool_alloc(pool, blocks, ids.ctypes.data_as(P_I32))
     table = np.ascontiguousarray(np.random.default_rng(seed + 60).permutation(ids)[:table_len])
     assert lib.phonon_flow_batch_create(model, pool, prompt, max_pos, ctypes.byref(batch))
+    if mode is not None:
+        assert lib.phonon_flow_batch_set_pipeline(batch, mode)
     stream = lib.phonon_flow_batch_stream(batch)
     rng = np.random.default_rng(seed + 61)
     pin = pkg.DeviceBuffer(lib, prompt * 512 * 4)
@@ -490,8 +493,9 @@ def b1_with_prefill(pkg, lib, layers, seed, prompt=256, frames=750, warmup=10):
             "prefill_tokens_per_s": round(prompt / (pre_ms * 1e-3), 1),
             "workload": f"B=1, {layers} layers: a {prompt}-position prompt through the batched "
                         f"prefill, then {frames} decode frames (contexts {prompt + 1}.."
-                        f"{prompt + frames}), each output fed back as the next input; the "
-                        f"library's default step mode",
+                        f"{prompt + frames}), each output fed back as the next input; "
+                        + ("the library's default step mode" if mode is None
+                           else f"step pipeline mode {mode}"),
             "clean": clean}
 
 
@@ -868,6 +872,9 @@ def main():
     ap.add_argument("--pmc-program", action="store_true",
                     help="run only the attention kernel and a calibration copy, for "
                          "rocprofv3 --pmc passes")
+    ap.add_argument("--b1-modes", type=str, default="",
+                    help="run only the B=1 prefill + decode workload, once per listed step "
+                         "pipeline mode (comma-separated, e.g. 0,2)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU: streams are independent and "
@@ -885,6 +892,11 @@ def main():
         return
     if args.large_batch:
         print(json.dumps(large_batch_with_prefill(pkg, lib, args.seed)), flush=True)
+        return
+    if args.b1_modes:
+        for mode in (int(m) for m in args.b1_modes.split(",")):
+            print(json.dumps(dict(b1_with_prefill(pkg, lib, args.layers, args.seed, mode=mode),
+                                  mode=mode)), flush=True)
         return
     if args.flow_head:
         for shared, graph in ((True, 1), (True, 0), (False, 1)):

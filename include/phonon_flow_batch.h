@@ -98,6 +98,12 @@ int phonon_flow_batch_prefill_device(PhononFlowBatch *batch, size_t streams, con
                                      const size_t *counts, const int32_t *tables,
                                      size_t table_len, const float *inputs, float theta,
                                      float *outputs);
+/* Attention arithmetic of phase-by-phase batched prefills: 0 (default) a
+ * causal kernel with one lane per query that reads each key block once per
+ * 64 positions (fp32, within 1e-4 of the decode step); 1 the decode step's
+ * split attention and merge, so every output row has the bits of single
+ * steps. The projections give the bits of single steps either way. */
+int phonon_flow_batch_set_prefill_exact(PhononFlowBatch *batch, int exact);
 /* Runs the streams as `groups` (1..4) independent groups of whole 16-stream
  * tiles, each on its own HIP stream inside the step's graph. Results do not
  * depend on it. Default 1: on MI355X under ROCm 7 kernels of different HIP

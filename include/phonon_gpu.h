@@ -254,6 +254,56 @@ int pgpu_prefill_attention(void *stream, const float *q, const pgpu_paged_kv *kv
                            int streams, int heads, int max_splits, const int32_t *entries,
                            int entry_count, const pgpu_attention_scratch *scratch,
                            int *status);
+/* -- batched prefill (pgpu_prefill.hip). M = streams pseudo-streams (one per
+ * prompt position); split fragments as in pgpu_gemm_input.split, with M
+ * rounded up to 16 rows in the allocation. -- */
+/* LayerNorm of rows [M][512] (weight, bias, epsilon), into split fragments:
+ * the decode step's LayerNorm prologue, the same bits. */
+int pgpu_rows_split_ln(void *stream, const float *rows, const float *weight, const float *bias,
+                       float epsilon, int streams, uint16_t *out_split, int *status);
+/* The split partials of pgpu_attention / pgpu_prefill_attention merged into
+ * split fragments with the out-projection prologue's arithmetic (the same
+ * bits as a projection with an attn_acc input). */
+int pgpu_rows_split_attention(void *stream, const pgpu_attention_scratch *scratch,
+                              const int32_t *positions, int streams, int max_splits,
+                              uint16_t *out_split, int *status);
+/* A projection's weights for the prefill projections: bf16 MFMA fragments
+ * in the order of pgpu_matrix values, and for Q8 weights the fp32 block
+ * scales [rows/16][columns/32][16] (scales NULL: BF16 weights, no scale). */
+typedef struct {
+    size_t rows, columns;
+    const uint16_t *values;
+    const float *scales;
+} pgpu_wide_matrix;
+/* Q8 matrix -> bf16 fragments [rows*columns] and fp32 scales
+ * [rows*columns/32] (device buffers): exact conversions. */
+int pgpu_wide_from_matrix(void *stream, const pgpu_matrix *w, uint16_t *values, float *scales);
+/* Projections of M rows of split fragments (K = 512 or 2048; rows a
+ * multiple of 128), with the epilogues of pgpu_gemm_qkv, pgpu_gemm_residual
+ * and pgpu_gemm_gelu_split. Each output has the bits of the single-phase
+ * projection of the same weights (the same per-block MFMA sequence, scale
+ * order and summation chains). */
+int pgpu_prefill_gemm_qkv(void *stream, const pgpu_wide_matrix *w, const uint16_t *split,
+                          int streams, const pgpu_paged_kv *kv, int layer,
+                          const int32_t *tables, int table_stride, const int32_t *positions,
+                          const float *rope, float *q_out, int *status);
+int pgpu_prefill_gemm_residual(void *stream, const pgpu_wide_matrix *w, const uint16_t *split,
+                               int streams, const float *residual, float *out, int *status);
+int pgpu_prefill_gemm_gelu_split(void *stream, const pgpu_wide_matrix *w, const uint16_t *split,
+                                 int streams, uint16_t *out_split, int *status);
+/* Causal attention of a batched prefill, one lane per query, into split
+ * fragments of the attention rows (fp32 arithmetic in its own summation
+ * order). `runs` (dev) holds run_count pairs (s0, n): pseudo-streams
+ * s0 .. s0+n-1 (1 <= n <= PGPU_PREFILL_RUN, all < streams) are consecutive
+ * positions of one stream and share the block table row of s0; every
+ * pseudo-stream must be in exactly one run. q as written by the QKV
+ * projection (scaled by 1/8). Keys [0, position] of each run's stream must
+ * be in the pool. */
+#define PGPU_PREFILL_RUN 64
+int pgpu_prefill_attention_rows(void *stream, const float *q, const pgpu_paged_kv *kv,
+                                int layer, const int32_t *tables, int table_stride,
+                                const int32_t *positions, int streams, const int32_t *runs,
+                                int run_count, uint16_t *out_split, int *status);
 /* pgpu_attention followed by pgpu_attention_merge (the same kernels, the
  * same bits), with the split partials in a fixed device-resident array of
  * PGPU_ATTENTION_STATIC_SLOTS (stream, head, split) slots (4.3 MB, held by

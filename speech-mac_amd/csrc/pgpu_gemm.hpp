@@ -74,6 +74,7 @@ struct GemmArgs {
     int max_splits;
     const void *w;            // weight fragments
     const uint16_t *wscale;   // Q8 only
+    const float *wscale_f;    // prefill projections: fp32 scales of bf16 fragments, or null
     int n_rows, k_cols, streams;
     float *out;               // STORE / RESIDUAL: [streams][ld_out]
     int ld_out;
@@ -98,6 +99,7 @@ struct GemmArgs {
     const float *mod;         // SRC_LN_MOD: shift row at mod + s * ld_mod, scale at +512
     int ld_mod;
     bool plain_rows;          // single-phase launch: ln_x rows are used as they are
+    bool plain_qkv;           // QKV: q and K/V stored plainly (read only by later launches)
 };
 
 // ---------------------------------------------------------------------------
@@ -239,13 +241,12 @@ __device__ inline void rows_load(Rows2 &r, const float *x, int streams, int st) 
     }
 }
 
-// LayerNorm of the loaded rows into the LDS operand buffer: two-pass fp32
-// moments per stream (one wave), then y = ((x - mean) * rstd) * w + b
-// unfused, as the reference writes it (src/phonon_transformer.c:179-183).
-// Returns true if a live output is not finite.
-__device__ inline bool rows_ln(Rows2 &r, const float *lw, const float *lb, float eps,
-                               uint16_t *bsh) {
-    const int wave = threadIdx.x >> 6, j = threadIdx.x & 63;
+// LayerNorm of the loaded rows, in place: two-pass fp32 moments per stream
+// (one wave), then y = ((x - mean) * rstd) * w + b unfused, as the
+// reference writes it (src/phonon_transformer.c:179-183); rows past the
+// streams become zeros. Returns true if a live output is not finite.
+__device__ inline bool rows_ln_values(Rows2 &r, const float *lw, const float *lb, float eps) {
+    const int j = threadIdx.x & 63;
     const float4 w0 = *(const float4 *)(lw + j * 8), w1 = *(const float4 *)(lw + j * 8 + 4);
     const float4 b0 = *(const float4 *)(lb + j * 8), b1 = *(const float4 *)(lb + j * 8 + 4);
     const float ws[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
@@ -273,8 +274,17 @@ __device__ inline bool rows_ln(Rows2 &r, const float *lw, const float *lb, float
             if (!r.live[i]) u[k] = 0.0f;
         }
         bad |= bad_i && r.live[i];
-        lds_store8(bsh, 2 * wave + i, j >> 2, j & 3, u);
     }
+    return bad;
+}
+
+// rows_ln_values, then into the LDS operand buffer.
+__device__ inline bool rows_ln(Rows2 &r, const float *lw, const float *lb, float eps,
+                               uint16_t *bsh) {
+    const int wave = threadIdx.x >> 6, j = threadIdx.x & 63;
+    const bool bad = rows_ln_values(r, lw, lb, eps);
+#pragma unroll
+    for (int i = 0; i < 2; i++) lds_store8(bsh, 2 * wave + i, j >> 2, j & 3, r.v[i]);
     return bad;
 }
 
@@ -668,13 +678,14 @@ __device__ inline bool epilogue(const GemmArgs &a, const EpiOperands &e, const f
             if (part == 0) {
                 // The 1/sqrt(64) score scale is a power of two: folding it
                 // into q is exact.
-                store_wt(a.q_out + (size_t)s * kWidth + rr,
-                         make_float4(o[0] * 0.125f, o[1] * 0.125f, o[2] * 0.125f, o[3] * 0.125f));
+                store_out(a.q_out + (size_t)s * kWidth + rr,
+                          make_float4(o[0] * 0.125f, o[1] * 0.125f, o[2] * 0.125f, o[3] * 0.125f),
+                          !a.plain_qkv);
             } else if (ok) {
                 float *dst = a.kv + (size_t)a.layer * a.layer_stride +
                              ((size_t)block * kHeads + head) * 2048 + (part - 1) * 1024 +
                              (pos & 15) * 64 + d0;
-                store_wt(dst, make_float4(o[0], o[1], o[2], o[3]));
+                store_out(dst, make_float4(o[0], o[1], o[2], o[3]), !a.plain_qkv);
             }
         }
     }

@@ -1,0 +1,635 @@
+// Batched causal prefill: every position of a prompt (or of several
+// streams' prompts) through one layer at once, as large-M projections and a
+// causal attention that reads each key block once per 64 queries
+// (src/phonon_transformer.c:578-702, phonon_flow_stack_prefill, whose
+// prefill_attention at :493-576 tiles queries against 512-key blocks).
+//
+// A layer is seven launches over the M pseudo-streams (one per position):
+//   rows -> split   LayerNorm of the layer input into split fragments
+//   QKV             projection, RoPE, q rows and the K/V append (pool)
+//   attention       causal softmax(q K^T) V of every position, written as
+//                   split fragments (or, exact mode, the decode step's split
+//                   partials merged by the rows -> split pass)
+//   OUT             projection + residual
+//   rows -> split   LayerNorm of r
+//   MLP_IN          projection + GELU, split fragments
+//   MLP_OUT         projection + residual
+//
+// Projections. A work-group computes (8 R row tiles) x (P position tiles)
+// of 16 x 16: wave w owns row tiles R w .. R w + R - 1 of the group and all
+// P position tiles, whose split fragments (three bf16 terms per value) are
+// staged in LDS one 32-column block at a time and read by all 8 waves. Each
+// weight block is converted once and used for P position tiles. The
+// arithmetic of every output is that of the decode step's tasks
+// (pgpu_gemm.hpp): per 32-column block three MFMAs from zero and
+// acc = fma(scale, c, acc) (Q8) or the MFMAs chained into acc (BF16), over
+// chains of 8 blocks, and the chains summed in order (K = 512: the two
+// halves of gemm_wide_task; K = 2048: the 8 wave ranges of gemm_split_task).
+// So a prefill's projections give the bits of single steps.
+//
+// Attention (fast). One lane per query: a work-group of 4 waves takes 64
+// consecutive positions of one stream and one head; wave w takes the key
+// blocks b = w mod 4 of keys [0, last query], stages each block's K and V
+// (16 keys x 64 x 2 fp32) in its LDS area, and keeps an online softmax
+// (running max, sum and 64 accumulators) per lane in fp32. Keys past a
+// lane's own position are skipped, never multiplied by a zero weight (pool
+// slots past the context hold whatever they held). The four waves' states
+// are merged in wave order through LDS, normalised and written as split
+// fragments for the OUT projection. Its arithmetic differs from the decode
+// step's in summation order only (fp32 throughout).
+#include "pgpu_attention.hpp"
+#include "pgpu_gemm.hpp"
+#include "phonon_gpu.h"
+
+namespace pgpu {
+namespace {
+
+// ---------------------------------------------------------------------------
+// Rows -> split fragments: 16 rows per 512-thread work-group, through the
+// decode step's own prologues (rows_ln: LayerNorm; prologue_attn: merge of
+// the split-attention partials), then the LDS operand buffer is copied out
+// in the global split layout (split_index, 16 column blocks).
+template <int SRC>
+__global__ __launch_bounds__(kTaskThreads) void k_rows_split(GemmArgs a, uint16_t *out) {
+    __shared__ uint4 bsh4[kTaskLds / 8];
+    uint16_t *bsh = (uint16_t *)bsh4;
+    const int st = blockIdx.x;
+    bool bad;
+    if constexpr (SRC == SRC_ATTN) {
+        bad = prologue_attn(a, st, bsh);
+    } else {
+        Rows2 r;
+        rows_load(r, a.ln_x, a.streams, st);
+        bad = rows_ln(r, a.ln_w, a.ln_b, a.ln_eps, bsh);
+    }
+    flag_nonfinite(a.status, bad);
+    __syncthreads();
+    constexpr int per_block = 1536 / 8, total = (kWidth / 32) * per_block;
+    uint4 *dst = (uint4 *)(out + (size_t)st * (kWidth / 32) * 1536);
+#pragma unroll
+    for (int i0 = 0; i0 < total; i0 += kTaskThreads) {
+        const int i = i0 + threadIdx.x;
+        dst[i] = *(const uint4 *)(bsh + (i / per_block) * kLdsBlock + (i % per_block) * 8);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Large-M projection. A work-group computes RT = WR RW row tiles x PT = WP PW
+// position tiles; wave (wr, wp) = (w / WP, w % WP) owns RW row tiles and PW
+// position tiles of them. Every 32-column block's operands - the PT
+// position tiles' split fragments (3 KB each), the RT row tiles' bf16 weight
+// fragments (1 KB each) and, for Q8 weights, their fp32 row scales - are
+// copied straight from global memory into one of NB LDS stages (LDS-DMA
+// loads, 1 KB per wave instruction) NB - 1 blocks ahead of the MFMAs that
+// use them, so the copies' latency overlaps NB - 1 blocks of MFMAs. The
+// epilogue's operands (RoPE phases, block ids, residual rows; none is
+// written by this launch) are loaded before the first block.
+//
+// Work-groups are dealt round-robin over the 8 XCDs, each with its own L2:
+// when the position groups divide by 8, XCD x takes position groups
+// x, x + 8, ... with all their row groups in turn, so the work-groups that
+// share a position group's operand rows share an L2.
+constexpr int kChain = 8;  // column blocks per summation chain
+
+// One 16-byte LDS-DMA load per lane: global src -> LDS bytes [lds + 16 lane,
+// +16) (lds wave-uniform). Issued as inline assembly so that the compiler,
+// which cannot tell which LDS bytes such a load writes, does not drain
+// every load in flight before each LDS read; the kernel's own vmcnt waits
+// and barriers order the copies and the reads. M0 (the LDS base of the
+// copy) is set right before the load; no other code of these kernels uses
+// it (the compiler reserves M0 and does not take clobbers of it).
+__device__ inline void dma16(const void *src, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off"
+                 :
+                 : "v"(src), "s"(lds)
+                 : "memory");
+}
+
+__device__ inline uint32_t lds_address(const void *p) {
+    return __builtin_amdgcn_readfirstlane(
+        (uint32_t)(size_t)(const __attribute__((address_space(3))) void *)p);
+}
+
+// s_waitcnt vmcnt(n) (expcnt and lgkmcnt left alone); n > 31 waits for 0.
+__device__ inline void wait_vm(int n) {
+    switch (n) {
+#define PGPU_VM(k) \
+    case k: __builtin_amdgcn_s_waitcnt(((k) & 15) | (((k) >> 4) << 14) | 0x0f70); break;
+        PGPU_VM(0) PGPU_VM(1) PGPU_VM(2) PGPU_VM(3) PGPU_VM(4) PGPU_VM(5) PGPU_VM(6)
+        PGPU_VM(7) PGPU_VM(8) PGPU_VM(9) PGPU_VM(10) PGPU_VM(11) PGPU_VM(12) PGPU_VM(13)
+        PGPU_VM(14) PGPU_VM(15) PGPU_VM(16) PGPU_VM(17) PGPU_VM(18) PGPU_VM(19) PGPU_VM(20)
+        PGPU_VM(21) PGPU_VM(22) PGPU_VM(23) PGPU_VM(24) PGPU_VM(25) PGPU_VM(26) PGPU_VM(27)
+        PGPU_VM(28) PGPU_VM(29) PGPU_VM(30) PGPU_VM(31)
+#undef PGPU_VM
+    default: __builtin_amdgcn_s_waitcnt(0x0f70); break;
+    }
+}
+
+template <int EPI, bool SCALED, int WR, int WP, int RW, int PW, int NB, int KS>
+__global__ __launch_bounds__(kTaskThreads) void k_prefill_gemm(GemmArgs a, int row_groups,
+                                                               int pos_groups) {
+    static_assert(WR * WP == kTaskWaves, "8 waves");
+    static_assert(kChain % KS == 0, "a stage never straddles a chain");
+    constexpr int RT = WR * RW, PT = WP * PW;
+    constexpr int kB = PT * 1536, kA = RT * 512;            // halves per block
+    constexpr int kS = SCALED ? RT * 32 : 0;                // halves (RT x 16 floats)
+    constexpr int kBlk = kB + kA + kS;                      // halves per block
+    constexpr int kStage = KS * kBlk;                       // halves per stage
+    constexpr int kChunks = PT * 3 + RT;                    // 1 KB DMA chunks per block
+    static_assert(!SCALED || RT * 4 <= 64, "one wave instruction moves the scales");
+    __shared__ uint4 lds4[NB * kStage / 8];
+    uint16_t *lds = (uint16_t *)lds4;
+
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    const int wr = wave / WP, wp = wave % WP;
+    const int kbn = a.k_cols >> 5;
+    const int stages = kbn / KS;
+    const int last_tile = (a.streams - 1) >> 4;
+    int row_group, pos_group;
+    if (pos_groups % 8 == 0) {
+        const int xcd = blockIdx.x & 7, local = blockIdx.x >> 3;
+        pos_group = xcd + 8 * (local / row_groups);
+        row_group = local % row_groups;
+    } else {
+        pos_group = blockIdx.x / row_groups;
+        row_group = blockIdx.x % row_groups;
+    }
+    const int pt0 = pos_group * PT, rt0 = row_group * RT;
+    const uint16_t *wv = (const uint16_t *)a.w;
+    // DMA loads this wave issues per stage (the vmcnt it waits down to).
+    const int mine =
+        KS * ((kChunks - wave + kTaskWaves - 1) / kTaskWaves + (SCALED && wave == 0));
+
+    auto issue = [&](int stage) {
+        for (int kk = 0; kk < KS; kk++) {
+            const int kb = stage * KS + kk;
+            uint16_t *st = lds + (stage % NB) * kStage + kk * kBlk;
+            for (int c = wave; c < kChunks; c += kTaskWaves) {  // uniform
+                const uint16_t *src;
+                uint16_t *dst;
+                if (c < PT * 3) {
+                    const int t = c / 3, term = c % 3;
+                    const int tile = min(pt0 + t, last_tile);
+                    src = a.xs + ((size_t)tile * kbn + kb) * 1536 + term * 512;
+                    dst = st + t * 1536 + term * 512;
+                } else {
+                    const int r = c - PT * 3;
+                    src = wv + ((size_t)(rt0 + r) * kbn + kb) * 512;
+                    dst = st + kB + r * 512;
+                }
+                dma16(src + lane * 8, lds_address(dst));
+            }
+            if (SCALED && wave == 0) {
+                const uint32_t dst = lds_address(st + kB + kA);
+                if (lane < RT * 4) {
+                    const int r = lane >> 2, part = lane & 3;
+                    dma16(a.wscale_f + ((size_t)(rt0 + r) * kbn + kb) * 16 + part * 4, dst);
+                }
+            }
+        }
+    };
+
+    f32x4 acc[RW][PW], tot[RW][PW];
+#pragma unroll
+    for (int r = 0; r < RW; r++)
+#pragma unroll
+        for (int p = 0; p < PW; p++) {
+            acc[r][p] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            tot[r][p] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        }
+
+    // Epilogue operands of every tile of the wave, requested first.
+    EpiOperands ep[RW][PW];
+#pragma unroll
+    for (int r = 0; r < RW; r++)
+#pragma unroll
+        for (int p = 0; p < PW; p++) {
+            const int s = (pt0 + wp * PW + p) * 16 + (lane & 15);
+            const int row0 = (rt0 + wr * RW + r) * 16 + (lane >> 4) * 4;
+            load_epilogue_static<EPI>(ep[r][p], a, s, row0, s < a.streams);
+            load_epilogue_dynamic<EPI>(ep[r][p], a, s, row0, s < a.streams);
+        }
+
+    for (int k = 0; k < NB - 1 && k < stages; k++) issue(k);
+    for (int sg = 0; sg < stages; sg++) {
+        // Stage sg is in once at most the later stages' loads are in
+        // flight; the barrier publishes every wave's copies and frees the
+        // stage the next issue overwrites (read in the previous iteration).
+        wait_vm(min(NB - 2, stages - 1 - sg) * mine);
+        __builtin_amdgcn_s_barrier();
+        __asm__ volatile("" ::: "memory");
+        if (sg + NB - 1 < stages) issue(sg + NB - 1);
+#pragma unroll
+        for (int kk = 0; kk < KS; kk++) {
+            const int kb = sg * KS + kk;
+            const uint16_t *st = lds + (sg % NB) * kStage + kk * kBlk;
+            bf16x8 wa[RW];
+            float4 sc[RW];
+#pragma unroll
+            for (int r = 0; r < RW; r++) {
+                wa[r] = *(const bf16x8 *)(st + kB + (wr * RW + r) * 512 + lane * 8);
+                if constexpr (SCALED)
+                    sc[r] = *(const float4 *)((const float *)(st + kB + kA) + (wr * RW + r) * 16 +
+                                              (lane >> 4) * 4);
+            }
+#pragma unroll
+            for (int p = 0; p < PW; p++) {
+                const uint16_t *xb = st + (wp * PW + p) * 1536 + lane * 8;
+                const bf16x8 xh = *(const bf16x8 *)xb;
+                const bf16x8 xm = *(const bf16x8 *)(xb + 512);
+                const bf16x8 xl = *(const bf16x8 *)(xb + 1024);
+#pragma unroll
+                for (int r = 0; r < RW; r++) {
+                    if constexpr (SCALED) {
+                        f32x4 c = {0.0f, 0.0f, 0.0f, 0.0f};
+                        c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wa[r], xh, c, 0, 0, 0);
+                        c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wa[r], xm, c, 0, 0, 0);
+                        c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wa[r], xl, c, 0, 0, 0);
+                        acc[r][p][0] = fmaf(sc[r].x, c[0], acc[r][p][0]);
+                        acc[r][p][1] = fmaf(sc[r].y, c[1], acc[r][p][1]);
+                        acc[r][p][2] = fmaf(sc[r].z, c[2], acc[r][p][2]);
+                        acc[r][p][3] = fmaf(sc[r].w, c[3], acc[r][p][3]);
+                    } else {
+                        acc[r][p] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wa[r], xh, acc[r][p], 0, 0, 0);
+                        acc[r][p] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wa[r], xm, acc[r][p], 0, 0, 0);
+                        acc[r][p] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wa[r], xl, acc[r][p], 0, 0, 0);
+                    }
+                }
+            }
+            if ((kb & (kChain - 1)) == kChain - 1) {
+                // End of a chain: the chains are summed in order.
+#pragma unroll
+                for (int r = 0; r < RW; r++)
+#pragma unroll
+                    for (int p = 0; p < PW; p++) {
+#pragma unroll
+                        for (int i = 0; i < 4; i++)
+                            tot[r][p][i] = kb == kChain - 1 ? acc[r][p][i]
+                                                            : __fadd_rn(tot[r][p][i], acc[r][p][i]);
+                        acc[r][p] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+                    }
+            }
+        }
+    }
+
+    bool bad = false;
+#pragma unroll
+    for (int r = 0; r < RW; r++)
+#pragma unroll
+        for (int p = 0; p < PW; p++) {
+            const int s = (pt0 + wp * PW + p) * 16 + (lane & 15);
+            const int row0 = (rt0 + wr * RW + r) * 16 + (lane >> 4) * 4;
+            bad |= epilogue<EPI>(a, ep[r][p], tot[r][p], s, row0, s < a.streams);
+        }
+    flag_nonfinite(a.status, bad);
+}
+
+// Q8 fragments to bf16 fragments (the same order; int8 values are exact in
+// bf16) and fp16 block scales to fp32 (exact).
+__global__ void k_wide_from_q8(const int8_t *__restrict__ values, const uint16_t *__restrict__ scales,
+                               size_t n_values, uint16_t *__restrict__ out_values,
+                               float *__restrict__ out_scales) {
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n_values / 8; i += stride) {
+        const uint2 raw = *(const uint2 *)(values + i * 8);
+        *(bf16x8 *)(out_values + i * 8) = q8_to_bf16(raw);
+    }
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n_values / 32; i += stride)
+        out_scales[i] = half_to_float(scales[i]);
+}
+
+// ---------------------------------------------------------------------------
+// Fast causal attention. entries: [count][2] (s0, n): pseudo-streams
+// s0 .. s0 + n - 1 (n <= 64) are consecutive positions of one stream and
+// share the block table row of s0. Grid (entries, heads), 4 waves.
+constexpr int kAttnWaves = 4;
+constexpr int kQueries = PGPU_PREFILL_RUN;
+static_assert(kQueries == 64, "one lane per query of a run");
+// LDS per wave: one key block's K then V (16 x 64 fp32 each); after the
+// key loop the same array holds waves 1..3's (max, sum, 64 accumulators).
+constexpr int kWaveKv = 2 * kBlockPos * kHeadDim;
+constexpr int kMergeFloats = (kAttnWaves - 1) * (2 + kHeadDim) * 64;
+constexpr int kAttnLds = kMergeFloats > kAttnWaves * kWaveKv ? kMergeFloats : kAttnWaves * kWaveKv;
+
+__global__ __launch_bounds__(64 * kAttnWaves) void k_prefill_attention_rows(
+    const float *__restrict__ q, const float *__restrict__ kv, size_t layer_stride,
+    unsigned blocks, int layer, const int32_t *__restrict__ tables, int table_stride,
+    const int32_t *__restrict__ positions, int streams, const int32_t *__restrict__ entries,
+    uint16_t *__restrict__ out_split, int *status) {
+    __shared__ float4 lds4[kAttnLds / 4];
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    const int head = blockIdx.y;
+    const int s0 = entries[2 * blockIdx.x], n = entries[2 * blockIdx.x + 1];
+    // A malformed entry is flagged and computes nothing.
+    if (n < 1 || n > kQueries || s0 < 0 || s0 > streams - n) {
+        if (threadIdx.x == 0) atomicOr(status, 2);
+        return;
+    }
+    const int p0 = positions[s0];
+    const int p_last = p0 + n - 1;
+    const bool mine = lane < n;
+    const int pos = p0 + lane;
+    const int32_t *table = tables + (size_t)s0 * table_stride;
+    const float *layer_kv = kv + (size_t)layer * layer_stride;
+
+    float qv[kHeadDim];
+    {
+        const float *qrow = q + (size_t)(s0 + (mine ? lane : 0)) * kWidth + head * kHeadDim;
+#pragma unroll
+        for (int d = 0; d < kHeadDim; d += 4) {
+            const float4 v = *(const float4 *)(qrow + d);
+            qv[d] = v.x;
+            qv[d + 1] = v.y;
+            qv[d + 2] = v.z;
+            qv[d + 3] = v.w;
+        }
+    }
+    float acc[kHeadDim];
+#pragma unroll
+    for (int d = 0; d < kHeadDim; d++) acc[d] = 0.0f;
+    float m = -INFINITY, l = 0.0f;
+
+    float4 *mine_kv = lds4 + wave * (kWaveKv / 4);
+    // A context the block table cannot cover is an error: flagged, and only
+    // the covered keys are read.
+    if (p_last / kBlockPos >= table_stride && wave == 0 && lane == 0) atomicOr(status, 2);
+    const int nblocks = min(p_last / kBlockPos + 1, table_stride);
+    bool bad_block = false;
+    // Keys of block b: the wave's 64 lanes move its K then V tile (1024
+    // floats each, contiguous in the pool) with four 16-byte loads per lane.
+    float4 n0, n1, n2, n3, n4, n5, n6, n7;
+#define PGPU_FETCH_KV(b_)                                                                    \
+    do {                                                                                     \
+        int id_ = table[(b_)];                                                               \
+        bad_block |= (unsigned)id_ >= blocks;                                                \
+        id_ = (unsigned)id_ < blocks ? id_ : 0;                                              \
+        const float4 *t_ = (const float4 *)(layer_kv + ((size_t)id_ * kHeads + head) * 2048) + \
+                           lane;                                                             \
+        n0 = t_[0];                                                                          \
+        n1 = t_[64];                                                                         \
+        n2 = t_[128];                                                                        \
+        n3 = t_[192];                                                                        \
+        n4 = t_[256];                                                                        \
+        n5 = t_[320];                                                                        \
+        n6 = t_[384];                                                                        \
+        n7 = t_[448];                                                                        \
+    } while (0)
+    int b = wave;
+    if (b < nblocks) PGPU_FETCH_KV(b);
+    for (; b < nblocks; b += kAttnWaves) {
+        mine_kv[lane] = n0;
+        mine_kv[64 + lane] = n1;
+        mine_kv[128 + lane] = n2;
+        mine_kv[192 + lane] = n3;
+        mine_kv[256 + lane] = n4;
+        mine_kv[320 + lane] = n5;
+        mine_kv[384 + lane] = n6;
+        mine_kv[448 + lane] = n7;
+        __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LDS writes done
+        __builtin_amdgcn_wave_barrier();
+        if (b + kAttnWaves < nblocks) PGPU_FETCH_KV(b + kAttnWaves);
+        const float *kt = (const float *)mine_kv;
+        const float *vt = kt + kBlockPos * kHeadDim;
+        const int key0 = b * kBlockPos;
+        const bool full = key0 + kBlockPos - 1 <= p0;  // every key at or before every query
+        float sc[kBlockPos];
+        float bm = -INFINITY;
+#pragma unroll
+        for (int j = 0; j < kBlockPos; j++) {
+            float dot = 0.0f;
+#pragma unroll
+            for (int d = 0; d < kHeadDim; d += 4) {
+                const float4 k = *(const float4 *)(kt + j * kHeadDim + d);
+                dot = fmaf(qv[d], k.x, dot);
+                dot = fmaf(qv[d + 1], k.y, dot);
+                dot = fmaf(qv[d + 2], k.z, dot);
+                dot = fmaf(qv[d + 3], k.w, dot);
+            }
+            const bool use = full || key0 + j <= pos;
+            sc[j] = use ? dot : -INFINITY;
+            bm = fmaxf(bm, sc[j]);
+        }
+        if (mine && bm > -INFINITY) {
+            const float mn = fmaxf(m, bm);
+            const float keep = expf(m - mn);  // 0 on the first block
+            m = mn;
+            l *= keep;
+#pragma unroll
+            for (int d = 0; d < kHeadDim; d++) acc[d] *= keep;
+#pragma unroll
+            for (int j = 0; j < kBlockPos; j++) {
+                if (sc[j] == -INFINITY) continue;
+                const float e = expf(sc[j] - mn);
+                l += e;
+#pragma unroll
+                for (int d = 0; d < kHeadDim; d += 4) {
+                    const float4 v = *(const float4 *)(vt + j * kHeadDim + d);
+                    acc[d] = fmaf(e, v.x, acc[d]);
+                    acc[d + 1] = fmaf(e, v.y, acc[d + 1]);
+                    acc[d + 2] = fmaf(e, v.z, acc[d + 2]);
+                    acc[d + 3] = fmaf(e, v.w, acc[d + 3]);
+                }
+            }
+        }
+        __builtin_amdgcn_wave_barrier();  // every lane is done with the tile
+    }
+#undef PGPU_FETCH_KV
+    if (bad_block) atomicOr(status, 2);
+
+    // Merge the four waves' states in wave order: waves 1..3 publish
+    // (m, l, acc) per lane, wave 0 folds them in.
+    __syncthreads();
+    float *pub = (float *)lds4;  // [wave-1][66][64]
+    if (wave > 0) {
+        float *dst = pub + (size_t)(wave - 1) * 66 * 64;
+        dst[lane] = m;
+        dst[64 + lane] = l;
+#pragma unroll
+        for (int d = 0; d < kHeadDim; d++) dst[(2 + d) * 64 + lane] = acc[d];
+    }
+    __syncthreads();
+    if (wave != 0 || !mine) return;
+#pragma unroll 1
+    for (int w = 1; w < kAttnWaves; w++) {
+        const float *src = pub + (size_t)(w - 1) * 66 * 64;
+        const float mw = src[lane];
+        if (mw == -INFINITY) continue;  // the wave saw no key of this lane
+        const float lw = src[64 + lane];
+        const float mn = fmaxf(m, mw);
+        const float keep = expf(m - mn), f = expf(mw - mn);
+        m = mn;
+        l = fmaf(lw, f, l * keep);
+#pragma unroll
+        for (int d = 0; d < kHeadDim; d++) acc[d] = fmaf(src[(2 + d) * 64 + lane], f, acc[d] * keep);
+    }
+    const bool ok = l > 0.0f && isfinite(l);
+    const float inv = 1.0f / l;
+    bool bad = !ok;
+#pragma unroll
+    for (int d = 0; d < kHeadDim; d += 4) {
+        float v[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            v[i] = ok ? acc[d + i] * inv : 0.0f;
+            bad |= !isfinite(v[i]);
+        }
+        store_split4(out_split, s0 + lane, head * kHeadDim + d, kWidth / 32, v, false);
+    }
+    flag_nonfinite(status, bad);
+}
+
+// ---------------------------------------------------------------------------
+template <int EPI, bool SCALED, int WR, int WP, int RW, int PW, int NB, int KS>
+int launch_gemm(const GemmArgs &a, hipStream_t stream) {
+    constexpr int RT = WR * RW, PT = WP * PW;
+    const int row_groups = (a.n_rows / 16) / RT;
+    const int pos_groups = ((a.streams + 15) / 16 + PT - 1) / PT;
+    hipLaunchKernelGGL((k_prefill_gemm<EPI, SCALED, WR, WP, RW, PW, NB, KS>),
+                       dim3(row_groups * pos_groups), dim3(kTaskThreads), 0, stream, a,
+                       row_groups, pos_groups);
+    return launch_ok("pgpu_prefill_gemm");
+}
+
+// Tile shapes (rows x positions per work-group): 128 x 128 for the wide
+// projections (4 LDS stages, 130 KB), 128 x 64 for the 512-row ones (6
+// stages, 126 KB), so that a few thousand positions give >= 256
+// work-groups.
+template <int EPI, bool SCALED>
+int dispatch_gemm(const GemmArgs &a, hipStream_t stream) {
+    if (a.n_rows > kWidth) return launch_gemm<EPI, SCALED, 2, 4, 4, 2, 2, 2>(a, stream);
+    return launch_gemm<EPI, SCALED, 4, 2, 2, 2, 2, 2>(a, stream);
+}
+
+template <int EPI>
+int run_gemm(const GemmArgs &a, const pgpu_wide_matrix *w, hipStream_t stream) {
+    if (!w || !w->values || a.n_rows % 128 || (a.k_cols != kWidth && a.k_cols != kFfn) ||
+        a.streams <= 0 || !a.xs || !a.status)
+        return bad_arguments("pgpu_prefill_gemm");
+    return w->scales ? dispatch_gemm<EPI, true>(a, stream) : dispatch_gemm<EPI, false>(a, stream);
+}
+
+GemmArgs gemm_args(const pgpu_wide_matrix *w, const uint16_t *split, int streams, int *status) {
+    GemmArgs a{};
+    if (!w) return a;
+    a.xs = split;
+    a.w = w->values;
+    a.wscale_f = w->scales;
+    a.n_rows = (int)w->rows;
+    a.k_cols = (int)w->columns;
+    a.streams = streams;
+    a.status = status;
+    return a;
+}
+
+}  // namespace
+}  // namespace pgpu
+
+using namespace pgpu;
+
+extern "C" int pgpu_rows_split_ln(void *stream, const float *rows, const float *weight,
+                                  const float *bias, float epsilon, int streams,
+                                  uint16_t *out_split, int *status) {
+    if (!rows || !weight || !bias || !out_split || !status || streams <= 0 || !(epsilon > 0.0f))
+        return bad_arguments("pgpu_rows_split_ln");
+    GemmArgs a{};
+    a.ln_x = rows;
+    a.ln_w = weight;
+    a.ln_b = bias;
+    a.ln_eps = epsilon;
+    a.streams = streams;
+    a.status = status;
+    hipLaunchKernelGGL(k_rows_split<SRC_LN>, dim3((streams + 15) / 16), dim3(kTaskThreads), 0,
+                       (hipStream_t)stream, a, out_split);
+    return launch_ok("pgpu_rows_split_ln");
+}
+
+extern "C" int pgpu_rows_split_attention(void *stream, const pgpu_attention_scratch *work,
+                                         const int32_t *positions, int streams, int max_splits,
+                                         uint16_t *out_split, int *status) {
+    if (!work || !positions || !out_split || !status || streams <= 0 ||
+        streams > work->max_streams || max_splits <= 0 || max_splits > work->max_splits)
+        return bad_arguments("pgpu_rows_split_attention");
+    GemmArgs a{};
+    a.part_acc = work->part_acc;
+    a.part_ml = work->part_ml;
+    a.max_splits = max_splits;
+    a.positions = positions;
+    a.streams = streams;
+    a.status = status;
+    hipLaunchKernelGGL(k_rows_split<SRC_ATTN>, dim3((streams + 15) / 16), dim3(kTaskThreads), 0,
+                       (hipStream_t)stream, a, out_split);
+    return launch_ok("pgpu_rows_split_attention");
+}
+
+extern "C" int pgpu_prefill_gemm_qkv(void *stream, const pgpu_wide_matrix *w, const uint16_t *split,
+                                     int streams, const pgpu_paged_kv *kv, int layer,
+                                     const int32_t *tables, int table_stride,
+                                     const int32_t *positions, const float *rope, float *q_out,
+                                     int *status) {
+    if (!w || w->rows != 3 * kWidth || w->columns != kWidth || !kv || layer < 0 ||
+        layer >= kv->layers || !tables || table_stride <= 0 || !positions || !rope || !q_out)
+        return bad_arguments("pgpu_prefill_gemm_qkv");
+    GemmArgs a = gemm_args(w, split, streams, status);
+    a.q_out = q_out;
+    a.kv = kv->base;
+    a.layer_stride = kv->layer_stride;
+    a.blocks = (unsigned)kv->blocks;
+    a.layer = layer;
+    a.tables = tables;
+    a.table_stride = table_stride;
+    a.positions = positions;
+    a.rope = (const float2 *)rope;
+    a.plain_qkv = true;  // read by the next launches only
+    return run_gemm<EPI_QKV>(a, w, (hipStream_t)stream);
+}
+
+extern "C" int pgpu_prefill_gemm_residual(void *stream, const pgpu_wide_matrix *w,
+                                          const uint16_t *split, int streams,
+                                          const float *residual, float *out, int *status) {
+    if (!w || !residual || !out) return bad_arguments("pgpu_prefill_gemm_residual");
+    GemmArgs a = gemm_args(w, split, streams, status);
+    a.out = out;
+    a.ld_out = (int)w->rows;
+    a.residual = residual;
+    return run_gemm<EPI_RESIDUAL>(a, w, (hipStream_t)stream);
+}
+
+extern "C" int pgpu_prefill_gemm_gelu_split(void *stream, const pgpu_wide_matrix *w,
+                                            const uint16_t *split, int streams,
+                                            uint16_t *out_split, int *status) {
+    if (!w || !out_split || w->rows % 32) return bad_arguments("pgpu_prefill_gemm_gelu_split");
+    GemmArgs a = gemm_args(w, split, streams, status);
+    a.out_split = out_split;
+    a.out_kb = (int)w->rows / 32;
+    return run_gemm<EPI_GELU_SPLIT>(a, w, (hipStream_t)stream);
+}
+
+extern "C" int pgpu_prefill_attention_rows(void *stream, const float *q, const pgpu_paged_kv *kv,
+                                           int layer, const int32_t *tables, int table_stride,
+                                           const int32_t *positions, int streams,
+                                           const int32_t *entries, int entry_count,
+                                           uint16_t *out_split, int *status) {
+    if (!q || !kv || !tables || !positions || !entries || !out_split || !status ||
+        streams <= 0 || layer < 0 || layer >= kv->layers || table_stride <= 0 ||
+        entry_count <= 0 || entry_count > 65535)
+        return bad_arguments("pgpu_prefill_attention_rows");
+    hipLaunchKernelGGL(k_prefill_attention_rows, dim3(entry_count, kHeads),
+                       dim3(64 * kAttnWaves), 0, (hipStream_t)stream, q, kv->base,
+                       kv->layer_stride, (unsigned)kv->blocks, layer, tables, table_stride,
+                       positions, streams, entries, out_split, status);
+    return launch_ok("pgpu_prefill_attention_rows");
+}
+
+extern "C" int pgpu_wide_from_matrix(void *stream, const pgpu_matrix *w, uint16_t *values,
+                                     float *scales) {
+    if (!w || !w->q8 || !w->values || !w->scales || !values || !scales || w->rows % 16 ||
+        w->columns % 32)
+        return bad_arguments("pgpu_wide_from_matrix");
+    const size_t n = w->rows * w->columns;
+    const unsigned blocks = (unsigned)((n / 8 + 255) / 256 < 2048 ? (n / 8 + 255) / 256 : 2048);
+    hipLaunchKernelGGL(k_wide_from_q8, dim3(blocks), dim3(256), 0, (hipStream_t)stream,
+                       (const int8_t *)w->values, w->scales, n, values, scales);
+    return launch_ok("pgpu_wide_from_matrix");
+}

@@ -18,7 +18,7 @@ enum { PH_FLOW_HEADROOM = 256 };
 /* Batched prefill attention (pgpu_prefill_attention): up to PH_PREFILL_RUN
  * consecutive positions per work entry, fewer while the entries would give
  * under PH_PREFILL_MIN_GROUPS work-groups (one per head per entry). */
-enum { PH_PREFILL_RUN = 64, PH_PREFILL_MIN_GROUPS = 1024 };
+enum { PH_PREFILL_RUN = PGPU_PREFILL_RUN, PH_PREFILL_MIN_GROUPS = 1024 };
 /* Decode batches of this many 16-stream tiles run as one launch by default
  * (phonon_flow_batch_set_pipeline): measured faster there on MI355X (us per
  * 12-layer step, contexts U{1..2048}, one launch vs phase by phase: B = 1:

@@ -18,6 +18,7 @@
 struct PhononFlowModel {
     size_t layers;
     pgpu_matrix *qkv, *out, *mlp_in, *mlp_out;
+    pgpu_wide_matrix *wide;       /* [layers][4]: the prefill projections' weights */
     float *norms; /* dev [layers][4][512]: norm1 w, b, norm2 w, b */
     pgpu_flow_layer *flow_layers; /* dev [layers]: operands of the one-launch step */
     int q8;                       /* 1/0: every matrix Q8/BF16; -1: mixed */
@@ -44,9 +45,14 @@ struct PhononFlowBatch {
     int32_t *table_src, *table_map; /* prefill staging, allocated on first use */
     struct {
         int active;                 /* the streams are a prefill's pseudo-streams */
+        int exact;                  /* attention with the decode step's arithmetic */
         int32_t *entries;           /* (dev) [cap][4]: work entries of pgpu_prefill_attention */
         int32_t *host;              /* [cap][4] */
         size_t count, cap;
+        int32_t *runs;              /* (dev) [runs_cap][2]: pgpu_prefill_attention_rows */
+        int32_t *runs_host;
+        size_t runs_count, runs_cap;
+        uint16_t *split;            /* (dev) split fragments [max_streams/16][16][1536] */
     } pre;
     int flow;                       /* 1: one launch per step (pgpu_flow_launch) */
     struct {
@@ -106,6 +112,7 @@ void phonon_flow_model_destroy(PhononFlowModel *model) {
     free(model->out);
     free(model->mlp_in);
     free(model->mlp_out);
+    free(model->wide);
     free(model);
 }
 
@@ -124,9 +131,11 @@ int phonon_flow_model_create(const PhononFlowLayerWeights *weights, size_t layer
     m->out = calloc(layers, sizeof(pgpu_matrix));
     m->mlp_in = calloc(layers, sizeof(pgpu_matrix));
     m->mlp_out = calloc(layers, sizeof(pgpu_matrix));
-    m->allocations = calloc(layers * 4 + 2, sizeof(void *));
+    m->wide = calloc(layers * 4, sizeof(pgpu_wide_matrix));
+    /* Per layer 4 uploads and up to 4 x 2 prefill copies; norms; table. */
+    m->allocations = calloc(layers * 12 + 2, sizeof(void *));
     float *norms = malloc(layers * 4 * PH_WIDTH * sizeof(float));
-    int ok = m->qkv && m->out && m->mlp_in && m->mlp_out && m->allocations && norms;
+    int ok = m->qkv && m->out && m->mlp_in && m->mlp_out && m->wide && m->allocations && norms;
     for (size_t l = 0; ok && l < layers; l++) {
         const PhononFlowLayerWeights *w = &weights[l];
         struct {
@@ -145,6 +154,27 @@ int phonon_flow_model_create(const PhononFlowLayerWeights *weights, size_t layer
                 m->device_bytes += mats[i].dst->rows * mats[i].dst->columns *
                                    (mats[i].dst->q8 ? 1 : 2) +
                                    (mats[i].dst->q8 ? mats[i].dst->rows * mats[i].dst->columns / 16 : 0);
+            }
+            /* The batched prefill's projections read bf16 fragments (and
+             * fp32 scales): converted once here from Q8 (exact). */
+            pgpu_wide_matrix *wide = &m->wide[l * 4 + i];
+            const pgpu_matrix *mat = mats[i].dst;
+            wide->rows = mat->rows;
+            wide->columns = mat->columns;
+            if (ok && !mat->q8) {
+                wide->values = mat->values;
+            } else if (ok) {
+                const size_t n = mat->rows * mat->columns;
+                uint16_t *values = pgpu_malloc(n * sizeof(uint16_t));
+                float *scales = values ? pgpu_malloc(n / 32 * sizeof(float)) : NULL;
+                if (values)
+                    m->allocations[m->allocation_count++] = values;
+                if (scales)
+                    m->allocations[m->allocation_count++] = scales;
+                ok = scales && pgpu_wide_from_matrix(ph_stream(), mat, values, scales);
+                wide->values = values;
+                wide->scales = scales;
+                m->device_bytes += n * sizeof(uint16_t) + n / 32 * sizeof(float);
             }
         }
         float *n = norms + l * 4 * PH_WIDTH;
@@ -378,6 +408,9 @@ void phonon_flow_batch_destroy(PhononFlowBatch *b) {
     pgpu_stream_destroy(b->stream);
     pgpu_free(b->pre.entries);
     free(b->pre.host);
+    pgpu_free(b->pre.runs);
+    free(b->pre.runs_host);
+    pgpu_free(b->pre.split);
     free(b->host_positions);
     free(b->fl.host_schedule);
     free(b->fl.cover);
@@ -513,9 +546,57 @@ static size_t splits_for(const PhononFlowBatch *b, size_t ahead) {
 /* Enqueues layers [first, first+count) for streams [s0, s0+n) of the batch
  * (s0 a multiple of 16) on `stream`. Every buffer is used at the group's
  * offset, so groups share no memory and may run concurrently. */
+/* Layers [first, first+count) of a batched prefill (pgpu_prefill.hip): per
+ * layer LayerNorm into split fragments, the large-M QKV projection (RoPE,
+ * K/V append), the causal attention (fast, or exact: the decode step's
+ * split partials merged by the OUT operand pass), the OUT projection, the
+ * second LayerNorm, MLP_IN and MLP_OUT. */
+static int enqueue_prefill(PhononFlowBatch *b, void *stream, size_t first, size_t count,
+                           size_t pool_offset, const float *input, float *output,
+                           const float *rope) {
+    const PhononFlowModel *m = b->model;
+    const int n = (int)b->streams;
+    const pgpu_attention_scratch scratch = {b->scratch.part_acc, b->scratch.part_ml, n,
+                                            (int)b->splits};
+    uint16_t *xs = b->pre.split;
+    const float *cur = input;
+    for (size_t l = first; l < first + count; l++) {
+        const float *norm = m->norms + l * 4 * PH_WIDTH;
+        float *next = (l + 1 == first + count) ? output : b->x;
+        const int layer = (int)(l + pool_offset);
+        if (!pgpu_rows_split_ln(stream, cur, norm, norm + PH_WIDTH, 1e-5f, n, xs, b->status) ||
+            !pgpu_prefill_gemm_qkv(stream, &m->wide[l * 4], xs, n, &b->pool->kv, layer, b->tables,
+                                   (int)b->table_len, b->positions, rope, b->q, b->status))
+            return 0;
+        if (!(b->pre.exact
+                  ? pgpu_prefill_attention(stream, b->q, &b->pool->kv, layer, b->tables,
+                                           (int)b->table_len, b->positions, n, PH_HEADS,
+                                           (int)b->splits, b->pre.entries, (int)b->pre.count,
+                                           &scratch, b->status) &&
+                        pgpu_rows_split_attention(stream, &scratch, b->positions, n,
+                                                  (int)b->splits, xs, b->status)
+                  : pgpu_prefill_attention_rows(stream, b->q, &b->pool->kv, layer, b->tables,
+                                                (int)b->table_len, b->positions, n,
+                                                b->pre.runs, (int)b->pre.runs_count, xs,
+                                                b->status)) ||
+            !pgpu_prefill_gemm_residual(stream, &m->wide[l * 4 + 1], xs, n, cur, b->r, b->status) ||
+            !pgpu_rows_split_ln(stream, b->r, norm + 2 * PH_WIDTH, norm + 3 * PH_WIDTH, 1e-5f,
+                                n, xs, b->status) ||
+            !pgpu_prefill_gemm_gelu_split(stream, &m->wide[l * 4 + 2], xs, n, b->xh,
+                                          b->status) ||
+            !pgpu_prefill_gemm_residual(stream, &m->wide[l * 4 + 3], b->xh, n, b->r, next,
+                                        b->status))
+            return 0;
+        cur = next;
+    }
+    return 1;
+}
+
 static int enqueue_group(PhononFlowBatch *b, void *stream, size_t s0, size_t n, size_t first,
                          size_t count, size_t pool_offset, const float *input, float *output,
                          const float *rope) {
+    if (b->pre.active)
+        return enqueue_prefill(b, stream, first, count, pool_offset, input, output, rope);
     const PhononFlowModel *m = b->model;
     const size_t slot0 = s0 * PH_HEADS * b->splits;
     const pgpu_attention_scratch scratch = {b->scratch.part_acc + slot0 * 64,
@@ -848,6 +929,57 @@ static int prefill_entries(PhononFlowBatch *b, size_t streams, const size_t *fir
     return pgpu_copy_h2d(b->stream, b->pre.entries, b->pre.host, n * 4 * sizeof(int32_t));
 }
 
+/* Work list of the fast prefill attention (pgpu_prefill_attention_rows):
+ * runs of up to 64 consecutive positions of one stream, as (first
+ * pseudo-stream, count), the runs with the most keys first so that the
+ * longest work-groups start earliest. */
+typedef struct {
+    size_t last;
+    int32_t s0, n;
+} PrefillRun;
+
+static int run_order(const void *x, const void *y) {
+    const PrefillRun *a = x, *b = y;
+    return a->last < b->last ? 1 : (a->last > b->last ? -1 : (a->s0 > b->s0) - (a->s0 < b->s0));
+}
+
+static int prefill_runs(PhononFlowBatch *b, size_t streams, const size_t *first,
+                        const size_t *counts) {
+    size_t n = 0;
+    for (size_t i = 0; i < streams; i++)
+        n += (counts[i] + PH_PREFILL_RUN - 1) / PH_PREFILL_RUN;
+    if (!n || n > 65535)
+        return ph_fail("prefill: attention work list size out of range");
+    PrefillRun *list = malloc(n * sizeof(PrefillRun));
+    if (!list)
+        return 0;
+    for (size_t i = 0, k = 0, offset = 0; i < streams; offset += counts[i], i++)
+        for (size_t q = 0; q < counts[i]; q += PH_PREFILL_RUN, k++) {
+            const size_t len = counts[i] - q < PH_PREFILL_RUN ? counts[i] - q : PH_PREFILL_RUN;
+            list[k] = (PrefillRun){first[i] + q + len - 1, (int32_t)(offset + q), (int32_t)len};
+        }
+    qsort(list, n, sizeof(PrefillRun), run_order);
+    if (n > b->pre.runs_cap) {
+        int32_t *host = realloc(b->pre.runs_host, n * 2 * sizeof(int32_t));
+        if (host)
+            b->pre.runs_host = host;
+        pgpu_free(b->pre.runs);
+        b->pre.runs = host ? pgpu_malloc(n * 2 * sizeof(int32_t)) : NULL;
+        b->pre.runs_cap = b->pre.runs ? n : 0;
+        if (!b->pre.runs) {
+            free(list);
+            return 0;
+        }
+    }
+    for (size_t k = 0; k < n; k++) {
+        b->pre.runs_host[2 * k] = list[k].s0;
+        b->pre.runs_host[2 * k + 1] = list[k].n;
+    }
+    free(list);
+    b->pre.runs_count = n;
+    return pgpu_copy_h2d(b->stream, b->pre.runs, b->pre.runs_host, n * 2 * sizeof(int32_t));
+}
+
 /* Pseudo-streams of a batched prefill: position first[i] + k (k < counts[i])
  * of stream i becomes its own stream with block-table row i of tables_dev
  * (device, [streams][table_len]). A step then runs every such position
@@ -867,6 +999,10 @@ int ph_batch_set_prefill(PhononFlowBatch *b, size_t streams, const size_t *first
         return 0;
     if (!b->table_map && !(b->table_map = pgpu_malloc(b->max_streams * sizeof(int32_t))))
         return 0;
+    if (!b->pre.split &&
+        !(b->pre.split = pgpu_malloc(b->padded_streams / 16 * (PH_WIDTH / 32) * 1536 *
+                                     sizeof(uint16_t))))
+        return 0;
     int32_t *pos32 = malloc(total * sizeof(int32_t)), *map = malloc(total * sizeof(int32_t));
     int ok = pos32 && map;
     for (size_t i = 0, p = 0; ok && i < streams; i++)
@@ -880,7 +1016,7 @@ int ph_batch_set_prefill(PhononFlowBatch *b, size_t streams, const size_t *first
          pgpu_copy_h2d(b->stream, b->table_map, map, total * sizeof(int32_t)) &&
          pgpu_gather_rows(b->stream, b->tables, tables_dev, b->table_map, (int)total,
                           (int)b->table_len) &&
-         prefill_entries(b, streams, first, counts);
+         prefill_entries(b, streams, first, counts) && prefill_runs(b, streams, first, counts);
     free(pos32);
     free(map);
     if (ok) {
@@ -907,6 +1043,13 @@ int phonon_flow_batch_prefill_device(PhononFlowBatch *b, size_t streams, const s
     if (flow_usable(b, 1))
         return flow_prepare(b, 1) && enqueue_flow(b, inputs, outputs, theta);
     return (b->splits = splits_for(b, 0)) > 0 && enqueue_step(b, inputs, outputs, theta);
+}
+
+int phonon_flow_batch_set_prefill_exact(PhononFlowBatch *b, int exact) {
+    if (!b || exact < 0 || exact > 1)
+        return 0;
+    b->pre.exact = exact;
+    return 1;
 }
 
 int phonon_flow_batch_set_groups(PhononFlowBatch *b, size_t groups) {
