@@ -104,6 +104,12 @@ int phonon_flow_batch_prefill_device(PhononFlowBatch *batch, size_t streams, con
  * split attention and merge, so every output row has the bits of single
  * steps. The projections give the bits of single steps either way. */
 int phonon_flow_batch_set_prefill_exact(PhononFlowBatch *batch, int exact);
+/* One-launch step: a task that has waited this many microseconds for its
+ * inputs (at most 10 s) gives up, sets status bit 2 (value 4) and makes
+ * every other waiting task give up, so the launch ends; its results are
+ * then unusable (phonon_flow_batch_sync returns 0). 0 (the default): one
+ * second. A small value forces that path from the host. */
+int phonon_flow_batch_set_wait_limit(PhononFlowBatch *batch, unsigned microseconds);
 /* Runs the streams as `groups` (1..4) independent groups of whole 16-stream
  * tiles, each on its own HIP stream inside the step's graph. Results do not
  * depend on it. Default 1: on MI355X under ROCm 7 kernels of different HIP

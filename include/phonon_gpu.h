@@ -194,6 +194,8 @@ typedef struct {
     uint64_t *trace;               /* (dev) NULL, or [tasks][4]: start, inputs ready, end
                                       (constant 100 MHz clock) of each task, and where it
                                       ran (XCC id << 32 | HW_ID register) */
+    unsigned wait_us;              /* a task's wait for its inputs gives up (status bit 4)
+                                      after this many microseconds; 0: one second */
 } pgpu_flow_step;
 
 /* Placement of each tile's projection chain in a task list, on a model

@@ -238,6 +238,7 @@ EXPORTS = {
     "pgpu_prefill_attention_rows": (_i, [_vp, _vp, _kvp, _i, _vp, _i, _vp, _i, _vp, _i, _vp,
                                          _vp]),
     "phonon_flow_batch_set_prefill_exact": (_i, [_vp, _i]),
+    "phonon_flow_batch_set_wait_limit": (_i, [_vp, ctypes.c_uint]),
     "pgpu_prefill_attention": (_i, [_vp, _vp, _kvp, _i, _vp, _i, _vp, _i, _i, _i, _vp, _i,
                                     _scp, _vp]),
     "pgpu_attention_static": (_i, [_vp, _vp, _kvp, _i, _vp, _i, _vp, _i, _i, _i, _vp, _vp,

@@ -59,6 +59,7 @@ struct FlowWait {
     const unsigned *flag;
     unsigned target;
     int *status;
+    uint64_t ticks;  // give-up bound on the 100 MHz constant clock
     __device__ unsigned probe() const {
         return threadIdx.x == 0 && flag
                    ? __hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
@@ -76,7 +77,7 @@ struct FlowWait {
                     __hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 const int st = __hip_atomic_load(status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 if (count >= target) break;
-                if ((st & 4) || wall_clock64() - t0 > kWaitTicks) {
+                if ((st & 4) || wall_clock64() - t0 > ticks) {
                     atomicOr(status, 4);
                     break;
                 }
@@ -88,9 +89,14 @@ struct FlowWait {
     __device__ void operator()() const { pass(probe()); }
 };
 
+// Waits give up after f.wait_us microseconds (0: 1 s).
+__device__ inline uint64_t wait_ticks(const pgpu_flow_step &f) {
+    return f.wait_us ? (uint64_t)f.wait_us * 100u : kWaitTicks;
+}
+
 __device__ inline FlowWait wait_for(const pgpu_flow_step &f, int layer, int tile, int kind,
                                     unsigned target) {
-    return FlowWait{phase_counter(f, layer, tile, kind), target, f.status};
+    return FlowWait{phase_counter(f, layer, tile, kind), target, f.status, wait_ticks(f)};
 }
 
 // Task timeline (optional): slot 0 = start, 1 = inputs ready, 2 = end,
@@ -284,7 +290,7 @@ __device__ inline void flow_step_task(const pgpu_flow_step &f, const pgpu_paged_
         a.table_stride = f.table_stride;
         a.positions = f.positions;
         a.rope = (const float2 *)f.rope;
-        const FlowWait w = layer == 0 ? FlowWait{nullptr, 0u, f.status}
+        const FlowWait w = layer == 0 ? FlowWait{nullptr, 0u, f.status, 0u}
                                       : wait_for(f, layer - 1, tile, PGPU_FLOW_MLP_OUT,
                                                  PGPU_FLOW_MLP_OUT_TASKS);
         gemm_wide_task<SRC_LN, EPI_QKV, Q8>(a, index, tile, lds, TracedWait{w, &f});

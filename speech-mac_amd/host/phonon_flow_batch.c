@@ -74,6 +74,7 @@ struct PhononFlowBatch {
         pgpu_flow_placement place;  /* chain placement in the task list */
         uint64_t *trace;            /* (dev) optional task timeline, trace_cap tasks */
         size_t trace_cap;
+        unsigned wait_us;           /* give-up bound of the tasks' waits (0: 1 s) */
     } fl;
     int *status;
     pgpu_attention_scratch scratch;
@@ -862,7 +863,8 @@ static int enqueue_flow(PhononFlowBatch *b, const float *input, float *output, f
                               .split_done = b->fl.counters + phase_words,
                               .status = b->status,
                               .trace = b->fl.trace_cap >= b->fl.tasks ? b->fl.trace : NULL,
-                              .attn_rounds = b->fl.rounds};
+                              .attn_rounds = b->fl.rounds,
+                              .wait_us = b->fl.wait_us};
     const size_t used = phase_words + layers * tiles * 16 * PH_HEADS;
     return (!b->time_before || pgpu_event_record(b->time_before, b->stream)) &&
            pgpu_flow_launch(b->stream, &f, &b->pool->kv) &&
@@ -1043,6 +1045,13 @@ int phonon_flow_batch_prefill_device(PhononFlowBatch *b, size_t streams, const s
     if (flow_usable(b, 1))
         return flow_prepare(b, 1) && enqueue_flow(b, inputs, outputs, theta);
     return (b->splits = splits_for(b, 0)) > 0 && enqueue_step(b, inputs, outputs, theta);
+}
+
+int phonon_flow_batch_set_wait_limit(PhononFlowBatch *b, unsigned microseconds) {
+    if (!b || microseconds > 10000000u)
+        return 0;
+    b->fl.wait_us = microseconds;
+    return 1;
 }
 
 int phonon_flow_batch_set_prefill_exact(PhononFlowBatch *b, int exact) {

@@ -837,3 +837,122 @@ def test_batch_reports_nonfinite_and_uncovered_positions(lib, syn, pkg):
     assert not lib.phonon_flow_batch_set_streams(
         bt.batch, 2, far.ctypes.data_as(ctypes.POINTER(ctypes.c_size_t)), i32p(tables), 4)
     bt.close()
+
+
+# ---------------------------------------------------------------- robustness
+def test_forced_wait_timeout_reports_and_recovers(lib, syn, pkg):
+    """The one-launch step's give-up path, forced from the host: with a 1 us
+    wait limit its tasks stop waiting, the launch still ends, status bit 2
+    (value 4) is set and the step reports failure; with the default limit
+    restored and the positions reset, the same batch gives the bits of a
+    batch that never timed out."""
+    layers, streams = 3, 64
+    model = scaled_model(syn, 231, layers)
+    views = pkg.Views()
+    w = views.layers(model)
+    max_pos = 700
+    table_len = (max_pos + 15) // 16
+    blocks = streams * table_len
+    rng = np.random.default_rng(232)
+    lengths = rng.integers(1, 600, size=streams)
+    ctx = rng.standard_normal((2, layers, max_pos, 512)).astype(np.float32)
+    x = rng.standard_normal((streams, 512)).astype(np.float32)
+    szp = ctypes.POINTER(ctypes.c_size_t)
+
+    def setup():
+        bt = Batch(lib, w, layers, streams, max_pos, blocks)
+        set_step_mode(lib, bt.batch, 2)
+        ids = np.zeros(blocks, np.int32)
+        assert lib.phonon_kv_pool_alloc(bt.pool, blocks, i32p(ids))
+        tables = np.ascontiguousarray(ids.reshape(streams, table_len))
+        for s_i in range(streams):
+            assert lib.phonon_kv_pool_write(bt.pool, i32p(tables[s_i]), table_len, 0,
+                                            int(lengths[s_i]), fp(ctx[0]), fp(ctx[1]), max_pos)
+        pos = lengths.astype(np.uintp)
+        assert lib.phonon_flow_batch_set_streams(bt.batch, streams, pos.ctypes.data_as(szp),
+                                                 i32p(tables), table_len)
+        return bt, tables
+
+    ref_bt, _ = setup()
+    want = np.zeros((streams, 512), np.float32)
+    assert lib.phonon_flow_batch_step(ref_bt.batch, fp(x), 10000.0, fp(want)), pkg.last_error(lib)
+    ref_bt.close()
+
+    bt, tables = setup()
+    assert not lib.phonon_flow_batch_set_wait_limit(bt.batch, 10000001)
+    assert lib.phonon_flow_batch_set_wait_limit(bt.batch, 1)
+    print("forced wait timeout: one-launch step with a 1 us wait limit", flush=True)
+    din = pkg.DeviceBuffer(lib, streams * 512 * 4)
+    dout = pkg.DeviceBuffer(lib, streams * 512 * 4)
+    din.upload(x)
+    assert lib.phonon_flow_batch_step_device(bt.batch, din.ptr, 10000.0, dout.ptr)
+    st = ctypes.c_int(0)
+    assert lib.phonon_flow_batch_status(bt.batch, ctypes.byref(st))
+    assert st.value & 4, st.value
+    assert not lib.phonon_flow_batch_sync(bt.batch)       # reports, then clears
+    assert lib.phonon_flow_batch_status(bt.batch, ctypes.byref(st)) and st.value == 0
+    din.free()
+    dout.free()
+    # Recovery: default limit, positions reset (the timed-out step's appended
+    # rows are overwritten), the reference bits.
+    assert lib.phonon_flow_batch_set_wait_limit(bt.batch, 0)
+    pos = lengths.astype(np.uintp)
+    assert lib.phonon_flow_batch_set_streams(bt.batch, streams, pos.ctypes.data_as(szp),
+                                             i32p(tables), table_len)
+    got = np.zeros((streams, 512), np.float32)
+    assert lib.phonon_flow_batch_step(bt.batch, fp(x), 10000.0, fp(got)), pkg.last_error(lib)
+    bt.close()
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_dropins_from_two_threads(lib, syn, pkg):
+    """Two host threads drive the reference-signature drop-in
+    phonon_flow_stack_step at once on two caches, as concurrent requests on
+    separate caches do: every output and both caches equal the same calls
+    made from one thread."""
+    import threading
+    model = scaled_model(syn, 241, L9)
+    views = pkg.Views()
+    w = views.layers(model)
+    steps = 12
+    rng = np.random.default_rng(242)
+    xs = rng.standard_normal((2, steps, 512)).astype(np.float32)
+
+    def run(k, outs, errors, barrier=None):
+        try:
+            cache = Cache(lib, steps)
+            if barrier is not None:
+                barrier.wait()
+            for pos in range(steps):
+                y = np.zeros(512, np.float32)
+                ok = lib.phonon_flow_stack_step(w, cache.ref(), pos,
+                                                fp(np.ascontiguousarray(xs[k, pos])), 10000.0,
+                                                fp(y))
+                if not ok:
+                    errors.append((k, pos, pkg.last_error(lib)))
+                    break
+                outs[k].append(y)
+            outs[k].append(cache.keys().copy())
+            cache.destroy()
+        except Exception as e:  # reported by the main thread
+            errors.append((k, repr(e)))
+
+    seq = {0: [], 1: []}
+    errors = []
+    run(0, seq, errors)
+    run(1, seq, errors)
+    assert not errors, errors
+    par = {0: [], 1: []}
+    barrier = threading.Barrier(2)
+    threads = [threading.Thread(target=run, args=(k, par, errors, barrier)) for k in (0, 1)]
+    print("drop-ins from two threads: 2 x 12 stack steps", flush=True)
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join(timeout=120)
+        assert not t.is_alive()
+    assert not errors, errors
+    for k in (0, 1):
+        assert len(par[k]) == len(seq[k]) == steps + 1
+        for a, b in zip(par[k], seq[k]):
+            assert np.array_equal(np.asarray(a).view(np.uint32), np.asarray(b).view(np.uint32))
