@@ -112,7 +112,8 @@ int pgpu_gemm_silu_split(void *stream, const pgpu_matrix *w, const pgpu_gemm_inp
                          int streams, const float *bias, const float *bias2, uint16_t *out_split,
                          int *status);
 /* out = residual + gate * (x.W^T + bias), rows of W->rows floats; gate rows
- * of ld_gate floats (out may alias residual). */
+ * of ld_gate floats, or one gate row for every stream when ld_gate is 0
+ * (out may alias residual). */
 int pgpu_gemm_gated(void *stream, const pgpu_matrix *w, const pgpu_gemm_input *x, int streams,
                     const float *bias, const float *gate, int ld_gate, const float *residual,
                     float *out, int *status);
@@ -256,6 +257,50 @@ int pgpu_prefill_attention(void *stream, const float *q, const pgpu_paged_kv *kv
                            int streams, int heads, int max_splits, const int32_t *entries,
                            int entry_count, const pgpu_attention_scratch *scratch,
                            int *status);
+/* -- audio decoder (pgpu_audio.hip). Positions are rows of row-major
+ * [positions][channels] device arrays; every kernel covers all positions of
+ * a call at once, taking earlier positions from the caller's history. -- */
+/* Mimi input of `frames` latent frames ([frames][32]): the 512 x 32
+ * projection (fp32 [512][32]) and the depthwise upsample (fp32 [512][32]:
+ * taps 0..15 current frame, 16..31 previous frame) into hidden
+ * [16 frames][512]; `previous` (the projection of the frame before, [512])
+ * is read for frame 0 and replaced by the last frame's projection. */
+int pgpu_mimi_input(void *stream, const float *latents, int frames, const float *projection,
+                    const float *upsample, float *previous, float *hidden, int *status);
+/* Interleaved RoPE of q (in place) and k of rows [rows][1536] (q | k | v)
+ * at positions first + r (rope: [rope_positions][32] (cos, sin) pairs), and
+ * k, v stored at ring slot (first + r) % ring of ring_k / ring_v
+ * ([ring][512]). */
+int pgpu_mimi_rope_store(void *stream, float *qkv, int rows, long long first, const float *rope,
+                         long long rope_positions, float *ring_k, float *ring_v, int ring);
+/* softmax(q k / 8) v of each row over the keys of positions
+ * max(0, p - context + 1) .. p (p = first + r) in the ring, into
+ * out [rows][512]; ring >= rows + context - 1 and context <= 256. */
+int pgpu_mimi_attention(void *stream, const float *qkv, int rows, long long first,
+                        const float *ring_k, const float *ring_v, int ring, int context,
+                        float *out, int *status);
+/* Causal Conv1d (kernel 1, 3 or 7; weight [cin][kernel][cout], bias [cout])
+ * of x [positions][cin] into y [positions][cout], y = residual + (dot + bias)
+ * when residual is given. history [kernel-1][cin] holds the inputs before x;
+ * history_out receives the last kernel - 1 inputs after x (a different
+ * buffer). */
+int pgpu_conv1d(void *stream, const float *x, int positions, int cin, int cout, int kernel,
+                const float *weight, const float *bias, const float *history, float *history_out,
+                const float *residual, float *y, int *status);
+/* Causal ConvTranspose1d (stride 4..6, kernel 2 stride; weight
+ * [cin][kernel][cout]) of x [positions][cin] into y [positions*stride][cout];
+ * overlap [stride][cout] carries the previous position's right half in and
+ * the last position's out. */
+int pgpu_convtr1d(void *stream, const float *x, int positions, int cin, int cout, int stride,
+                  const float *weight, const float *bias, float *overlap, float *y, int *status);
+/* One frame of the depthwise upsample: kernel [channels][2 stride],
+ * output[o*channels + c] = previous[c]*k[c][stride+o] + input[c]*k[c][o]. */
+int pgpu_upsample_frame(void *stream, const float *kernel, const float *input,
+                        const float *previous, int channels, int stride, float *output,
+                        int *status);
+/* y = x <= 0 ? exp(x) - 1 : x, elementwise (y may be x). */
+int pgpu_elu(void *stream, const float *x, float *y, size_t count);
+
 /* -- batched prefill (pgpu_prefill.hip). M = streams pseudo-streams (one per
  * prompt position); split fragments as in pgpu_gemm_input.split, with M
  * rounded up to 16 rows in the allocation. -- */

@@ -103,4 +103,36 @@ int oracle_lsd_one_step(const OracleFlowHead *head, const float condition[512],
 int oracle_eos_logit(const float *weight, const float *bias, const float state[512],
                      float *raw_logit);
 
+
+/* Audio decoder (oracle_audio.c): Mimi latent transformer, SEANet
+ * convolutions and the latent -> PCM chain, weights decoded to fp32. */
+typedef struct {
+    const float *projection;                 /* [512][32] */
+    const float *upsample;                   /* [512][32]: taps 0..15 current, 16..31 previous */
+    const float *qkv[2], *out[2];            /* [1536][512], [512][512] */
+    const float *mlp_in[2], *mlp_out[2];     /* [2048][512], [512][2048] */
+    const float *norm1_weight[2], *norm1_bias[2], *norm2_weight[2], *norm2_bias[2];
+    const float *scale1[2], *scale2[2];      /* layer_scale_1 / _2, [512] each */
+    float rope_theta;
+} OracleMimi;
+typedef struct OracleMimiState OracleMimiState;
+typedef struct OracleConv OracleConv;
+int oracle_mimi_upsample_frame(const float *kernel, const float *input, const float *previous,
+                               size_t channels, size_t stride, float *output);
+OracleMimiState *oracle_mimi_create(const OracleMimi *model);
+void oracle_mimi_destroy(OracleMimiState *state);
+size_t oracle_mimi_positions(const OracleMimiState *state);
+int oracle_mimi_process(OracleMimiState *state, const float *latents, size_t frames,
+                        float *features);
+/* weight: Conv1d [out][in][kernel]; transposed [in][out][kernel]. */
+OracleConv *oracle_conv_create(const float *weight, const float *bias, size_t in, size_t out,
+                               size_t kernel, size_t stride, int transpose);
+void oracle_conv_destroy(OracleConv *conv);
+int oracle_conv_process(OracleConv *conv, const float *input, size_t positions, float *output);
+void oracle_conv_elu(float *values, size_t count);
+int oracle_residual_process(OracleConv *conv3, OracleConv *conv1, const float *input,
+                            size_t positions, float *output);
+int oracle_pcm_process(OracleMimiState *mimi, OracleConv *const conv[11], const float *latents,
+                       size_t frames, float *pcm);
+
 #endif

@@ -307,3 +307,148 @@ class ReferenceQ8:
         out = np.zeros(1, np.float32)
         ok = self.lib.phonon_q8_dot(blocks.ctypes.data, _ptr(x), x.size, _ptr(out))
         return bool(ok), out[0]
+
+
+# ------------------------------------------------------------ audio decoder
+class OracleMimi(ctypes.Structure):
+    """OracleMimi (oracle.h): fp32 weights of the Mimi latent transformer."""
+    _fields_ = [("projection", _f32p), ("upsample", _f32p), ("qkv", _f32p * 2),
+                ("out", _f32p * 2), ("mlp_in", _f32p * 2), ("mlp_out", _f32p * 2),
+                ("norm1_weight", _f32p * 2), ("norm1_bias", _f32p * 2),
+                ("norm2_weight", _f32p * 2), ("norm2_bias", _f32p * 2),
+                ("scale1", _f32p * 2), ("scale2", _f32p * 2), ("rope_theta", ctypes.c_float)]
+
+
+def _audio_lib(oracle: Oracle):
+    lib = oracle.lib
+    if getattr(lib, "_audio_ready", False):
+        return lib
+    sigs = {
+        "oracle_mimi_upsample_frame": (ctypes.c_int, [_f32p, _f32p, _f32p, _sz, _sz, _f32p]),
+        "oracle_mimi_create": (_vp, [ctypes.POINTER(OracleMimi)]),
+        "oracle_mimi_destroy": (None, [_vp]),
+        "oracle_mimi_positions": (_sz, [_vp]),
+        "oracle_mimi_process": (ctypes.c_int, [_vp, _f32p, _sz, _f32p]),
+        "oracle_conv_create": (_vp, [_f32p, _f32p, _sz, _sz, _sz, _sz, ctypes.c_int]),
+        "oracle_conv_destroy": (None, [_vp]),
+        "oracle_conv_process": (ctypes.c_int, [_vp, _f32p, _sz, _f32p]),
+        "oracle_conv_elu": (None, [_f32p, _sz]),
+        "oracle_residual_process": (ctypes.c_int, [_vp, _vp, _f32p, _sz, _f32p]),
+        "oracle_pcm_process": (ctypes.c_int, [_vp, _vp * 11, _f32p, _sz, _f32p]),
+    }
+    for name, (res, args) in sigs.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    lib._audio_ready = True
+    return lib
+
+
+def _f32(a) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+class MimiOracle:
+    """A Mimi request state over fp32 weights: `weights` holds projection
+    [512,32], upsample [512,32] and per layer l the keys qkv, out, mlp_in,
+    mlp_out, norm1_w, norm1_b, norm2_w, norm2_b, scale1, scale2 as
+    weights[l][key]."""
+
+    KEYS = ("qkv", "out", "mlp_in", "mlp_out", "norm1_w", "norm1_b", "norm2_w", "norm2_b",
+            "scale1", "scale2")
+
+    def __init__(self, oracle: Oracle, weights: dict, theta: float = 10000.0):
+        self.lib = _audio_lib(oracle)
+        self._keep = {k: _f32(weights[k]) for k in ("projection", "upsample")}
+        m = OracleMimi()
+        m.projection = _ptr(self._keep["projection"])
+        m.upsample = _ptr(self._keep["upsample"])
+        names = {"qkv": "qkv", "out": "out", "mlp_in": "mlp_in", "mlp_out": "mlp_out",
+                 "norm1_w": "norm1_weight", "norm1_b": "norm1_bias",
+                 "norm2_w": "norm2_weight", "norm2_b": "norm2_bias",
+                 "scale1": "scale1", "scale2": "scale2"}
+        for l in range(2):
+            for key, field in names.items():
+                arr = _f32(weights[l][key])
+                self._keep[(l, key)] = arr
+                getattr(m, field)[l] = _ptr(arr)
+        m.rope_theta = theta
+        self.model = m
+        self.state = self.lib.oracle_mimi_create(ctypes.byref(m))
+        assert self.state
+
+    def positions(self) -> int:
+        return self.lib.oracle_mimi_positions(self.state)
+
+    def process(self, latents):
+        x = _f32(latents).reshape(-1, 32)
+        out = np.zeros((x.shape[0] * 16, 512), np.float32)
+        ok = self.lib.oracle_mimi_process(self.state, _ptr(x), x.shape[0], _ptr(out))
+        return bool(ok), out
+
+    def close(self):
+        if self.state:
+            self.lib.oracle_mimi_destroy(self.state)
+            self.state = None
+
+
+class ConvOracle:
+    """A causal Conv1d (weight [out,in,kernel]) or transposed conv (weight
+    [in,out,kernel], stride s, kernel 2s) with its history."""
+
+    def __init__(self, oracle: Oracle, weight, bias, stride: int, transpose: bool):
+        self.lib = _audio_lib(oracle)
+        w = _f32(weight)
+        self.w, self.b = w, _f32(bias)
+        if transpose:
+            self.cin, self.cout, self.kernel = w.shape
+        else:
+            self.cout, self.cin, self.kernel = w.shape
+        self.stride = stride
+        self.conv = self.lib.oracle_conv_create(_ptr(self.w), _ptr(self.b), self.cin, self.cout,
+                                                self.kernel, stride, int(transpose))
+        assert self.conv
+
+    def process(self, x):
+        x = _f32(x).reshape(-1, self.cin)
+        y = np.zeros((x.shape[0] * self.stride, self.cout), np.float32)
+        ok = self.lib.oracle_conv_process(self.conv, _ptr(x), x.shape[0], _ptr(y))
+        return bool(ok), y
+
+    def close(self):
+        if self.conv:
+            self.lib.oracle_conv_destroy(self.conv)
+            self.conv = None
+
+
+def conv_elu(oracle: Oracle, x):
+    lib = _audio_lib(oracle)
+    y = _f32(x).copy()
+    lib.oracle_conv_elu(_ptr(y), y.size)
+    return y
+
+
+def residual_process(oracle: Oracle, conv3: ConvOracle, conv1: ConvOracle, x):
+    lib = _audio_lib(oracle)
+    x = _f32(x).reshape(-1, conv3.cin)
+    y = np.zeros_like(x)
+    ok = lib.oracle_residual_process(conv3.conv, conv1.conv, _ptr(x), x.shape[0], _ptr(y))
+    return bool(ok), y
+
+
+def mimi_upsample_frame(oracle: Oracle, kernel, x, previous, channels: int, stride: int):
+    lib = _audio_lib(oracle)
+    k, x, p = _f32(kernel), _f32(x), _f32(previous)
+    out = np.zeros(stride * channels, np.float32)
+    ok = lib.oracle_mimi_upsample_frame(_ptr(k), _ptr(x), _ptr(p), channels, stride, _ptr(out))
+    return bool(ok), out
+
+
+def pcm_process(oracle: Oracle, mimi: MimiOracle, convs, latents):
+    """convs: the eleven ConvOracle of the reference's model.conv[] order."""
+    lib = _audio_lib(oracle)
+    x = _f32(latents).reshape(-1, 32)
+    out = np.zeros(x.shape[0] * 1920, np.float32)
+    arr = (_vp * 11)(*[c.conv for c in convs])
+    ok = lib.oracle_pcm_process(mimi.state, arr, _ptr(x), x.shape[0], _ptr(out))
+    return bool(ok), out

@@ -103,6 +103,18 @@ class PgpuGemmInput(ctypes.Structure):
                 ("attn_positions", _vp), ("attn_max_splits", _i), ("rows", _vp)]
 
 
+class PhononMimiConfig(ctypes.Structure):
+    """PhononMimiConfig (phonon_mimi.h, src/phonon_mimi.h:10-16)."""
+    _fields_ = [("sample_rate", ctypes.c_uint), ("frame_rate", _f),
+                ("ratios", ctypes.c_uint * 3), ("context", _sz), ("rope_theta", _f)]
+
+
+class PhononMimiModel(ctypes.Structure):
+    """PhononMimiModel (phonon_mimi.h, src/phonon_mimi.h:17-24)."""
+    _fields_ = [("config", PhononMimiConfig), ("stride", _sz), ("projection", _TV),
+                ("upsample", _TV), ("layers", (_TV * 10) * 2)]
+
+
 CANCEL_POLL = ctypes.CFUNCTYPE(ctypes.c_int, _vp)
 _wp = ctypes.POINTER(PhononFlowLayerWeights)
 _cachep = ctypes.POINTER(PhononKvCache)
@@ -272,6 +284,48 @@ EXPORTS = {
     "phonon_flow_head_prepare": (_i, [_vp]),
     "phonon_flow_head_release": (None, [_vp]),
     "phonon_flow_head_device_create": (_i, [_vp, _vp, _vp, _sz, _pp]),
+    # phonon_mimi.h / phonon_conv.h / phonon_pcm.h
+    "phonon_mimi_config": (PhononMimiConfig, []),
+    "phonon_mimi_model_load": (_i, [_vp, ctypes.POINTER(PhononMimiConfig),
+                                    ctypes.POINTER(PhononMimiModel)]),
+    "phonon_mimi_state_create": (_i, [ctypes.POINTER(PhononMimiModel), _pp]),
+    "phonon_mimi_state_reset": (None, [_vp]),
+    "phonon_mimi_state_destroy": (None, [_vp]),
+    "phonon_mimi_positions": (_sz, [_vp]),
+    "phonon_mimi_process": (_i, [_vp, _fp, _sz, _fp, _sz]),
+    "phonon_mimi_upsample_frame": (_i, [_viewp, _fp, _fp, _sz, _sz, _fp]),
+    "phonon_conv_model_create": (_i, [_viewp, _viewp, _sz, _i, _pp]),
+    "phonon_conv_model_destroy": (None, [_vp]),
+    "phonon_conv_input_channels": (_sz, [_vp]),
+    "phonon_conv_output_channels": (_sz, [_vp]),
+    "phonon_conv_stride": (_sz, [_vp]),
+    "phonon_conv_state_create": (_i, [_vp, _pp]),
+    "phonon_conv_state_destroy": (None, [_vp]),
+    "phonon_conv_state_reset": (None, [_vp]),
+    "phonon_conv_process": (_i, [_vp, _fp, _sz, _fp, _sz]),
+    "phonon_conv_elu": (None, [_fp, _sz]),
+    "phonon_residual_state_create": (_i, [_vp, _vp, _pp]),
+    "phonon_residual_state_destroy": (None, [_vp]),
+    "phonon_residual_state_reset": (None, [_vp]),
+    "phonon_residual_process": (_i, [_vp, _fp, _sz, _fp, _sz]),
+    "phonon_pcm_model_create": (_i, [_vp, _pp]),
+    "phonon_pcm_model_destroy": (None, [_vp]),
+    "phonon_pcm_state_create": (_i, [_vp, _pp]),
+    "phonon_pcm_state_destroy": (None, [_vp]),
+    "phonon_pcm_state_reset": (None, [_vp]),
+    "phonon_pcm_samples": (_sz, [_vp]),
+    "phonon_pcm_process": (_i, [_vp, _fp, _sz, _fp, _sz, _fp, _sz]),
+    "phonon_pcm_finish": (_i, [_vp]),
+    "phonon_pcm_model_from_parts": (_i, [ctypes.POINTER(PhononMimiModel), _vp * 11, _pp]),
+    "pgpu_mimi_input": (_i, [_vp, _vp, _i, _vp, _vp, _vp, _vp, _vp]),
+    "pgpu_mimi_rope_store": (_i, [_vp, _vp, _i, ctypes.c_longlong, _vp, ctypes.c_longlong, _vp,
+                                  _vp, _i]),
+    "pgpu_mimi_attention": (_i, [_vp, _vp, _i, ctypes.c_longlong, _vp, _vp, _i, _i, _vp,
+                                 _vp]),
+    "pgpu_conv1d": (_i, [_vp, _vp, _i, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "pgpu_convtr1d": (_i, [_vp, _vp, _i, _i, _i, _i, _vp, _vp, _vp, _vp, _vp]),
+    "pgpu_upsample_frame": (_i, [_vp, _vp, _vp, _vp, _i, _i, _vp, _vp]),
+    "pgpu_elu": (_i, [_vp, _vp, _vp, _sz]),
     "phonon_flow_head_device_destroy": (None, [_vp]),
     "phonon_flow_head_device_lsd": (_i, [_vp, _sz, _vp, _vp, _f, _vp, _vp]),
     "phonon_flow_head_device_set_graph": (_i, [_vp, _i]),

@@ -134,7 +134,7 @@ extern "C" int pgpu_gemm_gated(void *stream, const pgpu_matrix *w, const pgpu_ge
                                int streams, const float *bias, const float *gate, int ld_gate,
                                const float *residual, float *out, int *status) {
     GemmArgs a;
-    if (!gate || !residual || ld_gate < (int)w->rows || ld_gate % 4 ||
+    if (!gate || !residual || (ld_gate != 0 && ld_gate < (int)w->rows) || ld_gate % 4 ||
         !base_args(a, w, in, streams, status))
         return bad_arguments("pgpu_gemm_gated");
     a.bias = bias;

@@ -74,6 +74,10 @@ int ph_vector_decode(const PhononTensorView *view, size_t count, float *host);
 void ph_rope_row(float theta, size_t position, size_t head_width, float *cos_sin);
 /* Device table [8192][32] of (cos, sin) for theta (cached per theta). */
 const float *ph_rope_table(float theta);
+/* The same for positions [0, PH_ROPE_LONG_ROWS): the Mimi transformer's
+ * 16 positions per latent frame, up to 8192 frames. */
+enum { PH_ROPE_LONG_ROWS = 8192 * 16 };
+const float *ph_rope_table_long(float theta);
 
 int ph_all_finite(const float *values, size_t count);
 int ph_overlap(const void *a, size_t a_bytes, const void *b, size_t b_bytes);

@@ -205,32 +205,35 @@ void ph_rope_row(float theta, size_t position, size_t head_width, float *cos_sin
 }
 
 /* Tables are immutable once built (captured graphs keep their address), one
- * per theta value, kept until the process ends. */
+ * per (theta, length), kept until the process ends. */
 enum { ROPE_TABLES = 8 };
 static pthread_mutex_t g_rope_lock = PTHREAD_MUTEX_INITIALIZER;
 static float g_rope_theta[ROPE_TABLES];
+static size_t g_rope_rows[ROPE_TABLES];
 static float *g_rope_dev[ROPE_TABLES];
 
-const float *ph_rope_table(float theta) {
+static const float *rope_table(float theta, size_t rows) {
     if (!(theta > 0.0f) || !isfinite(theta))
         return NULL;
     pthread_mutex_lock(&g_rope_lock);
     const float *found = NULL;
     size_t slot = 0;
     for (; slot < ROPE_TABLES && g_rope_dev[slot]; slot++)
-        if (g_rope_theta[slot] == theta) {
+        if (g_rope_theta[slot] == theta && g_rope_rows[slot] == rows) {
             found = g_rope_dev[slot];
             break;
         }
     if (!found && slot < ROPE_TABLES) {
-        const size_t floats = (size_t)PHONON_FLOW_MAX_POSITIONS * 32 * 2;
+        const size_t floats = rows * 32 * 2;
         float *host = malloc(floats * sizeof(float));
         float *dev = host ? pgpu_malloc(floats * sizeof(float)) : NULL;
         if (dev) {
-            for (size_t p = 0; p < PHONON_FLOW_MAX_POSITIONS; p++)
+            for (size_t p = 0; p < rows; p++)
                 ph_rope_row(theta, p, 64, host + p * 64);
-            if (pgpu_copy_h2d(g_stream, dev, host, floats * sizeof(float))) {
+            if (pgpu_copy_h2d(g_stream, dev, host, floats * sizeof(float)) &&
+                pgpu_stream_sync(g_stream)) {
                 g_rope_theta[slot] = theta;
+                g_rope_rows[slot] = rows;
                 g_rope_dev[slot] = dev;
                 found = dev;
             } else {
@@ -242,3 +245,7 @@ const float *ph_rope_table(float theta) {
     pthread_mutex_unlock(&g_rope_lock);
     return found;
 }
+
+const float *ph_rope_table(float theta) { return rope_table(theta, PHONON_FLOW_MAX_POSITIONS); }
+
+const float *ph_rope_table_long(float theta) { return rope_table(theta, PH_ROPE_LONG_ROWS); }

@@ -273,3 +273,92 @@ def kpack_synthetic():
     q8 = b"\x00\x3c" + b"\x01" * 32
     return [(f"flow_lm.fixture_{i:03d}.weight", KPACK_Q8, (1, 32), q8) if i < 36 else
             (f"mimi.fixture_{i:03d}.weight", KPACK_BF16, (1,), b"\x80\x3f") for i in range(209)]
+
+
+# ------------------------------------------------------ audio decoder models
+def mimi_identity_model(route_only: bool = False) -> dict:
+    """fp32 weights of the reference tests' synthetic Mimi models.
+
+    route_only=False: tests/test_phonon_mimi.c:74-98 - projection routes
+    channel i to latent i % 32, upsample taps 1 (current) and .5 (previous),
+    per layer V = identity, Q = K = 0, out = identity, LayerNorm weights 1,
+    layer_scale_1 = .5 / .25, MLP and layer_scale_2 zero.
+    route_only=True: tests/test_phonon_pcm.c:65-77 - only channel 0 carries
+    latent 0 through 16 current taps; every layer weight is zero."""
+    proj = np.zeros((512, 32), np.float32)
+    up = np.zeros((512, 32), np.float32)
+    if route_only:
+        proj[0, 0] = 1.0
+        up[0, :16] = 1.0
+    else:
+        proj[np.arange(512), np.arange(512) % 32] = 1.0
+        up[:, :16] = 1.0
+        up[:, 16:] = 0.5
+    model = {"projection": proj, "upsample": up}
+    for l in range(2):
+        layer = {"qkv": np.zeros((1536, 512), np.float32), "out": np.zeros((512, 512), np.float32),
+                 "mlp_in": np.zeros((2048, 512), np.float32),
+                 "mlp_out": np.zeros((512, 2048), np.float32)}
+        for key in ("norm1_w", "norm1_b", "norm2_w", "norm2_b", "scale1", "scale2"):
+            layer[key] = np.zeros(512, np.float32)
+        if not route_only:
+            layer["qkv"][1024 + np.arange(512), np.arange(512)] = 1.0
+            layer["out"][np.arange(512), np.arange(512)] = 1.0
+            layer["norm1_w"][:] = 1.0
+            layer["norm2_w"][:] = 1.0
+            layer["scale1"][:] = 0.25 if l else 0.5
+        model[l] = layer
+    return model
+
+
+def pcm_scalar_convs():
+    """The eleven convolutions of tests/test_phonon_pcm.c:31-49,78-86 as
+    (weight, bias, stride, transposed), in the reference's model.conv[]
+    order: conv0, then per stride 6, 5, 4 the transposed conv (channel-0
+    route: taps 1 for the current position, .5 for the overlap) and a zero
+    residual pair, then the final conv (taps 1 and .25)."""
+    def conv(cin, cout, kernel, stride, route):
+        trans = stride > 1
+        w = np.zeros((cin, cout, kernel) if trans else (cout, cin, kernel), np.float32)
+        flat = w.reshape(-1)
+        if route:
+            flat[0 if trans else kernel - 1] = 1.0
+            if trans:
+                flat[1:stride] = 1.0
+                flat[stride:kernel] = 0.5
+            elif cout == 1:
+                flat[kernel - 2] = 0.25
+        return w, np.zeros(cout, np.float32), stride, trans
+
+    out = [conv(512, 512, 7, 1, True)]
+    ch = 512
+    for s in (6, 5, 4):
+        out += [conv(ch, ch // 2, 2 * s, s, True), conv(ch // 2, ch // 4, 3, 1, False),
+                conv(ch // 4, ch // 2, 1, 1, False)]
+        ch //= 2
+    out.append(conv(64, 1, 3, 1, True))
+    return out
+
+
+def pcm_scalar_expected(x: np.ndarray) -> np.ndarray:
+    """tests/test_phonon_pcm.c:92-118: the sparse scalar graph's samples
+    (float32 arithmetic, ELU through expf)."""
+    f32 = np.float32
+    elu = lambda v: v if v > 0 else f32(np.expm1(np.float64(v)))  # noqa: E731
+    prev = [f32(0), f32(0), f32(0)]
+    last = f32(0)
+    out = []
+    for t in range(x.shape[0] * 16):
+        a = elu(f32(x[t // 16, 0]))
+        for _ in range(6):
+            b = elu(f32(a + prev[0]))
+            for _ in range(5):
+                d = elu(f32(b + prev[1]))
+                for _ in range(4):
+                    e = elu(f32(d + prev[2]))
+                    out.append(f32(e + f32(0.25) * last))
+                    last = e
+                prev[2] = f32(0.5) * d
+            prev[1] = f32(0.5) * b
+        prev[0] = f32(0.5) * a
+    return np.array(out, np.float32)
