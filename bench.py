@@ -679,6 +679,99 @@ def frame_loop_bench(pkg, lib, layers=12, streams=64, frames=30, warmup=3, seed=
             "clean": clean}
 
 
+def pcm_flops_per_frame():
+    """Algorithmic flops (2 per multiply-add) of one latent frame through
+    Mimi (16 rows, 2 layers, full 250-key window) and the SEANet decoder."""
+    mimi_rows = 16 * 2 * 2 * (1536 * 512 + 512 * 512 + 2048 * 512 + 512 * 2048)
+    mimi_attention = 16 * 2 * 2 * 2 * 250 * 512
+    mimi_input = 2 * 512 * 32 + 16 * 512 * 2 * 2
+    seanet = 16 * 2 * 512 * 512 * 7
+    positions, ch = 16, 512
+    for s in (6, 5, 4):
+        seanet += positions * 2 * ch * (ch // 2) * 2 * s      # transposed conv, 2s taps
+        positions *= s
+        ch //= 2
+        seanet += positions * 2 * (ch * (ch // 2) * 3 + (ch // 2) * ch)  # residual k3 + k1
+    seanet += positions * 2 * 64 * 3
+    return mimi_rows + mimi_attention + mimi_input + seanet
+
+
+def pcm_bench(pkg, lib, seed=31, frames=256, stream_frames=40):
+    """Latent frames -> 24 kHz PCM through phonon_pcm_process (Mimi and the
+    SEANet decoder on the GPU), random weights of the real shapes: one
+    request of `frames` frames, then frame-by-frame calls (streaming). Host
+    buffers go in and out inside each call, as the drop-in's contract has
+    it; the call returns when the samples are in host memory."""
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import helpers
+    views = pkg.Views()
+    mimi, model = helpers.pcm_model(lib, pkg, views, helpers.random_mimi(seed),
+                                    helpers.random_pcm_convs(seed + 1))
+    h = ctypes.c_void_p()
+    assert lib.phonon_pcm_state_create(model, ctypes.byref(h))
+    x = np.random.default_rng(seed + 2).standard_normal((frames, 32)).astype(np.float32)
+    raw = np.zeros(frames * 1920, np.float32)
+    fpp = lambda a: a.ctypes.data_as(ctypes.POINTER(ctypes.c_float))  # noqa: E731
+    assert lib.phonon_pcm_process(h, fpp(x), 32, fpp(raw), raw.size, None, 0)
+    lib.phonon_pcm_state_reset(h)
+    t0 = time.perf_counter()
+    assert lib.phonon_pcm_process(h, fpp(x), frames, fpp(raw), raw.size, None, 0)
+    bulk = time.perf_counter() - t0
+    lib.phonon_pcm_state_reset(h)
+    one = np.zeros(1920, np.float32)
+    per = []
+    for f in range(stream_frames):
+        xf = np.ascontiguousarray(x[f:f + 1])
+        t0 = time.perf_counter()
+        assert lib.phonon_pcm_process(h, fpp(xf), 1, fpp(one), one.size, None, 0)
+        per.append(time.perf_counter() - t0)
+    lib.phonon_pcm_state_destroy(h)
+    lib.phonon_pcm_model_destroy(model)
+    flops = pcm_flops_per_frame()
+    audio_s = frames / 12.5
+    return {"workload": f"latent -> PCM decoding (Mimi 2 layers + SEANet, 1920 samples per "
+                        f"frame), random BF16 weights of the real shapes; one request of "
+                        f"{frames} frames ({audio_s:.1f} s of audio), then {stream_frames} "
+                        f"one-frame calls",
+            "bulk_ms": round(bulk * 1e3, 2),
+            "bulk_frames_per_s": round(frames / bulk, 1),
+            "bulk_realtime_factor": round(audio_s / bulk, 1),
+            "stream_ms_per_frame_median": round(float(np.median(per)) * 1e3, 3),
+            "stream_ms_per_frame_p90": round(float(np.percentile(per, 90)) * 1e3, 3),
+            "flops_per_frame": flops,
+            "bulk_TFLOPs": round(flops * frames / bulk / 1e12, 2),
+            "note": "wall clock around the synchronous host-buffer call (PCIe copies "
+                    "included); the real-time budget is 80 ms of audio per frame"}
+
+
+def cpu_pcm(seed=31, budget_s=10.0):
+    """The oracle's latent -> PCM chain (Mimi and SEANet restated in C from
+    the reference's sequential code) on one thread, 2-frame calls."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import oracle_py
+    import helpers
+    oracle = oracle_py.Oracle()
+    om = oracle_py.MimiOracle(oracle, helpers.random_mimi(seed))
+    oc = [oracle_py.ConvOracle(oracle, w, b, s, t)
+          for (w, b, s, t) in helpers.random_pcm_convs(seed + 1)]
+    x = np.random.default_rng(seed + 2).standard_normal((4096, 32)).astype(np.float32)
+    frames, elapsed = 0, 0.0
+    while elapsed < budget_s:
+        t0 = time.perf_counter()
+        ok, _ = oracle_py.pcm_process(oracle, om, oc, x[frames:frames + 2])
+        elapsed += time.perf_counter() - t0
+        assert ok
+        frames += 2
+    for c in oc:
+        c.close()
+    om.close()
+    return {"value": round(frames / elapsed, 2), "unit": "frames/s", "cores": 1, "kind": "port",
+            "realtime_factor": round(frames / 12.5 / elapsed, 2),
+            "sample": f"{frames} latent frames through the oracle's Mimi + SEANet chain in "
+                      f"2-frame calls, {elapsed:.1f} s"}
+
+
 def attention_curve(pkg, lib, seed=9):
     """One attention layer decode (H=8, dh=64): append + attention per step,
     vs context length, as one 1-layer batched step of one stream."""
@@ -869,6 +962,8 @@ def main():
                     help="run only the B=256 decode + batched prefill workload")
     ap.add_argument("--flow-head", action="store_true",
                     help="run only the flow head LSD step measurement")
+    ap.add_argument("--pcm", action="store_true",
+                    help="run only the latent -> PCM decoding measurement")
     ap.add_argument("--pmc-program", action="store_true",
                     help="run only the attention kernel and a calibration copy, for "
                          "rocprofv3 --pmc passes")
@@ -897,6 +992,9 @@ def main():
         for mode in (int(m) for m in args.b1_modes.split(",")):
             print(json.dumps(dict(b1_with_prefill(pkg, lib, args.layers, args.seed, mode=mode),
                                   mode=mode)), flush=True)
+        return
+    if args.pcm:
+        print(json.dumps(pcm_bench(pkg, lib)), flush=True)
         return
     if args.flow_head:
         for shared, graph in ((True, 1), (True, 0), (False, 1)):
@@ -949,12 +1047,15 @@ def main():
                              "b1": flow_head_bench(pkg, lib, streams=1),
                              "frame_loop_b64": frame_loop_bench(pkg, lib)}
         log(f"flow head: {line['flow_head']}")
+        line["pcm_decode"] = pcm_bench(pkg, lib)
+        log(f"pcm decode: {line['pcm_decode']}")
         line["attention_layer_curve"] = attention_curve(pkg, lib)
         log(f"attention curve: {line['attention_layer_curve']}")
         line["cpu_baseline"] = cpu_baseline(pkg, lib, args.layers, lengths, args.seed)
         line["cpu_baseline"]["b1_one_core"] = cpu_b1_stack(args.layers, args.seed)
         line["cpu_baseline"]["q8_matvec_one_core"] = cpu_q8_matvec()
         line["cpu_baseline"]["flow_head"] = cpu_flow_head()
+        line["cpu_baseline"]["pcm_decode"] = cpu_pcm()
         log(f"cpu baseline: {line['cpu_baseline']}")
     print(json.dumps(line), flush=True)
 

@@ -275,24 +275,40 @@ int pgpu_mimi_rope_store(void *stream, float *qkv, int rows, long long first, co
                          long long rope_positions, float *ring_k, float *ring_v, int ring);
 /* softmax(q k / 8) v of each row over the keys of positions
  * max(0, p - context + 1) .. p (p = first + r) in the ring, into
- * out [rows][512]; ring >= rows + context - 1 and context <= 256. */
+ * out [rows][512]; rows a multiple of 16 (whole latent frames), ring >=
+ * rows + context - 1 and context <= 256. */
 int pgpu_mimi_attention(void *stream, const float *qkv, int rows, long long first,
                         const float *ring_k, const float *ring_v, int ring, int context,
                         float *out, int *status);
-/* Causal Conv1d (kernel 1, 3 or 7; weight [cin][kernel][cout], bias [cout])
- * of x [positions][cin] into y [positions][cout], y = residual + (dot + bias)
- * when residual is given. history [kernel-1][cin] holds the inputs before x;
- * history_out receives the last kernel - 1 inputs after x (a different
- * buffer). */
-int pgpu_conv1d(void *stream, const float *x, int positions, int cin, int cout, int kernel,
-                const float *weight, const float *bias, const float *history, float *history_out,
-                const float *residual, float *y, int *status);
-/* Causal ConvTranspose1d (stride 4..6, kernel 2 stride; weight
- * [cin][kernel][cout]) of x [positions][cin] into y [positions*stride][cout];
- * overlap [stride][cout] carries the previous position's right half in and
- * the last position's out. */
-int pgpu_convtr1d(void *stream, const float *x, int positions, int cin, int cout, int stride,
-                  const float *weight, const float *bias, float *overlap, float *y, int *status);
+/* One SEANet convolution on the device. A causal Conv1d (stride 1, kernel
+ * K in {1, 3, 7}) reads taps = K input rows per output row; a causal
+ * ConvTranspose1d (stride s in 4..6, kernel 2s) reads taps = 2 (rows t - 1
+ * and t) and writes s output positions per input row, as the ncols =
+ * s * cout columns (k * cout + o: position t*s + k, channel o) of output
+ * row t. Either: `fragments` (cin % 32 == 0): the bf16 weights in MFMA
+ * operand order, [P/16][taps*cin/32] records of 64 lanes x 8 bf16, P being
+ * ncols rounded up to 32 (lane l of record (i, b): column 16 i + l % 16,
+ * zero past ncols, reduction index 32 b + 8 (l / 16) .. +7, index = tap *
+ * cin + channel, tap 0 reading row t - taps + 1); or `weight`: fp32
+ * [cin][K][cout] for the sequential path. bias [cout]. */
+typedef struct {
+    int cin, cout, kernel, stride, transpose, taps, ncols;
+    const uint16_t *fragments;
+    const float *weight;
+    const float *bias;
+} pgpu_conv_layer;
+/* x [positions][cin] -> y [positions][ncols]: y = (residual +) (conv +
+ * bias), ELU (x <= 0 ? exp(x) - 1 : x) applied to every input value first
+ * when elu is set. Input rows before x come from history [taps-1][cin];
+ * history_out (a different buffer) receives the last taps - 1 input rows
+ * of [history | x] (unused when taps == 1). With fragments: the MFMA path
+ * (bf16 weights times a three-term bf16 split of each input value, fp32
+ * accumulation in a fixed order per layer shape); else one fp32 multiply
+ * and add per term in the order input channel, then tap (transposed: the
+ * current row's sum plus the previous row's). */
+int pgpu_conv_rows(void *stream, const pgpu_conv_layer *layer, const float *x, int positions,
+                   const float *history, float *history_out, const float *residual, int elu,
+                   float *y, int *status);
 /* One frame of the depthwise upsample: kernel [channels][2 stride],
  * output[o*channels + c] = previous[c]*k[c][stride+o] + input[c]*k[c][o]. */
 int pgpu_upsample_frame(void *stream, const float *kernel, const float *input,

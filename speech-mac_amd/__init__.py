@@ -103,6 +103,12 @@ class PgpuGemmInput(ctypes.Structure):
                 ("attn_positions", _vp), ("attn_max_splits", _i), ("rows", _vp)]
 
 
+class PgpuConvLayer(ctypes.Structure):
+    """pgpu_conv_layer (phonon_gpu.h)."""
+    _fields_ = [("cin", _i), ("cout", _i), ("kernel", _i), ("stride", _i), ("transpose", _i),
+                ("taps", _i), ("ncols", _i), ("fragments", _vp), ("weight", _vp), ("bias", _vp)]
+
+
 class PhononMimiConfig(ctypes.Structure):
     """PhononMimiConfig (phonon_mimi.h, src/phonon_mimi.h:10-16)."""
     _fields_ = [("sample_rate", ctypes.c_uint), ("frame_rate", _f),
@@ -322,8 +328,8 @@ EXPORTS = {
                                   _vp, _i]),
     "pgpu_mimi_attention": (_i, [_vp, _vp, _i, ctypes.c_longlong, _vp, _vp, _i, _i, _vp,
                                  _vp]),
-    "pgpu_conv1d": (_i, [_vp, _vp, _i, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
-    "pgpu_convtr1d": (_i, [_vp, _vp, _i, _i, _i, _i, _vp, _vp, _vp, _vp, _vp]),
+    "pgpu_conv_rows": (_i, [_vp, ctypes.POINTER(PgpuConvLayer), _vp, _i, _vp, _vp, _vp, _i, _vp,
+                            _vp]),
     "pgpu_upsample_frame": (_i, [_vp, _vp, _vp, _vp, _i, _i, _vp, _vp]),
     "pgpu_elu": (_i, [_vp, _vp, _vp, _sz]),
     "phonon_flow_head_device_destroy": (None, [_vp]),

@@ -93,135 +93,329 @@ __global__ __launch_bounds__(256) void k_mimi_rope_store(float *__restrict__ qkv
     ring_v[slot + 2 * i + 1] = row[2 * kWidth + 2 * i + 1];
 }
 
-// Windowed causal attention: one wave per (row, head). Row r (position
-// p = first + r) attends the keys of positions max(0, p - context + 1) .. p.
-// Lane j scores keys j, j + 64, ...; the exponentials go through LDS and
-// lane d accumulates output dimension d.
-__global__ __launch_bounds__(64) void k_mimi_attention(const float *__restrict__ qkv,
-                                                       long long first,
-                                                       const float *__restrict__ ring_k,
-                                                       const float *__restrict__ ring_v, int ring,
-                                                       int context, float *__restrict__ out,
-                                                       int *status) {
-    __shared__ float weights[256];
-    __shared__ float q[kHeadDim];
-    const int r = blockIdx.x, head = blockIdx.y, lane = threadIdx.x;
-    const long long pos = first + r;
-    const int count = (int)(pos + 1 < context ? pos + 1 : context);
-    const long long start = pos + 1 - count;
-    q[lane] = qkv[(size_t)r * 3 * kWidth + head * kHeadDim + lane];
-    __syncthreads();
-    float mx = -INFINITY;
-    float s[4];
-#pragma unroll
-    for (int u = 0; u < 4; u++) {
-        const int key = lane + 64 * u;
-        s[u] = -INFINITY;
-        if (key < count) {
-            const float *k = ring_k + (size_t)((start + key) % ring) * kWidth + head * kHeadDim;
-            float dot = 0.0f;
-#pragma unroll 8
-            for (int d = 0; d < kHeadDim; d++) dot = dot + q[d] * k[d];
-            s[u] = dot * 0.125f;
-            mx = fmaxf(mx, s[u]);
-        }
+// Windowed causal attention of one latent frame's 16 rows and one head per
+// work-group: row i (position p = first + 16 f + i) attends the keys of
+// positions max(0, p - context + 1) .. p. The frame's key window (at most
+// context + 15 positions) goes through LDS in chunks of 64 keys: scores
+// (one thread per (key, 4 rows), q . k over the 64 dimensions in order,
+// times 1/8), a masked softmax per row (one wave per 4 rows), then the
+// value sums (one thread per (dimension, 4 rows), keys in order), scaled
+// by 1/total at the end.
+constexpr int kAttnChunk = 64;
+constexpr int kAttnKeys = 256 + 16;  // context <= 256, plus the frame's rows
+
+__global__ __launch_bounds__(256) void k_mimi_attention(const float *__restrict__ qkv,
+                                                        long long first,
+                                                        const float *__restrict__ ring_k,
+                                                        const float *__restrict__ ring_v,
+                                                        int ring, int context,
+                                                        float *__restrict__ out, int *status) {
+    __shared__ float q[16][kHeadDim];
+    __shared__ float kv[kAttnChunk][kHeadDim + 1];
+    __shared__ float sc[16][kAttnKeys];
+    __shared__ float totals[16];
+    const int f = blockIdx.x, head = blockIdx.y, t = threadIdx.x;
+    const int wave = t >> 6, lane = t & 63;
+    const long long p0 = first + 16LL * f;
+    const long long kstart = p0 - (context - 1) > 0 ? p0 - (context - 1) : 0;
+    const int nkeys = (int)(p0 + 16 - kstart);
+    {
+        const int row = t >> 4, d = (t & 15) * 4;
+        const float4 v = *(const float4 *)(qkv + (size_t)(16 * f + row) * 3 * kWidth +
+                                           head * kHeadDim + d);
+        q[row][d] = v.x; q[row][d + 1] = v.y; q[row][d + 2] = v.z; q[row][d + 3] = v.w;
     }
+    const int kk = t & 63, rg = (t >> 6) * 4;  // score / output thread roles
+    for (int c0 = 0; c0 < nkeys; c0 += kAttnChunk) {
+        {
+            const int key = t >> 2, d = (t & 3) * 16;
+            if (c0 + key < nkeys) {
+                const float4 *src = (const float4 *)(ring_k + (size_t)((kstart + c0 + key) % ring) *
+                                                                  kWidth + head * kHeadDim + d);
 #pragma unroll
-    for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
-    float total = 0.0f;
+                for (int u = 0; u < 4; u++) {
+                    const float4 v = src[u];
+                    kv[key][d + 4 * u] = v.x; kv[key][d + 4 * u + 1] = v.y;
+                    kv[key][d + 4 * u + 2] = v.z; kv[key][d + 4 * u + 3] = v.w;
+                }
+            }
+        }
+        __syncthreads();
+        if (c0 + kk < nkeys) {
+            const long long kpos = kstart + c0 + kk;
+            float dot[4] = {0.f, 0.f, 0.f, 0.f};
+            for (int d = 0; d < kHeadDim; d++) {
+                const float kd = kv[kk][d];
 #pragma unroll
-    for (int u = 0; u < 4; u++) {
-        const int key = lane + 64 * u;
-        if (key < count) {
-            const float e = expf(s[u] - mx);
-            weights[key] = e;
+                for (int i = 0; i < 4; i++) dot[i] = dot[i] + q[rg + i][d] * kd;
+            }
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const long long p = p0 + rg + i;
+                sc[rg + i][c0 + kk] = kpos <= p && kpos > p - context ? dot[i] * 0.125f : -INFINITY;
+            }
+        }
+        __syncthreads();
+    }
+    // Masked softmax: wave w takes rows 4w .. 4w+3.
+    for (int i = 0; i < 4; i++) {
+        const int row = wave * 4 + i;
+        float mx = -INFINITY;
+        for (int j = lane; j < nkeys; j += 64) mx = fmaxf(mx, sc[row][j]);
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+        float total = 0.0f;
+        for (int j = lane; j < nkeys; j += 64) {
+            const float s = sc[row][j];
+            const float e = s == -INFINITY ? 0.0f : expf(s - mx);
+            sc[row][j] = e;
             total += e;
         }
-    }
 #pragma unroll
-    for (int off = 32; off > 0; off >>= 1) total += __shfl_xor(total, off);
-    __syncthreads();
-    float acc = 0.0f;
-    for (int key = 0; key < count; key++)
-        acc = acc + weights[key] * ring_v[(size_t)((start + key) % ring) * kWidth + head * kHeadDim + lane];
-    const float v = acc * (1.0f / total);
-    out[(size_t)r * kWidth + head * kHeadDim + lane] = v;
-    flag_nonfinite(status, !isfinite(v) || !(total > 0.0f) || !isfinite(mx));
+        for (int off = 32; off > 0; off >>= 1) total += __shfl_xor(total, off);
+        if (lane == 0) totals[row] = total;
+    }
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+    for (int c0 = 0; c0 < nkeys; c0 += kAttnChunk) {
+        __syncthreads();  // scores final / previous chunk consumed
+        {
+            const int key = t >> 2, d = (t & 3) * 16;
+            if (c0 + key < nkeys) {
+                const float4 *src = (const float4 *)(ring_v + (size_t)((kstart + c0 + key) % ring) *
+                                                                  kWidth + head * kHeadDim + d);
+#pragma unroll
+                for (int u = 0; u < 4; u++) {
+                    const float4 v = src[u];
+                    kv[key][d + 4 * u] = v.x; kv[key][d + 4 * u + 1] = v.y;
+                    kv[key][d + 4 * u + 2] = v.z; kv[key][d + 4 * u + 3] = v.w;
+                }
+            }
+        }
+        __syncthreads();
+        const int n = nkeys - c0 < kAttnChunk ? nkeys - c0 : kAttnChunk;
+        for (int j = 0; j < n; j++) {
+            const float vd = kv[j][kk];
+#pragma unroll
+            for (int i = 0; i < 4; i++) acc[i] = acc[i] + sc[rg + i][c0 + j] * vd;
+        }
+    }
+    bool bad = false;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const float total = totals[rg + i];
+        const float v = acc[i] * (1.0f / total);
+        out[(size_t)(16 * f + rg + i) * kWidth + head * kHeadDim + kk] = v;
+        bad |= !isfinite(v) || !(total > 0.0f);
+    }
+    flag_nonfinite(status, bad);
 }
 
-// Causal Conv1d: y[t][o] = (sum_{c,k} W[o][c][k] in[t + k - (K-1)][c]) + b[o]
-// (+ residual[t][o] first when given: y = residual + (dot + b)). w is
-// [cin][K][cout]; in[j] for j < 0 is history row K - 1 + j ([K-1][cin]).
-__global__ __launch_bounds__(256) void k_conv1d(const float *__restrict__ x, int cin, int cout,
-                                                int kernel, const float *__restrict__ w,
-                                                const float *__restrict__ bias,
-                                                const float *__restrict__ history,
-                                                const float *__restrict__ residual,
-                                                float *__restrict__ y, int *status) {
-    const int t = blockIdx.x, o = blockIdx.y * 256 + threadIdx.x;
-    if (o >= cout) return;
+__device__ inline float elu1(float v) { return v <= 0.0f ? expf(v) - 1.0f : v; }
+
+// Input row r of a convolution call: x[r] for r >= 0, else history row
+// taps - 1 + r (the rows of earlier calls).
+__device__ inline const float *conv_row(const float *x, const float *history, int taps, int cin,
+                                        int r) {
+    return r < 0 ? history + (size_t)(taps - 1 + r) * cin : x + (size_t)r * cin;
+}
+
+// The state's next history, written by the call's first work-group: the
+// last `keep` rows of [history | x] (x has n rows) into `fresh`, a buffer
+// that no work-group of the call reads.
+__device__ inline void copy_history(const float *__restrict__ x, int n, int cin, int keep,
+                                    const float *__restrict__ old, float *__restrict__ fresh) {
+    if (keep <= 0 || blockIdx.x != 0 || blockIdx.y != 0 || blockIdx.z != 0) return;
+    for (int i = threadIdx.x; i < keep * cin; i += blockDim.x) {
+        const int row = i / cin, c = i % cin;
+        const int j = n - keep + row;  // index into [history | x] relative to x
+        fresh[i] = j < 0 ? old[(size_t)(keep + j) * cin + c] : x[(size_t)j * cin + c];
+    }
+}
+
+// Sequential Conv1d: y[t][o] = (residual[t][o] +) (sum_{c,k} W[o][c][k]
+// in(t + k - (K-1))[c] + b[o]), one thread per (t, o); w is [cin][K][cout].
+__global__ __launch_bounds__(256) void k_conv_seq(const float *__restrict__ x, int positions,
+                                                  int cin, int cout, int kernel,
+                                                  const float *__restrict__ w,
+                                                  const float *__restrict__ bias,
+                                                  const float *__restrict__ history,
+                                                  float *__restrict__ history_out,
+                                                  const float *__restrict__ residual, int elu,
+                                                  float *__restrict__ y, int *status) {
+    copy_history(x, positions, cin, kernel - 1, history, history_out);
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= (size_t)positions * cout) return;
+    const int t = (int)(i / cout), o = (int)(i % cout);
     float dot = 0.0f;
     for (int c = 0; c < cin; c++)
         for (int k = 0; k < kernel; k++) {
-            const int j = t + k - (kernel - 1);
-            const float v = j < 0 ? history[(size_t)(kernel - 1 + j) * cin + c] : x[(size_t)j * cin + c];
+            float v = conv_row(x, history, kernel, cin, t + k - (kernel - 1))[c];
+            if (elu) v = elu1(v);
             dot = dot + w[((size_t)c * kernel + k) * cout + o] * v;
         }
     float out = dot + bias[o];
-    if (residual) out = residual[(size_t)t * cout + o] + out;
-    y[(size_t)t * cout + o] = out;
+    if (residual) out = residual[i] + out;
+    y[i] = out;
     flag_nonfinite(status, !isfinite(out));
 }
 
-// New history: the last K-1 rows of [history | x] (positions n).
-__global__ void k_conv_history(const float *__restrict__ x, int n, int cin, int keep,
-                               const float *__restrict__ old, float *__restrict__ fresh) {
-    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= (size_t)keep * cin) return;
-    const int row = (int)(i / cin), c = (int)(i % cin);
-    const int j = n - keep + row;  // index into [history | x] relative to x
-    fresh[i] = j < 0 ? old[(size_t)(keep + j) * cin + c] : x[(size_t)j * cin + c];
-}
-
-// Causal ConvTranspose1d (stride s, kernel 2s): column (t, o, k) =
-// sum_c W[c][o][k] x[t][c]; y[t s + k][o] = (col(t, o, k) + col(t-1, o, s+k))
-// + b[o], col(-1, .) being the state's overlap. w is [cin][2s][cout].
-__global__ __launch_bounds__(256) void k_convtr1d(const float *__restrict__ x, int cin, int cout,
-                                                  int stride, const float *__restrict__ w,
-                                                  const float *__restrict__ bias,
-                                                  const float *__restrict__ overlap,
-                                                  float *__restrict__ y, int *status) {
-    const int t = blockIdx.x, k = blockIdx.z, o = blockIdx.y * 256 + threadIdx.x;
-    if (o >= cout) return;
+// Sequential ConvTranspose1d (stride s, kernel 2s): column sums
+// col(t, o, k) = sum_c W[c][o][k] in(t)[c], then y[t s + k][o] =
+// (col(t, o, k) + col(t - 1, o, s + k)) + b[o]; in(-1) is the history row.
+__global__ __launch_bounds__(256) void k_convtr_seq(const float *__restrict__ x, int positions,
+                                                    int cin, int cout, int stride,
+                                                    const float *__restrict__ w,
+                                                    const float *__restrict__ bias,
+                                                    const float *__restrict__ history,
+                                                    float *__restrict__ history_out, int elu,
+                                                    float *__restrict__ y, int *status) {
+    copy_history(x, positions, cin, 1, history, history_out);
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= (size_t)positions * stride * cout) return;
+    const int o = (int)(i % cout), k = (int)(i / cout % stride), t = (int)(i / cout / stride);
     const int kernel = 2 * stride;
-    float col = 0.0f;
-    for (int c = 0; c < cin; c++)
-        col = col + w[((size_t)c * kernel + k) * cout + o] * x[(size_t)t * cin + c];
-    float prev;
-    if (t == 0) {
-        prev = overlap[(size_t)k * cout + o];
-    } else {
-        prev = 0.0f;
-        for (int c = 0; c < cin; c++)
-            prev = prev + w[((size_t)c * kernel + stride + k) * cout + o] * x[(size_t)(t - 1) * cin + c];
+    const float *cur = x + (size_t)t * cin, *prev = conv_row(x, history, 2, cin, t - 1);
+    float col = 0.0f, old = 0.0f;
+    for (int c = 0; c < cin; c++) {
+        const float v = elu ? elu1(cur[c]) : cur[c];
+        col = col + w[((size_t)c * kernel + k) * cout + o] * v;
     }
-    const float out = (col + prev) + bias[o];
-    y[((size_t)t * stride + k) * cout + o] = out;
+    for (int c = 0; c < cin; c++) {
+        const float v = elu ? elu1(prev[c]) : prev[c];
+        old = old + w[((size_t)c * kernel + stride + k) * cout + o] * v;
+    }
+    const float out = (col + old) + bias[o];
+    y[i] = out;
     flag_nonfinite(status, !isfinite(out));
 }
 
-// The overlap the next call starts from: col(n - 1, o, s + k).
-__global__ __launch_bounds__(256) void k_convtr_tail(const float *__restrict__ x, int n, int cin,
-                                                     int cout, int stride,
-                                                     const float *__restrict__ w,
-                                                     float *__restrict__ overlap) {
-    const int k = blockIdx.x, o = blockIdx.y * 256 + threadIdx.x;
-    if (o >= cout) return;
-    const int kernel = 2 * stride;
-    float col = 0.0f;
-    for (int c = 0; c < cin; c++)
-        col = col + w[((size_t)c * kernel + stride + k) * cout + o] * x[(size_t)(n - 1) * cin + c];
-    overlap[(size_t)k * cout + o] = col;
+// MFMA convolution (pgpu_conv_rows with fragments). A wave computes a
+// 32-row x 32-column tile (columns past ncols have zero weights and are not
+// stored) as 2 x 2 blocks of v_mfma_f32_16x16x32_bf16:
+// A = weight fragments (16 columns x 32 reduction indices), B = 16 input
+// rows x 32 channels of one tap, split into three bf16 terms (hi, mid, lo:
+// exact), each term one MFMA into the same accumulator. KS = 1: the four
+// waves of a work-group take four row tiles, each the whole reduction;
+// KS = 4: they take quarters of the reduction of one tile and wave 0 adds
+// the partial sums in wave order. Either way an output's arithmetic does
+// not depend on how many rows a call has.
+template <int KS>
+__global__ __launch_bounds__(256) void k_conv_mfma(const float *__restrict__ x, int positions,
+                                                   int cin, int cout, int taps, int ncols,
+                                                   const uint16_t *__restrict__ frag,
+                                                   const float *__restrict__ bias,
+                                                   const float *__restrict__ history,
+                                                   float *__restrict__ history_out,
+                                                   const float *__restrict__ residual, int elu,
+                                                   float *__restrict__ y, int *status) {
+    __shared__ f32x4 part[KS > 1 ? 3 * 4 * 64 : 1];
+    copy_history(x, positions, cin, taps - 1, history, history_out);
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int t0 = (KS > 1 ? blockIdx.x : blockIdx.x * 4 + wave) * 32;
+    const int ct0 = blockIdx.y * 2;  // first 16-column tile
+    const int cbn = cin >> 5, kbn = taps * cbn;
+    const int kb0 = KS > 1 ? kbn * wave / KS : 0, kb1 = KS > 1 ? kbn * (wave + 1) / KS : kbn;
+    f32x4 acc[2][2];
+#pragma unroll
+    for (int p = 0; p < 2; p++)
+#pragma unroll
+        for (int q = 0; q < 2; q++) acc[p][q] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const bool rows_live = t0 < positions;
+    if (rows_live) {
+        for (int kb = kb0; kb < kb1; kb++) {
+            const int tap = kb / cbn, c = (kb - tap * cbn) * 32 + 8 * (lane >> 4);
+            bf16x8 xs[2][3];
+#pragma unroll
+            for (int p = 0; p < 2; p++) {
+                const int t = t0 + p * 16 + (lane & 15);
+                float v[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+                if (t < positions) {
+                    const float4 *src =
+                        (const float4 *)(conv_row(x, history, taps, cin, t + tap - (taps - 1)) + c);
+                    const float4 lo4 = src[0], hi4 = src[1];
+                    v[0] = lo4.x; v[1] = lo4.y; v[2] = lo4.z; v[3] = lo4.w;
+                    v[4] = hi4.x; v[5] = hi4.y; v[6] = hi4.z; v[7] = hi4.w;
+                    if (elu) {
+#pragma unroll
+                        for (int e = 0; e < 8; e++) v[e] = elu1(v[e]);
+                    }
+                }
+                uint16_t h[8], m[8], l[8];
+#pragma unroll
+                for (int e = 0; e < 8; e++) split3(v[e], h[e], m[e], l[e]);
+                uint4 qh, qm, ql;
+                qh.x = h[0] | (uint32_t)h[1] << 16; qh.y = h[2] | (uint32_t)h[3] << 16;
+                qh.z = h[4] | (uint32_t)h[5] << 16; qh.w = h[6] | (uint32_t)h[7] << 16;
+                qm.x = m[0] | (uint32_t)m[1] << 16; qm.y = m[2] | (uint32_t)m[3] << 16;
+                qm.z = m[4] | (uint32_t)m[5] << 16; qm.w = m[6] | (uint32_t)m[7] << 16;
+                ql.x = l[0] | (uint32_t)l[1] << 16; ql.y = l[2] | (uint32_t)l[3] << 16;
+                ql.z = l[4] | (uint32_t)l[5] << 16; ql.w = l[6] | (uint32_t)l[7] << 16;
+                xs[p][0] = __builtin_bit_cast(bf16x8, qh);
+                xs[p][1] = __builtin_bit_cast(bf16x8, qm);
+                xs[p][2] = __builtin_bit_cast(bf16x8, ql);
+            }
+#pragma unroll
+            for (int q = 0; q < 2; q++) {
+                const bf16x8 wa = *(const bf16x8 *)(frag + (((size_t)(ct0 + q) * kbn + kb) * 64 +
+                                                            lane) * 8);
+#pragma unroll
+                for (int p = 0; p < 2; p++) {
+                    acc[p][q] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wa, xs[p][0], acc[p][q], 0, 0, 0);
+                    acc[p][q] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wa, xs[p][1], acc[p][q], 0, 0, 0);
+                    acc[p][q] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wa, xs[p][2], acc[p][q], 0, 0, 0);
+                }
+            }
+        }
+    }
+    if constexpr (KS > 1) {
+        if (wave > 0) {
+#pragma unroll
+            for (int p = 0; p < 2; p++)
+#pragma unroll
+                for (int q = 0; q < 2; q++) part[((wave - 1) * 4 + p * 2 + q) * 64 + lane] = acc[p][q];
+        }
+        __syncthreads();
+        if (wave > 0) return;
+#pragma unroll
+        for (int w = 0; w < 3; w++)
+#pragma unroll
+            for (int p = 0; p < 2; p++)
+#pragma unroll
+                for (int q = 0; q < 2; q++) {
+                    const f32x4 o = part[(w * 4 + p * 2 + q) * 64 + lane];
+#pragma unroll
+                    for (int r = 0; r < 4; r++) acc[p][q][r] = __fadd_rn(acc[p][q][r], o[r]);
+                }
+    }
+    if (!rows_live) return;
+    bool bad = false;
+#pragma unroll
+    for (int p = 0; p < 2; p++) {
+        const int t = t0 + p * 16 + (lane & 15);
+        if (t >= positions) continue;
+#pragma unroll
+        for (int q = 0; q < 2; q++) {
+            const int col = (ct0 + q) * 16 + 4 * (lane >> 4);
+            if (col >= ncols) continue;
+            const size_t at = (size_t)t * ncols + col;
+            float o[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                if (col + r >= ncols) break;
+                o[r] = __fadd_rn(acc[p][q][r], bias[(col + r) % cout]);
+                if (residual) o[r] = __fadd_rn(residual[at + r], o[r]);
+                bad |= !isfinite(o[r]);
+            }
+            if ((ncols & 3) == 0) {
+                *(float4 *)(y + at) = make_float4(o[0], o[1], o[2], o[3]);
+            } else {
+#pragma unroll
+                for (int r = 0; r < 4; r++)
+                    if (col + r < ncols) y[at + r] = o[r];
+            }
+        }
+    }
+    flag_nonfinite(status, bad);
 }
 
 // x <= 0 -> exp(x) - 1 (y may be x).
@@ -291,46 +485,53 @@ extern "C" int pgpu_mimi_rope_store(void *stream, float *qkv, int rows, long lon
 extern "C" int pgpu_mimi_attention(void *stream, const float *qkv, int rows, long long first,
                                    const float *ring_k, const float *ring_v, int ring,
                                    int context, float *out, int *status) {
-    if (!qkv || rows <= 0 || rows > 65535 || first < 0 || !ring_k || !ring_v || context <= 0 ||
-        context > 256 || ring < rows + context - 1 || !out || !status)
+    if (!qkv || rows <= 0 || rows % 16 || rows > 65535 || first < 0 || !ring_k || !ring_v ||
+        context <= 0 || context > 256 || ring < rows + context - 1 || !out || !status)
         return bad_arguments("pgpu_mimi_attention");
-    hipLaunchKernelGGL(k_mimi_attention, dim3(rows, kHeads), dim3(64), 0, (hipStream_t)stream,
-                       qkv, first, ring_k, ring_v, ring, context, out, status);
+    hipLaunchKernelGGL(k_mimi_attention, dim3(rows / 16, kHeads), dim3(256), 0,
+                       (hipStream_t)stream, qkv, first, ring_k, ring_v, ring, context, out, status);
     return launch_ok("pgpu_mimi_attention");
 }
 
-extern "C" int pgpu_conv1d(void *stream, const float *x, int positions, int cin, int cout,
-                           int kernel, const float *weight, const float *bias,
-                           const float *history, float *history_out, const float *residual,
-                           float *y, int *status) {
-    if (!x || positions <= 0 || positions > 65535 || cin <= 0 || cin > 512 || cout <= 0 ||
-        cout > 512 || (kernel != 1 && kernel != 3 && kernel != 7) || !weight || !bias ||
-        (kernel > 1 && (!history || !history_out)) || !y || !status)
-        return bad_arguments("pgpu_conv1d");
-    hipLaunchKernelGGL(k_conv1d, dim3(positions, (cout + 255) / 256), dim3(256), 0,
-                       (hipStream_t)stream, x, cin, cout, kernel, weight, bias, history, residual,
-                       y, status);
-    if (kernel > 1) {
-        const size_t n = (size_t)(kernel - 1) * cin;
-        hipLaunchKernelGGL(k_conv_history, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
-                           (hipStream_t)stream, x, positions, cin, kernel - 1, history,
-                           history_out);
+extern "C" int pgpu_conv_rows(void *stream, const pgpu_conv_layer *L, const float *x,
+                              int positions, const float *history, float *history_out,
+                              const float *residual, int elu, float *y, int *status) {
+    if (!L || !x || positions <= 0 || !y || !status || L->cin <= 0 || L->cin > 512 ||
+        L->cout <= 0 || L->cout > 512 || !L->bias)
+        return bad_arguments("pgpu_conv_rows");
+    const bool tr = L->transpose != 0;
+    const bool shape_ok = tr ? (L->stride >= 4 && L->stride <= 6 && L->kernel == 2 * L->stride &&
+                                L->taps == 2 && L->ncols == L->stride * L->cout)
+                             : (L->stride == 1 && (L->kernel == 1 || L->kernel == 3 ||
+                                                   L->kernel == 7) &&
+                                L->taps == L->kernel && L->ncols == L->cout);
+    const size_t outs = (size_t)positions * L->ncols;
+    if (!shape_ok || (L->taps > 1 && (!history || !history_out)) ||
+        (tr && residual) || (L->fragments && L->cin % 32) ||
+        (!L->fragments && !L->weight) || outs > (size_t)0x7fffffff)
+        return bad_arguments("pgpu_conv_rows");
+    hipStream_t st = (hipStream_t)stream;
+    if (L->fragments) {
+        const int kbn = L->taps * L->cin / 32, tiles = (positions + 31) / 32;
+        const int col_tiles = (L->ncols + 31) / 32;
+        if (kbn >= 16)
+            hipLaunchKernelGGL(k_conv_mfma<4>, dim3(tiles, col_tiles), dim3(256), 0, st, x,
+                               positions, L->cin, L->cout, L->taps, L->ncols, L->fragments,
+                               L->bias, history, history_out, residual, elu, y, status);
+        else
+            hipLaunchKernelGGL(k_conv_mfma<1>, dim3((tiles + 3) / 4, col_tiles), dim3(256), 0,
+                               st, x, positions, L->cin, L->cout, L->taps, L->ncols, L->fragments,
+                               L->bias, history, history_out, residual, elu, y, status);
+    } else if (tr) {
+        hipLaunchKernelGGL(k_convtr_seq, dim3((unsigned)((outs + 255) / 256)), dim3(256), 0, st,
+                           x, positions, L->cin, L->cout, L->stride, L->weight, L->bias, history,
+                           history_out, elu, y, status);
+    } else {
+        hipLaunchKernelGGL(k_conv_seq, dim3((unsigned)((outs + 255) / 256)), dim3(256), 0, st, x,
+                           positions, L->cin, L->cout, L->kernel, L->weight, L->bias, history,
+                           history_out, residual, elu, y, status);
     }
-    return launch_ok("pgpu_conv1d");
-}
-
-extern "C" int pgpu_convtr1d(void *stream, const float *x, int positions, int cin, int cout,
-                             int stride, const float *weight, const float *bias, float *overlap,
-                             float *y, int *status) {
-    if (!x || positions <= 0 || positions > 65535 || cin <= 0 || cin > 512 || cout <= 0 ||
-        cout > 512 || stride < 4 || stride > 6 || !weight || !bias || !overlap || !y || !status)
-        return bad_arguments("pgpu_convtr1d");
-    hipLaunchKernelGGL(k_convtr1d, dim3(positions, (cout + 255) / 256, stride), dim3(256), 0,
-                       (hipStream_t)stream, x, cin, cout, stride, weight, bias, overlap, y,
-                       status);
-    hipLaunchKernelGGL(k_convtr_tail, dim3(stride, (cout + 255) / 256), dim3(256), 0,
-                       (hipStream_t)stream, x, positions, cin, cout, stride, weight, overlap);
-    return launch_ok("pgpu_convtr1d");
+    return launch_ok("pgpu_conv_rows");
 }
 
 extern "C" int pgpu_elu(void *stream, const float *x, float *y, size_t count) {

@@ -2,6 +2,7 @@
 CPU oracle, and conversions of synthetic weights for the oracle."""
 from __future__ import annotations
 
+import ctypes
 import importlib.util
 import os
 import sys
@@ -362,3 +363,85 @@ def pcm_scalar_expected(x: np.ndarray) -> np.ndarray:
             prev[1] = f32(0.5) * b
         prev[0] = f32(0.5) * a
     return np.array(out, np.float32)
+
+
+# ------------------------------------------------- audio decoder weights
+
+MIMI_KEYS = ("qkv", "out", "mlp_in", "mlp_out", "norm1_w", "norm1_b", "norm2_w", "norm2_b",
+             "scale1", "scale2")
+
+
+def rounded(w):
+    """fp32 weights -> the values bf16 holds (what both sides compute with)."""
+    if isinstance(w, dict):
+        return {k: rounded(v) for k, v in w.items()}
+    return bf16_float(bf16_bits(w)).reshape(np.shape(w))
+
+
+def random_mimi(seed):
+    """Random Mimi weights of the real shapes (bf16-representable), scaled so
+    that activations stay O(1) through both layers."""
+    rng = np.random.default_rng(seed)
+    n = lambda shape, s: (rng.standard_normal(shape) * s).astype(np.float32)  # noqa: E731
+    w = {"projection": n((512, 32), 0.3), "upsample": n((512, 32), 0.3)}
+    for l in range(2):
+        w[l] = {"qkv": n((1536, 512), 512 ** -0.5), "out": n((512, 512), 512 ** -0.5),
+                "mlp_in": n((2048, 512), 512 ** -0.5), "mlp_out": n((512, 2048), 2048 ** -0.5),
+                "norm1_w": 1 + n(512, 0.1), "norm1_b": n(512, 0.1),
+                "norm2_w": 1 + n(512, 0.1), "norm2_b": n(512, 0.1),
+                "scale1": n(512, 0.3), "scale2": n(512, 0.3)}
+    return rounded(w)
+
+
+def mimi_model(lib, pkg, views, w):
+    """fp32 Mimi weights (bf16-representable) -> PhononMimiModel of BF16 views
+    kept alive by `views`."""
+    m = pkg.PhononMimiModel()
+    m.config = lib.phonon_mimi_config()
+    m.stride = 16
+    m.projection = views.bf16(bf16_bits(w["projection"]), (512, 32, 1))
+    m.upsample = views.bf16(bf16_bits(w["upsample"]), (512, 1, 32))
+    for l in range(2):
+        for f, key in enumerate(MIMI_KEYS):
+            arr = w[l][key]
+            m.layers[l][f] = views.bf16(bf16_bits(arr), arr.shape)
+    return m
+
+
+def conv_model(lib, views, w, b, stride, trans):
+    """A PhononConvModel handle from fp32 weight/bias (bf16-representable)."""
+    wv = views.bf16(bf16_bits(w), w.shape)
+    bv = views.bf16(bf16_bits(b), b.shape)
+    h = ctypes.c_void_p()
+    assert lib.phonon_conv_model_create(ctypes.byref(wv), ctypes.byref(bv), stride, int(trans),
+                                        ctypes.byref(h)) == 1
+    return h
+
+
+def random_pcm_convs(seed):
+    """Random weights for the eleven SEANet convolutions (the shapes and
+    order of pcm_scalar_convs), scaled so that activations stay O(1)."""
+    rng = np.random.default_rng(seed)
+    out = []
+    for (w, b, s, t) in pcm_scalar_convs():
+        if t:
+            cin, cout, k = w.shape
+        else:
+            cout, cin, k = w.shape
+        gain = 0.5 if k > 1 and not t and cout != 1 and cin == cout else 1.0
+        w = rounded((rng.standard_normal(w.shape) * gain * (cin * k / s) ** -0.5)
+                    .astype(np.float32))
+        b = rounded((rng.standard_normal(cout) * 0.05).astype(np.float32))
+        out.append((w, b, s, t))
+    return out
+
+
+def pcm_model(lib, pkg, views, mimi_w, convs):
+    """(PhononMimiModel, PhononPCMModel handle) from Mimi weights and the
+    eleven (weight, bias, stride, transposed) convolutions."""
+    mimi = mimi_model(lib, pkg, views, mimi_w)
+    arr = (ctypes.c_void_p * 11)(*[conv_model(lib, views, w, b, s, t).value
+                                   for (w, b, s, t) in convs])
+    model = ctypes.c_void_p()
+    assert lib.phonon_pcm_model_from_parts(ctypes.byref(mimi), arr, ctypes.byref(model)) == 1
+    return mimi, model
