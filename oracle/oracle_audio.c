@@ -21,7 +21,7 @@ static int finite_all(const float *p, size_t n) {
     return 1;
 }
 
-/* src/phonon_mimi.c:112-135, kernel decoded: [channels][2 stride]. */
+/* src/phonon_mimi.c:109-131, kernel decoded: [channels][2 stride]. */
 int oracle_mimi_upsample_frame(const float *kernel, const float *input, const float *previous,
                                size_t channels, size_t stride, float *output) {
     if (!kernel || !input || !previous || !output || !channels || channels > 512 || !stride ||
@@ -64,7 +64,7 @@ void oracle_mimi_destroy(OracleMimiState *s) { free(s); }
 
 size_t oracle_mimi_positions(const OracleMimiState *s) { return s ? s->position : 0; }
 
-/* head_order of src/phonon_mimi.c:140-145: even components, then odd. */
+/* head_order of src/phonon_mimi.c:135-143: even components, then odd. */
 static void head_order(const float *in, float *out) {
     for (size_t i = 0; i < 32; i++) {
         out[i] = in[2 * i];
@@ -240,7 +240,7 @@ void oracle_conv_destroy(OracleConv *c) {
     free(c);
 }
 
-/* src/phonon_conv.c:146-186. Causal Conv1d: weight [out][in][kernel], the
+/* src/phonon_conv.c:135-172. Causal Conv1d: weight [out][in][kernel], the
  * history [in][kernel] (im2col order), y = (W . h) + bias. Transposed:
  * weight [in][out][kernel], columns [out][kernel] = W^T x, then
  * y = (column + overlap) + bias for the first `stride` taps and the last
@@ -284,14 +284,14 @@ int oracle_conv_process(OracleConv *c, const float *x, size_t n, float *y) {
     return 1;
 }
 
-/* src/phonon_conv.c:187-200: exp(x) - 1 for x <= 0, in place. */
+/* src/phonon_conv.c:173-186: exp(x) - 1 for x <= 0, in place. */
 void oracle_conv_elu(float *x, size_t n) {
     for (size_t i = 0; i < n; i++)
         if (x[i] <= 0.0f)
             x[i] = expf(x[i]) - 1.0f;
 }
 
-/* src/phonon_conv.c:226-246: y = x + conv1(ELU(conv3(ELU(x)))), one position
+/* src/phonon_conv.c:219-246: y = x + conv1(ELU(conv3(ELU(x)))), one position
  * at a time (conv3: channels -> channels/2, kernel 3; conv1: back, kernel 1). */
 int oracle_residual_process(OracleConv *conv3, OracleConv *conv1, const float *x, size_t n,
                             float *y) {
@@ -315,7 +315,7 @@ int oracle_residual_process(OracleConv *conv3, OracleConv *conv1, const float *x
     return 1;
 }
 
-/* src/phonon_pcm.c:126-170: per latent frame, Mimi's 16 feature rows, each
+/* src/phonon_pcm.c:130-175: per latent frame, Mimi's 16 feature rows, each
  * through conv0, three (ELU, transposed conv, residual) stages of strides
  * 6, 5, 4 and ELU + the final conv: 1920 samples per frame. conv holds
  * conv0, then per stage the transposed conv, conv3 and conv1, then the

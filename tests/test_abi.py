@@ -33,7 +33,19 @@ def test_headers_declare_the_reference_entry_points():
               "phonon_erf_gelu", "phonon_rope_interleaved", "phonon_linear",
               "phonon_linear_batch", "phonon_flow_layer_step", "phonon_flow_stack_step",
               "phonon_flow_stack_step_cancel", "phonon_flow_stack_prefill",
-              "phonon_flow_stack_prefill_cancel", "phonon_attention_test"):
+              "phonon_flow_stack_prefill_cancel", "phonon_attention_test",
+              # src/phonon_mimi.h:27-46, src/phonon_conv.h:11-44, src/phonon_pcm.h:10-36
+              "phonon_mimi_config", "phonon_mimi_model_load", "phonon_mimi_state_create",
+              "phonon_mimi_state_reset", "phonon_mimi_state_destroy", "phonon_mimi_positions",
+              "phonon_mimi_process", "phonon_mimi_upsample_frame", "phonon_conv_model_create",
+              "phonon_conv_model_destroy", "phonon_conv_input_channels",
+              "phonon_conv_output_channels", "phonon_conv_stride", "phonon_conv_state_create",
+              "phonon_conv_state_destroy", "phonon_conv_state_reset", "phonon_conv_process",
+              "phonon_conv_elu", "phonon_residual_state_create",
+              "phonon_residual_state_destroy", "phonon_residual_state_reset",
+              "phonon_residual_process", "phonon_pcm_model_create", "phonon_pcm_model_destroy",
+              "phonon_pcm_state_create", "phonon_pcm_state_destroy", "phonon_pcm_state_reset",
+              "phonon_pcm_samples", "phonon_pcm_process", "phonon_pcm_finish"):
         assert n in names, n
 
 
@@ -63,6 +75,32 @@ def test_struct_layouts_match_the_reference(pkg):
     assert ctypes.sizeof(pkg.PhononFlowHead) == 68 * 96
     assert pkg.PhononFlowHead.block_ada_weight.offset == 16 * 96
     assert pkg.PhononFlowHead.final_ada_weight.offset == 64 * 96
+    # PhononMimiConfig {unsigned, float, unsigned[3], size_t, float} and
+    # PhononMimiModel {config, size_t stride, 2 views, 2 x 10 views}
+    # (src/phonon_mimi.h:10-24) on LP64.
+    assert ctypes.sizeof(pkg.PhononMimiConfig) == 40
+    assert pkg.PhononMimiConfig.context.offset == 24
+    assert pkg.PhononMimiConfig.rope_theta.offset == 32
+    assert pkg.PhononMimiModel.stride.offset == 40
+    assert pkg.PhononMimiModel.projection.offset == 48
+    assert pkg.PhononMimiModel.layers.offset == 48 + 2 * 96
+    assert ctypes.sizeof(pkg.PhononMimiModel) == 48 + 22 * 96
+
+
+def test_c_layouts_of_the_audio_headers(tmp_path):
+    """The C compiler's layout of include/phonon_mimi.h agrees with the
+    reference's field order (checked by static assertions)."""
+    src = tmp_path / "mimi.c"
+    src.write_text(
+        '#include <stddef.h>\n#include "phonon_pcm.h"\n'
+        '_Static_assert(sizeof(PhononMimiConfig) == 40, "config");\n'
+        '_Static_assert(offsetof(PhononMimiConfig, context) == 24, "context");\n'
+        '_Static_assert(offsetof(PhononMimiModel, stride) == 40, "stride");\n'
+        '_Static_assert(offsetof(PhononMimiModel, layers) == 48 + 2 * 96, "layers");\n'
+        '_Static_assert(sizeof(PhononMimiModel) == 48 + 22 * 96, "model");\n'
+        'int main(void){return 0;}\n')
+    subprocess.run(["gcc", "-std=c17", "-Wall", "-Wextra", "-Wpedantic", "-Werror",
+                    "-I", INCLUDE, "-fsyntax-only", str(src)], check=True)
 
 
 def test_library_has_no_cpu_compute_symbols(pkg):
