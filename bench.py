@@ -536,7 +536,7 @@ def q8_matvec_bench(pkg, lib, seed=1, calls=2000):
     return res
 
 
-def flow_head_bench(pkg, lib, streams=64, calls=200, seed=11, graph=1):
+def flow_head_bench(pkg, lib, streams=64, calls=200, seed=11, graph=1, one_launch=0):
     """The flow head's batched LSD step (phonon_flow_head_device_lsd: noise
     scaling, input/condition projections, seven adaLN projections as one, six
     residual MLP blocks, final layer, EOS logit) for `streams` streams, on a
@@ -555,6 +555,7 @@ def flow_head_bench(pkg, lib, streams=64, calls=200, seed=11, graph=1):
     assert lib.phonon_flow_head_device_create(ctypes.byref(head), ctypes.byref(ew),
                                               ctypes.byref(eb), streams, ctypes.byref(dev))
     assert lib.phonon_flow_head_device_set_graph(dev, graph)
+    assert lib.phonon_flow_head_device_set_one_launch(dev, one_launch)
     stream = lib.phonon_flow_head_device_stream(dev)
     cond = pkg.DeviceBuffer(lib, streams * 512 * 4)
     raw = pkg.DeviceBuffer(lib, streams * 32 * 4)
@@ -591,7 +592,8 @@ def flow_head_bench(pkg, lib, streams=64, calls=200, seed=11, graph=1):
                         f"reference's shapes (6 adaLN blocks, 8.68 M weights per step)",
             "us_per_step": round(ms * 1e3, 2),
             "frames_per_s": round(streams / (ms * 1e-3), 1),
-            "launches_per_step": 15,
+            "launches_per_step": 2 if one_launch else 15,
+            "one_launch": bool(one_launch),
             "weight_bytes_per_step": weight_bytes,
             "weight_GBps": round(weight_bytes / (ms * 1e-3) / 1e9, 1),
             "hbm_frac": round(weight_bytes / (ms * 1e-3) / 8e12, 4),
@@ -602,7 +604,7 @@ def flow_head_bench(pkg, lib, streams=64, calls=200, seed=11, graph=1):
 
 
 def frame_loop_bench(pkg, lib, layers=12, streams=64, frames=30, warmup=3, seed=2026,
-                     shared_stream=True, graph=1):
+                     shared_stream=True, graph=1, one_launch=0):
     """The whole per-frame loop of B streams on the GPU: the decode step
     (library default mode), then phonon_flow_head_device_frame (output norm,
     LSD step + EOS logit, latent embedding + condition) writing the next
@@ -631,6 +633,7 @@ def frame_loop_bench(pkg, lib, layers=12, streams=64, frames=30, warmup=3, seed=
     if shared_stream:
         assert lib.phonon_flow_head_device_set_stream(h, d.stream)
     assert lib.phonon_flow_head_device_set_graph(h, graph)
+    assert lib.phonon_flow_head_device_set_one_launch(h, one_launch)
     hs = lib.phonon_flow_head_device_stream(h)
     cond = pkg.DeviceBuffer(lib, streams * 512 * 4)
     raw = pkg.DeviceBuffer(lib, streams * 32 * 4)
@@ -675,6 +678,7 @@ def frame_loop_bench(pkg, lib, layers=12, streams=64, frames=30, warmup=3, seed=
                         f"next step's input, contexts U{{1..2048}}",
             "head_stream": "the batch's" if shared_stream else "its own, events between",
             "head_graph": bool(graph),
+            "head_one_launch": bool(one_launch),
             "us_per_frame": round(ms * 1e3, 1), "frames_per_s": round(streams / (ms * 1e-3), 1),
             "clean": clean}
 
@@ -997,13 +1001,15 @@ def main():
         print(json.dumps(pcm_bench(pkg, lib)), flush=True)
         return
     if args.flow_head:
-        for shared, graph in ((True, 1), (True, 0), (False, 1)):
-            print(json.dumps(frame_loop_bench(pkg, lib, shared_stream=shared, graph=graph)),
-                  flush=True)
-        for streams in (64, 1):
-            for graph in (1, 0):
-                r = flow_head_bench(pkg, lib, streams=streams, graph=graph)
-                print(json.dumps(dict(r, graph=graph)), flush=True)
+        for one in (1, 0):
+            for shared, graph in ((True, 1), (True, 0)):
+                print(json.dumps(frame_loop_bench(pkg, lib, shared_stream=shared, graph=graph,
+                                                  one_launch=one)), flush=True)
+        for streams in (64, 16, 1):
+            for one in (1, 0):
+                for graph in (1, 0):
+                    r = flow_head_bench(pkg, lib, streams=streams, graph=graph, one_launch=one)
+                    print(json.dumps(dict(r, graph=graph)), flush=True)
         return
 
     lengths = np.random.default_rng(args.seed).integers(1, 2049, size=args.batch) - 1

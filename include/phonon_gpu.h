@@ -426,6 +426,81 @@ int pgpu_head_time_phase(void *stream, const float *freqs, float value, uint16_t
 int pgpu_head_time_sum(void *stream, const float *out0, const float *out1, const float *alpha0,
                        const float *alpha1, float *tsum, int *status);
 
+/* -- the LSD step of the flow head as one launch (pgpu_head.hip) --
+ * The projections of pgpu_head_front / _mod / _mlp_in / pgpu_gemm_gated /
+ * pgpu_head_final (and, for a frame, the latent embedding) as work-group
+ * tasks of one launch, per 16-stream tile t:
+ *   COND    8   LN(condition) (or the rows) . cond + b, + tsum, SiLU, split
+ *   EOS     1   the EOS row (optional)
+ *   NOISE   1   noise = raw * scale, rows and split fragments
+ *   INPUT   32  x0 = input . noise + b                   (waits NOISE)
+ *   ADA     160 the 10240 modulation rows, 64 per task   (waits COND)
+ *   MLP_IN  8   per block b: SiLU(mlp_b0(LN(x_b) * (1 + scale) + shift))
+ *               (waits x_b complete and block b's 24 ADA tasks)
+ *   MLP_OUT 32  per block b: x_{b+1} = x_b + gate * (mlp_b1 . u + b)
+ *   FINAL   1   latent = noise + final(LN(x_6) * (1 + scale) + shift), and
+ *               the tile's EOS logits copied out
+ *   EMBED   32  next = input_linear . latent + embed (optional)
+ * Every task's arithmetic is the chain's, so both give the same bits. A task
+ * waits (one lane polls) for per-tile counters; the schedule lists every
+ * task after the tasks it waits for, so the launch cannot deadlock. Waits
+ * give up after wait_us microseconds (0: 1 s) and set status value 4.
+ * Values handed between tasks are stored write-through, each at its own
+ * address (x has one buffer per block). The counters must be zero at
+ * launch: pgpu_head_flow_reset after each launch. */
+enum {
+    PGPU_HEAD_COND, PGPU_HEAD_EOS, PGPU_HEAD_NOISE, PGPU_HEAD_INPUT, PGPU_HEAD_ADA,
+    PGPU_HEAD_MLP_IN, PGPU_HEAD_MLP_OUT, PGPU_HEAD_FINAL, PGPU_HEAD_EMBED
+};
+/* Descriptor: kind [0,4), block [4,8), tile [8,16), index [16,32). */
+#define PGPU_HEAD_TASK(kind, block, tile, index)                                          \
+    ((uint32_t)(kind) | (uint32_t)(block) << 4 | (uint32_t)(tile) << 8 |                  \
+     (uint32_t)(index) << 16)
+/* Counters per tile (PGPU_HEAD_COUNTER_STRIDE unsigned apart): COND, EOS,
+ * NOISE, ADA of blocks 0..6 (6: the final layer's rows), U of blocks 0..5
+ * (MLP_IN done), X of versions 0..6, FINAL. */
+enum {
+    PGPU_HEADC_COND = 0, PGPU_HEADC_EOS = 1, PGPU_HEADC_NOISE = 2, PGPU_HEADC_ADA = 3,
+    PGPU_HEADC_U = 10, PGPU_HEADC_X = 16, PGPU_HEADC_FINAL = 23, PGPU_HEADC_KINDS = 24
+};
+#define PGPU_HEAD_COUNTER_STRIDE 16
+#define PGPU_HEAD_BLOCKS 6
+typedef struct {
+    const uint32_t *schedule; /* (dev) [tasks] */
+    int tasks, streams, tiles;
+    pgpu_matrix cond_w, eos_w, ada_w, input_w, mlp_w[PGPU_HEAD_BLOCKS][2], final_w, embed_w;
+    int with_eos, with_embed;
+    const float *conditions;  /* [streams][512] */
+    const float *out_norm;    /* [2][512] LayerNorm of the conditions, or NULL */
+    const float *b_cond, *tsum, *b_eos, *b_ada, *b_input, *b_mlp[PGPU_HEAD_BLOCKS][2], *b_final;
+    const float *norm_w[PGPU_HEAD_BLOCKS], *norm_b[PGPU_HEAD_BLOCKS];
+    const float *raw;         /* [streams][32] */
+    float scale;
+    float *noise;             /* [tiles*16][32] */
+    uint16_t *noise_split;    /* split fragments, K = 32 */
+    uint16_t *silu_split;     /* K = 512 */
+    float *mod;               /* [tiles*16][10240] */
+    float *x;                 /* [7][tiles*16][512] */
+    uint16_t *u_split;        /* [6] split fragments, K = 512 */
+    float *eos_rows;          /* [tiles*16][16] */
+    float *eos;               /* [streams] or NULL */
+    const float *ones;        /* [32] of 1.0f */
+    float *latents;           /* [streams][32] */
+    uint16_t *latent_split;   /* K = 32 (embed only) */
+    const float *embed_in;    /* [streams][512] (embed only) */
+    float *next;              /* [streams][512] (embed only) */
+    unsigned *counters;       /* [tiles][PGPU_HEADC_KINDS][PGPU_HEAD_COUNTER_STRIDE], zero */
+    int *status;
+    unsigned wait_us;
+} pgpu_head_flow;
+/* The task list of one launch for `tiles` 16-stream tiles (host code): every
+ * task after the tasks it waits for. Writes at most `capacity` descriptors
+ * and returns the count (0 if they do not fit; out = NULL only counts). */
+int pgpu_head_flow_schedule(uint32_t *out, int capacity, int tiles, int with_eos,
+                            int with_embed);
+int pgpu_head_flow_launch(void *stream, const pgpu_head_flow *f);
+int pgpu_head_flow_reset(void *stream, unsigned *counters, size_t count);
+
 /* -- rows and elements (pgpu_elementwise.hip) -- */
 int pgpu_ln_split(void *stream, const float *x, int streams, const float *w, const float *b,
                   float eps, uint16_t *xs, float *y, int *status);

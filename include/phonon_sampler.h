@@ -101,6 +101,15 @@ int phonon_flow_head_device_frame(PhononFlowHeadDevice *head, size_t streams,
  * graph per (streams, buffers, temperature), two kept, and replayed; 0:
  * each kernel is launched directly. */
 int phonon_flow_head_device_set_graph(PhononFlowHeadDevice *head, int use_graph);
+/* one_launch = 1: the step runs as one dataflow launch (pgpu_head_flow:
+ * every projection a work-group task that waits for its inputs on
+ * counters), plus a counter reset; 0 (the default): the chain of launches.
+ * Both give the same bits. */
+int phonon_flow_head_device_set_one_launch(PhononFlowHeadDevice *head, int one_launch);
+/* Bounds a one-launch task's wait for its inputs (microseconds; 0 = 1 s).
+ * A wait that gives up ends the launch early and the next sync reports
+ * failure. */
+int phonon_flow_head_device_set_wait_limit(PhononFlowHeadDevice *head, unsigned microseconds);
 /* Runs the head's work on `stream` (a caller's HIP stream, e.g. the decode
  * batch's, so a frame needs no cross-stream hand-off; NULL = the head's
  * own). The caller keeps that stream alive while the head uses it. */

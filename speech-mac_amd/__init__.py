@@ -328,6 +328,11 @@ EXPORTS = {
                                   _vp, _i]),
     "pgpu_mimi_attention": (_i, [_vp, _vp, _i, ctypes.c_longlong, _vp, _vp, _i, _i, _vp,
                                  _vp]),
+    "pgpu_head_flow_schedule": (_i, [_vp, _i, _i, _i, _i]),
+    "pgpu_head_flow_launch": (_i, [_vp, _vp]),
+    "pgpu_head_flow_reset": (_i, [_vp, _vp, _sz]),
+    "phonon_flow_head_device_set_one_launch": (_i, [_vp, _i]),
+    "phonon_flow_head_device_set_wait_limit": (_i, [_vp, ctypes.c_uint]),
     "pgpu_conv_rows": (_i, [_vp, ctypes.POINTER(PgpuConvLayer), _vp, _i, _vp, _vp, _vp, _i, _vp,
                             _vp]),
     "pgpu_upsample_frame": (_i, [_vp, _vp, _vp, _vp, _i, _i, _vp, _vp]),

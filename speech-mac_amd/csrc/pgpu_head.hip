@@ -343,3 +343,302 @@ extern "C" int pgpu_head_time_sum(void *stream, const float *out0, const float *
                        alpha0, alpha1, tsum, status);
     return launch_ok(__func__);
 }
+
+// ---------------------------------------------------------------------------
+// The LSD step as one launch (pgpu_head_flow in phonon_gpu.h): the tasks of
+// the launches above, each first waiting for per-tile counters.
+namespace pgpu {
+namespace {
+
+constexpr uint64_t kHeadWaitTicks = 100000000ull;  // 1 s at 100 MHz
+
+__device__ inline unsigned *head_counter(const pgpu_head_flow &f, int tile, int which) {
+    return f.counters + ((size_t)tile * PGPU_HEADC_KINDS + which) * PGPU_HEAD_COUNTER_STRIDE;
+}
+
+// Up to three (counter, target) conditions (unused: null counter): one lane
+// polls them in turn (each poll loads the counter and the status word
+// together), then the work-group barrier releases the task. A wait that
+// exceeds `ticks` of the 100 MHz clock, or sees another task's give-up,
+// sets status value 4 and stops waiting, so the launch always ends.
+struct HeadWait {
+    const unsigned *flag0, *flag1, *flag2;
+    unsigned target0, target1, target2;
+    int *status;
+    uint64_t ticks;
+    __device__ bool poll(const unsigned *flag, unsigned target, uint64_t t0) const {
+        for (;;) {
+            const unsigned count =
+                __hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            const int st = __hip_atomic_load(status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (count >= target) return true;
+            if ((st & 4) || wall_clock64() - t0 > ticks) {
+                atomicOr(status, 4);
+                return false;
+            }
+            __builtin_amdgcn_s_sleep(2);
+        }
+    }
+    __device__ void operator()() const {
+        if (threadIdx.x == 0) {
+            const uint64_t t0 = wall_clock64();
+            bool ok = !flag0 || poll(flag0, target0, t0);
+            ok = ok && (!flag1 || poll(flag1, target1, t0));
+            ok = ok && (!flag2 || poll(flag2, target2, t0));
+        }
+        __syncthreads();
+    }
+};
+
+// The wait for (which, target) pairs of this tile's counters (which < 0:
+// none).
+__device__ inline HeadWait head_wait(const pgpu_head_flow &f, int tile, int c0 = -1,
+                                     unsigned t0 = 0, int c1 = -1, unsigned t1 = 0,
+                                     int c2 = -1, unsigned t2 = 0) {
+    HeadWait w;
+    w.flag0 = c0 < 0 ? nullptr : head_counter(f, tile, c0);
+    w.flag1 = c1 < 0 ? nullptr : head_counter(f, tile, c1);
+    w.flag2 = c2 < 0 ? nullptr : head_counter(f, tile, c2);
+    w.target0 = t0;
+    w.target1 = t1;
+    w.target2 = t2;
+    w.status = f.status;
+    w.ticks = f.wait_us ? (uint64_t)f.wait_us * 100u : kHeadWaitTicks;
+    return w;
+}
+
+// Completes a task: every wave's write-through stores have drained, then
+// one lane counts it.
+__device__ inline void head_signal(const pgpu_head_flow &f, int tile, int which) {
+    __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (threadIdx.x == 0)
+        __hip_atomic_fetch_add(head_counter(f, tile, which), 1u, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ inline GemmArgs flow_args(const pgpu_head_flow &f, const pgpu_matrix &w) {
+    GemmArgs a{};
+    a.w = w.values;
+    a.n_rows = (int)w.rows;
+    a.k_cols = (int)w.columns;
+    a.streams = f.streams;
+    a.status = f.status;
+    a.wt_out = true;  // read by tasks on other XCDs within the launch
+    return a;
+}
+
+__device__ inline float *x_rows(const pgpu_head_flow &f, int version) {
+    return f.x + (size_t)version * f.tiles * 16 * kWidth;
+}
+
+__device__ inline uint16_t *u_rows(const pgpu_head_flow &f, int block) {
+    return f.u_split + (size_t)block * f.tiles * (kWidth / 32) * 1536;
+}
+
+constexpr int kAdaRows = 3 * kWidth;                 // one block's shift, scale, gate
+constexpr int kModCols = PGPU_HEAD_BLOCKS * kAdaRows + 2 * kWidth;
+constexpr int kAdaGroupsPerBlock = kAdaRows / 64;    // 24
+constexpr int kFinalAdaGroups = 2 * kWidth / 64;     // 16
+
+__global__ __launch_bounds__(kTaskThreads) void k_head_flow(pgpu_head_flow f) {
+    __shared__ uint4 lds4[kTaskLds / 8];
+    uint16_t *lds = (uint16_t *)lds4;
+    const uint32_t d = f.schedule[blockIdx.x];
+    const int kind = d & 15, blk = (d >> 4) & 15, tile = (d >> 8) & 255, index = (int)(d >> 16);
+    switch (kind) {
+    case PGPU_HEAD_COND: {
+        GemmArgs a = flow_args(f, f.cond_w);
+        a.ln_x = f.conditions;
+        a.ln_w = f.out_norm;
+        a.ln_b = f.out_norm ? f.out_norm + kWidth : nullptr;
+        a.ln_eps = 1e-5f;
+        a.bias = f.b_cond;
+        a.bias2 = f.tsum;
+        a.out_split = f.silu_split;
+        a.out_kb = kWidth / 32;
+        if (f.out_norm)
+            gemm_wide_task<SRC_LN, EPI_SILU_SPLIT, false>(a, index, tile, lds, NoWait{});
+        else
+            gemm_wide_task<SRC_ROWS, EPI_SILU_SPLIT, false>(a, index, tile, lds, NoWait{});
+        head_signal(f, tile, PGPU_HEADC_COND);
+        break;
+    }
+    case PGPU_HEAD_EOS: {
+        GemmArgs a = flow_args(f, f.eos_w);
+        a.ln_x = f.conditions;
+        a.ln_w = f.out_norm;
+        a.ln_b = f.out_norm ? f.out_norm + kWidth : nullptr;
+        a.ln_eps = 1e-5f;
+        a.bias = f.b_eos;
+        a.out = f.eos_rows;
+        a.ld_out = 16;
+        if (f.out_norm)
+            gemm_wide_task<SRC_LN, EPI_STORE, false>(a, 0, tile, lds, NoWait{});
+        else
+            gemm_wide_task<SRC_ROWS, EPI_STORE, false>(a, 0, tile, lds, NoWait{});
+        head_signal(f, tile, PGPU_HEADC_EOS);
+        break;
+    }
+    case PGPU_HEAD_NOISE: {
+        // noise = raw * scale (src/phonon_sampler.c:371-376), 8 values per
+        // thread: rows and split fragments, both written through.
+        const int i = threadIdx.x, s = tile * 16 + (i >> 2), g = i & 3;
+        if (i < 64 && s < f.streams) {
+            const float *r = f.raw + (size_t)s * 32 + g * 8;
+            float v[8];
+            bool bad = false;
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                v[j] = __fmul_rn(r[j], f.scale);
+                bad |= !isfinite(v[j]);
+            }
+            float *o = f.noise + (size_t)s * 32 + g * 8;
+            store_wt(o, make_float4(v[0], v[1], v[2], v[3]));
+            store_wt(o + 4, make_float4(v[4], v[5], v[6], v[7]));
+            store_split4(f.noise_split, s, g * 8, 1, v, true);
+            store_split4(f.noise_split, s, g * 8 + 4, 1, v + 4, true);
+            flag_nonfinite(f.status, bad);
+        }
+        head_signal(f, tile, PGPU_HEADC_NOISE);
+        break;
+    }
+    case PGPU_HEAD_INPUT: {
+        GemmArgs a = flow_args(f, f.input_w);
+        a.xs = f.noise_split;
+        a.bias = f.b_input;
+        a.out = x_rows(f, 0);
+        a.ld_out = kWidth;
+        gemm_split_task<EPI_STORE, false>(a, index, tile, lds,
+                                          head_wait(f, tile, PGPU_HEADC_NOISE, 1u));
+        head_signal(f, tile, PGPU_HEADC_X);
+        break;
+    }
+    case PGPU_HEAD_ADA: {
+        GemmArgs a = flow_args(f, f.ada_w);
+        a.xs = f.silu_split;
+        a.bias = f.b_ada;
+        a.out = f.mod;
+        a.ld_out = kModCols;
+        gemm_wide_task<SRC_SPLIT_LDS, EPI_STORE, false>(
+            a, index, tile, lds, head_wait(f, tile, PGPU_HEADC_COND, (kWidth / 16 + 3) / 4));
+        head_signal(f, tile, PGPU_HEADC_ADA + index / kAdaGroupsPerBlock);
+        break;
+    }
+    case PGPU_HEAD_MLP_IN: {
+        GemmArgs a = flow_args(f, f.mlp_w[blk][0]);
+        a.ln_x = x_rows(f, blk);
+        a.ln_w = f.norm_w[blk];
+        a.ln_b = f.norm_b[blk];
+        a.ln_eps = 1e-6f;
+        a.mod = f.mod + (size_t)blk * kAdaRows;
+        a.ld_mod = kModCols;
+        a.bias = f.b_mlp[blk][0];
+        a.out_split = u_rows(f, blk);
+        a.out_kb = kWidth / 32;
+        gemm_wide_task<SRC_LN_MOD, EPI_SILU_SPLIT, false>(
+            a, index, tile, lds,
+            head_wait(f, tile, PGPU_HEADC_X + blk, kWidth / 16, PGPU_HEADC_ADA + blk,
+                      kAdaGroupsPerBlock));
+        head_signal(f, tile, PGPU_HEADC_U + blk);
+        break;
+    }
+    case PGPU_HEAD_MLP_OUT: {
+        GemmArgs a = flow_args(f, f.mlp_w[blk][1]);
+        a.xs = u_rows(f, blk);
+        a.bias = f.b_mlp[blk][1];
+        a.gate = f.mod + (size_t)blk * kAdaRows + 2 * kWidth;
+        a.ld_gate = kModCols;
+        a.residual = x_rows(f, blk);
+        a.out = x_rows(f, blk + 1);
+        a.ld_out = kWidth;
+        gemm_split_task<EPI_GATED, false>(a, index, tile, lds,
+                                          head_wait(f, tile, PGPU_HEADC_U + blk,
+                                                    (kWidth / 16 + 3) / 4));
+        head_signal(f, tile, PGPU_HEADC_X + blk + 1);
+        break;
+    }
+    case PGPU_HEAD_FINAL: {
+        GemmArgs a = flow_args(f, f.final_w);
+        a.ln_x = x_rows(f, PGPU_HEAD_BLOCKS);
+        a.ln_eps = 1e-6f;
+        a.out_split = f.latent_split;
+        a.out_kb = (int)f.final_w.rows / 32;
+        a.mod = f.mod + (size_t)PGPU_HEAD_BLOCKS * kAdaRows;
+        a.ld_mod = kModCols;
+        a.bias = f.b_final;
+        a.out = f.latents;
+        a.ld_out = (int)f.final_w.rows;
+        a.residual = f.noise;
+        a.gate = f.ones;
+        a.ld_gate = 0;
+        gemm_wide_task<SRC_LN_MOD, EPI_GATED, false>(
+            a, 0, tile, lds,
+            head_wait(f, tile, PGPU_HEADC_X + PGPU_HEAD_BLOCKS, kWidth / 16,
+                      PGPU_HEADC_ADA + PGPU_HEAD_BLOCKS, kFinalAdaGroups,
+                      f.with_eos ? PGPU_HEADC_EOS : -1, 1u));
+        if (f.with_eos && f.eos) {
+            const int s = tile * 16 + (int)threadIdx.x;
+            if (threadIdx.x < 16 && s < f.streams) {
+                const float e = f.eos_rows[(size_t)s * 16];
+                f.eos[s] = e;
+                flag_nonfinite(f.status, !isfinite(e));
+            }
+        }
+        head_signal(f, tile, PGPU_HEADC_FINAL);
+        break;
+    }
+    case PGPU_HEAD_EMBED: {
+        GemmArgs a = flow_args(f, f.embed_w);
+        a.xs = f.latent_split;
+        a.out = f.next;
+        a.ld_out = kWidth;
+        a.residual = f.embed_in;
+        a.wt_out = false;  // read after the launch only
+        gemm_split_task<EPI_RESIDUAL, false>(a, index, tile, lds,
+                                             head_wait(f, tile, PGPU_HEADC_FINAL, 1u));
+        break;
+    }
+    default:
+        break;
+    }
+}
+
+__global__ void k_head_flow_reset(unsigned *counters, size_t n) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (size_t)gridDim.x * blockDim.x)
+        counters[i] = 0u;
+}
+
+}  // namespace
+}  // namespace pgpu
+
+extern "C" int pgpu_head_flow_launch(void *stream, const pgpu_head_flow *f) {
+    if (!f || !f->schedule || f->tasks <= 0 || f->streams <= 0 ||
+        f->tiles != (f->streams + 15) / 16 || f->tiles > 255 ||
+        !bf16_matrix(&f->cond_w, kWidth, kWidth) || !bf16_matrix(&f->input_w, kWidth, 32) ||
+        !bf16_matrix(&f->ada_w, (size_t)pgpu::kModCols, kWidth) ||
+        !bf16_matrix(&f->final_w, 32, kWidth) || !f->conditions || !f->b_cond || !f->tsum ||
+        !f->b_ada || !f->b_input || !f->b_final || !f->raw || !(f->scale > 0.0f) ||
+        !std::isfinite(f->scale) || !f->noise || !f->noise_split || !f->silu_split || !f->mod ||
+        !f->x || !f->u_split || !f->ones || !f->latents || !f->counters || !f->status ||
+        (f->with_eos && (!bf16_matrix(&f->eos_w, 16, kWidth) || !f->eos_rows)) ||
+        (f->with_embed && (!bf16_matrix(&f->embed_w, kWidth, 32) || !f->latent_split ||
+                           !f->embed_in || !f->next)))
+        return bad_arguments("pgpu_head_flow_launch");
+    for (int b = 0; b < PGPU_HEAD_BLOCKS; b++)
+        if (!bf16_matrix(&f->mlp_w[b][0], kWidth, kWidth) ||
+            !bf16_matrix(&f->mlp_w[b][1], kWidth, kWidth) || !f->norm_w[b] || !f->norm_b[b])
+            return bad_arguments("pgpu_head_flow_launch");
+    hipLaunchKernelGGL(pgpu::k_head_flow, dim3((unsigned)f->tasks), dim3(kTaskThreads), 0,
+                       (hipStream_t)stream, *f);
+    return launch_ok("pgpu_head_flow_launch");
+}
+
+extern "C" int pgpu_head_flow_reset(void *stream, unsigned *counters, size_t count) {
+    if (!counters || !count) return bad_arguments("pgpu_head_flow_reset");
+    const unsigned blocks = (unsigned)((count + 255) / 256 < 64 ? (count + 255) / 256 : 64);
+    hipLaunchKernelGGL(pgpu::k_head_flow_reset, dim3(blocks), dim3(256), 0, (hipStream_t)stream,
+                       counters, count);
+    return launch_ok("pgpu_head_flow_reset");
+}

@@ -58,6 +58,20 @@ struct PhononFlowHeadDevice {
     } graphs[2];
     size_t graph_victim;
     int eager; /* launch each kernel directly instead of replaying a graph */
+    /* One-launch step (pgpu_head_flow): x of every block, u of every block,
+     * counters, and the task lists built so far. */
+    int one_launch;
+    unsigned wait_us;
+    void *flow_buffers;
+    float *fx;
+    uint16_t *fu, *latent_split;
+    unsigned *counters;
+    size_t counter_count;
+    struct {
+        int tiles, eos, embed, tasks;
+        uint32_t *dev;
+    } lists[8];
+    size_t nlists;
 };
 
 static size_t split_elems(size_t streams, size_t k_cols) {
@@ -155,6 +169,116 @@ static int upload_vectors(PhononFlowHeadDevice *h, const PhononFlowHead *head,
          pgpu_stream_sync(h->stream);
     free(host);
     return ok;
+}
+
+/* The buffers of the one-launch step for up to h->cap streams. */
+static int alloc_flow_buffers(PhononFlowHeadDevice *h) {
+    const size_t cap = h->cap, tiles = cap / 16;
+    const size_t floats = (HB + 1) * cap * PH_WIDTH;
+    const size_t halves = HB * split_elems(cap, PH_WIDTH) + split_elems(cap, LAT);
+    const size_t counters = tiles * PGPU_HEADC_KINDS * PGPU_HEAD_COUNTER_STRIDE;
+    const size_t bytes = floats * sizeof(float) + halves * sizeof(uint16_t) +
+                         counters * sizeof(unsigned);
+    char *p = pgpu_malloc(bytes);
+    if (!p || !pgpu_memset(h->stream, p, 0, bytes)) {
+        pgpu_free(p);
+        return 0;
+    }
+    h->flow_buffers = p;
+    h->fx = (float *)p;
+    h->fu = (uint16_t *)(h->fx + floats);
+    h->latent_split = h->fu + HB * split_elems(cap, PH_WIDTH);
+    h->counters = (unsigned *)(h->latent_split + split_elems(cap, LAT));
+    h->counter_count = counters;
+    return 1;
+}
+
+/* The one-launch task list (pgpu_head_flow): every task after the tasks it
+ * waits for. The modulation rows of block b + 1 are listed between block
+ * b's MLP_IN and MLP_OUT tasks, so that they are computed while the chain
+ * works on block b. Returns the number of tasks (with out == NULL: only
+ * counts them; 0 if `capacity` is too small). */
+int pgpu_head_flow_schedule(uint32_t *out, int capacity, int tiles, int with_eos,
+                            int with_embed) {
+    if (tiles <= 0 || tiles > 255 || capacity < 0)
+        return 0;
+    int n = 0;
+#define PUT(kind, block, tile, index)                                                      \
+    do {                                                                                   \
+        if (out && n < capacity)                                                           \
+            out[n] = PGPU_HEAD_TASK(kind, block, tile, index);                             \
+        n++;                                                                               \
+    } while (0)
+    const int groups512 = (PH_WIDTH / 16 + 3) / 4, rows512 = PH_WIDTH / 16;
+    const int ada_block = ADA / 64, ada_final = FINAL_ADA / 64;
+    for (int t = 0; t < tiles; t++) {
+        for (int i = 0; i < groups512; i++)
+            PUT(PGPU_HEAD_COND, 0, t, i);
+        if (with_eos)
+            PUT(PGPU_HEAD_EOS, 0, t, 0);
+        PUT(PGPU_HEAD_NOISE, 0, t, 0);
+    }
+    for (int t = 0; t < tiles; t++)
+        for (int i = 0; i < rows512; i++)
+            PUT(PGPU_HEAD_INPUT, 0, t, i);
+    for (int t = 0; t < tiles; t++)
+        for (int i = 0; i < ada_block; i++)
+            PUT(PGPU_HEAD_ADA, 0, t, i);
+    for (int t = 0; t < tiles; t++)
+        for (int i = 0; i < groups512; i++)
+            PUT(PGPU_HEAD_MLP_IN, 0, t, i);
+    for (int b = 0; b < HB; b++) {
+        const int nb = b + 1, groups = nb < HB ? ada_block : ada_final;
+        for (int t = 0; t < tiles; t++)
+            for (int i = 0; i < groups; i++)
+                PUT(PGPU_HEAD_ADA, 0, t, nb * ada_block + i);
+        for (int t = 0; t < tiles; t++)
+            for (int i = 0; i < rows512; i++)
+                PUT(PGPU_HEAD_MLP_OUT, b, t, i);
+        if (nb < HB)
+            for (int t = 0; t < tiles; t++)
+                for (int i = 0; i < groups512; i++)
+                    PUT(PGPU_HEAD_MLP_IN, nb, t, i);
+    }
+    for (int t = 0; t < tiles; t++)
+        PUT(PGPU_HEAD_FINAL, 0, t, 0);
+    if (with_embed)
+        for (int t = 0; t < tiles; t++)
+            for (int i = 0; i < rows512; i++)
+                PUT(PGPU_HEAD_EMBED, 0, t, i);
+#undef PUT
+    return !out || n <= capacity ? n : 0;
+}
+
+/* The device copy of the task list for (tiles, eos, embed), built once. */
+static const uint32_t *flow_list(PhononFlowHeadDevice *h, int tiles, int eos, int embed,
+                                 int *tasks) {
+    for (size_t i = 0; i < h->nlists; i++)
+        if (h->lists[i].tiles == tiles && h->lists[i].eos == eos && h->lists[i].embed == embed) {
+            *tasks = h->lists[i].tasks;
+            return h->lists[i].dev;
+        }
+    if (h->nlists == sizeof(h->lists) / sizeof(h->lists[0]))
+        return NULL;
+    const int n = pgpu_head_flow_schedule(NULL, 0, tiles, eos, embed);
+    uint32_t *host = n > 0 ? malloc((size_t)n * sizeof(uint32_t)) : NULL;
+    uint32_t *dev = host ? pgpu_malloc((size_t)n * sizeof(uint32_t)) : NULL;
+    const int ok = dev && pgpu_head_flow_schedule(host, n, tiles, eos, embed) == n &&
+                   pgpu_copy_h2d(h->stream, dev, host, (size_t)n * sizeof(uint32_t)) &&
+                   pgpu_stream_sync(h->stream);
+    free(host);
+    if (!ok) {
+        pgpu_free(dev);
+        return NULL;
+    }
+    h->lists[h->nlists].tiles = tiles;
+    h->lists[h->nlists].eos = eos;
+    h->lists[h->nlists].embed = embed;
+    h->lists[h->nlists].tasks = n;
+    h->lists[h->nlists].dev = dev;
+    h->nlists++;
+    *tasks = n;
+    return dev;
 }
 
 static int alloc_buffers(PhononFlowHeadDevice *h, size_t streams) {
@@ -266,6 +390,7 @@ int phonon_flow_head_device_create(const PhononFlowHead *head, const PhononTenso
         ok = upload(h, eos_weight, 1, PH_WIDTH, &h->eos);
     }
     ok = ok && upload_vectors(h, head, eos_bias) && alloc_buffers(h, max_streams) &&
+         alloc_flow_buffers(h) &&
          enqueue_tsum(h, 0.0f, 1.0f, h->tsum_lsd) && phonon_flow_head_device_sync(h);
     if (!ok) {
         phonon_flow_head_device_destroy(h);
@@ -288,6 +413,9 @@ void phonon_flow_head_device_destroy(PhononFlowHeadDevice *h) {
     pgpu_free(h->out_norm);
     pgpu_free(h->input_linear_dev);
     pgpu_free(h->buffers);
+    pgpu_free(h->flow_buffers);
+    for (size_t i = 0; i < h->nlists; i++)
+        pgpu_free(h->lists[i].dev);
     pgpu_free(h->status);
     if (h->own_stream && h->stream != h->own_stream)
         (void)pgpu_stream_sync(h->own_stream);
@@ -308,6 +436,65 @@ int phonon_flow_head_device_sync(PhononFlowHeadDevice *h) {
     return status == 0;
 }
 
+/* The LSD step as one launch (and the counter reset): the same tasks and
+ * bits as enqueue_head + the embedding. */
+static int enqueue_flow(PhononFlowHeadDevice *h, size_t streams, const float *conditions,
+                        const float *norm, const float *raw_noise, float scale,
+                        float *latents, float *eos_logits, const float *embed, float *next) {
+    pgpu_head_flow f;
+    memset(&f, 0, sizeof(f));
+    f.streams = (int)streams;
+    f.tiles = (int)((streams + 15) / 16);
+    f.with_eos = eos_logits != NULL;
+    f.with_embed = next != NULL;
+    f.schedule = flow_list(h, f.tiles, f.with_eos, f.with_embed, &f.tasks);
+    if (!f.schedule)
+        return ph_fail("flow head: task list");
+    f.cond_w = h->cond;
+    f.eos_w = h->eos;
+    f.ada_w = h->ada;
+    f.input_w = h->input;
+    f.final_w = h->final;
+    f.embed_w = h->input_linear;
+    f.conditions = conditions;
+    f.out_norm = norm;
+    f.b_cond = h->b_cond;
+    f.tsum = h->tsum_lsd;
+    f.b_eos = h->b_eos;
+    f.b_ada = h->b_ada;
+    f.b_input = h->b_input;
+    f.b_final = h->b_final;
+    for (size_t b = 0; b < HB; b++) {
+        f.mlp_w[b][0] = h->mlp[b][0];
+        f.mlp_w[b][1] = h->mlp[b][1];
+        f.b_mlp[b][0] = h->b_mlp[b][0];
+        f.b_mlp[b][1] = h->b_mlp[b][1];
+        f.norm_w[b] = h->norm_w[b];
+        f.norm_b[b] = h->norm_b[b];
+    }
+    f.raw = raw_noise;
+    f.scale = scale;
+    f.noise = h->noise;
+    f.noise_split = h->noise_split;
+    f.silu_split = h->silu_split;
+    f.mod = h->mod;
+    f.x = h->fx;
+    f.u_split = h->fu;
+    f.eos_rows = h->eos_rows;
+    f.eos = eos_logits;
+    f.ones = h->ones;
+    f.latents = latents;
+    f.latent_split = h->latent_split;
+    f.embed_in = embed;
+    f.next = next;
+    f.counters = h->counters;
+    f.status = h->status;
+    f.wait_us = h->wait_us;
+    return pgpu_head_flow_launch(h->stream, &f) &&
+           pgpu_head_flow_reset(h->stream, h->counters,
+                                (size_t)f.tiles * PGPU_HEADC_KINDS * PGPU_HEAD_COUNTER_STRIDE);
+}
+
 /* The LSD step; with `next` (a frame): the conditions are the decoder's
  * outputs, normalized by out_norm in the head's first launch, and next =
  * input_linear . latents + embed (the latent's embedding; the final launch
@@ -316,6 +503,9 @@ int phonon_flow_head_device_sync(PhononFlowHeadDevice *h) {
 static int enqueue_lsd(PhononFlowHeadDevice *h, size_t streams, const float *conditions,
                        const float *raw_noise, float temperature, float *latents,
                        float *eos_logits, const float *embed, float *next) {
+    if (h->one_launch)
+        return enqueue_flow(h, streams, conditions, next ? h->out_norm : NULL, raw_noise,
+                            sqrtf(temperature), latents, eos_logits, embed, next);
     if (!enqueue_head(h, streams, conditions, next ? h->out_norm : NULL, raw_noise,
                       sqrtf(temperature), h->tsum_lsd, 1, latents, next ? h->noise_split : NULL,
                       eos_logits, NULL, NULL))
@@ -343,6 +533,11 @@ static int run_lsd(PhononFlowHeadDevice *h, size_t streams, const float *conditi
     for (size_t i = 0; i < sizeof(aligned) / sizeof(aligned[0]); i++)
         if ((uintptr_t)aligned[i] % 16)
             return ph_fail("flow head: device rows must be 16-byte aligned");
+    /* The one-launch task list is built (and uploaded) outside any capture. */
+    int tasks;
+    if (h->one_launch &&
+        !flow_list(h, (int)((streams + 15) / 16), eos_logits != NULL, next != NULL, &tasks))
+        return ph_fail("flow head: task list");
     if (h->eager)
         return enqueue_lsd(h, streams, conditions, raw_noise, temperature, latents, eos_logits,
                            embed, next);
@@ -441,6 +636,28 @@ int phonon_flow_head_device_set_graph(PhononFlowHeadDevice *h, int use_graph) {
     if (!pgpu_stream_sync(h->stream))
         return 0;
     h->eager = !use_graph;
+    for (size_t i = 0; i < 2; i++) {
+        pgpu_graph_destroy(h->graphs[i].exec);
+        h->graphs[i].exec = NULL;
+    }
+    return 1;
+}
+
+int phonon_flow_head_device_set_one_launch(PhononFlowHeadDevice *h, int one_launch) {
+    if (!h || !pgpu_stream_sync(h->stream))
+        return 0;
+    h->one_launch = one_launch != 0;
+    for (size_t i = 0; i < 2; i++) {
+        pgpu_graph_destroy(h->graphs[i].exec);
+        h->graphs[i].exec = NULL;
+    }
+    return 1;
+}
+
+int phonon_flow_head_device_set_wait_limit(PhononFlowHeadDevice *h, unsigned microseconds) {
+    if (!h || !pgpu_stream_sync(h->stream))
+        return 0;
+    h->wait_us = microseconds;
     for (size_t i = 0; i < 2; i++) {
         pgpu_graph_destroy(h->graphs[i].exec);
         h->graphs[i].exec = NULL;

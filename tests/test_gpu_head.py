@@ -265,3 +265,107 @@ def test_head_on_a_callers_stream(lib, pkg):
         b.free()
     lib.phonon_flow_head_device_destroy(dev)
     lib.pgpu_stream_destroy(mine)
+
+
+def _head_with_frame(lib, pkg, views, seed, max_streams=64):
+    """A device head with the EOS row and the frame's output norm and
+    latent embedding, random BF16 weights."""
+    rng = np.random.default_rng(seed)
+    head = views.flow_head(helpers.random_flow_head_bits(seed))
+    ew = views.bf16(helpers.bf16_bits(rng.standard_normal((1, 512)).astype(np.float32) * 0.05),
+                    (1, 512))
+    eb = views.bf16(helpers.bf16_bits(np.array([0.0625], np.float32)), (1,))
+    nw = views.bf16(helpers.bf16_bits(1.0 + 0.1 * rng.standard_normal(512).astype(np.float32)),
+                    (512,))
+    nb = views.bf16(helpers.bf16_bits(0.1 * rng.standard_normal(512).astype(np.float32)),
+                    (512,))
+    lv = views.bf16(helpers.bf16_bits(rng.standard_normal((512, 32)).astype(np.float32) * 0.2),
+                    (512, 32))
+    dev = ctypes.c_void_p()
+    assert lib.phonon_flow_head_device_create(ctypes.byref(head), ctypes.byref(ew),
+                                              ctypes.byref(eb), max_streams, ctypes.byref(dev))
+    assert lib.phonon_flow_head_device_set_frame(dev, ctypes.byref(nw), ctypes.byref(nb),
+                                                 ctypes.byref(lv))
+    return dev
+
+
+@pytest.mark.parametrize("streams", [1, 5, 17, 64])
+def test_one_launch_head_equals_the_chain(lib, pkg, streams):
+    """phonon_flow_head_device_set_one_launch: the LSD step (with and
+    without the EOS logit) and the frame as one dataflow launch give the
+    chain's bits, from a replayed graph and launched directly, and again on
+    a second call (the counters are reset after each launch)."""
+    views = pkg.Views()
+    dev = _head_with_frame(lib, pkg, views, 51 + streams)
+    stream = lib.phonon_flow_head_device_stream(dev)
+    rng = np.random.default_rng(52)
+    outputs = (rng.standard_normal((streams, 512)) * 2).astype(np.float32)
+    cond = rng.standard_normal((streams, 512)).astype(np.float32)
+    raw = rng.standard_normal((streams, 32)).astype(np.float32)
+    bufs = [pkg.DeviceBuffer(lib, n) for n in (outputs.nbytes, cond.nbytes, raw.nbytes,
+                                               raw.nbytes, streams * 4, cond.nbytes)]
+    do, dc, dr, dl, de, dn = bufs
+    do.upload(outputs)
+    dc.upload(cond)
+    dr.upload(raw)
+
+    def run(mode):
+        got = {}
+        for eos in (True, False):
+            assert lib.phonon_flow_head_device_lsd(dev, streams, dc.ptr, dr.ptr, 0.8, dl.ptr,
+                                                   de.ptr if eos else None)
+            assert lib.phonon_flow_head_device_sync(dev), (mode, pkg.last_error(lib))
+            got[f"lat{int(eos)}"] = dl.download((streams, 32), stream=stream)
+            if eos:
+                got["eos"] = de.download((streams,), stream=stream)
+        assert lib.phonon_flow_head_device_frame(dev, streams, do.ptr, dc.ptr, dr.ptr, 0.6,
+                                                 dl.ptr, de.ptr, dn.ptr)
+        assert lib.phonon_flow_head_device_sync(dev), (mode, pkg.last_error(lib))
+        got["frame_lat"] = dl.download((streams, 32), stream=stream)
+        got["frame_eos"] = de.download((streams,), stream=stream)
+        got["next"] = dn.download((streams, 512), stream=stream)
+        return got
+
+    assert lib.phonon_flow_head_device_set_one_launch(dev, 0)
+    chain = run("chain")
+    for graph in (1, 0):
+        assert lib.phonon_flow_head_device_set_graph(dev, graph)
+        assert lib.phonon_flow_head_device_set_one_launch(dev, 1)
+        for rep in range(2):
+            one = run(f"one launch graph={graph} rep={rep}")
+            for k in chain:
+                assert np.array_equal(one[k], chain[k]), (k, graph, rep)
+    for b in bufs:
+        b.free()
+    lib.phonon_flow_head_device_destroy(dev)
+
+
+def test_one_launch_head_forced_wait_timeout_recovers(lib, pkg):
+    """A 1 us wait limit, set from the host, makes the one-launch head's
+    waiting tasks give up: the launch ends, sync reports failure; with the
+    limit lifted the same call gives the chain's bits again."""
+    streams = 64
+    views = pkg.Views()
+    dev = _head_with_frame(lib, pkg, views, 61)
+    stream = lib.phonon_flow_head_device_stream(dev)
+    rng = np.random.default_rng(62)
+    cond = rng.standard_normal((streams, 512)).astype(np.float32)
+    raw = rng.standard_normal((streams, 32)).astype(np.float32)
+    dc, dr, dl, de = (pkg.DeviceBuffer(lib, n) for n in (cond.nbytes, raw.nbytes, raw.nbytes,
+                                                          streams * 4))
+    dc.upload(cond)
+    dr.upload(raw)
+    assert lib.phonon_flow_head_device_lsd(dev, streams, dc.ptr, dr.ptr, 0.8, dl.ptr, de.ptr)
+    assert lib.phonon_flow_head_device_sync(dev)
+    want = dl.download((streams, 32), stream=stream)
+    assert lib.phonon_flow_head_device_set_one_launch(dev, 1)
+    assert lib.phonon_flow_head_device_set_wait_limit(dev, 1)
+    assert lib.phonon_flow_head_device_lsd(dev, streams, dc.ptr, dr.ptr, 0.8, dl.ptr, de.ptr)
+    assert not lib.phonon_flow_head_device_sync(dev)
+    assert lib.phonon_flow_head_device_set_wait_limit(dev, 0)
+    assert lib.phonon_flow_head_device_lsd(dev, streams, dc.ptr, dr.ptr, 0.8, dl.ptr, de.ptr)
+    assert lib.phonon_flow_head_device_sync(dev), pkg.last_error(lib)
+    assert np.array_equal(dl.download((streams, 32), stream=stream), want)
+    for b in (dc, dr, dl, de):
+        b.free()
+    lib.phonon_flow_head_device_destroy(dev)
