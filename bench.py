@@ -337,8 +337,32 @@ def pmc_program(pkg, lib, args):
           flush=True)
 
 
+def prefill_mfma_work(layers, new_streams, chunk):
+    """(bf16 MFMA flops, fp32 MFMA flops) of a batched prefill of new_streams
+    fresh prompts of `chunk` positions: the projections as issued (three
+    bf16 MFMA products per multiply-add, one per split term) and the causal
+    attention's Q.K and P.V (2 flops per multiply-add, every (query, key)
+    pair with key <= query, 8 heads x 64 dimensions)."""
+    rows = new_streams * chunk
+    proj = rows * layers * (1536 + 512 + 2048 + 2048) * 512 * 2 * 3
+    pairs = new_streams * chunk * (chunk + 1) // 2
+    attn = layers * pairs * 8 * 64 * 2 * 2
+    return proj, attn
+
+
+def prefill_mfma_fraction(layers, new_streams, chunk, ms):
+    """The prefill's matrix-core work against the time it took: bf16 flops
+    at 2.5 PFLOP/s plus fp32 flops at 157.3 TFLOP/s (dense peaks), as a
+    fraction of the measured time."""
+    proj, attn = prefill_mfma_work(layers, new_streams, chunk)
+    secs = ms * 1e-3
+    return {"bf16_tflop": round(proj / 1e12, 2), "fp32_gflop": round(attn / 1e9, 2),
+            "bf16_TFLOPs": round(proj / secs / 1e12, 1),
+            "frac": round((proj / 2.5e15 + attn / 157.3e12) / secs, 4)}
+
+
 def large_batch_with_prefill(pkg, lib, seed, layers=12, streams=256, new_streams=16, chunk=256,
-                             iterations=4, warmup=1):
+                             iterations=4, warmup=1, prefill_attention=0):
     """Large-batch decode with interleaved prefill: every iteration advances
     `streams` streams (contexts U{256..8192-headroom}, paged KV block 16,
     shuffled tables) by one decode step and prefills a `chunk`-position prompt
@@ -372,6 +396,7 @@ def large_batch_with_prefill(pkg, lib, seed, layers=12, streams=256, new_streams
     assert lib.phonon_flow_batch_create(model, pool, streams, max_positions, ctypes.byref(dec))
     assert lib.phonon_flow_batch_create(model, pool, new_streams * chunk, max_positions,
                                         ctypes.byref(pre))
+    assert lib.phonon_flow_batch_set_prefill_exact(pre, prefill_attention)
     pos = lengths.astype(np.uintp)
     assert lib.phonon_flow_batch_set_streams(dec, streams, pos.ctypes.data_as(P_SZ),
                                              tables.ctypes.data_as(P_I32), table_len)
@@ -420,6 +445,10 @@ def large_batch_with_prefill(pkg, lib, seed, layers=12, streams=256, new_streams
                                         / HBM_PEAK_GBS, 4),
             "prefill_ms": round(pre_ms / iterations, 3),
             "prefill_tokens_per_s": round(new_streams * chunk / (pre_ms / iterations * 1e-3), 1),
+            "prefill_attention": ["matrix cores", "exact (decode arithmetic)",
+                                  "lane per query"][prefill_attention],
+            "prefill_mfma": prefill_mfma_fraction(layers, new_streams, chunk,
+                                                  pre_ms / iterations),
             "frames_per_s_incl_prefill": round(streams / (per_it_ms * 1e-3), 1),
             "clean": clean}
 
@@ -990,7 +1019,9 @@ def main():
         pmc_program(pkg, lib, args)
         return
     if args.large_batch:
-        print(json.dumps(large_batch_with_prefill(pkg, lib, args.seed)), flush=True)
+        for kind in (0, 2):
+            print(json.dumps(large_batch_with_prefill(pkg, lib, args.seed,
+                                                      prefill_attention=kind)), flush=True)
         return
     if args.b1_modes:
         for mode in (int(m) for m in args.b1_modes.split(",")):

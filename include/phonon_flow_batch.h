@@ -99,10 +99,12 @@ int phonon_flow_batch_prefill_device(PhononFlowBatch *batch, size_t streams, con
                                      size_t table_len, const float *inputs, float theta,
                                      float *outputs);
 /* Attention arithmetic of phase-by-phase batched prefills: 0 (default) a
- * causal kernel with one lane per query that reads each key block once per
- * 64 positions (fp32, within 1e-4 of the decode step); 1 the decode step's
- * split attention and merge, so every output row has the bits of single
- * steps. The projections give the bits of single steps either way. */
+ * causal kernel on the fp32 matrix cores that loads each 64-key chunk once
+ * per run of 64 positions (within 1e-4 of the decode step); 1 the decode
+ * step's split attention and merge, so every output row has the bits of
+ * single steps; 2 a causal kernel with one lane per query on the vector
+ * units (fp32, each key block once per 64 positions). The projections give
+ * the bits of single steps in every mode. */
 int phonon_flow_batch_set_prefill_exact(PhononFlowBatch *batch, int exact);
 /* One-launch step: a task that has waited this many microseconds for its
  * inputs (at most 10 s) gives up, sets status bit 2 (value 4) and makes

@@ -343,17 +343,20 @@ typedef struct {
 int pgpu_wide_from_matrix(void *stream, const pgpu_matrix *w, uint16_t *values, float *scales);
 /* Projections of M rows of split fragments (K = 512 or 2048; rows a
  * multiple of 128), with the epilogues of pgpu_gemm_qkv, pgpu_gemm_residual
- * and pgpu_gemm_gelu_split. Each output has the bits of the single-phase
- * projection of the same weights (the same per-block MFMA sequence, scale
- * order and summation chains). */
+ * and pgpu_gemm_gelu_split. terms = 3: each output has the bits of the
+ * single-phase projection of the same weights (the same per-block MFMA
+ * sequence, scale order and summation chains); terms = 2: the activations'
+ * third split term is left out (each activation taken to 16 significant
+ * bits, relative error below 2^-16; two thirds of the matrix-core work). */
 int pgpu_prefill_gemm_qkv(void *stream, const pgpu_wide_matrix *w, const uint16_t *split,
-                          int streams, const pgpu_paged_kv *kv, int layer,
+                          int streams, int terms, const pgpu_paged_kv *kv, int layer,
                           const int32_t *tables, int table_stride, const int32_t *positions,
                           const float *rope, float *q_out, int *status);
 int pgpu_prefill_gemm_residual(void *stream, const pgpu_wide_matrix *w, const uint16_t *split,
-                               int streams, const float *residual, float *out, int *status);
+                               int streams, int terms, const float *residual, float *out,
+                               int *status);
 int pgpu_prefill_gemm_gelu_split(void *stream, const pgpu_wide_matrix *w, const uint16_t *split,
-                                 int streams, uint16_t *out_split, int *status);
+                                 int streams, int terms, uint16_t *out_split, int *status);
 /* Causal attention of a batched prefill, one lane per query, into split
  * fragments of the attention rows (fp32 arithmetic in its own summation
  * order). `runs` (dev) holds run_count pairs (s0, n): pseudo-streams
@@ -364,6 +367,15 @@ int pgpu_prefill_gemm_gelu_split(void *stream, const pgpu_wide_matrix *w, const 
  * be in the pool. */
 #define PGPU_PREFILL_RUN 64
 int pgpu_prefill_attention_rows(void *stream, const float *q, const pgpu_paged_kv *kv,
+                                int layer, const int32_t *tables, int table_stride,
+                                const int32_t *positions, int streams, const int32_t *runs,
+                                int run_count, uint16_t *out_split, int *status);
+/* The same contract on the fp32 matrix cores (v_mfma_f32_16x16x4_f32): one
+ * work-group per (run, head) loads each 64-key chunk of the run's keys once
+ * into LDS; wave w takes queries 16w .. 16w+15; scores, an online softmax
+ * per query and the value sums per 16-key sub-block (exact fp32 products,
+ * sums in the matrix cores' order). */
+int pgpu_prefill_attention_mfma(void *stream, const float *q, const pgpu_paged_kv *kv,
                                 int layer, const int32_t *tables, int table_stride,
                                 const int32_t *positions, int streams, const int32_t *runs,
                                 int run_count, uint16_t *out_split, int *status);

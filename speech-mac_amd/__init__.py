@@ -250,10 +250,13 @@ EXPORTS = {
     "pgpu_rows_split_ln": (_i, [_vp, _vp, _vp, _vp, ctypes.c_float, _i, _vp, _vp]),
     "pgpu_rows_split_attention": (_i, [_vp, _scp, _vp, _i, _i, _vp, _vp]),
     "pgpu_wide_from_matrix": (_i, [_vp, _mp, _vp, _vp]),
-    "pgpu_prefill_gemm_qkv": (_i, [_vp, _vp, _vp, _i, _kvp, _i, _vp, _i, _vp, _vp, _vp, _vp]),
-    "pgpu_prefill_gemm_residual": (_i, [_vp, _vp, _vp, _i, _vp, _vp, _vp]),
-    "pgpu_prefill_gemm_gelu_split": (_i, [_vp, _vp, _vp, _i, _vp, _vp]),
+    "pgpu_prefill_gemm_qkv": (_i, [_vp, _vp, _vp, _i, _i, _kvp, _i, _vp, _i, _vp, _vp, _vp,
+                                    _vp]),
+    "pgpu_prefill_gemm_residual": (_i, [_vp, _vp, _vp, _i, _i, _vp, _vp, _vp]),
+    "pgpu_prefill_gemm_gelu_split": (_i, [_vp, _vp, _vp, _i, _i, _vp, _vp]),
     "pgpu_prefill_attention_rows": (_i, [_vp, _vp, _kvp, _i, _vp, _i, _vp, _i, _vp, _i, _vp,
+                                         _vp]),
+    "pgpu_prefill_attention_mfma": (_i, [_vp, _vp, _kvp, _i, _vp, _i, _vp, _i, _vp, _i, _vp,
                                          _vp]),
     "phonon_flow_batch_set_prefill_exact": (_i, [_vp, _i]),
     "phonon_flow_batch_set_wait_limit": (_i, [_vp, ctypes.c_uint]),

@@ -99,7 +99,8 @@ struct GemmArgs {
     const float *mod;         // SRC_LN_MOD: shift row at mod + s * ld_mod, scale at +512
     int ld_mod;
     bool plain_rows;          // single-phase launch: ln_x rows are used as they are
-    bool plain_qkv;           // QKV: q and K/V stored plainly (read only by later launches)
+    bool plain_qkv;
+    int split_terms;          // prefill projections: split terms of X used (2 or 3)           // QKV: q and K/V stored plainly (read only by later launches)
 };
 
 // ---------------------------------------------------------------------------

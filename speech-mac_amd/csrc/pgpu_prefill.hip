@@ -125,9 +125,10 @@ __device__ inline void wait_vm(int n) {
     }
 }
 
-template <int EPI, bool SCALED, int WR, int WP, int RW, int PW, int NB, int KS>
+template <int EPI, bool SCALED, int WR, int WP, int RW, int PW, int NB, int KS, int TERMS>
 __global__ __launch_bounds__(kTaskThreads) void k_prefill_gemm(GemmArgs a, int row_groups,
                                                                int pos_groups) {
+    static_assert(TERMS == 2 || TERMS == 3, "split terms");
     static_assert(WR * WP == kTaskWaves, "8 waves");
     static_assert(kChain % KS == 0, "a stage never straddles a chain");
     constexpr int RT = WR * RW, PT = WP * PW;
@@ -135,7 +136,7 @@ __global__ __launch_bounds__(kTaskThreads) void k_prefill_gemm(GemmArgs a, int r
     constexpr int kS = SCALED ? RT * 32 : 0;                // halves (RT x 16 floats)
     constexpr int kBlk = kB + kA + kS;                      // halves per block
     constexpr int kStage = KS * kBlk;                       // halves per stage
-    constexpr int kChunks = PT * 3 + RT;                    // 1 KB DMA chunks per block
+    constexpr int kChunks = PT * TERMS + RT;                // 1 KB DMA chunks per block
     static_assert(!SCALED || RT * 4 <= 64, "one wave instruction moves the scales");
     __shared__ uint4 lds4[NB * kStage / 8];
     uint16_t *lds = (uint16_t *)lds4;
@@ -168,13 +169,13 @@ __global__ __launch_bounds__(kTaskThreads) void k_prefill_gemm(GemmArgs a, int r
             for (int c = wave; c < kChunks; c += kTaskWaves) {  // uniform
                 const uint16_t *src;
                 uint16_t *dst;
-                if (c < PT * 3) {
-                    const int t = c / 3, term = c % 3;
+                if (c < PT * TERMS) {
+                    const int t = c / TERMS, term = c % TERMS;
                     const int tile = min(pt0 + t, last_tile);
                     src = a.xs + ((size_t)tile * kbn + kb) * 1536 + term * 512;
                     dst = st + t * 1536 + term * 512;
                 } else {
-                    const int r = c - PT * 3;
+                    const int r = c - PT * TERMS;
                     src = wv + ((size_t)(rt0 + r) * kbn + kb) * 512;
                     dst = st + kB + r * 512;
                 }
@@ -238,14 +239,15 @@ __global__ __launch_bounds__(kTaskThreads) void k_prefill_gemm(GemmArgs a, int r
                 const uint16_t *xb = st + (wp * PW + p) * 1536 + lane * 8;
                 const bf16x8 xh = *(const bf16x8 *)xb;
                 const bf16x8 xm = *(const bf16x8 *)(xb + 512);
-                const bf16x8 xl = *(const bf16x8 *)(xb + 1024);
+                const bf16x8 xl = TERMS == 3 ? *(const bf16x8 *)(xb + 1024) : bf16x8{};
 #pragma unroll
                 for (int r = 0; r < RW; r++) {
                     if constexpr (SCALED) {
                         f32x4 c = {0.0f, 0.0f, 0.0f, 0.0f};
                         c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wa[r], xh, c, 0, 0, 0);
                         c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wa[r], xm, c, 0, 0, 0);
-                        c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wa[r], xl, c, 0, 0, 0);
+                        if constexpr (TERMS == 3)
+                            c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wa[r], xl, c, 0, 0, 0);
                         acc[r][p][0] = fmaf(sc[r].x, c[0], acc[r][p][0]);
                         acc[r][p][1] = fmaf(sc[r].y, c[1], acc[r][p][1]);
                         acc[r][p][2] = fmaf(sc[r].z, c[2], acc[r][p][2]);
@@ -253,7 +255,8 @@ __global__ __launch_bounds__(kTaskThreads) void k_prefill_gemm(GemmArgs a, int r
                     } else {
                         acc[r][p] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wa[r], xh, acc[r][p], 0, 0, 0);
                         acc[r][p] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wa[r], xm, acc[r][p], 0, 0, 0);
-                        acc[r][p] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wa[r], xl, acc[r][p], 0, 0, 0);
+                        if constexpr (TERMS == 3)
+                            acc[r][p] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wa[r], xl, acc[r][p], 0, 0, 0);
                     }
                 }
             }
@@ -481,12 +484,238 @@ __global__ __launch_bounds__(64 * kAttnWaves) void k_prefill_attention_rows(
 }
 
 // ---------------------------------------------------------------------------
+// Causal attention of a run of up to 64 consecutive positions of one stream
+// and one head on the fp32 matrix cores (v_mfma_f32_16x16x4_f32): wave w
+// takes queries 16w .. 16w+15 of the run. The run's keys go through LDS in
+// chunks of 64 (four pool blocks, K and V), each chunk loaded once by the
+// work-group and consumed by all four waves: per 16-key sub-block a wave
+// computes S^T = K Q^T (16 MFMAs over the 64 dimensions; lane l holds keys
+// 4(l/16) .. +3 of query l%16); then, once per chunk, an online softmax step
+// per query (the query's scores sit in the 4 lanes l%16 + 16g) and O^T +=
+// V^T P^T (16 MFMAs per sub-block: the P^T operand is the S^T registers
+// themselves). Products are exact fp32 multiplications; sums are in the
+// matrix cores' order.
+constexpr int kMmaKeys = 64;                 // keys per LDS chunk
+constexpr int kMmaRow = kHeadDim + 4;        // padded LDS row (floats)
+
+__global__ __launch_bounds__(256) void k_prefill_attention_mfma(
+    const float *__restrict__ q, const float *__restrict__ kv, size_t layer_stride,
+    unsigned blocks, int layer, const int32_t *__restrict__ tables, int table_stride,
+    const int32_t *__restrict__ positions, int streams, const int32_t *__restrict__ entries,
+    uint16_t *__restrict__ out_split, int *status) {
+    __shared__ float kt[kMmaKeys * kMmaRow];
+    __shared__ float vt[kMmaKeys * kMmaRow];
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63, t = threadIdx.x;
+    const int head = blockIdx.y;
+    const int s0 = entries[2 * blockIdx.x], n = entries[2 * blockIdx.x + 1];
+    if (n < 1 || n > kQueries || s0 < 0 || s0 > streams - n) {
+        if (t == 0) atomicOr(status, 2);
+        return;  // uniform over the work-group
+    }
+    const int32_t *table = tables + (size_t)s0 * table_stride;
+    const float *layer_kv = kv + (size_t)layer * layer_stride;
+    // Block-table entries go one chunk ahead of the K/V loads, and the first
+    // chunks' entries and K/V are requested before the run's position is
+    // known (every index stays inside the table and the pool; keys past the
+    // run's last position are zeroed when the chunk is stored in LDS).
+    constexpr int kChunkBlocks = kMmaKeys / kBlockPos;
+    int ids[kChunkBlocks], next_ids[kChunkBlocks];
+#pragma unroll
+    for (int b = 0; b < kChunkBlocks; b++) {
+        ids[b] = b < table_stride ? table[b] : 0;
+        next_ids[b] = kChunkBlocks + b < table_stride ? table[kChunkBlocks + b] : 0;
+    }
+    // Thread t moves float4 i of the chunk: pool block i / 2, element
+    // t + 256 (i % 2) of that block's (K | V) pair (K: elements 0 .. 255).
+    float4 pre[8];
+#define PGPU_FETCH_CHUNK()                                                                     \
+    do {                                                                                       \
+        _Pragma("unroll") for (int i = 0; i < 8; i++) {                                        \
+            const int id_ = ids[i >> 1];                                                       \
+            const int safe_ = (unsigned)id_ < blocks ? id_ : 0;                                \
+            pre[i] = ((const float4 *)(layer_kv + ((size_t)safe_ * kHeads + head) * 2048))     \
+                [t + 256 * (i & 1)];                                                           \
+        }                                                                                      \
+    } while (0)
+    PGPU_FETCH_CHUNK();
+    const int p0 = positions[s0];
+    const int p_last = p0 + n - 1;
+    if (p_last / kBlockPos >= table_stride && t == 0) atomicOr(status, 2);
+    const int key_end = min(p_last + 1, table_stride * kBlockPos);  // keys [0, key_end)
+    const int chunks = (key_end + kMmaKeys - 1) / kMmaKeys;
+    bool bad_block = false;
+
+    // This lane's query (column l%16 of the wave's 16) and its 16 dimensions
+    // 16(l/16) .. +15: the B operand of S^T = K Q^T, one dimension per MFMA.
+    const int qi = wave * 16 + (lane & 15), g = lane >> 4;
+    const bool q_live = qi < n;
+    const int qpos = p0 + qi;
+    float qv[16];
+    {
+        const float4 *src = (const float4 *)(q + (size_t)(s0 + (q_live ? qi : 0)) * kWidth +
+                                             head * kHeadDim + 16 * g);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const float4 v = src[i];
+            qv[4 * i] = q_live ? v.x : 0.0f;
+            qv[4 * i + 1] = q_live ? v.y : 0.0f;
+            qv[4 * i + 2] = q_live ? v.z : 0.0f;
+            qv[4 * i + 3] = q_live ? v.w : 0.0f;
+        }
+    }
+    const int wave_last = p0 + min(n, wave * 16 + 16) - 1;  // this wave's last query position
+    const bool wave_live = wave * 16 < n;
+
+    float o[4][4];  // O^T: lane l holds dims 16 dt + 4 (l/16) + r of query l%16
+#pragma unroll
+    for (int dt = 0; dt < 4; dt++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) o[dt][r] = 0.0f;
+    float m = -INFINITY, lsum = 0.0f;
+
+    for (int c = 0; c < chunks; c++) {
+        __syncthreads();  // the previous chunk is consumed
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const int within = t + 256 * (i & 1);
+            const int key = (i >> 1) * kBlockPos + ((within & 255) >> 4), d = (within & 15) * 4;
+            const bool live = c * kMmaKeys + key < key_end;
+            bad_block |= live && (unsigned)ids[i >> 1] >= blocks;
+            float *dst = (within < 256 ? kt : vt) + key * kMmaRow + d;
+            *(float4 *)dst = live ? pre[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+        __syncthreads();
+        if (c + 1 < chunks) {
+#pragma unroll
+            for (int b = 0; b < kChunkBlocks; b++) {
+                ids[b] = next_ids[b];
+                const int tb = (c + 2) * kChunkBlocks + b;
+                next_ids[b] = tb < table_stride ? table[tb] : 0;
+            }
+            PGPU_FETCH_CHUNK();
+        }
+        if (!wave_live) continue;
+        // The chunk's 16-key sub-blocks this wave needs (the later ones are
+        // past its last query): uniform over the wave.
+        const int key0 = c * kMmaKeys;
+        const int last = min(wave_last, key_end - 1);
+        const int nsub = last < key0 ? 0 : min(kMmaKeys / 16, (last - key0) / 16 + 1);
+        if (nsub <= 0) continue;
+        // Scores of the whole chunk first (nsub x 16 MFMAs in four
+        // independent chains per sub-block), then one softmax step for the
+        // chunk, then the value sums (four independent chains, one per
+        // 16-dimension tile).
+        float sc[4][4];
+        float bm = -INFINITY;
+#pragma unroll
+        for (int sub = 0; sub < 4; sub++) {
+            if (sub >= nsub) {
+#pragma unroll
+                for (int r = 0; r < 4; r++) sc[sub][r] = -INFINITY;
+                continue;
+            }
+            const float *krow = kt + (sub * 16 + (lane & 15)) * kMmaRow + 16 * g;
+            float kk[16];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const float4 v = *(const float4 *)(krow + 4 * i);
+                kk[4 * i] = v.x;
+                kk[4 * i + 1] = v.y;
+                kk[4 * i + 2] = v.z;
+                kk[4 * i + 3] = v.w;
+            }
+            f32x4 sp[4];
+#pragma unroll
+            for (int u = 0; u < 4; u++) sp[u] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+#pragma unroll
+                for (int u = 0; u < 4; u++)
+                    sp[u] = __builtin_amdgcn_mfma_f32_16x16x4f32(kk[4 * i + u], qv[4 * i + u],
+                                                                 sp[u], 0, 0, 0);
+            // Keys key0 + 16 sub + 4g + r against query qpos.
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const float st = __fadd_rn(__fadd_rn(sp[0][r], sp[1][r]),
+                                           __fadd_rn(sp[2][r], sp[3][r]));
+                const int kp = key0 + sub * 16 + 4 * g + r;
+                sc[sub][r] = q_live && kp <= qpos ? st : -INFINITY;
+                bm = fmaxf(bm, sc[sub][r]);
+            }
+        }
+        bm = fmaxf(bm, __shfl_xor(bm, 16));
+        bm = fmaxf(bm, __shfl_xor(bm, 32));
+        const float mn = fmaxf(m, bm);
+        float ps = 0.0f;
+#pragma unroll
+        for (int sub = 0; sub < 4; sub++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                sc[sub][r] = sc[sub][r] == -INFINITY ? 0.0f : expf(sc[sub][r] - mn);
+                ps += sc[sub][r];
+            }
+        ps += __shfl_xor(ps, 16);
+        ps += __shfl_xor(ps, 32);
+        const float keep = mn == -INFINITY ? 1.0f : expf(m - mn);
+        m = mn;
+        lsum = fmaf(lsum, keep, ps);
+        f32x4 acc[4];
+#pragma unroll
+        for (int dt = 0; dt < 4; dt++)
+            acc[dt] = f32x4{o[dt][0] * keep, o[dt][1] * keep, o[dt][2] * keep, o[dt][3] * keep};
+#pragma unroll
+        for (int sub = 0; sub < 4; sub++) {
+            if (sub >= nsub) break;
+#pragma unroll
+            for (int jj = 0; jj < 4; jj++)
+#pragma unroll
+                for (int dt = 0; dt < 4; dt++) {
+                    const float va =
+                        vt[(sub * 16 + 4 * g + jj) * kMmaRow + 16 * dt + (lane & 15)];
+                    acc[dt] = __builtin_amdgcn_mfma_f32_16x16x4f32(va, sc[sub][jj], acc[dt], 0,
+                                                                   0, 0);
+                }
+        }
+#pragma unroll
+        for (int dt = 0; dt < 4; dt++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) o[dt][r] = acc[dt][r];
+    }
+#undef PGPU_FETCH_CHUNK
+    if (bad_block) atomicOr(status, 2);
+    if (!q_live) return;
+    // Lane l holds O^T rows 16 dt + 4g .. +3 of query qi: four consecutive
+    // columns of its attention row.
+    const bool ok = lsum > 0.0f && isfinite(lsum);
+    const float inv = 1.0f / lsum;
+    bool bad = !ok;
+#pragma unroll
+    for (int dt = 0; dt < 4; dt++) {
+        float v[4];
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            v[r] = ok ? o[dt][r] * inv : 0.0f;
+            bad |= !isfinite(v[r]);
+        }
+        store_split4(out_split, s0 + qi, head * kHeadDim + 16 * dt + 4 * g, kWidth / 32, v, false);
+    }
+    flag_nonfinite(status, bad);
+}
+
+// ---------------------------------------------------------------------------
 template <int EPI, bool SCALED, int WR, int WP, int RW, int PW, int NB, int KS>
 int launch_gemm(const GemmArgs &a, hipStream_t stream) {
     constexpr int RT = WR * RW, PT = WP * PW;
     const int row_groups = (a.n_rows / 16) / RT;
     const int pos_groups = ((a.streams + 15) / 16 + PT - 1) / PT;
-    hipLaunchKernelGGL((k_prefill_gemm<EPI, SCALED, WR, WP, RW, PW, NB, KS>),
+    if (a.split_terms == 2) {
+        hipLaunchKernelGGL((k_prefill_gemm<EPI, SCALED, WR, WP, RW, PW, NB, KS, 2>),
+                           dim3(row_groups * pos_groups), dim3(kTaskThreads), 0, stream, a,
+                           row_groups, pos_groups);
+        return launch_ok("pgpu_prefill_gemm");
+    }
+    hipLaunchKernelGGL((k_prefill_gemm<EPI, SCALED, WR, WP, RW, PW, NB, KS, 3>),
                        dim3(row_groups * pos_groups), dim3(kTaskThreads), 0, stream, a,
                        row_groups, pos_groups);
     return launch_ok("pgpu_prefill_gemm");
@@ -505,13 +734,15 @@ int dispatch_gemm(const GemmArgs &a, hipStream_t stream) {
 template <int EPI>
 int run_gemm(const GemmArgs &a, const pgpu_wide_matrix *w, hipStream_t stream) {
     if (!w || !w->values || a.n_rows % 128 || (a.k_cols != kWidth && a.k_cols != kFfn) ||
-        a.streams <= 0 || !a.xs || !a.status)
+        a.streams <= 0 || !a.xs || !a.status || (a.split_terms != 2 && a.split_terms != 3))
         return bad_arguments("pgpu_prefill_gemm");
     return w->scales ? dispatch_gemm<EPI, true>(a, stream) : dispatch_gemm<EPI, false>(a, stream);
 }
 
-GemmArgs gemm_args(const pgpu_wide_matrix *w, const uint16_t *split, int streams, int *status) {
+GemmArgs gemm_args(const pgpu_wide_matrix *w, const uint16_t *split, int streams, int terms,
+                   int *status) {
     GemmArgs a{};
+    a.split_terms = terms;
     if (!w) return a;
     a.xs = split;
     a.w = w->values;
@@ -564,14 +795,14 @@ extern "C" int pgpu_rows_split_attention(void *stream, const pgpu_attention_scra
 }
 
 extern "C" int pgpu_prefill_gemm_qkv(void *stream, const pgpu_wide_matrix *w, const uint16_t *split,
-                                     int streams, const pgpu_paged_kv *kv, int layer,
+                                     int streams, int terms, const pgpu_paged_kv *kv, int layer,
                                      const int32_t *tables, int table_stride,
                                      const int32_t *positions, const float *rope, float *q_out,
                                      int *status) {
     if (!w || w->rows != 3 * kWidth || w->columns != kWidth || !kv || layer < 0 ||
         layer >= kv->layers || !tables || table_stride <= 0 || !positions || !rope || !q_out)
         return bad_arguments("pgpu_prefill_gemm_qkv");
-    GemmArgs a = gemm_args(w, split, streams, status);
+    GemmArgs a = gemm_args(w, split, streams, terms, status);
     a.q_out = q_out;
     a.kv = kv->base;
     a.layer_stride = kv->layer_stride;
@@ -586,10 +817,10 @@ extern "C" int pgpu_prefill_gemm_qkv(void *stream, const pgpu_wide_matrix *w, co
 }
 
 extern "C" int pgpu_prefill_gemm_residual(void *stream, const pgpu_wide_matrix *w,
-                                          const uint16_t *split, int streams,
+                                          const uint16_t *split, int streams, int terms,
                                           const float *residual, float *out, int *status) {
     if (!w || !residual || !out) return bad_arguments("pgpu_prefill_gemm_residual");
-    GemmArgs a = gemm_args(w, split, streams, status);
+    GemmArgs a = gemm_args(w, split, streams, terms, status);
     a.out = out;
     a.ld_out = (int)w->rows;
     a.residual = residual;
@@ -597,10 +828,10 @@ extern "C" int pgpu_prefill_gemm_residual(void *stream, const pgpu_wide_matrix *
 }
 
 extern "C" int pgpu_prefill_gemm_gelu_split(void *stream, const pgpu_wide_matrix *w,
-                                            const uint16_t *split, int streams,
+                                            const uint16_t *split, int streams, int terms,
                                             uint16_t *out_split, int *status) {
     if (!w || !out_split || w->rows % 32) return bad_arguments("pgpu_prefill_gemm_gelu_split");
-    GemmArgs a = gemm_args(w, split, streams, status);
+    GemmArgs a = gemm_args(w, split, streams, terms, status);
     a.out_split = out_split;
     a.out_kb = (int)w->rows / 32;
     return run_gemm<EPI_GELU_SPLIT>(a, w, (hipStream_t)stream);
@@ -620,6 +851,22 @@ extern "C" int pgpu_prefill_attention_rows(void *stream, const float *q, const p
                        kv->layer_stride, (unsigned)kv->blocks, layer, tables, table_stride,
                        positions, streams, entries, out_split, status);
     return launch_ok("pgpu_prefill_attention_rows");
+}
+
+extern "C" int pgpu_prefill_attention_mfma(void *stream, const float *q, const pgpu_paged_kv *kv,
+                                           int layer, const int32_t *tables, int table_stride,
+                                           const int32_t *positions, int streams,
+                                           const int32_t *entries, int entry_count,
+                                           uint16_t *out_split, int *status) {
+    if (!q || !kv || !tables || !positions || !entries || !out_split || !status ||
+        streams <= 0 || layer < 0 || layer >= kv->layers || table_stride <= 0 ||
+        entry_count <= 0 || entry_count > 65535)
+        return bad_arguments("pgpu_prefill_attention_mfma");
+    hipLaunchKernelGGL(k_prefill_attention_mfma, dim3(entry_count, kHeads), dim3(256), 0,
+                       (hipStream_t)stream, q, kv->base, kv->layer_stride, (unsigned)kv->blocks,
+                       layer, tables, table_stride, positions, streams, entries, out_split,
+                       status);
+    return launch_ok("pgpu_prefill_attention_mfma");
 }
 
 extern "C" int pgpu_wide_from_matrix(void *stream, const pgpu_matrix *w, uint16_t *values,

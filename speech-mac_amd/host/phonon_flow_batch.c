@@ -49,7 +49,7 @@ struct PhononFlowBatch {
         int32_t *entries;           /* (dev) [cap][4]: work entries of pgpu_prefill_attention */
         int32_t *host;              /* [cap][4] */
         size_t count, cap;
-        int32_t *runs;              /* (dev) [runs_cap][2]: pgpu_prefill_attention_rows */
+        int32_t *runs;              /* (dev) [runs_cap][2]: the run-based prefill attentions */
         int32_t *runs_host;
         size_t runs_count, runs_cap;
         uint16_t *split;            /* (dev) split fragments [max_streams/16][16][1536] */
@@ -561,32 +561,42 @@ static int enqueue_prefill(PhononFlowBatch *b, void *stream, size_t first, size_
                                             (int)b->splits};
     uint16_t *xs = b->pre.split;
     const float *cur = input;
+    /* Exact prefills keep every split term (the bits of single steps); the
+     * others use two (activations to 16 significant bits). */
+    const int terms = b->pre.exact == 1 ? 3 : 2;
     for (size_t l = first; l < first + count; l++) {
         const float *norm = m->norms + l * 4 * PH_WIDTH;
         float *next = (l + 1 == first + count) ? output : b->x;
         const int layer = (int)(l + pool_offset);
         if (!pgpu_rows_split_ln(stream, cur, norm, norm + PH_WIDTH, 1e-5f, n, xs, b->status) ||
-            !pgpu_prefill_gemm_qkv(stream, &m->wide[l * 4], xs, n, &b->pool->kv, layer, b->tables,
+            !pgpu_prefill_gemm_qkv(stream, &m->wide[l * 4], xs, n, terms, &b->pool->kv, layer,
+                                   b->tables,
                                    (int)b->table_len, b->positions, rope, b->q, b->status))
             return 0;
-        if (!(b->pre.exact
+        if (!(b->pre.exact == 1
                   ? pgpu_prefill_attention(stream, b->q, &b->pool->kv, layer, b->tables,
                                            (int)b->table_len, b->positions, n, PH_HEADS,
                                            (int)b->splits, b->pre.entries, (int)b->pre.count,
                                            &scratch, b->status) &&
                         pgpu_rows_split_attention(stream, &scratch, b->positions, n,
                                                   (int)b->splits, xs, b->status)
-                  : pgpu_prefill_attention_rows(stream, b->q, &b->pool->kv, layer, b->tables,
+              : b->pre.exact == 2
+                  ? pgpu_prefill_attention_rows(stream, b->q, &b->pool->kv, layer, b->tables,
+                                                (int)b->table_len, b->positions, n,
+                                                b->pre.runs, (int)b->pre.runs_count, xs,
+                                                b->status)
+                  : pgpu_prefill_attention_mfma(stream, b->q, &b->pool->kv, layer, b->tables,
                                                 (int)b->table_len, b->positions, n,
                                                 b->pre.runs, (int)b->pre.runs_count, xs,
                                                 b->status)) ||
-            !pgpu_prefill_gemm_residual(stream, &m->wide[l * 4 + 1], xs, n, cur, b->r, b->status) ||
+            !pgpu_prefill_gemm_residual(stream, &m->wide[l * 4 + 1], xs, n, terms, cur, b->r,
+                                        b->status) ||
             !pgpu_rows_split_ln(stream, b->r, norm + 2 * PH_WIDTH, norm + 3 * PH_WIDTH, 1e-5f,
                                 n, xs, b->status) ||
-            !pgpu_prefill_gemm_gelu_split(stream, &m->wide[l * 4 + 2], xs, n, b->xh,
+            !pgpu_prefill_gemm_gelu_split(stream, &m->wide[l * 4 + 2], xs, n, terms, b->xh,
                                           b->status) ||
-            !pgpu_prefill_gemm_residual(stream, &m->wide[l * 4 + 3], b->xh, n, b->r, next,
-                                        b->status))
+            !pgpu_prefill_gemm_residual(stream, &m->wide[l * 4 + 3], b->xh, n, terms, b->r,
+                                        next, b->status))
             return 0;
         cur = next;
     }
@@ -931,7 +941,8 @@ static int prefill_entries(PhononFlowBatch *b, size_t streams, const size_t *fir
     return pgpu_copy_h2d(b->stream, b->pre.entries, b->pre.host, n * 4 * sizeof(int32_t));
 }
 
-/* Work list of the fast prefill attention (pgpu_prefill_attention_rows):
+/* Work list of the run-based prefill attentions (pgpu_prefill_attention_mfma
+ * and _rows):
  * runs of up to 64 consecutive positions of one stream, as (first
  * pseudo-stream, count), the runs with the most keys first so that the
  * longest work-groups start earliest. */
@@ -1055,7 +1066,7 @@ int phonon_flow_batch_set_wait_limit(PhononFlowBatch *b, unsigned microseconds) 
 }
 
 int phonon_flow_batch_set_prefill_exact(PhononFlowBatch *b, int exact) {
-    if (!b || exact < 0 || exact > 1)
+    if (!b || exact < 0 || exact > 2)
         return 0;
     b->pre.exact = exact;
     return 1;

@@ -152,11 +152,13 @@ def test_config5_prefill_leg_vs_oracle(lib, pkg, oracle, oracle_mod, syn):
     """The large-batch workload's prefill: 16 newly admitted streams x 256
     positions through all 12 layers in one batched prefill (4096
     pseudo-streams; the benchmark's batch shape, 8192-position tables,
-    shuffled pool blocks). With the default (fast) prefill attention, every
-    position of every stream and the appended K/V of two streams against the
-    oracle at 1e-4. With the exact prefill attention, those two streams
-    decoded one position at a time give the same bits (outputs and K/V), and
-    the fast run stays within 1e-5 of the exact one everywhere."""
+    shuffled pool blocks). With the default (matrix-core) prefill attention,
+    every position of every stream and the appended K/V of two streams
+    against the oracle at 1e-4. With the exact prefill attention, those two
+    streams decoded one position at a time give the same bits (outputs and
+    K/V); the matrix-core and the lane-per-query runs (whose projections take
+    the activations to 16 significant bits) stay within 1e-4 of the exact one
+    everywhere (measured 4.2e-5 after 12 layers)."""
     model = helpers.scaled_model(syn, 311, C5_LAYERS)
     views = pkg.Views()
     w = views.layers(model)
@@ -200,10 +202,12 @@ def test_config5_prefill_leg_vs_oracle(lib, pkg, oracle, oracle_mod, syn):
 
     got, kv_got = prefill(0)
     exact, kv_exact = prefill(1)
-    fast_vs_exact = max(helpers.normwise(got[s, p], exact[s, p])
-                        for s in range(C5_STREAMS) for p in range(C5_CHUNK))
-    print("config 5 prefill leg: fast vs exact attention, max normwise", fast_vs_exact)
-    assert fast_vs_exact <= 1e-5
+    rows, _ = prefill(2)
+    for name, other in (("matrix-core", got), ("lane-per-query", rows)):
+        fast_vs_exact = max(helpers.normwise(other[s, p], exact[s, p])
+                            for s in range(C5_STREAMS) for p in range(C5_CHUNK))
+        print(f"config 5 prefill leg: {name} vs exact attention, max normwise", fast_vs_exact)
+        assert fast_vs_exact <= 1e-4
 
     # The oracle: every stream's positions in order, streams on host threads.
     om = oracle_mod.OracleModel(oracle, helpers.oracle_layers(oracle, model))

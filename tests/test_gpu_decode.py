@@ -622,16 +622,18 @@ def test_graph_ping_pong_equals_eager(lib, syn, pkg):
         assert np.array_equal(a, b)
 
 
-@pytest.mark.parametrize("mode,exact", [(0, 1), (2, 0), (0, 0)])
+@pytest.mark.parametrize("mode,exact", [(0, 1), (2, 0), (0, 0), (0, 2)])
 def test_batched_prefill_equals_single_steps(lib, syn, pkg, mode, exact):
     """phonon_flow_batch_prefill_device over several streams and chunks
     (a fresh stream, a continuation after an existing context, a one-position
     chunk) gives, bit for bit, the outputs and appended K/V of decoding the
     same positions one step at a time: phase by phase with the exact prefill
     attention (mode 0) and as one launch (mode 2, which always attends like
-    the decode step). Phase by phase with the fast prefill attention, the
-    first layer's K/V keep the bits (the projections are exact) and
-    everything else stays within 1e-5 (normwise per row)."""
+    the decode step). Phase by phase with the matrix-core (exact=0) or
+    lane-per-query (exact=2) prefill attention, whose projections also take
+    the activations to 16 significant bits (two split terms), every output
+    row and K/V row stays within 1e-4 (normwise per row, the fp32 contract;
+    measured <= 2e-5)."""
     layers = 2
     model = scaled_model(syn, 171, layers)
     views = pkg.Views()
@@ -701,22 +703,21 @@ def test_batched_prefill_equals_single_steps(lib, syn, pkg, mode, exact):
         v = np.zeros_like(k)
         assert lib.phonon_kv_pool_read(bt.pool, i32p(tables[i]), table_len, 0, end, fp(k), fp(v),
                                        max_pos)
-        if mode == 2 or exact:
+        if mode == 2 or exact == 1:
             assert np.array_equal(k[:, :end].view(np.uint32), kv_got[i][0].view(np.uint32)), i
             assert np.array_equal(v[:, :end].view(np.uint32), kv_got[i][1].view(np.uint32)), i
         else:
-            assert np.array_equal(k[0, :end].view(np.uint32), kv_got[i][0][0].view(np.uint32))
-            assert np.array_equal(v[0, :end].view(np.uint32), kv_got[i][1][0].view(np.uint32))
             for a, b in ((k[:, :end], kv_got[i][0]), (v[:, :end], kv_got[i][1])):
                 for ly in range(layers):
                     for p in range(end):
-                        assert helpers.normwise(b[ly, p], a[ly, p]) <= 1e-5, (i, ly, p)
+                        assert helpers.normwise(b[ly, p], a[ly, p]) <= 1e-4, (i, ly, p)
     bt.close()
-    if mode == 2 or exact:
+    if mode == 2 or exact == 1:
         assert np.array_equal(np.stack(want).view(np.uint32), got.view(np.uint32))
     else:
-        for a, b in zip(want, got):
-            assert helpers.normwise(b, a) <= 1e-5
+        worst = max(helpers.normwise(b, a) for a, b in zip(want, got))
+        print(f"prefill (attention mode {exact}) vs single steps: max normwise {worst:.3g}")
+        assert worst <= 1e-4
 
 
 @pytest.mark.parametrize("streams", [1, 16, 17, 40, 64])
