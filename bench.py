@@ -565,6 +565,55 @@ def q8_matvec_bench(pkg, lib, seed=1, calls=2000):
     return res
 
 
+def gemv_valu_vs_mfma(pkg, lib, seed=3, calls=400, copies=300):
+    """Small-batch Q8 products, vector units (phonon_q8_device_matvec_valu:
+    pgpu_q8_gemv, the reference's arithmetic, one lane per 32-column block)
+    against the matrix cores (phonon_q8_device_matvec: the projection task,
+    exact split MFMA), for batch 1, 2, 4, 8 at the two projection shapes of
+    the decode step; each call reads one of `copies` weight copies in turn
+    (more bytes than the 256 MB Infinity Cache holds). Kernel time from HIP
+    events over `calls` back-to-back calls on one stream."""
+    import speech_mac_amd.synthetic as syn
+    stream = ctypes.c_void_p()
+    assert lib.pgpu_stream_create(ctypes.byref(stream))
+    timer = Timer(lib, stream)
+    out = {}
+    for rows, cols in ((2048, 512), (512, 2048)):
+        rng = np.random.default_rng(seed + rows)
+        w = syn.q8_matrix(rng, rows, cols)
+        h = ctypes.c_void_p()
+        assert lib.phonon_q8_device_create(w.ctypes.data, rows, cols, copies, ctypes.byref(h))
+        x = rng.standard_normal((8, cols)).astype(np.float32)
+        dx = pkg.DeviceBuffer(lib, x.nbytes)
+        dx.upload(x)
+        dy = pkg.DeviceBuffer(lib, 8 * rows * 4)
+        shape = {}
+        for batch in (1, 2, 4, 8):
+            row = {}
+            for name, fn in (("valu", lib.phonon_q8_device_matvec_valu),
+                             ("mfma", lib.phonon_q8_device_matvec)):
+                for i in range(20):
+                    assert fn(h, i % copies, dx.ptr, dy.ptr, batch, stream)
+                timer.start()
+                for i in range(calls):
+                    fn(h, i % copies, dx.ptr, dy.ptr, batch, stream)
+                ms = timer.stop_ms() / calls
+                nbytes = lib.phonon_q8_device_bytes_per_call(h, batch)
+                row[name] = {"us_per_call": round(ms * 1e3, 2),
+                             "GBps": round(nbytes / (ms * 1e-3) / 1e9, 1)}
+            shape[f"batch_{batch}"] = row
+        assert lib.phonon_q8_device_status(h, stream)
+        out[f"{rows}x{cols}"] = shape
+        dx.free()
+        dy.free()
+        lib.phonon_q8_device_destroy(h)
+    lib.pgpu_stream_destroy(stream)
+    out["note"] = ("kernel time per call from HIP events (back-to-back calls, rotating "
+                   f"{copies} weight copies); valu = vector-unit GEMV with the reference's "
+                   "rounding order (bit-exact), mfma = the exact-split projection task")
+    return out
+
+
 def flow_head_bench(pkg, lib, streams=64, calls=200, seed=11, graph=1, one_launch=0):
     """The flow head's batched LSD step (phonon_flow_head_device_lsd: noise
     scaling, input/condition projections, seven adaLN projections as one, six
@@ -995,6 +1044,8 @@ def main():
                     help="run only the B=256 decode + batched prefill workload")
     ap.add_argument("--flow-head", action="store_true",
                     help="run only the flow head LSD step measurement")
+    ap.add_argument("--gemv", action="store_true",
+                    help="run only the small-batch Q8 GEMV comparison (vector units vs MFMA)")
     ap.add_argument("--pcm", action="store_true",
                     help="run only the latent -> PCM decoding measurement")
     ap.add_argument("--pmc-program", action="store_true",
@@ -1030,6 +1081,9 @@ def main():
         return
     if args.pcm:
         print(json.dumps(pcm_bench(pkg, lib)), flush=True)
+        return
+    if args.gemv:
+        print(json.dumps(gemv_valu_vs_mfma(pkg, lib)), flush=True)
         return
     if args.flow_head:
         for one in (1, 0):
@@ -1080,6 +1134,8 @@ def main():
         log(f"B=256 + prefill: {line['b256_with_prefill']}")
         line["q8_matvec_2048x512"] = q8_matvec_bench(pkg, lib)
         log(f"q8 matvec: {line['q8_matvec_2048x512']}")
+        line["q8_gemv_valu_vs_mfma"] = gemv_valu_vs_mfma(pkg, lib)
+        log(f"q8 gemv valu vs mfma: {line['q8_gemv_valu_vs_mfma']}")
         line["flow_head"] = {"b64": flow_head_bench(pkg, lib, streams=64),
                              "b1": flow_head_bench(pkg, lib, streams=1),
                              "frame_loop_b64": frame_loop_bench(pkg, lib)}

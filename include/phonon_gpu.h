@@ -123,6 +123,18 @@ int pgpu_gemm_qkv(void *stream, const pgpu_matrix *w, const pgpu_gemm_input *x, 
                   const pgpu_paged_kv *kv, int layer, const int32_t *tables, int table_stride,
                   const int32_t *positions, const float *rope, float *q_out, int *status);
 
+/* -- small-batch Q8_0 products on the vector units (pgpu_gemv.hip) --
+ * y[s][r] = sum over blocks b of scale[r][b] * (sum_i (float)q[r][32b+i] *
+ * x[s][32b+i]) for s < batch <= PGPU_GEMV_MAX_BATCH, with the reference's
+ * arithmetic (src/phonon_q8.c:36-62: products rounded, added in column
+ * order; blocks added in order), so each output has the bits of
+ * phonon_q8_matvec. values: row-major int8 [rows][columns] (16-byte
+ * aligned), scales: fp16 bits [rows][columns/32], x [batch][columns]
+ * (16-byte aligned), y [batch][rows]; columns = 32 x a divisor of 64. */
+#define PGPU_GEMV_MAX_BATCH 8
+int pgpu_q8_gemv(void *stream, const int8_t *values, const uint16_t *scales, int rows,
+                 int columns, const float *x, int batch, float *y, int *status);
+
 /* -- one-launch decode step (pgpu_flow.hip) --
  * A whole decode step of B streams (all layers) in one launch: every
  * work-group runs one task of the step, named by its descriptor in

@@ -32,6 +32,13 @@ void phonon_q8_device_destroy(PhononQ8Device *matrix);
  * non-finite outputs are reported by phonon_q8_device_status. */
 int phonon_q8_device_matvec(PhononQ8Device *matrix, size_t copy, const float *x, float *y,
                             size_t batch, void *stream);
+/* The same product for batch <= 8 on the vector units (pgpu_q8_gemv: one
+ * lane per 32-column block of a row, 16-byte int8 loads from a row-major
+ * copy made at creation, the reference's arithmetic, so y has the bits of
+ * phonon_q8_matvec). Columns must be 32 x a divisor of 64; returns 0
+ * otherwise. */
+int phonon_q8_device_matvec_valu(PhononQ8Device *matrix, size_t copy, const float *x, float *y,
+                                 size_t batch, void *stream);
 /* Waits for `stream`; 1 iff no call since the last check produced a
  * non-finite output (and clears the record). */
 int phonon_q8_device_status(PhononQ8Device *matrix, void *stream);

@@ -336,6 +336,8 @@ EXPORTS = {
     "pgpu_head_flow_reset": (_i, [_vp, _vp, _sz]),
     "phonon_flow_head_device_set_one_launch": (_i, [_vp, _i]),
     "phonon_flow_head_device_set_wait_limit": (_i, [_vp, ctypes.c_uint]),
+    "pgpu_q8_gemv": (_i, [_vp, _vp, _vp, _i, _i, _vp, _i, _vp, _vp]),
+    "phonon_q8_device_matvec_valu": (_i, [_vp, _sz, _vp, _vp, _sz, _vp]),
     "pgpu_conv_rows": (_i, [_vp, ctypes.POINTER(PgpuConvLayer), _vp, _i, _vp, _vp, _vp, _i, _vp,
                             _vp]),
     "pgpu_upsample_frame": (_i, [_vp, _vp, _vp, _vp, _i, _i, _vp, _vp]),

@@ -3,8 +3,12 @@
  *
  * Argument checks follow src/phonon_q8.c:36-92. The arithmetic per row is
  * the reference's: for every 32-column block, partial = sum q*x, then
- * sum += scale * partial (the partial computed exactly on split bf16 MFMA
- * terms, see pgpu_gemm.hip). */
+ * sum += scale * partial. The drop-ins and phonon_q8_device_matvec_valu
+ * run it on the vector units with the reference's rounding order
+ * (pgpu_gemv.hip: the same bits); phonon_q8_device_matvec runs it on the
+ * matrix cores (each block's partial from exact split bf16 MFMA terms,
+ * pgpu_gemm.hip), and the drop-in matvec falls back to that path when the
+ * column count is not 32 x a divisor of 64. */
 #include "phonon_q8_device.h"
 #include "ph_internal.h"
 
@@ -14,6 +18,8 @@
 struct PhononQ8Device {
     pgpu_matrix *copies;
     void **allocations;
+    int8_t **row_values;   /* per copy: row-major int8 [rows][columns] */
+    uint16_t **row_scales; /* per copy: fp16 bits [rows][columns/32] */
     size_t count, rows, columns, max_batch;
     uint16_t *xs;
     int *status;
@@ -23,8 +29,15 @@ void phonon_q8_device_destroy(PhononQ8Device *m) {
     if (!m)
         return;
     (void)pgpu_stream_sync(NULL);
-    for (size_t i = 0; i < m->count; i++)
+    for (size_t i = 0; i < m->count; i++) {
         pgpu_free(m->allocations[i]);
+        if (m->row_values)
+            pgpu_free(m->row_values[i]);
+        if (m->row_scales)
+            pgpu_free(m->row_scales[i]);
+    }
+    free(m->row_values);
+    free(m->row_scales);
     pgpu_free(m->xs);
     pgpu_free(m->status);
     free(m->copies);
@@ -53,12 +66,27 @@ int phonon_q8_device_create(const PhononQ8Block *weights, size_t rows, size_t co
                              .shape = {rows, columns},
                              .data = weights,
                              .byte_count = rows * columns / 32 * sizeof(PhononQ8Block)};
-    int ok = m->copies && m->allocations;
+    m->row_values = calloc(copies, sizeof(int8_t *));
+    m->row_scales = calloc(copies, sizeof(uint16_t *));
+    const size_t nb = columns / 32;
+    int8_t *rv = malloc(rows * columns);
+    uint16_t *rs = malloc(rows * nb * sizeof(uint16_t));
+    int ok = m->copies && m->allocations && m->row_values && m->row_scales && rv && rs;
+    for (size_t i = 0; ok && i < rows * nb; i++) {
+        memcpy(rv + i * 32, weights[i].values, 32);
+        rs[i] = weights[i].scale_bits;
+    }
     for (size_t i = 0; ok && i < copies; i++) {
         ok = ph_matrix_upload(&view, rows, columns, &m->copies[i], &m->allocations[i]);
         if (ok)
             m->count++;
+        ok = ok && (m->row_values[i] = pgpu_malloc(rows * columns)) &&
+             (m->row_scales[i] = pgpu_malloc(rows * nb * sizeof(uint16_t))) &&
+             pgpu_copy_h2d(NULL, m->row_values[i], rv, rows * columns) &&
+             pgpu_copy_h2d(NULL, m->row_scales[i], rs, rows * nb * sizeof(uint16_t));
     }
+    free(rv);
+    free(rs);
     const size_t split_bytes = m->max_batch * (ok ? m->copies[0].columns : 0) * 3 * 2;
     if (ok) {
         m->xs = pgpu_malloc(split_bytes);
@@ -93,6 +121,15 @@ int phonon_q8_device_matvec(PhononQ8Device *m, size_t copy, const float *x, floa
            pgpu_gemm_store(stream, w, &in, (int)batch, NULL, y, (int)w->rows, m->status);
 }
 
+int phonon_q8_device_matvec_valu(PhononQ8Device *m, size_t copy, const float *x, float *y,
+                                 size_t batch, void *stream) {
+    if (!m || copy >= m->count || !x || !y || !batch || batch > PGPU_GEMV_MAX_BATCH ||
+        (uintptr_t)x % 16 || (uintptr_t)y % 16)
+        return 0;
+    return pgpu_q8_gemv(stream, m->row_values[copy], m->row_scales[copy], (int)m->rows,
+                        (int)m->columns, x, (int)batch, y, m->status);
+}
+
 int phonon_q8_device_status(PhononQ8Device *m, void *stream) {
     int st = 1;
     if (!m || !pgpu_stream_sync(stream) || !pgpu_copy_d2h(stream, &st, m->status, sizeof(int)))
@@ -110,6 +147,41 @@ size_t phonon_q8_device_bytes_per_call(const PhononQ8Device *m, size_t batch) {
 }
 
 /* ------------------------------------------------------------- drop-ins -- */
+
+/* The reference's matvec on the vector units (pgpu_q8_gemv): the row-major
+ * int8 values and fp16 scales of the blocks go to the device, and every
+ * output has the bits of src/phonon_q8.c:64-92. Arguments already checked. */
+static int q8_matvec_valu(const PhononQ8Block *weights, const float *input, size_t rows,
+                          size_t columns, float *output) {
+    const size_t nb = columns / 32, blocks = rows * nb;
+    int8_t *rv = malloc(rows * columns);
+    uint16_t *rs = malloc(blocks * sizeof(uint16_t));
+    int ok = rv && rs;
+    for (size_t i = 0; ok && i < blocks; i++) {
+        memcpy(rv + i * 32, weights[i].values, 32);
+        rs[i] = weights[i].scale_bits;
+    }
+    ph_lock();
+    void *s = ph_stream();
+    int8_t *dv = ok ? ph_scratch(4, rows * columns) : NULL;
+    uint16_t *ds = ok ? ph_scratch(5, blocks * sizeof(uint16_t)) : NULL;
+    float *x = ok ? ph_scratch(2, columns * sizeof(float)) : NULL;
+    float *y = ok ? ph_scratch(3, rows * sizeof(float)) : NULL;
+    int *status = ph_scratch(1, sizeof(int));
+    int st = 1;
+    ok = ok && dv && ds && x && y && status && pgpu_memset(s, status, 0, sizeof(int)) &&
+         pgpu_copy_h2d(s, dv, rv, rows * columns) &&
+         pgpu_copy_h2d(s, ds, rs, blocks * sizeof(uint16_t)) &&
+         pgpu_copy_h2d(s, x, input, columns * sizeof(float)) &&
+         pgpu_q8_gemv(s, dv, ds, (int)rows, (int)columns, x, 1, y, status) &&
+         pgpu_copy_d2h(s, &st, status, sizeof(int)) &&
+         pgpu_copy_d2h(s, output, y, rows * sizeof(float));
+    (void)pgpu_stream_sync(s);
+    ph_unlock();
+    free(rv);
+    free(rs);
+    return ok && st == 0;
+}
 
 int phonon_q8_matvec(const PhononQ8Block *weights, const float *input, size_t rows,
                      size_t columns, float *output) {
@@ -136,6 +208,9 @@ int phonon_q8_matvec(const PhononQ8Block *weights, const float *input, size_t ro
             return 0;
     if (rows > INT32_MAX / 2 || columns > INT32_MAX / 2 || !ph_init())
         return 0;
+    const size_t nb = columns / 32;
+    if (nb <= 64 && 64 % nb == 0)
+        return q8_matvec_valu(weights, input, rows, columns, output);
     ph_lock();
     void *s = ph_stream();
     pgpu_matrix w;
