@@ -337,24 +337,25 @@ def pmc_program(pkg, lib, args):
           flush=True)
 
 
-def prefill_mfma_work(layers, new_streams, chunk):
+def prefill_mfma_work(layers, new_streams, chunk, terms=3):
     """(bf16 MFMA flops, fp32 MFMA flops) of a batched prefill of new_streams
-    fresh prompts of `chunk` positions: the projections as issued (three
-    bf16 MFMA products per multiply-add, one per split term) and the causal
-    attention's Q.K and P.V (2 flops per multiply-add, every (query, key)
-    pair with key <= query, 8 heads x 64 dimensions)."""
+    fresh prompts of `chunk` positions: the projections as issued (one bf16
+    MFMA product per multiply-add and split term: 3 in the exact mode, 2 in
+    the fast one) and the causal attention's Q.K and P.V (2 flops per
+    multiply-add, every (query, key) pair with key <= query, 8 heads x 64
+    dimensions)."""
     rows = new_streams * chunk
-    proj = rows * layers * (1536 + 512 + 2048 + 2048) * 512 * 2 * 3
+    proj = rows * layers * (1536 + 512 + 2048 + 2048) * 512 * 2 * terms
     pairs = new_streams * chunk * (chunk + 1) // 2
     attn = layers * pairs * 8 * 64 * 2 * 2
     return proj, attn
 
 
-def prefill_mfma_fraction(layers, new_streams, chunk, ms):
+def prefill_mfma_fraction(layers, new_streams, chunk, ms, terms):
     """The prefill's matrix-core work against the time it took: bf16 flops
     at 2.5 PFLOP/s plus fp32 flops at 157.3 TFLOP/s (dense peaks), as a
     fraction of the measured time."""
-    proj, attn = prefill_mfma_work(layers, new_streams, chunk)
+    proj, attn = prefill_mfma_work(layers, new_streams, chunk, terms)
     secs = ms * 1e-3
     return {"bf16_tflop": round(proj / 1e12, 2), "fp32_gflop": round(attn / 1e9, 2),
             "bf16_TFLOPs": round(proj / secs / 1e12, 1),
@@ -448,7 +449,8 @@ def large_batch_with_prefill(pkg, lib, seed, layers=12, streams=256, new_streams
             "prefill_attention": ["matrix cores", "exact (decode arithmetic)",
                                   "lane per query"][prefill_attention],
             "prefill_mfma": prefill_mfma_fraction(layers, new_streams, chunk,
-                                                  pre_ms / iterations),
+                                                  pre_ms / iterations,
+                                                  3 if prefill_attention == 1 else 2),
             "frames_per_s_incl_prefill": round(streams / (per_it_ms * 1e-3), 1),
             "clean": clean}
 

@@ -132,7 +132,7 @@ __global__ __launch_bounds__(kTaskThreads) void k_prefill_gemm(GemmArgs a, int r
     static_assert(WR * WP == kTaskWaves, "8 waves");
     static_assert(kChain % KS == 0, "a stage never straddles a chain");
     constexpr int RT = WR * RW, PT = WP * PW;
-    constexpr int kB = PT * 1536, kA = RT * 512;            // halves per block
+    constexpr int kB = PT * TERMS * 512, kA = RT * 512;     // halves per block
     constexpr int kS = SCALED ? RT * 32 : 0;                // halves (RT x 16 floats)
     constexpr int kBlk = kB + kA + kS;                      // halves per block
     constexpr int kStage = KS * kBlk;                       // halves per stage
@@ -173,7 +173,7 @@ __global__ __launch_bounds__(kTaskThreads) void k_prefill_gemm(GemmArgs a, int r
                     const int t = c / TERMS, term = c % TERMS;
                     const int tile = min(pt0 + t, last_tile);
                     src = a.xs + ((size_t)tile * kbn + kb) * 1536 + term * 512;
-                    dst = st + t * 1536 + term * 512;
+                    dst = st + t * (TERMS * 512) + term * 512;
                 } else {
                     const int r = c - PT * TERMS;
                     src = wv + ((size_t)(rt0 + r) * kbn + kb) * 512;
@@ -236,7 +236,7 @@ __global__ __launch_bounds__(kTaskThreads) void k_prefill_gemm(GemmArgs a, int r
             }
 #pragma unroll
             for (int p = 0; p < PW; p++) {
-                const uint16_t *xb = st + (wp * PW + p) * 1536 + lane * 8;
+                const uint16_t *xb = st + (wp * PW + p) * (TERMS * 512) + lane * 8;
                 const bf16x8 xh = *(const bf16x8 *)xb;
                 const bf16x8 xm = *(const bf16x8 *)(xb + 512);
                 const bf16x8 xl = TERMS == 3 ? *(const bf16x8 *)(xb + 1024) : bf16x8{};
@@ -722,12 +722,19 @@ int launch_gemm(const GemmArgs &a, hipStream_t stream) {
 }
 
 // Tile shapes (rows x positions per work-group): 128 x 128 for the wide
-// projections (4 LDS stages, 130 KB), 128 x 64 for the 512-row ones (6
-// stages, 126 KB), so that a few thousand positions give >= 256
-// work-groups.
+// projections, 128 x 64 for the 512-row ones, so that a few thousand
+// positions give >= 256 work-groups. LDS rings (stages x blocks): 2 x 2
+// (one work-group per CU for the wide shapes, two for the 512-row ones),
+// except the MLP-in projection with two split terms: 3 x 1 (73.5 KB, two
+// work-groups per CU, so one's prologue and GELU epilogue overlap the
+// other's main loop: 41.5 vs 47.9 us for 4096 positions; the QKV projection
+// is slower that way, 51.0 vs 46.4 us). Chosen by measurement on MI355X.
 template <int EPI, bool SCALED>
 int dispatch_gemm(const GemmArgs &a, hipStream_t stream) {
-    if (a.n_rows > kWidth) return launch_gemm<EPI, SCALED, 2, 4, 4, 2, 2, 2>(a, stream);
+    if (a.n_rows > kWidth)
+        return EPI == EPI_GELU_SPLIT && a.split_terms == 2
+                   ? launch_gemm<EPI, SCALED, 2, 4, 4, 2, 3, 1>(a, stream)
+                   : launch_gemm<EPI, SCALED, 2, 4, 4, 2, 2, 2>(a, stream);
     return launch_gemm<EPI, SCALED, 4, 2, 2, 2, 2, 2>(a, stream);
 }
 
