@@ -91,17 +91,18 @@ __global__ __launch_bounds__(kTaskThreads) void k_rows_split(GemmArgs a, uint16_
 // share a position group's operand rows share an L2.
 constexpr int kChain = 8;  // column blocks per summation chain
 
-// One 16-byte LDS-DMA load per lane: global src -> LDS bytes [lds + 16 lane,
-// +16) (lds wave-uniform). Issued as inline assembly so that the compiler,
+// One 16-byte LDS-DMA load per lane: global bytes [base + off, +16) -> LDS
+// bytes [lds + 16 lane, +16) (base and lds wave-uniform, in SGPRs; off a
+// per-lane byte offset). Issued as inline assembly so that the compiler,
 // which cannot tell which LDS bytes such a load writes, does not drain
 // every load in flight before each LDS read; the kernel's own vmcnt waits
 // and barriers order the copies and the reads. M0 (the LDS base of the
 // copy) is set right before the load; no other code of these kernels uses
 // it (the compiler reserves M0 and does not take clobbers of it).
-__device__ inline void dma16(const void *src, uint32_t lds) {
-    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off"
+__device__ inline void dma16(const void *base, uint32_t off, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1"
                  :
-                 : "v"(src), "s"(lds)
+                 : "v"(off), "s"(base), "s"(lds)
                  : "memory");
 }
 
@@ -110,18 +111,25 @@ __device__ inline uint32_t lds_address(const void *p) {
         (uint32_t)(size_t)(const __attribute__((address_space(3))) void *)p);
 }
 
-// s_waitcnt vmcnt(n) (expcnt and lgkmcnt left alone); n > 31 waits for 0.
-__device__ inline void wait_vm(int n) {
-    switch (n) {
-#define PGPU_VM(k) \
-    case k: __builtin_amdgcn_s_waitcnt(((k) & 15) | (((k) >> 4) << 14) | 0x0f70); break;
-        PGPU_VM(0) PGPU_VM(1) PGPU_VM(2) PGPU_VM(3) PGPU_VM(4) PGPU_VM(5) PGPU_VM(6)
-        PGPU_VM(7) PGPU_VM(8) PGPU_VM(9) PGPU_VM(10) PGPU_VM(11) PGPU_VM(12) PGPU_VM(13)
-        PGPU_VM(14) PGPU_VM(15) PGPU_VM(16) PGPU_VM(17) PGPU_VM(18) PGPU_VM(19) PGPU_VM(20)
-        PGPU_VM(21) PGPU_VM(22) PGPU_VM(23) PGPU_VM(24) PGPU_VM(25) PGPU_VM(26) PGPU_VM(27)
-        PGPU_VM(28) PGPU_VM(29) PGPU_VM(30) PGPU_VM(31)
-#undef PGPU_VM
-    default: __builtin_amdgcn_s_waitcnt(0x0f70); break;
+// s_waitcnt vmcnt(N) (expcnt and lgkmcnt left alone).
+template <int N>
+__device__ inline void wait_vm() {
+    static_assert(N >= 0 && N < 64, "vmcnt is six bits");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0f70);
+}
+
+// Waits until at most `later` blocks' loads of this wave are in flight,
+// where the wave issues `per_block` loads per block (uniform; PER - 1, PER or
+// PER + 1). Every count is an immediate: no per-stage scalar arithmetic.
+template <int PER, int LATER>
+__device__ inline void wait_blocks(int per_block) {
+    if constexpr (LATER == 0) {
+        wait_vm<0>();
+    } else {
+        if (per_block == PER) wait_vm<LATER * PER>();
+        else if (per_block == PER + 1) wait_vm<LATER * (PER + 1)>();
+        else if (per_block == PER - 1) wait_vm<LATER * (PER - 1)>();
+        else wait_vm<0>();
     }
 }
 
@@ -158,35 +166,56 @@ __global__ __launch_bounds__(kTaskThreads) void k_prefill_gemm(GemmArgs a, int r
     }
     const int pt0 = pos_group * PT, rt0 = row_group * RT;
     const uint16_t *wv = (const uint16_t *)a.w;
-    // DMA loads this wave issues per stage (the vmcnt it waits down to).
-    const int mine =
-        KS * ((kChunks - wave + kTaskWaves - 1) / kTaskWaves + (SCALED && wave == 0));
+    // This wave's share of every block's DMA chunks: chunk c = wave + 8 j.
+    // Each keeps a running source pointer (uniform, advanced one block per
+    // issue), its byte stride per block and its LDS offset within a block,
+    // so that issuing a chunk is four scalar instructions and a load.
+    constexpr int kPer = (kChunks + kTaskWaves - 1) / kTaskWaves;
+    const char *csrc[kPer];
+    uint32_t cstride[kPer], cdst[kPer];
+    bool clive[kPer];
+    int per_block = 0;  // loads this wave issues per block
+#pragma unroll
+    for (int j = 0; j < kPer; j++) {
+        const int c = wave + kTaskWaves * j;
+        clive[j] = (kChunks % kTaskWaves == 0 || j < kPer - 1) ? true : c < kChunks;
+        per_block += clive[j];
+        if (c < PT * TERMS) {
+            const int t = c / TERMS, term = c % TERMS;
+            const int tile = min(pt0 + t, last_tile);
+            csrc[j] = (const char *)(a.xs + (size_t)tile * kbn * 1536 + term * 512);
+            cstride[j] = 1536 * 2;
+            cdst[j] = (t * (TERMS * 512) + term * 512) * 2;
+        } else {
+            const int r = min(c - PT * TERMS, RT - 1);
+            csrc[j] = (const char *)(wv + (size_t)(rt0 + r) * kbn * 512);
+            cstride[j] = 512 * 2;
+            cdst[j] = (kB + r * 512) * 2;
+        }
+    }
+    // Q8 scales: wave 0, lane (r, part) -> the 16 bytes `part` of row tile
+    // r's 16 row scales of the block.
+    const char *ssrc = (const char *)(a.wscale_f + (size_t)rt0 * kbn * 16);
+    const uint32_t soff = (uint32_t)((((lane >> 2) & (RT - 1)) * kbn * 16 + (lane & 3) * 4) * 4);
+    if (SCALED && wave == 0) per_block++;
+    const uint32_t lds0 = lds_address(lds);
+    const uint32_t lane_off = lane * 16;
+    int slot_next = 0;  // ring slot of the next stage issued
 
-    auto issue = [&](int stage) {
+    auto issue = [&]() {
+        const uint32_t sbase = lds0 + slot_next * (kStage * 2);
+        slot_next = slot_next == NB - 1 ? 0 : slot_next + 1;
+#pragma unroll
         for (int kk = 0; kk < KS; kk++) {
-            const int kb = stage * KS + kk;
-            uint16_t *st = lds + (stage % NB) * kStage + kk * kBlk;
-            for (int c = wave; c < kChunks; c += kTaskWaves) {  // uniform
-                const uint16_t *src;
-                uint16_t *dst;
-                if (c < PT * TERMS) {
-                    const int t = c / TERMS, term = c % TERMS;
-                    const int tile = min(pt0 + t, last_tile);
-                    src = a.xs + ((size_t)tile * kbn + kb) * 1536 + term * 512;
-                    dst = st + t * (TERMS * 512) + term * 512;
-                } else {
-                    const int r = c - PT * TERMS;
-                    src = wv + ((size_t)(rt0 + r) * kbn + kb) * 512;
-                    dst = st + kB + r * 512;
-                }
-                dma16(src + lane * 8, lds_address(dst));
+            const uint32_t bbase = sbase + kk * (kBlk * 2);
+#pragma unroll
+            for (int j = 0; j < kPer; j++) {
+                if (clive[j]) dma16(csrc[j], lane_off, bbase + cdst[j]);
+                csrc[j] += cstride[j];
             }
             if (SCALED && wave == 0) {
-                const uint32_t dst = lds_address(st + kB + kA);
-                if (lane < RT * 4) {
-                    const int r = lane >> 2, part = lane & 3;
-                    dma16(a.wscale_f + ((size_t)(rt0 + r) * kbn + kb) * 16 + part * 4, dst);
-                }
+                if (lane < RT * 4) dma16(ssrc, soff, bbase + (kB + kA) * 2);
+                ssrc += 64;
             }
         }
     };
@@ -212,15 +241,18 @@ __global__ __launch_bounds__(kTaskThreads) void k_prefill_gemm(GemmArgs a, int r
             load_epilogue_dynamic<EPI>(ep[r][p], a, s, row0, s < a.streams);
         }
 
-    for (int k = 0; k < NB - 1 && k < stages; k++) issue(k);
+    for (int k = 0; k < NB - 1 && k < stages; k++) issue();
     for (int sg = 0; sg < stages; sg++) {
         // Stage sg is in once at most the later stages' loads are in
-        // flight; the barrier publishes every wave's copies and frees the
-        // stage the next issue overwrites (read in the previous iteration).
-        wait_vm(min(NB - 2, stages - 1 - sg) * mine);
+        // flight (all of them issued while sg + NB - 2 < stages; in the
+        // last stages every load is waited for); the barrier publishes
+        // every wave's copies and frees the stage the next issue
+        // overwrites (read in the previous iteration).
+        if (sg + NB - 2 < stages) wait_blocks<kPer, (NB - 2) * KS>(per_block);
+        else wait_vm<0>();
         __builtin_amdgcn_s_barrier();
         __asm__ volatile("" ::: "memory");
-        if (sg + NB - 1 < stages) issue(sg + NB - 1);
+        if (sg + NB - 1 < stages) issue();
 #pragma unroll
         for (int kk = 0; kk < KS; kk++) {
             const int kb = sg * KS + kk;
