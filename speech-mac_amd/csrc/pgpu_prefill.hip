@@ -220,13 +220,16 @@ __global__ __launch_bounds__(kTaskThreads) void k_prefill_gemm(GemmArgs a, int r
         }
     };
 
+    // acc: the running chain (reset at its end); tot: the chains
+    // summed in order. tot starts at -0, the identity of fp32 addition, so
+    // that adding the first chain gives that chain's bits exactly.
     f32x4 acc[RW][PW], tot[RW][PW];
 #pragma unroll
     for (int r = 0; r < RW; r++)
 #pragma unroll
         for (int p = 0; p < PW; p++) {
             acc[r][p] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-            tot[r][p] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            tot[r][p] = f32x4{-0.0f, -0.0f, -0.0f, -0.0f};
         }
 
     // Epilogue operands of every tile of the wave, requested first.
@@ -241,6 +244,60 @@ __global__ __launch_bounds__(kTaskThreads) void k_prefill_gemm(GemmArgs a, int r
             load_epilogue_dynamic<EPI>(ep[r][p], a, s, row0, s < a.streams);
         }
 
+    // One 32-column block from LDS stage area st. Every tile's products
+    // are issued term by term into its own registers (consecutive MFMAs
+    // never depend on each other), then the Q8 scales are applied.
+    auto block = [&](const uint16_t *st) {
+        bf16x8 wa[RW], xt[PW][TERMS];
+        float4 sc[RW];
+#pragma unroll
+        for (int r = 0; r < RW; r++) {
+            wa[r] = *(const bf16x8 *)(st + kB + (wr * RW + r) * 512 + lane * 8);
+            if constexpr (SCALED)
+                sc[r] = *(const float4 *)((const float *)(st + kB + kA) + (wr * RW + r) * 16 +
+                                          (lane >> 4) * 4);
+        }
+#pragma unroll
+        for (int p = 0; p < PW; p++)
+#pragma unroll
+            for (int t = 0; t < TERMS; t++)
+                xt[p][t] = *(const bf16x8 *)(st + (wp * PW + p) * (TERMS * 512) + t * 512 + lane * 8);
+        if constexpr (SCALED) {
+            f32x4 c[RW][PW];
+#pragma unroll
+            for (int t = 0; t < TERMS; t++)
+#pragma unroll
+                for (int r = 0; r < RW; r++)
+#pragma unroll
+                    for (int p = 0; p < PW; p++)
+                        c[r][p] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                            wa[r], xt[p][t], t == 0 ? f32x4{0.0f, 0.0f, 0.0f, 0.0f} : c[r][p], 0,
+                            0, 0);
+#pragma unroll
+            for (int r = 0; r < RW; r++)
+#pragma unroll
+                for (int p = 0; p < PW; p++) {
+                    acc[r][p][0] = fmaf(sc[r].x, c[r][p][0], acc[r][p][0]);
+                    acc[r][p][1] = fmaf(sc[r].y, c[r][p][1], acc[r][p][1]);
+                    acc[r][p][2] = fmaf(sc[r].z, c[r][p][2], acc[r][p][2]);
+                    acc[r][p][3] = fmaf(sc[r].w, c[r][p][3], acc[r][p][3]);
+                }
+        } else {
+#pragma unroll
+            for (int t = 0; t < TERMS; t++)
+#pragma unroll
+                for (int r = 0; r < RW; r++)
+#pragma unroll
+                    for (int p = 0; p < PW; p++)
+                        acc[r][p] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wa[r], xt[p][t],
+                                                                            acc[r][p], 0, 0, 0);
+        }
+        // The next block's code is not scheduled into this one: that would
+        // keep two blocks' products and operands live at once.
+        __builtin_amdgcn_sched_barrier(0);
+    };
+
+    int slot = 0;  // ring slot of stage sg
     for (int k = 0; k < NB - 1 && k < stages; k++) issue();
     for (int sg = 0; sg < stages; sg++) {
         // Stage sg is in once at most the later stages' loads are in
@@ -253,58 +310,21 @@ __global__ __launch_bounds__(kTaskThreads) void k_prefill_gemm(GemmArgs a, int r
         __builtin_amdgcn_s_barrier();
         __asm__ volatile("" ::: "memory");
         if (sg + NB - 1 < stages) issue();
+        const uint16_t *st = lds + slot * kStage;
+        slot = slot == NB - 1 ? 0 : slot + 1;
 #pragma unroll
-        for (int kk = 0; kk < KS; kk++) {
-            const int kb = sg * KS + kk;
-            const uint16_t *st = lds + (sg % NB) * kStage + kk * kBlk;
-            bf16x8 wa[RW];
-            float4 sc[RW];
+        for (int kk = 0; kk < KS; kk++) block(st + kk * kBlk);
+        if ((((sg + 1) * KS) & (kChain - 1)) == 0) {
+            // End of a chain: the chains are summed in order.
 #pragma unroll
-            for (int r = 0; r < RW; r++) {
-                wa[r] = *(const bf16x8 *)(st + kB + (wr * RW + r) * 512 + lane * 8);
-                if constexpr (SCALED)
-                    sc[r] = *(const float4 *)((const float *)(st + kB + kA) + (wr * RW + r) * 16 +
-                                              (lane >> 4) * 4);
-            }
+            for (int r = 0; r < RW; r++)
 #pragma unroll
-            for (int p = 0; p < PW; p++) {
-                const uint16_t *xb = st + (wp * PW + p) * (TERMS * 512) + lane * 8;
-                const bf16x8 xh = *(const bf16x8 *)xb;
-                const bf16x8 xm = *(const bf16x8 *)(xb + 512);
-                const bf16x8 xl = TERMS == 3 ? *(const bf16x8 *)(xb + 1024) : bf16x8{};
+                for (int p = 0; p < PW; p++) {
 #pragma unroll
-                for (int r = 0; r < RW; r++) {
-                    if constexpr (SCALED) {
-                        f32x4 c = {0.0f, 0.0f, 0.0f, 0.0f};
-                        c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wa[r], xh, c, 0, 0, 0);
-                        c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wa[r], xm, c, 0, 0, 0);
-                        if constexpr (TERMS == 3)
-                            c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wa[r], xl, c, 0, 0, 0);
-                        acc[r][p][0] = fmaf(sc[r].x, c[0], acc[r][p][0]);
-                        acc[r][p][1] = fmaf(sc[r].y, c[1], acc[r][p][1]);
-                        acc[r][p][2] = fmaf(sc[r].z, c[2], acc[r][p][2]);
-                        acc[r][p][3] = fmaf(sc[r].w, c[3], acc[r][p][3]);
-                    } else {
-                        acc[r][p] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wa[r], xh, acc[r][p], 0, 0, 0);
-                        acc[r][p] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wa[r], xm, acc[r][p], 0, 0, 0);
-                        if constexpr (TERMS == 3)
-                            acc[r][p] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wa[r], xl, acc[r][p], 0, 0, 0);
-                    }
+                    for (int e = 0; e < 4; e++)
+                        tot[r][p][e] = __fadd_rn(tot[r][p][e], acc[r][p][e]);
+                    acc[r][p] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
                 }
-            }
-            if ((kb & (kChain - 1)) == kChain - 1) {
-                // End of a chain: the chains are summed in order.
-#pragma unroll
-                for (int r = 0; r < RW; r++)
-#pragma unroll
-                    for (int p = 0; p < PW; p++) {
-#pragma unroll
-                        for (int i = 0; i < 4; i++)
-                            tot[r][p][i] = kb == kChain - 1 ? acc[r][p][i]
-                                                            : __fadd_rn(tot[r][p][i], acc[r][p][i]);
-                        acc[r][p] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-                    }
-            }
         }
     }
 
@@ -753,20 +773,18 @@ int launch_gemm(const GemmArgs &a, hipStream_t stream) {
     return launch_ok("pgpu_prefill_gemm");
 }
 
-// Tile shapes (rows x positions per work-group): 128 x 128 for the wide
-// projections, 128 x 64 for the 512-row ones, so that a few thousand
-// positions give >= 256 work-groups. LDS rings (stages x blocks): 2 x 2
-// (one work-group per CU for the wide shapes, two for the 512-row ones),
-// except the MLP-in projection with two split terms: 3 x 1 (73.5 KB, two
-// work-groups per CU, so one's prologue and GELU epilogue overlap the
-// other's main loop: 41.5 vs 47.9 us for 4096 positions; the QKV projection
-// is slower that way, 51.0 vs 46.4 us). Chosen by measurement on MI355X.
+// Tile shapes (rows x positions per work-group), chosen by measurement on
+// MI355X (4096 positions, two split terms):
+//  - 1536 / 2048 rows, K = 512 (QKV, MLP in): 128 x 64 with a 3 x 1 ring
+//    (50 KB of LDS, <= 128 VGPRs: two work-groups per CU, so that one's
+//    epilogue overlaps the other's main loop). MLP in: 31.1 us, against
+//    36.1 for 128 x 128 with a 2 x 2 ring (one work-group per CU).
+//  - 512 rows (out, MLP out): 128 x 64 with a 2 x 2 ring (256 work-groups,
+//    one per CU): 10.6 / 28.4 us; deeper rings (3 x 2, 4 x 1 .. 8 x 1) and
+//    64-row or 32-position tiles were slower.
 template <int EPI, bool SCALED>
 int dispatch_gemm(const GemmArgs &a, hipStream_t stream) {
-    if (a.n_rows > kWidth)
-        return EPI == EPI_GELU_SPLIT && a.split_terms == 2
-                   ? launch_gemm<EPI, SCALED, 2, 4, 4, 2, 3, 1>(a, stream)
-                   : launch_gemm<EPI, SCALED, 2, 4, 4, 2, 2, 2>(a, stream);
+    if (a.n_rows > kWidth) return launch_gemm<EPI, SCALED, 4, 2, 2, 2, 3, 1>(a, stream);
     return launch_gemm<EPI, SCALED, 4, 2, 2, 2, 2, 2>(a, stream);
 }
 
