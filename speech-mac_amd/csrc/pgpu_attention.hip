@@ -180,8 +180,7 @@ __global__ __launch_bounds__(64 * kUnitWaves) void k_prefill_attention(AttnArgs 
                     score[t][i] = key < count ? d : -INFINITY;
                     m = fmaxf(m, score[t][i]);
                 }
-            m = fmaxf(m, __shfl_xor(m, 16));
-            m = fmaxf(m, __shfl_xor(m, 32));
+            m = xor16_32_max(m);
 #pragma unroll
             for (int t = 0; t < kBlocksPerWave; t++)
 #pragma unroll
@@ -194,16 +193,11 @@ __global__ __launch_bounds__(64 * kUnitWaves) void k_prefill_attention(AttnArgs 
                     acc.z = fmaf(ex, vr[t][i].z, acc.z);
                     acc.w = fmaf(ex, vr[t][i].w, acc.w);
                 }
-            l += __shfl_xor(l, 16);
-            l += __shfl_xor(l, 32);
-            acc.x += __shfl_xor(acc.x, 16);
-            acc.y += __shfl_xor(acc.y, 16);
-            acc.z += __shfl_xor(acc.z, 16);
-            acc.w += __shfl_xor(acc.w, 16);
-            acc.x += __shfl_xor(acc.x, 32);
-            acc.y += __shfl_xor(acc.y, 32);
-            acc.z += __shfl_xor(acc.z, 32);
-            acc.w += __shfl_xor(acc.w, 32);
+            l = xor16_32_sum(l);
+            acc.x = xor16_32_sum(acc.x);
+            acc.y = xor16_32_sum(acc.y);
+            acc.z = xor16_32_sum(acc.z);
+            acc.w = xor16_32_sum(acc.w);
             if (lane < 16) sh[u].acc[wave][lane] = acc;
             if (lane == 0) {
                 sh[u].m[wave] = m;

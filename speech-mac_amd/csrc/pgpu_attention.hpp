@@ -169,8 +169,7 @@ __device__ inline int attend_unit(const AttnArgs &a, int head, int split0, int s
                     m = fmaxf(m, score[t][i]);
                 }
             if (next) load(r + 1, false, 2);
-            m = fmaxf(m, __shfl_xor(m, 16));
-            m = fmaxf(m, __shfl_xor(m, 32));
+            m = xor16_32_max(m);
 #pragma unroll
             for (int t = 0; t < kBlocksPerWave; t++)
 #pragma unroll
@@ -188,16 +187,11 @@ __device__ inline int attend_unit(const AttnArgs &a, int head, int split0, int s
                 }
             if (next) load(r + 1, true, 2);
             // Lanes of one key row hold the same l; sum the four rows.
-            l += __shfl_xor(l, 16);
-            l += __shfl_xor(l, 32);
-            acc.x += __shfl_xor(acc.x, 16);
-            acc.y += __shfl_xor(acc.y, 16);
-            acc.z += __shfl_xor(acc.z, 16);
-            acc.w += __shfl_xor(acc.w, 16);
-            acc.x += __shfl_xor(acc.x, 32);
-            acc.y += __shfl_xor(acc.y, 32);
-            acc.z += __shfl_xor(acc.z, 32);
-            acc.w += __shfl_xor(acc.w, 32);
+            l = xor16_32_sum(l);
+            acc.x = xor16_32_sum(acc.x);
+            acc.y = xor16_32_sum(acc.y);
+            acc.z = xor16_32_sum(acc.z);
+            acc.w = xor16_32_sum(acc.w);
             if (lane < 16) sh[r].acc[wave][lane] = acc;
             if (lane == 0) {
                 sh[r].m[wave] = m;

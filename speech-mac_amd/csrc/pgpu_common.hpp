@@ -115,6 +115,30 @@ __device__ inline float row16_sum(float v) {
     return v;
 }
 
+// v + (v of the lane 16 apart within each half-wave), then + (the same of
+// the lane 32 apart): the bits of v += shfl_xor(v, 16); v += shfl_xor(v, 32)
+// (IEEE addition commutes), with gfx950's VALU lane swaps instead of LDS
+// permutes. v_permlane16_swap(v, v) leaves rows (0, 0, 2, 2) in the first
+// result and (1, 1, 3, 3) in the second; v_permlane32_swap(v, v) leaves the
+// low half twice in the first and the high half twice in the second.
+__device__ inline float xor16_32_sum(float v) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v),
+                                                    false, false);
+    v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v),
+                                                    false, false);
+    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
+__device__ inline float xor16_32_max(float v) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v),
+                                                    false, false);
+    v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v),
+                                                    false, false);
+    return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+
 __device__ inline float wave_sum(float v) {
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);

@@ -206,10 +206,7 @@ __device__ inline void lds_store8(uint16_t *bsh, int n, int kb, int g, const flo
 
 // Sum over the 64 lanes of a wave; every lane gets the same bits.
 __device__ inline float wave_sum64(float v) {
-    v = row16_sum(v);
-    v += __shfl_xor(v, 16);
-    v += __shfl_xor(v, 32);
-    return v;
+    return xor16_32_sum(row16_sum(v));
 }
 
 // ---------------------------------------------------------------------------
@@ -809,13 +806,15 @@ __device__ inline void gemm_split_task(const GemmArgs &a, int tile, int st, uint
     const uint16_t *xs = a.xs + (size_t)st * kbn * 1536 + lane * 8;
     f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
     for (int kb0 = kb_begin; kb0 < kb_end; kb0 += CH) {
+        // A lane whose stream is past the batch loads nothing: its MFMA
+        // column is zero and its outputs are never stored.
         bf16x8 xh[CH], xm[CH], xl[CH];
 #pragma unroll
         for (int u = 0; u < CH; u++) {
             const size_t kb = (size_t)min(kb0 + u, kb_end - 1) * 1536;
-            xh[u] = *(const bf16x8 *)(xs + kb);
-            xm[u] = *(const bf16x8 *)(xs + kb + 512);
-            xl[u] = *(const bf16x8 *)(xs + kb + 1024);
+            xh[u] = live ? *(const bf16x8 *)(xs + kb) : bf16x8{};
+            xm[u] = live ? *(const bf16x8 *)(xs + kb + 512) : bf16x8{};
+            xl[u] = live ? *(const bf16x8 *)(xs + kb + 1024) : bf16x8{};
         }
         WChunk<Q8, CH> next;
         if (kb0 + CH < kb_end) load_weights(next, a, tile, kbn, lane, kb0 + CH, kb_end);

@@ -696,8 +696,7 @@ __global__ __launch_bounds__(256) void k_prefill_attention_mfma(
                 bm = fmaxf(bm, sc[sub][r]);
             }
         }
-        bm = fmaxf(bm, __shfl_xor(bm, 16));
-        bm = fmaxf(bm, __shfl_xor(bm, 32));
+        bm = xor16_32_max(bm);
         const float mn = fmaxf(m, bm);
         float ps = 0.0f;
 #pragma unroll
@@ -707,8 +706,7 @@ __global__ __launch_bounds__(256) void k_prefill_attention_mfma(
                 sc[sub][r] = sc[sub][r] == -INFINITY ? 0.0f : expf(sc[sub][r] - mn);
                 ps += sc[sub][r];
             }
-        ps += __shfl_xor(ps, 16);
-        ps += __shfl_xor(ps, 32);
+        ps = xor16_32_sum(ps);
         const float keep = mn == -INFINITY ? 1.0f : expf(m - mn);
         m = mn;
         lsum = fmaf(lsum, keep, ps);
