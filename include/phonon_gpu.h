@@ -138,8 +138,9 @@ int pgpu_q8_gemv(void *stream, const int8_t *values, const uint16_t *scales, int
 /* -- one-launch decode step (pgpu_flow.hip) --
  * A whole decode step of B streams (all layers) in one launch: every
  * work-group runs one task of the step, named by its descriptor in
- * `schedule`, and first waits (on counters in device memory) for the tasks
- * whose outputs it reads. Tasks, per 16-stream tile t and layer l:
+ * `schedule`, and first waits for the tasks whose outputs it reads: on
+ * counters in device memory, or (tagged mode) by polling the tagged words
+ * they write. Tasks, per 16-stream tile t and layer l:
  *   QKV    LayerNorm 1 + QKV projection + RoPE + K/V append, 64 rows each
  *   ATTN   attn_rounds (1..PGPU_FLOW_ATTN_ROUNDS) consecutive 256-key splits
  *          of one (stream, head), one after the other; the task that
@@ -173,6 +174,7 @@ int pgpu_q8_gemv(void *stream, const int8_t *values, const uint16_t *scales, int
 #define PGPU_FLOW_MLP_OUT_TASKS 32
 #define PGPU_FLOW_COUNTER_STRIDE 16 /* 32-bit words between phase counters */
 #define PGPU_FLOW_ATTN_ROUNDS 2    /* most 256-key splits per ATTN task */
+#define PGPU_FLOW_PART_WORDS 72    /* tagged words per split partial (66 used) */
 
 #define PGPU_FLOW_TASK(kind, layer, tile, index)                                      \
     ((uint32_t)(kind) | (uint32_t)(layer) << 3 | (uint32_t)(tile) << 9 |             \
@@ -209,6 +211,15 @@ typedef struct {
                                       ran (XCC id << 32 | HW_ID register) */
     unsigned wait_us;              /* a task's wait for its inputs gives up (status bit 4)
                                       after this many microseconds; 0: one second */
+    int tagged;                    /* 1: x, r, the merged attention rows and the split
+                                      partials are handed over as tagged words in `rows`
+                                      and `parts` (part_acc, part_ml and act's x, r and
+                                      attention rows are then unused) */
+    uint64_t *rows;                /* (dev, tagged) [layer_count][3][tiles*16][512]: x, r,
+                                      merged attention */
+    uint64_t *parts;               /* (dev, tagged) [layer_count][tiles*16][8][max_splits]
+                                      [PGPU_FLOW_PART_WORDS]: P.V [64], max, sum */
+    const uint32_t *epoch;         /* (dev, tagged) this step's tag, never 0 */
 } pgpu_flow_step;
 
 /* Placement of each tile's projection chain in a task list, on a model
@@ -237,9 +248,10 @@ size_t pgpu_flow_schedule(size_t streams, size_t layers, const size_t *units,
 /* prefill = 1: pseudo-streams of one stream share its block table, so an
  * ATTN task waits for the QKV tasks of every tile (one layer-wide count). */
 int pgpu_flow_launch(void *stream, const pgpu_flow_step *step, const pgpu_paged_kv *kv);
-/* After a step: zero `n` counter words and advance positions[0..streams). */
+/* After a step: zero `n` counter words, advance positions[0..streams) and,
+ * if `epoch` is not NULL, the tagged mode's tag (skipping 0). */
 int pgpu_flow_finish(void *stream, unsigned *counters, size_t n, int32_t *positions,
-                     int streams);
+                     int streams, uint32_t *epoch);
 /* Fills n 32-bit words with `value` (a kernel: usable inside a captured graph). */
 int pgpu_fill_u32(void *stream, uint32_t *dst, size_t n, uint32_t value);
 

@@ -204,6 +204,7 @@ EXPORTS = {
     "phonon_flow_batch_set_trace": (_i, [_vp, _vp, _sz]),
     "phonon_flow_batch_set_placement": (_i, [_vp, _vp]),
     "phonon_flow_batch_schedule": (_sz, [_vp, ctypes.POINTER(ctypes.c_uint32), _sz]),
+    "phonon_flow_batch_set_handoff": (_i, [_vp, _i]),
     "phonon_flow_batch_prefill_device": (_i, [_vp, _sz, _vp, _vp, _vp, _sz, _vp, _f, _vp]),
     "phonon_flow_batch_sync": (_i, [_vp]),
     "phonon_flow_batch_status": (_i, [_vp, _vp]),
@@ -350,7 +351,7 @@ EXPORTS = {
     "phonon_flow_head_device_frame": (_i, [_vp, _sz, _vp, _vp, _vp, _f, _vp, _vp, _vp]),
     "phonon_flow_head_device_stream": (_vp, [_vp]),
     "phonon_flow_head_device_sync": (_i, [_vp]),
-    "pgpu_flow_finish": (_i, [_vp, _vp, _sz, _vp, _i]),
+    "pgpu_flow_finish": (_i, [_vp, _vp, _sz, _vp, _i, _vp]),
 }
 
 _LIB = None

@@ -19,7 +19,8 @@
 // holding its slot.
 //
 // Synchronisation without cache maintenance. Each XCD has its own L2, and
-// an agent-scope fence writes back or invalidates a whole L2. Instead:
+// an agent-scope fence writes back or invalidates a whole L2. Instead
+// (counter mode, f.tagged = 0):
 //  - every value a task writes for another task is stored write-through at
 //    device scope (global_store ... sc1: pgpu_gemm.hpp store_wt), and the
 //    storing waves drain vmcnt before the task's counter is incremented;
@@ -31,6 +32,18 @@
 //  - counters are atomics; a waiting lane polls with device-scope loads.
 // Read-only operands (weights, norms, positions, block tables, the RoPE
 // table, older K/V) are plain loads and stay cacheable.
+//
+// Tagged mode (f.tagged = 1, for a batch of a few streams): the layer
+// output x, the out projection r, the merged attention rows and the split
+// partials are tagged words (pgpu_gemm.hpp TagPoll), stored without a
+// drain; the consumer polls the words themselves, so a hand-off costs one
+// memory round trip less. A consumer first waits (one lane, one counter)
+// for the phase before its producers, so that tasks dispatched long before
+// their inputs do not poll all that time. Polls fetch from memory on every
+// round (device scope), which with many streams per tile costs more than
+// the counter mode's shared, cacheable loads (measured), hence the two
+// modes. q, the appended K/V and the MLP hidden fragments keep their
+// counters in both.
 //
 // Every wait is bounded (1 s of the 100 MHz constant clock): a task that
 // times out sets status bit 4, and every other waiter then stops waiting,
@@ -154,15 +167,72 @@ __device__ inline uint16_t *hidden_rows(const pgpu_flow_step &f, int layer) {
     return f.hidden + (size_t)layer * f.tiles * (kFfn / 32) * 1536;
 }
 
+// Tagged mode: per-layer rows [tiles*16][512] of tagged words: 0 = layer
+// output x, 1 = r, 2 = merged attention output.
+enum { ROWS_X = 0, ROWS_R = 1, ROWS_ATTN = 2 };
+__device__ inline uint64_t *tagged_rows(const pgpu_flow_step &f, int layer, int which) {
+    return f.rows + ((size_t)layer * 3 + which) * (size_t)f.tiles * 16 * kWidth;
+}
+
 __device__ inline GemmArgs base_args(const pgpu_flow_step &f, const pgpu_flow_layer &ly,
-                                     int which) {
+                                     int which, uint32_t tag) {
     GemmArgs a{};
     a.w = ly.values[which];
     a.wscale = ly.scales[which];
     a.streams = f.streams;
     a.status = f.status;
     a.wt_out = true;  // read by tasks on other XCDs within the launch
+    a.tp = TagPoll{tag, f.status, wait_ticks(f), false};
     return a;
+}
+
+// Tagged mode: the wait before a task polls its tagged inputs (the count of
+// the phase before its producers, or none).
+__device__ inline FlowWait no_wait(const pgpu_flow_step &f) {
+    return FlowWait{nullptr, 0u, f.status, 0u};
+}
+
+// Polls splits j0 .. nsplit-1 of one (stream, head) from its tagged partial
+// records (lanes 0..15 of the wave: dims [4 lane, 4 lane + 4)) and folds
+// them into the running merge in split order (merge_step: the arithmetic of
+// merge_splits). Every lane of the wave must call it.
+__device__ inline void merge_tagged_splits(const uint64_t *part, int j0, int nsplit, float &mx,
+                                           float &total, float *v, const TagPoll &tp) {
+    constexpr int G = 4;
+    const int lane = threadIdx.x & 63;
+    const bool mine = lane < 16;
+    const __amdgpu_buffer_rsrc_t r =
+        tag_rsrc(part, (uint32_t)(nsplit * PGPU_FLOW_PART_WORDS * 8));
+    for (int g0 = j0; g0 < nsplit; g0 += G) {
+        u32x4 acc[G][2], ml[G];
+        const uint64_t t0 = wall_clock64();
+        for (int round = 0;; round++) {
+            __asm__ volatile("" ::: "memory");
+            bool ok = true;
+#pragma unroll
+            for (int u = 0; u < G; u++) {
+                const int j = min(g0 + u, nsplit - 1);
+                const uint32_t rec = (uint32_t)(j * PGPU_FLOW_PART_WORDS * 8);
+                if (mine) {
+                    acc[u][0] = tag_load2(r, rec + lane * 32);
+                    acc[u][1] = tag_load2(r, rec + lane * 32 + 16);
+                    ml[u] = tag_load2(r, rec + 64 * 8);
+                    ok &= tag_ok2(acc[u][0], tp.tag) && tag_ok2(acc[u][1], tp.tag) &&
+                          tag_ok2(ml[u], tp.tag);
+                }
+            }
+            if (__all(ok)) break;
+            if (tag_give_up(tp, t0, round)) break;
+            __builtin_amdgcn_s_sleep(1);
+        }
+#pragma unroll
+        for (int u = 0; u < G; u++) {
+            if (g0 + u >= nsplit) break;
+            const float a4[4] = {bitsf(acc[u][0].x), bitsf(acc[u][0].z), bitsf(acc[u][1].x),
+                                 bitsf(acc[u][1].z)};
+            merge_step(mx, total, v, 4, bitsf(ml[u].x), bitsf(ml[u].z), a4);
+        }
+    }
 }
 
 // ATTN task: splits [unit, unit + 1) x f.attn_rounds of (stream t*16 + n,
@@ -176,8 +246,67 @@ __device__ inline GemmArgs base_args(const pgpu_flow_step &f, const pgpu_flow_la
 constexpr int kFlowRounds = PGPU_FLOW_ATTN_ROUNDS;
 static_assert(kFlowRounds * sizeof(AttnShared) <= kTaskLds * 2, "attention LDS");
 
+// Tagged mode, after the unit (wave 0): every split's partial goes out as a
+// tagged record with no drain; the task whose count completes the group
+// polls all records and merges them in split order (the arithmetic of the
+// counter mode); a task that holds every split merges from registers. The
+// merged row goes out as tagged words, then the tile's ATTN count (a hint
+// for the MLP-in tasks' first wait).
+__device__ inline void tagged_attention_tail(const pgpu_flow_step &f, int layer, int tile, int s,
+                                             int head, int split0, int nsplit, int rounds,
+                                             bool covered, const float4 *aa, const float *mm,
+                                             const float *ll, size_t group, uint32_t tag) {
+    const int lane = threadIdx.x & 63, d = (lane & 15) * 4;
+    uint64_t *part = f.parts + group * f.max_splits * PGPU_FLOW_PART_WORDS;
+    float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    bool bad = false;
+    if (covered && nsplit <= f.attn_rounds) {
+        float mx = -INFINITY, total = 0.0f;
+#pragma unroll
+        for (int r = 0; r < kFlowRounds; r++) {
+            if (r >= nsplit) break;
+            const float acc[4] = {aa[r].x, aa[r].y, aa[r].z, aa[r].w};
+            merge_step(mx, total, v, 4, mm[r], ll[r], acc);
+        }
+        bad = merge_finish<4>(total, v);
+    } else if (covered) {
+#pragma unroll
+        for (int r = 0; r < kFlowRounds; r++) {
+            if (r >= rounds) break;
+            uint64_t *rec = part + (size_t)(split0 + r) * PGPU_FLOW_PART_WORDS;
+            if (lane < 16) store_tagged4(rec + d, aa[r], tag);
+            if (lane == 0) {
+                store_tagged(rec + 64, mm[r], tag);
+                store_tagged(rec + 65, ll[r], tag);
+            }
+        }
+        unsigned done = 0;
+        if (lane == 0)
+            done = __hip_atomic_fetch_add(f.split_done + group, (unsigned)rounds,
+                                          __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        done = __shfl(done, 0);
+        if (done + rounds != (unsigned)nsplit) {
+            trace_mark(f, 2);
+            return;
+        }
+        float mx = -INFINITY, total = 0.0f;
+        merge_tagged_splits(part, 0, nsplit, mx, total, v,
+                            TagPoll{tag, f.status, wait_ticks(f), false});
+        bad = merge_finish<4>(total, v);
+    }
+    if (lane < 16)
+        store_tagged4(tagged_rows(f, layer, ROWS_ATTN) + (size_t)s * kWidth + head * kHeadDim + d,
+                      make_float4(v[0], v[1], v[2], v[3]), tag);
+    flag_nonfinite(f.status, bad && lane < 16);
+    if (lane == 0)
+        __hip_atomic_fetch_add(phase_counter(f, layer, tile, PGPU_FLOW_ATTN), 1u,
+                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    trace_mark(f, 2);
+}
+
 __device__ inline void attention_task(const pgpu_flow_step &f, const pgpu_paged_kv &kv,
-                                      int layer, int tile, int index, AttnShared *sh) {
+                                      int layer, int tile, int index, AttnShared *sh,
+                                      uint32_t tag) {
     const int head = index & 7, split0 = ((index >> 3) & 255) * f.attn_rounds, n = index >> 11;
     const int s = tile * 16 + n;
     if (s >= f.streams) return;  // uniform
@@ -214,6 +343,11 @@ __device__ inline void attention_task(const pgpu_flow_step &f, const pgpu_paged_
 
     const int lane = threadIdx.x & 63, d = (lane & 15) * 4;
     const size_t group = ((size_t)layer * f.tiles * 16 + s) * kHeads + head;
+    if (f.tagged) {
+        tagged_attention_tail(f, layer, tile, s, head, split0, nsplit, rounds, covered, aa, mm,
+                              ll, group, tag);
+        return;
+    }
     float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     bool finish = !covered, bad = false;
     if (covered && nsplit <= f.attn_rounds) {
@@ -267,15 +401,18 @@ __device__ inline void flow_step_task(const pgpu_flow_step &f, const pgpu_paged_
     uint16_t *lds = (uint16_t *)lds4;
     trace_mark(f, 0);
     const uint32_t desc = f.schedule[blockIdx.x];
+    const uint32_t tag = f.tagged ? *f.epoch : 0u;  // written by the previous launch only
     const int kind = desc & 7, layer = (desc >> 3) & 63, tile = (desc >> 9) & 255,
               index = desc >> 17;
     const pgpu_flow_layer &ly = f.layers[layer];
     const float *norm = ly.norms;
     const int live = min(16, f.streams - tile * 16);
+    const bool tagged = f.tagged != 0, last = layer + 1 == f.layer_count;
+    uint64_t *const ready_mark =
+        tagged && f.trace ? f.trace + (size_t)blockIdx.x * 4 + 1 : nullptr;
     switch (kind) {
     case PGPU_FLOW_QKV: {
-        GemmArgs a = base_args(f, ly, 0);
-        a.ln_x = layer_input(f, layer);
+        GemmArgs a = base_args(f, ly, 0, tag);
         a.ln_w = norm;
         a.ln_b = norm + kWidth;
         a.ln_eps = 1e-5f;
@@ -290,35 +427,65 @@ __device__ inline void flow_step_task(const pgpu_flow_step &f, const pgpu_paged_
         a.table_stride = f.table_stride;
         a.positions = f.positions;
         a.rope = (const float2 *)f.rope;
-        const FlowWait w = layer == 0 ? FlowWait{nullptr, 0u, f.status, 0u}
-                                      : wait_for(f, layer - 1, tile, PGPU_FLOW_MLP_OUT,
-                                                 PGPU_FLOW_MLP_OUT_TASKS);
-        gemm_wide_task<SRC_LN, EPI_QKV, Q8>(a, index, tile, lds, TracedWait{w, &f});
+        if (tagged) {
+            // The previous layer's output, polled once its MLP-in tasks are
+            // done (the phase before its producers).
+            a.ln_x = layer == 0 ? f.input : nullptr;
+            a.tx = layer == 0 ? nullptr : tagged_rows(f, layer - 1, ROWS_X);
+            a.ready_mark = ready_mark;
+            gemm_wide_task<SRC_LN, EPI_QKV, Q8>(
+                a, index, tile, lds,
+                layer == 0 ? no_wait(f)
+                           : wait_for(f, layer - 1, tile, PGPU_FLOW_MLP_IN,
+                                      PGPU_FLOW_MLP_IN_TASKS));
+        } else {
+            a.ln_x = layer_input(f, layer);
+            const FlowWait w = layer == 0 ? no_wait(f)
+                                          : wait_for(f, layer - 1, tile, PGPU_FLOW_MLP_OUT,
+                                                     PGPU_FLOW_MLP_OUT_TASKS);
+            gemm_wide_task<SRC_LN, EPI_QKV, Q8>(a, index, tile, lds, TracedWait{w, &f});
+        }
         // Rows [64 index, +64): q, k or v of head index % 8.
         flow_signal(f, phase_counter(f, layer, tile, PGPU_FLOW_QKV_HEAD + (index & 7)),
                     f.prefill ? phase_counter(f, layer, 0, PGPU_FLOW_QKV_ALL) : nullptr);
         break;
     }
     case PGPU_FLOW_ATTN:
-        attention_task(f, kv, layer, tile, index, (AttnShared *)lds4);
+        attention_task(f, kv, layer, tile, index, (AttnShared *)lds4, tag);
         break;
     case PGPU_FLOW_OUT: {
-        GemmArgs a = base_args(f, ly, 1);
-        a.ln_x = act_rows(f, layer, 3);
+        GemmArgs a = base_args(f, ly, 1, tag);
         a.n_rows = kWidth;
         a.k_cols = kWidth;
-        a.out = act_rows(f, layer, 1);
         a.ld_out = kWidth;
-        a.residual = layer_input(f, layer);
-        gemm_wide_task<SRC_ROWS, EPI_RESIDUAL, Q8>(
-            a, index, tile, lds,
-            TracedWait{wait_for(f, layer, tile, PGPU_FLOW_ATTN, (unsigned)(kHeads * live)), &f});
-        flow_signal(f, phase_counter(f, layer, tile, PGPU_FLOW_OUT));
+        if (tagged) {
+            // Merged attention rows, polled once the tile's QKV tasks are
+            // done (head 7's are listed last).
+            a.tx = tagged_rows(f, layer, ROWS_ATTN);
+            a.tout = tagged_rows(f, layer, ROWS_R);
+            a.residual = layer == 0 ? f.input : nullptr;
+            a.tres = layer == 0 ? nullptr : tagged_rows(f, layer - 1, ROWS_X);
+            a.ready_mark = ready_mark;
+            gemm_wide_task<SRC_ROWS, EPI_RESIDUAL, Q8>(
+                a, index, tile, lds,
+                f.prefill ? wait_for(f, layer, 0, PGPU_FLOW_QKV_ALL,
+                                     (unsigned)(PGPU_FLOW_QKV_TASKS * f.tiles))
+                          : wait_for(f, layer, tile, PGPU_FLOW_QKV_HEAD + kHeads - 1, 3u));
+            trace_mark(f, 2);
+        } else {
+            a.ln_x = act_rows(f, layer, 3);
+            a.out = act_rows(f, layer, 1);
+            a.residual = layer_input(f, layer);
+            gemm_wide_task<SRC_ROWS, EPI_RESIDUAL, Q8>(
+                a, index, tile, lds,
+                TracedWait{wait_for(f, layer, tile, PGPU_FLOW_ATTN, (unsigned)(kHeads * live)),
+                           &f});
+            flow_signal(f, phase_counter(f, layer, tile, PGPU_FLOW_OUT));
+        }
         break;
     }
     case PGPU_FLOW_MLP_IN: {
-        GemmArgs a = base_args(f, ly, 2);
-        a.ln_x = act_rows(f, layer, 1);
+        GemmArgs a = base_args(f, ly, 2, tag);
         a.ln_w = norm + 2 * kWidth;
         a.ln_b = norm + 3 * kWidth;
         a.ln_eps = 1e-5f;
@@ -326,24 +493,45 @@ __device__ inline void flow_step_task(const pgpu_flow_step &f, const pgpu_paged_
         a.k_cols = kWidth;
         a.out_split = hidden_rows(f, layer);
         a.out_kb = kFfn / 32;
-        gemm_wide_task<SRC_LN, EPI_GELU_SPLIT, Q8>(
-            a, index, tile, lds,
-            TracedWait{wait_for(f, layer, tile, PGPU_FLOW_OUT, PGPU_FLOW_OUT_TASKS), &f});
+        if (tagged) {
+            // r, polled once every (stream, head) of the tile is merged.
+            a.tx = tagged_rows(f, layer, ROWS_R);
+            a.ready_mark = ready_mark;
+            gemm_wide_task<SRC_LN, EPI_GELU_SPLIT, Q8>(
+                a, index, tile, lds,
+                wait_for(f, layer, tile, PGPU_FLOW_ATTN, (unsigned)(kHeads * live)));
+        } else {
+            a.ln_x = act_rows(f, layer, 1);
+            gemm_wide_task<SRC_LN, EPI_GELU_SPLIT, Q8>(
+                a, index, tile, lds,
+                TracedWait{wait_for(f, layer, tile, PGPU_FLOW_OUT, PGPU_FLOW_OUT_TASKS), &f});
+        }
         flow_signal(f, phase_counter(f, layer, tile, PGPU_FLOW_MLP_IN));
         break;
     }
     case PGPU_FLOW_MLP_OUT: {
-        GemmArgs a = base_args(f, ly, 3);
+        GemmArgs a = base_args(f, ly, 3, tag);
         a.xs = hidden_rows(f, layer);
         a.n_rows = kWidth;
         a.k_cols = kFfn;
-        a.out = layer_output(f, layer);
         a.ld_out = kWidth;
-        a.residual = act_rows(f, layer, 1);
+        if (tagged) {
+            // The last layer's output is the step's (plain rows, read after
+            // the launch); the others go out as tagged rows.
+            a.out = last ? f.output : nullptr;
+            a.tout = last ? nullptr : tagged_rows(f, layer, ROWS_X);
+            a.tres = tagged_rows(f, layer, ROWS_R);
+        } else {
+            a.out = layer_output(f, layer);
+            a.residual = act_rows(f, layer, 1);
+        }
         gemm_split_task<EPI_RESIDUAL, Q8>(
             a, index, tile, lds,
             TracedWait{wait_for(f, layer, tile, PGPU_FLOW_MLP_IN, PGPU_FLOW_MLP_IN_TASKS), &f});
-        flow_signal(f, phase_counter(f, layer, tile, PGPU_FLOW_MLP_OUT));
+        if (tagged)
+            trace_mark(f, 2);
+        else
+            flow_signal(f, phase_counter(f, layer, tile, PGPU_FLOW_MLP_OUT));
         break;
     }
     default:
@@ -359,10 +547,15 @@ __global__ __launch_bounds__(kTaskThreads) void k_flow_step(pgpu_flow_step f, pg
     flow_step_task<Q8>(f, kv, lds4);
 }
 
-__global__ void k_flow_finish(unsigned *counters, size_t n, int32_t *positions, int streams) {
+__global__ void k_flow_finish(unsigned *counters, size_t n, int32_t *positions, int streams,
+                              uint32_t *epoch) {
     const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
     for (size_t j = i; j < n; j += (size_t)gridDim.x * blockDim.x) counters[j] = 0u;
     if (i < (size_t)streams) positions[i] += 1;
+    if (i == 0 && epoch) {
+        const uint32_t next = *epoch + 1u;
+        *epoch = next ? next : 1u;
+    }
 }
 
 }  // namespace
@@ -380,6 +573,8 @@ extern "C" int pgpu_flow_launch(void *stream, const pgpu_flow_step *step,
         !step->positions || step->table_stride <= 0 || !step->rope || !step->schedule ||
         !step->tasks || !step->phase || !step->split_done || !step->status ||
         step->attn_rounds < 1 || step->attn_rounds > PGPU_FLOW_ATTN_ROUNDS ||
+        (step->tagged && (!step->rows || !step->parts || !step->epoch ||
+                          step->max_splits > 32)) ||
         step->pool_offset < 0 || step->pool_offset + step->layer_count > kv->layers)
         return bad_arguments("pgpu_flow_launch");
     if (step->q8)
@@ -392,11 +587,11 @@ extern "C" int pgpu_flow_launch(void *stream, const pgpu_flow_step *step,
 }
 
 extern "C" int pgpu_flow_finish(void *stream, unsigned *counters, size_t n, int32_t *positions,
-                                int streams) {
+                                int streams, uint32_t *epoch) {
     if (!counters || !n || !positions || streams <= 0) return bad_arguments("pgpu_flow_finish");
     const size_t work = n > (size_t)streams ? n : (size_t)streams;
     const unsigned blocks = (unsigned)((work + 255) / 256 < 1024 ? (work + 255) / 256 : 1024);
     hipLaunchKernelGGL(k_flow_finish, dim3(blocks), dim3(256), 0, (hipStream_t)stream, counters,
-                       n, positions, streams);
+                       n, positions, streams, epoch);
     return launch_ok("pgpu_flow_finish");
 }

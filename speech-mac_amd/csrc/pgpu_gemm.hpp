@@ -64,6 +64,96 @@ enum Epilogue {
 
 constexpr int kTaskWaves = 8, kTaskThreads = 64 * kTaskWaves;
 
+// ---------------------------------------------------------------------------
+// Tagged hand-off words (one-launch step). A value handed from one task to
+// another is a 64-bit word: its fp32 bits in the low half and the tag of
+// the step that produced it in the high half, written by one 64-bit
+// device-scope store. The consumer loads the words themselves with
+// device-scope loads until every tag is the current step's: a word that
+// carries the tag carries its value, so the producer neither drains its
+// stores nor counts itself done, and the consumer needs no counter. Every
+// such word has its own address per layer and is written at most once per
+// step, so a stale word carries an older tag.
+struct TagPoll {
+    uint32_t tag;
+    int *status;      // bit 4: some wait gave up; every poll then stops
+    uint64_t ticks;   // give-up bound on the 100 MHz constant clock
+    // The first load is a plain one (cacheable in the XCD's L2, so the
+    // tasks of an XCD that read the same words share one fetch): for a
+    // consumer that first waited for its producers' count. Words whose tag
+    // it does not find are then polled at device scope.
+    bool plain_first;
+};
+
+typedef __attribute__((ext_vector_type(4))) uint32_t u32x4;
+
+// Buffer resource of `bytes` bytes from `base`; both must be the same in
+// every lane of the wave (they are read from the first active lane, so the
+// resource lives in scalar registers).
+__device__ inline __amdgpu_buffer_rsrc_t tag_rsrc(const void *base, uint32_t bytes) {
+    const uint64_t p = (uint64_t)base;
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)p);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(p >> 32));
+    return __builtin_amdgcn_make_buffer_rsrc((void *)((uint64_t)hi << 32 | lo), 0,
+                                             __builtin_amdgcn_readfirstlane(bytes), 0x00020000);
+}
+
+// Two consecutive words at byte offset `off`: one 16-byte load at device
+// scope (sc1), so it is served coherently across the XCDs' L2s; or, with
+// `plain`, a cacheable load.
+__device__ inline u32x4 tag_load2(__amdgpu_buffer_rsrc_t r, uint32_t off, bool plain = false) {
+    return plain ? __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0)
+                 : __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 16);
+}
+
+__device__ inline bool tag_ok2(const u32x4 &w, uint32_t tag) {
+    return w.y == tag && w.w == tag;
+}
+
+// Between two polls of a wave: true (and the status bit set) once the wave
+// has polled longer than the bound, or another wait gave up.
+__device__ inline bool tag_give_up(const TagPoll &tp, uint64_t t0, int round) {
+    bool stop = wall_clock64() - t0 > tp.ticks;
+    if ((round & 7) == 7)
+        stop |= (__hip_atomic_load(tp.status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) & 4) != 0;
+    if (stop && (threadIdx.x & 63) == 0) atomicOr(tp.status, 4);
+    return stop;
+}
+
+__device__ inline void store_tagged(uint64_t *p, float v, uint32_t tag) {
+    __hip_atomic_store(p, (uint64_t)fbits(v) | (uint64_t)tag << 32, __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ inline void store_tagged4(uint64_t *p, float4 v, uint32_t tag) {
+    store_tagged(p, v.x, tag);
+    store_tagged(p + 1, v.y, tag);
+    store_tagged(p + 2, v.z, tag);
+    store_tagged(p + 3, v.w, tag);
+}
+
+// Four consecutive tagged values at byte offset `off` of r, for a lane that
+// needs them (`live`; the others get zeros), polled until all carry the
+// tag. Every lane of the wave must call it.
+__device__ inline float4 poll_tagged4(__amdgpu_buffer_rsrc_t r, uint32_t off, bool live,
+                                      const TagPoll &tp) {
+    u32x4 a = {0u, 0u, 0u, 0u}, b = {0u, 0u, 0u, 0u};
+    const uint64_t t0 = wall_clock64();
+    for (int round = 0;; round++) {
+        // Each round loads again: nothing may be hoisted out of the loop.
+        __asm__ volatile("" ::: "memory");
+        if (live) {
+            const bool plain = round == 0 && tp.plain_first;
+            a = tag_load2(r, off, plain);
+            b = tag_load2(r, off + 16, plain);
+        }
+        if (__all(!live || (tag_ok2(a, tp.tag) && tag_ok2(b, tp.tag)))) break;
+        if (tag_give_up(tp, t0, round)) break;
+        __builtin_amdgcn_s_sleep(1);
+    }
+    return make_float4(bitsf(a.x), bitsf(a.z), bitsf(b.x), bitsf(b.z));
+}
+
 struct GemmArgs {
     const uint16_t *xs;       // SRC_SPLIT: split fragments, k_cols/32 blocks per row
     const float *ln_x;        // SRC_LN / SRC_ROWS: [streams][512] rows
@@ -99,8 +189,16 @@ struct GemmArgs {
     const float *mod;         // SRC_LN_MOD: shift row at mod + s * ld_mod, scale at +512
     int ld_mod;
     bool plain_rows;          // single-phase launch: ln_x rows are used as they are
-    bool plain_qkv;
-    int split_terms;          // prefill projections: split terms of X used (2 or 3)           // QKV: q and K/V stored plainly (read only by later launches)
+    bool plain_qkv;           // QKV: q and K/V stored plainly (read only by later launches)
+    int split_terms;          // prefill projections: split terms of X used (2 or 3)
+    // Tagged hand-off rows of the one-launch step (null: the plain operands
+    // above): tx replaces ln_x, tres replaces residual, tout replaces out,
+    // each [tile][16][512] words (see TagPoll); ready_mark (optional)
+    // receives the time the polled inputs were all seen.
+    const uint64_t *tx, *tres;
+    uint64_t *tout;
+    TagPoll tp;
+    uint64_t *ready_mark;
 };
 
 // ---------------------------------------------------------------------------
@@ -237,6 +335,42 @@ __device__ inline void rows_load(Rows2 &r, const float *x, int streams, int st) 
             for (int k = 0; k < 8; k++) r.v[i][k] = 0.0f;
         }
     }
+}
+
+// rows_load from tagged rows (tile st's 16 rows of 512 words at `rows`):
+// each wave polls its two streams' words until all carry the tag.
+__device__ inline void rows_poll(Rows2 &r, const uint64_t *rows, int streams, int st,
+                                 const TagPoll &tp) {
+    const int wave = threadIdx.x >> 6, j = threadIdx.x & 63;
+    const __amdgpu_buffer_rsrc_t rs = tag_rsrc(rows + (size_t)st * 16 * kWidth, 16 * kWidth * 8);
+    u32x4 w[2][4];
+#pragma unroll
+    for (int i = 0; i < 2; i++) r.live[i] = st * 16 + 2 * wave + i < streams;  // uniform
+    const uint64_t t0 = wall_clock64();
+    for (int round = 0;; round++) {
+        __asm__ volatile("" ::: "memory");
+        bool ok = true;
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            if (!r.live[i]) continue;
+            const uint32_t off = (uint32_t)(((2 * wave + i) * kWidth + 8 * j) * 8);
+            const bool plain = round == 0 && tp.plain_first;
+#pragma unroll
+            for (int k = 0; k < 4; k++) w[i][k] = tag_load2(rs, off + 16 * k, plain);
+#pragma unroll
+            for (int k = 0; k < 4; k++) ok &= tag_ok2(w[i][k], tp.tag);
+        }
+        if (__all(ok)) break;
+        if (tag_give_up(tp, t0, round)) break;
+        __builtin_amdgcn_s_sleep(1);
+    }
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            r.v[i][2 * k] = r.live[i] ? bitsf(w[i][k].x) : 0.0f;
+            r.v[i][2 * k + 1] = r.live[i] ? bitsf(w[i][k].z) : 0.0f;
+        }
 }
 
 // LayerNorm of the loaded rows, in place: two-pass fp32 moments per stream
@@ -574,12 +708,18 @@ __device__ inline void load_epilogue_static(EpiOperands &e, const GemmArgs &a, i
 }
 
 // Operands produced by earlier tasks of the step (the residual rows): loaded
-// only after the task's wait.
+// only after the task's wait (tagged residual rows: polled). Every lane of
+// the wave must call it.
 template <int EPI>
-__device__ inline void load_epilogue_dynamic(EpiOperands &e, const GemmArgs &a, int s, int row0,
-                                             bool live) {
+__device__ inline void load_epilogue_dynamic(EpiOperands &e, const GemmArgs &a, int st, int s,
+                                             int row0, bool live) {
     if constexpr (EPI == EPI_RESIDUAL) {
-        if (live) {
+        if (a.tres) {
+            const __amdgpu_buffer_rsrc_t r =
+                tag_rsrc(a.tres + (size_t)st * 16 * kWidth, 16 * kWidth * 8);
+            e.add = poll_tagged4(r, (uint32_t)(((s & 15) * kWidth + row0) * 8), live, a.tp);
+            e.has_add = live;
+        } else if (live) {
             e.add = *(const float4 *)(a.residual + (size_t)s * a.ld_out + row0);
             e.has_add = true;
         }
@@ -611,7 +751,11 @@ __device__ inline bool epilogue(const GemmArgs &a, const EpiOperands &e, const f
                                         : __fadd_rn(add[r], v[r]);
                 bad |= !isfinite(y[r]);
             }
-            store_out(o, make_float4(y[0], y[1], y[2], y[3]), wt);
+            if (a.tout)
+                store_tagged4(a.tout + (size_t)s * kWidth + row0,
+                              make_float4(y[0], y[1], y[2], y[3]), a.tp.tag);
+            else
+                store_out(o, make_float4(y[0], y[1], y[2], y[3]), wt);
         }
     } else if constexpr (EPI == EPI_GELU_SPLIT) {
         if (live) {
@@ -722,7 +866,7 @@ __device__ inline void gemm_wide_task(const GemmArgs &a, int bx, int st, uint16_
     EpiOperands e;
     if (active && half == 0) load_epilogue_static<EPI>(e, a, s, row0, live);
     wait();
-    if (active && half == 0) load_epilogue_dynamic<EPI>(e, a, s, row0, live);
+    if (active && half == 0) load_epilogue_dynamic<EPI>(e, a, st, s, row0, live);
 
     bool bad_in = false;
     if constexpr (SRC == SRC_ATTN) {
@@ -731,7 +875,10 @@ __device__ inline void gemm_wide_task(const GemmArgs &a, int bx, int st, uint16_
         split_to_lds(a.xs, st, bsh);
     } else {
         Rows2 r;
-        rows_load(r, a.ln_x, a.streams, st);
+        if (a.tx)
+            rows_poll(r, a.tx, a.streams, st, a.tp);
+        else
+            rows_load(r, a.ln_x, a.streams, st);
         if constexpr (SRC == SRC_LN)
             bad_in = rows_ln(r, a.ln_w, a.ln_b, a.ln_eps, bsh);
         else if constexpr (SRC == SRC_LN_MOD)
@@ -741,6 +888,7 @@ __device__ inline void gemm_wide_task(const GemmArgs &a, int bx, int st, uint16_
     }
     flag_nonfinite(a.status, bad_in);
     __syncthreads();
+    if (a.ready_mark && threadIdx.x == 0) *a.ready_mark = wall_clock64();
 
     f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
     if (active) {
@@ -801,7 +949,7 @@ __device__ inline void gemm_split_task(const GemmArgs &a, int tile, int st, uint
     EpiOperands e;
     if (wave == 0) load_epilogue_static<EPI>(e, a, s, row0, live);
     wait();
-    if (wave == 0) load_epilogue_dynamic<EPI>(e, a, s, row0, live);
+    if (wave == 0) load_epilogue_dynamic<EPI>(e, a, st, s, row0, live);
 
     const uint16_t *xs = a.xs + (size_t)st * kbn * 1536 + lane * 8;
     f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};

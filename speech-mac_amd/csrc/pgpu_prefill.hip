@@ -241,7 +241,7 @@ __global__ __launch_bounds__(kTaskThreads) void k_prefill_gemm(GemmArgs a, int r
             const int s = (pt0 + wp * PW + p) * 16 + (lane & 15);
             const int row0 = (rt0 + wr * RW + r) * 16 + (lane >> 4) * 4;
             load_epilogue_static<EPI>(ep[r][p], a, s, row0, s < a.streams);
-            load_epilogue_dynamic<EPI>(ep[r][p], a, s, row0, s < a.streams);
+            load_epilogue_dynamic<EPI>(ep[r][p], a, s >> 4, s, row0, s < a.streams);
         }
 
     // One 32-column block from LDS stage area st. Every tile's products

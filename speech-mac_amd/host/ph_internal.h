@@ -36,6 +36,9 @@ enum {
     PH_FLOW_ONE_ROUND_MIN_TILES = 3,
     PH_FLOW_ONE_ROUND_MAX_TILES = 4
 };
+/* One-launch steps of at most this many streams hand values over as tagged
+ * words (phonon_flow_batch_set_handoff). */
+enum { PH_FLOW_TAGGED_MAX_STREAMS = 4 };
 /* Chain placement of the one-launch step's task list (pgpu_flow_placement):
  * measured on MI355X at B = 64 (ph_flow_schedule.c). */
 pgpu_flow_placement ph_flow_default_placement(int rounds);

@@ -61,6 +61,11 @@ struct PhononFlowBatch {
         uint16_t *hidden;
         unsigned *counters;         /* all zero between steps */
         size_t counter_words;
+        uint64_t *rows, *parts;     /* (dev) tagged mode's hand-off words (pgpu_flow_step) */
+        size_t rows_words, parts_words;
+        uint32_t *epoch;            /* (dev) tagged mode's tag of the next step */
+        uint32_t epoch_host;        /* the same, as far as the host has enqueued */
+        int tagged_set;             /* -1: by batch size, else the caller's choice */
         uint32_t *schedule, *host_schedule;
         size_t schedule_cap, host_cap, tasks;
         size_t *cover;              /* [max_streams] splits the schedule lists per stream */
@@ -403,7 +408,7 @@ void phonon_flow_batch_destroy(PhononFlowBatch *b) {
                     b->rows, b->xh, b->positions, b->tables, b->status,
                     b->scratch.part_acc, b->scratch.part_ml, b->table_src, b->table_map,
                     b->fl.act, b->fl.part_acc, b->fl.part_ml, b->fl.hidden, b->fl.counters,
-                    b->fl.schedule};
+                    b->fl.rows, b->fl.parts, b->fl.epoch, b->fl.schedule};
     for (size_t i = 0; i < sizeof(bufs) / sizeof(bufs[0]); i++)
         pgpu_free(bufs[i]);
     pgpu_stream_destroy(b->stream);
@@ -433,6 +438,7 @@ int phonon_flow_batch_create(const PhononFlowModel *model, PhononKvPool *pool,
         return 0;
     b->model = model;
     b->pool = pool;
+    b->fl.tagged_set = -1;
     b->max_streams = max_streams;
     b->padded_streams = (max_streams + 15) / 16 * 16;
     b->max_positions = max_positions;
@@ -737,6 +743,16 @@ static int flow_usable(const PhononFlowBatch *b, int prefill) {
            (!prefill && tiles >= PH_FLOW_MIN_TILES && tiles <= PH_FLOW_MAX_TILES);
 }
 
+/* Every tagged hand-off word to tag 0 and the next step's tag to 1: no
+ * stale word carries a tag a later step uses until the tag wraps. */
+static int flow_clear_tags(PhononFlowBatch *b) {
+    const uint32_t one = 1;
+    b->fl.epoch_host = 1;
+    return pgpu_memset(b->stream, b->fl.rows, 0, b->fl.rows_words * sizeof(uint64_t)) &&
+           pgpu_memset(b->stream, b->fl.parts, 0, b->fl.parts_words * sizeof(uint64_t)) &&
+           pgpu_copy_h2d(b->stream, b->fl.epoch, &one, sizeof(one));
+}
+
 /* Grows the per-layer buffers of the one-launch step to hold `streams`
  * streams of the model's layers. Every value a step's task hands to another
  * has its own address per layer (see pgpu_flow.hip). */
@@ -749,13 +765,15 @@ static int flow_reserve(PhononFlowBatch *b, size_t streams) {
     if (!pgpu_stream_sync(b->stream))
         return 0;
     drop_graphs(b);
-    void *old[] = {b->fl.act, b->fl.part_acc, b->fl.part_ml, b->fl.hidden, b->fl.counters};
+    void *old[] = {b->fl.act,     b->fl.part_acc, b->fl.part_ml, b->fl.hidden,
+                   b->fl.counters, b->fl.rows,     b->fl.parts};
     for (size_t i = 0; i < sizeof(old) / sizeof(old[0]); i++)
         pgpu_free(old[i]);
     b->fl.act = NULL;
     b->fl.part_acc = b->fl.part_ml = NULL;
     b->fl.hidden = NULL;
     b->fl.counters = NULL;
+    b->fl.rows = b->fl.parts = NULL;
     b->fl.cap = b->fl.cap_layers = 0;
     b->fl.streams = 0; /* the schedule is rebuilt against the new buffers */
     const size_t groups = new_layers * new_cap * PH_HEADS;
@@ -766,11 +784,18 @@ static int flow_reserve(PhononFlowBatch *b, size_t streams) {
     b->fl.part_ml = pgpu_malloc(groups * flow_ml_group(b) * sizeof(float));
     b->fl.hidden = pgpu_malloc(new_layers * new_cap * PH_FFN * 3 * sizeof(uint16_t));
     b->fl.counters = pgpu_malloc(b->fl.counter_words * sizeof(unsigned));
+    b->fl.rows_words = new_layers * 3 * new_cap * PH_WIDTH;
+    b->fl.parts_words = groups * b->max_splits * PGPU_FLOW_PART_WORDS;
+    b->fl.rows = pgpu_malloc(b->fl.rows_words * sizeof(uint64_t));
+    b->fl.parts = pgpu_malloc(b->fl.parts_words * sizeof(uint64_t));
+    if (!b->fl.epoch)
+        b->fl.epoch = pgpu_malloc(sizeof(uint32_t));
     if (!b->fl.act || !b->fl.part_acc || !b->fl.part_ml || !b->fl.hidden || !b->fl.counters ||
+        !b->fl.rows || !b->fl.parts || !b->fl.epoch ||
         !pgpu_memset(b->stream, b->fl.counters, 0, b->fl.counter_words * sizeof(unsigned)) ||
         !pgpu_memset(b->stream, b->fl.hidden, 0,
                      new_layers * new_cap * PH_FFN * 3 * sizeof(uint16_t)) ||
-        !pgpu_stream_sync(b->stream))
+        !flow_clear_tags(b) || !pgpu_stream_sync(b->stream))
         return 0;
     b->fl.cap = new_cap;
     b->fl.cap_layers = new_layers;
@@ -834,9 +859,30 @@ static int flow_schedule(PhononFlowBatch *b, int prefill) {
 }
 
 /* Makes buffers and schedule ready for the batch's current streams (outside
- * any graph capture). */
+ * any graph capture); called once per one-launch step. The tagged mode's
+ * tag advances once per step (pgpu_flow_finish, skipping 0): before it
+ * could come back to a value a stale word still carries, every word is
+ * cleared. */
 static int flow_prepare(PhononFlowBatch *b, int prefill) {
-    return flow_reserve(b, b->streams) && flow_schedule(b, prefill);
+    if (!flow_reserve(b, b->streams) || !flow_schedule(b, prefill))
+        return 0;
+    if (b->fl.epoch_host >= UINT32_MAX - 1 &&
+        !(pgpu_stream_sync(b->stream) && flow_clear_tags(b)))
+        return 0;
+    b->fl.epoch_host++;
+    return 1;
+}
+
+/* Whether a one-launch step hands x, r, the merged attention rows and the
+ * split partials over as tagged words (pgpu_flow.hip): one memory round
+ * trip less per hand-off, but every poll fetches from memory, which costs
+ * more than the counter mode's shared loads once the tile holds more than
+ * a few streams (measured on MI355X, us per 12-layer step, contexts
+ * U{1..2048}, counter vs tagged: B = 1: 324 vs 291; B = 16: 482 vs 529). */
+static int flow_tagged(const PhononFlowBatch *b) {
+    if (b->fl.tagged_set >= 0)
+        return b->fl.tagged_set;
+    return b->streams <= PH_FLOW_TAGGED_MAX_STREAMS;
 }
 
 /* One step as a single launch, then the launch that zeroes its counters and
@@ -874,12 +920,17 @@ static int enqueue_flow(PhononFlowBatch *b, const float *input, float *output, f
                               .status = b->status,
                               .trace = b->fl.trace_cap >= b->fl.tasks ? b->fl.trace : NULL,
                               .attn_rounds = b->fl.rounds,
-                              .wait_us = b->fl.wait_us};
+                              .wait_us = b->fl.wait_us,
+                              .tagged = flow_tagged(b),
+                              .rows = b->fl.rows,
+                              .parts = b->fl.parts,
+                              .epoch = b->fl.epoch};
     const size_t used = phase_words + layers * tiles * 16 * PH_HEADS;
     return (!b->time_before || pgpu_event_record(b->time_before, b->stream)) &&
            pgpu_flow_launch(b->stream, &f, &b->pool->kv) &&
            (!b->time_after || pgpu_event_record(b->time_after, b->stream)) &&
-           pgpu_flow_finish(b->stream, b->fl.counters, used, b->positions, (int)b->streams);
+           pgpu_flow_finish(b->stream, b->fl.counters, used, b->positions, (int)b->streams,
+                            b->fl.epoch);
 }
 
 /* Work entries of the prefill attention (pgpu_prefill_attention): for each
@@ -1117,6 +1168,13 @@ int phonon_flow_batch_set_pipeline(PhononFlowBatch *b, int mode) {
         drop_graphs(b);
         b->flow = mode;
     }
+    return 1;
+}
+
+int phonon_flow_batch_set_handoff(PhononFlowBatch *b, int tagged) {
+    if (!b || tagged < -1 || tagged > 1)
+        return 0;
+    b->fl.tagged_set = tagged;
     return 1;
 }
 

@@ -720,13 +720,13 @@ def test_batched_prefill_equals_single_steps(lib, syn, pkg, mode, exact):
         assert worst <= 1e-4
 
 
-@pytest.mark.parametrize("streams", [1, 16, 17, 40, 64])
+@pytest.mark.parametrize("streams", [1, 3, 16, 17, 40, 64])
 def test_one_launch_step_equals_phase_launches(lib, syn, pkg, streams):
     """The one-launch step (every layer's tasks in one dataflow launch) gives
     the same bits as one launch per phase, with one or two attention splits
-    per task, over several steps with ragged contexts, in graph replay and in
-    direct launches; then again after the contexts jump past the task
-    schedule's headroom (schedule rebuilt)."""
+    per task, with counter and tagged hand-offs, over several steps with
+    ragged contexts, in graph replay and in direct launches; then again after
+    the contexts jump past the task schedule's headroom (schedule rebuilt)."""
     layers = 3
     model = scaled_model(syn, 181, layers)
     views = pkg.Views()
@@ -739,12 +739,14 @@ def test_one_launch_step_equals_phase_launches(lib, syn, pkg, streams):
     ctx = rng.standard_normal((2, layers, max_pos, 512)).astype(np.float32)
     xs = rng.standard_normal((4, streams, 512)).astype(np.float32)
     runs = []
-    for flow, graph, rounds in ((0, 1, 0), (2, 1, 1), (2, 1, 2), (2, 0, 0)):
+    for flow, graph, rounds, handoff in ((0, 1, 0, -1), (2, 1, 1, 0), (2, 1, 2, 0),
+                                         (2, 0, 0, -1), (2, 1, 1, 1), (2, 0, 2, 1)):
         print(f"one-launch vs phases: streams={streams} flow={flow} graph={graph} "
-              f"rounds={rounds}", flush=True)
+              f"rounds={rounds} handoff={handoff}", flush=True)
         bt = Batch(lib, w, layers, streams, max_pos, blocks)
         set_step_mode(lib, bt.batch, flow)
         assert lib.phonon_flow_batch_set_attention_rounds(bt.batch, rounds)
+        assert lib.phonon_flow_batch_set_handoff(bt.batch, handoff)
         assert lib.phonon_flow_batch_set_graph(bt.batch, graph)
         ids = np.zeros(blocks, np.int32)
         assert lib.phonon_kv_pool_alloc(bt.pool, blocks, i32p(ids))
@@ -841,12 +843,14 @@ def test_batch_reports_nonfinite_and_uncovered_positions(lib, syn, pkg):
 
 
 # ---------------------------------------------------------------- robustness
-def test_forced_wait_timeout_reports_and_recovers(lib, syn, pkg):
+@pytest.mark.parametrize("handoff", [0, 1])
+def test_forced_wait_timeout_reports_and_recovers(lib, syn, pkg, handoff):
     """The one-launch step's give-up path, forced from the host: with a 1 us
-    wait limit its tasks stop waiting, the launch still ends, status bit 2
-    (value 4) is set and the step reports failure; with the default limit
-    restored and the positions reset, the same batch gives the bits of a
-    batch that never timed out."""
+    wait limit its tasks stop waiting (counter waits, and with tagged
+    hand-offs their polls), the launch still ends, status bit 2 (value 4) is
+    set and the step reports failure; with the default limit restored and
+    the positions reset, the same batch gives the bits of a batch that never
+    timed out."""
     layers, streams = 3, 64
     model = scaled_model(syn, 231, layers)
     views = pkg.Views()
@@ -863,6 +867,7 @@ def test_forced_wait_timeout_reports_and_recovers(lib, syn, pkg):
     def setup():
         bt = Batch(lib, w, layers, streams, max_pos, blocks)
         set_step_mode(lib, bt.batch, 2)
+        assert lib.phonon_flow_batch_set_handoff(bt.batch, handoff)
         ids = np.zeros(blocks, np.int32)
         assert lib.phonon_kv_pool_alloc(bt.pool, blocks, i32p(ids))
         tables = np.ascontiguousarray(ids.reshape(streams, table_len))
@@ -882,7 +887,8 @@ def test_forced_wait_timeout_reports_and_recovers(lib, syn, pkg):
     bt, tables = setup()
     assert not lib.phonon_flow_batch_set_wait_limit(bt.batch, 10000001)
     assert lib.phonon_flow_batch_set_wait_limit(bt.batch, 1)
-    print("forced wait timeout: one-launch step with a 1 us wait limit", flush=True)
+    print(f"forced wait timeout: one-launch step with a 1 us wait limit, handoff={handoff}",
+          flush=True)
     din = pkg.DeviceBuffer(lib, streams * 512 * 4)
     dout = pkg.DeviceBuffer(lib, streams * 512 * 4)
     din.upload(x)
