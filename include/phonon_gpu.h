@@ -175,6 +175,9 @@ int pgpu_q8_gemv(void *stream, const int8_t *values, const uint16_t *scales, int
 #define PGPU_FLOW_COUNTER_STRIDE 16 /* 32-bit words between phase counters */
 #define PGPU_FLOW_ATTN_ROUNDS 2    /* most 256-key splits per ATTN task */
 #define PGPU_FLOW_PART_WORDS 72    /* tagged words per split partial (66 used) */
+#define PGPU_FLOW_HANDOFF_COUNTER 0 /* pgpu_flow_step.tagged: counters and shared loads */
+#define PGPU_FLOW_HANDOFF_TAGGED 1  /* x, r, merged attention rows, split partials tagged */
+#define PGPU_FLOW_HANDOFF_PARTS 2   /* split partials tagged, the rest by counters */
 
 #define PGPU_FLOW_TASK(kind, layer, tile, index)                                      \
     ((uint32_t)(kind) | (uint32_t)(layer) << 3 | (uint32_t)(tile) << 9 |             \
@@ -211,15 +214,18 @@ typedef struct {
                                       ran (XCC id << 32 | HW_ID register) */
     unsigned wait_us;              /* a task's wait for its inputs gives up (status bit 4)
                                       after this many microseconds; 0: one second */
-    int tagged;                    /* 1: x, r, the merged attention rows and the split
-                                      partials are handed over as tagged words in `rows`
-                                      and `parts` (part_acc, part_ml and act's x, r and
-                                      attention rows are then unused) */
-    uint64_t *rows;                /* (dev, tagged) [layer_count][3][tiles*16][512]: x, r,
+    int tagged;                    /* PGPU_FLOW_HANDOFF_*: TAGGED: x, r, the merged
+                                      attention rows and the split partials are handed
+                                      over as tagged words in `rows` and `parts`
+                                      (part_acc, part_ml and act's x, r and attention
+                                      rows are then unused); PARTS: only the split
+                                      partials, in `parts` (part_acc, part_ml unused) */
+    uint64_t *rows;                /* (dev, TAGGED) [layer_count][3][tiles*16][512]: x, r,
                                       merged attention */
-    uint64_t *parts;               /* (dev, tagged) [layer_count][tiles*16][8][max_splits]
-                                      [PGPU_FLOW_PART_WORDS]: P.V [64], max, sum */
-    const uint32_t *epoch;         /* (dev, tagged) this step's tag, never 0 */
+    uint64_t *parts;               /* (dev, TAGGED or PARTS) [layer_count][tiles*16][8]
+                                      [max_splits][PGPU_FLOW_PART_WORDS]: P.V [64], max,
+                                      sum */
+    const uint32_t *epoch;         /* (dev, TAGGED or PARTS) this step's tag, never 0 */
 } pgpu_flow_step;
 
 /* Placement of each tile's projection chain in a task list, on a model

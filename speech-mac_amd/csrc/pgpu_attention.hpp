@@ -67,7 +67,8 @@ struct NoGate {
 // wave of the work-group must call it (it holds one work-group barrier); a
 // unit without live keys (or that does not `exist`: past the end of a grid)
 // only takes part in the barrier. If the result is UNIT_LIVE, lanes 0..15 of
-// wave 0 hold the partial of each split r that starts inside the context:
+// waves 0 .. merge_waves - 1 (each computes the same bits) hold the partial
+// of each split r that starts inside the context:
 // max score mm[r], sum of exp ll[r] and the unnormalised P.V dims
 // [4 lane, 4 lane + 4) in aa[r]. `count` receives the stream's keys (0 if
 // the unit does not exist). sh holds ROUNDS AttnShared. `rounds` (at most
@@ -78,7 +79,7 @@ template <int ROUNDS = 1, class Gate = NoGate>
 __device__ inline int attend_unit(const AttnArgs &a, int head, int split0, int s, int wave,
                                   AttnShared *sh, bool exists, float4 *aa, float *mm, float *ll,
                                   int &count, const Gate &gate = Gate{}, int rounds = ROUNDS,
-                                  bool early = true) {
+                                  bool early = true, int merge_waves = 1) {
     const int lane = threadIdx.x & 63;
     const int krow = lane >> 4, dcol = lane & 15;
     // First loads, in flight together: the context length, the wave's block
@@ -202,7 +203,7 @@ __device__ inline int attend_unit(const AttnArgs &a, int head, int split0, int s
     }
     __syncthreads();
     const int state = live ? UNIT_LIVE : (exists && !covered ? UNIT_UNCOVERED : UNIT_EMPTY);
-    if (!live || wave != 0 || lane >= 16) return state;
+    if (!live || wave >= merge_waves || lane >= 16) return state;
 
     // Merge the unit's waves (fixed order), per split. A wave without keys
     // has l = 0.

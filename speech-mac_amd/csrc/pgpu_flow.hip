@@ -33,17 +33,25 @@
 // Read-only operands (weights, norms, positions, block tables, the RoPE
 // table, older K/V) are plain loads and stay cacheable.
 //
-// Tagged mode (f.tagged = 1, for a batch of a few streams): the layer
-// output x, the out projection r, the merged attention rows and the split
-// partials are tagged words (pgpu_gemm.hpp TagPoll), stored without a
-// drain; the consumer polls the words themselves, so a hand-off costs one
-// memory round trip less. A consumer first waits (one lane, one counter)
-// for the phase before its producers, so that tasks dispatched long before
-// their inputs do not poll all that time. Polls fetch from memory on every
-// round (device scope), which with many streams per tile costs more than
-// the counter mode's shared, cacheable loads (measured), hence the two
-// modes. q, the appended K/V and the MLP hidden fragments keep their
-// counters in both.
+// Tagged mode (f.tagged = PGPU_FLOW_HANDOFF_TAGGED, for a batch of a few
+// streams): the layer output x, the out projection r, the merged attention
+// rows and the split partials are tagged words (pgpu_gemm.hpp TagPoll),
+// stored without a drain; the consumer polls the words themselves, so a
+// hand-off costs one memory round trip less. A consumer first waits (one
+// lane, one counter) for the phase before its producers, so that tasks
+// dispatched long before their inputs do not poll all that time. Polls
+// fetch from memory on every round (device scope), which with many streams
+// per tile costs more than the counter mode's shared, cacheable loads
+// (measured), hence the modes. q, the appended K/V and the MLP hidden
+// fragments keep their counters in all of them.
+//
+// Tagged partials (f.tagged = PGPU_FLOW_HANDOFF_PARTS): only the split
+// partials are tagged. An attention task that does not complete its
+// (stream, head) then ends right after its split count, without waiting for
+// its partial stores to reach memory (the drain took about a quarter of an
+// attention task's life at 64 streams); the task that completes the group
+// polls the 66 words of each partial, which is cheap, and hands the merged
+// row over as in the counter mode.
 //
 // Every wait is bounded (1 s of the 100 MHz constant clock): a task that
 // times out sets status bit 4, and every other waiter then stops waiting,
@@ -246,21 +254,41 @@ __device__ inline void merge_tagged_splits(const uint64_t *part, int j0, int nsp
 constexpr int kFlowRounds = PGPU_FLOW_ATTN_ROUNDS;
 static_assert(kFlowRounds * sizeof(AttnShared) <= kTaskLds * 2, "attention LDS");
 
-// Tagged mode, after the unit (wave 0): every split's partial goes out as a
-// tagged record with no drain; the task whose count completes the group
-// polls all records and merges them in split order (the arithmetic of the
-// counter mode); a task that holds every split merges from registers. The
+// Tagged partials, after the unit. Wave 1 stores every split's partial as
+// a tagged record and ends; wave 0 counts the splits (it does not wait for
+// wave 1's stores: each wave's memory operations retire in order, and only
+// its own), and if its count completes the group it polls all records and
+// merges them in split order (the arithmetic of the counter mode). A task
+// that holds every split merges from registers. With `rows_tagged` the
 // merged row goes out as tagged words, then the tile's ATTN count (a hint
-// for the MLP-in tasks' first wait).
+// for the MLP-in tasks' first wait); otherwise it is stored write-through
+// and drained before the count, as in the counter mode.
 __device__ inline void tagged_attention_tail(const pgpu_flow_step &f, int layer, int tile, int s,
                                              int head, int split0, int nsplit, int rounds,
                                              bool covered, const float4 *aa, const float *mm,
-                                             const float *ll, size_t group, uint32_t tag) {
+                                             const float *ll, size_t group, uint32_t tag,
+                                             bool rows_tagged, int wave) {
     const int lane = threadIdx.x & 63, d = (lane & 15) * 4;
     uint64_t *part = f.parts + group * f.max_splits * PGPU_FLOW_PART_WORDS;
+    const bool in_registers = covered && nsplit <= f.attn_rounds;
+    if (wave == 1) {
+        if (covered && !in_registers) {
+#pragma unroll
+            for (int r = 0; r < kFlowRounds; r++) {
+                if (r >= rounds) break;
+                uint64_t *rec = part + (size_t)(split0 + r) * PGPU_FLOW_PART_WORDS;
+                if (lane < 16) store_tagged4(rec + d, aa[r], tag);
+                if (lane == 0) {
+                    store_tagged(rec + 64, mm[r], tag);
+                    store_tagged(rec + 65, ll[r], tag);
+                }
+            }
+        }
+        return;
+    }
     float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     bool bad = false;
-    if (covered && nsplit <= f.attn_rounds) {
+    if (in_registers) {
         float mx = -INFINITY, total = 0.0f;
 #pragma unroll
         for (int r = 0; r < kFlowRounds; r++) {
@@ -270,16 +298,6 @@ __device__ inline void tagged_attention_tail(const pgpu_flow_step &f, int layer,
         }
         bad = merge_finish<4>(total, v);
     } else if (covered) {
-#pragma unroll
-        for (int r = 0; r < kFlowRounds; r++) {
-            if (r >= rounds) break;
-            uint64_t *rec = part + (size_t)(split0 + r) * PGPU_FLOW_PART_WORDS;
-            if (lane < 16) store_tagged4(rec + d, aa[r], tag);
-            if (lane == 0) {
-                store_tagged(rec + 64, mm[r], tag);
-                store_tagged(rec + 65, ll[r], tag);
-            }
-        }
         unsigned done = 0;
         if (lane == 0)
             done = __hip_atomic_fetch_add(f.split_done + group, (unsigned)rounds,
@@ -294,10 +312,19 @@ __device__ inline void tagged_attention_tail(const pgpu_flow_step &f, int layer,
                             TagPoll{tag, f.status, wait_ticks(f), false});
         bad = merge_finish<4>(total, v);
     }
-    if (lane < 16)
-        store_tagged4(tagged_rows(f, layer, ROWS_ATTN) + (size_t)s * kWidth + head * kHeadDim + d,
-                      make_float4(v[0], v[1], v[2], v[3]), tag);
-    flag_nonfinite(f.status, bad && lane < 16);
+    if (!rows_tagged) {
+        if (lane < 16)
+            store_wt(act_rows(f, layer, 3) + (size_t)s * kWidth + head * kHeadDim + d,
+                     make_float4(v[0], v[1], v[2], v[3]));
+        flag_nonfinite(f.status, bad && lane < 16);
+        __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    } else {
+        if (lane < 16)
+            store_tagged4(tagged_rows(f, layer, ROWS_ATTN) + (size_t)s * kWidth +
+                              head * kHeadDim + d,
+                          make_float4(v[0], v[1], v[2], v[3]), tag);
+        flag_nonfinite(f.status, bad && lane < 16);
+    }
     if (lane == 0)
         __hip_atomic_fetch_add(phase_counter(f, layer, tile, PGPU_FLOW_ATTN), 1u,
                                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -334,18 +361,22 @@ __device__ inline void attention_task(const pgpu_flow_step &f, const pgpu_paged_
     float4 aa[kFlowRounds];
     float mm[kFlowRounds], ll[kFlowRounds];
     int count;
+    const bool tagged_parts = f.tagged != PGPU_FLOW_HANDOFF_COUNTER;
     const int state = attend_unit<kFlowRounds>(a, head, split0, s, wave, sh, true, aa, mm, ll,
-                                               count, ready, f.attn_rounds, !f.prefill);
-    if (wave != 0 || state == UNIT_EMPTY || (state == UNIT_UNCOVERED && split0 != 0)) return;
+                                               count, ready, f.attn_rounds, !f.prefill,
+                                               tagged_parts ? 2 : 1);
+    if (wave > (tagged_parts ? 1 : 0) || state == UNIT_EMPTY ||
+        (state == UNIT_UNCOVERED && split0 != 0))
+        return;
     const bool covered = state == UNIT_LIVE;
     const int nsplit = (count + kSplitKeys - 1) / kSplitKeys;
     const int rounds = min(f.attn_rounds, nsplit - split0);  // splits of this task (if covered)
 
     const int lane = threadIdx.x & 63, d = (lane & 15) * 4;
     const size_t group = ((size_t)layer * f.tiles * 16 + s) * kHeads + head;
-    if (f.tagged) {
+    if (tagged_parts) {
         tagged_attention_tail(f, layer, tile, s, head, split0, nsplit, rounds, covered, aa, mm,
-                              ll, group, tag);
+                              ll, group, tag, f.tagged == PGPU_FLOW_HANDOFF_TAGGED, wave);
         return;
     }
     float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -401,13 +432,14 @@ __device__ inline void flow_step_task(const pgpu_flow_step &f, const pgpu_paged_
     uint16_t *lds = (uint16_t *)lds4;
     trace_mark(f, 0);
     const uint32_t desc = f.schedule[blockIdx.x];
-    const uint32_t tag = f.tagged ? *f.epoch : 0u;  // written by the previous launch only
+    // written by the previous launch only
+    const uint32_t tag = f.tagged != PGPU_FLOW_HANDOFF_COUNTER ? *f.epoch : 0u;
     const int kind = desc & 7, layer = (desc >> 3) & 63, tile = (desc >> 9) & 255,
               index = desc >> 17;
     const pgpu_flow_layer &ly = f.layers[layer];
     const float *norm = ly.norms;
     const int live = min(16, f.streams - tile * 16);
-    const bool tagged = f.tagged != 0, last = layer + 1 == f.layer_count;
+    const bool tagged = f.tagged == PGPU_FLOW_HANDOFF_TAGGED, last = layer + 1 == f.layer_count;
     uint64_t *const ready_mark =
         tagged && f.trace ? f.trace + (size_t)blockIdx.x * 4 + 1 : nullptr;
     switch (kind) {
@@ -573,8 +605,10 @@ extern "C" int pgpu_flow_launch(void *stream, const pgpu_flow_step *step,
         !step->positions || step->table_stride <= 0 || !step->rope || !step->schedule ||
         !step->tasks || !step->phase || !step->split_done || !step->status ||
         step->attn_rounds < 1 || step->attn_rounds > PGPU_FLOW_ATTN_ROUNDS ||
-        (step->tagged && (!step->rows || !step->parts || !step->epoch ||
-                          step->max_splits > 32)) ||
+        step->tagged < PGPU_FLOW_HANDOFF_COUNTER || step->tagged > PGPU_FLOW_HANDOFF_PARTS ||
+        (step->tagged != PGPU_FLOW_HANDOFF_COUNTER &&
+         (!step->parts || !step->epoch || step->max_splits > 32)) ||
+        (step->tagged == PGPU_FLOW_HANDOFF_TAGGED && !step->rows) ||
         step->pool_offset < 0 || step->pool_offset + step->layer_count > kv->layers)
         return bad_arguments("pgpu_flow_launch");
     if (step->q8)

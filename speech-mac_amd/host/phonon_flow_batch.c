@@ -1172,7 +1172,7 @@ int phonon_flow_batch_set_pipeline(PhononFlowBatch *b, int mode) {
 }
 
 int phonon_flow_batch_set_handoff(PhononFlowBatch *b, int tagged) {
-    if (!b || tagged < -1 || tagged > 1)
+    if (!b || tagged < -1 || tagged > PGPU_FLOW_HANDOFF_PARTS)
         return 0;
     b->fl.tagged_set = tagged;
     return 1;

@@ -724,7 +724,7 @@ def test_batched_prefill_equals_single_steps(lib, syn, pkg, mode, exact):
 def test_one_launch_step_equals_phase_launches(lib, syn, pkg, streams):
     """The one-launch step (every layer's tasks in one dataflow launch) gives
     the same bits as one launch per phase, with one or two attention splits
-    per task, with counter and tagged hand-offs, over several steps with
+    per task, with counter, tagged and tagged-partial hand-offs, over several steps with
     ragged contexts, in graph replay and in direct launches; then again after
     the contexts jump past the task schedule's headroom (schedule rebuilt)."""
     layers = 3
@@ -740,7 +740,8 @@ def test_one_launch_step_equals_phase_launches(lib, syn, pkg, streams):
     xs = rng.standard_normal((4, streams, 512)).astype(np.float32)
     runs = []
     for flow, graph, rounds, handoff in ((0, 1, 0, -1), (2, 1, 1, 0), (2, 1, 2, 0),
-                                         (2, 0, 0, -1), (2, 1, 1, 1), (2, 0, 2, 1)):
+                                         (2, 0, 0, -1), (2, 1, 1, 1), (2, 0, 2, 1),
+                                         (2, 1, 1, 2), (2, 0, 2, 2)):
         print(f"one-launch vs phases: streams={streams} flow={flow} graph={graph} "
               f"rounds={rounds} handoff={handoff}", flush=True)
         bt = Batch(lib, w, layers, streams, max_pos, blocks)
@@ -843,7 +844,7 @@ def test_batch_reports_nonfinite_and_uncovered_positions(lib, syn, pkg):
 
 
 # ---------------------------------------------------------------- robustness
-@pytest.mark.parametrize("handoff", [0, 1])
+@pytest.mark.parametrize("handoff", [0, 1, 2])
 def test_forced_wait_timeout_reports_and_recovers(lib, syn, pkg, handoff):
     """The one-launch step's give-up path, forced from the host: with a 1 us
     wait limit its tasks stop waiting (counter waits, and with tagged
