@@ -536,41 +536,50 @@ __global__ __launch_bounds__(64 * kAttnWaves) void k_prefill_attention_rows(
 }
 
 // ---------------------------------------------------------------------------
-// Causal attention of a run of up to 64 consecutive positions of one stream
-// and one head on the fp32 matrix cores (v_mfma_f32_16x16x4_f32): wave w
-// takes queries 16w .. 16w+15 of the run. The run's keys go through LDS in
-// chunks of 64 (four pool blocks, K and V), each chunk loaded once by the
-// work-group and consumed by all four waves: per 16-key sub-block a wave
-// computes S^T = K Q^T (16 MFMAs over the 64 dimensions; lane l holds keys
+// Causal attention of a pair of runs (each up to 64 consecutive positions)
+// of one stream and one head on the fp32 matrix cores
+// (v_mfma_f32_16x16x4_f32): waves 0-3 take the first run, waves 4-7 the
+// second (none if its count is 0), wave 16w .. 16w+15 of its run's queries.
+// The host pairs a stream's run with the most keys with the one with the
+// fewest, so that every work-group does about the same work under the
+// causal mask. The pair's keys go through LDS in chunks of 64 (four pool
+// blocks, K and V), each chunk loaded once by the work-group and consumed
+// by every wave that needs it: per 16-key sub-block a wave computes
+// S^T = K Q^T (16 MFMAs over the 64 dimensions; lane l holds keys
 // 4(l/16) .. +3 of query l%16); then, once per chunk, an online softmax step
 // per query (the query's scores sit in the 4 lanes l%16 + 16g) and O^T +=
 // V^T P^T (16 MFMAs per sub-block: the P^T operand is the S^T registers
 // themselves). Products are exact fp32 multiplications; sums are in the
-// matrix cores' order.
+// matrix cores' order. A query's arithmetic does not depend on the run it
+// is paired with.
 constexpr int kMmaKeys = 64;                 // keys per LDS chunk
 constexpr int kMmaRow = kHeadDim + 4;        // padded LDS row (floats)
+constexpr int kPairThreads = 512;
 
-__global__ __launch_bounds__(256) void k_prefill_attention_mfma(
+__global__ __launch_bounds__(kPairThreads) void k_prefill_attention_mfma(
     const float *__restrict__ q, const float *__restrict__ kv, size_t layer_stride,
     unsigned blocks, int layer, const int32_t *__restrict__ tables, int table_stride,
-    const int32_t *__restrict__ positions, int streams, const int32_t *__restrict__ entries,
+    const int32_t *__restrict__ positions, int streams, const int32_t *__restrict__ pairs,
     uint16_t *__restrict__ out_split, int *status) {
     __shared__ float kt[kMmaKeys * kMmaRow];
     __shared__ float vt[kMmaKeys * kMmaRow];
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63, t = threadIdx.x;
-    const int head = blockIdx.y;
-    const int s0 = entries[2 * blockIdx.x], n = entries[2 * blockIdx.x + 1];
-    if (n < 1 || n > kQueries || s0 < 0 || s0 > streams - n) {
+    const int head = blockIdx.y, half = wave >> 2, hw = wave & 3;
+    const int s0a = pairs[4 * blockIdx.x], na = pairs[4 * blockIdx.x + 1];
+    const int s0b = pairs[4 * blockIdx.x + 2], nb = pairs[4 * blockIdx.x + 3];
+    if (na < 1 || na > kQueries || s0a < 0 || s0a > streams - na || nb < 0 || nb > kQueries ||
+        (nb > 0 && (s0b < 0 || s0b > streams - nb))) {
         if (t == 0) atomicOr(status, 2);
         return;  // uniform over the work-group
     }
-    const int32_t *table = tables + (size_t)s0 * table_stride;
+    // Both runs are positions of one stream: they share its block table.
+    const int32_t *table = tables + (size_t)s0a * table_stride;
     const float *layer_kv = kv + (size_t)layer * layer_stride;
     // Block-table entries go one chunk ahead of the K/V loads, and the first
-    // chunks' entries and K/V are requested before the run's position is
+    // chunks' entries and K/V are requested before the runs' positions are
     // known (every index stays inside the table and the pool; keys past the
-    // run's last position are zeroed when the chunk is stored in LDS).
+    // pair's last position are zeroed when the chunk is stored in LDS).
     constexpr int kChunkBlocks = kMmaKeys / kBlockPos;
     int ids[kChunkBlocks], next_ids[kChunkBlocks];
 #pragma unroll
@@ -578,29 +587,30 @@ __global__ __launch_bounds__(256) void k_prefill_attention_mfma(
         ids[b] = b < table_stride ? table[b] : 0;
         next_ids[b] = kChunkBlocks + b < table_stride ? table[kChunkBlocks + b] : 0;
     }
-    // Thread t moves float4 i of the chunk: pool block i / 2, element
-    // t + 256 (i % 2) of that block's (K | V) pair (K: elements 0 .. 255).
-    float4 pre[8];
+    // Thread t moves float4 t of each of the chunk's pool blocks' (K | V)
+    // pair (K: float4 0 .. 255, V: 256 .. 511).
+    float4 pre[kChunkBlocks];
 #define PGPU_FETCH_CHUNK()                                                                     \
     do {                                                                                       \
-        _Pragma("unroll") for (int i = 0; i < 8; i++) {                                        \
-            const int id_ = ids[i >> 1];                                                       \
+        _Pragma("unroll") for (int i = 0; i < kChunkBlocks; i++) {                             \
+            const int id_ = ids[i];                                                            \
             const int safe_ = (unsigned)id_ < blocks ? id_ : 0;                                \
-            pre[i] = ((const float4 *)(layer_kv + ((size_t)safe_ * kHeads + head) * 2048))     \
-                [t + 256 * (i & 1)];                                                           \
+            pre[i] = ((const float4 *)(layer_kv + ((size_t)safe_ * kHeads + head) * 2048))[t]; \
         }                                                                                      \
     } while (0)
     PGPU_FETCH_CHUNK();
-    const int p0 = positions[s0];
-    const int p_last = p0 + n - 1;
+    const int pa = positions[s0a], pb = nb > 0 ? positions[s0b] : 0;
+    const int p_last = max(pa + na - 1, nb > 0 ? pb + nb - 1 : -1);
     if (p_last / kBlockPos >= table_stride && t == 0) atomicOr(status, 2);
     const int key_end = min(p_last + 1, table_stride * kBlockPos);  // keys [0, key_end)
     const int chunks = (key_end + kMmaKeys - 1) / kMmaKeys;
     bool bad_block = false;
+    // This wave's run.
+    const int s0 = half ? s0b : s0a, n = half ? nb : na, p0 = half ? pb : pa;
 
     // This lane's query (column l%16 of the wave's 16) and its 16 dimensions
     // 16(l/16) .. +15: the B operand of S^T = K Q^T, one dimension per MFMA.
-    const int qi = wave * 16 + (lane & 15), g = lane >> 4;
+    const int qi = hw * 16 + (lane & 15), g = lane >> 4;
     const bool q_live = qi < n;
     const int qpos = p0 + qi;
     float qv[16];
@@ -616,8 +626,8 @@ __global__ __launch_bounds__(256) void k_prefill_attention_mfma(
             qv[4 * i + 3] = q_live ? v.w : 0.0f;
         }
     }
-    const int wave_last = p0 + min(n, wave * 16 + 16) - 1;  // this wave's last query position
-    const bool wave_live = wave * 16 < n;
+    const int wave_last = p0 + min(n, hw * 16 + 16) - 1;  // this wave's last query position
+    const bool wave_live = hw * 16 < n;
 
     float o[4][4];  // O^T: lane l holds dims 16 dt + 4 (l/16) + r of query l%16
 #pragma unroll
@@ -629,12 +639,11 @@ __global__ __launch_bounds__(256) void k_prefill_attention_mfma(
     for (int c = 0; c < chunks; c++) {
         __syncthreads();  // the previous chunk is consumed
 #pragma unroll
-        for (int i = 0; i < 8; i++) {
-            const int within = t + 256 * (i & 1);
-            const int key = (i >> 1) * kBlockPos + ((within & 255) >> 4), d = (within & 15) * 4;
+        for (int i = 0; i < kChunkBlocks; i++) {
+            const int key = i * kBlockPos + ((t & 255) >> 4), d = (t & 15) * 4;
             const bool live = c * kMmaKeys + key < key_end;
-            bad_block |= live && (unsigned)ids[i >> 1] >= blocks;
-            float *dst = (within < 256 ? kt : vt) + key * kMmaRow + d;
+            bad_block |= live && (unsigned)ids[i] >= blocks;
+            float *dst = (t < 256 ? kt : vt) + key * kMmaRow + d;
             *(float4 *)dst = live ? pre[i] : make_float4(0.f, 0.f, 0.f, 0.f);
         }
         __syncthreads();
@@ -911,15 +920,15 @@ extern "C" int pgpu_prefill_attention_rows(void *stream, const float *q, const p
 extern "C" int pgpu_prefill_attention_mfma(void *stream, const float *q, const pgpu_paged_kv *kv,
                                            int layer, const int32_t *tables, int table_stride,
                                            const int32_t *positions, int streams,
-                                           const int32_t *entries, int entry_count,
+                                           const int32_t *pairs, int pair_count,
                                            uint16_t *out_split, int *status) {
-    if (!q || !kv || !tables || !positions || !entries || !out_split || !status ||
+    if (!q || !kv || !tables || !positions || !pairs || !out_split || !status ||
         streams <= 0 || layer < 0 || layer >= kv->layers || table_stride <= 0 ||
-        entry_count <= 0 || entry_count > 65535)
+        pair_count <= 0 || pair_count > 65535)
         return bad_arguments("pgpu_prefill_attention_mfma");
-    hipLaunchKernelGGL(k_prefill_attention_mfma, dim3(entry_count, kHeads), dim3(256), 0,
+    hipLaunchKernelGGL(k_prefill_attention_mfma, dim3(pair_count, kHeads), dim3(kPairThreads), 0,
                        (hipStream_t)stream, q, kv->base, kv->layer_stride, (unsigned)kv->blocks,
-                       layer, tables, table_stride, positions, streams, entries, out_split,
+                       layer, tables, table_stride, positions, streams, pairs, out_split,
                        status);
     return launch_ok("pgpu_prefill_attention_mfma");
 }

@@ -52,6 +52,9 @@ struct PhononFlowBatch {
         int32_t *runs;              /* (dev) [runs_cap][2]: the run-based prefill attentions */
         int32_t *runs_host;
         size_t runs_count, runs_cap;
+        int32_t *pairs;             /* (dev) [pairs_cap][4]: runs paired per stream (mfma) */
+        int32_t *pairs_host;
+        size_t pairs_count, pairs_cap;
         uint16_t *split;            /* (dev) split fragments [max_streams/16][16][1536] */
     } pre;
     int flow;                       /* 1: one launch per step (pgpu_flow_launch) */
@@ -416,6 +419,8 @@ void phonon_flow_batch_destroy(PhononFlowBatch *b) {
     free(b->pre.host);
     pgpu_free(b->pre.runs);
     free(b->pre.runs_host);
+    pgpu_free(b->pre.pairs);
+    free(b->pre.pairs_host);
     pgpu_free(b->pre.split);
     free(b->host_positions);
     free(b->fl.host_schedule);
@@ -593,7 +598,7 @@ static int enqueue_prefill(PhononFlowBatch *b, void *stream, size_t first, size_
                                                 b->status)
                   : pgpu_prefill_attention_mfma(stream, b->q, &b->pool->kv, layer, b->tables,
                                                 (int)b->table_len, b->positions, n,
-                                                b->pre.runs, (int)b->pre.runs_count, xs,
+                                                b->pre.pairs, (int)b->pre.pairs_count, xs,
                                                 b->status)) ||
             !pgpu_prefill_gemm_residual(stream, &m->wide[l * 4 + 1], xs, n, terms, cur, b->r,
                                         b->status) ||
@@ -1007,6 +1012,75 @@ static int run_order(const void *x, const void *y) {
     return a->last < b->last ? 1 : (a->last > b->last ? -1 : (a->s0 > b->s0) - (a->s0 < b->s0));
 }
 
+/* Work list of pgpu_prefill_attention_mfma: a stream's runs paired so that
+ * its run with the most keys shares a work-group with the one with the
+ * fewest (the causal mask makes a run's work grow with its last position),
+ * then the pairs with the most keys first. A stream with an odd number of
+ * runs leaves its middle run unpaired. */
+typedef struct {
+    size_t keys;
+    int32_t s0, n, s1, n1;
+} PrefillPair;
+
+static int pair_order(const void *x, const void *y) {
+    const PrefillPair *a = x, *b = y;
+    return a->keys < b->keys ? 1 : (a->keys > b->keys ? -1 : (a->s0 > b->s0) - (a->s0 < b->s0));
+}
+
+static int prefill_pairs(PhononFlowBatch *b, size_t streams, const size_t *first,
+                         const size_t *counts) {
+    size_t n = 0;
+    for (size_t i = 0; i < streams; i++)
+        n += ((counts[i] + PH_PREFILL_RUN - 1) / PH_PREFILL_RUN + 1) / 2;
+    PrefillPair *list = malloc(n * sizeof(PrefillPair));
+    if (!list)
+        return 0;
+    size_t k = 0;
+    for (size_t i = 0, offset = 0; i < streams; offset += counts[i], i++) {
+        const size_t runs = (counts[i] + PH_PREFILL_RUN - 1) / PH_PREFILL_RUN; /* >= 1 */
+        for (size_t lo = 0, hi = runs - 1;; lo++, hi--) {
+            /* Run j: positions [64 j, min(64 (j + 1), count)) of the stream;
+             * a run paired as `lo` is never the stream's last, so it is full. */
+            const size_t q_hi = hi * PH_PREFILL_RUN, q_lo = lo * PH_PREFILL_RUN;
+            const size_t n_hi = counts[i] - q_hi < PH_PREFILL_RUN ? counts[i] - q_hi
+                                                                   : PH_PREFILL_RUN;
+            list[k] = (PrefillPair){first[i] + q_hi + n_hi, (int32_t)(offset + q_hi),
+                                    (int32_t)n_hi, 0, 0};
+            if (lo < hi) {
+                list[k].s1 = (int32_t)(offset + q_lo);
+                list[k].n1 = PH_PREFILL_RUN;
+                list[k].keys += first[i] + q_lo + PH_PREFILL_RUN;
+            }
+            k++;
+            if (lo + 1 >= hi)
+                break;
+        }
+    }
+    n = k;
+    qsort(list, n, sizeof(PrefillPair), pair_order);
+    if (n > b->pre.pairs_cap) {
+        int32_t *host = realloc(b->pre.pairs_host, n * 4 * sizeof(int32_t));
+        if (host)
+            b->pre.pairs_host = host;
+        pgpu_free(b->pre.pairs);
+        b->pre.pairs = host ? pgpu_malloc(n * 4 * sizeof(int32_t)) : NULL;
+        b->pre.pairs_cap = b->pre.pairs ? n : 0;
+        if (!b->pre.pairs) {
+            free(list);
+            return 0;
+        }
+    }
+    for (size_t j = 0; j < n; j++) {
+        b->pre.pairs_host[4 * j] = list[j].s0;
+        b->pre.pairs_host[4 * j + 1] = list[j].n;
+        b->pre.pairs_host[4 * j + 2] = list[j].s1;
+        b->pre.pairs_host[4 * j + 3] = list[j].n1;
+    }
+    free(list);
+    b->pre.pairs_count = n;
+    return pgpu_copy_h2d(b->stream, b->pre.pairs, b->pre.pairs_host, n * 4 * sizeof(int32_t));
+}
+
 static int prefill_runs(PhononFlowBatch *b, size_t streams, const size_t *first,
                         const size_t *counts) {
     size_t n = 0;
@@ -1041,7 +1115,8 @@ static int prefill_runs(PhononFlowBatch *b, size_t streams, const size_t *first,
     }
     free(list);
     b->pre.runs_count = n;
-    return pgpu_copy_h2d(b->stream, b->pre.runs, b->pre.runs_host, n * 2 * sizeof(int32_t));
+    return pgpu_copy_h2d(b->stream, b->pre.runs, b->pre.runs_host, n * 2 * sizeof(int32_t)) &&
+           prefill_pairs(b, streams, first, counts);
 }
 
 /* Pseudo-streams of a batched prefill: position first[i] + k (k < counts[i])
