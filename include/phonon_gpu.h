@@ -351,9 +351,10 @@ int pgpu_elu(void *stream, const float *x, float *y, size_t count);
  * prompt position); split fragments as in pgpu_gemm_input.split, with M
  * rounded up to 16 rows in the allocation. -- */
 /* LayerNorm of rows [M][512] (weight, bias, epsilon), into split fragments:
- * the decode step's LayerNorm prologue, the same bits. */
+ * the decode step's LayerNorm prologue, the same bits. Only the first
+ * `terms` (1..3) split terms of each value are written. */
 int pgpu_rows_split_ln(void *stream, const float *rows, const float *weight, const float *bias,
-                       float epsilon, int streams, uint16_t *out_split, int *status);
+                       float epsilon, int streams, int terms, uint16_t *out_split, int *status);
 /* The split partials of pgpu_attention / pgpu_prefill_attention merged into
  * split fragments with the out-projection prologue's arithmetic (the same
  * bits as a projection with an attn_acc input). */

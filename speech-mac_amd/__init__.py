@@ -248,7 +248,7 @@ EXPORTS = {
     "pgpu_gemm_qkv": (_i, [_vp, _mp, _gip, _i, _kvp, _i, _vp, _i, _vp, _vp, _vp, _vp]),
     "pgpu_attention": (_i, [_vp, _vp, _kvp, _i, _vp, _i, _vp, _i, _i, _i, _scp, _vp]),
     "pgpu_attention_merge": (_i, [_vp, _scp, _vp, _i, _i, _i, _vp, _vp, _vp]),
-    "pgpu_rows_split_ln": (_i, [_vp, _vp, _vp, _vp, ctypes.c_float, _i, _vp, _vp]),
+    "pgpu_rows_split_ln": (_i, [_vp, _vp, _vp, _vp, ctypes.c_float, _i, _i, _vp, _vp]),
     "pgpu_rows_split_attention": (_i, [_vp, _scp, _vp, _i, _i, _vp, _vp]),
     "pgpu_wide_from_matrix": (_i, [_vp, _mp, _vp, _vp]),
     "pgpu_prefill_gemm_qkv": (_i, [_vp, _vp, _vp, _i, _i, _kvp, _i, _vp, _i, _vp, _vp, _vp,

@@ -73,6 +73,60 @@ __global__ __launch_bounds__(kTaskThreads) void k_rows_split(GemmArgs a, uint16_
     }
 }
 
+// LayerNorm rows -> split fragments without the LDS operand buffer: 8 rows
+// per 256-thread work-group (wave w: rows 2w, 2w + 1), the decode
+// prologue's LayerNorm arithmetic (rows_ln_values: the same bits), and each
+// lane stores its 8 columns' split terms straight into their fragment
+// records (row n of tile st, columns [8j, 8j + 8): block j / 4, record
+// (j % 4) 16 + n). Only the first `terms` terms are written (the
+// projections of a two-term prefill never read the third). Rows past
+// `streams` up to the tile's end become zeros.
+constexpr int kLnRowsPerGroup = 8;
+__global__ __launch_bounds__(256) void k_rows_split_ln(const float *__restrict__ x,
+                                                       const float *__restrict__ lw,
+                                                       const float *__restrict__ lb, float eps,
+                                                       int streams, int terms, uint16_t *out,
+                                                       int *status) {
+    const int wave = threadIdx.x >> 6, j = threadIdx.x & 63;
+    Rows2 r;
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+        const int s = blockIdx.x * kLnRowsPerGroup + 2 * wave + i;
+        r.live[i] = s < streams;  // uniform per wave
+        if (r.live[i]) {
+            const float4 x0 = *(const float4 *)(x + (size_t)s * kWidth + j * 8);
+            const float4 x1 = *(const float4 *)(x + (size_t)s * kWidth + j * 8 + 4);
+            r.v[i][0] = x0.x; r.v[i][1] = x0.y; r.v[i][2] = x0.z; r.v[i][3] = x0.w;
+            r.v[i][4] = x1.x; r.v[i][5] = x1.y; r.v[i][6] = x1.z; r.v[i][7] = x1.w;
+        } else {
+#pragma unroll
+            for (int k = 0; k < 8; k++) r.v[i][k] = 0.0f;
+        }
+    }
+    const bool bad = rows_ln_values(r, lw, lb, eps);
+    flag_nonfinite(status, bad);
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+        const int s = blockIdx.x * kLnRowsPerGroup + 2 * wave + i;
+        const int st = s >> 4, n = s & 15, kb = j >> 2, g = j & 3;
+        uint16_t h[8], m[8], l[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++) split3(r.v[i][k], h[k], m[k], l[k]);
+        uint16_t *rec = out + ((size_t)st * (kWidth / 32) + kb) * 1536 + (g * 16 + n) * 8;
+#pragma unroll
+        for (int p = 0; p < 3; p++) {
+            if (p >= terms) break;
+            const uint16_t *src = p == 0 ? h : (p == 1 ? m : l);
+            uint4 q;
+            q.x = src[0] | (uint32_t)src[1] << 16;
+            q.y = src[2] | (uint32_t)src[3] << 16;
+            q.z = src[4] | (uint32_t)src[5] << 16;
+            q.w = src[6] | (uint32_t)src[7] << 16;
+            *(uint4 *)(rec + p * 512) = q;
+        }
+    }
+}
+
 // ---------------------------------------------------------------------------
 // Large-M projection. A work-group computes RT = WR RW row tiles x PT = WP PW
 // position tiles; wave (wr, wp) = (w / WP, w % WP) owns RW row tiles and PW
@@ -824,19 +878,15 @@ GemmArgs gemm_args(const pgpu_wide_matrix *w, const uint16_t *split, int streams
 using namespace pgpu;
 
 extern "C" int pgpu_rows_split_ln(void *stream, const float *rows, const float *weight,
-                                  const float *bias, float epsilon, int streams,
+                                  const float *bias, float epsilon, int streams, int terms,
                                   uint16_t *out_split, int *status) {
-    if (!rows || !weight || !bias || !out_split || !status || streams <= 0 || !(epsilon > 0.0f))
+    if (!rows || !weight || !bias || !out_split || !status || streams <= 0 ||
+        !(epsilon > 0.0f) || terms < 1 || terms > 3)
         return bad_arguments("pgpu_rows_split_ln");
-    GemmArgs a{};
-    a.ln_x = rows;
-    a.ln_w = weight;
-    a.ln_b = bias;
-    a.ln_eps = epsilon;
-    a.streams = streams;
-    a.status = status;
-    hipLaunchKernelGGL(k_rows_split<SRC_LN>, dim3((streams + 15) / 16), dim3(kTaskThreads), 0,
-                       (hipStream_t)stream, a, out_split);
+    // Whole 16-row tiles: the rows past `streams` are written as zeros.
+    const int groups = (streams + 15) / 16 * (16 / kLnRowsPerGroup);
+    hipLaunchKernelGGL(k_rows_split_ln, dim3(groups), dim3(256), 0, (hipStream_t)stream, rows,
+                       weight, bias, epsilon, streams, terms, out_split, status);
     return launch_ok("pgpu_rows_split_ln");
 }
 

@@ -579,7 +579,8 @@ static int enqueue_prefill(PhononFlowBatch *b, void *stream, size_t first, size_
         const float *norm = m->norms + l * 4 * PH_WIDTH;
         float *next = (l + 1 == first + count) ? output : b->x;
         const int layer = (int)(l + pool_offset);
-        if (!pgpu_rows_split_ln(stream, cur, norm, norm + PH_WIDTH, 1e-5f, n, xs, b->status) ||
+        if (!pgpu_rows_split_ln(stream, cur, norm, norm + PH_WIDTH, 1e-5f, n, terms, xs,
+                                b->status) ||
             !pgpu_prefill_gemm_qkv(stream, &m->wide[l * 4], xs, n, terms, &b->pool->kv, layer,
                                    b->tables,
                                    (int)b->table_len, b->positions, rope, b->q, b->status))
@@ -603,7 +604,7 @@ static int enqueue_prefill(PhononFlowBatch *b, void *stream, size_t first, size_
             !pgpu_prefill_gemm_residual(stream, &m->wide[l * 4 + 1], xs, n, terms, cur, b->r,
                                         b->status) ||
             !pgpu_rows_split_ln(stream, b->r, norm + 2 * PH_WIDTH, norm + 3 * PH_WIDTH, 1e-5f,
-                                n, xs, b->status) ||
+                                n, terms, xs, b->status) ||
             !pgpu_prefill_gemm_gelu_split(stream, &m->wide[l * 4 + 2], xs, n, terms, b->xh,
                                           b->status) ||
             !pgpu_prefill_gemm_residual(stream, &m->wide[l * 4 + 3], b->xh, n, terms, b->r,
