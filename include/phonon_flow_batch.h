@@ -151,8 +151,10 @@ int phonon_flow_batch_set_attention_rounds(PhononFlowBatch *batch, int rounds);
  * tagged words the consumer polls (one memory round trip less per hand-off,
  * for a few streams); 0 through counters and shared cacheable loads; 2 the
  * split partials as tagged words, the rest through counters (an attention
- * task then need not wait for its partial to reach memory); -1 (the
- * default) by the batch size. Results are identical for every choice. */
+ * task then need not wait for its partial to reach memory); 3 as 1, but
+ * the out-projection tasks merge the split partials themselves (no
+ * attention task waits to merge); -1 (the default) by the batch size.
+ * Results are identical for every choice. */
 int phonon_flow_batch_set_handoff(PhononFlowBatch *batch, int tagged);
 /* Kernel timing: while `before` and `after` are events (pgpu_event_create),
  * each step launches its kernels directly (no graph replay) and records

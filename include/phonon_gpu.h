@@ -178,6 +178,8 @@ int pgpu_q8_gemv(void *stream, const int8_t *values, const uint16_t *scales, int
 #define PGPU_FLOW_HANDOFF_COUNTER 0 /* pgpu_flow_step.tagged: counters and shared loads */
 #define PGPU_FLOW_HANDOFF_TAGGED 1  /* x, r, merged attention rows, split partials tagged */
 #define PGPU_FLOW_HANDOFF_PARTS 2   /* split partials tagged, the rest by counters */
+#define PGPU_FLOW_HANDOFF_MERGE_OUT 3 /* TAGGED, with no merging attention task: the out
+                                       projection merges the split partials itself */
 
 #define PGPU_FLOW_TASK(kind, layer, tile, index)                                      \
     ((uint32_t)(kind) | (uint32_t)(layer) << 3 | (uint32_t)(tile) << 9 |             \
@@ -219,13 +221,16 @@ typedef struct {
                                       over as tagged words in `rows` and `parts`
                                       (part_acc, part_ml and act's x, r and attention
                                       rows are then unused); PARTS: only the split
-                                      partials, in `parts` (part_acc, part_ml unused) */
-    uint64_t *rows;                /* (dev, TAGGED) [layer_count][3][tiles*16][512]: x, r,
+                                      partials, in `parts` (part_acc, part_ml unused);
+                                      MERGE_OUT: as TAGGED, but every attention task
+                                      only stores its partials and the out-projection
+                                      tasks merge them (no merged attention rows) */
+    uint64_t *rows;                /* (dev, TAGGED, MERGE_OUT) [layer_count][3][tiles*16][512]: x, r,
                                       merged attention */
-    uint64_t *parts;               /* (dev, TAGGED or PARTS) [layer_count][tiles*16][8]
+    uint64_t *parts;               /* (dev, all but COUNTER) [layer_count][tiles*16][8]
                                       [max_splits][PGPU_FLOW_PART_WORDS]: P.V [64], max,
                                       sum */
-    const uint32_t *epoch;         /* (dev, TAGGED or PARTS) this step's tag, never 0 */
+    const uint32_t *epoch;         /* (dev, all but COUNTER) this step's tag, never 0 */
 } pgpu_flow_step;
 
 /* Placement of each tile's projection chain in a task list, on a model

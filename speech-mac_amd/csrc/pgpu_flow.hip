@@ -200,49 +200,6 @@ __device__ inline FlowWait no_wait(const pgpu_flow_step &f) {
     return FlowWait{nullptr, 0u, f.status, 0u};
 }
 
-// Polls splits j0 .. nsplit-1 of one (stream, head) from its tagged partial
-// records (lanes 0..15 of the wave: dims [4 lane, 4 lane + 4)) and folds
-// them into the running merge in split order (merge_step: the arithmetic of
-// merge_splits). Every lane of the wave must call it.
-__device__ inline void merge_tagged_splits(const uint64_t *part, int j0, int nsplit, float &mx,
-                                           float &total, float *v, const TagPoll &tp) {
-    constexpr int G = 4;
-    const int lane = threadIdx.x & 63;
-    const bool mine = lane < 16;
-    const __amdgpu_buffer_rsrc_t r =
-        tag_rsrc(part, (uint32_t)(nsplit * PGPU_FLOW_PART_WORDS * 8));
-    for (int g0 = j0; g0 < nsplit; g0 += G) {
-        u32x4 acc[G][2], ml[G];
-        const uint64_t t0 = wall_clock64();
-        for (int round = 0;; round++) {
-            __asm__ volatile("" ::: "memory");
-            bool ok = true;
-#pragma unroll
-            for (int u = 0; u < G; u++) {
-                const int j = min(g0 + u, nsplit - 1);
-                const uint32_t rec = (uint32_t)(j * PGPU_FLOW_PART_WORDS * 8);
-                if (mine) {
-                    acc[u][0] = tag_load2(r, rec + lane * 32);
-                    acc[u][1] = tag_load2(r, rec + lane * 32 + 16);
-                    ml[u] = tag_load2(r, rec + 64 * 8);
-                    ok &= tag_ok2(acc[u][0], tp.tag) && tag_ok2(acc[u][1], tp.tag) &&
-                          tag_ok2(ml[u], tp.tag);
-                }
-            }
-            if (__all(ok)) break;
-            if (tag_give_up(tp, t0, round)) break;
-            __builtin_amdgcn_s_sleep(1);
-        }
-#pragma unroll
-        for (int u = 0; u < G; u++) {
-            if (g0 + u >= nsplit) break;
-            const float a4[4] = {bitsf(acc[u][0].x), bitsf(acc[u][0].z), bitsf(acc[u][1].x),
-                                 bitsf(acc[u][1].z)};
-            merge_step(mx, total, v, 4, bitsf(ml[u].x), bitsf(ml[u].z), a4);
-        }
-    }
-}
-
 // ATTN task: splits [unit, unit + 1) x f.attn_rounds of (stream t*16 + n,
 // head), one after the other. Each split's partial goes
 // to its slot of the (layer, stream, head) group; the task whose splits
@@ -362,9 +319,30 @@ __device__ inline void attention_task(const pgpu_flow_step &f, const pgpu_paged_
     float mm[kFlowRounds], ll[kFlowRounds];
     int count;
     const bool tagged_parts = f.tagged != PGPU_FLOW_HANDOFF_COUNTER;
-    const int state = attend_unit<kFlowRounds>(a, head, split0, s, wave, sh, true, aa, mm, ll,
-                                               count, ready, f.attn_rounds, !f.prefill,
-                                               tagged_parts ? 2 : 1);
+    const int state = attend_unit<kFlowRounds>(
+        a, head, split0, s, wave, sh, true, aa, mm, ll, count, ready, f.attn_rounds, !f.prefill,
+        tagged_parts && f.tagged != PGPU_FLOW_HANDOFF_MERGE_OUT ? 2 : 1);
+    if (f.tagged == PGPU_FLOW_HANDOFF_MERGE_OUT) {
+        // Every split's partial goes out as a tagged record; the tile's
+        // out-projection tasks poll and merge them.
+        if (wave != 0 || state != UNIT_LIVE) return;
+        const int lane = threadIdx.x & 63;
+        const size_t group = ((size_t)layer * f.tiles * 16 + s) * kHeads + head;
+        uint64_t *part = f.parts + group * f.max_splits * PGPU_FLOW_PART_WORDS;
+        const int nsplit = (count + kSplitKeys - 1) / kSplitKeys;
+#pragma unroll
+        for (int r = 0; r < kFlowRounds; r++) {
+            if (r >= f.attn_rounds || split0 + r >= nsplit) break;
+            uint64_t *rec = part + (size_t)(split0 + r) * PGPU_FLOW_PART_WORDS;
+            if (lane < 16) store_tagged4(rec + lane * 4, aa[r], tag);
+            if (lane == 0) {
+                store_tagged(rec + 64, mm[r], tag);
+                store_tagged(rec + 65, ll[r], tag);
+            }
+        }
+        trace_mark(f, 2);
+        return;
+    }
     if (wave > (tagged_parts ? 1 : 0) || state == UNIT_EMPTY ||
         (state == UNIT_UNCOVERED && split0 != 0))
         return;
@@ -439,7 +417,9 @@ __device__ inline void flow_step_task(const pgpu_flow_step &f, const pgpu_paged_
     const pgpu_flow_layer &ly = f.layers[layer];
     const float *norm = ly.norms;
     const int live = min(16, f.streams - tile * 16);
-    const bool tagged = f.tagged == PGPU_FLOW_HANDOFF_TAGGED, last = layer + 1 == f.layer_count;
+    const bool merge_out = f.tagged == PGPU_FLOW_HANDOFF_MERGE_OUT;
+    const bool tagged = f.tagged == PGPU_FLOW_HANDOFF_TAGGED || merge_out,
+               last = layer + 1 == f.layer_count;
     uint64_t *const ready_mark =
         tagged && f.trace ? f.trace + (size_t)blockIdx.x * 4 + 1 : nullptr;
     switch (kind) {
@@ -498,11 +478,27 @@ __device__ inline void flow_step_task(const pgpu_flow_step &f, const pgpu_paged_
             a.residual = layer == 0 ? f.input : nullptr;
             a.tres = layer == 0 ? nullptr : tagged_rows(f, layer - 1, ROWS_X);
             a.ready_mark = ready_mark;
-            gemm_wide_task<SRC_ROWS, EPI_RESIDUAL, Q8>(
-                a, index, tile, lds,
+            const FlowWait w =
                 f.prefill ? wait_for(f, layer, 0, PGPU_FLOW_QKV_ALL,
                                      (unsigned)(PGPU_FLOW_QKV_TASKS * f.tiles))
-                          : wait_for(f, layer, tile, PGPU_FLOW_QKV_HEAD + kHeads - 1, 3u));
+                          : wait_for(f, layer, tile, PGPU_FLOW_QKV_HEAD + kHeads - 1, 3u);
+            if (merge_out) {
+                // The split partials of the tile's streams, merged here.
+                a.tparts = f.parts + (size_t)layer * f.tiles * 16 * kHeads * f.max_splits *
+                                         PGPU_FLOW_PART_WORDS;
+                a.positions = f.positions;
+                a.max_splits = f.max_splits;
+                a.table_stride = f.table_stride;
+                gemm_wide_task<SRC_ATTN_TAGGED, EPI_RESIDUAL, Q8>(a, index, tile, lds, w);
+                // A count for the MLP-in tasks' first wait only (the r words
+                // carry their own tags): no drain.
+                __syncthreads();
+                if (threadIdx.x == 0)
+                    __hip_atomic_fetch_add(phase_counter(f, layer, tile, PGPU_FLOW_OUT), 1u,
+                                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            } else {
+                gemm_wide_task<SRC_ROWS, EPI_RESIDUAL, Q8>(a, index, tile, lds, w);
+            }
             trace_mark(f, 2);
         } else {
             a.ln_x = act_rows(f, layer, 3);
@@ -526,12 +522,15 @@ __device__ inline void flow_step_task(const pgpu_flow_step &f, const pgpu_paged_
         a.out_split = hidden_rows(f, layer);
         a.out_kb = kFfn / 32;
         if (tagged) {
-            // r, polled once every (stream, head) of the tile is merged.
+            // r, polled once every (stream, head) of the tile is merged
+            // (or, with the merge in the out projection, once its tasks
+            // have stored their rows).
             a.tx = tagged_rows(f, layer, ROWS_R);
             a.ready_mark = ready_mark;
             gemm_wide_task<SRC_LN, EPI_GELU_SPLIT, Q8>(
                 a, index, tile, lds,
-                wait_for(f, layer, tile, PGPU_FLOW_ATTN, (unsigned)(kHeads * live)));
+                merge_out ? wait_for(f, layer, tile, PGPU_FLOW_OUT, PGPU_FLOW_OUT_TASKS)
+                          : wait_for(f, layer, tile, PGPU_FLOW_ATTN, (unsigned)(kHeads * live)));
         } else {
             a.ln_x = act_rows(f, layer, 1);
             gemm_wide_task<SRC_LN, EPI_GELU_SPLIT, Q8>(
@@ -605,10 +604,11 @@ extern "C" int pgpu_flow_launch(void *stream, const pgpu_flow_step *step,
         !step->positions || step->table_stride <= 0 || !step->rope || !step->schedule ||
         !step->tasks || !step->phase || !step->split_done || !step->status ||
         step->attn_rounds < 1 || step->attn_rounds > PGPU_FLOW_ATTN_ROUNDS ||
-        step->tagged < PGPU_FLOW_HANDOFF_COUNTER || step->tagged > PGPU_FLOW_HANDOFF_PARTS ||
+        step->tagged < PGPU_FLOW_HANDOFF_COUNTER || step->tagged > PGPU_FLOW_HANDOFF_MERGE_OUT ||
         (step->tagged != PGPU_FLOW_HANDOFF_COUNTER &&
          (!step->parts || !step->epoch || step->max_splits > 32)) ||
-        (step->tagged == PGPU_FLOW_HANDOFF_TAGGED && !step->rows) ||
+        ((step->tagged == PGPU_FLOW_HANDOFF_TAGGED ||
+          step->tagged == PGPU_FLOW_HANDOFF_MERGE_OUT) && !step->rows) ||
         step->pool_offset < 0 || step->pool_offset + step->layer_count > kv->layers)
         return bad_arguments("pgpu_flow_launch");
     if (step->q8)

@@ -42,6 +42,7 @@
 #include <hip/hip_fp16.h>
 
 #include "pgpu_common.hpp"
+#include "phonon_gpu.h"
 
 namespace pgpu {
 
@@ -52,6 +53,7 @@ enum Source {
     SRC_ROWS = 3,
     SRC_LN_MOD = 4,
     SRC_SPLIT_LDS = 5,
+    SRC_ATTN_TAGGED = 6,  // merge of tagged split partials, polled (one-launch step)
 };
 enum Epilogue {
     EPI_STORE = 0,
@@ -198,6 +200,9 @@ struct GemmArgs {
     const uint64_t *tx, *tres;
     uint64_t *tout;
     TagPoll tp;
+    // SRC_ATTN_TAGGED: the layer's tagged split partials,
+    // [tiles*16][8][max_splits][PGPU_FLOW_PART_WORDS] (P.V [64], max, sum).
+    const uint64_t *tparts;
     uint64_t *ready_mark;
 };
 
@@ -572,6 +577,134 @@ __device__ inline bool merge_splits(const float *acc, const float *ml, int nspli
     return merge_finish<N>(total, v);
 }
 
+// Polls splits j0 .. nsplit-1 of one (stream, head) from its tagged partial
+// records (lanes 0..15 of the wave: dims [4 lane, 4 lane + 4)) and folds
+// them into the running merge in split order (merge_step: the arithmetic of
+// merge_splits). Every lane of the wave must call it.
+__device__ inline void merge_tagged_splits(const uint64_t *part, int j0, int nsplit, float &mx,
+                                           float &total, float *v, const TagPoll &tp) {
+    constexpr int G = 4;
+    const int lane = threadIdx.x & 63;
+    const bool mine = lane < 16;
+    const __amdgpu_buffer_rsrc_t r =
+        tag_rsrc(part, (uint32_t)(nsplit * PGPU_FLOW_PART_WORDS * 8));
+    for (int g0 = j0; g0 < nsplit; g0 += G) {
+        u32x4 acc[G][2], ml[G];
+        const uint64_t t0 = wall_clock64();
+        for (int round = 0;; round++) {
+            __asm__ volatile("" ::: "memory");
+            bool ok = true;
+#pragma unroll
+            for (int u = 0; u < G; u++) {
+                const int j = min(g0 + u, nsplit - 1);
+                const uint32_t rec = (uint32_t)(j * PGPU_FLOW_PART_WORDS * 8);
+                if (mine) {
+                    acc[u][0] = tag_load2(r, rec + lane * 32);
+                    acc[u][1] = tag_load2(r, rec + lane * 32 + 16);
+                    ml[u] = tag_load2(r, rec + 64 * 8);
+                    ok &= tag_ok2(acc[u][0], tp.tag) && tag_ok2(acc[u][1], tp.tag) &&
+                          tag_ok2(ml[u], tp.tag);
+                }
+            }
+            if (__all(ok)) break;
+            if (tag_give_up(tp, t0, round)) break;
+            __builtin_amdgcn_s_sleep(1);
+        }
+#pragma unroll
+        for (int u = 0; u < G; u++) {
+            if (g0 + u >= nsplit) break;
+            const float a4[4] = {bitsf(acc[u][0].x), bitsf(acc[u][0].z), bitsf(acc[u][1].x),
+                                 bitsf(acc[u][1].z)};
+            merge_step(mx, total, v, 4, bitsf(ml[u].x), bitsf(ml[u].z), a4);
+        }
+    }
+}
+
+// All splits of one (stream, head) from its tagged partial records, merged
+// in split order with one dimension per lane (lane l: dimension l): the
+// merge_step arithmetic, so dimension l gets the bits of merge_splits. Up
+// to 8 records are requested per poll round (each lane its P.V word of
+// each, lane u the record's max and sum, read back uniform), so a consumer
+// that polls before the partials land sees them one round trip after the
+// last one lands. Every lane of the wave must call it; returns true (and
+// v = 0) if the result is not finite.
+__device__ inline bool merge_tagged_dim(const uint64_t *part, int nsplit, const TagPoll &tp,
+                                        float &v) {
+    constexpr int G = 8;
+    typedef __attribute__((ext_vector_type(2))) uint32_t u32x2;
+    const int lane = threadIdx.x & 63;
+    const __amdgpu_buffer_rsrc_t r =
+        tag_rsrc(part, (uint32_t)(nsplit * PGPU_FLOW_PART_WORDS * 8));
+    float mx = -INFINITY, total = 0.0f;
+    v = 0.0f;
+    for (int g0 = 0; g0 < nsplit; g0 += G) {
+        u32x2 acc[G];
+        u32x4 ml;
+        const uint32_t own = (uint32_t)(min(g0 + (lane & (G - 1)), nsplit - 1) *
+                                        PGPU_FLOW_PART_WORDS * 8);
+        const uint64_t t0 = wall_clock64();
+        for (int round = 0;; round++) {
+            __asm__ volatile("" ::: "memory");
+            bool ok = true;
+#pragma unroll
+            for (int u = 0; u < G; u++) {
+                const uint32_t rec = (uint32_t)(min(g0 + u, nsplit - 1) * PGPU_FLOW_PART_WORDS * 8);
+                acc[u] = __builtin_amdgcn_raw_buffer_load_b64(r, rec + lane * 8, 0, 16);
+                ok &= acc[u].y == tp.tag;
+            }
+            ml = tag_load2(r, own + 64 * 8);
+            ok &= tag_ok2(ml, tp.tag);
+            if (__all(ok)) break;
+            if (tag_give_up(tp, t0, round)) break;
+            __builtin_amdgcn_s_sleep(1);
+        }
+#pragma unroll
+        for (int u = 0; u < G; u++) {
+            if (g0 + u >= nsplit) break;
+            const float m_j = bitsf(__builtin_amdgcn_readlane(ml.x, u));
+            const float l_j = bitsf(__builtin_amdgcn_readlane(ml.z, u));
+            const float a = bitsf(acc[u].x);
+            merge_step(mx, total, &v, 1, m_j, l_j, &a);
+        }
+    }
+    return merge_finish<1>(total, &v);
+}
+
+// The out projection's operand when it merges the attention splits itself
+// (one-launch step, PGPU_FLOW_HANDOFF_MERGE_OUT): wave w merges head w of
+// every live stream of tile st from the tagged partial records
+// (merge_tagged_dim: lane l, dimension l) and writes the head's 64 values
+// into the LDS operand buffer (column 64w + l: block 2w + l / 32, group
+// (l % 32) / 8, element l % 8). A context the attention units cannot cover
+// (they flag it and store nothing) and streams past the batch give zeros.
+// `position`: lane n < 16 holds the position of stream n of the tile (loaded
+// before the task's wait: positions are not written within the step).
+__device__ inline bool prologue_attn_tagged(const GemmArgs &a, int st, int position,
+                                            uint16_t *bsh) {
+    const int h = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int kb = 2 * h + (lane >> 5), g = (lane & 31) >> 3, e = lane & 7;
+    bool bad = false;
+#pragma unroll 1
+    for (int n = 0; n < 16; n++) {
+        const int s = st * 16 + n;
+        float v = 0.0f;
+        if (s < a.streams) {  // uniform
+            const int count = __builtin_amdgcn_readlane(position, n) + 1;
+            const int nsplit = (count + kSplitKeys - 1) / kSplitKeys;
+            if (count >= 1 && nsplit <= a.max_splits && count <= a.table_stride * kBlockPos)
+                bad |= merge_tagged_dim(
+                    a.tparts + ((size_t)s * kHeads + h) * a.max_splits * PGPU_FLOW_PART_WORDS,
+                    nsplit, a.tp, v);
+        }
+        uint16_t t[3];
+        split3(v, t[0], t[1], t[2]);
+        uint16_t *rec = bsh + kb * kLdsBlock + (g * 16 + n) * 8 + e;
+#pragma unroll
+        for (int p = 0; p < 3; p++) rec[p * 512] = t[p];
+    }
+    return bad;
+}
+
 // Merge of the split partials of 16 streams x 8 heads (layout of
 // pgpu_attention_scratch): wave w merges streams 2w, 2w+1; lane
 // (h = j/8, part = j%8) dims [8 part, 8 part + 8) of head h.
@@ -865,12 +998,17 @@ __device__ inline void gemm_wide_task(const GemmArgs &a, int bx, int st, uint16_
     if (active) load_weights(w, a, tile, kbn, lane, kb0, kb0 + KBW);
     EpiOperands e;
     if (active && half == 0) load_epilogue_static<EPI>(e, a, s, row0, live);
+    int position = 0;
+    if constexpr (SRC == SRC_ATTN_TAGGED)
+        if (lane < 16 && st * 16 + lane < a.streams) position = a.positions[st * 16 + lane];
     wait();
     if (active && half == 0) load_epilogue_dynamic<EPI>(e, a, st, s, row0, live);
 
     bool bad_in = false;
     if constexpr (SRC == SRC_ATTN) {
         bad_in = prologue_attn(a, st, bsh);
+    } else if constexpr (SRC == SRC_ATTN_TAGGED) {
+        bad_in = prologue_attn_tagged(a, st, position, bsh);
     } else if constexpr (SRC == SRC_SPLIT_LDS) {
         split_to_lds(a.xs, st, bsh);
     } else {

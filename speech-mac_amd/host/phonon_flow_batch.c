@@ -879,16 +879,20 @@ static int flow_prepare(PhononFlowBatch *b, int prefill) {
     return 1;
 }
 
-/* Whether a one-launch step hands x, r, the merged attention rows and the
- * split partials over as tagged words (pgpu_flow.hip): one memory round
- * trip less per hand-off, but every poll fetches from memory, which costs
- * more than the counter mode's shared loads once the tile holds more than
- * a few streams (measured on MI355X, us per 12-layer step, contexts
- * U{1..2048}, counter vs tagged: B = 1: 324 vs 291; B = 16: 482 vs 529). */
+/* How a one-launch step hands values between its tasks (pgpu_flow.hip).
+ * Tagged words save one memory round trip per hand-off, but every poll
+ * fetches from memory, which costs more than the counter mode's shared
+ * loads once the tile holds more than a few streams (measured on MI355X,
+ * us per 12-layer step, contexts U{1..2048}, counter vs tagged: B = 1: 324
+ * vs 291; B = 16: 482 vs 529). For those few streams, the out projection
+ * merges the split partials itself, which removes the merging attention
+ * task's hop (tagged vs merged in the out projection: B = 1: 319 vs 300;
+ * B = 2: 329 vs 315; B = 3: 327 vs 319; B = 4: 343 vs 342). */
 static int flow_tagged(const PhononFlowBatch *b) {
     if (b->fl.tagged_set >= 0)
         return b->fl.tagged_set;
-    return b->streams <= PH_FLOW_TAGGED_MAX_STREAMS;
+    return b->streams <= PH_FLOW_TAGGED_MAX_STREAMS ? PGPU_FLOW_HANDOFF_MERGE_OUT
+                                                    : PGPU_FLOW_HANDOFF_COUNTER;
 }
 
 /* One step as a single launch, then the launch that zeroes its counters and
@@ -1248,7 +1252,7 @@ int phonon_flow_batch_set_pipeline(PhononFlowBatch *b, int mode) {
 }
 
 int phonon_flow_batch_set_handoff(PhononFlowBatch *b, int tagged) {
-    if (!b || tagged < -1 || tagged > PGPU_FLOW_HANDOFF_PARTS)
+    if (!b || tagged < -1 || tagged > PGPU_FLOW_HANDOFF_MERGE_OUT)
         return 0;
     b->fl.tagged_set = tagged;
     return 1;

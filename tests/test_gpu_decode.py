@@ -724,7 +724,8 @@ def test_batched_prefill_equals_single_steps(lib, syn, pkg, mode, exact):
 def test_one_launch_step_equals_phase_launches(lib, syn, pkg, streams):
     """The one-launch step (every layer's tasks in one dataflow launch) gives
     the same bits as one launch per phase, with one or two attention splits
-    per task, with counter, tagged and tagged-partial hand-offs, over several steps with
+    per task, with counter, tagged and tagged-partial hand-offs and with the
+    split partials merged by the out projection, over several steps with
     ragged contexts, in graph replay and in direct launches; then again after
     the contexts jump past the task schedule's headroom (schedule rebuilt)."""
     layers = 3
@@ -741,7 +742,8 @@ def test_one_launch_step_equals_phase_launches(lib, syn, pkg, streams):
     runs = []
     for flow, graph, rounds, handoff in ((0, 1, 0, -1), (2, 1, 1, 0), (2, 1, 2, 0),
                                          (2, 0, 0, -1), (2, 1, 1, 1), (2, 0, 2, 1),
-                                         (2, 1, 1, 2), (2, 0, 2, 2)):
+                                         (2, 1, 1, 2), (2, 0, 2, 2), (2, 1, 1, 3),
+                                         (2, 0, 2, 3)):
         print(f"one-launch vs phases: streams={streams} flow={flow} graph={graph} "
               f"rounds={rounds} handoff={handoff}", flush=True)
         bt = Batch(lib, w, layers, streams, max_pos, blocks)
@@ -844,7 +846,7 @@ def test_batch_reports_nonfinite_and_uncovered_positions(lib, syn, pkg):
 
 
 # ---------------------------------------------------------------- robustness
-@pytest.mark.parametrize("handoff", [0, 1, 2])
+@pytest.mark.parametrize("handoff", [0, 1, 2, 3])
 def test_forced_wait_timeout_reports_and_recovers(lib, syn, pkg, handoff):
     """The one-launch step's give-up path, forced from the host: with a 1 us
     wait limit its tasks stop waiting (counter waits, and with tagged
