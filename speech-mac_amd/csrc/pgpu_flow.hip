@@ -490,12 +490,6 @@ __device__ inline void flow_step_task(const pgpu_flow_step &f, const pgpu_paged_
                 a.max_splits = f.max_splits;
                 a.table_stride = f.table_stride;
                 gemm_wide_task<SRC_ATTN_TAGGED, EPI_RESIDUAL, Q8>(a, index, tile, lds, w);
-                // A count for the MLP-in tasks' first wait only (the r words
-                // carry their own tags): no drain.
-                __syncthreads();
-                if (threadIdx.x == 0)
-                    __hip_atomic_fetch_add(phase_counter(f, layer, tile, PGPU_FLOW_OUT), 1u,
-                                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             } else {
                 gemm_wide_task<SRC_ROWS, EPI_RESIDUAL, Q8>(a, index, tile, lds, w);
             }
@@ -523,13 +517,13 @@ __device__ inline void flow_step_task(const pgpu_flow_step &f, const pgpu_paged_
         a.out_kb = kFfn / 32;
         if (tagged) {
             // r, polled once every (stream, head) of the tile is merged
-            // (or, with the merge in the out projection, once its tasks
-            // have stored their rows).
+            // (with the merge in the out projection: once the tile's QKV
+            // tasks are done, as the out projection itself).
             a.tx = tagged_rows(f, layer, ROWS_R);
             a.ready_mark = ready_mark;
             gemm_wide_task<SRC_LN, EPI_GELU_SPLIT, Q8>(
                 a, index, tile, lds,
-                merge_out ? wait_for(f, layer, tile, PGPU_FLOW_OUT, PGPU_FLOW_OUT_TASKS)
+                merge_out ? wait_for(f, layer, tile, PGPU_FLOW_QKV_HEAD + kHeads - 1, 3u)
                           : wait_for(f, layer, tile, PGPU_FLOW_ATTN, (unsigned)(kHeads * live)));
         } else {
             a.ln_x = act_rows(f, layer, 1);
