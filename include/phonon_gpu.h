@@ -393,6 +393,10 @@ int pgpu_prefill_gemm_residual(void *stream, const pgpu_wide_matrix *w, const ui
                                int *status);
 int pgpu_prefill_gemm_gelu_split(void *stream, const pgpu_wide_matrix *w, const uint16_t *split,
                                  int streams, int terms, uint16_t *out_split, int *status);
+/* (The GELU outputs are written as `terms` split terms: the MLP-out
+ * projection reads as many. Likewise `terms` of the attention entry points
+ * below, 2 or 3: the split terms of the attention rows written for the out
+ * projection.) */
 /* Causal attention of a batched prefill, one lane per query, into split
  * fragments of the attention rows (fp32 arithmetic in its own summation
  * order). `runs` (dev) holds run_count pairs (s0, n): pseudo-streams
@@ -405,7 +409,7 @@ int pgpu_prefill_gemm_gelu_split(void *stream, const pgpu_wide_matrix *w, const 
 int pgpu_prefill_attention_rows(void *stream, const float *q, const pgpu_paged_kv *kv,
                                 int layer, const int32_t *tables, int table_stride,
                                 const int32_t *positions, int streams, const int32_t *runs,
-                                int run_count, uint16_t *out_split, int *status);
+                                int run_count, uint16_t *out_split, int terms, int *status);
 /* The same contract on the fp32 matrix cores (v_mfma_f32_16x16x4_f32), over
  * pairs of runs: `pairs` holds (s0, n, s0', n') per pair, two runs of ONE
  * stream (their pseudo-streams share its block-table row; n' = 0: no second
@@ -418,7 +422,7 @@ int pgpu_prefill_attention_rows(void *stream, const float *q, const pgpu_paged_k
 int pgpu_prefill_attention_mfma(void *stream, const float *q, const pgpu_paged_kv *kv,
                                 int layer, const int32_t *tables, int table_stride,
                                 const int32_t *positions, int streams, const int32_t *pairs,
-                                int pair_count, uint16_t *out_split, int *status);
+                                int pair_count, uint16_t *out_split, int terms, int *status);
 /* pgpu_attention followed by pgpu_attention_merge (the same kernels, the
  * same bits), with the split partials in a fixed device-resident array of
  * PGPU_ATTENTION_STATIC_SLOTS (stream, head, split) slots (4.3 MB, held by

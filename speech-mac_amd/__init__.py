@@ -256,9 +256,9 @@ EXPORTS = {
     "pgpu_prefill_gemm_residual": (_i, [_vp, _vp, _vp, _i, _i, _vp, _vp, _vp]),
     "pgpu_prefill_gemm_gelu_split": (_i, [_vp, _vp, _vp, _i, _i, _vp, _vp]),
     "pgpu_prefill_attention_rows": (_i, [_vp, _vp, _kvp, _i, _vp, _i, _vp, _i, _vp, _i, _vp,
-                                         _vp]),
+                                         _i, _vp]),
     "pgpu_prefill_attention_mfma": (_i, [_vp, _vp, _kvp, _i, _vp, _i, _vp, _i, _vp, _i, _vp,
-                                         _vp]),
+                                         _i, _vp]),
     "phonon_flow_batch_set_prefill_exact": (_i, [_vp, _i]),
     "phonon_flow_batch_set_wait_limit": (_i, [_vp, ctypes.c_uint]),
     "pgpu_prefill_attention": (_i, [_vp, _vp, _kvp, _i, _vp, _i, _vp, _i, _i, _i, _vp, _i,

@@ -174,6 +174,7 @@ struct GemmArgs {
     const float *residual;    // RESIDUAL: [streams][ld_out]
     uint16_t *out_split;      // GELU_SPLIT: split fragments with out_kb blocks per row
     int out_kb;
+    int out_terms;            // GELU_SPLIT: split terms written (0: all three)
     float *q_out;             // QKV: [streams][512]
     float *kv;                // QKV: paged pool base
     size_t layer_stride;      // floats per layer of the pool
@@ -246,8 +247,10 @@ __device__ inline void store_out(float *p, float4 v, bool wt) {
 
 // 4 consecutive activations of stream s from column k (k % 4 == 0) as
 // split fragments: three 8-byte stores.
+// Only the first `terms` split terms are written (a consumer that reads two
+// terms never reads the third).
 __device__ inline void store_split4(uint16_t *__restrict__ xs, int s, int k, int kb_count,
-                                    const float *v, bool wt) {
+                                    const float *v, bool wt, int terms = 3) {
     uint16_t h[4], m[4], l[4];
 #pragma unroll
     for (int i = 0; i < 4; i++) split3(v[i], h[i], m[i], l[i]);
@@ -256,8 +259,9 @@ __device__ inline void store_split4(uint16_t *__restrict__ xs, int s, int k, int
               make_uint2(h[0] | (uint32_t)h[1] << 16, h[2] | (uint32_t)h[3] << 16), wt);
     store_out((uint2 *)(xs + base + 512),
               make_uint2(m[0] | (uint32_t)m[1] << 16, m[2] | (uint32_t)m[3] << 16), wt);
-    store_out((uint2 *)(xs + base + 1024),
-              make_uint2(l[0] | (uint32_t)l[1] << 16, l[2] | (uint32_t)l[3] << 16), wt);
+    if (terms > 2)
+        store_out((uint2 *)(xs + base + 1024),
+                  make_uint2(l[0] | (uint32_t)l[1] << 16, l[2] | (uint32_t)l[3] << 16), wt);
 }
 
 // ---------------------------------------------------------------------------
@@ -898,7 +902,7 @@ __device__ inline bool epilogue(const GemmArgs &a, const EpiOperands &e, const f
                 g[r] = gelu_erf(v[r]);
                 bad |= !isfinite(g[r]);
             }
-            store_split4(a.out_split, s, row0, a.out_kb, g, wt);
+            store_split4(a.out_split, s, row0, a.out_kb, g, wt, a.out_terms ? a.out_terms : 3);
         }
     } else if constexpr (EPI == EPI_SILU_SPLIT) {
         if (live) {

@@ -425,7 +425,7 @@ __global__ __launch_bounds__(64 * kAttnWaves) void k_prefill_attention_rows(
     const float *__restrict__ q, const float *__restrict__ kv, size_t layer_stride,
     unsigned blocks, int layer, const int32_t *__restrict__ tables, int table_stride,
     const int32_t *__restrict__ positions, int streams, const int32_t *__restrict__ entries,
-    uint16_t *__restrict__ out_split, int *status) {
+    uint16_t *__restrict__ out_split, int terms, int *status) {
     __shared__ float4 lds4[kAttnLds / 4];
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
@@ -584,7 +584,7 @@ __global__ __launch_bounds__(64 * kAttnWaves) void k_prefill_attention_rows(
             v[i] = ok ? acc[d + i] * inv : 0.0f;
             bad |= !isfinite(v[i]);
         }
-        store_split4(out_split, s0 + lane, head * kHeadDim + d, kWidth / 32, v, false);
+        store_split4(out_split, s0 + lane, head * kHeadDim + d, kWidth / 32, v, false, terms);
     }
     flag_nonfinite(status, bad);
 }
@@ -614,7 +614,7 @@ __global__ __launch_bounds__(kPairThreads) void k_prefill_attention_mfma(
     const float *__restrict__ q, const float *__restrict__ kv, size_t layer_stride,
     unsigned blocks, int layer, const int32_t *__restrict__ tables, int table_stride,
     const int32_t *__restrict__ positions, int streams, const int32_t *__restrict__ pairs,
-    uint16_t *__restrict__ out_split, int *status) {
+    uint16_t *__restrict__ out_split, int terms, int *status) {
     __shared__ float kt[kMmaKeys * kMmaRow];
     __shared__ float vt[kMmaKeys * kMmaRow];
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -811,7 +811,8 @@ __global__ __launch_bounds__(kPairThreads) void k_prefill_attention_mfma(
             v[r] = ok ? o[dt][r] * inv : 0.0f;
             bad |= !isfinite(v[r]);
         }
-        store_split4(out_split, s0 + qi, head * kHeadDim + 16 * dt + 4 * g, kWidth / 32, v, false);
+        store_split4(out_split, s0 + qi, head * kHeadDim + 16 * dt + 4 * g, kWidth / 32, v, false,
+                     terms);
     }
     flag_nonfinite(status, bad);
 }
@@ -948,6 +949,7 @@ extern "C" int pgpu_prefill_gemm_gelu_split(void *stream, const pgpu_wide_matrix
     GemmArgs a = gemm_args(w, split, streams, terms, status);
     a.out_split = out_split;
     a.out_kb = (int)w->rows / 32;
+    a.out_terms = terms;  // the MLP-out projection reads as many terms
     return run_gemm<EPI_GELU_SPLIT>(a, w, (hipStream_t)stream);
 }
 
@@ -955,15 +957,15 @@ extern "C" int pgpu_prefill_attention_rows(void *stream, const float *q, const p
                                            int layer, const int32_t *tables, int table_stride,
                                            const int32_t *positions, int streams,
                                            const int32_t *entries, int entry_count,
-                                           uint16_t *out_split, int *status) {
+                                           uint16_t *out_split, int terms, int *status) {
     if (!q || !kv || !tables || !positions || !entries || !out_split || !status ||
         streams <= 0 || layer < 0 || layer >= kv->layers || table_stride <= 0 ||
-        entry_count <= 0 || entry_count > 65535)
+        entry_count <= 0 || entry_count > 65535 || terms < 2 || terms > 3)
         return bad_arguments("pgpu_prefill_attention_rows");
     hipLaunchKernelGGL(k_prefill_attention_rows, dim3(entry_count, kHeads),
                        dim3(64 * kAttnWaves), 0, (hipStream_t)stream, q, kv->base,
                        kv->layer_stride, (unsigned)kv->blocks, layer, tables, table_stride,
-                       positions, streams, entries, out_split, status);
+                       positions, streams, entries, out_split, terms, status);
     return launch_ok("pgpu_prefill_attention_rows");
 }
 
@@ -971,15 +973,15 @@ extern "C" int pgpu_prefill_attention_mfma(void *stream, const float *q, const p
                                            int layer, const int32_t *tables, int table_stride,
                                            const int32_t *positions, int streams,
                                            const int32_t *pairs, int pair_count,
-                                           uint16_t *out_split, int *status) {
+                                           uint16_t *out_split, int terms, int *status) {
     if (!q || !kv || !tables || !positions || !pairs || !out_split || !status ||
         streams <= 0 || layer < 0 || layer >= kv->layers || table_stride <= 0 ||
-        pair_count <= 0 || pair_count > 65535)
+        pair_count <= 0 || pair_count > 65535 || terms < 2 || terms > 3)
         return bad_arguments("pgpu_prefill_attention_mfma");
     hipLaunchKernelGGL(k_prefill_attention_mfma, dim3(pair_count, kHeads), dim3(kPairThreads), 0,
                        (hipStream_t)stream, q, kv->base, kv->layer_stride, (unsigned)kv->blocks,
                        layer, tables, table_stride, positions, streams, pairs, out_split,
-                       status);
+                       terms, status);
     return launch_ok("pgpu_prefill_attention_mfma");
 }
 

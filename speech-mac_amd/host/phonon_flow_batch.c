@@ -596,11 +596,11 @@ static int enqueue_prefill(PhononFlowBatch *b, void *stream, size_t first, size_
                   ? pgpu_prefill_attention_rows(stream, b->q, &b->pool->kv, layer, b->tables,
                                                 (int)b->table_len, b->positions, n,
                                                 b->pre.runs, (int)b->pre.runs_count, xs,
-                                                b->status)
+                                                terms, b->status)
                   : pgpu_prefill_attention_mfma(stream, b->q, &b->pool->kv, layer, b->tables,
                                                 (int)b->table_len, b->positions, n,
                                                 b->pre.pairs, (int)b->pre.pairs_count, xs,
-                                                b->status)) ||
+                                                terms, b->status)) ||
             !pgpu_prefill_gemm_residual(stream, &m->wide[l * 4 + 1], xs, n, terms, cur, b->r,
                                         b->status) ||
             !pgpu_rows_split_ln(stream, b->r, norm + 2 * PH_WIDTH, norm + 3 * PH_WIDTH, 1e-5f,
