@@ -79,6 +79,12 @@ void pgpu_free(void *ptr);
 int pgpu_memset(void *stream, void *dst, int value, size_t bytes);
 /* Host copies complete before returning. */
 int pgpu_copy_h2d(void *stream, void *dst, const void *src, size_t bytes);
+/* Pinned host memory (hipHostMalloc), and a host-to-device copy that only
+ * enqueues: `src` must be pinned and stay unchanged until the stream has
+ * passed the copy. */
+void *pgpu_host_malloc(size_t bytes);
+void pgpu_host_free(void *ptr);
+int pgpu_copy_h2d_async(void *stream, void *dst, const void *src, size_t bytes);
 int pgpu_copy_d2h(void *stream, void *dst, const void *src, size_t bytes);
 int pgpu_copy_d2d(void *stream, void *dst, const void *src, size_t bytes);
 int pgpu_stream_create(void **stream);

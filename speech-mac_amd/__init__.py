@@ -227,6 +227,9 @@ EXPORTS = {
     "pgpu_free": (None, [_vp]),
     "pgpu_memset": (_i, [_vp, _vp, _i, _sz]),
     "pgpu_copy_h2d": (_i, [_vp, _vp, _vp, _sz]),
+    "pgpu_host_malloc": (_vp, [_sz]),
+    "pgpu_host_free": (None, [_vp]),
+    "pgpu_copy_h2d_async": (_i, [_vp, _vp, _vp, _sz]),
     "pgpu_copy_d2h": (_i, [_vp, _vp, _vp, _sz]),
     "pgpu_copy_d2d": (_i, [_vp, _vp, _vp, _sz]),
     "pgpu_stream_create": (_i, [_pp]),

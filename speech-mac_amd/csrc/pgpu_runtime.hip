@@ -82,6 +82,23 @@ extern "C" int pgpu_copy_h2d(void *stream, void *dst, const void *src, size_t by
            check(hipStreamSynchronize((hipStream_t)stream), "hipStreamSynchronize");
 }
 
+extern "C" void *pgpu_host_malloc(size_t bytes) {
+    void *p = NULL;
+    if (!bytes) bytes = 1;
+    if (!check(hipHostMalloc(&p, bytes, hipHostMallocDefault), "hipHostMalloc")) return NULL;
+    return p;
+}
+
+extern "C" void pgpu_host_free(void *ptr) {
+    if (ptr) (void)hipHostFree(ptr);
+}
+
+extern "C" int pgpu_copy_h2d_async(void *stream, void *dst, const void *src, size_t bytes) {
+    if (!bytes) return 1;
+    return check(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, (hipStream_t)stream),
+                 "hipMemcpyAsync H2D");
+}
+
 extern "C" int pgpu_copy_d2h(void *stream, void *dst, const void *src, size_t bytes) {
     if (!bytes) return 1;
     return check(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, (hipStream_t)stream),

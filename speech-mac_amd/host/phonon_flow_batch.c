@@ -56,6 +56,8 @@ struct PhononFlowBatch {
         int32_t *pairs_host;
         size_t pairs_count, pairs_cap;
         uint16_t *split;            /* (dev) split fragments [max_streams/16][16][1536] */
+        unsigned char *stage;       /* pinned host staging of a prefill call's uploads */
+        size_t stage_cap, stage_used;
     } pre;
     int flow;                       /* 1: one launch per step (pgpu_flow_launch) */
     struct {
@@ -417,6 +419,7 @@ void phonon_flow_batch_destroy(PhononFlowBatch *b) {
     pgpu_stream_destroy(b->stream);
     pgpu_free(b->pre.entries);
     free(b->pre.host);
+    pgpu_host_free(b->pre.stage);
     pgpu_free(b->pre.runs);
     free(b->pre.runs_host);
     pgpu_free(b->pre.pairs);
@@ -971,6 +974,38 @@ static size_t entry_list(size_t streams, const size_t *first, const size_t *coun
     return n;
 }
 
+/* A prefill call's small uploads (block tables, positions, work lists) go
+ * through one pinned staging area as asynchronous copies on the batch's
+ * stream: no host round trip per upload. stage_begin runs after the stream
+ * was synchronized, so no copy of an earlier call still reads the area. */
+static int stage_begin(PhononFlowBatch *b, size_t bytes) {
+    if (bytes > b->pre.stage_cap) {
+        pgpu_host_free(b->pre.stage);
+        b->pre.stage = pgpu_host_malloc(bytes);
+        b->pre.stage_cap = b->pre.stage ? bytes : 0;
+        if (!b->pre.stage)
+            return 0;
+    }
+    b->pre.stage_used = 0;
+    return 1;
+}
+
+static int stage_upload(PhononFlowBatch *b, void *dst, const void *src, size_t bytes) {
+    const size_t at = (b->pre.stage_used + 255) & ~(size_t)255;
+    if (at > b->pre.stage_cap || bytes > b->pre.stage_cap - at)
+        return ph_fail("prefill: staging area too small");
+    memcpy(b->pre.stage + at, src, bytes);
+    b->pre.stage_used = at + bytes;
+    return pgpu_copy_h2d_async(b->stream, dst, b->pre.stage + at, bytes);
+}
+
+/* Staging bytes of a prefill of `total` positions: positions and table map,
+ * the three attention work lists at their 65535-entry limits, and `extra`. */
+static size_t stage_bytes(size_t total, size_t extra) {
+    return extra + 2 * total * sizeof(int32_t) + 65535 * (4 + 2 + 4) * sizeof(int32_t) +
+           8 * 256;
+}
+
 /* The prefill attention's work list, uploaded: positions per entry halved
  * from PH_PREFILL_RUN while the list would give fewer than
  * PH_PREFILL_MIN_GROUPS work-groups (8 per entry), so a short prompt still
@@ -999,7 +1034,7 @@ static int prefill_entries(PhononFlowBatch *b, size_t streams, const size_t *fir
     if (entry_list(streams, first, counts, run, b->pre.host, b->pre.cap) != n)
         return 0;
     b->pre.count = n;
-    return pgpu_copy_h2d(b->stream, b->pre.entries, b->pre.host, n * 4 * sizeof(int32_t));
+    return stage_upload(b, b->pre.entries, b->pre.host, n * 4 * sizeof(int32_t));
 }
 
 /* Work list of the run-based prefill attentions (pgpu_prefill_attention_mfma
@@ -1083,7 +1118,7 @@ static int prefill_pairs(PhononFlowBatch *b, size_t streams, const size_t *first
     }
     free(list);
     b->pre.pairs_count = n;
-    return pgpu_copy_h2d(b->stream, b->pre.pairs, b->pre.pairs_host, n * 4 * sizeof(int32_t));
+    return stage_upload(b, b->pre.pairs, b->pre.pairs_host, n * 4 * sizeof(int32_t));
 }
 
 static int prefill_runs(PhononFlowBatch *b, size_t streams, const size_t *first,
@@ -1120,7 +1155,7 @@ static int prefill_runs(PhononFlowBatch *b, size_t streams, const size_t *first,
     }
     free(list);
     b->pre.runs_count = n;
-    return pgpu_copy_h2d(b->stream, b->pre.runs, b->pre.runs_host, n * 2 * sizeof(int32_t)) &&
+    return stage_upload(b, b->pre.runs, b->pre.runs_host, n * 2 * sizeof(int32_t)) &&
            prefill_pairs(b, streams, first, counts);
 }
 
@@ -1130,8 +1165,8 @@ static int prefill_runs(PhononFlowBatch *b, size_t streams, const size_t *first,
  * through all layers at once: each layer's projection appends the K/V of all
  * of them before its attention runs, and position p attends p + 1 keys, so
  * the pass is causal and computes what `counts` consecutive steps would. */
-int ph_batch_set_prefill(PhononFlowBatch *b, size_t streams, const size_t *first,
-                         const size_t *counts, const int32_t *tables_dev) {
+static size_t prefill_total(const PhononFlowBatch *b, size_t streams, const size_t *first,
+                            const size_t *counts) {
     size_t total = 0;
     for (size_t i = 0; i < streams; i++) {
         if (!counts[i] || first[i] >= b->max_positions ||
@@ -1139,6 +1174,14 @@ int ph_batch_set_prefill(PhononFlowBatch *b, size_t streams, const size_t *first
             return 0;
         total += counts[i];
     }
+    return total;
+}
+
+/* ph_batch_set_prefill after the stream was synchronized and the staging
+ * area begun (it holds stage_bytes(total, 0) more). */
+static int set_prefill(PhononFlowBatch *b, size_t streams, const size_t *first,
+                       const size_t *counts, const int32_t *tables_dev) {
+    const size_t total = prefill_total(b, streams, first, counts);
     if (!total)
         return 0;
     if (!b->table_map && !(b->table_map = pgpu_malloc(b->max_streams * sizeof(int32_t))))
@@ -1155,9 +1198,8 @@ int ph_batch_set_prefill(PhononFlowBatch *b, size_t streams, const size_t *first
             map[p] = (int32_t)i;
             b->host_positions[p] = first[i] + k;
         }
-    ok = ok && pgpu_stream_sync(b->stream) &&
-         pgpu_copy_h2d(b->stream, b->positions, pos32, total * sizeof(int32_t)) &&
-         pgpu_copy_h2d(b->stream, b->table_map, map, total * sizeof(int32_t)) &&
+    ok = ok && stage_upload(b, b->positions, pos32, total * sizeof(int32_t)) &&
+         stage_upload(b, b->table_map, map, total * sizeof(int32_t)) &&
          pgpu_gather_rows(b->stream, b->tables, tables_dev, b->table_map, (int)total,
                           (int)b->table_len) &&
          prefill_entries(b, streams, first, counts) && prefill_runs(b, streams, first, counts);
@@ -1170,6 +1212,13 @@ int ph_batch_set_prefill(PhononFlowBatch *b, size_t streams, const size_t *first
     return ok;
 }
 
+int ph_batch_set_prefill(PhononFlowBatch *b, size_t streams, const size_t *first,
+                         const size_t *counts, const int32_t *tables_dev) {
+    const size_t total = prefill_total(b, streams, first, counts);
+    return total && pgpu_stream_sync(b->stream) && stage_begin(b, stage_bytes(total, 0)) &&
+           set_prefill(b, streams, first, counts, tables_dev);
+}
+
 int phonon_flow_batch_prefill_device(PhononFlowBatch *b, size_t streams, const size_t *first,
                                      const size_t *counts, const int32_t *tables,
                                      size_t table_len, const float *inputs, float theta,
@@ -1180,9 +1229,12 @@ int phonon_flow_batch_prefill_device(PhononFlowBatch *b, size_t streams, const s
     if (!b->table_src &&
         !(b->table_src = pgpu_malloc(b->max_streams * b->table_len * sizeof(int32_t))))
         return 0;
-    if (!pgpu_stream_sync(b->stream) ||
-        !pgpu_copy_h2d(b->stream, b->table_src, tables, streams * table_len * sizeof(int32_t)) ||
-        !ph_batch_set_prefill(b, streams, first, counts, b->table_src))
+    const size_t total = prefill_total(b, streams, first, counts),
+                 table_bytes = streams * table_len * sizeof(int32_t);
+    if (!total || !pgpu_stream_sync(b->stream) ||
+        !stage_begin(b, stage_bytes(total, table_bytes)) ||
+        !stage_upload(b, b->table_src, tables, table_bytes) ||
+        !set_prefill(b, streams, first, counts, b->table_src))
         return 0;
     if (flow_usable(b, 1))
         return flow_prepare(b, 1) && enqueue_flow(b, inputs, outputs, theta);
