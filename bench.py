@@ -284,7 +284,7 @@ def flow_roofline(pkg, lib, d, steps=20):
             "traffic_source": f"{FLOW_PMC_SUMMARY} (FETCH_SIZE/WRITE_SIZE, copy-calibrated): "
                               f"{measured[0]} B for {measured[1]} B algorithmic"
                               if measured else None,
-            "kernel": "pgpu::k_flow_step<true>", "us_per_launch": round(us, 2),
+            "kernel": "pgpu::k_flow_step<true, false>", "us_per_launch": round(us, 2),
             "launches": steps, "algorithmic_bytes_per_launch": int(per_launch),
             "algorithmic_bytes": "Q8 weights of 12 layers once + K/V of every attended key "
                                  "per layer + the appended K/V row per stream per layer",
@@ -455,7 +455,45 @@ def large_batch_with_prefill(pkg, lib, seed, layers=12, streams=256, new_streams
             "clean": clean}
 
 
-def b1_with_prefill(pkg, lib, layers, seed, prompt=256, frames=750, warmup=10, mode=None):
+def task_trace_summary(sched, trace):
+    """Per-phase timing of one traced one-launch step (phonon_flow_batch_set_trace:
+    start, inputs ready and end of every task on the 100 MHz constant clock),
+    averaged over the layers past the first: for each phase, when its first
+    task saw its inputs, when its last task ended, the median task body
+    (inputs ready -> end) and the gap from the previous phase's last end to
+    this phase's first inputs-ready (microseconds)."""
+    names = ["QKV", "ATTN", "OUT", "MLP_IN", "MLP_OUT"]
+    kind, layer = sched & 7, (sched >> 3) & 63
+    tr = trace.astype(np.int64)
+    done = (tr[:, 0] > 0) & (tr[:, 2] > 0)
+    t0 = tr[done, 0].min()
+    ready, end = (tr[:, 1] - t0) / 100.0, (tr[:, 2] - t0) / 100.0
+    layers = int(layer[done].max()) + 1
+    rows = {n: {"body_us": [], "gap_us": [], "span_us": []} for n in names}
+    per_layer = []
+    prev_end = None
+    for l in range(layers):
+        for k, n in enumerate(names):
+            m = done & (layer == l) & (kind == k)
+            if not m.any():
+                continue
+            r0, e1 = float(ready[m].min()), float(end[m].max())
+            if l > 0:
+                rows[n]["body_us"].append(float(np.median(end[m] - ready[m])))
+                rows[n]["span_us"].append(e1 - r0)
+                if prev_end is not None:
+                    rows[n]["gap_us"].append(r0 - prev_end)
+            prev_end = e1
+        per_layer.append(prev_end)
+    out = {n: {key: round(float(np.mean(v)), 2) for key, v in d.items() if v}
+           for n, d in rows.items()}
+    out["us_per_layer"] = round((per_layer[-1] - per_layer[0]) / (layers - 1), 2)
+    out["step_span_us"] = round(float(end[done].max()), 1)
+    return out
+
+
+def b1_with_prefill(pkg, lib, layers, seed, prompt=256, frames=750, warmup=10, mode=None,
+                    trace_steps=0):
     """B=1: one stream, `layers` layers. A `prompt`-position prefill (the
     batched causal prefill, positions 0..prompt-1 through every layer in one
     pass), then `frames` decode steps, each step's output fed back as the
@@ -511,6 +549,28 @@ def b1_with_prefill(pkg, lib, layers, seed, prompt=256, frames=750, warmup=10, m
     clean = bool(lib.phonon_flow_batch_sync(batch))
     pre_ms, dec_ms = run(frames)
     clean = clean and bool(lib.phonon_flow_batch_sync(batch))
+    traced = None
+    if trace_steps:
+        # One more traced step at the end of the run (context prompt + frames).
+        ntask = lib.phonon_flow_batch_schedule(batch, None, 0)
+        sched = np.zeros(ntask, np.uint32)
+        lib.phonon_flow_batch_schedule(batch, sched.ctypes.data_as(ctypes.POINTER(ctypes.c_uint32)),
+                                       ntask)
+        buf = pkg.DeviceBuffer(lib, ntask * 4 * 8)
+        assert lib.phonon_flow_batch_set_trace(batch, buf.ptr, ntask)
+        summaries = []
+        for _ in range(trace_steps):
+            assert lib.phonon_flow_batch_step_device(batch, din, 10000.0, dout)
+            din, dout = dout, din
+            assert lib.pgpu_stream_sync(stream)
+            tr = np.zeros((ntask, 4), np.uint64)
+            assert lib.pgpu_copy_d2h(stream, tr.ctypes.data, buf.ptr, tr.nbytes)
+            assert lib.pgpu_stream_sync(stream)
+            summaries.append(task_trace_summary(sched, tr))
+        assert lib.phonon_flow_batch_set_trace(batch, None, 0)
+        buf.free()
+        traced = {"context": prompt + frames + 1, "tasks": int(ntask), "steps": summaries}
+        clean = clean and bool(lib.phonon_flow_batch_sync(batch))
     pin.free()
     pout.free()
     lib.phonon_flow_batch_destroy(batch)
@@ -527,7 +587,7 @@ def b1_with_prefill(pkg, lib, layers, seed, prompt=256, frames=750, warmup=10, m
                         f"{prompt + frames}), each output fed back as the next input; "
                         + ("the library's default step mode" if mode is None
                            else f"step pipeline mode {mode}"),
-            "clean": clean}
+            "clean": clean, **({"task_trace": traced} if traced else {})}
 
 
 def q8_matvec_bench(pkg, lib, seed=1, calls=2000):
@@ -1053,6 +1113,9 @@ def main():
     ap.add_argument("--pmc-program", action="store_true",
                     help="run only the attention kernel and a calibration copy, for "
                          "rocprofv3 --pmc passes")
+    ap.add_argument("--b1-trace", action="store_true",
+                    help="run only the B=1 prefill + decode workload, then trace three "
+                         "one-launch steps task by task and print each phase's timing")
     ap.add_argument("--b1-modes", type=str, default="",
                     help="run only the B=1 prefill + decode workload, once per listed step "
                          "pipeline mode (comma-separated, e.g. 0,2)")
@@ -1075,6 +1138,10 @@ def main():
         for kind in (0, 2):
             print(json.dumps(large_batch_with_prefill(pkg, lib, args.seed,
                                                       prefill_attention=kind)), flush=True)
+        return
+    if args.b1_trace:
+        print(json.dumps(b1_with_prefill(pkg, lib, args.layers, args.seed, trace_steps=3)),
+              flush=True)
         return
     if args.b1_modes:
         for mode in (int(m) for m in args.b1_modes.split(",")):

@@ -288,6 +288,7 @@ __device__ inline void tagged_attention_tail(const pgpu_flow_step &f, int layer,
     trace_mark(f, 2);
 }
 
+template <bool MO>
 __device__ inline void attention_task(const pgpu_flow_step &f, const pgpu_paged_kv &kv,
                                       int layer, int tile, int index, AttnShared *sh,
                                       uint32_t tag) {
@@ -321,8 +322,8 @@ __device__ inline void attention_task(const pgpu_flow_step &f, const pgpu_paged_
     const bool tagged_parts = f.tagged != PGPU_FLOW_HANDOFF_COUNTER;
     const int state = attend_unit<kFlowRounds>(
         a, head, split0, s, wave, sh, true, aa, mm, ll, count, ready, f.attn_rounds, !f.prefill,
-        tagged_parts && f.tagged != PGPU_FLOW_HANDOFF_MERGE_OUT ? 2 : 1);
-    if (f.tagged == PGPU_FLOW_HANDOFF_MERGE_OUT) {
+        tagged_parts && !MO ? 2 : 1);
+    if constexpr (MO) {
         // Every split's partial goes out as a tagged record; the tile's
         // out-projection tasks poll and merge them.
         if (wave != 0 || state != UNIT_LIVE) return;
@@ -404,7 +405,9 @@ __device__ inline void attention_task(const pgpu_flow_step &f, const pgpu_paged_
     trace_mark(f, 2);
 }
 
-template <bool Q8>
+// MO: the launch runs in PGPU_FLOW_HANDOFF_MERGE_OUT mode (a kernel of its
+// own, so that the other modes' code carries none of its registers).
+template <bool Q8, bool MO>
 __device__ inline void flow_step_task(const pgpu_flow_step &f, const pgpu_paged_kv &kv,
                                       uint4 *lds4) {
     uint16_t *lds = (uint16_t *)lds4;
@@ -417,8 +420,8 @@ __device__ inline void flow_step_task(const pgpu_flow_step &f, const pgpu_paged_
     const pgpu_flow_layer &ly = f.layers[layer];
     const float *norm = ly.norms;
     const int live = min(16, f.streams - tile * 16);
-    const bool merge_out = f.tagged == PGPU_FLOW_HANDOFF_MERGE_OUT;
-    const bool tagged = f.tagged == PGPU_FLOW_HANDOFF_TAGGED || merge_out,
+    constexpr bool merge_out = MO;
+    const bool tagged = MO || f.tagged == PGPU_FLOW_HANDOFF_TAGGED,
                last = layer + 1 == f.layer_count;
     uint64_t *const ready_mark =
         tagged && f.trace ? f.trace + (size_t)blockIdx.x * 4 + 1 : nullptr;
@@ -463,7 +466,7 @@ __device__ inline void flow_step_task(const pgpu_flow_step &f, const pgpu_paged_
         break;
     }
     case PGPU_FLOW_ATTN:
-        attention_task(f, kv, layer, tile, index, (AttnShared *)lds4, tag);
+        attention_task<MO>(f, kv, layer, tile, index, (AttnShared *)lds4, tag);
         break;
     case PGPU_FLOW_OUT: {
         GemmArgs a = base_args(f, ly, 1, tag);
@@ -482,7 +485,7 @@ __device__ inline void flow_step_task(const pgpu_flow_step &f, const pgpu_paged_
                 f.prefill ? wait_for(f, layer, 0, PGPU_FLOW_QKV_ALL,
                                      (unsigned)(PGPU_FLOW_QKV_TASKS * f.tiles))
                           : wait_for(f, layer, tile, PGPU_FLOW_QKV_HEAD + kHeads - 1, 3u);
-            if (merge_out) {
+            if constexpr (merge_out) {
                 // The split partials of the tile's streams, merged here.
                 a.tparts = f.parts + (size_t)layer * f.tiles * 16 * kHeads * f.max_splits *
                                          PGPU_FLOW_PART_WORDS;
@@ -566,10 +569,10 @@ __device__ inline void flow_step_task(const pgpu_flow_step &f, const pgpu_paged_
 
 // Two 512-thread work-groups per CU: the projection tasks' registers and
 // 49 KB of LDS (the prologue's operand buffer) set the occupancy.
-template <bool Q8>
+template <bool Q8, bool MO>
 __global__ __launch_bounds__(kTaskThreads) void k_flow_step(pgpu_flow_step f, pgpu_paged_kv kv) {
     __shared__ uint4 lds4[kTaskLds / 8];
-    flow_step_task<Q8>(f, kv, lds4);
+    flow_step_task<Q8, MO>(f, kv, lds4);
 }
 
 __global__ void k_flow_finish(unsigned *counters, size_t n, int32_t *positions, int streams,
@@ -605,12 +608,11 @@ extern "C" int pgpu_flow_launch(void *stream, const pgpu_flow_step *step,
           step->tagged == PGPU_FLOW_HANDOFF_MERGE_OUT) && !step->rows) ||
         step->pool_offset < 0 || step->pool_offset + step->layer_count > kv->layers)
         return bad_arguments("pgpu_flow_launch");
-    if (step->q8)
-        hipLaunchKernelGGL(k_flow_step<true>, dim3(step->tasks), dim3(kTaskThreads), 0,
-                           (hipStream_t)stream, *step, *kv);
-    else
-        hipLaunchKernelGGL(k_flow_step<false>, dim3(step->tasks), dim3(kTaskThreads), 0,
-                           (hipStream_t)stream, *step, *kv);
+    const bool mo = step->tagged == PGPU_FLOW_HANDOFF_MERGE_OUT;
+    auto kernel = step->q8 ? (mo ? k_flow_step<true, true> : k_flow_step<true, false>)
+                           : (mo ? k_flow_step<false, true> : k_flow_step<false, false>);
+    hipLaunchKernelGGL(kernel, dim3(step->tasks), dim3(kTaskThreads), 0, (hipStream_t)stream,
+                       *step, *kv);
     return launch_ok("pgpu_flow_launch");
 }
 
