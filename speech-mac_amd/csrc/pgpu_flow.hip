@@ -288,7 +288,7 @@ __device__ inline void tagged_attention_tail(const pgpu_flow_step &f, int layer,
     trace_mark(f, 2);
 }
 
-template <bool MO>
+template <int MODE>
 __device__ inline void attention_task(const pgpu_flow_step &f, const pgpu_paged_kv &kv,
                                       int layer, int tile, int index, AttnShared *sh,
                                       uint32_t tag) {
@@ -319,7 +319,8 @@ __device__ inline void attention_task(const pgpu_flow_step &f, const pgpu_paged_
     float4 aa[kFlowRounds];
     float mm[kFlowRounds], ll[kFlowRounds];
     int count;
-    const bool tagged_parts = f.tagged != PGPU_FLOW_HANDOFF_COUNTER;
+    constexpr bool tagged_parts = MODE != PGPU_FLOW_HANDOFF_COUNTER;
+    constexpr bool MO = MODE == PGPU_FLOW_HANDOFF_MERGE_OUT;
     const int state = attend_unit<kFlowRounds>(
         a, head, split0, s, wave, sh, true, aa, mm, ll, count, ready, f.attn_rounds, !f.prefill,
         tagged_parts && !MO ? 2 : 1);
@@ -353,9 +354,9 @@ __device__ inline void attention_task(const pgpu_flow_step &f, const pgpu_paged_
 
     const int lane = threadIdx.x & 63, d = (lane & 15) * 4;
     const size_t group = ((size_t)layer * f.tiles * 16 + s) * kHeads + head;
-    if (tagged_parts) {
+    if constexpr (tagged_parts) {
         tagged_attention_tail(f, layer, tile, s, head, split0, nsplit, rounds, covered, aa, mm,
-                              ll, group, tag, f.tagged == PGPU_FLOW_HANDOFF_TAGGED, wave);
+                              ll, group, tag, MODE == PGPU_FLOW_HANDOFF_TAGGED, wave);
         return;
     }
     float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -405,24 +406,24 @@ __device__ inline void attention_task(const pgpu_flow_step &f, const pgpu_paged_
     trace_mark(f, 2);
 }
 
-// MO: the launch runs in PGPU_FLOW_HANDOFF_MERGE_OUT mode (a kernel of its
-// own, so that the other modes' code carries none of its registers).
-template <bool Q8, bool MO>
+// MODE: the launch's hand-off mode (PGPU_FLOW_HANDOFF_*, f.tagged), one
+// kernel per mode, so that no mode's code carries another's registers.
+template <bool Q8, int MODE>
 __device__ inline void flow_step_task(const pgpu_flow_step &f, const pgpu_paged_kv &kv,
                                       uint4 *lds4) {
     uint16_t *lds = (uint16_t *)lds4;
     trace_mark(f, 0);
     const uint32_t desc = f.schedule[blockIdx.x];
     // written by the previous launch only
-    const uint32_t tag = f.tagged != PGPU_FLOW_HANDOFF_COUNTER ? *f.epoch : 0u;
+    const uint32_t tag = MODE != PGPU_FLOW_HANDOFF_COUNTER ? *f.epoch : 0u;
     const int kind = desc & 7, layer = (desc >> 3) & 63, tile = (desc >> 9) & 255,
               index = desc >> 17;
     const pgpu_flow_layer &ly = f.layers[layer];
     const float *norm = ly.norms;
     const int live = min(16, f.streams - tile * 16);
-    constexpr bool merge_out = MO;
-    const bool tagged = MO || f.tagged == PGPU_FLOW_HANDOFF_TAGGED,
-               last = layer + 1 == f.layer_count;
+    constexpr bool merge_out = MODE == PGPU_FLOW_HANDOFF_MERGE_OUT;
+    constexpr bool tagged = merge_out || MODE == PGPU_FLOW_HANDOFF_TAGGED;
+    const bool last = layer + 1 == f.layer_count;
     uint64_t *const ready_mark =
         tagged && f.trace ? f.trace + (size_t)blockIdx.x * 4 + 1 : nullptr;
     switch (kind) {
@@ -442,7 +443,7 @@ __device__ inline void flow_step_task(const pgpu_flow_step &f, const pgpu_paged_
         a.table_stride = f.table_stride;
         a.positions = f.positions;
         a.rope = (const float2 *)f.rope;
-        if (tagged) {
+        if constexpr (tagged) {
             // The previous layer's output, polled once its MLP-in tasks are
             // done (the phase before its producers).
             a.ln_x = layer == 0 ? f.input : nullptr;
@@ -466,14 +467,14 @@ __device__ inline void flow_step_task(const pgpu_flow_step &f, const pgpu_paged_
         break;
     }
     case PGPU_FLOW_ATTN:
-        attention_task<MO>(f, kv, layer, tile, index, (AttnShared *)lds4, tag);
+        attention_task<MODE>(f, kv, layer, tile, index, (AttnShared *)lds4, tag);
         break;
     case PGPU_FLOW_OUT: {
         GemmArgs a = base_args(f, ly, 1, tag);
         a.n_rows = kWidth;
         a.k_cols = kWidth;
         a.ld_out = kWidth;
-        if (tagged) {
+        if constexpr (tagged) {
             // Merged attention rows, polled once the tile's QKV tasks are
             // done (head 7's are listed last).
             a.tx = tagged_rows(f, layer, ROWS_ATTN);
@@ -518,7 +519,7 @@ __device__ inline void flow_step_task(const pgpu_flow_step &f, const pgpu_paged_
         a.k_cols = kWidth;
         a.out_split = hidden_rows(f, layer);
         a.out_kb = kFfn / 32;
-        if (tagged) {
+        if constexpr (tagged) {
             // r, polled once every (stream, head) of the tile is merged
             // (with the merge in the out projection: once the tile's QKV
             // tasks are done, as the out projection itself).
@@ -543,7 +544,7 @@ __device__ inline void flow_step_task(const pgpu_flow_step &f, const pgpu_paged_
         a.n_rows = kWidth;
         a.k_cols = kFfn;
         a.ld_out = kWidth;
-        if (tagged) {
+        if constexpr (tagged) {
             // The last layer's output is the step's (plain rows, read after
             // the launch); the others go out as tagged rows.
             a.out = last ? f.output : nullptr;
@@ -556,7 +557,7 @@ __device__ inline void flow_step_task(const pgpu_flow_step &f, const pgpu_paged_
         gemm_split_task<EPI_RESIDUAL, Q8>(
             a, index, tile, lds,
             TracedWait{wait_for(f, layer, tile, PGPU_FLOW_MLP_IN, PGPU_FLOW_MLP_IN_TASKS), &f});
-        if (tagged)
+        if constexpr (tagged)
             trace_mark(f, 2);
         else
             flow_signal(f, phase_counter(f, layer, tile, PGPU_FLOW_MLP_OUT));
@@ -569,10 +570,19 @@ __device__ inline void flow_step_task(const pgpu_flow_step &f, const pgpu_paged_
 
 // Two 512-thread work-groups per CU: the projection tasks' registers and
 // 49 KB of LDS (the prologue's operand buffer) set the occupancy.
-template <bool Q8, bool MO>
+template <bool Q8, int MODE>
 __global__ __launch_bounds__(kTaskThreads) void k_flow_step(pgpu_flow_step f, pgpu_paged_kv kv) {
     __shared__ uint4 lds4[kTaskLds / 8];
-    flow_step_task<Q8, MO>(f, kv, lds4);
+    flow_step_task<Q8, MODE>(f, kv, lds4);
+}
+
+template <bool Q8>
+void launch_step(const pgpu_flow_step *step, const pgpu_paged_kv *kv, hipStream_t stream) {
+    auto kernel = step->tagged == PGPU_FLOW_HANDOFF_TAGGED      ? k_flow_step<Q8, 1>
+                  : step->tagged == PGPU_FLOW_HANDOFF_PARTS     ? k_flow_step<Q8, 2>
+                  : step->tagged == PGPU_FLOW_HANDOFF_MERGE_OUT ? k_flow_step<Q8, 3>
+                                                                : k_flow_step<Q8, 0>;
+    hipLaunchKernelGGL(kernel, dim3(step->tasks), dim3(kTaskThreads), 0, stream, *step, *kv);
 }
 
 __global__ void k_flow_finish(unsigned *counters, size_t n, int32_t *positions, int streams,
@@ -608,11 +618,10 @@ extern "C" int pgpu_flow_launch(void *stream, const pgpu_flow_step *step,
           step->tagged == PGPU_FLOW_HANDOFF_MERGE_OUT) && !step->rows) ||
         step->pool_offset < 0 || step->pool_offset + step->layer_count > kv->layers)
         return bad_arguments("pgpu_flow_launch");
-    const bool mo = step->tagged == PGPU_FLOW_HANDOFF_MERGE_OUT;
-    auto kernel = step->q8 ? (mo ? k_flow_step<true, true> : k_flow_step<true, false>)
-                           : (mo ? k_flow_step<false, true> : k_flow_step<false, false>);
-    hipLaunchKernelGGL(kernel, dim3(step->tasks), dim3(kTaskThreads), 0, (hipStream_t)stream,
-                       *step, *kv);
+    if (step->q8)
+        launch_step<true>(step, kv, (hipStream_t)stream);
+    else
+        launch_step<false>(step, kv, (hipStream_t)stream);
     return launch_ok("pgpu_flow_launch");
 }
 
