@@ -231,8 +231,8 @@ typedef struct {
                                       MERGE_OUT: as TAGGED, but every attention task
                                       only stores its partials and the out-projection
                                       tasks merge them (no merged attention rows) */
-    uint64_t *rows;                /* (dev, TAGGED, MERGE_OUT) [layer_count][3][tiles*16][512]: x, r,
-                                      merged attention */
+    uint64_t *rows;                /* (dev, TAGGED, MERGE_OUT) [layer_count][6][tiles*16][512]: x, r,
+                                      merged attention, and (MERGE_OUT) q, k, v */
     uint64_t *parts;               /* (dev, all but COUNTER) [layer_count][tiles*16][8]
                                       [max_splits][PGPU_FLOW_PART_WORDS]: P.V [64], max,
                                       sum */

@@ -3,6 +3,8 @@
 // the pool layout and the work decomposition.
 #pragma once
 
+#include <type_traits>
+
 #include "pgpu_common.hpp"
 
 namespace pgpu {
@@ -58,6 +60,16 @@ struct NoGate {
     __device__ unsigned probe() const { return 0u; }
     __device__ void pass(unsigned, bool) const {}
 };
+
+// A gate with `kTaggedQkv` (true) hands the unit this step's q and the
+// appended key's K and V itself (poll_qkv, after pass): the unit then
+// requests every block, the context's last one included, before the gate,
+// and replaces the appended key's slot with the handed-over K and V.
+template <class G, class = void>
+struct GateTaggedQkv : std::false_type {};
+template <class G>
+struct GateTaggedQkv<G, std::void_t<decltype(G::kTaggedQkv)>>
+    : std::integral_constant<bool, G::kTaggedQkv> {};
 
 // Splits split0 .. split0 + ROUNDS - 1 of head `head` of stream `s`, one
 // after the other, by the unit's 8 waves (`wave` = 0..7 within the unit).
@@ -137,16 +149,37 @@ __device__ inline int attend_unit(const AttnArgs &a, int head, int split0, int s
             }
         }
     };
-    if (live && early) {
-        load(0, false, 0);
-        load(0, true, 0);
+    constexpr bool TQ = GateTaggedQkv<Gate>::value;
+    if (live && (early || TQ)) {
+        load(0, false, TQ ? 2 : 0);
+        load(0, true, TQ ? 2 : 0);
     }
     gate.pass(probe, live);
 
     if (live) {
-        load(0, false, early ? 1 : 2);
-        load(0, true, early ? 1 : 2);
-        const float4 q = *(const float4 *)(a.q + (size_t)s * kWidth + head * kHeadDim + dcol * 4);
+        float4 q, knew = {}, vnew = {};
+        // The appended key (index count - 1): its block, and its slot there
+        // (float4 kk / 4 of the lanes of key row kk % 4).
+        const int cur_block = (count - 1) >> 4, kk = (count - 1) & 15;
+        auto patch = [&](int r, float4(&regs)[kBlocksPerWave][4], const float4 &v) {
+#pragma unroll
+            for (int t = 0; t < kBlocksPerWave; t++)
+                if ((split0 + r) * 16 + wave * kBlocksPerWave + t == cur_block &&
+                    krow == (kk & 3)) {
+#pragma unroll
+                    for (int i = 0; i < 4; i++)
+                        if (i == (kk >> 2)) regs[t][i] = v;
+                }
+        };
+        if constexpr (TQ) {
+            gate.poll_qkv(s, head, dcol, q, knew, vnew);
+            patch(0, kr, knew);
+            patch(0, vr, vnew);
+        } else {
+            load(0, false, early ? 1 : 2);
+            load(0, true, early ? 1 : 2);
+            q = *(const float4 *)(a.q + (size_t)s * kWidth + head * kHeadDim + dcol * 4);
+        }
 #pragma unroll
         for (int r = 0; r < ROUNDS; r++) {
             if (r >= rounds || (split0 + r) * kSplitKeys >= count) break;  // uniform
@@ -169,7 +202,10 @@ __device__ inline int attend_unit(const AttnArgs &a, int head, int split0, int s
                     score[t][i] = key < count ? d : -INFINITY;
                     m = fmaxf(m, score[t][i]);
                 }
-            if (next) load(r + 1, false, 2);
+            if (next) {
+                load(r + 1, false, 2);
+                if constexpr (TQ) patch(r + 1, kr, knew);
+            }
             m = xor16_32_max(m);
 #pragma unroll
             for (int t = 0; t < kBlocksPerWave; t++)
@@ -186,7 +222,10 @@ __device__ inline int attend_unit(const AttnArgs &a, int head, int split0, int s
                     acc.z = fmaf(e, vr[t][i].z, acc.z);
                     acc.w = fmaf(e, vr[t][i].w, acc.w);
                 }
-            if (next) load(r + 1, true, 2);
+            if (next) {
+                load(r + 1, true, 2);
+                if constexpr (TQ) patch(r + 1, vr, vnew);
+            }
             // Lanes of one key row hold the same l; sum the four rows.
             l = xor16_32_sum(l);
             acc.x = xor16_32_sum(acc.x);

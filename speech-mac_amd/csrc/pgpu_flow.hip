@@ -177,10 +177,49 @@ __device__ inline uint16_t *hidden_rows(const pgpu_flow_step &f, int layer) {
 
 // Tagged mode: per-layer rows [tiles*16][512] of tagged words: 0 = layer
 // output x, 1 = r, 2 = merged attention output.
-enum { ROWS_X = 0, ROWS_R = 1, ROWS_ATTN = 2 };
+// Merge-in-out mode adds 3 = q (scaled), 4 = k, 5 = v of the QKV tasks.
+enum { ROWS_X = 0, ROWS_R = 1, ROWS_ATTN = 2, ROWS_Q = 3, ROWS_KINDS = 6 };
 __device__ inline uint64_t *tagged_rows(const pgpu_flow_step &f, int layer, int which) {
-    return f.rows + ((size_t)layer * 3 + which) * (size_t)f.tiles * 16 * kWidth;
+    return f.rows + ((size_t)layer * ROWS_KINDS + which) * (size_t)f.tiles * 16 * kWidth;
 }
+
+// Attention gate of the merge-in-out mode (outside a prefill): a first wait
+// for one of the head's QKV tasks (a count without a drain), then the
+// unit's q and the appended key's K and V polled as tagged words
+// (attend_unit: GateTaggedQkv).
+struct TaggedQkvGate {
+    static constexpr bool kTaggedQkv = true;
+    FlowWait hint;
+    const uint64_t *qkv;  // the layer's tagged q rows; k and v follow, `part` words apart
+    size_t part;
+    TagPoll tp;
+    __device__ unsigned probe() const { return hint.probe(); }
+    __device__ void pass(unsigned first, bool needed) const { hint.pass(first, needed); }
+    // Dimensions [4 dcol, 4 dcol + 4) of head `head` of stream s.
+    __device__ void poll_qkv(int s, int head, int dcol, float4 &q, float4 &k, float4 &v) const {
+        const __amdgpu_buffer_rsrc_t r = tag_rsrc(qkv, (uint32_t)(3 * part * 8));
+        const uint32_t off = (uint32_t)(((size_t)s * kWidth + head * kHeadDim + dcol * 4) * 8);
+        const uint32_t step = (uint32_t)(part * 8);
+        u32x4 w[6];
+        const uint64_t t0 = wall_clock64();
+        for (int round = 0;; round++) {
+            __asm__ volatile("" ::: "memory");
+            bool ok = true;
+#pragma unroll
+            for (int p = 0; p < 3; p++) {
+                w[2 * p] = tag_load2(r, off + p * step);
+                w[2 * p + 1] = tag_load2(r, off + p * step + 16);
+                ok &= tag_ok2(w[2 * p], tp.tag) && tag_ok2(w[2 * p + 1], tp.tag);
+            }
+            if (__all(ok)) break;
+            if (tag_give_up(tp, t0, round)) break;
+            __builtin_amdgcn_s_sleep(1);
+        }
+        q = make_float4(bitsf(w[0].x), bitsf(w[0].z), bitsf(w[1].x), bitsf(w[1].z));
+        k = make_float4(bitsf(w[2].x), bitsf(w[2].z), bitsf(w[3].x), bitsf(w[3].z));
+        v = make_float4(bitsf(w[4].x), bitsf(w[4].z), bitsf(w[5].x), bitsf(w[5].z));
+    }
+};
 
 __device__ inline GemmArgs base_args(const pgpu_flow_step &f, const pgpu_flow_layer &ly,
                                      int which, uint32_t tag) {
@@ -321,9 +360,19 @@ __device__ inline void attention_task(const pgpu_flow_step &f, const pgpu_paged_
     int count;
     constexpr bool tagged_parts = MODE != PGPU_FLOW_HANDOFF_COUNTER;
     constexpr bool MO = MODE == PGPU_FLOW_HANDOFF_MERGE_OUT;
-    const int state = attend_unit<kFlowRounds>(
-        a, head, split0, s, wave, sh, true, aa, mm, ll, count, ready, f.attn_rounds, !f.prefill,
-        tagged_parts && !MO ? 2 : 1);
+    int state;
+    if (MO && !f.prefill) {
+        const TaggedQkvGate gate{wait_for(f, layer, tile, PGPU_FLOW_QKV_HEAD + head, 1u),
+                                 tagged_rows(f, layer, ROWS_Q),
+                                 (size_t)f.tiles * 16 * kWidth,
+                                 TagPoll{tag, f.status, wait_ticks(f), false}};
+        state = attend_unit<kFlowRounds>(a, head, split0, s, wave, sh, true, aa, mm, ll, count,
+                                         gate, f.attn_rounds, true, 1);
+    } else {
+        state = attend_unit<kFlowRounds>(a, head, split0, s, wave, sh, true, aa, mm, ll, count,
+                                         ready, f.attn_rounds, !f.prefill,
+                                         tagged_parts && !MO ? 2 : 1);
+    }
     if constexpr (MO) {
         // Every split's partial goes out as a tagged record; the tile's
         // out-projection tasks poll and merge them.
@@ -449,11 +498,27 @@ __device__ inline void flow_step_task(const pgpu_flow_step &f, const pgpu_paged_
             a.ln_x = layer == 0 ? f.input : nullptr;
             a.tx = layer == 0 ? nullptr : tagged_rows(f, layer - 1, ROWS_X);
             a.ready_mark = ready_mark;
+            if (merge_out && !f.prefill) {
+                // q, k and v also go out as tagged words for the attention
+                // units; the pool's K/V are read by later launches only.
+                a.tqkv = tagged_rows(f, layer, ROWS_Q);
+                a.tqkv_part = (size_t)f.tiles * 16 * kWidth;
+            }
             gemm_wide_task<SRC_LN, EPI_QKV, Q8>(
                 a, index, tile, lds,
                 layer == 0 ? no_wait(f)
                            : wait_for(f, layer - 1, tile, PGPU_FLOW_MLP_IN,
                                       PGPU_FLOW_MLP_IN_TASKS));
+            if (merge_out && !f.prefill) {
+                // A count for first waits only: no drain.
+                __syncthreads();
+                if (threadIdx.x == 0)
+                    __hip_atomic_fetch_add(
+                        phase_counter(f, layer, tile, PGPU_FLOW_QKV_HEAD + (index & 7)), 1u,
+                        __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                trace_mark(f, 2);
+                break;
+            }
         } else {
             a.ln_x = layer_input(f, layer);
             const FlowWait w = layer == 0 ? no_wait(f)

@@ -204,6 +204,10 @@ struct GemmArgs {
     // SRC_ATTN_TAGGED: the layer's tagged split partials,
     // [tiles*16][8][max_splits][PGPU_FLOW_PART_WORDS] (P.V [64], max, sum).
     const uint64_t *tparts;
+    // QKV (optional): q (scaled), k and v also as tagged words, part p at
+    // tqkv + p * tqkv_part, [tiles*16][512] each.
+    uint64_t *tqkv;
+    size_t tqkv_part;
     uint64_t *ready_mark;
 };
 
@@ -954,6 +958,12 @@ __device__ inline bool epilogue(const GemmArgs &a, const EpiOperands &e, const f
             }
 #pragma unroll
             for (int r = 0; r < 4; r++) bad |= !isfinite(o[r]);
+            if (a.tqkv)  // every live lane, also for a flagged position
+                store_tagged4(a.tqkv + (size_t)part * a.tqkv_part + (size_t)s * kWidth + rr,
+                              part == 0 ? make_float4(o[0] * 0.125f, o[1] * 0.125f,
+                                                      o[2] * 0.125f, o[3] * 0.125f)
+                                        : make_float4(o[0], o[1], o[2], o[3]),
+                              a.tp.tag);
             if (part == 0) {
                 // The 1/sqrt(64) score scale is a power of two: folding it
                 // into q is exact.

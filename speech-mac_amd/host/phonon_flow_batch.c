@@ -793,7 +793,7 @@ static int flow_reserve(PhononFlowBatch *b, size_t streams) {
     b->fl.part_ml = pgpu_malloc(groups * flow_ml_group(b) * sizeof(float));
     b->fl.hidden = pgpu_malloc(new_layers * new_cap * PH_FFN * 3 * sizeof(uint16_t));
     b->fl.counters = pgpu_malloc(b->fl.counter_words * sizeof(unsigned));
-    b->fl.rows_words = new_layers * 3 * new_cap * PH_WIDTH;
+    b->fl.rows_words = new_layers * 6 * new_cap * PH_WIDTH;
     b->fl.parts_words = groups * b->max_splits * PGPU_FLOW_PART_WORDS;
     b->fl.rows = pgpu_malloc(b->fl.rows_words * sizeof(uint64_t));
     b->fl.parts = pgpu_malloc(b->fl.parts_words * sizeof(uint64_t));
