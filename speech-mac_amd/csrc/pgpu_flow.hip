@@ -193,6 +193,7 @@ struct TaggedQkvGate {
     const uint64_t *qkv;  // the layer's tagged q rows; k and v follow, `part` words apart
     size_t part;
     TagPoll tp;
+    const pgpu_flow_step *f;  // for the task trace's inputs-ready mark
     __device__ unsigned probe() const { return hint.probe(); }
     __device__ void pass(unsigned first, bool needed) const { hint.pass(first, needed); }
     // Dimensions [4 dcol, 4 dcol + 4) of head `head` of stream s.
@@ -218,6 +219,7 @@ struct TaggedQkvGate {
         q = make_float4(bitsf(w[0].x), bitsf(w[0].z), bitsf(w[1].x), bitsf(w[1].z));
         k = make_float4(bitsf(w[2].x), bitsf(w[2].z), bitsf(w[3].x), bitsf(w[3].z));
         v = make_float4(bitsf(w[4].x), bitsf(w[4].z), bitsf(w[5].x), bitsf(w[5].z));
+        trace_mark(*f, 1);
     }
 };
 
@@ -365,7 +367,7 @@ __device__ inline void attention_task(const pgpu_flow_step &f, const pgpu_paged_
         const TaggedQkvGate gate{wait_for(f, layer, tile, PGPU_FLOW_QKV_HEAD + head, 1u),
                                  tagged_rows(f, layer, ROWS_Q),
                                  (size_t)f.tiles * 16 * kWidth,
-                                 TagPoll{tag, f.status, wait_ticks(f), false}};
+                                 TagPoll{tag, f.status, wait_ticks(f), false}, &f};
         state = attend_unit<kFlowRounds>(a, head, split0, s, wave, sh, true, aa, mm, ll, count,
                                          gate, f.attn_rounds, true, 1);
     } else {
