@@ -329,7 +329,7 @@ __device__ inline void tagged_attention_tail(const pgpu_flow_step &f, int layer,
     trace_mark(f, 2);
 }
 
-template <int MODE>
+template <int MODE, bool PRE>
 __device__ inline void attention_task(const pgpu_flow_step &f, const pgpu_paged_kv &kv,
                                       int layer, int tile, int index, AttnShared *sh,
                                       uint32_t tag) {
@@ -337,7 +337,7 @@ __device__ inline void attention_task(const pgpu_flow_step &f, const pgpu_paged_
     const int s = tile * 16 + n;
     if (s >= f.streams) return;  // uniform
     const TracedWait ready{
-        f.prefill
+        PRE
             ? wait_for(f, layer, 0, PGPU_FLOW_QKV_ALL, (unsigned)(PGPU_FLOW_QKV_TASKS * f.tiles))
             : wait_for(f, layer, tile, PGPU_FLOW_QKV_HEAD + head, 3u),
         &f};
@@ -363,7 +363,7 @@ __device__ inline void attention_task(const pgpu_flow_step &f, const pgpu_paged_
     constexpr bool tagged_parts = MODE != PGPU_FLOW_HANDOFF_COUNTER;
     constexpr bool MO = MODE == PGPU_FLOW_HANDOFF_MERGE_OUT;
     int state;
-    if (MO && !f.prefill) {
+    if constexpr (MO && !PRE) {
         const TaggedQkvGate gate{wait_for(f, layer, tile, PGPU_FLOW_QKV_HEAD + head, 1u),
                                  tagged_rows(f, layer, ROWS_Q),
                                  (size_t)f.tiles * 16 * kWidth,
@@ -372,7 +372,7 @@ __device__ inline void attention_task(const pgpu_flow_step &f, const pgpu_paged_
                                          gate, f.attn_rounds, true, 1);
     } else {
         state = attend_unit<kFlowRounds>(a, head, split0, s, wave, sh, true, aa, mm, ll, count,
-                                         ready, f.attn_rounds, !f.prefill,
+                                         ready, f.attn_rounds, !PRE,
                                          tagged_parts && !MO ? 2 : 1);
     }
     if constexpr (MO) {
@@ -459,7 +459,7 @@ __device__ inline void attention_task(const pgpu_flow_step &f, const pgpu_paged_
 
 // MODE: the launch's hand-off mode (PGPU_FLOW_HANDOFF_*, f.tagged), one
 // kernel per mode, so that no mode's code carries another's registers.
-template <bool Q8, int MODE>
+template <bool Q8, int MODE, bool PRE>
 __device__ inline void flow_step_task(const pgpu_flow_step &f, const pgpu_paged_kv &kv,
                                       uint4 *lds4) {
     uint16_t *lds = (uint16_t *)lds4;
@@ -500,7 +500,7 @@ __device__ inline void flow_step_task(const pgpu_flow_step &f, const pgpu_paged_
             a.ln_x = layer == 0 ? f.input : nullptr;
             a.tx = layer == 0 ? nullptr : tagged_rows(f, layer - 1, ROWS_X);
             a.ready_mark = ready_mark;
-            if (merge_out && !f.prefill) {
+            if constexpr (merge_out && !PRE) {
                 // q, k and v also go out as tagged words for the attention
                 // units; the pool's K/V are read by later launches only.
                 a.tqkv = tagged_rows(f, layer, ROWS_Q);
@@ -511,7 +511,7 @@ __device__ inline void flow_step_task(const pgpu_flow_step &f, const pgpu_paged_
                 layer == 0 ? no_wait(f)
                            : wait_for(f, layer - 1, tile, PGPU_FLOW_MLP_IN,
                                       PGPU_FLOW_MLP_IN_TASKS));
-            if (merge_out && !f.prefill) {
+            if constexpr (merge_out && !PRE) {
                 // A count for first waits only: no drain.
                 __syncthreads();
                 if (threadIdx.x == 0)
@@ -530,11 +530,11 @@ __device__ inline void flow_step_task(const pgpu_flow_step &f, const pgpu_paged_
         }
         // Rows [64 index, +64): q, k or v of head index % 8.
         flow_signal(f, phase_counter(f, layer, tile, PGPU_FLOW_QKV_HEAD + (index & 7)),
-                    f.prefill ? phase_counter(f, layer, 0, PGPU_FLOW_QKV_ALL) : nullptr);
+                    PRE ? phase_counter(f, layer, 0, PGPU_FLOW_QKV_ALL) : nullptr);
         break;
     }
     case PGPU_FLOW_ATTN:
-        attention_task<MODE>(f, kv, layer, tile, index, (AttnShared *)lds4, tag);
+        attention_task<MODE, PRE>(f, kv, layer, tile, index, (AttnShared *)lds4, tag);
         break;
     case PGPU_FLOW_OUT: {
         GemmArgs a = base_args(f, ly, 1, tag);
@@ -550,7 +550,7 @@ __device__ inline void flow_step_task(const pgpu_flow_step &f, const pgpu_paged_
             a.tres = layer == 0 ? nullptr : tagged_rows(f, layer - 1, ROWS_X);
             a.ready_mark = ready_mark;
             const FlowWait w =
-                f.prefill ? wait_for(f, layer, 0, PGPU_FLOW_QKV_ALL,
+                PRE ? wait_for(f, layer, 0, PGPU_FLOW_QKV_ALL,
                                      (unsigned)(PGPU_FLOW_QKV_TASKS * f.tiles))
                           : wait_for(f, layer, tile, PGPU_FLOW_QKV_HEAD + kHeads - 1, 3u);
             if constexpr (merge_out) {
@@ -637,18 +637,20 @@ __device__ inline void flow_step_task(const pgpu_flow_step &f, const pgpu_paged_
 
 // Two 512-thread work-groups per CU: the projection tasks' registers and
 // 49 KB of LDS (the prologue's operand buffer) set the occupancy.
-template <bool Q8, int MODE>
+template <bool Q8, int MODE, bool PRE>
 __global__ __launch_bounds__(kTaskThreads) void k_flow_step(pgpu_flow_step f, pgpu_paged_kv kv) {
     __shared__ uint4 lds4[kTaskLds / 8];
-    flow_step_task<Q8, MODE>(f, kv, lds4);
+    flow_step_task<Q8, MODE, PRE>(f, kv, lds4);
 }
 
-template <bool Q8>
+// One kernel per (hand-off mode, prefill or decode): each resolves its
+// mode's branches at compile time and carries no other mode's registers.
+template <bool Q8, bool PRE>
 void launch_step(const pgpu_flow_step *step, const pgpu_paged_kv *kv, hipStream_t stream) {
-    auto kernel = step->tagged == PGPU_FLOW_HANDOFF_TAGGED      ? k_flow_step<Q8, 1>
-                  : step->tagged == PGPU_FLOW_HANDOFF_PARTS     ? k_flow_step<Q8, 2>
-                  : step->tagged == PGPU_FLOW_HANDOFF_MERGE_OUT ? k_flow_step<Q8, 3>
-                                                                : k_flow_step<Q8, 0>;
+    auto kernel = step->tagged == PGPU_FLOW_HANDOFF_TAGGED      ? k_flow_step<Q8, 1, PRE>
+                  : step->tagged == PGPU_FLOW_HANDOFF_PARTS     ? k_flow_step<Q8, 2, PRE>
+                  : step->tagged == PGPU_FLOW_HANDOFF_MERGE_OUT ? k_flow_step<Q8, 3, PRE>
+                                                                : k_flow_step<Q8, 0, PRE>;
     hipLaunchKernelGGL(kernel, dim3(step->tasks), dim3(kTaskThreads), 0, stream, *step, *kv);
 }
 
@@ -685,10 +687,16 @@ extern "C" int pgpu_flow_launch(void *stream, const pgpu_flow_step *step,
           step->tagged == PGPU_FLOW_HANDOFF_MERGE_OUT) && !step->rows) ||
         step->pool_offset < 0 || step->pool_offset + step->layer_count > kv->layers)
         return bad_arguments("pgpu_flow_launch");
-    if (step->q8)
-        launch_step<true>(step, kv, (hipStream_t)stream);
-    else
-        launch_step<false>(step, kv, (hipStream_t)stream);
+    if (step->prefill) {
+        if (step->q8)
+            launch_step<true, true>(step, kv, (hipStream_t)stream);
+        else
+            launch_step<false, true>(step, kv, (hipStream_t)stream);
+    } else if (step->q8) {
+        launch_step<true, false>(step, kv, (hipStream_t)stream);
+    } else {
+        launch_step<false, false>(step, kv, (hipStream_t)stream);
+    }
     return launch_ok("pgpu_flow_launch");
 }
 
