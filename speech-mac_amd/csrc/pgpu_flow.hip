@@ -261,6 +261,7 @@ static_assert(kFlowRounds * sizeof(AttnShared) <= kTaskLds * 2, "attention LDS")
 // merged row goes out as tagged words, then the tile's ATTN count (a hint
 // for the MLP-in tasks' first wait); otherwise it is stored write-through
 // and drained before the count, as in the counter mode.
+template <int R>
 __device__ inline void tagged_attention_tail(const pgpu_flow_step &f, int layer, int tile, int s,
                                              int head, int split0, int nsplit, int rounds,
                                              bool covered, const float4 *aa, const float *mm,
@@ -268,11 +269,11 @@ __device__ inline void tagged_attention_tail(const pgpu_flow_step &f, int layer,
                                              bool rows_tagged, int wave) {
     const int lane = threadIdx.x & 63, d = (lane & 15) * 4;
     uint64_t *part = f.parts + group * f.max_splits * PGPU_FLOW_PART_WORDS;
-    const bool in_registers = covered && nsplit <= f.attn_rounds;
+    const bool in_registers = covered && nsplit <= R;
     if (wave == 1) {
         if (covered && !in_registers) {
 #pragma unroll
-            for (int r = 0; r < kFlowRounds; r++) {
+            for (int r = 0; r < R; r++) {
                 if (r >= rounds) break;
                 uint64_t *rec = part + (size_t)(split0 + r) * PGPU_FLOW_PART_WORDS;
                 if (lane < 16) store_tagged4(rec + d, aa[r], tag);
@@ -289,7 +290,7 @@ __device__ inline void tagged_attention_tail(const pgpu_flow_step &f, int layer,
     if (in_registers) {
         float mx = -INFINITY, total = 0.0f;
 #pragma unroll
-        for (int r = 0; r < kFlowRounds; r++) {
+        for (int r = 0; r < R; r++) {
             if (r >= nsplit) break;
             const float acc[4] = {aa[r].x, aa[r].y, aa[r].z, aa[r].w};
             merge_step(mx, total, v, 4, mm[r], ll[r], acc);
@@ -329,11 +330,11 @@ __device__ inline void tagged_attention_tail(const pgpu_flow_step &f, int layer,
     trace_mark(f, 2);
 }
 
-template <int MODE, bool PRE>
+template <int MODE, bool PRE, int R>
 __device__ inline void attention_task(const pgpu_flow_step &f, const pgpu_paged_kv &kv,
                                       int layer, int tile, int index, AttnShared *sh,
                                       uint32_t tag) {
-    const int head = index & 7, split0 = ((index >> 3) & 255) * f.attn_rounds, n = index >> 11;
+    const int head = index & 7, split0 = ((index >> 3) & 255) * R, n = index >> 11;
     const int s = tile * 16 + n;
     if (s >= f.streams) return;  // uniform
     const TracedWait ready{
@@ -357,8 +358,8 @@ __device__ inline void attention_task(const pgpu_flow_step &f, const pgpu_paged_
     a.part_ml = nullptr;
     a.status = f.status;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    float4 aa[kFlowRounds];
-    float mm[kFlowRounds], ll[kFlowRounds];
+    float4 aa[R];
+    float mm[R], ll[R];
     int count;
     constexpr bool tagged_parts = MODE != PGPU_FLOW_HANDOFF_COUNTER;
     constexpr bool MO = MODE == PGPU_FLOW_HANDOFF_MERGE_OUT;
@@ -368,11 +369,11 @@ __device__ inline void attention_task(const pgpu_flow_step &f, const pgpu_paged_
                                  tagged_rows(f, layer, ROWS_Q),
                                  (size_t)f.tiles * 16 * kWidth,
                                  TagPoll{tag, f.status, wait_ticks(f), false}, &f};
-        state = attend_unit<kFlowRounds>(a, head, split0, s, wave, sh, true, aa, mm, ll, count,
-                                         gate, f.attn_rounds, true, 1);
+        state = attend_unit<R>(a, head, split0, s, wave, sh, true, aa, mm, ll, count,
+                                         gate, R, true, 1);
     } else {
-        state = attend_unit<kFlowRounds>(a, head, split0, s, wave, sh, true, aa, mm, ll, count,
-                                         ready, f.attn_rounds, !PRE,
+        state = attend_unit<R>(a, head, split0, s, wave, sh, true, aa, mm, ll, count,
+                                         ready, R, !PRE,
                                          tagged_parts && !MO ? 2 : 1);
     }
     if constexpr (MO) {
@@ -384,8 +385,8 @@ __device__ inline void attention_task(const pgpu_flow_step &f, const pgpu_paged_
         uint64_t *part = f.parts + group * f.max_splits * PGPU_FLOW_PART_WORDS;
         const int nsplit = (count + kSplitKeys - 1) / kSplitKeys;
 #pragma unroll
-        for (int r = 0; r < kFlowRounds; r++) {
-            if (r >= f.attn_rounds || split0 + r >= nsplit) break;
+        for (int r = 0; r < R; r++) {
+            if (r >= R || split0 + r >= nsplit) break;
             uint64_t *rec = part + (size_t)(split0 + r) * PGPU_FLOW_PART_WORDS;
             if (lane < 16) store_tagged4(rec + lane * 4, aa[r], tag);
             if (lane == 0) {
@@ -401,21 +402,21 @@ __device__ inline void attention_task(const pgpu_flow_step &f, const pgpu_paged_
         return;
     const bool covered = state == UNIT_LIVE;
     const int nsplit = (count + kSplitKeys - 1) / kSplitKeys;
-    const int rounds = min(f.attn_rounds, nsplit - split0);  // splits of this task (if covered)
+    const int rounds = min(R, nsplit - split0);  // splits of this task (if covered)
 
     const int lane = threadIdx.x & 63, d = (lane & 15) * 4;
     const size_t group = ((size_t)layer * f.tiles * 16 + s) * kHeads + head;
     if constexpr (tagged_parts) {
-        tagged_attention_tail(f, layer, tile, s, head, split0, nsplit, rounds, covered, aa, mm,
+        tagged_attention_tail<R>(f, layer, tile, s, head, split0, nsplit, rounds, covered, aa, mm,
                               ll, group, tag, MODE == PGPU_FLOW_HANDOFF_TAGGED, wave);
         return;
     }
     float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     bool finish = !covered, bad = false;
-    if (covered && nsplit <= f.attn_rounds) {
+    if (covered && nsplit <= R) {
         float mx = -INFINITY, total = 0.0f;
 #pragma unroll
-        for (int r = 0; r < kFlowRounds; r++) {
+        for (int r = 0; r < R; r++) {
             if (r >= nsplit) break;
             const float acc[4] = {aa[r].x, aa[r].y, aa[r].z, aa[r].w};
             merge_step(mx, total, v, 4, mm[r], ll[r], acc);
@@ -426,7 +427,7 @@ __device__ inline void attention_task(const pgpu_flow_step &f, const pgpu_paged_
         float *acc = f.part_acc + group * f.max_splits * 64;
         float *ml = f.part_ml + group * f.ml_group;
 #pragma unroll
-        for (int r = 0; r < kFlowRounds; r++) {
+        for (int r = 0; r < R; r++) {
             if (r >= rounds) break;
             if (lane < 16) store_wt(acc + (split0 + r) * 64 + d, aa[r]);
             if (lane == 0) store_wt((float2 *)(ml + 2 * (split0 + r)), make_float2(mm[r], ll[r]));
@@ -459,7 +460,7 @@ __device__ inline void attention_task(const pgpu_flow_step &f, const pgpu_paged_
 
 // MODE: the launch's hand-off mode (PGPU_FLOW_HANDOFF_*, f.tagged), one
 // kernel per mode, so that no mode's code carries another's registers.
-template <bool Q8, int MODE, bool PRE>
+template <bool Q8, int MODE, bool PRE, int R>
 __device__ inline void flow_step_task(const pgpu_flow_step &f, const pgpu_paged_kv &kv,
                                       uint4 *lds4) {
     uint16_t *lds = (uint16_t *)lds4;
@@ -534,7 +535,7 @@ __device__ inline void flow_step_task(const pgpu_flow_step &f, const pgpu_paged_
         break;
     }
     case PGPU_FLOW_ATTN:
-        attention_task<MODE, PRE>(f, kv, layer, tile, index, (AttnShared *)lds4, tag);
+        attention_task<MODE, PRE, R>(f, kv, layer, tile, index, (AttnShared *)lds4, tag);
         break;
     case PGPU_FLOW_OUT: {
         GemmArgs a = base_args(f, ly, 1, tag);
@@ -637,21 +638,31 @@ __device__ inline void flow_step_task(const pgpu_flow_step &f, const pgpu_paged_
 
 // Two 512-thread work-groups per CU: the projection tasks' registers and
 // 49 KB of LDS (the prologue's operand buffer) set the occupancy.
-template <bool Q8, int MODE, bool PRE>
+template <bool Q8, int MODE, bool PRE, int R>
 __global__ __launch_bounds__(kTaskThreads) void k_flow_step(pgpu_flow_step f, pgpu_paged_kv kv) {
     __shared__ uint4 lds4[kTaskLds / 8];
-    flow_step_task<Q8, MODE, PRE>(f, kv, lds4);
+    flow_step_task<Q8, MODE, PRE, R>(f, kv, lds4);
 }
 
-// One kernel per (hand-off mode, prefill or decode): each resolves its
-// mode's branches at compile time and carries no other mode's registers.
-template <bool Q8, bool PRE>
+// One kernel per (hand-off mode, prefill or decode, splits per attention
+// task): each resolves its branches at compile time and carries no other
+// variant's registers.
+template <bool Q8, bool PRE, int R>
 void launch_step(const pgpu_flow_step *step, const pgpu_paged_kv *kv, hipStream_t stream) {
-    auto kernel = step->tagged == PGPU_FLOW_HANDOFF_TAGGED      ? k_flow_step<Q8, 1, PRE>
-                  : step->tagged == PGPU_FLOW_HANDOFF_PARTS     ? k_flow_step<Q8, 2, PRE>
-                  : step->tagged == PGPU_FLOW_HANDOFF_MERGE_OUT ? k_flow_step<Q8, 3, PRE>
-                                                                : k_flow_step<Q8, 0, PRE>;
+    auto kernel = step->tagged == PGPU_FLOW_HANDOFF_TAGGED      ? k_flow_step<Q8, 1, PRE, R>
+                  : step->tagged == PGPU_FLOW_HANDOFF_PARTS     ? k_flow_step<Q8, 2, PRE, R>
+                  : step->tagged == PGPU_FLOW_HANDOFF_MERGE_OUT ? k_flow_step<Q8, 3, PRE, R>
+                                                                : k_flow_step<Q8, 0, PRE, R>;
     hipLaunchKernelGGL(kernel, dim3(step->tasks), dim3(kTaskThreads), 0, stream, *step, *kv);
+}
+
+template <bool Q8, bool PRE>
+void launch_rounds(const pgpu_flow_step *step, const pgpu_paged_kv *kv, hipStream_t stream) {
+    static_assert(PGPU_FLOW_ATTN_ROUNDS == 2, "one kernel per rounds value");
+    if (step->attn_rounds == 1)
+        launch_step<Q8, PRE, 1>(step, kv, stream);
+    else
+        launch_step<Q8, PRE, 2>(step, kv, stream);
 }
 
 __global__ void k_flow_finish(unsigned *counters, size_t n, int32_t *positions, int streams,
@@ -689,13 +700,13 @@ extern "C" int pgpu_flow_launch(void *stream, const pgpu_flow_step *step,
         return bad_arguments("pgpu_flow_launch");
     if (step->prefill) {
         if (step->q8)
-            launch_step<true, true>(step, kv, (hipStream_t)stream);
+            launch_rounds<true, true>(step, kv, (hipStream_t)stream);
         else
-            launch_step<false, true>(step, kv, (hipStream_t)stream);
+            launch_rounds<false, true>(step, kv, (hipStream_t)stream);
     } else if (step->q8) {
-        launch_step<true, false>(step, kv, (hipStream_t)stream);
+        launch_rounds<true, false>(step, kv, (hipStream_t)stream);
     } else {
-        launch_step<false, false>(step, kv, (hipStream_t)stream);
+        launch_rounds<false, false>(step, kv, (hipStream_t)stream);
     }
     return launch_ok("pgpu_flow_launch");
 }
