@@ -284,7 +284,7 @@ def flow_roofline(pkg, lib, d, steps=20):
             "traffic_source": f"{FLOW_PMC_SUMMARY} (FETCH_SIZE/WRITE_SIZE, copy-calibrated): "
                               f"{measured[0]} B for {measured[1]} B algorithmic"
                               if measured else None,
-            "kernel": "pgpu::k_flow_step<true, 0>", "us_per_launch": round(us, 2),
+            "kernel": "pgpu::k_flow_step<true, 0, false, 1>", "us_per_launch": round(us, 2),
             "launches": steps, "algorithmic_bytes_per_launch": int(per_launch),
             "algorithmic_bytes": "Q8 weights of 12 layers once + K/V of every attended key "
                                  "per layer + the appended K/V row per stream per layer",
