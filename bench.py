@@ -56,20 +56,27 @@ def log(msg):
     print(msg, file=sys.stderr, flush=True)
 
 
+def last_error(lib):
+    """The library's last recorded error (pgpu_last_error), for assert messages."""
+    msg = lib.pgpu_last_error()
+    return msg.decode(errors="replace") if msg else ""
+
+
 class Timer:
     def __init__(self, lib, stream):
         self.lib, self.stream = lib, stream
         self.a, self.b = ctypes.c_void_p(), ctypes.c_void_p()
-        assert lib.pgpu_event_create(ctypes.byref(self.a))
-        assert lib.pgpu_event_create(ctypes.byref(self.b))
+        assert lib.pgpu_event_create(ctypes.byref(self.a)), last_error(lib)
+        assert lib.pgpu_event_create(ctypes.byref(self.b)), last_error(lib)
 
     def start(self):
-        assert self.lib.pgpu_event_record(self.a, self.stream)
+        assert self.lib.pgpu_event_record(self.a, self.stream), last_error(self.lib)
 
     def stop_ms(self) -> float:
-        assert self.lib.pgpu_event_record(self.b, self.stream)
+        assert self.lib.pgpu_event_record(self.b, self.stream), last_error(self.lib)
         ms = ctypes.c_float()
-        assert self.lib.pgpu_event_elapsed_ms(self.a, self.b, ctypes.byref(ms))
+        assert self.lib.pgpu_event_elapsed_ms(self.a, self.b, ctypes.byref(ms)), \
+            last_error(self.lib)
         return ms.value
 
 
@@ -88,36 +95,40 @@ class DecodeSetup:
         self.views = views
         weights = views.layers(syn.flow_model(seed, layers))
         self.model, self.pool, self.batch = ctypes.c_void_p(), ctypes.c_void_p(), ctypes.c_void_p()
-        assert lib.phonon_flow_model_create(weights, layers, ctypes.byref(self.model))
-        assert lib.phonon_kv_pool_create(layers, blocks, ctypes.byref(self.pool))
-        assert lib.phonon_kv_pool_fill_normal(self.pool, seed + 1)
+        assert lib.phonon_flow_model_create(weights, layers, ctypes.byref(self.model)), \
+            last_error(lib)
+        assert lib.phonon_kv_pool_create(layers, blocks, ctypes.byref(self.pool)), last_error(lib)
+        assert lib.phonon_kv_pool_fill_normal(self.pool, seed + 1), last_error(lib)
         ids = np.zeros(blocks, np.int32)
-        assert lib.phonon_kv_pool_alloc(self.pool, blocks, ids.ctypes.data_as(P_I32))
+        assert lib.phonon_kv_pool_alloc(self.pool, blocks, ids.ctypes.data_as(P_I32)), \
+            last_error(lib)
         perm = np.random.default_rng(seed + 2).permutation(ids)   # shuffled tables
         self.tables = np.ascontiguousarray(perm.reshape(streams, self.table_len).astype(np.int32))
         assert lib.phonon_flow_batch_create(self.model, self.pool, streams, self.max_positions,
-                                            ctypes.byref(self.batch))
+                                            ctypes.byref(self.batch)), last_error(lib)
         self.stream = lib.phonon_flow_batch_stream(self.batch)
         self.din = lib.phonon_flow_batch_device_inputs(self.batch)
         self.dout = lib.phonon_flow_batch_device_outputs(self.batch)
         x = np.random.default_rng(seed + 3).standard_normal((streams, 512)).astype(np.float32)
-        assert lib.pgpu_copy_h2d(self.stream, self.din, x.ctypes.data, x.nbytes)
+        assert lib.pgpu_copy_h2d(self.stream, self.din, x.ctypes.data, x.nbytes), last_error(lib)
         self.reset()
 
     def reset(self):
         pos = self.lengths.astype(np.uintp)
         assert self.lib.phonon_flow_batch_set_streams(
             self.batch, self.streams, pos.ctypes.data_as(P_SZ), self.tables.ctypes.data_as(P_I32),
-            self.table_len)
+            self.table_len), last_error(self.lib)
 
     def step(self):
         # Output feeds the next step's input: a closed-loop decode.
-        assert self.lib.phonon_flow_batch_step_device(self.batch, self.din, 10000.0, self.dout)
+        assert self.lib.phonon_flow_batch_step_device(self.batch, self.din, 10000.0, self.dout), \
+            last_error(self.lib)
         self.din, self.dout = self.dout, self.din
 
     def positions(self):
         out = np.zeros(self.streams, np.uintp)
-        assert self.lib.phonon_flow_batch_positions(self.batch, out.ctypes.data_as(P_SZ))
+        assert self.lib.phonon_flow_batch_positions(self.batch, out.ctypes.data_as(P_SZ)), \
+            last_error(self.lib)
         return out.astype(np.int64)
 
     def close(self):
@@ -139,21 +150,21 @@ def run_decode(pkg, lib, layers, streams, lengths, steps, warmup, seed, groups=N
     # headroom: the timed steps, then the roofline's timed launches
     d = DecodeSetup(pkg, lib, layers, streams, lengths, steps + warmup + 41, seed)
     if groups:
-        assert lib.phonon_flow_batch_set_groups(d.batch, groups)
+        assert lib.phonon_flow_batch_set_groups(d.batch, groups), last_error(lib)
     if eager:
-        assert lib.phonon_flow_batch_set_graph(d.batch, 0)
+        assert lib.phonon_flow_batch_set_graph(d.batch, 0), last_error(lib)
     for _ in range(warmup):
         d.step()
     assert lib.phonon_flow_batch_sync(d.batch), "non-finite value during warmup"
     first = d.positions()
     timer = Timer(lib, d.stream)
-    assert lib.pgpu_stream_sync(d.stream)
+    assert lib.pgpu_stream_sync(d.stream), last_error(lib)
     t0 = time.perf_counter()
     timer.start()
     for _ in range(steps):
         d.step()
     ms = timer.stop_ms()
-    assert lib.pgpu_stream_sync(d.stream)
+    assert lib.pgpu_stream_sync(d.stream), last_error(lib)
     wall = time.perf_counter() - t0
     clean = lib.phonon_flow_batch_sync(d.batch)
     # keys attended at step i = position + 1
@@ -185,7 +196,7 @@ def attention_roofline(pkg, lib, d, iterations=20):
     timed with HIP events on the stream it is launched on."""
     pos = d.positions()
     view = pkg.PgpuPagedKv()
-    assert lib.phonon_kv_pool_view(d.pool, ctypes.byref(view))
+    assert lib.phonon_kv_pool_view(d.pool, ctypes.byref(view)), last_error(lib)
     streams = d.streams
     max_splits = (d.max_positions + 255) // 256
     q = pkg.DeviceBuffer(lib, streams * 512 * 4)
@@ -204,7 +215,7 @@ def attention_roofline(pkg, lib, d, iterations=20):
     def launch(layer):
         assert lib.pgpu_attention(d.stream, q.ptr, ctypes.byref(view), layer, tables.ptr,
                                   d.table_len, positions.ptr, streams, 8, max_splits,
-                                  ctypes.byref(scratch), status)
+                                  ctypes.byref(scratch), status), last_error(lib)
 
     # Layers in turn, as in a decode step: a launch never finds the previous
     # launch's keys in the last-level cache.
@@ -249,15 +260,16 @@ def flow_roofline(pkg, lib, d, steps=20):
     events = []
     for _ in range(2 * steps):
         e = ctypes.c_void_p()
-        assert lib.pgpu_event_create(ctypes.byref(e))
+        assert lib.pgpu_event_create(ctypes.byref(e)), last_error(lib)
         events.append(e)
     step_bytes_sum = 0
     for i in range(steps):
         step_bytes_sum += step_bytes(d.layers, d.positions() + 1)
-        assert lib.phonon_flow_batch_set_timing(d.batch, events[2 * i], events[2 * i + 1])
+        assert lib.phonon_flow_batch_set_timing(d.batch, events[2 * i], events[2 * i + 1]), \
+            last_error(lib)
         d.step()
-    assert lib.phonon_flow_batch_set_timing(d.batch, None, None)
-    assert lib.pgpu_stream_sync(d.stream)
+    assert lib.phonon_flow_batch_set_timing(d.batch, None, None), last_error(lib)
+    assert lib.pgpu_stream_sync(d.stream), last_error(lib)
     clean = bool(lib.phonon_flow_batch_sync(d.batch))
     total_ms = 0.0
     for i in range(steps):
@@ -297,7 +309,7 @@ def calibration_copy(pkg, lib, d, repeats=5):
     (pgpu_kv_copy, 16 KiB-aligned 4 KiB tiles). Returns bytes read (= bytes
     written) per launch."""
     view = pkg.PgpuPagedKv()
-    assert lib.phonon_kv_pool_view(d.pool, ctypes.byref(view))
+    assert lib.phonon_kv_pool_view(d.pool, ctypes.byref(view)), last_error(lib)
     n = (d.max_positions // 16) * 16
     row_bytes = 512 * 4
     keys = pkg.DeviceBuffer(lib, d.layers * n * row_bytes)
@@ -308,8 +320,8 @@ def calibration_copy(pkg, lib, d, repeats=5):
     lib.pgpu_memset(d.stream, words.ptr, 0, 4)
     for _ in range(repeats):
         assert lib.pgpu_kv_copy(d.stream, ctypes.byref(view), tables.ptr, 0, n, 0, d.layers,
-                                keys.ptr, values.ptr, n, 1, words.ptr)
-    assert lib.pgpu_stream_sync(d.stream)
+                                keys.ptr, values.ptr, n, 1, words.ptr), last_error(lib)
+    assert lib.pgpu_stream_sync(d.stream), last_error(lib)
     for b in (keys, values, tables, words):
         b.free()
     return 2 * d.layers * n * row_bytes
@@ -380,11 +392,12 @@ def large_batch_with_prefill(pkg, lib, seed, layers=12, streams=256, new_streams
     views = pkg.Views()
     weights = views.layers(syn.flow_model(seed, layers))
     model, pool, dec, pre = (ctypes.c_void_p() for _ in range(4))
-    assert lib.phonon_flow_model_create(weights, layers, ctypes.byref(model))
-    assert lib.phonon_kv_pool_create(layers, decode_blocks + prefill_blocks, ctypes.byref(pool))
-    assert lib.phonon_kv_pool_fill_normal(pool, seed + 51)
+    assert lib.phonon_flow_model_create(weights, layers, ctypes.byref(model)), last_error(lib)
+    assert lib.phonon_kv_pool_create(layers, decode_blocks + prefill_blocks, ctypes.byref(pool)), \
+        last_error(lib)
+    assert lib.phonon_kv_pool_fill_normal(pool, seed + 51), last_error(lib)
     ids = np.zeros(decode_blocks + prefill_blocks, np.int32)
-    assert lib.phonon_kv_pool_alloc(pool, ids.size, ids.ctypes.data_as(P_I32))
+    assert lib.phonon_kv_pool_alloc(pool, ids.size, ids.ctypes.data_as(P_I32)), last_error(lib)
     ids = np.random.default_rng(seed + 52).permutation(ids).astype(np.int32)
     tables = np.zeros((streams, table_len), np.int32)
     at = 0
@@ -394,35 +407,37 @@ def large_batch_with_prefill(pkg, lib, seed, layers=12, streams=256, new_streams
         at += need
     pre_tables = np.zeros((new_streams, table_len), np.int32)
     pre_tables[:, :chunk // 16] = ids[at:at + prefill_blocks].reshape(new_streams, chunk // 16)
-    assert lib.phonon_flow_batch_create(model, pool, streams, max_positions, ctypes.byref(dec))
+    assert lib.phonon_flow_batch_create(model, pool, streams, max_positions, ctypes.byref(dec)), \
+        last_error(lib)
     assert lib.phonon_flow_batch_create(model, pool, new_streams * chunk, max_positions,
-                                        ctypes.byref(pre))
-    assert lib.phonon_flow_batch_set_prefill_exact(pre, prefill_attention)
+                                        ctypes.byref(pre)), last_error(lib)
+    assert lib.phonon_flow_batch_set_prefill_exact(pre, prefill_attention), last_error(lib)
     pos = lengths.astype(np.uintp)
     assert lib.phonon_flow_batch_set_streams(dec, streams, pos.ctypes.data_as(P_SZ),
-                                             tables.ctypes.data_as(P_I32), table_len)
+                                             tables.ctypes.data_as(P_I32), table_len), \
+                                                 last_error(lib)
     stream = lib.phonon_flow_batch_stream(dec)
     pstream = lib.phonon_flow_batch_stream(pre)
     din, dout = lib.phonon_flow_batch_device_inputs(dec), lib.phonon_flow_batch_device_outputs(dec)
     pin, pout = lib.phonon_flow_batch_device_inputs(pre), lib.phonon_flow_batch_device_outputs(pre)
     x = np.random.default_rng(seed + 53).standard_normal((streams, 512)).astype(np.float32)
-    assert lib.pgpu_copy_h2d(stream, din, x.ctypes.data, x.nbytes)
+    assert lib.pgpu_copy_h2d(stream, din, x.ctypes.data, x.nbytes), last_error(lib)
     px = np.random.default_rng(seed + 54).standard_normal((new_streams * chunk, 512))
     px = px.astype(np.float32)
-    assert lib.pgpu_copy_h2d(pstream, pin, px.ctypes.data, px.nbytes)
+    assert lib.pgpu_copy_h2d(pstream, pin, px.ctypes.data, px.nbytes), last_error(lib)
     first = np.zeros(new_streams, np.uintp)
     counts = np.full(new_streams, chunk, np.uintp)
     dec_t, pre_t = Timer(lib, stream), Timer(lib, pstream)
     dec_ms = pre_ms = 0.0
     for it in range(steps):
         dec_t.start()
-        assert lib.phonon_flow_batch_step_device(dec, din, 10000.0, dout)
+        assert lib.phonon_flow_batch_step_device(dec, din, 10000.0, dout), last_error(lib)
         d_ms = dec_t.stop_ms()
         din, dout = dout, din
         pre_t.start()
         assert lib.phonon_flow_batch_prefill_device(
             pre, new_streams, first.ctypes.data_as(P_SZ), counts.ctypes.data_as(P_SZ),
-            pre_tables.ctypes.data_as(P_I32), table_len, pin, 10000.0, pout)
+            pre_tables.ctypes.data_as(P_I32), table_len, pin, 10000.0, pout), last_error(lib)
         p_ms = pre_t.stop_ms()
         if it >= warmup:
             dec_ms += d_ms
@@ -507,14 +522,15 @@ def b1_with_prefill(pkg, lib, layers, seed, prompt=256, frames=750, warmup=10, m
     views = pkg.Views()
     weights = views.layers(syn.flow_model(seed, layers))
     model, pool, batch = ctypes.c_void_p(), ctypes.c_void_p(), ctypes.c_void_p()
-    assert lib.phonon_flow_model_create(weights, layers, ctypes.byref(model))
-    assert lib.phonon_kv_pool_create(layers, blocks, ctypes.byref(pool))
+    assert lib.phonon_flow_model_create(weights, layers, ctypes.byref(model)), last_error(lib)
+    assert lib.phonon_kv_pool_create(layers, blocks, ctypes.byref(pool)), last_error(lib)
     ids = np.zeros(blocks, np.int32)
-    assert lib.phonon_kv_pool_alloc(pool, blocks, ids.ctypes.data_as(P_I32))
+    assert lib.phonon_kv_pool_alloc(pool, blocks, ids.ctypes.data_as(P_I32)), last_error(lib)
     table = np.ascontiguousarray(np.random.default_rng(seed + 60).permutation(ids)[:table_len])
-    assert lib.phonon_flow_batch_create(model, pool, prompt, max_pos, ctypes.byref(batch))
+    assert lib.phonon_flow_batch_create(model, pool, prompt, max_pos, ctypes.byref(batch)), \
+        last_error(lib)
     if mode is not None:
-        assert lib.phonon_flow_batch_set_pipeline(batch, mode)
+        assert lib.phonon_flow_batch_set_pipeline(batch, mode), last_error(lib)
     stream = lib.phonon_flow_batch_stream(batch)
     rng = np.random.default_rng(seed + 61)
     pin = pkg.DeviceBuffer(lib, prompt * 512 * 4)
@@ -529,18 +545,19 @@ def b1_with_prefill(pkg, lib, layers, seed, prompt=256, frames=750, warmup=10, m
 
     def run(steps):
         nonlocal din, dout
-        assert lib.pgpu_copy_h2d(stream, din, x0.ctypes.data, x0.nbytes)
+        assert lib.pgpu_copy_h2d(stream, din, x0.ctypes.data, x0.nbytes), last_error(lib)
         timer.start()
         assert lib.phonon_flow_batch_prefill_device(
             batch, 1, first.ctypes.data_as(P_SZ), counts.ctypes.data_as(P_SZ),
-            table.ctypes.data_as(P_I32), table_len, pin.ptr, 10000.0, pout.ptr)
+            table.ctypes.data_as(P_I32), table_len, pin.ptr, 10000.0, pout.ptr), last_error(lib)
         pre_ms = timer.stop_ms()
         pos = np.array([prompt], np.uintp)
         assert lib.phonon_flow_batch_set_streams(batch, 1, pos.ctypes.data_as(P_SZ),
-                                                 table.ctypes.data_as(P_I32), table_len)
+                                                 table.ctypes.data_as(P_I32), table_len), \
+                                                     last_error(lib)
         timer.start()
         for _ in range(steps):
-            assert lib.phonon_flow_batch_step_device(batch, din, 10000.0, dout)
+            assert lib.phonon_flow_batch_step_device(batch, din, 10000.0, dout), last_error(lib)
             din, dout = dout, din
         dec_ms = timer.stop_ms()
         return pre_ms, dec_ms
@@ -557,17 +574,17 @@ def b1_with_prefill(pkg, lib, layers, seed, prompt=256, frames=750, warmup=10, m
         lib.phonon_flow_batch_schedule(batch, sched.ctypes.data_as(ctypes.POINTER(ctypes.c_uint32)),
                                        ntask)
         buf = pkg.DeviceBuffer(lib, ntask * 4 * 8)
-        assert lib.phonon_flow_batch_set_trace(batch, buf.ptr, ntask)
+        assert lib.phonon_flow_batch_set_trace(batch, buf.ptr, ntask), last_error(lib)
         summaries = []
         for _ in range(trace_steps):
-            assert lib.phonon_flow_batch_step_device(batch, din, 10000.0, dout)
+            assert lib.phonon_flow_batch_step_device(batch, din, 10000.0, dout), last_error(lib)
             din, dout = dout, din
-            assert lib.pgpu_stream_sync(stream)
+            assert lib.pgpu_stream_sync(stream), last_error(lib)
             tr = np.zeros((ntask, 4), np.uint64)
-            assert lib.pgpu_copy_d2h(stream, tr.ctypes.data, buf.ptr, tr.nbytes)
-            assert lib.pgpu_stream_sync(stream)
+            assert lib.pgpu_copy_d2h(stream, tr.ctypes.data, buf.ptr, tr.nbytes), last_error(lib)
+            assert lib.pgpu_stream_sync(stream), last_error(lib)
             summaries.append(task_trace_summary(sched, tr))
-        assert lib.phonon_flow_batch_set_trace(batch, None, 0)
+        assert lib.phonon_flow_batch_set_trace(batch, None, 0), last_error(lib)
         buf.free()
         traced = {"context": prompt + frames + 1, "tasks": int(ntask), "steps": summaries}
         clean = clean and bool(lib.phonon_flow_batch_sync(batch))
@@ -598,26 +615,28 @@ def q8_matvec_bench(pkg, lib, seed=1, calls=2000):
     x = rng.standard_normal(512).astype(np.float32)
     copies = 300
     h = ctypes.c_void_p()
-    assert lib.phonon_q8_device_create(w.ctypes.data, 2048, 512, copies, ctypes.byref(h))
+    assert lib.phonon_q8_device_create(w.ctypes.data, 2048, 512, copies, ctypes.byref(h)), \
+        last_error(lib)
     stream = ctypes.c_void_p()
-    assert lib.pgpu_stream_create(ctypes.byref(stream))
+    assert lib.pgpu_stream_create(ctypes.byref(stream)), last_error(lib)
     dx = pkg.DeviceBuffer(lib, 512 * 4)
     dx.upload(x)
     dy = pkg.DeviceBuffer(lib, 2048 * 4)
     for i in range(20):
-        assert lib.phonon_q8_device_matvec(h, i % copies, dx.ptr, dy.ptr, 1, stream)
+        assert lib.phonon_q8_device_matvec(h, i % copies, dx.ptr, dy.ptr, 1, stream), \
+            last_error(lib)
     timer = Timer(lib, stream)
     res = {}
     for label, rotate in (("rotating_300_copies", True), ("same_copy_cache_resident", False)):
         timer.start()
         for i in range(calls):
             assert lib.phonon_q8_device_matvec(h, i % copies if rotate else 0, dx.ptr, dy.ptr, 1,
-                                               stream)
+                                               stream), last_error(lib)
         ms = timer.stop_ms() / calls
         nbytes = lib.phonon_q8_device_bytes_per_call(h, 1)
         res[label] = {"us_per_call": round(ms * 1e3, 3),
                       "GBps": round(nbytes / (ms * 1e-3) / 1e9, 1)}
-    assert lib.phonon_q8_device_status(h, stream)
+    assert lib.phonon_q8_device_status(h, stream), last_error(lib)
     res["bytes_per_call"] = int(lib.phonon_q8_device_bytes_per_call(h, 1))
     res["launches_per_call"] = 1  # 512 columns: the projection splits the fp32 rows itself
     dx.free()
@@ -637,14 +656,15 @@ def gemv_valu_vs_mfma(pkg, lib, seed=3, calls=400, copies=300):
     events over `calls` back-to-back calls on one stream."""
     import speech_mac_amd.synthetic as syn
     stream = ctypes.c_void_p()
-    assert lib.pgpu_stream_create(ctypes.byref(stream))
+    assert lib.pgpu_stream_create(ctypes.byref(stream)), last_error(lib)
     timer = Timer(lib, stream)
     out = {}
     for rows, cols in ((2048, 512), (512, 2048)):
         rng = np.random.default_rng(seed + rows)
         w = syn.q8_matrix(rng, rows, cols)
         h = ctypes.c_void_p()
-        assert lib.phonon_q8_device_create(w.ctypes.data, rows, cols, copies, ctypes.byref(h))
+        assert lib.phonon_q8_device_create(w.ctypes.data, rows, cols, copies, ctypes.byref(h)), \
+            last_error(lib)
         x = rng.standard_normal((8, cols)).astype(np.float32)
         dx = pkg.DeviceBuffer(lib, x.nbytes)
         dx.upload(x)
@@ -664,7 +684,7 @@ def gemv_valu_vs_mfma(pkg, lib, seed=3, calls=400, copies=300):
                 row[name] = {"us_per_call": round(ms * 1e3, 2),
                              "GBps": round(nbytes / (ms * 1e-3) / 1e9, 1)}
             shape[f"batch_{batch}"] = row
-        assert lib.phonon_q8_device_status(h, stream)
+        assert lib.phonon_q8_device_status(h, stream), last_error(lib)
         out[f"{rows}x{cols}"] = shape
         dx.free()
         dy.free()
@@ -693,9 +713,10 @@ def flow_head_bench(pkg, lib, streams=64, calls=200, seed=11, graph=1, one_launc
     ew, eb = views.bf16(eos_w.reshape(1, 512), (1, 512)), views.bf16(eos_b, (1,))
     dev = ctypes.c_void_p()
     assert lib.phonon_flow_head_device_create(ctypes.byref(head), ctypes.byref(ew),
-                                              ctypes.byref(eb), streams, ctypes.byref(dev))
-    assert lib.phonon_flow_head_device_set_graph(dev, graph)
-    assert lib.phonon_flow_head_device_set_one_launch(dev, one_launch)
+                                              ctypes.byref(eb), streams, ctypes.byref(dev)), \
+                                                  last_error(lib)
+    assert lib.phonon_flow_head_device_set_graph(dev, graph), last_error(lib)
+    assert lib.phonon_flow_head_device_set_one_launch(dev, one_launch), last_error(lib)
     stream = lib.phonon_flow_head_device_stream(dev)
     cond = pkg.DeviceBuffer(lib, streams * 512 * 4)
     raw = pkg.DeviceBuffer(lib, streams * 32 * 4)
@@ -705,8 +726,8 @@ def flow_head_bench(pkg, lib, streams=64, calls=200, seed=11, graph=1, one_launc
     raw.upload(rng.standard_normal((streams, 32)).astype(np.float32))
     for _ in range(5):
         assert lib.phonon_flow_head_device_lsd(dev, streams, cond.ptr, raw.ptr, 0.7, lat.ptr,
-                                               eos.ptr)
-    assert lib.phonon_flow_head_device_sync(dev)
+                                               eos.ptr), last_error(lib)
+    assert lib.phonon_flow_head_device_sync(dev), last_error(lib)
     timer = Timer(lib, stream)
     timer.start()
     for _ in range(calls):
@@ -718,7 +739,8 @@ def flow_head_bench(pkg, lib, streams=64, calls=200, seed=11, graph=1, one_launc
     n1 = np.random.default_rng(seed + 3).standard_normal(32).astype(np.float32)
     o1 = np.zeros(32, np.float32)
     fpp = lambda a: a.ctypes.data_as(ctypes.POINTER(ctypes.c_float))  # noqa: E731
-    assert lib.phonon_flow_lsd_one_step(ctypes.byref(head), fpp(c1), fpp(n1), 0.7, fpp(o1))
+    assert lib.phonon_flow_lsd_one_step(ctypes.byref(head), fpp(c1), fpp(n1), 0.7, fpp(o1)), \
+        last_error(lib)
     t0 = time.perf_counter()
     reps = 100
     for _ in range(reps):
@@ -767,13 +789,14 @@ def frame_loop_bench(pkg, lib, layers=12, streams=64, frames=30, warmup=3, seed=
                     (512, 32))
     h = ctypes.c_void_p()
     assert lib.phonon_flow_head_device_create(ctypes.byref(head), ctypes.byref(ew),
-                                              ctypes.byref(eb), streams, ctypes.byref(h))
+                                              ctypes.byref(eb), streams, ctypes.byref(h)), \
+                                                  last_error(lib)
     assert lib.phonon_flow_head_device_set_frame(h, ctypes.byref(nw), ctypes.byref(nb),
-                                                 ctypes.byref(lv))
+                                                 ctypes.byref(lv)), last_error(lib)
     if shared_stream:
-        assert lib.phonon_flow_head_device_set_stream(h, d.stream)
-    assert lib.phonon_flow_head_device_set_graph(h, graph)
-    assert lib.phonon_flow_head_device_set_one_launch(h, one_launch)
+        assert lib.phonon_flow_head_device_set_stream(h, d.stream), last_error(lib)
+    assert lib.phonon_flow_head_device_set_graph(h, graph), last_error(lib)
+    assert lib.phonon_flow_head_device_set_one_launch(h, one_launch), last_error(lib)
     hs = lib.phonon_flow_head_device_stream(h)
     cond = pkg.DeviceBuffer(lib, streams * 512 * 4)
     raw = pkg.DeviceBuffer(lib, streams * 32 * 4)
@@ -782,24 +805,24 @@ def frame_loop_bench(pkg, lib, layers=12, streams=64, frames=30, warmup=3, seed=
     cond.upload(rng.standard_normal((streams, 512)).astype(np.float32))
     raw.upload(rng.standard_normal((streams, 32)).astype(np.float32))
     decoded, framed = ctypes.c_void_p(), ctypes.c_void_p()
-    assert lib.pgpu_event_create(ctypes.byref(decoded))
-    assert lib.pgpu_event_create(ctypes.byref(framed))
+    assert lib.pgpu_event_create(ctypes.byref(decoded)), last_error(lib)
+    assert lib.pgpu_event_create(ctypes.byref(framed)), last_error(lib)
     din, dout = d.din, d.dout
 
     def frame():
-        assert lib.phonon_flow_batch_step_device(d.batch, din, 10000.0, dout)
+        assert lib.phonon_flow_batch_step_device(d.batch, din, 10000.0, dout), last_error(lib)
         if not shared_stream:
-            assert lib.pgpu_event_record(decoded, d.stream)
-            assert lib.pgpu_stream_wait_event(hs, decoded)
+            assert lib.pgpu_event_record(decoded, d.stream), last_error(lib)
+            assert lib.pgpu_stream_wait_event(hs, decoded), last_error(lib)
         assert lib.phonon_flow_head_device_frame(h, streams, dout, cond.ptr, raw.ptr, 0.7, lat.ptr,
-                                                 eos.ptr, din)
+                                                 eos.ptr, din), last_error(lib)
         if not shared_stream:
-            assert lib.pgpu_event_record(framed, hs)
-            assert lib.pgpu_stream_wait_event(d.stream, framed)
+            assert lib.pgpu_event_record(framed, hs), last_error(lib)
+            assert lib.pgpu_stream_wait_event(d.stream, framed), last_error(lib)
 
     for _ in range(warmup):
         frame()
-    assert lib.pgpu_stream_sync(d.stream)
+    assert lib.pgpu_stream_sync(d.stream), last_error(lib)
     timer = Timer(lib, d.stream)
     timer.start()
     for _ in range(frames):
@@ -852,14 +875,14 @@ def pcm_bench(pkg, lib, seed=31, frames=256, stream_frames=40):
     mimi, model = helpers.pcm_model(lib, pkg, views, helpers.random_mimi(seed),
                                     helpers.random_pcm_convs(seed + 1))
     h = ctypes.c_void_p()
-    assert lib.phonon_pcm_state_create(model, ctypes.byref(h))
+    assert lib.phonon_pcm_state_create(model, ctypes.byref(h)), last_error(lib)
     x = np.random.default_rng(seed + 2).standard_normal((frames, 32)).astype(np.float32)
     raw = np.zeros(frames * 1920, np.float32)
     fpp = lambda a: a.ctypes.data_as(ctypes.POINTER(ctypes.c_float))  # noqa: E731
-    assert lib.phonon_pcm_process(h, fpp(x), 32, fpp(raw), raw.size, None, 0)
+    assert lib.phonon_pcm_process(h, fpp(x), 32, fpp(raw), raw.size, None, 0), last_error(lib)
     lib.phonon_pcm_state_reset(h)
     t0 = time.perf_counter()
-    assert lib.phonon_pcm_process(h, fpp(x), frames, fpp(raw), raw.size, None, 0)
+    assert lib.phonon_pcm_process(h, fpp(x), frames, fpp(raw), raw.size, None, 0), last_error(lib)
     bulk = time.perf_counter() - t0
     lib.phonon_pcm_state_reset(h)
     one = np.zeros(1920, np.float32)
@@ -867,7 +890,7 @@ def pcm_bench(pkg, lib, seed=31, frames=256, stream_frames=40):
     for f in range(stream_frames):
         xf = np.ascontiguousarray(x[f:f + 1])
         t0 = time.perf_counter()
-        assert lib.phonon_pcm_process(h, fpp(xf), 1, fpp(one), one.size, None, 0)
+        assert lib.phonon_pcm_process(h, fpp(xf), 1, fpp(one), one.size, None, 0), last_error(lib)
         per.append(time.perf_counter() - t0)
     lib.phonon_pcm_state_destroy(h)
     lib.phonon_pcm_model_destroy(model)

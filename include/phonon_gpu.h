@@ -181,6 +181,7 @@ int pgpu_q8_gemv(void *stream, const int8_t *values, const uint16_t *scales, int
 #define PGPU_FLOW_COUNTER_STRIDE 16 /* 32-bit words between phase counters */
 #define PGPU_FLOW_ATTN_ROUNDS 2    /* most 256-key splits per ATTN task */
 #define PGPU_FLOW_PART_WORDS 72    /* tagged words per split partial (66 used) */
+#define PGPU_FLOW_CLEAR_WORDS 2048 /* pgpu_flow_step.clear words zeroed per work-group */
 #define PGPU_FLOW_HANDOFF_COUNTER 0 /* pgpu_flow_step.tagged: counters and shared loads */
 #define PGPU_FLOW_HANDOFF_TAGGED 1  /* x, r, merged attention rows, split partials tagged */
 #define PGPU_FLOW_HANDOFF_PARTS 2   /* split partials tagged, the rest by counters */
@@ -208,13 +209,18 @@ typedef struct {
     float *part_acc;               /* (dev) [layer_count][tiles*16][8][max_splits][64] */
     float *part_ml;                /* (dev) [layer_count][tiles*16][8][ml_group] */
     int max_splits, ml_group;      /* ml_group: floats per (max, sum) group, % 32 == 0 */
-    const int32_t *tables, *positions; /* (dev) */
+    const int32_t *tables, *positions; /* (dev); not written by the step */
+    int pos_delta;                 /* stream s is at position positions[s] + pos_delta */
     int table_stride;
     const float *rope;             /* (dev) [8192][32] (cos, sin) */
     const uint32_t *schedule;      /* (dev) one descriptor per work-group */
     unsigned tasks;
     unsigned *phase;               /* (dev) [layer_count][tiles][KINDS] x COUNTER_STRIDE, 0 */
     unsigned *split_done;          /* (dev) [layer_count][tiles*16][8], 0 */
+    unsigned *clear;               /* (dev) clear_words words the step sets to 0 (the
+                                      counters of the next step), or NULL */
+    unsigned clear_words;          /* a multiple of 4, at most PGPU_FLOW_CLEAR_WORDS per
+                                      task of the schedule */
     int attn_rounds;               /* 256-key splits per ATTN task, 1..PGPU_FLOW_ATTN_ROUNDS */
     int *status;
     uint64_t *trace;               /* (dev) NULL, or [tasks][4]: start, inputs ready, end
@@ -236,7 +242,7 @@ typedef struct {
     uint64_t *parts;               /* (dev, all but COUNTER) [layer_count][tiles*16][8]
                                       [max_splits][PGPU_FLOW_PART_WORDS]: P.V [64], max,
                                       sum */
-    const uint32_t *epoch;         /* (dev, all but COUNTER) this step's tag, never 0 */
+    uint32_t tag;                  /* (all but COUNTER) this step's tag, never 0 */
 } pgpu_flow_step;
 
 /* Placement of each tile's projection chain in a task list, on a model
@@ -263,12 +269,11 @@ size_t pgpu_flow_schedule(size_t streams, size_t layers, const size_t *units,
                           const pgpu_flow_placement *place, int prefill, uint32_t *schedule,
                           size_t capacity);
 /* prefill = 1: pseudo-streams of one stream share its block table, so an
- * ATTN task waits for the QKV tasks of every tile (one layer-wide count). */
+ * ATTN task waits for the QKV tasks of every tile (one layer-wide count).
+ * A step is this one launch: it leaves `positions` as they are (the caller
+ * counts the steps in pos_delta) and zeroes `clear` for the next step, so
+ * nothing runs between two steps. */
 int pgpu_flow_launch(void *stream, const pgpu_flow_step *step, const pgpu_paged_kv *kv);
-/* After a step: zero `n` counter words, advance positions[0..streams) and,
- * if `epoch` is not NULL, the tagged mode's tag (skipping 0). */
-int pgpu_flow_finish(void *stream, unsigned *counters, size_t n, int32_t *positions,
-                     int streams, uint32_t *epoch);
 /* Fills n 32-bit words with `value` (a kernel: usable inside a captured graph). */
 int pgpu_fill_u32(void *stream, uint32_t *dst, size_t n, uint32_t value);
 
@@ -582,8 +587,15 @@ int pgpu_rope(void *stream, float *values, int heads, int head_width, const floa
 int pgpu_kv_copy(void *stream, const pgpu_paged_kv *kv, const int32_t *table,
                  int first_position, int count, int first_layer, int layers, float *keys,
                  float *values, size_t capacity, int to_contiguous, int *status);
+/* dst[0..count) (count even) = N(0,1) values from `seed` and each pair's
+ * index, as pgpu_fill_normal_plan dispatches: it returns their number and,
+ * for i below it, the pairs [*first, *first + *pairs) dispatch i fills, at
+ * most PGPU_FILL_MAX_GROUPS work-groups of 256 pairs each. */
+#define PGPU_FILL_MAX_GROUPS (1u << 23)
+size_t pgpu_fill_normal_plan(size_t count, size_t i, size_t *first, size_t *pairs);
 int pgpu_fill_normal(void *stream, float *dst, size_t count, uint64_t seed);
-int pgpu_advance_positions(void *stream, int32_t *positions, int streams);
+/* positions[0..streams) += delta. */
+int pgpu_advance_positions(void *stream, int32_t *positions, int streams, int delta);
 /* dst[r][0..width) = src[map[r]][0..width) for r < rows (int32 rows; map
  * entries must index rows of src). */
 int pgpu_gather_rows(void *stream, int32_t *dst, const int32_t *src, const int32_t *map,

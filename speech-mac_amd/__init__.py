@@ -275,7 +275,8 @@ EXPORTS = {
     "pgpu_rope": (_i, [_vp, _vp, _i, _i, _vp, _vp]),
     "pgpu_kv_copy": (_i, [_vp, _kvp, _vp, _i, _i, _i, _i, _vp, _vp, _sz, _i, _vp]),
     "pgpu_fill_normal": (_i, [_vp, _vp, _sz, ctypes.c_uint64]),
-    "pgpu_advance_positions": (_i, [_vp, _vp, _i]),
+    "pgpu_advance_positions": (_i, [_vp, _vp, _i, _i]),
+    "pgpu_fill_normal_plan": (_sz, [_sz, _sz, _szp, _szp]),
     "pgpu_gather_rows": (_i, [_vp, _vp, _vp, _vp, _i, _i]),
     "pgpu_fill_u32": (_i, [_vp, _vp, _sz, ctypes.c_uint32]),
     "pgpu_flow_schedule": (_sz, [_sz, _sz, _szp, _vp, _i, ctypes.POINTER(ctypes.c_uint32),
@@ -354,7 +355,6 @@ EXPORTS = {
     "phonon_flow_head_device_frame": (_i, [_vp, _sz, _vp, _vp, _vp, _f, _vp, _vp, _vp]),
     "phonon_flow_head_device_stream": (_vp, [_vp]),
     "phonon_flow_head_device_sync": (_i, [_vp]),
-    "pgpu_flow_finish": (_i, [_vp, _vp, _sz, _vp, _i, _vp]),
 }
 
 _LIB = None

@@ -17,7 +17,8 @@ struct AttnArgs {
     int layer;
     const int32_t *tables;
     int table_stride;
-    const int32_t *positions; // keys attended = positions[s] + 1
+    const int32_t *positions; // keys attended = positions[s] + pos_delta + 1
+    int pos_delta = 0;        // steps the stored positions trail the step's
     int streams, max_splits;
     float *part_acc;          // [streams*8*max_splits][64]
     float *part_ml;           // [streams*8*max_splits][2]
@@ -98,7 +99,7 @@ __device__ inline int attend_unit(const AttnArgs &a, int head, int split0, int s
     // table entries (index clamped into the row; entries past the context
     // are not used) and the gate's first check.
     const int32_t *__restrict__ table = a.tables + (size_t)s * a.table_stride;
-    const int position = exists ? a.positions[s] : -1;
+    const int position = exists ? a.positions[s] + a.pos_delta : -1;
     int ids[ROUNDS][kBlocksPerWave];
 #pragma unroll
     for (int r = 0; r < ROUNDS; r++)

@@ -212,9 +212,9 @@ __global__ __launch_bounds__(256) void k_fill_normal(float *__restrict__ dst, si
     *(float2 *)(dst + 2 * i) = make_float2(rad * cn, rad * sn);
 }
 
-__global__ void k_advance(int32_t *positions, int streams) {
+__global__ void k_advance(int32_t *positions, int streams, int delta) {
     const int s = blockIdx.x * 256 + threadIdx.x;
-    if (s < streams) positions[s] += 1;
+    if (s < streams) positions[s] += delta;
 }
 
 __global__ void k_fill_u32(uint32_t *dst, size_t n, uint32_t value) {
@@ -288,24 +288,38 @@ extern "C" int pgpu_kv_copy(void *stream, const pgpu_paged_kv *kv, const int32_t
     return launch_ok(__func__);
 }
 
+// A dispatch packet counts work-items in 32 bits (grid_size_x), so one
+// dispatch of this kernel covers at most PGPU_FILL_MAX_GROUPS work-groups of
+// 256 work-items (2^31 pairs): a 103 GB pool is 12.9 G pairs, i.e. 6
+// dispatches. Dispatch i fills pairs [first, first + pairs).
+extern "C" size_t pgpu_fill_normal_plan(size_t count, size_t i, size_t *first, size_t *pairs) {
+    const size_t total = count / 2, per = (size_t)PGPU_FILL_MAX_GROUPS * 256;
+    const size_t n = (total + per - 1) / per;
+    if (i < n && first && pairs) {
+        *first = i * per;
+        *pairs = total - i * per < per ? total - i * per : per;
+    }
+    return n;
+}
+
 extern "C" int pgpu_fill_normal(void *stream, float *dst, size_t count, uint64_t seed) {
-    if (count % 2) return bad_arguments(__func__);
-    const size_t pairs = count / 2;
-    const size_t grid = (pairs + 255) / 256;
-    const size_t max_grid = (size_t)1 << 30;
-    for (size_t first = 0; first < grid; first += max_grid) {
-        const size_t chunk = grid - first < max_grid ? grid - first : max_grid;
-        hipLaunchKernelGGL(k_fill_normal, dim3((unsigned)chunk), dim3(256), 0,
-                           (hipStream_t)stream, dst, pairs, first * 256, seed);
+    if (!dst || count % 2) return bad_arguments(__func__);
+    const size_t n = pgpu_fill_normal_plan(count, 0, nullptr, nullptr);
+    for (size_t i = 0; i < n; i++) {
+        size_t first = 0, pairs = 0;
+        pgpu_fill_normal_plan(count, i, &first, &pairs);
+        const unsigned groups = (unsigned)((pairs + 255) / 256);
+        hipLaunchKernelGGL(k_fill_normal, dim3(groups), dim3(256), 0, (hipStream_t)stream, dst,
+                           first + pairs, first, seed);
         if (!launch_ok(__func__)) return 0;
     }
     return 1;
 }
 
-extern "C" int pgpu_advance_positions(void *stream, int32_t *positions, int streams) {
-    if (streams <= 0) return bad_arguments(__func__);
+extern "C" int pgpu_advance_positions(void *stream, int32_t *positions, int streams, int delta) {
+    if (!positions || streams <= 0) return bad_arguments(__func__);
     hipLaunchKernelGGL(k_advance, dim3((streams + 255) / 256), dim3(256), 0,
-                       (hipStream_t)stream, positions, streams);
+                       (hipStream_t)stream, positions, streams, delta);
     return launch_ok(__func__);
 }
 

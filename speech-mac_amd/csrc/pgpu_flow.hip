@@ -232,6 +232,7 @@ __device__ inline GemmArgs base_args(const pgpu_flow_step &f, const pgpu_flow_la
     a.status = f.status;
     a.wt_out = true;  // read by tasks on other XCDs within the launch
     a.tp = TagPoll{tag, f.status, wait_ticks(f), false};
+    a.pos_delta = f.pos_delta;
     return a;
 }
 
@@ -352,6 +353,7 @@ __device__ inline void attention_task(const pgpu_flow_step &f, const pgpu_paged_
     a.tables = f.tables;
     a.table_stride = f.table_stride;
     a.positions = f.positions;
+    a.pos_delta = f.pos_delta;
     a.streams = f.streams;
     a.max_splits = f.max_splits;
     a.part_acc = nullptr;
@@ -369,12 +371,11 @@ __device__ inline void attention_task(const pgpu_flow_step &f, const pgpu_paged_
                                  tagged_rows(f, layer, ROWS_Q),
                                  (size_t)f.tiles * 16 * kWidth,
                                  TagPoll{tag, f.status, wait_ticks(f), false}, &f};
-        state = attend_unit<R>(a, head, split0, s, wave, sh, true, aa, mm, ll, count,
-                                         gate, R, true, 1);
+        state = attend_unit<R>(a, head, split0, s, wave, sh, true, aa, mm, ll, count, gate, R,
+                               true, 1);
     } else {
-        state = attend_unit<R>(a, head, split0, s, wave, sh, true, aa, mm, ll, count,
-                                         ready, R, !PRE,
-                                         tagged_parts && !MO ? 2 : 1);
+        state = attend_unit<R>(a, head, split0, s, wave, sh, true, aa, mm, ll, count, ready, R,
+                               !PRE, tagged_parts && !MO ? 2 : 1);
     }
     if constexpr (MO) {
         // Every split's partial goes out as a tagged record; the tile's
@@ -466,8 +467,14 @@ __device__ inline void flow_step_task(const pgpu_flow_step &f, const pgpu_paged_
     uint16_t *lds = (uint16_t *)lds4;
     trace_mark(f, 0);
     const uint32_t desc = f.schedule[blockIdx.x];
-    // written by the previous launch only
-    const uint32_t tag = MODE != PGPU_FLOW_HANDOFF_COUNTER ? *f.epoch : 0u;
+    // The next step's counters: zeroed by the first work-groups, one 16-byte
+    // store per lane (no task of this step reads them; the launch boundary
+    // orders the stores before the next step).
+    if (blockIdx.x * PGPU_FLOW_CLEAR_WORDS < f.clear_words) {
+        const unsigned i = blockIdx.x * PGPU_FLOW_CLEAR_WORDS + threadIdx.x * 4;
+        if (i < f.clear_words) *(uint4 *)(f.clear + i) = make_uint4(0u, 0u, 0u, 0u);
+    }
+    const uint32_t tag = MODE != PGPU_FLOW_HANDOFF_COUNTER ? f.tag : 0u;
     const int kind = desc & 7, layer = (desc >> 3) & 63, tile = (desc >> 9) & 255,
               index = desc >> 17;
     const pgpu_flow_layer &ly = f.layers[layer];
@@ -665,17 +672,6 @@ void launch_rounds(const pgpu_flow_step *step, const pgpu_paged_kv *kv, hipStrea
         launch_step<Q8, PRE, 2>(step, kv, stream);
 }
 
-__global__ void k_flow_finish(unsigned *counters, size_t n, int32_t *positions, int streams,
-                              uint32_t *epoch) {
-    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    for (size_t j = i; j < n; j += (size_t)gridDim.x * blockDim.x) counters[j] = 0u;
-    if (i < (size_t)streams) positions[i] += 1;
-    if (i == 0 && epoch) {
-        const uint32_t next = *epoch + 1u;
-        *epoch = next ? next : 1u;
-    }
-}
-
 }  // namespace
 }  // namespace pgpu
 
@@ -693,7 +689,10 @@ extern "C" int pgpu_flow_launch(void *stream, const pgpu_flow_step *step,
         step->attn_rounds < 1 || step->attn_rounds > PGPU_FLOW_ATTN_ROUNDS ||
         step->tagged < PGPU_FLOW_HANDOFF_COUNTER || step->tagged > PGPU_FLOW_HANDOFF_MERGE_OUT ||
         (step->tagged != PGPU_FLOW_HANDOFF_COUNTER &&
-         (!step->parts || !step->epoch || step->max_splits > 32)) ||
+         (!step->parts || !step->tag || step->max_splits > 32)) ||
+        step->pos_delta < 0 || step->clear_words % 4 ||
+        (step->clear_words && (!step->clear || (step->clear_words + PGPU_FLOW_CLEAR_WORDS - 1) /
+                                                       PGPU_FLOW_CLEAR_WORDS > step->tasks)) ||
         ((step->tagged == PGPU_FLOW_HANDOFF_TAGGED ||
           step->tagged == PGPU_FLOW_HANDOFF_MERGE_OUT) && !step->rows) ||
         step->pool_offset < 0 || step->pool_offset + step->layer_count > kv->layers)
@@ -709,14 +708,4 @@ extern "C" int pgpu_flow_launch(void *stream, const pgpu_flow_step *step,
         launch_rounds<false, false>(step, kv, (hipStream_t)stream);
     }
     return launch_ok("pgpu_flow_launch");
-}
-
-extern "C" int pgpu_flow_finish(void *stream, unsigned *counters, size_t n, int32_t *positions,
-                                int streams, uint32_t *epoch) {
-    if (!counters || !n || !positions || streams <= 0) return bad_arguments("pgpu_flow_finish");
-    const size_t work = n > (size_t)streams ? n : (size_t)streams;
-    const unsigned blocks = (unsigned)((work + 255) / 256 < 1024 ? (work + 255) / 256 : 1024);
-    hipLaunchKernelGGL(k_flow_finish, dim3(blocks), dim3(256), 0, (hipStream_t)stream, counters,
-                       n, positions, streams, epoch);
-    return launch_ok("pgpu_flow_finish");
 }

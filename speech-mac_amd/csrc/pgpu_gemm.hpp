@@ -182,7 +182,8 @@ struct GemmArgs {
     int layer;
     const int32_t *tables;
     int table_stride;
-    const int32_t *positions; // QKV and SRC_ATTN
+    const int32_t *positions; // QKV and SRC_ATTN: positions[s] + pos_delta
+    int pos_delta = 0;        // steps the stored positions trail the step's
     const float2 *rope;       // [8192][32] (cos, sin)
     int *status;
     bool wt_out;              // STORE / RESIDUAL / GELU_SPLIT outputs write-through
@@ -725,7 +726,7 @@ __device__ inline bool prologue_attn(const GemmArgs &a, int st, uint16_t *bsh) {
         const int n = 2 * wave + i, s = st * 16 + n;
         float v[8];
         if (s < a.streams) {
-            const int count = a.positions[s] + 1;
+            const int count = a.positions[s] + a.pos_delta + 1;
             const int nsplit = min((count + kSplitKeys - 1) / kSplitKeys, a.max_splits);
             const size_t first = ((size_t)s * kHeads + h) * a.max_splits;
             bad |= merge_splits<8>(a.part_acc + first * 64, a.part_ml + first * 2, nsplit,
@@ -833,7 +834,7 @@ __device__ inline void load_epilogue_static(EpiOperands &e, const GemmArgs &a, i
     } else if constexpr (EPI == EPI_QKV) {
         // Positions past the rope table or the block table, and block ids
         // outside the pool, are errors: flagged, and nothing is written.
-        int pos = a.positions[s];
+        int pos = a.positions[s] + a.pos_delta;
         e.ok = pos >= 0 && pos < kMaxPositions && (pos >> 4) < a.table_stride;
         e.block = 0;
         if (e.ok) {
@@ -1014,7 +1015,8 @@ __device__ inline void gemm_wide_task(const GemmArgs &a, int bx, int st, uint16_
     if (active && half == 0) load_epilogue_static<EPI>(e, a, s, row0, live);
     int position = 0;
     if constexpr (SRC == SRC_ATTN_TAGGED)
-        if (lane < 16 && st * 16 + lane < a.streams) position = a.positions[st * 16 + lane];
+        if (lane < 16 && st * 16 + lane < a.streams)
+            position = a.positions[st * 16 + lane] + a.pos_delta;
     wait();
     if (active && half == 0) load_epilogue_dynamic<EPI>(e, a, st, s, row0, live);
 

@@ -64,12 +64,13 @@ struct PhononFlowBatch {
         size_t cap, cap_layers;     /* padded streams and layers the buffers hold */
         float *act, *part_acc, *part_ml;
         uint16_t *hidden;
-        unsigned *counters;         /* all zero between steps */
+        unsigned *counters;         /* two sets of counter_words: the next step's set is
+                                       all zero (the step before zeroes it) */
         size_t counter_words;
+        int parity;                 /* the set the next step uses */
         uint64_t *rows, *parts;     /* (dev) tagged mode's hand-off words (pgpu_flow_step) */
         size_t rows_words, parts_words;
-        uint32_t *epoch;            /* (dev) tagged mode's tag of the next step */
-        uint32_t epoch_host;        /* the same, as far as the host has enqueued */
+        uint32_t tag;               /* tagged mode's tag of the next step, never 0 */
         int tagged_set;             /* -1: by batch size, else the caller's choice */
         uint32_t *schedule, *host_schedule;
         size_t schedule_cap, host_cap, tasks;
@@ -89,6 +90,8 @@ struct PhononFlowBatch {
     int *status;
     pgpu_attention_scratch scratch;
     size_t *host_positions;
+    int pos_lag;                    /* one-launch steps the device positions trail
+                                       host_positions by (pgpu_flow_step.pos_delta) */
     /* Captured steps, keyed by what the capture baked in. Two entries, so a
      * caller that alternates two buffers (output feeding the next input)
      * replays both without capturing again. */
@@ -98,8 +101,6 @@ struct PhononFlowBatch {
         float theta;
         const float *input;
         float *output;
-        int flow;
-        unsigned version;
     } graphs[2];
     size_t graph_victim;
     int eager;                         /* launch kernels directly, no graph */
@@ -413,7 +414,7 @@ void phonon_flow_batch_destroy(PhononFlowBatch *b) {
                     b->rows, b->xh, b->positions, b->tables, b->status,
                     b->scratch.part_acc, b->scratch.part_ml, b->table_src, b->table_map,
                     b->fl.act, b->fl.part_acc, b->fl.part_ml, b->fl.hidden, b->fl.counters,
-                    b->fl.rows, b->fl.parts, b->fl.epoch, b->fl.schedule};
+                    b->fl.rows, b->fl.parts, b->fl.schedule};
     for (size_t i = 0; i < sizeof(bufs) / sizeof(bufs[0]); i++)
         pgpu_free(bufs[i]);
     pgpu_stream_destroy(b->stream);
@@ -519,6 +520,7 @@ int phonon_flow_batch_set_streams(PhononFlowBatch *b, size_t streams, const size
     if (!ok)
         return 0;
     memcpy(b->host_positions, positions, streams * sizeof(size_t));
+    b->pos_lag = 0;
     b->streams = streams;
     b->pre.active = 0;
     return 1;
@@ -540,8 +542,21 @@ int ph_batch_set_single(PhononFlowBatch *b, size_t position, const int32_t *tabl
         !pgpu_copy_d2d(b->stream, b->tables, table_dev, b->table_len * sizeof(int32_t)))
         return 0;
     b->host_positions[0] = position;
+    b->pos_lag = 0;
     b->streams = 1;
     b->pre.active = 0;
+    return 1;
+}
+
+/* Brings the device positions up to host_positions: a one-launch step
+ * leaves them as they are (its kernels add pos_lag), every other kernel
+ * reads them as stored. */
+static int fold_positions(PhononFlowBatch *b) {
+    if (!b->pos_lag)
+        return 1;
+    if (!pgpu_advance_positions(b->stream, b->positions, (int)b->streams, b->pos_lag))
+        return 0;
+    b->pos_lag = 0;
     return 1;
 }
 
@@ -673,8 +688,9 @@ int ph_batch_enqueue_layers(PhononFlowBatch *b, size_t first, size_t count, size
         return 0;
     const float *rope = ph_rope_table(theta);
     b->splits = splits_for(b, 0);
-    return rope && enqueue_group(b, b->stream, 0, b->streams, first, count, pool_offset, input,
-                                 output, rope);
+    return rope && fold_positions(b) &&
+           enqueue_group(b, b->stream, 0, b->streams, first, count, pool_offset, input, output,
+                         rope);
 }
 
 /* Stream groups of the step: tiles of 16 streams dealt into `groups` runs.
@@ -715,7 +731,7 @@ static int enqueue_step(PhononFlowBatch *b, const float *input, float *output, f
         if (!pgpu_event_record(b->join[g - 1], b->side[g - 1]) ||
             !pgpu_stream_wait_event(b->stream, b->join[g - 1]))
             return 0;
-    return pgpu_advance_positions(b->stream, b->positions, (int)b->streams);
+    return pgpu_advance_positions(b->stream, b->positions, (int)b->streams, 1);
 }
 
 /* ------------------------------------------------------ one-launch step -- */
@@ -755,11 +771,9 @@ static int flow_usable(const PhononFlowBatch *b, int prefill) {
 /* Every tagged hand-off word to tag 0 and the next step's tag to 1: no
  * stale word carries a tag a later step uses until the tag wraps. */
 static int flow_clear_tags(PhononFlowBatch *b) {
-    const uint32_t one = 1;
-    b->fl.epoch_host = 1;
+    b->fl.tag = 1;
     return pgpu_memset(b->stream, b->fl.rows, 0, b->fl.rows_words * sizeof(uint64_t)) &&
-           pgpu_memset(b->stream, b->fl.parts, 0, b->fl.parts_words * sizeof(uint64_t)) &&
-           pgpu_copy_h2d(b->stream, b->fl.epoch, &one, sizeof(one));
+           pgpu_memset(b->stream, b->fl.parts, 0, b->fl.parts_words * sizeof(uint64_t));
 }
 
 /* Grows the per-layer buffers of the one-launch step to hold `streams`
@@ -786,22 +800,23 @@ static int flow_reserve(PhononFlowBatch *b, size_t streams) {
     b->fl.cap = b->fl.cap_layers = 0;
     b->fl.streams = 0; /* the schedule is rebuilt against the new buffers */
     const size_t groups = new_layers * new_cap * PH_HEADS;
-    b->fl.counter_words = new_layers * (new_cap / 16) * PGPU_FLOW_KINDS *
-                              PGPU_FLOW_COUNTER_STRIDE + groups;
+    /* a multiple of 64 words: each set starts on a 256-byte line */
+    b->fl.counter_words =
+        (new_layers * (new_cap / 16) * PGPU_FLOW_KINDS * PGPU_FLOW_COUNTER_STRIDE + groups + 63) /
+        64 * 64;
     b->fl.act = pgpu_malloc(new_layers * 4 * new_cap * PH_WIDTH * sizeof(float));
     b->fl.part_acc = pgpu_malloc(groups * b->max_splits * 64 * sizeof(float));
     b->fl.part_ml = pgpu_malloc(groups * flow_ml_group(b) * sizeof(float));
     b->fl.hidden = pgpu_malloc(new_layers * new_cap * PH_FFN * 3 * sizeof(uint16_t));
-    b->fl.counters = pgpu_malloc(b->fl.counter_words * sizeof(unsigned));
+    b->fl.counters = pgpu_malloc(2 * b->fl.counter_words * sizeof(unsigned));
     b->fl.rows_words = new_layers * 6 * new_cap * PH_WIDTH;
     b->fl.parts_words = groups * b->max_splits * PGPU_FLOW_PART_WORDS;
     b->fl.rows = pgpu_malloc(b->fl.rows_words * sizeof(uint64_t));
     b->fl.parts = pgpu_malloc(b->fl.parts_words * sizeof(uint64_t));
-    if (!b->fl.epoch)
-        b->fl.epoch = pgpu_malloc(sizeof(uint32_t));
+    b->fl.parity = 0;
     if (!b->fl.act || !b->fl.part_acc || !b->fl.part_ml || !b->fl.hidden || !b->fl.counters ||
-        !b->fl.rows || !b->fl.parts || !b->fl.epoch ||
-        !pgpu_memset(b->stream, b->fl.counters, 0, b->fl.counter_words * sizeof(unsigned)) ||
+        !b->fl.rows || !b->fl.parts ||
+        !pgpu_memset(b->stream, b->fl.counters, 0, 2 * b->fl.counter_words * sizeof(unsigned)) ||
         !pgpu_memset(b->stream, b->fl.hidden, 0,
                      new_layers * new_cap * PH_FFN * 3 * sizeof(uint16_t)) ||
         !flow_clear_tags(b) || !pgpu_stream_sync(b->stream))
@@ -869,16 +884,13 @@ static int flow_schedule(PhononFlowBatch *b, int prefill) {
 
 /* Makes buffers and schedule ready for the batch's current streams (outside
  * any graph capture); called once per one-launch step. The tagged mode's
- * tag advances once per step (pgpu_flow_finish, skipping 0): before it
- * could come back to a value a stale word still carries, every word is
- * cleared. */
+ * tag advances once per step: before it could come back to a value a stale
+ * word still carries, every word is cleared. */
 static int flow_prepare(PhononFlowBatch *b, int prefill) {
     if (!flow_reserve(b, b->streams) || !flow_schedule(b, prefill))
         return 0;
-    if (b->fl.epoch_host >= UINT32_MAX - 1 &&
-        !(pgpu_stream_sync(b->stream) && flow_clear_tags(b)))
+    if (b->fl.tag >= UINT32_MAX - 1 && !(pgpu_stream_sync(b->stream) && flow_clear_tags(b)))
         return 0;
-    b->fl.epoch_host++;
     return 1;
 }
 
@@ -898,8 +910,10 @@ static int flow_tagged(const PhononFlowBatch *b) {
                                                     : PGPU_FLOW_HANDOFF_COUNTER;
 }
 
-/* One step as a single launch, then the launch that zeroes its counters and
- * advances the positions. */
+/* One step as a single launch. It uses one set of counters and zeroes the
+ * other for the next step, and reads the positions as stored plus pos_lag
+ * (the steps since they were last written), so that nothing has to run
+ * between two steps. */
 static int enqueue_flow(PhononFlowBatch *b, const float *input, float *output, float theta) {
     const PhononFlowModel *m = b->model;
     const float *rope = ph_rope_table(theta);
@@ -907,6 +921,12 @@ static int enqueue_flow(PhononFlowBatch *b, const float *input, float *output, f
     if (!rope)
         return 0;
     const size_t phase_words = layers * tiles * PGPU_FLOW_KINDS * PGPU_FLOW_COUNTER_STRIDE;
+    const size_t used = (phase_words + layers * tiles * 16 * PH_HEADS + 3) / 4 * 4;
+    unsigned *set = b->fl.counters + (size_t)b->fl.parity * b->fl.counter_words;
+    unsigned *next = b->fl.counters + (size_t)(1 - b->fl.parity) * b->fl.counter_words;
+    if (used > b->fl.counter_words ||
+        (used + PGPU_FLOW_CLEAR_WORDS - 1) / PGPU_FLOW_CLEAR_WORDS > b->fl.tasks)
+        return ph_fail("flow step: counters outgrow the clearing work-groups");
     const pgpu_flow_step f = {.layers = m->flow_layers,
                               .layer_count = (int)layers,
                               .q8 = m->q8,
@@ -924,12 +944,15 @@ static int enqueue_flow(PhononFlowBatch *b, const float *input, float *output, f
                               .ml_group = (int)flow_ml_group(b),
                               .tables = b->tables,
                               .positions = b->positions,
+                              .pos_delta = b->pos_lag,
                               .table_stride = (int)b->table_len,
                               .rope = rope,
                               .schedule = b->fl.schedule,
                               .tasks = (unsigned)b->fl.tasks,
-                              .phase = b->fl.counters,
-                              .split_done = b->fl.counters + phase_words,
+                              .phase = set,
+                              .split_done = set + phase_words,
+                              .clear = next,
+                              .clear_words = (unsigned)used,
                               .status = b->status,
                               .trace = b->fl.trace_cap >= b->fl.tasks ? b->fl.trace : NULL,
                               .attn_rounds = b->fl.rounds,
@@ -937,13 +960,15 @@ static int enqueue_flow(PhononFlowBatch *b, const float *input, float *output, f
                               .tagged = flow_tagged(b),
                               .rows = b->fl.rows,
                               .parts = b->fl.parts,
-                              .epoch = b->fl.epoch};
-    const size_t used = phase_words + layers * tiles * 16 * PH_HEADS;
-    return (!b->time_before || pgpu_event_record(b->time_before, b->stream)) &&
-           pgpu_flow_launch(b->stream, &f, &b->pool->kv) &&
-           (!b->time_after || pgpu_event_record(b->time_after, b->stream)) &&
-           pgpu_flow_finish(b->stream, b->fl.counters, used, b->positions, (int)b->streams,
-                            b->fl.epoch);
+                              .tag = b->fl.tag};
+    if (!((!b->time_before || pgpu_event_record(b->time_before, b->stream)) &&
+          pgpu_flow_launch(b->stream, &f, &b->pool->kv) &&
+          (!b->time_after || pgpu_event_record(b->time_after, b->stream))))
+        return 0;
+    b->fl.parity = 1 - b->fl.parity;
+    b->fl.tag++;
+    b->pos_lag++;
+    return 1;
 }
 
 /* Work entries of the prefill attention (pgpu_prefill_attention): for each
@@ -1207,6 +1232,7 @@ static int set_prefill(PhononFlowBatch *b, size_t streams, const size_t *first,
     free(map);
     if (ok) {
         b->streams = total;
+        b->pos_lag = 0;
         b->pre.active = 1;
     }
     return ok;
@@ -1341,10 +1367,13 @@ int phonon_flow_batch_step_device(PhononFlowBatch *b, const float *inputs, float
         if (b->host_positions[s] >= b->max_positions)
             return 0;
     const int flow = flow_usable(b, 0);
-    if (flow && !flow_prepare(b, 0))
+    /* A one-launch step reads the positions as stored plus pos_lag; the
+     * phase kernels (and a captured graph of them) read them as stored. */
+    if (flow ? !flow_prepare(b, 0) : !fold_positions(b))
         return 0;
-    /* A one-launch step is two kernels: launched directly, without the graph
-     * launch's overhead (measured 7 us per step faster on MI355X). */
+    /* A one-launch step is one kernel, launched directly (a graph launch
+     * costs 7 us per step more on MI355X), with the step's tag, counter set
+     * and position lag as arguments: it is never captured. */
     if (b->eager || b->time_before || flow) {
         b->splits = splits_for(b, 0);
         if (!(flow ? enqueue_flow(b, inputs, outputs, theta)
@@ -1354,17 +1383,15 @@ int phonon_flow_batch_step_device(PhononFlowBatch *b, const float *inputs, float
             b->host_positions[s]++;
         return 1;
     }
-    /* A captured step covers contexts up to its attention grid (phase by
-     * phase) or its task schedule (one launch): captured with 256 positions
-     * of headroom, re-captured when a context outgrows it. */
+    /* A captured phase-by-phase step covers contexts up to its attention
+     * grid: captured with 256 positions of headroom, re-captured when a
+     * context outgrows it. */
     const size_t need = splits_for(b, 0);
     void *exec = NULL;
     for (size_t i = 0; i < 2 && !exec; i++)
         if (b->graphs[i].exec && b->graphs[i].streams == b->streams &&
-            b->graphs[i].flow == flow &&
-            (flow ? b->graphs[i].version == b->fl.version : b->graphs[i].splits >= need) &&
-            b->graphs[i].theta == theta && b->graphs[i].input == inputs &&
-            b->graphs[i].output == outputs)
+            b->graphs[i].splits >= need && b->graphs[i].theta == theta &&
+            b->graphs[i].input == inputs && b->graphs[i].output == outputs)
             exec = b->graphs[i].exec;
     if (!exec) {
         const size_t slot = b->graph_victim;
@@ -1373,8 +1400,7 @@ int phonon_flow_batch_step_device(PhononFlowBatch *b, const float *inputs, float
         b->splits = splits_for(b, PH_SPLIT_KEYS);
         if (!ph_rope_table(theta) || !pgpu_graph_begin(b->stream))
             return 0;
-        const int enqueued = flow ? enqueue_flow(b, inputs, outputs, theta)
-                                  : enqueue_step(b, inputs, outputs, theta);
+        const int enqueued = enqueue_step(b, inputs, outputs, theta);
         const int ended = pgpu_graph_end(b->stream, &exec);
         if (!enqueued || !ended) {
             pgpu_graph_destroy(exec);
@@ -1386,8 +1412,6 @@ int phonon_flow_batch_step_device(PhononFlowBatch *b, const float *inputs, float
         b->graphs[slot].theta = theta;
         b->graphs[slot].input = inputs;
         b->graphs[slot].output = outputs;
-        b->graphs[slot].flow = flow;
-        b->graphs[slot].version = b->fl.version;
         b->graph_victim = 1 - slot;
     }
     if (!pgpu_graph_launch(exec, b->stream))
