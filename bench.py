@@ -145,14 +145,33 @@ def step_bytes(layers, contexts):
                                                          + KV_BYTES_PER_KEY))
 
 
+# Untimed steps before the warmup: the GPU's clock ramps up over the first
+# tens of milliseconds of load (measured on MI355X at B=64: steps 10-19 of a
+# cold start take 696 us, steps 20-29 680 us although they attend more keys;
+# after a 2 s idle the next 10 steps take 849 us and need ~20 steps to come
+# back). A serving loop runs at the settled clock.
+SETTLE_STEPS = 80
+
+
 def run_decode(pkg, lib, layers, streams, lengths, steps, warmup, seed, groups=None,
-               eager=False):
-    # headroom: the timed steps, then the roofline's timed launches
-    d = DecodeSetup(pkg, lib, layers, streams, lengths, steps + warmup + 41, seed)
+               eager=False, settle=SETTLE_STEPS):
+    # headroom: the settling steps, or the timed steps and then the
+    # roofline's timed launches
+    d = DecodeSetup(pkg, lib, layers, streams, lengths, max(settle, steps + warmup + 41) + 8,
+                    seed)
     if groups:
         assert lib.phonon_flow_batch_set_groups(d.batch, groups), last_error(lib)
     if eager:
         assert lib.phonon_flow_batch_set_graph(d.batch, 0), last_error(lib)
+    # Settle the clock, then back to the configured contexts: the warmup and
+    # timed steps attend exactly the keys they would from a cold start.
+    for i in range(settle):
+        d.step()
+        if i % 10 == 9:
+            assert lib.pgpu_stream_sync(d.stream), last_error(lib)
+    if settle:
+        assert lib.phonon_flow_batch_sync(d.batch), "non-finite value while settling"
+        d.reset()
     for _ in range(warmup):
         d.step()
     assert lib.phonon_flow_batch_sync(d.batch), "non-finite value during warmup"
@@ -1207,7 +1226,8 @@ def main():
     line = {
         "metric": "decode frames/sec at B=64 (12L d512 Q8); achieved HBM GB/s vs peak",
         "value": round(value, 1), "unit": "frames/s", "n_gpus": 1, "steps": args.steps,
-        "warmup": args.warmup, "ms_per_step": round(ms_step, 4), "higher_is_better": True,
+        "warmup": args.warmup, "settle_steps": SETTLE_STEPS,
+        "ms_per_step": round(ms_step, 4), "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "fp32",
         "data": "synthetic (seeded Q8 weights, N(0,1) KV contexts)",
         "config": {"workload": f"batched decode B={args.batch}, {args.layers} layers d512 "
