@@ -483,8 +483,7 @@ def large_batch_with_prefill(pkg, lib, seed, layers=12, streams=256, new_streams
             "prefill_attention": ["matrix cores", "exact (decode arithmetic)",
                                   "lane per query"][prefill_attention],
             "prefill_mfma": prefill_mfma_fraction(layers, new_streams, chunk,
-                                                  pre_ms / iterations,
-                                                  3 if prefill_attention == 1 else 2),
+                                                  pre_ms / iterations, 3),
             "frames_per_s_incl_prefill": round(streams / (per_it_ms * 1e-3), 1),
             "clean": clean}
 

@@ -156,9 +156,9 @@ def test_config5_prefill_leg_vs_oracle(lib, pkg, oracle, oracle_mod, syn):
     every position of every stream and the appended K/V of two streams
     against the oracle at 1e-4. With the exact prefill attention, those two
     streams decoded one position at a time give the same bits (outputs and
-    K/V); the matrix-core and the lane-per-query runs (whose projections take
-    the activations to 16 significant bits) stay within 1e-4 of the exact one
-    everywhere (measured 4.2e-5 after 12 layers)."""
+    K/V); the matrix-core and the lane-per-query runs (the same projections,
+    attention in their own order) stay within 1e-4 of the exact one
+    everywhere."""
     model = helpers.scaled_model(syn, 311, C5_LAYERS)
     views = pkg.Views()
     w = views.layers(model)
@@ -248,6 +248,84 @@ def test_config5_prefill_leg_vs_oracle(lib, pkg, oracle, oracle_mod, syn):
         assert np.array_equal(bits(k), bits(kv_exact[s][0]))
         assert np.array_equal(bits(v), bits(kv_exact[s][1]))
     bt.close()
+
+
+def test_config5_prefill_at_benchmark_weights_vs_float64(lib, pkg, oracle, oracle_mod, syn):
+    """The prefill the large-batch benchmark runs: 16 streams x 256
+    positions through all 12 layers with the benchmark's own (unscaled)
+    weights and N(0,1) inputs, in the default mode (matrix-core attention;
+    every projection reads the three bf16 terms of each activation).
+
+    At these weights the 12-layer stack over its own K/V is ill-conditioned:
+    the oracle (fp32 in the reference's order) drifts up to ~5e-2 from a
+    float64 restatement within 64 positions, so no fp32 order can be held to
+    1e-2 of another everywhere. For eight streams' first 128 positions,
+    replayed in float64: the GPU's worst and mean distance from float64 at
+    most 3x the oracle's; and wherever the oracle is itself within 1e-3 of
+    float64, the GPU within 1e-2 of the oracle (the tolerance of the bf16
+    matrix-core path)."""
+    layers, streams, chunk, checked = 12, 16, 256, 128
+    model = syn.flow_model(2026, layers)
+    ol = helpers.oracle_layers(oracle, model)
+    om = oracle_mod.OracleModel(oracle, ol)
+    views = pkg.Views()
+    w = views.layers(model)
+    max_pos, n = 8192, streams * chunk
+    table_len = max_pos // 16
+    used = chunk // 16
+    rng = np.random.default_rng(2026 + 54)
+    xs = rng.standard_normal((streams, chunk, 512)).astype(np.float32)
+    blocks = streams * used
+    tables = np.zeros((streams, table_len), np.int32)
+    print("benchmark-weight prefill: 16 x 256 positions, 12 layers", flush=True)
+    bt = Batch(lib, w, layers, n, max_pos, blocks)
+    ids = np.zeros(blocks, np.int32)
+    assert lib.phonon_kv_pool_alloc(bt.pool, blocks, i32p(ids))
+    tables[:, :used] = np.random.default_rng(2026 + 52).permutation(ids).reshape(streams, used)
+    din = pkg.DeviceBuffer(lib, n * 512 * 4)
+    dout = pkg.DeviceBuffer(lib, n * 512 * 4)
+    din.upload(xs.reshape(n, 512))
+    first = np.zeros(streams, np.uintp)
+    counts = np.full(streams, chunk, np.uintp)
+    assert lib.phonon_flow_batch_prefill_device(
+        bt.batch, streams, first.ctypes.data_as(SZP), counts.ctypes.data_as(SZP),
+        i32p(tables), table_len, din.ptr, 10000.0, dout.ptr), pkg.last_error(lib)
+    assert lib.phonon_flow_batch_sync(bt.batch)
+    got = dout.download((streams, chunk, 512))
+    din.free()
+    dout.free()
+    bt.close()
+    assert np.all(np.isfinite(got))
+
+    okeys = np.zeros((streams, layers, checked, 512), np.float32)
+    ovals = np.zeros_like(okeys)
+    ref = np.zeros((streams, checked, 512), np.float32)
+    for p in range(checked):
+        ok, ref[:, p] = om.stack_step_streams(okeys, ovals, checked, np.full(streams, p),
+                                              xs[:, p], 16)
+        assert ok
+
+    ol64 = [{k: np.asarray(a, np.float64) for k, a in layer.items()} for layer in ol]
+    e_gpu, e_oracle, tight = [], [], []
+    for s in range(0, streams, 2):
+        k64 = np.zeros((layers, checked, 512))
+        v64 = np.zeros_like(k64)
+        for p in range(checked):
+            exact = xs[s, p].astype(np.float64)
+            for layer in range(layers):
+                exact = helpers.f64_layer(ol64[layer], exact, k64[layer], v64[layer], p)
+            e_gpu.append(helpers.normwise(got[s, p], exact))
+            e_oracle.append(helpers.normwise(ref[s, p], exact))
+            if e_oracle[-1] <= 1e-3:
+                tight.append(helpers.normwise(got[s, p], ref[s, p]))
+    e_gpu, e_oracle, tight = np.array(e_gpu), np.array(e_oracle), np.array(tight)
+    print(f"benchmark-weight prefill: from float64 worst GPU {e_gpu.max():.2e} oracle "
+          f"{e_oracle.max():.2e}; mean GPU {e_gpu.mean():.2e} oracle {e_oracle.mean():.2e}; "
+          f"{len(tight)} positions where the oracle is within 1e-3 of float64: GPU vs oracle "
+          f"max {tight.max():.2e}")
+    assert e_gpu.max() <= 3.0 * e_oracle.max()
+    assert e_gpu.mean() <= 3.0 * e_oracle.mean()
+    assert len(tight) >= 64 and tight.max() <= 1e-2
 
 
 # ------------------------------------------------ benchmark weights, 12 layers
