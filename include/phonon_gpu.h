@@ -96,7 +96,11 @@ int pgpu_event_record(void *event, void *stream);
 int pgpu_event_elapsed_ms(void *start, void *stop, float *ms);
 /* Work enqueued on `stream` after this call waits for `event`. */
 int pgpu_stream_wait_event(void *stream, void *event);
+/* Stream capture into a graph: pgpu_graph_begin in thread-local mode;
+ * pgpu_graph_begin_global in global mode, where any allocation call made
+ * while the capture is open (by any thread) fails the capture. */
 int pgpu_graph_begin(void *stream);
+int pgpu_graph_begin_global(void *stream);
 int pgpu_graph_end(void *stream, void **exec);
 int pgpu_graph_launch(void *exec, void *stream);
 void pgpu_graph_destroy(void *exec);

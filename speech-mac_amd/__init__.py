@@ -241,6 +241,7 @@ EXPORTS = {
     "pgpu_event_elapsed_ms": (_i, [_vp, _vp, _fp]),
     "pgpu_stream_wait_event": (_i, [_vp, _vp]),
     "pgpu_graph_begin": (_i, [_vp]),
+    "pgpu_graph_begin_global": (_i, [_vp]),
     "pgpu_graph_end": (_i, [_vp, _pp]),
     "pgpu_graph_launch": (_i, [_vp, _vp]),
     "pgpu_graph_destroy": (None, [_vp]),

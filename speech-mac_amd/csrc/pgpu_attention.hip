@@ -349,8 +349,8 @@ extern "C" int pgpu_attention_static(void *stream, const float *q, const pgpu_pa
                                      int max_splits, float *out, uint16_t *out_split,
                                      int *status) {
     if (!q || !kv || !tables || !positions || !status || streams <= 0 || heads <= 0 ||
-        heads > kHeads || max_splits <= 0 || layer < 0 || layer >= kv->layers ||
-        (!out && !out_split))
+        heads > kHeads || max_splits <= 0 || table_stride <= 0 || layer < 0 ||
+        layer >= kv->layers || (!out && !out_split))
         return bad_arguments("pgpu_attention_static");
     // The partial layout is [stream][8 heads][max_splits] whatever `heads` is.
     if ((size_t)streams * kHeads * (size_t)max_splits > (size_t)kStaticSlots) {

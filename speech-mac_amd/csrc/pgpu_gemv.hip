@@ -8,8 +8,14 @@
 // arithmetic (each product rounded to fp32, then added, in column order)
 // and scales it; the row's first lane then adds the rows' scaled partials
 // in block order. The result therefore has the bits of the reference's
-// phonon_q8_matvec. A wave holds 64 / (columns / 32) whole rows, so the
-// columns must be 32 times a divisor of 64 (32 .. 2048).
+// phonon_q8_matvec compiled without multiply-add contraction
+// (-ffp-contract=off, as its golden vectors here are built). The
+// reference's own build (clang, no contraction flag) may contract
+// `partial += (float)q * x` and `sum += scale * partial` into fused
+// multiply-adds, whose results can differ in the last bits: against such a
+// build the outputs agree within the fp32 tolerance, not bit for bit. A wave
+// holds 64 / (columns / 32) whole rows, so the columns must be 32 times a
+// divisor of 64 (32 .. 2048).
 #include "pgpu_gemm.hpp"
 #include "phonon_gpu.h"
 

@@ -158,6 +158,11 @@ extern "C" int pgpu_graph_begin(void *stream) {
                  "hipStreamBeginCapture");
 }
 
+extern "C" int pgpu_graph_begin_global(void *stream) {
+    return check(hipStreamBeginCapture((hipStream_t)stream, hipStreamCaptureModeGlobal),
+                 "hipStreamBeginCapture");
+}
+
 extern "C" int pgpu_graph_end(void *stream, void **exec) {
     hipGraph_t graph = NULL;
     hipGraphExec_t instance = NULL;

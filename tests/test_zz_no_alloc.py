@@ -3,7 +3,9 @@ partials live in the library's fixed device array instead of a caller's
 pgpu_attention_scratch. Its output must equal, bit for bit, pgpu_attention
 followed by pgpu_attention_merge on the same inputs (the same kernels), on
 two calls in a row (the second smaller, over the partials the first left
-behind); sizes past the array's limit are rejected before any launch."""
+behind); sizes past the array's limit are rejected before any launch. The
+call can be captured into a HIP graph in global capture mode (where any
+allocation call during the capture fails it) and replayed."""
 import ctypes
 
 import numpy as np
@@ -74,15 +76,16 @@ class Case:
         assert lib.pgpu_stream_sync(None)
         return self.out[0].download((self.streams, 512))
 
+    def enqueue_static(self, layer, max_splits=None, stream=None, table_len=None):
+        return self.lib.pgpu_attention_static(
+            stream, self.q.ptr, ctypes.byref(self.kv), layer, self.dtab.ptr,
+            self.table_len if table_len is None else table_len, self.dpos.ptr, self.streams, 8,
+            max_splits or self.max_splits, self.out[1].ptr, None, self.status.ptr)
+
     def static(self, layer, max_splits=None):
-        lib = self.lib
-        ok = lib.pgpu_attention_static(None, self.q.ptr, ctypes.byref(self.kv), layer,
-                                       self.dtab.ptr, self.table_len, self.dpos.ptr,
-                                       self.streams, 8, max_splits or self.max_splits,
-                                       self.out[1].ptr, None, self.status.ptr)
-        if not ok:
+        if not self.enqueue_static(layer, max_splits):
             return None
-        assert lib.pgpu_stream_sync(None)
+        assert self.lib.pgpu_stream_sync(None)
         return self.out[1].download((self.streams, 512))
 
     def clean(self):
@@ -116,3 +119,36 @@ def test_static_attention_equals_the_scratch_path(lib, pkg):
     finally:
         first.close()
         second.close()
+
+
+def test_static_attention_replays_from_a_graph_captured_in_global_mode(lib, pkg):
+    """One pgpu_attention_static call captured on a stream in global capture
+    mode: had the call allocated (hipMalloc and the like), the capture would
+    fail. The graph, replayed three times over a NaN-filled output with the
+    scratch path run eagerly in between, gives its bits every time. A table
+    stride below 1 is rejected."""
+    rng = np.random.default_rng(911)
+    case = Case(pkg, lib, 2, 24, rng.integers(0, 1500, size=24), 912)
+    stream, exec_ = ctypes.c_void_p(), ctypes.c_void_p()
+    assert lib.pgpu_stream_create(ctypes.byref(stream))
+    try:
+        assert not case.enqueue_static(1, table_len=0)
+        assert b"invalid arguments" in lib.pgpu_last_error()
+        want = case.existing(1)
+        assert lib.pgpu_graph_begin_global(stream), pkg.last_error(lib)
+        enqueued = case.enqueue_static(1, stream=stream)
+        ended = lib.pgpu_graph_end(stream, ctypes.byref(exec_))
+        assert enqueued and ended, pkg.last_error(lib)
+        nan = np.full((case.streams, 512), np.nan, np.float32)
+        for replay in range(3):
+            case.out[1].upload(nan)
+            assert lib.pgpu_graph_launch(exec_, stream), pkg.last_error(lib)
+            assert lib.pgpu_stream_sync(stream)
+            got = case.out[1].download((case.streams, 512))
+            assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), replay
+            assert np.array_equal(case.existing(1).view(np.uint32), want.view(np.uint32))
+        assert case.clean()
+    finally:
+        lib.pgpu_graph_destroy(exec_)
+        lib.pgpu_stream_destroy(stream)
+        case.close()
