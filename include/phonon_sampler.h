@@ -36,11 +36,23 @@ typedef struct {
     PhononTensorView final_ada_weight, final_ada_bias, final_weight, final_bias;
 } PhononFlowHead;
 
+/* src/phonon_sampler.h:63 (src/phonon_sampler.c:163-212): every head view
+ * from the pack by its checkpoint name (flow_lm.flow_net.*), shapes and
+ * BF16 vectors checked; the views are borrowed from the pack. */
+int phonon_flow_head_load(const PhononPack *pack, PhononFlowHead *head);
 /* src/phonon_sampler.h:64-66: the head's velocity at flow times (s, t) for
  * a normalized latent state. */
 int phonon_flow_head_forward(const PhononFlowHead *head, const float condition[512],
                              const float normalized_state[PHONON_LATENT_WIDTH], float s, float t,
                              float velocity[PHONON_LATENT_WIDTH]);
+/* src/phonon_sampler.h:68 (src/phonon_sampler.c:395-401): the raw EOS
+ * logit flow_lm.out_eos . state + bias (on the device linear). */
+int phonon_flow_eos_logit(const PhononPack *pack, const float state[512], float *raw_logit);
+/* src/phonon_sampler.h:69-70 (src/phonon_sampler.c:403-418): normalized *
+ * flow_lm.emb_std + flow_lm.emb_mean per channel; 0 if a result is not
+ * finite. */
+int phonon_flow_denormalize_latent(const PhononPack *pack, const float normalized[32],
+                                   float denormalized[32]);
 /* src/phonon_sampler.h:72-74: noise * sqrt(temperature) plus the velocity at
  * (s, t) = (0, 1). */
 int phonon_flow_lsd_one_step(const PhononFlowHead *head, const float condition[512],

@@ -294,6 +294,9 @@ EXPORTS = {
     "pgpu_head_time_phase": (_i, [_vp, _vp, _f, _vp, _vp]),
     "pgpu_head_time_sum": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "phonon_flow_head_forward": (_i, [_vp, _vp, _vp, _f, _f, _vp]),
+    "phonon_flow_head_load": (_i, [_vp, _vp]),
+    "phonon_flow_eos_logit": (_i, [_vp, _vp, _vp]),
+    "phonon_flow_denormalize_latent": (_i, [_vp, _vp, _vp]),
     "phonon_flow_lsd_one_step": (_i, [_vp, _vp, _vp, _f, _vp]),
     "phonon_flow_lsd_one_step_cancel": (_i, [_vp, _vp, _vp, _f, _vp, _vp, _vp]),
     "phonon_flow_head_prepare": (_i, [_vp]),

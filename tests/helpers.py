@@ -155,6 +155,34 @@ def reference_flow_head_bits() -> dict:
     return h
 
 
+def flow_head_checkpoint_names() -> dict:
+    """Checkpoint tensor name of each role of the head builders above (the
+    names src/phonon_sampler.c:163-212 reads)."""
+    net = "flow_lm.flow_net"
+    names = {"input_weight": f"{net}.input_proj.weight", "input_bias": f"{net}.input_proj.bias",
+             "cond_weight": f"{net}.cond_embed.weight", "cond_bias": f"{net}.cond_embed.bias",
+             "final_ada_weight": f"{net}.final_layer.adaLN_modulation.1.weight",
+             "final_ada_bias": f"{net}.final_layer.adaLN_modulation.1.bias",
+             "final_weight": f"{net}.final_layer.linear.weight",
+             "final_bias": f"{net}.final_layer.linear.bias"}
+    for t in range(2):
+        for j, layer in ((0, 0), (1, 2)):
+            names[f"time_weight_{t}_{j}"] = f"{net}.time_embed.{t}.mlp.{layer}.weight"
+            names[f"time_bias_{t}_{j}"] = f"{net}.time_embed.{t}.mlp.{layer}.bias"
+        names[f"time_freqs_{t}"] = f"{net}.time_embed.{t}.freqs"
+        names[f"time_alpha_{t}"] = f"{net}.time_embed.{t}.mlp.3.alpha"
+    for b in range(HEAD_BLOCKS):
+        blk = f"{net}.res_blocks.{b}"
+        names[f"block_ada_weight_{b}"] = f"{blk}.adaLN_modulation.1.weight"
+        names[f"block_ada_bias_{b}"] = f"{blk}.adaLN_modulation.1.bias"
+        names[f"block_norm_weight_{b}"] = f"{blk}.in_ln.weight"
+        names[f"block_norm_bias_{b}"] = f"{blk}.in_ln.bias"
+        for j in range(2):
+            names[f"block_mlp_weight_{b}_{j}"] = f"{blk}.mlp.{2 * j}.weight"
+            names[f"block_mlp_bias_{b}_{j}"] = f"{blk}.mlp.{2 * j}.bias"
+    return names
+
+
 def reference_flow_head_inputs():
     """condition and state of tests/test_phonon_sampler.c:185-188."""
     i = np.arange(512)

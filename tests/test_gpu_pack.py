@@ -122,3 +122,45 @@ def test_voice_projection_and_condition_vs_oracle(lib, pkg, oracle):
     assert ok and ok2 and helpers.normwise(cond, a[0] + b[0]) <= TOL
     assert not lib.phonon_flow_condition(ctypes.byref(table), ctypes.byref(sp), ctypes.byref(du),
                                          4, delta, f32(cond))   # speaker out of range
+
+
+def test_pack_flow_head_and_eos_vs_golden_and_oracle(lib, pkg, oracle, oracle_mod, syn,
+                                                     scaled_pack):
+    """The flow head loaded from the pack by its checkpoint names
+    (phonon_flow_head_load) drives phonon_flow_head_forward to the reference
+    test's golden velocity (tests/test_phonon_sampler.c:148-195, its 2e-4)
+    and to the oracle within 1e-4, so every view is wired to its role; the
+    pack's EOS row (phonon_flow_eos_logit, on the device linear) against the
+    oracle's dot product within 1e-4 relative; bad arguments rejected."""
+    _, extra, path = scaled_pack
+    ok, pack = opened(lib, path)
+    assert ok
+    head = pkg.PhononFlowHead()
+    assert lib.phonon_flow_head_load(pack, ctypes.byref(head))
+    g = __import__("json").load(open(helpers.GOLDEN_DIR + "/reference_vectors.json"))
+    g = g["flow_head_synthetic"]
+    condition, state = helpers.reference_flow_head_inputs()
+    out = np.zeros(32, np.float32)
+    assert lib.phonon_flow_head_forward(ctypes.byref(head), f32(condition), f32(state), 0.0, 1.0,
+                                        f32(out)), pkg.last_error(lib)
+    assert np.max(np.abs(out - np.asarray(g["expected"], np.float32))) < g["tolerance"]
+    floats = {k: helpers.bf16_float(v) for k, v in helpers.reference_flow_head_bits().items()}
+    oh = oracle_mod.OracleHead(oracle, floats)
+    ok, ref = oh.forward(condition, state, 0.0, 1.0)
+    assert ok and helpers.normwise(out, ref) <= TOL
+    lib.phonon_flow_head_release(ctypes.byref(head))
+
+    w = syn.bf16_to_f32(extra["flow_lm.out_eos.weight"]).reshape(512)
+    b = syn.bf16_to_f32(extra["flow_lm.out_eos.bias"])
+    rng = np.random.default_rng(417)
+    for _ in range(3):
+        x = rng.standard_normal(512).astype(np.float32)
+        logit = np.zeros(1, np.float32)
+        assert lib.phonon_flow_eos_logit(pack, f32(x), f32(logit)), pkg.last_error(lib)
+        ok, want = oh.eos_logit(w, b, x)
+        assert ok
+        assert abs(float(logit[0]) - want) <= TOL * max(abs(want), float(np.abs(w * x).sum()))
+    assert not lib.phonon_flow_eos_logit(None, f32(x), f32(logit))
+    x[0] = np.nan
+    assert not lib.phonon_flow_eos_logit(pack, f32(x), f32(logit))
+    lib.phonon_pack_close(pack)

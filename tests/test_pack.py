@@ -230,8 +230,10 @@ def test_prepare_linears_bounded_with_rollback(lib, pkg, tmp_path):
 def model_pack_tensors(syn, seed=404, vocab=48, factor=1.0):
     """A 209-tensor pack holding the nine Flow layers under their checkpoint
     names (36 Q8_0), their norms, the decoder's out_norm, input_linear,
-    bos_emb, emb_mean/emb_std and a transcript embedding table (BF16), filled
-    up to 173 BF16 tensors with small vectors."""
+    bos_emb, emb_mean/emb_std, a transcript embedding table, the flow head
+    (the reference test's synthetic head, tests/test_phonon_sampler.c:104-180,
+    68 tensors) and out_eos (BF16), filled up to 173 BF16 tensors with small
+    vectors."""
     rng = np.random.default_rng(seed)
     model = helpers.scaled_model(syn, seed, 9, factor) if factor != 1.0 else syn.flow_model(seed, 9)
     t = []
@@ -256,6 +258,11 @@ def model_pack_tensors(syn, seed=404, vocab=48, factor=1.0):
     extra["flow_lm.emb_std"] = ((32,), bf(rng.uniform(0.5, 2.0, 32)))
     extra["flow_lm.condition_provider.conditioners.transcript_in_segment.embed.weight"] = (
         (vocab, 512), bf(rng.standard_normal((vocab, 512))))
+    extra["flow_lm.out_eos.weight"] = ((1, 512), bf(0.05 * rng.standard_normal((1, 512))))
+    extra["flow_lm.out_eos.bias"] = ((1,), bf([0.125]))
+    names = helpers.flow_head_checkpoint_names()
+    for key, bits in helpers.reference_flow_head_bits().items():
+        extra[names[key]] = (bits.shape, bits)
     for name, (shape, bits) in extra.items():
         t.append((name, helpers.KPACK_BF16, shape, bits.tobytes()))
     i = 0
@@ -339,3 +346,73 @@ def test_pack_helpers_without_the_device(lib, pkg, syn, model_pack):
     two_bos = np.array([9, 7, 7, 9, 2], np.int32)
     assert not lib.phonon_flow_prepare_prefix(i32(two_bos), 5, f32(tok), 7, 9, f32(voice), 2,
                                               f32(bos), f32(out))
+
+
+def test_flow_head_load_gives_the_checkpoint_views(lib, pkg, syn, model_pack, tmp_path):
+    """phonon_flow_head_load fills every PhononFlowHead view with its
+    checkpoint tensor (bytes and shapes), and fails when a tensor is missing
+    or has another shape."""
+    _, extra, path = model_pack
+    ok, pack = opened(lib, path)
+    assert ok
+    head = pkg.PhononFlowHead()
+    assert lib.phonon_flow_head_load(pack, ctypes.byref(head))
+    names = helpers.flow_head_checkpoint_names()
+    bits = helpers.reference_flow_head_bits()
+
+    def view(key):
+        parts = key.split("_")
+        if key.startswith(("time_weight", "time_bias", "block_mlp")):
+            field = "_".join(parts[:-2])
+            return getattr(head, field)[int(parts[-2])][int(parts[-1])]
+        if key.startswith(("time_freqs", "time_alpha", "block_")):
+            return getattr(head, "_".join(parts[:-1]))[int(parts[-1])]
+        return getattr(head, key)
+
+    for key, want in bits.items():
+        v = view(key)
+        assert v.dtype == 2 and list(v.shape[:v.rank]) == list(want.shape), key
+        assert ctypes.string_at(v.data, v.byte_count) == want.tobytes(), key
+    lib.phonon_pack_close(pack)
+    assert not lib.phonon_flow_head_load(None, ctypes.byref(head))
+
+    # A missing tensor, or one of another shape: the load fails.
+    model, _, tensors = model_pack_tensors(syn)
+    for mutate in ("missing", "shape"):
+        bad = []
+        for name, dtype, shape, data in tensors:
+            if name == names["time_freqs_1"]:
+                if mutate == "missing":
+                    name = "flow_lm.flow_net.time_embed.1.freq"
+                else:
+                    shape, data = (127,), data[:254]
+            bad.append((name, dtype, shape, data))
+        p = tmp_path / f"{mutate}.kpack"
+        p.write_bytes(helpers.kpack_bytes(bad))
+        ok, other = opened(lib, str(p).encode())
+        assert ok, mutate
+        assert not lib.phonon_flow_head_load(other, ctypes.byref(head)), mutate
+        lib.phonon_pack_close(other)
+
+
+def test_denormalize_latent_without_the_device(lib, pkg, syn, model_pack):
+    """x * emb_std + emb_mean per channel, as float32 rounds it (two
+    operations, no contraction); a non-finite result fails."""
+    _, extra, path = model_pack
+    ok, pack = opened(lib, path)
+    assert ok
+    f32 = lambda a: a.ctypes.data_as(ctypes.POINTER(ctypes.c_float))  # noqa: E731
+    mean = syn.bf16_to_f32(extra["flow_lm.emb_mean"])
+    std = syn.bf16_to_f32(extra["flow_lm.emb_std"])
+    x = np.random.default_rng(7).standard_normal(32).astype(np.float32)
+    y = np.zeros(32, np.float32)
+    assert lib.phonon_flow_denormalize_latent(pack, f32(x), f32(y))
+    assert np.array_equal(y, (x * std).astype(np.float32) + mean)
+    # normalize then denormalize: back within a few ulps
+    z = np.zeros(32, np.float32)
+    assert lib.phonon_flow_normalize_latent(pack, f32(y), f32(z))
+    np.testing.assert_allclose(z, x, rtol=1e-6, atol=1e-6)
+    x[5] = np.inf
+    assert not lib.phonon_flow_denormalize_latent(pack, f32(x), f32(y))
+    assert not lib.phonon_flow_denormalize_latent(None, f32(x), f32(y))
+    lib.phonon_pack_close(pack)
