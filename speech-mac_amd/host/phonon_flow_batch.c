@@ -459,9 +459,11 @@ int phonon_flow_batch_create(const PhononFlowModel *model, PhononKvPool *pool,
     b->groups = PH_DEFAULT_GROUPS;
     b->flow = 1;
     b->fl.place = ph_flow_default_placement(1);
-    int ok = pgpu_stream_create(&b->stream) && pgpu_event_create(&b->fork);
-    for (size_t g = 0; ok && g + 1 < PH_MAX_GROUPS; g++)
-        ok = pgpu_stream_create(&b->side[g]) && pgpu_event_create(&b->join[g]);
+    /* One HIP stream; the side streams of stream groups are made when groups
+     * are asked for (phonon_flow_batch_set_groups), so a batch per request
+     * holds one stream and requests on separate caches spread over the
+     * GPU's hardware queues. */
+    int ok = pgpu_stream_create(&b->stream);
     b->x = pgpu_malloc(rows);
     b->r = pgpu_malloc(rows);
     b->q = pgpu_malloc(rows);
@@ -1287,6 +1289,15 @@ int phonon_flow_batch_set_prefill_exact(PhononFlowBatch *b, int exact) {
 int phonon_flow_batch_set_groups(PhononFlowBatch *b, size_t groups) {
     if (!b || !groups || groups > PH_MAX_GROUPS)
         return 0;
+    if (groups > 1) {
+        /* each made once; a failure leaves the groups as they were */
+        int ok = b->fork || pgpu_event_create(&b->fork);
+        for (size_t g = 0; ok && g + 1 < PH_MAX_GROUPS; g++)
+            ok = (b->side[g] || pgpu_stream_create(&b->side[g])) &&
+                 (b->join[g] || pgpu_event_create(&b->join[g]));
+        if (!ok)
+            return 0;
+    }
     if (b->groups != groups) {
         drop_graphs(b);
         b->groups = groups;

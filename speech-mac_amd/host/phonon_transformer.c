@@ -6,11 +6,17 @@
  * as a batch of one stream (phonon_flow_batch.c); the rows a step appends on
  * the device are copied back into keys/values before the call returns.
  * Weights come from phonon_flow_prepare_weights when registered, otherwise
- * they are uploaded for the call (and may change between calls). */
+ * they are uploaded for the call (and may change between calls).
+ *
+ * Concurrency (src/speech.h:40-41: requests on separate caches may run at
+ * once): the library lock covers only finding the weights and the cache's
+ * device copy; each copy has its own lock, batches and HIP stream, so steps
+ * of different caches run at the same time on the host and the GPU. */
 #include "ph_internal.h"
 
 #include <limits.h>
 #include <math.h>
+#include <pthread.h>
 #include <stdlib.h>
 #include <string.h>
 
@@ -21,6 +27,7 @@ typedef struct Mirror {
     int32_t *table_host, *table_dev;
     PhononFlowBatch *batch;   /* one stream: decode steps */
     PhononFlowBatch *prefill; /* up to PH_PREFILL_CHUNK positions at once */
+    pthread_mutex_t lock;     /* held by a step or prefill of this cache */
     struct Mirror *next;
 } Mirror;
 
@@ -40,6 +47,7 @@ static void mirror_free(Mirror *m) {
         (void)pgpu_stream_sync(ph_stream());
         pgpu_free(m->table_dev);
     }
+    pthread_mutex_destroy(&m->lock);
     free(m);
 }
 
@@ -70,6 +78,10 @@ static Mirror *mirror_create(const PhononKvCache *cache) {
     Mirror *m = calloc(1, sizeof(*m));
     if (!m)
         return NULL;
+    if (pthread_mutex_init(&m->lock, NULL)) {
+        free(m);
+        return NULL;
+    }
     m->keys = cache->keys;
     m->capacity = cache->capacity;
     m->positions = cache->capacity < PHONON_FLOW_MAX_POSITIONS ? cache->capacity
@@ -487,6 +499,42 @@ static const PhononFlowModel *model_for(const PhononFlowLayerWeights *weights, s
     return *owned;
 }
 
+/* The device weights and the cache's device copy, found under the library
+ * lock; the copy is returned locked (its own lock), so steps of different
+ * caches run concurrently. NULL if either is missing. */
+static Mirror *acquire(const PhononFlowLayerWeights *weights, size_t layers,
+                       const PhononKvCache *cache, PhononFlowModel **owned,
+                       const PhononFlowModel **model) {
+    ph_lock();
+    *model = model_for(weights, layers, owned);
+    Mirror *m = *model ? mirror_get(cache) : NULL;
+    ph_unlock();
+    if (m)
+        pthread_mutex_lock(&m->lock);
+    else if (*owned) {
+        ph_lock();
+        phonon_flow_model_destroy(*owned);
+        *owned = NULL;
+        ph_unlock();
+    }
+    return m;
+}
+
+/* Ends a step: a weight upload of this call is freed once the batch that
+ * used it has finished. */
+static void release(Mirror *m, PhononFlowBatch *used, PhononFlowModel *owned) {
+    if (!m)
+        return;
+    if (used && owned)
+        (void)ph_batch_status(used);
+    pthread_mutex_unlock(&m->lock);
+    if (owned) {
+        ph_lock();
+        phonon_flow_model_destroy(owned);
+        ph_unlock();
+    }
+}
+
 int phonon_flow_layer_step(const PhononFlowLayerWeights *weights, PhononKvCache *cache,
                            size_t layer, size_t position, const float input[PHONON_FLOW_WIDTH],
                            float theta, float output[PHONON_FLOW_WIDTH]) {
@@ -495,18 +543,14 @@ int phonon_flow_layer_step(const PhononFlowLayerWeights *weights, PhononKvCache 
         cache->length != position || !cache->keys || !cache->values ||
         !ph_all_finite(input, PHONON_FLOW_WIDTH) || !ph_init())
         return 0;
-    ph_lock();
     PhononFlowModel *owned = NULL;
-    const PhononFlowModel *model = model_for(weights, 1, &owned);
-    Mirror *m = model ? mirror_get(cache) : NULL;
+    const PhononFlowModel *model;
+    Mirror *m = acquire(weights, 1, cache, &owned, &model);
     int cancelled = 0;
     float result[PHONON_FLOW_WIDTH];
     const int ok = m && run_position(model, m, cache, layer, position, input, theta, result, NULL,
                                      NULL, &cancelled);
-    if (m && m->batch && owned)
-        (void)ph_batch_status(m->batch);
-    phonon_flow_model_destroy(owned);
-    ph_unlock();
+    release(m, m ? m->batch : NULL, owned);
     if (ok)
         memcpy(output, result, sizeof(result));
     return ok;
@@ -522,18 +566,14 @@ int phonon_flow_stack_step_cancel(const PhononFlowLayerWeights weights[PHONON_FL
     if (position >= PHONON_FLOW_MAX_POSITIONS || !cache->keys || !cache->values ||
         !ph_all_finite(input, PHONON_FLOW_WIDTH) || !ph_init())
         return 0;
-    ph_lock();
     PhononFlowModel *owned = NULL;
-    const PhononFlowModel *model = model_for(weights, PHONON_FLOW_LAYERS, &owned);
-    Mirror *m = model ? mirror_get(cache) : NULL;
+    const PhononFlowModel *model;
+    Mirror *m = acquire(weights, PHONON_FLOW_LAYERS, cache, &owned, &model);
     int cancelled = 0;
     float result[PHONON_FLOW_WIDTH];
     int ok = m && run_position(model, m, cache, 0, position, input, theta, result, cancel,
                                context, &cancelled);
-    if (m && m->batch && owned)
-        (void)ph_batch_status(m->batch);
-    phonon_flow_model_destroy(owned);
-    ph_unlock();
+    release(m, m ? m->batch : NULL, owned);
     if (cancelled) {
         phonon_kv_cache_reset(cache);
         return 0;
@@ -564,18 +604,14 @@ int phonon_flow_stack_prefill_cancel(const PhononFlowLayerWeights weights[PHONON
         phonon_kv_cache_reset(cache);
         return 0;
     }
-    ph_lock();
     PhononFlowModel *owned = NULL;
-    const PhononFlowModel *model = model_for(weights, PHONON_FLOW_LAYERS, &owned);
-    Mirror *m = model ? mirror_get(cache) : NULL;
+    const PhononFlowModel *model;
+    Mirror *m = acquire(weights, PHONON_FLOW_LAYERS, cache, &owned, &model);
     int cancelled = 0;
     float result[PHONON_FLOW_WIDTH];
     const int ok = m && run_prefill(model, m, cache, input, length, theta, result, cancel,
                                     context, &cancelled);
-    if (m && m->prefill && owned)
-        (void)ph_batch_status(m->prefill);
-    phonon_flow_model_destroy(owned);
-    ph_unlock();
+    release(m, m ? m->prefill : NULL, owned);
     if (!ok || cancelled) {
         phonon_kv_cache_reset(cache);
         return 0;

@@ -1046,3 +1046,100 @@ def test_dropins_from_two_threads(lib, syn, pkg):
         assert len(par[k]) == len(seq[k]) == steps + 1
         for a, b in zip(par[k], seq[k]):
             assert np.array_equal(np.asarray(a).view(np.uint32), np.asarray(b).view(np.uint32))
+
+
+def test_dropin_requests_on_separate_caches_overlap(lib, syn, pkg, oracle, oracle_mod):
+    """Concurrent requests on separate caches (src/speech.h:40-41): two host
+    threads each run a request through the reference-signature drop-ins (a
+    64-position phonon_flow_stack_prefill, then 48 phonon_flow_stack_step
+    calls) on its own cache, with the weights registered once, as a shared
+    engine holds them. Each request's outputs match the oracle's stack steps
+    at 1e-4, and the pair takes under 1.6x the wall time of one request
+    alone: the two caches' steps run at the same time on the host and the
+    GPU."""
+    import threading
+    import time
+    model = scaled_model(syn, 251, L9)
+    om = oracle_for(oracle, oracle_mod, model)
+    views = pkg.Views()
+    w = views.layers(model)
+    assert lib.phonon_flow_prepare_weights(w, L9), pkg.last_error(lib)
+    prompt, steps = 64, 48
+    cap = prompt + steps
+    rng = np.random.default_rng(252)
+    xs = rng.standard_normal((2, cap, 512)).astype(np.float32)
+    caches = [Cache(lib, cap) for _ in range(2)]
+
+    def request(k, outs, errors, barrier=None):
+        try:
+            c = caches[k]
+            lib.phonon_kv_cache_reset(c.ref())
+            if barrier is not None:
+                barrier.wait()
+            y = np.zeros(512, np.float32)
+            prefix = np.ascontiguousarray(xs[k, :prompt])
+            if not lib.phonon_flow_stack_prefill(w, c.ref(), fp(prefix), prompt, 10000.0, fp(y)):
+                errors.append((k, "prefill", pkg.last_error(lib)))
+                return
+            outs.append(y.copy())
+            for pos in range(prompt, cap):
+                if not lib.phonon_flow_stack_step(w, c.ref(), pos,
+                                                  fp(np.ascontiguousarray(xs[k, pos])), 10000.0,
+                                                  fp(y)):
+                    errors.append((k, pos, pkg.last_error(lib)))
+                    return
+                outs.append(y.copy())
+        except Exception as e:  # reported by the main thread
+            errors.append((k, repr(e)))
+
+    def timed_pair():
+        outs, errors = ([], []), []
+        barrier = threading.Barrier(3)
+        threads = [threading.Thread(target=request, args=(k, outs[k], errors, barrier))
+                   for k in (0, 1)]
+        for t in threads:
+            t.start()
+        barrier.wait()
+        t0 = time.perf_counter()
+        for t in threads:
+            t.join(timeout=120)
+            assert not t.is_alive()
+        wall = time.perf_counter() - t0
+        assert not errors, errors
+        return wall, outs
+
+    try:
+        warm = ([], [])
+        errors = []
+        for k in (0, 1):
+            request(k, warm[k], errors)   # batches and device copies made
+        assert not errors, errors
+        single = []
+        for _ in range(2):
+            outs = []
+            t0 = time.perf_counter()
+            request(0, outs, errors)
+            single.append(time.perf_counter() - t0)
+            assert not errors, errors
+        pair, outs = zip(*(timed_pair() for _ in range(2)))
+        print(f"drop-in requests: one alone {min(single) * 1e3:.1f} ms, two at once "
+              f"{min(pair) * 1e3:.1f} ms ({min(pair) / min(single):.2f}x)", flush=True)
+        # Outputs: the oracle's stack steps over the same positions.
+        for k in (0, 1):
+            keys = np.zeros((L9, cap, 512), np.float32)
+            vals = np.zeros_like(keys)
+            want = []
+            for pos in range(cap):
+                ok, ref = om.stack_step(keys, vals, cap, pos, xs[k, pos])
+                assert ok
+                if pos >= prompt - 1:
+                    want.append(ref)
+            for got in (outs[0][k], outs[1][k], warm[k]):
+                assert len(got) == len(want) == steps + 1
+                for i, (a, b) in enumerate(zip(got, want)):
+                    assert helpers.normwise(a, b) <= TOL, (k, i, helpers.normwise(a, b))
+        assert min(pair) < 1.6 * min(single)
+    finally:
+        for c in caches:
+            c.destroy()
+        lib.phonon_flow_release_weights(w)
