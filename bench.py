@@ -273,8 +273,8 @@ def flow_roofline(pkg, lib, d, steps=20):
     """Average duration of the one-launch step kernel (k_flow_step: every
     layer's projections, K/V appends and attention of one decode step) on
     the decode workload, timed with HIP events recorded on the batch's stream
-    right before and after each launch (the counter reset that follows it is
-    outside). Continues the decode from where the timed run left it. Returns
+    right before and after each launch (the step is that one launch: its
+    work-groups clear the next step's counters themselves). Continues the decode from where the timed run left it. Returns
     None if the batch does not run its step as one launch."""
     events = []
     for _ in range(2 * steps):

@@ -159,12 +159,12 @@ int phonon_flow_batch_set_handoff(PhononFlowBatch *batch, int tagged);
 /* Kernel timing: while `before` and `after` are events (pgpu_event_create),
  * each step launches its kernels directly (no graph replay) and records
  * `before` right before and `after` right after its one-launch kernel
- * (k_flow_step; the counter reset that follows it is outside) on the batch's
- * stream. Phase-by-phase steps record nothing. NULL, NULL turns it off. */
+ * (k_flow_step, the whole step) on the batch's stream. Phase-by-phase steps
+ * record nothing. NULL, NULL turns it off. */
 int phonon_flow_batch_set_timing(PhononFlowBatch *batch, void *before, void *after);
 /* use_graph = 1 (default): a phase-by-phase step_device replays a captured
- * HIP graph (a one-launch step is always launched directly: its two kernels
- * gain nothing from a graph); 0: it launches the step's kernels directly
+ * HIP graph (a one-launch step is always launched directly: one kernel
+ * gains nothing from a graph); 0: it launches the step's kernels directly
  * (e.g. for a caller that is itself capturing a graph). Results are
  * identical. */
 int phonon_flow_batch_set_graph(PhononFlowBatch *batch, int use_graph);
