@@ -810,6 +810,41 @@ struct EpiOperands {
     bool ok;             // QKV: position and block are valid
 };
 
+// The K/V append slot of stream s: its position and pool block. Positions
+// past the rope table or the block table, and block ids outside the pool,
+// are errors: flagged by the epilogue, and nothing is written.
+struct QkvSlot {
+    int pos, block;
+    bool ok;
+};
+
+__device__ inline QkvSlot qkv_slot(const GemmArgs &a, int s, bool live) {
+    QkvSlot q{0, 0, false};
+    if (!live) return q;
+    int pos = a.positions[s] + a.pos_delta;
+    q.ok = pos >= 0 && pos < kMaxPositions && (pos >> 4) < a.table_stride;
+    if (q.ok) {
+        q.block = a.tables[(size_t)s * a.table_stride + (pos >> 4)];
+        q.ok = (unsigned)q.block < a.blocks;
+    }
+    q.pos = q.ok ? pos : 0;
+    return q;
+}
+
+// The QKV epilogue's operands of rows row0..row0+3 at slot q: the slot and
+// the RoPE phases of the lane's two interleaved pairs (those of position 0
+// for a slot in error).
+__device__ inline void qkv_operands(EpiOperands &e, const GemmArgs &a, const QkvSlot &q,
+                                    int row0, bool live) {
+    e.ok = live && q.ok;
+    e.pos = q.pos;
+    e.block = q.block;
+    if (!live) return;
+    const int d0 = (row0 & 511) & 63;
+    e.cs0 = a.rope[(size_t)q.pos * 32 + (d0 >> 1)];
+    e.cs1 = a.rope[(size_t)q.pos * 32 + (d0 >> 1) + 1];
+}
+
 // Operands that no task of the step writes (bias, positions, block tables,
 // RoPE table): may be loaded before the task waits for its inputs.
 template <int EPI>
@@ -832,20 +867,7 @@ __device__ inline void load_epilogue_static(EpiOperands &e, const GemmArgs &a, i
             e.has_add2 = true;
         }
     } else if constexpr (EPI == EPI_QKV) {
-        // Positions past the rope table or the block table, and block ids
-        // outside the pool, are errors: flagged, and nothing is written.
-        int pos = a.positions[s] + a.pos_delta;
-        e.ok = pos >= 0 && pos < kMaxPositions && (pos >> 4) < a.table_stride;
-        e.block = 0;
-        if (e.ok) {
-            e.block = a.tables[(size_t)s * a.table_stride + (pos >> 4)];
-            e.ok = (unsigned)e.block < a.blocks;
-        }
-        if (!e.ok) pos = 0;
-        e.pos = pos;
-        const int d0 = (row0 & 511) & 63;
-        e.cs0 = a.rope[(size_t)pos * 32 + (d0 >> 1)];
-        e.cs1 = a.rope[(size_t)pos * 32 + (d0 >> 1) + 1];
+        qkv_operands(e, a, qkv_slot(a, s, true), row0, true);
     }
 }
 

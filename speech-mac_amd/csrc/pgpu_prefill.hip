@@ -73,25 +73,30 @@ __global__ __launch_bounds__(kTaskThreads) void k_rows_split(GemmArgs a, uint16_
     }
 }
 
-// LayerNorm rows -> split fragments without the LDS operand buffer: 8 rows
-// per 256-thread work-group (wave w: rows 2w, 2w + 1), the decode
-// prologue's LayerNorm arithmetic (rows_ln_values: the same bits), and each
-// lane stores its 8 columns' split terms straight into their fragment
-// records (row n of tile st, columns [8j, 8j + 8): block j / 4, record
-// (j % 4) 16 + n). Only the first `terms` terms are written (the
-// projections of a two-term prefill never read the third). Rows past
-// `streams` up to the tile's end become zeros.
-constexpr int kLnRowsPerGroup = 8;
-__global__ __launch_bounds__(256) void k_rows_split_ln(const float *__restrict__ x,
+// LayerNorm rows -> split fragments: one 16-row tile per 512-thread
+// work-group. Wave w normalises rows 2w, 2w + 1 with the decode prologue's
+// LayerNorm arithmetic (rows_ln_values: the same bits) into an LDS tile;
+// then wave w writes column blocks 2w, 2w + 1: lane (g, n) = (lane / 16,
+// lane % 16) splits row n, columns [8g, 8g + 8) of the block into its three
+// terms, so that each term's 1 KB fragment record is one contiguous store.
+// Only the first `terms` terms are written (the projections of a two-term
+// prefill never read the third). Rows past `streams` up to the tile's end
+// become zeros.
+constexpr int kLnTileStride = kWidth + 4;  // floats per LDS row: 8 lanes of a
+                                           // 16-byte read hit distinct banks
+__global__ __launch_bounds__(512) void k_rows_split_ln(const float *__restrict__ x,
                                                        const float *__restrict__ lw,
                                                        const float *__restrict__ lb, float eps,
                                                        int streams, int terms, uint16_t *out,
                                                        int *status) {
+    __shared__ float4 tile4[16 * kLnTileStride / 4];
+    float *tile = (float *)tile4;
     const int wave = threadIdx.x >> 6, j = threadIdx.x & 63;
+    const int st = blockIdx.x;
     Rows2 r;
 #pragma unroll
     for (int i = 0; i < 2; i++) {
-        const int s = blockIdx.x * kLnRowsPerGroup + 2 * wave + i;
+        const int s = st * 16 + 2 * wave + i;
         r.live[i] = s < streams;  // uniform per wave
         if (r.live[i]) {
             const float4 x0 = *(const float4 *)(x + (size_t)s * kWidth + j * 8);
@@ -107,21 +112,31 @@ __global__ __launch_bounds__(256) void k_rows_split_ln(const float *__restrict__
     flag_nonfinite(status, bad);
 #pragma unroll
     for (int i = 0; i < 2; i++) {
-        const int s = blockIdx.x * kLnRowsPerGroup + 2 * wave + i;
-        const int st = s >> 4, n = s & 15, kb = j >> 2, g = j & 3;
+        float4 *row = (float4 *)(tile + (2 * wave + i) * kLnTileStride + j * 8);
+        row[0] = make_float4(r.v[i][0], r.v[i][1], r.v[i][2], r.v[i][3]);
+        row[1] = make_float4(r.v[i][4], r.v[i][5], r.v[i][6], r.v[i][7]);
+    }
+    __syncthreads();
+    const int g = j >> 4, n = j & 15;
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+        const int kb = 2 * wave + i;
+        const float4 *src = (const float4 *)(tile + n * kLnTileStride + kb * 32 + g * 8);
+        const float4 v0 = src[0], v1 = src[1];
+        const float v[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
         uint16_t h[8], m[8], l[8];
 #pragma unroll
-        for (int k = 0; k < 8; k++) split3(r.v[i][k], h[k], m[k], l[k]);
-        uint16_t *rec = out + ((size_t)st * (kWidth / 32) + kb) * 1536 + (g * 16 + n) * 8;
+        for (int k = 0; k < 8; k++) split3(v[k], h[k], m[k], l[k]);
+        uint16_t *rec = out + ((size_t)st * (kWidth / 32) + kb) * 1536 + j * 8;
 #pragma unroll
         for (int p = 0; p < 3; p++) {
             if (p >= terms) break;
-            const uint16_t *src = p == 0 ? h : (p == 1 ? m : l);
+            const uint16_t *t = p == 0 ? h : (p == 1 ? m : l);
             uint4 q;
-            q.x = src[0] | (uint32_t)src[1] << 16;
-            q.y = src[2] | (uint32_t)src[3] << 16;
-            q.z = src[4] | (uint32_t)src[5] << 16;
-            q.w = src[6] | (uint32_t)src[7] << 16;
+            q.x = t[0] | (uint32_t)t[1] << 16;
+            q.y = t[2] | (uint32_t)t[3] << 16;
+            q.z = t[4] | (uint32_t)t[5] << 16;
+            q.w = t[6] | (uint32_t)t[7] << 16;
             *(uint4 *)(rec + p * 512) = q;
         }
     }
@@ -250,7 +265,7 @@ __global__ __launch_bounds__(kTaskThreads) void k_prefill_gemm(GemmArgs a, int r
     // Q8 scales: wave 0, lane (r, part) -> the 16 bytes `part` of row tile
     // r's 16 row scales of the block.
     const char *ssrc = (const char *)(a.wscale_f + (size_t)rt0 * kbn * 16);
-    const uint32_t soff = (uint32_t)((((lane >> 2) & (RT - 1)) * kbn * 16 + (lane & 3) * 4) * 4);
+    const uint32_t soff = (uint32_t)((min(lane >> 2, RT - 1) * kbn * 16 + (lane & 3) * 4) * 4);
     if (SCALED && wave == 0) per_block++;
     const uint32_t lds0 = lds_address(lds);
     const uint32_t lane_off = lane * 16;
@@ -286,56 +301,95 @@ __global__ __launch_bounds__(kTaskThreads) void k_prefill_gemm(GemmArgs a, int r
             tot[r][p] = f32x4{-0.0f, -0.0f, -0.0f, -0.0f};
         }
 
-    // Epilogue operands of every tile of the wave, requested first.
+    // Epilogue operands of every tile of the wave: requested first when the
+    // wave holds at most 4 tiles; with more, after the main loop, where the
+    // operand registers are free again.
+    constexpr bool kLateEpi = RW * PW > 4;
     EpiOperands ep[RW][PW];
+    auto load_epilogues = [&]() {
 #pragma unroll
-    for (int r = 0; r < RW; r++)
+        for (int r = 0; r < RW; r++)
+#pragma unroll
+            for (int p = 0; p < PW; p++) {
+                const int s = (pt0 + wp * PW + p) * 16 + (lane & 15);
+                const int row0 = (rt0 + wr * RW + r) * 16 + (lane >> 4) * 4;
+                load_epilogue_static<EPI>(ep[r][p], a, s, row0, s < a.streams);
+                load_epilogue_dynamic<EPI>(ep[r][p], a, s >> 4, s, row0, s < a.streams);
+            }
+    };
+    // Late QKV operands: a lane's append position and pool block depend on
+    // its stream only (one per position tile), and are loaded before the
+    // main loop; the RoPE phases they select follow it.
+    QkvSlot qs[PW];
+    if constexpr (kLateEpi && EPI == EPI_QKV) {
 #pragma unroll
         for (int p = 0; p < PW; p++) {
             const int s = (pt0 + wp * PW + p) * 16 + (lane & 15);
-            const int row0 = (rt0 + wr * RW + r) * 16 + (lane >> 4) * 4;
-            load_epilogue_static<EPI>(ep[r][p], a, s, row0, s < a.streams);
-            load_epilogue_dynamic<EPI>(ep[r][p], a, s >> 4, s, row0, s < a.streams);
+            qs[p] = qkv_slot(a, s, s < a.streams);
         }
+    }
+    auto load_late_epilogues = [&]() {
+        if constexpr (EPI == EPI_QKV) {
+#pragma unroll
+            for (int r = 0; r < RW; r++)
+#pragma unroll
+                for (int p = 0; p < PW; p++) {
+                    const int s = (pt0 + wp * PW + p) * 16 + (lane & 15);
+                    const int row0 = (rt0 + wr * RW + r) * 16 + (lane >> 4) * 4;
+                    qkv_operands(ep[r][p], a, qs[p], row0, s < a.streams);
+                }
+        } else {
+            load_epilogues();
+        }
+    };
+    if constexpr (!kLateEpi) load_epilogues();
 
     // One 32-column block from LDS stage area st. Every tile's products
     // are issued term by term into its own registers (consecutive MFMAs
-    // never depend on each other), then the Q8 scales are applied.
-    auto block = [&](const uint16_t *st) {
+    // never depend on each other), then the Q8 scales are applied, one row
+    // tile at a time (so that only PW tiles' block products are live).
+    struct Frags {
         bf16x8 wa[RW], xt[PW][TERMS];
         float4 sc[RW];
+    };
+    auto load_frags = [&](Frags &f, const uint16_t *st) {
 #pragma unroll
         for (int r = 0; r < RW; r++) {
-            wa[r] = *(const bf16x8 *)(st + kB + (wr * RW + r) * 512 + lane * 8);
+            f.wa[r] = *(const bf16x8 *)(st + kB + (wr * RW + r) * 512 + lane * 8);
             if constexpr (SCALED)
-                sc[r] = *(const float4 *)((const float *)(st + kB + kA) + (wr * RW + r) * 16 +
-                                          (lane >> 4) * 4);
+                f.sc[r] = *(const float4 *)((const float *)(st + kB + kA) + (wr * RW + r) * 16 +
+                                            (lane >> 4) * 4);
         }
 #pragma unroll
         for (int p = 0; p < PW; p++)
 #pragma unroll
             for (int t = 0; t < TERMS; t++)
-                xt[p][t] = *(const bf16x8 *)(st + (wp * PW + p) * (TERMS * 512) + t * 512 + lane * 8);
+                f.xt[p][t] =
+                    *(const bf16x8 *)(st + (wp * PW + p) * (TERMS * 512) + t * 512 + lane * 8);
+    };
+    auto compute = [&](const Frags &f) {
+        const auto &wa = f.wa;
+        const auto &xt = f.xt;
+        const auto &sc = f.sc;
         if constexpr (SCALED) {
-            f32x4 c[RW][PW];
 #pragma unroll
-            for (int t = 0; t < TERMS; t++)
+            for (int r = 0; r < RW; r++) {
+                f32x4 c[PW];
 #pragma unroll
-                for (int r = 0; r < RW; r++)
+                for (int t = 0; t < TERMS; t++)
 #pragma unroll
                     for (int p = 0; p < PW; p++)
-                        c[r][p] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                            wa[r], xt[p][t], t == 0 ? f32x4{0.0f, 0.0f, 0.0f, 0.0f} : c[r][p], 0,
+                        c[p] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                            wa[r], xt[p][t], t == 0 ? f32x4{0.0f, 0.0f, 0.0f, 0.0f} : c[p], 0,
                             0, 0);
 #pragma unroll
-            for (int r = 0; r < RW; r++)
-#pragma unroll
                 for (int p = 0; p < PW; p++) {
-                    acc[r][p][0] = fmaf(sc[r].x, c[r][p][0], acc[r][p][0]);
-                    acc[r][p][1] = fmaf(sc[r].y, c[r][p][1], acc[r][p][1]);
-                    acc[r][p][2] = fmaf(sc[r].z, c[r][p][2], acc[r][p][2]);
-                    acc[r][p][3] = fmaf(sc[r].w, c[r][p][3], acc[r][p][3]);
+                    acc[r][p][0] = fmaf(sc[r].x, c[p][0], acc[r][p][0]);
+                    acc[r][p][1] = fmaf(sc[r].y, c[p][1], acc[r][p][1]);
+                    acc[r][p][2] = fmaf(sc[r].z, c[p][2], acc[r][p][2]);
+                    acc[r][p][3] = fmaf(sc[r].w, c[p][3], acc[r][p][3]);
                 }
+            }
         } else {
 #pragma unroll
             for (int t = 0; t < TERMS; t++)
@@ -346,13 +400,32 @@ __global__ __launch_bounds__(kTaskThreads) void k_prefill_gemm(GemmArgs a, int r
                         acc[r][p] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wa[r], xt[p][t],
                                                                             acc[r][p], 0, 0, 0);
         }
+    };
+    auto block = [&](const uint16_t *st) {
+        Frags f;
+        load_frags(f, st);
+        compute(f);
         // The next block's code is not scheduled into this one: that would
         // keep two blocks' products and operands live at once.
         __builtin_amdgcn_sched_barrier(0);
     };
+    auto chain_end = [&](int blocks_done) {
+        if ((blocks_done & (kChain - 1)) == 0) {
+            // End of a chain: the chains are summed in order.
+#pragma unroll
+            for (int r = 0; r < RW; r++)
+#pragma unroll
+                for (int p = 0; p < PW; p++) {
+#pragma unroll
+                    for (int e = 0; e < 4; e++)
+                        tot[r][p][e] = __fadd_rn(tot[r][p][e], acc[r][p][e]);
+                    acc[r][p] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+                }
+        }
+    };
 
-    int slot = 0;  // ring slot of stage sg
     for (int k = 0; k < NB - 1 && k < stages; k++) issue();
+    int slot = 0;  // ring slot of stage sg
     for (int sg = 0; sg < stages; sg++) {
         // Stage sg is in once at most the later stages' loads are in
         // flight (all of them issued while sg + NB - 2 < stages; in the
@@ -368,20 +441,10 @@ __global__ __launch_bounds__(kTaskThreads) void k_prefill_gemm(GemmArgs a, int r
         slot = slot == NB - 1 ? 0 : slot + 1;
 #pragma unroll
         for (int kk = 0; kk < KS; kk++) block(st + kk * kBlk);
-        if ((((sg + 1) * KS) & (kChain - 1)) == 0) {
-            // End of a chain: the chains are summed in order.
-#pragma unroll
-            for (int r = 0; r < RW; r++)
-#pragma unroll
-                for (int p = 0; p < PW; p++) {
-#pragma unroll
-                    for (int e = 0; e < 4; e++)
-                        tot[r][p][e] = __fadd_rn(tot[r][p][e], acc[r][p][e]);
-                    acc[r][p] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-                }
-        }
+        chain_end((sg + 1) * KS);
     }
 
+    if constexpr (kLateEpi) load_late_epilogues();
     bool bad = false;
 #pragma unroll
     for (int r = 0; r < RW; r++)
@@ -836,16 +899,25 @@ int launch_gemm(const GemmArgs &a, hipStream_t stream) {
 }
 
 // Tile shapes (rows x positions per work-group), chosen by measurement on
-// MI355X (4096 positions, two split terms):
-//  - 1536 / 2048 rows, K = 512 (QKV, MLP in): 128 x 64 with a 3 x 1 ring
-//    (50 KB of LDS, <= 128 VGPRs: two work-groups per CU, so that one's
-//    epilogue overlaps the other's main loop). MLP in: 31.1 us, against
-//    36.1 for 128 x 128 with a 2 x 2 ring (one work-group per CU).
+// MI355X (4096 positions, three split terms):
+//  - MLP in (2048 rows, K = 512): 256 x 128, waves of 4 x 4 tiles, a 3 x 1
+//    ring (126 KB of LDS, 256 work-groups, one per CU): 37.6 us against
+//    39.5 for 128 x 64 tiles two per CU (2 x 2 tiles per wave).
+//  - QKV (1536 rows): 192 x 128 (3 x 4 tiles per wave, 256 work-groups):
+//    32.2 against 32.8 us.
+//    With more than 4 tiles per wave the epilogue operands are loaded after
+//    the main loop. A software-pipelined loop (a wave's LDS reads of block
+//    k + 1 in flight during block k's MFMAs, two register sets of 4 x 2
+//    tiles) was slower for every shape: 34.1-47.6 against 13.8-37.9 us.
 //  - 512 rows (out, MLP out): 128 x 64 with a 2 x 2 ring (256 work-groups,
-//    one per CU): 10.6 / 28.4 us; deeper rings (3 x 2, 4 x 1 .. 8 x 1) and
-//    64-row or 32-position tiles were slower.
+//    one per CU): 13.8 / 37.1 us; deeper rings (3 x 2, 4 x 1 .. 8 x 1) and
+//    64-row or 32-position tiles were slower (two terms).
 template <int EPI, bool SCALED>
 int dispatch_gemm(const GemmArgs &a, hipStream_t stream) {
+    if constexpr (EPI == EPI_GELU_SPLIT)
+        if (a.n_rows % (8 * 256) == 0) return launch_gemm<EPI, SCALED, 4, 2, 4, 4, 3, 1>(a, stream);
+    if constexpr (EPI == EPI_QKV)
+        if (a.n_rows % (8 * 192) == 0) return launch_gemm<EPI, SCALED, 4, 2, 3, 4, 3, 1>(a, stream);
     if (a.n_rows > kWidth) return launch_gemm<EPI, SCALED, 4, 2, 2, 2, 3, 1>(a, stream);
     return launch_gemm<EPI, SCALED, 4, 2, 2, 2, 2, 2>(a, stream);
 }
@@ -885,8 +957,8 @@ extern "C" int pgpu_rows_split_ln(void *stream, const float *rows, const float *
         !(epsilon > 0.0f) || terms < 1 || terms > 3)
         return bad_arguments("pgpu_rows_split_ln");
     // Whole 16-row tiles: the rows past `streams` are written as zeros.
-    const int groups = (streams + 15) / 16 * (16 / kLnRowsPerGroup);
-    hipLaunchKernelGGL(k_rows_split_ln, dim3(groups), dim3(256), 0, (hipStream_t)stream, rows,
+    const int tiles = (streams + 15) / 16;
+    hipLaunchKernelGGL(k_rows_split_ln, dim3(tiles), dim3(512), 0, (hipStream_t)stream, rows,
                        weight, bias, epsilon, streams, terms, out_split, status);
     return launch_ok("pgpu_rows_split_ln");
 }
