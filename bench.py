@@ -145,31 +145,40 @@ def step_bytes(layers, contexts):
                                                          + KV_BYTES_PER_KEY))
 
 
-# Untimed steps before the warmup: the GPU's clock ramps up over the first
-# tens of milliseconds of load (measured on MI355X at B=64: steps 10-19 of a
-# cold start take 696 us, steps 20-29 680 us although they attend more keys;
-# after a 2 s idle the next 10 steps take 849 us and need ~20 steps to come
-# back). A serving loop runs at the settled clock.
-SETTLE_STEPS = 80
+# Untimed steps before the warmup. Two things slow the first steps of a run
+# (measured on MI355X at B=64): the GPU's clock ramps up over the first
+# ~150 ms of load after an idle spell (20-step blocks at 688.6, 688.9, 683.3
+# and then 673-674 us for the next 8 s), and a run that starts right after
+# another process freed a large allocation (a 103 GB KV pool) steps at
+# 688-690 us for ~1.1 s, then at 670-674 us from one block to the next. The
+# settle runs rounds of SETTLE_ROUND steps, the positions back at the
+# configured contexts after each, until SETTLE_SECONDS have passed, so the
+# timed steps measure the settled GPU. A serving loop runs at the settled
+# clock.
+SETTLE_ROUND = 80
+SETTLE_SECONDS = 2.0
 
 
 def run_decode(pkg, lib, layers, streams, lengths, steps, warmup, seed, groups=None,
-               eager=False, settle=SETTLE_STEPS):
-    # headroom: the settling steps, or the timed steps and then the
+               eager=False, settle_s=SETTLE_SECONDS):
+    # headroom: a settling round, or the timed steps and then the
     # roofline's timed launches
-    d = DecodeSetup(pkg, lib, layers, streams, lengths, max(settle, steps + warmup + 41) + 8,
-                    seed)
+    d = DecodeSetup(pkg, lib, layers, streams, lengths,
+                    max(SETTLE_ROUND, steps + warmup + 41) + 8, seed)
     if groups:
         assert lib.phonon_flow_batch_set_groups(d.batch, groups), last_error(lib)
     if eager:
         assert lib.phonon_flow_batch_set_graph(d.batch, 0), last_error(lib)
     # Settle the clock, then back to the configured contexts: the warmup and
     # timed steps attend exactly the keys they would from a cold start.
-    for i in range(settle):
-        d.step()
-        if i % 10 == 9:
-            assert lib.pgpu_stream_sync(d.stream), last_error(lib)
-    if settle:
+    settled = 0
+    t_settle = time.perf_counter()
+    while settle_s > 0 and time.perf_counter() - t_settle < settle_s:
+        for i in range(SETTLE_ROUND):
+            d.step()
+            if i % 10 == 9:
+                assert lib.pgpu_stream_sync(d.stream), last_error(lib)
+        settled += SETTLE_ROUND
         assert lib.phonon_flow_batch_sync(d.batch), "non-finite value while settling"
         d.reset()
     for _ in range(warmup):
@@ -189,7 +198,7 @@ def run_decode(pkg, lib, layers, streams, lengths, steps, warmup, seed, groups=N
     # keys attended at step i = position + 1
     total_bytes = sum(step_bytes(layers, first + i + 1) for i in range(steps))
     return d, {"ms": ms, "wall_s": wall, "clean": bool(clean), "bytes": total_bytes,
-               "first_positions": first}
+               "first_positions": first, "settle_steps": settled}
 
 
 PMC_SUMMARY = "profiles/k_attention_b64_hbm_traffic.md"
@@ -1225,7 +1234,7 @@ def main():
     line = {
         "metric": "decode frames/sec at B=64 (12L d512 Q8); achieved HBM GB/s vs peak",
         "value": round(value, 1), "unit": "frames/s", "n_gpus": 1, "steps": args.steps,
-        "warmup": args.warmup, "settle_steps": SETTLE_STEPS,
+        "warmup": args.warmup, "settle_steps": r["settle_steps"],
         "ms_per_step": round(ms_step, 4), "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "fp32",
         "data": "synthetic (seeded Q8 weights, N(0,1) KV contexts)",
