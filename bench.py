@@ -23,7 +23,6 @@ import ctypes
 import importlib.util
 import json
 import os
-import subprocess
 import sys
 import time
 
@@ -1015,14 +1014,27 @@ def cpu_flow_head(seed=11, budget_s=2.0):
 
 def cpu_host():
     """What the CPU baselines ran on: nproc, the CPUs this process may use,
-    the CPU model and whether SMT is on (lscpu / sysfs)."""
+    the CPU model and whether SMT is on, read from /proc/cpuinfo and sysfs
+    (no child process)."""
     info = {"nproc": os.cpu_count(), "usable_cpus": len(os.sched_getaffinity(0))}
     try:
-        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
-        fields = dict(line.split(":", 1) for line in out.splitlines() if ":" in line)
-        info["model"] = fields.get("Model name", "").strip()
-        info["threads_per_core"] = int(fields.get("Thread(s) per core", "0").strip() or 0)
-    except (OSError, ValueError, subprocess.SubprocessError):
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                key, _, value = line.partition(":")
+                if key.strip() == "model name":
+                    info["model"] = value.strip()
+                    break
+    except OSError:
+        pass
+    try:
+        with open("/sys/devices/system/cpu/cpu0/topology/thread_siblings_list") as f:
+            # a cpulist ("0,64", "0-1"): the logical CPUs sharing cpu0's core
+            count = 0
+            for part in f.read().strip().split(","):
+                first, _, last = part.partition("-")
+                count += int(last or first) - int(first) + 1
+            info["threads_per_core"] = count
+    except (OSError, ValueError):
         pass
     try:
         with open("/sys/devices/system/cpu/smt/active") as f:
