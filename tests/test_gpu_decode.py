@@ -446,6 +446,64 @@ def test_batch_full_size_vs_oracle(lib, oracle, oracle_mod, syn, pkg, streams, l
         assert err <= TOL, (s, int(lengths[s]), err)
 
 
+def test_batch_b64_benchmark_weights_closed_loop_vs_oracle(lib, oracle, oracle_mod, syn, pkg):
+    """The decode benchmark itself: B=64 streams x 12 layers with the
+    benchmark's own (unscaled) weights, contexts U{1..2048} on shuffled
+    tables, the library's default step (one launch), four steps with each
+    output fed back as the next input. Every 4th stream, every step, against
+    the oracle's 12-layer stack step on the same inputs over its own copy of
+    the stream's context (the keys appended by its own earlier steps): within
+    1e-4 normwise (measured: 2.8e-5 at worst)."""
+    streams, layers, steps = 64, 12, 4
+    model = syn.flow_model(2026, layers)
+    ol = helpers.oracle_layers(oracle, model)
+    om = oracle_mod.OracleModel(oracle, ol)
+    views = pkg.Views()
+    w = views.layers(model)
+    rng = np.random.default_rng(2031)
+    lengths = rng.integers(1, 2049, size=streams) - 1   # positions; keys = lengths + 1
+    lengths[0] = 0
+    max_pos = int(lengths.max()) + steps
+    table_len = (max_pos + 15) // 16
+    blocks = streams * table_len
+    keys = rng.standard_normal((layers, max_pos, 512)).astype(np.float32)
+    vals = rng.standard_normal((layers, max_pos, 512)).astype(np.float32)
+    print(f"B=64 x 12 layers, benchmark weights: {steps} closed-loop steps", flush=True)
+    bt = Batch(lib, w, layers, streams, max_pos, blocks)
+    ids = np.zeros(blocks, np.int32)
+    assert lib.phonon_kv_pool_alloc(bt.pool, blocks, i32p(ids))
+    tables = np.ascontiguousarray(rng.permutation(ids).reshape(streams, table_len))
+    for s in range(streams):
+        if lengths[s]:
+            assert lib.phonon_kv_pool_write(bt.pool, i32p(tables[s]), table_len, 0,
+                                            int(lengths[s]), fp(keys), fp(vals), max_pos)
+    pos = lengths.astype(np.uintp)
+    assert lib.phonon_flow_batch_set_streams(
+        bt.batch, streams, pos.ctypes.data_as(ctypes.POINTER(ctypes.c_size_t)), i32p(tables),
+        table_len)
+    xs = [rng.standard_normal((streams, 512)).astype(np.float32)]
+    for _ in range(steps):
+        y = np.zeros_like(xs[-1])
+        assert lib.phonon_flow_batch_step(bt.batch, fp(xs[-1]), 10000.0, fp(y)), \
+            pkg.last_error(lib)
+        xs.append(y)
+    bt.close()
+    sampled = np.arange(0, streams, 4)
+    okeys = np.ascontiguousarray(np.broadcast_to(keys, (len(sampled),) + keys.shape))
+    ovals = np.ascontiguousarray(np.broadcast_to(vals, (len(sampled),) + vals.shape))
+    worst = 0.0
+    for t in range(steps):
+        ok, ref = om.stack_step_streams(okeys, ovals, max_pos, lengths[sampled] + t,
+                                        xs[t][sampled], 16)
+        assert ok
+        for i, s in enumerate(sampled):
+            err = helpers.normwise(xs[t + 1][s], ref[i])
+            worst = max(worst, err)
+            assert err <= TOL, (t, int(s), int(lengths[s]) + t, err)
+    print(f"B=64 x 12 layers, benchmark weights: max normwise error vs oracle {worst:.2e} over "
+          f"{steps} steps of {len(sampled)} streams")
+
+
 @pytest.mark.parametrize("weights", ["scaled", "benchmark"])
 def test_batch_b256_twelve_layers_vs_oracle(lib, oracle, oracle_mod, syn, pkg, weights):
     """The large-batch decode at its full shape: B=256 streams, contexts
