@@ -534,13 +534,14 @@ def task_trace_summary(sched, trace):
 
 
 def b1_with_prefill(pkg, lib, layers, seed, prompt=256, frames=750, warmup=10, mode=None,
-                    trace_steps=0):
+                    trace_steps=0, handoff=None):
     """B=1: one stream, `layers` layers. A `prompt`-position prefill (the
     batched causal prefill, positions 0..prompt-1 through every layer in one
     pass), then `frames` decode steps, each step's output fed back as the
     next input. Run once untimed (prefill + `warmup` steps), then again from
     position 0: prefill and decode timed separately with HIP events. `mode`:
-    the step's pipeline mode (None: the library's default)."""
+    the step's pipeline mode (None: the library's default); `handoff`: the
+    one-launch step's hand-off mode (None: the library's default)."""
     import speech_mac_amd.synthetic as syn
     max_pos = prompt + frames + 16
     table_len = (max_pos + 15) // 16
@@ -557,6 +558,8 @@ def b1_with_prefill(pkg, lib, layers, seed, prompt=256, frames=750, warmup=10, m
         last_error(lib)
     if mode is not None:
         assert lib.phonon_flow_batch_set_pipeline(batch, mode), last_error(lib)
+    if handoff is not None:
+        assert lib.phonon_flow_batch_set_handoff(batch, handoff), last_error(lib)
     stream = lib.phonon_flow_batch_stream(batch)
     rng = np.random.default_rng(seed + 61)
     pin = pkg.DeviceBuffer(lib, prompt * 512 * 4)
@@ -629,7 +632,8 @@ def b1_with_prefill(pkg, lib, layers, seed, prompt=256, frames=750, warmup=10, m
                         f"prefill, then {frames} decode frames (contexts {prompt + 1}.."
                         f"{prompt + frames}), each output fed back as the next input; "
                         + ("the library's default step mode" if mode is None
-                           else f"step pipeline mode {mode}"),
+                           else f"step pipeline mode {mode}")
+                        + ("" if handoff is None else f", hand-off mode {handoff}"),
             "clean": clean, **({"task_trace": traced} if traced else {})}
 
 
@@ -1178,6 +1182,12 @@ def main():
     ap.add_argument("--b1-trace", action="store_true",
                     help="run only the B=1 prefill + decode workload, then trace three "
                          "one-launch steps task by task and print each phase's timing")
+    ap.add_argument("--b1-handoff", type=int, default=None,
+                    help="the one-launch hand-off mode of the --b1-trace run (default: the "
+                         "library's)")
+    ap.add_argument("--b1-handoffs", type=str, default="",
+                    help="run only the B=1 prefill + decode workload, once per listed "
+                         "one-launch hand-off mode (comma-separated, e.g. 3,4)")
     ap.add_argument("--b1-modes", type=str, default="",
                     help="run only the B=1 prefill + decode workload, once per listed step "
                          "pipeline mode (comma-separated, e.g. 0,2)")
@@ -1202,8 +1212,15 @@ def main():
                                                       prefill_attention=kind)), flush=True)
         return
     if args.b1_trace:
-        print(json.dumps(b1_with_prefill(pkg, lib, args.layers, args.seed, trace_steps=3)),
-              flush=True)
+        print(json.dumps(b1_with_prefill(pkg, lib, args.layers, args.seed, trace_steps=3,
+                                         handoff=args.b1_handoff)), flush=True)
+        return
+    if args.b1_handoffs:
+        for rep_i in range(2):
+            for h in (int(m) for m in args.b1_handoffs.split(",")):
+                print(json.dumps(dict(b1_with_prefill(pkg, lib, args.layers, args.seed,
+                                                      handoff=h), handoff=h, repeat=rep_i)),
+                      flush=True)
         return
     if args.b1_modes:
         for mode in (int(m) for m in args.b1_modes.split(",")):

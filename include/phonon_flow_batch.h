@@ -153,8 +153,12 @@ int phonon_flow_batch_set_attention_rounds(PhononFlowBatch *batch, int rounds);
  * split partials as tagged words, the rest through counters (an attention
  * task then need not wait for its partial to reach memory); 3 as 1, but
  * the out-projection tasks merge the split partials themselves (no
- * attention task waits to merge); -1 (the default) by the batch size.
- * Results are identical for every choice. */
+ * attention task waits to merge); 4 as 3, with no MLP-out phase: each
+ * MLP-in task multiplies its GELU rows by its columns of the MLP-out matrix
+ * and the next layer's QKV tasks add the 32 partials (batches of at most 4
+ * streams; larger batches run mode 3); -1 (the default) by the batch size.
+ * Modes 0-3 give identical results; mode 4 sums the MLP-out products in
+ * another order (within fp32 rounding of the others). */
 int phonon_flow_batch_set_handoff(PhononFlowBatch *batch, int tagged);
 /* Kernel timing: while `before` and `after` are events (pgpu_event_create),
  * each step launches its kernels directly (no graph replay) and records

@@ -157,7 +157,9 @@ int pgpu_q8_gemv(void *stream, const int8_t *values, const uint16_t *scales, int
  *          completes a (stream, head) merges all its splits
  *   OUT    out projection + residual, 64 rows each
  *   MLP_IN LayerNorm 2 + MLP in projection + GELU, 64 rows each
- *   MLP_OUT MLP out projection + residual, 16 rows each
+ *   MLP_OUT MLP out projection + residual, 16 rows each (FUSED_MLP: the last
+ *          layer only, its output rows from r and the MLP_IN partials,
+ *          64 dimensions each)
  * Descriptor (PGPU_FLOW_TASK) bits: kind [0,3), layer [3,9), tile [9,17),
  * index [17,32); an
  * ATTN index is head | unit << 3 | (stream in tile) << 11, for splits
@@ -191,6 +193,20 @@ int pgpu_q8_gemv(void *stream, const int8_t *values, const uint16_t *scales, int
 #define PGPU_FLOW_HANDOFF_PARTS 2   /* split partials tagged, the rest by counters */
 #define PGPU_FLOW_HANDOFF_MERGE_OUT 3 /* TAGGED, with no merging attention task: the out
                                        projection merges the split partials itself */
+#define PGPU_FLOW_HANDOFF_FUSED_MLP 4 /* MERGE_OUT without an MLP_OUT phase (one tile, decode
+                                       only): MLP_IN task i multiplies its 64 GELU rows by
+                                       columns [64i, 64i + 64) of the MLP-out matrix,
+                                       stores the 512-row partial in `mlp_parts` and counts;
+                                       the next layer's QKV tasks wait for the count and add
+                                       the PGPU_FLOW_MLP_IN_TASKS partials in task order to
+                                       r (QKV tasks 0..7 hand x on to the out projection);
+                                       after the last layer PGPU_FLOW_FUSED_OUT_TASKS
+                                       MLP_OUT tasks (64 dimensions each) write the output
+                                       rows the same way */
+#define PGPU_FLOW_FUSED_OUT_TASKS 8
+#define PGPU_FLOW_FUSED_MAX_STREAMS 4 /* streams of a FUSED_MLP step */
+#define PGPU_FLOW_SCHEDULE_PREFILL 1   /* pgpu_flow_schedule flags */
+#define PGPU_FLOW_SCHEDULE_FUSED_MLP 2
 
 #define PGPU_FLOW_TASK(kind, layer, tile, index)                                      \
     ((uint32_t)(kind) | (uint32_t)(layer) << 3 | (uint32_t)(tile) << 9 |             \
@@ -247,6 +263,9 @@ typedef struct {
                                       [max_splits][PGPU_FLOW_PART_WORDS]: P.V [64], max,
                                       sum */
     uint32_t tag;                  /* (all but COUNTER) this step's tag, never 0 */
+    float *mlp_parts;              /* (dev, FUSED_MLP) [layer_count][PGPU_FLOW_MLP_IN_TASKS]
+                                      [16][512]: each MLP_IN task's partial of the MLP-out
+                                      projection */
 } pgpu_flow_step;
 
 /* Placement of each tile's projection chain in a task list, on a model
@@ -267,10 +286,12 @@ typedef struct {
  * for each layer l and tile t, ATTN(t, l) by (stream, split, head) with
  * heads fastest, with the chains OUT, MLP_IN, MLP_OUT (l) and QKV (l+1) of
  * earlier tiles interleaved as `place` (NULL: all zero) sets. Every task
- * follows the tasks it waits for; prefill = 1 lists all QKV of a layer
- * before its first ATTN (and ignores `place`). Host code only. */
+ * follows the tasks it waits for. flags: PGPU_FLOW_SCHEDULE_PREFILL lists
+ * all QKV of a layer before its first ATTN (and ignores `place`);
+ * PGPU_FLOW_SCHEDULE_FUSED_MLP (decode, one tile) lists no MLP_OUT tasks but
+ * the last layer's PGPU_FLOW_FUSED_OUT_TASKS. Host code only. */
 size_t pgpu_flow_schedule(size_t streams, size_t layers, const size_t *units,
-                          const pgpu_flow_placement *place, int prefill, uint32_t *schedule,
+                          const pgpu_flow_placement *place, int flags, uint32_t *schedule,
                           size_t capacity);
 /* prefill = 1: pseudo-streams of one stream share its block table, so an
  * ATTN task waits for the QKV tasks of every tile (one layer-wide count).

@@ -183,6 +183,35 @@ __device__ inline uint64_t *tagged_rows(const pgpu_flow_step &f, int layer, int 
     return f.rows + ((size_t)layer * ROWS_KINDS + which) * (size_t)f.tiles * 16 * kWidth;
 }
 
+// Fused MLP: MLP_IN task `task`'s partial of `layer`, [16 streams][512]
+// fp32.
+__device__ inline float *fused_parts(const pgpu_flow_step &f, int layer, int task) {
+    return f.mlp_parts + ((size_t)layer * PGPU_FLOW_MLP_IN_TASKS + task) * 16 * kWidth;
+}
+
+// Fused MLP, after the last layer: output dimensions [64 index, 64 index +
+// 64) of each stream (wave n: stream n of the tile) = r + the layer's MLP
+// partials, summed as the QKV prologue sums them (fused_sum), stored plainly
+// (read after the launch).
+__device__ inline void fused_output_task(const pgpu_flow_step &f, int layer, int tile, int index,
+                                         uint32_t tag) {
+    wait_for(f, layer, tile, PGPU_FLOW_MLP_IN, PGPU_FLOW_MLP_IN_TASKS)();
+    trace_mark(f, 1);
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int d = index * kHeadDim + (threadIdx.x & 63);
+    bool bad = false;
+    if (wave < min(PGPU_FLOW_FUSED_MAX_STREAMS, f.streams - tile * 16)) {  // uniform
+        const int s = tile * 16 + wave;
+        const float x = fused_sum(tagged_rows(f, layer, ROWS_R) + (size_t)s * kWidth,
+                                  fused_parts(f, layer, 0), 16, s, d,
+                                  TagPoll{tag, f.status, wait_ticks(f), false});
+        f.output[(size_t)s * kWidth + d] = x;
+        bad = !isfinite(x);
+    }
+    flag_nonfinite(f.status, bad);
+    trace_mark(f, 2);
+}
+
 // Attention gate of the merge-in-out mode (outside a prefill): a first wait
 // for one of the head's QKV tasks (a count without a drain), then the
 // unit's q and the appended key's K and V polled as tagged words
@@ -364,7 +393,8 @@ __device__ inline void attention_task(const pgpu_flow_step &f, const pgpu_paged_
     float mm[R], ll[R];
     int count;
     constexpr bool tagged_parts = MODE != PGPU_FLOW_HANDOFF_COUNTER;
-    constexpr bool MO = MODE == PGPU_FLOW_HANDOFF_MERGE_OUT;
+    constexpr bool MO =
+        MODE == PGPU_FLOW_HANDOFF_MERGE_OUT || MODE == PGPU_FLOW_HANDOFF_FUSED_MLP;
     int state;
     if constexpr (MO && !PRE) {
         const TaggedQkvGate gate{wait_for(f, layer, tile, PGPU_FLOW_QKV_HEAD + head, 1u),
@@ -480,7 +510,8 @@ __device__ inline void flow_step_task(const pgpu_flow_step &f, const pgpu_paged_
     const pgpu_flow_layer &ly = f.layers[layer];
     const float *norm = ly.norms;
     const int live = min(16, f.streams - tile * 16);
-    constexpr bool merge_out = MODE == PGPU_FLOW_HANDOFF_MERGE_OUT;
+    constexpr bool fused = MODE == PGPU_FLOW_HANDOFF_FUSED_MLP && !PRE;
+    constexpr bool merge_out = MODE == PGPU_FLOW_HANDOFF_MERGE_OUT || fused;
     constexpr bool tagged = merge_out || MODE == PGPU_FLOW_HANDOFF_TAGGED;
     const bool last = layer + 1 == f.layer_count;
     uint64_t *const ready_mark =
@@ -504,7 +535,8 @@ __device__ inline void flow_step_task(const pgpu_flow_step &f, const pgpu_paged_
         a.rope = (const float2 *)f.rope;
         if constexpr (tagged) {
             // The previous layer's output, polled once its MLP-in tasks are
-            // done (the phase before its producers).
+            // done (the phase before its producers; with the fused MLP, the
+            // MLP-in tasks are its producers, and their count is the wait).
             a.ln_x = layer == 0 ? f.input : nullptr;
             a.tx = layer == 0 ? nullptr : tagged_rows(f, layer - 1, ROWS_X);
             a.ready_mark = ready_mark;
@@ -514,11 +546,25 @@ __device__ inline void flow_step_task(const pgpu_flow_step &f, const pgpu_paged_
                 a.tqkv = tagged_rows(f, layer, ROWS_Q);
                 a.tqkv_part = (size_t)f.tiles * 16 * kWidth;
             }
-            gemm_wide_task<SRC_LN, EPI_QKV, Q8>(
-                a, index, tile, lds,
-                layer == 0 ? no_wait(f)
-                           : wait_for(f, layer - 1, tile, PGPU_FLOW_MLP_IN,
-                                      PGPU_FLOW_MLP_IN_TASKS));
+            const FlowWait w = layer == 0 ? no_wait(f)
+                                          : wait_for(f, layer - 1, tile, PGPU_FLOW_MLP_IN,
+                                                     PGPU_FLOW_MLP_IN_TASKS);
+            bool done = false;
+            if constexpr (fused) {
+                if (layer > 0) {
+                    // x = r + the previous layer's MLP partials; tasks 0..7
+                    // hand 64 dimensions each on to the out projection.
+                    a.tx = nullptr;
+                    a.tres = tagged_rows(f, layer - 1, ROWS_R);
+                    a.tmlp = fused_parts(f, layer - 1, 0);
+                    a.mlp_streams = 16;
+                    a.tpub = tagged_rows(f, layer - 1, ROWS_X);
+                    a.pub0 = index < kHeads ? index * kHeadDim : -1;
+                    gemm_wide_task<SRC_LN_PARTS, EPI_QKV, Q8>(a, index, tile, lds, w);
+                    done = true;
+                }
+            }
+            if (!done) gemm_wide_task<SRC_LN, EPI_QKV, Q8>(a, index, tile, lds, w);
             if constexpr (merge_out && !PRE) {
                 // A count for first waits only: no drain.
                 __syncthreads();
@@ -594,7 +640,18 @@ __device__ inline void flow_step_task(const pgpu_flow_step &f, const pgpu_paged_
         a.k_cols = kWidth;
         a.out_split = hidden_rows(f, layer);
         a.out_kb = kFfn / 32;
-        if constexpr (tagged) {
+        if constexpr (fused) {
+            // r polled as in MERGE_OUT; the task's partial of the MLP-out
+            // projection is stored write-through, drained and counted
+            // (flow_signal below).
+            a.tx = tagged_rows(f, layer, ROWS_R);
+            a.ready_mark = ready_mark;
+            a.w2 = ly.values[3];
+            a.w2scale = ly.scales[3];
+            a.tmlp_out = fused_parts(f, layer, index);
+            gemm_wide_task<SRC_LN, EPI_GELU_W2, Q8>(
+                a, index, tile, lds, wait_for(f, layer, tile, PGPU_FLOW_QKV_HEAD + kHeads - 1, 3u));
+        } else if constexpr (tagged) {
             // r, polled once every (stream, head) of the tile is merged
             // (with the merge in the out projection: once the tile's QKV
             // tasks are done, as the out projection itself).
@@ -614,6 +671,10 @@ __device__ inline void flow_step_task(const pgpu_flow_step &f, const pgpu_paged_
         break;
     }
     case PGPU_FLOW_MLP_OUT: {
+        if constexpr (fused) {
+            fused_output_task(f, layer, tile, index, tag);
+            break;
+        }
         GemmArgs a = base_args(f, ly, 3, tag);
         a.xs = hidden_rows(f, layer);
         a.n_rows = kWidth;
@@ -659,7 +720,10 @@ void launch_step(const pgpu_flow_step *step, const pgpu_paged_kv *kv, hipStream_
     auto kernel = step->tagged == PGPU_FLOW_HANDOFF_TAGGED      ? k_flow_step<Q8, 1, PRE, R>
                   : step->tagged == PGPU_FLOW_HANDOFF_PARTS     ? k_flow_step<Q8, 2, PRE, R>
                   : step->tagged == PGPU_FLOW_HANDOFF_MERGE_OUT ? k_flow_step<Q8, 3, PRE, R>
-                                                                : k_flow_step<Q8, 0, PRE, R>;
+                  : step->tagged == PGPU_FLOW_HANDOFF_FUSED_MLP
+                      // decode only (pgpu_flow_launch rejects a fused prefill)
+                      ? k_flow_step<Q8, PRE ? 3 : 4, PRE, R>
+                      : k_flow_step<Q8, 0, PRE, R>;
     hipLaunchKernelGGL(kernel, dim3(step->tasks), dim3(kTaskThreads), 0, stream, *step, *kv);
 }
 
@@ -687,14 +751,17 @@ extern "C" int pgpu_flow_launch(void *stream, const pgpu_flow_step *step,
         !step->positions || step->table_stride <= 0 || !step->rope || !step->schedule ||
         !step->tasks || !step->phase || !step->split_done || !step->status ||
         step->attn_rounds < 1 || step->attn_rounds > PGPU_FLOW_ATTN_ROUNDS ||
-        step->tagged < PGPU_FLOW_HANDOFF_COUNTER || step->tagged > PGPU_FLOW_HANDOFF_MERGE_OUT ||
+        step->tagged < PGPU_FLOW_HANDOFF_COUNTER || step->tagged > PGPU_FLOW_HANDOFF_FUSED_MLP ||
+        (step->tagged == PGPU_FLOW_HANDOFF_FUSED_MLP &&
+         (step->prefill || step->tiles != 1 || step->streams > PGPU_FLOW_FUSED_MAX_STREAMS ||
+          !step->mlp_parts)) ||
         (step->tagged != PGPU_FLOW_HANDOFF_COUNTER &&
          (!step->parts || !step->tag || step->max_splits > 32)) ||
         step->pos_delta < 0 || step->clear_words % 4 ||
         (step->clear_words && (!step->clear || (step->clear_words + PGPU_FLOW_CLEAR_WORDS - 1) /
                                                        PGPU_FLOW_CLEAR_WORDS > step->tasks)) ||
-        ((step->tagged == PGPU_FLOW_HANDOFF_TAGGED ||
-          step->tagged == PGPU_FLOW_HANDOFF_MERGE_OUT) && !step->rows) ||
+        ((step->tagged == PGPU_FLOW_HANDOFF_TAGGED || step->tagged == PGPU_FLOW_HANDOFF_MERGE_OUT ||
+          step->tagged == PGPU_FLOW_HANDOFF_FUSED_MLP) && !step->rows) ||
         step->pool_offset < 0 || step->pool_offset + step->layer_count > kv->layers)
         return bad_arguments("pgpu_flow_launch");
     if (step->prefill) {

@@ -54,6 +54,7 @@ enum Source {
     SRC_LN_MOD = 4,
     SRC_SPLIT_LDS = 5,
     SRC_ATTN_TAGGED = 6,  // merge of tagged split partials, polled (one-launch step)
+    SRC_LN_PARTS = 7,     // LayerNorm of r + the fused MLP's partials, polled (one-launch step)
 };
 enum Epilogue {
     EPI_STORE = 0,
@@ -62,6 +63,7 @@ enum Epilogue {
     EPI_QKV = 3,
     EPI_SILU_SPLIT = 4,  // split fragments of SiLU((dot + bias) + bias2)
     EPI_GATED = 5,       // residual + gate * (dot + bias); optionally also split fragments
+    EPI_GELU_W2 = 6,     // GELU, then times the task's 64 columns of W2: a tagged partial
 };
 
 constexpr int kTaskWaves = 8, kTaskThreads = 64 * kTaskWaves;
@@ -210,6 +212,21 @@ struct GemmArgs {
     uint64_t *tqkv;
     size_t tqkv_part;
     uint64_t *ready_mark;
+    // Fused MLP (one-launch step, PGPU_FLOW_HANDOFF_FUSED_MLP):
+    // SRC_LN_PARTS: x = r + sum of the PGPU_FLOW_MLP_IN_TASKS partials at
+    // tmlp ([task][mlp_streams][512] fp32), r at tres; QKV tasks with
+    // pub0 >= 0 also hand x's dimensions [pub0, pub0 + 64) on as tagged
+    // words at tpub ([tiles*16][512]).
+    const float *tmlp;
+    int mlp_streams;
+    uint64_t *tpub;
+    int pub0;
+    // EPI_GELU_W2: the MLP-out matrix (fragments, K = 2048) and its scale
+    // plane; the task's partial goes to tmlp_out ([mlp_streams][512] fp32,
+    // write-through).
+    const void *w2;
+    const uint16_t *w2scale;
+    float *tmlp_out;
 };
 
 // ---------------------------------------------------------------------------
@@ -741,6 +758,116 @@ __device__ inline bool prologue_attn(const GemmArgs &a, int st, uint16_t *bsh) {
     return bad;
 }
 
+// Fused MLP (one-launch step, PGPU_FLOW_HANDOFF_FUSED_MLP): dimension d of
+// stream s of a layer output, x = r + (P_0 + P_1 + ... + P_31). The MLP_IN
+// tasks' partials (P_j at parts[(j * pstreams + s) * 512 + d]) are fp32
+// values their tasks drained before counting: the caller has seen the count,
+// so they are plain loads, shared through the XCD's L2 by the tasks that
+// read them. r is the out projection's tagged row (r_row, the same in every
+// lane of the wave), polled. Every lane of the wave must call it.
+__device__ inline float fused_sum(const uint64_t *r_row, const float *parts, int pstreams, int s,
+                                  int d, const TagPoll &tp) {
+    constexpr int P = PGPU_FLOW_MLP_IN_TASKS;
+    typedef __attribute__((ext_vector_type(2))) uint32_t u32x2;
+    const __amdgpu_buffer_rsrc_t rr = tag_rsrc(r_row, (uint32_t)(kWidth * 8));
+    const __amdgpu_buffer_rsrc_t rp =
+        tag_rsrc(parts, (uint32_t)((size_t)P * pstreams * kWidth * sizeof(float)));
+    // r's word and every partial in one round trip; r is polled again only
+    // if its word does not carry the tag yet.
+    u32x2 w = __builtin_amdgcn_raw_buffer_load_b64(rr, (uint32_t)(d * 8), 0, 16);
+    const uint32_t off = (uint32_t)(((size_t)s * kWidth + d) * sizeof(float));
+    const uint32_t step = (uint32_t)((size_t)pstreams * kWidth * sizeof(float));
+    float v[P];
+#pragma unroll
+    for (int j = 0; j < P; j++)
+        v[j] = bitsf(__builtin_amdgcn_raw_buffer_load_b32(rp, off, j * step, 0));
+    const uint64_t t0 = wall_clock64();
+    for (int round = 0; !__all(w.y == tp.tag); round++) {
+        if (tag_give_up(tp, t0, round)) break;
+        __builtin_amdgcn_s_sleep(1);
+        __asm__ volatile("" ::: "memory");
+        w = __builtin_amdgcn_raw_buffer_load_b64(rr, (uint32_t)(d * 8), 0, 16);
+    }
+    float sum = v[0];
+#pragma unroll
+    for (int j = 1; j < P; j++) sum = __fadd_rn(sum, v[j]);
+    return __fadd_rn(bitsf(w.x), sum);  // residual + dot, as EPI_RESIDUAL
+}
+
+// SRC_LN_PARTS: the fused MLP's QKV prologue. For each live stream n of
+// tile st (at most PGPU_FLOW_FUSED_MAX_STREAMS), thread d computes
+// dimension d of the layer input x (fused_sum; dimensions [pub0, pub0 + 64)
+// are handed on at tpub for the out projection's residual) and its
+// LayerNorm (two-pass fp32 moments over the work-group, the waves' sums
+// added in wave order; y = ((x - mean) * rstd) * w + b, as rows_ln_values)
+// into an fp32 staging row; then each thread writes whole 16-byte split
+// records of the LDS operand buffer (lds_store8: 8 columns of one stream),
+// zeros for the streams past the batch. Returns true if a live output is
+// not finite.
+__device__ inline bool prologue_ln_parts(const GemmArgs &a, int st, uint16_t *bsh) {
+    constexpr int N = PGPU_FLOW_FUSED_MAX_STREAMS;
+    __shared__ float red[2][N][kTaskWaves];
+    __shared__ __align__(16) float stage[N][kWidth];
+    const int d = threadIdx.x, wave = d >> 6, lane = d & 63;
+    const int live = min(N, a.streams - st * 16);
+    const float lw = a.ln_w[d], lb = a.ln_b[d];
+    const bool pub = a.tpub && a.pub0 >= 0 && d >= a.pub0 && d < a.pub0 + 64;
+    float x[N];
+#pragma unroll
+    for (int n = 0; n < N; n++) {
+        x[n] = 0.0f;
+        if (n >= live) break;  // uniform
+        const int s = st * 16 + n;
+        x[n] = fused_sum(a.tres + (size_t)s * kWidth, a.tmlp, a.mlp_streams, s, d, a.tp);
+        if (pub) store_tagged(a.tpub + (size_t)s * kWidth + d, x[n], a.tp.tag);
+        const float sum = wave_sum64(x[n]);
+        if (lane == 0) red[0][n][wave] = sum;
+    }
+    __syncthreads();
+    float mean[N];
+#pragma unroll
+    for (int n = 0; n < N; n++) {
+        mean[n] = 0.0f;
+        if (n >= live) break;
+        float t = red[0][n][0];
+#pragma unroll
+        for (int w = 1; w < kTaskWaves; w++) t = __fadd_rn(t, red[0][n][w]);
+        mean[n] = t * (1.0f / kWidth);
+        const float c = __fsub_rn(x[n], mean[n]);
+        const float q = wave_sum64(__fmul_rn(c, c));
+        if (lane == 0) red[1][n][wave] = q;
+    }
+    __syncthreads();
+    bool bad = false;
+#pragma unroll
+    for (int n = 0; n < N; n++) {
+        if (n >= live) break;
+        float t = red[1][n][0];
+#pragma unroll
+        for (int w = 1; w < kTaskWaves; w++) t = __fadd_rn(t, red[1][n][w]);
+        const float var = t * (1.0f / kWidth);
+        const float rstd = 1.0f / sqrtf(var + a.ln_eps);
+        const float y = __fadd_rn(__fmul_rn(__fmul_rn(__fsub_rn(x[n], mean[n]), rstd), lw), lb);
+        bad |= !isfinite(y);
+        stage[n][d] = y;
+    }
+    __syncthreads();
+    // Records (stream n, 8-column group c): n = r % 16, c = r / 16.
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+        const int r = threadIdx.x + i * kTaskThreads, n = r & 15, c = r >> 4;
+        float v[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+        if (n < live) {
+            const float4 v0 = *(const float4 *)&stage[n][c * 8];
+            const float4 v1 = *(const float4 *)&stage[n][c * 8 + 4];
+            v[0] = v0.x; v[1] = v0.y; v[2] = v0.z; v[3] = v0.w;
+            v[4] = v1.x; v[5] = v1.y; v[6] = v1.z; v[7] = v1.w;
+        }
+        lds_store8(bsh, n, c >> 2, c & 3, v);
+    }
+    return bad;
+}
+
 // ---------------------------------------------------------------------------
 // Weights of one lane: CH column blocks.
 template <bool Q8, int CH>
@@ -754,23 +881,30 @@ struct WChunk<false, CH> {
     bf16x8 w[CH];
 };
 
-// Blocks kb0 .. kb0+CH-1 of row tile `tile` (clamped to kb_end - 1).
+// Blocks kb0 .. kb0+CH-1 of row tile `tile` of matrix (w, wscale) with kbn
+// column blocks (clamped to kb_end - 1).
 template <bool Q8, int CH>
-__device__ inline void load_weights(WChunk<Q8, CH> &c, const GemmArgs &a, int tile, int kbn,
-                                    int lane, int kb0, int kb_end) {
+__device__ inline void load_weights_of(WChunk<Q8, CH> &c, const void *w, const uint16_t *wscale,
+                                       int tile, int kbn, int lane, int kb0, int kb_end) {
 #pragma unroll
     for (int u = 0; u < CH; u++) {
         const size_t kb = (size_t)min(kb0 + u, kb_end - 1);
         if constexpr (Q8) {
-            c.raw[u] = *(const uint2 *)((const int8_t *)a.w + ((size_t)tile * kbn + kb) * 512 +
+            c.raw[u] = *(const uint2 *)((const int8_t *)w + ((size_t)tile * kbn + kb) * 512 +
                                         lane * 8);
-            c.sc[u] = *(const uint2 *)(a.wscale + ((size_t)tile * kbn + kb) * 16 +
+            c.sc[u] = *(const uint2 *)(wscale + ((size_t)tile * kbn + kb) * 16 +
                                        (lane >> 4) * 4);
         } else {
-            c.w[u] = *(const bf16x8 *)((const uint16_t *)a.w + ((size_t)tile * kbn + kb) * 512 +
+            c.w[u] = *(const bf16x8 *)((const uint16_t *)w + ((size_t)tile * kbn + kb) * 512 +
                                        lane * 8);
         }
     }
+}
+
+template <bool Q8, int CH>
+__device__ inline void load_weights(WChunk<Q8, CH> &c, const GemmArgs &a, int tile, int kbn,
+                                    int lane, int kb0, int kb_end) {
+    load_weights_of(c, a.w, a.wscale, tile, kbn, lane, kb0, kb_end);
 }
 
 // acc += W_block . X_block for block u of a chunk; `used` false makes the
@@ -1004,6 +1138,78 @@ __device__ inline bool epilogue(const GemmArgs &a, const EpiOperands &e, const f
     return bad;
 }
 
+// EPI_GELU_W2's MLP-out weights of one wave (row tiles 4w .. 4w+3, the
+// task's two column blocks); empty for every other epilogue.
+template <bool Q8, bool ON>
+struct W2Weights {
+    WChunk<Q8, 2> w[4];
+    __device__ void load(const GemmArgs &a, int bx, int wave, int lane) {
+#pragma unroll
+        for (int u = 0; u < 4; u++)
+            load_weights_of(w[u], a.w2, a.w2scale, wave * 4 + u, kFfn / 32, lane, 2 * bx,
+                            2 * bx + 2);
+    }
+};
+template <bool Q8>
+struct W2Weights<Q8, false> {
+    __device__ void load(const GemmArgs &, int, int, int) {}
+};
+
+// EPI_GELU_W2 (fused MLP), after gemm_wide_task's half sums: the task's 64
+// GELU rows are hidden columns [64 bx, 64 bx + 64) of the MLP-out
+// projection. Waves (t, half 0) put them into LDS as split fragments (two
+// column blocks, past the half sums), then every wave multiplies its 4 row
+// tiles of the MLP-out matrix by them (mfma_block: per-block Q8 order) and
+// stores its rows of the task's partial write-through (the task drains
+// them before it counts).
+template <bool Q8>
+__device__ inline void gelu_w2_partial(const GemmArgs &a, uint16_t *bsh, const f32x4 &acc,
+                                       const W2Weights<Q8, true> &w2, int t, int half, int s,
+                                       bool live) {
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    uint16_t *hb = bsh + 2 * kLdsBlock;
+    bool bad = false;
+    if (half == 0) {
+        const f32x4 p = ((const f32x4 *)bsh)[t * 64 + lane];
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            float g = gelu_erf(__fadd_rn(acc[r], p[r]));
+            bad |= live && !isfinite(g);
+            if (!live) g = 0.0f;
+            const int c = 16 * t + (lane >> 4) * 4 + r;  // hidden column within the task
+            uint16_t h, m, l;
+            split3(g, h, m, l);
+            uint16_t *rec = hb + (c >> 5) * kLdsBlock + ((c & 31) >> 3) * 128 + (lane & 15) * 8 +
+                            (c & 7);
+            rec[0] = h;
+            rec[512] = m;
+            rec[1024] = l;
+        }
+    }
+    __syncthreads();
+    bf16x8 xh[2], xm[2], xl[2];
+#pragma unroll
+    for (int u = 0; u < 2; u++) {
+        const uint16_t *x = hb + u * kLdsBlock + lane * 8;
+        xh[u] = *(const bf16x8 *)x;
+        xm[u] = *(const bf16x8 *)(x + 512);
+        xl[u] = *(const bf16x8 *)(x + 1024);
+    }
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        f32x4 y = {0.0f, 0.0f, 0.0f, 0.0f};
+        mfma_block(y, w2.w[q], 0, xh[0], xm[0], xl[0], true);
+        mfma_block(y, w2.w[q], 1, xh[1], xm[1], xl[1], true);
+        if (live) {
+            bad |= !isfinite(y[0]) || !isfinite(y[1]) || !isfinite(y[2]) || !isfinite(y[3]);
+            store_wt(a.tmlp_out + (size_t)s * kWidth + (wave * 4 + q) * 16 + (lane >> 4) * 4,
+                     make_float4(y[0], y[1], y[2], y[3]));
+        }
+    }
+    flag_nonfinite(a.status, bad);
+}
+
 // A task's wait for its inputs: NoWait in the single-phase kernels. Every
 // wait ends with a work-group barrier.
 struct NoWait {
@@ -1035,6 +1241,11 @@ __device__ inline void gemm_wide_task(const GemmArgs &a, int bx, int st, uint16_
     if (active) load_weights(w, a, tile, kbn, lane, kb0, kb0 + KBW);
     EpiOperands e;
     if (active && half == 0) load_epilogue_static<EPI>(e, a, s, row0, live);
+    // The fused epilogue's MLP-out weights, requested with the projection's
+    // own (the fused kernel runs one work-group per CU, so registers are
+    // not what limits it).
+    W2Weights<Q8, EPI == EPI_GELU_W2> w2;
+    w2.load(a, bx, wave, lane);
     int position = 0;
     if constexpr (SRC == SRC_ATTN_TAGGED)
         if (lane < 16 && st * 16 + lane < a.streams)
@@ -1049,6 +1260,8 @@ __device__ inline void gemm_wide_task(const GemmArgs &a, int bx, int st, uint16_
         bad_in = prologue_attn_tagged(a, st, position, bsh);
     } else if constexpr (SRC == SRC_SPLIT_LDS) {
         split_to_lds(a.xs, st, bsh);
+    } else if constexpr (SRC == SRC_LN_PARTS) {
+        bad_in = prologue_ln_parts(a, st, bsh);
     } else {
         Rows2 r;
         if (a.tx)
@@ -1088,6 +1301,10 @@ __device__ inline void gemm_wide_task(const GemmArgs &a, int bx, int st, uint16_
     f32x4 *partial = (f32x4 *)bsh;
     if (half == 1) partial[t * 64 + lane] = acc;
     __syncthreads();
+    if constexpr (EPI == EPI_GELU_W2) {
+        gelu_w2_partial<Q8>(a, bsh, acc, w2, t, half, s, live);
+        return;
+    }
     if (half == 0 && active) {
         const f32x4 p = partial[t * 64 + lane];
         f32x4 v;

@@ -25,24 +25,28 @@ typedef struct {
 typedef struct {
     Pending *items;
     size_t count, seq;
+    int fused;  /* fused MLP: MLP_OUT only after the last layer */
 } Queue;
 
 static const uint32_t kChainKinds[4] = {PGPU_FLOW_OUT, PGPU_FLOW_MLP_IN, PGPU_FLOW_MLP_OUT,
                                         PGPU_FLOW_QKV};
 
-static uint32_t phase_tasks(uint32_t kind) {
+/* Tasks of one phase of a (layer, tile); with the fused MLP, MLP_OUT is the
+ * last layer's output tasks. */
+static uint32_t phase_tasks(uint32_t kind, int fused) {
     switch (kind) {
     case PGPU_FLOW_QKV: return PGPU_FLOW_QKV_TASKS;
     case PGPU_FLOW_OUT: return PGPU_FLOW_OUT_TASKS;
     case PGPU_FLOW_MLP_IN: return PGPU_FLOW_MLP_IN_TASKS;
-    default: return PGPU_FLOW_MLP_OUT_TASKS;
+    default: return fused ? PGPU_FLOW_FUSED_OUT_TASKS : PGPU_FLOW_MLP_OUT_TASKS;
     }
 }
 
 /* QKV tasks head by head (q, k, v of head 0, then of head 1, ...): the
  * attention of a head waits only for its own three. */
-static void emit_phase(uint32_t *d, size_t *k, uint32_t kind, uint32_t layer, uint32_t tile) {
-    const uint32_t n = phase_tasks(kind);
+static void emit_phase(uint32_t *d, size_t *k, uint32_t kind, uint32_t layer, uint32_t tile,
+                       int fused) {
+    const uint32_t n = phase_tasks(kind, fused);
     for (uint32_t i = 0; i < n; i++) {
         const uint32_t index = kind == PGPU_FLOW_QKV ? (i % 3) * PH_HEADS + i / 3 : i;
         d[(*k)++] = PGPU_FLOW_TASK(kind, layer, tile, index);
@@ -74,7 +78,7 @@ static void flush_by_phase(Queue *q, uint32_t *d, size_t *k) {
         for (size_t i = 0; i < q->count;) {
             const Pending e = q->items[i];
             if (e.kind == kChainKinds[p]) {
-                emit_phase(d, k, e.kind, e.layer, e.tile);
+                emit_phase(d, k, e.kind, e.layer, e.tile, q->fused);
                 remove_at(q, i);
             } else {
                 i++;
@@ -87,7 +91,7 @@ static void flush(Queue *q, int tile, uint32_t *d, size_t *k) {
     for (size_t i = 0; i < q->count;) {
         const Pending e = q->items[i];
         if (tile < 0 || e.tile == (uint32_t)tile) {
-            emit_phase(d, k, e.kind, e.layer, e.tile);
+            emit_phase(d, k, e.kind, e.layer, e.tile, q->fused);
             remove_at(q, i);
         } else {
             i++;
@@ -105,16 +109,22 @@ pgpu_flow_placement ph_flow_default_placement(int rounds) {
 }
 
 size_t pgpu_flow_schedule(size_t streams, size_t layers, const size_t *units,
-                          const pgpu_flow_placement *place, int prefill, uint32_t *schedule,
+                          const pgpu_flow_placement *place, int flags, uint32_t *schedule,
                           size_t capacity) {
-    if (!streams || !layers || !units)
+    if (!streams || !layers || !units || (flags & ~(PGPU_FLOW_SCHEDULE_PREFILL |
+                                                    PGPU_FLOW_SCHEDULE_FUSED_MLP)))
         return 0;
+    const int prefill = (flags & PGPU_FLOW_SCHEDULE_PREFILL) != 0;
+    const int fused = !prefill && (flags & PGPU_FLOW_SCHEDULE_FUSED_MLP) != 0;
     const size_t tiles = (streams + 15) / 16;
     size_t attn = 0;
     for (size_t s = 0; s < streams; s++)
         attn += units[s];
-    const size_t chain = PGPU_FLOW_OUT_TASKS + PGPU_FLOW_MLP_IN_TASKS + PGPU_FLOW_MLP_OUT_TASKS;
-    const size_t tasks = layers * tiles * (PGPU_FLOW_QKV_TASKS + chain) + layers * PH_HEADS * attn;
+    const size_t chain = PGPU_FLOW_QKV_TASKS + PGPU_FLOW_OUT_TASKS + PGPU_FLOW_MLP_IN_TASKS;
+    const size_t tasks = layers * tiles * chain +
+                         (fused ? tiles * PGPU_FLOW_FUSED_OUT_TASKS
+                                : layers * tiles * PGPU_FLOW_MLP_OUT_TASKS) +
+                         layers * PH_HEADS * attn;
     if (!schedule || capacity < tasks)
         return tasks;
     double after[4] = {0.0, 0.0, 0.0, 0.0}, unit_us = 0.0;
@@ -125,13 +135,13 @@ size_t pgpu_flow_schedule(size_t streams, size_t layers, const size_t *units,
             after[p] = p && a < after[p - 1] ? after[p - 1] : a;  /* phases in order */
         }
     }
-    Queue q = {malloc(4 * tiles * sizeof(Pending)), 0, 0};
+    Queue q = {malloc(4 * tiles * sizeof(Pending)), 0, 0, fused};
     if (!q.items)
         return 0;
     uint32_t *d = schedule;
     size_t k = 0;
     for (size_t t = 0; t < tiles; t++)
-        emit_phase(d, &k, PGPU_FLOW_QKV, 0, (uint32_t)t);
+        emit_phase(d, &k, PGPU_FLOW_QKV, 0, (uint32_t)t, fused);
     double now = 0.0;
     for (size_t l = 0; l < layers; l++) {
         /* With prefill every ATTN task of layer l waits for the QKV of all
@@ -145,7 +155,7 @@ size_t pgpu_flow_schedule(size_t streams, size_t layers, const size_t *units,
                     for (uint32_t h = 0; h < PH_HEADS; h++) {
                         while (q.count && q.items[0].at <= now) {
                             emit_phase(d, &k, q.items[0].kind, q.items[0].layer,
-                                       q.items[0].tile);
+                                       q.items[0].tile, fused);
                             remove_at(&q, 0);
                         }
                         d[k++] = PGPU_FLOW_TASK(PGPU_FLOW_ATTN, l, t, h | j << 3 | n << 11);
@@ -154,6 +164,8 @@ size_t pgpu_flow_schedule(size_t streams, size_t layers, const size_t *units,
             for (int p = 0; p < 4; p++) {
                 if (p == 3 && l + 1 == layers)
                     break;
+                if (p == 2 && fused && l + 1 < layers)
+                    continue; /* the next layer's QKV tasks sum the MLP partials */
                 /* prefill: the layer's chains wait for the next layer's flush */
                 push(&q, prefill ? 1e300 : now + after[p], kChainKinds[p],
                      (uint32_t)(p == 3 ? l + 1 : l), (uint32_t)t);

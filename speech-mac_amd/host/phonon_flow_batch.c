@@ -70,6 +70,8 @@ struct PhononFlowBatch {
         int parity;                 /* the set the next step uses */
         uint64_t *rows, *parts;     /* (dev) tagged mode's hand-off words (pgpu_flow_step) */
         size_t rows_words, parts_words;
+        float *mlp_parts;           /* (dev) fused MLP's partials, made on first use */
+        size_t mlp_words;
         uint32_t tag;               /* tagged mode's tag of the next step, never 0 */
         int tagged_set;             /* -1: by batch size, else the caller's choice */
         uint32_t *schedule, *host_schedule;
@@ -80,7 +82,7 @@ struct PhononFlowBatch {
         int rounds_set;             /* 0: by batch size, else the caller's choice */
         int place_set;              /* the caller set the placement */
         size_t streams, layers;     /* what the schedule was built for (0: none) */
-        int prefill;
+        int prefill, fused;
         unsigned version;           /* bumped by every rebuild */
         pgpu_flow_placement place;  /* chain placement in the task list */
         uint64_t *trace;            /* (dev) optional task timeline, trace_cap tasks */
@@ -414,7 +416,7 @@ void phonon_flow_batch_destroy(PhononFlowBatch *b) {
                     b->rows, b->xh, b->positions, b->tables, b->status,
                     b->scratch.part_acc, b->scratch.part_ml, b->table_src, b->table_map,
                     b->fl.act, b->fl.part_acc, b->fl.part_ml, b->fl.hidden, b->fl.counters,
-                    b->fl.rows, b->fl.parts, b->fl.schedule};
+                    b->fl.rows, b->fl.parts, b->fl.mlp_parts, b->fl.schedule};
     for (size_t i = 0; i < sizeof(bufs) / sizeof(bufs[0]); i++)
         pgpu_free(bufs[i]);
     pgpu_stream_destroy(b->stream);
@@ -793,8 +795,8 @@ static int flow_reserve(PhononFlowBatch *b, size_t streams) {
     if (!pgpu_stream_sync(b->stream))
         return 0;
     drop_graphs(b);
-    void *old[] = {b->fl.act,     b->fl.part_acc, b->fl.part_ml, b->fl.hidden,
-                   b->fl.counters, b->fl.rows,     b->fl.parts};
+    void *old[] = {b->fl.act,      b->fl.part_acc, b->fl.part_ml, b->fl.hidden,
+                   b->fl.counters, b->fl.rows,     b->fl.parts,   b->fl.mlp_parts};
     for (size_t i = 0; i < sizeof(old) / sizeof(old[0]); i++)
         pgpu_free(old[i]);
     b->fl.act = NULL;
@@ -802,6 +804,8 @@ static int flow_reserve(PhononFlowBatch *b, size_t streams) {
     b->fl.hidden = NULL;
     b->fl.counters = NULL;
     b->fl.rows = b->fl.parts = NULL;
+    b->fl.mlp_parts = NULL;
+    b->fl.mlp_words = 0;
     b->fl.cap = b->fl.cap_layers = 0;
     b->fl.streams = 0; /* the schedule is rebuilt against the new buffers */
     const size_t groups = new_layers * new_cap * PH_HEADS;
@@ -831,6 +835,33 @@ static int flow_reserve(PhononFlowBatch *b, size_t streams) {
     return 1;
 }
 
+/* How a one-launch step hands values between its tasks (pgpu_flow.hip).
+ * Tagged words save one memory round trip per hand-off, but every poll
+ * fetches from memory, which costs more than the counter mode's shared
+ * loads once the tile holds more than a few streams (measured on MI355X,
+ * us per 12-layer step, contexts U{1..2048}, counter vs tagged: B = 1: 324
+ * vs 291; B = 16: 482 vs 529). For those few streams, the out projection
+ * merges the split partials itself, which removes the merging attention
+ * task's hop (tagged vs merged in the out projection: B = 1: 319 vs 300;
+ * B = 2: 329 vs 315; B = 3: 327 vs 319; B = 4: 343 vs 342). */
+static int flow_tagged(const PhononFlowBatch *b) {
+    if (b->fl.tagged_set >= 0)
+        return b->fl.tagged_set;
+    return b->streams <= PH_FLOW_TAGGED_MAX_STREAMS ? PGPU_FLOW_HANDOFF_MERGE_OUT
+                                                    : PGPU_FLOW_HANDOFF_COUNTER;
+}
+
+/* The hand-off mode a step runs in: the fused MLP only for a decode step of
+ * at most PGPU_FLOW_FUSED_MAX_STREAMS streams (otherwise the merge in the
+ * out projection, whose hand-offs it extends). */
+static int flow_mode(const PhononFlowBatch *b, int prefill) {
+    const int mode = flow_tagged(b);
+    if (mode == PGPU_FLOW_HANDOFF_FUSED_MLP &&
+        (prefill || b->streams > PGPU_FLOW_FUSED_MAX_STREAMS))
+        return PGPU_FLOW_HANDOFF_MERGE_OUT;
+    return mode;
+}
+
 /* Rebuilds (and uploads) the step's task list (pgpu_flow_schedule) when the
  * streams, the layers or a context outgrow it. A stream lists the splits of
  * its context PH_FLOW_HEADROOM positions ahead; tasks past its live context
@@ -838,8 +869,11 @@ static int flow_reserve(PhononFlowBatch *b, size_t streams) {
 static int flow_schedule(PhononFlowBatch *b, int prefill) {
     const size_t streams = b->streams, layers = b->model->layers;
     const int rounds = flow_rounds(b);
+    const int fused = flow_mode(b, prefill) == PGPU_FLOW_HANDOFF_FUSED_MLP;
+    const int flags = (prefill ? PGPU_FLOW_SCHEDULE_PREFILL : 0) |
+                      (fused ? PGPU_FLOW_SCHEDULE_FUSED_MLP : 0);
     int valid = b->fl.streams == streams && b->fl.layers == layers && b->fl.prefill == prefill &&
-                b->fl.rounds == rounds;
+                b->fl.rounds == rounds && b->fl.fused == fused;
     for (size_t s = 0; valid && s < streams; s++)
         valid = (b->host_positions[s] + PH_SPLIT_KEYS) / PH_SPLIT_KEYS <= b->fl.cover[s];
     if (valid)
@@ -853,7 +887,7 @@ static int flow_schedule(PhononFlowBatch *b, int prefill) {
     const pgpu_flow_placement place =
         b->fl.place_set ? b->fl.place : ph_flow_default_placement(rounds);
     const size_t tasks =
-        pgpu_flow_schedule(streams, layers, b->fl.units, &place, prefill, NULL, 0);
+        pgpu_flow_schedule(streams, layers, b->fl.units, &place, flags, NULL, 0);
     if (tasks > b->fl.host_cap) {
         uint32_t *grown = realloc(b->fl.host_schedule, tasks * sizeof(uint32_t));
         if (!grown)
@@ -862,7 +896,7 @@ static int flow_schedule(PhononFlowBatch *b, int prefill) {
         b->fl.host_cap = tasks;
     }
     uint32_t *d = b->fl.host_schedule;
-    const size_t k = pgpu_flow_schedule(streams, layers, b->fl.units, &place, prefill, d,
+    const size_t k = pgpu_flow_schedule(streams, layers, b->fl.units, &place, flags, d,
                                         b->fl.host_cap);
     if (k != tasks)
         return ph_fail("flow schedule: task count mismatch");
@@ -883,6 +917,7 @@ static int flow_schedule(PhononFlowBatch *b, int prefill) {
     b->fl.streams = streams;
     b->fl.layers = layers;
     b->fl.prefill = prefill;
+    b->fl.fused = fused;
     b->fl.version++;
     return 1;
 }
@@ -894,26 +929,19 @@ static int flow_schedule(PhononFlowBatch *b, int prefill) {
 static int flow_prepare(PhononFlowBatch *b, int prefill) {
     if (!flow_reserve(b, b->streams) || !flow_schedule(b, prefill))
         return 0;
+    if (b->fl.fused && !b->fl.mlp_parts) {
+        /* [layers][MLP_IN tasks][16][512] fp32, read only after their count */
+        const size_t words = b->fl.cap_layers * PGPU_FLOW_MLP_IN_TASKS * 16 * PH_WIDTH;
+        b->fl.mlp_parts = pgpu_malloc(words * sizeof(float));
+        if (!b->fl.mlp_parts)
+            return 0;
+        b->fl.mlp_words = words;
+    }
     if (b->fl.tag >= UINT32_MAX - 1 && !(pgpu_stream_sync(b->stream) && flow_clear_tags(b)))
         return 0;
     return 1;
 }
 
-/* How a one-launch step hands values between its tasks (pgpu_flow.hip).
- * Tagged words save one memory round trip per hand-off, but every poll
- * fetches from memory, which costs more than the counter mode's shared
- * loads once the tile holds more than a few streams (measured on MI355X,
- * us per 12-layer step, contexts U{1..2048}, counter vs tagged: B = 1: 324
- * vs 291; B = 16: 482 vs 529). For those few streams, the out projection
- * merges the split partials itself, which removes the merging attention
- * task's hop (tagged vs merged in the out projection: B = 1: 319 vs 300;
- * B = 2: 329 vs 315; B = 3: 327 vs 319; B = 4: 343 vs 342). */
-static int flow_tagged(const PhononFlowBatch *b) {
-    if (b->fl.tagged_set >= 0)
-        return b->fl.tagged_set;
-    return b->streams <= PH_FLOW_TAGGED_MAX_STREAMS ? PGPU_FLOW_HANDOFF_MERGE_OUT
-                                                    : PGPU_FLOW_HANDOFF_COUNTER;
-}
 
 /* One step as a single launch. It uses one set of counters and zeroes the
  * other for the next step, and reads the positions as stored plus pos_lag
@@ -962,10 +990,11 @@ static int enqueue_flow(PhononFlowBatch *b, const float *input, float *output, f
                               .trace = b->fl.trace_cap >= b->fl.tasks ? b->fl.trace : NULL,
                               .attn_rounds = b->fl.rounds,
                               .wait_us = b->fl.wait_us,
-                              .tagged = flow_tagged(b),
+                              .tagged = flow_mode(b, b->fl.prefill),
                               .rows = b->fl.rows,
                               .parts = b->fl.parts,
-                              .tag = b->fl.tag};
+                              .tag = b->fl.tag,
+                              .mlp_parts = b->fl.mlp_parts};
     if (!((!b->time_before || pgpu_event_record(b->time_before, b->stream)) &&
           pgpu_flow_launch(b->stream, &f, &b->pool->kv) &&
           (!b->time_after || pgpu_event_record(b->time_after, b->stream))))
@@ -1344,7 +1373,7 @@ int phonon_flow_batch_set_pipeline(PhononFlowBatch *b, int mode) {
 }
 
 int phonon_flow_batch_set_handoff(PhononFlowBatch *b, int tagged) {
-    if (!b || tagged < -1 || tagged > PGPU_FLOW_HANDOFF_MERGE_OUT)
+    if (!b || tagged < -1 || tagged > PGPU_FLOW_HANDOFF_FUSED_MLP)
         return 0;
     b->fl.tagged_set = tagged;
     return 1;

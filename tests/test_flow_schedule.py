@@ -12,6 +12,8 @@ import pytest
 
 QKV, ATTN, OUT, MLP_IN, MLP_OUT = range(5)
 TASKS = {QKV: 24, OUT: 8, MLP_IN: 32, MLP_OUT: 32}
+FUSED_OUT_TASKS = 8          # PGPU_FLOW_FUSED_OUT_TASKS
+PREFILL, FUSED = 1, 2        # pgpu_flow_schedule flags
 
 
 PLACEMENTS = [None, (0.024, (4.0, 10.0, 16.0, 22.0)), (0.001, (0.0, 0.0, 0.0, 0.0)),
@@ -39,9 +41,12 @@ def decode(d):
     return d & 7, (d >> 3) & 63, (d >> 9) & 255, d >> 17
 
 
-def check_order(sched, splits, layers, prefill=False):
+def check_order(sched, splits, layers, prefill=False, fused=False):
     """Replays the step: each task must find its waits satisfied by the tasks
-    listed before it. Raises AssertionError at the first violation."""
+    listed before it. Raises AssertionError at the first violation. fused:
+    the fused MLP's list (no MLP_OUT phase; a layer's QKV tasks sum the
+    previous layer's MLP_IN partials and read its r; the last layer's 8
+    MLP_OUT tasks write the output from them)."""
     streams = len(splits)
     tiles = (streams + 15) // 16
     kind, layer, tile, index = decode(sched)
@@ -58,7 +63,10 @@ def check_order(sched, splits, layers, prefill=False):
         live = min(16, streams - 16 * t)
         if k == QKV:
             assert x < TASKS[QKV]
-            if l > 0:
+            if l > 0 and fused:
+                assert done[l - 1, t, MLP_IN] == TASKS[MLP_IN], f"QKV({l},{t}) before MLP_IN"
+                assert done[l - 1, t, OUT] == TASKS[OUT], f"QKV({l},{t}) before OUT"
+            elif l > 0:
                 assert done[l - 1, t, MLP_OUT] == TASKS[MLP_OUT], f"QKV({l},{t}) before MLP_OUT"
             qkv_head[l, t, x % 8] += 1   # rows [64x, 64x + 64): q, k or v of head x % 8
         elif k == ATTN:
@@ -82,7 +90,8 @@ def check_order(sched, splits, layers, prefill=False):
             assert x < TASKS[MLP_IN]
             assert done[l, t, OUT] == TASKS[OUT], f"MLP_IN({l},{t}) before OUT"
         elif k == MLP_OUT:
-            assert x < TASKS[MLP_OUT]
+            assert x < (FUSED_OUT_TASKS if fused else TASKS[MLP_OUT])
+            assert not fused or l == layers - 1, f"fused MLP_OUT({l},{t}) before the last layer"
             assert done[l, t, MLP_IN] == TASKS[MLP_IN], f"MLP_OUT({l},{t}) before MLP_IN"
         else:
             raise AssertionError(f"bad kind {k}")
@@ -93,6 +102,8 @@ def check_order(sched, splits, layers, prefill=False):
         for t in range(tiles):
             live = min(16, streams - 16 * t)
             for k, n in TASKS.items():
+                if fused and k == MLP_OUT:
+                    n = FUSED_OUT_TASKS if l == layers - 1 else 0
                 assert done[l, t, k] == n, (l, t, k)
             assert done[l, t, ATTN] == 8 * live
     return True
@@ -181,3 +192,56 @@ def test_order_checker_allows_attention_after_its_own_head(pkg):
     # move it right behind head 0's three QKV tasks, ahead of heads 1..7
     moved = np.insert(np.delete(sched, a), int(qkv[2]) + 1, sched[a])
     assert check_order(moved, splits, 1)
+
+
+@pytest.mark.parametrize("streams,layers", [(1, 1), (1, 12), (3, 5), (4, 12)])
+@pytest.mark.parametrize("place", range(len(PLACEMENTS)))
+def test_fused_mlp_schedule_lists_every_task_after_its_inputs(pkg, streams, layers, place):
+    """The fused MLP's list (PGPU_FLOW_SCHEDULE_FUSED_MLP): no MLP_OUT phase
+    but the last layer's output tasks, every task after its inputs; with the
+    prefill flag as well the fused flag is ignored."""
+    lib = pkg.load()
+    rng = np.random.default_rng(streams * 10 + layers)
+    splits = rng.integers(1, 33, size=streams)
+    count = layers * (24 + 8 + 32) + FUSED_OUT_TASKS + layers * 8 * int(splits.sum())
+    sched = build(lib, splits, layers, PLACEMENTS[place], prefill=FUSED)
+    assert len(sched) == count
+    assert check_order(sched, splits, layers, fused=True)
+    # the fused list fails the unfused replay (its QKV tasks follow no MLP_OUT)
+    if layers > 1:
+        with pytest.raises(AssertionError):
+            check_order(sched, splits, layers)
+    pre = build(lib, splits, layers, PLACEMENTS[place], prefill=PREFILL | FUSED)
+    assert np.array_equal(pre, build(lib, splits, layers, PLACEMENTS[place], prefill=PREFILL))
+    assert check_order(pre, splits, layers, prefill=True)
+
+
+def test_fused_order_checker_rejects_planted_mistakes(pkg):
+    """A QKV task of layer 1 moved in front of the last MLP_IN task of layer
+    0, or an output task in front of the last layer's last MLP_IN task,
+    fails the fused replay."""
+    lib = pkg.load()
+    splits = np.array([3, 1, 2])
+    sched = build(lib, splits, 2, prefill=FUSED)
+    kind, layer, _, _ = decode(sched)
+    cases = []
+    q = int(np.flatnonzero((kind == QKV) & (layer == 1))[0])
+    m = int(np.flatnonzero((kind == MLP_IN) & (layer == 0))[-1])
+    bad = sched.copy()
+    bad[m], bad[q] = sched[q], sched[m]
+    cases.append(bad)
+    o = int(np.flatnonzero(kind == MLP_OUT)[0])
+    m = int(np.flatnonzero((kind == MLP_IN) & (layer == 1))[-1])
+    bad = sched.copy()
+    bad[m], bad[o] = sched[o], sched[m]
+    cases.append(bad)
+    for bad in cases:
+        with pytest.raises(AssertionError):
+            check_order(bad, splits, 2, fused=True)
+
+
+def test_schedule_rejects_unknown_flags(pkg):
+    lib = pkg.load()
+    splits = np.ascontiguousarray([1], dtype=np.uintp)
+    szp = splits.ctypes.data_as(ctypes.POINTER(ctypes.c_size_t))
+    assert lib.pgpu_flow_schedule(1, 1, szp, None, 4, None, 0) == 0

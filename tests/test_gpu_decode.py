@@ -917,6 +917,79 @@ def test_one_launch_step_equals_phase_launches(lib, syn, pkg, streams):
             assert np.array_equal(a, b)
 
 
+@pytest.mark.parametrize("streams", [1, 2, 4])
+def test_fused_mlp_step_vs_oracle(lib, oracle, oracle_mod, syn, pkg, streams):
+    """The fused-MLP hand-off (mode 4: no MLP-out phase; each MLP-in task's
+    partial of the MLP-out projection summed by the next layer's QKV tasks)
+    through 12 layers over four steps with ragged contexts, as one launch
+    and in graph replay: every stream within 1e-4 of the oracle's stack step,
+    the appended K/V rows too, and within 1e-5 of the merge-in-out mode it
+    extends (its sums are ordered differently, so the bits differ)."""
+    layers, steps = 12, 4
+    model = scaled_model(syn, 241, layers)
+    om = oracle_for(oracle, oracle_mod, model)
+    views = pkg.Views()
+    w = views.layers(model)
+    lengths = np.array([0, 1000, 255, 16])[:streams]
+    max_pos = 1040
+    table_len = (max_pos + 15) // 16
+    blocks = streams * table_len
+    rng = np.random.default_rng(242)
+    okeys = np.zeros((streams, layers, max_pos, 512), np.float32)
+    ovals = np.zeros_like(okeys)
+    for s, n in enumerate(lengths):
+        okeys[s, :, :n] = rng.standard_normal((layers, n, 512)).astype(np.float32)
+        ovals[s, :, :n] = rng.standard_normal((layers, n, 512)).astype(np.float32)
+    xs = rng.standard_normal((steps, streams, 512)).astype(np.float32)
+    outs = {}
+    for handoff, graph in ((4, 0), (4, 1), (3, 0)):
+        print(f"fused MLP: streams={streams} handoff={handoff} graph={graph}", flush=True)
+        bt = Batch(lib, w, layers, streams, max_pos, blocks)
+        set_step_mode(lib, bt.batch, 2)
+        assert lib.phonon_flow_batch_set_handoff(bt.batch, handoff)
+        assert lib.phonon_flow_batch_set_graph(bt.batch, graph)
+        ids = np.zeros(blocks, np.int32)
+        assert lib.phonon_kv_pool_alloc(bt.pool, blocks, i32p(ids))
+        tables = np.ascontiguousarray(
+            np.random.default_rng(243).permutation(ids).reshape(streams, table_len))
+        for s in range(streams):
+            if lengths[s]:
+                assert lib.phonon_kv_pool_write(bt.pool, i32p(tables[s]), table_len, 0,
+                                                int(lengths[s]), fp(okeys[s]), fp(ovals[s]),
+                                                max_pos)
+        pos = lengths.astype(np.uintp)
+        assert lib.phonon_flow_batch_set_streams(
+            bt.batch, streams, pos.ctypes.data_as(ctypes.POINTER(ctypes.c_size_t)),
+            i32p(tables), table_len)
+        ys = []
+        for step in range(steps):
+            y = np.zeros((streams, 512), np.float32)
+            assert lib.phonon_flow_batch_step(bt.batch, fp(np.ascontiguousarray(xs[step])),
+                                              10000.0, fp(y)), pkg.last_error(lib)
+            ys.append(y)
+        k = np.zeros((streams, layers, max_pos, 512), np.float32)
+        v = np.zeros_like(k)
+        for s in range(streams):
+            assert lib.phonon_kv_pool_read(bt.pool, i32p(tables[s]), table_len,
+                                           int(lengths[s]), steps, fp(k[s]), fp(v[s]), max_pos)
+        outs[(handoff, graph)] = (np.array(ys), k, v)
+        bt.close()
+    ys, k, v = outs[(4, 0)]
+    assert np.array_equal(ys.view(np.uint32), outs[(4, 1)][0].view(np.uint32))
+    for step in range(steps):
+        for s in range(streams):
+            ok, ref = om.stack_step(okeys[s], ovals[s], max_pos, int(lengths[s]) + step,
+                                    xs[step, s])
+            assert ok
+            err = helpers.normwise(ys[step, s], ref)
+            assert err <= TOL, (step, s, err)
+            assert helpers.normwise(ys[step, s], outs[(3, 0)][0][step, s]) <= 1e-5
+    for s in range(streams):
+        n0 = int(lengths[s])
+        assert helpers.normwise(k[s, :, n0:n0 + steps], okeys[s, :, n0:n0 + steps]) <= TOL
+        assert helpers.normwise(v[s, :, n0:n0 + steps], ovals[s, :, n0:n0 + steps]) <= TOL
+
+
 def test_unwritten_pool_slots_never_reach_the_output(lib, oracle, oracle_mod, syn, pkg):
     """Regression: slots past a stream's context inside its last block may
     hold anything (here NaN); attention must skip them, not weight them 0."""
@@ -984,15 +1057,15 @@ def test_batch_reports_nonfinite_and_uncovered_positions(lib, syn, pkg):
 
 
 # ---------------------------------------------------------------- robustness
-@pytest.mark.parametrize("handoff", [0, 1, 2, 3])
-def test_forced_wait_timeout_reports_and_recovers(lib, syn, pkg, handoff):
+@pytest.mark.parametrize("handoff,streams", [(0, 64), (1, 64), (2, 64), (3, 64), (4, 3)])
+def test_forced_wait_timeout_reports_and_recovers(lib, syn, pkg, handoff, streams):
     """The one-launch step's give-up path, forced from the host: with a 1 us
     wait limit its tasks stop waiting (counter waits, and with tagged
     hand-offs their polls), the launch still ends, status bit 2 (value 4) is
     set and the step reports failure; with the default limit restored and
     the positions reset, the same batch gives the bits of a batch that never
     timed out."""
-    layers, streams = 3, 64
+    layers = 3
     model = scaled_model(syn, 231, layers)
     views = pkg.Views()
     w = views.layers(model)
