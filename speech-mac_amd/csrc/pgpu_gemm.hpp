@@ -901,6 +901,20 @@ __device__ inline void load_weights_of(WChunk<Q8, CH> &c, const void *w, const u
     }
 }
 
+// Makes the chunk's loads complete here: a task that is about to wait for
+// its inputs then has its weights in registers for certain (the compiler
+// may otherwise sink the loads past the wait, out of register pressure).
+template <bool Q8, int CH>
+__device__ inline void hold_weights(const WChunk<Q8, CH> &c) {
+#pragma unroll
+    for (int u = 0; u < CH; u++) {
+        if constexpr (Q8)
+            __asm__ volatile("" ::"v"(c.raw[u].x), "v"(c.raw[u].y), "v"(c.sc[u].x), "v"(c.sc[u].y));
+        else
+            __asm__ volatile("" ::"v"(c.w[u]));
+    }
+}
+
 template <bool Q8, int CH>
 __device__ inline void load_weights(WChunk<Q8, CH> &c, const GemmArgs &a, int tile, int kbn,
                                     int lane, int kb0, int kb_end) {
@@ -1149,10 +1163,15 @@ struct W2Weights {
             load_weights_of(w[u], a.w2, a.w2scale, wave * 4 + u, kFfn / 32, lane, 2 * bx,
                             2 * bx + 2);
     }
+    __device__ void hold() const {
+#pragma unroll
+        for (int u = 0; u < 4; u++) hold_weights(w[u]);
+    }
 };
 template <bool Q8>
 struct W2Weights<Q8, false> {
     __device__ void load(const GemmArgs &, int, int, int) {}
+    __device__ void hold() const {}
 };
 
 // EPI_GELU_W2 (fused MLP), after gemm_wide_task's half sums: the task's 64
@@ -1246,6 +1265,9 @@ __device__ inline void gemm_wide_task(const GemmArgs &a, int bx, int st, uint16_
     // not what limits it).
     W2Weights<Q8, EPI == EPI_GELU_W2> w2;
     w2.load(a, bx, wave, lane);
+    if constexpr (SRC == SRC_LN_PARTS || EPI == EPI_GELU_W2)
+        if (active) hold_weights(w);
+    w2.hold();
     int position = 0;
     if constexpr (SRC == SRC_ATTN_TAGGED)
         if (lane < 16 && st * 16 + lane < a.streams)

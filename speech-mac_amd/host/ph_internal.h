@@ -39,6 +39,9 @@ enum {
 /* One-launch steps of at most this many streams hand values over as tagged
  * words (phonon_flow_batch_set_handoff). */
 enum { PH_FLOW_TAGGED_MAX_STREAMS = 4 };
+/* ... and of at most this many streams skip the MLP-out phase (the fused
+ * MLP, PGPU_FLOW_HANDOFF_FUSED_MLP). */
+enum { PH_FLOW_FUSED_DEFAULT_MAX_STREAMS = 2 };
 /* Chain placement of the one-launch step's task list (pgpu_flow_placement):
  * measured on MI355X at B = 64 (ph_flow_schedule.c). */
 pgpu_flow_placement ph_flow_default_placement(int rounds);

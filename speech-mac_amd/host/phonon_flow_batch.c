@@ -843,10 +843,16 @@ static int flow_reserve(PhononFlowBatch *b, size_t streams) {
  * vs 291; B = 16: 482 vs 529). For those few streams, the out projection
  * merges the split partials itself, which removes the merging attention
  * task's hop (tagged vs merged in the out projection: B = 1: 319 vs 300;
- * B = 2: 329 vs 315; B = 3: 327 vs 319; B = 4: 343 vs 342). */
+ * B = 2: 329 vs 315; B = 3: 327 vs 319; B = 4: 343 vs 342). Up to two
+ * streams, the fused MLP also removes the MLP-out hop; with more, its
+ * QKV tasks' per-stream partial sums cost more than the hop (merge in the
+ * out projection vs fused MLP, contexts U{1..2048}: B = 1: 276 vs 256;
+ * B = 2: 300 vs 285; B = 3: 307 vs 314; B = 4: 330 vs 354). */
 static int flow_tagged(const PhononFlowBatch *b) {
     if (b->fl.tagged_set >= 0)
         return b->fl.tagged_set;
+    if (b->streams <= PH_FLOW_FUSED_DEFAULT_MAX_STREAMS)
+        return PGPU_FLOW_HANDOFF_FUSED_MLP;
     return b->streams <= PH_FLOW_TAGGED_MAX_STREAMS ? PGPU_FLOW_HANDOFF_MERGE_OUT
                                                     : PGPU_FLOW_HANDOFF_COUNTER;
 }

@@ -227,8 +227,11 @@ def test_config5_prefill_leg_vs_oracle(lib, pkg, oracle, oracle_mod, syn):
         assert helpers.normwise(kv_got[s][0], okeys[s]) <= TOL
         assert helpers.normwise(kv_got[s][1], ovals[s]) <= TOL
 
-    # Single decode steps of the same two streams: the exact prefill's bits.
+    # Single decode steps of the same two streams: the exact prefill's bits
+    # (with the merge in the out projection: the one-stream default, the
+    # fused MLP, orders the MLP-out sums differently).
     bt = Batch(lib, w, C5_LAYERS, 1, max_pos, blocks)
+    assert lib.phonon_flow_batch_set_handoff(bt.batch, 3)
     ids = np.zeros(blocks, np.int32)
     assert lib.phonon_kv_pool_alloc(bt.pool, blocks, i32p(ids))
     for s in checked:
