@@ -377,12 +377,12 @@ def pmc_program(pkg, lib, args):
 
 
 def prefill_mfma_work(layers, new_streams, chunk, terms=3):
-    """(bf16 MFMA flops, fp32 MFMA flops) of a batched prefill of new_streams
-    fresh prompts of `chunk` positions: the projections as issued (one bf16
-    MFMA product per multiply-add and split term: 3 in the exact mode, 2 in
-    the fast one) and the causal attention's Q.K and P.V (2 flops per
-    multiply-add, every (query, key) pair with key <= query, 8 heads x 64
-    dimensions)."""
+    """(16-bit MFMA flops, fp32 MFMA flops) of a batched prefill of
+    new_streams fresh prompts of `chunk` positions: the projections as issued
+    (one MFMA product per multiply-add and split term: 3 bf16 terms in the
+    exact mode, 2 fp16 terms in the fast ones) and the causal attention's Q.K
+    and P.V (2 flops per multiply-add, every (query, key) pair with key <=
+    query, 8 heads x 64 dimensions)."""
     rows = new_streams * chunk
     proj = rows * layers * (1536 + 512 + 2048 + 2048) * 512 * 2 * terms
     pairs = new_streams * chunk * (chunk + 1) // 2
@@ -391,13 +391,14 @@ def prefill_mfma_work(layers, new_streams, chunk, terms=3):
 
 
 def prefill_mfma_fraction(layers, new_streams, chunk, ms, terms):
-    """The prefill's matrix-core work against the time it took: bf16 flops
-    at 2.5 PFLOP/s plus fp32 flops at 157.3 TFLOP/s (dense peaks), as a
-    fraction of the measured time."""
+    """The prefill's matrix-core work against the time it took: bf16 / fp16
+    flops at 2.5 PFLOP/s plus fp32 flops at 157.3 TFLOP/s (dense peaks), as
+    a fraction of the measured time."""
     proj, attn = prefill_mfma_work(layers, new_streams, chunk, terms)
     secs = ms * 1e-3
-    return {"bf16_tflop": round(proj / 1e12, 2), "fp32_gflop": round(attn / 1e9, 2),
-            "bf16_TFLOPs": round(proj / secs / 1e12, 1),
+    return {"projection_operands": "three bf16 terms" if terms == 3 else "two fp16 terms",
+            "proj_tflop": round(proj / 1e12, 2), "fp32_gflop": round(attn / 1e9, 2),
+            "proj_TFLOPs": round(proj / secs / 1e12, 1),
             "frac": round((proj / 2.5e15 + attn / 157.3e12) / secs, 4)}
 
 
@@ -490,8 +491,11 @@ def large_batch_with_prefill(pkg, lib, seed, layers=12, streams=256, new_streams
             "prefill_tokens_per_s": round(new_streams * chunk / (pre_ms / iterations * 1e-3), 1),
             "prefill_attention": ["matrix cores", "exact (decode arithmetic)",
                                   "lane per query"][prefill_attention],
+            # the exact attention keeps three bf16 split terms; the fast
+            # modes take two fp16 terms (Q8 weights)
             "prefill_mfma": prefill_mfma_fraction(layers, new_streams, chunk,
-                                                  pre_ms / iterations, 3),
+                                                  pre_ms / iterations,
+                                                  3 if prefill_attention == 1 else 2),
             "frames_per_s_incl_prefill": round(streams / (per_it_ms * 1e-3), 1),
             "clean": clean}
 

@@ -393,7 +393,8 @@ int pgpu_elu(void *stream, const float *x, float *y, size_t count);
  * rounded up to 16 rows in the allocation. -- */
 /* LayerNorm of rows [M][512] (weight, bias, epsilon), into split fragments:
  * the decode step's LayerNorm prologue, the same bits. Only the first
- * `terms` (1..3) split terms of each value are written. */
+ * `terms` (1..3) split terms of each value are written, or the two fp16
+ * terms of PGPU_SPLIT_F16_PAIR. */
 int pgpu_rows_split_ln(void *stream, const float *rows, const float *weight, const float *bias,
                        float epsilon, int streams, int terms, uint16_t *out_split, int *status);
 /* The split partials of pgpu_attention / pgpu_prefill_attention merged into
@@ -404,22 +405,35 @@ int pgpu_rows_split_attention(void *stream, const pgpu_attention_scratch *scratc
                               uint16_t *out_split, int *status);
 /* A projection's weights for the prefill projections: bf16 MFMA fragments
  * in the order of pgpu_matrix values, and for Q8 weights the fp32 block
- * scales [rows/16][columns/32][16] (scales NULL: BF16 weights, no scale). */
+ * scales [rows/16][columns/32][16] (scales NULL: BF16 weights, no scale)
+ * and the same values as fp16 fragments (values_f16, for split terms
+ * PGPU_SPLIT_F16_PAIR; NULL: not available). */
 typedef struct {
     size_t rows, columns;
     const uint16_t *values;
     const float *scales;
+    const uint16_t *values_f16;
 } pgpu_wide_matrix;
 /* Q8 matrix -> bf16 fragments [rows*columns] and fp32 scales
- * [rows*columns/32] (device buffers): exact conversions. */
-int pgpu_wide_from_matrix(void *stream, const pgpu_matrix *w, uint16_t *values, float *scales);
+ * [rows*columns/32] (device buffers): exact conversions. values_f16
+ * (optional, NULL: skipped): the int8 values as fp16 fragments (exact). */
+int pgpu_wide_from_matrix(void *stream, const pgpu_matrix *w, uint16_t *values, float *scales,
+                          uint16_t *values_f16);
+/* `terms` value of the split-fragment entry points below: two fp16 terms
+ * per activation (hi = fp16(x), lo = fp16(x - hi): 22 significant bits
+ * while |x| < 65504; beyond, the outputs are non-finite and flagged) in the
+ * records of the first two terms, multiplied on the fp16 matrix cores with
+ * the values_f16 weights (two thirds of the three-term work). */
+#define PGPU_SPLIT_F16_PAIR 4
 /* Projections of M rows of split fragments (K = 512 or 2048; rows a
  * multiple of 128), with the epilogues of pgpu_gemm_qkv, pgpu_gemm_residual
  * and pgpu_gemm_gelu_split. terms = 3: each output has the bits of the
  * single-phase projection of the same weights (the same per-block MFMA
  * sequence, scale order and summation chains); terms = 2: the activations'
  * third split term is left out (each activation taken to 16 significant
- * bits, relative error below 2^-16; two thirds of the matrix-core work). */
+ * bits, relative error below 2^-16; two thirds of the matrix-core work);
+ * terms = PGPU_SPLIT_F16_PAIR: two fp16 terms with the fp16 weights (22
+ * significant bits, two thirds of the work; w->values_f16 required). */
 int pgpu_prefill_gemm_qkv(void *stream, const pgpu_wide_matrix *w, const uint16_t *split,
                           int streams, int terms, const pgpu_paged_kv *kv, int layer,
                           const int32_t *tables, int table_stride, const int32_t *positions,
@@ -431,8 +445,8 @@ int pgpu_prefill_gemm_gelu_split(void *stream, const pgpu_wide_matrix *w, const 
                                  int streams, int terms, uint16_t *out_split, int *status);
 /* (The GELU outputs are written as `terms` split terms: the MLP-out
  * projection reads as many. Likewise `terms` of the attention entry points
- * below, 2 or 3: the split terms of the attention rows written for the out
- * projection.) */
+ * below, 2, 3 or PGPU_SPLIT_F16_PAIR: the split terms of the attention rows
+ * written for the out projection.) */
 /* Causal attention of a batched prefill, one lane per query, into split
  * fragments of the attention rows (fp32 arithmetic in its own summation
  * order). `runs` (dev) holds run_count pairs (s0, n): pseudo-streams

@@ -254,7 +254,7 @@ EXPORTS = {
     "pgpu_attention_merge": (_i, [_vp, _scp, _vp, _i, _i, _i, _vp, _vp, _vp]),
     "pgpu_rows_split_ln": (_i, [_vp, _vp, _vp, _vp, ctypes.c_float, _i, _i, _vp, _vp]),
     "pgpu_rows_split_attention": (_i, [_vp, _scp, _vp, _i, _i, _vp, _vp]),
-    "pgpu_wide_from_matrix": (_i, [_vp, _mp, _vp, _vp]),
+    "pgpu_wide_from_matrix": (_i, [_vp, _mp, _vp, _vp, _vp]),
     "pgpu_prefill_gemm_qkv": (_i, [_vp, _vp, _vp, _i, _i, _kvp, _i, _vp, _i, _vp, _vp, _vp,
                                     _vp]),
     "pgpu_prefill_gemm_residual": (_i, [_vp, _vp, _vp, _i, _i, _vp, _vp, _vp]),

@@ -13,6 +13,8 @@
 #include <stdint.h>
 #include <stdio.h>
 
+#include "phonon_gpu.h"
+
 extern "C" void pgpu_record_error(const char *what);
 
 namespace pgpu {
@@ -44,7 +46,14 @@ constexpr int kSplitKeys = 256;  // keys per attention work-group (16 blocks)
 constexpr int kMaxPositions = 8192;
 
 typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
+typedef __attribute__((ext_vector_type(8))) _Float16 f16x8;
 typedef __attribute__((ext_vector_type(4))) float f32x4;
+
+// Split formats (the `terms` of a split-fragment buffer): 3 bf16 terms
+// (exact), the first 2 of them, or kF16Pair: two fp16 terms in the first two
+// records (split2h).
+constexpr int kF16Pair = PGPU_SPLIT_F16_PAIR;
+__host__ __device__ constexpr int split_records(int terms) { return terms == kF16Pair ? 2 : terms; }
 
 // Index (in bf16 elements) of activation x[s][k], part p (0 hi, 1 mid, 2 lo),
 // inside a split-fragment buffer whose rows have kb_count 32-wide blocks.
@@ -67,6 +76,18 @@ __device__ inline void split3(float x, uint16_t &hi, uint16_t &mid, uint16_t &lo
     hi = (uint16_t)(h >> 16);
     mid = (uint16_t)(m >> 16);
     lo = (uint16_t)(fbits(r2) >> 16);
+}
+
+// Two-term fp16 split: hi = fp16(x) (round to nearest), lo = fp16(x - hi);
+// x - hi is exact in fp32, so hi + lo carries 22 significant bits of x
+// while |x| stays inside the fp16 range (beyond 65504, hi is infinite and
+// the products become non-finite, which the consumers flag); below 2^-14
+// the terms lose bits to fp16 subnormals (absolute error under 2^-25).
+__device__ inline void split2h(float x, uint16_t &hi, uint16_t &lo) {
+    const _Float16 h = (_Float16)x;
+    const _Float16 l = (_Float16)__fsub_rn(x, (float)h);
+    hi = __builtin_bit_cast(uint16_t, h);
+    lo = __builtin_bit_cast(uint16_t, l);
 }
 
 // Writes n (n = 4 or 8) consecutive activations of one stream starting at a
@@ -171,6 +192,23 @@ __device__ inline float erf_as7126(float x) {
 // 0.5*x*(1+erf(x/sqrt2)), unfused as in src/phonon_transformer.c:208-211.
 __device__ inline float gelu_erf(float x) {
     const float e = erf_as7126(__fmul_rn(x, 0.7071067811865475244f));
+    return __fmul_rn(__fmul_rn(0.5f, x), __fadd_rn(1.0f, e));
+}
+
+// gelu_erf with the hardware reciprocal (v_rcp_f32, 1 ulp) and exp2
+// (v_exp_f32) in place of the correctly rounded division and libm exp: a
+// few ulp from gelu_erf, against the 1.5e-7 error of A&S 7.1.26 itself.
+// For the fast prefill, whose activations carry 22 bits.
+__device__ inline float gelu_erf_fast(float x) {
+    const float z = __fmul_rn(x, 0.7071067811865475244f);
+    const float t = __builtin_amdgcn_rcpf(fmaf(0.3275911f, fabsf(z), 1.0f));
+    float r = fmaf(1.061405429f, t, -1.453152027f);
+    r = fmaf(r, t, 1.421413741f);
+    r = fmaf(r, t, -0.284496736f);
+    r = fmaf(r, t, 0.254829592f);
+    // e^(-z^2) = 2^(-z^2 log2 e); below 2^-126 it flushes to 0 (erf is 1 there)
+    const float neg_exp = -__builtin_amdgcn_exp2f(__fmul_rn(__fmul_rn(z, z), -1.4426950408889634f));
+    const float e = copysignf(fmaf(__fmul_rn(t, neg_exp), r, 1.0f), z);
     return __fmul_rn(__fmul_rn(0.5f, x), __fadd_rn(1.0f, e));
 }
 

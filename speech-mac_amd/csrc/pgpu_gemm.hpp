@@ -271,17 +271,23 @@ __device__ inline void store_out(float *p, float4 v, bool wt) {
 // split fragments: three 8-byte stores.
 // Only the first `terms` split terms are written (a consumer that reads two
 // terms never reads the third).
+// terms = kF16Pair: the two fp16 terms of split2h in the first two records.
 __device__ inline void store_split4(uint16_t *__restrict__ xs, int s, int k, int kb_count,
                                     const float *v, bool wt, int terms = 3) {
     uint16_t h[4], m[4], l[4];
+    if (terms == kF16Pair) {
 #pragma unroll
-    for (int i = 0; i < 4; i++) split3(v[i], h[i], m[i], l[i]);
+        for (int i = 0; i < 4; i++) split2h(v[i], h[i], m[i]);
+    } else {
+#pragma unroll
+        for (int i = 0; i < 4; i++) split3(v[i], h[i], m[i], l[i]);
+    }
     const size_t base = split_index(s, k, 0, kb_count);
     store_out((uint2 *)(xs + base),
               make_uint2(h[0] | (uint32_t)h[1] << 16, h[2] | (uint32_t)h[3] << 16), wt);
     store_out((uint2 *)(xs + base + 512),
               make_uint2(m[0] | (uint32_t)m[1] << 16, m[2] | (uint32_t)m[3] << 16), wt);
-    if (terms > 2)
+    if (terms == 3)
         store_out((uint2 *)(xs + base + 1024),
                   make_uint2(l[0] | (uint32_t)l[1] << 16, l[2] | (uint32_t)l[3] << 16), wt);
 }
@@ -1072,9 +1078,11 @@ __device__ inline bool epilogue(const GemmArgs &a, const EpiOperands &e, const f
     } else if constexpr (EPI == EPI_GELU_SPLIT) {
         if (live) {
             float g[4];
+            // fp16 pairs (the fast prefill): the fast GELU
+            const bool fast = a.out_terms == kF16Pair;
 #pragma unroll
             for (int r = 0; r < 4; r++) {
-                g[r] = gelu_erf(v[r]);
+                g[r] = fast ? gelu_erf_fast(v[r]) : gelu_erf(v[r]);
                 bad |= !isfinite(g[r]);
             }
             store_split4(a.out_split, s, row0, a.out_kb, g, wt, a.out_terms ? a.out_terms : 3);

@@ -80,8 +80,8 @@ __global__ __launch_bounds__(kTaskThreads) void k_rows_split(GemmArgs a, uint16_
 // lane % 16) splits row n, columns [8g, 8g + 8) of the block into its three
 // terms, so that each term's 1 KB fragment record is one contiguous store.
 // Only the first `terms` terms are written (the projections of a two-term
-// prefill never read the third). Rows past `streams` up to the tile's end
-// become zeros.
+// prefill never read the third), or the two fp16 terms of kF16Pair. Rows
+// past `streams` up to the tile's end become zeros.
 constexpr int kLnTileStride = kWidth + 4;  // floats per LDS row: 8 lanes of a
                                            // 16-byte read hit distinct banks
 __global__ __launch_bounds__(512) void k_rows_split_ln(const float *__restrict__ x,
@@ -125,12 +125,17 @@ __global__ __launch_bounds__(512) void k_rows_split_ln(const float *__restrict__
         const float4 v0 = src[0], v1 = src[1];
         const float v[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
         uint16_t h[8], m[8], l[8];
+        if (terms == kF16Pair) {
 #pragma unroll
-        for (int k = 0; k < 8; k++) split3(v[k], h[k], m[k], l[k]);
+            for (int k = 0; k < 8; k++) split2h(v[k], h[k], m[k]);
+        } else {
+#pragma unroll
+            for (int k = 0; k < 8; k++) split3(v[k], h[k], m[k], l[k]);
+        }
         uint16_t *rec = out + ((size_t)st * (kWidth / 32) + kb) * 1536 + j * 8;
 #pragma unroll
         for (int p = 0; p < 3; p++) {
-            if (p >= terms) break;
+            if (p >= split_records(terms)) break;
             const uint16_t *t = p == 0 ? h : (p == 1 ? m : l);
             uint4 q;
             q.x = t[0] | (uint32_t)t[1] << 16;
@@ -202,10 +207,23 @@ __device__ inline void wait_blocks(int per_block) {
     }
 }
 
-template <int EPI, bool SCALED, int WR, int WP, int RW, int PW, int NB, int KS, int TERMS>
+// TERMS: the split format (2 or 3 bf16 terms, or kF16Pair: two fp16 terms
+// with fp16 weights on the fp16 matrix cores).
+template <bool F16>
+__device__ inline f32x4 mfma16(const bf16x8 &w, const bf16x8 &x, const f32x4 &c) {
+    if constexpr (F16)
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, w),
+                                                      __builtin_bit_cast(f16x8, x), c, 0, 0, 0);
+    else
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(w, x, c, 0, 0, 0);
+}
+
+template <int EPI, bool SCALED, int WR, int WP, int RW, int PW, int NB, int KS, int FORMAT>
 __global__ __launch_bounds__(kTaskThreads) void k_prefill_gemm(GemmArgs a, int row_groups,
                                                                int pos_groups) {
-    static_assert(TERMS == 2 || TERMS == 3, "split terms");
+    static_assert(FORMAT == 2 || FORMAT == 3 || FORMAT == kF16Pair, "split terms");
+    constexpr int TERMS = split_records(FORMAT);
+    constexpr bool F16 = FORMAT == kF16Pair;
     static_assert(WR * WP == kTaskWaves, "8 waves");
     static_assert(kChain % KS == 0, "a stage never straddles a chain");
     constexpr int RT = WR * RW, PT = WP * PW;
@@ -379,9 +397,8 @@ __global__ __launch_bounds__(kTaskThreads) void k_prefill_gemm(GemmArgs a, int r
                 for (int t = 0; t < TERMS; t++)
 #pragma unroll
                     for (int p = 0; p < PW; p++)
-                        c[p] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                            wa[r], xt[p][t], t == 0 ? f32x4{0.0f, 0.0f, 0.0f, 0.0f} : c[p], 0,
-                            0, 0);
+                        c[p] = mfma16<F16>(wa[r], xt[p][t],
+                                           t == 0 ? f32x4{0.0f, 0.0f, 0.0f, 0.0f} : c[p]);
 #pragma unroll
                 for (int p = 0; p < PW; p++) {
                     acc[r][p][0] = fmaf(sc[r].x, c[p][0], acc[r][p][0]);
@@ -397,8 +414,7 @@ __global__ __launch_bounds__(kTaskThreads) void k_prefill_gemm(GemmArgs a, int r
                 for (int r = 0; r < RW; r++)
 #pragma unroll
                     for (int p = 0; p < PW; p++)
-                        acc[r][p] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wa[r], xt[p][t],
-                                                                            acc[r][p], 0, 0, 0);
+                        acc[r][p] = mfma16<F16>(wa[r], xt[p][t], acc[r][p]);
         }
     };
     auto block = [&](const uint16_t *st) {
@@ -458,14 +474,23 @@ __global__ __launch_bounds__(kTaskThreads) void k_prefill_gemm(GemmArgs a, int r
 }
 
 // Q8 fragments to bf16 fragments (the same order; int8 values are exact in
-// bf16) and fp16 block scales to fp32 (exact).
+// bf16), optionally to fp16 fragments too, and fp16 block scales to fp32
+// (exact).
 __global__ void k_wide_from_q8(const int8_t *__restrict__ values, const uint16_t *__restrict__ scales,
                                size_t n_values, uint16_t *__restrict__ out_values,
-                               float *__restrict__ out_scales) {
+                               float *__restrict__ out_scales, uint16_t *__restrict__ out_f16) {
     const size_t stride = (size_t)gridDim.x * blockDim.x;
     for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n_values / 8; i += stride) {
         const uint2 raw = *(const uint2 *)(values + i * 8);
         *(bf16x8 *)(out_values + i * 8) = q8_to_bf16(raw);
+        if (out_f16) {
+            // int8 values are exact in fp16 as well
+            f16x8 h;
+#pragma unroll
+            for (int k = 0; k < 8; k++)
+                h[k] = (_Float16)(float)(int8_t)((k < 4 ? raw.x : raw.y) >> (8 * (k & 3)));
+            *(f16x8 *)(out_f16 + i * 8) = h;
+        }
     }
     for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n_values / 32; i += stride)
         out_scales[i] = half_to_float(scales[i]);
@@ -881,25 +906,27 @@ __global__ __launch_bounds__(kPairThreads) void k_prefill_attention_mfma(
 }
 
 // ---------------------------------------------------------------------------
-template <int EPI, bool SCALED, int WR, int WP, int RW, int PW, int NB, int KS>
-int launch_gemm(const GemmArgs &a, hipStream_t stream) {
+template <int EPI, bool SCALED, int WR, int WP, int RW, int PW, int NB, int KS, int FORMAT>
+int launch_format(const GemmArgs &a, hipStream_t stream) {
     constexpr int RT = WR * RW, PT = WP * PW;
     const int row_groups = (a.n_rows / 16) / RT;
     const int pos_groups = ((a.streams + 15) / 16 + PT - 1) / PT;
-    if (a.split_terms == 2) {
-        hipLaunchKernelGGL((k_prefill_gemm<EPI, SCALED, WR, WP, RW, PW, NB, KS, 2>),
-                           dim3(row_groups * pos_groups), dim3(kTaskThreads), 0, stream, a,
-                           row_groups, pos_groups);
-        return launch_ok("pgpu_prefill_gemm");
-    }
-    hipLaunchKernelGGL((k_prefill_gemm<EPI, SCALED, WR, WP, RW, PW, NB, KS, 3>),
+    hipLaunchKernelGGL((k_prefill_gemm<EPI, SCALED, WR, WP, RW, PW, NB, KS, FORMAT>),
                        dim3(row_groups * pos_groups), dim3(kTaskThreads), 0, stream, a,
                        row_groups, pos_groups);
     return launch_ok("pgpu_prefill_gemm");
 }
 
+template <int EPI, bool SCALED, int WR, int WP, int RW, int PW, int NB, int KS>
+int launch_gemm(const GemmArgs &a, hipStream_t stream) {
+    if (a.split_terms == 2)
+        return launch_format<EPI, SCALED, WR, WP, RW, PW, NB, KS, 2>(a, stream);
+    return launch_format<EPI, SCALED, WR, WP, RW, PW, NB, KS, 3>(a, stream);
+}
+
 // Tile shapes (rows x positions per work-group), chosen by measurement on
-// MI355X (4096 positions, three split terms):
+// MI355X (4096 positions).
+// Three split terms:
 //  - MLP in (2048 rows, K = 512): 256 x 128, waves of 4 x 4 tiles, a 3 x 1
 //    ring (126 KB of LDS, 256 work-groups, one per CU): 37.6 us against
 //    39.5 for 128 x 64 tiles two per CU (2 x 2 tiles per wave).
@@ -912,8 +939,23 @@ int launch_gemm(const GemmArgs &a, hipStream_t stream) {
 //  - 512 rows (out, MLP out): 128 x 64 with a 2 x 2 ring (256 work-groups,
 //    one per CU): 13.8 / 37.1 us; deeper rings (3 x 2, 4 x 1 .. 8 x 1) and
 //    64-row or 32-position tiles were slower (two terms).
+// fp16 pairs (a stage holds two thirds of the operand bytes), swept over
+// six shapes per projection, ms per 16 x 256 set with the others fixed:
+//  - 512 rows: 128 x 64 with a 3 x 2 ring (1.606 against 1.701 for 2 x 2);
+//  - QKV: 192 x 64, 3 x 1 ring (1.651 against 1.717 for 192 x 128);
+//  - MLP in: 256 x 128 with a 2 x 2 ring (1.541 against 1.552 for 3 x 1,
+//    with the two above).
 template <int EPI, bool SCALED>
 int dispatch_gemm(const GemmArgs &a, hipStream_t stream) {
+    if (a.split_terms == kF16Pair) {
+        if constexpr (EPI == EPI_GELU_SPLIT)
+            if (a.n_rows % (8 * 256) == 0)
+                return launch_format<EPI, SCALED, 4, 2, 4, 4, 2, 2, kF16Pair>(a, stream);
+        if constexpr (EPI == EPI_QKV)
+            if (a.n_rows % (8 * 192) == 0)
+                return launch_format<EPI, SCALED, 4, 2, 3, 2, 3, 1, kF16Pair>(a, stream);
+        return launch_format<EPI, SCALED, 4, 2, 2, 2, 3, 2, kF16Pair>(a, stream);
+    }
     if constexpr (EPI == EPI_GELU_SPLIT)
         if (a.n_rows % (8 * 256) == 0) return launch_gemm<EPI, SCALED, 4, 2, 4, 4, 3, 1>(a, stream);
     if constexpr (EPI == EPI_QKV)
@@ -925,7 +967,9 @@ int dispatch_gemm(const GemmArgs &a, hipStream_t stream) {
 template <int EPI>
 int run_gemm(const GemmArgs &a, const pgpu_wide_matrix *w, hipStream_t stream) {
     if (!w || !w->values || a.n_rows % 128 || (a.k_cols != kWidth && a.k_cols != kFfn) ||
-        a.streams <= 0 || !a.xs || !a.status || (a.split_terms != 2 && a.split_terms != 3))
+        a.streams <= 0 || !a.xs || !a.status ||
+        (a.split_terms != 2 && a.split_terms != 3 && a.split_terms != kF16Pair) ||
+        (a.split_terms == kF16Pair && !w->values_f16))
         return bad_arguments("pgpu_prefill_gemm");
     return w->scales ? dispatch_gemm<EPI, true>(a, stream) : dispatch_gemm<EPI, false>(a, stream);
 }
@@ -936,7 +980,7 @@ GemmArgs gemm_args(const pgpu_wide_matrix *w, const uint16_t *split, int streams
     a.split_terms = terms;
     if (!w) return a;
     a.xs = split;
-    a.w = w->values;
+    a.w = terms == kF16Pair ? w->values_f16 : w->values;
     a.wscale_f = w->scales;
     a.n_rows = (int)w->rows;
     a.k_cols = (int)w->columns;
@@ -954,7 +998,7 @@ extern "C" int pgpu_rows_split_ln(void *stream, const float *rows, const float *
                                   const float *bias, float epsilon, int streams, int terms,
                                   uint16_t *out_split, int *status) {
     if (!rows || !weight || !bias || !out_split || !status || streams <= 0 ||
-        !(epsilon > 0.0f) || terms < 1 || terms > 3)
+        !(epsilon > 0.0f) || terms < 1 || terms > kF16Pair)
         return bad_arguments("pgpu_rows_split_ln");
     // Whole 16-row tiles: the rows past `streams` are written as zeros.
     const int tiles = (streams + 15) / 16;
@@ -1032,7 +1076,7 @@ extern "C" int pgpu_prefill_attention_rows(void *stream, const float *q, const p
                                            uint16_t *out_split, int terms, int *status) {
     if (!q || !kv || !tables || !positions || !entries || !out_split || !status ||
         streams <= 0 || layer < 0 || layer >= kv->layers || table_stride <= 0 ||
-        entry_count <= 0 || entry_count > 65535 || terms < 2 || terms > 3)
+        entry_count <= 0 || entry_count > 65535 || terms < 2 || terms > kF16Pair)
         return bad_arguments("pgpu_prefill_attention_rows");
     hipLaunchKernelGGL(k_prefill_attention_rows, dim3(entry_count, kHeads),
                        dim3(64 * kAttnWaves), 0, (hipStream_t)stream, q, kv->base,
@@ -1048,7 +1092,7 @@ extern "C" int pgpu_prefill_attention_mfma(void *stream, const float *q, const p
                                            uint16_t *out_split, int terms, int *status) {
     if (!q || !kv || !tables || !positions || !pairs || !out_split || !status ||
         streams <= 0 || layer < 0 || layer >= kv->layers || table_stride <= 0 ||
-        pair_count <= 0 || pair_count > 65535 || terms < 2 || terms > 3)
+        pair_count <= 0 || pair_count > 65535 || terms < 2 || terms > kF16Pair)
         return bad_arguments("pgpu_prefill_attention_mfma");
     hipLaunchKernelGGL(k_prefill_attention_mfma, dim3(pair_count, kHeads), dim3(kPairThreads), 0,
                        (hipStream_t)stream, q, kv->base, kv->layer_stride, (unsigned)kv->blocks,
@@ -1058,13 +1102,13 @@ extern "C" int pgpu_prefill_attention_mfma(void *stream, const float *q, const p
 }
 
 extern "C" int pgpu_wide_from_matrix(void *stream, const pgpu_matrix *w, uint16_t *values,
-                                     float *scales) {
+                                     float *scales, uint16_t *values_f16) {
     if (!w || !w->q8 || !w->values || !w->scales || !values || !scales || w->rows % 16 ||
         w->columns % 32)
         return bad_arguments("pgpu_wide_from_matrix");
     const size_t n = w->rows * w->columns;
     const unsigned blocks = (unsigned)((n / 8 + 255) / 256 < 2048 ? (n / 8 + 255) / 256 : 2048);
     hipLaunchKernelGGL(k_wide_from_q8, dim3(blocks), dim3(256), 0, (hipStream_t)stream,
-                       (const int8_t *)w->values, w->scales, n, values, scales);
+                       (const int8_t *)w->values, w->scales, n, values, scales, values_f16);
     return launch_ok("pgpu_wide_from_matrix");
 }

@@ -146,8 +146,8 @@ int phonon_flow_model_create(const PhononFlowLayerWeights *weights, size_t layer
     m->mlp_in = calloc(layers, sizeof(pgpu_matrix));
     m->mlp_out = calloc(layers, sizeof(pgpu_matrix));
     m->wide = calloc(layers * 4, sizeof(pgpu_wide_matrix));
-    /* Per layer 4 uploads and up to 4 x 2 prefill copies; norms; table. */
-    m->allocations = calloc(layers * 12 + 2, sizeof(void *));
+    /* Per layer 4 uploads and up to 4 x 3 prefill copies; norms; table. */
+    m->allocations = calloc(layers * 16 + 2, sizeof(void *));
     float *norms = malloc(layers * 4 * PH_WIDTH * sizeof(float));
     int ok = m->qkv && m->out && m->mlp_in && m->mlp_out && m->wide && m->allocations && norms;
     for (size_t l = 0; ok && l < layers; l++) {
@@ -169,8 +169,8 @@ int phonon_flow_model_create(const PhononFlowLayerWeights *weights, size_t layer
                                    (mats[i].dst->q8 ? 1 : 2) +
                                    (mats[i].dst->q8 ? mats[i].dst->rows * mats[i].dst->columns / 16 : 0);
             }
-            /* The batched prefill's projections read bf16 fragments (and
-             * fp32 scales): converted once here from Q8 (exact). */
+            /* The batched prefill's projections read bf16 or fp16 fragments
+             * (and fp32 scales): converted once here from Q8 (exact). */
             pgpu_wide_matrix *wide = &m->wide[l * 4 + i];
             const pgpu_matrix *mat = mats[i].dst;
             wide->rows = mat->rows;
@@ -181,14 +181,18 @@ int phonon_flow_model_create(const PhononFlowLayerWeights *weights, size_t layer
                 const size_t n = mat->rows * mat->columns;
                 uint16_t *values = pgpu_malloc(n * sizeof(uint16_t));
                 float *scales = values ? pgpu_malloc(n / 32 * sizeof(float)) : NULL;
+                uint16_t *f16 = scales ? pgpu_malloc(n * sizeof(uint16_t)) : NULL;
                 if (values)
                     m->allocations[m->allocation_count++] = values;
                 if (scales)
                     m->allocations[m->allocation_count++] = scales;
-                ok = scales && pgpu_wide_from_matrix(ph_stream(), mat, values, scales);
+                if (f16)
+                    m->allocations[m->allocation_count++] = f16;
+                ok = f16 && pgpu_wide_from_matrix(ph_stream(), mat, values, scales, f16);
                 wide->values = values;
                 wide->scales = scales;
-                m->device_bytes += n * sizeof(uint16_t) + n / 32 * sizeof(float);
+                wide->values_f16 = f16;
+                m->device_bytes += 2 * n * sizeof(uint16_t) + n / 32 * sizeof(float);
             }
         }
         float *n = norms + l * 4 * PH_WIDTH;
@@ -594,13 +598,20 @@ static int enqueue_prefill(PhononFlowBatch *b, void *stream, size_t first, size_
                                             (int)b->splits};
     uint16_t *xs = b->pre.split;
     const float *cur = input;
-    /* Every mode keeps the three split terms of each activation (exact:
-     * the projections have the bits of single steps). Two terms (16
-     * significant bits) measured 10x the oracle's distance from float64 at
-     * the benchmark weights over a 256-position prefill of the 12-layer
-     * stack (max 0.25 vs 0.046), three terms below it (0.005-0.024). */
-    const int terms = 3;
+    /* The exact mode keeps the three bf16 split terms of each activation
+     * (the projections have the bits of single steps). The fast modes take
+     * two fp16 terms (22 significant bits) on the fp16 matrix cores where a
+     * layer's matrices are Q8 (exact in fp16): two thirds of the work. Two
+     * bf16 terms (16 significant bits) measured 10x the oracle's distance
+     * from float64 at the benchmark weights over a 256-position prefill of
+     * the 12-layer stack (max 0.25 vs 0.046), three terms below it
+     * (0.005-0.024). */
     for (size_t l = first; l < first + count; l++) {
+        const pgpu_wide_matrix *wide = &m->wide[l * 4];
+        const int terms = b->pre.exact != 1 && wide[0].values_f16 && wide[1].values_f16 &&
+                                  wide[2].values_f16 && wide[3].values_f16
+                              ? PGPU_SPLIT_F16_PAIR
+                              : 3;
         const float *norm = m->norms + l * 4 * PH_WIDTH;
         float *next = (l + 1 == first + count) ? output : b->x;
         const int layer = (int)(l + pool_offset);
