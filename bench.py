@@ -470,6 +470,15 @@ def large_batch_with_prefill(pkg, lib, seed, layers=12, streams=256, new_streams
         if it >= warmup:
             dec_ms += d_ms
             pre_ms += p_ms
+    # The prefill set alone: back to back, after three untimed sets (each
+    # set above directly follows an 8.9 ms HBM-bound decode step).
+    for it in range(13):
+        if it == 3:
+            pre_t.start()
+        assert lib.phonon_flow_batch_prefill_device(
+            pre, new_streams, first.ctypes.data_as(P_SZ), counts.ctypes.data_as(P_SZ),
+            pre_tables.ctypes.data_as(P_I32), table_len, pin, 10000.0, pout), last_error(lib)
+    alone_ms = pre_t.stop_ms() / 10
     clean = bool(lib.phonon_flow_batch_sync(dec)) and bool(lib.phonon_flow_batch_sync(pre))
     lib.phonon_flow_batch_destroy(pre)
     lib.phonon_flow_batch_destroy(dec)
@@ -488,6 +497,7 @@ def large_batch_with_prefill(pkg, lib, seed, layers=12, streams=256, new_streams
             "decode_frac_of_hbm": round(dec_bytes / (dec_ms / iterations * 1e-3) / 1e9
                                         / HBM_PEAK_GBS, 4),
             "prefill_ms": round(pre_ms / iterations, 3),
+            "prefill_alone_ms": round(alone_ms, 3),
             "prefill_tokens_per_s": round(new_streams * chunk / (pre_ms / iterations * 1e-3), 1),
             "prefill_attention": ["matrix cores", "exact (decode arithmetic)",
                                   "lane per query"][prefill_attention],

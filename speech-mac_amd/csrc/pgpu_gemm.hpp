@@ -271,13 +271,16 @@ __device__ inline void store_out(float *p, float4 v, bool wt) {
 // split fragments: three 8-byte stores.
 // Only the first `terms` split terms are written (a consumer that reads two
 // terms never reads the third).
-// terms = kF16Pair: the two fp16 terms of split2h in the first two records.
+// F16: the two fp16 terms of split2h in the first two records (terms is
+// then ignored).
+template <bool F16 = false>
 __device__ inline void store_split4(uint16_t *__restrict__ xs, int s, int k, int kb_count,
                                     const float *v, bool wt, int terms = 3) {
     uint16_t h[4], m[4], l[4];
-    if (terms == kF16Pair) {
+    if constexpr (F16) {
 #pragma unroll
         for (int i = 0; i < 4; i++) split2h(v[i], h[i], m[i]);
+        terms = 2;
     } else {
 #pragma unroll
         for (int i = 0; i < 4; i++) split3(v[i], h[i], m[i], l[i]);
@@ -1050,8 +1053,9 @@ __device__ inline void load_epilogue_dynamic(EpiOperands &e, const GemmArgs &a, 
 }
 
 // Consumer of one lane's four results v (rows row0..row0+3 of stream s).
-// Returns true if a non-finite value was produced.
-template <int EPI>
+// Returns true if a non-finite value was produced. FORMAT = kF16Pair (the
+// fast prefill): the GELU outputs as fp16 pairs, with the fast GELU.
+template <int EPI, int FORMAT = 3>
 __device__ inline bool epilogue(const GemmArgs &a, const EpiOperands &e, const f32x4 &v, int s,
                                 int row0, bool live) {
     bool bad = false;
@@ -1078,14 +1082,14 @@ __device__ inline bool epilogue(const GemmArgs &a, const EpiOperands &e, const f
     } else if constexpr (EPI == EPI_GELU_SPLIT) {
         if (live) {
             float g[4];
-            // fp16 pairs (the fast prefill): the fast GELU
-            const bool fast = a.out_terms == kF16Pair;
+            constexpr bool F16 = FORMAT == kF16Pair;
 #pragma unroll
             for (int r = 0; r < 4; r++) {
-                g[r] = fast ? gelu_erf_fast(v[r]) : gelu_erf(v[r]);
+                g[r] = F16 ? gelu_erf_fast(v[r]) : gelu_erf(v[r]);
                 bad |= !isfinite(g[r]);
             }
-            store_split4(a.out_split, s, row0, a.out_kb, g, wt, a.out_terms ? a.out_terms : 3);
+            store_split4<F16>(a.out_split, s, row0, a.out_kb, g, wt,
+                              a.out_terms ? a.out_terms : 3);
         }
     } else if constexpr (EPI == EPI_SILU_SPLIT) {
         if (live) {

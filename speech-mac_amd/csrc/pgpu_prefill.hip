@@ -468,7 +468,7 @@ __global__ __launch_bounds__(kTaskThreads) void k_prefill_gemm(GemmArgs a, int r
         for (int p = 0; p < PW; p++) {
             const int s = (pt0 + wp * PW + p) * 16 + (lane & 15);
             const int row0 = (rt0 + wr * RW + r) * 16 + (lane >> 4) * 4;
-            bad |= epilogue<EPI>(a, ep[r][p], tot[r][p], s, row0, s < a.streams);
+            bad |= epilogue<EPI, FORMAT>(a, ep[r][p], tot[r][p], s, row0, s < a.streams);
         }
     flag_nonfinite(a.status, bad);
 }
@@ -672,7 +672,10 @@ __global__ __launch_bounds__(64 * kAttnWaves) void k_prefill_attention_rows(
             v[i] = ok ? acc[d + i] * inv : 0.0f;
             bad |= !isfinite(v[i]);
         }
-        store_split4(out_split, s0 + lane, head * kHeadDim + d, kWidth / 32, v, false, terms);
+        if (terms == kF16Pair)
+            store_split4<true>(out_split, s0 + lane, head * kHeadDim + d, kWidth / 32, v, false);
+        else
+            store_split4(out_split, s0 + lane, head * kHeadDim + d, kWidth / 32, v, false, terms);
     }
     flag_nonfinite(status, bad);
 }
@@ -899,8 +902,12 @@ __global__ __launch_bounds__(kPairThreads) void k_prefill_attention_mfma(
             v[r] = ok ? o[dt][r] * inv : 0.0f;
             bad |= !isfinite(v[r]);
         }
-        store_split4(out_split, s0 + qi, head * kHeadDim + 16 * dt + 4 * g, kWidth / 32, v, false,
-                     terms);
+        if (terms == kF16Pair)
+            store_split4<true>(out_split, s0 + qi, head * kHeadDim + 16 * dt + 4 * g,
+                               kWidth / 32, v, false);
+        else
+            store_split4(out_split, s0 + qi, head * kHeadDim + 16 * dt + 4 * g, kWidth / 32, v,
+                         false, terms);
     }
     flag_nonfinite(status, bad);
 }
