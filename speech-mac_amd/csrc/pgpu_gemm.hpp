@@ -927,7 +927,19 @@ __device__ inline void hold_weights(const WChunk<Q8, CH> &c) {
 template <bool Q8, int CH>
 __device__ inline void load_weights(WChunk<Q8, CH> &c, const GemmArgs &a, int tile, int kbn,
                                     int lane, int kb0, int kb_end) {
-    load_weights_of(c, a.w, a.wscale, tile, kbn, lane, kb0, kb_end);
+#pragma unroll
+    for (int u = 0; u < CH; u++) {
+        const size_t kb = (size_t)min(kb0 + u, kb_end - 1);
+        if constexpr (Q8) {
+            c.raw[u] = *(const uint2 *)((const int8_t *)a.w + ((size_t)tile * kbn + kb) * 512 +
+                                        lane * 8);
+            c.sc[u] = *(const uint2 *)(a.wscale + ((size_t)tile * kbn + kb) * 16 +
+                                       (lane >> 4) * 4);
+        } else {
+            c.w[u] = *(const bf16x8 *)((const uint16_t *)a.w + ((size_t)tile * kbn + kb) * 512 +
+                                       lane * 8);
+        }
+    }
 }
 
 // acc += W_block . X_block for block u of a chunk; `used` false makes the
