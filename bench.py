@@ -740,7 +740,7 @@ def gemv_valu_vs_mfma(pkg, lib, seed=3, calls=400, copies=300):
     return out
 
 
-def flow_head_bench(pkg, lib, streams=64, calls=200, seed=11, graph=1, one_launch=0):
+def flow_head_bench(pkg, lib, streams=64, calls=200, seed=11, graph=1, one_launch=0, fused=-1):
     """The flow head's batched LSD step (phonon_flow_head_device_lsd: noise
     scaling, input/condition projections, seven adaLN projections as one, six
     residual MLP blocks, final layer, EOS logit) for `streams` streams, on a
@@ -761,6 +761,7 @@ def flow_head_bench(pkg, lib, streams=64, calls=200, seed=11, graph=1, one_launc
                                                   last_error(lib)
     assert lib.phonon_flow_head_device_set_graph(dev, graph), last_error(lib)
     assert lib.phonon_flow_head_device_set_one_launch(dev, one_launch), last_error(lib)
+    assert lib.phonon_flow_head_device_set_fused_mlp(dev, fused), last_error(lib)
     stream = lib.phonon_flow_head_device_stream(dev)
     cond = pkg.DeviceBuffer(lib, streams * 512 * 4)
     raw = pkg.DeviceBuffer(lib, streams * 32 * 4)
@@ -794,12 +795,15 @@ def flow_head_bench(pkg, lib, streams=64, calls=200, seed=11, graph=1, one_launc
     for b in (cond, raw, lat, eos):
         b.free()
     lib.phonon_flow_head_device_destroy(dev)
+    # The library's default (-1) fuses the blocks of steps of at most 2 streams.
+    fused_chain = not one_launch and (fused == 1 or (fused == -1 and streams <= 2))
     return {"workload": f"flow head LSD step + EOS logit, B={streams} streams, BF16 head of the "
                         f"reference's shapes (6 adaLN blocks, 8.68 M weights per step)",
             "us_per_step": round(ms * 1e3, 2),
             "frames_per_s": round(streams / (ms * 1e-3), 1),
-            "launches_per_step": 2 if one_launch else 15,
+            "launches_per_step": 2 if one_launch else 9 if fused_chain else 15,
             "one_launch": bool(one_launch),
+            "fused_mlp": fused_chain,
             "weight_bytes_per_step": weight_bytes,
             "weight_GBps": round(weight_bytes / (ms * 1e-3) / 1e9, 1),
             "hbm_frac": round(weight_bytes / (ms * 1e-3) / 8e12, 4),
@@ -810,7 +814,7 @@ def flow_head_bench(pkg, lib, streams=64, calls=200, seed=11, graph=1, one_launc
 
 
 def frame_loop_bench(pkg, lib, layers=12, streams=64, frames=30, warmup=3, seed=2026,
-                     shared_stream=True, graph=1, one_launch=0):
+                     shared_stream=True, graph=1, one_launch=0, fused=-1):
     """The whole per-frame loop of B streams on the GPU: the decode step
     (library default mode), then phonon_flow_head_device_frame (output norm,
     LSD step + EOS logit, latent embedding + condition) writing the next
@@ -841,6 +845,7 @@ def frame_loop_bench(pkg, lib, layers=12, streams=64, frames=30, warmup=3, seed=
         assert lib.phonon_flow_head_device_set_stream(h, d.stream), last_error(lib)
     assert lib.phonon_flow_head_device_set_graph(h, graph), last_error(lib)
     assert lib.phonon_flow_head_device_set_one_launch(h, one_launch), last_error(lib)
+    assert lib.phonon_flow_head_device_set_fused_mlp(h, fused), last_error(lib)
     hs = lib.phonon_flow_head_device_stream(h)
     cond = pkg.DeviceBuffer(lib, streams * 512 * 4)
     raw = pkg.DeviceBuffer(lib, streams * 32 * 4)
@@ -886,6 +891,7 @@ def frame_loop_bench(pkg, lib, layers=12, streams=64, frames=30, warmup=3, seed=
             "head_stream": "the batch's" if shared_stream else "its own, events between",
             "head_graph": bool(graph),
             "head_one_launch": bool(one_launch),
+            "head_fused_mlp": not one_launch and (fused == 1 or (fused == -1 and streams <= 2)),
             "us_per_frame": round(ms * 1e3, 1), "frames_per_s": round(streams / (ms * 1e-3), 1),
             "clean": clean}
 
@@ -1248,14 +1254,18 @@ def main():
         print(json.dumps(gemv_valu_vs_mfma(pkg, lib)), flush=True)
         return
     if args.flow_head:
-        for one in (1, 0):
-            for shared, graph in ((True, 1), (True, 0)):
-                print(json.dumps(frame_loop_bench(pkg, lib, shared_stream=shared, graph=graph,
-                                                  one_launch=one)), flush=True)
+        # (one launch, fused chain): the dataflow launch, the fused chain
+        # (the default), the two-launch-per-block chain.
+        modes = ((1, 0), (0, 1), (0, 0))
+        for one, fused in modes:
+            for graph in (1, 0):
+                print(json.dumps(frame_loop_bench(pkg, lib, shared_stream=True, graph=graph,
+                                                  one_launch=one, fused=fused)), flush=True)
         for streams in (64, 16, 1):
-            for one in (1, 0):
+            for one, fused in modes:
                 for graph in (1, 0):
-                    r = flow_head_bench(pkg, lib, streams=streams, graph=graph, one_launch=one)
+                    r = flow_head_bench(pkg, lib, streams=streams, graph=graph, one_launch=one,
+                                        fused=fused)
                     print(json.dumps(dict(r, graph=graph)), flush=True)
         return
 

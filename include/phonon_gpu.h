@@ -516,14 +516,42 @@ int pgpu_head_mod(void *stream, const pgpu_matrix *ada_w, const uint16_t *silu_s
 int pgpu_head_mlp_in(void *stream, const pgpu_matrix *w, const float *x, int streams,
                      const float *norm_w, const float *norm_b, float eps, const float *mod,
                      int ld_mod, const float *bias, uint16_t *out_split, int *status);
+/* A residual block's output handed to the next launch as partials (the
+ * fused head chain): x = x_prev + gate * ((P_0 + P_1 + ... + P_7) + bias),
+ * the order of pgpu_gemm_gated at K = 512, so x has that launch's bits.
+ * P_j = parts + j * ld_parts * 512 ([streams][512] fp32, ld_parts >=
+ * streams) is the MLP-out product of hidden columns [64 j, 64 j + 64);
+ * gate rows at gate + s * ld_gate; bias [512] (optional). */
+typedef struct pgpu_head_parts {
+    const float *parts;
+    int ld_parts;
+    const float *gate;
+    int ld_gate;
+    const float *bias;
+} pgpu_head_parts;
+/* A residual block of the head as one launch (the fused chain): x = the
+ * rows x, or (prev set) the previous block's output from its partials,
+ * whose 512 dimensions are also stored to x_out (required with prev); h =
+ * LN(x; norm_w, norm_b, eps) * (1 + scale) + shift (mod rows as
+ * pgpu_head_mlp_in); u = SiLU(w_in . h + in_bias); parts_out receives this
+ * block's partials of w_out . u (8 of [ld_parts][512], ld_parts >= streams)
+ * for the next launch. parts_out and x_out must not overlap x or
+ * prev->parts. */
+int pgpu_head_block(void *stream, const pgpu_matrix *w_in, const pgpu_matrix *w_out,
+                    const float *x, int streams, const pgpu_head_parts *prev, float *x_out,
+                    const float *norm_w, const float *norm_b, float eps, const float *mod,
+                    int ld_mod, const float *in_bias, float *parts_out, int ld_parts,
+                    int *status);
 /* out [streams][w->rows] = (residual +) (w . h + bias), h = LN(x; eps) *
- * (1 + scale) + shift as above; with a residual, `ones` is a [w->rows]
+ * (1 + scale) + shift as above, x = the rows x or (prev set) the last
+ * block's output from its partials; with a residual, `ones` is a [w->rows]
  * vector of 1.0f, and out_split (optional) receives out's split fragments
  * (K = w->rows). If eos: eos[s] = eos_rows[s * eos_ld]. */
-int pgpu_head_final(void *stream, const pgpu_matrix *w, const float *x, int streams, float eps,
-                    const float *mod, int ld_mod, const float *bias, const float *residual,
-                    const float *ones, float *out, uint16_t *out_split, const float *eos_rows,
-                    int eos_ld, float *eos, int *status);
+int pgpu_head_final(void *stream, const pgpu_matrix *w, const float *x, int streams,
+                    const pgpu_head_parts *prev, float eps, const float *mod, int ld_mod,
+                    const float *bias, const float *residual, const float *ones, float *out,
+                    uint16_t *out_split, const float *eos_rows, int eos_ld, float *eos,
+                    int *status);
 /* Split fragments (K = 256, stream 0) of [cos | sin](value * freqs[128]). */
 int pgpu_head_time_phase(void *stream, const float *freqs, float value, uint16_t *xs,
                          int *status);

@@ -118,6 +118,13 @@ int phonon_flow_head_device_set_graph(PhononFlowHeadDevice *head, int use_graph)
  * counters), plus a counter reset; 0 (the default): the chain of launches.
  * Both give the same bits. */
 int phonon_flow_head_device_set_one_launch(PhononFlowHeadDevice *head, int one_launch);
+/* fused = 1: the chain runs each residual block as one launch
+ * (pgpu_head_block: the MLP-in work-groups also multiply their 64 hidden
+ * columns by the MLP-out matrix, and the next launch adds the 8 partials in
+ * the MLP-out projection's order), 9 launches per step; 0: two launches per
+ * block, 15 per step; -1 (the default): fused for steps of at most 2
+ * streams. All give the same bits. Returns 0 for any other value. */
+int phonon_flow_head_device_set_fused_mlp(PhononFlowHeadDevice *head, int fused);
 /* Bounds a one-launch task's wait for its inputs (microseconds; 0 = 1 s).
  * A wait that gives up ends the launch early and the next sync reports
  * failure. */

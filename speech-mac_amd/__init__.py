@@ -289,8 +289,10 @@ EXPORTS = {
                              _vp, _f, _vp, _vp, _vp]),
     "pgpu_head_mod": (_i, [_vp, _vp, _vp, _i, _vp, _vp, _i, _vp, _vp, _vp, _vp, _vp]),
     "pgpu_head_mlp_in": (_i, [_vp, _vp, _vp, _i, _vp, _vp, _f, _vp, _i, _vp, _vp, _vp]),
-    "pgpu_head_final": (_i, [_vp, _vp, _vp, _i, _f, _vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _i,
-                             _vp, _vp]),
+    "pgpu_head_block": (_i, [_vp, _vp, _vp, _vp, _i, _vp, _vp, _vp, _vp, _f, _vp, _i, _vp,
+                             _vp, _i, _vp]),
+    "pgpu_head_final": (_i, [_vp, _vp, _vp, _i, _vp, _f, _vp, _i, _vp, _vp, _vp, _vp, _vp, _vp,
+                             _i, _vp, _vp]),
     "pgpu_head_time_phase": (_i, [_vp, _vp, _f, _vp, _vp]),
     "pgpu_head_time_sum": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "phonon_flow_head_forward": (_i, [_vp, _vp, _vp, _f, _f, _vp]),
@@ -344,6 +346,7 @@ EXPORTS = {
     "pgpu_head_flow_launch": (_i, [_vp, _vp]),
     "pgpu_head_flow_reset": (_i, [_vp, _vp, _sz]),
     "phonon_flow_head_device_set_one_launch": (_i, [_vp, _i]),
+    "phonon_flow_head_device_set_fused_mlp": (_i, [_vp, _i]),
     "phonon_flow_head_device_set_wait_limit": (_i, [_vp, ctypes.c_uint]),
     "pgpu_q8_gemv": (_i, [_vp, _vp, _vp, _i, _i, _vp, _i, _vp, _vp]),
     "phonon_q8_device_matvec_valu": (_i, [_vp, _sz, _vp, _vp, _sz, _vp]),

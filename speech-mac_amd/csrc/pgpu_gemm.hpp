@@ -55,6 +55,7 @@ enum Source {
     SRC_SPLIT_LDS = 5,
     SRC_ATTN_TAGGED = 6,  // merge of tagged split partials, polled (one-launch step)
     SRC_LN_PARTS = 7,     // LayerNorm of r + the fused MLP's partials, polled (one-launch step)
+    SRC_LN_MOD_PARTS = 8, // SRC_LN_MOD of x_prev + gate * (the partials' sum + bias) (head chain)
 };
 enum Epilogue {
     EPI_STORE = 0,
@@ -63,7 +64,8 @@ enum Epilogue {
     EPI_QKV = 3,
     EPI_SILU_SPLIT = 4,  // split fragments of SiLU((dot + bias) + bias2)
     EPI_GATED = 5,       // residual + gate * (dot + bias); optionally also split fragments
-    EPI_GELU_W2 = 6,     // GELU, then times the task's 64 columns of W2: a tagged partial
+    EPI_GELU_W2 = 6,     // GELU, then times the task's 64 columns of W2: a partial
+    EPI_SILU_W2 = 7,     // SiLU(dot + bias), then times the task's 64 columns of W2: a partial
 };
 
 constexpr int kTaskWaves = 8, kTaskThreads = 64 * kTaskWaves;
@@ -221,12 +223,20 @@ struct GemmArgs {
     int mlp_streams;
     uint64_t *tpub;
     int pub0;
-    // EPI_GELU_W2: the MLP-out matrix (fragments, K = 2048) and its scale
-    // plane; the task's partial goes to tmlp_out ([mlp_streams][512] fp32,
-    // write-through).
+    // EPI_GELU_W2 / EPI_SILU_W2: the MLP-out matrix (fragments, K = 2048 /
+    // 512) and its scale plane (Q8); the task's partial goes to tmlp_out
+    // ([mlp_streams][512] fp32, write-through).
     const void *w2;
     const uint16_t *w2scale;
     float *tmlp_out;
+    // SRC_LN_MOD_PARTS: the previous block's gated residual, x = ln_x +
+    // part_gate * ((P_0 + ... + P_7) + part_bias), P_j at tmlp + (j *
+    // mlp_streams + s) * 512 and the gate row at part_gate + s *
+    // ld_part_gate; dimensions [pub0, pub0 + 64) of x are stored at x_pub
+    // ([streams][512]; null: none).
+    const float *part_gate, *part_bias;
+    int ld_part_gate;
+    float *x_pub;
 };
 
 // ---------------------------------------------------------------------------
@@ -460,42 +470,55 @@ __device__ inline bool rows_ln(Rows2 &r, const float *lw, const float *lb, float
     return bad;
 }
 
-// LayerNorm with an optional affine (lw, lb may be null), then the adaLN
-// modulation h * (1 + scale) + shift by the stream's own rows (shift at
-// mod + s * ld, scale 512 further), in the element order of the flow head
-// (src/phonon_sampler.c:250-278, 330-334, 350-354); fp32 two-pass moments.
-// Returns true if a live output is not finite.
-__device__ inline bool rows_ln_mod(Rows2 &r, const float *lw, const float *lb, float eps,
-                                   const float *mod, int ld, int streams, int st,
-                                   uint16_t *bsh) {
+// The operands of rows_ln_mod_apply for the wave's two streams: the
+// LayerNorm affine (lw, lb may be null) and the streams' shift and scale
+// rows (shift at mod + s * ld, scale 512 further; rows past `streams` read
+// the last stream's).
+struct ModRows {
+    float ws[8], bs[8];
+    float4 m4[2][4];
+    bool has_w, has_b;
+};
+
+__device__ inline void mod_load(ModRows &m, const float *lw, const float *lb, const float *mod,
+                                int ld, int streams, int st) {
     const int wave = threadIdx.x >> 6, j = threadIdx.x & 63;
-    // Every operand is requested before the first reduction: the affine
-    // vectors once (when present), both streams' modulation rows.
-    const bool has_w = lw != nullptr, has_b = lb != nullptr;
+    m.has_w = lw != nullptr;
+    m.has_b = lb != nullptr;
     float4 w0 = make_float4(1.f, 1.f, 1.f, 1.f), w1 = w0;
     float4 b0 = make_float4(0.f, 0.f, 0.f, 0.f), b1 = b0;
-    if (has_w) w0 = *(const float4 *)(lw + j * 8), w1 = *(const float4 *)(lw + j * 8 + 4);
-    if (has_b) b0 = *(const float4 *)(lb + j * 8), b1 = *(const float4 *)(lb + j * 8 + 4);
+    if (m.has_w) w0 = *(const float4 *)(lw + j * 8), w1 = *(const float4 *)(lw + j * 8 + 4);
+    if (m.has_b) b0 = *(const float4 *)(lb + j * 8), b1 = *(const float4 *)(lb + j * 8 + 4);
     const float ws[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
     const float bs[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
-    float4 m4[2][4];
+#pragma unroll
+    for (int k = 0; k < 8; k++) m.ws[k] = ws[k], m.bs[k] = bs[k];
 #pragma unroll
     for (int i = 0; i < 2; i++) {
         const int s = min(st * 16 + 2 * wave + i, streams - 1);
         const float *sh = mod + (size_t)s * ld + j * 8;
-        m4[i][0] = *(const float4 *)sh;
-        m4[i][1] = *(const float4 *)(sh + 4);
-        m4[i][2] = *(const float4 *)(sh + kWidth);
-        m4[i][3] = *(const float4 *)(sh + kWidth + 4);
+        m.m4[i][0] = *(const float4 *)sh;
+        m.m4[i][1] = *(const float4 *)(sh + 4);
+        m.m4[i][2] = *(const float4 *)(sh + kWidth);
+        m.m4[i][3] = *(const float4 *)(sh + kWidth + 4);
     }
+}
+
+// LayerNorm with the optional affine, then the adaLN modulation
+// h * (1 + scale) + shift by the stream's own rows, in the element order of
+// the flow head (src/phonon_sampler.c:250-278, 330-334, 350-354); fp32
+// two-pass moments; into the LDS operand buffer. Returns true if a live
+// output is not finite.
+__device__ inline bool rows_ln_mod_apply(Rows2 &r, const ModRows &m, float eps, uint16_t *bsh) {
+    const int wave = threadIdx.x >> 6, j = threadIdx.x & 63;
     bool bad = false;
 #pragma unroll
     for (int i = 0; i < 2; i++) {
         float *u = r.v[i];
-        const float shift[8] = {m4[i][0].x, m4[i][0].y, m4[i][0].z, m4[i][0].w,
-                                m4[i][1].x, m4[i][1].y, m4[i][1].z, m4[i][1].w};
-        const float scale[8] = {m4[i][2].x, m4[i][2].y, m4[i][2].z, m4[i][2].w,
-                                m4[i][3].x, m4[i][3].y, m4[i][3].z, m4[i][3].w};
+        const float shift[8] = {m.m4[i][0].x, m.m4[i][0].y, m.m4[i][0].z, m.m4[i][0].w,
+                                m.m4[i][1].x, m.m4[i][1].y, m.m4[i][1].z, m.m4[i][1].w};
+        const float scale[8] = {m.m4[i][2].x, m.m4[i][2].y, m.m4[i][2].z, m.m4[i][2].w,
+                                m.m4[i][3].x, m.m4[i][3].y, m.m4[i][3].z, m.m4[i][3].w};
         const float mean =
             wave_sum64(((u[0] + u[1]) + (u[2] + u[3])) + ((u[4] + u[5]) + (u[6] + u[7]))) *
             (1.0f / kWidth);
@@ -511,8 +534,8 @@ __device__ inline bool rows_ln_mod(Rows2 &r, const float *lw, const float *lb, f
 #pragma unroll
         for (int k = 0; k < 8; k++) {
             float h = __fmul_rn(__fsub_rn(u[k], mean), rstd);
-            if (has_w) h = __fmul_rn(h, ws[k]);
-            if (has_b) h = __fadd_rn(h, bs[k]);
+            if (m.has_w) h = __fmul_rn(h, m.ws[k]);
+            if (m.has_b) h = __fadd_rn(h, m.bs[k]);
             u[k] = __fadd_rn(__fmul_rn(h, __fadd_rn(1.0f, scale[k])), shift[k]);
             bad_i |= !isfinite(u[k]);
             if (!r.live[i]) u[k] = 0.0f;
@@ -520,6 +543,80 @@ __device__ inline bool rows_ln_mod(Rows2 &r, const float *lw, const float *lb, f
         bad |= bad_i && r.live[i];
         lds_store8(bsh, 2 * wave + i, j >> 2, j & 3, u);
     }
+    return bad;
+}
+
+// mod_load, then rows_ln_mod_apply (every operand is requested before the
+// first reduction).
+__device__ inline bool rows_ln_mod(Rows2 &r, const float *lw, const float *lb, float eps,
+                                   const float *mod, int ld, int streams, int st,
+                                   uint16_t *bsh) {
+    ModRows m;
+    mod_load(m, lw, lb, mod, ld, streams, st);
+    return rows_ln_mod_apply(r, m, eps, bsh);
+}
+
+// SRC_LN_MOD_PARTS (fused flow-head chain): the previous block's gated
+// residual x = x_prev + gate * ((P_0 + P_1 + ... + P_7) + bias), its
+// MLP-out dot given as the 8 partials of its MLP-in tasks (P_j covers hidden
+// columns [64 j, 64 j + 64)). The partials are added in order, as
+// gemm_split_task adds its 8 waves' column ranges at K = 512, and then the
+// bias, gate and residual in EPI_GATED's order, so x has the bits of the
+// unfused chain. Dimensions [pub0, pub0 + 64) of x go to x_pub (when set);
+// then rows_ln_mod. Returns true if a live value is not finite.
+__device__ inline bool prologue_ln_mod_parts(const GemmArgs &a, int st, uint16_t *bsh) {
+    constexpr int P = kWidth / 64;
+    const int wave = threadIdx.x >> 6, j = threadIdx.x & 63;
+    // Every operand is requested first: x_prev, the modulation rows, the
+    // bias, then per stream its gate and partials (rows past the batch read
+    // the last stream's; their results are never stored).
+    Rows2 r;
+    rows_load(r, a.ln_x, a.streams, st);
+    ModRows m;
+    mod_load(m, a.ln_w, a.ln_b, a.mod, a.ld_mod, a.streams, st);
+    const bool has_b = a.part_bias != nullptr;
+    float4 b0 = make_float4(0.f, 0.f, 0.f, 0.f), b1 = b0;
+    if (has_b) {
+        b0 = *(const float4 *)(a.part_bias + j * 8);
+        b1 = *(const float4 *)(a.part_bias + j * 8 + 4);
+    }
+    const float bias[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+    const bool pub = a.x_pub && a.pub0 >= 0 && (j >> 3) == (a.pub0 >> 6);
+    bool bad = false;
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+        const int s = min(st * 16 + 2 * wave + i, a.streams - 1);
+        const float *g = a.part_gate + (size_t)s * a.ld_part_gate + j * 8;
+        const float4 g0 = *(const float4 *)g, g1 = *(const float4 *)(g + 4);
+        const float gate[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+        float sum[8];
+#pragma unroll
+        for (int p = 0; p < P; p++) {
+            const float *q = a.tmlp + ((size_t)p * a.mlp_streams + s) * kWidth + j * 8;
+            const float4 q0 = *(const float4 *)q, q1 = *(const float4 *)(q + 4);
+            const float v[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+#pragma unroll
+            for (int k = 0; k < 8; k++) sum[k] = p == 0 ? v[k] : __fadd_rn(sum[k], v[k]);
+        }
+        float *u = r.v[i];
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const float lin = has_b ? __fadd_rn(sum[k], bias[k]) : sum[k];
+            u[k] = __fadd_rn(u[k], __fmul_rn(gate[k], lin));
+            bad |= r.live[i] && !isfinite(u[k]);
+        }
+    }
+    if (pub) {
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            if (!r.live[i]) continue;  // uniform per wave
+            float *o = a.x_pub + (size_t)(st * 16 + 2 * wave + i) * kWidth + j * 8;
+            const float *u = r.v[i];
+            store_out(o, make_float4(u[0], u[1], u[2], u[3]), a.wt_out);
+            store_out(o + 4, make_float4(u[4], u[5], u[6], u[7]), a.wt_out);
+        }
+    }
+    bad |= rows_ln_mod_apply(r, m, a.ln_eps, bsh);
     return bad;
 }
 
@@ -1026,7 +1123,8 @@ __device__ inline void load_epilogue_static(EpiOperands &e, const GemmArgs &a, i
     e.gate = make_float4(0.f, 0.f, 0.f, 0.f);
     e.ok = false;
     if (!live) return;
-    if constexpr (EPI == EPI_STORE || EPI == EPI_SILU_SPLIT || EPI == EPI_GATED) {
+    if constexpr (EPI == EPI_STORE || EPI == EPI_SILU_SPLIT || EPI == EPI_GATED ||
+                  EPI == EPI_SILU_W2) {
         if (a.bias) {
             e.add = *(const float4 *)(a.bias + row0);
             e.has_add = true;
@@ -1176,16 +1274,15 @@ __device__ inline bool epilogue(const GemmArgs &a, const EpiOperands &e, const f
     return bad;
 }
 
-// EPI_GELU_W2's MLP-out weights of one wave (row tiles 4w .. 4w+3, the
-// task's two column blocks); empty for every other epilogue.
+// The fused MLP's MLP-out weights of one wave (row tiles 4w .. 4w+3, the
+// task's two column blocks of kbn); empty for every other epilogue.
 template <bool Q8, bool ON>
 struct W2Weights {
     WChunk<Q8, 2> w[4];
-    __device__ void load(const GemmArgs &a, int bx, int wave, int lane) {
+    __device__ void load(const GemmArgs &a, int bx, int wave, int lane, int kbn) {
 #pragma unroll
         for (int u = 0; u < 4; u++)
-            load_weights_of(w[u], a.w2, a.w2scale, wave * 4 + u, kFfn / 32, lane, 2 * bx,
-                            2 * bx + 2);
+            load_weights_of(w[u], a.w2, a.w2scale, wave * 4 + u, kbn, lane, 2 * bx, 2 * bx + 2);
     }
     __device__ void hold() const {
 #pragma unroll
@@ -1194,30 +1291,40 @@ struct W2Weights {
 };
 template <bool Q8>
 struct W2Weights<Q8, false> {
-    __device__ void load(const GemmArgs &, int, int, int) {}
+    __device__ void load(const GemmArgs &, int, int, int, int) {}
     __device__ void hold() const {}
 };
 
-// EPI_GELU_W2 (fused MLP), after gemm_wide_task's half sums: the task's 64
-// GELU rows are hidden columns [64 bx, 64 bx + 64) of the MLP-out
+// EPI_GELU_W2 / EPI_SILU_W2 (fused MLP), after gemm_wide_task's half sums:
+// the task's 64 activated rows (GELU of the dot; SiLU of dot + bias, as
+// EPI_SILU_SPLIT) are hidden columns [64 bx, 64 bx + 64) of the MLP-out
 // projection. Waves (t, half 0) put them into LDS as split fragments (two
 // column blocks, past the half sums), then every wave multiplies its 4 row
 // tiles of the MLP-out matrix by them (mfma_block: per-block Q8 order) and
-// stores its rows of the task's partial write-through (the task drains
-// them before it counts).
-template <bool Q8>
-__device__ inline void gelu_w2_partial(const GemmArgs &a, uint16_t *bsh, const f32x4 &acc,
-                                       const W2Weights<Q8, true> &w2, int t, int half, int s,
-                                       bool live) {
+// stores its rows of the task's partial write-through (the one-launch step
+// drains them before it counts).
+template <bool Q8, int EPI>
+__device__ inline void act_w2_partial(const GemmArgs &a, uint16_t *bsh, const f32x4 &acc,
+                                      const EpiOperands &e, const W2Weights<Q8, true> &w2, int t,
+                                      int half, int s, bool live) {
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     uint16_t *hb = bsh + 2 * kLdsBlock;
     bool bad = false;
     if (half == 0) {
         const f32x4 p = ((const f32x4 *)bsh)[t * 64 + lane];
+        const float add[4] = {e.add.x, e.add.y, e.add.z, e.add.w};
 #pragma unroll
         for (int r = 0; r < 4; r++) {
-            float g = gelu_erf(__fadd_rn(acc[r], p[r]));
+            float g;
+            if constexpr (EPI == EPI_SILU_W2) {
+                float y = __fadd_rn(acc[r], p[r]);
+                if (e.has_add) y = __fadd_rn(y, add[r]);
+                bad |= live && !isfinite(y);
+                g = __fdiv_rn(y, __fadd_rn(1.0f, expf(-y)));
+            } else {
+                g = gelu_erf(__fadd_rn(acc[r], p[r]));
+            }
             bad |= live && !isfinite(g);
             if (!live) g = 0.0f;
             const int c = 16 * t + (lane >> 4) * 4 + r;  // hidden column within the task
@@ -1287,11 +1394,14 @@ __device__ inline void gemm_wide_task(const GemmArgs &a, int bx, int st, uint16_
     // The fused epilogue's MLP-out weights, requested with the projection's
     // own (the fused kernel runs one work-group per CU, so registers are
     // not what limits it).
-    W2Weights<Q8, EPI == EPI_GELU_W2> w2;
-    w2.load(a, bx, wave, lane);
+    // The head's fused block (EPI_SILU_W2) requests them after its prologue
+    // instead, whose loads they would otherwise queue behind.
+    constexpr bool fused = EPI == EPI_GELU_W2 || EPI == EPI_SILU_W2;
+    W2Weights<Q8, fused> w2;
+    if constexpr (EPI == EPI_GELU_W2) w2.load(a, bx, wave, lane, kFfn / 32);
     if constexpr (SRC == SRC_LN_PARTS || EPI == EPI_GELU_W2)
         if (active) hold_weights(w);
-    w2.hold();
+    if constexpr (EPI == EPI_GELU_W2) w2.hold();
     int position = 0;
     if constexpr (SRC == SRC_ATTN_TAGGED)
         if (lane < 16 && st * 16 + lane < a.streams)
@@ -1308,6 +1418,8 @@ __device__ inline void gemm_wide_task(const GemmArgs &a, int bx, int st, uint16_
         split_to_lds(a.xs, st, bsh);
     } else if constexpr (SRC == SRC_LN_PARTS) {
         bad_in = prologue_ln_parts(a, st, bsh);
+    } else if constexpr (SRC == SRC_LN_MOD_PARTS) {
+        bad_in = prologue_ln_mod_parts(a, st, bsh);
     } else {
         Rows2 r;
         if (a.tx)
@@ -1322,6 +1434,7 @@ __device__ inline void gemm_wide_task(const GemmArgs &a, int bx, int st, uint16_
             rows_plain(r, bsh);
     }
     flag_nonfinite(a.status, bad_in);
+    if constexpr (EPI == EPI_SILU_W2) w2.load(a, bx, wave, lane, kWidth / 32);
     __syncthreads();
     if (a.ready_mark && threadIdx.x == 0) *a.ready_mark = wall_clock64();
 
@@ -1347,8 +1460,8 @@ __device__ inline void gemm_wide_task(const GemmArgs &a, int bx, int st, uint16_
     f32x4 *partial = (f32x4 *)bsh;
     if (half == 1) partial[t * 64 + lane] = acc;
     __syncthreads();
-    if constexpr (EPI == EPI_GELU_W2) {
-        gelu_w2_partial<Q8>(a, bsh, acc, w2, t, half, s, live);
+    if constexpr (fused) {
+        act_w2_partial<Q8, EPI>(a, bsh, acc, e, w2, t, half, s, live);
         return;
     }
     if (half == 0 && active) {

@@ -5,7 +5,11 @@
 // modulation in front of each block's first MLP projection and of the final
 // layer, the Euler update and the EOS copy in the final launch. A step of B
 // streams is 15 launches: front, modulation + input, 6 x (MLP in, MLP out),
-// final. The time embedding's sincos and RMS scaling run once per (s, t).
+// final. The fused chain (pgpu_head_block) makes each block one launch:
+// the block's MLP-in work-groups also multiply their 64 hidden columns by
+// the MLP-out matrix, and the next launch adds the 8 partials in the
+// MLP-out projection's own order (9 launches, the same bits). The time
+// embedding's sincos and RMS scaling run once per (s, t).
 #include <cmath>
 
 #include "pgpu_gemm.hpp"
@@ -108,16 +112,33 @@ __global__ __launch_bounds__(kTaskThreads) void k_head_mlp_in(GemmArgs a) {
     wide_at<SRC_LN_MOD, EPI_SILU_SPLIT>(a, blockIdx.x, (uint16_t *)lds4);
 }
 
-// Last launch: the final layer on the modulated LayerNorm of x, either the
-// velocity (EPI_STORE) or noise + velocity (EPI_GATED with a gate of ones,
-// exact); one more work-group copies the EOS logits out of their padded
-// rows.
-template <int EPI>
+// A residual block of the fused chain, one launch: x (the rows, SRC_LN_MOD,
+// or the previous block's output from its partials, SRC_LN_MOD_PARTS, each
+// work-group storing its 64 dimensions of it), LayerNorm + modulation, the
+// MLP-in projection + SiLU of the work-group's 64 hidden columns, and their
+// product with the MLP-out matrix: partial bx of the block
+// ([ld_parts][512] at parts_out + bx * ld_parts * 512).
+template <int SRC>
+__global__ __launch_bounds__(kTaskThreads) void k_head_block(GemmArgs a, int ld_parts) {
+    __shared__ uint4 lds4[kTaskLds / 8];
+    constexpr int groups = kWidth / 64;
+    const int bx = (int)blockIdx.x % groups, st = (int)blockIdx.x / groups;
+    a.tmlp_out += (size_t)bx * ld_parts * kWidth;
+    a.pub0 = bx * 64;
+    gemm_wide_task<SRC, EPI_SILU_W2, false>(a, bx, st, (uint16_t *)lds4, NoWait{});
+}
+
+// Last launch: the final layer on the modulated LayerNorm of x (SRC_LN_MOD:
+// the rows; SRC_LN_MOD_PARTS: the last block's output from its partials),
+// either the velocity (EPI_STORE) or noise + velocity (EPI_GATED with a gate
+// of ones, exact); one more work-group copies the EOS logits out of their
+// padded rows.
+template <int SRC, int EPI>
 __global__ __launch_bounds__(kTaskThreads) void k_head_final(GemmArgs a, const float *eos_rows,
                                                              int eos_ld, float *eos) {
     __shared__ uint4 lds4[kTaskLds / 8];
     const int n = wide_groups(a);
-    if ((int)blockIdx.x < n) return wide_at<SRC_LN_MOD, EPI>(a, blockIdx.x, (uint16_t *)lds4);
+    if ((int)blockIdx.x < n) return wide_at<SRC, EPI>(a, blockIdx.x, (uint16_t *)lds4);
     bool bad = false;
     for (int s = threadIdx.x; s < a.streams; s += kTaskThreads) {
         const float e = eos_rows[(size_t)s * eos_ld];
@@ -292,16 +313,73 @@ extern "C" int pgpu_head_mlp_in(void *stream, const pgpu_matrix *w, const float 
     return launch_ok(__func__);
 }
 
+// The previous block's partials (pgpu_head_parts) checked and set into a.
+static bool set_parts(GemmArgs &a, const pgpu_head_parts *prev, int streams) {
+    if (!prev->parts || prev->ld_parts < streams || !prev->gate || prev->ld_gate < kWidth ||
+        prev->ld_gate % 4 || prev->ld_parts % 4)
+        return false;
+    a.tmlp = prev->parts;
+    a.mlp_streams = prev->ld_parts;
+    a.part_gate = prev->gate;
+    a.ld_part_gate = prev->ld_gate;
+    a.part_bias = prev->bias;
+    return true;
+}
+
+// True if [a, a + na) and [b, b + nb) (floats) share an address.
+static bool overlap(const float *a, size_t na, const float *b, size_t nb) {
+    return a < b + nb && b < a + na;
+}
+
+extern "C" int pgpu_head_block(void *stream, const pgpu_matrix *w_in, const pgpu_matrix *w_out,
+                               const float *x, int streams, const pgpu_head_parts *prev,
+                               float *x_out, const float *norm_w, const float *norm_b, float eps,
+                               const float *mod, int ld_mod, const float *in_bias,
+                               float *parts_out, int ld_parts, int *status) {
+    if (!bf16_matrix(w_in, kWidth, kWidth) || !bf16_matrix(w_out, kWidth, kWidth) || !x ||
+        streams <= 0 || !mod || ld_mod < 2 * kWidth || ld_mod % 4 || !(eps > 0.0f) ||
+        !parts_out || ld_parts < streams || ld_parts % 4 || (prev && !x_out))
+        return bad_arguments(__func__);
+    const size_t rows = (size_t)streams * kWidth, parts = (size_t)8 * ld_parts * kWidth;
+    GemmArgs a = head_args(w_in, streams, status);
+    if (prev) {
+        if (!set_parts(a, prev, streams) || overlap(x_out, rows, x, rows) ||
+            overlap(parts_out, parts, prev->parts, (size_t)8 * prev->ld_parts * kWidth) ||
+            overlap(x_out, rows, parts_out, parts))
+            return bad_arguments(__func__);
+        a.x_pub = x_out;
+    }
+    a.ln_x = x;
+    a.ln_w = norm_w;
+    a.ln_b = norm_b;
+    a.ln_eps = eps;
+    a.mod = mod;
+    a.ld_mod = ld_mod;
+    a.bias = in_bias;
+    a.w2 = w_out->values;
+    a.tmlp_out = parts_out;
+    const dim3 grid((unsigned)wide_groups(a)), block(kTaskThreads);
+    if (prev)
+        hipLaunchKernelGGL(k_head_block<SRC_LN_MOD_PARTS>, grid, block, 0, (hipStream_t)stream, a,
+                           ld_parts);
+    else
+        hipLaunchKernelGGL(k_head_block<SRC_LN_MOD>, grid, block, 0, (hipStream_t)stream, a,
+                           ld_parts);
+    return launch_ok(__func__);
+}
+
 extern "C" int pgpu_head_final(void *stream, const pgpu_matrix *w, const float *x, int streams,
-                               float eps, const float *mod, int ld_mod, const float *bias,
-                               const float *residual, const float *ones, float *out,
-                               uint16_t *out_split, const float *eos_rows, int eos_ld, float *eos,
-                               int *status) {
+                               const pgpu_head_parts *prev, float eps, const float *mod,
+                               int ld_mod, const float *bias, const float *residual,
+                               const float *ones, float *out, uint16_t *out_split,
+                               const float *eos_rows, int eos_ld, float *eos, int *status) {
     if (!w || !bf16_matrix(w, w->rows, kWidth) || w->rows % 16 || !x || streams <= 0 || !mod ||
         ld_mod < 2 * kWidth || ld_mod % 4 || !out || (residual && !ones) || !(eps > 0.0f) ||
         (eos && (!eos_rows || eos_ld < 1)) || (out_split && (!residual || w->rows % 32)))
         return bad_arguments(__func__);
     GemmArgs a = head_args(w, streams, status);
+    if (prev && !set_parts(a, prev, streams))
+        return bad_arguments(__func__);
     a.ln_x = x;
     a.ln_eps = eps;
     // With a residual: the output's split fragments too, w->rows / 32 column
@@ -318,12 +396,20 @@ extern "C" int pgpu_head_final(void *stream, const pgpu_matrix *w, const float *
         a.residual = residual;
         a.gate = ones;
         a.ld_gate = 0;
-        hipLaunchKernelGGL(k_head_final<EPI_GATED>, dim3(blocks), dim3(kTaskThreads), 0,
-                           (hipStream_t)stream, a, eos_rows, eos_ld, eos);
-    } else {
-        hipLaunchKernelGGL(k_head_final<EPI_STORE>, dim3(blocks), dim3(kTaskThreads), 0,
-                           (hipStream_t)stream, a, eos_rows, eos_ld, eos);
     }
+    const hipStream_t st = (hipStream_t)stream;
+    if (residual && prev)
+        hipLaunchKernelGGL((k_head_final<SRC_LN_MOD_PARTS, EPI_GATED>), dim3(blocks),
+                           dim3(kTaskThreads), 0, st, a, eos_rows, eos_ld, eos);
+    else if (residual)
+        hipLaunchKernelGGL((k_head_final<SRC_LN_MOD, EPI_GATED>), dim3(blocks), dim3(kTaskThreads),
+                           0, st, a, eos_rows, eos_ld, eos);
+    else if (prev)
+        hipLaunchKernelGGL((k_head_final<SRC_LN_MOD_PARTS, EPI_STORE>), dim3(blocks),
+                           dim3(kTaskThreads), 0, st, a, eos_rows, eos_ld, eos);
+    else
+        hipLaunchKernelGGL((k_head_final<SRC_LN_MOD, EPI_STORE>), dim3(blocks), dim3(kTaskThreads),
+                           0, st, a, eos_rows, eos_ld, eos);
     return launch_ok(__func__);
 }
 

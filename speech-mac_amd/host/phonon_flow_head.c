@@ -22,6 +22,11 @@
 
 enum {
     HB = PHONON_FLOW_HEAD_BLOCKS,
+    /* The fused chain reads its 8 partials of every live stream of a tile
+     * in each of the tile's 8 work-groups (16 KB per stream): it is faster
+     * than two launches per block only for the smallest steps (B = 1, 2:
+     * 1-4 us of 72; B = 4: 3 us slower, B = 64: 18 us slower). */
+    FUSED_AUTO_STREAMS = 2,
     ADA = 3 * PH_WIDTH,              /* rows of one block's adaLN */
     FINAL_ADA = 2 * PH_WIDTH,
     MOD = HB * ADA + FINAL_ADA,      /* 10240 modulation columns */
@@ -45,6 +50,12 @@ struct PhononFlowHeadDevice {
     size_t cap;                        /* streams, a multiple of 16 */
     void *buffers;
     float *noise, *x, *mod, *velocity, *eos_rows, *stage;
+    /* The fused chain (pgpu_head_block): the second x buffer and two sets
+     * of a block's 8 partials [8][cap][512], used alternately. fused: 1
+     * always, 0 never, -1 (the default) for steps of at most
+     * FUSED_AUTO_STREAMS streams. */
+    int fused;
+    float *x2, *parts[2];
     uint16_t *noise_split, *silu_split, *first_split, *time_split, *time_hidden;
     int has_eos;
     int *status;
@@ -283,7 +294,9 @@ static const uint32_t *flow_list(PhononFlowHeadDevice *h, int tiles, int eos, in
 
 static int alloc_buffers(PhononFlowHeadDevice *h, size_t streams) {
     const size_t cap = (streams + 15) / 16 * 16;
-    const size_t floats = cap * (LAT + PH_WIDTH + MOD + LAT + EOS_ROWS) + PH_WIDTH + LAT;
+    const size_t floats =
+        cap * (LAT + PH_WIDTH + MOD + LAT + EOS_ROWS + PH_WIDTH + 2 * 8 * PH_WIDTH) + PH_WIDTH +
+        LAT;
     const size_t halves = split_elems(cap, LAT) + 2 * split_elems(cap, PH_WIDTH) +
                           split_elems(16, 256) + split_elems(16, PH_WIDTH);
     const size_t bytes = floats * sizeof(float) + halves * sizeof(uint16_t);
@@ -295,6 +308,9 @@ static int alloc_buffers(PhononFlowHeadDevice *h, size_t streams) {
     float *f = (float *)p;
     h->noise = f, f += cap * LAT;
     h->x = f, f += cap * PH_WIDTH;
+    h->x2 = f, f += cap * PH_WIDTH;
+    h->parts[0] = f, f += 8 * cap * PH_WIDTH;
+    h->parts[1] = f, f += 8 * cap * PH_WIDTH;
     h->mod = f, f += cap * MOD;
     h->velocity = f, f += cap * LAT;
     h->eos_rows = f, f += cap * EOS_ROWS;
@@ -345,6 +361,32 @@ static int enqueue_head(PhononFlowHeadDevice *h, size_t n, const float *conditio
         !pgpu_head_mod(st, &h->ada, h->silu_split, B, h->b_ada, h->mod, MOD, &h->input,
                        h->noise_split, h->b_input, h->x, h->status))
         return 0;
+    if (h->fused > 0 || (h->fused < 0 && n <= FUSED_AUTO_STREAMS)) {
+        /* x_0 (the input projection) is in xs[0]; block b >= 1 reads
+         * x_(b-1) from xs[(b-1) % 2] and block b-1's partials from
+         * parts[(b-1) % 2], and writes x_b to xs[b % 2] and its partials to
+         * parts[b % 2]; the final layer reads x_5 and block 5's partials. */
+        float *xs[2] = {h->x, h->x2};
+        pgpu_head_parts prev = {.ld_parts = (int)h->cap, .ld_gate = MOD};
+        for (size_t b = 0; b < HB; b++) {
+            if (cancel && cancel(context))
+                return 0;
+            const float *x = b ? xs[(b - 1) % 2] : h->x;
+            if (!pgpu_head_block(st, &h->mlp[b][0], &h->mlp[b][1], x, B, b ? &prev : NULL,
+                                 b ? xs[b % 2] : NULL, h->norm_w[b], h->norm_b[b], 1e-6f,
+                                 h->mod + b * ADA, MOD, h->b_mlp[b][0], h->parts[b % 2],
+                                 (int)h->cap, h->status))
+                return 0;
+            prev.parts = h->parts[b % 2];
+            prev.gate = h->mod + b * ADA + 2 * PH_WIDTH;
+            prev.bias = h->b_mlp[b][1];
+        }
+        if (cancel && cancel(context))
+            return 0;
+        return pgpu_head_final(st, &h->final, xs[(HB - 1) % 2], B, &prev, 1e-6f,
+                               h->mod + HB * ADA, MOD, h->b_final, lsd ? h->noise : NULL,
+                               h->ones, out, out_split, h->eos_rows, EOS_ROWS, eos, h->status);
+    }
     for (size_t b = 0; b < HB; b++) {
         if (cancel && cancel(context))
             return 0;
@@ -357,9 +399,9 @@ static int enqueue_head(PhononFlowHeadDevice *h, size_t n, const float *conditio
     }
     if (cancel && cancel(context))
         return 0;
-    return pgpu_head_final(st, &h->final, h->x, B, 1e-6f, h->mod + HB * ADA, MOD, h->b_final,
-                           lsd ? h->noise : NULL, h->ones, out, out_split, h->eos_rows, EOS_ROWS,
-                           eos, h->status);
+    return pgpu_head_final(st, &h->final, h->x, B, NULL, 1e-6f, h->mod + HB * ADA, MOD,
+                           h->b_final, lsd ? h->noise : NULL, h->ones, out, out_split,
+                           h->eos_rows, EOS_ROWS, eos, h->status);
 }
 
 int phonon_flow_head_device_create(const PhononFlowHead *head, const PhononTensorView *eos_weight,
@@ -373,6 +415,7 @@ int phonon_flow_head_device_create(const PhononFlowHead *head, const PhononTenso
     PhononFlowHeadDevice *h = calloc(1, sizeof(*h));
     if (!h)
         return 0;
+    h->fused = -1;
     int ok = pgpu_stream_create(&h->own_stream) && (h->stream = h->own_stream) &&
              (h->status = pgpu_malloc(sizeof(int))) &&
              pgpu_memset(h->stream, h->status, 0, sizeof(int)) &&
@@ -647,6 +690,19 @@ int phonon_flow_head_device_set_one_launch(PhononFlowHeadDevice *h, int one_laun
     if (!h || !pgpu_stream_sync(h->stream))
         return 0;
     h->one_launch = one_launch != 0;
+    for (size_t i = 0; i < 2; i++) {
+        pgpu_graph_destroy(h->graphs[i].exec);
+        h->graphs[i].exec = NULL;
+    }
+    return 1;
+}
+
+int phonon_flow_head_device_set_fused_mlp(PhononFlowHeadDevice *h, int fused) {
+    if (!h || !pgpu_stream_sync(h->stream))
+        return 0;
+    if (fused < -1 || fused > 1)
+        return ph_fail("flow head: fused MLP mode must be -1, 0 or 1");
+    h->fused = fused;
     for (size_t i = 0; i < 2; i++) {
         pgpu_graph_destroy(h->graphs[i].exec);
         h->graphs[i].exec = NULL;

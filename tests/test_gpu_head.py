@@ -291,10 +291,17 @@ def _head_with_frame(lib, pkg, views, seed, max_streams=64):
 
 @pytest.mark.parametrize("streams", [1, 5, 17, 64])
 def test_one_launch_head_equals_the_chain(lib, pkg, streams):
-    """phonon_flow_head_device_set_one_launch: the LSD step (with and
-    without the EOS logit) and the frame as one dataflow launch give the
-    chain's bits, from a replayed graph and launched directly, and again on
-    a second call (the counters are reset after each launch)."""
+    """The three forms of the LSD step (with and without the EOS logit) and
+    of the frame give the same bits, from a replayed graph and launched
+    directly, each twice in a row:
+    - the two-launch-per-block chain (phonon_flow_head_device_set_fused_mlp
+      0);
+    - the fused chain (set to 1, and the default -1, which fuses at most 2
+      streams: one launch per residual block, whose MLP-out product reaches
+      the next launch as 8 partials added in the MLP-out projection's
+      order);
+    - the one dataflow launch (phonon_flow_head_device_set_one_launch; the
+      counters are reset after each launch)."""
     views = pkg.Views()
     dev = _head_with_frame(lib, pkg, views, 51 + streams)
     stream = lib.phonon_flow_head_device_stream(dev)
@@ -327,14 +334,19 @@ def test_one_launch_head_equals_the_chain(lib, pkg, streams):
         return got
 
     assert lib.phonon_flow_head_device_set_one_launch(dev, 0)
+    assert not lib.phonon_flow_head_device_set_fused_mlp(dev, 2)  # -1, 0 or 1
+    assert lib.phonon_flow_head_device_set_fused_mlp(dev, 0)
     chain = run("chain")
     for graph in (1, 0):
         assert lib.phonon_flow_head_device_set_graph(dev, graph)
-        assert lib.phonon_flow_head_device_set_one_launch(dev, 1)
-        for rep in range(2):
-            one = run(f"one launch graph={graph} rep={rep}")
-            for k in chain:
-                assert np.array_equal(one[k], chain[k]), (k, graph, rep)
+        for fused, one_launch in ((1, 0), (-1, 0), (0, 1)):
+            assert lib.phonon_flow_head_device_set_fused_mlp(dev, fused)
+            assert lib.phonon_flow_head_device_set_one_launch(dev, one_launch)
+            for rep in range(2):
+                mode = f"fused={fused} one launch={one_launch} graph={graph} rep={rep}"
+                got = run(mode)
+                for k in chain:
+                    assert np.array_equal(got[k], chain[k]), (k, mode)
     for b in bufs:
         b.free()
     lib.phonon_flow_head_device_destroy(dev)
