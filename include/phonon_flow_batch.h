@@ -98,13 +98,16 @@ int phonon_flow_batch_prefill_device(PhononFlowBatch *batch, size_t streams, con
                                      const size_t *counts, const int32_t *tables,
                                      size_t table_len, const float *inputs, float theta,
                                      float *outputs);
-/* Attention arithmetic of phase-by-phase batched prefills: 0 (default) a
- * causal kernel on the fp32 matrix cores that loads each 64-key chunk once
- * per run of 64 positions (within 1e-4 of the decode step); 1 the decode
- * step's split attention and merge, so every output row has the bits of
- * single steps; 2 a causal kernel with one lane per query on the vector
- * units (fp32, each key block once per 64 positions). The projections give
- * the bits of single steps in every mode. */
+/* Arithmetic of phase-by-phase batched prefills: 1 exact: the projections
+ * with the decode step's three bf16 split terms and the decode step's split
+ * attention and merge, so every output row has the bits of single steps;
+ * 0 (default) and 2 fast: where a layer's matrices are Q8, the projections
+ * on the fp16 matrix cores with two fp16 split terms of each activation (22
+ * significant bits), and a causal attention that loads each 64-key chunk
+ * once per run of 64 positions: 0 on the fp16 matrix cores with the same
+ * two-term splits of q, K, V and the probabilities, 2 with one lane per
+ * query on the vector units (fp32). The fast modes stay within 1e-4 of the
+ * exact one (normwise per row). */
 int phonon_flow_batch_set_prefill_exact(PhononFlowBatch *batch, int exact);
 /* One-launch step: a task that has waited this many microseconds for its
  * inputs (at most 10 s) gives up, sets status bit 2 (value 4) and makes

@@ -460,15 +460,19 @@ int pgpu_prefill_attention_rows(void *stream, const float *q, const pgpu_paged_k
                                 int layer, const int32_t *tables, int table_stride,
                                 const int32_t *positions, int streams, const int32_t *runs,
                                 int run_count, uint16_t *out_split, int terms, int *status);
-/* The same contract on the fp32 matrix cores (v_mfma_f32_16x16x4_f32), over
- * pairs of runs: `pairs` holds (s0, n, s0', n') per pair, two runs of ONE
- * stream (their pseudo-streams share its block-table row; n' = 0: no second
- * run). One work-group per (pair, head) loads each 64-key chunk of the
- * pair's keys once into LDS; waves 0-3 take the first run, 4-7 the second,
- * wave w of a run its queries 16w .. 16w+15; scores, an online softmax per
- * query and the value sums per 16-key sub-block (exact fp32 products, sums
- * in the matrix cores' order; a query's result does not depend on its
- * pairing). Every pseudo-stream must be in exactly one run. */
+/* The same contract on the matrix cores, over pairs of runs: `pairs` holds
+ * (s0, n, s0', n') per pair, two runs of ONE stream (their pseudo-streams
+ * share its block-table row; n' = 0: no second run). One work-group per
+ * (pair, head) loads each 64-key chunk of the pair's keys once into LDS;
+ * waves 0-3 take the first run, 4-7 the second, wave w of a run its queries
+ * 16w .. 16w+15; scores, an online softmax per query and the value sums per
+ * 16-key sub-block (a query's result does not depend on its pairing).
+ * terms 2 or 3: on the fp32 matrix cores (v_mfma_f32_16x16x4_f32, exact
+ * fp32 products, sums in the matrix cores' order); PGPU_SPLIT_F16_PAIR: on
+ * the fp16 matrix cores, q, K, V and the probabilities each split into two
+ * fp16 terms (22 significant bits; products hi.hi + hi.lo + lo.hi; values
+ * of magnitude 65520 or more make the output non-finite). Every
+ * pseudo-stream must be in exactly one run. */
 int pgpu_prefill_attention_mfma(void *stream, const float *q, const pgpu_paged_kv *kv,
                                 int layer, const int32_t *tables, int table_stride,
                                 const int32_t *positions, int streams, const int32_t *pairs,

@@ -697,17 +697,48 @@ __global__ __launch_bounds__(64 * kAttnWaves) void k_prefill_attention_rows(
 // themselves). Products are exact fp32 multiplications; sums are in the
 // matrix cores' order. A query's arithmetic does not depend on the run it
 // is paired with.
+//
+// FAST (the fast prefill): the products on the 16-bit matrix cores.
+// - S^T = K Q^T with q and K each split into three bf16 terms (split3: 24
+//   significant bits, fp32's exponent range) and the six products
+//   m.m + l.h + h.l + m.h + h.m + h.h (the dropped ones are 2^-24 of the
+//   product): 12 v_mfma_f32_16x16x32_bf16 per 16-key sub-block. The scores
+//   are the sensitive part (at the benchmark weights they reach tens, and
+//   their error moves every probability): two fp16 terms (22 bits) there
+//   put 4x the fp32 kernel's distance from the oracle at the end of the
+//   12-layer stack.
+// - O^T += V^T P^T with V and P each split into two fp16 terms, hi =
+//   fp16(x), lo = fp16(x - hi) (22 significant bits, 5e-7 of the output),
+//   and the products hi.hi + hi.lo + lo.hi: 3 v_mfma_f32_16x16x32_f16 per
+//   (16-dimension tile, 32 keys). P is scaled by 2^12 before its split
+//   (exact; P <= 1) so that the lo terms of small probabilities stay out of
+//   fp16's subnormal range; the output's normalisation takes the 2^-12 back.
+//   A value of magnitude 65520 or more overflows fp16 and makes the output
+//   non-finite, which the status word reports.
+// K goes into LDS as [key][h 64 | m 64 | l 64] and V transposed,
+// [dimension][hi 64 keys | lo 64 keys], so that every operand is one or two
+// LDS reads. The 32 keys of a value step are the lane's keys 4g .. 4g+3 of
+// two sub-blocks (the slots of the score registers): V^T's lanes read the
+// same keys.
 constexpr int kMmaKeys = 64;                 // keys per LDS chunk
 constexpr int kMmaRow = kHeadDim + 4;        // padded LDS row (floats)
+constexpr int kF16Row = 2 * kMmaRow;         // FAST V^T row (halves): hi 64 | lo 64 | pad
+constexpr int kKRow = 3 * kHeadDim + 8;      // FAST K row (bf16): h 64 | m 64 | l 64 | pad
 constexpr int kPairThreads = 512;
+constexpr float kPScale = 4096.0f;           // FAST: P is split as P * 2^12
 
+__device__ inline f16x8 f16x8_of(uint2 a, uint2 b) {
+    return __builtin_bit_cast(f16x8, make_uint4(a.x, a.y, b.x, b.y));
+}
+
+template <bool FAST>
 __global__ __launch_bounds__(kPairThreads) void k_prefill_attention_mfma(
     const float *__restrict__ q, const float *__restrict__ kv, size_t layer_stride,
     unsigned blocks, int layer, const int32_t *__restrict__ tables, int table_stride,
     const int32_t *__restrict__ positions, int streams, const int32_t *__restrict__ pairs,
     uint16_t *__restrict__ out_split, int terms, int *status) {
-    __shared__ float kt[kMmaKeys * kMmaRow];
-    __shared__ float vt[kMmaKeys * kMmaRow];
+    __shared__ __align__(16) float kt[FAST ? kMmaKeys * kKRow / 2 : kMmaKeys * kMmaRow];
+    __shared__ __align__(16) float vt[kMmaKeys * kMmaRow];
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63, t = threadIdx.x;
     const int head = blockIdx.y, half = wave >> 2, hw = wave & 3;
@@ -733,15 +764,20 @@ __global__ __launch_bounds__(kPairThreads) void k_prefill_attention_mfma(
         next_ids[b] = kChunkBlocks + b < table_stride ? table[kChunkBlocks + b] : 0;
     }
     // Thread t moves float4 t of each of the chunk's pool blocks' (K | V)
-    // pair (K: float4 0 .. 255, V: 256 .. 511).
+    // pair (K: float4 0 .. 255, V: 256 .. 511). FAST: the V threads take
+    // the float4s column-wise instead (position t % 16, dimensions
+    // 4 ((t - 256) / 16) .. +3), so that the lanes of a wave write
+    // consecutive keys of one dimension into the transposed V.
+    const int fidx = FAST && t >= 256 ? 256 + ((t & 15) << 4) + ((t - 256) >> 4) : t;
     float4 pre[kChunkBlocks];
-#define PGPU_FETCH_CHUNK()                                                                     \
-    do {                                                                                       \
-        _Pragma("unroll") for (int i = 0; i < kChunkBlocks; i++) {                             \
-            const int id_ = ids[i];                                                            \
-            const int safe_ = (unsigned)id_ < blocks ? id_ : 0;                                \
-            pre[i] = ((const float4 *)(layer_kv + ((size_t)safe_ * kHeads + head) * 2048))[t]; \
-        }                                                                                      \
+#define PGPU_FETCH_CHUNK()                                                                  \
+    do {                                                                                    \
+        _Pragma("unroll") for (int i = 0; i < kChunkBlocks; i++) {                          \
+            const int id_ = ids[i];                                                         \
+            const int safe_ = (unsigned)id_ < blocks ? id_ : 0;                             \
+            const float *blk_ = layer_kv + ((size_t)safe_ * kHeads + head) * 2048;          \
+            pre[i] = ((const float4 *)blk_)[fidx];                                          \
+        }                                                                                   \
     } while (0)
     PGPU_FETCH_CHUNK();
     const int pa = positions[s0a], pb = nb > 0 ? positions[s0b] : 0;
@@ -759,7 +795,29 @@ __global__ __launch_bounds__(kPairThreads) void k_prefill_attention_mfma(
     const bool q_live = qi < n;
     const int qpos = p0 + qi;
     float qv[16];
-    {
+    // FAST: the lane's dimensions 32h + 8g .. +7 (h = 0, 1) as three bf16
+    // terms q3[term][h].
+    bf16x8 q3[3][2];
+    if constexpr (FAST) {
+        const float *src =
+            q + (size_t)(s0 + (q_live ? qi : 0)) * kWidth + head * kHeadDim + 8 * g;
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            const float4 a = *(const float4 *)(src + 32 * h);
+            const float4 b = *(const float4 *)(src + 32 * h + 4);
+            const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+            uint16_t t3[3][8];
+#pragma unroll
+            for (int j = 0; j < 8; j++) split3(q_live ? v[j] : 0.0f, t3[0][j], t3[1][j], t3[2][j]);
+#pragma unroll
+            for (int p = 0; p < 3; p++)
+                q3[p][h] = __builtin_bit_cast(
+                    bf16x8, make_uint4(t3[p][0] | (uint32_t)t3[p][1] << 16,
+                                       t3[p][2] | (uint32_t)t3[p][3] << 16,
+                                       t3[p][4] | (uint32_t)t3[p][5] << 16,
+                                       t3[p][6] | (uint32_t)t3[p][7] << 16));
+        }
+    } else {
         const float4 *src = (const float4 *)(q + (size_t)(s0 + (q_live ? qi : 0)) * kWidth +
                                              head * kHeadDim + 16 * g);
 #pragma unroll
@@ -785,11 +843,39 @@ __global__ __launch_bounds__(kPairThreads) void k_prefill_attention_mfma(
         __syncthreads();  // the previous chunk is consumed
 #pragma unroll
         for (int i = 0; i < kChunkBlocks; i++) {
-            const int key = i * kBlockPos + ((t & 255) >> 4), d = (t & 15) * 4;
+            const int pos = (fidx & 255) >> 4, d = (fidx & 15) * 4;
+            const int key = i * kBlockPos + pos;
             const bool live = c * kMmaKeys + key < key_end;
             bad_block |= live && (unsigned)ids[i] >= blocks;
-            float *dst = (t < 256 ? kt : vt) + key * kMmaRow + d;
-            *(float4 *)dst = live ? pre[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+            const float4 cur = pre[i];
+            if constexpr (FAST) {
+                const float4 v = live ? cur : make_float4(0.f, 0.f, 0.f, 0.f);
+                const float x[4] = {v.x, v.y, v.z, v.w};
+                if (t < 256) {  // K: [key][h | m | l], 4 dimensions
+                    uint16_t t3[3][4];
+#pragma unroll
+                    for (int j = 0; j < 4; j++) split3(x[j], t3[0][j], t3[1][j], t3[2][j]);
+                    uint16_t *kp = (uint16_t *)kt + key * kKRow + d;
+#pragma unroll
+                    for (int p = 0; p < 3; p++)
+                        *(uint2 *)(kp + p * kHeadDim) =
+                            make_uint2(t3[p][0] | (uint32_t)t3[p][1] << 16,
+                                       t3[p][2] | (uint32_t)t3[p][3] << 16);
+                } else {  // V transposed: [dimension][hi keys | lo keys]
+                    uint16_t hi[4], lo[4];
+#pragma unroll
+                    for (int j = 0; j < 4; j++) split2h(x[j], hi[j], lo[j]);
+                    uint16_t *vp = (uint16_t *)vt + d * kF16Row + key;
+#pragma unroll
+                    for (int j = 0; j < 4; j++) {
+                        vp[j * kF16Row] = hi[j];
+                        vp[j * kF16Row + kMmaKeys] = lo[j];
+                    }
+                }
+            } else {
+                float *dst = (t < 256 ? kt : vt) + key * kMmaRow + d;
+                *(float4 *)dst = live ? cur : make_float4(0.f, 0.f, 0.f, 0.f);
+            }
         }
         __syncthreads();
         if (c + 1 < chunks) {
@@ -821,28 +907,50 @@ __global__ __launch_bounds__(kPairThreads) void k_prefill_attention_mfma(
                 for (int r = 0; r < 4; r++) sc[sub][r] = -INFINITY;
                 continue;
             }
-            const float *krow = kt + (sub * 16 + (lane & 15)) * kMmaRow + 16 * g;
-            float kk[16];
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const float4 v = *(const float4 *)(krow + 4 * i);
-                kk[4 * i] = v.x;
-                kk[4 * i + 1] = v.y;
-                kk[4 * i + 2] = v.z;
-                kk[4 * i + 3] = v.w;
-            }
             f32x4 sp[4];
 #pragma unroll
             for (int u = 0; u < 4; u++) sp[u] = f32x4{0.f, 0.f, 0.f, 0.f};
+            if constexpr (FAST) {
+                const uint16_t *krow =
+                    (const uint16_t *)kt + (sub * 16 + (lane & 15)) * kKRow + 8 * g;
 #pragma unroll
-            for (int i = 0; i < 4; i++)
+                for (int h = 0; h < 2; h++) {
+                    bf16x8 k3[3];
 #pragma unroll
-                for (int u = 0; u < 4; u++)
-                    sp[u] = __builtin_amdgcn_mfma_f32_16x16x4f32(kk[4 * i + u], qv[4 * i + u],
-                                                                 sp[u], 0, 0, 0);
+                    for (int p = 0; p < 3; p++)
+                        k3[p] = *(const bf16x8 *)(krow + p * kHeadDim + 32 * h);
+                    // Smallest products first: m.m, l.h, h.l, m.h, h.m, h.h.
+                    f32x4 &c = sp[h];
+                    c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k3[1], q3[1][h], c, 0, 0, 0);
+                    c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k3[2], q3[0][h], c, 0, 0, 0);
+                    c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k3[0], q3[2][h], c, 0, 0, 0);
+                    c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k3[1], q3[0][h], c, 0, 0, 0);
+                    c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k3[0], q3[1][h], c, 0, 0, 0);
+                    c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k3[0], q3[0][h], c, 0, 0, 0);
+                }
+            } else {
+                const float *krow = kt + (sub * 16 + (lane & 15)) * kMmaRow + 16 * g;
+                float kk[16];
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const float4 v = *(const float4 *)(krow + 4 * i);
+                    kk[4 * i] = v.x;
+                    kk[4 * i + 1] = v.y;
+                    kk[4 * i + 2] = v.z;
+                    kk[4 * i + 3] = v.w;
+                }
+#pragma unroll
+                for (int i = 0; i < 4; i++)
+#pragma unroll
+                    for (int u = 0; u < 4; u++)
+                        sp[u] = __builtin_amdgcn_mfma_f32_16x16x4f32(kk[4 * i + u],
+                                                                     qv[4 * i + u], sp[u], 0, 0,
+                                                                     0);
+            }
             // Keys key0 + 16 sub + 4g + r against query qpos.
 #pragma unroll
             for (int r = 0; r < 4; r++) {
+                // (FAST: sp[2], sp[3] are zero; adding them is exact.)
                 const float st = __fadd_rn(__fadd_rn(sp[0][r], sp[1][r]),
                                            __fadd_rn(sp[2][r], sp[3][r]));
                 const int kp = key0 + sub * 16 + 4 * g + r;
@@ -857,29 +965,60 @@ __global__ __launch_bounds__(kPairThreads) void k_prefill_attention_mfma(
         for (int sub = 0; sub < 4; sub++)
 #pragma unroll
             for (int r = 0; r < 4; r++) {
-                sc[sub][r] = sc[sub][r] == -INFINITY ? 0.0f : expf(sc[sub][r] - mn);
+                // FAST: the hardware exp2 of (s - max) * log2(e) (within
+                // 2e-6 relative at |s - max| < 50, like the scores' own error).
+                const float z = sc[sub][r] - mn;
+                sc[sub][r] = sc[sub][r] == -INFINITY ? 0.0f : FAST ? __expf(z) : expf(z);
                 ps += sc[sub][r];
             }
         ps = xor16_32_sum(ps);
-        const float keep = mn == -INFINITY ? 1.0f : expf(m - mn);
+        const float keep = mn == -INFINITY ? 1.0f : FAST ? __expf(m - mn) : expf(m - mn);
         m = mn;
         lsum = fmaf(lsum, keep, ps);
         f32x4 acc[4];
 #pragma unroll
         for (int dt = 0; dt < 4; dt++)
             acc[dt] = f32x4{o[dt][0] * keep, o[dt][1] * keep, o[dt][2] * keep, o[dt][3] * keep};
+        if constexpr (FAST) {
 #pragma unroll
-        for (int sub = 0; sub < 4; sub++) {
-            if (sub >= nsub) break;
+            for (int p2 = 0; p2 < 2; p2++) {
+                if (2 * p2 >= nsub) break;
+                // P^T: slots 0-3 keys 32 p2 + 4g + r, slots 4-7 keys 32 p2 + 16 + 4g + r.
+                f16x8 ph, pl;
 #pragma unroll
-            for (int jj = 0; jj < 4; jj++)
+                for (int j = 0; j < 8; j++) {
+                    const float x = sc[2 * p2 + (j >> 2)][j & 3] * kPScale;
+                    const _Float16 hi = (_Float16)x;
+                    ph[j] = hi;
+                    pl[j] = (_Float16)__fsub_rn(x, (float)hi);
+                }
 #pragma unroll
                 for (int dt = 0; dt < 4; dt++) {
-                    const float va =
-                        vt[(sub * 16 + 4 * g + jj) * kMmaRow + 16 * dt + (lane & 15)];
-                    acc[dt] = __builtin_amdgcn_mfma_f32_16x16x4f32(va, sc[sub][jj], acc[dt], 0,
-                                                                   0, 0);
+                    const uint16_t *vrow = (const uint16_t *)vt +
+                                           (16 * dt + (lane & 15)) * kF16Row + 32 * p2 + 4 * g;
+                    const f16x8 vh =
+                        f16x8_of(*(const uint2 *)vrow, *(const uint2 *)(vrow + 16));
+                    const f16x8 vl = f16x8_of(*(const uint2 *)(vrow + kMmaKeys),
+                                              *(const uint2 *)(vrow + kMmaKeys + 16));
+                    acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vh, ph, acc[dt], 0, 0, 0);
+                    acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vh, pl, acc[dt], 0, 0, 0);
+                    acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vl, ph, acc[dt], 0, 0, 0);
                 }
+            }
+        } else {
+#pragma unroll
+            for (int sub = 0; sub < 4; sub++) {
+                if (sub >= nsub) break;
+#pragma unroll
+                for (int jj = 0; jj < 4; jj++)
+#pragma unroll
+                    for (int dt = 0; dt < 4; dt++) {
+                        const float va =
+                            vt[(sub * 16 + 4 * g + jj) * kMmaRow + 16 * dt + (lane & 15)];
+                        acc[dt] = __builtin_amdgcn_mfma_f32_16x16x4f32(va, sc[sub][jj], acc[dt],
+                                                                       0, 0, 0);
+                    }
+            }
         }
 #pragma unroll
         for (int dt = 0; dt < 4; dt++)
@@ -899,7 +1038,9 @@ __global__ __launch_bounds__(kPairThreads) void k_prefill_attention_mfma(
         float v[4];
 #pragma unroll
         for (int r = 0; r < 4; r++) {
-            v[r] = ok ? o[dt][r] * inv : 0.0f;
+            // FAST: o carries the 2^12 of P (taking it out is exact).
+            const float acc = FAST ? o[dt][r] * (1.0f / kPScale) : o[dt][r];
+            v[r] = ok ? acc * inv : 0.0f;
             bad |= !isfinite(v[r]);
         }
         if (terms == kF16Pair)
@@ -1101,10 +1242,15 @@ extern "C" int pgpu_prefill_attention_mfma(void *stream, const float *q, const p
         streams <= 0 || layer < 0 || layer >= kv->layers || table_stride <= 0 ||
         pair_count <= 0 || pair_count > 65535 || terms < 2 || terms > kF16Pair)
         return bad_arguments("pgpu_prefill_attention_mfma");
-    hipLaunchKernelGGL(k_prefill_attention_mfma, dim3(pair_count, kHeads), dim3(kPairThreads), 0,
-                       (hipStream_t)stream, q, kv->base, kv->layer_stride, (unsigned)kv->blocks,
-                       layer, tables, table_stride, positions, streams, pairs, out_split,
-                       terms, status);
+    const dim3 grid(pair_count, kHeads), block(kPairThreads);
+    if (terms == kF16Pair)
+        hipLaunchKernelGGL(k_prefill_attention_mfma<true>, grid, block, 0, (hipStream_t)stream, q,
+                           kv->base, kv->layer_stride, (unsigned)kv->blocks, layer, tables,
+                           table_stride, positions, streams, pairs, out_split, terms, status);
+    else
+        hipLaunchKernelGGL(k_prefill_attention_mfma<false>, grid, block, 0, (hipStream_t)stream,
+                           q, kv->base, kv->layer_stride, (unsigned)kv->blocks, layer, tables,
+                           table_stride, positions, streams, pairs, out_split, terms, status);
     return launch_ok("pgpu_prefill_attention_mfma");
 }
 

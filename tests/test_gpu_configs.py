@@ -156,9 +156,9 @@ def test_config5_prefill_leg_vs_oracle(lib, pkg, oracle, oracle_mod, syn):
     every position of every stream and the appended K/V of two streams
     against the oracle at 1e-4. With the exact prefill attention, those two
     streams decoded one position at a time give the same bits (outputs and
-    K/V); the matrix-core and the lane-per-query runs (the same projections,
-    attention in their own order) stay within 1e-4 of the exact one
-    everywhere."""
+    K/V); the matrix-core and the lane-per-query runs (projections on two
+    fp16 split terms; the matrix-core attention on fp16 pairs too) stay
+    within 1e-4 of the exact one everywhere."""
     model = helpers.scaled_model(syn, 311, C5_LAYERS)
     views = pkg.Views()
     w = views.layers(model)

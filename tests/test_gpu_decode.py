@@ -771,10 +771,10 @@ def test_batched_prefill_equals_single_steps(lib, syn, pkg, mode, exact):
     chunk) gives, bit for bit, the outputs and appended K/V of decoding the
     same positions one step at a time: phase by phase with the exact prefill
     attention (mode 0) and as one launch (mode 2, which always attends like
-    the decode step). Phase by phase with the matrix-core (exact=0) or
-    lane-per-query (exact=2) prefill attention (projections with the bits of
-    single steps, attention in its own order), every output row and K/V row
-    stays within 1e-4 (normwise per row, the fp32 contract)."""
+    the decode step). Phase by phase with the fast prefills (projections on
+    two fp16 split terms; the matrix-core attention, exact=0, on fp16 pairs
+    too, the lane-per-query one, exact=2, in fp32), every output row and K/V
+    row stays within 1e-4 (normwise per row, the fp32 contract)."""
     layers = 2
     model = scaled_model(syn, 171, layers)
     views = pkg.Views()
