@@ -376,27 +376,33 @@ def pmc_program(pkg, lib, args):
           flush=True)
 
 
-def prefill_mfma_work(layers, new_streams, chunk, terms=3):
+def prefill_mfma_work(layers, new_streams, chunk, terms=3, attn16=False):
     """(16-bit MFMA flops, fp32 MFMA flops) of a batched prefill of
     new_streams fresh prompts of `chunk` positions: the projections as issued
     (one MFMA product per multiply-add and split term: 3 bf16 terms in the
     exact mode, 2 fp16 terms in the fast ones) and the causal attention's Q.K
     and P.V (2 flops per multiply-add, every (query, key) pair with key <=
-    query, 8 heads x 64 dimensions)."""
+    query, 8 heads x 64 dimensions): in fp32, or with attn16 on the 16-bit
+    matrix cores as issued (6 products per Q.K multiply-add, bf16 terms; 3
+    per P.V multiply-add, fp16 pairs), counted with the projections."""
     rows = new_streams * chunk
     proj = rows * layers * (1536 + 512 + 2048 + 2048) * 512 * 2 * terms
     pairs = new_streams * chunk * (chunk + 1) // 2
-    attn = layers * pairs * 8 * 64 * 2 * 2
-    return proj, attn
+    mac = layers * pairs * 8 * 64 * 2
+    if attn16:
+        return proj + mac * (6 + 3), 0
+    return proj, mac * 2
 
 
-def prefill_mfma_fraction(layers, new_streams, chunk, ms, terms):
+def prefill_mfma_fraction(layers, new_streams, chunk, ms, terms, attn16=False):
     """The prefill's matrix-core work against the time it took: bf16 / fp16
     flops at 2.5 PFLOP/s plus fp32 flops at 157.3 TFLOP/s (dense peaks), as
     a fraction of the measured time."""
-    proj, attn = prefill_mfma_work(layers, new_streams, chunk, terms)
+    proj, attn = prefill_mfma_work(layers, new_streams, chunk, terms, attn16)
     secs = ms * 1e-3
     return {"projection_operands": "three bf16 terms" if terms == 3 else "two fp16 terms",
+            "attention": ("16-bit matrix cores (bf16 x3 scores, fp16-pair values; counted "
+                          "with the projections)" if attn16 else "fp32"),
             "proj_tflop": round(proj / 1e12, 2), "fp32_gflop": round(attn / 1e9, 2),
             "proj_TFLOPs": round(proj / secs / 1e12, 1),
             "frac": round((proj / 2.5e15 + attn / 157.3e12) / secs, 4)}
@@ -505,7 +511,8 @@ def large_batch_with_prefill(pkg, lib, seed, layers=12, streams=256, new_streams
             # modes take two fp16 terms (Q8 weights)
             "prefill_mfma": prefill_mfma_fraction(layers, new_streams, chunk,
                                                   pre_ms / iterations,
-                                                  3 if prefill_attention == 1 else 2),
+                                                  3 if prefill_attention == 1 else 2,
+                                                  attn16=prefill_attention == 0),
             "frames_per_s_incl_prefill": round(streams / (per_it_ms * 1e-3), 1),
             "clean": clean}
 
