@@ -747,7 +747,8 @@ def gemv_valu_vs_mfma(pkg, lib, seed=3, calls=400, copies=300):
     return out
 
 
-def flow_head_bench(pkg, lib, streams=64, calls=200, seed=11, graph=1, one_launch=0, fused=-1):
+def flow_head_bench(pkg, lib, streams=64, calls=200, seed=11, graph=1, one_launch=-1,
+                    fused=-1):
     """The flow head's batched LSD step (phonon_flow_head_device_lsd: noise
     scaling, input/condition projections, seven adaLN projections as one, six
     residual MLP blocks, final layer, EOS logit) for `streams` streams, on a
@@ -802,14 +803,18 @@ def flow_head_bench(pkg, lib, streams=64, calls=200, seed=11, graph=1, one_launc
     for b in (cond, raw, lat, eos):
         b.free()
     lib.phonon_flow_head_device_destroy(dev)
-    # The library's default (-1) fuses the blocks of steps of at most 2 streams.
-    fused_chain = not one_launch and (fused == 1 or (fused == -1 and streams <= 2))
+    # The library's defaults (-1): steps of at most 2 streams run as one
+    # launch with tagged hand-offs, larger ones as the chain (whose blocks
+    # the fused mode -1 would fuse at most 2 streams).
+    mode = one_launch if one_launch >= 0 else (2 if streams <= 2 else 0)
+    fused_chain = not mode and (fused == 1 or (fused == -1 and streams <= 2))
     return {"workload": f"flow head LSD step + EOS logit, B={streams} streams, BF16 head of the "
                         f"reference's shapes (6 adaLN blocks, 8.68 M weights per step)",
             "us_per_step": round(ms * 1e3, 2),
             "frames_per_s": round(streams / (ms * 1e-3), 1),
-            "launches_per_step": 2 if one_launch else 9 if fused_chain else 15,
-            "one_launch": bool(one_launch),
+            "launches_per_step": 2 if mode else 9 if fused_chain else 15,
+            "one_launch": bool(mode),
+            "tagged_handoffs": mode == 2,
             "fused_mlp": fused_chain,
             "weight_bytes_per_step": weight_bytes,
             "weight_GBps": round(weight_bytes / (ms * 1e-3) / 1e9, 1),
@@ -821,7 +826,7 @@ def flow_head_bench(pkg, lib, streams=64, calls=200, seed=11, graph=1, one_launc
 
 
 def frame_loop_bench(pkg, lib, layers=12, streams=64, frames=30, warmup=3, seed=2026,
-                     shared_stream=True, graph=1, one_launch=0, fused=-1):
+                     shared_stream=True, graph=1, one_launch=-1, fused=-1):
     """The whole per-frame loop of B streams on the GPU: the decode step
     (library default mode), then phonon_flow_head_device_frame (output norm,
     LSD step + EOS logit, latent embedding + condition) writing the next
@@ -897,8 +902,9 @@ def frame_loop_bench(pkg, lib, layers=12, streams=64, frames=30, warmup=3, seed=
                         f"next step's input, contexts U{{1..2048}}",
             "head_stream": "the batch's" if shared_stream else "its own, events between",
             "head_graph": bool(graph),
-            "head_one_launch": bool(one_launch),
-            "head_fused_mlp": not one_launch and (fused == 1 or (fused == -1 and streams <= 2)),
+            "head_one_launch": one_launch > 0 or (one_launch == -1 and streams <= 2),
+            "head_tagged": one_launch == 2 or (one_launch == -1 and streams <= 2),
+            "head_fused_mlp": one_launch == 0 and (fused == 1 or (fused == -1 and streams <= 2)),
             "us_per_frame": round(ms * 1e3, 1), "frames_per_s": round(streams / (ms * 1e-3), 1),
             "clean": clean}
 
@@ -1261,9 +1267,9 @@ def main():
         print(json.dumps(gemv_valu_vs_mfma(pkg, lib)), flush=True)
         return
     if args.flow_head:
-        # (one launch, fused chain): the dataflow launch, the fused chain
-        # (the default), the two-launch-per-block chain.
-        modes = ((1, 0), (0, 1), (0, 0))
+        # (one launch, fused chain): the dataflow launch with tagged and with
+        # counted hand-offs, the fused chain, the two-launch-per-block chain.
+        modes = ((2, 0), (1, 0), (0, 1), (0, 0))
         for one, fused in modes:
             for graph in (1, 0):
                 print(json.dumps(frame_loop_bench(pkg, lib, shared_stream=True, graph=graph,

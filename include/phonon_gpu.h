@@ -630,6 +630,14 @@ typedef struct {
     unsigned *counters;       /* [tiles][PGPU_HEADC_KINDS][PGPU_HEAD_COUNTER_STRIDE], zero */
     int *status;
     unsigned wait_us;
+    /* Tagged hand-offs along the chain (tagged != 0): x of versions 0..6 (tx)
+     * and SiLU(u) of blocks 0..5 (tu) as 64-bit words, the fp32 value in the
+     * low half and the launch's tag in the high half, [7 or 6][tiles*16][512]
+     * each; consumers poll the words themselves instead of a producer count.
+     * The tag is *tag_word (never 0; pgpu_head_flow_reset advances it). */
+    int tagged;
+    uint64_t *tx, *tu;
+    const unsigned *tag_word;
 } pgpu_head_flow;
 /* The task list of one launch for `tiles` 16-stream tiles (host code): every
  * task after the tasks it waits for. Writes at most `capacity` descriptors
@@ -637,7 +645,10 @@ typedef struct {
 int pgpu_head_flow_schedule(uint32_t *out, int capacity, int tiles, int with_eos,
                             int with_embed);
 int pgpu_head_flow_launch(void *stream, const pgpu_head_flow *f);
-int pgpu_head_flow_reset(void *stream, unsigned *counters, size_t count);
+/* Zeroes the launch's counters; with tag_word (optional), also advances the
+ * tagged launch's tag (tag_word must not reach 0: its owner clears the
+ * tagged words and sets it to 1 before then). */
+int pgpu_head_flow_reset(void *stream, unsigned *counters, size_t count, unsigned *tag_word);
 
 /* -- rows and elements (pgpu_elementwise.hip) -- */
 int pgpu_ln_split(void *stream, const float *x, int streams, const float *w, const float *b,

@@ -115,8 +115,12 @@ int phonon_flow_head_device_frame(PhononFlowHeadDevice *head, size_t streams,
 int phonon_flow_head_device_set_graph(PhononFlowHeadDevice *head, int use_graph);
 /* one_launch = 1: the step runs as one dataflow launch (pgpu_head_flow:
  * every projection a work-group task that waits for its inputs on
- * counters), plus a counter reset; 0 (the default): the chain of launches.
- * Both give the same bits. */
+ * counters), plus a counter reset; 2: the same launch with the chain's
+ * rows (x of each block, its MLP hidden) handed over as tagged words that
+ * the consumers poll, no counter between them; 0: the chain of launches;
+ * -1 (the default): 2 for steps of at most 2 streams (where it is the
+ * fastest form), else 0. All give the same bits. Returns 0 for any other
+ * value. */
 int phonon_flow_head_device_set_one_launch(PhononFlowHeadDevice *head, int one_launch);
 /* fused = 1: the chain runs each residual block as one launch
  * (pgpu_head_block: the MLP-in work-groups also multiply their 64 hidden

@@ -344,7 +344,7 @@ EXPORTS = {
                                  _vp]),
     "pgpu_head_flow_schedule": (_i, [_vp, _i, _i, _i, _i]),
     "pgpu_head_flow_launch": (_i, [_vp, _vp]),
-    "pgpu_head_flow_reset": (_i, [_vp, _vp, _sz]),
+    "pgpu_head_flow_reset": (_i, [_vp, _vp, _sz, _vp]),
     "phonon_flow_head_device_set_one_launch": (_i, [_vp, _i]),
     "phonon_flow_head_device_set_fused_mlp": (_i, [_vp, _i]),
     "phonon_flow_head_device_set_wait_limit": (_i, [_vp, ctypes.c_uint]),

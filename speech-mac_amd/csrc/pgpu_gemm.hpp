@@ -1155,7 +1155,12 @@ __device__ inline void load_epilogue_dynamic(EpiOperands &e, const GemmArgs &a, 
             e.has_add = true;
         }
     } else if constexpr (EPI == EPI_GATED) {
-        if (live) {
+        if (a.tres) {  // tagged residual rows [tiles*16][512], polled
+            const __amdgpu_buffer_rsrc_t r =
+                tag_rsrc(a.tres + (size_t)st * 16 * kWidth, 16 * kWidth * 8);
+            e.add2 = poll_tagged4(r, (uint32_t)(((s & 15) * kWidth + row0) * 8), live, a.tp);
+            if (live) e.gate = *(const float4 *)(a.gate + (size_t)s * a.ld_gate + row0);
+        } else if (live) {
             e.add2 = *(const float4 *)(a.residual + (size_t)s * a.ld_out + row0);
             e.gate = *(const float4 *)(a.gate + (size_t)s * a.ld_gate + row0);
         }
@@ -1215,7 +1220,11 @@ __device__ inline bool epilogue(const GemmArgs &a, const EpiOperands &e, const f
                 g[r] = __fdiv_rn(y, __fadd_rn(1.0f, expf(-y)));
                 bad |= !isfinite(g[r]);
             }
-            store_split4(a.out_split, s, row0, a.out_kb, g, wt);
+            if (a.tout)  // fp32 tagged rows, split by the consumer
+                store_tagged4(a.tout + (size_t)s * kWidth + row0,
+                              make_float4(g[0], g[1], g[2], g[3]), a.tp.tag);
+            else
+                store_split4(a.out_split, s, row0, a.out_kb, g, wt);
         }
     } else if constexpr (EPI == EPI_GATED) {
         if (live) {
@@ -1230,7 +1239,11 @@ __device__ inline bool epilogue(const GemmArgs &a, const EpiOperands &e, const f
                 y[r] = __fadd_rn(res[r], __fmul_rn(gate[r], lin));
                 bad |= !isfinite(y[r]);
             }
-            store_out(o, make_float4(y[0], y[1], y[2], y[3]), wt);
+            if (a.tout)
+                store_tagged4(a.tout + (size_t)s * kWidth + row0,
+                              make_float4(y[0], y[1], y[2], y[3]), a.tp.tag);
+            else
+                store_out(o, make_float4(y[0], y[1], y[2], y[3]), wt);
             if (a.out_split) store_split4(a.out_split, s, row0, a.out_kb, y, wt);
         }
     } else {  // EPI_QKV: rows [0,512) q, [512,1024) k, [1024,1536) v
@@ -1503,9 +1516,67 @@ __device__ inline void gemm_split_task(const GemmArgs &a, int tile, int st, uint
     wait();
     if (wave == 0) load_epilogue_dynamic<EPI>(e, a, st, s, row0, live);
 
-    const uint16_t *xs = a.xs + (size_t)st * kbn * 1536 + lane * 8;
     f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-    for (int kb0 = kb_begin; kb0 < kb_end; kb0 += CH) {
+    if (a.tx && kb_begin < kb_end) {
+        // Operand from tagged fp32 rows [tiles*16][512] (K = 512, at most 2
+        // blocks per wave): lane (n, g) = (lane % 16, lane / 16) polls the 8
+        // columns kb*32 + 8g .. +7 of stream st*16 + n for each of its
+        // blocks and splits them as store_split4 would have (the same MFMA
+        // operands, so the same bits as the fragment path).
+        const __amdgpu_buffer_rsrc_t r =
+            tag_rsrc(a.tx + (size_t)st * 16 * kWidth, 16 * kWidth * 8);
+        u32x4 wv[2][4];
+        const uint64_t t0 = wall_clock64();
+        for (int round = 0;; round++) {
+            __asm__ volatile("" ::: "memory");
+            bool ok = true;
+#pragma unroll
+            for (int b = 0; b < 2; b++) {
+                const int kb = min(kb_begin + b, kb_end - 1);
+                const uint32_t off =
+                    (uint32_t)(((lane & 15) * kWidth + kb * 32 + 8 * (lane >> 4)) * 8);
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    if (live) wv[b][q] = tag_load2(r, off + 16 * q, round == 0 && a.tp.plain_first);
+                    ok &= !live || tag_ok2(wv[b][q], a.tp.tag);
+                }
+            }
+            if (__all(ok)) break;
+            if (tag_give_up(a.tp, t0, round)) break;
+            __builtin_amdgcn_s_sleep(1);
+        }
+        bf16x8 xh[2], xm[2], xl[2];
+#pragma unroll
+        for (int b = 0; b < 2; b++) {
+            uint16_t h[8], m[8], l[8];
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                split3(live ? bitsf(wv[b][q].x) : 0.0f, h[2 * q], m[2 * q], l[2 * q]);
+                split3(live ? bitsf(wv[b][q].z) : 0.0f, h[2 * q + 1], m[2 * q + 1], l[2 * q + 1]);
+            }
+            xh[b] = __builtin_bit_cast(bf16x8, make_uint4(h[0] | (uint32_t)h[1] << 16,
+                                                           h[2] | (uint32_t)h[3] << 16,
+                                                           h[4] | (uint32_t)h[5] << 16,
+                                                           h[6] | (uint32_t)h[7] << 16));
+            xm[b] = __builtin_bit_cast(bf16x8, make_uint4(m[0] | (uint32_t)m[1] << 16,
+                                                           m[2] | (uint32_t)m[3] << 16,
+                                                           m[4] | (uint32_t)m[5] << 16,
+                                                           m[6] | (uint32_t)m[7] << 16));
+            xl[b] = __builtin_bit_cast(bf16x8, make_uint4(l[0] | (uint32_t)l[1] << 16,
+                                                           l[2] | (uint32_t)l[3] << 16,
+                                                           l[4] | (uint32_t)l[5] << 16,
+                                                           l[6] | (uint32_t)l[7] << 16));
+        }
+        // The fragment path's chunk of CH blocks: blocks past the wave's
+        // range repeat its last one with zero weights.
+#pragma unroll
+        for (int u = 0; u < CH; u++) {
+            const int b = min(u, 1);
+            mfma_block(acc, w, u, xh[b], xm[b], xl[b], kb_begin + u < kb_end);
+        }
+    }
+    const uint16_t *xs = a.xs + (size_t)st * kbn * 1536 + lane * 8;
+    for (int kb0 = kb_begin; !a.tx && kb0 < kb_end; kb0 += CH) {
         // A lane whose stream is past the batch loads nothing: its MFMA
         // column is zero and its outputs are never stored.
         bf16x8 xh[CH], xm[CH], xl[CH];

@@ -522,6 +522,15 @@ __device__ inline uint16_t *u_rows(const pgpu_head_flow &f, int block) {
     return f.u_split + (size_t)block * f.tiles * (kWidth / 32) * 1536;
 }
 
+// Tagged hand-off rows: x version v, SiLU(u) of block b ([tiles*16][512]).
+__device__ inline uint64_t *tx_rows(const pgpu_head_flow &f, int version) {
+    return f.tx + (size_t)version * f.tiles * 16 * kWidth;
+}
+
+__device__ inline uint64_t *tu_rows(const pgpu_head_flow &f, int block) {
+    return f.tu + (size_t)block * f.tiles * 16 * kWidth;
+}
+
 constexpr int kAdaRows = 3 * kWidth;                 // one block's shift, scale, gate
 constexpr int kModCols = PGPU_HEAD_BLOCKS * kAdaRows + 2 * kWidth;
 constexpr int kAdaGroupsPerBlock = kAdaRows / 64;    // 24
@@ -532,6 +541,13 @@ __global__ __launch_bounds__(kTaskThreads) void k_head_flow(pgpu_head_flow f) {
     uint16_t *lds = (uint16_t *)lds4;
     const uint32_t d = f.schedule[blockIdx.x];
     const int kind = d & 15, blk = (d >> 4) & 15, tile = (d >> 8) & 255, index = (int)(d >> 16);
+    // Tagged mode: x and u go from task to task as tagged words, polled by
+    // their consumers (the other hand-offs keep their counters).
+    const bool tagged = f.tagged != 0;
+    const TagPoll tp{tagged ? __hip_atomic_load(f.tag_word, __ATOMIC_RELAXED,
+                                                __HIP_MEMORY_SCOPE_AGENT)
+                            : 0u,
+                     f.status, f.wait_us ? (uint64_t)f.wait_us * 100u : kHeadWaitTicks, false};
     switch (kind) {
     case PGPU_HEAD_COND: {
         GemmArgs a = flow_args(f, f.cond_w);
@@ -595,9 +611,10 @@ __global__ __launch_bounds__(kTaskThreads) void k_head_flow(pgpu_head_flow f) {
         a.bias = f.b_input;
         a.out = x_rows(f, 0);
         a.ld_out = kWidth;
+        if (tagged) a.tout = tx_rows(f, 0), a.tp = tp;
         gemm_split_task<EPI_STORE, false>(a, index, tile, lds,
                                           head_wait(f, tile, PGPU_HEADC_NOISE, 1u));
-        head_signal(f, tile, PGPU_HEADC_X);
+        if (!tagged) head_signal(f, tile, PGPU_HEADC_X);
         break;
     }
     case PGPU_HEAD_ADA: {
@@ -622,6 +639,15 @@ __global__ __launch_bounds__(kTaskThreads) void k_head_flow(pgpu_head_flow f) {
         a.bias = f.b_mlp[blk][0];
         a.out_split = u_rows(f, blk);
         a.out_kb = kWidth / 32;
+        if (tagged) {
+            a.tx = tx_rows(f, blk);
+            a.tout = tu_rows(f, blk);
+            a.tp = tp;
+            gemm_wide_task<SRC_LN_MOD, EPI_SILU_SPLIT, false>(
+                a, index, tile, lds,
+                head_wait(f, tile, PGPU_HEADC_ADA + blk, kAdaGroupsPerBlock));
+            break;
+        }
         gemm_wide_task<SRC_LN_MOD, EPI_SILU_SPLIT, false>(
             a, index, tile, lds,
             head_wait(f, tile, PGPU_HEADC_X + blk, kWidth / 16, PGPU_HEADC_ADA + blk,
@@ -638,6 +664,18 @@ __global__ __launch_bounds__(kTaskThreads) void k_head_flow(pgpu_head_flow f) {
         a.residual = x_rows(f, blk);
         a.out = x_rows(f, blk + 1);
         a.ld_out = kWidth;
+        if (tagged) {
+            a.tx = tu_rows(f, blk);
+            a.tres = tx_rows(f, blk);
+            a.tout = tx_rows(f, blk + 1);
+            a.tp = tp;
+            // The gate rows come from the block's ADA tasks: nothing the task
+            // polls implies they are done (the counted chain's MLP_IN count
+            // did), so their count is waited for.
+            gemm_split_task<EPI_GATED, false>(
+                a, index, tile, lds, head_wait(f, tile, PGPU_HEADC_ADA + blk, kAdaGroupsPerBlock));
+            break;
+        }
         gemm_split_task<EPI_GATED, false>(a, index, tile, lds,
                                           head_wait(f, tile, PGPU_HEADC_U + blk,
                                                     (kWidth / 16 + 3) / 4));
@@ -658,11 +696,17 @@ __global__ __launch_bounds__(kTaskThreads) void k_head_flow(pgpu_head_flow f) {
         a.residual = f.noise;
         a.gate = f.ones;
         a.ld_gate = 0;
+        if (tagged) {
+            a.tx = tx_rows(f, PGPU_HEAD_BLOCKS);
+            a.tp = tp;
+        }
         gemm_wide_task<SRC_LN_MOD, EPI_GATED, false>(
             a, 0, tile, lds,
-            head_wait(f, tile, PGPU_HEADC_X + PGPU_HEAD_BLOCKS, kWidth / 16,
-                      PGPU_HEADC_ADA + PGPU_HEAD_BLOCKS, kFinalAdaGroups,
-                      f.with_eos ? PGPU_HEADC_EOS : -1, 1u));
+            tagged ? head_wait(f, tile, PGPU_HEADC_ADA + PGPU_HEAD_BLOCKS, kFinalAdaGroups,
+                               f.with_eos ? PGPU_HEADC_EOS : -1, 1u)
+                   : head_wait(f, tile, PGPU_HEADC_X + PGPU_HEAD_BLOCKS, kWidth / 16,
+                               PGPU_HEADC_ADA + PGPU_HEAD_BLOCKS, kFinalAdaGroups,
+                               f.with_eos ? PGPU_HEADC_EOS : -1, 1u));
         if (f.with_eos && f.eos) {
             const int s = tile * 16 + (int)threadIdx.x;
             if (threadIdx.x < 16 && s < f.streams) {
@@ -690,10 +734,11 @@ __global__ __launch_bounds__(kTaskThreads) void k_head_flow(pgpu_head_flow f) {
     }
 }
 
-__global__ void k_head_flow_reset(unsigned *counters, size_t n) {
+__global__ void k_head_flow_reset(unsigned *counters, size_t n, unsigned *tag_word) {
     for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
          i += (size_t)gridDim.x * blockDim.x)
         counters[i] = 0u;
+    if (tag_word && blockIdx.x == 0 && threadIdx.x == 0) *tag_word = *tag_word + 1u;
 }
 
 }  // namespace
@@ -710,7 +755,8 @@ extern "C" int pgpu_head_flow_launch(void *stream, const pgpu_head_flow *f) {
         !f->x || !f->u_split || !f->ones || !f->latents || !f->counters || !f->status ||
         (f->with_eos && (!bf16_matrix(&f->eos_w, 16, kWidth) || !f->eos_rows)) ||
         (f->with_embed && (!bf16_matrix(&f->embed_w, kWidth, 32) || !f->latent_split ||
-                           !f->embed_in || !f->next)))
+                           !f->embed_in || !f->next)) ||
+        (f->tagged && (!f->tx || !f->tu || !f->tag_word)))
         return bad_arguments("pgpu_head_flow_launch");
     for (int b = 0; b < PGPU_HEAD_BLOCKS; b++)
         if (!bf16_matrix(&f->mlp_w[b][0], kWidth, kWidth) ||
@@ -721,10 +767,11 @@ extern "C" int pgpu_head_flow_launch(void *stream, const pgpu_head_flow *f) {
     return launch_ok("pgpu_head_flow_launch");
 }
 
-extern "C" int pgpu_head_flow_reset(void *stream, unsigned *counters, size_t count) {
+extern "C" int pgpu_head_flow_reset(void *stream, unsigned *counters, size_t count,
+                                    unsigned *tag_word) {
     if (!counters || !count) return bad_arguments("pgpu_head_flow_reset");
     const unsigned blocks = (unsigned)((count + 255) / 256 < 64 ? (count + 255) / 256 : 64);
     hipLaunchKernelGGL(pgpu::k_head_flow_reset, dim3(blocks), dim3(256), 0, (hipStream_t)stream,
-                       counters, count);
+                       counters, count, tag_word);
     return launch_ok("pgpu_head_flow_reset");
 }

@@ -27,6 +27,12 @@ enum {
      * than two launches per block only for the smallest steps (B = 1, 2:
      * 1-4 us of 72; B = 4: 3 us slower, B = 64: 18 us slower). */
     FUSED_AUTO_STREAMS = 2,
+    /* The tagged one-launch step: each consumer polls its operand words
+     * itself, so the poll traffic grows with the live streams of a tile; it
+     * is the fastest form at B = 1 and 2 (63 / 68 us against 72 / 73 for
+     * the chain, graph replay) and slower from 4 streams on (B = 16: 117 vs
+     * 74 us). */
+    TAGGED_AUTO_STREAMS = 2,
     ADA = 3 * PH_WIDTH,              /* rows of one block's adaLN */
     FINAL_ADA = 2 * PH_WIDTH,
     MOD = HB * ADA + FINAL_ADA,      /* 10240 modulation columns */
@@ -71,8 +77,17 @@ struct PhononFlowHeadDevice {
     int eager; /* launch each kernel directly instead of replaying a graph */
     /* One-launch step (pgpu_head_flow): x of every block, u of every block,
      * counters, and the task lists built so far. */
-    int one_launch;
+    int one_launch; /* 0: the chain, 1: one launch, 2: one launch with tagged hand-offs,
+                       -1 (the default): 2 for steps of at most TAGGED_AUTO_STREAMS
+                       streams, else 0 */
     unsigned wait_us;
+    /* Tagged one-launch step: x and u rows as tagged words ([7 + 6][cap][512],
+     * allocated on first use), the device tag word, and the tag the next
+     * launch uses (tracked here so that the words are cleared before the
+     * 32-bit tag would wrap). */
+    uint64_t *tagged_rows;
+    unsigned *tag_word;
+    uint64_t tag_next;
     void *flow_buffers;
     float *fx;
     uint16_t *fu, *latent_split;
@@ -416,6 +431,7 @@ int phonon_flow_head_device_create(const PhononFlowHead *head, const PhononTenso
     if (!h)
         return 0;
     h->fused = -1;
+    h->one_launch = -1;
     int ok = pgpu_stream_create(&h->own_stream) && (h->stream = h->own_stream) &&
              (h->status = pgpu_malloc(sizeof(int))) &&
              pgpu_memset(h->stream, h->status, 0, sizeof(int)) &&
@@ -457,6 +473,8 @@ void phonon_flow_head_device_destroy(PhononFlowHeadDevice *h) {
     pgpu_free(h->input_linear_dev);
     pgpu_free(h->buffers);
     pgpu_free(h->flow_buffers);
+    pgpu_free(h->tagged_rows);
+    pgpu_free(h->tag_word);
     for (size_t i = 0; i < h->nlists; i++)
         pgpu_free(h->lists[i].dev);
     pgpu_free(h->status);
@@ -481,6 +499,14 @@ int phonon_flow_head_device_sync(PhononFlowHeadDevice *h) {
 
 /* The LSD step as one launch (and the counter reset): the same tasks and
  * bits as enqueue_head + the embedding. */
+/* The step form for `streams` streams: 0 the chain, 1 one launch, 2 one
+ * launch with tagged hand-offs. */
+static int lsd_mode(const PhononFlowHeadDevice *h, size_t streams) {
+    if (h->one_launch >= 0)
+        return h->one_launch;
+    return streams <= TAGGED_AUTO_STREAMS ? 2 : 0;
+}
+
 static int enqueue_flow(PhononFlowHeadDevice *h, size_t streams, const float *conditions,
                         const float *norm, const float *raw_noise, float scale,
                         float *latents, float *eos_logits, const float *embed, float *next) {
@@ -533,9 +559,33 @@ static int enqueue_flow(PhononFlowHeadDevice *h, size_t streams, const float *co
     f.counters = h->counters;
     f.status = h->status;
     f.wait_us = h->wait_us;
+    f.tagged = lsd_mode(h, streams) == 2;
+    if (f.tagged) {
+        f.tx = h->tagged_rows;
+        f.tu = h->tagged_rows + (size_t)(HB + 1) * h->cap * PH_WIDTH;
+        f.tag_word = h->tag_word;
+    }
     return pgpu_head_flow_launch(h->stream, &f) &&
            pgpu_head_flow_reset(h->stream, h->counters,
-                                (size_t)f.tiles * PGPU_HEADC_KINDS * PGPU_HEAD_COUNTER_STRIDE);
+                                (size_t)f.tiles * PGPU_HEADC_KINDS * PGPU_HEAD_COUNTER_STRIDE,
+                                f.tagged ? h->tag_word : NULL);
+}
+
+/* The tagged words of the one-launch step, cleared, and the tag word set to
+ * 1 (allocated on first use). Outside any capture. */
+static int reset_tagged(PhononFlowHeadDevice *h) {
+    const size_t words = (size_t)(2 * HB + 1) * h->cap * PH_WIDTH;
+    if (!h->tagged_rows &&
+        !((h->tagged_rows = pgpu_malloc(words * sizeof(uint64_t))) &&
+          (h->tag_word = pgpu_malloc(sizeof(unsigned)))))
+        return 0;
+    const unsigned one = 1;
+    if (!pgpu_stream_sync(h->stream) ||
+        !pgpu_memset(h->stream, h->tagged_rows, 0, words * sizeof(uint64_t)) ||
+        !pgpu_copy_h2d(h->stream, h->tag_word, &one, sizeof(one)) || !pgpu_stream_sync(h->stream))
+        return 0;
+    h->tag_next = 1;
+    return 1;
 }
 
 /* The LSD step; with `next` (a frame): the conditions are the decoder's
@@ -546,7 +596,7 @@ static int enqueue_flow(PhononFlowHeadDevice *h, size_t streams, const float *co
 static int enqueue_lsd(PhononFlowHeadDevice *h, size_t streams, const float *conditions,
                        const float *raw_noise, float temperature, float *latents,
                        float *eos_logits, const float *embed, float *next) {
-    if (h->one_launch)
+    if (lsd_mode(h, streams))
         return enqueue_flow(h, streams, conditions, next ? h->out_norm : NULL, raw_noise,
                             sqrtf(temperature), latents, eos_logits, embed, next);
     if (!enqueue_head(h, streams, conditions, next ? h->out_norm : NULL, raw_noise,
@@ -578,9 +628,17 @@ static int run_lsd(PhononFlowHeadDevice *h, size_t streams, const float *conditi
             return ph_fail("flow head: device rows must be 16-byte aligned");
     /* The one-launch task list is built (and uploaded) outside any capture. */
     int tasks;
-    if (h->one_launch &&
+    const int mode = lsd_mode(h, streams);
+    if (mode &&
         !flow_list(h, (int)((streams + 15) / 16), eos_logits != NULL, next != NULL, &tasks))
         return ph_fail("flow head: task list");
+    /* Every call launches the step once (directly or from its graph), and
+     * each launch advances the device tag: the words are allocated on first
+     * use and cleared before the tag would wrap. */
+    if (mode == 2 && (!h->tagged_rows || h->tag_next >= UINT32_MAX - 1) && !reset_tagged(h))
+        return ph_fail("flow head: tagged words");
+    if (mode == 2)
+        h->tag_next++;
     if (h->eager)
         return enqueue_lsd(h, streams, conditions, raw_noise, temperature, latents, eos_logits,
                            embed, next);
@@ -689,7 +747,11 @@ int phonon_flow_head_device_set_graph(PhononFlowHeadDevice *h, int use_graph) {
 int phonon_flow_head_device_set_one_launch(PhononFlowHeadDevice *h, int one_launch) {
     if (!h || !pgpu_stream_sync(h->stream))
         return 0;
-    h->one_launch = one_launch != 0;
+    if (one_launch < -1 || one_launch > 2)
+        return ph_fail("flow head: one-launch mode must be -1, 0, 1 or 2");
+    if (one_launch == 2 && !h->tagged_rows && !reset_tagged(h))
+        return ph_fail("flow head: tagged words");
+    h->one_launch = one_launch;
     for (size_t i = 0; i < 2; i++) {
         pgpu_graph_destroy(h->graphs[i].exec);
         h->graphs[i].exec = NULL;

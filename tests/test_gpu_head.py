@@ -300,8 +300,11 @@ def test_one_launch_head_equals_the_chain(lib, pkg, streams):
       streams: one launch per residual block, whose MLP-out product reaches
       the next launch as 8 partials added in the MLP-out projection's
       order);
-    - the one dataflow launch (phonon_flow_head_device_set_one_launch; the
-      counters are reset after each launch)."""
+    - the one dataflow launch (phonon_flow_head_device_set_one_launch 1;
+      the counters are reset after each launch), and the same launch with
+      tagged hand-offs along the chain (2; each launch has its own tag);
+    - the library's defaults (-1, -1): the tagged launch for at most 2
+      streams, the chain otherwise."""
     views = pkg.Views()
     dev = _head_with_frame(lib, pkg, views, 51 + streams)
     stream = lib.phonon_flow_head_device_stream(dev)
@@ -335,11 +338,12 @@ def test_one_launch_head_equals_the_chain(lib, pkg, streams):
 
     assert lib.phonon_flow_head_device_set_one_launch(dev, 0)
     assert not lib.phonon_flow_head_device_set_fused_mlp(dev, 2)  # -1, 0 or 1
+    assert not lib.phonon_flow_head_device_set_one_launch(dev, 3)  # -1, 0, 1 or 2
     assert lib.phonon_flow_head_device_set_fused_mlp(dev, 0)
     chain = run("chain")
     for graph in (1, 0):
         assert lib.phonon_flow_head_device_set_graph(dev, graph)
-        for fused, one_launch in ((1, 0), (-1, 0), (0, 1)):
+        for fused, one_launch in ((1, 0), (-1, 0), (0, 1), (0, 2), (-1, -1)):
             assert lib.phonon_flow_head_device_set_fused_mlp(dev, fused)
             assert lib.phonon_flow_head_device_set_one_launch(dev, one_launch)
             for rep in range(2):
@@ -352,10 +356,13 @@ def test_one_launch_head_equals_the_chain(lib, pkg, streams):
     lib.phonon_flow_head_device_destroy(dev)
 
 
-def test_one_launch_head_forced_wait_timeout_recovers(lib, pkg):
+@pytest.mark.parametrize("one_launch", [1, 2])
+def test_one_launch_head_forced_wait_timeout_recovers(lib, pkg, one_launch):
     """A 1 us wait limit, set from the host, makes the one-launch head's
-    waiting tasks give up: the launch ends, sync reports failure; with the
-    limit lifted the same call gives the chain's bits again."""
+    waiting tasks give up (counter waits, and with tagged hand-offs the
+    polls of the tagged rows): the launch ends, sync reports failure; with
+    the limit lifted the same call gives the chain's bits again (the next
+    launch's tag differs from the abandoned one's)."""
     streams = 64
     views = pkg.Views()
     dev = _head_with_frame(lib, pkg, views, 61)
@@ -370,7 +377,7 @@ def test_one_launch_head_forced_wait_timeout_recovers(lib, pkg):
     assert lib.phonon_flow_head_device_lsd(dev, streams, dc.ptr, dr.ptr, 0.8, dl.ptr, de.ptr)
     assert lib.phonon_flow_head_device_sync(dev)
     want = dl.download((streams, 32), stream=stream)
-    assert lib.phonon_flow_head_device_set_one_launch(dev, 1)
+    assert lib.phonon_flow_head_device_set_one_launch(dev, one_launch)
     assert lib.phonon_flow_head_device_set_wait_limit(dev, 1)
     assert lib.phonon_flow_head_device_lsd(dev, streams, dc.ptr, dr.ptr, 0.8, dl.ptr, de.ptr)
     assert not lib.phonon_flow_head_device_sync(dev)
