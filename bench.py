@@ -747,7 +747,7 @@ def gemv_valu_vs_mfma(pkg, lib, seed=3, calls=400, copies=300):
     return out
 
 
-def flow_head_bench(pkg, lib, streams=64, calls=200, seed=11, graph=1, one_launch=-1,
+def flow_head_bench(pkg, lib, streams=64, calls=200, seed=11, graph=-1, one_launch=-1,
                     fused=-1):
     """The flow head's batched LSD step (phonon_flow_head_device_lsd: noise
     scaling, input/condition projections, seven adaLN projections as one, six
@@ -826,7 +826,7 @@ def flow_head_bench(pkg, lib, streams=64, calls=200, seed=11, graph=1, one_launc
 
 
 def frame_loop_bench(pkg, lib, layers=12, streams=64, frames=30, warmup=3, seed=2026,
-                     shared_stream=True, graph=1, one_launch=-1, fused=-1):
+                     shared_stream=True, graph=-1, one_launch=-1, fused=-1):
     """The whole per-frame loop of B streams on the GPU: the decode step
     (library default mode), then phonon_flow_head_device_frame (output norm,
     LSD step + EOS logit, latent embedding + condition) writing the next
@@ -901,7 +901,9 @@ def frame_loop_bench(pkg, lib, layers=12, streams=64, frames=30, warmup=3, seed=
                         f"output norm + flow head LSD step + EOS + latent embedding into the "
                         f"next step's input, contexts U{{1..2048}}",
             "head_stream": "the batch's" if shared_stream else "its own, events between",
-            "head_graph": bool(graph),
+            # -1: the library's default (a graph for the chain of launches)
+            "head_graph": graph == 1 or (graph == -1 and not (one_launch > 0 or
+                                                             (one_launch == -1 and streams <= 2))),
             "head_one_launch": one_launch > 0 or (one_launch == -1 and streams <= 2),
             "head_tagged": one_launch == 2 or (one_launch == -1 and streams <= 2),
             "head_fused_mlp": one_launch == 0 and (fused == 1 or (fused == -1 and streams <= 2)),

@@ -109,9 +109,11 @@ int phonon_flow_head_device_frame(PhononFlowHeadDevice *head, size_t streams,
                                   const float *outputs, const float *conditions,
                                   const float *raw_noise, float temperature, float *latents,
                                   float *eos_logits, float *next_inputs);
-/* use_graph = 1 (the default): the step's kernels are captured in a HIP
- * graph per (streams, buffers, temperature), two kept, and replayed; 0:
- * each kernel is launched directly. */
+/* use_graph = 1: the step's kernels are captured in a HIP graph per
+ * (streams, buffers, temperature), two kept, and replayed; 0: each kernel
+ * is launched directly; -1 (the default): a graph for the chain of
+ * launches, direct launches for the one-launch forms (two kernels: a graph
+ * replay costs them 4-5 us at B=1). Returns 0 for any other value. */
 int phonon_flow_head_device_set_graph(PhononFlowHeadDevice *head, int use_graph);
 /* one_launch = 1: the step runs as one dataflow launch (pgpu_head_flow:
  * every projection a work-group task that waits for its inputs on

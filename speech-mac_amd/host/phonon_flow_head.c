@@ -74,7 +74,9 @@ struct PhononFlowHeadDevice {
         float *latents, *eos_logits, *next;
     } graphs[2];
     size_t graph_victim;
-    int eager; /* launch each kernel directly instead of replaying a graph */
+    int use_graph; /* 1: replay a captured graph; 0: launch each kernel directly;
+                      -1 (the default): a graph for the chain of launches, the
+                      one-launch forms launched directly */
     /* One-launch step (pgpu_head_flow): x of every block, u of every block,
      * counters, and the task lists built so far. */
     int one_launch; /* 0: the chain, 1: one launch, 2: one launch with tagged hand-offs,
@@ -432,6 +434,7 @@ int phonon_flow_head_device_create(const PhononFlowHead *head, const PhononTenso
         return 0;
     h->fused = -1;
     h->one_launch = -1;
+    h->use_graph = -1;
     int ok = pgpu_stream_create(&h->own_stream) && (h->stream = h->own_stream) &&
              (h->status = pgpu_malloc(sizeof(int))) &&
              pgpu_memset(h->stream, h->status, 0, sizeof(int)) &&
@@ -639,7 +642,7 @@ static int run_lsd(PhononFlowHeadDevice *h, size_t streams, const float *conditi
         return ph_fail("flow head: tagged words");
     if (mode == 2)
         h->tag_next++;
-    if (h->eager)
+    if (h->use_graph == 0 || (h->use_graph < 0 && mode != 0))
         return enqueue_lsd(h, streams, conditions, raw_noise, temperature, latents, eos_logits,
                            embed, next);
     void *exec = NULL;
@@ -736,7 +739,9 @@ int phonon_flow_head_device_set_graph(PhononFlowHeadDevice *h, int use_graph) {
         return 0;
     if (!pgpu_stream_sync(h->stream))
         return 0;
-    h->eager = !use_graph;
+    if (use_graph < -1 || use_graph > 1)
+        return ph_fail("flow head: graph mode must be -1, 0 or 1");
+    h->use_graph = use_graph;
     for (size_t i = 0; i < 2; i++) {
         pgpu_graph_destroy(h->graphs[i].exec);
         h->graphs[i].exec = NULL;
