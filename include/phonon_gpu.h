@@ -682,6 +682,11 @@ int pgpu_advance_positions(void *stream, int32_t *positions, int streams, int de
  * entries must index rows of src). */
 int pgpu_gather_rows(void *stream, int32_t *dst, const int32_t *src, const int32_t *map,
                      int rows, int width);
+/* pgpu_gather_rows, and copy_dst[r] = copy_src[r] for r < rows in the same
+ * launch (both NULL or both given). A batched prefill gathers its
+ * pseudo-streams' block-table rows and copies their positions this way. */
+int pgpu_gather_rows_copy(void *stream, int32_t *dst, const int32_t *src, const int32_t *map,
+                          int rows, int width, int32_t *copy_dst, const int32_t *copy_src);
 
 #ifdef __cplusplus
 }

@@ -279,6 +279,7 @@ EXPORTS = {
     "pgpu_advance_positions": (_i, [_vp, _vp, _i, _i]),
     "pgpu_fill_normal_plan": (_sz, [_sz, _sz, _szp, _szp]),
     "pgpu_gather_rows": (_i, [_vp, _vp, _vp, _vp, _i, _i]),
+    "pgpu_gather_rows_copy": (_i, [_vp, _vp, _vp, _vp, _i, _i, _vp, _vp]),
     "pgpu_fill_u32": (_i, [_vp, _vp, _sz, ctypes.c_uint32]),
     "pgpu_flow_schedule": (_sz, [_sz, _sz, _szp, _vp, _i, ctypes.POINTER(ctypes.c_uint32),
                                  _sz]),

@@ -224,10 +224,15 @@ __global__ void k_fill_u32(uint32_t *dst, size_t n, uint32_t value) {
 
 // dst row r = src row map[r] (int32 rows of `width`): per-token copies of a
 // stream's block table for a batched prefill. Grid (ceil(width/256), rows).
+// Row r of dst = row map[r] of src; with copy_dst, also copy_dst[r] =
+// copy_src[r] (one value per row, by the row's first work-group).
 __global__ void k_gather_rows(int32_t *__restrict__ dst, const int32_t *__restrict__ src,
-                              const int32_t *__restrict__ map, int width) {
+                              const int32_t *__restrict__ map, int width,
+                              int32_t *__restrict__ copy_dst,
+                              const int32_t *__restrict__ copy_src) {
     const int i = blockIdx.x * 256 + threadIdx.x, r = blockIdx.y;
     if (i < width) dst[(size_t)r * width + i] = src[(size_t)map[r] * width + i];
+    if (copy_dst && i == 0) copy_dst[r] = copy_src[r];
 }
 
 }  // namespace pgpu
@@ -323,12 +328,19 @@ extern "C" int pgpu_advance_positions(void *stream, int32_t *positions, int stre
     return launch_ok(__func__);
 }
 
+extern "C" int pgpu_gather_rows_copy(void *stream, int32_t *dst, const int32_t *src,
+                                     const int32_t *map, int rows, int width, int32_t *copy_dst,
+                                     const int32_t *copy_src) {
+    if (!dst || !src || !map || rows <= 0 || width <= 0 || !copy_dst != !copy_src)
+        return bad_arguments(__func__);
+    hipLaunchKernelGGL(k_gather_rows, dim3((width + 255) / 256, rows), dim3(256), 0,
+                       (hipStream_t)stream, dst, src, map, width, copy_dst, copy_src);
+    return launch_ok(__func__);
+}
+
 extern "C" int pgpu_gather_rows(void *stream, int32_t *dst, const int32_t *src,
                                 const int32_t *map, int rows, int width) {
-    if (!dst || !src || !map || rows <= 0 || width <= 0) return bad_arguments(__func__);
-    hipLaunchKernelGGL(k_gather_rows, dim3((width + 255) / 256, rows), dim3(256), 0,
-                       (hipStream_t)stream, dst, src, map, width);
-    return launch_ok(__func__);
+    return pgpu_gather_rows_copy(stream, dst, src, map, rows, width, nullptr, nullptr);
 }
 
 extern "C" int pgpu_fill_u32(void *stream, uint32_t *dst, size_t n, uint32_t value) {

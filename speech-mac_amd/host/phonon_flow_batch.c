@@ -42,21 +42,22 @@ struct PhononFlowBatch {
     float *x, *r, *q, *in, *out, *rows;
     uint16_t *xh; /* split fragments of the MLP hidden rows */
     int32_t *positions, *tables;
-    int32_t *table_src, *table_map; /* prefill staging, allocated on first use */
+    const int32_t *table_src, *table_map; /* a prefill call's uploads (in pre.stage_dev) */
     struct {
         int active;                 /* the streams are a prefill's pseudo-streams */
         int exact;                  /* attention with the decode step's arithmetic */
-        int32_t *entries;           /* (dev) [cap][4]: work entries of pgpu_prefill_attention */
+        const int32_t *entries;     /* (dev) [count][4]: work entries of pgpu_prefill_attention */
         int32_t *host;              /* [cap][4] */
         size_t count, cap;
-        int32_t *runs;              /* (dev) [runs_cap][2]: the run-based prefill attentions */
+        const int32_t *runs;        /* (dev) [runs_count][2]: the run-based prefill attentions */
         int32_t *runs_host;
         size_t runs_count, runs_cap;
-        int32_t *pairs;             /* (dev) [pairs_cap][4]: runs paired per stream (mfma) */
+        const int32_t *pairs;       /* (dev) [pairs_count][4]: runs paired per stream (mfma) */
         int32_t *pairs_host;
         size_t pairs_count, pairs_cap;
         uint16_t *split;            /* (dev) split fragments [max_streams/16][16][1536] */
         unsigned char *stage;       /* pinned host staging of a prefill call's uploads */
+        unsigned char *stage_dev;   /* (dev) the same layout: one copy moves the whole area */
         size_t stage_cap, stage_used;
     } pre;
     int flow;                       /* 1: one launch per step (pgpu_flow_launch) */
@@ -418,18 +419,15 @@ void phonon_flow_batch_destroy(PhononFlowBatch *b) {
     pgpu_event_destroy(b->fork);
     void *bufs[] = {b->x,    b->r,  b->q,         b->in,     b->out,
                     b->rows, b->xh, b->positions, b->tables, b->status,
-                    b->scratch.part_acc, b->scratch.part_ml, b->table_src, b->table_map,
+                    b->scratch.part_acc, b->scratch.part_ml, b->pre.stage_dev,
                     b->fl.act, b->fl.part_acc, b->fl.part_ml, b->fl.hidden, b->fl.counters,
                     b->fl.rows, b->fl.parts, b->fl.mlp_parts, b->fl.schedule};
     for (size_t i = 0; i < sizeof(bufs) / sizeof(bufs[0]); i++)
         pgpu_free(bufs[i]);
     pgpu_stream_destroy(b->stream);
-    pgpu_free(b->pre.entries);
     free(b->pre.host);
     pgpu_host_free(b->pre.stage);
-    pgpu_free(b->pre.runs);
     free(b->pre.runs_host);
-    pgpu_free(b->pre.pairs);
     free(b->pre.pairs_host);
     pgpu_free(b->pre.split);
     free(b->host_positions);
@@ -1050,29 +1048,41 @@ static size_t entry_list(size_t streams, const size_t *first, const size_t *coun
     return n;
 }
 
-/* A prefill call's small uploads (block tables, positions, work lists) go
- * through one pinned staging area as asynchronous copies on the batch's
- * stream: no host round trip per upload. stage_begin runs after the stream
- * was synchronized, so no copy of an earlier call still reads the area. */
+/* A prefill call's small uploads (block tables, positions, work lists) are
+ * laid out in one pinned staging area whose device mirror has the same
+ * layout: stage_put places a piece and returns its device address, and
+ * stage_flush moves the whole area up as one asynchronous copy on the
+ * batch's stream (one copy instead of one per piece, and no host round
+ * trip). The kernels read the pieces where the copy puts them. stage_begin
+ * runs after the stream was synchronized, so no copy or kernel of an
+ * earlier call still reads either area. */
 static int stage_begin(PhononFlowBatch *b, size_t bytes) {
     if (bytes > b->pre.stage_cap) {
         pgpu_host_free(b->pre.stage);
+        pgpu_free(b->pre.stage_dev);
         b->pre.stage = pgpu_host_malloc(bytes);
-        b->pre.stage_cap = b->pre.stage ? bytes : 0;
-        if (!b->pre.stage)
+        b->pre.stage_dev = pgpu_malloc(bytes);
+        b->pre.stage_cap = b->pre.stage && b->pre.stage_dev ? bytes : 0;
+        if (!b->pre.stage_cap)
             return 0;
     }
     b->pre.stage_used = 0;
     return 1;
 }
 
-static int stage_upload(PhononFlowBatch *b, void *dst, const void *src, size_t bytes) {
+static const int32_t *stage_put(PhononFlowBatch *b, const void *src, size_t bytes) {
     const size_t at = (b->pre.stage_used + 255) & ~(size_t)255;
-    if (at > b->pre.stage_cap || bytes > b->pre.stage_cap - at)
-        return ph_fail("prefill: staging area too small");
+    if (at > b->pre.stage_cap || bytes > b->pre.stage_cap - at) {
+        ph_fail("prefill: staging area too small");
+        return NULL;
+    }
     memcpy(b->pre.stage + at, src, bytes);
     b->pre.stage_used = at + bytes;
-    return pgpu_copy_h2d_async(b->stream, dst, b->pre.stage + at, bytes);
+    return (const int32_t *)(b->pre.stage_dev + at);
+}
+
+static int stage_flush(PhononFlowBatch *b) {
+    return pgpu_copy_h2d_async(b->stream, b->pre.stage_dev, b->pre.stage, b->pre.stage_used);
 }
 
 /* Staging bytes of a prefill of `total` positions: positions and table map,
@@ -1101,16 +1111,12 @@ static int prefill_entries(PhononFlowBatch *b, size_t streams, const size_t *fir
         if (!host)
             return 0;
         b->pre.host = host;
-        pgpu_free(b->pre.entries);
-        b->pre.entries = pgpu_malloc(n * 4 * sizeof(int32_t));
-        b->pre.cap = b->pre.entries ? n : 0;
-        if (!b->pre.entries)
-            return 0;
+        b->pre.cap = n;
     }
     if (entry_list(streams, first, counts, run, b->pre.host, b->pre.cap) != n)
         return 0;
     b->pre.count = n;
-    return stage_upload(b, b->pre.entries, b->pre.host, n * 4 * sizeof(int32_t));
+    return (b->pre.entries = stage_put(b, b->pre.host, n * 4 * sizeof(int32_t))) != NULL;
 }
 
 /* Work list of the run-based prefill attentions (pgpu_prefill_attention_mfma
@@ -1176,15 +1182,12 @@ static int prefill_pairs(PhononFlowBatch *b, size_t streams, const size_t *first
     qsort(list, n, sizeof(PrefillPair), pair_order);
     if (n > b->pre.pairs_cap) {
         int32_t *host = realloc(b->pre.pairs_host, n * 4 * sizeof(int32_t));
-        if (host)
-            b->pre.pairs_host = host;
-        pgpu_free(b->pre.pairs);
-        b->pre.pairs = host ? pgpu_malloc(n * 4 * sizeof(int32_t)) : NULL;
-        b->pre.pairs_cap = b->pre.pairs ? n : 0;
-        if (!b->pre.pairs) {
+        if (!host) {
             free(list);
             return 0;
         }
+        b->pre.pairs_host = host;
+        b->pre.pairs_cap = n;
     }
     for (size_t j = 0; j < n; j++) {
         b->pre.pairs_host[4 * j] = list[j].s0;
@@ -1194,7 +1197,7 @@ static int prefill_pairs(PhononFlowBatch *b, size_t streams, const size_t *first
     }
     free(list);
     b->pre.pairs_count = n;
-    return stage_upload(b, b->pre.pairs, b->pre.pairs_host, n * 4 * sizeof(int32_t));
+    return (b->pre.pairs = stage_put(b, b->pre.pairs_host, n * 4 * sizeof(int32_t))) != NULL;
 }
 
 static int prefill_runs(PhononFlowBatch *b, size_t streams, const size_t *first,
@@ -1215,15 +1218,12 @@ static int prefill_runs(PhononFlowBatch *b, size_t streams, const size_t *first,
     qsort(list, n, sizeof(PrefillRun), run_order);
     if (n > b->pre.runs_cap) {
         int32_t *host = realloc(b->pre.runs_host, n * 2 * sizeof(int32_t));
-        if (host)
-            b->pre.runs_host = host;
-        pgpu_free(b->pre.runs);
-        b->pre.runs = host ? pgpu_malloc(n * 2 * sizeof(int32_t)) : NULL;
-        b->pre.runs_cap = b->pre.runs ? n : 0;
-        if (!b->pre.runs) {
+        if (!host) {
             free(list);
             return 0;
         }
+        b->pre.runs_host = host;
+        b->pre.runs_cap = n;
     }
     for (size_t k = 0; k < n; k++) {
         b->pre.runs_host[2 * k] = list[k].s0;
@@ -1231,7 +1231,7 @@ static int prefill_runs(PhononFlowBatch *b, size_t streams, const size_t *first,
     }
     free(list);
     b->pre.runs_count = n;
-    return stage_upload(b, b->pre.runs, b->pre.runs_host, n * 2 * sizeof(int32_t)) &&
+    return (b->pre.runs = stage_put(b, b->pre.runs_host, n * 2 * sizeof(int32_t))) != NULL &&
            prefill_pairs(b, streams, first, counts);
 }
 
@@ -1260,8 +1260,6 @@ static int set_prefill(PhononFlowBatch *b, size_t streams, const size_t *first,
     const size_t total = prefill_total(b, streams, first, counts);
     if (!total)
         return 0;
-    if (!b->table_map && !(b->table_map = pgpu_malloc(b->max_streams * sizeof(int32_t))))
-        return 0;
     if (!b->pre.split &&
         !(b->pre.split = pgpu_malloc(b->padded_streams / 16 * (PH_WIDTH / 32) * 1536 *
                                      sizeof(uint16_t))))
@@ -1274,11 +1272,13 @@ static int set_prefill(PhononFlowBatch *b, size_t streams, const size_t *first,
             map[p] = (int32_t)i;
             b->host_positions[p] = first[i] + k;
         }
-    ok = ok && stage_upload(b, b->positions, pos32, total * sizeof(int32_t)) &&
-         stage_upload(b, b->table_map, map, total * sizeof(int32_t)) &&
-         pgpu_gather_rows(b->stream, b->tables, tables_dev, b->table_map, (int)total,
-                          (int)b->table_len) &&
-         prefill_entries(b, streams, first, counts) && prefill_runs(b, streams, first, counts);
+    const int32_t *pos_dev = NULL;
+    ok = ok && (pos_dev = stage_put(b, pos32, total * sizeof(int32_t))) &&
+         (b->table_map = stage_put(b, map, total * sizeof(int32_t))) &&
+         prefill_entries(b, streams, first, counts) && prefill_runs(b, streams, first, counts) &&
+         stage_flush(b) &&
+         pgpu_gather_rows_copy(b->stream, b->tables, tables_dev, b->table_map, (int)total,
+                               (int)b->table_len, b->positions, pos_dev);
     free(pos32);
     free(map);
     if (ok) {
@@ -1303,14 +1303,11 @@ int phonon_flow_batch_prefill_device(PhononFlowBatch *b, size_t streams, const s
     if (!b || !streams || streams > b->max_streams || !first || !counts || !tables ||
         table_len != b->table_len || !inputs || !outputs || !isfinite(theta) || theta <= 0.0f)
         return 0;
-    if (!b->table_src &&
-        !(b->table_src = pgpu_malloc(b->max_streams * b->table_len * sizeof(int32_t))))
-        return 0;
     const size_t total = prefill_total(b, streams, first, counts),
                  table_bytes = streams * table_len * sizeof(int32_t);
     if (!total || !pgpu_stream_sync(b->stream) ||
         !stage_begin(b, stage_bytes(total, table_bytes)) ||
-        !stage_upload(b, b->table_src, tables, table_bytes) ||
+        !(b->table_src = stage_put(b, tables, table_bytes)) ||
         !set_prefill(b, streams, first, counts, b->table_src))
         return 0;
     if (flow_usable(b, 1))

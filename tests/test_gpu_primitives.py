@@ -391,3 +391,28 @@ def test_attention_rejects_bad_arguments(lib):
     assert not lib.phonon_attention_test(fp(q), fp(k), fp(k), 8193, 64, fp(out))
     k[1, 3] = np.nan
     assert not lib.phonon_attention_test(fp(q), fp(k), fp(k), 4, 64, fp(out))
+
+
+@pytest.mark.parametrize("rows,width", [(1, 1), (7, 300), (4096, 512)])
+def test_gather_rows_copy(lib, pkg, rows, width):
+    """The table gather of a batched prefill: row r of dst is row map[r] of
+    src, and the same launch copies one value per row (the positions)."""
+    rng = np.random.default_rng(rows + width)
+    src_rows = 16
+    src = rng.integers(-2**31, 2**31 - 1, size=(src_rows, width), dtype=np.int64).astype(np.int32)
+    mp = rng.integers(0, src_rows, size=rows).astype(np.int32)
+    vals = rng.integers(0, 8192, size=rows).astype(np.int32)
+    d_src, d_map, d_vals = (pkg.DeviceBuffer(lib, a.nbytes) for a in (src, mp, vals))
+    d_src.upload(src), d_map.upload(mp), d_vals.upload(vals)
+    d_dst = pkg.DeviceBuffer(lib, rows * width * 4)
+    d_copy = pkg.DeviceBuffer(lib, rows * 4)
+    assert lib.pgpu_gather_rows_copy(None, d_dst.ptr, d_src.ptr, d_map.ptr, rows, width,
+                                     d_copy.ptr, d_vals.ptr), pkg.last_error(lib)
+    assert np.array_equal(d_dst.download((rows, width), np.int32), src[mp])
+    assert np.array_equal(d_copy.download(rows, np.int32), vals)
+    # Without the copy pair it is pgpu_gather_rows; half a pair is refused.
+    assert lib.pgpu_gather_rows(None, d_dst.ptr, d_src.ptr, d_map.ptr, rows, width)
+    assert not lib.pgpu_gather_rows_copy(None, d_dst.ptr, d_src.ptr, d_map.ptr, rows, width,
+                                         d_copy.ptr, None)
+    for b in (d_src, d_map, d_vals, d_dst, d_copy):
+        b.free()
