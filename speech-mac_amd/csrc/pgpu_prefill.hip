@@ -1093,9 +1093,17 @@ int launch_gemm(const GemmArgs &a, hipStream_t stream) {
 //  - QKV: 192 x 64, 3 x 1 ring (1.651 against 1.717 for 192 x 128);
 //  - MLP in: 256 x 128 with a 2 x 2 ring (1.541 against 1.552 for 3 x 1,
 //    with the two above).
+// A short prompt (at most kShortPrefillTiles 16-position tiles) takes
+// 64 x 32 tiles, one MFMA tile per wave, so that its projections still
+// spread over the CUs (a 256-position prompt: 64-256 work-groups instead
+// of 16-32); a work-group's time hardly depends on its tile's size here.
+constexpr int kShortPrefillTiles = 32;
+
 template <int EPI, bool SCALED>
 int dispatch_gemm(const GemmArgs &a, hipStream_t stream) {
     if (a.split_terms == kF16Pair) {
+        if ((a.streams + 15) / 16 <= kShortPrefillTiles)
+            return launch_format<EPI, SCALED, 4, 2, 1, 1, 3, 1, kF16Pair>(a, stream);
         if constexpr (EPI == EPI_GELU_SPLIT)
             if (a.n_rows % (8 * 256) == 0)
                 return launch_format<EPI, SCALED, 4, 2, 4, 4, 2, 2, kF16Pair>(a, stream);
