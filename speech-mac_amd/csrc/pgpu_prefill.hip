@@ -1096,14 +1096,23 @@ int launch_gemm(const GemmArgs &a, hipStream_t stream) {
 // A short prompt (at most kShortPrefillTiles 16-position tiles) takes
 // 64 x 32 tiles, one MFMA tile per wave, so that its projections still
 // spread over the CUs (a 256-position prompt: 64-256 work-groups instead
-// of 16-32); a work-group's time hardly depends on its tile's size here.
+// of 16-32; a work-group's time hardly depends on its tile's size here),
+// and stages of 4 blocks (8 at K = 2048, two stages in the ring): a stage
+// costs a barrier and a copy wait whatever its size. Measured on the B=1
+// workload's 256-position prefill, 12 layers: 1.18 ms with the large tiles,
+// 0.81 with 64 x 32 tiles and 1-block stages, 0.73 with 4-block stages at
+// K = 2048, 0.70 as chosen.
 constexpr int kShortPrefillTiles = 32;
 
 template <int EPI, bool SCALED>
 int dispatch_gemm(const GemmArgs &a, hipStream_t stream) {
     if (a.split_terms == kF16Pair) {
-        if ((a.streams + 15) / 16 <= kShortPrefillTiles)
-            return launch_format<EPI, SCALED, 4, 2, 1, 1, 3, 1, kF16Pair>(a, stream);
+        if ((a.streams + 15) / 16 <= kShortPrefillTiles) {
+            if constexpr (EPI == EPI_RESIDUAL)
+                if (a.k_cols == kFfn)
+                    return launch_format<EPI, SCALED, 4, 2, 1, 1, 2, 8, kF16Pair>(a, stream);
+            return launch_format<EPI, SCALED, 4, 2, 1, 1, 3, 4, kF16Pair>(a, stream);
+        }
         if constexpr (EPI == EPI_GELU_SPLIT)
             if (a.n_rows % (8 * 256) == 0)
                 return launch_format<EPI, SCALED, 4, 2, 4, 4, 2, 2, kF16Pair>(a, stream);
