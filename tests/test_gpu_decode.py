@@ -864,6 +864,56 @@ def test_batched_prefill_equals_single_steps(lib, syn, pkg, mode, exact):
         assert worst <= 1e-4
 
 
+@pytest.mark.parametrize("counts,first", [([256, 256], [0, 0]), ([200, 57, 255], [0, 40, 0]),
+                                          ([257, 256], [0, 0])])
+def test_fast_prefill_around_the_short_prompt_path(lib, syn, pkg, counts, first):
+    """The fast prefill of 512 positions in one call (the short-prompt path:
+    64 x 32 projection tiles, attention runs of 16 positions; with ragged
+    counts and a continued context) and of 513 (the large tiles, runs of
+    64) against the exact prefill of the same call, which gives the bits of
+    single decode steps: every output row within 1e-4 normwise."""
+    layers = 2
+    model = scaled_model(syn, 191, layers)
+    w = pkg.Views().layers(model)
+    max_pos = 320
+    table_len = max_pos // 16
+    nstreams, total = len(counts), sum(counts)
+    rng = np.random.default_rng(192)
+    ctx_k = rng.standard_normal((layers, max_pos, 512)).astype(np.float32)
+    ctx_v = rng.standard_normal((layers, max_pos, 512)).astype(np.float32)
+    x = rng.standard_normal((total, 512)).astype(np.float32)
+    szp = ctypes.POINTER(ctypes.c_size_t)
+    f = np.array(first, np.uintp)
+    c = np.array(counts, np.uintp)
+    outs = []
+    for exact in (1, 0):
+        bt = Batch(lib, w, layers, total, max_pos, nstreams * table_len)
+        ids = np.zeros(nstreams * table_len, np.int32)
+        assert lib.phonon_kv_pool_alloc(bt.pool, ids.size, i32p(ids))
+        tables = np.ascontiguousarray(ids.reshape(nstreams, table_len))
+        for i in range(nstreams):
+            if first[i]:
+                assert lib.phonon_kv_pool_write(bt.pool, i32p(tables[i]), table_len, 0, first[i],
+                                                fp(ctx_k), fp(ctx_v), max_pos)
+        assert lib.phonon_flow_batch_set_prefill_exact(bt.batch, exact)
+        din = pkg.DeviceBuffer(lib, total * 512 * 4)
+        dout = pkg.DeviceBuffer(lib, total * 512 * 4)
+        din.upload(x)
+        assert lib.phonon_flow_batch_prefill_device(bt.batch, nstreams, f.ctypes.data_as(szp),
+                                                    c.ctypes.data_as(szp), i32p(tables),
+                                                    table_len, din.ptr, 10000.0, dout.ptr), \
+            pkg.last_error(lib)
+        assert lib.phonon_flow_batch_sync(bt.batch)
+        outs.append(dout.download((total, 512)))
+        din.free()
+        dout.free()
+        bt.close()
+    assert np.all(np.isfinite(outs[1]))
+    worst = max(helpers.normwise(b, a) for a, b in zip(outs[0], outs[1]))
+    print(f"fast prefill of {total} positions vs exact: max normwise {worst:.3g}")
+    assert worst <= 1e-4
+
+
 @pytest.mark.parametrize("streams", [1, 3, 16, 17, 40, 64])
 def test_one_launch_step_equals_phase_launches(lib, syn, pkg, streams):
     """The one-launch step (every layer's tasks in one dataflow launch) gives
