@@ -1,6 +1,6 @@
 /* CPU restatement of the speech-mac Flow-transformer decode step.
  *
- * TEST INFRASTRUCTURE ONLY. This library is the checker for the MI355X
+ * TEST INFRASTRUCTURE ONLY. This library is the oracle of the MI355X
  * product (libphonon_mi355x): only tests/, __graft_entry__.smoke() and the
  * cpu_baseline leg of bench.py load it. The product never links, calls or
  * falls back to it.

@@ -1,8 +1,9 @@
 """ctypes binding of liboracle.so (the CPU restatement) and of _ref/libref_q8.so
 (the reference's own phonon_q8.c, compiled from its sources).
 
-TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and the
-cpu_baseline leg of bench.py, as the checker. The product never imports it.
+TEST INFRASTRUCTURE ONLY: imported by tests/ and __graft_entry__.smoke(), which
+check the GPU results against it, and by the cpu_baseline leg of bench.py, which
+times it. The product never imports it.
 """
 from __future__ import annotations
 

@@ -1,4 +1,4 @@
-"""Pins the CPU oracle (oracle/oracle.c) before it is trusted as the checker:
+"""Pins the CPU oracle (oracle/oracle.c) before GPU results are checked against it:
 against the reference's own golden vectors and known answers, against the
 reference's phonon_q8.c compiled from its source (oracle/_ref), and against
 closed forms, exact special cases and float64 brute force."""

@@ -1,5 +1,5 @@
 """Pins the oracle's flow head (oracle/oracle.c, src/phonon_sampler.c:229-401)
-before it is trusted as the checker: the reference's own synthetic-head
+before GPU results are checked against it: the reference's own synthetic-head
 golden vector (an independent PyTorch 2.7.1 run), closed forms and float64
 restatements of each stage, and the exact cascade of mean_512."""
 import json
