@@ -914,6 +914,54 @@ def test_fast_prefill_around_the_short_prompt_path(lib, syn, pkg, counts, first)
     assert worst <= 1e-4
 
 
+def test_prefill_calls_enqueued_back_to_back(lib, syn, pkg):
+    """Prefill calls enqueued one after another with no wait between them
+    give the bits of the same calls with a synchronize after each: three
+    calls with different prompts, block tables and work lists, each
+    reusing the staging area of the call before it."""
+    layers = 2
+    model = scaled_model(syn, 193, layers)
+    w = pkg.Views().layers(model)
+    max_pos = 320
+    table_len = max_pos // 16
+    calls = [([0, 0], [100, 37]), ([0], [300]), ([0, 0, 0], [16, 1, 200])]
+    rng = np.random.default_rng(194)
+    xs = [rng.standard_normal((sum(c), 512)).astype(np.float32) for _, c in calls]
+    szp = ctypes.POINTER(ctypes.c_size_t)
+    results = []
+    for wait_each in (True, False):
+        bt = Batch(lib, w, layers, 300, max_pos, 6 * table_len)
+        ids = np.zeros(6 * table_len, np.int32)
+        assert lib.phonon_kv_pool_alloc(bt.pool, ids.size, i32p(ids))
+        rows = np.ascontiguousarray(ids.reshape(6, table_len))
+        outs, bufs, at = [], [], 0
+        for (first, counts), x in zip(calls, xs):
+            n = len(counts)
+            tables = np.ascontiguousarray(rows[at:at + n])
+            at += n
+            din = pkg.DeviceBuffer(lib, x.nbytes)
+            dout = pkg.DeviceBuffer(lib, x.nbytes)
+            din.upload(x)
+            f = np.array(first, np.uintp)
+            c = np.array(counts, np.uintp)
+            assert lib.phonon_flow_batch_prefill_device(bt.batch, n, f.ctypes.data_as(szp),
+                                                        c.ctypes.data_as(szp), i32p(tables),
+                                                        table_len, din.ptr, 10000.0,
+                                                        dout.ptr), pkg.last_error(lib)
+            if wait_each:
+                assert lib.phonon_flow_batch_sync(bt.batch)
+            bufs += [din, dout]
+            outs.append((dout, x.shape))
+        assert lib.phonon_flow_batch_sync(bt.batch)
+        results.append([d.download(shape) for d, shape in outs])
+        for b in bufs:
+            b.free()
+        bt.close()
+    for a, b in zip(results[0], results[1]):
+        assert np.all(np.isfinite(a))
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
 @pytest.mark.parametrize("streams", [1, 3, 16, 17, 40, 64])
 def test_one_launch_step_equals_phase_launches(lib, syn, pkg, streams):
     """The one-launch step (every layer's tasks in one dataflow launch) gives
